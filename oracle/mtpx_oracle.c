@@ -1,0 +1,823 @@
+/*
+ * mtpx CPU oracle -- TEST INFRASTRUCTURE ONLY (see mtpx_oracle.h).
+ *
+ * Reference semantics followed (paths relative to the reference checkout):
+ *   MLX = Vendor/mlx-swift/Source/Cmlx/mlx/mlx
+ *   FM  = Runner/FastModel
+ *
+ * Parity status of each function is listed in the header comment of the
+ * function and summarised in tests/test_oracle_pin.py.
+ */
+#include "mtpx_oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ======================================================================== */
+/* scalar numerics                                                           */
+/* ======================================================================== */
+
+float o_bf2f(o_bf16 h) {
+  uint32_t u = (uint32_t)h << 16;
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+o_bf16 o_f2bf(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0; /* NaN */
+  u += 0x7fffu + ((u >> 16) & 1u);                      /* round to nearest even */
+  return (o_bf16)(u >> 16);
+}
+
+float o_round_bf(float f) { return o_bf2f(o_f2bf(f)); }
+
+static float f_from_bits(uint32_t u) {
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+/*
+ * exp(x) in float: Cody-Waite reduction x = n*ln2 + r with a two-part ln2,
+ * degree-7 Taylor polynomial on |r| <= ln2/2 (truncation error < 2^-27
+ * relative), scale by 2^n in two exact steps.  Inputs below -87.3 return 0
+ * (no subnormal results), above 88.7 return +inf.  Pinned against libm expf
+ * (<= 2 ulp over a dense sweep) in tests/test_oracle_pin.py.
+ */
+float o_expf(float x) {
+  if (x != x) return x;
+  if (x < -87.3f) return 0.0f;
+  if (x > 88.7f) return f_from_bits(0x7f800000u);
+  const float n = rintf(x * 1.44269504f);
+  float r = fmaf(-n, 0.693145751953125f, x);
+  r = fmaf(-n, 1.428606765330187e-06f, r);
+  float p = 1.98412698e-04f;
+  p = fmaf(p, r, 1.38888889e-03f);
+  p = fmaf(p, r, 8.33333333e-03f);
+  p = fmaf(p, r, 4.16666667e-02f);
+  p = fmaf(p, r, 1.66666667e-01f);
+  p = fmaf(p, r, 0.5f);
+  p = fmaf(p, r, 1.0f);
+  p = fmaf(p, r, 1.0f);
+  const int ni = (int)n;
+  const int n1 = ni / 2, n2 = ni - n1;
+  p = p * f_from_bits((uint32_t)(n1 + 127) << 23);
+  p = p * f_from_bits((uint32_t)(n2 + 127) << 23);
+  return p;
+}
+
+/*
+ * MLX's Sigmoid functor evaluated in bf16 (each operation rounds to bf16):
+ * y = 1 / (1 + exp(|x|)); x < 0 ? y : 1 - y.
+ * Follows FM/TrackFastKernels2.swift:21-30 (mlx_sigmoid / mlx_silu).
+ */
+float o_sigmoid_bf16(float x) {
+  const float e = o_round_bf(o_expf(fabsf(x)));
+  const float d = o_round_bf(1.0f + e);
+  const float y = o_round_bf(1.0f / d);
+  return (x < 0.0f) ? y : o_round_bf(1.0f - y);
+}
+
+float o_silu_bf16(float x) { return o_round_bf(x * o_sigmoid_bf16(x)); }
+
+/* Lanes that share one row of the q4 GEMV: the largest power of two <= 64
+ * that still leaves each lane >= 4 blocks of 32 elements. */
+int o_lanes_for_blocks(int nb) {
+  int L = 1;
+  while (L < 64 && (L * 2) * 4 <= nb) L *= 2;
+  return L;
+}
+
+/* ======================================================================== */
+/* a1: MLX affine quantize (MLX/backend/cpu/quantized.cpp:1158-1220,         */
+/*     MLX/ops.cpp:5036-5090, pack MLX/ops.cpp:4988-5020)                    */
+/* ======================================================================== */
+
+void o_affine_quantize(const o_bf16* w, int64_t rows, int K, int gs, uint32_t* wq,
+                       o_bf16* scales, o_bf16* biases) {
+  const int ng = K / gs;
+  for (int64_t r = 0; r < rows; ++r) {
+    for (int g = 0; g < ng; ++g) {
+      const o_bf16* wg = w + r * K + (int64_t)g * gs;
+      float wmin = INFINITY, wmax = -INFINITY;
+      for (int j = 0; j < gs; ++j) {
+        const float v = o_bf2f(wg[j]);
+        wmax = fmaxf(wmax, v);
+        wmin = fminf(wmin, v);
+      }
+      const int mask = fabsf(wmin) > fabsf(wmax);
+      float scale = fmaxf((wmax - wmin) / 15.0f, 1e-7f);
+      scale = mask ? scale : -scale;
+      const float edge = mask ? wmin : wmax;
+      const float q0 = rintf(edge / scale);
+      float bias = 0.0f;
+      if (q0 != 0.0f) {
+        scale = edge / q0;
+        bias = edge;
+      }
+      for (int j = 0; j < gs / 8; ++j) {
+        uint32_t word = 0;
+        for (int t = 0; t < 8; ++t) {
+          float v = rintf((o_bf2f(wg[j * 8 + t]) - bias) / scale);
+          v = fminf(fmaxf(v, 0.0f), 15.0f);
+          word |= (uint32_t)v << (4 * t);
+        }
+        wq[r * (K / 8) + (int64_t)g * (gs / 8) + j] = word;
+      }
+      scales[r * ng + g] = o_f2bf(scale);
+      biases[r * ng + g] = o_f2bf(bias);
+    }
+  }
+}
+
+/* ======================================================================== */
+/* a2-a4, a12: q4 GEMV                                                       */
+/* ======================================================================== */
+
+/*
+ * Activation block transform.  A block of 32 bf16 values shares the exponent
+ * E = max biased exponent field (a zero field counts as 1).  Each value
+ * becomes the integer m = x / 2^(E-149), truncated toward zero, so
+ * |m| < 2^23: exact for every element within 2^15 of the block maximum.
+ */
+void o_xblock(const o_bf16* x32, int32_t* m, int32_t* E_out) {
+  int E = 1;
+  for (int i = 0; i < 32; ++i) {
+    int f = (x32[i] >> 7) & 0xff;
+    if (f < 1) f = 1;
+    if (f > E) E = f;
+  }
+  for (int i = 0; i < 32; ++i) {
+    const uint32_t h = x32[i];
+    const int field = (h >> 7) & 0xff;
+    const int f = field < 1 ? 1 : field;
+    const int32_t sig = (int32_t)((field ? 0x80u : 0u) | (h & 0x7fu));
+    const int sh = f - E + 15;
+    int32_t mag;
+    if (sh >= 0)
+      mag = sig << sh;
+    else if (sh > -31)
+      mag = sig >> (-sh);
+    else
+      mag = 0;
+    m[i] = (h & 0x8000u) ? -mag : mag;
+  }
+  *E_out = E;
+}
+
+static float block_scale(int E) {
+  /* 2^(E - 149) as a float */
+  if (E >= 23) return f_from_bits((uint32_t)(E - 22) << 23);
+  return f_from_bits(1u << E);
+}
+
+/* One row of the GEMV over pre-transformed activation blocks.
+ * Per block j: D = sum_i q_i * m_i split over the 24-bit two's-complement
+ * limbs of m (l0, l1 unsigned bytes, l2 signed byte); each limb sum is exact.
+ *   DXraw = fmaf((float)D2, 65536, (float)(D1*256 + D0))
+ *   DX = DXraw * p_j,  SX = (float)(sum_i m_i) * p_j,  p_j = 2^(E_j-149)
+ *   acc_lane = fmaf(b_g, SX, fmaf(s_g, DX, acc_lane))
+ * Lane l of L accumulates blocks l, l+L, ... in order from 0.0f; the L lane
+ * values are then folded by an xor butterfly (offsets L/2 ... 1). */
+static float qmv_row(const uint32_t* wrow, const o_bf16* srow, const o_bf16* brow, int K, int gs,
+                     const int32_t* m /* [nb*32] */, const float* p /* [nb] */,
+                     const float* SX /* [nb] */) {
+  const int nb = K / 32;
+  const int L = o_lanes_for_blocks(nb);
+  float lane[64];
+  for (int l = 0; l < L; ++l) {
+    float acc = 0.0f;
+    for (int j = l; j < nb; j += L) {
+      int64_t d0 = 0, d1 = 0, d2 = 0;
+      for (int i = 0; i < 32; ++i) {
+        const uint32_t q = (wrow[(j * 32 + i) / 8] >> (4 * ((j * 32 + i) % 8))) & 0xfu;
+        const uint32_t u = (uint32_t)m[j * 32 + i] & 0xffffffu;
+        const int32_t l0 = (int32_t)(u & 0xffu), l1 = (int32_t)((u >> 8) & 0xffu);
+        const int32_t l2 = (int32_t)(int8_t)(uint8_t)(u >> 16);
+        d0 += (int64_t)q * l0;
+        d1 += (int64_t)q * l1;
+        d2 += (int64_t)q * l2;
+      }
+      const int32_t low = (int32_t)(d1 * 256 + d0);
+      const float dxraw = fmaf((float)(int32_t)d2, 65536.0f, (float)low);
+      const float dx = dxraw * p[j];
+      const int g = (j * 32) / gs;
+      acc = fmaf(o_bf2f(srow[g]), dx, acc);
+      acc = fmaf(o_bf2f(brow[g]), SX[j], acc);
+    }
+    lane[l] = acc;
+  }
+  for (int off = L / 2; off >= 1; off /= 2) {
+    float nv[64];
+    for (int l = 0; l < L; ++l) nv[l] = lane[l] + lane[l ^ off];
+    memcpy(lane, nv, sizeof(float) * L);
+  }
+  return lane[0];
+}
+
+typedef struct {
+  int nb;
+  int32_t* m;
+  float* p;
+  float* SX;
+} xprep_t;
+
+static void xprep(const o_bf16* x, int K, xprep_t* xp) {
+  xp->nb = K / 32;
+  xp->m = (int32_t*)malloc(sizeof(int32_t) * K);
+  xp->p = (float*)malloc(sizeof(float) * xp->nb);
+  xp->SX = (float*)malloc(sizeof(float) * xp->nb);
+  for (int j = 0; j < xp->nb; ++j) {
+    int32_t E;
+    o_xblock(x + j * 32, xp->m + j * 32, &E);
+    int32_t sm = 0;
+    for (int i = 0; i < 32; ++i) sm += xp->m[j * 32 + i];
+    xp->p[j] = block_scale(E);
+    xp->SX[j] = (float)sm * xp->p[j];
+  }
+}
+
+static void xfree(xprep_t* xp) {
+  free(xp->m);
+  free(xp->p);
+  free(xp->SX);
+}
+
+void o_qmv(const uint32_t* wq, const o_bf16* scales, const o_bf16* biases, int64_t N, int K,
+           int gs, const o_bf16* x, int M, o_bf16* y, float* yf) {
+  const int ng = K / gs;
+  for (int mm = 0; mm < M; ++mm) {
+    xprep_t xp;
+    xprep(x + (int64_t)mm * K, K, &xp);
+    for (int64_t r = 0; r < N; ++r) {
+      const float v = qmv_row(wq + r * (K / 8), scales + r * ng, biases + r * ng, K, gs, xp.m,
+                              xp.p, xp.SX);
+      if (y) y[(int64_t)mm * N + r] = o_f2bf(v);
+      if (yf) yf[(int64_t)mm * N + r] = v;
+    }
+    xfree(&xp);
+  }
+}
+
+/* ======================================================================== */
+/* a6 / a9: router GEMV (FM/TrackFastMoE.swift:2246-2310: bf16 weight, f32   */
+/* activation, f32 result).  Order: 64 lanes; lane l walks 8-element chunks  */
+/* c = l, l+64, ... and accumulates acc = fmaf(w, x, acc) element by element; */
+/* then an xor butterfly over the 64 lanes.                                  */
+/* ======================================================================== */
+
+static float router_row(const o_bf16* wrow, int H, const float* x) {
+  float lane[64];
+  const int nc = H / 8;
+  for (int l = 0; l < 64; ++l) {
+    float acc = 0.0f;
+    for (int c = l; c < nc; c += 64)
+      for (int i = 0; i < 8; ++i) acc = fmaf(o_bf2f(wrow[c * 8 + i]), x[c * 8 + i], acc);
+    lane[l] = acc;
+  }
+  for (int off = 32; off >= 1; off /= 2) {
+    float nv[64];
+    for (int l = 0; l < 64; ++l) nv[l] = lane[l] + lane[l ^ off];
+    memcpy(lane, nv, sizeof(nv));
+  }
+  return lane[0];
+}
+
+void o_router_gemv(const o_bf16* W, int rows, int H, const float* x, int M, float* out) {
+  for (int m = 0; m < M; ++m)
+    for (int r = 0; r < rows; ++r)
+      out[(int64_t)m * rows + r] = router_row(W + (int64_t)r * H, H, x + (int64_t)m * H);
+}
+
+/* ======================================================================== */
+/* a8: top-k + softmax (FM/TrackFastMoE.swift:780-878): the K largest logits, */
+/* value descending, ties to the lowest index; softmax over the K selected:   */
+/* max, e_k = exp(v_k - max), sum in rank order, w_k = e_k * (1 / sum).       */
+/* ======================================================================== */
+
+void o_topk_softmax(const float* logits, int M, int E, int K, int32_t* idx, float* w) {
+  unsigned char* taken = (unsigned char*)malloc((size_t)E);
+  for (int m = 0; m < M; ++m) {
+    const float* lr = logits + (int64_t)m * E;
+    memset(taken, 0, (size_t)E);
+    float v[64];
+    for (int k = 0; k < K; ++k) {
+      int best = -1;
+      for (int e = 0; e < E; ++e) {
+        if (taken[e]) continue;
+        if (best < 0 || lr[e] > lr[best]) best = e;
+      }
+      taken[best] = 1;
+      idx[m * K + k] = best;
+      v[k] = lr[best];
+    }
+    const float mx = v[0];
+    float e[64];
+    float sum = 0.0f;
+    for (int k = 0; k < K; ++k) {
+      e[k] = o_expf(v[k] - mx);
+      sum = sum + e[k];
+    }
+    const float inv = 1.0f / sum;
+    for (int k = 0; k < K; ++k) w[m * K + k] = e[k] * inv;
+  }
+  free(taken);
+}
+
+/* ======================================================================== */
+/* a5, a10, a11: the MoE block (FM/TrackFastModel.swift:867-954,             */
+/* FM/TrackFastMoE.swift:1192-1576, FM/TrackFastKernels2.swift:512-567)      */
+/* ======================================================================== */
+
+/* MLX col_reduce_small fold over K products (FM/TrackFastKernels2.swift:31-44). */
+static float colsum_small(const float* r, int K) {
+  const int TY = K < 8 ? K : 8;
+  float t[8];
+  for (int y = 0; y < TY; ++y) {
+    float acc = 0.0f;
+    for (int rr = y; rr < K; rr += TY) acc = r[rr] + acc;
+    t[y] = acc;
+  }
+  float total = t[0];
+  for (int j = 1; j < TY; ++j) total = t[j] + total;
+  return total;
+}
+
+/* gate|up GEMV of one expert + SwiGLU: act[f] = bf16(silu_bf16(g) * u). */
+static void expert_act(const uint32_t* gw, const o_bf16* gs_, const o_bf16* gb,
+                       const uint32_t* uw, const o_bf16* us, const o_bf16* ub, int F, int H,
+                       int gsz, const o_bf16* x, o_bf16* act) {
+  o_bf16* g = (o_bf16*)malloc(sizeof(o_bf16) * F);
+  o_bf16* u = (o_bf16*)malloc(sizeof(o_bf16) * F);
+  o_qmv(gw, gs_, gb, F, H, gsz, x, 1, g, NULL);
+  o_qmv(uw, us, ub, F, H, gsz, x, 1, u, NULL);
+  for (int f = 0; f < F; ++f)
+    act[f] = o_f2bf(o_silu_bf16(o_bf2f(g[f])) * o_bf2f(u[f]));
+  free(g);
+  free(u);
+}
+
+void o_moe_block(const o_moe_weights* mw, const o_bf16* x, int M, o_bf16* y, int32_t* idx,
+                 float* w, float* logits, o_bf16* gate, o_bf16* act_out) {
+  const int H = mw->H, E = mw->E, K = mw->K, F = mw->F, gsz = mw->gs;
+  const int64_t ngH = H / gsz, ngF = F / gsz;
+  float* xf = (float*)malloc(sizeof(float) * H);
+  o_bf16* act = (o_bf16*)malloc(sizeof(o_bf16) * (size_t)(K + 1) * F);
+  o_bf16* r = (o_bf16*)malloc(sizeof(o_bf16) * (size_t)(K + 1) * H);
+  float* lg = (float*)malloc(sizeof(float) * E);
+  for (int m = 0; m < M; ++m) {
+    const o_bf16* xm = x + (int64_t)m * H;
+    for (int h = 0; h < H; ++h) xf[h] = o_bf2f(xm[h]);
+    o_router_gemv(mw->router, E, H, xf, 1, lg);
+    float gl;
+    o_router_gemv(mw->shared_gate, 1, H, xf, 1, &gl);
+    const float gbf = o_round_bf(gl);
+    if (logits) memcpy(logits + (int64_t)m * E, lg, sizeof(float) * E);
+    if (gate) gate[m] = o_f2bf(gl);
+    int32_t id[64];
+    float wk[64];
+    o_topk_softmax(lg, 1, E, K, id, wk);
+    if (idx) memcpy(idx + m * K, id, sizeof(int32_t) * K);
+    if (w) memcpy(w + m * K, wk, sizeof(float) * K);
+    for (int k = 0; k < K; ++k) {
+      const int64_t e = id[k];
+      expert_act(mw->gate_w + e * F * (H / 8), mw->gate_s + e * F * ngH, mw->gate_b + e * F * ngH,
+                 mw->up_w + e * F * (H / 8), mw->up_s + e * F * ngH, mw->up_b + e * F * ngH, F, H,
+                 gsz, xm, act + (int64_t)k * F);
+      o_qmv(mw->down_w + e * H * (F / 8), mw->down_s + e * H * ngF, mw->down_b + e * H * ngF, H,
+            F, gsz, act + (int64_t)k * F, 1, r + (int64_t)k * H, NULL);
+    }
+    expert_act(mw->sh_gate_w, mw->sh_gate_s, mw->sh_gate_b, mw->sh_up_w, mw->sh_up_s,
+               mw->sh_up_b, F, H, gsz, xm, act + (int64_t)K * F);
+    o_qmv(mw->sh_down_w, mw->sh_down_s, mw->sh_down_b, H, F, gsz, act + (int64_t)K * F, 1,
+          r + (int64_t)K * H, NULL);
+    if (act_out) {
+      for (int k = 0; k < K; ++k)
+        memcpy(act_out + ((int64_t)m * K + k) * F, act + (int64_t)k * F, sizeof(o_bf16) * F);
+      memcpy(act_out + ((int64_t)M * K + m) * F, act + (int64_t)K * F, sizeof(o_bf16) * F);
+    }
+    const float sg = o_sigmoid_bf16(gbf);
+    for (int h = 0; h < H; ++h) {
+      float prod[64];
+      for (int k = 0; k < K; ++k) prod[k] = o_bf2f(r[(int64_t)k * H + h]) * wk[k];
+      const float rr = o_round_bf(colsum_small(prod, K));
+      const float sh = o_round_bf(sg * o_bf2f(r[(int64_t)K * H + h]));
+      y[(int64_t)m * H + h] = o_f2bf(rr + sh);
+    }
+  }
+  free(xf);
+  free(act);
+  free(r);
+  free(lg);
+}
+
+/* ======================================================================== */
+/* a13: attention prep (FM/TrackFastKernels2.swift:381-476)                  */
+/* ======================================================================== */
+
+/* Rotate-half RoPE tables [positions, rot] (bf16): entry d uses frequency
+ * theta^(-2*(d mod rot/2)/rot); angles and cos/sin in double, then bf16. */
+void o_rope_table(int positions, int rot, double theta, o_bf16* cos_t, o_bf16* sin_t) {
+  const int half = rot / 2;
+  for (int p = 0; p < positions; ++p)
+    for (int d = 0; d < rot; ++d) {
+      const int i = d % half;
+      const double inv = pow(theta, -2.0 * (double)i / (double)rot);
+      const double a = (double)p * inv;
+      cos_t[(int64_t)p * rot + d] = o_f2bf((float)cos(a));
+      sin_t[(int64_t)p * rot + d] = o_f2bf((float)sin(a));
+    }
+}
+
+/* RMS statistic of one head of D values: D/4 lanes, lane t squares elements
+ * 4t..4t+3 into acc = fmaf(x, x, acc), then an xor butterfly over D/4 lanes;
+ * inv = 1 / sqrtf(sum / D + eps). */
+static float head_inv_rms(const float* x, int D, float eps) {
+  const int L = D / 4;
+  float lane[256];
+  for (int t = 0; t < L; ++t) {
+    float acc = 0.0f;
+    for (int i = 0; i < 4; ++i) acc = fmaf(x[4 * t + i], x[4 * t + i], acc);
+    lane[t] = acc;
+  }
+  for (int off = L / 2; off >= 1; off /= 2) {
+    float nv[256];
+    for (int t = 0; t < L; ++t) nv[t] = lane[t] + lane[t ^ off];
+    memcpy(lane, nv, sizeof(float) * L);
+  }
+  return 1.0f / sqrtf(lane[0] / (float)D + eps);
+}
+
+static void norm_rope_head(const o_bf16* src, const o_bf16* wn, int D, int ROT, float eps,
+                           const o_bf16* cs, const o_bf16* sn, o_bf16* dst) {
+  float x[1024], v[1024];
+  for (int d = 0; d < D; ++d) x[d] = o_bf2f(src[d]);
+  const float inv = head_inv_rms(x, D, eps);
+  for (int d = 0; d < D; ++d) v[d] = o_round_bf(o_bf2f(wn[d]) * o_round_bf(x[d] * inv));
+  const int half = ROT / 2;
+  for (int d = 0; d < D; ++d) {
+    float o = v[d];
+    if (d < ROT) {
+      const float c = o_bf2f(cs[d]), s = o_bf2f(sn[d]);
+      if (d < half) {
+        const float t1 = o_round_bf(v[d] * c);
+        const float t2 = o_round_bf(-v[d + half] * s);
+        o = o_round_bf(t1 + t2);
+      } else {
+        const float t1 = o_round_bf(v[d] * c);
+        const float t2 = o_round_bf(v[d - half] * s);
+        o = o_round_bf(t1 + t2);
+      }
+    }
+    dst[d] = o_f2bf(o);
+  }
+}
+
+/* qkv rows [S, QW] = q(HQ*D) | gate(HQ*D) | k(HK*D) | v(HK*D) | ...
+ * -> q [S, HQ, D], k [S, HK, D], v [S, HK, D]; row s uses rope position pos0+s. */
+void o_attn_prep(const o_bf16* qkv, int S, int QW, int HQ, int HK, int D, int ROT,
+                 const o_bf16* qnorm, const o_bf16* knorm, float eps, const o_bf16* cos_t,
+                 const o_bf16* sin_t, int pos0, o_bf16* q, o_bf16* k, o_bf16* v) {
+  for (int s = 0; s < S; ++s) {
+    const o_bf16* row = qkv + (int64_t)s * QW;
+    const o_bf16* cs = cos_t + (int64_t)(pos0 + s) * ROT;
+    const o_bf16* sn = sin_t + (int64_t)(pos0 + s) * ROT;
+    for (int h = 0; h < HQ; ++h)
+      norm_rope_head(row + h * D, qnorm, D, ROT, eps, cs, sn, q + ((int64_t)s * HQ + h) * D);
+    for (int h = 0; h < HK; ++h) {
+      norm_rope_head(row + 2 * HQ * D + h * D, knorm, D, ROT, eps, cs, sn,
+                     k + ((int64_t)s * HK + h) * D);
+      memcpy(v + ((int64_t)s * HK + h) * D, row + 2 * HQ * D + HK * D + h * D,
+             sizeof(o_bf16) * D);
+    }
+  }
+}
+
+/* ======================================================================== */
+/* a14: verify attention over a contiguous KV cache                          */
+/* (MLX/backend/metal/kernels/sdpa_vector.h:14-175: f32 online softmax,      */
+/* causal rule key i visible to query s iff i <= T - S + s, GQA HQ/HK).      */
+/* Order: keys split into chunks of `chunk`; per (head, query, chunk):       */
+/*   score_i = sequential fmaf over d of (scale*q_d) * k_d from 0.0f         */
+/*   m_c = max score; e_i = exp(score_i - m_c); l_c = sum e_i (key order);   */
+/*   o_c[d] = sum_i fmaf(e_i, v_i[d], .) (key order)                         */
+/* then over visible chunks in order: M = max m_c; f_c = exp(m_c - M);       */
+/*   L = fmaf(l_c, f_c, L); O[d] = fmaf(o_c[d], f_c, O[d]); out = bf16(O/L). */
+/* kc/vc layout [HK, tmax, D].                                               */
+/* ======================================================================== */
+
+void o_attn_verify(const o_bf16* q, int S, int HQ, int HK, int D, const o_bf16* kc,
+                   const o_bf16* vc, int64_t tmax, int T, float scale, int chunk,
+                   o_bf16* out) {
+  const int G = HQ / HK;
+  const int nch = (T + chunk - 1) / chunk;
+  float* oc = (float*)malloc(sizeof(float) * (size_t)nch * D);
+  float* mc = (float*)malloc(sizeof(float) * (size_t)nch);
+  float* lc = (float*)malloc(sizeof(float) * (size_t)nch);
+  float qs[1024];
+  for (int s = 0; s < S; ++s)
+    for (int h = 0; h < HQ; ++h) {
+      const int hk = h / G;
+      const o_bf16* qh = q + ((int64_t)s * HQ + h) * D;
+      for (int d = 0; d < D; ++d) qs[d] = scale * o_bf2f(qh[d]);
+      const int last = T - S + s; /* last visible key */
+      for (int c = 0; c < nch; ++c) {
+        const int i0 = c * chunk;
+        int i1 = i0 + chunk;
+        if (i1 > last + 1) i1 = last + 1;
+        float sc[4096];
+        float mx = -INFINITY;
+        int n = 0;
+        for (int i = i0; i < i1; ++i) {
+          const o_bf16* kr = kc + ((int64_t)hk * tmax + i) * D;
+          float acc = 0.0f;
+          for (int d = 0; d < D; ++d) acc = fmaf(qs[d], o_bf2f(kr[d]), acc);
+          sc[i - i0] = acc;
+          if (acc > mx) mx = acc;
+          ++n;
+        }
+        mc[c] = mx;
+        float l = 0.0f;
+        float* o = oc + (int64_t)c * D;
+        for (int d = 0; d < D; ++d) o[d] = 0.0f;
+        for (int i = i0; i < i0 + n; ++i) {
+          const float e = o_expf(sc[i - i0] - mx);
+          l = l + e;
+          const o_bf16* vr = vc + ((int64_t)hk * tmax + i) * D;
+          for (int d = 0; d < D; ++d) o[d] = fmaf(e, o_bf2f(vr[d]), o[d]);
+        }
+        lc[c] = (n > 0) ? l : 0.0f;
+        if (n == 0) mc[c] = -INFINITY;
+      }
+      float M = -INFINITY;
+      for (int c = 0; c < nch; ++c)
+        if (lc[c] > 0.0f && mc[c] > M) M = mc[c];
+      float L = 0.0f;
+      float O[1024];
+      for (int d = 0; d < D; ++d) O[d] = 0.0f;
+      for (int c = 0; c < nch; ++c) {
+        if (!(lc[c] > 0.0f)) continue;
+        const float f = o_expf(mc[c] - M);
+        L = fmaf(lc[c], f, L);
+        for (int d = 0; d < D; ++d) O[d] = fmaf(oc[(int64_t)c * D + d], f, O[d]);
+      }
+      o_bf16* dst = out + ((int64_t)s * HQ + h) * D;
+      for (int d = 0; d < D; ++d) dst[d] = o_f2bf(O[d] / L);
+    }
+  free(oc);
+  free(mc);
+  free(lc);
+}
+
+/* a15: out[s, j] = bf16(att[s, j] * sigmoid_bf16(gate[s, j]))
+ * (FM/TrackFastKernels2.swift:478-510); att [S, width], gate = qkv[s, gate_off + j]. */
+void o_attn_gate(const o_bf16* att, const o_bf16* qkv, int S, int QW, int gate_off, int width,
+                 o_bf16* out) {
+  for (int s = 0; s < S; ++s)
+    for (int j = 0; j < width; ++j) {
+      const float a = o_bf2f(att[(int64_t)s * width + j]);
+      const float g = o_bf2f(qkv[(int64_t)s * QW + gate_off + j]);
+      out[(int64_t)s * width + j] = o_f2bf(a * o_sigmoid_bf16(g));
+    }
+}
+
+/* Row RMSNorm used around the decoder sublayers: 256 lanes, lane t squares
+ * elements t, t+256, ... (acc = fmaf(x, x, acc)); the four 64-lane waves fold
+ * by xor butterfly; total = ((w0 + w1) + w2) + w3.
+ * y = bf16(w * bf16(x * (1 / sqrtf(total / H + eps)))). */
+static float block_sum256(const float* lanes256) {
+  float w[4];
+  for (int wv = 0; wv < 4; ++wv) {
+    float lane[64];
+    memcpy(lane, lanes256 + wv * 64, sizeof(lane));
+    for (int off = 32; off >= 1; off /= 2) {
+      float nv[64];
+      for (int l = 0; l < 64; ++l) nv[l] = lane[l] + lane[l ^ off];
+      memcpy(lane, nv, sizeof(nv));
+    }
+    w[wv] = lane[0];
+  }
+  return ((w[0] + w[1]) + w[2]) + w[3];
+}
+
+void o_rmsnorm(const o_bf16* x, int M, int H, const o_bf16* w, float eps, o_bf16* y) {
+  for (int m = 0; m < M; ++m) {
+    const o_bf16* xr = x + (int64_t)m * H;
+    float lanes[256];
+    for (int t = 0; t < 256; ++t) {
+      float acc = 0.0f;
+      for (int i = t; i < H; i += 256) acc = fmaf(o_bf2f(xr[i]), o_bf2f(xr[i]), acc);
+      lanes[t] = acc;
+    }
+    const float total = block_sum256(lanes);
+    const float inv = 1.0f / sqrtf(total / (float)H + eps);
+    for (int i = 0; i < H; ++i)
+      y[(int64_t)m * H + i] = o_f2bf(o_bf2f(w[i]) * o_round_bf(o_bf2f(xr[i]) * inv));
+  }
+}
+
+/* ======================================================================== */
+/* a18 / a21: argmax and greedy acceptance                                   */
+/* Tie rule: the lowest id (Runner/Qwen4ExpMTPDrafter.swift:25-27).          */
+/* Accept rule (docs/qwen38-125b-a6b-port-notes.md:313-327): a_i = argmax of  */
+/* verify row i; n = longest prefix with drafts[i] == a_i; commit            */
+/* d_1..d_n then a_n; KV rollback index = kv_offset + n + 1 (pending + n).    */
+/* out3 = {n, bonus token, kv index}.                                        */
+/* ======================================================================== */
+
+void o_argmax_rows(const float* x, int rows, int64_t V, int32_t* out) {
+  for (int r = 0; r < rows; ++r) {
+    const float* xr = x + (int64_t)r * V;
+    int64_t b = 0;
+    for (int64_t v = 1; v < V; ++v)
+      if (xr[v] > xr[b]) b = v;
+    out[r] = (int32_t)b;
+  }
+}
+
+void o_accept_greedy(const float* logits, int k, int64_t V, const int32_t* drafts,
+                     int32_t kv_offset, int32_t* out3) {
+  int32_t a[64];
+  o_argmax_rows(logits, k + 1, V, a);
+  int n = 0;
+  while (n < k && drafts[n] == a[n]) ++n;
+  out3[0] = n;
+  out3[1] = a[n];
+  out3[2] = kv_offset + n + 1;
+}
+
+/* ======================================================================== */
+/* a22: temperature rejection sampling (Leviathan et al. 2023, Chen et al.   */
+/* 2023) with Philox4x32-10 (Salmon et al., SC'11).  No counterpart in the   */
+/* reference (it is greedy only).                                            */
+/* ======================================================================== */
+
+void o_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]) {
+  uint32_t c0 = ctr[0], c1 = ctr[1], c2 = ctr[2], c3 = ctr[3];
+  uint32_t k0 = key[0], k1 = key[1];
+  for (int r = 0; r < 10; ++r) {
+    if (r > 0) {
+      k0 += 0x9E3779B9u;
+      k1 += 0xBB67AE85u;
+    }
+    const uint64_t p0 = (uint64_t)0xD2511F53u * c0;
+    const uint64_t p1 = (uint64_t)0xCD9E8D57u * c2;
+    const uint32_t hi0 = (uint32_t)(p0 >> 32), lo0 = (uint32_t)p0;
+    const uint32_t hi1 = (uint32_t)(p1 >> 32), lo1 = (uint32_t)p1;
+    const uint32_t n0 = hi1 ^ c1 ^ k0, n1 = lo1, n2 = hi0 ^ c3 ^ k1, n3 = lo0;
+    c0 = n0;
+    c1 = n1;
+    c2 = n2;
+    c3 = n3;
+  }
+  out[0] = c0;
+  out[1] = c1;
+  out[2] = c2;
+  out[3] = c3;
+}
+
+/* top 24 bits -> [0, 1) exactly */
+float o_uniform(uint32_t r) { return (float)(r >> 8) * 5.9604644775390625e-08f; }
+
+#define O_CHUNK 1024
+/* Chunk sum: 64 lanes, lane l adds elements base+l, base+l+64, ... (16 per
+ * lane) in order from 0.0f; then an xor butterfly over 64 lanes. */
+static float chunk_sum(const float* v, int64_t base, int64_t V) {
+  float lane[64];
+  for (int l = 0; l < 64; ++l) {
+    float acc = 0.0f;
+    for (int j = 0; j < O_CHUNK / 64; ++j) {
+      const int64_t i = base + l + 64 * j;
+      if (i < V) acc = acc + v[i];
+    }
+    lane[l] = acc;
+  }
+  for (int off = 32; off >= 1; off /= 2) {
+    float nv[64];
+    for (int l = 0; l < 64; ++l) nv[l] = lane[l] + lane[l ^ off];
+    memcpy(lane, nv, sizeof(nv));
+  }
+  return lane[0];
+}
+
+/* Row total: chunk sums added in chunk order from 0.0f. */
+float o_softmax_row_sum(const float* e, int64_t V) {
+  float t = 0.0f;
+  for (int64_t b = 0; b < V; b += O_CHUNK) t = t + chunk_sum(e, b, V);
+  return t;
+}
+
+/* Inverse CDF over non-negative vals: tau = u * total; pick the first chunk
+ * whose running sum passes tau, then scan that chunk in index order against
+ * tau - (sum before the chunk).  If rounding lets the scan run off the chunk,
+ * return the chunk's last positive entry; if no chunk passes, the last
+ * positive entry overall; if every entry is 0, -1. */
+static int64_t icdf(const float* vals, int64_t V, float u) {
+  const int64_t nc = (V + O_CHUNK - 1) / O_CHUNK;
+  float* S = (float*)malloc(sizeof(float) * (size_t)nc);
+  float total = 0.0f;
+  for (int64_t c = 0; c < nc; ++c) {
+    S[c] = chunk_sum(vals, c * O_CHUNK, V);
+    total = total + S[c];
+  }
+  const float tau = u * total;
+  float cum = 0.0f;
+  int64_t res = -1;
+  for (int64_t c = 0; c < nc && res < 0; ++c) {
+    const float nxt = cum + S[c];
+    if (nxt > tau) {
+      const float t2 = tau - cum;
+      float run = 0.0f;
+      const int64_t b = c * O_CHUNK;
+      const int64_t e = (b + O_CHUNK < V) ? b + O_CHUNK : V;
+      for (int64_t i = b; i < e; ++i) {
+        run = run + vals[i];
+        if (run > t2) {
+          res = i;
+          break;
+        }
+      }
+      if (res < 0)
+        for (int64_t i = e - 1; i >= b; --i)
+          if (vals[i] > 0.0f) {
+            res = i;
+            break;
+          }
+    }
+    cum = nxt;
+  }
+  if (res < 0)
+    for (int64_t i = V - 1; i >= 0; --i)
+      if (vals[i] > 0.0f) {
+        res = i;
+        break;
+      }
+  free(S);
+  return res;
+}
+
+/* Softmax at temperature: e_v = exp((l_v - max) * (1/T)); p_v = e_v * (1/Z). */
+static void row_probs(const float* l, int64_t V, float invT, float* p) {
+  float mx = l[0];
+  for (int64_t v = 1; v < V; ++v)
+    if (l[v] > mx) mx = l[v];
+  for (int64_t v = 0; v < V; ++v) p[v] = o_expf((l[v] - mx) * invT);
+  const float invZ = 1.0f / o_softmax_row_sum(p, V);
+  for (int64_t v = 0; v < V; ++v) p[v] = p[v] * invZ;
+}
+
+/* tlogits [k+1, V]: verify rows; dlogits [k, V]: the draft distribution that
+ * proposed drafts[i] is row i.  For i = 1..k (counter {offset lo, offset hi,
+ * i, 0}, key {seed lo, seed hi}): u = U(word0), u2 = U(word1); accept draft i
+ * iff u * p_d(d_i) < p_t(d_i) (p_t from verify row i-1).  First rejection at
+ * i: token = icdf(max(0, p_t - p_d), u2) over row i-1, n = i-1.  All
+ * accepted: n = k, token = icdf(p_t row k, u2 of counter i = k+1).
+ * out3 = {n, token, kv_offset + n + 1}. */
+void o_accept_sample(const float* tlogits, const float* dlogits, int k, int64_t V,
+                     const int32_t* drafts, float temperature, uint64_t seed, uint64_t offset,
+                     int32_t kv_offset, int32_t* out3) {
+  const float invT = 1.0f / temperature;
+  float* pt = (float*)malloc(sizeof(float) * (size_t)V);
+  float* pd = (float*)malloc(sizeof(float) * (size_t)V);
+  const uint32_t key[2] = {(uint32_t)seed, (uint32_t)(seed >> 32)};
+  int n = 0;
+  int64_t tok = -1;
+  for (int i = 1; i <= k + 1; ++i) {
+    uint32_t ctr[4] = {(uint32_t)offset, (uint32_t)(offset >> 32), (uint32_t)i, 0u};
+    uint32_t rnd[4];
+    o_philox4x32_10(ctr, key, rnd);
+    const float u = o_uniform(rnd[0]), u2 = o_uniform(rnd[1]);
+    row_probs(tlogits + (int64_t)(i - 1) * V, V, invT, pt);
+    if (i == k + 1) {
+      n = k;
+      tok = icdf(pt, V, u2);
+      if (tok < 0) {
+        int32_t a;
+        o_argmax_rows(tlogits + (int64_t)k * V, 1, V, &a);
+        tok = a;
+      }
+      break;
+    }
+    row_probs(dlogits + (int64_t)(i - 1) * V, V, invT, pd);
+    const int32_t d = drafts[i - 1];
+    if (u * pd[d] < pt[d]) continue;
+    n = i - 1;
+    for (int64_t v = 0; v < V; ++v) pd[v] = fmaxf(pt[v] - pd[v], 0.0f);
+    tok = icdf(pd, V, u2);
+    if (tok < 0) {
+      int32_t a;
+      o_argmax_rows(tlogits + (int64_t)(i - 1) * V, 1, V, &a);
+      tok = a;
+    }
+    break;
+  }
+  out3[0] = n;
+  out3[1] = (int32_t)tok;
+  out3[2] = kv_offset + n + 1;
+  free(pt);
+  free(pd);
+}

@@ -1,0 +1,280 @@
+"""ctypes binding of the CPU oracle (liboracle.so) -- TEST INFRASTRUCTURE ONLY.
+
+Only tests/, ``__graft_entry__.smoke()`` and bench.py's cpu_baseline leg import
+this module.  bf16 arrays are numpy ``uint16`` bit patterns.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB = None
+
+
+def build() -> str:
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+    return os.path.join(_HERE, "liboracle.so")
+
+
+def lib():
+    global _LIB
+    if _LIB is None:
+        path = os.path.join(_HERE, "liboracle.so")
+        if not os.path.exists(path):
+            build()
+        _LIB = C.CDLL(path)
+        _declare(_LIB)
+    return _LIB
+
+
+P = C.c_void_p
+I32, I64, U64, F32, F64 = C.c_int32, C.c_int64, C.c_uint64, C.c_float, C.c_double
+
+
+def _declare(L):
+    sig = {
+        "o_bf2f": (F32, [C.c_uint16]),
+        "o_f2bf": (C.c_uint16, [F32]),
+        "o_expf": (F32, [F32]),
+        "o_sigmoid_bf16": (F32, [F32]),
+        "o_silu_bf16": (F32, [F32]),
+        "o_lanes_for_blocks": (C.c_int, [C.c_int]),
+        "o_affine_quantize": (None, [P, I64, C.c_int, C.c_int, P, P, P]),
+        "o_qmv": (None, [P, P, P, I64, C.c_int, C.c_int, P, C.c_int, P, P]),
+        "o_xblock": (None, [P, P, P]),
+        "o_router_gemv": (None, [P, C.c_int, C.c_int, P, C.c_int, P]),
+        "o_topk_softmax": (None, [P, C.c_int, C.c_int, C.c_int, P, P]),
+        "o_moe_block": (None, [P, P, C.c_int, P, P, P, P, P, P]),
+        "o_rope_table": (None, [C.c_int, C.c_int, F64, P, P]),
+        "o_attn_prep": (None, [P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, P, P,
+                               F32, P, P, C.c_int, P, P, P]),
+        "o_attn_verify": (None, [P, C.c_int, C.c_int, C.c_int, C.c_int, P, P, I64, C.c_int,
+                                 F32, C.c_int, P]),
+        "o_attn_gate": (None, [P, P, C.c_int, C.c_int, C.c_int, C.c_int, P]),
+        "o_rmsnorm": (None, [P, C.c_int, C.c_int, P, F32, P]),
+        "o_argmax_rows": (None, [P, C.c_int, I64, P]),
+        "o_accept_greedy": (None, [P, C.c_int, I64, P, I32, P]),
+        "o_philox4x32_10": (None, [P, P, P]),
+        "o_uniform": (F32, [C.c_uint32]),
+        "o_accept_sample": (None, [P, P, C.c_int, I64, P, F32, U64, U64, I32, P]),
+        "o_softmax_row_sum": (F32, [P, I64]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+
+
+def _p(a: np.ndarray):
+    assert a.flags.c_contiguous
+    return a.ctypes.data_as(P)
+
+
+# --------------------------------------------------------------------------- bf16 helpers
+def f32_to_bf16(x) -> np.ndarray:
+    """Round-to-nearest-even float32 -> bf16 bit patterns (uint16)."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    r[nan] = 0x7FC0
+    return r
+
+
+def bf16_to_f32(h) -> np.ndarray:
+    return (np.ascontiguousarray(h, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+# --------------------------------------------------------------------------- wrappers
+def expf(x: float) -> float:
+    return lib().o_expf(x)
+
+
+def lanes_for_blocks(nb: int) -> int:
+    return lib().o_lanes_for_blocks(nb)
+
+
+def affine_quantize(w_bf16: np.ndarray, gs: int):
+    w = np.ascontiguousarray(w_bf16, dtype=np.uint16)
+    K = w.shape[-1]
+    rows = w.size // K
+    wq = np.zeros(w.shape[:-1] + (K // 8,), np.uint32)
+    s = np.zeros(w.shape[:-1] + (K // gs,), np.uint16)
+    b = np.zeros_like(s)
+    lib().o_affine_quantize(_p(w), rows, K, gs, _p(wq), _p(s), _p(b))
+    return wq, s, b
+
+
+def dequantize(wq, s, b, gs) -> np.ndarray:
+    """float64 dequantisation s*q + b (exact); test helper."""
+    wq = np.asarray(wq, np.uint32)
+    K = wq.shape[-1] * 8
+    q = ((wq[..., None] >> (4 * np.arange(8, dtype=np.uint32))) & 0xF).reshape(wq.shape[:-1] + (K,))
+    sf = np.repeat(bf16_to_f32(s).astype(np.float64), gs, axis=-1)
+    bf = np.repeat(bf16_to_f32(b).astype(np.float64), gs, axis=-1)
+    return sf * q + bf
+
+
+def qmv(wq, s, b, gs, x_bf16):
+    wq = np.ascontiguousarray(wq, np.uint32)
+    s = np.ascontiguousarray(s, np.uint16)
+    b = np.ascontiguousarray(b, np.uint16)
+    x = np.ascontiguousarray(x_bf16, np.uint16)
+    K = x.shape[-1]
+    M = x.size // K
+    N = wq.size // (K // 8)
+    y = np.zeros((M, N), np.uint16)
+    yf = np.zeros((M, N), np.float32)
+    lib().o_qmv(_p(wq), _p(s), _p(b), N, K, gs, _p(x), M, _p(y), _p(yf))
+    return y, yf
+
+
+def xblock(x32):
+    x = np.ascontiguousarray(x32, np.uint16)
+    m = np.zeros(32, np.int32)
+    E = np.zeros(1, np.int32)
+    lib().o_xblock(_p(x), _p(m), _p(E))
+    return m, int(E[0])
+
+
+def router_gemv(W_bf16, x_f32):
+    W = np.ascontiguousarray(W_bf16, np.uint16)
+    x = np.ascontiguousarray(x_f32, np.float32)
+    H = W.shape[-1]
+    rows = W.size // H
+    M = x.size // H
+    out = np.zeros((M, rows), np.float32)
+    lib().o_router_gemv(_p(W), rows, H, _p(x), M, _p(out))
+    return out
+
+
+def topk_softmax(logits, K):
+    lg = np.ascontiguousarray(logits, np.float32)
+    M, E = lg.shape
+    idx = np.zeros((M, K), np.int32)
+    w = np.zeros((M, K), np.float32)
+    lib().o_topk_softmax(_p(lg), M, E, K, _p(idx), _p(w))
+    return idx, w
+
+
+class MoEWeightsStruct(C.Structure):
+    _fields_ = [("H", C.c_int), ("E", C.c_int), ("K", C.c_int), ("F", C.c_int), ("gs", C.c_int)] + [
+        (n, P) for n in [
+            "router", "shared_gate",
+            "gate_w", "gate_s", "gate_b", "up_w", "up_s", "up_b", "down_w", "down_s", "down_b",
+            "sh_gate_w", "sh_gate_s", "sh_gate_b", "sh_up_w", "sh_up_s", "sh_up_b",
+            "sh_down_w", "sh_down_s", "sh_down_b"]]
+
+
+def moe_block(w: dict, x_bf16, H, E, K, F, gs):
+    """w: dict of numpy arrays named like MoEWeightsStruct fields."""
+    st = MoEWeightsStruct(H, E, K, F, gs)
+    keep = {}
+    for name, _ in MoEWeightsStruct._fields_[5:]:
+        a = np.ascontiguousarray(w[name])
+        keep[name] = a
+        setattr(st, name, a.ctypes.data)
+    x = np.ascontiguousarray(x_bf16, np.uint16)
+    M = x.shape[0]
+    y = np.zeros((M, H), np.uint16)
+    idx = np.zeros((M, K), np.int32)
+    wk = np.zeros((M, K), np.float32)
+    logits = np.zeros((M, E), np.float32)
+    gate = np.zeros(M, np.uint16)
+    act = np.zeros((M * (K + 1), F), np.uint16)
+    lib().o_moe_block(C.byref(st), _p(x), M, _p(y), _p(idx), _p(wk), _p(logits), _p(gate), _p(act))
+    return dict(y=y, idx=idx, w=wk, logits=logits, gate=gate, act=act)
+
+
+def rope_table(positions, rot, theta):
+    c = np.zeros((positions, rot), np.uint16)
+    s = np.zeros((positions, rot), np.uint16)
+    lib().o_rope_table(positions, rot, theta, _p(c), _p(s))
+    return c, s
+
+
+def attn_prep(qkv, HQ, HK, D, ROT, qnorm, knorm, eps, cos_t, sin_t, pos0):
+    qkv = np.ascontiguousarray(qkv, np.uint16)
+    S, QW = qkv.shape
+    q = np.zeros((S, HQ, D), np.uint16)
+    k = np.zeros((S, HK, D), np.uint16)
+    v = np.zeros((S, HK, D), np.uint16)
+    lib().o_attn_prep(_p(qkv), S, QW, HQ, HK, D, ROT, _p(np.ascontiguousarray(qnorm, np.uint16)),
+                      _p(np.ascontiguousarray(knorm, np.uint16)), eps,
+                      _p(np.ascontiguousarray(cos_t, np.uint16)),
+                      _p(np.ascontiguousarray(sin_t, np.uint16)), pos0, _p(q), _p(k), _p(v))
+    return q, k, v
+
+
+def attn_verify(q, kc, vc, T, scale, chunk):
+    q = np.ascontiguousarray(q, np.uint16)
+    S, HQ, D = q.shape
+    HK, tmax, _ = kc.shape
+    out = np.zeros((S, HQ, D), np.uint16)
+    lib().o_attn_verify(_p(q), S, HQ, HK, D, _p(np.ascontiguousarray(kc, np.uint16)),
+                        _p(np.ascontiguousarray(vc, np.uint16)), tmax, T, scale, chunk, _p(out))
+    return out
+
+
+def attn_gate(att, qkv, gate_off):
+    att = np.ascontiguousarray(att, np.uint16)
+    qkv = np.ascontiguousarray(qkv, np.uint16)
+    S, width = att.shape
+    out = np.zeros_like(att)
+    lib().o_attn_gate(_p(att), _p(qkv), S, qkv.shape[1], gate_off, width, _p(out))
+    return out
+
+
+def rmsnorm(x, w, eps):
+    x = np.ascontiguousarray(x, np.uint16)
+    M, H = x.shape
+    y = np.zeros_like(x)
+    lib().o_rmsnorm(_p(x), M, H, _p(np.ascontiguousarray(w, np.uint16)), eps, _p(y))
+    return y
+
+
+def argmax_rows(x):
+    x = np.ascontiguousarray(x, np.float32)
+    rows, V = x.shape
+    out = np.zeros(rows, np.int32)
+    lib().o_argmax_rows(_p(x), rows, V, _p(out))
+    return out
+
+
+def accept_greedy(logits, drafts, kv_offset):
+    lg = np.ascontiguousarray(logits, np.float32)
+    d = np.ascontiguousarray(drafts, np.int32)
+    k = d.size
+    out = np.zeros(3, np.int32)
+    lib().o_accept_greedy(_p(lg), k, lg.shape[1], _p(d), kv_offset, _p(out))
+    return out
+
+
+def philox(ctr, key):
+    c = np.ascontiguousarray(ctr, np.uint32)
+    k = np.ascontiguousarray(key, np.uint32)
+    out = np.zeros(4, np.uint32)
+    lib().o_philox4x32_10(_p(c), _p(k), _p(out))
+    return out
+
+
+def uniform(r: int) -> float:
+    return lib().o_uniform(r)
+
+
+def accept_sample(tlogits, dlogits, drafts, temperature, seed, offset, kv_offset):
+    t = np.ascontiguousarray(tlogits, np.float32)
+    dl = np.ascontiguousarray(dlogits, np.float32)
+    d = np.ascontiguousarray(drafts, np.int32)
+    out = np.zeros(3, np.int32)
+    lib().o_accept_sample(_p(t), _p(dl), d.size, t.shape[1], _p(d), temperature, seed, offset,
+                          kv_offset, _p(out))
+    return out
+
+
+def softmax_row_sum(e):
+    e = np.ascontiguousarray(e, np.float32)
+    return lib().o_softmax_row_sum(_p(e), e.size)

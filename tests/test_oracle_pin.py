@@ -1,0 +1,425 @@
+"""Pins the CPU oracle independently of the GPU.
+
+Each oracle function is checked against something that does not share its
+code: float64 brute force on small inputs, torch's bf16 rounding, libm's exp,
+closed forms and hand-computed known answers, the published Philox4x32-10
+known-answer vectors, and distributional properties of speculative sampling.
+A plausible slip (dropped bias term, wrong nibble order, transposed operand,
+off-by-one in the accept prefix) fails at least one of these.
+"""
+import math
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+
+
+def rng(seed=0):
+    return np.random.default_rng(seed)
+
+
+def bf16(x):
+    return O.f32_to_bf16(np.asarray(x, np.float32))
+
+
+def f32(h):
+    return O.bf16_to_f32(h)
+
+
+# ---------------------------------------------------------------------------- scalars
+def test_bf16_rounding_matches_torch():
+    import torch
+
+    r = rng(1)
+    x = np.concatenate([
+        r.standard_normal(20000).astype(np.float32) * np.float32(10.0) ** r.integers(-30, 30, 20000),
+        np.array([0.0, -0.0, 1.0, 1.00390625, 1.01171875, 65504.0, 3.3895314e38, 1e-40], np.float32),
+    ]).astype(np.float32)
+    want = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(O.f32_to_bf16(x), want)
+    lib = O.lib()
+    for v in x[:2000]:
+        assert lib.o_f2bf(float(v)) == O.f32_to_bf16(np.array([v], np.float32))[0]
+
+
+def test_expf_within_2ulp_of_libm():
+    xs = np.concatenate([np.linspace(-87.0, 88.5, 40001), rng(2).uniform(-20, 20, 20000)]).astype(np.float32)
+    lib = O.lib()
+    got = np.array([lib.o_expf(float(v)) for v in xs], np.float32)
+    want = np.exp(xs.astype(np.float64)).astype(np.float32)
+    ulp = np.abs(got.view(np.int32).astype(np.int64) - want.view(np.int32).astype(np.int64))
+    assert ulp.max() <= 2, ulp.max()
+    assert lib.o_expf(0.0) == 1.0
+    assert lib.o_expf(-100.0) == 0.0
+    assert math.isinf(lib.o_expf(100.0))
+
+
+def test_sigmoid_silu_bf16_close_to_float64():
+    lib = O.lib()
+    xs = f32(bf16(np.linspace(-12, 12, 3001)))
+    for x in xs:
+        s = lib.o_sigmoid_bf16(float(x))
+        ref = 1.0 / (1.0 + math.exp(-float(x)))
+        # four bf16 roundings (exp, 1+e, 1/d, 1-y): within 4 bf16 ulps
+        assert abs(s - ref) <= 2 ** -6 * max(abs(ref), 2 ** -7), (x, s, ref)
+        si = lib.o_silu_bf16(float(x))
+        assert abs(si - x * ref) <= 2 ** -5 * abs(x * ref) + 1e-6, (x, si)
+
+
+# ---------------------------------------------------------------------------- a1 quantize
+def test_quantize_known_answer():
+    # a group of 0, 1/15, ..., 1 (twice): mask false (|min| < |max|), edge = max = 1,
+    # scale = (1-0)/15 negated -> q0 = rint(1/scale) = -15, scale = 1/-15, bias = 1,
+    # q_j = rint((w_j - 1) / scale) = 15 - j.
+    w = np.tile(np.arange(16, dtype=np.float64) / 15.0, 2)
+    wb = bf16(w.astype(np.float32)).reshape(1, 32)
+    wq, s, b = O.affine_quantize(wb, 32)
+    q = ((wq[0][:, None] >> (4 * np.arange(8, dtype=np.uint32))) & 0xF).reshape(-1)
+    wv = f32(wb[0]).astype(np.float64)
+    expect_q = np.rint((wv - 1.0) / np.float32(1.0 / -15.0)).clip(0, 15)
+    assert np.array_equal(q, expect_q)
+    assert np.array_equal(q[:16], 15 - np.arange(16))
+    assert f32(b)[0, 0] == 1.0
+    assert f32(s)[0, 0] == f32(bf16(np.float32(1.0) / np.float32(-15.0)))
+
+
+@pytest.mark.parametrize("gs", [32, 64])
+def test_quantize_invariants(gs):
+    r = rng(3)
+    w = bf16(r.standard_normal((64, 256)).astype(np.float32) * 0.02)
+    wq, s, b = O.affine_quantize(w, gs)
+    deq = O.dequantize(wq, s, b, gs)
+    wf = f32(w).astype(np.float64).reshape(64, 256)
+    sc = np.repeat(np.abs(f32(s).astype(np.float64)), gs, axis=-1)
+    bb = np.repeat(np.abs(f32(b).astype(np.float64)), gs, axis=-1)
+    # round trip: within one step (the snapped scale can clip the far end of the
+    # range), within half a step for the bulk, plus the bf16 rounding of s and b
+    err = np.abs(deq - wf)
+    slack = 15 * sc * 2 ** -8 + bb * 2 ** -8 + 1e-12
+    assert np.all(err <= sc + slack)
+    assert np.mean(err <= 0.5 * sc + slack) > 0.97
+    q = ((wq[..., None] >> (4 * np.arange(8, dtype=np.uint32))) & 0xF).reshape(64, 256)
+    assert q.max() <= 15
+    # the group's edge value (bf16 already) is stored as the bias and reconstructs exactly
+    gsz = wf.reshape(64, -1, gs)
+    mx, mn = gsz.max(-1), gsz.min(-1)
+    edge = np.where(np.abs(mn) > np.abs(mx), mn, mx)
+    assert np.array_equal(f32(b).astype(np.float64), edge)
+    # an independent vectorised restatement of the MLX algorithm gives the same bits
+    g = wf.reshape(64, -1, gs).astype(np.float32)
+    wmax, wmin = g.max(-1), g.min(-1)
+    mask = np.abs(wmin) > np.abs(wmax)
+    scale = np.maximum((wmax - wmin) / np.float32(15), np.float32(1e-7)).astype(np.float32)
+    scale = np.where(mask, scale, -scale).astype(np.float32)
+    edge = np.where(mask, wmin, wmax).astype(np.float32)
+    q0 = np.rint(edge / scale)
+    scale = np.where(q0 != 0, edge / np.where(q0 == 0, 1, q0), scale).astype(np.float32)
+    bias = np.where(q0 == 0, 0, edge).astype(np.float32)
+    qq = np.clip(np.rint((g - bias[..., None]) / scale[..., None]), 0, 15).astype(np.uint32)
+    words = (qq.reshape(64, -1, 8) << (4 * np.arange(8, dtype=np.uint32))).sum(-1).astype(np.uint32)
+    assert np.array_equal(words.reshape(wq.shape), wq)
+    assert np.array_equal(bf16(scale), s)
+    assert np.array_equal(bf16(bias), b)
+
+
+# ---------------------------------------------------------------------------- a2-a4 GEMV
+def test_xblock_is_exact_fixed_point():
+    r = rng(4)
+    for trial in range(200):
+        x = bf16(r.standard_normal(32).astype(np.float32) * np.float32(2.0) ** r.integers(-20, 20, 32))
+        m, E = O.xblock(x)
+        p = 2.0 ** (E - 149)
+        xv = f32(x).astype(np.float64)
+        # exact for every element within 2^15 of the block maximum, truncated toward zero below
+        big = np.abs(xv) >= np.abs(xv).max() * 2.0 ** -14
+        assert np.array_equal(m[big] * p, xv[big])
+        assert np.all(np.abs(m * p) <= np.abs(xv))
+        assert np.all(np.abs(xv - m * p) < 2.0 ** (E - 149) + 1e-300)
+        assert np.abs(m).max() < 2 ** 23
+
+
+@pytest.mark.parametrize("K,gs,M", [(256, 32, 1), (640, 64, 3), (768, 64, 2), (2048, 32, 1), (96, 32, 4)])
+def test_qmv_matches_float64_dequant_matmul(K, gs, M):
+    r = rng(K + gs + M)
+    N = 48
+    w = bf16(r.standard_normal((N, K)).astype(np.float32) * 0.02)
+    wq, s, b = O.affine_quantize(w, gs)
+    x = bf16(r.standard_normal((M, K)).astype(np.float32))
+    y, yf = O.qmv(wq, s, b, gs, x)
+    W = O.dequantize(wq, s, b, gs)
+    X = f32(x).astype(np.float64)
+    ref = X @ W.T
+    mag = np.abs(X) @ np.abs(W).T
+    assert np.all(np.abs(yf - ref) <= 1e-6 * mag + 1e-30)
+    assert np.array_equal(y, bf16(yf))
+
+
+def test_qmv_rows_are_independent():
+    r = rng(7)
+    K, gs = 512, 64
+    w = bf16(r.standard_normal((40, K)).astype(np.float32) * 0.02)
+    wq, s, b = O.affine_quantize(w, gs)
+    x = bf16(r.standard_normal((3, K)).astype(np.float32))
+    y, _ = O.qmv(wq, s, b, gs, x)
+    # row concatenation and per-row M splitting are bit-neutral
+    ya, _ = O.qmv(wq[:17], s[:17], b[:17], gs, x)
+    yb, _ = O.qmv(wq[17:], s[17:], b[17:], gs, x)
+    assert np.array_equal(np.concatenate([ya, yb], 1), y)
+    for m in range(3):
+        ym, _ = O.qmv(wq, s, b, gs, x[m:m + 1])
+        assert np.array_equal(ym[0], y[m])
+
+
+def test_lanes_rule():
+    assert [O.lanes_for_blocks(n) for n in (1, 7, 8, 10, 20, 24, 64, 80, 192, 320, 1000)] == \
+        [1, 1, 2, 2, 4, 4, 16, 16, 32, 64, 64]
+
+
+# ---------------------------------------------------------------------------- router
+def test_router_gemv_matches_float64():
+    r = rng(8)
+    E, H, M = 96, 1024, 3
+    W = bf16(r.standard_normal((E, H)).astype(np.float32) * 0.02)
+    x = r.standard_normal((M, H)).astype(np.float32)
+    out = O.router_gemv(W, x)
+    Wf = f32(W).astype(np.float64).reshape(E, H)
+    ref = x.astype(np.float64) @ Wf.T
+    mag = np.abs(x.astype(np.float64)) @ np.abs(Wf).T
+    assert np.all(np.abs(out - ref) <= 2e-6 * mag)
+
+
+def test_topk_softmax_rule_and_ties():
+    r = rng(9)
+    lg = r.standard_normal((5, 64)).astype(np.float32)
+    lg[0, [3, 7, 9, 40]] = 5.0  # a four-way tie at the top
+    lg[1, :] = 1.0              # all equal
+    idx, w = O.topk_softmax(lg, 8)
+    for m in range(5):
+        order = np.lexsort((np.arange(64), -lg[m]))[:8]
+        assert np.array_equal(idx[m], order)
+        v = lg[m, order].astype(np.float64)
+        e = np.exp(v - v.max())
+        assert np.allclose(w[m], e / e.sum(), rtol=2e-6, atol=0)
+    assert list(idx[0, :4]) == [3, 7, 9, 40]
+    assert list(idx[1]) == list(range(8))
+
+
+# ---------------------------------------------------------------------------- MoE block
+def _moe_weights(r, H, E, K, F, gs):
+    def q(shape):
+        w = bf16(r.standard_normal(shape).astype(np.float32) * 0.02)
+        return O.affine_quantize(w, gs)
+    gw, gsc, gb = q((E, F, H))
+    uw, usc, ub = q((E, F, H))
+    dw, dsc, db = q((E, H, F))
+    sgw, sgs, sgb = q((F, H))
+    suw, sus, sub = q((F, H))
+    sdw, sds, sdb = q((H, F))
+    return dict(
+        router=bf16(r.standard_normal((E, H)).astype(np.float32) * 0.02),
+        shared_gate=bf16(r.standard_normal(H).astype(np.float32) * 0.02),
+        gate_w=gw, gate_s=gsc, gate_b=gb, up_w=uw, up_s=usc, up_b=ub, down_w=dw, down_s=dsc, down_b=db,
+        sh_gate_w=sgw, sh_gate_s=sgs, sh_gate_b=sgb, sh_up_w=suw, sh_up_s=sus, sh_up_b=sub,
+        sh_down_w=sdw, sh_down_s=sds, sh_down_b=sdb)
+
+
+def test_moe_block_matches_float64_textbook():
+    H, E, K, F, gs, M = 256, 16, 4, 128, 64, 3
+    r = rng(10)
+    w = _moe_weights(r, H, E, K, F, gs)
+    x = bf16(r.standard_normal((M, H)).astype(np.float32))
+    out = O.moe_block(w, x, H, E, K, F, gs)
+    X = f32(x).astype(np.float64)
+    R = f32(w["router"]).astype(np.float64).reshape(E, H)
+    logits = X @ R.T
+    assert np.allclose(out["logits"], logits, rtol=0, atol=1e-5)
+    G = O.dequantize(w["gate_w"], w["gate_s"], w["gate_b"], gs)
+    U = O.dequantize(w["up_w"], w["up_s"], w["up_b"], gs)
+    Dn = O.dequantize(w["down_w"], w["down_s"], w["down_b"], gs)
+    SG = O.dequantize(w["sh_gate_w"], w["sh_gate_s"], w["sh_gate_b"], gs)
+    SU = O.dequantize(w["sh_up_w"], w["sh_up_s"], w["sh_up_b"], gs)
+    SD = O.dequantize(w["sh_down_w"], w["sh_down_s"], w["sh_down_b"], gs)
+    sgate = f32(w["shared_gate"]).astype(np.float64)
+    silu = lambda v: v / (1 + np.exp(-v))
+    for m in range(M):
+        order = np.argsort(-logits[m], kind="stable")[:K]
+        assert np.array_equal(np.sort(out["idx"][m]), np.sort(order))
+        v = logits[m, order]
+        p = np.exp(v - v.max()); p /= p.sum()
+        y = np.zeros(H)
+        for k, e in enumerate(order):
+            a = silu(G[e] @ X[m]) * (U[e] @ X[m])
+            y += p[k] * (Dn[e] @ a)
+        a = silu(SG @ X[m]) * (SU @ X[m])
+        g = 1 / (1 + np.exp(-(sgate @ X[m])))
+        y += g * (SD @ a)
+        got = f32(out["y"][m]).astype(np.float64)
+        assert np.linalg.norm(got - y) <= 2e-2 * np.linalg.norm(y), np.linalg.norm(got - y) / np.linalg.norm(y)
+
+
+# ---------------------------------------------------------------------------- attention
+def test_rope_table_against_numpy():
+    c, s = O.rope_table(64, 16, 1e7)
+    half = 8
+    i = np.arange(16) % half
+    inv = 1e7 ** (-2.0 * i / 16)
+    ang = np.arange(64)[:, None] * inv[None, :]
+    assert np.max(np.abs(f32(c) - np.cos(ang))) <= 2 ** -8
+    assert np.max(np.abs(f32(s) - np.sin(ang))) <= 2 ** -8
+
+
+def test_attn_prep_matches_float64():
+    r = rng(11)
+    S, HQ, HK, D, ROT = 3, 4, 2, 64, 16
+    QW = 2 * HQ * D + 2 * HK * D + 8
+    qkv = bf16(r.standard_normal((S, QW)).astype(np.float32))
+    qn = bf16(1 + 0.1 * r.standard_normal(D).astype(np.float32))
+    kn = bf16(1 + 0.1 * r.standard_normal(D).astype(np.float32))
+    c, s = O.rope_table(32, ROT, 1e7)
+    q, k, v = O.attn_prep(qkv, HQ, HK, D, ROT, qn, kn, 1e-6, c, s, 5)
+    X = f32(qkv).astype(np.float64)
+
+    def ref(vec, wn, pos):
+        y = vec / np.sqrt(np.mean(vec ** 2) + 1e-6) * f32(wn)
+        cc, ss = f32(c[pos]).astype(np.float64), f32(s[pos]).astype(np.float64)
+        o = y.copy()
+        h = ROT // 2
+        o[:h] = y[:h] * cc[:h] - y[h:ROT] * ss[:h]
+        o[h:ROT] = y[h:ROT] * cc[h:ROT] + y[:h] * ss[h:ROT]
+        return o
+
+    for si in range(S):
+        for h in range(HQ):
+            want = ref(X[si, h * D:(h + 1) * D], qn, 5 + si)
+            assert np.max(np.abs(f32(q[si, h]) - want)) <= 3e-2 * np.max(np.abs(want))
+        for h in range(HK):
+            off = 2 * HQ * D
+            want = ref(X[si, off + h * D: off + (h + 1) * D], kn, 5 + si)
+            assert np.max(np.abs(f32(k[si, h]) - want)) <= 3e-2 * np.max(np.abs(want))
+            assert np.array_equal(v[si, h], qkv[si, off + HK * D + h * D: off + HK * D + (h + 1) * D])
+
+
+@pytest.mark.parametrize("T,S,chunk", [(1, 1, 32), (33, 2, 32), (70, 4, 16), (40, 6, 64)])
+def test_attn_verify_matches_float64(T, S, chunk):
+    r = rng(T * 10 + S)
+    HQ, HK, D, tmax = 6, 2, 64, 128
+    q = bf16(r.standard_normal((S, HQ, D)).astype(np.float32))
+    kc = bf16(r.standard_normal((HK, tmax, D)).astype(np.float32))
+    vc = bf16(r.standard_normal((HK, tmax, D)).astype(np.float32))
+    scale = D ** -0.5
+    out = O.attn_verify(q, kc, vc, T, scale, chunk)
+    Q, Kf, Vf = (f32(a).astype(np.float64) for a in (q, kc, vc))
+    for s in range(S):
+        for h in range(HQ):
+            hk = h // (HQ // HK)
+            last = T - S + s
+            sc = Kf[hk, :last + 1] @ Q[s, h] * scale
+            p = np.exp(sc - sc.max()); p /= p.sum()
+            want = p @ Vf[hk, :last + 1]
+            assert np.max(np.abs(f32(out[s, h]) - want)) <= 1e-2 * max(1.0, np.max(np.abs(want)))
+
+
+def test_attn_gate_closed_form():
+    r = rng(12)
+    att = bf16(r.standard_normal((2, 32)).astype(np.float32))
+    qkv = bf16(r.standard_normal((2, 80)).astype(np.float32))
+    out = O.attn_gate(att, qkv, 10)
+    g = f32(qkv[:, 10:42]).astype(np.float64)
+    want = f32(att) * (1 / (1 + np.exp(-g)))
+    assert np.max(np.abs(f32(out) - want)) <= 2 ** -6 * np.max(np.abs(want))
+
+
+def test_rmsnorm_matches_float64():
+    r = rng(13)
+    x = bf16(r.standard_normal((3, 640)).astype(np.float32) * 3)
+    w = bf16(1 + 0.1 * r.standard_normal(640).astype(np.float32))
+    y = O.rmsnorm(x, w, 1e-6)
+    X = f32(x).astype(np.float64)
+    want = X / np.sqrt(np.mean(X ** 2, axis=1, keepdims=True) + 1e-6) * f32(w)
+    assert np.max(np.abs(f32(y) - want)) <= 2 ** -6 * np.max(np.abs(want))
+
+
+# ---------------------------------------------------------------------------- acceptance
+def test_greedy_accept_known_answers():
+    V = 10
+    def rows(args):
+        lg = np.zeros((len(args), V), np.float32)
+        for i, a in enumerate(args):
+            lg[i, a] = 1.0
+        return lg
+    # all accepted: n = k, bonus = argmax of the last row
+    assert list(O.accept_greedy(rows([1, 2, 3, 4]), [1, 2, 3], 100)) == [3, 4, 104]
+    # first rejected: commit a_0
+    assert list(O.accept_greedy(rows([1, 2, 3, 4]), [5, 2, 3], 100)) == [0, 1, 101]
+    # mid rejection
+    assert list(O.accept_greedy(rows([1, 2, 3, 4]), [1, 2, 9], 7)) == [2, 3, 10]
+    # ties resolve to the lowest id on the target side
+    lg = rows([1, 2])
+    lg[0, 6] = 1.0
+    assert list(O.accept_greedy(lg, [6], 0)) == [0, 1, 1]
+    assert list(O.accept_greedy(lg, [1], 0)) == [1, 2, 2]
+
+
+def test_philox_known_answer_vectors():
+    # Random123 philox4x32_10 known-answer vectors (Salmon et al., SC'11).
+    kat = [
+        ([0, 0, 0, 0], [0, 0], [0x6627E8D5, 0xE169C58D, 0xBC57AC4C, 0x9B00DBD8]),
+        ([0xFFFFFFFF] * 4, [0xFFFFFFFF] * 2, [0x408F276D, 0x41C83B0E, 0xA20BC7C6, 0x6D5451FD]),
+        ([0x243F6A88, 0x85A308D3, 0x13198A2E, 0x03707344], [0xA4093822, 0x299F31D0],
+         [0xD16CFE09, 0x94FDCCEB, 0x5001E420, 0x24126EA1]),
+    ]
+    for ctr, key, want in kat:
+        assert [int(v) for v in O.philox(ctr, key)] == want
+
+
+def test_uniform_mapping():
+    assert O.uniform(0) == 0.0
+    assert O.uniform(0xFFFFFFFF) == 1.0 - 2.0 ** -24
+    assert O.uniform(0x80000000) == 0.5
+
+
+def test_sample_identical_distributions_always_accept():
+    r = rng(14)
+    V, k = 64, 3
+    t = (r.standard_normal((k + 1, V)) * 2).astype(np.float32)
+    d = t[:k].copy()
+    for off in range(40):
+        drafts = r.integers(0, V, k).astype(np.int32)
+        out = O.accept_sample(t, d, drafts, 0.7, 1234, off, 50)
+        assert out[0] == k and out[2] == 50 + k + 1
+
+
+def test_sample_disjoint_support_always_rejects():
+    V, k = 32, 2
+    t = np.full((k + 1, V), -200.0, np.float32)
+    t[:, :8] = 0.0  # target mass on ids 0..7
+    d = np.full((k, V), -200.0, np.float32)
+    d[:, 16:] = 0.0  # draft mass on ids 16..31
+    for off in range(30):
+        out = O.accept_sample(t, d, np.array([20, 21], np.int32), 0.7, 99, off, 0)
+        assert out[0] == 0 and 0 <= out[1] < 8 and out[2] == 1
+
+
+def test_sample_emits_target_distribution():
+    """Speculative sampling is exact: the first emitted token ~ p_target (chi-square)."""
+    V, T = 6, 0.7
+    r = rng(15)
+    t = (r.standard_normal((2, V)) * 1.5).astype(np.float32)
+    d = (r.standard_normal((1, V)) * 1.5).astype(np.float32)
+    pt = np.exp((t[0] - t[0].max()) / T); pt /= pt.sum()
+    pd = np.exp((d[0] - d[0].max()) / T); pd /= pd.sum()
+    counts = np.zeros(V)
+    n = 6000
+    dr = r.choice(V, size=n, p=pd).astype(np.int32)
+    for i in range(n):
+        out = O.accept_sample(t, d, dr[i:i + 1], T, 777, i, 0)
+        first = dr[i] if out[0] == 1 else out[1]
+        counts[first] += 1
+    chi2 = ((counts - n * pt) ** 2 / (n * pt)).sum()
+    assert chi2 < 25.0, (chi2, counts, n * pt)  # 5 dof, p ~ 1e-4
+
+
+def test_softmax_row_sum_close_to_fsum():
+    e = rng(16).random(151936).astype(np.float32)
+    assert abs(O.softmax_row_sum(e) - math.fsum(e.astype(np.float64))) <= 1e-6 * e.sum()

@@ -1,0 +1,210 @@
+/*
+ * mtpx -- MI355X (gfx950) single-stream MTP speculative-decode step for the
+ * Qwen3.8-125B-A6B affine-4-bit MoE.  C ABI.
+ *
+ * Conventions (mirroring the mlx-c C ABI the reference's kernels bottom out in,
+ * Vendor/mlx-swift/Source/Cmlx/mlx-c/mlx/c/fast.h:145-161, error.h:15-27):
+ *   - every entry point returns int: 0 = MTPX_OK, nonzero = error; the message
+ *     is in mtpx_last_error() (thread-local);
+ *   - opaque handles are structs holding one `void* ctx`, created by *_new and
+ *     released by *_free;
+ *   - array arguments are plain device pointers to row-contiguous memory
+ *     (bf16 as uint16_t bit patterns), sizes are explicit; outputs are written
+ *     into caller-owned buffers;
+ *   - work is enqueued on the context's HIP stream (mtpx_ctx_set_stream) and is
+ *     asynchronous unless the function says otherwise.  One context is not
+ *     re-entrant: calls on one context must not overlap.
+ *
+ * Weight format: MLX affine 4-bit (packed uint32 [N, K/8], element k at bits
+ * 4*(k%8) of word k/8; bf16 scales and biases [N, K/gs]; gs in {32, 64}).
+ */
+#ifndef MTPX_H
+#define MTPX_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MTPX_OK 0
+#define MTPX_ERR_ARG 1   /* invalid argument or unsupported shape */
+#define MTPX_ERR_HIP 2   /* HIP runtime error */
+#define MTPX_ERR_STATE 3 /* call out of sequence (round state machine) */
+#define MTPX_ERR_OOM 4   /* device allocation failed */
+
+typedef struct mtpx_ctx_ { void* ctx; } mtpx_ctx;
+typedef struct mtpx_kv_ { void* ctx; } mtpx_kv;
+typedef struct mtpx_layer_ { void* ctx; } mtpx_layer;
+
+/* Thread-local text of the last error (replaces mlx-c's error handler,
+ * mlx-c/mlx/c/error.h:15-27). */
+const char* mtpx_last_error(void);
+/* Library version string. */
+const char* mtpx_version(void);
+
+/* ---- context: device, stream and reusable workspace ------------------------
+ * Replaces the implicit MLX default stream the reference's kernels run on
+ * (Vendor/mlx-swift/Source/MLX/MLXFastKernel.swift:176-183 stream argument). */
+int mtpx_ctx_new(mtpx_ctx* out, int device);
+int mtpx_ctx_free(mtpx_ctx ctx);
+/* Enqueue subsequent work on `hip_stream` (NULL = the legacy default stream). */
+int mtpx_ctx_set_stream(mtpx_ctx ctx, void* hip_stream);
+/* Return to the context's own non-blocking stream. */
+int mtpx_ctx_use_own_stream(mtpx_ctx ctx);
+int mtpx_ctx_synchronize(mtpx_ctx ctx);
+
+/* ---- a1: MLX affine 4-bit quantisation on the device -----------------------
+ * Replaces mlx::core::affine_quantize (MLX/ops.cpp:5036-5090; CPU semantics
+ * MLX/backend/cpu/quantized.cpp:1158-1220). w bf16 [rows, K] -> wq, s, b. */
+int mtpx_affine_quantize(mtpx_ctx ctx, const uint16_t* w, int64_t rows, int K, int gs,
+                         uint32_t* wq, uint16_t* scales, uint16_t* biases);
+
+/* Seeded N(0, sigma) bf16 fill (Philox4x32-10 + Box-Muller); `tensor` selects
+ * an independent stream.  Random-init weights only (the reference loads a
+ * checkpoint). */
+int mtpx_randn_bf16(mtpx_ctx ctx, uint16_t* out, int64_t n, uint64_t seed, uint32_t tensor,
+                    float sigma);
+
+/* ---- a2-a4, a12: q4 GEMV / small-M GEMM ------------------------------------
+ * y[M, N] = x[M, K] . W[N, K]^T, M <= 8, bf16 out (yf: optional f32 before
+ * rounding).  Replaces MLX quantizedMM's qmv_fast / qmv / qmv_wide
+ * (MLX/backend/metal/kernels/quantized.h:758,825,989) and the track's
+ * TrackQuantWeight.apply / TrackLUTGemv (Runner/FastModel/TrackFastWeights.swift:40-49,
+ * Runner/FastModel/TrackAffineLUT.swift:121-368). */
+int mtpx_qmv(mtpx_ctx ctx, const uint32_t* wq, const uint16_t* scales, const uint16_t* biases,
+             int N, int K, int gs, const uint16_t* x, int M, uint16_t* y, float* yf);
+
+/* ---- a5-a11: the MoE block -------------------------------------------------- */
+typedef struct {
+  int hidden;        /* H */
+  int experts;       /* E */
+  int top_k;         /* K */
+  int expert_width;  /* F (routed and shared) */
+  int group_size;    /* gs */
+  const uint16_t* router;       /* bf16 [E, H] */
+  const uint16_t* shared_gate;  /* bf16 [H]: the shared expert's sigmoid gate row */
+  const uint32_t* gate_w; const uint16_t* gate_s; const uint16_t* gate_b; /* [E,F,H/8], [E,F,H/gs] */
+  const uint32_t* up_w;   const uint16_t* up_s;   const uint16_t* up_b;
+  const uint32_t* down_w; const uint16_t* down_s; const uint16_t* down_b; /* [E,H,F/8], [E,H,F/gs] */
+  const uint32_t* sh_gate_w; const uint16_t* sh_gate_s; const uint16_t* sh_gate_b; /* [F,H/8] */
+  const uint32_t* sh_up_w;   const uint16_t* sh_up_s;   const uint16_t* sh_up_b;
+  const uint32_t* sh_down_w; const uint16_t* sh_down_s; const uint16_t* sh_down_b; /* [H,F/8] */
+} mtpx_moe_weights;
+
+/* y[M, H] = MoE(x[M, H]) for a decode/verify window of M <= 8 tokens: router
+ * GEMV (bf16 weight, f32 activation), top-k (value desc, index asc) + softmax,
+ * expert-grouped gate|up + SwiGLU, down + rank-ordered combine + sigmoid-gated
+ * shared expert.  Optional outputs (NULL to skip): idx int32 [M, K], w f32
+ * [M, K], logits f32 [M, E], n_unique int32 [1] (distinct routed experts).
+ * Replaces TrackQwen4ExpFastModel.moeForwardShared's decode branch
+ * (Runner/FastModel/TrackFastModel.swift:867-954) and its kernels
+ * TrackFastMoEKernels.routerGemv / route / gateUpAct / downCombine
+ * (Runner/FastModel/TrackFastMoE.swift:2246-2310, 780-911, 1192-1404, 1412-1576). */
+int mtpx_moe_forward(mtpx_ctx ctx, const mtpx_moe_weights* w, const uint16_t* x, int M,
+                     uint16_t* y, int32_t* idx, float* wts, float* logits, int32_t* n_unique);
+
+/* ---- a13-a15: attention pieces -----------------------------------------------
+ * attn_prep: qkv rows [S, QW] = q(HQ*D) | gate(HQ*D) | k(HK*D) | v(HK*D) | ...
+ * -> q [S, HQ, D]; k and v written into the cache (layout [HK, tmax, D]) at
+ * positions pos0 .. pos0+S-1.  RMSNorm (eps) + rotate-half RoPE on the first
+ * `rot` dims with bf16 tables cos/sin [positions, rot].
+ * Replaces TrackFastKernels.attnPrep (Runner/FastModel/TrackFastKernels2.swift:381-476)
+ * plus the cache append of Qwen4ExpAttentionCache.updateAndAttend
+ * (called at Runner/FastModel/TrackFastModel.swift:790-792). */
+int mtpx_attn_prep(mtpx_ctx ctx, const uint16_t* qkv, int S, int QW, int HQ, int HK, int D,
+                   int rot, const uint16_t* qnorm, const uint16_t* knorm, float eps,
+                   const uint16_t* cos_t, const uint16_t* sin_t, int pos0, uint16_t* q,
+                   uint16_t* kcache, uint16_t* vcache, int64_t tmax);
+
+/* Verify attention of S queries against T cached positions (key i visible to
+ * query s iff i <= T - S + s), GQA HQ/HK, f32 online softmax.  out bf16
+ * [S, HQ, D] (optional) and out_gated = out * sigmoid(gate) [S, HQ*D] with the
+ * gate read from qkv[:, gate_off:] (optional).
+ * Replaces the SDPA vector kernels (MLX/backend/metal/kernels/sdpa_vector.h:14-175,
+ * MLX/backend/metal/scaled_dot_product_attention.cpp:364-452) and
+ * TrackFastKernels.attnGate (Runner/FastModel/TrackFastKernels2.swift:478-510). */
+int mtpx_attn_verify(mtpx_ctx ctx, const uint16_t* q, int S, int HQ, int HK, int D,
+                     const uint16_t* kcache, const uint16_t* vcache, int64_t tmax, int T,
+                     float scale, const uint16_t* qkv, int QW, int gate_off, uint16_t* out,
+                     uint16_t* out_gated);
+
+/* Row RMSNorm; with resid != NULL the input is bf16(x + resid), also written to
+ * sum_out when that is not NULL. */
+int mtpx_rmsnorm(mtpx_ctx ctx, const uint16_t* x, const uint16_t* resid, int M, int H,
+                 const uint16_t* w, float eps, uint16_t* sum_out, uint16_t* y);
+
+/* ---- a16: KV cache with rollback ----------------------------------------------
+ * Contiguous bf16 K and V [kv_heads, tmax, head_dim]; rollback = offset rewind
+ * (Qwen4ExpAttentionCache.trim, used at Runner/Qwen4ExpMTPDrafter.swift:461-470
+ * and Runner/Qwen4ExpRunner.swift:385-394). */
+int mtpx_kv_new(mtpx_ctx ctx, int kv_heads, int head_dim, int64_t tmax, mtpx_kv* out);
+int mtpx_kv_free(mtpx_kv kv);
+int mtpx_kv_offset(mtpx_kv kv, int64_t* offset);
+int mtpx_kv_set_offset(mtpx_kv kv, int64_t offset);
+/* rewind by n positions; *trimmed receives the count actually removed */
+int mtpx_kv_trim(mtpx_kv kv, int64_t n, int64_t* trimmed);
+int mtpx_kv_buffers(mtpx_kv kv, uint16_t** k, uint16_t** v, int64_t* tmax);
+
+/* ---- a18, a21: argmax and greedy acceptance ---------------------------------
+ * argmax over V per row, lowest id on ties (Runner/Qwen4ExpMTPDrafter.swift:25-27). */
+int mtpx_argmax_rows(mtpx_ctx ctx, const float* x, int rows, int64_t V, int32_t* out);
+/* logits f32 [k+1, V] (verify rows), drafts int32 [k] -> out3 int32 {n accepted,
+ * bonus token, KV rollback index = kv_offset + n + 1}.  The engine-core accept
+ * loop (docs/qwen38-125b-a6b-port-notes.md:313-343), decided on the device. */
+int mtpx_accept_greedy(mtpx_ctx ctx, const float* logits, int k, int64_t V,
+                       const int32_t* drafts, int32_t kv_offset, int32_t* out3);
+
+/* ---- a22: temperature rejection sampling (no reference counterpart) ----------
+ * tlogits f32 [k+1, V], dlogits f32 [k, V] (row i proposed drafts[i]);
+ * Philox4x32-10 key = seed, counter = {offset lo, offset hi, i, 0}. */
+int mtpx_accept_sample(mtpx_ctx ctx, const float* tlogits, const float* dlogits, int k,
+                       int64_t V, const int32_t* drafts, float temperature, uint64_t seed,
+                       uint64_t offset, int32_t kv_offset, int32_t* out3);
+
+/* ---- one full-shape decoder layer (attention + MoE) for verify windows -------
+ * x -> h1 = rms(x); qkv = W_qkv h1; prep + KV append; verify attention with
+ * output gate; o = W_o att; s = x + o; h2 = rms(s); y = s + MoE(h2).
+ * Replaces the attention + MoE sublayers of the fast forward
+ * (Runner/FastModel/TrackFastModel.swift:747-795, 867-954) without the
+ * hyper-connection mixers. */
+typedef struct {
+  int hidden, experts, top_k, expert_width, group_size;
+  int heads, kv_heads, head_dim, rot_dims, index_dim;
+  float rope_theta, eps;
+  int64_t max_positions;
+} mtpx_layer_config;
+
+typedef struct {
+  const uint16_t* attn_norm; const uint16_t* post_norm; /* bf16 [H] */
+  const uint32_t* qkv_w; const uint16_t* qkv_s; const uint16_t* qkv_b; /* [QW, H] */
+  const uint16_t* q_norm; const uint16_t* k_norm; /* bf16 [D] */
+  const uint32_t* o_w; const uint16_t* o_s; const uint16_t* o_b; /* [H, HQ*D] */
+  const uint16_t* rope_cos; const uint16_t* rope_sin; /* bf16 [max_positions, rot] */
+  mtpx_moe_weights moe;
+  int qkv_rows;
+} mtpx_layer_weights;
+
+int mtpx_layer_new_random(mtpx_ctx ctx, const mtpx_layer_config* cfg, uint64_t seed,
+                          mtpx_layer* out);
+int mtpx_layer_free(mtpx_layer layer);
+int mtpx_layer_weights_get(mtpx_layer layer, mtpx_layer_weights* out);
+/* y[M, H] for M tokens at the cache's offset; advances the offset by M. */
+int mtpx_layer_forward(mtpx_ctx ctx, mtpx_layer layer, mtpx_kv kv, const uint16_t* x, int M,
+                       uint16_t* y);
+/* ---- per-kernel timing (replaces TrackFastProfile, Runner/FastModel/TrackFastWeights.swift:81-98) ----
+ * With profiling on, every launch the library issues is bracketed by HIP events
+ * on the context stream.  mtpx_profile_dump synchronises and writes one line per
+ * kernel name: "<name> <launches> <total ms>\n". */
+int mtpx_profile_enable(mtpx_ctx ctx, int on);
+int mtpx_profile_reset(mtpx_ctx ctx);
+int mtpx_profile_dump(mtpx_ctx ctx, char* buf, size_t n);
+
+/* Algorithmic HBM bytes of the last mtpx_moe_forward / layer forward's MoE on
+ * this context (distinct experts read back from the device; synchronises). */
+int mtpx_last_moe_bytes(mtpx_ctx ctx, int64_t* bytes, int32_t* n_unique);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,336 @@
+// Speculative acceptance, decided on the device.
+//   greedy : argmax of each verify row (lowest id on ties), longest prefix of
+//            drafts equal to the row argmaxes, bonus token, KV rollback index
+//   sample : temperature rejection sampling (Leviathan et al. 2023) with a
+//            Philox4x32-10 stream; probabilities and sums in a fixed order
+// Reference: accept/rollback semantics docs/qwen38-125b-a6b-port-notes.md:313-343,
+// tie rule Runner/Qwen4ExpMTPDrafter.swift:25-27.  Sampling has no reference
+// counterpart (the reference is greedy only).
+#include "mtpx_kernels.h"
+
+namespace mtpx {
+
+constexpr int AM_SPAN = 8192;  // elements per argmax partial
+
+struct VI {
+  float v;
+  int i;
+};
+
+__device__ __forceinline__ VI vi_best(VI a, VI b) {
+  // larger value; lower index on equal values
+  if (b.v > a.v || (b.v == a.v && b.i < a.i)) return b;
+  return a;
+}
+
+__device__ __forceinline__ VI wave_best(VI x) {
+#pragma unroll
+  for (int off = 32; off >= 1; off /= 2) {
+    VI o;
+    o.v = __shfl_xor(x.v, off, 64);
+    o.i = __shfl_xor(x.i, off, 64);
+    x = vi_best(x, o);
+  }
+  return x;
+}
+
+// grid (parts, rows): best (value, index) of each AM_SPAN slice of a row.
+__global__ __launch_bounds__(256) void k_argmax_part(const float* __restrict__ x, int64_t V, int parts,
+                                                     float* __restrict__ pval, int32_t* __restrict__ pidx) {
+  __shared__ VI wb[4];
+  const int part = blockIdx.x, row = blockIdx.y;
+  const float* xr = x + (size_t)row * V;
+  const int64_t b = (int64_t)part * AM_SPAN;
+  const int64_t e = b + AM_SPAN < V ? b + AM_SPAN : V;
+  VI best{-__uint_as_float(0x7f800000u), 0x7fffffff};
+  for (int64_t i = b + threadIdx.x; i < e; i += 256) best = vi_best(best, VI{xr[i], (int)i});
+  best = wave_best(best);
+  if ((threadIdx.x & 63) == 0) wb[threadIdx.x >> 6] = best;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    VI r = wb[0];
+    for (int w = 1; w < 4; ++w) r = vi_best(r, wb[w]);
+    pval[(size_t)row * parts + part] = r.v;
+    pidx[(size_t)row * parts + part] = r.i;
+  }
+}
+
+__device__ VI reduce_parts(const float* pval, const int32_t* pidx, int parts, int row, int lane) {
+  VI best{-__uint_as_float(0x7f800000u), 0x7fffffff};
+  for (int p = lane; p < parts; p += 64) best = vi_best(best, VI{pval[(size_t)row * parts + p], pidx[(size_t)row * parts + p]});
+  return wave_best(best);
+}
+
+// one wave per row
+__global__ void k_argmax_final(const float* __restrict__ pval, const int32_t* __restrict__ pidx, int rows,
+                               int parts, int32_t* __restrict__ out) {
+  const int row = blockIdx.x;
+  const VI b = reduce_parts(pval, pidx, parts, row, threadIdx.x);
+  if (threadIdx.x == 0) out[row] = b.i;
+}
+
+// one workgroup: wave r reduces row r, then thread 0 decides.
+__global__ __launch_bounds__(512) void k_accept_greedy(const float* __restrict__ pval,
+                                                       const int32_t* __restrict__ pidx, int k, int parts,
+                                                       const int32_t* __restrict__ drafts, int32_t kv_offset,
+                                                       int32_t* __restrict__ out3) {
+  __shared__ int am[MAX_TOKENS];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  if (wave <= k) {
+    const VI b = reduce_parts(pval, pidx, parts, wave, lane);
+    if (lane == 0) am[wave] = b.i;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int n = 0;
+    while (n < k && drafts[n] == am[n]) ++n;
+    out3[0] = n;
+    out3[1] = am[n];
+    out3[2] = kv_offset + n + 1;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// sampling
+constexpr int S_CHUNK = 1024;
+
+__device__ __forceinline__ uint4 philox4x32_10(uint4 c, uint2 k) {
+#pragma unroll
+  for (int r = 0; r < 10; ++r) {
+    if (r > 0) {
+      k.x += 0x9E3779B9u;
+      k.y += 0xBB67AE85u;
+    }
+    const uint32_t hi0 = __umulhi(0xD2511F53u, c.x), lo0 = 0xD2511F53u * c.x;
+    const uint32_t hi1 = __umulhi(0xCD9E8D57u, c.z), lo1 = 0xCD9E8D57u * c.z;
+    c = make_uint4(hi1 ^ c.y ^ k.x, lo1, hi0 ^ c.w ^ k.y, lo0);
+  }
+  return c;
+}
+
+__device__ __forceinline__ float uniform24(uint32_t r) { return (float)(r >> 8) * 5.9604644775390625e-08f; }
+
+// Work layout (floats): rowmax[2k+1], invZ[2k+1], state[8], csum[(2k+1)*nch], vsum[nch]
+// rows 0..k: verify rows (tlogits); rows k+1..2k: draft rows (dlogits).
+struct SampleWork {
+  float* rowmax;
+  float* invz;
+  float* state;  // [0] mode (0 residual, 1 bonus), [1] row, [2] u2, [3] n
+  float* csum;
+  float* vsum;
+};
+
+__device__ __forceinline__ const float* srow(const float* t, const float* d, int k, int64_t V, int r) {
+  return r <= k ? t + (size_t)r * V : d + (size_t)(r - k - 1) * V;
+}
+
+// one wave per row: row max from the argmax partials
+__global__ void k_sample_rowmax(const float* __restrict__ pval, const int32_t* __restrict__ pidx, int parts,
+                                float* __restrict__ rowmax) {
+  const VI b = reduce_parts(pval, pidx, parts, blockIdx.x, threadIdx.x);
+  if (threadIdx.x == 0) rowmax[blockIdx.x] = b.v;
+}
+
+// grid (nch, rows), one wave: chunk sum of exp((l - max) * invT), lane-strided
+// (lane l adds base+l, base+l+64, ...) then an xor butterfly.
+__global__ void k_sample_chunks(const float* __restrict__ t, const float* __restrict__ d, int k, int64_t V,
+                                float invT, const float* __restrict__ rowmax, int nch, float* __restrict__ csum) {
+  const int c = blockIdx.x, r = blockIdx.y, lane = threadIdx.x;
+  const float* x = srow(t, d, k, V, r);
+  const float mx = rowmax[r];
+  float acc = 0.0f;
+  for (int j = 0; j < S_CHUNK / 64; ++j) {
+    const int64_t i = (int64_t)c * S_CHUNK + lane + 64 * j;
+    if (i < V) acc = acc + expf_det((x[i] - mx) * invT);
+  }
+  acc = wave_fold64(acc);
+  if (lane == 0) csum[(size_t)r * nch + c] = acc;
+}
+
+__device__ __forceinline__ float prob(const float* x, int64_t v, float mx, float invT, float invz) {
+  return expf_det((x[v] - mx) * invT) * invz;
+}
+
+// single thread: Z per row, then the accept/reject walk
+__global__ void k_sample_decide(const float* __restrict__ t, const float* __restrict__ d, int k, int64_t V,
+                                const int32_t* __restrict__ drafts, float invT, uint64_t seed, uint64_t offset,
+                                int nch, SampleWork w, int32_t* __restrict__ out3, int32_t kv_offset) {
+  if (threadIdx.x != 0) return;
+  for (int r = 0; r < 2 * k + 1; ++r) {
+    float z = 0.0f;
+    for (int c = 0; c < nch; ++c) z = z + w.csum[(size_t)r * nch + c];
+    w.invz[r] = 1.0f / z;
+  }
+  const uint2 key = make_uint2((uint32_t)seed, (uint32_t)(seed >> 32));
+  for (int i = 1; i <= k + 1; ++i) {
+    const uint4 rnd = philox4x32_10(make_uint4((uint32_t)offset, (uint32_t)(offset >> 32), (uint32_t)i, 0u), key);
+    const float u = uniform24(rnd.x), u2 = uniform24(rnd.y);
+    if (i == k + 1) {
+      w.state[0] = 1.0f;
+      w.state[1] = (float)k;
+      w.state[2] = u2;
+      w.state[3] = (float)k;
+      out3[0] = k;
+      out3[2] = kv_offset + k + 1;
+      return;
+    }
+    const int dt = drafts[i - 1];
+    const float* tr = srow(t, d, k, V, i - 1);
+    const float* dr = srow(t, d, k, V, k + i);
+    // a draft id outside the vocabulary is rejected
+    const bool ok = dt >= 0 && dt < V;
+    const float pt = ok ? prob(tr, dt, w.rowmax[i - 1], invT, w.invz[i - 1]) : 0.0f;
+    const float pd = ok ? prob(dr, dt, w.rowmax[k + i], invT, w.invz[k + i]) : 1.0f;
+    if (u * pd < pt) continue;
+    w.state[0] = 0.0f;
+    w.state[1] = (float)(i - 1);
+    w.state[2] = u2;
+    w.state[3] = (float)(i - 1);
+    out3[0] = i - 1;
+    out3[2] = kv_offset + i;
+    return;
+  }
+}
+
+__device__ __forceinline__ float sample_val(const float* t, const float* d, int k, int64_t V, const SampleWork& w,
+                                            float invT, int64_t v) {
+  const int row = (int)w.state[1];
+  const float pt = prob(srow(t, d, k, V, row), v, w.rowmax[row], invT, w.invz[row]);
+  if (w.state[0] != 0.0f) return pt;
+  const float pd = prob(srow(t, d, k, V, k + 1 + row), v, w.rowmax[k + 1 + row], invT, w.invz[k + 1 + row]);
+  return fmaxf(pt - pd, 0.0f);
+}
+
+// grid (nch), one wave: chunk sums of the residual (or bonus) distribution
+__global__ void k_sample_vchunks(const float* __restrict__ t, const float* __restrict__ d, int k, int64_t V,
+                                 float invT, SampleWork w) {
+  const int c = blockIdx.x, lane = threadIdx.x;
+  float acc = 0.0f;
+  for (int j = 0; j < S_CHUNK / 64; ++j) {
+    const int64_t i = (int64_t)c * S_CHUNK + lane + 64 * j;
+    if (i < V) acc = acc + sample_val(t, d, k, V, w, invT, i);
+  }
+  acc = wave_fold64(acc);
+  if (lane == 0) w.vsum[c] = acc;
+}
+
+// single thread: inverse CDF over the chunk sums, then inside the chunk
+__global__ void k_sample_icdf(const float* __restrict__ t, const float* __restrict__ d, int k, int64_t V, float invT,
+                              int nch, SampleWork w, const float* __restrict__ pval,
+                              const int32_t* __restrict__ pidx, int parts, int32_t* __restrict__ out3) {
+  if (threadIdx.x != 0) return;
+  float total = 0.0f;
+  for (int c = 0; c < nch; ++c) total = total + w.vsum[c];
+  const float tau = w.state[2] * total;
+  float cum = 0.0f;
+  int64_t res = -1;
+  for (int c = 0; c < nch && res < 0; ++c) {
+    const float nxt = cum + w.vsum[c];
+    if (nxt > tau) {
+      const float t2 = tau - cum;
+      float run = 0.0f;
+      const int64_t b = (int64_t)c * S_CHUNK;
+      const int64_t e = b + S_CHUNK < V ? b + S_CHUNK : V;
+      for (int64_t i = b; i < e; ++i) {
+        run = run + sample_val(t, d, k, V, w, invT, i);
+        if (run > t2) {
+          res = i;
+          break;
+        }
+      }
+      if (res < 0)
+        for (int64_t i = e - 1; i >= b; --i)
+          if (sample_val(t, d, k, V, w, invT, i) > 0.0f) {
+            res = i;
+            break;
+          }
+    }
+    cum = nxt;
+  }
+  if (res < 0)
+    for (int64_t i = V - 1; i >= 0; --i)
+      if (sample_val(t, d, k, V, w, invT, i) > 0.0f) {
+        res = i;
+        break;
+      }
+  if (res < 0) {
+    // every entry zero: the target row's argmax (lowest id on ties)
+    const int row = (int)w.state[1];
+    VI best{-__uint_as_float(0x7f800000u), 0x7fffffff};
+    for (int p = 0; p < parts; ++p) best = vi_best(best, VI{pval[(size_t)row * parts + p], pidx[(size_t)row * parts + p]});
+    res = best.i;
+  }
+  out3[1] = (int32_t)res;
+}
+
+// ---------------------------------------------------------------------------
+size_t argmax_work_items(int rows, int64_t V) { return (size_t)rows * ((V + AM_SPAN - 1) / AM_SPAN); }
+
+hipError_t launch_argmax_rows(const float* x, int rows, int64_t V, float* pval, int32_t* pidx, int32_t* out,
+                              hipStream_t st) {
+  const int parts = (int)((V + AM_SPAN - 1) / AM_SPAN);
+  hipLaunchKernelGGL(k_argmax_part, dim3(parts, rows), dim3(256), 0, st, x, V, parts, pval, pidx);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(k_argmax_final, dim3(rows), dim3(64), 0, st, pval, pidx, rows, parts, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_accept_greedy(const float* logits, int k, int64_t V, const int32_t* drafts, int32_t kv_offset,
+                                float* pval, int32_t* pidx, int32_t* out3, hipStream_t st) {
+  const int parts = (int)((V + AM_SPAN - 1) / AM_SPAN);
+  hipLaunchKernelGGL(k_argmax_part, dim3(parts, k + 1), dim3(256), 0, st, logits, V, parts, pval, pidx);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(k_accept_greedy, dim3(1), dim3(64 * (k + 1)), 0, st, pval, pidx, k, parts, drafts, kv_offset,
+                     out3);
+  return hipGetLastError();
+}
+
+size_t accept_sample_work_floats(int k, int64_t V) {
+  const int64_t nch = (V + S_CHUNK - 1) / S_CHUNK;
+  const int rows = 2 * k + 1;
+  const size_t parts = (size_t)((V + AM_SPAN - 1) / AM_SPAN);
+  return (size_t)rows * 2 + 8 + (size_t)rows * nch + nch + 2 * rows * parts;
+}
+
+hipError_t launch_accept_sample(const float* tlogits, const float* dlogits, int k, int64_t V, const int32_t* drafts,
+                                float temperature, uint64_t seed, uint64_t offset, int32_t kv_offset, float* work,
+                                int32_t* out3, hipStream_t st) {
+  const int rows = 2 * k + 1;
+  const int nch = (int)((V + S_CHUNK - 1) / S_CHUNK);
+  const int parts = (int)((V + AM_SPAN - 1) / AM_SPAN);
+  SampleWork w;
+  w.rowmax = work;
+  w.invz = work + rows;
+  w.state = work + 2 * rows;
+  w.csum = w.state + 8;
+  w.vsum = w.csum + (size_t)rows * nch;
+  float* pval = w.vsum + nch;
+  int32_t* pidx = reinterpret_cast<int32_t*>(pval + (size_t)rows * parts);
+  const float invT = 1.0f / temperature;
+  hipError_t e;
+  // row maxima: verify rows then draft rows (two launches over the two arrays)
+  hipLaunchKernelGGL(k_argmax_part, dim3(parts, k + 1), dim3(256), 0, st, tlogits, V, parts, pval, pidx);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  if (k > 0) {
+    hipLaunchKernelGGL(k_argmax_part, dim3(parts, k), dim3(256), 0, st, dlogits, V, parts,
+                       pval + (size_t)(k + 1) * parts, pidx + (size_t)(k + 1) * parts);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+  }
+  hipLaunchKernelGGL(k_sample_rowmax, dim3(rows), dim3(64), 0, st, pval, pidx, parts, w.rowmax);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  hipLaunchKernelGGL(k_sample_chunks, dim3(nch, rows), dim3(64), 0, st, tlogits, dlogits, k, V, invT, w.rowmax, nch,
+                     w.csum);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  hipLaunchKernelGGL(k_sample_decide, dim3(1), dim3(64), 0, st, tlogits, dlogits, k, V, drafts, invT, seed, offset,
+                     nch, w, out3, kv_offset);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  hipLaunchKernelGGL(k_sample_vchunks, dim3(nch), dim3(64), 0, st, tlogits, dlogits, k, V, invT, w);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  hipLaunchKernelGGL(k_sample_icdf, dim3(1), dim3(64), 0, st, tlogits, dlogits, k, V, invT, nch, w, pval, pidx, parts,
+                     out3);
+  return hipGetLastError();
+}
+
+}  // namespace mtpx

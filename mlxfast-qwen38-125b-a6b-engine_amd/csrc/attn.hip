@@ -1,0 +1,254 @@
+// Verify attention over a contiguous bf16 KV cache, plus the row norms and
+// residual adds around the decoder sublayers.
+//   prep    : per (head, token): q/k RMSNorm over D, rotate-half RoPE on the
+//             first ROT dims (bf16 arithmetic), k and v written straight into
+//             the cache at position pos0 + token (the KV append)
+//   partial : per (key chunk, kv head): scores of every query row of the GQA
+//             group against the chunk, chunk max, exp, sum and P.V partial
+//   combine : per (query row, kv head): fold the chunk partials in chunk order,
+//             bf16 output and the sigmoid output gate
+// Rollback of rejected draft positions is an offset rewind: positions past the
+// offset are overwritten by the next append.
+// Reference: FM/TrackFastKernels2.swift:381-510 (prep, gate),
+// MLX/backend/metal/kernels/sdpa_vector.h:14-175 (online softmax, causal rule).
+#include "mtpx_kernels.h"
+
+namespace mtpx {
+
+__global__ void k_attn_prep(const bf16* __restrict__ qkv, int S, int QW, int HQ, int HK, int D, int ROT,
+                            const bf16* __restrict__ qnorm, const bf16* __restrict__ knorm, float eps,
+                            const bf16* __restrict__ cos_t, const bf16* __restrict__ sin_t, int pos0,
+                            bf16* __restrict__ q, bf16* __restrict__ kc, bf16* __restrict__ vc, int64_t tmax) {
+  __shared__ float vec[1024];
+  const int h = blockIdx.x, s = blockIdx.y, t = threadIdx.x;
+  const int L = D / 4;
+  const bf16* row = qkv + (size_t)s * QW;
+  const int pos = pos0 + s;
+  if (h >= HQ + HK) {  // v: passthrough into the cache
+    const int hv = h - HQ - HK;
+    const bf16* src = row + 2 * HQ * D + HK * D + hv * D;
+    bf16* dst = vc + ((size_t)hv * tmax + pos) * D;
+    for (int i = 0; i < 4; ++i) dst[4 * t + i] = src[4 * t + i];
+    return;
+  }
+  const bool isq = h < HQ;
+  const int hh = isq ? h : h - HQ;
+  const bf16* src = isq ? row + hh * D : row + 2 * HQ * D + hh * D;
+  const bf16* wn = isq ? qnorm : knorm;
+  float x[4];
+  float acc = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    x[i] = bf2f(src[4 * t + i]);
+    acc = __builtin_fmaf(x[i], x[i], acc);
+  }
+  for (int off = L / 2; off >= 1; off >>= 1) acc = acc + __shfl_xor(acc, off, 64);
+  const float inv = 1.0f / sqrtf(acc / (float)D + eps);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) vec[4 * t + i] = round_bf(bf2f(wn[4 * t + i]) * round_bf(x[i] * inv));
+  __syncthreads();
+  bf16* dst = isq ? q + ((size_t)s * HQ + hh) * D : kc + ((size_t)hh * tmax + pos) * D;
+  const int half = ROT / 2;
+  const bf16* cs = cos_t + (size_t)pos * ROT;
+  const bf16* sn = sin_t + (size_t)pos * ROT;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int d = 4 * t + i;
+    float o = vec[d];
+    if (d < ROT) {
+      const float c = bf2f(cs[d]), sv = bf2f(sn[d]);
+      if (d < half) {
+        const float t1 = round_bf(vec[d] * c);
+        const float t2 = round_bf(-vec[d + half] * sv);
+        o = round_bf(t1 + t2);
+      } else {
+        const float t1 = round_bf(vec[d] * c);
+        const float t2 = round_bf(vec[d - half] * sv);
+        o = round_bf(t1 + t2);
+      }
+    }
+    dst[d] = f2bf(o);
+  }
+}
+
+// part layout: [(hk * nch + c) * R + ri] * (D + 2): {m, l, o[0..D)}, R = S * G
+__global__ __launch_bounds__(256) void k_attn_partial(const bf16* __restrict__ q, int S, int HQ, int HK, int D,
+                                                      const bf16* __restrict__ kc, const bf16* __restrict__ vc,
+                                                      int64_t tmax, int T, float scale, int nch,
+                                                      float* __restrict__ part) {
+  extern __shared__ float smem[];
+  const int c = blockIdx.x, hk = blockIdx.y;
+  const int G = HQ / HK, R = S * G, C = ATTN_CHUNK;
+  const int i0 = c * C;
+  bf16* qb = reinterpret_cast<bf16*>(smem);                 // [R][D]
+  bf16* kb = qb + (size_t)R * D;                            // [C][D]
+  bf16* vb = kb + (size_t)C * D;                            // [C][D]
+  float* sc = reinterpret_cast<float*>(vb + (size_t)C * D);  // [R][C]
+  float* ml = sc + (size_t)R * C;                           // [R][2]
+  for (int i = threadIdx.x; i < R * D; i += blockDim.x) {
+    const int ri = i / D, d = i % D;
+    const int s = ri / G, g = ri % G;
+    qb[i] = q[((size_t)s * HQ + hk * G + g) * D + d];
+  }
+  for (int i = threadIdx.x; i < C * D; i += blockDim.x) {
+    const int j = i / D, d = i % D;
+    const int key = i0 + j;
+    kb[i] = key < T ? kc[((size_t)hk * tmax + key) * D + d] : (bf16)0;
+    vb[i] = key < T ? vc[((size_t)hk * tmax + key) * D + d] : (bf16)0;
+  }
+  __syncthreads();
+  for (int p = threadIdx.x; p < R * C; p += blockDim.x) {
+    const int ri = p / C, j = p % C;
+    const int s = ri / G;
+    const int last = T - S + s;
+    const int key = i0 + j;
+    float acc = 0.0f;
+    if (key <= last) {
+      const bf16* qr = qb + (size_t)ri * D;
+      const bf16* kr = kb + (size_t)j * D;
+      for (int d = 0; d < D; ++d) acc = __builtin_fmaf(scale * bf2f(qr[d]), bf2f(kr[d]), acc);
+    }
+    sc[p] = acc;
+  }
+  __syncthreads();
+  for (int ri = threadIdx.x; ri < R; ri += blockDim.x) {
+    const int s = ri / G;
+    const int last = T - S + s;
+    int n = last + 1 - i0;
+    n = n < 0 ? 0 : (n > C ? C : n);
+    float mx = -__uint_as_float(0x7f800000u);
+    for (int j = 0; j < n; ++j) mx = sc[ri * C + j] > mx ? sc[ri * C + j] : mx;
+    float l = 0.0f;
+    for (int j = 0; j < n; ++j) {
+      const float e = expf_det(sc[ri * C + j] - mx);
+      sc[ri * C + j] = e;
+      l = l + e;
+    }
+    ml[2 * ri] = (n > 0) ? mx : -__uint_as_float(0x7f800000u);
+    ml[2 * ri + 1] = (n > 0) ? l : 0.0f;
+    for (int j = n; j < C; ++j) sc[ri * C + j] = 0.0f;
+  }
+  __syncthreads();
+  for (int p = threadIdx.x; p < R * D; p += blockDim.x) {
+    const int ri = p / D, d = p % D;
+    const int s = ri / G;
+    int n = T - S + s + 1 - i0;
+    n = n < 0 ? 0 : (n > C ? C : n);
+    float o = 0.0f;
+    for (int j = 0; j < n; ++j) o = __builtin_fmaf(sc[ri * C + j], bf2f(vb[(size_t)j * D + d]), o);
+    float* dst = part + (((size_t)hk * nch + c) * R + ri) * (D + 2);
+    dst[2 + d] = o;
+    if (d == 0) {
+      dst[0] = ml[2 * ri];
+      dst[1] = ml[2 * ri + 1];
+    }
+  }
+}
+
+__global__ void k_attn_combine(const float* __restrict__ part, int S, int HQ, int HK, int D, int nch,
+                               const bf16* __restrict__ qkv, int QW, int gate_off, bf16* __restrict__ out,
+                               bf16* __restrict__ out_gated) {
+  const int ri = blockIdx.x, hk = blockIdx.y;
+  const int G = HQ / HK, R = S * G;
+  const int s = ri / G, h = hk * G + ri % G;
+  float M = -__uint_as_float(0x7f800000u);
+  for (int c = 0; c < nch; ++c) {
+    const float* p = part + (((size_t)hk * nch + c) * R + ri) * (D + 2);
+    if (p[1] > 0.0f && p[0] > M) M = p[0];
+  }
+  for (int d = threadIdx.x; d < D; d += blockDim.x) {
+    float L = 0.0f, O = 0.0f;
+    for (int c = 0; c < nch; ++c) {
+      const float* p = part + (((size_t)hk * nch + c) * R + ri) * (D + 2);
+      if (!(p[1] > 0.0f)) continue;
+      const float f = expf_det(p[0] - M);
+      L = __builtin_fmaf(p[1], f, L);
+      O = __builtin_fmaf(p[2 + d], f, O);
+    }
+    const bf16 att = f2bf(O / L);
+    if (out) out[((size_t)s * HQ + h) * D + d] = att;
+    if (out_gated) {
+      const float g = bf2f(qkv[(size_t)s * QW + gate_off + h * D + d]);
+      out_gated[(size_t)s * HQ * D + h * D + d] = f2bf(bf2f(att) * sigmoid_bf16(g));
+    }
+  }
+}
+
+// y = bf16(w * bf16(h * inv)), h = x or bf16(x + resid); 256 threads per row.
+__global__ __launch_bounds__(256) void k_rmsnorm(const bf16* __restrict__ x, const bf16* __restrict__ resid,
+                                                 int H, const bf16* __restrict__ w, float eps,
+                                                 bf16* __restrict__ sum_out, bf16* __restrict__ y) {
+  __shared__ float wsum[4];
+  const int m = blockIdx.x, t = threadIdx.x;
+  const bf16* xr = x + (size_t)m * H;
+  const bf16* rr = resid ? resid + (size_t)m * H : nullptr;
+  float acc = 0.0f;
+  for (int i = t; i < H; i += 256) {
+    float v = bf2f(xr[i]);
+    if (rr) {
+      v = round_bf(v + bf2f(rr[i]));
+      if (sum_out) sum_out[(size_t)m * H + i] = f2bf(v);
+    }
+    acc = __builtin_fmaf(v, v, acc);
+  }
+  acc = wave_fold64(acc);
+  if ((t & 63) == 0) wsum[t >> 6] = acc;
+  __syncthreads();
+  const float total = ((wsum[0] + wsum[1]) + wsum[2]) + wsum[3];
+  const float inv = 1.0f / sqrtf(total / (float)H + eps);
+  for (int i = t; i < H; i += 256) {
+    float v = bf2f(xr[i]);
+    if (rr) v = round_bf(v + bf2f(rr[i]));
+    y[(size_t)m * H + i] = f2bf(bf2f(w[i]) * round_bf(v * inv));
+  }
+}
+
+__global__ void k_add(const bf16* __restrict__ a, const bf16* __restrict__ b, int64_t n, bf16* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) out[i] = f2bf(bf2f(a[i]) + bf2f(b[i]));
+}
+
+// ---------------------------------------------------------------------------
+size_t attn_partial_floats(int S, int HQ, int D, int T) {
+  const int nch = (T + ATTN_CHUNK - 1) / ATTN_CHUNK;
+  return (size_t)nch * S * HQ * (D + 2);
+}
+
+hipError_t launch_attn_prep(const bf16* qkv, int S, int QW, int HQ, int HK, int D, int ROT, const bf16* qnorm,
+                            const bf16* knorm, float eps, const bf16* cos_t, const bf16* sin_t, int pos0, bf16* q,
+                            bf16* kcache, bf16* vcache, int64_t tmax, hipStream_t st) {
+  hipLaunchKernelGGL(k_attn_prep, dim3(HQ + 2 * HK, S), dim3(D / 4), 0, st, qkv, S, QW, HQ, HK, D, ROT, qnorm, knorm,
+                     eps, cos_t, sin_t, pos0, q, kcache, vcache, tmax);
+  return hipGetLastError();
+}
+
+hipError_t launch_attn_verify(const bf16* q, int S, int HQ, int HK, int D, const bf16* kc, const bf16* vc,
+                              int64_t tmax, int T, float scale, float* part, const bf16* qkv, int QW, int gate_off,
+                              bf16* out, bf16* out_gated, hipStream_t st) {
+  const int nch = (T + ATTN_CHUNK - 1) / ATTN_CHUNK;
+  const int G = HQ / HK, R = S * G;
+  const size_t lds = (size_t)R * D * 2 + 2 * (size_t)ATTN_CHUNK * D * 2 + (size_t)R * ATTN_CHUNK * 4 + (size_t)R * 8;
+  static size_t cur = 0;
+  hipError_t e = ensure_lds(k_attn_partial, lds, cur);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(k_attn_partial, dim3(nch, HK), dim3(256), lds, st, q, S, HQ, HK, D, kc, vc, tmax, T, scale, nch,
+                     part);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  hipLaunchKernelGGL(k_attn_combine, dim3(R, HK), dim3(D < 256 ? D : 256), 0, st, part, S, HQ, HK, D, nch, qkv, QW,
+                     gate_off, out, out_gated);
+  return hipGetLastError();
+}
+
+hipError_t launch_rmsnorm(const bf16* x, const bf16* resid, int M, int H, const bf16* w, float eps, bf16* sum_out,
+                          bf16* y, hipStream_t st) {
+  hipLaunchKernelGGL(k_rmsnorm, dim3(M), dim3(256), 0, st, x, resid, H, w, eps, sum_out, y);
+  return hipGetLastError();
+}
+
+hipError_t launch_add(const bf16* a, const bf16* b, int64_t n, bf16* out, hipStream_t st) {
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_add, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, a, b, n, out);
+  return hipGetLastError();
+}
+
+}  // namespace mtpx

@@ -1,0 +1,764 @@
+// C-ABI layer of libmtpx: argument checks, contexts, workspace, handles.
+// No torch types, no host fallbacks: every compute entry point enqueues HIP
+// kernels and fails with an error code when it cannot.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <string>
+#include <vector>
+
+#include "../../include/mtpx.h"
+#include "mtpx_kernels.h"
+
+using namespace mtpx;
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+#define HIP_OK(expr)                                                                              \
+  do {                                                                                            \
+    hipError_t e_ = (expr);                                                                       \
+    if (e_ != hipSuccess) return fail(MTPX_ERR_HIP, "%s: %s", #expr, hipGetErrorString(e_));      \
+  } while (0)
+
+#define ARG(cond, ...)                                 \
+  do {                                                 \
+    if (!(cond)) return fail(MTPX_ERR_ARG, __VA_ARGS__); \
+  } while (0)
+
+struct Ctx {
+  int device = 0;
+  hipStream_t own = nullptr;
+  hipStream_t stream = nullptr;
+  void* ws = nullptr;
+  size_t ws_size = 0;
+  size_t ws_used = 0;
+  uint32_t* counters = nullptr;
+  int counters_n = 0;
+  MoeDispatch* last_disp = nullptr;  // inside the workspace of the last MoE call
+  int last_H = 0, last_E = 0, last_F = 0, last_gs = 0;
+  // per-kernel timing with events on the launch stream (off by default)
+  bool prof = false;
+  struct Rec {
+    const char* name;
+    hipEvent_t a, b;
+  };
+  std::vector<hipEvent_t> ev_free;
+  std::vector<Rec> pending;
+  std::map<std::string, std::pair<int64_t, double>> stats;  // launches, total ms
+};
+
+hipEvent_t ev_get(Ctx* c) {
+  if (!c->ev_free.empty()) {
+    hipEvent_t e = c->ev_free.back();
+    c->ev_free.pop_back();
+    return e;
+  }
+  hipEvent_t e = nullptr;
+  if (hipEventCreate(&e) != hipSuccess) return nullptr;
+  return e;
+}
+
+// Launch `expr`; with profiling on, bracket it with events on the context stream.
+#define LAUNCH(c, name, expr)                                        \
+  do {                                                               \
+    hipEvent_t a_ = nullptr;                                         \
+    if ((c)->prof && (a_ = ev_get(c))) hipEventRecord(a_, (c)->stream); \
+    HIP_OK(expr);                                                    \
+    if (a_) {                                                        \
+      hipEvent_t b_ = ev_get(c);                                     \
+      if (b_) {                                                      \
+        hipEventRecord(b_, (c)->stream);                             \
+        (c)->pending.push_back({name, a_, b_});                      \
+      } else {                                                       \
+        (c)->ev_free.push_back(a_);                                  \
+      }                                                              \
+    }                                                                \
+  } while (0)
+
+int prof_fold(Ctx* c) {
+  if (c->pending.empty()) return MTPX_OK;
+  HIP_OK(hipStreamSynchronize(c->stream));
+  for (auto& r : c->pending) {
+    float ms = 0.0f;
+    HIP_OK(hipEventElapsedTime(&ms, r.a, r.b));
+    auto& st = c->stats[r.name];
+    st.first += 1;
+    st.second += ms;
+    c->ev_free.push_back(r.a);
+    c->ev_free.push_back(r.b);
+  }
+  c->pending.clear();
+  return MTPX_OK;
+}
+
+// Workspace bump allocation.  Calls on one context are serialised on its
+// stream, so every call may reuse the whole workspace from offset 0.
+int ws_reserve(Ctx* c, size_t bytes) {
+  if (bytes <= c->ws_size) return MTPX_OK;
+  if (c->ws) {
+    HIP_OK(hipStreamSynchronize(c->stream));
+    HIP_OK(hipFree(c->ws));
+    c->ws = nullptr;
+    c->last_disp = nullptr;
+  }
+  size_t sz = bytes < ((size_t)64 << 20) ? ((size_t)64 << 20) : bytes + (bytes >> 2);
+  if (hipMalloc(&c->ws, sz) != hipSuccess) {
+    c->ws = nullptr;
+    c->ws_size = 0;
+    return fail(MTPX_ERR_OOM, "workspace allocation of %zu bytes failed", sz);
+  }
+  c->ws_size = sz;
+  return MTPX_OK;
+}
+
+template <typename T>
+T* ws_take(Ctx* c, size_t count) {
+  const size_t off = (c->ws_used + 255) & ~(size_t)255;
+  c->ws_used = off + count * sizeof(T);
+  return reinterpret_cast<T*>(static_cast<char*>(c->ws) + off);
+}
+
+size_t al(size_t b) { return (b + 255) & ~(size_t)255; }
+
+int counters_reserve(Ctx* c, int n) {
+  if (n <= c->counters_n) return MTPX_OK;
+  if (c->counters) {
+    HIP_OK(hipStreamSynchronize(c->stream));
+    HIP_OK(hipFree(c->counters));
+  }
+  if (hipMalloc(&c->counters, sizeof(uint32_t) * n) != hipSuccess) return fail(MTPX_ERR_OOM, "counters");
+  HIP_OK(hipMemset(c->counters, 0, sizeof(uint32_t) * n));
+  c->counters_n = n;
+  return MTPX_OK;
+}
+
+Ctx* C(mtpx_ctx h) { return static_cast<Ctx*>(h.ctx); }
+
+int set_device(Ctx* c) {
+  HIP_OK(hipSetDevice(c->device));
+  return MTPX_OK;
+}
+
+bool gs_ok(int gs) { return gs == 32 || gs == 64; }
+
+// K limits of the GEMV: multiple of 32 and of gs, at most QMV_IT blocks per lane.
+bool k_ok(int K, int gs) {
+  if (K <= 0 || K % 32 || K % gs) return false;
+  const int nb = K / 32;
+  return nb <= QMV_IT * lanes_for_blocks(nb);
+}
+
+struct Kv {
+  Ctx* ctx;
+  int heads, dim;
+  int64_t tmax, offset = 0;
+  uint16_t *k = nullptr, *v = nullptr;
+};
+
+struct Layer {
+  mtpx_layer_config cfg;
+  mtpx_layer_weights w;
+  std::vector<void*> allocs;
+  int QW;
+};
+
+int moe_check(const mtpx_moe_weights* w, int M) {
+  ARG(w, "moe weights is NULL");
+  ARG(M >= 1 && M <= MAX_TOKENS, "M=%d outside 1..%d", M, MAX_TOKENS);
+  ARG(gs_ok(w->group_size), "group size %d not in {32, 64}", w->group_size);
+  ARG(w->top_k >= 1 && w->top_k <= MAX_TOPK && w->top_k <= w->experts, "top_k=%d", w->top_k);
+  ARG(w->experts >= 1 && w->experts <= 1024, "experts=%d outside 1..1024", w->experts);
+  ARG(w->hidden % 8 == 0 && w->hidden <= 4096, "hidden=%d", w->hidden);
+  ARG(k_ok(w->hidden, w->group_size), "hidden=%d not a supported GEMV depth", w->hidden);
+  ARG(k_ok(w->expert_width, w->group_size), "expert_width=%d not a supported GEMV depth", w->expert_width);
+  ARG(w->router && w->shared_gate && w->gate_w && w->up_w && w->down_w && w->sh_gate_w && w->sh_up_w &&
+          w->sh_down_w,
+      "missing MoE weight pointer");
+  return MTPX_OK;
+}
+
+size_t moe_ws_bytes(const mtpx_moe_weights* w, int M) {
+  const int H = w->hidden, E = w->experts, K = w->top_k, F = w->expert_width;
+  const int slots = M * (K + 1);
+  return al(4 * (size_t)M * E) + al(4 * (size_t)M) + al(4 * (size_t)M * K) * 2 + al(sizeof(MoeDispatch)) +
+         al(4 * (size_t)M * (H / 32) * XP_DW) + al(2 * (size_t)slots * F) + al(4 * (size_t)slots * (F / 32) * XP_DW) +
+         al(2 * (size_t)slots * H) + 4096;
+}
+
+// Enqueue the MoE block; workspace already reserved.
+int moe_enqueue(Ctx* c, const mtpx_moe_weights* w, const uint16_t* x, int M, uint16_t* y, int32_t* idx,
+                float* wts, float* logits) {
+  MoeArgs a;
+  a.H = w->hidden;
+  a.E = w->experts;
+  a.K = w->top_k;
+  a.F = w->expert_width;
+  a.gs = w->group_size;
+  a.M = M;
+  a.router = w->router;
+  a.shared_gate = w->shared_gate;
+  a.gate_w = w->gate_w; a.gate_s = w->gate_s; a.gate_b = w->gate_b;
+  a.up_w = w->up_w; a.up_s = w->up_s; a.up_b = w->up_b;
+  a.down_w = w->down_w; a.down_s = w->down_s; a.down_b = w->down_b;
+  a.sh_gate_w = w->sh_gate_w; a.sh_gate_s = w->sh_gate_s; a.sh_gate_b = w->sh_gate_b;
+  a.sh_up_w = w->sh_up_w; a.sh_up_s = w->sh_up_s; a.sh_up_b = w->sh_up_b;
+  a.sh_down_w = w->sh_down_w; a.sh_down_s = w->sh_down_s; a.sh_down_b = w->sh_down_b;
+  a.x = x;
+  a.y = y;
+  const int slots = M * (a.K + 1);
+  a.logits = logits ? logits : ws_take<float>(c, (size_t)M * a.E);
+  a.gate_logit = ws_take<float>(c, M);
+  a.idx = idx ? idx : ws_take<int32_t>(c, (size_t)M * a.K);
+  a.w = wts ? wts : ws_take<float>(c, (size_t)M * a.K);
+  a.disp = ws_take<MoeDispatch>(c, 1);
+  a.xp_x = ws_take<uint32_t>(c, (size_t)M * (a.H / 32) * XP_DW);
+  a.act = ws_take<uint16_t>(c, (size_t)slots * a.F);
+  a.xp_act = ws_take<uint32_t>(c, (size_t)slots * (a.F / 32) * XP_DW);
+  a.r = ws_take<uint16_t>(c, (size_t)slots * a.H);
+  int rc = counters_reserve(c, (a.H + DOWN_ROWS - 1) / DOWN_ROWS);
+  if (rc) return rc;
+  a.counters = c->counters;
+  c->last_disp = a.disp;
+  c->last_H = a.H;
+  c->last_E = a.E;
+  c->last_F = a.F;
+  c->last_gs = a.gs;
+  LAUNCH(c, "moe_router", launch_moe_router(a, c->stream));
+  LAUNCH(c, "moe_route", launch_moe_route(a, c->stream));
+  LAUNCH(c, "moe_gate_up", launch_moe_gate_up(a, c->stream));
+  LAUNCH(c, "moe_down", launch_moe_down(a, c->stream));
+  return MTPX_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* mtpx_last_error(void) { return g_err.c_str(); }
+const char* mtpx_version(void) { return "mtpx 0.1 gfx950"; }
+
+int mtpx_ctx_new(mtpx_ctx* out, int device) {
+  ARG(out, "out is NULL");
+  int n = 0;
+  HIP_OK(hipGetDeviceCount(&n));
+  ARG(device >= 0 && device < n, "device %d of %d", device, n);
+  Ctx* c = new Ctx();
+  c->device = device;
+  if (hipSetDevice(device) != hipSuccess || hipStreamCreateWithFlags(&c->own, hipStreamNonBlocking) != hipSuccess) {
+    delete c;
+    return fail(MTPX_ERR_HIP, "stream creation failed on device %d", device);
+  }
+  c->stream = c->own;
+  out->ctx = c;
+  return MTPX_OK;
+}
+
+int mtpx_ctx_free(mtpx_ctx h) {
+  Ctx* c = C(h);
+  if (!c) return MTPX_OK;
+  hipSetDevice(c->device);
+  hipStreamSynchronize(c->stream);
+  if (c->ws) hipFree(c->ws);
+  if (c->counters) hipFree(c->counters);
+  for (auto& r : c->pending) {
+    hipEventDestroy(r.a);
+    hipEventDestroy(r.b);
+  }
+  for (hipEvent_t e : c->ev_free) hipEventDestroy(e);
+  if (c->own) hipStreamDestroy(c->own);
+  delete c;
+  return MTPX_OK;
+}
+
+int mtpx_ctx_set_stream(mtpx_ctx h, void* s) {
+  Ctx* c = C(h);
+  ARG(c, "null context");
+  c->stream = static_cast<hipStream_t>(s);
+  return MTPX_OK;
+}
+
+int mtpx_ctx_use_own_stream(mtpx_ctx h) {
+  Ctx* c = C(h);
+  ARG(c, "null context");
+  c->stream = c->own;
+  return MTPX_OK;
+}
+
+int mtpx_ctx_synchronize(mtpx_ctx h) {
+  Ctx* c = C(h);
+  ARG(c, "null context");
+  HIP_OK(hipStreamSynchronize(c->stream));
+  return MTPX_OK;
+}
+
+int mtpx_affine_quantize(mtpx_ctx h, const uint16_t* w, int64_t rows, int K, int gs, uint32_t* wq, uint16_t* s,
+                         uint16_t* b) {
+  Ctx* c = C(h);
+  ARG(c && w && wq && s && b, "null argument");
+  ARG(gs_ok(gs) && K > 0 && K % gs == 0 && rows >= 0, "K=%d gs=%d rows=%lld", K, gs, (long long)rows);
+  if (set_device(c)) return MTPX_ERR_HIP;
+  HIP_OK(launch_quantize(w, rows, K, gs, wq, s, b, c->stream));
+  return MTPX_OK;
+}
+
+int mtpx_randn_bf16(mtpx_ctx h, uint16_t* out, int64_t n, uint64_t seed, uint32_t tensor, float sigma) {
+  Ctx* c = C(h);
+  ARG(c && out && n >= 0, "bad argument");
+  if (set_device(c)) return MTPX_ERR_HIP;
+  HIP_OK(launch_randn_bf16(out, n, seed, tensor, sigma, c->stream));
+  return MTPX_OK;
+}
+
+int mtpx_qmv(mtpx_ctx h, const uint32_t* wq, const uint16_t* s, const uint16_t* b, int N, int K, int gs,
+             const uint16_t* x, int M, uint16_t* y, float* yf) {
+  Ctx* c = C(h);
+  ARG(c && wq && s && b && x && y, "null argument");
+  ARG(N >= 1 && M >= 1 && M <= MAX_TOKENS, "N=%d M=%d", N, M);
+  ARG(gs_ok(gs) && k_ok(K, gs), "K=%d gs=%d unsupported", K, gs);
+  ARG((size_t)M * (K / 32) * XP_DW * 4 <= 160 * 1024, "M*K too large for one workgroup's LDS");
+  if (set_device(c)) return MTPX_ERR_HIP;
+  const size_t xpn = (size_t)M * (K / 32) * XP_DW;
+  int rc = ws_reserve(c, al(xpn * 4) + 256);
+  if (rc) return rc;
+  c->ws_used = 0;
+  uint32_t* xp = ws_take<uint32_t>(c, xpn);
+  LAUNCH(c, "xprep", launch_xprep(x, M, K, xp, c->stream));
+  LAUNCH(c, "qmv", launch_qmv(wq, s, b, N, K, gs, xp, M, y, yf, c->stream));
+  return MTPX_OK;
+}
+
+int mtpx_moe_forward(mtpx_ctx h, const mtpx_moe_weights* w, const uint16_t* x, int M, uint16_t* y, int32_t* idx,
+                     float* wts, float* logits, int32_t* n_unique) {
+  Ctx* c = C(h);
+  ARG(c && x && y, "null argument");
+  int rc = moe_check(w, M);
+  if (rc) return rc;
+  if (set_device(c)) return MTPX_ERR_HIP;
+  if ((rc = ws_reserve(c, moe_ws_bytes(w, M)))) return rc;
+  c->ws_used = 0;
+  if ((rc = moe_enqueue(c, w, x, M, y, idx, wts, logits))) return rc;
+  if (n_unique) HIP_OK(hipMemcpyAsync(n_unique, &c->last_disp->n_unique, 4, hipMemcpyDeviceToDevice, c->stream));
+  return MTPX_OK;
+}
+
+int mtpx_attn_prep(mtpx_ctx h, const uint16_t* qkv, int S, int QW, int HQ, int HK, int D, int rot,
+                   const uint16_t* qnorm, const uint16_t* knorm, float eps, const uint16_t* cos_t,
+                   const uint16_t* sin_t, int pos0, uint16_t* q, uint16_t* kc, uint16_t* vc, int64_t tmax) {
+  Ctx* c = C(h);
+  ARG(c && qkv && qnorm && knorm && cos_t && sin_t && q && kc && vc, "null argument");
+  ARG(S >= 1 && S <= MAX_TOKENS, "S=%d", S);
+  ARG(D >= 8 && D <= 256 && (D & (D - 1)) == 0, "head_dim=%d must be a power of two in 8..256", D);
+  ARG(HK >= 1 && HQ % HK == 0, "heads %d / kv heads %d", HQ, HK);
+  ARG(rot >= 2 && rot <= D && rot % 2 == 0, "rot=%d", rot);
+  ARG(QW >= 2 * HQ * D + 2 * HK * D, "QW=%d too small", QW);
+  ARG(pos0 >= 0 && pos0 + S <= tmax, "positions %d..%d beyond cache %lld", pos0, pos0 + S, (long long)tmax);
+  if (set_device(c)) return MTPX_ERR_HIP;
+  HIP_OK(launch_attn_prep(qkv, S, QW, HQ, HK, D, rot, qnorm, knorm, eps, cos_t, sin_t, pos0, q, kc, vc, tmax,
+                          c->stream));
+  return MTPX_OK;
+}
+
+int mtpx_attn_verify(mtpx_ctx h, const uint16_t* q, int S, int HQ, int HK, int D, const uint16_t* kc,
+                     const uint16_t* vc, int64_t tmax, int T, float scale, const uint16_t* qkv, int QW,
+                     int gate_off, uint16_t* out, uint16_t* out_gated) {
+  Ctx* c = C(h);
+  ARG(c && q && kc && vc, "null argument");
+  ARG(out || out_gated, "no output requested");
+  ARG(!out_gated || qkv, "out_gated needs qkv");
+  ARG(S >= 1 && S <= MAX_TOKENS && T >= S && T <= tmax, "S=%d T=%d tmax=%lld", S, T, (long long)tmax);
+  ARG(D >= 8 && D <= 256 && (D & (D - 1)) == 0, "head_dim=%d", D);
+  ARG(HK >= 1 && HQ % HK == 0, "heads %d / kv heads %d", HQ, HK);
+  {
+    const size_t R = (size_t)(HQ / HK) * S;
+    const size_t lds = R * D * 2 + 2 * (size_t)ATTN_CHUNK * D * 2 + R * ATTN_CHUNK * 4 + R * 8;
+    ARG(lds <= 160 * 1024, "GQA group %d x %d rows exceeds one workgroup's LDS", HQ / HK, S);
+  }
+  ARG(!out_gated || (gate_off >= 0 && gate_off + HQ * D <= QW), "gate columns outside qkv rows");
+  if (set_device(c)) return MTPX_ERR_HIP;
+  const size_t pf = attn_partial_floats(S, HQ, D, T);
+  int rc = ws_reserve(c, al(pf * 4) + 256);
+  if (rc) return rc;
+  c->ws_used = 0;
+  float* part = ws_take<float>(c, pf);
+  HIP_OK(launch_attn_verify(q, S, HQ, HK, D, kc, vc, tmax, T, scale, part, qkv, QW, gate_off, out, out_gated,
+                            c->stream));
+  return MTPX_OK;
+}
+
+int mtpx_rmsnorm(mtpx_ctx h, const uint16_t* x, const uint16_t* resid, int M, int H, const uint16_t* w, float eps,
+                 uint16_t* sum_out, uint16_t* y) {
+  Ctx* c = C(h);
+  ARG(c && x && w && y, "null argument");
+  ARG(M >= 1 && H >= 1, "M=%d H=%d", M, H);
+  if (set_device(c)) return MTPX_ERR_HIP;
+  HIP_OK(launch_rmsnorm(x, resid, M, H, w, eps, sum_out, y, c->stream));
+  return MTPX_OK;
+}
+
+int mtpx_kv_new(mtpx_ctx h, int kv_heads, int head_dim, int64_t tmax, mtpx_kv* out) {
+  Ctx* c = C(h);
+  ARG(c && out && kv_heads >= 1 && head_dim >= 1 && tmax >= 1, "bad argument");
+  if (set_device(c)) return MTPX_ERR_HIP;
+  Kv* kv = new Kv();
+  kv->ctx = c;
+  kv->heads = kv_heads;
+  kv->dim = head_dim;
+  kv->tmax = tmax;
+  const size_t bytes = (size_t)kv_heads * tmax * head_dim * 2;
+  if (hipMalloc(&kv->k, bytes) != hipSuccess || hipMalloc(&kv->v, bytes) != hipSuccess) {
+    if (kv->k) hipFree(kv->k);
+    delete kv;
+    return fail(MTPX_ERR_OOM, "kv cache of 2 x %zu bytes", bytes);
+  }
+  hipMemsetAsync(kv->k, 0, bytes, c->stream);
+  hipMemsetAsync(kv->v, 0, bytes, c->stream);
+  out->ctx = kv;
+  return MTPX_OK;
+}
+
+int mtpx_kv_free(mtpx_kv h) {
+  Kv* kv = static_cast<Kv*>(h.ctx);
+  if (!kv) return MTPX_OK;
+  hipStreamSynchronize(kv->ctx->stream);
+  hipFree(kv->k);
+  hipFree(kv->v);
+  delete kv;
+  return MTPX_OK;
+}
+
+int mtpx_kv_offset(mtpx_kv h, int64_t* off) {
+  Kv* kv = static_cast<Kv*>(h.ctx);
+  ARG(kv && off, "null argument");
+  *off = kv->offset;
+  return MTPX_OK;
+}
+
+int mtpx_kv_set_offset(mtpx_kv h, int64_t off) {
+  Kv* kv = static_cast<Kv*>(h.ctx);
+  ARG(kv && off >= 0 && off <= kv->tmax, "offset %lld outside 0..tmax", (long long)off);
+  kv->offset = off;
+  return MTPX_OK;
+}
+
+int mtpx_kv_trim(mtpx_kv h, int64_t n, int64_t* trimmed) {
+  Kv* kv = static_cast<Kv*>(h.ctx);
+  ARG(kv && n >= 0, "bad argument");
+  const int64_t t = n < kv->offset ? n : kv->offset;
+  kv->offset -= t;
+  if (trimmed) *trimmed = t;
+  return MTPX_OK;
+}
+
+int mtpx_kv_buffers(mtpx_kv h, uint16_t** k, uint16_t** v, int64_t* tmax) {
+  Kv* kv = static_cast<Kv*>(h.ctx);
+  ARG(kv, "null kv");
+  if (k) *k = kv->k;
+  if (v) *v = kv->v;
+  if (tmax) *tmax = kv->tmax;
+  return MTPX_OK;
+}
+
+int mtpx_argmax_rows(mtpx_ctx h, const float* x, int rows, int64_t V, int32_t* out) {
+  Ctx* c = C(h);
+  ARG(c && x && out && rows >= 1 && V >= 1 && V < (int64_t)1 << 31, "bad argument");
+  if (set_device(c)) return MTPX_ERR_HIP;
+  const size_t n = argmax_work_items(rows, V);
+  int rc = ws_reserve(c, al(n * 4) * 2 + 256);
+  if (rc) return rc;
+  c->ws_used = 0;
+  float* pv = ws_take<float>(c, n);
+  int32_t* pi = ws_take<int32_t>(c, n);
+  HIP_OK(launch_argmax_rows(x, rows, V, pv, pi, out, c->stream));
+  return MTPX_OK;
+}
+
+int mtpx_accept_greedy(mtpx_ctx h, const float* logits, int k, int64_t V, const int32_t* drafts, int32_t kv_offset,
+                       int32_t* out3) {
+  Ctx* c = C(h);
+  ARG(c && logits && out3 && (drafts || k == 0), "null argument");
+  ARG(k >= 0 && k + 1 <= MAX_TOKENS && V >= 1 && V < (int64_t)1 << 31, "k=%d V=%lld", k, (long long)V);
+  if (set_device(c)) return MTPX_ERR_HIP;
+  const size_t n = argmax_work_items(k + 1, V);
+  int rc = ws_reserve(c, al(n * 4) * 2 + 256);
+  if (rc) return rc;
+  c->ws_used = 0;
+  float* pv = ws_take<float>(c, n);
+  int32_t* pi = ws_take<int32_t>(c, n);
+  HIP_OK(launch_accept_greedy(logits, k, V, drafts, kv_offset, pv, pi, out3, c->stream));
+  return MTPX_OK;
+}
+
+int mtpx_accept_sample(mtpx_ctx h, const float* tlogits, const float* dlogits, int k, int64_t V,
+                       const int32_t* drafts, float temperature, uint64_t seed, uint64_t offset, int32_t kv_offset,
+                       int32_t* out3) {
+  Ctx* c = C(h);
+  ARG(c && tlogits && out3 && (k == 0 || (dlogits && drafts)), "null argument");
+  ARG(k >= 0 && k + 1 <= MAX_TOKENS && V >= 1 && V < (int64_t)1 << 31, "k=%d V=%lld", k, (long long)V);
+  ARG(temperature > 0.0f && std::isfinite(temperature), "temperature must be > 0");
+  if (set_device(c)) return MTPX_ERR_HIP;
+  const size_t n = accept_sample_work_floats(k, V);
+  int rc = ws_reserve(c, al(n * 4) + 256);
+  if (rc) return rc;
+  c->ws_used = 0;
+  float* work = ws_take<float>(c, n);
+  HIP_OK(launch_accept_sample(tlogits, dlogits, k, V, drafts, temperature, seed, offset, kv_offset, work, out3,
+                              c->stream));
+  return MTPX_OK;
+}
+
+// ---------------------------------------------------------------------------
+// decoder layer
+
+int mtpx_layer_new_random(mtpx_ctx h, const mtpx_layer_config* cfg, uint64_t seed, mtpx_layer* out) {
+  Ctx* c = C(h);
+  ARG(c && cfg && out, "null argument");
+  const int H = cfg->hidden, E = cfg->experts, F = cfg->expert_width, gs = cfg->group_size;
+  const int HQ = cfg->heads, HK = cfg->kv_heads, D = cfg->head_dim;
+  ARG(gs_ok(gs) && k_ok(H, gs) && k_ok(F, gs) && k_ok(HQ * D, gs), "unsupported GEMV depths");
+  ARG(HK >= 1 && HQ % HK == 0 && D <= 256 && cfg->rot_dims <= D && cfg->max_positions >= 1, "attention dims");
+  if (set_device(c)) return MTPX_ERR_HIP;
+  Layer* L = new Layer();
+  L->cfg = *cfg;
+  memset(&L->w, 0, sizeof(L->w));
+  const int QW = 2 * HQ * D + 2 * HK * D + cfg->index_dim;
+  L->QW = QW;
+  L->w.qkv_rows = QW;
+  auto alloc = [&](size_t bytes) -> void* {
+    void* p = nullptr;
+    if (hipMalloc(&p, bytes) != hipSuccess) return nullptr;
+    L->allocs.push_back(p);
+    return p;
+  };
+  bool ok = true;
+  uint32_t tensor = 1;
+  uint16_t* tmp = nullptr;
+  size_t tmp_n = 0;
+  auto qmat = [&](int64_t rows, int K, const uint32_t** w, const uint16_t** s, const uint16_t** b) {
+    uint32_t* pw = (uint32_t*)alloc((size_t)rows * K / 2);
+    uint16_t* ps = (uint16_t*)alloc((size_t)rows * (K / gs) * 2);
+    uint16_t* pb = (uint16_t*)alloc((size_t)rows * (K / gs) * 2);
+    if (!pw || !ps || !pb) {
+      ok = false;
+      return;
+    }
+    // generate and quantise in slices through one bf16 staging buffer
+    const int64_t slice = (int64_t)1 << 24;  // elements
+    const int64_t rows_per = slice / K > 0 ? slice / K : 1;
+    if (!tmp) {
+      tmp_n = (size_t)rows_per * K > (size_t)slice ? (size_t)rows_per * K : (size_t)slice;
+      if (hipMalloc(&tmp, tmp_n * 2) != hipSuccess) {
+        ok = false;
+        return;
+      }
+    }
+    for (int64_t r0 = 0; r0 < rows && ok; r0 += rows_per) {
+      const int64_t nr = rows - r0 < rows_per ? rows - r0 : rows_per;
+      if (launch_randn_bf16(tmp, nr * K, seed, tensor * 65536u + (uint32_t)(r0 / rows_per), 0.02f, c->stream) ||
+          launch_quantize(tmp, nr, K, gs, pw + r0 * (K / 8), ps + r0 * (K / gs), pb + r0 * (K / gs), c->stream))
+        ok = false;
+    }
+    ++tensor;
+    *w = pw;
+    *s = ps;
+    *b = pb;
+  };
+  auto dense = [&](int64_t n, float sigma) -> const uint16_t* {
+    uint16_t* p = (uint16_t*)alloc((size_t)n * 2);
+    if (!p) {
+      ok = false;
+      return nullptr;
+    }
+    if (sigma > 0.0f) {
+      if (launch_randn_bf16(p, n, seed, tensor * 65536u, sigma, c->stream)) ok = false;
+    } else if (launch_fill_bf16(p, n, 0x3f80, c->stream)) {
+      ok = false;
+    }
+    ++tensor;
+    return p;
+  };
+  L->w.attn_norm = dense(H, 0.0f);
+  L->w.post_norm = dense(H, 0.0f);
+  L->w.q_norm = dense(D, 0.0f);
+  L->w.k_norm = dense(D, 0.0f);
+  qmat(QW, H, &L->w.qkv_w, &L->w.qkv_s, &L->w.qkv_b);
+  qmat(H, HQ * D, &L->w.o_w, &L->w.o_s, &L->w.o_b);
+  mtpx_moe_weights& m = L->w.moe;
+  m.hidden = H;
+  m.experts = E;
+  m.top_k = cfg->top_k;
+  m.expert_width = F;
+  m.group_size = gs;
+  m.router = dense((int64_t)E * H, 0.02f);
+  m.shared_gate = dense(H, 0.02f);
+  qmat((int64_t)E * F, H, &m.gate_w, &m.gate_s, &m.gate_b);
+  qmat((int64_t)E * F, H, &m.up_w, &m.up_s, &m.up_b);
+  qmat((int64_t)E * H, F, &m.down_w, &m.down_s, &m.down_b);
+  qmat(F, H, &m.sh_gate_w, &m.sh_gate_s, &m.sh_gate_b);
+  qmat(F, H, &m.sh_up_w, &m.sh_up_s, &m.sh_up_b);
+  qmat(H, F, &m.sh_down_w, &m.sh_down_s, &m.sh_down_b);
+  // rotate-half RoPE tables: entry d uses theta^(-2*(d mod rot/2)/rot)
+  const int rot = cfg->rot_dims;
+  std::vector<uint16_t> ct((size_t)cfg->max_positions * rot), st((size_t)cfg->max_positions * rot);
+  auto tobf = [](float f) -> uint16_t {
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0;
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+  };
+  for (int64_t p = 0; p < cfg->max_positions; ++p)
+    for (int d = 0; d < rot; ++d) {
+      const int i = d % (rot / 2);
+      const double inv = std::pow((double)cfg->rope_theta, -2.0 * (double)i / (double)rot);
+      const double a = (double)p * inv;
+      ct[(size_t)p * rot + d] = tobf((float)std::cos(a));
+      st[(size_t)p * rot + d] = tobf((float)std::sin(a));
+    }
+  uint16_t* dc = (uint16_t*)alloc(ct.size() * 2);
+  uint16_t* ds = (uint16_t*)alloc(st.size() * 2);
+  if (dc && ds) {
+    if (hipMemcpyAsync(dc, ct.data(), ct.size() * 2, hipMemcpyHostToDevice, c->stream) != hipSuccess ||
+        hipMemcpyAsync(ds, st.data(), st.size() * 2, hipMemcpyHostToDevice, c->stream) != hipSuccess)
+      ok = false;
+  } else {
+    ok = false;
+  }
+  L->w.rope_cos = dc;
+  L->w.rope_sin = ds;
+  const hipError_t se = hipStreamSynchronize(c->stream);
+  if (tmp) hipFree(tmp);
+  if (!ok || se != hipSuccess) {
+    for (void* p : L->allocs) hipFree(p);
+    delete L;
+    return fail(ok ? MTPX_ERR_HIP : MTPX_ERR_OOM, "layer initialisation failed");
+  }
+  out->ctx = L;
+  return MTPX_OK;
+}
+
+int mtpx_layer_free(mtpx_layer h) {
+  Layer* L = static_cast<Layer*>(h.ctx);
+  if (!L) return MTPX_OK;
+  for (void* p : L->allocs) hipFree(p);
+  delete L;
+  return MTPX_OK;
+}
+
+int mtpx_layer_weights_get(mtpx_layer h, mtpx_layer_weights* out) {
+  Layer* L = static_cast<Layer*>(h.ctx);
+  ARG(L && out, "null argument");
+  *out = L->w;
+  return MTPX_OK;
+}
+
+int mtpx_layer_forward(mtpx_ctx h, mtpx_layer lh, mtpx_kv kvh, const uint16_t* x, int M, uint16_t* y) {
+  Ctx* c = C(h);
+  Layer* L = static_cast<Layer*>(lh.ctx);
+  Kv* kv = static_cast<Kv*>(kvh.ctx);
+  ARG(c && L && kv && x && y, "null argument");
+  const mtpx_layer_config& g = L->cfg;
+  ARG(M >= 1 && M <= MAX_TOKENS, "M=%d", M);
+  ARG(kv->heads == g.kv_heads && kv->dim == g.head_dim, "kv cache geometry does not match the layer");
+  ARG(kv->offset + M <= kv->tmax && kv->offset + M <= g.max_positions, "cache full (offset %lld + %d)",
+      (long long)kv->offset, M);
+  int rc = moe_check(&L->w.moe, M);
+  if (rc) return rc;
+  if (set_device(c)) return MTPX_ERR_HIP;
+  const int H = g.hidden, HQ = g.heads, HK = g.kv_heads, D = g.head_dim, QW = L->QW, gs = g.group_size;
+  const int T = (int)(kv->offset + M);
+  const size_t need = moe_ws_bytes(&L->w.moe, M) + al(2 * (size_t)M * H) * 4 + al(2 * (size_t)M * QW) +
+                      al(2 * (size_t)M * HQ * D) * 2 + al(4 * (size_t)M * ((QW > HQ * D ? QW : HQ * D) / 32) * XP_DW) +
+                      al(4 * attn_partial_floats(M, HQ, D, T)) + 4096;
+  if ((rc = ws_reserve(c, need))) return rc;
+  c->ws_used = 0;
+  uint16_t* h1 = ws_take<uint16_t>(c, (size_t)M * H);
+  uint16_t* qkv = ws_take<uint16_t>(c, (size_t)M * QW);
+  uint16_t* q = ws_take<uint16_t>(c, (size_t)M * HQ * D);
+  uint16_t* att = ws_take<uint16_t>(c, (size_t)M * HQ * D);
+  uint16_t* o = ws_take<uint16_t>(c, (size_t)M * H);
+  uint16_t* s = ws_take<uint16_t>(c, (size_t)M * H);
+  uint16_t* h2 = ws_take<uint16_t>(c, (size_t)M * H);
+  uint32_t* xp = ws_take<uint32_t>(c, (size_t)M * ((QW > HQ * D ? QW : HQ * D) / 32) * XP_DW);
+  float* part = ws_take<float>(c, attn_partial_floats(M, HQ, D, T));
+  hipStream_t st = c->stream;
+  LAUNCH(c, "rmsnorm", launch_rmsnorm(x, nullptr, M, H, L->w.attn_norm, g.eps, nullptr, h1, st));
+  LAUNCH(c, "xprep", launch_xprep(h1, M, H, xp, st));
+  LAUNCH(c, "qmv_qkv", launch_qmv(L->w.qkv_w, L->w.qkv_s, L->w.qkv_b, QW, H, gs, xp, M, qkv, nullptr, st));
+  LAUNCH(c, "attn_prep", launch_attn_prep(qkv, M, QW, HQ, HK, D, g.rot_dims, L->w.q_norm, L->w.k_norm, g.eps, L->w.rope_cos,
+                          L->w.rope_sin, (int)kv->offset, q, kv->k, kv->v, kv->tmax, st));
+  LAUNCH(c, "attn_verify", launch_attn_verify(q, M, HQ, HK, D, kv->k, kv->v, kv->tmax, T, 1.0f / std::sqrt((float)D), part, qkv, QW,
+                            HQ * D, nullptr, att, st));
+  LAUNCH(c, "xprep", launch_xprep(att, M, HQ * D, xp, st));
+  LAUNCH(c, "qmv_o", launch_qmv(L->w.o_w, L->w.o_s, L->w.o_b, H, HQ * D, gs, xp, M, o, nullptr, st));
+  LAUNCH(c, "rmsnorm", launch_rmsnorm(x, o, M, H, L->w.post_norm, g.eps, s, h2, st));
+  uint16_t* moe_out = h1;  // h1 is dead after the qkv GEMV
+  if ((rc = moe_enqueue(c, &L->w.moe, h2, M, moe_out, nullptr, nullptr, nullptr))) return rc;
+  LAUNCH(c, "add", launch_add(s, moe_out, (int64_t)M * H, y, st));
+  kv->offset += M;
+  return MTPX_OK;
+}
+
+int mtpx_profile_enable(mtpx_ctx h, int on) {
+  Ctx* c = C(h);
+  ARG(c, "null context");
+  c->prof = on != 0;
+  return MTPX_OK;
+}
+
+int mtpx_profile_reset(mtpx_ctx h) {
+  Ctx* c = C(h);
+  ARG(c, "null context");
+  int rc = prof_fold(c);
+  if (rc) return rc;
+  c->stats.clear();
+  return MTPX_OK;
+}
+
+int mtpx_profile_dump(mtpx_ctx h, char* buf, size_t n) {
+  Ctx* c = C(h);
+  ARG(c && buf && n > 0, "bad argument");
+  int rc = prof_fold(c);
+  if (rc) return rc;
+  std::string out;
+  for (auto& kv : c->stats) {
+    char line[160];
+    snprintf(line, sizeof(line), "%s %lld %.6f\n", kv.first.c_str(), (long long)kv.second.first, kv.second.second);
+    out += line;
+  }
+  ARG(out.size() < n, "buffer of %zu bytes too small", n);
+  memcpy(buf, out.c_str(), out.size() + 1);
+  return MTPX_OK;
+}
+
+int mtpx_last_moe_bytes(mtpx_ctx h, int64_t* bytes, int32_t* n_unique) {
+  Ctx* c = C(h);
+  ARG(c && bytes, "null argument");
+  ARG(c->last_disp, "no MoE call on this context yet");
+  if (set_device(c)) return MTPX_ERR_HIP;
+  int nu = 0;
+  HIP_OK(hipMemcpyAsync(&nu, &c->last_disp->n_unique, 4, hipMemcpyDeviceToHost, c->stream));
+  HIP_OK(hipStreamSynchronize(c->stream));
+  const int64_t H = c->last_H, E = c->last_E, F = c->last_F, gs = c->last_gs;
+  auto B = [&](int64_t N, int64_t K) { return N * K / 2 + 4 * N * K / gs; };
+  *bytes = (int64_t)(nu + 1) * (2 * B(F, H) + B(H, F)) + 2 * E * H + 2 * H;
+  if (n_unique) *n_unique = nu;
+  return MTPX_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,180 @@
+// mtpx device numerics for gfx950.
+//
+// Every routine here fixes an evaluation order; the kernels are compiled with
+// -ffp-contract=off so no multiply-add is fused unless written as fmaf.  The
+// affine-4-bit dot product is exact integer arithmetic: activations become
+// 24-bit fixed point per 32-element block (three byte limbs), nibble x limb
+// products are summed with v_dot4 integer instructions (exact and
+// order-independent), and only the per-block float combine is ordered.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mtpx {
+
+typedef uint16_t bf16;
+
+__device__ __forceinline__ float bf2f(bf16 h) { return __uint_as_float((uint32_t)h << 16); }
+
+// Round to nearest even; NaN -> 0x7fc0.
+__device__ __forceinline__ bf16 f2bf(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (bf16)(u >> 16);
+}
+
+__device__ __forceinline__ float round_bf(float f) { return bf2f(f2bf(f)); }
+
+// exp(x): Cody-Waite split with a two-part ln2, degree-7 Taylor polynomial on
+// |r| <= ln2/2, 2^n applied in two exact steps; x < -87.3 -> 0, x > 88.7 -> inf.
+__device__ __forceinline__ float expf_det(float x) {
+  if (x != x) return x;
+  if (x < -87.3f) return 0.0f;
+  if (x > 88.7f) return __uint_as_float(0x7f800000u);
+  const float n = __builtin_rintf(x * 1.44269504f);
+  float r = __builtin_fmaf(-n, 0.693145751953125f, x);
+  r = __builtin_fmaf(-n, 1.428606765330187e-06f, r);
+  float p = 1.98412698e-04f;
+  p = __builtin_fmaf(p, r, 1.38888889e-03f);
+  p = __builtin_fmaf(p, r, 8.33333333e-03f);
+  p = __builtin_fmaf(p, r, 4.16666667e-02f);
+  p = __builtin_fmaf(p, r, 1.66666667e-01f);
+  p = __builtin_fmaf(p, r, 0.5f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  const int ni = (int)n;
+  const int n1 = ni / 2, n2 = ni - n1;
+  p = p * __uint_as_float((uint32_t)(n1 + 127) << 23);
+  p = p * __uint_as_float((uint32_t)(n2 + 127) << 23);
+  return p;
+}
+
+// MLX Sigmoid functor in bf16 arithmetic (every operation rounds to bf16).
+__device__ __forceinline__ float sigmoid_bf16(float x) {
+  const float e = round_bf(expf_det(__builtin_fabsf(x)));
+  const float d = round_bf(1.0f + e);
+  const float y = round_bf(1.0f / d);
+  return (x < 0.0f) ? y : round_bf(1.0f - y);
+}
+
+__device__ __forceinline__ float silu_bf16(float x) { return round_bf(x * sigmoid_bf16(x)); }
+
+// Lanes sharing one row of the q4 GEMV: largest power of two <= 64 leaving
+// every lane at least 4 blocks of 32 elements.
+__host__ __device__ constexpr int lanes_for_blocks(int nb) {
+  int L = 1;
+  while (L < 64 && (L * 2) * 4 <= nb) L *= 2;
+  return L;
+}
+
+// ---------------------------------------------------------------------------
+// Prepared activation block: 26 dwords.
+//   [0..7]   limb 0 (bits 0-7 of m):   dwords e0 e1 e2 e3 o0 o1 o2 o3
+//   [8..15]  limb 1 (bits 8-15)
+//   [16..23] limb 2 (bits 16-23, signed byte)
+//   [24] p = 2^(E-149) as float bits, [25] SX = (float)(sum m) * p
+// e_t holds the limb bytes of elements 8t, 8t+2, 8t+4, 8t+6 and o_t those of
+// 8t+1, 8t+3, 8t+5, 8t+7 -- the byte order that (w & 0x0f0f0f0f) and
+// ((w >> 4) & 0x0f0f0f0f) give a packed weight word.
+constexpr int XP_DW = 26;
+
+__device__ __forceinline__ float block_scale(int E) {
+  return (E >= 23) ? __uint_as_float((uint32_t)(E - 22) << 23) : __uint_as_float(1u << E);
+}
+
+// Build one prepared block from 32 bf16 values (one thread does a block).
+__device__ inline void xprep_block(const bf16* __restrict__ x32, uint32_t* __restrict__ out) {
+  uint32_t h[32];
+  int E = 1;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) {
+    h[i] = x32[i];
+    int f = (h[i] >> 7) & 0xff;
+    f = f < 1 ? 1 : f;
+    E = f > E ? f : E;
+  }
+  uint32_t limb[3][8];
+#pragma unroll
+  for (int k = 0; k < 3; ++k)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) limb[k][j] = 0;
+  int32_t sm = 0;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) {
+    const int field = (h[i] >> 7) & 0xff;
+    const int f = field < 1 ? 1 : field;
+    const int32_t sig = (int32_t)((field ? 0x80u : 0u) | (h[i] & 0x7fu));
+    const int sh = f - E + 15;
+    int32_t mag = (sh >= 0) ? (sig << sh) : ((sh > -31) ? (sig >> (-sh)) : 0);
+    const int32_t m = (h[i] & 0x8000u) ? -mag : mag;
+    sm += m;
+    const uint32_t u = (uint32_t)m & 0xffffffu;
+    const int t = i >> 3, k8 = i & 7;
+    const int slot = (k8 & 1) ? 4 + t : t;  // odd elements -> o_t
+    const int byte = k8 >> 1;
+    limb[0][slot] |= (u & 0xffu) << (8 * byte);
+    limb[1][slot] |= ((u >> 8) & 0xffu) << (8 * byte);
+    limb[2][slot] |= ((u >> 16) & 0xffu) << (8 * byte);
+  }
+#pragma unroll
+  for (int k = 0; k < 3; ++k)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) out[k * 8 + j] = limb[k][j];
+  const float p = block_scale(E);
+  out[24] = __float_as_uint(p);
+  out[25] = __float_as_uint((float)sm * p);
+}
+
+// Exact nibble x limb sums of one 32-element block; w = 4 packed words.
+// Returns DXraw = fmaf((float)D2, 65536, (float)(D1*256 + D0)).
+__device__ __forceinline__ float block_dot(const uint32_t w[4], const uint32_t* __restrict__ xl) {
+  uint32_t d0 = 0, d1 = 0;
+  int32_t d2 = 0;
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const uint32_t lo = w[t] & 0x0f0f0f0fu;
+    const uint32_t hi = (w[t] >> 4) & 0x0f0f0f0fu;
+    d0 = __builtin_amdgcn_udot4(lo, xl[t], d0, false);
+    d0 = __builtin_amdgcn_udot4(hi, xl[4 + t], d0, false);
+    d1 = __builtin_amdgcn_udot4(lo, xl[8 + t], d1, false);
+    d1 = __builtin_amdgcn_udot4(hi, xl[12 + t], d1, false);
+    d2 = __builtin_amdgcn_sdot4((int)lo, (int)xl[16 + t], d2, false);
+    d2 = __builtin_amdgcn_sdot4((int)hi, (int)xl[20 + t], d2, false);
+  }
+  const int32_t low = (int32_t)(d1 * 256u + d0);
+  return __builtin_fmaf((float)d2, 65536.0f, (float)low);
+}
+
+// acc <- fmaf(b, SX, fmaf(s, DXraw * p, acc))
+__device__ __forceinline__ float block_accum(float acc, float dxraw, float s, float b,
+                                             const uint32_t* __restrict__ xl) {
+  const float p = __uint_as_float(xl[24]);
+  const float sx = __uint_as_float(xl[25]);
+  acc = __builtin_fmaf(s, dxraw * p, acc);
+  return __builtin_fmaf(b, sx, acc);
+}
+
+// xor butterfly over groups of L lanes (every lane of the group ends with the sum)
+template <int L>
+__device__ __forceinline__ float lane_fold(float v) {
+#pragma unroll
+  for (int off = L / 2; off >= 1; off /= 2) v = v + __shfl_xor(v, off, 64);
+  return v;
+}
+
+__device__ __forceinline__ float wave_fold64(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off /= 2) v = v + __shfl_xor(v, off, 64);
+  return v;
+}
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// 16-byte streaming load of packed weights (read once per step: non-temporal)
+__device__ __forceinline__ uint4 ldg16(const uint32_t* p) {
+  const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+}  // namespace mtpx

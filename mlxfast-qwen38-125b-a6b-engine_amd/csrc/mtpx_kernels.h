@@ -1,0 +1,101 @@
+// Kernel launchers shared by the C-ABI layer (host side) and the .hip files.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "mtpx_device.h"
+
+namespace mtpx {
+
+constexpr int QMV_IT = 8;        // max blocks per lane: K <= 8 * 32 * lanes_for_blocks(K/32)
+constexpr int MAX_TOKENS = 8;    // verify width ceiling (draft depth <= 7)
+constexpr int MAX_TOPK = 16;
+constexpr int ATTN_CHUNK = 64;   // keys per split-KV partial
+
+// Raise a kernel's dynamic-LDS limit to `bytes` (only when above what it has;
+// `cur` caches the value already set for that kernel).
+template <typename Kern>
+inline hipError_t ensure_lds(Kern* kernel, size_t bytes, size_t& cur) {
+  if (bytes <= cur || bytes <= 64 * 1024) return hipSuccess;
+  const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+  if (e == hipSuccess) cur = bytes;
+  return e;
+}
+
+// --- dense q4 GEMV and friends (qmv.hip)
+hipError_t launch_xprep(const bf16* x, int M, int K, uint32_t* xp, hipStream_t st);
+hipError_t launch_qmv(const uint32_t* wq, const bf16* s, const bf16* b, int N, int K, int gs,
+                      const uint32_t* xp, int M, bf16* y, float* yf, hipStream_t st);
+hipError_t launch_quantize(const bf16* w, int64_t rows, int K, int gs, uint32_t* wq, bf16* s, bf16* b,
+                           hipStream_t st);
+hipError_t launch_randn_bf16(bf16* out, int64_t n, uint64_t seed, uint32_t tensor, float sigma,
+                             hipStream_t st);
+hipError_t launch_fill_bf16(bf16* out, int64_t n, bf16 v, hipStream_t st);
+
+// --- MoE (moe.hip)
+struct MoeDispatch {
+  int n_unique;  // routed experts selected by at least one token (the shared expert is entry n_unique)
+  int pad[3];
+  int expert[MAX_TOKENS * MAX_TOPK + 1];
+  int count[MAX_TOKENS * MAX_TOPK + 1];
+  int16_t slot[MAX_TOKENS * MAX_TOPK + 1][MAX_TOKENS];  // m*K + k (routed) or M*K + m (shared)
+};
+
+struct MoeArgs {
+  int H, E, K, F, gs, M;
+  const bf16* router;       // [E, H]
+  const bf16* shared_gate;  // [H]
+  const uint32_t *gate_w, *up_w, *down_w;
+  const bf16 *gate_s, *gate_b, *up_s, *up_b, *down_s, *down_b;
+  const uint32_t *sh_gate_w, *sh_up_w, *sh_down_w;
+  const bf16 *sh_gate_s, *sh_gate_b, *sh_up_s, *sh_up_b, *sh_down_s, *sh_down_b;
+  // activations and workspace
+  const bf16* x;       // [M, H]
+  bf16* y;             // [M, H]
+  float* logits;       // [M, E]
+  float* gate_logit;   // [M]
+  int32_t* idx;        // [M, K]
+  float* w;            // [M, K]
+  MoeDispatch* disp;
+  uint32_t* xp_x;      // [M, H/32, XP_DW]
+  bf16* act;           // [M*(K+1), F]
+  uint32_t* xp_act;    // [M*(K+1), F/32, XP_DW]
+  bf16* r;             // [M*(K+1), H]
+  uint32_t* counters;  // [H / DOWN_ROWS] zero at rest
+};
+constexpr int DOWN_ROWS = 64;
+
+hipError_t launch_moe_router(const MoeArgs& a, hipStream_t st);
+hipError_t launch_moe_route(const MoeArgs& a, hipStream_t st);
+hipError_t launch_moe_gate_up(const MoeArgs& a, hipStream_t st);
+hipError_t launch_moe_down(const MoeArgs& a, hipStream_t st);
+hipError_t launch_moe_block(const MoeArgs& a, hipStream_t st);
+
+// --- attention (attn.hip)
+hipError_t launch_attn_prep(const bf16* qkv, int S, int QW, int HQ, int HK, int D, int ROT,
+                            const bf16* qnorm, const bf16* knorm, float eps, const bf16* cos_t,
+                            const bf16* sin_t, int pos0, bf16* q, bf16* kcache, bf16* vcache,
+                            int64_t tmax, hipStream_t st);
+hipError_t launch_attn_verify(const bf16* q, int S, int HQ, int HK, int D, const bf16* kc,
+                              const bf16* vc, int64_t tmax, int T, float scale, float* part,
+                              const bf16* qkv, int QW, int gate_off, bf16* out, bf16* out_gated,
+                              hipStream_t st);
+hipError_t launch_rmsnorm(const bf16* x, const bf16* resid, int M, int H, const bf16* w, float eps,
+                          bf16* sum_out, bf16* y, hipStream_t st);
+hipError_t launch_add(const bf16* a, const bf16* b, int64_t n, bf16* out, hipStream_t st);
+size_t attn_partial_floats(int S, int HQ, int D, int T);
+
+// --- acceptance (accept.hip)
+hipError_t launch_argmax_rows(const float* x, int rows, int64_t V, float* pval, int32_t* pidx,
+                              int32_t* out, hipStream_t st);
+hipError_t launch_accept_greedy(const float* logits, int k, int64_t V, const int32_t* drafts,
+                                int32_t kv_offset, float* pval, int32_t* pidx, int32_t* out3,
+                                hipStream_t st);
+hipError_t launch_accept_sample(const float* tlogits, const float* dlogits, int k, int64_t V,
+                                const int32_t* drafts, float temperature, uint64_t seed, uint64_t offset,
+                                int32_t kv_offset, float* work, int32_t* out3, hipStream_t st);
+size_t accept_sample_work_floats(int k, int64_t V);
+size_t argmax_work_items(int rows, int64_t V);
+
+}  // namespace mtpx

@@ -1,0 +1,215 @@
+"""mtpx -- Python host binding of the MI355X MTP speculative-decode step.
+
+Thin wrappers over the C ABI (include/mtpx.h).  torch is used only to own
+device memory: every compute call goes to libmtpx.so's HIP kernels; if the
+library is missing the import of any op raises.
+
+bf16 tensors are torch.bfloat16 (the C ABI sees their uint16 bit patterns).
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+from . import _lib
+from ._lib import Handle, LayerConfig, LayerWeights, MoEWeights, MtpxError, check
+
+__all__ = ["Context", "KVCache", "DecoderLayer", "MoEWeights", "LayerConfig", "MtpxError", "moe_weights_from"]
+
+
+def _ptr(t):
+    """A tensor's device address (or a raw address given as int)."""
+    if t is None:
+        return None
+    if isinstance(t, int):
+        return C.c_void_p(t)
+    assert t.is_contiguous(), "row-contiguous tensors only"
+    return C.c_void_p(t.data_ptr())
+
+
+class Context:
+    """A device, a HIP stream and a reusable workspace (mtpx_ctx)."""
+
+    def __init__(self, device: int = 0):
+        self.lib = _lib.lib()
+        self.h = Handle()
+        check(self.lib.mtpx_ctx_new(C.byref(self.h), device), "mtpx_ctx_new")
+        self.device = device
+        # run on torch's current stream so torch's fills and copies are ordered with the kernels
+        import torch
+        self.set_stream(torch.cuda.current_stream(device).cuda_stream)
+
+    def set_stream(self, stream: int):
+        check(self.lib.mtpx_ctx_set_stream(self.h, C.c_void_p(stream) if stream else None), "set_stream")
+
+    def close(self):
+        if self.h.ctx:
+            self.lib.mtpx_ctx_free(self.h)
+            self.h.ctx = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def synchronize(self):
+        check(self.lib.mtpx_ctx_synchronize(self.h), "synchronize")
+
+    # -- kernels ---------------------------------------------------------------------------
+    def affine_quantize(self, w, gs, wq, s, b):
+        K = w.shape[-1]
+        check(self.lib.mtpx_affine_quantize(self.h, _ptr(w), w.numel() // K, K, gs, _ptr(wq), _ptr(s), _ptr(b)),
+              "affine_quantize")
+
+    def randn_bf16(self, out, seed, tensor, sigma):
+        check(self.lib.mtpx_randn_bf16(self.h, _ptr(out), out.numel(), seed, tensor, sigma), "randn_bf16")
+
+    def qmv(self, wq, s, b, gs, x, y, yf=None):
+        K = x.shape[-1]
+        M = x.numel() // K
+        N = wq.numel() // (K // 8)
+        check(self.lib.mtpx_qmv(self.h, _ptr(wq), _ptr(s), _ptr(b), N, K, gs, _ptr(x), M, _ptr(y), _ptr(yf)),
+              "qmv")
+
+    def moe_forward(self, w: MoEWeights, x, y, idx=None, wts=None, logits=None, n_unique=None):
+        M = x.shape[0]
+        check(self.lib.mtpx_moe_forward(self.h, C.byref(w), _ptr(x), M, _ptr(y), _ptr(idx), _ptr(wts),
+                                        _ptr(logits), _ptr(n_unique)), "moe_forward")
+
+    def attn_prep(self, qkv, HQ, HK, D, rot, qnorm, knorm, eps, cos_t, sin_t, pos0, q, kcache, vcache,
+                  tmax=None):
+        S, QW = qkv.shape
+        tmax = kcache.shape[1] if tmax is None else tmax
+        check(self.lib.mtpx_attn_prep(self.h, _ptr(qkv), S, QW, HQ, HK, D, rot, _ptr(qnorm), _ptr(knorm), eps,
+                                      _ptr(cos_t), _ptr(sin_t), pos0, _ptr(q), _ptr(kcache), _ptr(vcache), tmax),
+              "attn_prep")
+
+    def attn_verify(self, q, kcache, vcache, T, scale, out=None, qkv=None, gate_off=0, out_gated=None,
+                    HK=None, tmax=None):
+        S, HQ, D = q.shape
+        if HK is None:
+            HK, tmax, _ = kcache.shape
+        QW = qkv.shape[1] if qkv is not None else 0
+        check(self.lib.mtpx_attn_verify(self.h, _ptr(q), S, HQ, HK, D, _ptr(kcache), _ptr(vcache), tmax, T,
+                                        scale, _ptr(qkv), QW, gate_off, _ptr(out), _ptr(out_gated)),
+              "attn_verify")
+
+    def rmsnorm(self, x, w, eps, y, resid=None, sum_out=None):
+        M, H = x.shape
+        check(self.lib.mtpx_rmsnorm(self.h, _ptr(x), _ptr(resid), M, H, _ptr(w), eps, _ptr(sum_out), _ptr(y)),
+              "rmsnorm")
+
+    def argmax_rows(self, x, out):
+        rows, V = x.shape
+        check(self.lib.mtpx_argmax_rows(self.h, _ptr(x), rows, V, _ptr(out)), "argmax_rows")
+
+    def accept_greedy(self, logits, drafts, kv_offset, out3):
+        k = drafts.numel()
+        check(self.lib.mtpx_accept_greedy(self.h, _ptr(logits), k, logits.shape[1], _ptr(drafts), kv_offset,
+                                          _ptr(out3)), "accept_greedy")
+
+    def accept_sample(self, tlogits, dlogits, drafts, temperature, seed, offset, kv_offset, out3):
+        k = drafts.numel()
+        check(self.lib.mtpx_accept_sample(self.h, _ptr(tlogits), _ptr(dlogits), k, tlogits.shape[1],
+                                          _ptr(drafts), temperature, seed, offset, kv_offset, _ptr(out3)),
+              "accept_sample")
+
+    def profile(self, on: bool = True):
+        check(self.lib.mtpx_profile_enable(self.h, 1 if on else 0), "profile_enable")
+
+    def profile_reset(self):
+        check(self.lib.mtpx_profile_reset(self.h), "profile_reset")
+
+    def profile_stats(self) -> dict:
+        """{kernel: (launches, total_ms)} from the events recorded on the context stream."""
+        buf = C.create_string_buffer(1 << 16)
+        check(self.lib.mtpx_profile_dump(self.h, buf, len(buf)), "profile_dump")
+        out = {}
+        for line in buf.value.decode().splitlines():
+            name, n, ms = line.split()
+            out[name] = (int(n), float(ms))
+        return out
+
+    def last_moe_bytes(self):
+        b = C.c_int64()
+        nu = C.c_int32()
+        check(self.lib.mtpx_last_moe_bytes(self.h, C.byref(b), C.byref(nu)), "last_moe_bytes")
+        return b.value, nu.value
+
+
+class KVCache:
+    """Contiguous bf16 K/V [kv_heads, tmax, head_dim] with offset rollback (mtpx_kv)."""
+
+    def __init__(self, ctx: Context, kv_heads: int, head_dim: int, tmax: int):
+        self.ctx = ctx
+        self.h = Handle()
+        check(ctx.lib.mtpx_kv_new(ctx.h, kv_heads, head_dim, tmax, C.byref(self.h)), "kv_new")
+
+    def close(self):
+        if self.h.ctx:
+            self.ctx.lib.mtpx_kv_free(self.h)
+            self.h.ctx = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def offset(self) -> int:
+        o = C.c_int64()
+        check(self.ctx.lib.mtpx_kv_offset(self.h, C.byref(o)), "kv_offset")
+        return o.value
+
+    @offset.setter
+    def offset(self, v: int):
+        check(self.ctx.lib.mtpx_kv_set_offset(self.h, v), "kv_set_offset")
+
+    def trim(self, n: int) -> int:
+        t = C.c_int64()
+        check(self.ctx.lib.mtpx_kv_trim(self.h, n, C.byref(t)), "kv_trim")
+        return t.value
+
+    def buffers(self):
+        k, v, tmax = C.c_void_p(), C.c_void_p(), C.c_int64()
+        check(self.ctx.lib.mtpx_kv_buffers(self.h, C.byref(k), C.byref(v), C.byref(tmax)), "kv_buffers")
+        return k.value, v.value, tmax.value
+
+
+class DecoderLayer:
+    """One full-shape attention + MoE decoder layer with seeded random weights (mtpx_layer)."""
+
+    def __init__(self, ctx: Context, cfg: LayerConfig, seed: int):
+        self.ctx = ctx
+        self.cfg = cfg
+        self.h = Handle()
+        check(ctx.lib.mtpx_layer_new_random(ctx.h, C.byref(cfg), seed, C.byref(self.h)), "layer_new_random")
+
+    def close(self):
+        if self.h.ctx:
+            self.ctx.lib.mtpx_layer_free(self.h)
+            self.h.ctx = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def weights(self) -> LayerWeights:
+        w = LayerWeights()
+        check(self.ctx.lib.mtpx_layer_weights_get(self.h, C.byref(w)), "layer_weights_get")
+        return w
+
+    def forward(self, kv: KVCache, x, y):
+        check(self.ctx.lib.mtpx_layer_forward(self.ctx.h, self.h, kv.h, _ptr(x), x.shape[0], _ptr(y)),
+              "layer_forward")
+
+
+def moe_weights_from(tensors: dict, H, E, K, F, gs) -> MoEWeights:
+    """Build the C struct from a dict of device tensors named like its fields."""
+    w = MoEWeights(H, E, K, F, gs)
+    for name, _ in MoEWeights._fields_[5:]:
+        setattr(w, name, tensors[name].data_ptr())
+    return w

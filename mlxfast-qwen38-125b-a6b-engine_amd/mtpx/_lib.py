@@ -1,0 +1,110 @@
+"""ctypes binding of libmtpx.so (the C ABI declared in include/mtpx.h).
+
+The library is required: there is no fallback path.  A missing or unloadable
+libmtpx.so raises immediately.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import re
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libmtpx.so")
+HEADER = os.path.join(os.path.dirname(os.path.dirname(HERE)), "include", "mtpx.h")
+
+P = C.c_void_p
+I32, I64, U32, U64, F32 = C.c_int32, C.c_int64, C.c_uint32, C.c_uint64, C.c_float
+INT = C.c_int
+
+
+class Handle(C.Structure):
+    _fields_ = [("ctx", P)]
+
+
+class MoEWeights(C.Structure):
+    _fields_ = [("hidden", INT), ("experts", INT), ("top_k", INT), ("expert_width", INT),
+                ("group_size", INT)] + [(n, P) for n in (
+                    "router", "shared_gate",
+                    "gate_w", "gate_s", "gate_b", "up_w", "up_s", "up_b", "down_w", "down_s", "down_b",
+                    "sh_gate_w", "sh_gate_s", "sh_gate_b", "sh_up_w", "sh_up_s", "sh_up_b",
+                    "sh_down_w", "sh_down_s", "sh_down_b")]
+
+
+class LayerConfig(C.Structure):
+    _fields_ = [(n, INT) for n in ("hidden", "experts", "top_k", "expert_width", "group_size", "heads",
+                                   "kv_heads", "head_dim", "rot_dims", "index_dim")] + [
+        ("rope_theta", F32), ("eps", F32), ("max_positions", I64)]
+
+
+class LayerWeights(C.Structure):
+    _fields_ = [(n, P) for n in ("attn_norm", "post_norm", "qkv_w", "qkv_s", "qkv_b", "q_norm", "k_norm",
+                                 "o_w", "o_s", "o_b", "rope_cos", "rope_sin")] + [
+        ("moe", MoEWeights), ("qkv_rows", INT)]
+
+
+_SIGS = {
+    "mtpx_last_error": (C.c_char_p, []),
+    "mtpx_version": (C.c_char_p, []),
+    "mtpx_ctx_new": (INT, [C.POINTER(Handle), INT]),
+    "mtpx_ctx_free": (INT, [Handle]),
+    "mtpx_ctx_set_stream": (INT, [Handle, P]),
+    "mtpx_ctx_use_own_stream": (INT, [Handle]),
+    "mtpx_ctx_synchronize": (INT, [Handle]),
+    "mtpx_affine_quantize": (INT, [Handle, P, I64, INT, INT, P, P, P]),
+    "mtpx_randn_bf16": (INT, [Handle, P, I64, U64, U32, F32]),
+    "mtpx_qmv": (INT, [Handle, P, P, P, INT, INT, INT, P, INT, P, P]),
+    "mtpx_moe_forward": (INT, [Handle, C.POINTER(MoEWeights), P, INT, P, P, P, P, P]),
+    "mtpx_attn_prep": (INT, [Handle, P, INT, INT, INT, INT, INT, INT, P, P, F32, P, P, INT, P, P, P, I64]),
+    "mtpx_attn_verify": (INT, [Handle, P, INT, INT, INT, INT, P, P, I64, INT, F32, P, INT, INT, P, P]),
+    "mtpx_rmsnorm": (INT, [Handle, P, P, INT, INT, P, F32, P, P]),
+    "mtpx_kv_new": (INT, [Handle, INT, INT, I64, C.POINTER(Handle)]),
+    "mtpx_kv_free": (INT, [Handle]),
+    "mtpx_kv_offset": (INT, [Handle, C.POINTER(I64)]),
+    "mtpx_kv_set_offset": (INT, [Handle, I64]),
+    "mtpx_kv_trim": (INT, [Handle, I64, C.POINTER(I64)]),
+    "mtpx_kv_buffers": (INT, [Handle, C.POINTER(P), C.POINTER(P), C.POINTER(I64)]),
+    "mtpx_argmax_rows": (INT, [Handle, P, INT, I64, P]),
+    "mtpx_accept_greedy": (INT, [Handle, P, INT, I64, P, I32, P]),
+    "mtpx_accept_sample": (INT, [Handle, P, P, INT, I64, P, F32, U64, U64, I32, P]),
+    "mtpx_layer_new_random": (INT, [Handle, C.POINTER(LayerConfig), U64, C.POINTER(Handle)]),
+    "mtpx_layer_free": (INT, [Handle]),
+    "mtpx_layer_weights_get": (INT, [Handle, C.POINTER(LayerWeights)]),
+    "mtpx_layer_forward": (INT, [Handle, Handle, Handle, P, INT, P]),
+    "mtpx_last_moe_bytes": (INT, [Handle, C.POINTER(I64), C.POINTER(I32)]),
+    "mtpx_profile_enable": (INT, [Handle, INT]),
+    "mtpx_profile_reset": (INT, [Handle]),
+    "mtpx_profile_dump": (INT, [Handle, C.c_char_p, C.c_size_t]),
+}
+
+_LIB = None
+
+
+class MtpxError(RuntimeError):
+    pass
+
+
+def header_symbols() -> list[str]:
+    """Every entry point declared in include/mtpx.h."""
+    txt = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(mtpx_\w+)\s*\(", txt, re.M)))
+
+
+def lib():
+    global _LIB
+    if _LIB is None:
+        if not os.path.exists(LIB_PATH):
+            raise MtpxError(f"{LIB_PATH} is not built; run __graft_entry__.build()")
+        L = C.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGS.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _LIB = L
+    return _LIB
+
+
+def check(rc: int, what: str = ""):
+    if rc != 0:
+        msg = lib().mtpx_last_error().decode(errors="replace")
+        raise MtpxError(f"{what} failed (code {rc}): {msg}")

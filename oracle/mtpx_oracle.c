@@ -804,7 +804,9 @@ void o_accept_sample(const float* tlogits, const float* dlogits, int k, int64_t 
     }
     row_probs(dlogits + (int64_t)(i - 1) * V, V, invT, pd);
     const int32_t d = drafts[i - 1];
-    if (u * pd[d] < pt[d]) continue;
+    /* a draft id outside the vocabulary is rejected */
+    const int ok = d >= 0 && d < V;
+    if (ok && u * pd[d] < pt[d]) continue;
     n = i - 1;
     for (int64_t v = 0; v < V; ++v) pd[v] = fmaxf(pt[v] - pd[v], 0.0f);
     tok = icdf(pd, V, u2);

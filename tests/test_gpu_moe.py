@@ -1,0 +1,100 @@
+"""GPU parity of the MoE block (router, top-k, expert-grouped gate|up + SwiGLU,
+down + combine) against the oracle: routed ids, weights, logits and the FFN
+output bit-exact.  Config 1 of BASELINE.json (H 2048, 64 experts, top-8 + shared,
+F 768, gs 64, M in {1, 4}) and the full expert shapes (H 2560, top-10, F 640) with
+a reduced expert count, at gs 32 and 64."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+from gpu_util import dev, empty_bf16, host, need_gpu, rand_bf16  # noqa: E402
+
+NAMES = ["router", "shared_gate", "gate_w", "gate_s", "gate_b", "up_w", "up_s", "up_b", "down_w", "down_s",
+         "down_b", "sh_gate_w", "sh_gate_s", "sh_gate_b", "sh_up_w", "sh_up_s", "sh_up_b", "sh_down_w",
+         "sh_down_s", "sh_down_b"]
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    need_gpu()
+    import mtpx
+    c = mtpx.Context(0)
+    yield c
+    c.close()
+
+
+def make_moe(seed, H, E, K, F, gs):
+    """Seeded N(0, 0.02) bf16 weights quantised to MLX affine 4-bit (the config-1 recipe)."""
+    r = np.random.default_rng(seed)
+
+    def q(rows, k):
+        return O.affine_quantize(rand_bf16(r, (rows, k), 0.02), gs)
+    w = {}
+    w["router"] = rand_bf16(r, (E, H), 0.02)
+    w["shared_gate"] = rand_bf16(r, (H,), 0.02)
+    for name, (rows, k) in {"gate": (E * F, H), "up": (E * F, H), "down": (E * H, F),
+                            "sh_gate": (F, H), "sh_up": (F, H), "sh_down": (H, F)}.items():
+        w[name + "_w"], w[name + "_s"], w[name + "_b"] = q(rows, k)
+    return w
+
+
+def run_case(ctx, w, H, E, K, F, gs, M, xseed):
+    import mtpx
+    r = np.random.default_rng(xseed)
+    x = rand_bf16(r, (M, H), 1.0)
+    ref = O.moe_block(w, x, H, E, K, F, gs)
+    dw = {n: dev(w[n]) for n in NAMES}
+    mw = mtpx.moe_weights_from(dw, H, E, K, F, gs)
+    y = empty_bf16(M, H)
+    idx = torch.zeros(M, K, dtype=torch.int32, device="cuda")
+    wt = torch.zeros(M, K, dtype=torch.float32, device="cuda")
+    lg = torch.zeros(M, E, dtype=torch.float32, device="cuda")
+    nu = torch.zeros(1, dtype=torch.int32, device="cuda")
+    ctx.moe_forward(mw, dev(x), y, idx, wt, lg, nu)
+    ctx.synchronize()
+    assert np.array_equal(host(lg).view(np.uint32), ref["logits"].view(np.uint32))
+    assert np.array_equal(host(idx), ref["idx"])
+    assert np.array_equal(host(wt).view(np.uint32), ref["w"].view(np.uint32))
+    assert int(host(nu)[0]) == len(np.unique(ref["idx"]))
+    got = host(y)
+    assert np.array_equal(got, ref["y"]), np.abs(O.bf16_to_f32(got) - O.bf16_to_f32(ref["y"])).max()
+    nbytes, n_unique = ctx.last_moe_bytes()
+    assert n_unique == len(np.unique(ref["idx"]))
+    B = lambda N, Kd: N * Kd // 2 + 4 * N * Kd // gs
+    assert nbytes == (n_unique + 1) * (2 * B(F, H) + B(H, F)) + 2 * E * H + 2 * H
+    return ref
+
+
+@pytest.mark.parametrize("M", [1, 4])
+def test_moe_config1_bit_exact(ctx, M):
+    print("case config1 M", M, flush=True)
+    H, E, K, F, gs = 2048, 64, 8, 768, 64
+    w = make_moe(0x5EED0001, H, E, K, F, gs)
+    run_case(ctx, w, H, E, K, F, gs, M, 0x5EED0002 + M)
+
+
+@pytest.mark.parametrize("gs,M", [(64, 1), (64, 6), (32, 2), (32, 8)])
+def test_moe_full_expert_shapes_bit_exact(ctx, gs, M):
+    print("case fullshape gs", gs, "M", M, flush=True)
+    H, E, K, F = 2560, 24, 10, 640
+    w = make_moe(1000 + gs, H, E, K, F, gs)
+    run_case(ctx, w, H, E, K, F, gs, M, 77 + M)
+
+
+def test_moe_router_ties_lowest_index(ctx):
+    print("case router ties", flush=True)
+    H, E, K, F, gs = 256, 16, 4, 64, 32
+    w = make_moe(5, H, E, K, F, gs)
+    # identical router rows 3, 9, 12 -> identical logits; lower index must win
+    w["router"][9] = w["router"][3]
+    w["router"][12] = w["router"][3]
+    ref = run_case(ctx, w, H, E, K, F, gs, 3, 9)
+    for m in range(3):
+        sel = list(ref["idx"][m])
+        for a, b in ((3, 9), (9, 12), (3, 12)):
+            if b in sel:
+                assert a in sel and sel.index(a) < sel.index(b)

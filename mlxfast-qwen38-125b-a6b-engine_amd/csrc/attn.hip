@@ -71,83 +71,90 @@ __global__ void k_attn_prep(const bf16* __restrict__ qkv, int S, int QW, int HQ,
   }
 }
 
-// part layout: [(hk * nch + c) * R + ri] * (D + 2): {m, l, o[0..D)}, R = S * G
+// part layout: [(hk * nch + c) * R + ri] * (D + 2): {m, l, o[0..D)}, R = S * G,
+// ri = s * G + g.  grid (nch, HK, S): one workgroup per (key chunk, kv head,
+// query); its rows are the G query heads of the group.
 __global__ __launch_bounds__(256) void k_attn_partial(const bf16* __restrict__ q, int S, int HQ, int HK, int D,
                                                       const bf16* __restrict__ kc, const bf16* __restrict__ vc,
                                                       int64_t tmax, int T, float scale, int nch,
                                                       float* __restrict__ part) {
   extern __shared__ float smem[];
-  const int c = blockIdx.x, hk = blockIdx.y;
+  const int c = blockIdx.x, hk = blockIdx.y, s = blockIdx.z;
   const int G = HQ / HK, R = S * G, C = ATTN_CHUNK;
   const int i0 = c * C;
-  bf16* qb = reinterpret_cast<bf16*>(smem);                 // [R][D]
-  bf16* kb = qb + (size_t)R * D;                            // [C][D]
-  bf16* vb = kb + (size_t)C * D;                            // [C][D]
-  float* sc = reinterpret_cast<float*>(vb + (size_t)C * D);  // [R][C]
-  float* ml = sc + (size_t)R * C;                           // [R][2]
-  for (int i = threadIdx.x; i < R * D; i += blockDim.x) {
-    const int ri = i / D, d = i % D;
-    const int s = ri / G, g = ri % G;
-    qb[i] = q[((size_t)s * HQ + hk * G + g) * D + d];
+  const int last = T - S + s;                // last key visible to this query
+  int n = last + 1 - i0;                     // visible keys of the chunk (a prefix)
+  n = n < 0 ? 0 : (n > C ? C : n);
+  // K rows padded by one dword: lanes walking different keys hit different banks
+  const int KS = D / 2 + 1;
+  uint32_t* qb = reinterpret_cast<uint32_t*>(smem);         // [G][D/2] bf16 pairs
+  uint32_t* kb = qb + (size_t)G * (D / 2);                  // [C][KS]
+  bf16* vb = reinterpret_cast<bf16*>(kb + (size_t)C * KS);  // [C][D]
+  float* sc = reinterpret_cast<float*>(vb + (size_t)C * D); // [G][C]
+  float* ml = sc + (size_t)G * C;                           // [G][2]
+  const uint32_t* q32 = reinterpret_cast<const uint32_t*>(q);
+  const uint32_t* k32 = reinterpret_cast<const uint32_t*>(kc);
+  const uint32_t* v32 = reinterpret_cast<const uint32_t*>(vc);
+  for (int i = threadIdx.x; i < G * (D / 2); i += blockDim.x) {
+    const int g = i / (D / 2), d2 = i % (D / 2);
+    qb[i] = q32[(((size_t)s * HQ + hk * G + g) * D) / 2 + d2];
   }
-  for (int i = threadIdx.x; i < C * D; i += blockDim.x) {
-    const int j = i / D, d = i % D;
-    const int key = i0 + j;
-    kb[i] = key < T ? kc[((size_t)hk * tmax + key) * D + d] : (bf16)0;
-    vb[i] = key < T ? vc[((size_t)hk * tmax + key) * D + d] : (bf16)0;
+  for (int i = threadIdx.x; i < n * (D / 2); i += blockDim.x) {
+    const int j = i / (D / 2), d2 = i % (D / 2);
+    const size_t src = (((size_t)hk * tmax + i0 + j) * D) / 2 + d2;
+    kb[j * KS + d2] = k32[src];
+    reinterpret_cast<uint32_t*>(vb)[j * (D / 2) + d2] = v32[src];
   }
   __syncthreads();
-  for (int p = threadIdx.x; p < R * C; p += blockDim.x) {
-    const int ri = p / C, j = p % C;
-    const int s = ri / G;
-    const int last = T - S + s;
-    const int key = i0 + j;
+  for (int p = threadIdx.x; p < G * C; p += blockDim.x) {
+    const int g = p / C, j = p % C;
     float acc = 0.0f;
-    if (key <= last) {
-      const bf16* qr = qb + (size_t)ri * D;
-      const bf16* kr = kb + (size_t)j * D;
-      for (int d = 0; d < D; ++d) acc = __builtin_fmaf(scale * bf2f(qr[d]), bf2f(kr[d]), acc);
+    if (j < n) {
+      const uint32_t* qr = qb + (size_t)g * (D / 2);
+      const uint32_t* kr = kb + (size_t)j * KS;
+      for (int d2 = 0; d2 < D / 2; ++d2) {
+        const uint32_t qq = qr[d2], kk = kr[d2];
+        acc = __builtin_fmaf(scale * __uint_as_float(qq << 16), __uint_as_float(kk << 16), acc);
+        acc = __builtin_fmaf(scale * __uint_as_float(qq & 0xffff0000u), __uint_as_float(kk & 0xffff0000u), acc);
+      }
     }
     sc[p] = acc;
   }
   __syncthreads();
-  for (int ri = threadIdx.x; ri < R; ri += blockDim.x) {
-    const int s = ri / G;
-    const int last = T - S + s;
-    int n = last + 1 - i0;
-    n = n < 0 ? 0 : (n > C ? C : n);
+  for (int g = threadIdx.x; g < G; g += blockDim.x) {
     float mx = -__uint_as_float(0x7f800000u);
-    for (int j = 0; j < n; ++j) mx = sc[ri * C + j] > mx ? sc[ri * C + j] : mx;
+    for (int j = 0; j < n; ++j) mx = sc[g * C + j] > mx ? sc[g * C + j] : mx;
     float l = 0.0f;
     for (int j = 0; j < n; ++j) {
-      const float e = expf_det(sc[ri * C + j] - mx);
-      sc[ri * C + j] = e;
+      const float e = expf_det(sc[g * C + j] - mx);
+      sc[g * C + j] = e;
       l = l + e;
     }
-    ml[2 * ri] = (n > 0) ? mx : -__uint_as_float(0x7f800000u);
-    ml[2 * ri + 1] = (n > 0) ? l : 0.0f;
-    for (int j = n; j < C; ++j) sc[ri * C + j] = 0.0f;
+    ml[2 * g] = (n > 0) ? mx : -__uint_as_float(0x7f800000u);
+    ml[2 * g + 1] = (n > 0) ? l : 0.0f;
   }
   __syncthreads();
-  for (int p = threadIdx.x; p < R * D; p += blockDim.x) {
-    const int ri = p / D, d = p % D;
-    const int s = ri / G;
-    int n = T - S + s + 1 - i0;
-    n = n < 0 ? 0 : (n > C ? C : n);
+  for (int p = threadIdx.x; p < G * D; p += blockDim.x) {
+    const int g = p / D, d = p % D;
     float o = 0.0f;
-    for (int j = 0; j < n; ++j) o = __builtin_fmaf(sc[ri * C + j], bf2f(vb[(size_t)j * D + d]), o);
-    float* dst = part + (((size_t)hk * nch + c) * R + ri) * (D + 2);
+    for (int j = 0; j < n; ++j) o = __builtin_fmaf(sc[g * C + j], bf2f(vb[(size_t)j * D + d]), o);
+    float* dst = part + (((size_t)hk * nch + c) * R + s * G + g) * (D + 2);
     dst[2 + d] = o;
     if (d == 0) {
-      dst[0] = ml[2 * ri];
-      dst[1] = ml[2 * ri + 1];
+      dst[0] = ml[2 * g];
+      dst[1] = ml[2 * g + 1];
     }
   }
 }
 
-__global__ void k_attn_combine(const float* __restrict__ part, int S, int HQ, int HK, int D, int nch,
-                               const bf16* __restrict__ qkv, int QW, int gate_off, bf16* __restrict__ out,
-                               bf16* __restrict__ out_gated) {
+// grid (R, HK), min(D, 256) threads.  Fold the chunk partials in chunk order,
+// then bf16 output, the sigmoid gate, and (optionally) the prepared activation
+// blocks of the gated row for the o_proj GEMV (32 lanes per block).
+__global__ __launch_bounds__(256) void k_attn_combine(const float* __restrict__ part, int S, int HQ, int HK, int D,
+                                                      int nch, const bf16* __restrict__ qkv, int QW, int gate_off,
+                                                      bf16* __restrict__ out, bf16* __restrict__ out_gated,
+                                                      uint32_t* __restrict__ xp_gated) {
+  __shared__ uint32_t scratch[8][24];
   const int ri = blockIdx.x, hk = blockIdx.y;
   const int G = HQ / HK, R = S * G;
   const int s = ri / G, h = hk * G + ri % G;
@@ -156,29 +163,49 @@ __global__ void k_attn_combine(const float* __restrict__ part, int S, int HQ, in
     const float* p = part + (((size_t)hk * nch + c) * R + ri) * (D + 2);
     if (p[1] > 0.0f && p[0] > M) M = p[0];
   }
-  for (int d = threadIdx.x; d < D; d += blockDim.x) {
-    float L = 0.0f, O = 0.0f;
-    for (int c = 0; c < nch; ++c) {
-      const float* p = part + (((size_t)hk * nch + c) * R + ri) * (D + 2);
-      if (!(p[1] > 0.0f)) continue;
-      const float f = expf_det(p[0] - M);
-      L = __builtin_fmaf(p[1], f, L);
-      O = __builtin_fmaf(p[2 + d], f, O);
+  for (int d0 = 0; d0 < D; d0 += blockDim.x) {  // uniform loop (barriers inside)
+    const int d = d0 + threadIdx.x;
+    bf16 gated = 0;
+    if (d < D) {
+      float L = 0.0f, O = 0.0f;
+      for (int c = 0; c < nch; ++c) {
+        const float* p = part + (((size_t)hk * nch + c) * R + ri) * (D + 2);
+        if (!(p[1] > 0.0f)) continue;
+        const float f = expf_det(p[0] - M);
+        L = __builtin_fmaf(p[1], f, L);
+        O = __builtin_fmaf(p[2 + d], f, O);
+      }
+      const bf16 att = f2bf(O / L);
+      if (out) out[((size_t)s * HQ + h) * D + d] = att;
+      if (out_gated) {
+        const float g = bf2f(qkv[(size_t)s * QW + gate_off + h * D + d]);
+        gated = f2bf(bf2f(att) * sigmoid_bf16(g));
+        out_gated[(size_t)s * HQ * D + h * D + d] = gated;
+      }
     }
-    const bf16 att = f2bf(O / L);
-    if (out) out[((size_t)s * HQ + h) * D + d] = att;
-    if (out_gated) {
-      const float g = bf2f(qkv[(size_t)s * QW + gate_off + h * D + d]);
-      out_gated[(size_t)s * HQ * D + h * D + d] = f2bf(bf2f(att) * sigmoid_bf16(g));
+    if (xp_gated) {
+      // block (h*D + d) / 32 of row s; D % 32 == 0 so blocks never straddle heads
+      const int grp = threadIdx.x >> 5, i = threadIdx.x & 31;
+      int E, sm;
+      xprep_lanes_build(gated, i, scratch[grp], E, sm);
+      __syncthreads();
+      if (d < D) {
+        const size_t blk = (size_t)s * (HQ * D / 32) + (h * D + d0) / 32 + grp;
+        xprep_lanes_store(i, scratch[grp], E, sm, xp_gated + blk * XP_DW);
+      }
+      __syncthreads();
     }
   }
 }
 
-// y = bf16(w * bf16(h * inv)), h = x or bf16(x + resid); 256 threads per row.
+// Row RMSNorm, 256 threads per row: h = x or bf16(x + resid); y = bf16(w * bf16(h * inv)).
+// With xp != nullptr also writes the prepared activation blocks of y (32 lanes per block).
 __global__ __launch_bounds__(256) void k_rmsnorm(const bf16* __restrict__ x, const bf16* __restrict__ resid,
                                                  int H, const bf16* __restrict__ w, float eps,
-                                                 bf16* __restrict__ sum_out, bf16* __restrict__ y) {
+                                                 bf16* __restrict__ sum_out, bf16* __restrict__ y,
+                                                 uint32_t* __restrict__ xp) {
   __shared__ float wsum[4];
+  __shared__ uint32_t scratch[8][24];
   const int m = blockIdx.x, t = threadIdx.x;
   const bf16* xr = x + (size_t)m * H;
   const bf16* rr = resid ? resid + (size_t)m * H : nullptr;
@@ -196,10 +223,23 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const bf16* __restrict__ x, con
   __syncthreads();
   const float total = ((wsum[0] + wsum[1]) + wsum[2]) + wsum[3];
   const float inv = 1.0f / sqrtf(total / (float)H + eps);
-  for (int i = t; i < H; i += 256) {
-    float v = bf2f(xr[i]);
-    if (rr) v = round_bf(v + bf2f(rr[i]));
-    y[(size_t)m * H + i] = f2bf(bf2f(w[i]) * round_bf(v * inv));
+  for (int i0 = 0; i0 < H; i0 += 256) {  // uniform loop (barriers inside)
+    const int i = i0 + t;
+    bf16 out = 0;
+    if (i < H) {
+      float v = bf2f(xr[i]);
+      if (rr) v = round_bf(v + bf2f(rr[i]));
+      out = f2bf(bf2f(w[i]) * round_bf(v * inv));
+      y[(size_t)m * H + i] = out;
+    }
+    if (xp) {
+      const int grp = t >> 5, li = t & 31;
+      int E, sm;
+      xprep_lanes_build(out, li, scratch[grp], E, sm);
+      __syncthreads();
+      if (i < H) xprep_lanes_store(li, scratch[grp], E, sm, xp + ((size_t)m * (H / 32) + i / 32) * XP_DW);
+      __syncthreads();
+    }
   }
 }
 
@@ -210,7 +250,7 @@ __global__ void k_add(const bf16* __restrict__ a, const bf16* __restrict__ b, in
 
 // ---------------------------------------------------------------------------
 size_t attn_partial_floats(int S, int HQ, int D, int T) {
-  const int nch = (T + ATTN_CHUNK - 1) / ATTN_CHUNK;
+  const int nch = (T + ATTN_CHUNK - 1) / ATTN_CHUNK;  // chunks of ATTN_CHUNK keys
   return (size_t)nch * S * HQ * (D + 2);
 }
 
@@ -224,24 +264,29 @@ hipError_t launch_attn_prep(const bf16* qkv, int S, int QW, int HQ, int HK, int 
 
 hipError_t launch_attn_verify(const bf16* q, int S, int HQ, int HK, int D, const bf16* kc, const bf16* vc,
                               int64_t tmax, int T, float scale, float* part, const bf16* qkv, int QW, int gate_off,
-                              bf16* out, bf16* out_gated, hipStream_t st) {
+                              bf16* out, bf16* out_gated, uint32_t* xp_gated, hipStream_t st) {
   const int nch = (T + ATTN_CHUNK - 1) / ATTN_CHUNK;
   const int G = HQ / HK, R = S * G;
-  const size_t lds = (size_t)R * D * 2 + 2 * (size_t)ATTN_CHUNK * D * 2 + (size_t)R * ATTN_CHUNK * 4 + (size_t)R * 8;
+  const size_t lds = attn_partial_lds(HQ / HK, D);
   static size_t cur = 0;
   hipError_t e = ensure_lds(k_attn_partial, lds, cur);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(k_attn_partial, dim3(nch, HK), dim3(256), lds, st, q, S, HQ, HK, D, kc, vc, tmax, T, scale, nch,
-                     part);
+  hipLaunchKernelGGL(k_attn_partial, dim3(nch, HK, S), dim3(256), lds, st, q, S, HQ, HK, D, kc, vc, tmax, T, scale,
+                     nch, part);
   if ((e = hipGetLastError()) != hipSuccess) return e;
   hipLaunchKernelGGL(k_attn_combine, dim3(R, HK), dim3(D < 256 ? D : 256), 0, st, part, S, HQ, HK, D, nch, qkv, QW,
-                     gate_off, out, out_gated);
+                     gate_off, out, out_gated, xp_gated);
   return hipGetLastError();
 }
 
+size_t attn_partial_lds(int G, int D) {
+  return (size_t)G * D * 2 + (size_t)ATTN_CHUNK * (D + 2) * 2 + (size_t)ATTN_CHUNK * D * 2 +
+         (size_t)G * ATTN_CHUNK * 4 + (size_t)G * 8;
+}
+
 hipError_t launch_rmsnorm(const bf16* x, const bf16* resid, int M, int H, const bf16* w, float eps, bf16* sum_out,
-                          bf16* y, hipStream_t st) {
-  hipLaunchKernelGGL(k_rmsnorm, dim3(M), dim3(256), 0, st, x, resid, H, w, eps, sum_out, y);
+                          bf16* y, uint32_t* xp, hipStream_t st) {
+  hipLaunchKernelGGL(k_rmsnorm, dim3(M), dim3(256), 0, st, x, resid, H, w, eps, sum_out, y, xp);
   return hipGetLastError();
 }
 

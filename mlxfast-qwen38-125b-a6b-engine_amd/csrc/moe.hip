@@ -6,15 +6,16 @@
 //   gate_up: per (32-row block of F, selected expert): gate and up rows of the
 //            expert against every token routed to it, SwiGLU, and the block
 //            preparation of the activation for the down projection
-//   down   : per (64-row block of H, selected expert): down rows against the
-//            expert's activations; the last workgroup to finish a row block
-//            folds the routed outputs in rank order and adds the gated shared
-//            expert (MLX col_reduce_small association)
+//   down   : per (128-row block of H, selected expert): down rows against the
+//            expert's activations -> routed/shared outputs per slot
+//   combine: per (token, 256 rows of H): fold the routed outputs in rank order,
+//            add the sigmoid-gated shared expert (MLX col_reduce_small
+//            association), optionally add the residual stream
 // Reference: FM/TrackFastModel.swift:867-954 (orchestration),
 // FM/TrackFastMoE.swift:780-911 (route), :1192-1404 (gate|up+act),
 // :1412-1576 (down+combine), :2246-2310 (router GEMV),
 // FM/TrackFastKernels2.swift:21-58,512-544 (sigmoid, colsum fold, combine).
-#include "mtpx_kernels.h"
+#include "qrows.h"
 
 namespace mtpx {
 
@@ -27,10 +28,17 @@ constexpr int ROUTER_IT = 8;  // H <= 8 * 64 * 8
 __global__ __launch_bounds__(256) void k_moe_router(MoeArgs a, int row_wgs) {
   const int H = a.H, E = a.E, M = a.M;
   if ((int)blockIdx.x >= row_wgs) {
-    // activation block preparation of x for the expert GEMVs
+    // activation block preparation of x for the expert GEMVs: 32 lanes per block
+    __shared__ uint32_t scratch[8][24];
     const int nb = H / 32;
-    const int i = ((int)blockIdx.x - row_wgs) * blockDim.x + threadIdx.x;
-    if (i < M * nb) xprep_block(a.x + (size_t)(i / nb) * H + (size_t)(i % nb) * 32, a.xp_x + (size_t)i * XP_DW);
+    const int g = threadIdx.x >> 5, i = threadIdx.x & 31;
+    const int blk = ((int)blockIdx.x - row_wgs) * 8 + g;
+    const bool valid = blk < M * nb;
+    const uint32_t h = valid ? a.x[(size_t)(blk / nb) * H + (size_t)(blk % nb) * 32 + i] : 0u;
+    int E, sm;
+    xprep_lanes_build(h, i, scratch[g], E, sm);
+    __syncthreads();
+    if (valid) xprep_lanes_store(i, scratch[g], E, sm, a.xp_x + (size_t)blk * XP_DW);
     return;
   }
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -72,31 +80,40 @@ __global__ __launch_bounds__(256) void k_moe_router(MoeArgs a, int row_wgs) {
 }
 
 // ---------------------------------------------------------------------------
-// route: wave m selects token m's top-k; then thread 0 builds the dispatch.
+// route: wave m selects token m's top-k; then the dispatch table is built in
+// LDS by all threads: each expert once (ordered by its first (token, rank)
+// slot), with its slots ordered by token.
 constexpr int ROUTE_EPER = 16;  // E <= 1024
 
 __global__ __launch_bounds__(512) void k_moe_route(MoeArgs a) {
   const int E = a.E, K = a.K, M = a.M;
+  const int MK = M * K;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  __shared__ int sel[MAX_TOKENS][MAX_TOPK];
+  __shared__ int sel[MAX_TOKENS * MAX_TOPK];
   __shared__ float selv[MAX_TOKENS][MAX_TOPK];
+  __shared__ int first[1024];
+  __shared__ uint32_t tokbits[MAX_TOKENS][32];  // expert membership per token
+  __shared__ uint64_t leadmask[2];
+  __shared__ int uid[MAX_TOKENS * MAX_TOPK];
+  for (int i = threadIdx.x; i < E; i += blockDim.x) first[i] = 0x7fffffff;
+  for (int i = threadIdx.x; i < MAX_TOKENS * 32; i += blockDim.x) (&tokbits[0][0])[i] = 0u;
+  __syncthreads();
   if (wave < M) {
     const float* lr = a.logits + (size_t)wave * E;
     float v[ROUTE_EPER];
+    uint32_t taken = 0;  // bit j: expert lane + 64*j already selected (or absent)
 #pragma unroll
     for (int j = 0; j < ROUTE_EPER; ++j) {
       const int e = lane + 64 * j;
       v[j] = (e < E) ? lr[e] : -__uint_as_float(0x7f800000u);
+      if (e >= E) taken |= 1u << j;
     }
-    bool taken[ROUTE_EPER];
-#pragma unroll
-    for (int j = 0; j < ROUTE_EPER; ++j) taken[j] = (lane + 64 * j) >= E;
     for (int k = 0; k < K; ++k) {
       float bv = -__uint_as_float(0x7f800000u);
       int bj = -1;
 #pragma unroll
       for (int j = 0; j < ROUTE_EPER; ++j)
-        if (!taken[j] && (bj < 0 || v[j] > bv)) {
+        if (!((taken >> j) & 1u) && (bj < 0 || v[j] > bv)) {
           bv = v[j];
           bj = j;
         }
@@ -106,98 +123,85 @@ __global__ __launch_bounds__(512) void k_moe_route(MoeArgs a) {
       int cand = (bj >= 0 && bv == gmax) ? lane + 64 * bj : 0x7fffffff;
 #pragma unroll
       for (int off = 32; off >= 1; off /= 2) cand = min(cand, __shfl_xor(cand, off, 64));
-      if (bj >= 0 && cand == lane + 64 * bj) taken[bj] = true;
+      if (bj >= 0 && cand == lane + 64 * bj) taken |= 1u << bj;
       // only NaN logits leave no candidate; keep the index addressable
       if (cand >= E) cand = 0;
       if (lane == 0) {
-        sel[wave][k] = cand;
+        sel[wave * K + k] = cand;
         selv[wave][k] = gmax;
       }
     }
+    // softmax over the K selected: exp per lane, sum in rank order on lane 0
+    const float mx = selv[wave][0];
+    if (lane < K) selv[wave][lane] = expf_det(selv[wave][lane] - mx);
     if (lane == 0) {
-      const float mx = selv[wave][0];
-      float e[MAX_TOPK];
       float sum = 0.0f;
-      for (int k = 0; k < K; ++k) {
-        e[k] = expf_det(selv[wave][k] - mx);
-        sum = sum + e[k];
-      }
-      const float inv = 1.0f / sum;
-      for (int k = 0; k < K; ++k) {
-        a.idx[wave * K + k] = sel[wave][k];
-        a.w[wave * K + k] = e[k] * inv;
-      }
+      for (int k = 0; k < K; ++k) sum = sum + selv[wave][k];
+      sum = 1.0f / sum;
+      for (int k = 0; k < K; ++k) selv[wave][k] = selv[wave][k] * sum;
+    }
+    if (lane < K) {
+      a.idx[wave * K + lane] = sel[wave * K + lane];
+      a.w[wave * K + lane] = selv[wave][lane];
     }
   }
   __syncthreads();
-  if (threadIdx.x == 0) {
-    MoeDispatch* d = a.disp;
-    int n = 0;
-    for (int m = 0; m < M; ++m)
-      for (int k = 0; k < K; ++k) {
-        const int e = sel[m][k];
-        int u = 0;
-        while (u < n && d->expert[u] != e) ++u;
-        if (u == n) {
-          d->expert[n] = e;
-          d->count[n] = 0;
-          ++n;
-        }
-        if (d->count[u] < MAX_TOKENS) d->slot[u][d->count[u]++] = (int16_t)(m * K + k);
-      }
+  const int t = threadIdx.x;
+  int e = 0;
+  if (t < MK) {
+    e = sel[t];
+    atomicMin(&first[e], t);
+    atomicOr(&tokbits[t / K][e >> 5], 1u << (e & 31));
+  }
+  __syncthreads();
+  const bool leader = t < MK && first[e] == t;
+  const uint64_t bal = __ballot(leader);
+  if (lane == 0 && wave < 2) leadmask[wave] = bal;
+  __syncthreads();
+  MoeDispatch* d = a.disp;
+  if (leader) {
+    const uint64_t below = (t & 63) ? (leadmask[t >> 6] & ((~0ull) >> (64 - (t & 63)))) : 0ull;
+    const int u = __popcll(below) + (t >= 64 ? __popcll(leadmask[0]) : 0);
+    uid[t] = u;
+    int count = 0;
+    for (int m = 0; m < M; ++m) count += (tokbits[m][e >> 5] >> (e & 31)) & 1u;
+    d->expert[u] = e;
+    d->count[u] = count;
+  }
+  __syncthreads();
+  if (t < MK) {
+    const int u = uid[first[e]];
+    int pos = 0;
+    for (int m = 0; m < t / K; ++m) pos += (tokbits[m][e >> 5] >> (e & 31)) & 1u;
+    d->slot[u][pos] = (int16_t)t;
+  }
+  if (t == 0) {
+    const int n = __popcll(leadmask[0]) + (MK > 64 ? __popcll(leadmask[1]) : 0);
     d->n_unique = n;
     d->expert[n] = -1;
     d->count[n] = M;
-    for (int m = 0; m < M; ++m) d->slot[n][m] = (int16_t)(M * K + m);
+    for (int m = 0; m < M; ++m) d->slot[n][m] = (int16_t)(MK + m);
   }
 }
-
-// ---------------------------------------------------------------------------
-// gate|up + SwiGLU.  grid (F/32, M*K+1).  Lanes: L per row, each lane-group
-// owns one f and walks its gate row and its up row (the two RowLoads).
-template <int L>
-struct RowLoad1 {
-  uint32_t w[QMV_IT][4];
-  float s[QMV_IT], b[QMV_IT];
-  __device__ __forceinline__ void load(const uint32_t* __restrict__ wrow, const bf16* __restrict__ srow,
-                                       const bf16* __restrict__ brow, int nb, int gs, int sub, bool valid) {
-#pragma unroll
-    for (int it = 0; it < QMV_IT; ++it) {
-      const int j = sub + it * L;
-      if (valid && j < nb) {
-        const uint4 v = ldg16(wrow + (size_t)j * 4);
-        w[it][0] = v.x; w[it][1] = v.y; w[it][2] = v.z; w[it][3] = v.w;
-        const int g = (j * 32) / gs;
-        s[it] = bf2f(srow[g]);
-        b[it] = bf2f(brow[g]);
-      } else {
-        w[it][0] = w[it][1] = w[it][2] = w[it][3] = 0u;
-        s[it] = b[it] = 0.0f;
-      }
-    }
-  }
-  __device__ __forceinline__ float dot(const uint32_t* __restrict__ xpv, int nb, int sub) const {
-    float acc = 0.0f;
-#pragma unroll
-    for (int it = 0; it < QMV_IT; ++it) {
-      const int j = sub + it * L;
-      if (j < nb) {
-        const uint32_t* xl = xpv + (size_t)j * XP_DW;
-        acc = block_accum(acc, block_dot(w[it], xl), s[it], b[it], xl);
-      }
-    }
-    return acc;
-  }
-};
 
 __device__ __forceinline__ int slot_token(int slot, int M, int K) {
   return slot < M * K ? slot / K : slot - M * K;
 }
 
-template <int L>
-__global__ __launch_bounds__(256) void k_moe_gate_up(MoeArgs a) {
+// ---------------------------------------------------------------------------
+// gate|up + SwiGLU.  grid (F/32, M*K+1), GU_THREADS threads.  Every lane-group
+// owns one f of the block and walks its gate row and up row; the weight loads
+// are issued before the activations are staged into LDS.
+constexpr int GU_THREADS = 512;
+
+template <int L, int IT>
+__global__ __launch_bounds__(GU_THREADS) void k_moe_gate_up(MoeArgs a) {
   extern __shared__ uint32_t lds[];
   __shared__ bf16 actb[MAX_TOKENS][32];
+  __shared__ uint32_t scratch[MAX_TOKENS][24];
+  constexpr int WAVES = GU_THREADS / 64;
+  constexpr int RW = 64 / L;                                  // f rows per wave pass
+  constexpr int NI = (32 + WAVES * RW - 1) / (WAVES * RW);     // passes for 32 rows
   const int H = a.H, F = a.F, M = a.M, K = a.K, gs = a.gs;
   const int nb = H / 32, ng = H / gs;
   const int u = blockIdx.y;
@@ -206,49 +210,113 @@ __global__ __launch_bounds__(256) void k_moe_gate_up(MoeArgs a) {
   const bool shared = (u == nu);
   const int e = a.disp->expert[u];
   const int cnt = a.disp->count[u];
-  for (int i = threadIdx.x; i < cnt * nb * XP_DW; i += blockDim.x) {
-    const int t = i / (nb * XP_DW), rem = i % (nb * XP_DW);
-    const int m = slot_token(a.disp->slot[u][t], M, K);
-    lds[i] = a.xp_x[(size_t)m * nb * XP_DW + rem];
-  }
-  __syncthreads();
   const uint32_t* gw = shared ? a.sh_gate_w : a.gate_w + (size_t)e * F * (H / 8);
   const bf16* gsc = shared ? a.sh_gate_s : a.gate_s + (size_t)e * F * ng;
   const bf16* gbi = shared ? a.sh_gate_b : a.gate_b + (size_t)e * F * ng;
   const uint32_t* uw = shared ? a.sh_up_w : a.up_w + (size_t)e * F * (H / 8);
   const bf16* usc = shared ? a.sh_up_s : a.up_s + (size_t)e * F * ng;
   const bf16* ubi = shared ? a.sh_up_b : a.up_b + (size_t)e * F * ng;
-  constexpr int RW = 64 / L;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int sub = lane % L, grp = lane / L;
   const int f0 = blockIdx.x * 32;
-  for (int fi0 = wave * RW; fi0 < 32; fi0 += 4 * RW) {  // uniform per wave (shuffles below)
-    const int fi = fi0 + grp;
+  QRow<L, IT> G[NI], U[NI];
+#pragma unroll
+  for (int p = 0; p < NI; ++p) {
+    const int fi = (wave + p * WAVES) * RW + grp;
     const bool valid = fi < 32;
     const int f = f0 + (valid ? fi : 0);
-    RowLoad1<L> G, U;
-    G.load(gw + (size_t)f * (H / 8), gsc + (size_t)f * ng, gbi + (size_t)f * ng, nb, gs, sub, valid);
-    U.load(uw + (size_t)f * (H / 8), usc + (size_t)f * ng, ubi + (size_t)f * ng, nb, gs, sub, valid);
-    for (int t = 0; t < cnt; ++t) {
-      const uint32_t* xm = lds + (size_t)t * nb * XP_DW;
-      const float g = lane_fold<L>(G.dot(xm, nb, sub));
-      const float up = lane_fold<L>(U.dot(xm, nb, sub));
-      if (sub == 0 && valid) {
+    G[p].load(gw + (size_t)f * (H / 8), gsc + (size_t)f * ng, gbi + (size_t)f * ng, nb, gs, sub, valid);
+    U[p].load(uw + (size_t)f * (H / 8), usc + (size_t)f * ng, ubi + (size_t)f * ng, nb, gs, sub, valid);
+  }
+  for (int tk = 0; tk < cnt; ++tk) {
+    const int m = slot_token(a.disp->slot[u][tk], M, K);
+    stage16(lds + (size_t)tk * nb * XP_DW, a.xp_x + (size_t)m * nb * XP_DW, nb * XP_DW);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int p = 0; p < NI; ++p) {
+    const int fi = (wave + p * WAVES) * RW + grp;
+    if ((wave + p * WAVES) * RW >= 32) break;  // uniform per wave
+    for (int tk = 0; tk < cnt; ++tk) {
+      float g, up;
+      dot2(G[p], U[p], lds + (size_t)tk * nb * XP_DW, nb, sub, g, up);
+      g = lane_fold<L>(g);
+      up = lane_fold<L>(up);
+      if (sub == 0 && fi < 32) {
         const bf16 act = f2bf(silu_bf16(round_bf(g)) * round_bf(up));
-        actb[t][fi] = act;
-        a.act[(size_t)a.disp->slot[u][t] * F + f] = act;
+        actb[tk][fi] = act;
+        a.act[(size_t)a.disp->slot[u][tk] * F + f0 + fi] = act;
       }
     }
   }
   __syncthreads();
-  if ((int)threadIdx.x < cnt) {
-    const int slot = a.disp->slot[u][threadIdx.x];
-    xprep_block(actb[threadIdx.x], a.xp_act + ((size_t)slot * (F / 32) + blockIdx.x) * XP_DW);
+  // prepared activation block of this f-block for every slot: 32 lanes per slot
+  {
+    const int tk = threadIdx.x >> 5, i = threadIdx.x & 31;
+    int E = 0, sm = 0;
+    if (tk < MAX_TOKENS) xprep_lanes_build(tk < cnt ? actb[tk][i] : (bf16)0, i, scratch[tk], E, sm);
+    __syncthreads();
+    if (tk < cnt)
+      xprep_lanes_store(i, scratch[tk], E, sm,
+                        a.xp_act + ((size_t)a.disp->slot[u][tk] * (F / 32) + blockIdx.x) * XP_DW);
   }
 }
 
 // ---------------------------------------------------------------------------
-// down + combine.  grid (H/64, M*K+1).
+// down: grid (H/DOWN_ROWS, M*K+1), 256 threads; each lane-group owns two rows
+// (RPL = 2) so each LDS read of an activation block feeds two rows.
+template <int L, int IT>
+__global__ __launch_bounds__(256) void k_moe_down(MoeArgs a) {
+  extern __shared__ uint32_t lds[];
+  constexpr int RW = 64 / L;
+  constexpr int NI = (DOWN_ROWS + 8 * RW - 1) / (8 * RW);  // passes of 2*RW rows per wave
+  const int H = a.H, F = a.F, K = a.K, gs = a.gs;
+  const int nb = F / 32, ng = F / gs;
+  const int u = blockIdx.y;
+  const int nu = a.disp->n_unique;
+  if (u > nu) return;
+  const bool shared = (u == nu);
+  const int e = a.disp->expert[u];
+  const int cnt = a.disp->count[u];
+  const uint32_t* dw = shared ? a.sh_down_w : a.down_w + (size_t)e * H * (F / 8);
+  const bf16* dsc = shared ? a.sh_down_s : a.down_s + (size_t)e * H * ng;
+  const bf16* dbi = shared ? a.sh_down_b : a.down_b + (size_t)e * H * ng;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int sub = lane % L, grp = lane / L;
+  const int h0 = blockIdx.x * DOWN_ROWS;
+  QRow<L, IT> A[NI], B[NI];
+#pragma unroll
+  for (int p = 0; p < NI; ++p) {
+    const int hi = (wave + 4 * p) * 2 * RW + 2 * grp;
+    const bool va = hi < DOWN_ROWS && h0 + hi < H, vb = hi + 1 < DOWN_ROWS && h0 + hi + 1 < H;
+    const int ha = va ? h0 + hi : h0, hb = vb ? h0 + hi + 1 : h0;
+    A[p].load(dw + (size_t)ha * (F / 8), dsc + (size_t)ha * ng, dbi + (size_t)ha * ng, nb, gs, sub, va);
+    B[p].load(dw + (size_t)hb * (F / 8), dsc + (size_t)hb * ng, dbi + (size_t)hb * ng, nb, gs, sub, vb);
+  }
+  for (int tk = 0; tk < cnt; ++tk)
+    stage16(lds + (size_t)tk * nb * XP_DW, a.xp_act + (size_t)a.disp->slot[u][tk] * nb * XP_DW, nb * XP_DW);
+  __syncthreads();
+#pragma unroll
+  for (int p = 0; p < NI; ++p) {
+    if ((wave + 4 * p) * 2 * RW >= DOWN_ROWS) break;  // uniform per wave
+    const int hi = (wave + 4 * p) * 2 * RW + 2 * grp;
+    for (int tk = 0; tk < cnt; ++tk) {
+      float ra, rb;
+      dot2(A[p], B[p], lds + (size_t)tk * nb * XP_DW, nb, sub, ra, rb);
+      ra = lane_fold<L>(ra);
+      rb = lane_fold<L>(rb);
+      if (sub == 0) {
+        bf16* dst = a.r + (size_t)a.disp->slot[u][tk] * H + h0;
+        if (hi < DOWN_ROWS && h0 + hi < H) dst[hi] = f2bf(ra);
+        if (hi + 1 < DOWN_ROWS && h0 + hi + 1 < H) dst[hi + 1] = f2bf(rb);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// combine: grid (ceil(H/256), M).  out = bf16(fold_k r_k*w_k) + bf16(sig(g)*shared);
+// y = bf16(out) and, with a residual, y2 = bf16(resid + out).
 __device__ __forceinline__ float colsum_small(const float* r, int K) {
   const int TY = K < 8 ? K : 8;
   float t[8];
@@ -262,118 +330,64 @@ __device__ __forceinline__ float colsum_small(const float* r, int K) {
   return total;
 }
 
-template <int L>
-__global__ __launch_bounds__(256) void k_moe_down(MoeArgs a) {
-  extern __shared__ uint32_t lds[];
-  __shared__ int is_last;
-  const int H = a.H, F = a.F, M = a.M, K = a.K, gs = a.gs;
-  const int nb = F / 32, ng = F / gs;
-  const int u = blockIdx.y;
-  const int nu = a.disp->n_unique;
-  if (u > nu) return;
-  const bool shared = (u == nu);
-  const int e = a.disp->expert[u];
-  const int cnt = a.disp->count[u];
-  for (int i = threadIdx.x; i < cnt * nb * XP_DW; i += blockDim.x) {
-    const int t = i / (nb * XP_DW), rem = i % (nb * XP_DW);
-    lds[i] = a.xp_act[(size_t)a.disp->slot[u][t] * nb * XP_DW + rem];
-  }
-  __syncthreads();
-  const uint32_t* dw = shared ? a.sh_down_w : a.down_w + (size_t)e * H * (F / 8);
-  const bf16* dsc = shared ? a.sh_down_s : a.down_s + (size_t)e * H * ng;
-  const bf16* dbi = shared ? a.sh_down_b : a.down_b + (size_t)e * H * ng;
-  constexpr int RW = 64 / L;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int sub = lane % L, grp = lane / L;
-  const int h0 = blockIdx.x * DOWN_ROWS;
-  for (int hi0 = wave * RW; hi0 < DOWN_ROWS; hi0 += 4 * RW) {
-    const int hi = hi0 + grp;
-    const bool valid = hi < DOWN_ROWS && h0 + hi < H;
-    const int h = valid ? h0 + hi : h0;
-    RowLoad1<L> D;
-    D.load(dw + (size_t)h * (F / 8), dsc + (size_t)h * ng, dbi + (size_t)h * ng, nb, gs, sub, valid);
-    for (int t = 0; t < cnt; ++t) {
-      const float r = lane_fold<L>(D.dot(lds + (size_t)t * nb * XP_DW, nb, sub));
-      if (sub == 0 && valid) a.r[(size_t)a.disp->slot[u][t] * H + h] = f2bf(r);
-    }
-  }
-  // the last workgroup of this row block folds every expert's rows
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const uint32_t old = atomicAdd(&a.counters[blockIdx.x], 1u);
-    is_last = (old == (uint32_t)nu);
-  }
-  __syncthreads();
-  if (!is_last) return;
-  __threadfence();
-  for (int i = threadIdx.x; i < M * DOWN_ROWS; i += blockDim.x) {
-    const int m = i / DOWN_ROWS, h = h0 + i % DOWN_ROWS;
-    if (h >= H) continue;
-    float prod[MAX_TOPK];
-    for (int k = 0; k < K; ++k)
-      prod[k] = bf2f(a.r[(size_t)(m * K + k) * H + h]) * a.w[m * K + k];
-    const float rr = round_bf(colsum_small(prod, K));
-    const float sg = sigmoid_bf16(round_bf(a.gate_logit[m]));
-    const float sh = round_bf(sg * bf2f(a.r[(size_t)(M * K + m) * H + h]));
-    a.y[(size_t)m * H + h] = f2bf(rr + sh);
-  }
-  if (threadIdx.x == 0) a.counters[blockIdx.x] = 0u;
+__global__ __launch_bounds__(256) void k_moe_combine(MoeArgs a, const bf16* __restrict__ resid,
+                                                     bf16* __restrict__ y2) {
+  const int H = a.H, M = a.M, K = a.K;
+  const int m = blockIdx.y, h = blockIdx.x * 256 + threadIdx.x;
+  if (h >= H) return;
+  float prod[MAX_TOPK];
+  for (int k = 0; k < K; ++k) prod[k] = bf2f(a.r[(size_t)(m * K + k) * H + h]) * a.w[m * K + k];
+  const float rr = round_bf(colsum_small(prod, K));
+  const float sg = sigmoid_bf16(round_bf(a.gate_logit[m]));
+  const float sh = round_bf(sg * bf2f(a.r[(size_t)(M * K + m) * H + h]));
+  const bf16 out = f2bf(rr + sh);
+  if (a.y) a.y[(size_t)m * H + h] = out;
+  if (y2) y2[(size_t)m * H + h] = f2bf(bf2f(resid[(size_t)m * H + h]) + bf2f(out));
 }
 
 // ---------------------------------------------------------------------------
 hipError_t launch_moe_router(const MoeArgs& a, hipStream_t st) {
   const int row_wgs = (a.E + 1 + 3) / 4;
-  const int prep_wgs = (a.M * (a.H / 32) + 255) / 256;
+  const int prep_wgs = a.xp_ready ? 0 : (a.M * (a.H / 32) + 7) / 8;
   hipLaunchKernelGGL(k_moe_router, dim3(row_wgs + prep_wgs), dim3(256), 0, st, a, row_wgs);
   return hipGetLastError();
 }
 
 hipError_t launch_moe_route(const MoeArgs& a, hipStream_t st) {
-  hipLaunchKernelGGL(k_moe_route, dim3(1), dim3(64 * a.M), 0, st, a);
+  const int threads = 64 * (a.M > 2 ? a.M : 2);  // at least two waves: the dispatch covers 128 slots
+  hipLaunchKernelGGL(k_moe_route, dim3(1), dim3(threads), 0, st, a);
   return hipGetLastError();
 }
 
-hipError_t launch_moe_gate_up(const MoeArgs& a, hipStream_t st) {
+template <int L, int IT>
+static hipError_t gate_up_li(const MoeArgs& a, hipStream_t st) {
   const dim3 grid(a.F / 32, a.M * a.K + 1);
   const size_t lds = (size_t)a.M * (a.H / 32) * XP_DW * 4;
-  switch (lanes_for_blocks(a.H / 32)) {
-#define GU(Lv)                                                            \
-  case Lv: {                                                              \
-    static size_t cur = 0;                                                \
-    hipError_t e = ensure_lds(k_moe_gate_up<Lv>, lds, cur);                   \
-    if (e != hipSuccess) return e;                                        \
-    hipLaunchKernelGGL(k_moe_gate_up<Lv>, grid, dim3(256), lds, st, a);       \
-  } break;
-    GU(1) GU(2) GU(4) GU(8) GU(16) GU(32) GU(64)
-#undef GU
-  }
+  static size_t cur = 0;
+  hipError_t e = ensure_lds(k_moe_gate_up<L, IT>, lds, cur);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL((k_moe_gate_up<L, IT>), grid, dim3(GU_THREADS), lds, st, a);
   return hipGetLastError();
 }
 
-hipError_t launch_moe_down(const MoeArgs& a, hipStream_t st) {
+template <int L, int IT>
+static hipError_t down_li(const MoeArgs& a, hipStream_t st) {
   const dim3 grid((a.H + DOWN_ROWS - 1) / DOWN_ROWS, a.M * a.K + 1);
   const size_t lds = (size_t)a.M * (a.F / 32) * XP_DW * 4;
-  switch (lanes_for_blocks(a.F / 32)) {
-#define DN(Lv)                                                            \
-  case Lv: {                                                              \
-    static size_t cur = 0;                                                \
-    hipError_t e = ensure_lds(k_moe_down<Lv>, lds, cur);                   \
-    if (e != hipSuccess) return e;                                        \
-    hipLaunchKernelGGL(k_moe_down<Lv>, grid, dim3(256), lds, st, a);       \
-  } break;
-    DN(1) DN(2) DN(4) DN(8) DN(16) DN(32) DN(64)
-#undef DN
-  }
+  static size_t cur = 0;
+  hipError_t e = ensure_lds(k_moe_down<L, IT>, lds, cur);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL((k_moe_down<L, IT>), grid, dim3(256), lds, st, a);
   return hipGetLastError();
 }
 
-hipError_t launch_moe_block(const MoeArgs& a, hipStream_t st) {
-  hipError_t e;
-  if ((e = launch_moe_router(a, st)) != hipSuccess) return e;
-  if ((e = launch_moe_route(a, st)) != hipSuccess) return e;
-  if ((e = launch_moe_gate_up(a, st)) != hipSuccess) return e;
-  return launch_moe_down(a, st);
+hipError_t launch_moe_gate_up(const MoeArgs& a, hipStream_t st) { MTPX_QROW_DISPATCH(a.H / 32, gate_up_li, a, st); }
+
+hipError_t launch_moe_down(const MoeArgs& a, hipStream_t st) { MTPX_QROW_DISPATCH(a.F / 32, down_li, a, st); }
+
+hipError_t launch_moe_combine(const MoeArgs& a, const bf16* resid, bf16* y2, hipStream_t st) {
+  hipLaunchKernelGGL(k_moe_combine, dim3((a.H + 255) / 256, a.M), dim3(256), 0, st, a, resid, y2);
+  return hipGetLastError();
 }
 
 }  // namespace mtpx

@@ -48,8 +48,6 @@ struct Ctx {
   void* ws = nullptr;
   size_t ws_size = 0;
   size_t ws_used = 0;
-  uint32_t* counters = nullptr;
-  int counters_n = 0;
   MoeDispatch* last_disp = nullptr;  // inside the workspace of the last MoE call
   int last_H = 0, last_E = 0, last_F = 0, last_gs = 0;
   // per-kernel timing with events on the launch stream (off by default)
@@ -136,18 +134,6 @@ T* ws_take(Ctx* c, size_t count) {
 
 size_t al(size_t b) { return (b + 255) & ~(size_t)255; }
 
-int counters_reserve(Ctx* c, int n) {
-  if (n <= c->counters_n) return MTPX_OK;
-  if (c->counters) {
-    HIP_OK(hipStreamSynchronize(c->stream));
-    HIP_OK(hipFree(c->counters));
-  }
-  if (hipMalloc(&c->counters, sizeof(uint32_t) * n) != hipSuccess) return fail(MTPX_ERR_OOM, "counters");
-  HIP_OK(hipMemset(c->counters, 0, sizeof(uint32_t) * n));
-  c->counters_n = n;
-  return MTPX_OK;
-}
-
 Ctx* C(mtpx_ctx h) { return static_cast<Ctx*>(h.ctx); }
 
 int set_device(Ctx* c) {
@@ -203,7 +189,8 @@ size_t moe_ws_bytes(const mtpx_moe_weights* w, int M) {
 
 // Enqueue the MoE block; workspace already reserved.
 int moe_enqueue(Ctx* c, const mtpx_moe_weights* w, const uint16_t* x, int M, uint16_t* y, int32_t* idx,
-                float* wts, float* logits) {
+                float* wts, float* logits, const uint16_t* resid = nullptr, uint16_t* y2 = nullptr,
+                uint32_t* xp_ready = nullptr) {
   MoeArgs a;
   a.H = w->hidden;
   a.E = w->experts;
@@ -227,13 +214,11 @@ int moe_enqueue(Ctx* c, const mtpx_moe_weights* w, const uint16_t* x, int M, uin
   a.idx = idx ? idx : ws_take<int32_t>(c, (size_t)M * a.K);
   a.w = wts ? wts : ws_take<float>(c, (size_t)M * a.K);
   a.disp = ws_take<MoeDispatch>(c, 1);
-  a.xp_x = ws_take<uint32_t>(c, (size_t)M * (a.H / 32) * XP_DW);
+  a.xp_x = xp_ready ? xp_ready : ws_take<uint32_t>(c, (size_t)M * (a.H / 32) * XP_DW);
+  a.xp_ready = xp_ready != nullptr;
   a.act = ws_take<uint16_t>(c, (size_t)slots * a.F);
   a.xp_act = ws_take<uint32_t>(c, (size_t)slots * (a.F / 32) * XP_DW);
   a.r = ws_take<uint16_t>(c, (size_t)slots * a.H);
-  int rc = counters_reserve(c, (a.H + DOWN_ROWS - 1) / DOWN_ROWS);
-  if (rc) return rc;
-  a.counters = c->counters;
   c->last_disp = a.disp;
   c->last_H = a.H;
   c->last_E = a.E;
@@ -243,6 +228,7 @@ int moe_enqueue(Ctx* c, const mtpx_moe_weights* w, const uint16_t* x, int M, uin
   LAUNCH(c, "moe_route", launch_moe_route(a, c->stream));
   LAUNCH(c, "moe_gate_up", launch_moe_gate_up(a, c->stream));
   LAUNCH(c, "moe_down", launch_moe_down(a, c->stream));
+  LAUNCH(c, "moe_combine", launch_moe_combine(a, resid, y2, c->stream));
   return MTPX_OK;
 }
 
@@ -275,7 +261,6 @@ int mtpx_ctx_free(mtpx_ctx h) {
   hipSetDevice(c->device);
   hipStreamSynchronize(c->stream);
   if (c->ws) hipFree(c->ws);
-  if (c->counters) hipFree(c->counters);
   for (auto& r : c->pending) {
     hipEventDestroy(r.a);
     hipEventDestroy(r.b);
@@ -331,7 +316,6 @@ int mtpx_qmv(mtpx_ctx h, const uint32_t* wq, const uint16_t* s, const uint16_t* 
   ARG(c && wq && s && b && x && y, "null argument");
   ARG(N >= 1 && M >= 1 && M <= MAX_TOKENS, "N=%d M=%d", N, M);
   ARG(gs_ok(gs) && k_ok(K, gs), "K=%d gs=%d unsupported", K, gs);
-  ARG((size_t)M * (K / 32) * XP_DW * 4 <= 160 * 1024, "M*K too large for one workgroup's LDS");
   if (set_device(c)) return MTPX_ERR_HIP;
   const size_t xpn = (size_t)M * (K / 32) * XP_DW;
   int rc = ws_reserve(c, al(xpn * 4) + 256);
@@ -384,11 +368,8 @@ int mtpx_attn_verify(mtpx_ctx h, const uint16_t* q, int S, int HQ, int HK, int D
   ARG(S >= 1 && S <= MAX_TOKENS && T >= S && T <= tmax, "S=%d T=%d tmax=%lld", S, T, (long long)tmax);
   ARG(D >= 8 && D <= 256 && (D & (D - 1)) == 0, "head_dim=%d", D);
   ARG(HK >= 1 && HQ % HK == 0, "heads %d / kv heads %d", HQ, HK);
-  {
-    const size_t R = (size_t)(HQ / HK) * S;
-    const size_t lds = R * D * 2 + 2 * (size_t)ATTN_CHUNK * D * 2 + R * ATTN_CHUNK * 4 + R * 8;
-    ARG(lds <= 160 * 1024, "GQA group %d x %d rows exceeds one workgroup's LDS", HQ / HK, S);
-  }
+  ARG(D % 32 == 0, "head_dim=%d must be a multiple of 32", D);
+  ARG(attn_partial_lds(HQ / HK, D) <= 160 * 1024, "GQA group of %d heads exceeds one workgroup's LDS", HQ / HK);
   ARG(!out_gated || (gate_off >= 0 && gate_off + HQ * D <= QW), "gate columns outside qkv rows");
   if (set_device(c)) return MTPX_ERR_HIP;
   const size_t pf = attn_partial_floats(S, HQ, D, T);
@@ -396,7 +377,7 @@ int mtpx_attn_verify(mtpx_ctx h, const uint16_t* q, int S, int HQ, int HK, int D
   if (rc) return rc;
   c->ws_used = 0;
   float* part = ws_take<float>(c, pf);
-  HIP_OK(launch_attn_verify(q, S, HQ, HK, D, kc, vc, tmax, T, scale, part, qkv, QW, gate_off, out, out_gated,
+  HIP_OK(launch_attn_verify(q, S, HQ, HK, D, kc, vc, tmax, T, scale, part, qkv, QW, gate_off, out, out_gated, nullptr,
                             c->stream));
   return MTPX_OK;
 }
@@ -407,7 +388,7 @@ int mtpx_rmsnorm(mtpx_ctx h, const uint16_t* x, const uint16_t* resid, int M, in
   ARG(c && x && w && y, "null argument");
   ARG(M >= 1 && H >= 1, "M=%d H=%d", M, H);
   if (set_device(c)) return MTPX_ERR_HIP;
-  HIP_OK(launch_rmsnorm(x, resid, M, H, w, eps, sum_out, y, c->stream));
+  HIP_OK(launch_rmsnorm(x, resid, M, H, w, eps, sum_out, y, nullptr, c->stream));
   return MTPX_OK;
 }
 
@@ -684,7 +665,7 @@ int mtpx_layer_forward(mtpx_ctx h, mtpx_layer lh, mtpx_kv kvh, const uint16_t* x
   const int T = (int)(kv->offset + M);
   const size_t need = moe_ws_bytes(&L->w.moe, M) + al(2 * (size_t)M * H) * 4 + al(2 * (size_t)M * QW) +
                       al(2 * (size_t)M * HQ * D) * 2 + al(4 * (size_t)M * ((QW > HQ * D ? QW : HQ * D) / 32) * XP_DW) +
-                      al(4 * attn_partial_floats(M, HQ, D, T)) + 4096;
+                      al(4 * attn_partial_floats(M, HQ, D, T)) + al(4 * (size_t)M * (H / 32) * XP_DW) + 4096;
   if ((rc = ws_reserve(c, need))) return rc;
   c->ws_used = 0;
   uint16_t* h1 = ws_take<uint16_t>(c, (size_t)M * H);
@@ -697,19 +678,19 @@ int mtpx_layer_forward(mtpx_ctx h, mtpx_layer lh, mtpx_kv kvh, const uint16_t* x
   uint32_t* xp = ws_take<uint32_t>(c, (size_t)M * ((QW > HQ * D ? QW : HQ * D) / 32) * XP_DW);
   float* part = ws_take<float>(c, attn_partial_floats(M, HQ, D, T));
   hipStream_t st = c->stream;
-  LAUNCH(c, "rmsnorm", launch_rmsnorm(x, nullptr, M, H, L->w.attn_norm, g.eps, nullptr, h1, st));
-  LAUNCH(c, "xprep", launch_xprep(h1, M, H, xp, st));
+  uint32_t* xp2 = ws_take<uint32_t>(c, (size_t)M * (H / 32) * XP_DW);
+  LAUNCH(c, "rmsnorm", launch_rmsnorm(x, nullptr, M, H, L->w.attn_norm, g.eps, nullptr, h1, xp, st));
   LAUNCH(c, "qmv_qkv", launch_qmv(L->w.qkv_w, L->w.qkv_s, L->w.qkv_b, QW, H, gs, xp, M, qkv, nullptr, st));
-  LAUNCH(c, "attn_prep", launch_attn_prep(qkv, M, QW, HQ, HK, D, g.rot_dims, L->w.q_norm, L->w.k_norm, g.eps, L->w.rope_cos,
-                          L->w.rope_sin, (int)kv->offset, q, kv->k, kv->v, kv->tmax, st));
-  LAUNCH(c, "attn_verify", launch_attn_verify(q, M, HQ, HK, D, kv->k, kv->v, kv->tmax, T, 1.0f / std::sqrt((float)D), part, qkv, QW,
-                            HQ * D, nullptr, att, st));
-  LAUNCH(c, "xprep", launch_xprep(att, M, HQ * D, xp, st));
+  LAUNCH(c, "attn_prep", launch_attn_prep(qkv, M, QW, HQ, HK, D, g.rot_dims, L->w.q_norm, L->w.k_norm, g.eps,
+                                          L->w.rope_cos, L->w.rope_sin, (int)kv->offset, q, kv->k, kv->v,
+                                          kv->tmax, st));
+  LAUNCH(c, "attn_verify", launch_attn_verify(q, M, HQ, HK, D, kv->k, kv->v, kv->tmax, T,
+                                              1.0f / std::sqrt((float)D), part, qkv, QW, HQ * D, nullptr, att,
+                                              xp, st));
   LAUNCH(c, "qmv_o", launch_qmv(L->w.o_w, L->w.o_s, L->w.o_b, H, HQ * D, gs, xp, M, o, nullptr, st));
-  LAUNCH(c, "rmsnorm", launch_rmsnorm(x, o, M, H, L->w.post_norm, g.eps, s, h2, st));
+  LAUNCH(c, "rmsnorm", launch_rmsnorm(x, o, M, H, L->w.post_norm, g.eps, s, h2, xp2, st));
   uint16_t* moe_out = h1;  // h1 is dead after the qkv GEMV
-  if ((rc = moe_enqueue(c, &L->w.moe, h2, M, moe_out, nullptr, nullptr, nullptr))) return rc;
-  LAUNCH(c, "add", launch_add(s, moe_out, (int64_t)M * H, y, st));
+  if ((rc = moe_enqueue(c, &L->w.moe, h2, M, moe_out, nullptr, nullptr, nullptr, s, y, xp2))) return rc;
   kv->offset += M;
   return MTPX_OK;
 }

@@ -69,15 +69,15 @@ __host__ __device__ constexpr int lanes_for_blocks(int nb) {
 }
 
 // ---------------------------------------------------------------------------
-// Prepared activation block: 26 dwords.
+// Prepared activation block: 28 dwords (16-byte aligned for 128-bit LDS reads).
 //   [0..7]   limb 0 (bits 0-7 of m):   dwords e0 e1 e2 e3 o0 o1 o2 o3
 //   [8..15]  limb 1 (bits 8-15)
 //   [16..23] limb 2 (bits 16-23, signed byte)
-//   [24] p = 2^(E-149) as float bits, [25] SX = (float)(sum m) * p
+//   [24] p = 2^(E-149) as float bits, [25] SX = (float)(sum m) * p, [26..27] 0
 // e_t holds the limb bytes of elements 8t, 8t+2, 8t+4, 8t+6 and o_t those of
 // 8t+1, 8t+3, 8t+5, 8t+7 -- the byte order that (w & 0x0f0f0f0f) and
 // ((w >> 4) & 0x0f0f0f0f) give a packed weight word.
-constexpr int XP_DW = 26;
+constexpr int XP_DW = 28;
 
 __device__ __forceinline__ float block_scale(int E) {
   return (E >= 23) ? __uint_as_float((uint32_t)(E - 22) << 23) : __uint_as_float(1u << E);
@@ -124,23 +124,76 @@ __device__ inline void xprep_block(const bf16* __restrict__ x32, uint32_t* __res
   const float p = block_scale(E);
   out[24] = __float_as_uint(p);
   out[25] = __float_as_uint((float)sm * p);
+  out[26] = 0u;
+  out[27] = 0u;
+}
+
+// The same prepared block built by 32 consecutive lanes, lane i holding element
+// i (bf16 bits h).  `scratch` is 24 dwords of LDS private to this 32-lane group;
+// the caller must place a workgroup barrier between this call and
+// xprep_lanes_store().  Integer sums are exact, so the lane reduction order
+// does not matter.
+__device__ __forceinline__ void xprep_lanes_build(uint32_t h, int i, uint32_t* scratch, int& E_out, int& sm_out) {
+  const int field = (h >> 7) & 0xff;
+  const int f = field < 1 ? 1 : field;
+  int E = f;
+#pragma unroll
+  for (int off = 16; off >= 1; off /= 2) {
+    const int o = __shfl_xor(E, off, 32);
+    E = o > E ? o : E;
+  }
+  const int32_t sig = (int32_t)((field ? 0x80u : 0u) | (h & 0x7fu));
+  const int sh = f - E + 15;
+  const int32_t mag = (sh >= 0) ? (sig << sh) : ((sh > -31) ? (sig >> (-sh)) : 0);
+  const int32_t m = (h & 0x8000u) ? -mag : mag;
+  int32_t sm = m;
+#pragma unroll
+  for (int off = 16; off >= 1; off /= 2) sm += __shfl_xor(sm, off, 32);
+  const uint32_t u = (uint32_t)m & 0xffffffu;
+  const int t = i >> 3, k8 = i & 7;
+  const int slot = (k8 & 1) ? 4 + t : t;
+  const int byte = k8 >> 1;
+  uint8_t* b = reinterpret_cast<uint8_t*>(scratch);
+  b[(0 * 8 + slot) * 4 + byte] = (uint8_t)(u & 0xffu);
+  b[(1 * 8 + slot) * 4 + byte] = (uint8_t)((u >> 8) & 0xffu);
+  b[(2 * 8 + slot) * 4 + byte] = (uint8_t)((u >> 16) & 0xffu);
+  E_out = E;
+  sm_out = sm;
+}
+
+__device__ __forceinline__ void xprep_lanes_store(int i, const uint32_t* scratch, int E, int sm,
+                                                  uint32_t* __restrict__ out) {
+  if (i < 24) {
+    out[i] = scratch[i];
+  } else if (i == 24) {
+    out[24] = __float_as_uint(block_scale(E));
+  } else if (i == 25) {
+    out[25] = __float_as_uint((float)sm * block_scale(E));
+  } else if (i < 28) {
+    out[i] = 0u;
+  }
 }
 
 // Exact nibble x limb sums of one 32-element block; w = 4 packed words.
 // Returns DXraw = fmaf((float)D2, 65536, (float)(D1*256 + D0)).
 __device__ __forceinline__ float block_dot(const uint32_t w[4], const uint32_t* __restrict__ xl) {
+  const uint4* x4 = reinterpret_cast<const uint4*>(xl);  // 16-byte aligned prepared block
+  const uint4 e0 = x4[0], o0 = x4[1], e1 = x4[2], o1 = x4[3], e2 = x4[4], o2 = x4[5];
+  const uint32_t l0e[4] = {e0.x, e0.y, e0.z, e0.w}, l0o[4] = {o0.x, o0.y, o0.z, o0.w};
+  const uint32_t l1e[4] = {e1.x, e1.y, e1.z, e1.w}, l1o[4] = {o1.x, o1.y, o1.z, o1.w};
+  const uint32_t l2e[4] = {e2.x, e2.y, e2.z, e2.w}, l2o[4] = {o2.x, o2.y, o2.z, o2.w};
   uint32_t d0 = 0, d1 = 0;
   int32_t d2 = 0;
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
     const uint32_t lo = w[t] & 0x0f0f0f0fu;
     const uint32_t hi = (w[t] >> 4) & 0x0f0f0f0fu;
-    d0 = __builtin_amdgcn_udot4(lo, xl[t], d0, false);
-    d0 = __builtin_amdgcn_udot4(hi, xl[4 + t], d0, false);
-    d1 = __builtin_amdgcn_udot4(lo, xl[8 + t], d1, false);
-    d1 = __builtin_amdgcn_udot4(hi, xl[12 + t], d1, false);
-    d2 = __builtin_amdgcn_sdot4((int)lo, (int)xl[16 + t], d2, false);
-    d2 = __builtin_amdgcn_sdot4((int)hi, (int)xl[20 + t], d2, false);
+    d0 = __builtin_amdgcn_udot4(lo, l0e[t], d0, false);
+    d0 = __builtin_amdgcn_udot4(hi, l0o[t], d0, false);
+    d1 = __builtin_amdgcn_udot4(lo, l1e[t], d1, false);
+    d1 = __builtin_amdgcn_udot4(hi, l1o[t], d1, false);
+    d2 = __builtin_amdgcn_sdot4((int)lo, (int)l2e[t], d2, false);
+    d2 = __builtin_amdgcn_sdot4((int)hi, (int)l2o[t], d2, false);
   }
   const int32_t low = (int32_t)(d1 * 256u + d0);
   return __builtin_fmaf((float)d2, 65536.0f, (float)low);
@@ -149,8 +202,9 @@ __device__ __forceinline__ float block_dot(const uint32_t w[4], const uint32_t* 
 // acc <- fmaf(b, SX, fmaf(s, DXraw * p, acc))
 __device__ __forceinline__ float block_accum(float acc, float dxraw, float s, float b,
                                              const uint32_t* __restrict__ xl) {
-  const float p = __uint_as_float(xl[24]);
-  const float sx = __uint_as_float(xl[25]);
+  const uint2 ps = reinterpret_cast<const uint2*>(xl)[12];
+  const float p = __uint_as_float(ps.x);
+  const float sx = __uint_as_float(ps.y);
   acc = __builtin_fmaf(s, dxraw * p, acc);
   return __builtin_fmaf(b, sx, acc);
 }

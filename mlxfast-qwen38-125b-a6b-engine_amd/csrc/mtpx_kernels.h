@@ -10,7 +10,7 @@ namespace mtpx {
 constexpr int QMV_IT = 8;        // max blocks per lane: K <= 8 * 32 * lanes_for_blocks(K/32)
 constexpr int MAX_TOKENS = 8;    // verify width ceiling (draft depth <= 7)
 constexpr int MAX_TOPK = 16;
-constexpr int ATTN_CHUNK = 64;   // keys per split-KV partial
+constexpr int ATTN_CHUNK = 32;   // keys per split-KV partial
 
 // Raise a kernel's dynamic-LDS limit to `bytes` (only when above what it has;
 // `cur` caches the value already set for that kernel).
@@ -59,18 +59,18 @@ struct MoeArgs {
   float* w;            // [M, K]
   MoeDispatch* disp;
   uint32_t* xp_x;      // [M, H/32, XP_DW]
+  int xp_ready;        // xp_x already holds the prepared x (the router skips its preparation)
   bf16* act;           // [M*(K+1), F]
   uint32_t* xp_act;    // [M*(K+1), F/32, XP_DW]
   bf16* r;             // [M*(K+1), H]
-  uint32_t* counters;  // [H / DOWN_ROWS] zero at rest
 };
-constexpr int DOWN_ROWS = 64;
+constexpr int DOWN_ROWS = 128;
 
 hipError_t launch_moe_router(const MoeArgs& a, hipStream_t st);
 hipError_t launch_moe_route(const MoeArgs& a, hipStream_t st);
 hipError_t launch_moe_gate_up(const MoeArgs& a, hipStream_t st);
 hipError_t launch_moe_down(const MoeArgs& a, hipStream_t st);
-hipError_t launch_moe_block(const MoeArgs& a, hipStream_t st);
+hipError_t launch_moe_combine(const MoeArgs& a, const bf16* resid, bf16* y2, hipStream_t st);
 
 // --- attention (attn.hip)
 hipError_t launch_attn_prep(const bf16* qkv, int S, int QW, int HQ, int HK, int D, int ROT,
@@ -80,9 +80,10 @@ hipError_t launch_attn_prep(const bf16* qkv, int S, int QW, int HQ, int HK, int 
 hipError_t launch_attn_verify(const bf16* q, int S, int HQ, int HK, int D, const bf16* kc,
                               const bf16* vc, int64_t tmax, int T, float scale, float* part,
                               const bf16* qkv, int QW, int gate_off, bf16* out, bf16* out_gated,
-                              hipStream_t st);
+                              uint32_t* xp_gated, hipStream_t st);
+size_t attn_partial_lds(int G, int D);
 hipError_t launch_rmsnorm(const bf16* x, const bf16* resid, int M, int H, const bf16* w, float eps,
-                          bf16* sum_out, bf16* y, hipStream_t st);
+                          bf16* sum_out, bf16* y, uint32_t* xp, hipStream_t st);
 hipError_t launch_add(const bf16* a, const bf16* b, int64_t n, bf16* out, hipStream_t st);
 size_t attn_partial_floats(int S, int HQ, int D, int T);
 

@@ -4,93 +4,68 @@
 // Weight format (MLX affine 4-bit, unchanged from the reference checkpoint):
 // packed uint32 [N, K/8], element k at bits 4*(k%8) of word k/8; bf16 scale
 // and bias [N, K/gs].  Arithmetic: see mtpx_device.h.
-#include "mtpx_kernels.h"
+#include "qrows.h"
 
 namespace mtpx {
 
-// One thread per 32-element block of x [M, K] -> xp [M, K/32, XP_DW].
-__global__ void k_xprep(const bf16* __restrict__ x, int M, int K, uint32_t* __restrict__ xp) {
+// Activation block preparation of x [M, K] -> xp [M, K/32, XP_DW]: a 32-lane
+// group per block, eight blocks per 256-thread workgroup.
+__global__ __launch_bounds__(256) void k_xprep(const bf16* __restrict__ x, int M, int K, uint32_t* __restrict__ xp) {
+  __shared__ uint32_t scratch[8][24];
   const int nb = K / 32;
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= M * nb) return;
-  const int m = i / nb, j = i % nb;
-  xprep_block(x + (size_t)m * K + (size_t)j * 32, xp + (size_t)i * XP_DW);
+  const int g = threadIdx.x >> 5, i = threadIdx.x & 31;
+  const int blk = blockIdx.x * 8 + g;
+  const bool valid = blk < M * nb;
+  const int m = valid ? blk / nb : 0, j = valid ? blk % nb : 0;
+  const uint32_t h = valid ? x[(size_t)m * K + (size_t)j * 32 + i] : 0u;
+  int E, sm;
+  xprep_lanes_build(h, i, scratch[g], E, sm);
+  __syncthreads();
+  if (valid) xprep_lanes_store(i, scratch[g], E, sm, xp + (size_t)blk * XP_DW);
 }
 
-// Rows of a 4-bit matrix walked by lanes: `sub` = lane within the row's L
-// lanes handles blocks sub, sub+L, ... (at most QMV_IT of them).
-template <int L>
-struct RowLoad {
-  uint32_t w[QMV_IT][4];
-  float s[QMV_IT], b[QMV_IT];
-  __device__ __forceinline__ void load(const uint32_t* __restrict__ wrow, const bf16* __restrict__ srow,
-                                       const bf16* __restrict__ brow, int nb, int gs, int sub,
-                                       bool valid) {
-#pragma unroll
-    for (int it = 0; it < QMV_IT; ++it) {
-      const int j = sub + it * L;
-      if (valid && j < nb) {
-        const uint4 v = ldg16(wrow + (size_t)j * 4);
-        w[it][0] = v.x; w[it][1] = v.y; w[it][2] = v.z; w[it][3] = v.w;
-        const int g = (j * 32) / gs;
-        s[it] = bf2f(srow[g]);
-        b[it] = bf2f(brow[g]);
-      } else {
-        w[it][0] = w[it][1] = w[it][2] = w[it][3] = 0u;
-        s[it] = 0.0f;
-        b[it] = 0.0f;
-      }
-    }
-  }
-  // lane partial of this row against one prepared activation vector (LDS)
-  __device__ __forceinline__ float dot(const uint32_t* __restrict__ xpv, int nb, int sub) const {
-    float acc = 0.0f;
-#pragma unroll
-    for (int it = 0; it < QMV_IT; ++it) {
-      const int j = sub + it * L;
-      if (j < nb) {
-        const uint32_t* xl = xpv + (size_t)j * XP_DW;
-        const float d = block_dot(w[it], xl);
-        acc = block_accum(acc, d, s[it], b[it], xl);
-      }
-    }
-    return acc;
-  }
-};
-
-// Dense GEMV.  256 threads; each lane owns two rows (RPL = 2) so every LDS
-// read of a prepared activation block feeds two weight rows.
-template <int L>
+// Dense GEMV.  256 threads; every lane-group owns two rows (RPL = 2) so each
+// LDS read of a prepared activation block feeds two weight rows.  A wave's
+// rows are loaded before the activations are staged.
+template <int L, int IT>
 __global__ __launch_bounds__(256) void k_qmv(const uint32_t* __restrict__ wq, const bf16* __restrict__ sc,
                                              const bf16* __restrict__ bi, int N, int K, int gs,
                                              const uint32_t* __restrict__ xp, int M, bf16* __restrict__ y,
                                              float* __restrict__ yf, int rows_per_wg) {
   extern __shared__ uint32_t lds[];
-  const int nb = K / 32, ng = K / gs;
-  const int words = M * nb * XP_DW;
-  for (int i = threadIdx.x; i < words; i += blockDim.x) lds[i] = xp[i];
-  __syncthreads();
   constexpr int RW = 64 / L;
+  constexpr int RPW = 2 * RW;  // rows per wave pass
+  const int nb = K / 32, ng = K / gs;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int sub = lane % L, grp = lane / L;
   const int row0 = blockIdx.x * rows_per_wg;
   const int row_end = min(row0 + rows_per_wg, N);
-  for (int base = row0 + wave * RW * 2; base < row_end; base += 4 * RW * 2) {
-    const int rA = base + grp * 2, rB = rA + 1;
+  QRow<L, IT> A, B;
+  int base = row0 + wave * RPW;
+  auto load2 = [&](int b0) {
+    const int rA = b0 + grp * 2, rB = rA + 1;
     const bool vA = rA < row_end, vB = rB < row_end;
-    RowLoad<L> A, B;
-    A.load(wq + (size_t)rA * (K / 8), sc + (size_t)rA * ng, bi + (size_t)rA * ng, nb, gs, sub, vA);
-    B.load(wq + (size_t)rB * (K / 8), sc + (size_t)rB * ng, bi + (size_t)rB * ng, nb, gs, sub, vB);
+    const int ra = vA ? rA : row0, rb = vB ? rB : row0;
+    A.load(wq + (size_t)ra * (K / 8), sc + (size_t)ra * ng, bi + (size_t)ra * ng, nb, gs, sub, vA);
+    B.load(wq + (size_t)rb * (K / 8), sc + (size_t)rb * ng, bi + (size_t)rb * ng, nb, gs, sub, vB);
+  };
+  if (base < row_end) load2(base);  // first rows in flight before the staging
+  stage16(lds, xp, M * nb * XP_DW);
+  __syncthreads();
+  for (bool first = true; base < row_end; base += 4 * RPW, first = false) {  // uniform per wave
+    if (!first) load2(base);
+    const int rA = base + grp * 2, rB = rA + 1;
     for (int m = 0; m < M; ++m) {
-      const uint32_t* xm = lds + (size_t)m * nb * XP_DW;
-      float a = lane_fold<L>(A.dot(xm, nb, sub));
-      float b = lane_fold<L>(B.dot(xm, nb, sub));
+      float a, b;
+      dot2(A, B, lds + (size_t)m * nb * XP_DW, nb, sub, a, b);
+      a = lane_fold<L>(a);
+      b = lane_fold<L>(b);
       if (sub == 0) {
-        if (vA) {
+        if (rA < row_end) {
           y[(size_t)m * N + rA] = f2bf(a);
           if (yf) yf[(size_t)m * N + rA] = a;
         }
-        if (vB) {
+        if (rB < row_end) {
           y[(size_t)m * N + rB] = f2bf(b);
           if (yf) yf[(size_t)m * N + rB] = b;
         }
@@ -181,40 +156,45 @@ __global__ void k_fill_bf16(bf16* __restrict__ out, int64_t n, bf16 v) {
 hipError_t launch_xprep(const bf16* x, int M, int K, uint32_t* xp, hipStream_t st) {
   const int n = M * (K / 32);
   if (n == 0) return hipSuccess;
-  hipLaunchKernelGGL(k_xprep, dim3((n + 127) / 128), dim3(128), 0, st, x, M, K, xp);
+  hipLaunchKernelGGL(k_xprep, dim3((n + 7) / 8), dim3(256), 0, st, x, M, K, xp);
   return hipGetLastError();
 }
 
-template <int L>
-static hipError_t qmv_l(const uint32_t* wq, const bf16* s, const bf16* b, int N, int K, int gs,
-                        const uint32_t* xp, int M, bf16* y, float* yf, hipStream_t st) {
-  constexpr int rows_iter = 4 * (64 / L) * 2;
-  // aim for >= 1024 workgroups where the matrix allows, at least one row iteration each
-  int iters = (N + rows_iter - 1) / rows_iter;
-  int per = (iters + 1023) / 1024;
-  if (per < 1) per = 1;
-  const int rows_per_wg = per * rows_iter;
+template <int L, int IT>
+static hipError_t qmv_li(const uint32_t* wq, const bf16* s, const bf16* b, int N, int K, int gs, const uint32_t* xp,
+                         int M, bf16* y, float* yf, hipStream_t st) {
+  constexpr int rows_pass = 4 * (64 / L) * 2;
+  // about two workgroups per CU, at least one pass each
+  const int passes = (N + rows_pass - 1) / rows_pass;
+  const int per = (passes + 511) / 512;
+  const int rows_per_wg = per * rows_pass;
   const int grid = (N + rows_per_wg - 1) / rows_per_wg;
   const size_t lds = (size_t)M * (K / 32) * XP_DW * 4;
   static size_t cur = 0;
-  hipError_t e = ensure_lds(k_qmv<L>, lds, cur);
+  hipError_t e = ensure_lds(k_qmv<L, IT>, lds, cur);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(k_qmv<L>, dim3(grid), dim3(256), lds, st, wq, s, b, N, K, gs, xp, M, y, yf,
-                     rows_per_wg);
+  hipLaunchKernelGGL((k_qmv<L, IT>), dim3(grid), dim3(256), lds, st, wq, s, b, N, K, gs, xp, M, y, yf, rows_per_wg);
   return hipGetLastError();
 }
 
-hipError_t launch_qmv(const uint32_t* wq, const bf16* s, const bf16* b, int N, int K, int gs,
-                      const uint32_t* xp, int M, bf16* y, float* yf, hipStream_t st) {
-  switch (lanes_for_blocks(K / 32)) {
-    case 1: return qmv_l<1>(wq, s, b, N, K, gs, xp, M, y, yf, st);
-    case 2: return qmv_l<2>(wq, s, b, N, K, gs, xp, M, y, yf, st);
-    case 4: return qmv_l<4>(wq, s, b, N, K, gs, xp, M, y, yf, st);
-    case 8: return qmv_l<8>(wq, s, b, N, K, gs, xp, M, y, yf, st);
-    case 16: return qmv_l<16>(wq, s, b, N, K, gs, xp, M, y, yf, st);
-    case 32: return qmv_l<32>(wq, s, b, N, K, gs, xp, M, y, yf, st);
-    default: return qmv_l<64>(wq, s, b, N, K, gs, xp, M, y, yf, st);
+static hipError_t qmv_tokens(const uint32_t* wq, const bf16* s, const bf16* b, int N, int K, int gs,
+                             const uint32_t* xp, int M, bf16* y, float* yf, hipStream_t st) {
+  MTPX_QROW_DISPATCH(K / 32, qmv_li, wq, s, b, N, K, gs, xp, M, y, yf, st);
+}
+
+hipError_t launch_qmv(const uint32_t* wq, const bf16* s, const bf16* b, int N, int K, int gs, const uint32_t* xp,
+                      int M, bf16* y, float* yf, hipStream_t st) {
+  // tokens per launch: as many prepared activation vectors as fit in one workgroup's LDS
+  const size_t per_token = (size_t)(K / 32) * XP_DW * 4;
+  int chunk = (int)((160 * 1024) / per_token);
+  chunk = chunk < 1 ? 1 : chunk;
+  for (int m0 = 0; m0 < M; m0 += chunk) {
+    const int mc = M - m0 < chunk ? M - m0 : chunk;
+    const hipError_t e = qmv_tokens(wq, s, b, N, K, gs, xp + (size_t)m0 * (K / 32) * XP_DW, mc, y + (size_t)m0 * N,
+                                    yf ? yf + (size_t)m0 * N : nullptr, st);
+    if (e != hipSuccess) return e;
   }
+  return hipSuccess;
 }
 
 hipError_t launch_quantize(const bf16* w, int64_t rows, int K, int gs, uint32_t* wq, bf16* s, bf16* b,

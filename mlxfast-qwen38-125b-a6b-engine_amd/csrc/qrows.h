@@ -1,0 +1,120 @@
+// Weight-row walker shared by the dense and the expert GEMVs.
+//
+// A row of an affine-4-bit matrix [*, K] is split over L lanes: lane `sub`
+// owns the 32-element blocks sub, sub+L, sub+2L, ... (IT of them when
+// K/32 == L*IT exactly; IT == 0 selects a predicated walker for up to QMV_IT
+// blocks).  load() issues the 16-byte weight loads and the scale/bias loads;
+// dot() consumes them against one prepared activation vector.
+#pragma once
+#include "mtpx_kernels.h"
+
+namespace mtpx {
+
+template <int L, int IT>
+struct QRow {
+  static constexpr int NB = IT ? IT : QMV_IT;
+  uint32_t w[NB][4];
+  uint32_t sb[NB];  // bf16 scale in the low half, bf16 bias in the high half
+
+  __device__ __forceinline__ void load(const uint32_t* __restrict__ wrow, const bf16* __restrict__ srow,
+                                       const bf16* __restrict__ brow, int nb, int gs, int sub, bool valid) {
+#pragma unroll
+    for (int it = 0; it < NB; ++it) {
+      const int j = sub + it * L;
+      if (valid && (IT ? true : j < nb)) {
+        const uint4 v = ldg16(wrow + (size_t)j * 4);
+        w[it][0] = v.x;
+        w[it][1] = v.y;
+        w[it][2] = v.z;
+        w[it][3] = v.w;
+        const int g = gs == 64 ? (j >> 1) : j;  // group of block j (gs is 32 or 64)
+        sb[it] = (uint32_t)srow[g] | ((uint32_t)brow[g] << 16);
+      } else {
+        w[it][0] = w[it][1] = w[it][2] = w[it][3] = 0u;
+        sb[it] = 0u;
+      }
+    }
+  }
+
+  // lane partial of the row against a prepared activation vector
+  __device__ __forceinline__ float dot(const uint32_t* __restrict__ xpv, int nb, int sub) const {
+    float acc = 0.0f;
+#pragma unroll
+    for (int it = 0; it < NB; ++it) {
+      const int j = sub + it * L;
+      if (IT ? true : j < nb) {
+        const uint32_t* xl = xpv + (size_t)j * XP_DW;
+        const float s = __uint_as_float(sb[it] << 16);
+        const float b = __uint_as_float(sb[it] & 0xffff0000u);
+        acc = block_accum(acc, block_dot(w[it], xl), s, b, xl);
+      }
+    }
+    return acc;
+  }
+};
+
+// Lane partials of two rows against one prepared activation vector: each
+// activation block is read from LDS once for both rows.
+template <int L, int IT>
+__device__ __forceinline__ void dot2(const QRow<L, IT>& A, const QRow<L, IT>& B, const uint32_t* __restrict__ xpv,
+                                     int nb, int sub, float& ra, float& rb) {
+  float a = 0.0f, b = 0.0f;
+#pragma unroll
+  for (int it = 0; it < QRow<L, IT>::NB; ++it) {
+    const int j = sub + it * L;
+    if (IT ? true : j < nb) {
+      const uint32_t* xl = xpv + (size_t)j * XP_DW;
+      a = block_accum(a, block_dot(A.w[it], xl), __uint_as_float(A.sb[it] << 16),
+                      __uint_as_float(A.sb[it] & 0xffff0000u), xl);
+      b = block_accum(b, block_dot(B.w[it], xl), __uint_as_float(B.sb[it] << 16),
+                      __uint_as_float(B.sb[it] & 0xffff0000u), xl);
+    }
+    // keep one block's activation words live at a time (no hoisting across blocks)
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  ra = a;
+  rb = b;
+}
+
+// Copy `words` dwords global -> LDS, 16 bytes per access when both ends allow it.
+__device__ __forceinline__ void stage16(uint32_t* __restrict__ dst, const uint32_t* __restrict__ src, int words) {
+  if ((((uintptr_t)src | (uintptr_t)dst) & 15) == 0 && (words & 3) == 0) {
+    const uint4* s4 = reinterpret_cast<const uint4*>(src);
+    uint4* d4 = reinterpret_cast<uint4*>(dst);
+    for (int i = threadIdx.x; i < words / 4; i += blockDim.x) d4[i] = s4[i];
+  } else {
+    for (int i = threadIdx.x; i < words; i += blockDim.x) dst[i] = src[i];
+  }
+}
+
+// Dispatch a launcher templated on <L, IT> for the shapes the model uses, with
+// the predicated walker for every other depth.
+#define MTPX_QROW_DISPATCH(nb, FN, ...)                                   \
+  do {                                                                     \
+    const int L_ = lanes_for_blocks(nb);                                   \
+    const int IT_ = ((nb) % L_ == 0) ? (nb) / L_ : 0;                      \
+    switch (L_ * 16 + (IT_ >= 4 && IT_ <= 7 ? IT_ : 0)) {                  \
+      case 2 * 16 + 4: return FN<2, 4>(__VA_ARGS__);                       \
+      case 2 * 16 + 5: return FN<2, 5>(__VA_ARGS__);                       \
+      case 4 * 16 + 4: return FN<4, 4>(__VA_ARGS__);                       \
+      case 4 * 16 + 5: return FN<4, 5>(__VA_ARGS__);                       \
+      case 4 * 16 + 6: return FN<4, 6>(__VA_ARGS__);                       \
+      case 8 * 16 + 4: return FN<8, 4>(__VA_ARGS__);                       \
+      case 16 * 16 + 4: return FN<16, 4>(__VA_ARGS__);                     \
+      case 16 * 16 + 5: return FN<16, 5>(__VA_ARGS__);                     \
+      case 32 * 16 + 6: return FN<32, 6>(__VA_ARGS__);                     \
+      case 64 * 16 + 5: return FN<64, 5>(__VA_ARGS__);                     \
+      default: break;                                                      \
+    }                                                                      \
+    switch (L_) {                                                          \
+      case 1: return FN<1, 0>(__VA_ARGS__);                                \
+      case 2: return FN<2, 0>(__VA_ARGS__);                                \
+      case 4: return FN<4, 0>(__VA_ARGS__);                                \
+      case 8: return FN<8, 0>(__VA_ARGS__);                                \
+      case 16: return FN<16, 0>(__VA_ARGS__);                              \
+      case 32: return FN<32, 0>(__VA_ARGS__);                              \
+      default: return FN<64, 0>(__VA_ARGS__);                              \
+    }                                                                      \
+  } while (0)
+
+}  // namespace mtpx

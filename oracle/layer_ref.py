@@ -62,7 +62,7 @@ def oracle_layer(w, cfg, kc, vc, x, pos0):
     for s in range(S):
         kc[:, pos0 + s] = k[s]
         vc[:, pos0 + s] = v[s]
-    att = O.attn_verify(q, kc, vc, pos0 + S, np.float32(1.0) / np.sqrt(np.float32(D)), 64)
+    att = O.attn_verify(q, kc, vc, pos0 + S, np.float32(1.0) / np.sqrt(np.float32(D)), O.ATTN_CHUNK)
     g = O.attn_gate(att.reshape(S, HQ * D), qkv, HQ * D)
     o, _ = O.qmv(*w["o"], gs, g)
     s_ = O.f32_to_bf16(O.bf16_to_f32(x) + O.bf16_to_f32(o))

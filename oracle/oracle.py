@@ -31,6 +31,10 @@ def lib():
     return _LIB
 
 
+# Keys per split-KV chunk of the device's verify attention (the chunk order is
+# part of its arithmetic: partials per chunk, then a fold over chunks).
+ATTN_CHUNK = 32
+
 P = C.c_void_p
 I32, I64, U64, F32, F64 = C.c_int32, C.c_int64, C.c_uint64, C.c_float, C.c_double
 

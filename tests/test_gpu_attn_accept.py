@@ -46,7 +46,7 @@ def test_attention_bit_exact(ctx, S, T0, HQ, HK, D, ROT):
         vc_o[:, T0 + s] = v_o[s]
     T = T0 + S
     scale = D ** -0.5
-    att_o = O.attn_verify(q_o, kc_o, vc_o, T, np.float32(scale), 64)
+    att_o = O.attn_verify(q_o, kc_o, vc_o, T, np.float32(scale), O.ATTN_CHUNK)
     gated_o = O.attn_gate(att_o.reshape(S, HQ * D), qkv, HQ * D)
     # device
     q = empty_bf16(S, HQ, D)

@@ -66,6 +66,7 @@ def test_randn_deterministic_and_normal(ctx):
 @pytest.mark.parametrize("N,K,gs,M", [
     (640, 2560, 64, 1), (1280, 2560, 32, 4), (2560, 640, 64, 6), (2048, 768, 64, 2),
     (768, 2048, 32, 1), (256, 6144, 64, 4), (100, 256, 32, 8), (13440, 2560, 64, 7), (37, 320, 32, 3),
+    (300, 6144, 64, 8), (64, 96, 32, 5),
 ])
 def test_qmv_bit_exact(ctx, N, K, gs, M):
     _print_case(N=N, K=K, gs=gs, M=M)

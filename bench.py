@@ -133,7 +133,7 @@ def main() -> int:
     kernels = {k: dict(launches=n, avg_us=round(1e3 * ms / n, 3)) for k, (n, ms) in stats.items()}
     gu_s = stats["moe_gate_up"][1] / stats["moe_gate_up"][0] / 1e3
     dn_s = stats["moe_down"][1] / stats["moe_down"][0] / 1e3
-    moe_s = sum(stats[k][1] / stats[k][0] for k in ("moe_router", "moe_route", "moe_gate_up", "moe_down")) / 1e3
+    moe_s = sum(stats[k][1] / stats[k][0] for k in ("moe_router_route", "moe_gate_up", "moe_down", "moe_combine")) / 1e3
     achieved = gate_up_bytes / gu_s / 1e9
     qkv_rows = cfg["heads"] * cfg["head_dim"] * 2 + 2 * cfg["kv_heads"] * cfg["head_dim"] + cfg["index_dim"]
     attn_bytes = qbytes(qkv_rows, H, gs) + qbytes(H, cfg["heads"] * cfg["head_dim"], gs)

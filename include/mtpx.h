@@ -129,8 +129,8 @@ int mtpx_attn_verify(mtpx_ctx ctx, const uint16_t* q, int S, int HQ, int HK, int
                      float scale, const uint16_t* qkv, int QW, int gate_off, uint16_t* out,
                      uint16_t* out_gated);
 
-/* Row RMSNorm; with resid != NULL the input is bf16(x + resid), also written to
- * sum_out when that is not NULL. */
+/* Row RMSNorm (H <= 4096); with resid != NULL the input is bf16(x + resid), also
+ * written to sum_out when that is not NULL. */
 int mtpx_rmsnorm(mtpx_ctx ctx, const uint16_t* x, const uint16_t* resid, int M, int H,
                  const uint16_t* w, float eps, uint16_t* sum_out, uint16_t* y);
 

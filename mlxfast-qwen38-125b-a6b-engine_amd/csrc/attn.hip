@@ -95,15 +95,44 @@ __global__ __launch_bounds__(256) void k_attn_partial(const bf16* __restrict__ q
   const uint32_t* q32 = reinterpret_cast<const uint32_t*>(q);
   const uint32_t* k32 = reinterpret_cast<const uint32_t*>(kc);
   const uint32_t* v32 = reinterpret_cast<const uint32_t*>(vc);
-  for (int i = threadIdx.x; i < G * (D / 2); i += blockDim.x) {
-    const int g = i / (D / 2), d2 = i % (D / 2);
-    qb[i] = q32[(((size_t)s * HQ + hk * G + g) * D) / 2 + d2];
-  }
-  for (int i = threadIdx.x; i < n * (D / 2); i += blockDim.x) {
-    const int j = i / (D / 2), d2 = i % (D / 2);
-    const size_t src = (((size_t)hk * tmax + i0 + j) * D) / 2 + d2;
-    kb[j * KS + d2] = k32[src];
-    reinterpret_cast<uint32_t*>(vb)[j * (D / 2) + d2] = v32[src];
+  // staging: 16-byte loads, up to 8 in flight per thread before the LDS stores
+  const uint4* q4 = reinterpret_cast<const uint4*>(q);
+  const uint4* k4 = reinterpret_cast<const uint4*>(kc);
+  const uint4* v4 = reinterpret_cast<const uint4*>(vc);
+  const int RV = D / 8;                   // uint4 per row
+  const int nq = G * RV, nkv = n * RV;    // uint4 of q rows, of each of K and V
+  for (int base = 0; base < nq + 2 * nkv; base += 8 * (int)blockDim.x) {
+    uint4 r[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int i = base + u * (int)blockDim.x + (int)threadIdx.x;
+      if (i < nq) {
+        r[u] = q4[((size_t)s * HQ + hk * G) * RV + i];
+      } else if (i < nq + nkv) {
+        const int ik = i - nq;
+        r[u] = k4[((size_t)hk * tmax + i0 + ik / RV) * RV + ik % RV];
+      } else if (i < nq + 2 * nkv) {
+        const int iv = i - nq - nkv;
+        r[u] = v4[((size_t)hk * tmax + i0 + iv / RV) * RV + iv % RV];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int i = base + u * (int)blockDim.x + (int)threadIdx.x;
+      if (i < nq) {
+        reinterpret_cast<uint4*>(qb)[i] = r[u];
+      } else if (i < nq + nkv) {
+        const int ik = i - nq;
+        uint32_t* dst = kb + (size_t)(ik / RV) * KS + (ik % RV) * 4;
+        dst[0] = r[u].x;
+        dst[1] = r[u].y;
+        dst[2] = r[u].z;
+        dst[3] = r[u].w;
+      } else if (i < nq + 2 * nkv) {
+        const int iv = i - nq - nkv;
+        reinterpret_cast<uint4*>(vb)[iv] = r[u];
+      }
+    }
   }
   __syncthreads();
   for (int p = threadIdx.x; p < G * C; p += blockDim.x) {
@@ -147,7 +176,7 @@ __global__ __launch_bounds__(256) void k_attn_partial(const bf16* __restrict__ q
   }
 }
 
-// grid (R, HK), min(D, 256) threads.  Fold the chunk partials in chunk order,
+// grid (R, HK), max(D, 64) threads (D <= 256).  Fold the chunk partials in chunk order,
 // then bf16 output, the sigmoid gate, and (optionally) the prepared activation
 // blocks of the gated row for the o_proj GEMV (32 lanes per block).
 __global__ __launch_bounds__(256) void k_attn_combine(const float* __restrict__ part, int S, int HQ, int HK, int D,
@@ -155,26 +184,56 @@ __global__ __launch_bounds__(256) void k_attn_combine(const float* __restrict__ 
                                                       bf16* __restrict__ out, bf16* __restrict__ out_gated,
                                                       uint32_t* __restrict__ xp_gated) {
   __shared__ uint32_t scratch[8][24];
+  __shared__ float fc[256], lc[256], red[4];
   const int ri = blockIdx.x, hk = blockIdx.y;
   const int G = HQ / HK, R = S * G;
   const int s = ri / G, h = hk * G + ri % G;
+  const int t = threadIdx.x, nt = blockDim.x;
+  auto chunk = [&](int c) { return part + (((size_t)hk * nch + c) * R + ri) * (D + 2); };
+  // M: max of the visible chunks' maxima (order-free)
   float M = -__uint_as_float(0x7f800000u);
-  for (int c = 0; c < nch; ++c) {
-    const float* p = part + (((size_t)hk * nch + c) * R + ri) * (D + 2);
+  for (int c = t; c < nch; c += nt) {
+    const float* p = chunk(c);
     if (p[1] > 0.0f && p[0] > M) M = p[0];
   }
-  for (int d0 = 0; d0 < D; d0 += blockDim.x) {  // uniform loop (barriers inside)
-    const int d = d0 + threadIdx.x;
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const float o = __shfl_xor(M, off, 64);
+    M = o > M ? o : M;
+  }
+  if ((t & 63) == 0) red[t >> 6] = M;
+  __syncthreads();
+  for (int wv = 0; wv < nt / 64; ++wv) M = red[wv] > M ? red[wv] : M;
+  // L and O[d] in chunk order, 256 chunks per tile, the factor f_c once per chunk
+  const int d = t;  // blockDim >= D
+  float L = 0.0f, O = 0.0f;
+  for (int c0 = 0; c0 < nch; c0 += 256) {
+    const int nc = nch - c0 < 256 ? nch - c0 : 256;
+    __syncthreads();
+    for (int c = t; c < nc; c += nt) {
+      const float* p = chunk(c0 + c);
+      const bool vis = p[1] > 0.0f;
+      fc[c] = vis ? expf_det(p[0] - M) : 0.0f;
+      lc[c] = vis ? p[1] : 0.0f;
+    }
+    __syncthreads();
+    for (int c = 0; c < nc; ++c)
+      if (lc[c] > 0.0f) L = __builtin_fmaf(lc[c], fc[c], L);
+    if (d < D) {
+      for (int cb = 0; cb < nc; cb += 8) {
+        float pv[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) pv[u] = (cb + u < nc) ? chunk(c0 + cb + u)[2 + d] : 0.0f;
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+          if (cb + u < nc && lc[cb + u] > 0.0f) O = __builtin_fmaf(pv[u], fc[cb + u], O);
+      }
+    }
+  }
+  {
+    const int d0 = 0;
     bf16 gated = 0;
     if (d < D) {
-      float L = 0.0f, O = 0.0f;
-      for (int c = 0; c < nch; ++c) {
-        const float* p = part + (((size_t)hk * nch + c) * R + ri) * (D + 2);
-        if (!(p[1] > 0.0f)) continue;
-        const float f = expf_det(p[0] - M);
-        L = __builtin_fmaf(p[1], f, L);
-        O = __builtin_fmaf(p[2 + d], f, O);
-      }
       const bf16 att = f2bf(O / L);
       if (out) out[((size_t)s * HQ + h) * D + d] = att;
       if (out_gated) {
@@ -200,46 +259,57 @@ __global__ __launch_bounds__(256) void k_attn_combine(const float* __restrict__ 
 
 // Row RMSNorm, 256 threads per row: h = x or bf16(x + resid); y = bf16(w * bf16(h * inv)).
 // With xp != nullptr also writes the prepared activation blocks of y (32 lanes per block).
+// grid (M, ceil(H/256)): every workgroup folds the whole row's sum of squares
+// (thread t: elements t, t+256, ... in order; waves summed ((w0+w1)+w2)+w3) and
+// writes the 256 outputs of its slice, plus their prepared activation blocks.
+constexpr int RMS_IT = 16;  // H <= 16 * 256
+
 __global__ __launch_bounds__(256) void k_rmsnorm(const bf16* __restrict__ x, const bf16* __restrict__ resid,
                                                  int H, const bf16* __restrict__ w, float eps,
                                                  bf16* __restrict__ sum_out, bf16* __restrict__ y,
                                                  uint32_t* __restrict__ xp) {
   __shared__ float wsum[4];
   __shared__ uint32_t scratch[8][24];
-  const int m = blockIdx.x, t = threadIdx.x;
+  const int m = blockIdx.x, t = threadIdx.x, sl = blockIdx.y;
   const bf16* xr = x + (size_t)m * H;
   const bf16* rr = resid ? resid + (size_t)m * H : nullptr;
-  float acc = 0.0f;
-  for (int i = t; i < H; i += 256) {
-    float v = bf2f(xr[i]);
-    if (rr) {
-      v = round_bf(v + bf2f(rr[i]));
-      if (sum_out) sum_out[(size_t)m * H + i] = f2bf(v);
+  float v[RMS_IT];
+#pragma unroll
+  for (int j = 0; j < RMS_IT; ++j) {
+    const int i = t + 256 * j;
+    v[j] = (i < H) ? bf2f(xr[i]) : 0.0f;
+  }
+  if (rr) {
+#pragma unroll
+    for (int j = 0; j < RMS_IT; ++j) {
+      const int i = t + 256 * j;
+      if (i < H) v[j] = round_bf(v[j] + bf2f(rr[i]));
     }
-    acc = __builtin_fmaf(v, v, acc);
+  }
+  float acc = 0.0f, vo = 0.0f;
+#pragma unroll
+  for (int j = 0; j < RMS_IT; ++j) {
+    if (t + 256 * j < H) acc = __builtin_fmaf(v[j], v[j], acc);
+    if (j == sl) vo = v[j];
   }
   acc = wave_fold64(acc);
   if ((t & 63) == 0) wsum[t >> 6] = acc;
   __syncthreads();
   const float total = ((wsum[0] + wsum[1]) + wsum[2]) + wsum[3];
   const float inv = 1.0f / sqrtf(total / (float)H + eps);
-  for (int i0 = 0; i0 < H; i0 += 256) {  // uniform loop (barriers inside)
-    const int i = i0 + t;
-    bf16 out = 0;
-    if (i < H) {
-      float v = bf2f(xr[i]);
-      if (rr) v = round_bf(v + bf2f(rr[i]));
-      out = f2bf(bf2f(w[i]) * round_bf(v * inv));
-      y[(size_t)m * H + i] = out;
-    }
-    if (xp) {
-      const int grp = t >> 5, li = t & 31;
-      int E, sm;
-      xprep_lanes_build(out, li, scratch[grp], E, sm);
-      __syncthreads();
-      if (i < H) xprep_lanes_store(li, scratch[grp], E, sm, xp + ((size_t)m * (H / 32) + i / 32) * XP_DW);
-      __syncthreads();
-    }
+  const int i = sl * 256 + t;
+  bf16 out = 0;
+  if (i < H) {
+    if (rr && sum_out) sum_out[(size_t)m * H + i] = f2bf(vo);
+    out = f2bf(bf2f(w[i]) * round_bf(vo * inv));
+    y[(size_t)m * H + i] = out;
+  }
+  if (xp) {
+    const int grp = t >> 5, li = t & 31;
+    int E, sm;
+    xprep_lanes_build(out, li, scratch[grp], E, sm);
+    __syncthreads();
+    if (i < H) xprep_lanes_store(li, scratch[grp], E, sm, xp + ((size_t)m * (H / 32) + i / 32) * XP_DW);
   }
 }
 
@@ -274,7 +344,7 @@ hipError_t launch_attn_verify(const bf16* q, int S, int HQ, int HK, int D, const
   hipLaunchKernelGGL(k_attn_partial, dim3(nch, HK, S), dim3(256), lds, st, q, S, HQ, HK, D, kc, vc, tmax, T, scale,
                      nch, part);
   if ((e = hipGetLastError()) != hipSuccess) return e;
-  hipLaunchKernelGGL(k_attn_combine, dim3(R, HK), dim3(D < 256 ? D : 256), 0, st, part, S, HQ, HK, D, nch, qkv, QW,
+  hipLaunchKernelGGL(k_attn_combine, dim3(R, HK), dim3(D < 64 ? 64 : D), 0, st, part, S, HQ, HK, D, nch, qkv, QW,
                      gate_off, out, out_gated, xp_gated);
   return hipGetLastError();
 }
@@ -286,7 +356,7 @@ size_t attn_partial_lds(int G, int D) {
 
 hipError_t launch_rmsnorm(const bf16* x, const bf16* resid, int M, int H, const bf16* w, float eps, bf16* sum_out,
                           bf16* y, uint32_t* xp, hipStream_t st) {
-  hipLaunchKernelGGL(k_rmsnorm, dim3(M), dim3(256), 0, st, x, resid, H, w, eps, sum_out, y, xp);
+  hipLaunchKernelGGL(k_rmsnorm, dim3(M, (H + 255) / 256), dim3(256), 0, st, x, resid, H, w, eps, sum_out, y, xp);
   return hipGetLastError();
 }
 

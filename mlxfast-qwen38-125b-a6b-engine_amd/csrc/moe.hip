@@ -1,8 +1,9 @@
-// The MoE block of the decode/verify window (M <= 8 tokens), four launches:
-//   router : bf16 router GEMV (+ shared-expert gate row) over f32(x), and the
-//            activation block preparation of x
-//   route  : top-k (value desc, index asc) + softmax, and the expert-grouped
-//            dispatch table (each selected expert once, with its tokens)
+// The MoE block of the decode/verify window (M <= 8 tokens), three launches:
+//   router+route: bf16 router GEMV (+ shared-expert gate row) over f32(x) and
+//            the activation block preparation of x; the last row workgroup to
+//            finish (ticket) runs the route: top-k (value desc, index asc) +
+//            softmax, and the expert-grouped dispatch table (each selected
+//            expert once, with its tokens)
 //   gate_up: per (32-row block of F, selected expert): gate and up rows of the
 //            expert against every token routed to it, SwiGLU, and the block
 //            preparation of the activation for the down projection
@@ -11,8 +12,15 @@
 //   combine: per (token, 256 rows of H): fold the routed outputs in rank order,
 //            add the sigmoid-gated shared expert (MLX col_reduce_small
 //            association), optionally add the residual stream
+// The ticket is a u32 counter that is zero at rest: the last arriver of a
+// launch puts it back to zero.  What it publishes (the router logits) is
+// written and read with agent-scope atomic stores/loads, which go
+// to the device-coherent level; each thread waits for its stores to complete
+// before the workgroup barrier that precedes the ticket, so no cache-wide
+// writeback or invalidate is needed.
 // Reference: FM/TrackFastModel.swift:867-954 (orchestration),
-// FM/TrackFastMoE.swift:780-911 (route), :1192-1404 (gate|up+act),
+// FM/TrackFastMoE.swift:2490-2638 (router + route in one launch with a
+// last-arriver ticket), :780-911 (route), :1192-1404 (gate|up+act),
 // :1412-1576 (down+combine), :2246-2310 (router GEMV),
 // FM/TrackFastKernels2.swift:21-58,512-544 (sigmoid, colsum fold, combine).
 #include "qrows.h"
@@ -20,72 +28,41 @@
 namespace mtpx {
 
 // ---------------------------------------------------------------------------
-// router: one wave per row (rows 0..E-1 router, row E the shared-expert gate).
-// Lane l walks 8-element chunks l, l+64, ...: acc = fmaf(w, x, acc) in element
-// order, then an xor butterfly over the wave.
-constexpr int ROUTER_IT = 8;  // H <= 8 * 64 * 8
+// Agent-coherent stores/loads of ticket-published data.
+__device__ __forceinline__ void st_pub(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_pub(const float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
-__global__ __launch_bounds__(256) void k_moe_router(MoeArgs a, int row_wgs) {
-  const int H = a.H, E = a.E, M = a.M;
-  if ((int)blockIdx.x >= row_wgs) {
-    // activation block preparation of x for the expert GEMVs: 32 lanes per block
-    __shared__ uint32_t scratch[8][24];
-    const int nb = H / 32;
-    const int g = threadIdx.x >> 5, i = threadIdx.x & 31;
-    const int blk = ((int)blockIdx.x - row_wgs) * 8 + g;
-    const bool valid = blk < M * nb;
-    const uint32_t h = valid ? a.x[(size_t)(blk / nb) * H + (size_t)(blk % nb) * 32 + i] : 0u;
-    int E, sm;
-    xprep_lanes_build(h, i, scratch[g], E, sm);
-    __syncthreads();
-    if (valid) xprep_lanes_store(i, scratch[g], E, sm, a.xp_x + (size_t)blk * XP_DW);
-    return;
+// Last-arriver ticket: every thread waits until its published stores are
+// complete, the workgroup synchronises, one thread takes the ticket; the
+// workgroup that draws `last` resets the counter and returns true.
+__device__ __forceinline__ bool ticket_last(uint32_t* ctr, uint32_t last) {
+  __shared__ int is_last;
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const uint32_t t = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    is_last = (t == last);
+    if (t == last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int r = blockIdx.x * 4 + wave;
-  if (r > E) return;
-  const bf16* wrow = (r < E) ? a.router + (size_t)r * H : a.shared_gate;
-  const int nc = H / 8;
-  uint4 wv[ROUTER_IT];
-#pragma unroll
-  for (int i = 0; i < ROUTER_IT; ++i) {
-    const int c = lane + 64 * i;
-    wv[i] = (c < nc) ? *reinterpret_cast<const uint4*>(wrow + (size_t)c * 8) : make_uint4(0, 0, 0, 0);
-  }
-  for (int m = 0; m < M; ++m) {
-    const bf16* xm = a.x + (size_t)m * H;
-    float acc = 0.0f;
-#pragma unroll
-    for (int i = 0; i < ROUTER_IT; ++i) {
-      const int c = lane + 64 * i;
-      if (c < nc) {
-        const uint4 xv = *reinterpret_cast<const uint4*>(xm + (size_t)c * 8);
-        const uint32_t ww[4] = {wv[i].x, wv[i].y, wv[i].z, wv[i].w};
-        const uint32_t xx[4] = {xv.x, xv.y, xv.z, xv.w};
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          acc = __builtin_fmaf(__uint_as_float(ww[t] << 16), __uint_as_float(xx[t] << 16), acc);
-          acc = __builtin_fmaf(__uint_as_float(ww[t] & 0xffff0000u), __uint_as_float(xx[t] & 0xffff0000u), acc);
-        }
-      }
-    }
-    acc = wave_fold64(acc);
-    if (lane == 0) {
-      if (r < E)
-        a.logits[(size_t)m * E + r] = acc;
-      else
-        a.gate_logit[m] = acc;
-    }
-  }
+  __syncthreads();
+  return is_last != 0;
 }
 
 // ---------------------------------------------------------------------------
-// route: wave m selects token m's top-k; then the dispatch table is built in
-// LDS by all threads: each expert once (ordered by its first (token, rank)
-// slot), with its slots ordered by token.
+// route (run by one workgroup of RR_THREADS threads): wave m selects token m's
+// top-k; then the dispatch table is built in LDS by all threads: each expert
+// once (ordered by its first (token, rank) slot), with its slots ordered by
+// token.
 constexpr int ROUTE_EPER = 16;  // E <= 1024
+constexpr int RR_THREADS = 512;
 
-__global__ __launch_bounds__(512) void k_moe_route(MoeArgs a) {
+__device__ void route_body(const MoeArgs& a) {
   const int E = a.E, K = a.K, M = a.M;
   const int MK = M * K;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -105,7 +82,7 @@ __global__ __launch_bounds__(512) void k_moe_route(MoeArgs a) {
 #pragma unroll
     for (int j = 0; j < ROUTE_EPER; ++j) {
       const int e = lane + 64 * j;
-      v[j] = (e < E) ? lr[e] : -__uint_as_float(0x7f800000u);
+      v[j] = (e < E) ? ld_pub(lr + e) : -__uint_as_float(0x7f800000u);
       if (e >= E) taken |= 1u << j;
     }
     for (int k = 0; k < K; ++k) {
@@ -182,6 +159,70 @@ __global__ __launch_bounds__(512) void k_moe_route(MoeArgs a) {
     d->count[n] = M;
     for (int m = 0; m < M; ++m) d->slot[n][m] = (int16_t)(MK + m);
   }
+}
+
+// ---------------------------------------------------------------------------
+// router + route: workgroups [0, row_wgs) hold one wave per router row (rows
+// 0..E-1 router, row E the shared-expert gate); lane l walks 8-element chunks
+// l, l+64, ...: acc = fmaf(w, x, acc) in element order, then an xor butterfly
+// over the wave.  The remaining workgroups prepare x's activation blocks for
+// the expert GEMVs (32 lanes per block) and take no ticket.
+constexpr int ROUTER_IT = 8;  // H <= 8 * 64 * 8
+
+__global__ __launch_bounds__(RR_THREADS) void k_moe_router_route(MoeArgs a, int row_wgs) {
+  const int H = a.H, E = a.E, M = a.M;
+  if ((int)blockIdx.x >= row_wgs) {
+    __shared__ uint32_t scratch[RR_THREADS / 32][24];
+    const int nb = H / 32;
+    const int g = threadIdx.x >> 5, i = threadIdx.x & 31;
+    const int blk = ((int)blockIdx.x - row_wgs) * (RR_THREADS / 32) + g;
+    const bool valid = blk < M * nb;
+    const uint32_t h = valid ? a.x[(size_t)(blk / nb) * H + (size_t)(blk % nb) * 32 + i] : 0u;
+    int E, sm;
+    xprep_lanes_build(h, i, scratch[g], E, sm);
+    __syncthreads();
+    if (valid) xprep_lanes_store(i, scratch[g], E, sm, a.xp_x + (size_t)blk * XP_DW);
+    return;
+  }
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int r = blockIdx.x * (RR_THREADS / 64) + wave;
+  if (r <= E) {
+    const bf16* wrow = (r < E) ? a.router + (size_t)r * H : a.shared_gate;
+    const int nc = H / 8;
+    uint4 wv[ROUTER_IT];
+#pragma unroll
+    for (int i = 0; i < ROUTER_IT; ++i) {
+      const int c = lane + 64 * i;
+      wv[i] = (c < nc) ? *reinterpret_cast<const uint4*>(wrow + (size_t)c * 8) : make_uint4(0, 0, 0, 0);
+    }
+    for (int m = 0; m < M; ++m) {
+      const bf16* xm = a.x + (size_t)m * H;
+      float acc = 0.0f;
+#pragma unroll
+      for (int i = 0; i < ROUTER_IT; ++i) {
+        const int c = lane + 64 * i;
+        if (c < nc) {
+          const uint4 xv = *reinterpret_cast<const uint4*>(xm + (size_t)c * 8);
+          const uint32_t ww[4] = {wv[i].x, wv[i].y, wv[i].z, wv[i].w};
+          const uint32_t xx[4] = {xv.x, xv.y, xv.z, xv.w};
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            acc = __builtin_fmaf(__uint_as_float(ww[t] << 16), __uint_as_float(xx[t] << 16), acc);
+            acc = __builtin_fmaf(__uint_as_float(ww[t] & 0xffff0000u), __uint_as_float(xx[t] & 0xffff0000u), acc);
+          }
+        }
+      }
+      acc = wave_fold64(acc);
+      if (lane == 0) {
+        if (r < E)
+          st_pub(a.logits + (size_t)m * E + r, acc);
+        else
+          a.gate_logit[m] = acc;
+      }
+    }
+  }
+  if (!ticket_last(a.ticket, (uint32_t)row_wgs - 1u)) return;
+  route_body(a);
 }
 
 __device__ __forceinline__ int slot_token(int slot, int M, int K) {
@@ -263,6 +304,36 @@ __global__ __launch_bounds__(GU_THREADS) void k_moe_gate_up(MoeArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// combine: grid (ceil(H/256), M).  out = bf16(fold_k r_k*w_k) + bf16(sig(g)*shared);
+// y = bf16(out) and, with a residual, y2 = bf16(resid + out).
+__device__ __forceinline__ float colsum_small(const float* r, int K) {
+  const int TY = K < 8 ? K : 8;
+  float t[8];
+  for (int y = 0; y < TY; ++y) {
+    float acc = 0.0f;
+    for (int rr = y; rr < K; rr += TY) acc = r[rr] + acc;
+    t[y] = acc;
+  }
+  float total = t[0];
+  for (int j = 1; j < TY; ++j) total = t[j] + total;
+  return total;
+}
+
+__global__ __launch_bounds__(256) void k_moe_combine(MoeArgs a) {
+  const int m = blockIdx.y, h = blockIdx.x * 256 + threadIdx.x;
+  if (h >= a.H) return;
+  const int H = a.H, M = a.M, K = a.K;
+  float prod[MAX_TOPK];
+  for (int k = 0; k < K; ++k) prod[k] = bf2f(a.r[(size_t)(m * K + k) * H + h]) * a.w[m * K + k];
+  const float rr = round_bf(colsum_small(prod, K));
+  const float sg = sigmoid_bf16(round_bf(a.gate_logit[m]));
+  const float sh = round_bf(sg * bf2f(a.r[(size_t)(M * K + m) * H + h]));
+  const bf16 out = f2bf(rr + sh);
+  if (a.y) a.y[(size_t)m * H + h] = out;
+  if (a.y2) a.y2[(size_t)m * H + h] = f2bf(bf2f(a.resid[(size_t)m * H + h]) + bf2f(out));
+}
+
+// ---------------------------------------------------------------------------
 // down: grid (H/DOWN_ROWS, M*K+1), 256 threads; each lane-group owns two rows
 // (RPL = 2) so each LDS read of an activation block feeds two rows.
 template <int L, int IT>
@@ -305,57 +376,20 @@ __global__ __launch_bounds__(256) void k_moe_down(MoeArgs a) {
       dot2(A[p], B[p], lds + (size_t)tk * nb * XP_DW, nb, sub, ra, rb);
       ra = lane_fold<L>(ra);
       rb = lane_fold<L>(rb);
-      if (sub == 0) {
-        bf16* dst = a.r + (size_t)a.disp->slot[u][tk] * H + h0;
-        if (hi < DOWN_ROWS && h0 + hi < H) dst[hi] = f2bf(ra);
-        if (hi + 1 < DOWN_ROWS && h0 + hi + 1 < H) dst[hi + 1] = f2bf(rb);
+      // rows hi, hi+1 (hi even, H a multiple of 8): one 4-byte store of both
+      if (sub == 0 && hi < DOWN_ROWS && h0 + hi < H) {
+        bf16* dst = a.r + (size_t)a.disp->slot[u][tk] * H + h0 + hi;
+        *reinterpret_cast<uint32_t*>(dst) = (uint32_t)f2bf(ra) | ((uint32_t)f2bf(rb) << 16);
       }
     }
   }
 }
 
 // ---------------------------------------------------------------------------
-// combine: grid (ceil(H/256), M).  out = bf16(fold_k r_k*w_k) + bf16(sig(g)*shared);
-// y = bf16(out) and, with a residual, y2 = bf16(resid + out).
-__device__ __forceinline__ float colsum_small(const float* r, int K) {
-  const int TY = K < 8 ? K : 8;
-  float t[8];
-  for (int y = 0; y < TY; ++y) {
-    float acc = 0.0f;
-    for (int rr = y; rr < K; rr += TY) acc = r[rr] + acc;
-    t[y] = acc;
-  }
-  float total = t[0];
-  for (int j = 1; j < TY; ++j) total = t[j] + total;
-  return total;
-}
-
-__global__ __launch_bounds__(256) void k_moe_combine(MoeArgs a, const bf16* __restrict__ resid,
-                                                     bf16* __restrict__ y2) {
-  const int H = a.H, M = a.M, K = a.K;
-  const int m = blockIdx.y, h = blockIdx.x * 256 + threadIdx.x;
-  if (h >= H) return;
-  float prod[MAX_TOPK];
-  for (int k = 0; k < K; ++k) prod[k] = bf2f(a.r[(size_t)(m * K + k) * H + h]) * a.w[m * K + k];
-  const float rr = round_bf(colsum_small(prod, K));
-  const float sg = sigmoid_bf16(round_bf(a.gate_logit[m]));
-  const float sh = round_bf(sg * bf2f(a.r[(size_t)(M * K + m) * H + h]));
-  const bf16 out = f2bf(rr + sh);
-  if (a.y) a.y[(size_t)m * H + h] = out;
-  if (y2) y2[(size_t)m * H + h] = f2bf(bf2f(resid[(size_t)m * H + h]) + bf2f(out));
-}
-
-// ---------------------------------------------------------------------------
-hipError_t launch_moe_router(const MoeArgs& a, hipStream_t st) {
-  const int row_wgs = (a.E + 1 + 3) / 4;
-  const int prep_wgs = a.xp_ready ? 0 : (a.M * (a.H / 32) + 7) / 8;
-  hipLaunchKernelGGL(k_moe_router, dim3(row_wgs + prep_wgs), dim3(256), 0, st, a, row_wgs);
-  return hipGetLastError();
-}
-
-hipError_t launch_moe_route(const MoeArgs& a, hipStream_t st) {
-  const int threads = 64 * (a.M > 2 ? a.M : 2);  // at least two waves: the dispatch covers 128 slots
-  hipLaunchKernelGGL(k_moe_route, dim3(1), dim3(threads), 0, st, a);
+hipError_t launch_moe_router_route(const MoeArgs& a, hipStream_t st) {
+  const int row_wgs = (a.E + 1 + RR_THREADS / 64 - 1) / (RR_THREADS / 64);
+  const int prep_wgs = a.xp_ready ? 0 : (a.M * (a.H / 32) + RR_THREADS / 32 - 1) / (RR_THREADS / 32);
+  hipLaunchKernelGGL(k_moe_router_route, dim3(row_wgs + prep_wgs), dim3(RR_THREADS), 0, st, a, row_wgs);
   return hipGetLastError();
 }
 
@@ -385,8 +419,8 @@ hipError_t launch_moe_gate_up(const MoeArgs& a, hipStream_t st) { MTPX_QROW_DISP
 
 hipError_t launch_moe_down(const MoeArgs& a, hipStream_t st) { MTPX_QROW_DISPATCH(a.F / 32, down_li, a, st); }
 
-hipError_t launch_moe_combine(const MoeArgs& a, const bf16* resid, bf16* y2, hipStream_t st) {
-  hipLaunchKernelGGL(k_moe_combine, dim3((a.H + 255) / 256, a.M), dim3(256), 0, st, a, resid, y2);
+hipError_t launch_moe_combine(const MoeArgs& a, hipStream_t st) {
+  hipLaunchKernelGGL(k_moe_combine, dim3((a.H + 255) / 256, a.M), dim3(256), 0, st, a);
   return hipGetLastError();
 }
 

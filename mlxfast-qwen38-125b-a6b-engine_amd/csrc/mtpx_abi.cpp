@@ -49,6 +49,7 @@ struct Ctx {
   size_t ws_size = 0;
   size_t ws_used = 0;
   MoeDispatch* last_disp = nullptr;  // inside the workspace of the last MoE call
+  uint32_t* tickets = nullptr;       // MOE_TICKETS counters, zero at rest
   int last_H = 0, last_E = 0, last_F = 0, last_gs = 0;
   // per-kernel timing with events on the launch stream (off by default)
   bool prof = false;
@@ -219,16 +220,18 @@ int moe_enqueue(Ctx* c, const mtpx_moe_weights* w, const uint16_t* x, int M, uin
   a.act = ws_take<uint16_t>(c, (size_t)slots * a.F);
   a.xp_act = ws_take<uint32_t>(c, (size_t)slots * (a.F / 32) * XP_DW);
   a.r = ws_take<uint16_t>(c, (size_t)slots * a.H);
+  a.resid = resid;
+  a.y2 = y2;
+  a.ticket = c->tickets;
   c->last_disp = a.disp;
   c->last_H = a.H;
   c->last_E = a.E;
   c->last_F = a.F;
   c->last_gs = a.gs;
-  LAUNCH(c, "moe_router", launch_moe_router(a, c->stream));
-  LAUNCH(c, "moe_route", launch_moe_route(a, c->stream));
+  LAUNCH(c, "moe_router_route", launch_moe_router_route(a, c->stream));
   LAUNCH(c, "moe_gate_up", launch_moe_gate_up(a, c->stream));
   LAUNCH(c, "moe_down", launch_moe_down(a, c->stream));
-  LAUNCH(c, "moe_combine", launch_moe_combine(a, resid, y2, c->stream));
+  LAUNCH(c, "moe_combine", launch_moe_combine(a, c->stream));
   return MTPX_OK;
 }
 
@@ -251,6 +254,14 @@ int mtpx_ctx_new(mtpx_ctx* out, int device) {
     return fail(MTPX_ERR_HIP, "stream creation failed on device %d", device);
   }
   c->stream = c->own;
+  // ticket counters of the fused MoE launches: zeroed once, every launch leaves them at zero
+  if (hipMalloc((void**)&c->tickets, MOE_TICKETS * 4) != hipSuccess ||
+      hipMemset(c->tickets, 0, MOE_TICKETS * 4) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
+    if (c->tickets) hipFree(c->tickets);
+    hipStreamDestroy(c->own);
+    delete c;
+    return fail(MTPX_ERR_HIP, "ticket allocation failed on device %d", device);
+  }
   out->ctx = c;
   return MTPX_OK;
 }
@@ -261,6 +272,7 @@ int mtpx_ctx_free(mtpx_ctx h) {
   hipSetDevice(c->device);
   hipStreamSynchronize(c->stream);
   if (c->ws) hipFree(c->ws);
+  if (c->tickets) hipFree(c->tickets);
   for (auto& r : c->pending) {
     hipEventDestroy(r.a);
     hipEventDestroy(r.b);
@@ -386,7 +398,7 @@ int mtpx_rmsnorm(mtpx_ctx h, const uint16_t* x, const uint16_t* resid, int M, in
                  uint16_t* sum_out, uint16_t* y) {
   Ctx* c = C(h);
   ARG(c && x && w && y, "null argument");
-  ARG(M >= 1 && H >= 1, "M=%d H=%d", M, H);
+  ARG(M >= 1 && H >= 1 && H <= 4096, "M=%d H=%d (H <= 4096)", M, H);
   if (set_device(c)) return MTPX_ERR_HIP;
   HIP_OK(launch_rmsnorm(x, resid, M, H, w, eps, sum_out, y, nullptr, c->stream));
   return MTPX_OK;

@@ -63,14 +63,17 @@ struct MoeArgs {
   bf16* act;           // [M*(K+1), F]
   uint32_t* xp_act;    // [M*(K+1), F/32, XP_DW]
   bf16* r;             // [M*(K+1), H]
+  const bf16* resid;   // [M, H] or null: y2 = bf16(resid + y)
+  bf16* y2;            // [M, H] or null
+  uint32_t* ticket;    // router+route ticket, zero at rest
 };
 constexpr int DOWN_ROWS = 128;
 
-hipError_t launch_moe_router(const MoeArgs& a, hipStream_t st);
-hipError_t launch_moe_route(const MoeArgs& a, hipStream_t st);
+constexpr int MOE_TICKETS = 64;
+hipError_t launch_moe_router_route(const MoeArgs& a, hipStream_t st);
 hipError_t launch_moe_gate_up(const MoeArgs& a, hipStream_t st);
 hipError_t launch_moe_down(const MoeArgs& a, hipStream_t st);
-hipError_t launch_moe_combine(const MoeArgs& a, const bf16* resid, bf16* y2, hipStream_t st);
+hipError_t launch_moe_combine(const MoeArgs& a, hipStream_t st);
 
 // --- attention (attn.hip)
 hipError_t launch_attn_prep(const bf16* qkv, int S, int QW, int HQ, int HK, int D, int ROT,

@@ -36,6 +36,7 @@ extern "C" {
 typedef struct mtpx_ctx_ { void* ctx; } mtpx_ctx;
 typedef struct mtpx_kv_ { void* ctx; } mtpx_kv;
 typedef struct mtpx_layer_ { void* ctx; } mtpx_layer;
+typedef struct mtpx_head_ { void* ctx; } mtpx_head;
 
 /* Thread-local text of the last error (replaces mlx-c's error handler,
  * mlx-c/mlx/c/error.h:15-27). */
@@ -192,6 +193,72 @@ int mtpx_layer_weights_get(mtpx_layer layer, mtpx_layer_weights* out);
 /* y[M, H] for M tokens at the cache's offset; advances the offset by M. */
 int mtpx_layer_forward(mtpx_ctx ctx, mtpx_layer layer, mtpx_kv kv, const uint16_t* x, int M,
                        uint16_t* y);
+/* ---- a18: shortlist draft argmax ----------------------------------------------
+ * The drafter's headStep tail (Runner/Qwen4ExpMTPDrafter.swift:68-75, 91-108,
+ * 122-153): logits = bf16(W_sl x) over the shortlist rows of lm_head (q4
+ * [rows, H]), argmax over the bf16 logits (lowest position on ties), mapped
+ * through ids (ascending) -> out[0].  x is one bf16 row [H] on the device. */
+int mtpx_shortlist_argmax(mtpx_ctx ctx, const uint16_t* x, int H, const uint32_t* w,
+                          const uint16_t* s, const uint16_t* b, int group_size, int rows,
+                          const int32_t* ids, int32_t* out);
+
+/* ---- a17: the MTP head (one draft step) ------------------------------------------
+ * TrackQwen4ExpMTPModule.callAsFunction (Runner/Qwen4ExpMTP.swift:101-130) over
+ * the fast kernels of TrackFastHead.forward (Runner/FastModel/TrackFastHead.swift:101-153):
+ *   e = fc_embedding(rms(embed(ids)));  h = fc_hidden(rms_W(multi)) per stream
+ *   hyper = e (every stream) + h
+ *   attention block : (st, n) = hc_norm(hyper); (x, j) = mix(attn_hc, n); a = attn(x)
+ *   MoE block       : (st, n) = hc_norm(st + a*j); (x, j) = mix(mlp_hc, n); m = MoE(x)
+ *   multi_next, n   = hc_norm(st + m*j);  sample = mix(final_hc, n)
+ *   draft           = shortlist argmax of the last row's sample
+ * mix(hc, n): lo = down n, inj = inject n, w = up silu(lo),
+ *   x = sum over streams of sigmoid(w) * n, j = 2 * sigmoid(inj). */
+typedef struct {
+  const uint32_t* w; const uint16_t* s; const uint16_t* b; /* q4 matrix; w == NULL: absent */
+} mtpx_q4;
+
+/* One hyper-connection mixer (TrackHC, Runner/FastModel/TrackFastModel.swift:182-195,
+ * bound at :374-402). */
+typedef struct {
+  const uint16_t* norm_scale; /* bf16 [hc*H]: hc_norm weight / hc_count */
+  mtpx_q4 down;               /* [lowrank, hc*H] input_mix_weight_down */
+  mtpx_q4 inject;             /* [hc, hc*H] block_inject_weight (w == NULL: none) */
+  mtpx_q4 up;                 /* [hc*H, lowrank] input_mix_weight_up */
+} mtpx_hc_weights;
+
+typedef struct {
+  mtpx_layer_config layer;     /* the head's decoder layer (attention + MoE) */
+  int hc;                      /* hc_count (4) */
+  int lowrank;                 /* hc_lowrank (320) */
+  int64_t vocab;               /* rows of embed_tokens / lm_head (248320) */
+  int shortlist_low;           /* shortlist ids 0..low-1 (98304; padded so the count % 8 == 0) */
+  int64_t shortlist_special_from; /* plus ids special_from..vocab-1 (248044) */
+} mtpx_head_config;
+
+typedef struct {
+  mtpx_q4 embed;                       /* [vocab, H] the target's embed_tokens */
+  const uint16_t* pre_norm_embedding;  /* bf16 [H] */
+  const uint16_t* pre_norm_hidden;     /* bf16 [hc*H]: one statistic over the flat row */
+  mtpx_q4 fc_embedding;                /* [H, H] */
+  mtpx_q4 fc_hidden;                   /* [H, H], applied to each stream */
+  mtpx_hc_weights attn_hc, mlp_hc, final_hc; /* final_hc has no inject */
+  mtpx_layer_weights layer;            /* attn_norm / post_norm unused */
+  mtpx_q4 shortlist;                   /* [shortlist_rows, H] lm_head rows */
+  const int32_t* shortlist_ids;        /* int32 [shortlist_rows], ascending */
+  int shortlist_rows;
+} mtpx_head_weights;
+
+int mtpx_head_new_random(mtpx_ctx ctx, const mtpx_head_config* cfg, uint64_t seed, mtpx_head* out);
+int mtpx_head_free(mtpx_head head);
+int mtpx_head_weights_get(mtpx_head head, mtpx_head_weights* out);
+/* One head application over S <= 8 inputs at the cache's offset (advances it by S):
+ * ids int32 [S] and multi bf16 [S, hc*H] on the device -> multi_next bf16 [S, hc*H],
+ * sample bf16 [S, H] (may be NULL), draft int32 [1] (the last row's shortlist argmax;
+ * may be NULL).  An id outside [0, vocab) embeds as a zero row. */
+int mtpx_head_forward(mtpx_ctx ctx, mtpx_head head, mtpx_kv kv, const int32_t* ids, int S,
+                      const uint16_t* multi, uint16_t* multi_next, uint16_t* sample,
+                      int32_t* draft);
+
 /* ---- per-kernel timing (replaces TrackFastProfile, Runner/FastModel/TrackFastWeights.swift:81-98) ----
  * With profiling on, every launch the library issues is bracketed by HIP events
  * on the context stream.  mtpx_profile_dump synchronises and writes one line per

@@ -34,16 +34,20 @@ __device__ __forceinline__ VI wave_best(VI x) {
   return x;
 }
 
+__device__ __forceinline__ float ld_val(const float* p) { return *p; }
+__device__ __forceinline__ float ld_val(const bf16* p) { return bf2f(*p); }
+
 // grid (parts, rows): best (value, index) of each AM_SPAN slice of a row.
-__global__ __launch_bounds__(256) void k_argmax_part(const float* __restrict__ x, int64_t V, int parts,
+template <typename T>
+__global__ __launch_bounds__(256) void k_argmax_part(const T* __restrict__ x, int64_t V, int parts,
                                                      float* __restrict__ pval, int32_t* __restrict__ pidx) {
   __shared__ VI wb[4];
   const int part = blockIdx.x, row = blockIdx.y;
-  const float* xr = x + (size_t)row * V;
+  const T* xr = x + (size_t)row * V;
   const int64_t b = (int64_t)part * AM_SPAN;
   const int64_t e = b + AM_SPAN < V ? b + AM_SPAN : V;
   VI best{-__uint_as_float(0x7f800000u), 0x7fffffff};
-  for (int64_t i = b + threadIdx.x; i < e; i += 256) best = vi_best(best, VI{xr[i], (int)i});
+  for (int64_t i = b + threadIdx.x; i < e; i += 256) best = vi_best(best, VI{ld_val(xr + i), (int)i});
   best = wave_best(best);
   if ((threadIdx.x & 63) == 0) wb[threadIdx.x >> 6] = best;
   __syncthreads();
@@ -61,12 +65,12 @@ __device__ VI reduce_parts(const float* pval, const int32_t* pidx, int parts, in
   return wave_best(best);
 }
 
-// one wave per row
+// one wave per row; with ids the winning position is mapped through them
 __global__ void k_argmax_final(const float* __restrict__ pval, const int32_t* __restrict__ pidx, int rows,
-                               int parts, int32_t* __restrict__ out) {
+                               int parts, const int32_t* __restrict__ ids, int32_t* __restrict__ out) {
   const int row = blockIdx.x;
   const VI b = reduce_parts(pval, pidx, parts, row, threadIdx.x);
-  if (threadIdx.x == 0) out[row] = b.i;
+  if (threadIdx.x == 0) out[row] = ids ? ids[b.i] : b.i;
 }
 
 // one workgroup: wave r reduces row r, then thread 0 decides.
@@ -269,17 +273,27 @@ size_t argmax_work_items(int rows, int64_t V) { return (size_t)rows * ((V + AM_S
 hipError_t launch_argmax_rows(const float* x, int rows, int64_t V, float* pval, int32_t* pidx, int32_t* out,
                               hipStream_t st) {
   const int parts = (int)((V + AM_SPAN - 1) / AM_SPAN);
-  hipLaunchKernelGGL(k_argmax_part, dim3(parts, rows), dim3(256), 0, st, x, V, parts, pval, pidx);
+  hipLaunchKernelGGL(k_argmax_part<float>, dim3(parts, rows), dim3(256), 0, st, x, V, parts, pval, pidx);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(k_argmax_final, dim3(rows), dim3(64), 0, st, pval, pidx, rows, parts, out);
+  hipLaunchKernelGGL(k_argmax_final, dim3(rows), dim3(64), 0, st, pval, pidx, rows, parts, nullptr, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_argmax_rows_bf16(const bf16* x, int rows, int64_t V, float* pval, int32_t* pidx,
+                                   const int32_t* ids, int32_t* out, hipStream_t st) {
+  const int parts = (int)((V + AM_SPAN - 1) / AM_SPAN);
+  hipLaunchKernelGGL(k_argmax_part<bf16>, dim3(parts, rows), dim3(256), 0, st, x, V, parts, pval, pidx);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(k_argmax_final, dim3(rows), dim3(64), 0, st, pval, pidx, rows, parts, ids, out);
   return hipGetLastError();
 }
 
 hipError_t launch_accept_greedy(const float* logits, int k, int64_t V, const int32_t* drafts, int32_t kv_offset,
                                 float* pval, int32_t* pidx, int32_t* out3, hipStream_t st) {
   const int parts = (int)((V + AM_SPAN - 1) / AM_SPAN);
-  hipLaunchKernelGGL(k_argmax_part, dim3(parts, k + 1), dim3(256), 0, st, logits, V, parts, pval, pidx);
+  hipLaunchKernelGGL(k_argmax_part<float>, dim3(parts, k + 1), dim3(256), 0, st, logits, V, parts, pval, pidx);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(k_accept_greedy, dim3(1), dim3(64 * (k + 1)), 0, st, pval, pidx, k, parts, drafts, kv_offset,
@@ -311,10 +325,10 @@ hipError_t launch_accept_sample(const float* tlogits, const float* dlogits, int 
   const float invT = 1.0f / temperature;
   hipError_t e;
   // row maxima: verify rows then draft rows (two launches over the two arrays)
-  hipLaunchKernelGGL(k_argmax_part, dim3(parts, k + 1), dim3(256), 0, st, tlogits, V, parts, pval, pidx);
+  hipLaunchKernelGGL(k_argmax_part<float>, dim3(parts, k + 1), dim3(256), 0, st, tlogits, V, parts, pval, pidx);
   if ((e = hipGetLastError()) != hipSuccess) return e;
   if (k > 0) {
-    hipLaunchKernelGGL(k_argmax_part, dim3(parts, k), dim3(256), 0, st, dlogits, V, parts,
+    hipLaunchKernelGGL(k_argmax_part<float>, dim3(parts, k), dim3(256), 0, st, dlogits, V, parts,
                        pval + (size_t)(k + 1) * parts, pidx + (size_t)(k + 1) * parts);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }

@@ -6,6 +6,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <map>
 #include <string>
@@ -130,6 +131,13 @@ template <typename T>
 T* ws_take(Ctx* c, size_t count) {
   const size_t off = (c->ws_used + 255) & ~(size_t)255;
   c->ws_used = off + count * sizeof(T);
+  // Every entry point reserves its whole need before the first take; running
+  // past the reservation is an internal accounting error, never a user error.
+  // Stop here rather than hand a kernel memory outside the allocation.
+  if (c->ws_used > c->ws_size) {
+    fprintf(stderr, "mtpx: internal workspace accounting error (%zu > %zu bytes)\n", c->ws_used, c->ws_size);
+    abort();
+  }
   return reinterpret_cast<T*>(static_cast<char*>(c->ws) + off);
 }
 
@@ -232,6 +240,297 @@ int moe_enqueue(Ctx* c, const mtpx_moe_weights* w, const uint16_t* x, int M, uin
   LAUNCH(c, "moe_gate_up", launch_moe_gate_up(a, c->stream));
   LAUNCH(c, "moe_down", launch_moe_down(a, c->stream));
   LAUNCH(c, "moe_combine", launch_moe_combine(a, c->stream));
+  return MTPX_OK;
+}
+
+// Random-init weights on the device: N(0, sigma) bf16 from the counter-based
+// generator (stream = seed, tensor id), q4 matrices quantised with MLX's
+// affine_quantize, through one bf16 staging buffer.
+struct RandInit {
+  Ctx* c;
+  uint64_t seed;
+  int gs;
+  std::vector<void*>* allocs;
+  uint32_t tensor = 1;
+  bool ok = true;
+  uint16_t* tmp = nullptr;
+
+  void* alloc(size_t bytes) {
+    void* p = nullptr;
+    if (hipMalloc(&p, bytes) != hipSuccess) {
+      ok = false;
+      return nullptr;
+    }
+    allocs->push_back(p);
+    return p;
+  }
+  void qmat(int64_t rows, int K, const uint32_t** w, const uint16_t** s, const uint16_t** b) {
+    uint32_t* pw = (uint32_t*)alloc((size_t)rows * K / 2);
+    uint16_t* ps = (uint16_t*)alloc((size_t)rows * (K / gs) * 2);
+    uint16_t* pb = (uint16_t*)alloc((size_t)rows * (K / gs) * 2);
+    *w = pw;
+    *s = ps;
+    *b = pb;
+    if (!pw || !ps || !pb) return;
+    const int64_t slice = (int64_t)1 << 24;  // staging elements
+    const int64_t rows_per = slice / K > 0 ? slice / K : 1;
+    if (!tmp && hipMalloc(&tmp, (size_t)(rows_per * K > slice ? rows_per * K : slice) * 2) != hipSuccess) {
+      tmp = nullptr;
+      ok = false;
+      return;
+    }
+    for (int64_t r0 = 0; r0 < rows && ok; r0 += rows_per) {
+      const int64_t nr = rows - r0 < rows_per ? rows - r0 : rows_per;
+      if (launch_randn_bf16(tmp, nr * K, seed, tensor * 65536u + (uint32_t)(r0 / rows_per), 0.02f, c->stream) ||
+          launch_quantize(tmp, nr, K, gs, pw + r0 * (K / 8), ps + r0 * (K / gs), pb + r0 * (K / gs), c->stream))
+        ok = false;
+    }
+    ++tensor;
+  }
+  void qmat(int64_t rows, int K, mtpx_q4* q) { qmat(rows, K, &q->w, &q->s, &q->b); }
+  // sigma > 0: N(0, sigma); sigma == 0: filled with the bf16 pattern `ones`
+  const uint16_t* dense(int64_t n, float sigma, uint16_t ones = 0x3f80) {
+    uint16_t* p = (uint16_t*)alloc((size_t)n * 2);
+    if (!p) return nullptr;
+    if (sigma > 0.0f) {
+      if (launch_randn_bf16(p, n, seed, tensor * 65536u, sigma, c->stream)) ok = false;
+    } else if (launch_fill_bf16(p, n, ones, c->stream)) {
+      ok = false;
+    }
+    ++tensor;
+    return p;
+  }
+  // synchronise, release the staging buffer; MTPX_OK or an error (allocations stay listed)
+  int finish(const char* what) {
+    const hipError_t se = hipStreamSynchronize(c->stream);
+    if (tmp) hipFree(tmp);
+    tmp = nullptr;
+    if (!ok || se != hipSuccess) return fail(ok ? MTPX_ERR_HIP : MTPX_ERR_OOM, "%s initialisation failed", what);
+    return MTPX_OK;
+  }
+};
+
+uint16_t bf16_bits(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+int layer_check(const mtpx_layer_config* cfg) {
+  const int H = cfg->hidden, F = cfg->expert_width, gs = cfg->group_size;
+  const int HQ = cfg->heads, HK = cfg->kv_heads, D = cfg->head_dim;
+  ARG(gs_ok(gs) && k_ok(H, gs) && k_ok(F, gs) && k_ok(HQ * D, gs), "unsupported GEMV depths");
+  ARG(HK >= 1 && HQ % HK == 0 && D <= 256 && cfg->rot_dims <= D && cfg->max_positions >= 1, "attention dims");
+  return MTPX_OK;
+}
+
+// Attention + MoE weights of one decoder layer (random init), RoPE tables from the host.
+int layer_create(Ctx* c, const mtpx_layer_config* cfg, uint64_t seed, Layer** out) {
+  int rc = layer_check(cfg);
+  if (rc) return rc;
+  const int H = cfg->hidden, E = cfg->experts, F = cfg->expert_width, gs = cfg->group_size;
+  const int HQ = cfg->heads, HK = cfg->kv_heads, D = cfg->head_dim;
+  Layer* L = new Layer();
+  L->cfg = *cfg;
+  memset(&L->w, 0, sizeof(L->w));
+  const int QW = 2 * HQ * D + 2 * HK * D + cfg->index_dim;
+  L->QW = QW;
+  L->w.qkv_rows = QW;
+  RandInit ri{c, seed, gs, &L->allocs};
+  L->w.attn_norm = ri.dense(H, 0.0f);
+  L->w.post_norm = ri.dense(H, 0.0f);
+  L->w.q_norm = ri.dense(D, 0.0f);
+  L->w.k_norm = ri.dense(D, 0.0f);
+  ri.qmat(QW, H, &L->w.qkv_w, &L->w.qkv_s, &L->w.qkv_b);
+  ri.qmat(H, HQ * D, &L->w.o_w, &L->w.o_s, &L->w.o_b);
+  mtpx_moe_weights& m = L->w.moe;
+  m.hidden = H;
+  m.experts = E;
+  m.top_k = cfg->top_k;
+  m.expert_width = F;
+  m.group_size = gs;
+  m.router = ri.dense((int64_t)E * H, 0.02f);
+  m.shared_gate = ri.dense(H, 0.02f);
+  ri.qmat((int64_t)E * F, H, &m.gate_w, &m.gate_s, &m.gate_b);
+  ri.qmat((int64_t)E * F, H, &m.up_w, &m.up_s, &m.up_b);
+  ri.qmat((int64_t)E * H, F, &m.down_w, &m.down_s, &m.down_b);
+  ri.qmat(F, H, &m.sh_gate_w, &m.sh_gate_s, &m.sh_gate_b);
+  ri.qmat(F, H, &m.sh_up_w, &m.sh_up_s, &m.sh_up_b);
+  ri.qmat(H, F, &m.sh_down_w, &m.sh_down_s, &m.sh_down_b);
+  // rotate-half RoPE tables: entry d uses theta^(-2*(d mod rot/2)/rot)
+  const int rot = cfg->rot_dims;
+  std::vector<uint16_t> ct((size_t)cfg->max_positions * rot), st((size_t)cfg->max_positions * rot);
+  for (int64_t p = 0; p < cfg->max_positions; ++p)
+    for (int d = 0; d < rot; ++d) {
+      const int i = d % (rot / 2);
+      const double inv = std::pow((double)cfg->rope_theta, -2.0 * (double)i / (double)rot);
+      const double a = (double)p * inv;
+      ct[(size_t)p * rot + d] = bf16_bits((float)std::cos(a));
+      st[(size_t)p * rot + d] = bf16_bits((float)std::sin(a));
+    }
+  uint16_t* dc = (uint16_t*)ri.alloc(ct.size() * 2);
+  uint16_t* ds = (uint16_t*)ri.alloc(st.size() * 2);
+  if (dc && ds &&
+      (hipMemcpyAsync(dc, ct.data(), ct.size() * 2, hipMemcpyHostToDevice, c->stream) != hipSuccess ||
+       hipMemcpyAsync(ds, st.data(), st.size() * 2, hipMemcpyHostToDevice, c->stream) != hipSuccess))
+    ri.ok = false;
+  L->w.rope_cos = dc;
+  L->w.rope_sin = ds;
+  if ((rc = ri.finish("layer"))) {
+    for (void* p : L->allocs) hipFree(p);
+    delete L;
+    return rc;
+  }
+  *out = L;
+  return MTPX_OK;
+}
+
+// Attention sublayer for M tokens whose prepared input blocks are in xp:
+// qkv GEMV, q/k norm + RoPE + KV append, verify attention with the output gate,
+// o_proj GEMV -> o [M, H].  xp is reused for the gated attention output, so it
+// holds max(H, HQ*D)/32 blocks per token.  Workspace already reserved.
+int attn_enqueue(Ctx* c, const Layer* L, Kv* kv, uint32_t* xp, int M, uint16_t* o) {
+  const mtpx_layer_config& g = L->cfg;
+  const int H = g.hidden, HQ = g.heads, HK = g.kv_heads, D = g.head_dim, QW = L->QW, gs = g.group_size;
+  const int T = (int)(kv->offset + M);
+  uint16_t* qkv = ws_take<uint16_t>(c, (size_t)M * QW);
+  uint16_t* q = ws_take<uint16_t>(c, (size_t)M * HQ * D);
+  uint16_t* att = ws_take<uint16_t>(c, (size_t)M * HQ * D);
+  float* part = ws_take<float>(c, attn_partial_floats(M, HQ, D, T));
+  hipStream_t st = c->stream;
+  LAUNCH(c, "qmv_qkv", launch_qmv(L->w.qkv_w, L->w.qkv_s, L->w.qkv_b, QW, H, gs, xp, M, qkv, nullptr, st));
+  LAUNCH(c, "attn_prep", launch_attn_prep(qkv, M, QW, HQ, HK, D, g.rot_dims, L->w.q_norm, L->w.k_norm, g.eps,
+                                          L->w.rope_cos, L->w.rope_sin, (int)kv->offset, q, kv->k, kv->v,
+                                          kv->tmax, st));
+  LAUNCH(c, "attn_verify", launch_attn_verify(q, M, HQ, HK, D, kv->k, kv->v, kv->tmax, T,
+                                              1.0f / std::sqrt((float)D), part, qkv, QW, HQ * D, nullptr, att,
+                                              xp, st));
+  LAUNCH(c, "qmv_o", launch_qmv(L->w.o_w, L->w.o_s, L->w.o_b, H, HQ * D, gs, xp, M, o, nullptr, st));
+  return MTPX_OK;
+}
+
+size_t attn_ws_bytes(const Layer* L, int M, int T) {
+  const mtpx_layer_config& g = L->cfg;
+  const int HQ = g.heads, D = g.head_dim;
+  return al(2 * (size_t)M * L->QW) + al(2 * (size_t)M * HQ * D) * 2 + al(4 * attn_partial_floats(M, HQ, D, T));
+}
+
+// ---------------------------------------------------------------------------
+// MTP head
+struct Head {
+  mtpx_head_config cfg;
+  Layer* layer = nullptr;
+  mtpx_head_weights w;
+  std::vector<void*> allocs;
+};
+
+int head_check(const mtpx_head_config* cfg) {
+  int rc = layer_check(&cfg->layer);
+  if (rc) return rc;
+  const int H = cfg->layer.hidden, gs = cfg->layer.group_size;
+  ARG(cfg->hc >= 1 && cfg->hc <= 8 && cfg->lowrank >= 32 && cfg->lowrank % 32 == 0, "hc=%d lowrank=%d", cfg->hc,
+      cfg->lowrank);
+  ARG(k_ok(cfg->hc * H, gs) && k_ok(cfg->lowrank, gs), "unsupported mixer GEMV depths");
+  ARG(cfg->hc * H <= 256 * 48, "hc*hidden=%d above 12288", cfg->hc * H);
+  ARG(cfg->vocab >= 1 && cfg->vocab < ((int64_t)1 << 31) && cfg->shortlist_low >= 0, "vocab=%lld",
+      (long long)cfg->vocab);
+  return MTPX_OK;
+}
+
+// The drafter's shortlist (Runner/Qwen4ExpMTPDrafter.swift:91-108): ids 0..low-1
+// with low padded so the count is a multiple of 8, then special_from..vocab-1.
+std::vector<int32_t> shortlist_ids(const mtpx_head_config* cfg) {
+  const int64_t n = cfg->vocab;
+  const int64_t sf = cfg->shortlist_special_from;
+  const int64_t specials = (sf > cfg->shortlist_low && sf < n) ? n - sf : 0;
+  int64_t low = cfg->shortlist_low < n ? cfg->shortlist_low : n;
+  low += (8 - (low + specials) % 8) % 8;
+  std::vector<int32_t> ids;
+  for (int64_t i = 0; i < (low < n ? low : n); ++i) ids.push_back((int32_t)i);
+  for (int64_t i = 0; i < specials; ++i) ids.push_back((int32_t)(sf + i));
+  return ids;
+}
+
+size_t head_ws_bytes(const Head* hd, int S, int T) {
+  const mtpx_head_config& g = hd->cfg;
+  const int H = g.layer.hidden, W = g.hc * H, LW = g.lowrank, HQ = g.layer.heads, D = g.layer.head_dim;
+  const int XB = (H > HQ * D ? H : HQ * D) / 32;
+  // per mixer call (three per step): lo, act [S, LW]; inj [S, hc]; xpL; w [S, W]
+  const size_t mix = al(2 * (size_t)S * LW) * 2 + al(2 * (size_t)S * g.hc) + al(4 * (size_t)S * (LW / 32) * XP_DW) +
+                     al(2 * (size_t)S * W);
+  return moe_ws_bytes(&hd->w.layer.moe, S) + attn_ws_bytes(hd->layer, S, T) + 3 * mix + al(2 * (size_t)S * H) * 6 +
+         al(2 * (size_t)S * W) * 5 + al(2 * (size_t)S * g.hc) + al(4 * (size_t)S * XB * XP_DW) +
+         al(4 * (size_t)S * (W / 32) * XP_DW) + al(2 * (size_t)hd->w.shortlist_rows) +
+         al(4 * argmax_work_items(1, hd->w.shortlist_rows)) * 2 + 8192;
+}
+
+// One hyper-connection mixer over the normed rows (prepared blocks in xpW):
+// lo = down n, inj = inject n, act = silu(lo), w = up act,
+// x = sum_c sigmoid(w) * n (+ its prepared blocks in xpH), j = 2 * sigmoid(inj).
+int hc_mix_enqueue(Ctx* c, const Head* hd, const mtpx_hc_weights* hw, const uint16_t* normed, const uint32_t* xpW,
+                   int S, uint16_t* x, uint16_t* j, uint32_t* xpH) {
+  const mtpx_head_config& g = hd->cfg;
+  const int H = g.layer.hidden, W = g.hc * H, LW = g.lowrank, gs = g.layer.group_size;
+  hipStream_t st = c->stream;
+  uint16_t* lo = ws_take<uint16_t>(c, (size_t)S * LW);
+  uint16_t* act = ws_take<uint16_t>(c, (size_t)S * LW);
+  uint16_t* inj = ws_take<uint16_t>(c, (size_t)S * g.hc);
+  uint32_t* xpL = ws_take<uint32_t>(c, (size_t)S * (LW / 32) * XP_DW);
+  uint16_t* wm = ws_take<uint16_t>(c, (size_t)S * W);
+  LAUNCH(c, "hc_down", launch_qmv(hw->down.w, hw->down.s, hw->down.b, LW, W, gs, xpW, S, lo, nullptr, st));
+  if (hw->inject.w)
+    LAUNCH(c, "hc_inject", launch_qmv(hw->inject.w, hw->inject.s, hw->inject.b, g.hc, W, gs, xpW, S, inj, nullptr, st));
+  LAUNCH(c, "hc_silu", launch_silu_xprep(lo, S, LW, act, xpL, st));
+  LAUNCH(c, "hc_up", launch_qmv(hw->up.w, hw->up.s, hw->up.b, W, LW, gs, xpL, S, wm, nullptr, st));
+  LAUNCH(c, "hc_mix", launch_hc_mix(wm, normed, hw->inject.w ? inj : nullptr, S, g.hc, H, x, j, xpH, st));
+  return MTPX_OK;
+}
+
+int head_create(Ctx* c, const mtpx_head_config* cfg, uint64_t seed, Head** out) {
+  int rc = head_check(cfg);
+  if (rc) return rc;
+  Head* hd = new Head();
+  hd->cfg = *cfg;
+  memset(&hd->w, 0, sizeof(hd->w));
+  if ((rc = layer_create(c, &cfg->layer, seed, &hd->layer))) {
+    delete hd;
+    return rc;
+  }
+  hd->w.layer = hd->layer->w;
+  const int H = cfg->layer.hidden, W = cfg->hc * H, LW = cfg->lowrank;
+  RandInit ri{c, seed ^ 0x9E3779B97F4A7C15ull, cfg->layer.group_size, &hd->allocs};
+  mtpx_head_weights& w = hd->w;
+  ri.qmat(cfg->vocab, H, &w.embed);
+  w.pre_norm_embedding = ri.dense(H, 0.0f);
+  w.pre_norm_hidden = ri.dense(W, 0.0f);
+  ri.qmat(H, H, &w.fc_embedding);
+  ri.qmat(H, H, &w.fc_hidden);
+  mtpx_hc_weights* hcs[3] = {&w.attn_hc, &w.mlp_hc, &w.final_hc};
+  for (int i = 0; i < 3; ++i) {
+    mtpx_hc_weights* m = hcs[i];
+    // hc_norm weight 1.0 divided by hc_count (a power of two for hc in {1, 2, 4, 8})
+    m->norm_scale = ri.dense(W, 0.0f, bf16_bits(1.0f / (float)cfg->hc));
+    ri.qmat(LW, W, &m->down);
+    if (i < 2) ri.qmat(cfg->hc, W, &m->inject);
+    ri.qmat(W, LW, &m->up);
+  }
+  const std::vector<int32_t> ids = shortlist_ids(cfg);
+  w.shortlist_rows = (int)ids.size();
+  ri.qmat((int64_t)ids.size(), H, &w.shortlist);
+  int32_t* dids = (int32_t*)ri.alloc(ids.size() * 4);
+  if (dids && hipMemcpyAsync(dids, ids.data(), ids.size() * 4, hipMemcpyHostToDevice, c->stream) != hipSuccess)
+    ri.ok = false;
+  w.shortlist_ids = dids;
+  if ((rc = ri.finish("head"))) {
+    for (void* p : hd->allocs) hipFree(p);
+    for (void* p : hd->layer->allocs) hipFree(p);
+    delete hd->layer;
+    delete hd;
+    return rc;
+  }
+  *out = hd;
   return MTPX_OK;
 }
 
@@ -521,126 +820,10 @@ int mtpx_accept_sample(mtpx_ctx h, const float* tlogits, const float* dlogits, i
 int mtpx_layer_new_random(mtpx_ctx h, const mtpx_layer_config* cfg, uint64_t seed, mtpx_layer* out) {
   Ctx* c = C(h);
   ARG(c && cfg && out, "null argument");
-  const int H = cfg->hidden, E = cfg->experts, F = cfg->expert_width, gs = cfg->group_size;
-  const int HQ = cfg->heads, HK = cfg->kv_heads, D = cfg->head_dim;
-  ARG(gs_ok(gs) && k_ok(H, gs) && k_ok(F, gs) && k_ok(HQ * D, gs), "unsupported GEMV depths");
-  ARG(HK >= 1 && HQ % HK == 0 && D <= 256 && cfg->rot_dims <= D && cfg->max_positions >= 1, "attention dims");
   if (set_device(c)) return MTPX_ERR_HIP;
-  Layer* L = new Layer();
-  L->cfg = *cfg;
-  memset(&L->w, 0, sizeof(L->w));
-  const int QW = 2 * HQ * D + 2 * HK * D + cfg->index_dim;
-  L->QW = QW;
-  L->w.qkv_rows = QW;
-  auto alloc = [&](size_t bytes) -> void* {
-    void* p = nullptr;
-    if (hipMalloc(&p, bytes) != hipSuccess) return nullptr;
-    L->allocs.push_back(p);
-    return p;
-  };
-  bool ok = true;
-  uint32_t tensor = 1;
-  uint16_t* tmp = nullptr;
-  size_t tmp_n = 0;
-  auto qmat = [&](int64_t rows, int K, const uint32_t** w, const uint16_t** s, const uint16_t** b) {
-    uint32_t* pw = (uint32_t*)alloc((size_t)rows * K / 2);
-    uint16_t* ps = (uint16_t*)alloc((size_t)rows * (K / gs) * 2);
-    uint16_t* pb = (uint16_t*)alloc((size_t)rows * (K / gs) * 2);
-    if (!pw || !ps || !pb) {
-      ok = false;
-      return;
-    }
-    // generate and quantise in slices through one bf16 staging buffer
-    const int64_t slice = (int64_t)1 << 24;  // elements
-    const int64_t rows_per = slice / K > 0 ? slice / K : 1;
-    if (!tmp) {
-      tmp_n = (size_t)rows_per * K > (size_t)slice ? (size_t)rows_per * K : (size_t)slice;
-      if (hipMalloc(&tmp, tmp_n * 2) != hipSuccess) {
-        ok = false;
-        return;
-      }
-    }
-    for (int64_t r0 = 0; r0 < rows && ok; r0 += rows_per) {
-      const int64_t nr = rows - r0 < rows_per ? rows - r0 : rows_per;
-      if (launch_randn_bf16(tmp, nr * K, seed, tensor * 65536u + (uint32_t)(r0 / rows_per), 0.02f, c->stream) ||
-          launch_quantize(tmp, nr, K, gs, pw + r0 * (K / 8), ps + r0 * (K / gs), pb + r0 * (K / gs), c->stream))
-        ok = false;
-    }
-    ++tensor;
-    *w = pw;
-    *s = ps;
-    *b = pb;
-  };
-  auto dense = [&](int64_t n, float sigma) -> const uint16_t* {
-    uint16_t* p = (uint16_t*)alloc((size_t)n * 2);
-    if (!p) {
-      ok = false;
-      return nullptr;
-    }
-    if (sigma > 0.0f) {
-      if (launch_randn_bf16(p, n, seed, tensor * 65536u, sigma, c->stream)) ok = false;
-    } else if (launch_fill_bf16(p, n, 0x3f80, c->stream)) {
-      ok = false;
-    }
-    ++tensor;
-    return p;
-  };
-  L->w.attn_norm = dense(H, 0.0f);
-  L->w.post_norm = dense(H, 0.0f);
-  L->w.q_norm = dense(D, 0.0f);
-  L->w.k_norm = dense(D, 0.0f);
-  qmat(QW, H, &L->w.qkv_w, &L->w.qkv_s, &L->w.qkv_b);
-  qmat(H, HQ * D, &L->w.o_w, &L->w.o_s, &L->w.o_b);
-  mtpx_moe_weights& m = L->w.moe;
-  m.hidden = H;
-  m.experts = E;
-  m.top_k = cfg->top_k;
-  m.expert_width = F;
-  m.group_size = gs;
-  m.router = dense((int64_t)E * H, 0.02f);
-  m.shared_gate = dense(H, 0.02f);
-  qmat((int64_t)E * F, H, &m.gate_w, &m.gate_s, &m.gate_b);
-  qmat((int64_t)E * F, H, &m.up_w, &m.up_s, &m.up_b);
-  qmat((int64_t)E * H, F, &m.down_w, &m.down_s, &m.down_b);
-  qmat(F, H, &m.sh_gate_w, &m.sh_gate_s, &m.sh_gate_b);
-  qmat(F, H, &m.sh_up_w, &m.sh_up_s, &m.sh_up_b);
-  qmat(H, F, &m.sh_down_w, &m.sh_down_s, &m.sh_down_b);
-  // rotate-half RoPE tables: entry d uses theta^(-2*(d mod rot/2)/rot)
-  const int rot = cfg->rot_dims;
-  std::vector<uint16_t> ct((size_t)cfg->max_positions * rot), st((size_t)cfg->max_positions * rot);
-  auto tobf = [](float f) -> uint16_t {
-    uint32_t u;
-    memcpy(&u, &f, 4);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0;
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return (uint16_t)(u >> 16);
-  };
-  for (int64_t p = 0; p < cfg->max_positions; ++p)
-    for (int d = 0; d < rot; ++d) {
-      const int i = d % (rot / 2);
-      const double inv = std::pow((double)cfg->rope_theta, -2.0 * (double)i / (double)rot);
-      const double a = (double)p * inv;
-      ct[(size_t)p * rot + d] = tobf((float)std::cos(a));
-      st[(size_t)p * rot + d] = tobf((float)std::sin(a));
-    }
-  uint16_t* dc = (uint16_t*)alloc(ct.size() * 2);
-  uint16_t* ds = (uint16_t*)alloc(st.size() * 2);
-  if (dc && ds) {
-    if (hipMemcpyAsync(dc, ct.data(), ct.size() * 2, hipMemcpyHostToDevice, c->stream) != hipSuccess ||
-        hipMemcpyAsync(ds, st.data(), st.size() * 2, hipMemcpyHostToDevice, c->stream) != hipSuccess)
-      ok = false;
-  } else {
-    ok = false;
-  }
-  L->w.rope_cos = dc;
-  L->w.rope_sin = ds;
-  const hipError_t se = hipStreamSynchronize(c->stream);
-  if (tmp) hipFree(tmp);
-  if (!ok || se != hipSuccess) {
-    for (void* p : L->allocs) hipFree(p);
-    delete L;
-    return fail(ok ? MTPX_ERR_HIP : MTPX_ERR_OOM, "layer initialisation failed");
-  }
+  Layer* L = nullptr;
+  int rc = layer_create(c, cfg, seed, &L);
+  if (rc) return rc;
   out->ctx = L;
   return MTPX_OK;
 }
@@ -673,36 +856,24 @@ int mtpx_layer_forward(mtpx_ctx h, mtpx_layer lh, mtpx_kv kvh, const uint16_t* x
   int rc = moe_check(&L->w.moe, M);
   if (rc) return rc;
   if (set_device(c)) return MTPX_ERR_HIP;
-  const int H = g.hidden, HQ = g.heads, HK = g.kv_heads, D = g.head_dim, QW = L->QW, gs = g.group_size;
+  const int H = g.hidden, HQ = g.heads, D = g.head_dim;
   const int T = (int)(kv->offset + M);
-  const size_t need = moe_ws_bytes(&L->w.moe, M) + al(2 * (size_t)M * H) * 4 + al(2 * (size_t)M * QW) +
-                      al(2 * (size_t)M * HQ * D) * 2 + al(4 * (size_t)M * ((QW > HQ * D ? QW : HQ * D) / 32) * XP_DW) +
-                      al(4 * attn_partial_floats(M, HQ, D, T)) + al(4 * (size_t)M * (H / 32) * XP_DW) + 4096;
+  const int XB = (H > HQ * D ? H : HQ * D) / 32;
+  const size_t need = moe_ws_bytes(&L->w.moe, M) + attn_ws_bytes(L, M, T) + al(2 * (size_t)M * H) * 4 +
+                      al(4 * (size_t)M * XB * XP_DW) + al(4 * (size_t)M * (H / 32) * XP_DW) + 4096;
   if ((rc = ws_reserve(c, need))) return rc;
   c->ws_used = 0;
   uint16_t* h1 = ws_take<uint16_t>(c, (size_t)M * H);
-  uint16_t* qkv = ws_take<uint16_t>(c, (size_t)M * QW);
-  uint16_t* q = ws_take<uint16_t>(c, (size_t)M * HQ * D);
-  uint16_t* att = ws_take<uint16_t>(c, (size_t)M * HQ * D);
   uint16_t* o = ws_take<uint16_t>(c, (size_t)M * H);
   uint16_t* s = ws_take<uint16_t>(c, (size_t)M * H);
   uint16_t* h2 = ws_take<uint16_t>(c, (size_t)M * H);
-  uint32_t* xp = ws_take<uint32_t>(c, (size_t)M * ((QW > HQ * D ? QW : HQ * D) / 32) * XP_DW);
-  float* part = ws_take<float>(c, attn_partial_floats(M, HQ, D, T));
-  hipStream_t st = c->stream;
+  uint32_t* xp = ws_take<uint32_t>(c, (size_t)M * XB * XP_DW);
   uint32_t* xp2 = ws_take<uint32_t>(c, (size_t)M * (H / 32) * XP_DW);
+  hipStream_t st = c->stream;
   LAUNCH(c, "rmsnorm", launch_rmsnorm(x, nullptr, M, H, L->w.attn_norm, g.eps, nullptr, h1, xp, st));
-  LAUNCH(c, "qmv_qkv", launch_qmv(L->w.qkv_w, L->w.qkv_s, L->w.qkv_b, QW, H, gs, xp, M, qkv, nullptr, st));
-  LAUNCH(c, "attn_prep", launch_attn_prep(qkv, M, QW, HQ, HK, D, g.rot_dims, L->w.q_norm, L->w.k_norm, g.eps,
-                                          L->w.rope_cos, L->w.rope_sin, (int)kv->offset, q, kv->k, kv->v,
-                                          kv->tmax, st));
-  LAUNCH(c, "attn_verify", launch_attn_verify(q, M, HQ, HK, D, kv->k, kv->v, kv->tmax, T,
-                                              1.0f / std::sqrt((float)D), part, qkv, QW, HQ * D, nullptr, att,
-                                              xp, st));
-  LAUNCH(c, "qmv_o", launch_qmv(L->w.o_w, L->w.o_s, L->w.o_b, H, HQ * D, gs, xp, M, o, nullptr, st));
+  if ((rc = attn_enqueue(c, L, kv, xp, M, o))) return rc;
   LAUNCH(c, "rmsnorm", launch_rmsnorm(x, o, M, H, L->w.post_norm, g.eps, s, h2, xp2, st));
-  uint16_t* moe_out = h1;  // h1 is dead after the qkv GEMV
-  if ((rc = moe_enqueue(c, &L->w.moe, h2, M, moe_out, nullptr, nullptr, nullptr, s, y, xp2))) return rc;
+  if ((rc = moe_enqueue(c, &L->w.moe, h2, M, h1, nullptr, nullptr, nullptr, s, y, xp2))) return rc;
   kv->offset += M;
   return MTPX_OK;
 }
@@ -751,6 +922,130 @@ int mtpx_last_moe_bytes(mtpx_ctx h, int64_t* bytes, int32_t* n_unique) {
   auto B = [&](int64_t N, int64_t K) { return N * K / 2 + 4 * N * K / gs; };
   *bytes = (int64_t)(nu + 1) * (2 * B(F, H) + B(H, F)) + 2 * E * H + 2 * H;
   if (n_unique) *n_unique = nu;
+  return MTPX_OK;
+}
+
+int mtpx_shortlist_argmax(mtpx_ctx h, const uint16_t* x, int H, const uint32_t* w, const uint16_t* s,
+                          const uint16_t* b, int gs, int rows, const int32_t* ids, int32_t* out) {
+  Ctx* c = C(h);
+  ARG(c && x && w && s && b && out, "null argument");
+  ARG(gs_ok(gs) && k_ok(H, gs), "H=%d gs=%d", H, gs);
+  ARG(rows >= 1, "rows=%d", rows);
+  if (set_device(c)) return MTPX_ERR_HIP;
+  const size_t n = argmax_work_items(1, rows);
+  int rc = ws_reserve(c, al(4 * (size_t)(H / 32) * XP_DW) + al(2 * (size_t)rows) + al(n * 4) * 2 + 1024);
+  if (rc) return rc;
+  c->ws_used = 0;
+  uint32_t* xp = ws_take<uint32_t>(c, (size_t)(H / 32) * XP_DW);
+  uint16_t* y = ws_take<uint16_t>(c, (size_t)rows);
+  float* pv = ws_take<float>(c, n);
+  int32_t* pi = ws_take<int32_t>(c, n);
+  hipStream_t st = c->stream;
+  LAUNCH(c, "xprep", launch_xprep(x, 1, H, xp, st));
+  LAUNCH(c, "qmv_shortlist", launch_qmv(w, s, b, rows, H, gs, xp, 1, y, nullptr, st));
+  LAUNCH(c, "shortlist_argmax", launch_argmax_rows_bf16(y, 1, rows, pv, pi, ids, out, st));
+  return MTPX_OK;
+}
+
+int mtpx_head_new_random(mtpx_ctx h, const mtpx_head_config* cfg, uint64_t seed, mtpx_head* out) {
+  Ctx* c = C(h);
+  ARG(c && cfg && out, "null argument");
+  if (set_device(c)) return MTPX_ERR_HIP;
+  Head* hd = nullptr;
+  int rc = head_create(c, cfg, seed, &hd);
+  if (rc) return rc;
+  out->ctx = hd;
+  return MTPX_OK;
+}
+
+int mtpx_head_free(mtpx_head h) {
+  Head* hd = static_cast<Head*>(h.ctx);
+  if (!hd) return MTPX_OK;
+  for (void* p : hd->allocs) hipFree(p);
+  if (hd->layer) {
+    for (void* p : hd->layer->allocs) hipFree(p);
+    delete hd->layer;
+  }
+  delete hd;
+  return MTPX_OK;
+}
+
+int mtpx_head_weights_get(mtpx_head h, mtpx_head_weights* out) {
+  Head* hd = static_cast<Head*>(h.ctx);
+  ARG(hd && out, "null argument");
+  *out = hd->w;
+  return MTPX_OK;
+}
+
+int mtpx_head_forward(mtpx_ctx h, mtpx_head hh, mtpx_kv kvh, const int32_t* ids, int S, const uint16_t* multi,
+                      uint16_t* multi_next, uint16_t* sample, int32_t* draft) {
+  Ctx* c = C(h);
+  Head* hd = static_cast<Head*>(hh.ctx);
+  Kv* kv = static_cast<Kv*>(kvh.ctx);
+  ARG(c && hd && kv && ids && multi && multi_next, "null argument");
+  const mtpx_head_config& g = hd->cfg;
+  const mtpx_layer_config& lg = g.layer;
+  ARG(S >= 1 && S <= MAX_TOKENS, "S=%d", S);
+  ARG(kv->heads == lg.kv_heads && kv->dim == lg.head_dim, "kv cache geometry does not match the head");
+  ARG(kv->offset + S <= kv->tmax && kv->offset + S <= lg.max_positions, "cache full (offset %lld + %d)",
+      (long long)kv->offset, S);
+  int rc = moe_check(&hd->w.layer.moe, S);
+  if (rc) return rc;
+  if (set_device(c)) return MTPX_ERR_HIP;
+  const int H = lg.hidden, hc = g.hc, W = hc * H, gs = lg.group_size, HQ = lg.heads, D = lg.head_dim;
+  const int XB = (H > HQ * D ? H : HQ * D) / 32;
+  const float eps = lg.eps;
+  const mtpx_head_weights& w = hd->w;
+  if ((rc = ws_reserve(c, head_ws_bytes(hd, S, (int)kv->offset + S)))) return rc;
+  c->ws_used = 0;
+  uint16_t* e = ws_take<uint16_t>(c, (size_t)S * H);
+  uint16_t* en = ws_take<uint16_t>(c, (size_t)S * H);
+  uint16_t* emb = ws_take<uint16_t>(c, (size_t)S * H);
+  uint16_t* x = ws_take<uint16_t>(c, (size_t)S * H);
+  uint16_t* ao = ws_take<uint16_t>(c, (size_t)S * H);
+  uint16_t* samp = sample ? sample : ws_take<uint16_t>(c, (size_t)S * H);
+  uint16_t* mn = ws_take<uint16_t>(c, (size_t)S * W);
+  uint16_t* hs = ws_take<uint16_t>(c, (size_t)S * W);
+  uint16_t* st0 = ws_take<uint16_t>(c, (size_t)S * W);
+  uint16_t* st1 = ws_take<uint16_t>(c, (size_t)S * W);
+  uint16_t* nrm = ws_take<uint16_t>(c, (size_t)S * W);
+  uint16_t* j = ws_take<uint16_t>(c, (size_t)S * hc);
+  uint32_t* xpH = ws_take<uint32_t>(c, (size_t)S * XB * XP_DW);
+  uint32_t* xpW = ws_take<uint32_t>(c, (size_t)S * (W / 32) * XP_DW);
+  hipStream_t st = c->stream;
+  // e = fc_embedding(rms(embed(ids))); h = fc_hidden(rms_W(multi)) per stream
+  LAUNCH(c, "embed", launch_embed_rows(w.embed.w, w.embed.s, w.embed.b, H, gs, g.vocab, ids, S, e, st));
+  LAUNCH(c, "hc_norm", launch_hc_norm(e, nullptr, nullptr, S, 1, H, 0, w.pre_norm_embedding, eps, nullptr, en, xpH,
+                                      st));
+  LAUNCH(c, "qmv_fc", launch_qmv(w.fc_embedding.w, w.fc_embedding.s, w.fc_embedding.b, H, H, gs, xpH, S, emb,
+                                 nullptr, st));
+  LAUNCH(c, "hc_norm", launch_hc_norm(multi, nullptr, nullptr, S, 1, W, 0, w.pre_norm_hidden, eps, nullptr, mn, xpW,
+                                      st));
+  LAUNCH(c, "qmv_fc", launch_qmv(w.fc_hidden.w, w.fc_hidden.s, w.fc_hidden.b, H, H, gs, xpW, S * hc, hs, nullptr,
+                                 st));
+  // attention block: hyper = e + h; (st0, n) = hc_norm(hyper); (x, j) = mix(attn_hc, n); ao = attn(x)
+  LAUNCH(c, "hc_norm", launch_hc_norm(hs, emb, nullptr, S, hc, H, 0, w.attn_hc.norm_scale, eps, st0, nrm, xpW, st));
+  if ((rc = hc_mix_enqueue(c, hd, &w.attn_hc, nrm, xpW, S, x, j, xpH))) return rc;
+  if ((rc = attn_enqueue(c, hd->layer, kv, xpH, S, ao))) return rc;
+  // MoE block
+  LAUNCH(c, "hc_norm", launch_hc_norm(st0, ao, j, S, hc, H, 0, w.mlp_hc.norm_scale, eps, st1, nrm, xpW, st));
+  if ((rc = hc_mix_enqueue(c, hd, &w.mlp_hc, nrm, xpW, S, x, j, xpH))) return rc;
+  if ((rc = moe_enqueue(c, &w.layer.moe, x, S, ao, nullptr, nullptr, nullptr, nullptr, nullptr, xpH))) return rc;
+  // final mixer: multi_next = st1 + m*j; sample = mix(final_hc, hc_norm(multi_next))
+  LAUNCH(c, "hc_norm", launch_hc_norm(st1, ao, j, S, hc, H, 0, w.final_hc.norm_scale, eps, multi_next, nrm, xpW,
+                                      st));
+  if ((rc = hc_mix_enqueue(c, hd, &w.final_hc, nrm, xpW, S, samp, nullptr, xpH))) return rc;
+  if (draft) {
+    const int NS = w.shortlist_rows;
+    const size_t n = argmax_work_items(1, NS);
+    uint16_t* yl = ws_take<uint16_t>(c, (size_t)NS);
+    float* pv = ws_take<float>(c, n);
+    int32_t* pi = ws_take<int32_t>(c, n);
+    LAUNCH(c, "qmv_shortlist", launch_qmv(w.shortlist.w, w.shortlist.s, w.shortlist.b, NS, H, gs,
+                                          xpH + (size_t)(S - 1) * (H / 32) * XP_DW, 1, yl, nullptr, st));
+    LAUNCH(c, "shortlist_argmax", launch_argmax_rows_bf16(yl, 1, NS, pv, pi, w.shortlist_ids, draft, st));
+  }
+  kv->offset += S;
   return MTPX_OK;
 }
 

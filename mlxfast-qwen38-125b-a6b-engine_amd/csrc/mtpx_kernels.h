@@ -101,5 +101,17 @@ hipError_t launch_accept_sample(const float* tlogits, const float* dlogits, int 
                                 int32_t kv_offset, float* work, int32_t* out3, hipStream_t st);
 size_t accept_sample_work_floats(int k, int64_t V);
 size_t argmax_work_items(int rows, int64_t V);
+hipError_t launch_argmax_rows_bf16(const bf16* x, int rows, int64_t V, float* pval, int32_t* pidx,
+                                   const int32_t* ids, int32_t* out, hipStream_t st);
+
+// --- MTP head pieces (head.hip)
+hipError_t launch_embed_rows(const uint32_t* wq, const bf16* s, const bf16* b, int H, int gs, int64_t V,
+                             const int32_t* ids, int S, bf16* out, hipStream_t st);
+hipError_t launch_hc_norm(const bf16* residual, const bf16* out, const bf16* inject, int S, int hc, int H,
+                          int tile, const bf16* scale, float eps, bf16* stream, bf16* normed, uint32_t* xp,
+                          hipStream_t st);
+hipError_t launch_silu_xprep(const bf16* lo, int S, int LW, bf16* act, uint32_t* xp, hipStream_t st);
+hipError_t launch_hc_mix(const bf16* w, const bf16* normed, const bf16* inj, int S, int hc, int H, bf16* input,
+                         bf16* inject_out, uint32_t* xp, hipStream_t st);
 
 }  // namespace mtpx

@@ -11,9 +11,11 @@ from __future__ import annotations
 import ctypes as C
 
 from . import _lib
-from ._lib import Handle, LayerConfig, LayerWeights, MoEWeights, MtpxError, check
+from ._lib import (Handle, HCWeights, HeadConfig, HeadWeights, LayerConfig, LayerWeights, MoEWeights,
+                   MtpxError, Q4, check)
 
-__all__ = ["Context", "KVCache", "DecoderLayer", "MoEWeights", "LayerConfig", "MtpxError", "moe_weights_from"]
+__all__ = ["Context", "KVCache", "DecoderLayer", "MTPHead", "MoEWeights", "LayerConfig", "HeadConfig", "MtpxError",
+           "moe_weights_from"]
 
 
 def _ptr(t):
@@ -114,6 +116,11 @@ class Context:
                                           _ptr(drafts), temperature, seed, offset, kv_offset, _ptr(out3)),
               "accept_sample")
 
+    def shortlist_argmax(self, x, w, s, b, gs, ids, out):
+        """out[0] = ids[argmax_j bf16(W_j . x)] over the shortlist rows (lowest position on ties)."""
+        check(self.lib.mtpx_shortlist_argmax(self.h, _ptr(x), x.shape[-1], _ptr(w), _ptr(s), _ptr(b), gs,
+                                             ids.shape[0], _ptr(ids), _ptr(out)), "shortlist_argmax")
+
     def profile(self, on: bool = True):
         check(self.lib.mtpx_profile_enable(self.h, 1 if on else 0), "profile_enable")
 
@@ -205,6 +212,38 @@ class DecoderLayer:
     def forward(self, kv: KVCache, x, y):
         check(self.ctx.lib.mtpx_layer_forward(self.ctx.h, self.h, kv.h, _ptr(x), x.shape[0], _ptr(y)),
               "layer_forward")
+
+
+class MTPHead:
+    """The MTP head (embedding, two projections, one attention + MoE layer between
+    hyper-connection mixers, shortlist lm_head) with seeded random weights (mtpx_head)."""
+
+    def __init__(self, ctx: Context, cfg: HeadConfig, seed: int):
+        self.ctx = ctx
+        self.cfg = cfg
+        self.h = Handle()
+        check(ctx.lib.mtpx_head_new_random(ctx.h, C.byref(cfg), seed, C.byref(self.h)), "head_new_random")
+
+    def close(self):
+        if self.h.ctx:
+            self.ctx.lib.mtpx_head_free(self.h)
+            self.h.ctx = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def weights(self) -> HeadWeights:
+        w = HeadWeights()
+        check(self.ctx.lib.mtpx_head_weights_get(self.h, C.byref(w)), "head_weights_get")
+        return w
+
+    def forward(self, kv: KVCache, ids, multi, multi_next, sample=None, draft=None):
+        """One draft step over S = len(ids) inputs; advances the head cache by S."""
+        check(self.ctx.lib.mtpx_head_forward(self.ctx.h, self.h, kv.h, _ptr(ids), ids.shape[0], _ptr(multi),
+                                             _ptr(multi_next), _ptr(sample), _ptr(draft)), "head_forward")
 
 
 def moe_weights_from(tensors: dict, H, E, K, F, gs) -> MoEWeights:

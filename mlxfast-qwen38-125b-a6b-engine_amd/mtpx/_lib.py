@@ -43,6 +43,25 @@ class LayerWeights(C.Structure):
         ("moe", MoEWeights), ("qkv_rows", INT)]
 
 
+class Q4(C.Structure):
+    _fields_ = [("w", P), ("s", P), ("b", P)]
+
+
+class HCWeights(C.Structure):
+    _fields_ = [("norm_scale", P), ("down", Q4), ("inject", Q4), ("up", Q4)]
+
+
+class HeadConfig(C.Structure):
+    _fields_ = [("layer", LayerConfig), ("hc", INT), ("lowrank", INT), ("vocab", I64), ("shortlist_low", INT),
+                ("shortlist_special_from", I64)]
+
+
+class HeadWeights(C.Structure):
+    _fields_ = [("embed", Q4), ("pre_norm_embedding", P), ("pre_norm_hidden", P), ("fc_embedding", Q4),
+                ("fc_hidden", Q4), ("attn_hc", HCWeights), ("mlp_hc", HCWeights), ("final_hc", HCWeights),
+                ("layer", LayerWeights), ("shortlist", Q4), ("shortlist_ids", P), ("shortlist_rows", INT)]
+
+
 _SIGS = {
     "mtpx_last_error": (C.c_char_p, []),
     "mtpx_version": (C.c_char_p, []),
@@ -72,6 +91,11 @@ _SIGS = {
     "mtpx_layer_weights_get": (INT, [Handle, C.POINTER(LayerWeights)]),
     "mtpx_layer_forward": (INT, [Handle, Handle, Handle, P, INT, P]),
     "mtpx_last_moe_bytes": (INT, [Handle, C.POINTER(I64), C.POINTER(I32)]),
+    "mtpx_shortlist_argmax": (INT, [Handle, P, INT, P, P, P, INT, INT, P, P]),
+    "mtpx_head_new_random": (INT, [Handle, C.POINTER(HeadConfig), U64, C.POINTER(Handle)]),
+    "mtpx_head_free": (INT, [Handle]),
+    "mtpx_head_weights_get": (INT, [Handle, C.POINTER(HeadWeights)]),
+    "mtpx_head_forward": (INT, [Handle, Handle, Handle, P, INT, P, P, P, P]),
     "mtpx_profile_enable": (INT, [Handle, INT]),
     "mtpx_profile_reset": (INT, [Handle]),
     "mtpx_profile_dump": (INT, [Handle, C.c_char_p, C.c_size_t]),

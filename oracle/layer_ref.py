@@ -53,11 +53,12 @@ def download(lw, cfg):
     return w
 
 
-def oracle_layer(w, cfg, kc, vc, x, pos0):
-    H, HQ, HK, D = cfg["hidden"], cfg["heads"], cfg["kv_heads"], cfg["head_dim"]
-    gs, eps, S = cfg["group_size"], cfg["eps"], x.shape[0]
-    h1 = O.rmsnorm(x, w["attn_norm"], eps)
-    qkv, _ = O.qmv(*w["qkv"], gs, h1)
+def oracle_attn(w, cfg, kc, vc, h, pos0):
+    """Attention sublayer on the (already normalised) input h: qkv, prep + KV append,
+    verify attention with the output gate, o_proj."""
+    HQ, HK, D = cfg["heads"], cfg["kv_heads"], cfg["head_dim"]
+    gs, eps, S = cfg["group_size"], cfg["eps"], h.shape[0]
+    qkv, _ = O.qmv(*w["qkv"], gs, h)
     q, k, v = O.attn_prep(qkv, HQ, HK, D, cfg["rot_dims"], w["q_norm"], w["k_norm"], eps, w["cos"], w["sin"], pos0)
     for s in range(S):
         kc[:, pos0 + s] = k[s]
@@ -65,6 +66,13 @@ def oracle_layer(w, cfg, kc, vc, x, pos0):
     att = O.attn_verify(q, kc, vc, pos0 + S, np.float32(1.0) / np.sqrt(np.float32(D)), O.ATTN_CHUNK)
     g = O.attn_gate(att.reshape(S, HQ * D), qkv, HQ * D)
     o, _ = O.qmv(*w["o"], gs, g)
+    return o
+
+
+def oracle_layer(w, cfg, kc, vc, x, pos0):
+    H, gs, eps = cfg["hidden"], cfg["group_size"], cfg["eps"]
+    h1 = O.rmsnorm(x, w["attn_norm"], eps)
+    o = oracle_attn(w, cfg, kc, vc, h1, pos0)
     s_ = O.f32_to_bf16(O.bf16_to_f32(x) + O.bf16_to_f32(o))
     h2 = O.rmsnorm(s_, w["post_norm"], eps)
     m = O.moe_block(w["moe"], h2, H, cfg["experts"], cfg["top_k"], cfg["expert_width"], gs)["y"]

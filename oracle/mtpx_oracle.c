@@ -621,6 +621,92 @@ void o_rmsnorm(const o_bf16* x, int M, int H, const o_bf16* w, float eps, o_bf16
 }
 
 /* ======================================================================== */
+/* a17: MTP head pieces                                                      */
+/* ======================================================================== */
+
+/* Rows of a q4 embedding table, dequantized with MLX's affine_dequantize
+ * arithmetic in bf16: w = bf16(bf16(scale * q) + bias)
+ * (MLX/backend/metal/kernels/quantized.h:3314-3372; the head reads the
+ * target's embed_tokens, Runner/Qwen4ExpMTP.swift:111). */
+void o_embed_rows(const uint32_t* wq, const o_bf16* scales, const o_bf16* biases, int H, int gs,
+                  const int32_t* ids, int S, o_bf16* out) {
+  for (int s = 0; s < S; ++s) {
+    const int64_t r = ids[s];
+    for (int k = 0; k < H; ++k) {
+      const uint32_t q = (wq[r * (H / 8) + k / 8] >> (4 * (k % 8))) & 0xfu;
+      const float sc = o_bf2f(scales[r * (H / gs) + k / gs]);
+      const float bi = o_bf2f(biases[r * (H / gs) + k / gs]);
+      out[(int64_t)s * H + k] = o_f2bf(o_round_bf(sc * (float)q) + bi);
+    }
+  }
+}
+
+/* Hyper-connection inject + group RMS norm (TrackFastKernels.injectNorm,
+ * Runner/FastModel/TrackFastKernels2.swift:60-113).  Per row s and stream c:
+ *   r = residual[s, c*H + d]   (tile: residual[s, d], one row for every stream)
+ *   with out and inject: r = bf16(r + bf16(out[s,d] * inject[s,c]))
+ *   with out only      : r = bf16(r + out[s,d])   (the head's embedding add,
+ *                        Runner/Qwen4ExpMTP.swift:111-115)
+ *   stream = r; group sum of squares in the 256-lane order of o_rmsnorm;
+ *   normed = bf16(scale[c*H+d] * bf16(r * inv)), inv = 1/sqrt(sum/H + eps). */
+void o_hc_norm(const o_bf16* residual, const o_bf16* out, const o_bf16* inject, int S, int hc,
+               int H, int tile, const o_bf16* scale, float eps, o_bf16* stream, o_bf16* normed) {
+  const int64_t W = (int64_t)hc * H;
+  float* r = (float*)malloc(sizeof(float) * (size_t)H);
+  for (int s = 0; s < S; ++s)
+    for (int c = 0; c < hc; ++c) {
+      const int64_t base = s * W + (int64_t)c * H;
+      for (int d = 0; d < H; ++d) {
+        float v = o_bf2f(residual[tile ? (int64_t)s * H + d : base + d]);
+        if (out && inject)
+          v = o_round_bf(v + o_round_bf(o_bf2f(out[(int64_t)s * H + d]) * o_bf2f(inject[(int64_t)s * hc + c])));
+        else if (out)
+          v = o_round_bf(v + o_bf2f(out[(int64_t)s * H + d]));
+        r[d] = v;
+        stream[base + d] = o_f2bf(v);
+      }
+      float lanes[256];
+      for (int t = 0; t < 256; ++t) {
+        float acc = 0.0f;
+        for (int d = t; d < H; d += 256) acc = fmaf(r[d], r[d], acc);
+        lanes[t] = acc;
+      }
+      const float inv = 1.0f / sqrtf(block_sum256(lanes) / (float)H + eps);
+      for (int d = 0; d < H; ++d)
+        normed[base + d] = o_f2bf(o_bf2f(scale[(int64_t)c * H + d]) * o_round_bf(r[d] * inv));
+    }
+  free(r);
+}
+
+void o_silu_rows(const o_bf16* x, int64_t n, o_bf16* y) {
+  for (int64_t i = 0; i < n; ++i) y[i] = o_f2bf(o_silu_bf16(o_bf2f(x[i])));
+}
+
+/* Mixer combine (TrackFastKernels.hcMix / TrackFastMixerKernels.upMix,
+ * Runner/FastModel/TrackFastKernels2.swift:229-280, TrackFastMixer.swift:125-180):
+ *   input[s,d] = bf16 running sum over c = 0..hc-1 of
+ *                bf16(sigmoid_bf16(w[s, c*H+d]) * normed[s, c*H+d])
+ *   inject_out[s,c] = bf16(2 * sigmoid_bf16(inj[s,c]))   (when inj != NULL) */
+void o_hc_mix(const o_bf16* w, const o_bf16* normed, const o_bf16* inj, int S, int hc, int H,
+              o_bf16* input, o_bf16* inject_out) {
+  const int64_t W = (int64_t)hc * H;
+  for (int s = 0; s < S; ++s) {
+    for (int d = 0; d < H; ++d) {
+      float acc = 0.0f;
+      for (int c = 0; c < hc; ++c) {
+        const int64_t i = s * W + (int64_t)c * H + d;
+        const float p = o_round_bf(o_sigmoid_bf16(o_bf2f(w[i])) * o_bf2f(normed[i]));
+        acc = o_round_bf(acc + p);
+      }
+      input[(int64_t)s * H + d] = o_f2bf(acc);
+    }
+    if (inj && inject_out)
+      for (int c = 0; c < hc; ++c)
+        inject_out[(int64_t)s * hc + c] = o_f2bf(2.0f * o_sigmoid_bf16(o_bf2f(inj[(int64_t)s * hc + c])));
+  }
+}
+
+/* ======================================================================== */
 /* a18 / a21: argmax and greedy acceptance                                   */
 /* Tie rule: the lowest id (Runner/Qwen4ExpMTPDrafter.swift:25-27).          */
 /* Accept rule (docs/qwen38-125b-a6b-port-notes.md:313-327): a_i = argmax of  */

@@ -79,6 +79,15 @@ void o_attn_gate(const o_bf16* att, const o_bf16* qkv, int S, int QW, int gate_o
                  int width, o_bf16* out);
 void o_rmsnorm(const o_bf16* x, int M, int H, const o_bf16* w, float eps, o_bf16* y);
 
+/* ---- a17: MTP head pieces (embedding, hyper-connection mixer) ------------ */
+void o_embed_rows(const uint32_t* wq, const o_bf16* scales, const o_bf16* biases, int H, int gs,
+                  const int32_t* ids, int S, o_bf16* out);
+void o_hc_norm(const o_bf16* residual, const o_bf16* out, const o_bf16* inject, int S, int hc,
+               int H, int tile, const o_bf16* scale, float eps, o_bf16* stream, o_bf16* normed);
+void o_silu_rows(const o_bf16* x, int64_t n, o_bf16* y);
+void o_hc_mix(const o_bf16* w, const o_bf16* normed, const o_bf16* inj, int S, int hc, int H,
+              o_bf16* input, o_bf16* inject_out);
+
 /* ---- a18, a21, a22: argmax and acceptance ------------------------------- */
 void o_argmax_rows(const float* x, int rows, int64_t V, int32_t* out);
 void o_accept_greedy(const float* logits, int k, int64_t V, const int32_t* drafts,

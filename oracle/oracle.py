@@ -66,6 +66,10 @@ def _declare(L):
         "o_uniform": (F32, [C.c_uint32]),
         "o_accept_sample": (None, [P, P, C.c_int, I64, P, F32, U64, U64, I32, P]),
         "o_softmax_row_sum": (F32, [P, I64]),
+        "o_embed_rows": (None, [P, P, P, C.c_int, C.c_int, P, C.c_int, P]),
+        "o_hc_norm": (None, [P, P, P, C.c_int, C.c_int, C.c_int, C.c_int, P, F32, P, P]),
+        "o_silu_rows": (None, [P, I64, P]),
+        "o_hc_mix": (None, [P, P, P, C.c_int, C.c_int, C.c_int, P, P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -238,6 +242,60 @@ def rmsnorm(x, w, eps):
     y = np.zeros_like(x)
     lib().o_rmsnorm(_p(x), M, H, _p(np.ascontiguousarray(w, np.uint16)), eps, _p(y))
     return y
+
+
+def embed_rows(wq, s, b, gs, ids):
+    """Rows ids of a q4 table, dequantized as bf16(bf16(s*q) + b)."""
+    wq = np.ascontiguousarray(wq, np.uint32)
+    H = wq.shape[1] * 8
+    ids = np.ascontiguousarray(ids, np.int32)
+    out = np.zeros((ids.size, H), np.uint16)
+    lib().o_embed_rows(_p(wq), _p(np.ascontiguousarray(s, np.uint16)), _p(np.ascontiguousarray(b, np.uint16)),
+                       H, gs, _p(ids), ids.size, _p(out))
+    return out
+
+
+def hc_norm(residual, out, inject, scale, hc, eps, tile=False):
+    """Hyper-connection inject + group RMS norm -> (stream [S, hc*H], normed [S, hc*H])."""
+    residual = np.ascontiguousarray(residual, np.uint16)
+    scale = np.ascontiguousarray(scale, np.uint16)
+    W = scale.size
+    H = W // hc
+    S = residual.shape[0]
+    stream = np.zeros((S, W), np.uint16)
+    normed = np.zeros((S, W), np.uint16)
+    o = None if out is None else np.ascontiguousarray(out, np.uint16)
+    i = None if inject is None else np.ascontiguousarray(inject, np.uint16)
+    lib().o_hc_norm(_p(residual), None if o is None else _p(o), None if i is None else _p(i), S, hc, H,
+                    1 if tile else 0, _p(scale), eps, _p(stream), _p(normed))
+    return stream, normed
+
+
+def silu_rows(x):
+    x = np.ascontiguousarray(x, np.uint16)
+    y = np.zeros_like(x)
+    lib().o_silu_rows(_p(x), x.size, _p(y))
+    return y
+
+
+def hc_mix(w, normed, inj, hc):
+    """Mixer combine -> (input [S, H], inject [S, hc] or None)."""
+    w = np.ascontiguousarray(w, np.uint16)
+    normed = np.ascontiguousarray(normed, np.uint16)
+    S, W = w.shape
+    H = W // hc
+    inp = np.zeros((S, H), np.uint16)
+    io = np.zeros((S, hc), np.uint16) if inj is not None else None
+    ij = None if inj is None else np.ascontiguousarray(inj, np.uint16)
+    lib().o_hc_mix(_p(w), _p(normed), None if ij is None else _p(ij), S, hc, H, _p(inp),
+                   None if io is None else _p(io))
+    return inp, io
+
+
+def shortlist_argmax(y_bf16, ids):
+    """Draft id: ids[argmax over the bf16 logits], lowest position on ties."""
+    v = bf16_to_f32(np.asarray(y_bf16, np.uint16).reshape(-1))
+    return int(np.asarray(ids, np.int32)[int(np.argmax(v))])
 
 
 def argmax_rows(x):

@@ -30,3 +30,38 @@ def test_struct_sizes_match_header_layout():
     # offsets of the pointer block after five ints (padded to 8)
     assert C.sizeof(_lib.MoEWeights) == 24 + 20 * 8
     assert _lib.LayerWeights.moe.offset == 12 * 8
+
+
+def test_struct_layouts_match_c_compiler(tmp_path):
+    """sizeof/offsetof of every ABI struct as gcc lays out include/mtpx.h, against ctypes."""
+    import shutil
+    import subprocess
+    if not shutil.which("gcc"):
+        pytest.skip("gcc not available")
+    inc = os.path.dirname(_lib.HEADER)
+    checks = {
+        "mtpx_moe_weights": (_lib.MoEWeights, ["router", "gate_w", "sh_down_b"]),
+        "mtpx_layer_config": (_lib.LayerConfig, ["rope_theta", "max_positions"]),
+        "mtpx_layer_weights": (_lib.LayerWeights, ["rope_sin", "moe", "qkv_rows"]),
+        "mtpx_q4": (_lib.Q4, ["s", "b"]),
+        "mtpx_hc_weights": (_lib.HCWeights, ["down", "inject", "up"]),
+        "mtpx_head_config": (_lib.HeadConfig, ["hc", "lowrank", "vocab", "shortlist_low", "shortlist_special_from"]),
+        "mtpx_head_weights": (_lib.HeadWeights, ["pre_norm_hidden", "attn_hc", "final_hc", "layer", "shortlist",
+                                                 "shortlist_ids", "shortlist_rows"]),
+    }
+    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "mtpx.h"', "int main(void) {"]
+    for name, (_, fields) in checks.items():
+        lines.append(f'printf("{name} %zu\\n", sizeof({name}));')
+        for f in fields:
+            lines.append(f'printf("{name}.{f} %zu\\n", offsetof({name}, {f}));')
+    lines.append("return 0; }")
+    src = tmp_path / "probe.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "probe"
+    subprocess.run(["gcc", "-I", inc, str(src), "-o", str(exe)], check=True)
+    got = dict(l.split() for l in subprocess.run([str(exe)], check=True, capture_output=True,
+                                                  text=True).stdout.splitlines())
+    for name, (cls, fields) in checks.items():
+        assert int(got[name]) == C.sizeof(cls), name
+        for f in fields:
+            assert int(got[f"{name}.{f}"]) == getattr(cls, f).offset, f"{name}.{f}"

@@ -37,6 +37,7 @@ typedef struct mtpx_ctx_ { void* ctx; } mtpx_ctx;
 typedef struct mtpx_kv_ { void* ctx; } mtpx_kv;
 typedef struct mtpx_layer_ { void* ctx; } mtpx_layer;
 typedef struct mtpx_head_ { void* ctx; } mtpx_head;
+typedef struct mtpx_drafter_ { void* ctx; } mtpx_drafter;
 
 /* Thread-local text of the last error (replaces mlx-c's error handler,
  * mlx-c/mlx/c/error.h:15-27). */
@@ -258,6 +259,46 @@ int mtpx_head_weights_get(mtpx_head head, mtpx_head_weights* out);
 int mtpx_head_forward(mtpx_ctx ctx, mtpx_head head, mtpx_kv kv, const int32_t* ids, int S,
                       const uint16_t* multi, uint16_t* multi_next, uint16_t* sample,
                       int32_t* draft);
+
+/* ---- a19: the drafter's per-request round state ---------------------------------
+ * CBv2MTPRequestStatefulDrafter as TrackQwen4ExpInlineMTPAssistant implements it
+ * (Runner/Qwen4ExpMTPDrafter.swift:162-475).  A drafter owns the head's KV cache
+ * for one request and the trusted target transitions (multi[t], token[t+1]) not
+ * yet in it.  Tokens and multi streams are device pointers (int32, bf16 [n, hc*H]);
+ * the state copies what it keeps.  Out-of-sequence calls (the reference's
+ * preconditions) return MTPX_ERR_STATE and leave the state unchanged. */
+#define MTPX_MAX_DRAFT_DEPTH 6 /* maximumDraftTokens */
+
+typedef struct {
+  int64_t cache_offset;      /* head cache positions */
+  int64_t committed_inputs;  /* trusted inputs: in the cache or in the backlog */
+  int64_t staged_inputs;     /* speculative inputs of the round in flight */
+  int64_t backlog_inputs;
+  int64_t round_base_offset, round_valid_offset;
+  int round_in_flight, round_draft_steps, has_frontier, released;
+} mtpx_drafter_info;
+
+/* makeRequestState (:277-279): a fresh state with an empty head cache. */
+int mtpx_drafter_new(mtpx_ctx ctx, mtpx_head head, mtpx_drafter* out);
+int mtpx_drafter_free(mtpx_drafter d);
+/* observeCommittedTarget (:288-316): n committed target inputs and their multi streams. */
+int mtpx_drafter_observe(mtpx_drafter d, const int32_t* tokens, const uint16_t* multi, int n);
+/* draftStep (:328-366): the first step of a round flushes the backlog plus this
+ * carry through the head; later steps feed back the previous draft and multi.
+ * -> draft int32 [1], multi bf16 [1, hc*H]. */
+int mtpx_drafter_step(mtpx_drafter d, const int32_t* token, const uint16_t* multi, int32_t* draft,
+                      uint16_t* multi_out);
+/* finalizeRound (:410-441): confirmed verify inputs; n committed drafts with the
+ * target's multi streams at their positions. */
+int mtpx_drafter_finalize(mtpx_drafter d, int confirmed_inputs, const int32_t* tokens,
+                          const uint16_t* multi, int n);
+/* discardRound (:443-454). */
+int mtpx_drafter_discard(mtpx_drafter d);
+/* releaseRequestState (:472-475): the state refuses every later call. */
+int mtpx_drafter_release(mtpx_drafter d);
+int mtpx_drafter_info_get(mtpx_drafter d, mtpx_drafter_info* out);
+/* requestStateBytesPerToken (:267-275). */
+int mtpx_drafter_bytes_per_token(mtpx_head head, int64_t* out);
 
 /* ---- per-kernel timing (replaces TrackFastProfile, Runner/FastModel/TrackFastWeights.swift:81-98) ----
  * With profiling on, every launch the library issues is bracketed by HIP events

@@ -13,6 +13,7 @@
 #include <vector>
 
 #include "../../include/mtpx.h"
+#include "drafter.h"
 #include "mtpx_kernels.h"
 
 using namespace mtpx;
@@ -534,6 +535,142 @@ int head_create(Ctx* c, const mtpx_head_config* cfg, uint64_t seed, Head** out) 
   return MTPX_OK;
 }
 
+// ---------------------------------------------------------------------------
+// Drafter backend: rows in pooled device buffers (token ids, then bf16 rows of
+// width W), the head run in windows of at most MAX_TOKENS inputs.  Buffers go
+// back to the pool when their Rows die; reuse is ordered behind earlier reads by
+// the one context stream.
+struct RowPool {
+  std::vector<std::pair<int, void*>> free_;  // (capacity rows, buffer)
+  std::vector<void*> all_;
+  void* get(int n, int W, int* cap) {
+    int c = 1;
+    while (c < n) c *= 2;
+    for (size_t i = 0; i < free_.size(); ++i)
+      if (free_[i].first == c) {
+        void* p = free_[i].second;
+        free_.erase(free_.begin() + i);
+        *cap = c;
+        return p;
+      }
+    void* p = nullptr;
+    if (hipMalloc(&p, al(4 * (size_t)c) + 2 * (size_t)c * W) != hipSuccess) return nullptr;
+    all_.push_back(p);
+    *cap = c;
+    return p;
+  }
+  void put(int cap, void* p) { free_.push_back({cap, p}); }
+  ~RowPool() {
+    for (void* p : all_) hipFree(p);
+  }
+};
+
+struct DevBackend {
+  struct Rows {
+    RowPool* pool = nullptr;
+    void* buf = nullptr;
+    int n = 0, cap = 0, W = 0;
+    Rows() = default;
+    Rows(const Rows&) = delete;
+    Rows& operator=(const Rows&) = delete;
+    Rows(Rows&& o) noexcept { *this = std::move(o); }
+    Rows& operator=(Rows&& o) noexcept {
+      if (this != &o) {
+        release();
+        pool = o.pool; buf = o.buf; n = o.n; cap = o.cap; W = o.W;
+        o.buf = nullptr; o.n = 0;
+      }
+      return *this;
+    }
+    ~Rows() { release(); }
+    void release() {
+      if (buf && pool) pool->put(cap, buf);
+      buf = nullptr;
+    }
+  };
+
+  Ctx* c = nullptr;
+  mtpx_head hh{nullptr};
+  Kv* kv = nullptr;
+  int W = 0;
+  RowPool pool;
+  uint16_t* multi_scratch = nullptr;  // [MAX_TOKENS, W]
+
+  static int count(const Rows& r) { return r.n; }
+  static int32_t* tok(const Rows& r) { return static_cast<int32_t*>(r.buf); }
+  static uint16_t* hid(const Rows& r) {
+    return reinterpret_cast<uint16_t*>(static_cast<char*>(r.buf) + al(4 * (size_t)r.cap));
+  }
+  bool ok(const Rows& r) const { return r.buf != nullptr; }
+
+  Rows make(const int32_t* t, const uint16_t* h, int n) {
+    Rows r;
+    r.pool = &pool;
+    r.W = W;
+    r.n = n;
+    r.buf = pool.get(n, W, &r.cap);
+    if (!r.buf) return r;
+    if ((t && hipMemcpyAsync(tok(r), t, 4 * (size_t)n, hipMemcpyDeviceToDevice, c->stream) != hipSuccess) ||
+        hipMemcpyAsync(hid(r), h, 2 * (size_t)n * W, hipMemcpyDeviceToDevice, c->stream) != hipSuccess)
+      r.release();
+    return r;
+  }
+
+  int head_run(const std::vector<const Rows*>& segs, int32_t* draft, uint16_t* multi) {
+    int S = 0;
+    for (const Rows* r : segs) S += r->n;
+    const int32_t* t = nullptr;
+    const uint16_t* h = nullptr;
+    Rows staged;
+    if (segs.size() == 1) {
+      t = tok(*segs[0]);
+      h = hid(*segs[0]);
+    } else {
+      staged.pool = &pool;
+      staged.W = W;
+      staged.n = S;
+      staged.buf = pool.get(S, W, &staged.cap);
+      if (!staged.buf) return MTPX_ERR_OOM;
+      int off = 0;
+      for (const Rows* r : segs) {
+        HIP_OK(hipMemcpyAsync(tok(staged) + off, tok(*r), 4 * (size_t)r->n, hipMemcpyDeviceToDevice, c->stream));
+        HIP_OK(hipMemcpyAsync(hid(staged) + (size_t)off * W, hid(*r), 2 * (size_t)r->n * W,
+                              hipMemcpyDeviceToDevice, c->stream));
+        off += r->n;
+      }
+      t = tok(staged);
+      h = hid(staged);
+    }
+    mtpx_ctx ch{c};
+    mtpx_kv kh{kv};
+    int rc = MTPX_OK, last = 0;
+    for (int off = 0; off < S; off += MAX_TOKENS) {
+      last = S - off < MAX_TOKENS ? S - off : MAX_TOKENS;
+      const bool end = off + last == S;
+      rc = mtpx_head_forward(ch, hh, kh, t + off, last, h + (size_t)off * W, multi_scratch, nullptr,
+                             end ? draft : nullptr);
+      if (rc) return rc;
+    }
+    HIP_OK(hipMemcpyAsync(multi, multi_scratch + (size_t)(last - 1) * W, 2 * (size_t)W, hipMemcpyDeviceToDevice,
+                          c->stream));
+    return MTPX_OK;
+  }
+  int head(const std::vector<const Rows*>& segs, int32_t* draft, uint16_t* multi) {
+    return head_run(segs, draft, multi);
+  }
+  int64_t offset() { return kv->offset; }
+  int64_t trim(int64_t n) {
+    const int64_t t = n < kv->offset ? n : kv->offset;
+    kv->offset -= t;
+    return t;
+  }
+};
+
+struct DrafterObj {
+  DevBackend be;
+  Drafter<DevBackend>* d = nullptr;
+};
+
 }  // namespace
 
 extern "C" {
@@ -1046,6 +1183,114 @@ int mtpx_head_forward(mtpx_ctx h, mtpx_head hh, mtpx_kv kvh, const int32_t* ids,
     LAUNCH(c, "shortlist_argmax", launch_argmax_rows_bf16(yl, 1, NS, pv, pi, w.shortlist_ids, draft, st));
   }
   kv->offset += S;
+  return MTPX_OK;
+}
+
+static int dr_status(DrafterObj* o, int rc) {
+  if (rc == DR_OK) return MTPX_OK;
+  if (rc == DR_ERR_BACKEND) return g_err.empty() ? fail(MTPX_ERR_HIP, "%s", o->d->error().c_str()) : MTPX_ERR_HIP;
+  return fail(rc == DR_ERR_ARG ? MTPX_ERR_ARG : MTPX_ERR_STATE, "%s", o->d->error().c_str());
+}
+
+int mtpx_drafter_new(mtpx_ctx h, mtpx_head hh, mtpx_drafter* out) {
+  Ctx* c = C(h);
+  Head* hd = static_cast<Head*>(hh.ctx);
+  ARG(c && hd && out, "null argument");
+  if (set_device(c)) return MTPX_ERR_HIP;
+  const mtpx_layer_config& lg = hd->cfg.layer;
+  mtpx_kv kv{nullptr};
+  int rc = mtpx_kv_new(h, lg.kv_heads, lg.head_dim, lg.max_positions, &kv);
+  if (rc) return rc;
+  DrafterObj* o = new DrafterObj();
+  o->be.c = c;
+  o->be.hh = hh;
+  o->be.kv = static_cast<Kv*>(kv.ctx);
+  o->be.W = hd->cfg.hc * lg.hidden;
+  if (hipMalloc((void**)&o->be.multi_scratch, 2 * (size_t)MAX_TOKENS * o->be.W) != hipSuccess) {
+    mtpx_kv_free(kv);
+    delete o;
+    return fail(MTPX_ERR_OOM, "drafter scratch");
+  }
+  o->d = new Drafter<DevBackend>(o->be);
+  out->ctx = o;
+  return MTPX_OK;
+}
+
+int mtpx_drafter_free(mtpx_drafter dh) {
+  DrafterObj* o = static_cast<DrafterObj*>(dh.ctx);
+  if (!o) return MTPX_OK;
+  hipSetDevice(o->be.c->device);
+  hipStreamSynchronize(o->be.c->stream);
+  delete o->d;  // rows go back to the pool first
+  if (o->be.multi_scratch) hipFree(o->be.multi_scratch);
+  mtpx_kv_free(mtpx_kv{o->be.kv});
+  delete o;
+  return MTPX_OK;
+}
+
+int mtpx_drafter_observe(mtpx_drafter dh, const int32_t* tokens, const uint16_t* multi, int n) {
+  DrafterObj* o = static_cast<DrafterObj*>(dh.ctx);
+  ARG(o, "null drafter");
+  if (set_device(o->be.c)) return MTPX_ERR_HIP;
+  g_err.clear();
+  return dr_status(o, o->d->observe(tokens, multi, n, o->be.W));
+}
+
+int mtpx_drafter_step(mtpx_drafter dh, const int32_t* token, const uint16_t* multi, int32_t* draft,
+                      uint16_t* multi_out) {
+  DrafterObj* o = static_cast<DrafterObj*>(dh.ctx);
+  ARG(o && draft && multi_out, "null argument");
+  if (set_device(o->be.c)) return MTPX_ERR_HIP;
+  g_err.clear();
+  return dr_status(o, o->d->step(token, multi, draft, multi_out));
+}
+
+int mtpx_drafter_finalize(mtpx_drafter dh, int confirmed_inputs, const int32_t* tokens, const uint16_t* multi,
+                          int n) {
+  DrafterObj* o = static_cast<DrafterObj*>(dh.ctx);
+  ARG(o, "null drafter");
+  if (set_device(o->be.c)) return MTPX_ERR_HIP;
+  g_err.clear();
+  return dr_status(o, o->d->finalize(confirmed_inputs, tokens, multi, n));
+}
+
+int mtpx_drafter_discard(mtpx_drafter dh) {
+  DrafterObj* o = static_cast<DrafterObj*>(dh.ctx);
+  ARG(o, "null drafter");
+  g_err.clear();
+  return dr_status(o, o->d->discard());
+}
+
+int mtpx_drafter_release(mtpx_drafter dh) {
+  DrafterObj* o = static_cast<DrafterObj*>(dh.ctx);
+  ARG(o, "null drafter");
+  o->d->release();
+  return MTPX_OK;
+}
+
+int mtpx_drafter_info_get(mtpx_drafter dh, mtpx_drafter_info* out) {
+  DrafterObj* o = static_cast<DrafterObj*>(dh.ctx);
+  ARG(o && out, "null argument");
+  Drafter<DevBackend>& d = *o->d;
+  out->cache_offset = d.cache_offset();
+  out->committed_inputs = d.committed_inputs();
+  out->staged_inputs = d.staged_inputs();
+  out->backlog_inputs = d.backlog_inputs();
+  out->round_base_offset = d.round_base_offset();
+  out->round_valid_offset = d.round_valid_offset();
+  out->round_in_flight = d.in_flight();
+  out->round_draft_steps = d.draft_steps();
+  out->has_frontier = d.has_frontier();
+  out->released = d.released();
+  return MTPX_OK;
+}
+
+int mtpx_drafter_bytes_per_token(mtpx_head hh, int64_t* out) {
+  Head* hd = static_cast<Head*>(hh.ctx);
+  ARG(hd && out, "null argument");
+  const mtpx_layer_config& lg = hd->cfg.layer;
+  const int64_t per_layer = 2 * (int64_t)lg.kv_heads * lg.head_dim + lg.index_dim;
+  *out = per_layer * 1 * 2 + (int64_t)hd->cfg.hc * lg.hidden * 2 + 4;  // one head layer, bf16 rows, one int32 id
   return MTPX_OK;
 }
 

@@ -11,10 +11,10 @@ from __future__ import annotations
 import ctypes as C
 
 from . import _lib
-from ._lib import (Handle, HCWeights, HeadConfig, HeadWeights, LayerConfig, LayerWeights, MoEWeights,
+from ._lib import (DrafterInfo, Handle, HCWeights, HeadConfig, HeadWeights, LayerConfig, LayerWeights, MoEWeights,
                    MtpxError, Q4, check)
 
-__all__ = ["Context", "KVCache", "DecoderLayer", "MTPHead", "MoEWeights", "LayerConfig", "HeadConfig", "MtpxError",
+__all__ = ["Context", "KVCache", "DecoderLayer", "MTPHead", "Drafter", "MoEWeights", "LayerConfig", "HeadConfig", "MtpxError",
            "moe_weights_from"]
 
 
@@ -244,6 +244,59 @@ class MTPHead:
         """One draft step over S = len(ids) inputs; advances the head cache by S."""
         check(self.ctx.lib.mtpx_head_forward(self.ctx.h, self.h, kv.h, _ptr(ids), ids.shape[0], _ptr(multi),
                                              _ptr(multi_next), _ptr(sample), _ptr(draft)), "head_forward")
+
+
+class Drafter:
+    """Per-request MTP drafter state (mtpx_drafter): the head's own KV cache plus the
+    trusted target transitions not yet in it; the CBv2 request-stateful drafter
+    protocol (observe / step / finalize / discard / release)."""
+
+    MAX_DEPTH = 6
+
+    def __init__(self, ctx: Context, head: MTPHead):
+        self.ctx = ctx
+        self.head = head
+        self.h = Handle()
+        check(ctx.lib.mtpx_drafter_new(ctx.h, head.h, C.byref(self.h)), "drafter_new")
+
+    def close(self):
+        if self.h.ctx:
+            self.ctx.lib.mtpx_drafter_free(self.h)
+            self.h.ctx = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def observe(self, tokens, multi):
+        check(self.ctx.lib.mtpx_drafter_observe(self.h, _ptr(tokens), _ptr(multi), tokens.shape[0]), "drafter_observe")
+
+    def step(self, token, multi, draft, multi_out):
+        check(self.ctx.lib.mtpx_drafter_step(self.h, _ptr(token), _ptr(multi), _ptr(draft), _ptr(multi_out)),
+              "drafter_step")
+
+    def finalize(self, confirmed_inputs: int, tokens=None, multi=None):
+        n = 0 if tokens is None else tokens.shape[0]
+        check(self.ctx.lib.mtpx_drafter_finalize(self.h, confirmed_inputs, _ptr(tokens), _ptr(multi), n),
+              "drafter_finalize")
+
+    def discard(self):
+        check(self.ctx.lib.mtpx_drafter_discard(self.h), "drafter_discard")
+
+    def release(self):
+        check(self.ctx.lib.mtpx_drafter_release(self.h), "drafter_release")
+
+    def info(self) -> dict:
+        i = DrafterInfo()
+        check(self.ctx.lib.mtpx_drafter_info_get(self.h, C.byref(i)), "drafter_info")
+        return {n: getattr(i, n) for n, _ in DrafterInfo._fields_}
+
+    def bytes_per_token(self) -> int:
+        v = C.c_int64()
+        check(self.ctx.lib.mtpx_drafter_bytes_per_token(self.head.h, C.byref(v)), "drafter_bytes_per_token")
+        return v.value
 
 
 def moe_weights_from(tensors: dict, H, E, K, F, gs) -> MoEWeights:

@@ -62,6 +62,12 @@ class HeadWeights(C.Structure):
                 ("layer", LayerWeights), ("shortlist", Q4), ("shortlist_ids", P), ("shortlist_rows", INT)]
 
 
+class DrafterInfo(C.Structure):
+    _fields_ = [(n, I64) for n in ("cache_offset", "committed_inputs", "staged_inputs", "backlog_inputs",
+                                   "round_base_offset", "round_valid_offset")] + [
+        (n, INT) for n in ("round_in_flight", "round_draft_steps", "has_frontier", "released")]
+
+
 _SIGS = {
     "mtpx_last_error": (C.c_char_p, []),
     "mtpx_version": (C.c_char_p, []),
@@ -96,6 +102,15 @@ _SIGS = {
     "mtpx_head_free": (INT, [Handle]),
     "mtpx_head_weights_get": (INT, [Handle, C.POINTER(HeadWeights)]),
     "mtpx_head_forward": (INT, [Handle, Handle, Handle, P, INT, P, P, P, P]),
+    "mtpx_drafter_new": (INT, [Handle, Handle, C.POINTER(Handle)]),
+    "mtpx_drafter_free": (INT, [Handle]),
+    "mtpx_drafter_observe": (INT, [Handle, P, P, INT]),
+    "mtpx_drafter_step": (INT, [Handle, P, P, P, P]),
+    "mtpx_drafter_finalize": (INT, [Handle, INT, P, P, INT]),
+    "mtpx_drafter_discard": (INT, [Handle]),
+    "mtpx_drafter_release": (INT, [Handle]),
+    "mtpx_drafter_info_get": (INT, [Handle, C.POINTER(DrafterInfo)]),
+    "mtpx_drafter_bytes_per_token": (INT, [Handle, C.POINTER(I64)]),
     "mtpx_profile_enable": (INT, [Handle, INT]),
     "mtpx_profile_reset": (INT, [Handle]),
     "mtpx_profile_dump": (INT, [Handle, C.c_char_p, C.c_size_t]),

@@ -46,6 +46,7 @@ def test_struct_layouts_match_c_compiler(tmp_path):
         "mtpx_q4": (_lib.Q4, ["s", "b"]),
         "mtpx_hc_weights": (_lib.HCWeights, ["down", "inject", "up"]),
         "mtpx_head_config": (_lib.HeadConfig, ["hc", "lowrank", "vocab", "shortlist_low", "shortlist_special_from"]),
+        "mtpx_drafter_info": (_lib.DrafterInfo, ["round_base_offset", "round_in_flight", "released"]),
         "mtpx_head_weights": (_lib.HeadWeights, ["pre_norm_hidden", "attn_hc", "final_hc", "layer", "shortlist",
                                                  "shortlist_ids", "shortlist_rows"]),
     }

@@ -42,7 +42,19 @@ def qbytes(N: int, K: int, gs: int) -> int:
     return N * K // 2 + 4 * N * K // gs
 
 
-def cpu_baseline(layer, ctx, kv, cfg, M, seconds=12.0, max_steps=6):
+def traffic_record(gs: int, M: int, T0: int):
+    """HBM bytes per launch of the gate|up kernel for this workload, as measured by the
+    rocprofv3 FETCH_SIZE / WRITE_SIZE passes summarised in profiles/ (None when absent)."""
+    path = os.path.join(ROOT, "profiles", "moe_gate_up_traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        rec = json.load(f)
+    key = f"gs{gs}_M{M}_T{T0}"
+    return rec.get(key)
+
+
+def cpu_baseline(layer, ctx, kv, cfg, M, seconds=15.0, max_steps=40):
     """Time the oracle's composition of the same layer step on the host (1 thread)."""
     import numpy as np
 
@@ -80,6 +92,8 @@ def main() -> int:
     ap.add_argument("--cached", type=int, default=1024)
     ap.add_argument("--group-size", type=int, default=64)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="after the timed steps, copy 256 MiB once (the reference kernel for HBM byte counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
@@ -179,6 +193,16 @@ def main() -> int:
         "step_GBps": round(step_bytes / (ms_per_step / 1e3) / 1e9, 1),
         "kernels": kernels,
     }
+    tr = traffic_record(gs, M, T0)
+    if tr is not None:
+        out["roofline"]["traffic"] = tr["gate_up_bytes_per_launch"]
+        out["roofline"]["traffic_source"] = tr["source"]
+    if args.copy_calibration:
+        a = torch.empty(128 << 20, dtype=torch.int16, device="cuda").fill_(1)
+        b = torch.empty_like(a)
+        torch.cuda.synchronize()
+        b.copy_(a)
+        torch.cuda.synchronize()
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(layer, ctx, kv, cfg, M)
     print(json.dumps(out))

@@ -225,6 +225,14 @@ __global__ __launch_bounds__(RR_THREADS) void k_moe_router_route(MoeArgs a, int 
   route_body(a);
 }
 
+// Dispatch entry of grid row y: row 0 is the shared expert (every token, the
+// most work per workgroup, so it is dispatched first), rows 1..nu the routed
+// experts in dispatch order; -1 for the rows beyond.
+__device__ __forceinline__ int expert_slot(int y, int nu) {
+  if (y == 0) return nu;
+  return y - 1 < nu ? y - 1 : -1;
+}
+
 __device__ __forceinline__ int slot_token(int slot, int M, int K) {
   return slot < M * K ? slot / K : slot - M * K;
 }
@@ -245,9 +253,9 @@ __global__ __launch_bounds__(GU_THREADS) void k_moe_gate_up(MoeArgs a) {
   constexpr int NI = (32 + WAVES * RW - 1) / (WAVES * RW);     // passes for 32 rows
   const int H = a.H, F = a.F, M = a.M, K = a.K, gs = a.gs;
   const int nb = H / 32, ng = H / gs;
-  const int u = blockIdx.y;
   const int nu = a.disp->n_unique;
-  if (u > nu) return;
+  const int u = expert_slot(blockIdx.y, nu);
+  if (u < 0) return;
   const bool shared = (u == nu);
   const int e = a.disp->expert[u];
   const int cnt = a.disp->count[u];
@@ -343,9 +351,9 @@ __global__ __launch_bounds__(256) void k_moe_down(MoeArgs a) {
   constexpr int NI = (DOWN_ROWS + 8 * RW - 1) / (8 * RW);  // passes of 2*RW rows per wave
   const int H = a.H, F = a.F, K = a.K, gs = a.gs;
   const int nb = F / 32, ng = F / gs;
-  const int u = blockIdx.y;
   const int nu = a.disp->n_unique;
-  if (u > nu) return;
+  const int u = expert_slot(blockIdx.y, nu);
+  if (u < 0) return;
   const bool shared = (u == nu);
   const int e = a.disp->expert[u];
   const int cnt = a.disp->count[u];

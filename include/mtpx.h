@@ -68,14 +68,30 @@ int mtpx_affine_quantize(mtpx_ctx ctx, const uint16_t* w, int64_t rows, int K, i
 int mtpx_randn_bf16(mtpx_ctx ctx, uint16_t* out, int64_t n, uint64_t seed, uint32_t tensor,
                     float sigma);
 
+/* ---- packed scale/bias rows ---------------------------------------------------
+ * Every q4 matrix may carry, next to its checkpoint-format bf16 scales and
+ * biases [rows, K/gs], a packed copy: each (scale, bias) pair as one u32 (scale
+ * in the low half) in the GEMV's lane order, mtpx_q4_sb_row_len(K, gs) u32 per
+ * row.  The GEMVs then fetch a lane's pairs with one or two vector loads instead
+ * of two 2-byte loads per 32-element block; values and results are identical.
+ * This is a load-time layout of the MI355X build (no reference counterpart:
+ * the reference reads scales and biases separately,
+ * MLX/backend/metal/kernels/quantized.h:12-393). */
+/* u32 entries per packed row; -1 for an unsupported (K, group_size). */
+int mtpx_q4_sb_row_len(int K, int group_size);
+/* out u32 [rows, mtpx_q4_sb_row_len(K, gs)] from scales and biases [rows, K/gs]. */
+int mtpx_q4_pack_sb(mtpx_ctx ctx, const uint16_t* scales, const uint16_t* biases, int64_t rows,
+                    int K, int gs, uint32_t* out);
+
 /* ---- a2-a4, a12: q4 GEMV / small-M GEMM ------------------------------------
  * y[M, N] = x[M, K] . W[N, K]^T, M <= 8, bf16 out (yf: optional f32 before
- * rounding).  Replaces MLX quantizedMM's qmv_fast / qmv / qmv_wide
- * (MLX/backend/metal/kernels/quantized.h:758,825,989) and the track's
- * TrackQuantWeight.apply / TrackLUTGemv (Runner/FastModel/TrackFastWeights.swift:40-49,
- * Runner/FastModel/TrackAffineLUT.swift:121-368). */
+ * rounding); sb: packed scale/bias rows or NULL.  Replaces MLX quantizedMM's
+ * qmv_fast / qmv / qmv_wide (MLX/backend/metal/kernels/quantized.h:758,825,989)
+ * and the track's TrackQuantWeight.apply / TrackLUTGemv
+ * (Runner/FastModel/TrackFastWeights.swift:40-49, Runner/FastModel/TrackAffineLUT.swift:121-368). */
 int mtpx_qmv(mtpx_ctx ctx, const uint32_t* wq, const uint16_t* scales, const uint16_t* biases,
-             int N, int K, int gs, const uint16_t* x, int M, uint16_t* y, float* yf);
+             const uint32_t* sb, int N, int K, int gs, const uint16_t* x, int M, uint16_t* y,
+             float* yf);
 
 /* ---- a5-a11: the MoE block -------------------------------------------------- */
 typedef struct {
@@ -92,6 +108,9 @@ typedef struct {
   const uint32_t* sh_gate_w; const uint16_t* sh_gate_s; const uint16_t* sh_gate_b; /* [F,H/8] */
   const uint32_t* sh_up_w;   const uint16_t* sh_up_s;   const uint16_t* sh_up_b;
   const uint32_t* sh_down_w; const uint16_t* sh_down_s; const uint16_t* sh_down_b; /* [H,F/8] */
+  /* packed scale/bias rows of the six matrices above (all six, or all NULL) */
+  const uint32_t* gate_sb; const uint32_t* up_sb; const uint32_t* down_sb;
+  const uint32_t* sh_gate_sb; const uint32_t* sh_up_sb; const uint32_t* sh_down_sb;
 } mtpx_moe_weights;
 
 /* y[M, H] = MoE(x[M, H]) for a decode/verify window of M <= 8 tokens: router
@@ -185,6 +204,7 @@ typedef struct {
   const uint16_t* rope_cos; const uint16_t* rope_sin; /* bf16 [max_positions, rot] */
   mtpx_moe_weights moe;
   int qkv_rows;
+  const uint32_t* qkv_sb; const uint32_t* o_sb; /* packed scale/bias rows (or NULL) */
 } mtpx_layer_weights;
 
 int mtpx_layer_new_random(mtpx_ctx ctx, const mtpx_layer_config* cfg, uint64_t seed,
@@ -200,8 +220,8 @@ int mtpx_layer_forward(mtpx_ctx ctx, mtpx_layer layer, mtpx_kv kv, const uint16_
  * [rows, H]), argmax over the bf16 logits (lowest position on ties), mapped
  * through ids (ascending) -> out[0].  x is one bf16 row [H] on the device. */
 int mtpx_shortlist_argmax(mtpx_ctx ctx, const uint16_t* x, int H, const uint32_t* w,
-                          const uint16_t* s, const uint16_t* b, int group_size, int rows,
-                          const int32_t* ids, int32_t* out);
+                          const uint16_t* s, const uint16_t* b, const uint32_t* sb,
+                          int group_size, int rows, const int32_t* ids, int32_t* out);
 
 /* ---- a17: the MTP head (one draft step) ------------------------------------------
  * TrackQwen4ExpMTPModule.callAsFunction (Runner/Qwen4ExpMTP.swift:101-130) over
@@ -216,6 +236,7 @@ int mtpx_shortlist_argmax(mtpx_ctx ctx, const uint16_t* x, int H, const uint32_t
  *   x = sum over streams of sigmoid(w) * n, j = 2 * sigmoid(inj). */
 typedef struct {
   const uint32_t* w; const uint16_t* s; const uint16_t* b; /* q4 matrix; w == NULL: absent */
+  const uint32_t* sb;                                      /* packed scale/bias rows or NULL */
 } mtpx_q4;
 
 /* One hyper-connection mixer (TrackHC, Runner/FastModel/TrackFastModel.swift:182-195,

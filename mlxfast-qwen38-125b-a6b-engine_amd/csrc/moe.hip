@@ -265,6 +265,9 @@ __global__ __launch_bounds__(GU_THREADS) void k_moe_gate_up(MoeArgs a) {
   const uint32_t* uw = shared ? a.sh_up_w : a.up_w + (size_t)e * F * (H / 8);
   const bf16* usc = shared ? a.sh_up_s : a.up_s + (size_t)e * F * ng;
   const bf16* ubi = shared ? a.sh_up_b : a.up_b + (size_t)e * F * ng;
+  const int P = sb_row_len(H, gs);
+  const uint32_t* gsb = a.gate_sb ? (shared ? a.sh_gate_sb : a.gate_sb + (size_t)e * F * P) : nullptr;
+  const uint32_t* usb = a.gate_sb ? (shared ? a.sh_up_sb : a.up_sb + (size_t)e * F * P) : nullptr;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int sub = lane % L, grp = lane / L;
   const int f0 = blockIdx.x * 32;
@@ -274,8 +277,10 @@ __global__ __launch_bounds__(GU_THREADS) void k_moe_gate_up(MoeArgs a) {
     const int fi = (wave + p * WAVES) * RW + grp;
     const bool valid = fi < 32;
     const int f = f0 + (valid ? fi : 0);
-    G[p].load(gw + (size_t)f * (H / 8), gsc + (size_t)f * ng, gbi + (size_t)f * ng, nb, gs, sub, valid);
-    U[p].load(uw + (size_t)f * (H / 8), usc + (size_t)f * ng, ubi + (size_t)f * ng, nb, gs, sub, valid);
+    G[p].load(gw + (size_t)f * (H / 8), gsc + (size_t)f * ng, gbi + (size_t)f * ng, gsb ? gsb + (size_t)f * P : nullptr,
+              nb, gs, sub, valid);
+    U[p].load(uw + (size_t)f * (H / 8), usc + (size_t)f * ng, ubi + (size_t)f * ng, usb ? usb + (size_t)f * P : nullptr,
+              nb, gs, sub, valid);
   }
   for (int tk = 0; tk < cnt; ++tk) {
     const int m = slot_token(a.disp->slot[u][tk], M, K);
@@ -360,6 +365,8 @@ __global__ __launch_bounds__(256) void k_moe_down(MoeArgs a) {
   const uint32_t* dw = shared ? a.sh_down_w : a.down_w + (size_t)e * H * (F / 8);
   const bf16* dsc = shared ? a.sh_down_s : a.down_s + (size_t)e * H * ng;
   const bf16* dbi = shared ? a.sh_down_b : a.down_b + (size_t)e * H * ng;
+  const int P = sb_row_len(F, gs);
+  const uint32_t* dsb = a.down_sb ? (shared ? a.sh_down_sb : a.down_sb + (size_t)e * H * P) : nullptr;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int sub = lane % L, grp = lane / L;
   const int h0 = blockIdx.x * DOWN_ROWS;
@@ -369,8 +376,10 @@ __global__ __launch_bounds__(256) void k_moe_down(MoeArgs a) {
     const int hi = (wave + 4 * p) * 2 * RW + 2 * grp;
     const bool va = hi < DOWN_ROWS && h0 + hi < H, vb = hi + 1 < DOWN_ROWS && h0 + hi + 1 < H;
     const int ha = va ? h0 + hi : h0, hb = vb ? h0 + hi + 1 : h0;
-    A[p].load(dw + (size_t)ha * (F / 8), dsc + (size_t)ha * ng, dbi + (size_t)ha * ng, nb, gs, sub, va);
-    B[p].load(dw + (size_t)hb * (F / 8), dsc + (size_t)hb * ng, dbi + (size_t)hb * ng, nb, gs, sub, vb);
+    A[p].load(dw + (size_t)ha * (F / 8), dsc + (size_t)ha * ng, dbi + (size_t)ha * ng,
+              dsb ? dsb + (size_t)ha * P : nullptr, nb, gs, sub, va);
+    B[p].load(dw + (size_t)hb * (F / 8), dsc + (size_t)hb * ng, dbi + (size_t)hb * ng,
+              dsb ? dsb + (size_t)hb * P : nullptr, nb, gs, sub, vb);
   }
   for (int tk = 0; tk < cnt; ++tk)
     stage16(lds + (size_t)tk * nb * XP_DW, a.xp_act + (size_t)a.disp->slot[u][tk] * nb * XP_DW, nb * XP_DW);

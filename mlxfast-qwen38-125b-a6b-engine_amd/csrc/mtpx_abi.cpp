@@ -186,6 +186,8 @@ int moe_check(const mtpx_moe_weights* w, int M) {
   ARG(w->router && w->shared_gate && w->gate_w && w->up_w && w->down_w && w->sh_gate_w && w->sh_up_w &&
           w->sh_down_w,
       "missing MoE weight pointer");
+  const int nsb = !!w->gate_sb + !!w->up_sb + !!w->down_sb + !!w->sh_gate_sb + !!w->sh_up_sb + !!w->sh_down_sb;
+  ARG(nsb == 0 || nsb == 6, "packed scale/bias rows: give all six matrices or none");
   return MTPX_OK;
 }
 
@@ -216,6 +218,8 @@ int moe_enqueue(Ctx* c, const mtpx_moe_weights* w, const uint16_t* x, int M, uin
   a.sh_gate_w = w->sh_gate_w; a.sh_gate_s = w->sh_gate_s; a.sh_gate_b = w->sh_gate_b;
   a.sh_up_w = w->sh_up_w; a.sh_up_s = w->sh_up_s; a.sh_up_b = w->sh_up_b;
   a.sh_down_w = w->sh_down_w; a.sh_down_s = w->sh_down_s; a.sh_down_b = w->sh_down_b;
+  a.gate_sb = w->gate_sb; a.up_sb = w->up_sb; a.down_sb = w->down_sb;
+  a.sh_gate_sb = w->sh_gate_sb; a.sh_up_sb = w->sh_up_sb; a.sh_down_sb = w->sh_down_sb;
   a.x = x;
   a.y = y;
   const int slots = M * (a.K + 1);
@@ -288,7 +292,14 @@ struct RandInit {
     }
     ++tensor;
   }
-  void qmat(int64_t rows, int K, mtpx_q4* q) { qmat(rows, K, &q->w, &q->s, &q->b); }
+  // the same, plus the packed scale/bias rows
+  void qmat(int64_t rows, int K, const uint32_t** w, const uint16_t** s, const uint16_t** b, const uint32_t** sb) {
+    qmat(rows, K, w, s, b);
+    uint32_t* p = (uint32_t*)alloc((size_t)rows * sb_row_len(K, gs) * 4);
+    *sb = p;
+    if (p && *s && *b && launch_pack_sb(*s, *b, rows, K, gs, p, c->stream)) ok = false;
+  }
+  void qmat(int64_t rows, int K, mtpx_q4* q) { qmat(rows, K, &q->w, &q->s, &q->b, &q->sb); }
   // sigma > 0: N(0, sigma); sigma == 0: filled with the bf16 pattern `ones`
   const uint16_t* dense(int64_t n, float sigma, uint16_t ones = 0x3f80) {
     uint16_t* p = (uint16_t*)alloc((size_t)n * 2);
@@ -344,8 +355,8 @@ int layer_create(Ctx* c, const mtpx_layer_config* cfg, uint64_t seed, Layer** ou
   L->w.post_norm = ri.dense(H, 0.0f);
   L->w.q_norm = ri.dense(D, 0.0f);
   L->w.k_norm = ri.dense(D, 0.0f);
-  ri.qmat(QW, H, &L->w.qkv_w, &L->w.qkv_s, &L->w.qkv_b);
-  ri.qmat(H, HQ * D, &L->w.o_w, &L->w.o_s, &L->w.o_b);
+  ri.qmat(QW, H, &L->w.qkv_w, &L->w.qkv_s, &L->w.qkv_b, &L->w.qkv_sb);
+  ri.qmat(H, HQ * D, &L->w.o_w, &L->w.o_s, &L->w.o_b, &L->w.o_sb);
   mtpx_moe_weights& m = L->w.moe;
   m.hidden = H;
   m.experts = E;
@@ -354,12 +365,12 @@ int layer_create(Ctx* c, const mtpx_layer_config* cfg, uint64_t seed, Layer** ou
   m.group_size = gs;
   m.router = ri.dense((int64_t)E * H, 0.02f);
   m.shared_gate = ri.dense(H, 0.02f);
-  ri.qmat((int64_t)E * F, H, &m.gate_w, &m.gate_s, &m.gate_b);
-  ri.qmat((int64_t)E * F, H, &m.up_w, &m.up_s, &m.up_b);
-  ri.qmat((int64_t)E * H, F, &m.down_w, &m.down_s, &m.down_b);
-  ri.qmat(F, H, &m.sh_gate_w, &m.sh_gate_s, &m.sh_gate_b);
-  ri.qmat(F, H, &m.sh_up_w, &m.sh_up_s, &m.sh_up_b);
-  ri.qmat(H, F, &m.sh_down_w, &m.sh_down_s, &m.sh_down_b);
+  ri.qmat((int64_t)E * F, H, &m.gate_w, &m.gate_s, &m.gate_b, &m.gate_sb);
+  ri.qmat((int64_t)E * F, H, &m.up_w, &m.up_s, &m.up_b, &m.up_sb);
+  ri.qmat((int64_t)E * H, F, &m.down_w, &m.down_s, &m.down_b, &m.down_sb);
+  ri.qmat(F, H, &m.sh_gate_w, &m.sh_gate_s, &m.sh_gate_b, &m.sh_gate_sb);
+  ri.qmat(F, H, &m.sh_up_w, &m.sh_up_s, &m.sh_up_b, &m.sh_up_sb);
+  ri.qmat(H, F, &m.sh_down_w, &m.sh_down_s, &m.sh_down_b, &m.sh_down_sb);
   // rotate-half RoPE tables: entry d uses theta^(-2*(d mod rot/2)/rot)
   const int rot = cfg->rot_dims;
   std::vector<uint16_t> ct((size_t)cfg->max_positions * rot), st((size_t)cfg->max_positions * rot);
@@ -401,14 +412,14 @@ int attn_enqueue(Ctx* c, const Layer* L, Kv* kv, uint32_t* xp, int M, uint16_t* 
   uint16_t* att = ws_take<uint16_t>(c, (size_t)M * HQ * D);
   float* part = ws_take<float>(c, attn_partial_floats(M, HQ, D, T));
   hipStream_t st = c->stream;
-  LAUNCH(c, "qmv_qkv", launch_qmv(L->w.qkv_w, L->w.qkv_s, L->w.qkv_b, QW, H, gs, xp, M, qkv, nullptr, st));
+  LAUNCH(c, "qmv_qkv", launch_qmv(L->w.qkv_w, L->w.qkv_s, L->w.qkv_b, L->w.qkv_sb, QW, H, gs, xp, M, qkv, nullptr, st));
   LAUNCH(c, "attn_prep", launch_attn_prep(qkv, M, QW, HQ, HK, D, g.rot_dims, L->w.q_norm, L->w.k_norm, g.eps,
                                           L->w.rope_cos, L->w.rope_sin, (int)kv->offset, q, kv->k, kv->v,
                                           kv->tmax, st));
   LAUNCH(c, "attn_verify", launch_attn_verify(q, M, HQ, HK, D, kv->k, kv->v, kv->tmax, T,
                                               1.0f / std::sqrt((float)D), part, qkv, QW, HQ * D, nullptr, att,
                                               xp, st));
-  LAUNCH(c, "qmv_o", launch_qmv(L->w.o_w, L->w.o_s, L->w.o_b, H, HQ * D, gs, xp, M, o, nullptr, st));
+  LAUNCH(c, "qmv_o", launch_qmv(L->w.o_w, L->w.o_s, L->w.o_b, L->w.o_sb, H, HQ * D, gs, xp, M, o, nullptr, st));
   return MTPX_OK;
 }
 
@@ -480,11 +491,11 @@ int hc_mix_enqueue(Ctx* c, const Head* hd, const mtpx_hc_weights* hw, const uint
   uint16_t* inj = ws_take<uint16_t>(c, (size_t)S * g.hc);
   uint32_t* xpL = ws_take<uint32_t>(c, (size_t)S * (LW / 32) * XP_DW);
   uint16_t* wm = ws_take<uint16_t>(c, (size_t)S * W);
-  LAUNCH(c, "hc_down", launch_qmv(hw->down.w, hw->down.s, hw->down.b, LW, W, gs, xpW, S, lo, nullptr, st));
+  LAUNCH(c, "hc_down", launch_qmv(hw->down.w, hw->down.s, hw->down.b, hw->down.sb, LW, W, gs, xpW, S, lo, nullptr, st));
   if (hw->inject.w)
-    LAUNCH(c, "hc_inject", launch_qmv(hw->inject.w, hw->inject.s, hw->inject.b, g.hc, W, gs, xpW, S, inj, nullptr, st));
+    LAUNCH(c, "hc_inject", launch_qmv(hw->inject.w, hw->inject.s, hw->inject.b, hw->inject.sb, g.hc, W, gs, xpW, S, inj, nullptr, st));
   LAUNCH(c, "hc_silu", launch_silu_xprep(lo, S, LW, act, xpL, st));
-  LAUNCH(c, "hc_up", launch_qmv(hw->up.w, hw->up.s, hw->up.b, W, LW, gs, xpL, S, wm, nullptr, st));
+  LAUNCH(c, "hc_up", launch_qmv(hw->up.w, hw->up.s, hw->up.b, hw->up.sb, W, LW, gs, xpL, S, wm, nullptr, st));
   LAUNCH(c, "hc_mix", launch_hc_mix(wm, normed, hw->inject.w ? inj : nullptr, S, g.hc, H, x, j, xpH, st));
   return MTPX_OK;
 }
@@ -758,7 +769,24 @@ int mtpx_randn_bf16(mtpx_ctx h, uint16_t* out, int64_t n, uint64_t seed, uint32_
   return MTPX_OK;
 }
 
-int mtpx_qmv(mtpx_ctx h, const uint32_t* wq, const uint16_t* s, const uint16_t* b, int N, int K, int gs,
+int mtpx_q4_sb_row_len(int K, int gs) {
+  if (!gs_ok(gs) || !k_ok(K, gs)) {
+    fail(MTPX_ERR_ARG, "K=%d gs=%d unsupported", K, gs);
+    return -1;
+  }
+  return sb_row_len(K, gs);
+}
+
+int mtpx_q4_pack_sb(mtpx_ctx h, const uint16_t* s, const uint16_t* b, int64_t rows, int K, int gs, uint32_t* out) {
+  Ctx* c = C(h);
+  ARG(c && s && b && out && rows >= 0, "bad argument");
+  ARG(gs_ok(gs) && k_ok(K, gs), "K=%d gs=%d", K, gs);
+  if (set_device(c)) return MTPX_ERR_HIP;
+  LAUNCH(c, "pack_sb", launch_pack_sb(s, b, rows, K, gs, out, c->stream));
+  return MTPX_OK;
+}
+
+int mtpx_qmv(mtpx_ctx h, const uint32_t* wq, const uint16_t* s, const uint16_t* b, const uint32_t* sb, int N, int K, int gs,
              const uint16_t* x, int M, uint16_t* y, float* yf) {
   Ctx* c = C(h);
   ARG(c && wq && s && b && x && y, "null argument");
@@ -771,7 +799,7 @@ int mtpx_qmv(mtpx_ctx h, const uint32_t* wq, const uint16_t* s, const uint16_t* 
   c->ws_used = 0;
   uint32_t* xp = ws_take<uint32_t>(c, xpn);
   LAUNCH(c, "xprep", launch_xprep(x, M, K, xp, c->stream));
-  LAUNCH(c, "qmv", launch_qmv(wq, s, b, N, K, gs, xp, M, y, yf, c->stream));
+  LAUNCH(c, "qmv", launch_qmv(wq, s, b, sb, N, K, gs, xp, M, y, yf, c->stream));
   return MTPX_OK;
 }
 
@@ -1063,7 +1091,7 @@ int mtpx_last_moe_bytes(mtpx_ctx h, int64_t* bytes, int32_t* n_unique) {
 }
 
 int mtpx_shortlist_argmax(mtpx_ctx h, const uint16_t* x, int H, const uint32_t* w, const uint16_t* s,
-                          const uint16_t* b, int gs, int rows, const int32_t* ids, int32_t* out) {
+                          const uint16_t* b, const uint32_t* sb, int gs, int rows, const int32_t* ids, int32_t* out) {
   Ctx* c = C(h);
   ARG(c && x && w && s && b && out, "null argument");
   ARG(gs_ok(gs) && k_ok(H, gs), "H=%d gs=%d", H, gs);
@@ -1079,7 +1107,7 @@ int mtpx_shortlist_argmax(mtpx_ctx h, const uint16_t* x, int H, const uint32_t* 
   int32_t* pi = ws_take<int32_t>(c, n);
   hipStream_t st = c->stream;
   LAUNCH(c, "xprep", launch_xprep(x, 1, H, xp, st));
-  LAUNCH(c, "qmv_shortlist", launch_qmv(w, s, b, rows, H, gs, xp, 1, y, nullptr, st));
+  LAUNCH(c, "qmv_shortlist", launch_qmv(w, s, b, sb, rows, H, gs, xp, 1, y, nullptr, st));
   LAUNCH(c, "shortlist_argmax", launch_argmax_rows_bf16(y, 1, rows, pv, pi, ids, out, st));
   return MTPX_OK;
 }
@@ -1154,11 +1182,11 @@ int mtpx_head_forward(mtpx_ctx h, mtpx_head hh, mtpx_kv kvh, const int32_t* ids,
   LAUNCH(c, "embed", launch_embed_rows(w.embed.w, w.embed.s, w.embed.b, H, gs, g.vocab, ids, S, e, st));
   LAUNCH(c, "hc_norm", launch_hc_norm(e, nullptr, nullptr, S, 1, H, 0, w.pre_norm_embedding, eps, nullptr, en, xpH,
                                       st));
-  LAUNCH(c, "qmv_fc", launch_qmv(w.fc_embedding.w, w.fc_embedding.s, w.fc_embedding.b, H, H, gs, xpH, S, emb,
+  LAUNCH(c, "qmv_fc", launch_qmv(w.fc_embedding.w, w.fc_embedding.s, w.fc_embedding.b, w.fc_embedding.sb, H, H, gs, xpH, S, emb,
                                  nullptr, st));
   LAUNCH(c, "hc_norm", launch_hc_norm(multi, nullptr, nullptr, S, 1, W, 0, w.pre_norm_hidden, eps, nullptr, mn, xpW,
                                       st));
-  LAUNCH(c, "qmv_fc", launch_qmv(w.fc_hidden.w, w.fc_hidden.s, w.fc_hidden.b, H, H, gs, xpW, S * hc, hs, nullptr,
+  LAUNCH(c, "qmv_fc", launch_qmv(w.fc_hidden.w, w.fc_hidden.s, w.fc_hidden.b, w.fc_hidden.sb, H, H, gs, xpW, S * hc, hs, nullptr,
                                  st));
   // attention block: hyper = e + h; (st0, n) = hc_norm(hyper); (x, j) = mix(attn_hc, n); ao = attn(x)
   LAUNCH(c, "hc_norm", launch_hc_norm(hs, emb, nullptr, S, hc, H, 0, w.attn_hc.norm_scale, eps, st0, nrm, xpW, st));
@@ -1178,7 +1206,7 @@ int mtpx_head_forward(mtpx_ctx h, mtpx_head hh, mtpx_kv kvh, const int32_t* ids,
     uint16_t* yl = ws_take<uint16_t>(c, (size_t)NS);
     float* pv = ws_take<float>(c, n);
     int32_t* pi = ws_take<int32_t>(c, n);
-    LAUNCH(c, "qmv_shortlist", launch_qmv(w.shortlist.w, w.shortlist.s, w.shortlist.b, NS, H, gs,
+    LAUNCH(c, "qmv_shortlist", launch_qmv(w.shortlist.w, w.shortlist.s, w.shortlist.b, w.shortlist.sb, NS, H, gs,
                                           xpH + (size_t)(S - 1) * (H / 32) * XP_DW, 1, yl, nullptr, st));
     LAUNCH(c, "shortlist_argmax", launch_argmax_rows_bf16(yl, 1, NS, pv, pi, w.shortlist_ids, draft, st));
   }

@@ -68,6 +68,16 @@ __host__ __device__ constexpr int lanes_for_blocks(int nb) {
   return L;
 }
 
+// Packed scale/bias row of a [*, K] q4 matrix (see qrows.h): lane classes Q x
+// entries per class, in u32.
+__host__ __device__ constexpr int sb_entries_per_class(int K) {
+  return (K / 32 + lanes_for_blocks(K / 32) - 1) / lanes_for_blocks(K / 32);
+}
+__host__ __device__ constexpr int sb_classes(int K, int gs) {
+  return lanes_for_blocks(K / 32) / (gs / 32) > 0 ? lanes_for_blocks(K / 32) / (gs / 32) : 1;
+}
+__host__ __device__ constexpr int sb_row_len(int K, int gs) { return sb_classes(K, gs) * sb_entries_per_class(K); }
+
 // ---------------------------------------------------------------------------
 // Prepared activation block: 28 dwords (16-byte aligned for 128-bit LDS reads).
 //   [0..7]   limb 0 (bits 0-7 of m):   dwords e0 e1 e2 e3 o0 o1 o2 o3

@@ -25,8 +25,10 @@ inline hipError_t ensure_lds(Kern* kernel, size_t bytes, size_t& cur) {
 
 // --- dense q4 GEMV and friends (qmv.hip)
 hipError_t launch_xprep(const bf16* x, int M, int K, uint32_t* xp, hipStream_t st);
-hipError_t launch_qmv(const uint32_t* wq, const bf16* s, const bf16* b, int N, int K, int gs,
+// sb: packed scale/bias rows (sb_row_len(K, gs) u32 per row) or null
+hipError_t launch_qmv(const uint32_t* wq, const bf16* s, const bf16* b, const uint32_t* sb, int N, int K, int gs,
                       const uint32_t* xp, int M, bf16* y, float* yf, hipStream_t st);
+hipError_t launch_pack_sb(const bf16* s, const bf16* b, int64_t N, int K, int gs, uint32_t* out, hipStream_t st);
 hipError_t launch_quantize(const bf16* w, int64_t rows, int K, int gs, uint32_t* wq, bf16* s, bf16* b,
                            hipStream_t st);
 hipError_t launch_randn_bf16(bf16* out, int64_t n, uint64_t seed, uint32_t tensor, float sigma,
@@ -50,6 +52,8 @@ struct MoeArgs {
   const bf16 *gate_s, *gate_b, *up_s, *up_b, *down_s, *down_b;
   const uint32_t *sh_gate_w, *sh_up_w, *sh_down_w;
   const bf16 *sh_gate_s, *sh_gate_b, *sh_up_s, *sh_up_b, *sh_down_s, *sh_down_b;
+  // packed scale/bias rows (all six or none)
+  const uint32_t *gate_sb, *up_sb, *down_sb, *sh_gate_sb, *sh_up_sb, *sh_down_sb;
   // activations and workspace
   const bf16* x;       // [M, H]
   bf16* y;             // [M, H]

@@ -29,13 +29,14 @@ __global__ __launch_bounds__(256) void k_xprep(const bf16* __restrict__ x, int M
 // rows are loaded before the activations are staged.
 template <int L, int IT>
 __global__ __launch_bounds__(256) void k_qmv(const uint32_t* __restrict__ wq, const bf16* __restrict__ sc,
-                                             const bf16* __restrict__ bi, int N, int K, int gs,
+                                             const bf16* __restrict__ bi, const uint32_t* __restrict__ sbp,
+                                             int N, int K, int gs,
                                              const uint32_t* __restrict__ xp, int M, bf16* __restrict__ y,
                                              float* __restrict__ yf, int rows_per_wg) {
   extern __shared__ uint32_t lds[];
   constexpr int RW = 64 / L;
   constexpr int RPW = 2 * RW;  // rows per wave pass
-  const int nb = K / 32, ng = K / gs;
+  const int nb = K / 32, ng = K / gs, P = sb_row_len(K, gs);
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int sub = lane % L, grp = lane / L;
   const int row0 = blockIdx.x * rows_per_wg;
@@ -46,8 +47,10 @@ __global__ __launch_bounds__(256) void k_qmv(const uint32_t* __restrict__ wq, co
     const int rA = b0 + grp * 2, rB = rA + 1;
     const bool vA = rA < row_end, vB = rB < row_end;
     const int ra = vA ? rA : row0, rb = vB ? rB : row0;
-    A.load(wq + (size_t)ra * (K / 8), sc + (size_t)ra * ng, bi + (size_t)ra * ng, nb, gs, sub, vA);
-    B.load(wq + (size_t)rb * (K / 8), sc + (size_t)rb * ng, bi + (size_t)rb * ng, nb, gs, sub, vB);
+    A.load(wq + (size_t)ra * (K / 8), sc + (size_t)ra * ng, bi + (size_t)ra * ng,
+           sbp ? sbp + (size_t)ra * P : nullptr, nb, gs, sub, vA);
+    B.load(wq + (size_t)rb * (K / 8), sc + (size_t)rb * ng, bi + (size_t)rb * ng,
+           sbp ? sbp + (size_t)rb * P : nullptr, nb, gs, sub, vB);
   };
   if (base < row_end) load2(base);  // first rows in flight before the staging
   stage16(lds, xp, M * nb * XP_DW);
@@ -150,8 +153,34 @@ __global__ void k_fill_bf16(bf16* __restrict__ out, int64_t n, bf16 v) {
   if (i < n) out[i] = v;
 }
 
+// Packed (scale, bias) pairs of a q4 matrix in the walker's lane order: one
+// thread per entry [row][q][it] = pair of the group of block q*r + L*it.
+__global__ void k_pack_sb(const bf16* __restrict__ s, const bf16* __restrict__ b, int64_t N, int K, int gs,
+                          uint32_t* __restrict__ out) {
+  const int P = sb_row_len(K, gs), nbv = sb_entries_per_class(K), L = lanes_for_blocks(K / 32);
+  const int r = gs / 32, nb = K / 32, ng = K / gs;
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= N * P) return;
+  const int64_t row = idx / P;
+  const int e = (int)(idx % P), q = e / nbv, it = e % nbv;
+  const int j = q * r + L * it;
+  uint32_t v = 0;
+  if (j < nb) {
+    const int g = j / r;
+    v = (uint32_t)s[row * ng + g] | ((uint32_t)b[row * ng + g] << 16);
+  }
+  out[idx] = v;
+}
+
 // ---------------------------------------------------------------------------
 // host launchers
+
+hipError_t launch_pack_sb(const bf16* s, const bf16* b, int64_t N, int K, int gs, uint32_t* out, hipStream_t st) {
+  const int64_t n = N * sb_row_len(K, gs);
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_pack_sb, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, s, b, N, K, gs, out);
+  return hipGetLastError();
+}
 
 hipError_t launch_xprep(const bf16* x, int M, int K, uint32_t* xp, hipStream_t st) {
   const int n = M * (K / 32);
@@ -161,8 +190,8 @@ hipError_t launch_xprep(const bf16* x, int M, int K, uint32_t* xp, hipStream_t s
 }
 
 template <int L, int IT>
-static hipError_t qmv_li(const uint32_t* wq, const bf16* s, const bf16* b, int N, int K, int gs, const uint32_t* xp,
-                         int M, bf16* y, float* yf, hipStream_t st) {
+static hipError_t qmv_li(const uint32_t* wq, const bf16* s, const bf16* b, const uint32_t* sb, int N, int K, int gs,
+                         const uint32_t* xp, int M, bf16* y, float* yf, hipStream_t st) {
   constexpr int rows_pass = 4 * (64 / L) * 2;
   // about two workgroups per CU, at least one pass each
   const int passes = (N + rows_pass - 1) / rows_pass;
@@ -173,24 +202,25 @@ static hipError_t qmv_li(const uint32_t* wq, const bf16* s, const bf16* b, int N
   static size_t cur = 0;
   hipError_t e = ensure_lds(k_qmv<L, IT>, lds, cur);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((k_qmv<L, IT>), dim3(grid), dim3(256), lds, st, wq, s, b, N, K, gs, xp, M, y, yf, rows_per_wg);
+  hipLaunchKernelGGL((k_qmv<L, IT>), dim3(grid), dim3(256), lds, st, wq, s, b, sb, N, K, gs, xp, M, y, yf,
+                     rows_per_wg);
   return hipGetLastError();
 }
 
-static hipError_t qmv_tokens(const uint32_t* wq, const bf16* s, const bf16* b, int N, int K, int gs,
-                             const uint32_t* xp, int M, bf16* y, float* yf, hipStream_t st) {
-  MTPX_QROW_DISPATCH(K / 32, qmv_li, wq, s, b, N, K, gs, xp, M, y, yf, st);
+static hipError_t qmv_tokens(const uint32_t* wq, const bf16* s, const bf16* b, const uint32_t* sb, int N, int K,
+                             int gs, const uint32_t* xp, int M, bf16* y, float* yf, hipStream_t st) {
+  MTPX_QROW_DISPATCH(K / 32, qmv_li, wq, s, b, sb, N, K, gs, xp, M, y, yf, st);
 }
 
-hipError_t launch_qmv(const uint32_t* wq, const bf16* s, const bf16* b, int N, int K, int gs, const uint32_t* xp,
-                      int M, bf16* y, float* yf, hipStream_t st) {
+hipError_t launch_qmv(const uint32_t* wq, const bf16* s, const bf16* b, const uint32_t* sb, int N, int K, int gs,
+                      const uint32_t* xp, int M, bf16* y, float* yf, hipStream_t st) {
   // tokens per launch: as many prepared activation vectors as fit in one workgroup's LDS
   const size_t per_token = (size_t)(K / 32) * XP_DW * 4;
   int chunk = (int)((160 * 1024) / per_token);
   chunk = chunk < 1 ? 1 : chunk;
   for (int m0 = 0; m0 < M; m0 += chunk) {
     const int mc = M - m0 < chunk ? M - m0 : chunk;
-    const hipError_t e = qmv_tokens(wq, s, b, N, K, gs, xp + (size_t)m0 * (K / 32) * XP_DW, mc, y + (size_t)m0 * N,
+    const hipError_t e = qmv_tokens(wq, s, b, sb, N, K, gs, xp + (size_t)m0 * (K / 32) * XP_DW, mc, y + (size_t)m0 * N,
                                     yf ? yf + (size_t)m0 * N : nullptr, st);
     if (e != hipSuccess) return e;
   }

@@ -5,6 +5,14 @@
 // K/32 == L*IT exactly; IT == 0 selects a predicated walker for up to QMV_IT
 // blocks).  load() issues the 16-byte weight loads and the scale/bias loads;
 // dot() consumes them against one prepared activation vector.
+//
+// Packed scale/bias rows.  Next to the checkpoint's bf16 scales [N, K/gs] and
+// biases [N, K/gs], a matrix may carry its (scale, bias) pairs as one u32 each
+// (scale in the low half), ordered so that every lane finds the pairs of its
+// blocks contiguous: entry [q][it] of a row is the pair of the group of block
+// q*r + L*it (r = gs/32, q = sub / r: lanes that share groups share entries).
+// A lane then fetches its pairs with one or two vector loads instead of two
+// 2-byte loads per block.  Same bytes, same values.
 #pragma once
 #include "mtpx_kernels.h"
 
@@ -16,8 +24,10 @@ struct QRow {
   uint32_t w[NB][4];
   uint32_t sb[NB];  // bf16 scale in the low half, bf16 bias in the high half
 
+  // sbrow: this row's packed pairs (null: the checkpoint's scale and bias rows)
   __device__ __forceinline__ void load(const uint32_t* __restrict__ wrow, const bf16* __restrict__ srow,
-                                       const bf16* __restrict__ brow, int nb, int gs, int sub, bool valid) {
+                                       const bf16* __restrict__ brow, const uint32_t* __restrict__ sbrow, int nb,
+                                       int gs, int sub, bool valid) {
 #pragma unroll
     for (int it = 0; it < NB; ++it) {
       const int j = sub + it * L;
@@ -27,11 +37,33 @@ struct QRow {
         w[it][1] = v.y;
         w[it][2] = v.z;
         w[it][3] = v.w;
-        const int g = gs == 64 ? (j >> 1) : j;  // group of block j (gs is 32 or 64)
-        sb[it] = (uint32_t)srow[g] | ((uint32_t)brow[g] << 16);
+        if (!sbrow) {
+          const int g = gs == 64 ? (j >> 1) : j;  // group of block j (gs is 32 or 64)
+          sb[it] = (uint32_t)srow[g] | ((uint32_t)brow[g] << 16);
+        }
       } else {
         w[it][0] = w[it][1] = w[it][2] = w[it][3] = 0u;
         sb[it] = 0u;
+      }
+    }
+    if (sbrow && valid) {
+      const int nbv = IT ? IT : (nb + L - 1) / L;  // entries per lane class
+      const uint32_t* e = sbrow + (size_t)(gs == 64 ? (sub >> 1) : sub) * nbv;
+      if constexpr (IT != 0) {
+#pragma unroll
+        for (int it = 0; it + 4 <= NB; it += 4) {
+          uint4 v;
+          __builtin_memcpy(&v, e + it, 16);
+          sb[it] = v.x;
+          sb[it + 1] = v.y;
+          sb[it + 2] = v.z;
+          sb[it + 3] = v.w;
+        }
+#pragma unroll
+        for (int it = NB & ~3; it < NB; ++it) sb[it] = e[it];
+      } else {
+#pragma unroll
+        for (int it = 0; it < NB; ++it) sb[it] = (sub + it * L < nb) ? e[it] : 0u;
       }
     }
   }
@@ -100,8 +132,10 @@ __device__ __forceinline__ void stage16(uint32_t* __restrict__ dst, const uint32
       case 4 * 16 + 5: return FN<4, 5>(__VA_ARGS__);                       \
       case 4 * 16 + 6: return FN<4, 6>(__VA_ARGS__);                       \
       case 8 * 16 + 4: return FN<8, 4>(__VA_ARGS__);                       \
+      case 8 * 16 + 5: return FN<8, 5>(__VA_ARGS__);                       \
       case 16 * 16 + 4: return FN<16, 4>(__VA_ARGS__);                     \
       case 16 * 16 + 5: return FN<16, 5>(__VA_ARGS__);                     \
+      case 32 * 16 + 4: return FN<32, 4>(__VA_ARGS__);                     \
       case 32 * 16 + 6: return FN<32, 6>(__VA_ARGS__);                     \
       case 64 * 16 + 5: return FN<64, 5>(__VA_ARGS__);                     \
       default: break;                                                      \

@@ -66,12 +66,27 @@ class Context:
     def randn_bf16(self, out, seed, tensor, sigma):
         check(self.lib.mtpx_randn_bf16(self.h, _ptr(out), out.numel(), seed, tensor, sigma), "randn_bf16")
 
-    def qmv(self, wq, s, b, gs, x, y, yf=None):
+    def qmv(self, wq, s, b, gs, x, y, yf=None, sb=None):
         K = x.shape[-1]
         M = x.numel() // K
         N = wq.numel() // (K // 8)
-        check(self.lib.mtpx_qmv(self.h, _ptr(wq), _ptr(s), _ptr(b), N, K, gs, _ptr(x), M, _ptr(y), _ptr(yf)),
-              "qmv")
+        check(self.lib.mtpx_qmv(self.h, _ptr(wq), _ptr(s), _ptr(b), _ptr(sb), N, K, gs, _ptr(x), M, _ptr(y),
+                                _ptr(yf)), "qmv")
+
+    def sb_row_len(self, K: int, gs: int) -> int:
+        n = self.lib.mtpx_q4_sb_row_len(K, gs)
+        if n < 0:
+            check(1, "q4_sb_row_len")
+        return n
+
+    def pack_sb(self, s, b, K: int, gs: int, out=None):
+        """Packed (scale, bias) rows of a q4 matrix (int32 tensor [rows, sb_row_len])."""
+        import torch
+        rows = s.numel() // (K // gs)
+        if out is None:
+            out = torch.empty(rows, self.sb_row_len(K, gs), dtype=torch.int32, device=s.device)
+        check(self.lib.mtpx_q4_pack_sb(self.h, _ptr(s), _ptr(b), rows, K, gs, _ptr(out)), "q4_pack_sb")
+        return out
 
     def moe_forward(self, w: MoEWeights, x, y, idx=None, wts=None, logits=None, n_unique=None):
         M = x.shape[0]
@@ -116,9 +131,9 @@ class Context:
                                           _ptr(drafts), temperature, seed, offset, kv_offset, _ptr(out3)),
               "accept_sample")
 
-    def shortlist_argmax(self, x, w, s, b, gs, ids, out):
+    def shortlist_argmax(self, x, w, s, b, gs, ids, out, sb=None):
         """out[0] = ids[argmax_j bf16(W_j . x)] over the shortlist rows (lowest position on ties)."""
-        check(self.lib.mtpx_shortlist_argmax(self.h, _ptr(x), x.shape[-1], _ptr(w), _ptr(s), _ptr(b), gs,
+        check(self.lib.mtpx_shortlist_argmax(self.h, _ptr(x), x.shape[-1], _ptr(w), _ptr(s), _ptr(b), _ptr(sb), gs,
                                              ids.shape[0], _ptr(ids), _ptr(out)), "shortlist_argmax")
 
     def profile(self, on: bool = True):
@@ -303,5 +318,6 @@ def moe_weights_from(tensors: dict, H, E, K, F, gs) -> MoEWeights:
     """Build the C struct from a dict of device tensors named like its fields."""
     w = MoEWeights(H, E, K, F, gs)
     for name, _ in MoEWeights._fields_[5:]:
-        setattr(w, name, tensors[name].data_ptr())
+        t = tensors.get(name)
+        setattr(w, name, t.data_ptr() if t is not None else None)
     return w

@@ -28,7 +28,8 @@ class MoEWeights(C.Structure):
                     "router", "shared_gate",
                     "gate_w", "gate_s", "gate_b", "up_w", "up_s", "up_b", "down_w", "down_s", "down_b",
                     "sh_gate_w", "sh_gate_s", "sh_gate_b", "sh_up_w", "sh_up_s", "sh_up_b",
-                    "sh_down_w", "sh_down_s", "sh_down_b")]
+                    "sh_down_w", "sh_down_s", "sh_down_b",
+                    "gate_sb", "up_sb", "down_sb", "sh_gate_sb", "sh_up_sb", "sh_down_sb")]
 
 
 class LayerConfig(C.Structure):
@@ -40,11 +41,11 @@ class LayerConfig(C.Structure):
 class LayerWeights(C.Structure):
     _fields_ = [(n, P) for n in ("attn_norm", "post_norm", "qkv_w", "qkv_s", "qkv_b", "q_norm", "k_norm",
                                  "o_w", "o_s", "o_b", "rope_cos", "rope_sin")] + [
-        ("moe", MoEWeights), ("qkv_rows", INT)]
+        ("moe", MoEWeights), ("qkv_rows", INT), ("qkv_sb", P), ("o_sb", P)]
 
 
 class Q4(C.Structure):
-    _fields_ = [("w", P), ("s", P), ("b", P)]
+    _fields_ = [("w", P), ("s", P), ("b", P), ("sb", P)]
 
 
 class HCWeights(C.Structure):
@@ -78,7 +79,9 @@ _SIGS = {
     "mtpx_ctx_synchronize": (INT, [Handle]),
     "mtpx_affine_quantize": (INT, [Handle, P, I64, INT, INT, P, P, P]),
     "mtpx_randn_bf16": (INT, [Handle, P, I64, U64, U32, F32]),
-    "mtpx_qmv": (INT, [Handle, P, P, P, INT, INT, INT, P, INT, P, P]),
+    "mtpx_q4_sb_row_len": (INT, [INT, INT]),
+    "mtpx_q4_pack_sb": (INT, [Handle, P, P, I64, INT, INT, P]),
+    "mtpx_qmv": (INT, [Handle, P, P, P, P, INT, INT, INT, P, INT, P, P]),
     "mtpx_moe_forward": (INT, [Handle, C.POINTER(MoEWeights), P, INT, P, P, P, P, P]),
     "mtpx_attn_prep": (INT, [Handle, P, INT, INT, INT, INT, INT, INT, P, P, F32, P, P, INT, P, P, P, I64]),
     "mtpx_attn_verify": (INT, [Handle, P, INT, INT, INT, INT, P, P, I64, INT, F32, P, INT, INT, P, P]),
@@ -97,7 +100,7 @@ _SIGS = {
     "mtpx_layer_weights_get": (INT, [Handle, C.POINTER(LayerWeights)]),
     "mtpx_layer_forward": (INT, [Handle, Handle, Handle, P, INT, P]),
     "mtpx_last_moe_bytes": (INT, [Handle, C.POINTER(I64), C.POINTER(I32)]),
-    "mtpx_shortlist_argmax": (INT, [Handle, P, INT, P, P, P, INT, INT, P, P]),
+    "mtpx_shortlist_argmax": (INT, [Handle, P, INT, P, P, P, P, INT, INT, P, P]),
     "mtpx_head_new_random": (INT, [Handle, C.POINTER(HeadConfig), U64, C.POINTER(Handle)]),
     "mtpx_head_free": (INT, [Handle]),
     "mtpx_head_weights_get": (INT, [Handle, C.POINTER(HeadWeights)]),

@@ -28,7 +28,7 @@ def test_version_and_error_string():
 
 def test_struct_sizes_match_header_layout():
     # offsets of the pointer block after five ints (padded to 8)
-    assert C.sizeof(_lib.MoEWeights) == 24 + 20 * 8
+    assert C.sizeof(_lib.MoEWeights) == 24 + 26 * 8
     assert _lib.LayerWeights.moe.offset == 12 * 8
 
 
@@ -40,10 +40,10 @@ def test_struct_layouts_match_c_compiler(tmp_path):
         pytest.skip("gcc not available")
     inc = os.path.dirname(_lib.HEADER)
     checks = {
-        "mtpx_moe_weights": (_lib.MoEWeights, ["router", "gate_w", "sh_down_b"]),
+        "mtpx_moe_weights": (_lib.MoEWeights, ["router", "gate_w", "sh_down_b", "gate_sb", "sh_down_sb"]),
         "mtpx_layer_config": (_lib.LayerConfig, ["rope_theta", "max_positions"]),
-        "mtpx_layer_weights": (_lib.LayerWeights, ["rope_sin", "moe", "qkv_rows"]),
-        "mtpx_q4": (_lib.Q4, ["s", "b"]),
+        "mtpx_layer_weights": (_lib.LayerWeights, ["rope_sin", "moe", "qkv_rows", "qkv_sb", "o_sb"]),
+        "mtpx_q4": (_lib.Q4, ["s", "b", "sb"]),
         "mtpx_hc_weights": (_lib.HCWeights, ["down", "inject", "up"]),
         "mtpx_head_config": (_lib.HeadConfig, ["hc", "lowrank", "vocab", "shortlist_low", "shortlist_special_from"]),
         "mtpx_drafter_info": (_lib.DrafterInfo, ["round_base_offset", "round_in_flight", "released"]),

@@ -37,9 +37,11 @@ def test_shortlist_argmax_bit_exact(ctx, rows, H, gs):
     ids = np.sort(r.choice(1 << 20, rows, replace=False)).astype(np.int32)
     y, _ = O.qmv(wq, s, b, gs, x)
     want = O.shortlist_argmax(y, ids)
-    out = torch.full((1,), -1, dtype=torch.int32, device="cuda")
-    ctx.shortlist_argmax(dev(x)[0], dev(wq), dev(s), dev(b), gs, dev(ids), out)
-    assert int(host(out)[0]) == want
+    ds, db = dev(s), dev(b)
+    for sb in (None, ctx.pack_sb(ds, db, H, gs)):
+        out = torch.full((1,), -1, dtype=torch.int32, device="cuda")
+        ctx.shortlist_argmax(dev(x)[0], dev(wq), ds, db, gs, dev(ids), out, sb=sb)
+        assert int(host(out)[0]) == want
 
 
 def test_shortlist_argmax_tie_takes_lowest_position(ctx):

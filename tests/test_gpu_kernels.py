@@ -74,12 +74,14 @@ def test_qmv_bit_exact(ctx, N, K, gs, M):
     wq, s, b = qweights(r, N, K, gs)
     x = rand_bf16(r, (M, K))
     y_o, yf_o = O.qmv(wq, s, b, gs, x)
-    y = empty_bf16(M, N)
-    yf = torch.zeros(M, N, dtype=torch.float32, device="cuda")
-    ctx.qmv(dev(wq), dev(s), dev(b), gs, dev(x), y, yf)
-    ctx.synchronize()
-    assert np.array_equal(host(yf).view(np.uint32), yf_o.view(np.uint32))
-    assert np.array_equal(host(y), y_o)
+    ds, db = dev(s), dev(b)
+    for sb in (None, ctx.pack_sb(ds, db, K, gs)):  # checkpoint scale/bias rows, then the packed pairs
+        y = empty_bf16(M, N)
+        yf = torch.zeros(M, N, dtype=torch.float32, device="cuda")
+        ctx.qmv(dev(wq), ds, db, gs, dev(x), y, yf, sb=sb)
+        ctx.synchronize()
+        assert np.array_equal(host(yf).view(np.uint32), yf_o.view(np.uint32))
+        assert np.array_equal(host(y), y_o)
 
 
 def test_qmv_repeat_is_bit_stable(ctx):

@@ -42,12 +42,15 @@ def make_moe(seed, H, E, K, F, gs):
     return w
 
 
-def run_case(ctx, w, H, E, K, F, gs, M, xseed):
+def run_case(ctx, w, H, E, K, F, gs, M, xseed, packed=False):
     import mtpx
     r = np.random.default_rng(xseed)
     x = rand_bf16(r, (M, H), 1.0)
     ref = O.moe_block(w, x, H, E, K, F, gs)
     dw = {n: dev(w[n]) for n in NAMES}
+    if packed:  # packed (scale, bias) rows for the expert GEMVs
+        for n, Kd in (("gate", H), ("up", H), ("down", F), ("sh_gate", H), ("sh_up", H), ("sh_down", F)):
+            dw[n + "_sb"] = ctx.pack_sb(dw[n + "_s"], dw[n + "_b"], Kd, gs)
     mw = mtpx.moe_weights_from(dw, H, E, K, F, gs)
     y = empty_bf16(M, H)
     idx = torch.zeros(M, K, dtype=torch.int32, device="cuda")
@@ -69,20 +72,20 @@ def run_case(ctx, w, H, E, K, F, gs, M, xseed):
     return ref
 
 
-@pytest.mark.parametrize("M", [1, 4])
-def test_moe_config1_bit_exact(ctx, M):
-    print("case config1 M", M, flush=True)
+@pytest.mark.parametrize("M,packed", [(1, False), (4, False), (4, True)])
+def test_moe_config1_bit_exact(ctx, M, packed):
+    print("case config1 M", M, "packed", packed, flush=True)
     H, E, K, F, gs = 2048, 64, 8, 768, 64
     w = make_moe(0x5EED0001, H, E, K, F, gs)
-    run_case(ctx, w, H, E, K, F, gs, M, 0x5EED0002 + M)
+    run_case(ctx, w, H, E, K, F, gs, M, 0x5EED0002 + M, packed)
 
 
-@pytest.mark.parametrize("gs,M", [(64, 1), (64, 6), (32, 2), (32, 8)])
-def test_moe_full_expert_shapes_bit_exact(ctx, gs, M):
-    print("case fullshape gs", gs, "M", M, flush=True)
+@pytest.mark.parametrize("gs,M,packed", [(64, 1, False), (64, 6, True), (32, 2, False), (32, 8, True)])
+def test_moe_full_expert_shapes_bit_exact(ctx, gs, M, packed):
+    print("case fullshape gs", gs, "M", M, "packed", packed, flush=True)
     H, E, K, F = 2560, 24, 10, 640
     w = make_moe(1000 + gs, H, E, K, F, gs)
-    run_case(ctx, w, H, E, K, F, gs, M, 77 + M)
+    run_case(ctx, w, H, E, K, F, gs, M, 77 + M, packed)
 
 
 def test_moe_router_ties_lowest_index(ctx):
@@ -98,3 +101,12 @@ def test_moe_router_ties_lowest_index(ctx):
         for a, b in ((3, 9), (9, 12), (3, 12)):
             if b in sel:
                 assert a in sel and sel.index(a) < sel.index(b)
+
+
+@pytest.mark.parametrize("H,E,K,F,gs,M", [(4096, 12, 4, 256, 64, 8), (1024, 16, 4, 320, 32, 5),
+                                          (512, 8, 2, 1024, 32, 3)])
+def test_moe_other_depths_bit_exact(ctx, H, E, K, F, gs, M):
+    # H 4096 at M 8 leaves no LDS for a prefetch ring in gate|up; F 1024 fills the down staging
+    print("case moe shape", H, E, K, F, gs, M, flush=True)
+    w = make_moe(H + F + M, H, E, K, F, gs)
+    run_case(ctx, w, H, E, K, F, gs, M, 31 + M, packed=True)

@@ -15,6 +15,10 @@
 
 namespace mtpx {
 
+constexpr int ATTN_THREADS = 512;    // partial-kernel workgroup
+constexpr int COMBINE_BATCH = 48;    // chunk partials per load round in the combine
+constexpr int COMBINE_MAXCH = 2048;  // chunks (T <= 2048 * ATTN_CHUNK = 65536)
+
 __global__ void k_attn_prep(const bf16* __restrict__ qkv, int S, int QW, int HQ, int HK, int D, int ROT,
                             const bf16* __restrict__ qnorm, const bf16* __restrict__ knorm, float eps,
                             const bf16* __restrict__ cos_t, const bf16* __restrict__ sin_t, int pos0,
@@ -74,7 +78,7 @@ __global__ void k_attn_prep(const bf16* __restrict__ qkv, int S, int QW, int HQ,
 // part layout: [(hk * nch + c) * R + ri] * (D + 2): {m, l, o[0..D)}, R = S * G,
 // ri = s * G + g.  grid (nch, HK, S): one workgroup per (key chunk, kv head,
 // query); its rows are the G query heads of the group.
-__global__ __launch_bounds__(256) void k_attn_partial(const bf16* __restrict__ q, int S, int HQ, int HK, int D,
+__global__ __launch_bounds__(ATTN_THREADS) void k_attn_partial(const bf16* __restrict__ q, int S, int HQ, int HK, int D,
                                                       const bf16* __restrict__ kc, const bf16* __restrict__ vc,
                                                       int64_t tmax, int T, float scale, int nch,
                                                       float* __restrict__ part) {
@@ -85,8 +89,9 @@ __global__ __launch_bounds__(256) void k_attn_partial(const bf16* __restrict__ q
   const int last = T - S + s;                // last key visible to this query
   int n = last + 1 - i0;                     // visible keys of the chunk (a prefix)
   n = n < 0 ? 0 : (n > C ? C : n);
-  // K rows padded by one dword: lanes walking different keys hit different banks
-  const int KS = D / 2 + 1;
+  // K rows padded by 4 dwords: 16-byte aligned rows for 128-bit reads, and 8
+  // consecutive keys cover all 32 banks
+  const int KS = D / 2 + 4;
   uint32_t* qb = reinterpret_cast<uint32_t*>(smem);         // [G][D/2] bf16 pairs
   uint32_t* kb = qb + (size_t)G * (D / 2);                  // [C][KS]
   bf16* vb = reinterpret_cast<bf16*>(kb + (size_t)C * KS);  // [C][D]
@@ -135,41 +140,76 @@ __global__ __launch_bounds__(256) void k_attn_partial(const bf16* __restrict__ q
     }
   }
   __syncthreads();
+  // scores: one (query row g, key j) chain per thread and pass: the sequential
+  // d-order fmaf of the canonical order, fed 8 dimensions per 128-bit LDS read
   for (int p = threadIdx.x; p < G * C; p += blockDim.x) {
-    const int g = p / C, j = p % C;
+    const bool on = (p % C) < n;
+    const uint32_t* qr = qb + (size_t)(p / C) * (D / 2);
+    const uint32_t* kr = kb + (size_t)(on ? p % C : 0) * KS;
     float acc = 0.0f;
-    if (j < n) {
-      const uint32_t* qr = qb + (size_t)g * (D / 2);
-      const uint32_t* kr = kb + (size_t)j * KS;
-      for (int d2 = 0; d2 < D / 2; ++d2) {
-        const uint32_t qq = qr[d2], kk = kr[d2];
-        acc = __builtin_fmaf(scale * __uint_as_float(qq << 16), __uint_as_float(kk << 16), acc);
-        acc = __builtin_fmaf(scale * __uint_as_float(qq & 0xffff0000u), __uint_as_float(kk & 0xffff0000u), acc);
+    for (int d0 = 0; d0 < D / 2; d0 += 4) {
+      const uint4 q4v = *reinterpret_cast<const uint4*>(qr + d0), k4v = *reinterpret_cast<const uint4*>(kr + d0);
+      const uint32_t qa[4] = {q4v.x, q4v.y, q4v.z, q4v.w}, ka[4] = {k4v.x, k4v.y, k4v.z, k4v.w};
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        acc = __builtin_fmaf(scale * __uint_as_float(qa[t] << 16), __uint_as_float(ka[t] << 16), acc);
+        acc = __builtin_fmaf(scale * __uint_as_float(qa[t] & 0xffff0000u), __uint_as_float(ka[t] & 0xffff0000u), acc);
       }
     }
-    sc[p] = acc;
+    sc[p] = on ? acc : 0.0f;
   }
   __syncthreads();
+  // chunk max per query row (order-free), every exp in parallel, then the row
+  // sums in key order
   for (int g = threadIdx.x; g < G; g += blockDim.x) {
     float mx = -__uint_as_float(0x7f800000u);
     for (int j = 0; j < n; ++j) mx = sc[g * C + j] > mx ? sc[g * C + j] : mx;
-    float l = 0.0f;
-    for (int j = 0; j < n; ++j) {
-      const float e = expf_det(sc[g * C + j] - mx);
-      sc[g * C + j] = e;
-      l = l + e;
-    }
     ml[2 * g] = (n > 0) ? mx : -__uint_as_float(0x7f800000u);
+  }
+  __syncthreads();
+  for (int p = threadIdx.x; p < G * C; p += blockDim.x) {
+    const int g = p / C, j = p % C;
+    if (j < n) sc[p] = expf_det(sc[p] - ml[2 * g]);
+  }
+  __syncthreads();
+  for (int g = threadIdx.x; g < G; g += blockDim.x) {
+    float l = 0.0f;
+#pragma unroll 8
+    for (int j = 0; j < n; ++j) l = l + sc[g * C + j];
     ml[2 * g + 1] = (n > 0) ? l : 0.0f;
   }
   __syncthreads();
-  for (int p = threadIdx.x; p < G * D; p += blockDim.x) {
-    const int g = p / D, d = p % D;
-    float o = 0.0f;
-    for (int j = 0; j < n; ++j) o = __builtin_fmaf(sc[g * C + j], bf2f(vb[(size_t)j * D + d]), o);
+  // P.V: a thread owns the adjacent outputs (g, 2e) and (g, 2e+1), one 32-bit V
+  // read per key for both; each output is the sequential key-order fmaf
+  const uint32_t* vb32 = reinterpret_cast<const uint32_t*>(vb);
+  for (int p = threadIdx.x; p < G * (D / 2); p += blockDim.x) {
+    const int g = p / (D / 2), e = p % (D / 2);
+    const float* sg = sc + (size_t)g * C;
+    float o0 = 0.0f, o1 = 0.0f;
+    int j = 0;
+    for (; j + 8 <= n; j += 8) {
+      float pv[8];
+      uint32_t vv[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        pv[u] = sg[j + u];
+        vv[u] = vb32[(size_t)(j + u) * (D / 2) + e];
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        o0 = __builtin_fmaf(pv[u], __uint_as_float(vv[u] << 16), o0);
+        o1 = __builtin_fmaf(pv[u], __uint_as_float(vv[u] & 0xffff0000u), o1);
+      }
+    }
+    for (; j < n; ++j) {
+      const uint32_t v = vb32[(size_t)j * (D / 2) + e];
+      o0 = __builtin_fmaf(sg[j], __uint_as_float(v << 16), o0);
+      o1 = __builtin_fmaf(sg[j], __uint_as_float(v & 0xffff0000u), o1);
+    }
     float* dst = part + (((size_t)hk * nch + c) * R + s * G + g) * (D + 2);
-    dst[2 + d] = o;
-    if (d == 0) {
+    dst[2 + 2 * e] = o0;
+    dst[3 + 2 * e] = o1;
+    if (e == 0) {
       dst[0] = ml[2 * g];
       dst[1] = ml[2 * g + 1];
     }
@@ -184,18 +224,28 @@ __global__ __launch_bounds__(256) void k_attn_combine(const float* __restrict__ 
                                                       bf16* __restrict__ out, bf16* __restrict__ out_gated,
                                                       uint32_t* __restrict__ xp_gated) {
   __shared__ uint32_t scratch[8][24];
-  __shared__ float fc[256], lc[256], red[4];
+  __shared__ float mc[COMBINE_MAXCH], fc[COMBINE_MAXCH], lc[COMBINE_MAXCH], red[4];
   const int ri = blockIdx.x, hk = blockIdx.y;
   const int G = HQ / HK, R = S * G;
   const int s = ri / G, h = hk * G + ri % G;
   const int t = threadIdx.x, nt = blockDim.x;
+  const int d = t;  // blockDim >= D
   auto chunk = [&](int c) { return part + (((size_t)hk * nch + c) * R + ri) * (D + 2); };
-  // M: max of the visible chunks' maxima (order-free)
-  float M = -__uint_as_float(0x7f800000u);
+  // one round of loads: every chunk's (m, l) into LDS, and this thread's first
+  // COMBINE_BATCH output partials into registers
+  float pv[COMBINE_BATCH];
+#pragma unroll
+  for (int u = 0; u < COMBINE_BATCH; ++u) pv[u] = (u < nch && d < D) ? chunk(u)[2 + d] : 0.0f;
   for (int c = t; c < nch; c += nt) {
     const float* p = chunk(c);
-    if (p[1] > 0.0f && p[0] > M) M = p[0];
+    mc[c] = p[0];
+    lc[c] = p[1];
   }
+  __syncthreads();
+  // M: max of the visible chunks' maxima (order-free)
+  float M = -__uint_as_float(0x7f800000u);
+  for (int c = t; c < nch; c += nt)
+    if (lc[c] > 0.0f && mc[c] > M) M = mc[c];
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) {
     const float o = __shfl_xor(M, off, 64);
@@ -204,31 +254,22 @@ __global__ __launch_bounds__(256) void k_attn_combine(const float* __restrict__ 
   if ((t & 63) == 0) red[t >> 6] = M;
   __syncthreads();
   for (int wv = 0; wv < nt / 64; ++wv) M = red[wv] > M ? red[wv] : M;
-  // L and O[d] in chunk order, 256 chunks per tile, the factor f_c once per chunk
-  const int d = t;  // blockDim >= D
+  // the factor of every chunk once, then L and O[d] in chunk order
+  for (int c = t; c < nch; c += nt) fc[c] = lc[c] > 0.0f ? expf_det(mc[c] - M) : 0.0f;
+  __syncthreads();
   float L = 0.0f, O = 0.0f;
-  for (int c0 = 0; c0 < nch; c0 += 256) {
-    const int nc = nch - c0 < 256 ? nch - c0 : 256;
-    __syncthreads();
-    for (int c = t; c < nc; c += nt) {
-      const float* p = chunk(c0 + c);
-      const bool vis = p[1] > 0.0f;
-      fc[c] = vis ? expf_det(p[0] - M) : 0.0f;
-      lc[c] = vis ? p[1] : 0.0f;
-    }
-    __syncthreads();
-    for (int c = 0; c < nc; ++c)
-      if (lc[c] > 0.0f) L = __builtin_fmaf(lc[c], fc[c], L);
-    if (d < D) {
-      for (int cb = 0; cb < nc; cb += 8) {
-        float pv[8];
+#pragma unroll 8
+  for (int c = 0; c < nch; ++c)
+    if (lc[c] > 0.0f) L = __builtin_fmaf(lc[c], fc[c], L);
 #pragma unroll
-        for (int u = 0; u < 8; ++u) pv[u] = (cb + u < nc) ? chunk(c0 + cb + u)[2 + d] : 0.0f;
+  for (int u = 0; u < COMBINE_BATCH; ++u)
+    if (u < nch && lc[u] > 0.0f) O = __builtin_fmaf(pv[u], fc[u], O);
+  for (int cb = COMBINE_BATCH; cb < nch; cb += COMBINE_BATCH) {
 #pragma unroll
-        for (int u = 0; u < 8; ++u)
-          if (cb + u < nc && lc[cb + u] > 0.0f) O = __builtin_fmaf(pv[u], fc[cb + u], O);
-      }
-    }
+    for (int u = 0; u < COMBINE_BATCH; ++u) pv[u] = (cb + u < nch && d < D) ? chunk(cb + u)[2 + d] : 0.0f;
+#pragma unroll
+    for (int u = 0; u < COMBINE_BATCH; ++u)
+      if (cb + u < nch && lc[cb + u] > 0.0f) O = __builtin_fmaf(pv[u], fc[cb + u], O);
   }
   {
     const int d0 = 0;
@@ -332,25 +373,37 @@ hipError_t launch_attn_prep(const bf16* qkv, int S, int QW, int HQ, int HK, int 
   return hipGetLastError();
 }
 
-hipError_t launch_attn_verify(const bf16* q, int S, int HQ, int HK, int D, const bf16* kc, const bf16* vc,
-                              int64_t tmax, int T, float scale, float* part, const bf16* qkv, int QW, int gate_off,
-                              bf16* out, bf16* out_gated, uint32_t* xp_gated, hipStream_t st) {
+hipError_t launch_attn_partial(const bf16* q, int S, int HQ, int HK, int D, const bf16* kc, const bf16* vc,
+                               int64_t tmax, int T, float scale, float* part, hipStream_t st) {
   const int nch = (T + ATTN_CHUNK - 1) / ATTN_CHUNK;
-  const int G = HQ / HK, R = S * G;
   const size_t lds = attn_partial_lds(HQ / HK, D);
   static size_t cur = 0;
   hipError_t e = ensure_lds(k_attn_partial, lds, cur);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(k_attn_partial, dim3(nch, HK, S), dim3(256), lds, st, q, S, HQ, HK, D, kc, vc, tmax, T, scale,
-                     nch, part);
-  if ((e = hipGetLastError()) != hipSuccess) return e;
+  hipLaunchKernelGGL(k_attn_partial, dim3(nch, HK, S), dim3(ATTN_THREADS), lds, st, q, S, HQ, HK, D, kc, vc, tmax, T,
+                     scale, nch, part);
+  return hipGetLastError();
+}
+
+hipError_t launch_attn_combine(int S, int HQ, int HK, int D, int T, const float* part, const bf16* qkv, int QW,
+                               int gate_off, bf16* out, bf16* out_gated, uint32_t* xp_gated, hipStream_t st) {
+  const int nch = (T + ATTN_CHUNK - 1) / ATTN_CHUNK;
+  const int R = S * (HQ / HK);
   hipLaunchKernelGGL(k_attn_combine, dim3(R, HK), dim3(D < 64 ? 64 : D), 0, st, part, S, HQ, HK, D, nch, qkv, QW,
                      gate_off, out, out_gated, xp_gated);
   return hipGetLastError();
 }
 
+hipError_t launch_attn_verify(const bf16* q, int S, int HQ, int HK, int D, const bf16* kc, const bf16* vc,
+                              int64_t tmax, int T, float scale, float* part, const bf16* qkv, int QW, int gate_off,
+                              bf16* out, bf16* out_gated, uint32_t* xp_gated, hipStream_t st) {
+  hipError_t e = launch_attn_partial(q, S, HQ, HK, D, kc, vc, tmax, T, scale, part, st);
+  if (e != hipSuccess) return e;
+  return launch_attn_combine(S, HQ, HK, D, T, part, qkv, QW, gate_off, out, out_gated, xp_gated, st);
+}
+
 size_t attn_partial_lds(int G, int D) {
-  return (size_t)G * D * 2 + (size_t)ATTN_CHUNK * (D + 2) * 2 + (size_t)ATTN_CHUNK * D * 2 +
+  return (size_t)G * D * 2 + (size_t)ATTN_CHUNK * (D + 8) * 2 + (size_t)ATTN_CHUNK * D * 2 +
          (size_t)G * ATTN_CHUNK * 4 + (size_t)G * 8;
 }
 

@@ -334,7 +334,9 @@ int layer_check(const mtpx_layer_config* cfg) {
   const int H = cfg->hidden, F = cfg->expert_width, gs = cfg->group_size;
   const int HQ = cfg->heads, HK = cfg->kv_heads, D = cfg->head_dim;
   ARG(gs_ok(gs) && k_ok(H, gs) && k_ok(F, gs) && k_ok(HQ * D, gs), "unsupported GEMV depths");
-  ARG(HK >= 1 && HQ % HK == 0 && D <= 256 && cfg->rot_dims <= D && cfg->max_positions >= 1, "attention dims");
+  ARG(HK >= 1 && HQ % HK == 0 && HQ / HK <= 32 && D <= 256 && cfg->rot_dims <= D && cfg->max_positions >= 1 &&
+          cfg->max_positions <= 65536,
+      "attention dims (max_positions <= 65536)");
   return MTPX_OK;
 }
 
@@ -416,9 +418,9 @@ int attn_enqueue(Ctx* c, const Layer* L, Kv* kv, uint32_t* xp, int M, uint16_t* 
   LAUNCH(c, "attn_prep", launch_attn_prep(qkv, M, QW, HQ, HK, D, g.rot_dims, L->w.q_norm, L->w.k_norm, g.eps,
                                           L->w.rope_cos, L->w.rope_sin, (int)kv->offset, q, kv->k, kv->v,
                                           kv->tmax, st));
-  LAUNCH(c, "attn_verify", launch_attn_verify(q, M, HQ, HK, D, kv->k, kv->v, kv->tmax, T,
-                                              1.0f / std::sqrt((float)D), part, qkv, QW, HQ * D, nullptr, att,
-                                              xp, st));
+  LAUNCH(c, "attn_partial", launch_attn_partial(q, M, HQ, HK, D, kv->k, kv->v, kv->tmax, T,
+                                                1.0f / std::sqrt((float)D), part, st));
+  LAUNCH(c, "attn_combine", launch_attn_combine(M, HQ, HK, D, T, part, qkv, QW, HQ * D, nullptr, att, xp, st));
   LAUNCH(c, "qmv_o", launch_qmv(L->w.o_w, L->w.o_s, L->w.o_b, L->w.o_sb, H, HQ * D, gs, xp, M, o, nullptr, st));
   return MTPX_OK;
 }
@@ -841,11 +843,13 @@ int mtpx_attn_verify(mtpx_ctx h, const uint16_t* q, int S, int HQ, int HK, int D
   ARG(c && q && kc && vc, "null argument");
   ARG(out || out_gated, "no output requested");
   ARG(!out_gated || qkv, "out_gated needs qkv");
-  ARG(S >= 1 && S <= MAX_TOKENS && T >= S && T <= tmax, "S=%d T=%d tmax=%lld", S, T, (long long)tmax);
+  ARG(S >= 1 && S <= MAX_TOKENS && T >= S && T <= tmax && T <= 65536, "S=%d T=%d tmax=%lld (T <= 65536)", S, T,
+      (long long)tmax);
   ARG(D >= 8 && D <= 256 && (D & (D - 1)) == 0, "head_dim=%d", D);
   ARG(HK >= 1 && HQ % HK == 0, "heads %d / kv heads %d", HQ, HK);
   ARG(D % 32 == 0, "head_dim=%d must be a multiple of 32", D);
-  ARG(attn_partial_lds(HQ / HK, D) <= 160 * 1024, "GQA group of %d heads exceeds one workgroup's LDS", HQ / HK);
+  ARG(HQ / HK <= 32 && attn_partial_lds(HQ / HK, D) <= 160 * 1024, "GQA group of %d heads unsupported (<= 32)",
+      HQ / HK);
   ARG(!out_gated || (gate_off >= 0 && gate_off + HQ * D <= QW), "gate columns outside qkv rows");
   if (set_device(c)) return MTPX_ERR_HIP;
   const size_t pf = attn_partial_floats(S, HQ, D, T);
@@ -853,8 +857,9 @@ int mtpx_attn_verify(mtpx_ctx h, const uint16_t* q, int S, int HQ, int HK, int D
   if (rc) return rc;
   c->ws_used = 0;
   float* part = ws_take<float>(c, pf);
-  HIP_OK(launch_attn_verify(q, S, HQ, HK, D, kc, vc, tmax, T, scale, part, qkv, QW, gate_off, out, out_gated, nullptr,
-                            c->stream));
+  LAUNCH(c, "attn_partial", launch_attn_partial(q, S, HQ, HK, D, kc, vc, tmax, T, scale, part, c->stream));
+  LAUNCH(c, "attn_combine", launch_attn_combine(S, HQ, HK, D, T, part, qkv, QW, gate_off, out, out_gated, nullptr,
+                                                c->stream));
   return MTPX_OK;
 }
 

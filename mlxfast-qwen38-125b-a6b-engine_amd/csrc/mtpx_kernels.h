@@ -89,6 +89,10 @@ hipError_t launch_attn_verify(const bf16* q, int S, int HQ, int HK, int D, const
                               const bf16* qkv, int QW, int gate_off, bf16* out, bf16* out_gated,
                               uint32_t* xp_gated, hipStream_t st);
 size_t attn_partial_lds(int G, int D);
+hipError_t launch_attn_partial(const bf16* q, int S, int HQ, int HK, int D, const bf16* kc, const bf16* vc,
+                               int64_t tmax, int T, float scale, float* part, hipStream_t st);
+hipError_t launch_attn_combine(int S, int HQ, int HK, int D, int T, const float* part, const bf16* qkv, int QW,
+                               int gate_off, bf16* out, bf16* out_gated, uint32_t* xp_gated, hipStream_t st);
 hipError_t launch_rmsnorm(const bf16* x, const bf16* resid, int M, int H, const bf16* w, float eps,
                           bf16* sum_out, bf16* y, uint32_t* xp, hipStream_t st);
 hipError_t launch_add(const bf16* a, const bf16* b, int64_t n, bf16* out, hipStream_t st);

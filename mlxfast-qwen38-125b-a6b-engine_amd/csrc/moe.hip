@@ -241,9 +241,10 @@ __device__ __forceinline__ int slot_token(int slot, int M, int K) {
 // gate|up + SwiGLU.  grid (F/32, M*K+1), GU_THREADS threads.  Every lane-group
 // owns one f of the block and walks its gate row and up row; the weight loads
 // are issued before the activations are staged into LDS.
-constexpr int GU_THREADS = 512;
-
-template <int L, int IT>
+// GU_THREADS threads: 512 (eight waves, one pass each) for a one-token window,
+// where only parallelism matters; 256 (four waves, two passes each: the second
+// pass's loads are in flight while the first is computed) for wider windows.
+template <int L, int IT, int GU_THREADS>
 __global__ __launch_bounds__(GU_THREADS) void k_moe_gate_up(MoeArgs a) {
   extern __shared__ uint32_t lds[];
   __shared__ bf16 actb[MAX_TOKENS][32];
@@ -410,15 +411,20 @@ hipError_t launch_moe_router_route(const MoeArgs& a, hipStream_t st) {
   return hipGetLastError();
 }
 
-template <int L, int IT>
-static hipError_t gate_up_li(const MoeArgs& a, hipStream_t st) {
+template <int L, int IT, int THREADS>
+static hipError_t gate_up_launch(const MoeArgs& a, hipStream_t st) {
   const dim3 grid(a.F / 32, a.M * a.K + 1);
   const size_t lds = (size_t)a.M * (a.H / 32) * XP_DW * 4;
   static size_t cur = 0;
-  hipError_t e = ensure_lds(k_moe_gate_up<L, IT>, lds, cur);
+  hipError_t e = ensure_lds(k_moe_gate_up<L, IT, THREADS>, lds, cur);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((k_moe_gate_up<L, IT>), grid, dim3(GU_THREADS), lds, st, a);
+  hipLaunchKernelGGL((k_moe_gate_up<L, IT, THREADS>), grid, dim3(THREADS), lds, st, a);
   return hipGetLastError();
+}
+
+template <int L, int IT>
+static hipError_t gate_up_li(const MoeArgs& a, hipStream_t st) {
+  return a.M == 1 ? gate_up_launch<L, IT, 512>(a, st) : gate_up_launch<L, IT, 256>(a, st);
 }
 
 template <int L, int IT>

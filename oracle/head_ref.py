@@ -5,6 +5,11 @@ same draft step through the CPU oracle, in the order of
 Runner/FastModel/TrackFastHead.swift:101-153 (the fast head forward) and
 Runner/Qwen4ExpMTP.swift:101-130 (the module wiring), with the drafter's
 shortlist argmax (Runner/Qwen4ExpMTPDrafter.swift:122-153).
+
+Parity unpinned: the wiring of oracle_head (which stream feeds which norm,
+mixer and sublayer) follows those files by reading only; no reference output
+exists to check it against.  Every piece it calls is pinned on its own
+(tests/test_oracle_pin.py, tests/test_oracle_head_pin.py).
 """
 import numpy as np
 

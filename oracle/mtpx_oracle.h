@@ -12,6 +12,11 @@
  * The orders are pinned independently of the GPU by the tests in
  * tests/test_oracle_*.py (float64 brute force, closed forms, known answers).
  *
+ * Parity unpinned: o_rope_table -- the fork's rotary table construction
+ * (Qwen4ExpRotary.cosSin) is in an absent submodule; this table is the
+ * standard rotate-half theta^(-2i/rot) one, which the tests pin only against
+ * float64 RoPE of that same definition.
+ *
  * Build: compile with -ffp-contract=off (no implicit FMA contraction).
  */
 #ifndef MTPX_ORACLE_H

@@ -309,7 +309,7 @@ __global__ __launch_bounds__(GU_THREADS) void k_moe_gate_up(MoeArgs a) {
   {
     const int tk = threadIdx.x >> 5, i = threadIdx.x & 31;
     int E = 0, sm = 0;
-    if (tk < MAX_TOKENS) xprep_lanes_build(tk < cnt ? actb[tk][i] : (bf16)0, i, scratch[tk], E, sm);
+    if (tk < cnt) xprep_lanes_build(actb[tk][i], i, scratch[tk], E, sm);
     __syncthreads();
     if (tk < cnt)
       xprep_lanes_store(i, scratch[tk], E, sm,

@@ -909,3 +909,225 @@ void o_accept_sample(const float* tlogits, const float* dlogits, int k, int64_t 
   free(pt);
   free(pd);
 }
+
+/* ======================================================================== */
+/* a20: the gated-deltanet (GDN) sublayer of the target                     */
+/* Runner/FastModel/TrackFastKernels.swift:48-117 (prep), :148-208 and      */
+/* :486-605 (recurrence, peeled Kahan form), TrackFastKernels2.swift:325-352 */
+/* (gated RMS), TrackFastModel.swift:404-432,655-737 (binding, forward).     */
+/* Every 128-channel reduction is 32 lanes x 4 consecutive elements, each    */
+/* lane in element order, then an xor butterfly over the 32 lanes.           */
+/* ======================================================================== */
+
+/* log1p(y) for y in [0, 1]: 2 atanh(s), s = y / (2 + y) <= 1/3, odd series to
+ * s^15 in Horner form (truncation < 4e-9 relative).  The build's own, so host
+ * and device agree bit for bit. */
+float o_log1p_det(float y) {
+  if (y != y) return y;
+  const float t = 2.0f + y;
+  const float s = y / t;
+  const float s2 = s * s;
+  float r = 1.0f / 15.0f;
+  r = 1.0f / 13.0f + s2 * r;
+  r = 1.0f / 11.0f + s2 * r;
+  r = 1.0f / 9.0f + s2 * r;
+  r = 1.0f / 7.0f + s2 * r;
+  r = 1.0f / 5.0f + s2 * r;
+  r = 1.0f / 3.0f + s2 * r;
+  r = s2 * r;
+  const float h = s + s * r;
+  return h + h;
+}
+
+/* MLX logaddexp(x, 0) in bf16 arithmetic (TrackFastKernels2.swift:48-58):
+ * max + log1p(exp(min - max)), each op rounded to bf16. */
+float o_logaddexp0_bf16(float x) {
+  if (x != x) return x;
+  const float inf = f_from_bits(0x7f800000u);
+  const float mx = x > 0.0f ? x : 0.0f;
+  const float mn = x < 0.0f ? x : 0.0f;
+  if (mn == -inf || mx == inf) return mx;
+  const float d = o_round_bf(mn - mx);
+  const float e = o_round_bf(o_expf(d));
+  const float l = o_round_bf(o_log1p_det(e));
+  return o_round_bf(mx + l);
+}
+
+/* MLX Sigmoid functor in f32: y = 1/(1+exp(|x|)); x < 0 ? y : 1 - y. */
+float o_sigmoid_f32(float x) {
+  const float e = o_expf(fabsf(x));
+  const float y = 1.0f / (1.0f + e);
+  return (x < 0.0f) ? y : 1.0f - y;
+}
+
+static float bfly32(const float* lanes) {
+  float v[32];
+  memcpy(v, lanes, sizeof(v));
+  for (int off = 16; off >= 1; off /= 2) {
+    float n[32];
+    for (int l = 0; l < 32; ++l) n[l] = v[l] + v[l ^ off];
+    memcpy(v, n, sizeof(v));
+  }
+  return v[0];
+}
+
+/* One position of the prep.  conv_state: the KC-1 previous conv input rows
+ * [KC-1][conv_dim]; prow: this position's projection row [proj_w].
+ *   conv  = sum_j win_j * w[ch][j] (f32, j = 0..KC-1, mul then add)
+ *   x     = silu_bf16(bf16(conv))
+ *   q/k heads: inv = 1/sqrt(sum x^2 / 128 + 1e-6); n = bf16(x * inv);
+ *              q = bf16(bf16(1/Dk) * n), k = bf16(bf16(1/sqrt(Dk)) * n)
+ *   v heads:   v = x
+ *   beta  = sigmoid_bf16(b);  decay = exp(-exp(A_log) * softplus_bf16(bf16(a + dt_bias))) */
+void o_gdn_prep(const o_gdn_geom* g, const o_bf16* conv_state, const o_bf16* prow, const o_bf16* conv_w,
+                const float* neg_exp_alog, const o_bf16* dt_bias, o_bf16* q, o_bf16* k, o_bf16* v,
+                float* decay, float* beta) {
+  const int KM1 = g->kc - 1, CD = g->conv_dim, D = 128;
+  const int nvec = 2 * g->hk + g->hv;
+  const float inv_scale = 1.0f / sqrtf((float)g->dk);
+  const float q_mul = o_round_bf(inv_scale * inv_scale);
+  const float k_mul = o_round_bf(inv_scale);
+  for (int vec = 0; vec < nvec; ++vec) {
+    float xs[128], lanes[32];
+    for (int l = 0; l < 32; ++l) {
+      float acc = 0.0f;
+      for (int i = 0; i < 4; ++i) {
+        const int ch = vec * D + l * 4 + i;
+        float c = 0.0f;
+        for (int j = 0; j < g->kc; ++j) {
+          const float win = j < KM1 ? o_bf2f(conv_state[(int64_t)j * CD + ch]) : o_bf2f(prow[ch]);
+          c = c + win * o_bf2f(conv_w[(int64_t)ch * g->kc + j]);
+        }
+        const float x = o_silu_bf16(o_round_bf(c));
+        xs[l * 4 + i] = x;
+        acc = fmaf(x, x, acc);
+      }
+      lanes[l] = acc;
+    }
+    if (vec < 2 * g->hk) {
+      const float inv = 1.0f / sqrtf(bfly32(lanes) / 128.0f + 1e-6f);
+      const float mul = vec < g->hk ? q_mul : k_mul;
+      o_bf16* dst = vec < g->hk ? q + (int64_t)vec * D : k + (int64_t)(vec - g->hk) * D;
+      for (int d = 0; d < D; ++d) dst[d] = o_f2bf(mul * o_round_bf(xs[d] * inv));
+    } else {
+      o_bf16* dst = v + (int64_t)(vec - 2 * g->hk) * D;
+      for (int d = 0; d < D; ++d) dst[d] = o_f2bf(xs[d]);
+    }
+  }
+  for (int h = 0; h < g->hv; ++h) {
+    beta[h] = o_sigmoid_bf16(o_bf2f(prow[g->b_off + h]));
+    const float ax = o_round_bf(o_bf2f(prow[g->a_off + h]) + o_bf2f(dt_bias[h]));
+    decay[h] = o_expf(neg_exp_alog[h] * o_logaddexp0_bf16(ax));
+  }
+}
+
+/* One position of the delta rule for every (value head, value row), in place
+ * on ssm [hv][dv][dk] (f32); y [hv][dv] bf16; delta_out [hv][dv] (may be NULL):
+ *   s *= decay; kv = Kahan sum of s*k (lane-peeled: i = 0 plain, i = 1..3
+ *   compensated, last compensation dropped), butterfly;
+ *   delta = (v - kv) * beta; s = fmaf(k, delta, s); out = sum fmaf(s, q, out). */
+void o_gdn_step(const o_gdn_geom* g, float* ssm, const o_bf16* q, const o_bf16* k, const o_bf16* v,
+                const float* decay, const float* beta, o_bf16* y, float* delta_out) {
+  const int ratio = g->hv / g->hk, D = 128;
+  for (int h = 0; h < g->hv; ++h) {
+    const o_bf16* qh = q + (int64_t)(h / ratio) * D;
+    const o_bf16* kh = k + (int64_t)(h / ratio) * D;
+    const float gd = decay[h], bt = beta[h];
+    for (int r = 0; r < D; ++r) {
+      float* s = ssm + ((int64_t)h * D + r) * D;
+      float kvl[32], ol[32];
+      for (int l = 0; l < 32; ++l) {
+        float* sl = s + 4 * l;
+        const o_bf16* kl = kh + 4 * l;
+        sl[0] = sl[0] * gd;
+        float kv = 0.0f + sl[0] * o_bf2f(kl[0]);
+        float comp = 0.0f;
+        for (int i = 1; i < 4; ++i) {
+          sl[i] = sl[i] * gd;
+          const float prod = sl[i] * o_bf2f(kl[i]);
+          const float corr = prod - comp;
+          const float next = kv + corr;
+          if (i + 1 < 4) comp = (next - kv) - corr;
+          kv = next;
+        }
+        kvl[l] = kv;
+      }
+      const float kvm = bfly32(kvl);
+      const float delta = (o_bf2f(v[(int64_t)h * D + r]) - kvm) * bt;
+      if (delta_out) delta_out[(int64_t)h * D + r] = delta;
+      for (int l = 0; l < 32; ++l) {
+        float o = 0.0f;
+        for (int i = 0; i < 4; ++i) {
+          const int d = 4 * l + i;
+          s[d] = fmaf(o_bf2f(kh[d]), delta, s[d]);
+          o = fmaf(s[d], o_bf2f(qh[d]), o);
+        }
+        ol[l] = o;
+      }
+      y[(int64_t)h * D + r] = o_f2bf(bfly32(ol));
+    }
+  }
+}
+
+/* Gated RMS of one position (TrackFastKernels2.swift:325-352):
+ *   inv = 1/sqrt(sum y^2 / 128 + eps); n = bf16(w * bf16(y * inv));
+ *   out = bf16(sigmoid_f32(z) * n). */
+void o_gdn_gated_rms(const o_gdn_geom* g, const o_bf16* y, const o_bf16* z, const o_bf16* w, float eps,
+                     o_bf16* out) {
+  const int D = 128;
+  for (int h = 0; h < g->hv; ++h) {
+    const o_bf16* yh = y + (int64_t)h * D;
+    float lanes[32];
+    for (int l = 0; l < 32; ++l) {
+      float acc = 0.0f;
+      for (int i = 0; i < 4; ++i) {
+        const float x = o_bf2f(yh[4 * l + i]);
+        acc = fmaf(x, x, acc);
+      }
+      lanes[l] = acc;
+    }
+    const float inv = 1.0f / sqrtf(bfly32(lanes) / 128.0f + eps);
+    for (int d = 0; d < D; ++d) {
+      const float n = o_round_bf(o_bf2f(w[d]) * o_round_bf(o_bf2f(yh[d]) * inv));
+      out[(int64_t)h * D + d] = o_f2bf(o_sigmoid_f32(o_bf2f(z[(int64_t)h * D + d])) * n);
+    }
+  }
+}
+
+/* S positions of the GDN core in order: prep, step, gated RMS; conv_state
+ * [KC-1][conv_dim] and ssm advance by S.  proj [S][proj_w] -> gated [S][hv*128];
+ * optional per-position outputs (NULL to skip): q,k [S][hk*128], v,y [S][hv*128],
+ * decay, beta [S][hv], delta [S][hv*128]. */
+void o_gdn_core(const o_gdn_geom* g, const o_bf16* proj, int S, o_bf16* conv_state, float* ssm,
+                const o_bf16* conv_w, const float* neg_exp_alog, const o_bf16* dt_bias, const o_bf16* norm_w,
+                float eps, o_bf16* gated, o_bf16* q_out, o_bf16* k_out, o_bf16* v_out, o_bf16* y_out,
+                float* decay_out, float* beta_out, float* delta_out) {
+  const int KM1 = g->kc - 1, CD = g->conv_dim, D = 128;
+  o_bf16* q = (o_bf16*)malloc(sizeof(o_bf16) * (size_t)g->hk * D);
+  o_bf16* k = (o_bf16*)malloc(sizeof(o_bf16) * (size_t)g->hk * D);
+  o_bf16* v = (o_bf16*)malloc(sizeof(o_bf16) * (size_t)g->hv * D);
+  o_bf16* y = (o_bf16*)malloc(sizeof(o_bf16) * (size_t)g->hv * D);
+  float* dec = (float*)malloc(sizeof(float) * (size_t)g->hv);
+  float* bet = (float*)malloc(sizeof(float) * (size_t)g->hv);
+  for (int t = 0; t < S; ++t) {
+    const o_bf16* prow = proj + (int64_t)t * g->proj_w;
+    o_gdn_prep(g, conv_state, prow, conv_w, neg_exp_alog, dt_bias, q, k, v, dec, bet);
+    o_gdn_step(g, ssm, q, k, v, dec, bet, y, delta_out ? delta_out + (int64_t)t * g->hv * D : NULL);
+    o_gdn_gated_rms(g, y, prow + g->z_off, norm_w, eps, gated + (int64_t)t * g->hv * D);
+    /* conv tail: drop the oldest row, append this position's conv input */
+    for (int j = 0; j + 1 < KM1; ++j) memcpy(conv_state + (int64_t)j * CD, conv_state + (int64_t)(j + 1) * CD, 2 * (size_t)CD);
+    if (KM1 > 0) memcpy(conv_state + (int64_t)(KM1 - 1) * CD, prow, 2 * (size_t)CD);
+    if (q_out) memcpy(q_out + (int64_t)t * g->hk * D, q, 2 * (size_t)g->hk * D);
+    if (k_out) memcpy(k_out + (int64_t)t * g->hk * D, k, 2 * (size_t)g->hk * D);
+    if (v_out) memcpy(v_out + (int64_t)t * g->hv * D, v, 2 * (size_t)g->hv * D);
+    if (y_out) memcpy(y_out + (int64_t)t * g->hv * D, y, 2 * (size_t)g->hv * D);
+    if (decay_out) memcpy(decay_out + (int64_t)t * g->hv, dec, 4 * (size_t)g->hv);
+    if (beta_out) memcpy(beta_out + (int64_t)t * g->hv, bet, 4 * (size_t)g->hv);
+  }
+  free(q);
+  free(k);
+  free(v);
+  free(y);
+  free(dec);
+  free(bet);
+}

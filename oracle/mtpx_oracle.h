@@ -93,6 +93,26 @@ void o_silu_rows(const o_bf16* x, int64_t n, o_bf16* y);
 void o_hc_mix(const o_bf16* w, const o_bf16* normed, const o_bf16* inj, int S, int hc, int H,
               o_bf16* input, o_bf16* inject_out);
 
+/* ---- a20: the gated-deltanet sublayer (head dims 128) -------------------- */
+typedef struct {
+  int hk, hv, dk, dv, kc, conv_dim; /* key heads, value heads, 128, 128, conv taps, (2hk+hv)*128 */
+  int proj_w, z_off, b_off, a_off;  /* projection row: qkv | z | b | a */
+} o_gdn_geom;
+float o_log1p_det(float y);        /* y in [0, 1] */
+float o_logaddexp0_bf16(float x);  /* MLX logaddexp(x, 0) in bf16 arithmetic */
+float o_sigmoid_f32(float x);      /* MLX Sigmoid in f32 */
+void o_gdn_prep(const o_gdn_geom* g, const o_bf16* conv_state, const o_bf16* prow, const o_bf16* conv_w,
+                const float* neg_exp_alog, const o_bf16* dt_bias, o_bf16* q, o_bf16* k, o_bf16* v,
+                float* decay, float* beta);
+void o_gdn_step(const o_gdn_geom* g, float* ssm, const o_bf16* q, const o_bf16* k, const o_bf16* v,
+                const float* decay, const float* beta, o_bf16* y, float* delta_out);
+void o_gdn_gated_rms(const o_gdn_geom* g, const o_bf16* y, const o_bf16* z, const o_bf16* w, float eps,
+                     o_bf16* out);
+void o_gdn_core(const o_gdn_geom* g, const o_bf16* proj, int S, o_bf16* conv_state, float* ssm,
+                const o_bf16* conv_w, const float* neg_exp_alog, const o_bf16* dt_bias, const o_bf16* norm_w,
+                float eps, o_bf16* gated, o_bf16* q_out, o_bf16* k_out, o_bf16* v_out, o_bf16* y_out,
+                float* decay_out, float* beta_out, float* delta_out);
+
 /* ---- a18, a21, a22: argmax and acceptance ------------------------------- */
 void o_argmax_rows(const float* x, int rows, int64_t V, int32_t* out);
 void o_accept_greedy(const float* logits, int k, int64_t V, const int32_t* drafts,

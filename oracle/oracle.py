@@ -70,6 +70,10 @@ def _declare(L):
         "o_hc_norm": (None, [P, P, P, C.c_int, C.c_int, C.c_int, C.c_int, P, F32, P, P]),
         "o_silu_rows": (None, [P, I64, P]),
         "o_hc_mix": (None, [P, P, P, C.c_int, C.c_int, C.c_int, P, P]),
+        "o_log1p_det": (F32, [F32]),
+        "o_logaddexp0_bf16": (F32, [F32]),
+        "o_sigmoid_f32": (F32, [F32]),
+        "o_gdn_core": (None, [P, P, C.c_int, P, P, P, P, P, P, F32, P, P, P, P, P, P, P, P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -340,3 +344,39 @@ def accept_sample(tlogits, dlogits, drafts, temperature, seed, offset, kv_offset
 def softmax_row_sum(e):
     e = np.ascontiguousarray(e, np.float32)
     return lib().o_softmax_row_sum(_p(e), e.size)
+
+
+# --------------------------------------------------------------------------- a20: GDN
+class GDNGeom(C.Structure):
+    _fields_ = [(n, C.c_int) for n in ("hk", "hv", "dk", "dv", "kc", "conv_dim", "proj_w", "z_off", "b_off",
+                                         "a_off")]
+
+
+def gdn_geom(hk, hv, kc=4):
+    """Projection row layout qkv | z | b | a (TrackFastModel.swift:404-432)."""
+    cd = (2 * hk + hv) * 128
+    return GDNGeom(hk, hv, 128, 128, kc, cd, cd + hv * 128 + 2 * hv, cd, cd + hv * 128, cd + hv * 128 + hv)
+
+
+def gdn_core(g, proj, conv_state, ssm, conv_w, neg_exp_alog, dt_bias, norm_w, eps=1e-6):
+    """S positions of the GDN core.  Returns dict(gated, conv_state, ssm, q, k, v, y, decay, beta, delta);
+    the input state arrays are not modified."""
+    proj = np.ascontiguousarray(proj, np.uint16)
+    S = proj.shape[0]
+    cs = np.array(conv_state, np.uint16, copy=True, order="C")
+    st = np.array(ssm, np.float32, copy=True, order="C")
+    D = 128
+    out = dict(gated=np.zeros((S, g.hv * D), np.uint16), q=np.zeros((S, g.hk * D), np.uint16),
+               k=np.zeros((S, g.hk * D), np.uint16), v=np.zeros((S, g.hv * D), np.uint16),
+               y=np.zeros((S, g.hv * D), np.uint16), decay=np.zeros((S, g.hv), np.float32),
+               beta=np.zeros((S, g.hv), np.float32), delta=np.zeros((S, g.hv * D), np.float32))
+    cw = np.ascontiguousarray(conv_w, np.uint16)
+    nea = np.ascontiguousarray(neg_exp_alog, np.float32)
+    dtb = np.ascontiguousarray(dt_bias, np.uint16)
+    nw = np.ascontiguousarray(norm_w, np.uint16)
+    lib().o_gdn_core(C.byref(g), _p(proj), S, _p(cs), _p(st), _p(cw), _p(nea), _p(dtb), _p(nw), eps,
+                     _p(out["gated"]), _p(out["q"]), _p(out["k"]), _p(out["v"]), _p(out["y"]), _p(out["decay"]),
+                     _p(out["beta"]), _p(out["delta"]))
+    out["conv_state"] = cs
+    out["ssm"] = st
+    return out

@@ -80,7 +80,8 @@ def test_moe_config1_bit_exact(ctx, M, packed):
     run_case(ctx, w, H, E, K, F, gs, M, 0x5EED0002 + M, packed)
 
 
-@pytest.mark.parametrize("gs,M,packed", [(64, 1, False), (64, 6, True), (32, 2, False), (32, 8, True)])
+@pytest.mark.parametrize("gs,M,packed", [(64, 1, False), (64, 4, True), (64, 6, True), (32, 2, False), (32, 3, True),
+                                         (32, 8, True)])
 def test_moe_full_expert_shapes_bit_exact(ctx, gs, M, packed):
     print("case fullshape gs", gs, "M", M, "packed", packed, flush=True)
     H, E, K, F = 2560, 24, 10, 640

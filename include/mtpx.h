@@ -321,6 +321,59 @@ int mtpx_drafter_info_get(mtpx_drafter d, mtpx_drafter_info* out);
 /* requestStateBytesPerToken (:267-275). */
 int mtpx_drafter_bytes_per_token(mtpx_head head, int64_t* out);
 
+/* ---- a20 (part): the gated-deltanet sublayer of the target's linear-attention layers ----
+ * TrackQwen4ExpFastModel.gdnForward (Runner/FastModel/TrackFastModel.swift:655-737):
+ *   proj = in_proj(x)  (rows qkv | z | b | a, TrackFastModel.swift:404-432)
+ *   per position: causal depthwise conv (kc taps) + SiLU; q/k RMS norm and 1/dk, 1/sqrt(dk)
+ *   scales; beta = sigmoid(b); decay = exp(-exp(A_log) * softplus(a + dt_bias))
+ *   (TrackFastKernels.swift:48-117); the delta rule with a Kahan key product (:486-605);
+ *   gated RMS norm (TrackFastKernels2.swift:325-352);  y = out_proj(gated).
+ * Head dims are 128.  Window state: a forward over S positions leaves the committed
+ * recurrent state unchanged and keeps a journal of the window; mtpx_gdn_commit(n) makes
+ * its first n positions committed (the capture-and-stage of TrackFastModel.swift:726-731,
+ * as an offset).  The next forward (or mtpx_gdn_state_store) applies them first. */
+typedef struct mtpx_gdn_ { void* ctx; } mtpx_gdn;
+typedef struct mtpx_gdn_state_ { void* ctx; } mtpx_gdn_state;
+
+typedef struct {
+  int hidden;        /* 2560 */
+  int key_heads;     /* linear_num_key_heads (16) */
+  int value_heads;   /* linear_num_value_heads (48), a multiple of key_heads */
+  int conv_kernel;   /* linear_conv_kernel_dim (4) */
+  int group_size;    /* 32 or 64 */
+  float eps;         /* gated RMS epsilon (1e-6) */
+} mtpx_gdn_config;
+
+typedef struct {
+  mtpx_q4 in_proj;              /* [conv_dim + value_heads*128 + 2*value_heads, hidden] */
+  const uint16_t* conv_w;       /* bf16 [conv_dim, conv_kernel], conv_dim = (2*key_heads + value_heads)*128 */
+  const float* neg_exp_alog;    /* f32 [value_heads]: -exp(A_log) */
+  const uint16_t* dt_bias;      /* bf16 [value_heads] */
+  const uint16_t* norm_w;       /* bf16 [128] */
+  mtpx_q4 out_proj;             /* [hidden, value_heads*128] */
+} mtpx_gdn_weights;
+
+int mtpx_gdn_new_random(mtpx_ctx ctx, const mtpx_gdn_config* cfg, uint64_t seed, mtpx_gdn* out);
+int mtpx_gdn_free(mtpx_gdn gdn);
+int mtpx_gdn_weights_get(mtpx_gdn gdn, mtpx_gdn_weights* out);
+/* Per-request recurrent state (Qwen4ExpCacheEvaluation's conv + ssm entries for one layer):
+ * zero conv rows and zero state. */
+int mtpx_gdn_state_new(mtpx_ctx ctx, const mtpx_gdn_config* cfg, mtpx_gdn_state* out);
+int mtpx_gdn_state_free(mtpx_gdn_state st);
+/* Committed state in/out (device pointers): conv bf16 [conv_kernel-1, conv_dim], ssm f32
+ * [value_heads, 128, 128].  load drops any window; store does not modify the state. */
+int mtpx_gdn_state_load(mtpx_ctx ctx, mtpx_gdn_state st, const uint16_t* conv, const float* ssm);
+int mtpx_gdn_state_store(mtpx_ctx ctx, mtpx_gdn_state st, uint16_t* conv, float* ssm);
+/* The first n (0..window) positions of the last window become committed. */
+int mtpx_gdn_commit(mtpx_gdn_state st, int n);
+int mtpx_gdn_state_info(mtpx_gdn_state st, int* window, int* committed);
+/* The core on given projections: proj bf16 [S, proj_w] -> gated bf16 [S, value_heads*128]. */
+int mtpx_gdn_core(mtpx_ctx ctx, mtpx_gdn gdn, mtpx_gdn_state st, const uint16_t* proj, int S,
+                  uint16_t* gated);
+/* The sublayer: x bf16 [S, hidden] -> y bf16 [S, hidden] (gated may be NULL). */
+int mtpx_gdn_forward(mtpx_ctx ctx, mtpx_gdn gdn, mtpx_gdn_state st, const uint16_t* x, int S,
+                     uint16_t* y, uint16_t* gated);
+
 /* ---- per-kernel timing (replaces TrackFastProfile, Runner/FastModel/TrackFastWeights.swift:81-98) ----
  * With profiling on, every launch the library issues is bracketed by HIP events
  * on the context stream.  mtpx_profile_dump synchronises and writes one line per

@@ -1,0 +1,285 @@
+// Gated-deltanet (GDN) sublayer core of the target's linear-attention layers
+// for a window of S <= 8 positions: causal depthwise conv + SiLU, q/k RMS
+// norms and scales, decay/beta gates, the delta-rule recurrence with a
+// Kahan-compensated key product, and the gated output RMS norm -- one launch,
+// one workgroup per value head.
+//
+// Window state.  The reference keeps the recurrent state after every window
+// position so the engine can roll back to any of them (Runner/FastModel/
+// TrackFastModel.swift:726-731, stageCaptured).  Here a window writes a
+// journal instead -- its conv input rows, the normalised keys, and per
+// (head, value row) the delta and per head the decay of every position, about
+// 50 KB per position against 3.1 MB of state -- and leaves the committed state
+// alone.  Committing n positions only records n; the next window first replays
+// those n steps (the same float operations, so the same bits) onto the
+// committed state and stores it, then runs its own positions.  Journal and conv
+// base are double-buffered (slot `cur` read, slot `nxt` written) so no
+// workgroup overwrites what another still reads; the recurrent state rows of a
+// head are read and written by that head's workgroup only.
+//
+// Lane structure (fixes the float order): every 128-element reduction is 32
+// lanes x 4 consecutive elements, each lane in element order, then an xor
+// butterfly over the 32 lanes (half a wave).
+// Reference: FM/TrackFastKernels.swift:48-117 (prep), :486-605 (recurrence,
+// peeled Kahan form), FM/TrackFastKernels2.swift:325-352 (gated RMS),
+// FM/TrackFastGDNDecode.swift:50-274 (the fused decode form this follows),
+// FM/TrackFastKernels2.swift:48-58 (logaddexp).
+#include "mtpx_kernels.h"
+
+namespace mtpx {
+
+constexpr int GDN_THREADS = 512;  // 16 half-waves
+constexpr int GDN_D = 128;
+
+// log1p(y), y in [0, 1]: 2 atanh(s), s = y / (2 + y), odd series to s^15.
+__device__ __forceinline__ float log1p_det(float y) {
+  if (y != y) return y;
+  const float t = 2.0f + y;
+  const float s = y / t;
+  const float s2 = s * s;
+  float r = 1.0f / 15.0f;
+  r = 1.0f / 13.0f + s2 * r;
+  r = 1.0f / 11.0f + s2 * r;
+  r = 1.0f / 9.0f + s2 * r;
+  r = 1.0f / 7.0f + s2 * r;
+  r = 1.0f / 5.0f + s2 * r;
+  r = 1.0f / 3.0f + s2 * r;
+  r = s2 * r;
+  const float h = s + s * r;
+  return h + h;
+}
+
+// MLX logaddexp(x, 0) in bf16 arithmetic.
+__device__ __forceinline__ float logaddexp0_bf16(float x) {
+  if (x != x) return x;
+  const float inf = __uint_as_float(0x7f800000u);
+  const float mx = x > 0.0f ? x : 0.0f;
+  const float mn = x < 0.0f ? x : 0.0f;
+  if (mn == -inf || mx == inf) return mx;
+  const float d = round_bf(mn - mx);
+  const float e = round_bf(expf_det(d));
+  const float l = round_bf(log1p_det(e));
+  return round_bf(mx + l);
+}
+
+// MLX Sigmoid in f32.
+__device__ __forceinline__ float sigmoid_f32(float x) {
+  const float e = expf_det(__builtin_fabsf(x));
+  const float y = 1.0f / (1.0f + e);
+  return (x < 0.0f) ? y : 1.0f - y;
+}
+
+__device__ __forceinline__ float half_wave_sum(float v) {
+#pragma unroll
+  for (int off = 16; off >= 1; off /= 2) v = v + __shfl_xor(v, off, 32);
+  return v;
+}
+
+// Row r of the virtual input sequence conv_cur (KC-1 rows) ++ the P committed
+// journal rows ++ the window's projection rows.
+__device__ __forceinline__ float gdn_row(const GdnArgs& a, int r, int ch) {
+  const int KM1 = a.kc - 1;
+  if (r < KM1) return bf2f(a.conv_cur[(size_t)r * a.cd + ch]);
+  r -= KM1;
+  if (r < a.P) return bf2f(a.win_cur[(size_t)r * a.cd + ch]);
+  r -= a.P;
+  return bf2f(a.proj[(size_t)r * a.pw + ch]);
+}
+
+__global__ __launch_bounds__(GDN_THREADS) void k_gdn_step(GdnArgs a) {
+  __shared__ float qs[MAX_TOKENS][GDN_D], ks[MAX_TOKENS][GDN_D], vs[MAX_TOKENS][GDN_D], ys[MAX_TOKENS][GDN_D];
+  __shared__ float dec[MAX_TOKENS], bet[MAX_TOKENS];
+  __shared__ bf16 gated[MAX_TOKENS][GDN_D];
+  __shared__ uint32_t scratch[GDN_THREADS / 32][24];
+  const int h = blockIdx.x, ratio = a.hv / a.hk, hk = h / ratio;
+  const bool lead = (h % ratio) == 0;  // writes the q/k channels' journal and conv rows
+  const int hw = threadIdx.x >> 5, l = threadIdx.x & 31;
+  const int S = a.S, P = a.P, KM1 = a.kc - 1;
+  const float inv_scale = 1.0f / sqrtf((float)GDN_D);
+  const float q_mul = round_bf(inv_scale * inv_scale), k_mul = round_bf(inv_scale);
+
+  // ---- prep: (q, k, v) vectors x positions, 32 lanes x 4 channels each
+  for (int task = hw; task < 3 * S; task += GDN_THREADS / 32) {
+    const int t = task / 3, kind = task % 3;
+    const int vec = kind == 0 ? hk : (kind == 1 ? a.hk + hk : 2 * a.hk + h);
+    float xs[4], acc = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int ch = vec * GDN_D + 4 * l + i;
+      float c = 0.0f;
+      for (int j = 0; j < a.kc; ++j) c = c + gdn_row(a, P + t + j, ch) * bf2f(a.conv_w[(size_t)ch * a.kc + j]);
+      const float x = silu_bf16(round_bf(c));
+      xs[i] = x;
+      acc = __builtin_fmaf(x, x, acc);
+      if (kind == 2 || lead) a.win_nxt[(size_t)t * a.cd + ch] = a.proj[(size_t)t * a.pw + ch];
+    }
+    if (kind < 2) {
+      const float inv = 1.0f / sqrtf(half_wave_sum(acc) / 128.0f + 1e-6f);
+      const float mul = kind == 0 ? q_mul : k_mul;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float val = round_bf(mul * round_bf(xs[i] * inv));
+        if (kind == 0) {
+          qs[t][4 * l + i] = val;
+        } else {
+          ks[t][4 * l + i] = val;
+          if (lead) a.key_nxt[((size_t)t * a.hk + hk) * GDN_D + 4 * l + i] = f2bf(val);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) vs[t][4 * l + i] = xs[i];
+    }
+  }
+  if ((int)threadIdx.x < S) {
+    const int t = threadIdx.x;
+    const bf16* prow = a.proj + (size_t)t * a.pw;
+    const float b = sigmoid_bf16(bf2f(prow[a.b_off + h]));
+    const float ax = round_bf(bf2f(prow[a.a_off + h]) + bf2f(a.dt_bias[h]));
+    const float d = expf_det(a.neg_exp_alog[h] * logaddexp0_bf16(ax));
+    dec[t] = d;
+    bet[t] = b;
+    a.decay_nxt[(size_t)t * a.hv + h] = d;
+  }
+  // the committed conv rows R[P .. P+KC-1) become the next window's base
+  for (int i = threadIdx.x; i < KM1 * 3 * GDN_D; i += GDN_THREADS) {
+    const int j = i / (3 * GDN_D), kind = (i / GDN_D) % 3, d = i % GDN_D;
+    if (kind < 2 && !lead) continue;
+    const int vec = kind == 0 ? hk : (kind == 1 ? a.hk + hk : 2 * a.hk + h);
+    const int ch = vec * GDN_D + d;
+    a.conv_nxt[(size_t)j * a.cd + ch] = f2bf(gdn_row(a, P + j, ch));
+  }
+  __syncthreads();
+
+  // ---- recurrence: 8 value rows per half-wave, lane l owns key elements 4l..4l+3
+  for (int r = hw; r < GDN_D; r += GDN_THREADS / 32) {
+    float* srow = a.ssm + ((size_t)h * GDN_D + r) * GDN_D + 4 * l;
+    const float4 s4 = *reinterpret_cast<const float4*>(srow);
+    float s[4] = {s4.x, s4.y, s4.z, s4.w};
+    for (int p = 0; p < P; ++p) {  // committed steps of the previous window
+      const float gd = a.decay_cur[(size_t)p * a.hv + h];
+      const float dl = a.delta_cur[((size_t)p * a.hv + h) * GDN_D + r];
+      const bf16* kp = a.key_cur + ((size_t)p * a.hk + hk) * GDN_D + 4 * l;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        s[i] = s[i] * gd;
+        s[i] = __builtin_fmaf(bf2f(kp[i]), dl, s[i]);
+      }
+    }
+    if (P > 0) *reinterpret_cast<float4*>(srow) = make_float4(s[0], s[1], s[2], s[3]);
+    for (int t = 0; t < S; ++t) {
+      const float gd = dec[t];
+      const float k0 = ks[t][4 * l], k1 = ks[t][4 * l + 1], k2 = ks[t][4 * l + 2], k3 = ks[t][4 * l + 3];
+      s[0] = s[0] * gd;
+      float kv = 0.0f + s[0] * k0;
+      float comp = 0.0f;
+      {
+        s[1] = s[1] * gd;
+        const float prod = s[1] * k1, corr = prod - comp, next = kv + corr;
+        comp = (next - kv) - corr;
+        kv = next;
+      }
+      {
+        s[2] = s[2] * gd;
+        const float prod = s[2] * k2, corr = prod - comp, next = kv + corr;
+        comp = (next - kv) - corr;
+        kv = next;
+      }
+      {
+        s[3] = s[3] * gd;
+        const float prod = s[3] * k3, corr = prod - comp, next = kv + corr;
+        kv = next;
+      }
+      const float kvm = half_wave_sum(kv);
+      const float delta = (vs[t][r] - kvm) * bet[t];
+      if (l == 0) a.delta_nxt[((size_t)t * a.hv + h) * GDN_D + r] = delta;
+      float o = 0.0f;
+      s[0] = __builtin_fmaf(k0, delta, s[0]);
+      o = __builtin_fmaf(s[0], qs[t][4 * l], o);
+      s[1] = __builtin_fmaf(k1, delta, s[1]);
+      o = __builtin_fmaf(s[1], qs[t][4 * l + 1], o);
+      s[2] = __builtin_fmaf(k2, delta, s[2]);
+      o = __builtin_fmaf(s[2], qs[t][4 * l + 2], o);
+      s[3] = __builtin_fmaf(k3, delta, s[3]);
+      o = __builtin_fmaf(s[3], qs[t][4 * l + 3], o);
+      const float y = half_wave_sum(o);
+      if (l == 0) ys[t][r] = round_bf(y);
+    }
+  }
+  __syncthreads();
+
+  // ---- gated RMS norm per position
+  for (int t = hw; t < S; t += GDN_THREADS / 32) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc = __builtin_fmaf(ys[t][4 * l + i], ys[t][4 * l + i], acc);
+    const float inv = 1.0f / sqrtf(half_wave_sum(acc) / 128.0f + a.eps);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int d = 4 * l + i;
+      const float n = round_bf(bf2f(a.norm_w[d]) * round_bf(ys[t][d] * inv));
+      const float z = bf2f(a.proj[(size_t)t * a.pw + a.z_off + h * GDN_D + d]);
+      const bf16 out = f2bf(sigmoid_f32(z) * n);
+      gated[t][d] = out;
+      if (a.gated) a.gated[(size_t)t * a.hv * GDN_D + h * GDN_D + d] = out;
+    }
+  }
+  __syncthreads();
+
+  // ---- prepared blocks of the gated rows for the output projection (4 per head and position)
+#pragma unroll
+  for (int round = 0; round < 2; ++round) {
+    const int task = hw + round * (GDN_THREADS / 32);
+    const bool act = a.xp && task < 4 * S;
+    const int t = task >> 2, blk = task & 3;
+    int E = 0, sm = 0;
+    if (act) xprep_lanes_build(gated[t][blk * 32 + l], l, scratch[hw], E, sm);
+    __syncthreads();
+    if (act) xprep_lanes_store(l, scratch[hw], E, sm, a.xp + ((size_t)t * a.hv * 4 + h * 4 + blk) * XP_DW);
+    __syncthreads();
+  }
+}
+
+// Committed state without modifying it: the P journal steps replayed onto the
+// state rows into ssm_dst, and the committed conv rows into conv_dst.
+__global__ __launch_bounds__(GDN_THREADS) void k_gdn_replay(GdnArgs a, float* ssm_dst, bf16* conv_dst) {
+  const int h = blockIdx.x, ratio = a.hv / a.hk, hk = h / ratio;
+  const bool lead = (h % ratio) == 0;
+  const int hw = threadIdx.x >> 5, l = threadIdx.x & 31;
+  const int P = a.P, KM1 = a.kc - 1;
+  for (int r = hw; r < GDN_D; r += GDN_THREADS / 32) {
+    const float* srow = a.ssm + ((size_t)h * GDN_D + r) * GDN_D + 4 * l;
+    const float4 s4 = *reinterpret_cast<const float4*>(srow);
+    float s[4] = {s4.x, s4.y, s4.z, s4.w};
+    for (int p = 0; p < P; ++p) {
+      const float gd = a.decay_cur[(size_t)p * a.hv + h];
+      const float dl = a.delta_cur[((size_t)p * a.hv + h) * GDN_D + r];
+      const bf16* kp = a.key_cur + ((size_t)p * a.hk + hk) * GDN_D + 4 * l;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        s[i] = s[i] * gd;
+        s[i] = __builtin_fmaf(bf2f(kp[i]), dl, s[i]);
+      }
+    }
+    *reinterpret_cast<float4*>(ssm_dst + ((size_t)h * GDN_D + r) * GDN_D + 4 * l) = make_float4(s[0], s[1], s[2], s[3]);
+  }
+  for (int i = threadIdx.x; i < KM1 * 3 * GDN_D; i += GDN_THREADS) {
+    const int j = i / (3 * GDN_D), kind = (i / GDN_D) % 3, d = i % GDN_D;
+    if (kind < 2 && !lead) continue;
+    const int vec = kind == 0 ? hk : (kind == 1 ? a.hk + hk : 2 * a.hk + h);
+    const int ch = vec * GDN_D + d;
+    conv_dst[(size_t)j * a.cd + ch] = f2bf(gdn_row(a, P + j, ch));
+  }
+}
+
+hipError_t launch_gdn_step(const GdnArgs& a, hipStream_t st) {
+  hipLaunchKernelGGL(k_gdn_step, dim3(a.hv), dim3(GDN_THREADS), 0, st, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_gdn_replay(const GdnArgs& a, float* ssm_dst, bf16* conv_dst, hipStream_t st) {
+  hipLaunchKernelGGL(k_gdn_replay, dim3(a.hv), dim3(GDN_THREADS), 0, st, a, ssm_dst, conv_dst);
+  return hipGetLastError();
+}
+
+}  // namespace mtpx

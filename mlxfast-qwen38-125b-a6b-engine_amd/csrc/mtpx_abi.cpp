@@ -686,6 +686,119 @@ struct DrafterObj {
 
 }  // namespace
 
+// ---------------------------------------------------------------------------
+// Gated-deltanet sublayer (gdn.hip).
+namespace {
+
+struct GdnGeom {
+  int hk, hv, kc, cd, pw, z_off, b_off, a_off;
+};
+
+GdnGeom gdn_geom(const mtpx_gdn_config& g) {
+  GdnGeom r;
+  r.hk = g.key_heads;
+  r.hv = g.value_heads;
+  r.kc = g.conv_kernel;
+  r.cd = (2 * g.key_heads + g.value_heads) * 128;
+  r.z_off = r.cd;
+  r.b_off = r.cd + g.value_heads * 128;
+  r.a_off = r.b_off + g.value_heads;
+  r.pw = r.a_off + g.value_heads;
+  return r;
+}
+
+int gdn_check(const mtpx_gdn_config* g) {
+  ARG(g, "null config");
+  ARG(gs_ok(g->group_size), "group_size=%d", g->group_size);
+  ARG(g->hidden >= 32 && k_ok(g->hidden, g->group_size), "hidden=%d unsupported", g->hidden);
+  ARG(g->key_heads >= 1 && g->value_heads >= g->key_heads && g->value_heads % g->key_heads == 0 &&
+          g->value_heads <= 256,
+      "key_heads=%d value_heads=%d", g->key_heads, g->value_heads);
+  ARG(k_ok(g->value_heads * 128, g->group_size), "value_heads*128=%d unsupported GEMV depth", g->value_heads * 128);
+  ARG(g->conv_kernel >= 2 && g->conv_kernel <= 8, "conv_kernel=%d", g->conv_kernel);
+  ARG(g->eps > 0.0f, "eps must be positive");
+  return MTPX_OK;
+}
+
+struct GdnLayer {
+  mtpx_gdn_config cfg;
+  mtpx_gdn_weights w;
+  std::vector<void*> allocs;
+};
+
+struct GdnState {
+  mtpx_gdn_config cfg;
+  uint16_t* conv[2] = {nullptr, nullptr};  // conv base per slot [kc-1, cd]
+  uint16_t* win[2] = {nullptr, nullptr};   // window conv input rows [MAX_TOKENS, cd]
+  uint16_t* key[2] = {nullptr, nullptr};   // [MAX_TOKENS, hk, 128]
+  float* delta[2] = {nullptr, nullptr};    // [MAX_TOKENS, hv, 128]
+  float* decay[2] = {nullptr, nullptr};    // [MAX_TOKENS, hv]
+  float* ssm = nullptr;                    // [hv, 128, 128]
+  int cur = 0, window = 0, committed = 0;
+  std::vector<void*> allocs;
+};
+
+// splitmix64 -> uniform [0, 1): host-side values of the small per-head vectors
+double host_uniform(uint64_t& s) {
+  uint64_t z = (s += 0x9e3779b97f4a7c15ull);
+  z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+  z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+  z ^= z >> 31;
+  return (double)(z >> 11) * (1.0 / 9007199254740992.0);
+}
+
+GdnArgs gdn_args(GdnState* st, const GdnLayer* L, const uint16_t* proj, int S, uint16_t* gated, uint32_t* xp) {
+  const GdnGeom g = gdn_geom(st->cfg);
+  GdnArgs a;
+  a.hk = g.hk;
+  a.hv = g.hv;
+  a.kc = g.kc;
+  a.cd = g.cd;
+  a.pw = g.pw;
+  a.z_off = g.z_off;
+  a.b_off = g.b_off;
+  a.a_off = g.a_off;
+  a.S = S;
+  a.P = st->committed;
+  a.eps = st->cfg.eps;
+  a.proj = reinterpret_cast<const bf16*>(proj);
+  a.conv_w = L ? reinterpret_cast<const bf16*>(L->w.conv_w) : nullptr;
+  a.neg_exp_alog = L ? L->w.neg_exp_alog : nullptr;
+  a.dt_bias = L ? reinterpret_cast<const bf16*>(L->w.dt_bias) : nullptr;
+  a.norm_w = L ? reinterpret_cast<const bf16*>(L->w.norm_w) : nullptr;
+  const int c = st->cur, n = st->cur ^ 1;
+  a.conv_cur = reinterpret_cast<const bf16*>(st->conv[c]);
+  a.win_cur = reinterpret_cast<const bf16*>(st->win[c]);
+  a.key_cur = reinterpret_cast<const bf16*>(st->key[c]);
+  a.delta_cur = st->delta[c];
+  a.decay_cur = st->decay[c];
+  a.conv_nxt = reinterpret_cast<bf16*>(st->conv[n]);
+  a.win_nxt = reinterpret_cast<bf16*>(st->win[n]);
+  a.key_nxt = reinterpret_cast<bf16*>(st->key[n]);
+  a.delta_nxt = st->delta[n];
+  a.decay_nxt = st->decay[n];
+  a.ssm = st->ssm;
+  a.gated = reinterpret_cast<bf16*>(gated);
+  a.xp = xp;
+  return a;
+}
+
+bool gdn_same(const mtpx_gdn_config& a, const mtpx_gdn_config& b) {
+  return a.key_heads == b.key_heads && a.value_heads == b.value_heads && a.conv_kernel == b.conv_kernel;
+}
+
+// one window through the core; the state's slots advance
+int gdn_enqueue(Ctx* c, const GdnLayer* L, GdnState* st, const uint16_t* proj, int S, uint16_t* gated, uint32_t* xp) {
+  const GdnArgs a = gdn_args(st, L, proj, S, gated, xp);
+  LAUNCH(c, "gdn_step", launch_gdn_step(a, c->stream));
+  st->cur ^= 1;
+  st->window = S;
+  st->committed = 0;
+  return MTPX_OK;
+}
+
+}  // namespace
+
 extern "C" {
 
 const char* mtpx_last_error(void) { return g_err.c_str(); }
@@ -1045,6 +1158,196 @@ int mtpx_layer_forward(mtpx_ctx h, mtpx_layer lh, mtpx_kv kvh, const uint16_t* x
   LAUNCH(c, "rmsnorm", launch_rmsnorm(x, o, M, H, L->w.post_norm, g.eps, s, h2, xp2, st));
   if ((rc = moe_enqueue(c, &L->w.moe, h2, M, h1, nullptr, nullptr, nullptr, s, y, xp2))) return rc;
   kv->offset += M;
+  return MTPX_OK;
+}
+
+
+int mtpx_gdn_new_random(mtpx_ctx h, const mtpx_gdn_config* cfg, uint64_t seed, mtpx_gdn* out) {
+  Ctx* c = C(h);
+  ARG(c && cfg && out, "null argument");
+  int rc = gdn_check(cfg);
+  if (rc) return rc;
+  if (set_device(c)) return MTPX_ERR_HIP;
+  const GdnGeom g = gdn_geom(*cfg);
+  GdnLayer* L = new GdnLayer();
+  L->cfg = *cfg;
+  RandInit ri{c, seed, cfg->group_size, &L->allocs};
+  ri.qmat(g.pw, cfg->hidden, &L->w.in_proj);
+  ri.qmat(cfg->hidden, g.hv * 128, &L->w.out_proj);
+  L->w.conv_w = ri.dense((int64_t)g.cd * g.kc, 0.3f);
+  // A_log = log U(1, 16); dt = U(0.001, 0.1) with dt_bias its softplus inverse; norm weight ~ 1
+  uint64_t hs = seed ^ 0x6a09e667f3bcc908ull;
+  std::vector<float> nea(g.hv);
+  std::vector<uint16_t> dtb(g.hv), nw(128);
+  for (int i = 0; i < g.hv; ++i) {
+    nea[i] = (float)(-(1.0 + 15.0 * host_uniform(hs)));
+    const double dt = 0.001 + 0.099 * host_uniform(hs);
+    dtb[i] = bf16_bits((float)std::log(std::expm1(dt)));
+  }
+  for (int i = 0; i < 128; ++i) nw[i] = bf16_bits((float)(0.9 + 0.2 * host_uniform(hs)));
+  float* pn = (float*)ri.alloc(4 * (size_t)g.hv);
+  uint16_t* pd = (uint16_t*)ri.alloc(2 * (size_t)g.hv);
+  uint16_t* pw = (uint16_t*)ri.alloc(2 * 128);
+  if (pn && pd && pw &&
+      (hipMemcpy(pn, nea.data(), 4 * (size_t)g.hv, hipMemcpyHostToDevice) != hipSuccess ||
+       hipMemcpy(pd, dtb.data(), 2 * (size_t)g.hv, hipMemcpyHostToDevice) != hipSuccess ||
+       hipMemcpy(pw, nw.data(), 2 * 128, hipMemcpyHostToDevice) != hipSuccess))
+    ri.ok = false;
+  L->w.neg_exp_alog = pn;
+  L->w.dt_bias = pd;
+  L->w.norm_w = pw;
+  if ((rc = ri.finish("gdn"))) {
+    for (void* p : L->allocs) hipFree(p);
+    delete L;
+    return rc;
+  }
+  out->ctx = L;
+  return MTPX_OK;
+}
+
+int mtpx_gdn_free(mtpx_gdn gh) {
+  GdnLayer* L = static_cast<GdnLayer*>(gh.ctx);
+  if (!L) return MTPX_OK;
+  for (void* p : L->allocs) hipFree(p);
+  delete L;
+  return MTPX_OK;
+}
+
+int mtpx_gdn_weights_get(mtpx_gdn gh, mtpx_gdn_weights* out) {
+  GdnLayer* L = static_cast<GdnLayer*>(gh.ctx);
+  ARG(L && out, "null argument");
+  *out = L->w;
+  return MTPX_OK;
+}
+
+int mtpx_gdn_state_new(mtpx_ctx h, const mtpx_gdn_config* cfg, mtpx_gdn_state* out) {
+  Ctx* c = C(h);
+  ARG(c && cfg && out, "null argument");
+  int rc = gdn_check(cfg);
+  if (rc) return rc;
+  if (set_device(c)) return MTPX_ERR_HIP;
+  const GdnGeom g = gdn_geom(*cfg);
+  GdnState* st = new GdnState();
+  st->cfg = *cfg;
+  bool ok = true;
+  auto take = [&](size_t bytes) -> void* {
+    void* p = nullptr;
+    if (hipMalloc(&p, bytes) != hipSuccess) {
+      ok = false;
+      return nullptr;
+    }
+    st->allocs.push_back(p);
+    return p;
+  };
+  for (int s = 0; s < 2; ++s) {
+    st->conv[s] = (uint16_t*)take(2 * (size_t)(g.kc - 1) * g.cd);
+    st->win[s] = (uint16_t*)take(2 * (size_t)MAX_TOKENS * g.cd);
+    st->key[s] = (uint16_t*)take(2 * (size_t)MAX_TOKENS * g.hk * 128);
+    st->delta[s] = (float*)take(4 * (size_t)MAX_TOKENS * g.hv * 128);
+    st->decay[s] = (float*)take(4 * (size_t)MAX_TOKENS * g.hv);
+  }
+  st->ssm = (float*)take(4 * (size_t)g.hv * 128 * 128);
+  if (ok) {
+    for (int s = 0; s < 2; ++s)
+      if (hipMemsetAsync(st->conv[s], 0, 2 * (size_t)(g.kc - 1) * g.cd, c->stream) != hipSuccess) ok = false;
+    if (hipMemsetAsync(st->ssm, 0, 4 * (size_t)g.hv * 128 * 128, c->stream) != hipSuccess) ok = false;
+    if (hipStreamSynchronize(c->stream) != hipSuccess) ok = false;
+  }
+  if (!ok) {
+    for (void* p : st->allocs) hipFree(p);
+    delete st;
+    return fail(MTPX_ERR_OOM, "gdn state allocation failed");
+  }
+  out->ctx = st;
+  return MTPX_OK;
+}
+
+int mtpx_gdn_state_free(mtpx_gdn_state sh) {
+  GdnState* st = static_cast<GdnState*>(sh.ctx);
+  if (!st) return MTPX_OK;
+  for (void* p : st->allocs) hipFree(p);
+  delete st;
+  return MTPX_OK;
+}
+
+int mtpx_gdn_state_load(mtpx_ctx h, mtpx_gdn_state sh, const uint16_t* conv, const float* ssm) {
+  Ctx* c = C(h);
+  GdnState* st = static_cast<GdnState*>(sh.ctx);
+  ARG(c && st && conv && ssm, "null argument");
+  if (set_device(c)) return MTPX_ERR_HIP;
+  const GdnGeom g = gdn_geom(st->cfg);
+  HIP_OK(hipMemcpyAsync(st->conv[st->cur], conv, 2 * (size_t)(g.kc - 1) * g.cd, hipMemcpyDeviceToDevice, c->stream));
+  HIP_OK(hipMemcpyAsync(st->ssm, ssm, 4 * (size_t)g.hv * 128 * 128, hipMemcpyDeviceToDevice, c->stream));
+  st->window = 0;
+  st->committed = 0;
+  return MTPX_OK;
+}
+
+int mtpx_gdn_state_store(mtpx_ctx h, mtpx_gdn_state sh, uint16_t* conv, float* ssm) {
+  Ctx* c = C(h);
+  GdnState* st = static_cast<GdnState*>(sh.ctx);
+  ARG(c && st && conv && ssm, "null argument");
+  if (set_device(c)) return MTPX_ERR_HIP;
+  const GdnArgs a = gdn_args(st, nullptr, nullptr, 0, nullptr, nullptr);
+  LAUNCH(c, "gdn_replay", launch_gdn_replay(a, ssm, reinterpret_cast<bf16*>(conv), c->stream));
+  return MTPX_OK;
+}
+
+int mtpx_gdn_commit(mtpx_gdn_state sh, int n) {
+  GdnState* st = static_cast<GdnState*>(sh.ctx);
+  ARG(st, "null state");
+  if (n < 0 || n > st->window)
+    return fail(MTPX_ERR_STATE, "commit of %d positions; the last window has %d", n, st->window);
+  st->committed = n;
+  return MTPX_OK;
+}
+
+int mtpx_gdn_state_info(mtpx_gdn_state sh, int* window, int* committed) {
+  GdnState* st = static_cast<GdnState*>(sh.ctx);
+  ARG(st, "null state");
+  if (window) *window = st->window;
+  if (committed) *committed = st->committed;
+  return MTPX_OK;
+}
+
+int mtpx_gdn_core(mtpx_ctx h, mtpx_gdn gh, mtpx_gdn_state sh, const uint16_t* proj, int S, uint16_t* gated) {
+  Ctx* c = C(h);
+  GdnLayer* L = static_cast<GdnLayer*>(gh.ctx);
+  GdnState* st = static_cast<GdnState*>(sh.ctx);
+  ARG(c && L && st && proj && gated, "null argument");
+  ARG(S >= 1 && S <= MAX_TOKENS, "S=%d", S);
+  ARG(gdn_same(L->cfg, st->cfg), "state geometry does not match the layer");
+  if (set_device(c)) return MTPX_ERR_HIP;
+  return gdn_enqueue(c, L, st, proj, S, gated, nullptr);
+}
+
+int mtpx_gdn_forward(mtpx_ctx h, mtpx_gdn gh, mtpx_gdn_state sh, const uint16_t* x, int S, uint16_t* y,
+                     uint16_t* gated) {
+  Ctx* c = C(h);
+  GdnLayer* L = static_cast<GdnLayer*>(gh.ctx);
+  GdnState* st = static_cast<GdnState*>(sh.ctx);
+  ARG(c && L && st && x && y, "null argument");
+  ARG(S >= 1 && S <= MAX_TOKENS, "S=%d", S);
+  ARG(gdn_same(L->cfg, st->cfg), "state geometry does not match the layer");
+  if (set_device(c)) return MTPX_ERR_HIP;
+  const mtpx_gdn_config& cfg = L->cfg;
+  const GdnGeom g = gdn_geom(cfg);
+  const int H = cfg.hidden, VD = g.hv * 128, gs = cfg.group_size;
+  const size_t xin = (size_t)S * (H / 32) * XP_DW, xout = (size_t)S * (VD / 32) * XP_DW;
+  int rc = ws_reserve(c, al(xin * 4) + al(2 * (size_t)S * g.pw) + al(xout * 4) + 1024);
+  if (rc) return rc;
+  c->ws_used = 0;
+  uint32_t* xp = ws_take<uint32_t>(c, xin);
+  uint16_t* proj = ws_take<uint16_t>(c, (size_t)S * g.pw);
+  uint32_t* xp2 = ws_take<uint32_t>(c, xout);
+  const mtpx_q4& ip = L->w.in_proj;
+  const mtpx_q4& op = L->w.out_proj;
+  LAUNCH(c, "xprep", launch_xprep(reinterpret_cast<const bf16*>(x), S, H, xp, c->stream));
+  LAUNCH(c, "qmv_gdn_in", launch_qmv(ip.w, reinterpret_cast<const bf16*>(ip.s), reinterpret_cast<const bf16*>(ip.b), ip.sb,
+                                      g.pw, H, gs, xp, S, reinterpret_cast<bf16*>(proj), nullptr, c->stream));
+  if ((rc = gdn_enqueue(c, L, st, proj, S, gated, xp2))) return rc;
+  LAUNCH(c, "qmv_gdn_out", launch_qmv(op.w, reinterpret_cast<const bf16*>(op.s), reinterpret_cast<const bf16*>(op.b),
+                                       op.sb, H, VD, gs, xp2, S, reinterpret_cast<bf16*>(y), nullptr, c->stream));
   return MTPX_OK;
 }
 

@@ -122,4 +122,28 @@ hipError_t launch_silu_xprep(const bf16* lo, int S, int LW, bf16* act, uint32_t*
 hipError_t launch_hc_mix(const bf16* w, const bf16* normed, const bf16* inj, int S, int hc, int H, bf16* input,
                          bf16* inject_out, uint32_t* xp, hipStream_t st);
 
+// --- gated-deltanet sublayer core (gdn.hip); head dims 128
+struct GdnArgs {
+  int hk, hv, kc, cd, pw, z_off, b_off, a_off;  // key/value heads, conv taps, conv channels, projection row layout
+  int S, P;                                     // window positions; committed steps of the previous window
+  float eps;                                    // gated RMS epsilon
+  const bf16* proj;                             // [S, pw]: qkv | z | b | a
+  const bf16* conv_w;                           // [cd, kc]
+  const float* neg_exp_alog;                    // [hv]: -exp(A_log)
+  const bf16* dt_bias;                          // [hv]
+  const bf16* norm_w;                           // [128]
+  const bf16* conv_cur;                         // [kc-1, cd] conv base of the previous window
+  const bf16* win_cur;                          // [*, cd]  previous window's conv input rows
+  const bf16* key_cur;                          // [*, hk, 128]
+  const float* delta_cur;                       // [*, hv, 128]
+  const float* decay_cur;                       // [*, hv]
+  bf16 *conv_nxt, *win_nxt, *key_nxt;           // this window's journal (same shapes)
+  float *delta_nxt, *decay_nxt;
+  float* ssm;                                   // [hv, 128, 128] committed recurrent state (in place)
+  bf16* gated;                                  // [S, hv*128] or null
+  uint32_t* xp;                                 // [S, hv*4, XP_DW] prepared gated rows or null
+};
+hipError_t launch_gdn_step(const GdnArgs& a, hipStream_t st);
+hipError_t launch_gdn_replay(const GdnArgs& a, float* ssm_dst, bf16* conv_dst, hipStream_t st);
+
 }  // namespace mtpx

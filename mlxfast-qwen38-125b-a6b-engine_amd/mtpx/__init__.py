@@ -11,11 +11,11 @@ from __future__ import annotations
 import ctypes as C
 
 from . import _lib
-from ._lib import (DrafterInfo, Handle, HCWeights, HeadConfig, HeadWeights, LayerConfig, LayerWeights, MoEWeights,
-                   MtpxError, Q4, check)
+from ._lib import (DrafterInfo, GDNConfig, GDNWeights, Handle, HCWeights, HeadConfig, HeadWeights, LayerConfig,
+                   LayerWeights, MoEWeights, MtpxError, Q4, check)
 
-__all__ = ["Context", "KVCache", "DecoderLayer", "MTPHead", "Drafter", "MoEWeights", "LayerConfig", "HeadConfig", "MtpxError",
-           "moe_weights_from"]
+__all__ = ["Context", "KVCache", "DecoderLayer", "MTPHead", "Drafter", "GDN", "GDNState", "MoEWeights", "LayerConfig",
+           "HeadConfig", "GDNConfig", "MtpxError", "moe_weights_from"]
 
 
 def _ptr(t):
@@ -312,6 +312,75 @@ class Drafter:
         v = C.c_int64()
         check(self.ctx.lib.mtpx_drafter_bytes_per_token(self.head.h, C.byref(v)), "drafter_bytes_per_token")
         return v.value
+
+
+class GDN:
+    """A gated-deltanet sublayer with seeded random weights (mtpx_gdn)."""
+
+    def __init__(self, ctx: Context, cfg: GDNConfig, seed: int):
+        self.ctx = ctx
+        self.cfg = cfg
+        self.h = Handle()
+        check(ctx.lib.mtpx_gdn_new_random(ctx.h, C.byref(cfg), seed, C.byref(self.h)), "gdn_new_random")
+
+    def close(self):
+        if self.h.ctx:
+            self.ctx.lib.mtpx_gdn_free(self.h)
+            self.h.ctx = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def weights(self) -> GDNWeights:
+        w = GDNWeights()
+        check(self.ctx.lib.mtpx_gdn_weights_get(self.h, C.byref(w)), "gdn_weights_get")
+        return w
+
+    def core(self, state: "GDNState", proj, gated):
+        check(self.ctx.lib.mtpx_gdn_core(self.ctx.h, self.h, state.h, _ptr(proj), proj.shape[0], _ptr(gated)),
+              "gdn_core")
+
+    def forward(self, state: "GDNState", x, y, gated=None):
+        check(self.ctx.lib.mtpx_gdn_forward(self.ctx.h, self.h, state.h, _ptr(x), x.shape[0], _ptr(y), _ptr(gated)),
+              "gdn_forward")
+
+
+class GDNState:
+    """Committed conv rows + recurrent state of one GDN layer for one request, with the
+    journal of the last window (mtpx_gdn_state)."""
+
+    def __init__(self, ctx: Context, cfg: GDNConfig):
+        self.ctx = ctx
+        self.h = Handle()
+        check(ctx.lib.mtpx_gdn_state_new(ctx.h, C.byref(cfg), C.byref(self.h)), "gdn_state_new")
+
+    def close(self):
+        if self.h.ctx:
+            self.ctx.lib.mtpx_gdn_state_free(self.h)
+            self.h.ctx = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def load(self, conv, ssm):
+        check(self.ctx.lib.mtpx_gdn_state_load(self.ctx.h, self.h, _ptr(conv), _ptr(ssm)), "gdn_state_load")
+
+    def store(self, conv, ssm):
+        check(self.ctx.lib.mtpx_gdn_state_store(self.ctx.h, self.h, _ptr(conv), _ptr(ssm)), "gdn_state_store")
+
+    def commit(self, n: int):
+        check(self.ctx.lib.mtpx_gdn_commit(self.h, n), "gdn_commit")
+
+    def info(self):
+        w, c = C.c_int(), C.c_int()
+        check(self.ctx.lib.mtpx_gdn_state_info(self.h, C.byref(w), C.byref(c)), "gdn_state_info")
+        return w.value, c.value
 
 
 def moe_weights_from(tensors: dict, H, E, K, F, gs) -> MoEWeights:

@@ -69,6 +69,16 @@ class DrafterInfo(C.Structure):
         (n, INT) for n in ("round_in_flight", "round_draft_steps", "has_frontier", "released")]
 
 
+class GDNConfig(C.Structure):
+    _fields_ = [("hidden", INT), ("key_heads", INT), ("value_heads", INT), ("conv_kernel", INT),
+                ("group_size", INT), ("eps", C.c_float)]
+
+
+class GDNWeights(C.Structure):
+    _fields_ = [("in_proj", Q4), ("conv_w", P), ("neg_exp_alog", P), ("dt_bias", P), ("norm_w", P),
+                ("out_proj", Q4)]
+
+
 _SIGS = {
     "mtpx_last_error": (C.c_char_p, []),
     "mtpx_version": (C.c_char_p, []),
@@ -114,6 +124,17 @@ _SIGS = {
     "mtpx_drafter_release": (INT, [Handle]),
     "mtpx_drafter_info_get": (INT, [Handle, C.POINTER(DrafterInfo)]),
     "mtpx_drafter_bytes_per_token": (INT, [Handle, C.POINTER(I64)]),
+    "mtpx_gdn_new_random": (INT, [Handle, C.POINTER(GDNConfig), U64, C.POINTER(Handle)]),
+    "mtpx_gdn_free": (INT, [Handle]),
+    "mtpx_gdn_weights_get": (INT, [Handle, C.POINTER(GDNWeights)]),
+    "mtpx_gdn_state_new": (INT, [Handle, C.POINTER(GDNConfig), C.POINTER(Handle)]),
+    "mtpx_gdn_state_free": (INT, [Handle]),
+    "mtpx_gdn_state_load": (INT, [Handle, Handle, P, P]),
+    "mtpx_gdn_state_store": (INT, [Handle, Handle, P, P]),
+    "mtpx_gdn_commit": (INT, [Handle, INT]),
+    "mtpx_gdn_state_info": (INT, [Handle, C.POINTER(INT), C.POINTER(INT)]),
+    "mtpx_gdn_core": (INT, [Handle, Handle, Handle, P, INT, P]),
+    "mtpx_gdn_forward": (INT, [Handle, Handle, Handle, P, INT, P, P]),
     "mtpx_profile_enable": (INT, [Handle, INT]),
     "mtpx_profile_reset": (INT, [Handle]),
     "mtpx_profile_dump": (INT, [Handle, C.c_char_p, C.c_size_t]),

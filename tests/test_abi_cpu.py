@@ -49,6 +49,8 @@ def test_struct_layouts_match_c_compiler(tmp_path):
         "mtpx_drafter_info": (_lib.DrafterInfo, ["round_base_offset", "round_in_flight", "released"]),
         "mtpx_head_weights": (_lib.HeadWeights, ["pre_norm_hidden", "attn_hc", "final_hc", "layer", "shortlist",
                                                  "shortlist_ids", "shortlist_rows"]),
+        "mtpx_gdn_config": (_lib.GDNConfig, ["value_heads", "group_size", "eps"]),
+        "mtpx_gdn_weights": (_lib.GDNWeights, ["conv_w", "neg_exp_alog", "norm_w", "out_proj"]),
     }
     lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "mtpx.h"', "int main(void) {"]
     for name, (_, fields) in checks.items():

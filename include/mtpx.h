@@ -374,6 +374,66 @@ int mtpx_gdn_core(mtpx_ctx ctx, mtpx_gdn gdn, mtpx_gdn_state st, const uint16_t*
 int mtpx_gdn_forward(mtpx_ctx ctx, mtpx_gdn gdn, mtpx_gdn_state st, const uint16_t* x, int S,
                      uint16_t* y, uint16_t* gated);
 
+/* ---- a20: the target's verify forward ------------------------------------------------------
+ * cbv2ForwardWithHiddenCaptured (Runner/FastModel/TrackFastModel.swift:1463-1475) over
+ * fastStreams (:1165-1265):  residual = embed(ids);  per layer
+ *   (stream, n) = hc_norm(residual + out * inject)   (the first layer: the embedding tiled)
+ *   (x, j) = mix(attn_hc, n);   a = gdn(x), or attention(x) on every interval-th layer
+ *   (stream, n) = hc_norm(stream + a * j);   (x, j) = mix(mlp_hc, n);   out = MoE(x)
+ * then (multi, n) = hc_norm(residual + out * inject) with the final mixer, mixed = mix(final, n)
+ * and logits = lm_head(mixed) (:1330-1333).  A verify leaves the committed state alone:
+ * attention caches rewind to it and GDN states keep a journal; mtpx_target_commit(n) keeps the
+ * window's first n positions.  The PLE n-gram block of layer 1 (:1188-1200) is not part of
+ * this forward. */
+#define MTPX_LAYER_GDN 0
+#define MTPX_LAYER_ATTENTION 1
+typedef struct mtpx_target_ { void* ctx; } mtpx_target;
+typedef struct mtpx_target_state_ { void* ctx; } mtpx_target_state;
+
+typedef struct {
+  mtpx_layer_config layer;       /* attention and MoE dims, group size, eps, max_positions */
+  int key_heads, value_heads;    /* GDN heads (dims 128) */
+  int conv_kernel;               /* GDN conv taps */
+  int num_layers;                /* 48 */
+  int full_attention_interval;   /* 4: layer i is attention iff (i + 1) % interval == 0 */
+  int hc, lowrank;               /* hyper-connection streams (4), mixer rank (320) */
+  int64_t vocab;                 /* 248320 */
+} mtpx_target_config;
+
+typedef struct {
+  int kind;                      /* MTPX_LAYER_GDN or MTPX_LAYER_ATTENTION */
+  mtpx_layer_weights attn;       /* attention weights (attention layers) and the layer's MoE */
+  mtpx_gdn_weights gdn;          /* GDN layers */
+  mtpx_hc_weights attn_hc, mlp_hc;
+} mtpx_target_layer_weights;
+
+typedef struct {
+  mtpx_q4 embed;                 /* [vocab, hidden] */
+  mtpx_hc_weights final_hc;      /* no inject */
+  mtpx_q4 lm_head;               /* [vocab, hidden] */
+} mtpx_target_weights;
+
+int mtpx_target_new_random(mtpx_ctx ctx, const mtpx_target_config* cfg, uint64_t seed, mtpx_target* out);
+int mtpx_target_free(mtpx_target t);
+int mtpx_target_weights_get(mtpx_target t, mtpx_target_weights* out);
+int mtpx_target_layer_weights_get(mtpx_target t, int layer, mtpx_target_layer_weights* out);
+/* Per-request caches (Qwen4ExpCBv2LayerCache per attention layer, recurrent state per GDN
+ * layer): empty attention caches of max_positions, zero GDN states. */
+int mtpx_target_state_new(mtpx_ctx ctx, mtpx_target t, mtpx_target_state* out);
+int mtpx_target_state_free(mtpx_target_state st);
+/* The cache of attention layer `layer` / the state of GDN layer `layer` (owned by st). */
+int mtpx_target_state_kv(mtpx_target_state st, int layer, mtpx_kv* out);
+int mtpx_target_state_gdn(mtpx_target_state st, int layer, mtpx_gdn_state* out);
+/* Committed positions of every attention cache (a prefix written through mtpx_kv_buffers). */
+int mtpx_target_state_set_offset(mtpx_target_state st, int64_t offset);
+int mtpx_target_state_info(mtpx_target_state st, int64_t* offset, int* window);
+/* S <= 8 tokens (device int32) at the committed offset -> logits bf16 [S, vocab], multi bf16
+ * [S, hc*hidden], mixed bf16 [S, hidden] (each may be NULL). */
+int mtpx_target_verify(mtpx_ctx ctx, mtpx_target t, mtpx_target_state st, const int32_t* ids, int S,
+                       uint16_t* logits, uint16_t* multi, uint16_t* mixed);
+/* The first n (0..window) positions of the last verify become committed. */
+int mtpx_target_commit(mtpx_target_state st, int n);
+
 /* ---- per-kernel timing (replaces TrackFastProfile, Runner/FastModel/TrackFastWeights.swift:81-98) ----
  * With profiling on, every launch the library issues is bracketed by HIP events
  * on the context stream.  mtpx_profile_dump synchronises and writes one line per

@@ -3,6 +3,7 @@
 // kernels and fails with an error code when it cannot.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -340,6 +341,25 @@ int layer_check(const mtpx_layer_config* cfg) {
   return MTPX_OK;
 }
 
+// MoE weights of one layer (random init): bf16 router and shared gate row, q4 experts.
+void moe_random(RandInit& ri, const mtpx_layer_config* cfg, mtpx_moe_weights* mw) {
+  const int H = cfg->hidden, E = cfg->experts, F = cfg->expert_width;
+  mtpx_moe_weights& m = *mw;
+  m.hidden = H;
+  m.experts = E;
+  m.top_k = cfg->top_k;
+  m.expert_width = F;
+  m.group_size = cfg->group_size;
+  m.router = ri.dense((int64_t)E * H, 0.02f);
+  m.shared_gate = ri.dense(H, 0.02f);
+  ri.qmat((int64_t)E * F, H, &m.gate_w, &m.gate_s, &m.gate_b, &m.gate_sb);
+  ri.qmat((int64_t)E * F, H, &m.up_w, &m.up_s, &m.up_b, &m.up_sb);
+  ri.qmat((int64_t)E * H, F, &m.down_w, &m.down_s, &m.down_b, &m.down_sb);
+  ri.qmat(F, H, &m.sh_gate_w, &m.sh_gate_s, &m.sh_gate_b, &m.sh_gate_sb);
+  ri.qmat(F, H, &m.sh_up_w, &m.sh_up_s, &m.sh_up_b, &m.sh_up_sb);
+  ri.qmat(H, F, &m.sh_down_w, &m.sh_down_s, &m.sh_down_b, &m.sh_down_sb);
+}
+
 // Attention + MoE weights of one decoder layer (random init), RoPE tables from the host.
 int layer_create(Ctx* c, const mtpx_layer_config* cfg, uint64_t seed, Layer** out) {
   int rc = layer_check(cfg);
@@ -359,20 +379,7 @@ int layer_create(Ctx* c, const mtpx_layer_config* cfg, uint64_t seed, Layer** ou
   L->w.k_norm = ri.dense(D, 0.0f);
   ri.qmat(QW, H, &L->w.qkv_w, &L->w.qkv_s, &L->w.qkv_b, &L->w.qkv_sb);
   ri.qmat(H, HQ * D, &L->w.o_w, &L->w.o_s, &L->w.o_b, &L->w.o_sb);
-  mtpx_moe_weights& m = L->w.moe;
-  m.hidden = H;
-  m.experts = E;
-  m.top_k = cfg->top_k;
-  m.expert_width = F;
-  m.group_size = gs;
-  m.router = ri.dense((int64_t)E * H, 0.02f);
-  m.shared_gate = ri.dense(H, 0.02f);
-  ri.qmat((int64_t)E * F, H, &m.gate_w, &m.gate_s, &m.gate_b, &m.gate_sb);
-  ri.qmat((int64_t)E * F, H, &m.up_w, &m.up_s, &m.up_b, &m.up_sb);
-  ri.qmat((int64_t)E * H, F, &m.down_w, &m.down_s, &m.down_b, &m.down_sb);
-  ri.qmat(F, H, &m.sh_gate_w, &m.sh_gate_s, &m.sh_gate_b, &m.sh_gate_sb);
-  ri.qmat(F, H, &m.sh_up_w, &m.sh_up_s, &m.sh_up_b, &m.sh_up_sb);
-  ri.qmat(H, F, &m.sh_down_w, &m.sh_down_s, &m.sh_down_b, &m.sh_down_sb);
+  moe_random(ri, cfg, &L->w.moe);
   // rotate-half RoPE tables: entry d uses theta^(-2*(d mod rot/2)/rot)
   const int rot = cfg->rot_dims;
   std::vector<uint16_t> ct((size_t)cfg->max_positions * rot), st((size_t)cfg->max_positions * rot);
@@ -483,10 +490,13 @@ size_t head_ws_bytes(const Head* hd, int S, int T) {
 // One hyper-connection mixer over the normed rows (prepared blocks in xpW):
 // lo = down n, inj = inject n, act = silu(lo), w = up act,
 // x = sum_c sigmoid(w) * n (+ its prepared blocks in xpH), j = 2 * sigmoid(inj).
-int hc_mix_enqueue(Ctx* c, const Head* hd, const mtpx_hc_weights* hw, const uint16_t* normed, const uint32_t* xpW,
+struct HcGeom {
+  int H, hc, LW, gs;  // hidden, streams, low rank, group size
+};
+
+int hc_mix_enqueue(Ctx* c, const HcGeom& g, const mtpx_hc_weights* hw, const uint16_t* normed, const uint32_t* xpW,
                    int S, uint16_t* x, uint16_t* j, uint32_t* xpH) {
-  const mtpx_head_config& g = hd->cfg;
-  const int H = g.layer.hidden, W = g.hc * H, LW = g.lowrank, gs = g.layer.group_size;
+  const int H = g.H, W = g.hc * H, LW = g.LW, gs = g.gs;
   hipStream_t st = c->stream;
   uint16_t* lo = ws_take<uint16_t>(c, (size_t)S * LW);
   uint16_t* act = ws_take<uint16_t>(c, (size_t)S * LW);
@@ -500,6 +510,22 @@ int hc_mix_enqueue(Ctx* c, const Head* hd, const mtpx_hc_weights* hw, const uint
   LAUNCH(c, "hc_up", launch_qmv(hw->up.w, hw->up.s, hw->up.b, hw->up.sb, W, LW, gs, xpL, S, wm, nullptr, st));
   LAUNCH(c, "hc_mix", launch_hc_mix(wm, normed, hw->inject.w ? inj : nullptr, S, g.hc, H, x, j, xpH, st));
   return MTPX_OK;
+}
+
+int hc_mix_enqueue(Ctx* c, const Head* hd, const mtpx_hc_weights* hw, const uint16_t* normed, const uint32_t* xpW,
+                   int S, uint16_t* x, uint16_t* j, uint32_t* xpH) {
+  const HcGeom g{hd->cfg.layer.hidden, hd->cfg.hc, hd->cfg.lowrank, hd->cfg.layer.group_size};
+  return hc_mix_enqueue(c, g, hw, normed, xpW, S, x, j, xpH);
+}
+
+// One hyper-connection mixer's weights (random init): hc_norm weight 1/hc (a
+// power of two for hc in {1, 2, 4, 8}), q4 down/inject/up.
+void hc_random(RandInit& ri, int H, int hc, int LW, bool inject, mtpx_hc_weights* m) {
+  const int W = hc * H;
+  m->norm_scale = ri.dense(W, 0.0f, bf16_bits(1.0f / (float)hc));
+  ri.qmat(LW, W, &m->down);
+  if (inject) ri.qmat(hc, W, &m->inject);
+  ri.qmat(W, LW, &m->up);
 }
 
 int head_create(Ctx* c, const mtpx_head_config* cfg, uint64_t seed, Head** out) {
@@ -522,14 +548,7 @@ int head_create(Ctx* c, const mtpx_head_config* cfg, uint64_t seed, Head** out) 
   ri.qmat(H, H, &w.fc_embedding);
   ri.qmat(H, H, &w.fc_hidden);
   mtpx_hc_weights* hcs[3] = {&w.attn_hc, &w.mlp_hc, &w.final_hc};
-  for (int i = 0; i < 3; ++i) {
-    mtpx_hc_weights* m = hcs[i];
-    // hc_norm weight 1.0 divided by hc_count (a power of two for hc in {1, 2, 4, 8})
-    m->norm_scale = ri.dense(W, 0.0f, bf16_bits(1.0f / (float)cfg->hc));
-    ri.qmat(LW, W, &m->down);
-    if (i < 2) ri.qmat(cfg->hc, W, &m->inject);
-    ri.qmat(W, LW, &m->up);
-  }
+  for (int i = 0; i < 3; ++i) hc_random(ri, H, cfg->hc, LW, i < 2, hcs[i]);
   const std::vector<int32_t> ids = shortlist_ids(cfg);
   w.shortlist_rows = (int)ids.size();
   ri.qmat((int64_t)ids.size(), H, &w.shortlist);
@@ -747,6 +766,36 @@ double host_uniform(uint64_t& s) {
   return (double)(z >> 11) * (1.0 / 9007199254740992.0);
 }
 
+// Weights of one GDN sublayer (random init): q4 projections, conv taps ~ N(0, 0.3);
+// A_log = log U(1, 16); dt = U(0.001, 0.1) with dt_bias its softplus inverse; norm
+// weight U(0.9, 1.1).
+void gdn_random(RandInit& ri, const mtpx_gdn_config& cfg, uint64_t seed, mtpx_gdn_weights* w) {
+  const GdnGeom g = gdn_geom(cfg);
+  ri.qmat(g.pw, cfg.hidden, &w->in_proj);
+  ri.qmat(cfg.hidden, g.hv * 128, &w->out_proj);
+  w->conv_w = ri.dense((int64_t)g.cd * g.kc, 0.3f);
+  uint64_t hs = seed ^ 0x6a09e667f3bcc908ull;
+  std::vector<float> nea(g.hv);
+  std::vector<uint16_t> dtb(g.hv), nw(128);
+  for (int i = 0; i < g.hv; ++i) {
+    nea[i] = (float)(-(1.0 + 15.0 * host_uniform(hs)));
+    const double dt = 0.001 + 0.099 * host_uniform(hs);
+    dtb[i] = bf16_bits((float)std::log(std::expm1(dt)));
+  }
+  for (int i = 0; i < 128; ++i) nw[i] = bf16_bits((float)(0.9 + 0.2 * host_uniform(hs)));
+  float* pn = (float*)ri.alloc(4 * (size_t)g.hv);
+  uint16_t* pd = (uint16_t*)ri.alloc(2 * (size_t)g.hv);
+  uint16_t* pw = (uint16_t*)ri.alloc(2 * 128);
+  if (pn && pd && pw &&
+      (hipMemcpy(pn, nea.data(), 4 * (size_t)g.hv, hipMemcpyHostToDevice) != hipSuccess ||
+       hipMemcpy(pd, dtb.data(), 2 * (size_t)g.hv, hipMemcpyHostToDevice) != hipSuccess ||
+       hipMemcpy(pw, nw.data(), 2 * 128, hipMemcpyHostToDevice) != hipSuccess))
+    ri.ok = false;
+  w->neg_exp_alog = pn;
+  w->dt_bias = pd;
+  w->norm_w = pw;
+}
+
 GdnArgs gdn_args(GdnState* st, const GdnLayer* L, const uint16_t* proj, int S, uint16_t* gated, uint32_t* xp) {
   const GdnGeom g = gdn_geom(st->cfg);
   GdnArgs a;
@@ -795,6 +844,94 @@ int gdn_enqueue(Ctx* c, const GdnLayer* L, GdnState* st, const uint16_t* proj, i
   st->window = S;
   st->committed = 0;
   return MTPX_OK;
+}
+
+}  // namespace
+
+
+// ---------------------------------------------------------------------------
+// The target model's verify forward.
+namespace {
+
+struct TargetLayer {
+  int kind = MTPX_LAYER_GDN;
+  Layer* attn = nullptr;     // attention layers: attention + MoE weights
+  GdnLayer* gdn = nullptr;   // GDN layers
+  mtpx_moe_weights moe;      // this layer's MoE
+  mtpx_hc_weights attn_hc, mlp_hc;
+};
+
+struct Target {
+  mtpx_target_config cfg;
+  std::vector<TargetLayer> layers;
+  mtpx_q4 embed, lm_head;
+  mtpx_hc_weights final_hc;
+  std::vector<void*> allocs;
+};
+
+struct TargetState {
+  Target* t = nullptr;
+  std::vector<Kv*> kv;          // per layer (attention layers), else null
+  std::vector<GdnState*> gdn;   // per layer (GDN layers), else null
+  std::vector<void*> allocs;
+  int64_t offset = 0;           // committed positions
+  int window = 0;
+};
+
+mtpx_gdn_config target_gdn_cfg(const mtpx_target_config& g) {
+  mtpx_gdn_config r;
+  r.hidden = g.layer.hidden;
+  r.key_heads = g.key_heads;
+  r.value_heads = g.value_heads;
+  r.conv_kernel = g.conv_kernel;
+  r.group_size = g.layer.group_size;
+  r.eps = g.layer.eps;
+  return r;
+}
+
+int target_check(const mtpx_target_config* g) {
+  ARG(g, "null config");
+  int rc = layer_check(&g->layer);
+  if (rc) return rc;
+  const mtpx_gdn_config gc = target_gdn_cfg(*g);
+  if ((rc = gdn_check(&gc))) return rc;
+  const int H = g->layer.hidden, gs = g->layer.group_size;
+  ARG(g->num_layers >= 1 && g->num_layers <= 256 && g->full_attention_interval >= 1, "num_layers=%d interval=%d",
+      g->num_layers, g->full_attention_interval);
+  ARG(g->hc >= 1 && g->hc <= 8 && g->lowrank >= 32 && g->lowrank % 32 == 0, "hc=%d lowrank=%d", g->hc, g->lowrank);
+  ARG(k_ok(g->hc * H, gs) && k_ok(g->lowrank, gs) && g->hc * H <= 256 * 48, "unsupported mixer GEMV depths");
+  ARG(g->vocab >= 1 && g->vocab < ((int64_t)1 << 31), "vocab=%lld", (long long)g->vocab);
+  return MTPX_OK;
+}
+
+void target_release(Target* t) {
+  for (TargetLayer& L : t->layers) {
+    if (L.attn) {
+      for (void* p : L.attn->allocs) hipFree(p);
+      delete L.attn;
+    }
+    if (L.gdn) {
+      for (void* p : L.gdn->allocs) hipFree(p);
+      delete L.gdn;
+    }
+  }
+  for (void* p : t->allocs) hipFree(p);
+  delete t;
+}
+
+void target_state_release(TargetState* s) {
+  for (Kv* kv : s->kv)
+    if (kv) {
+      hipFree(kv->k);
+      hipFree(kv->v);
+      delete kv;
+    }
+  for (GdnState* g : s->gdn)
+    if (g) {
+      for (void* p : g->allocs) hipFree(p);
+      delete g;
+    }
+  delete s;
 }
 
 }  // namespace
@@ -1168,34 +1305,10 @@ int mtpx_gdn_new_random(mtpx_ctx h, const mtpx_gdn_config* cfg, uint64_t seed, m
   int rc = gdn_check(cfg);
   if (rc) return rc;
   if (set_device(c)) return MTPX_ERR_HIP;
-  const GdnGeom g = gdn_geom(*cfg);
   GdnLayer* L = new GdnLayer();
   L->cfg = *cfg;
   RandInit ri{c, seed, cfg->group_size, &L->allocs};
-  ri.qmat(g.pw, cfg->hidden, &L->w.in_proj);
-  ri.qmat(cfg->hidden, g.hv * 128, &L->w.out_proj);
-  L->w.conv_w = ri.dense((int64_t)g.cd * g.kc, 0.3f);
-  // A_log = log U(1, 16); dt = U(0.001, 0.1) with dt_bias its softplus inverse; norm weight ~ 1
-  uint64_t hs = seed ^ 0x6a09e667f3bcc908ull;
-  std::vector<float> nea(g.hv);
-  std::vector<uint16_t> dtb(g.hv), nw(128);
-  for (int i = 0; i < g.hv; ++i) {
-    nea[i] = (float)(-(1.0 + 15.0 * host_uniform(hs)));
-    const double dt = 0.001 + 0.099 * host_uniform(hs);
-    dtb[i] = bf16_bits((float)std::log(std::expm1(dt)));
-  }
-  for (int i = 0; i < 128; ++i) nw[i] = bf16_bits((float)(0.9 + 0.2 * host_uniform(hs)));
-  float* pn = (float*)ri.alloc(4 * (size_t)g.hv);
-  uint16_t* pd = (uint16_t*)ri.alloc(2 * (size_t)g.hv);
-  uint16_t* pw = (uint16_t*)ri.alloc(2 * 128);
-  if (pn && pd && pw &&
-      (hipMemcpy(pn, nea.data(), 4 * (size_t)g.hv, hipMemcpyHostToDevice) != hipSuccess ||
-       hipMemcpy(pd, dtb.data(), 2 * (size_t)g.hv, hipMemcpyHostToDevice) != hipSuccess ||
-       hipMemcpy(pw, nw.data(), 2 * 128, hipMemcpyHostToDevice) != hipSuccess))
-    ri.ok = false;
-  L->w.neg_exp_alog = pn;
-  L->w.dt_bias = pd;
-  L->w.norm_w = pw;
+  gdn_random(ri, *cfg, seed, &L->w);
   if ((rc = ri.finish("gdn"))) {
     for (void* p : L->allocs) hipFree(p);
     delete L;
@@ -1348,6 +1461,257 @@ int mtpx_gdn_forward(mtpx_ctx h, mtpx_gdn gh, mtpx_gdn_state sh, const uint16_t*
   if ((rc = gdn_enqueue(c, L, st, proj, S, gated, xp2))) return rc;
   LAUNCH(c, "qmv_gdn_out", launch_qmv(op.w, reinterpret_cast<const bf16*>(op.s), reinterpret_cast<const bf16*>(op.b),
                                        op.sb, H, VD, gs, xp2, S, reinterpret_cast<bf16*>(y), nullptr, c->stream));
+  return MTPX_OK;
+}
+
+
+int mtpx_target_new_random(mtpx_ctx h, const mtpx_target_config* cfg, uint64_t seed, mtpx_target* out) {
+  Ctx* c = C(h);
+  ARG(c && cfg && out, "null argument");
+  int rc = target_check(cfg);
+  if (rc) return rc;
+  if (set_device(c)) return MTPX_ERR_HIP;
+  const mtpx_layer_config& lc = cfg->layer;
+  const mtpx_gdn_config gc = target_gdn_cfg(*cfg);
+  Target* t = new Target();
+  t->cfg = *cfg;
+  t->layers.resize(cfg->num_layers);
+  RandInit ri{c, seed, lc.group_size, &t->allocs};
+  ri.qmat(cfg->vocab, lc.hidden, &t->embed);
+  ri.qmat(cfg->vocab, lc.hidden, &t->lm_head);
+  hc_random(ri, lc.hidden, cfg->hc, cfg->lowrank, false, &t->final_hc);
+  for (int i = 0; i < cfg->num_layers && rc == MTPX_OK && ri.ok; ++i) {
+    TargetLayer& L = t->layers[i];
+    const uint64_t ls = seed + 0x9E3779B97F4A7C15ull * (uint64_t)(i + 1);
+    hc_random(ri, lc.hidden, cfg->hc, cfg->lowrank, true, &L.attn_hc);
+    hc_random(ri, lc.hidden, cfg->hc, cfg->lowrank, true, &L.mlp_hc);
+    if ((i + 1) % cfg->full_attention_interval == 0) {
+      L.kind = MTPX_LAYER_ATTENTION;
+      rc = layer_create(c, &lc, ls, &L.attn);
+      if (rc == MTPX_OK) L.moe = L.attn->w.moe;
+    } else {
+      L.kind = MTPX_LAYER_GDN;
+      L.gdn = new GdnLayer();
+      L.gdn->cfg = gc;
+      RandInit gi{c, ls, lc.group_size, &L.gdn->allocs};
+      gdn_random(gi, gc, ls, &L.gdn->w);
+      moe_random(gi, &lc, &L.moe);
+      rc = gi.finish("target gdn layer");
+    }
+  }
+  const int rc2 = ri.finish("target");
+  if (rc || rc2) {
+    target_release(t);
+    return rc ? rc : rc2;
+  }
+  out->ctx = t;
+  return MTPX_OK;
+}
+
+int mtpx_target_free(mtpx_target th) {
+  Target* t = static_cast<Target*>(th.ctx);
+  if (t) target_release(t);
+  return MTPX_OK;
+}
+
+int mtpx_target_weights_get(mtpx_target th, mtpx_target_weights* out) {
+  Target* t = static_cast<Target*>(th.ctx);
+  ARG(t && out, "null argument");
+  out->embed = t->embed;
+  out->final_hc = t->final_hc;
+  out->lm_head = t->lm_head;
+  return MTPX_OK;
+}
+
+int mtpx_target_layer_weights_get(mtpx_target th, int i, mtpx_target_layer_weights* out) {
+  Target* t = static_cast<Target*>(th.ctx);
+  ARG(t && out, "null argument");
+  ARG(i >= 0 && i < (int)t->layers.size(), "layer %d of %d", i, (int)t->layers.size());
+  const TargetLayer& L = t->layers[i];
+  memset(out, 0, sizeof(*out));
+  out->kind = L.kind;
+  if (L.attn) out->attn = L.attn->w;
+  out->attn.moe = L.moe;
+  if (L.gdn) out->gdn = L.gdn->w;
+  out->attn_hc = L.attn_hc;
+  out->mlp_hc = L.mlp_hc;
+  return MTPX_OK;
+}
+
+int mtpx_target_state_new(mtpx_ctx h, mtpx_target th, mtpx_target_state* out) {
+  Ctx* c = C(h);
+  Target* t = static_cast<Target*>(th.ctx);
+  ARG(c && t && out, "null argument");
+  if (set_device(c)) return MTPX_ERR_HIP;
+  const mtpx_layer_config& lc = t->cfg.layer;
+  const mtpx_gdn_config gc = target_gdn_cfg(t->cfg);
+  TargetState* s = new TargetState();
+  s->t = t;
+  const int n = (int)t->layers.size();
+  s->kv.assign(n, nullptr);
+  s->gdn.assign(n, nullptr);
+  int rc = MTPX_OK;
+  for (int i = 0; i < n && rc == MTPX_OK; ++i) {
+    if (t->layers[i].kind == MTPX_LAYER_ATTENTION) {
+      mtpx_kv k{nullptr};
+      rc = mtpx_kv_new(h, lc.kv_heads, lc.head_dim, lc.max_positions, &k);
+      s->kv[i] = static_cast<Kv*>(k.ctx);
+    } else {
+      mtpx_gdn_state g{nullptr};
+      rc = mtpx_gdn_state_new(h, &gc, &g);
+      s->gdn[i] = static_cast<GdnState*>(g.ctx);
+    }
+  }
+  if (rc) {
+    target_state_release(s);
+    return rc;
+  }
+  out->ctx = s;
+  return MTPX_OK;
+}
+
+int mtpx_target_state_free(mtpx_target_state sh) {
+  TargetState* s = static_cast<TargetState*>(sh.ctx);
+  if (!s) return MTPX_OK;
+  for (Kv* kv : s->kv)
+    if (kv) hipStreamSynchronize(kv->ctx->stream);
+  target_state_release(s);
+  return MTPX_OK;
+}
+
+int mtpx_target_state_kv(mtpx_target_state sh, int i, mtpx_kv* out) {
+  TargetState* s = static_cast<TargetState*>(sh.ctx);
+  ARG(s && out, "null argument");
+  ARG(i >= 0 && i < (int)s->kv.size() && s->kv[i], "layer %d is not an attention layer", i);
+  out->ctx = s->kv[i];
+  return MTPX_OK;
+}
+
+int mtpx_target_state_gdn(mtpx_target_state sh, int i, mtpx_gdn_state* out) {
+  TargetState* s = static_cast<TargetState*>(sh.ctx);
+  ARG(s && out, "null argument");
+  ARG(i >= 0 && i < (int)s->gdn.size() && s->gdn[i], "layer %d is not a GDN layer", i);
+  out->ctx = s->gdn[i];
+  return MTPX_OK;
+}
+
+int mtpx_target_state_set_offset(mtpx_target_state sh, int64_t offset) {
+  TargetState* s = static_cast<TargetState*>(sh.ctx);
+  ARG(s, "null state");
+  ARG(offset >= 0 && offset <= s->t->cfg.layer.max_positions, "offset %lld", (long long)offset);
+  s->offset = offset;
+  s->window = 0;
+  for (Kv* kv : s->kv)
+    if (kv) kv->offset = offset;
+  return MTPX_OK;
+}
+
+int mtpx_target_state_info(mtpx_target_state sh, int64_t* offset, int* window) {
+  TargetState* s = static_cast<TargetState*>(sh.ctx);
+  ARG(s, "null state");
+  if (offset) *offset = s->offset;
+  if (window) *window = s->window;
+  return MTPX_OK;
+}
+
+int mtpx_target_commit(mtpx_target_state sh, int n) {
+  TargetState* s = static_cast<TargetState*>(sh.ctx);
+  ARG(s, "null state");
+  if (n < 0 || n > s->window)
+    return fail(MTPX_ERR_STATE, "commit of %d positions; the last verify had %d", n, s->window);
+  if (s->window == 0) return MTPX_OK;  // nothing open: committing nothing again changes nothing
+  for (GdnState* g : s->gdn)
+    if (g) g->committed = n;
+  s->offset += n;
+  s->window = 0;
+  for (Kv* kv : s->kv)
+    if (kv) kv->offset = s->offset;
+  return MTPX_OK;
+}
+
+int mtpx_target_verify(mtpx_ctx h, mtpx_target th, mtpx_target_state sh, const int32_t* ids, int S, uint16_t* logits,
+                       uint16_t* multi, uint16_t* mixed) {
+  Ctx* c = C(h);
+  Target* t = static_cast<Target*>(th.ctx);
+  TargetState* s = static_cast<TargetState*>(sh.ctx);
+  ARG(c && t && s && ids, "null argument");
+  ARG(s->t == t, "state of another target");
+  ARG(S >= 1 && S <= MAX_TOKENS, "S=%d", S);
+  const mtpx_target_config& g = t->cfg;
+  const mtpx_layer_config& lc = g.layer;
+  ARG(s->offset + S <= lc.max_positions, "cache full (offset %lld + %d)", (long long)s->offset, S);
+  if (set_device(c)) return MTPX_ERR_HIP;
+  const int H = lc.hidden, hc = g.hc, W = hc * H, gs = lc.group_size, HQ = lc.heads, D = lc.head_dim;
+  const GdnGeom gg = gdn_geom(target_gdn_cfg(g));
+  const int VD = gg.hv * 128;
+  const int XB = std::max(H, HQ * D) / 32;
+  const HcGeom hg{H, hc, g.lowrank, gs};
+  const float eps = lc.eps;
+  // an uncommitted window is discarded: caches rewind to the committed offset
+  for (Kv* kv : s->kv)
+    if (kv) kv->offset = s->offset;
+  const int T = (int)s->offset + S;
+  const size_t mix = al(2 * (size_t)S * g.lowrank) * 2 + al(2 * (size_t)S * hc) +
+                     al(4 * (size_t)S * (g.lowrank / 32) * XP_DW) + al(2 * (size_t)S * W);
+  const Layer* any_attn = nullptr;
+  for (const TargetLayer& L : t->layers)
+    if (L.attn) any_attn = L.attn;
+  const size_t per_layer = std::max(mix + moe_ws_bytes(&t->layers[0].moe, S),
+                                    mix + (any_attn ? attn_ws_bytes(any_attn, S, T) : 0)) + 4096;
+  const size_t fixed = al(2 * (size_t)S * H) * 5 + al(2 * (size_t)S * W) * 4 + al(2 * (size_t)S * hc) * 2 +
+                       al(4 * (size_t)S * (W / 32) * XP_DW) + al(4 * (size_t)S * XB * XP_DW) +
+                       al(4 * (size_t)S * (VD / 32) * XP_DW) + al(2 * (size_t)S * gg.pw) + 4096;
+  int rc = ws_reserve(c, fixed + per_layer);
+  if (rc) return rc;
+  c->ws_used = 0;
+  uint16_t* e = ws_take<uint16_t>(c, (size_t)S * H);
+  uint16_t* x = ws_take<uint16_t>(c, (size_t)S * H);
+  uint16_t* ao = ws_take<uint16_t>(c, (size_t)S * H);
+  uint16_t* mo = ws_take<uint16_t>(c, (size_t)S * H);
+  uint16_t* mx = mixed ? mixed : ws_take<uint16_t>(c, (size_t)S * H);
+  uint16_t* sA = ws_take<uint16_t>(c, (size_t)S * W);
+  uint16_t* sM = ws_take<uint16_t>(c, (size_t)S * W);
+  uint16_t* nrm = ws_take<uint16_t>(c, (size_t)S * W);
+  uint16_t* mt = multi ? multi : ws_take<uint16_t>(c, (size_t)S * W);
+  uint16_t* jA = ws_take<uint16_t>(c, (size_t)S * hc);
+  uint16_t* jM = ws_take<uint16_t>(c, (size_t)S * hc);
+  uint32_t* xpW = ws_take<uint32_t>(c, (size_t)S * (W / 32) * XP_DW);
+  uint32_t* xpH = ws_take<uint32_t>(c, (size_t)S * XB * XP_DW);
+  uint32_t* xpG = ws_take<uint32_t>(c, (size_t)S * (VD / 32) * XP_DW);
+  uint16_t* proj = ws_take<uint16_t>(c, (size_t)S * gg.pw);
+  const size_t mark = c->ws_used;
+  hipStream_t st = c->stream;
+  LAUNCH(c, "embed", launch_embed_rows(t->embed.w, t->embed.s, t->embed.b, H, gs, g.vocab, ids, S, e, st));
+  for (int i = 0; i < (int)t->layers.size(); ++i) {
+    const TargetLayer& L = t->layers[i];
+    const bool first = i == 0;
+    LAUNCH(c, "hc_norm", launch_hc_norm(first ? e : sM, first ? nullptr : mo, first ? nullptr : jM, S, hc, H,
+                                        first ? 1 : 0, L.attn_hc.norm_scale, eps, sA, nrm, xpW, st));
+    c->ws_used = mark;
+    if ((rc = hc_mix_enqueue(c, hg, &L.attn_hc, nrm, xpW, S, x, jA, xpH))) return rc;
+    if (L.kind == MTPX_LAYER_GDN) {
+      const mtpx_q4& ip = L.gdn->w.in_proj;
+      const mtpx_q4& op = L.gdn->w.out_proj;
+      LAUNCH(c, "qmv_gdn_in", launch_qmv(ip.w, ip.s, ip.b, ip.sb, gg.pw, H, gs, xpH, S, proj, nullptr, st));
+      if ((rc = gdn_enqueue(c, L.gdn, s->gdn[i], proj, S, nullptr, xpG))) return rc;
+      LAUNCH(c, "qmv_gdn_out", launch_qmv(op.w, op.s, op.b, op.sb, H, VD, gs, xpG, S, ao, nullptr, st));
+    } else {
+      if ((rc = attn_enqueue(c, L.attn, s->kv[i], xpH, S, ao))) return rc;
+    }
+    LAUNCH(c, "hc_norm", launch_hc_norm(sA, ao, jA, S, hc, H, 0, L.mlp_hc.norm_scale, eps, sM, nrm, xpW, st));
+    c->ws_used = mark;
+    if ((rc = hc_mix_enqueue(c, hg, &L.mlp_hc, nrm, xpW, S, x, jM, xpH))) return rc;
+    if ((rc = moe_enqueue(c, &L.moe, x, S, mo, nullptr, nullptr, nullptr, nullptr, nullptr, xpH))) return rc;
+  }
+  LAUNCH(c, "hc_norm", launch_hc_norm(sM, mo, jM, S, hc, H, 0, t->final_hc.norm_scale, eps, mt, nrm, xpW, st));
+  c->ws_used = mark;
+  if ((rc = hc_mix_enqueue(c, hg, &t->final_hc, nrm, xpW, S, mx, nullptr, xpH))) return rc;
+  if (logits)
+    LAUNCH(c, "qmv_lm_head", launch_qmv(t->lm_head.w, t->lm_head.s, t->lm_head.b, t->lm_head.sb, (int)g.vocab, H, gs,
+                                        xpH, S, logits, nullptr, st));
+  for (Kv* kv : s->kv)
+    if (kv) kv->offset = s->offset + S;
+  s->window = S;
   return MTPX_OK;
 }
 

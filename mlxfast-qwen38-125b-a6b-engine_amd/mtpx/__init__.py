@@ -12,10 +12,10 @@ import ctypes as C
 
 from . import _lib
 from ._lib import (DrafterInfo, GDNConfig, GDNWeights, Handle, HCWeights, HeadConfig, HeadWeights, LayerConfig,
-                   LayerWeights, MoEWeights, MtpxError, Q4, check)
+                   LayerWeights, MoEWeights, MtpxError, Q4, TargetConfig, TargetLayerWeights, TargetWeights, check)
 
-__all__ = ["Context", "KVCache", "DecoderLayer", "MTPHead", "Drafter", "GDN", "GDNState", "MoEWeights", "LayerConfig",
-           "HeadConfig", "GDNConfig", "MtpxError", "moe_weights_from"]
+__all__ = ["Context", "KVCache", "DecoderLayer", "MTPHead", "Drafter", "GDN", "GDNState", "Target", "TargetState",
+           "MoEWeights", "LayerConfig", "HeadConfig", "GDNConfig", "TargetConfig", "MtpxError", "moe_weights_from"]
 
 
 def _ptr(t):
@@ -381,6 +381,92 @@ class GDNState:
         w, c = C.c_int(), C.c_int()
         check(self.ctx.lib.mtpx_gdn_state_info(self.h, C.byref(w), C.byref(c)), "gdn_state_info")
         return w.value, c.value
+
+
+def _borrowed(cls, ctx, handle):
+    """A wrapper around a handle owned by another object (its close() frees nothing)."""
+    o = cls.__new__(cls)
+    o.ctx = ctx
+    o.h = Handle(handle.ctx)
+    o.close = lambda: None
+    return o
+
+
+class Target:
+    """The target model with seeded random weights (mtpx_target): embedding, the
+    layer stack (GDN or attention + MoE, hyper-connection mixers), final mixer, lm_head."""
+
+    def __init__(self, ctx: Context, cfg: TargetConfig, seed: int):
+        self.ctx = ctx
+        self.cfg = cfg
+        self.h = Handle()
+        check(ctx.lib.mtpx_target_new_random(ctx.h, C.byref(cfg), seed, C.byref(self.h)), "target_new_random")
+
+    def close(self):
+        if self.h.ctx:
+            self.ctx.lib.mtpx_target_free(self.h)
+            self.h.ctx = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def weights(self) -> TargetWeights:
+        w = TargetWeights()
+        check(self.ctx.lib.mtpx_target_weights_get(self.h, C.byref(w)), "target_weights_get")
+        return w
+
+    def layer_weights(self, i: int) -> TargetLayerWeights:
+        w = TargetLayerWeights()
+        check(self.ctx.lib.mtpx_target_layer_weights_get(self.h, i, C.byref(w)), "target_layer_weights_get")
+        return w
+
+    def verify(self, state: "TargetState", ids, logits=None, multi=None, mixed=None):
+        check(self.ctx.lib.mtpx_target_verify(self.ctx.h, self.h, state.h, _ptr(ids), ids.shape[0], _ptr(logits),
+                                              _ptr(multi), _ptr(mixed)), "target_verify")
+
+
+class TargetState:
+    """Per-request caches of a Target (mtpx_target_state)."""
+
+    def __init__(self, ctx: Context, target: Target):
+        self.ctx = ctx
+        self.h = Handle()
+        check(ctx.lib.mtpx_target_state_new(ctx.h, target.h, C.byref(self.h)), "target_state_new")
+
+    def close(self):
+        if self.h.ctx:
+            self.ctx.lib.mtpx_target_state_free(self.h)
+            self.h.ctx = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def kv(self, layer: int) -> KVCache:
+        h = Handle()
+        check(self.ctx.lib.mtpx_target_state_kv(self.h, layer, C.byref(h)), "target_state_kv")
+        return _borrowed(KVCache, self.ctx, h)
+
+    def gdn(self, layer: int) -> GDNState:
+        h = Handle()
+        check(self.ctx.lib.mtpx_target_state_gdn(self.h, layer, C.byref(h)), "target_state_gdn")
+        return _borrowed(GDNState, self.ctx, h)
+
+    def set_offset(self, offset: int):
+        check(self.ctx.lib.mtpx_target_state_set_offset(self.h, offset), "target_state_set_offset")
+
+    def info(self):
+        o, w = C.c_int64(), C.c_int()
+        check(self.ctx.lib.mtpx_target_state_info(self.h, C.byref(o), C.byref(w)), "target_state_info")
+        return o.value, w.value
+
+    def commit(self, n: int):
+        check(self.ctx.lib.mtpx_target_commit(self.h, n), "target_commit")
 
 
 def moe_weights_from(tensors: dict, H, E, K, F, gs) -> MoEWeights:

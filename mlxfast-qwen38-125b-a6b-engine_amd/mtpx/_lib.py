@@ -79,6 +79,21 @@ class GDNWeights(C.Structure):
                 ("out_proj", Q4)]
 
 
+class TargetConfig(C.Structure):
+    _fields_ = [("layer", LayerConfig), ("key_heads", INT), ("value_heads", INT), ("conv_kernel", INT),
+                ("num_layers", INT), ("full_attention_interval", INT), ("hc", INT), ("lowrank", INT),
+                ("vocab", I64)]
+
+
+class TargetLayerWeights(C.Structure):
+    _fields_ = [("kind", INT), ("attn", LayerWeights), ("gdn", GDNWeights), ("attn_hc", HCWeights),
+                ("mlp_hc", HCWeights)]
+
+
+class TargetWeights(C.Structure):
+    _fields_ = [("embed", Q4), ("final_hc", HCWeights), ("lm_head", Q4)]
+
+
 _SIGS = {
     "mtpx_last_error": (C.c_char_p, []),
     "mtpx_version": (C.c_char_p, []),
@@ -135,6 +150,18 @@ _SIGS = {
     "mtpx_gdn_state_info": (INT, [Handle, C.POINTER(INT), C.POINTER(INT)]),
     "mtpx_gdn_core": (INT, [Handle, Handle, Handle, P, INT, P]),
     "mtpx_gdn_forward": (INT, [Handle, Handle, Handle, P, INT, P, P]),
+    "mtpx_target_new_random": (INT, [Handle, C.POINTER(TargetConfig), U64, C.POINTER(Handle)]),
+    "mtpx_target_free": (INT, [Handle]),
+    "mtpx_target_weights_get": (INT, [Handle, C.POINTER(TargetWeights)]),
+    "mtpx_target_layer_weights_get": (INT, [Handle, INT, C.POINTER(TargetLayerWeights)]),
+    "mtpx_target_state_new": (INT, [Handle, Handle, C.POINTER(Handle)]),
+    "mtpx_target_state_free": (INT, [Handle]),
+    "mtpx_target_state_kv": (INT, [Handle, INT, C.POINTER(Handle)]),
+    "mtpx_target_state_gdn": (INT, [Handle, INT, C.POINTER(Handle)]),
+    "mtpx_target_state_set_offset": (INT, [Handle, I64]),
+    "mtpx_target_state_info": (INT, [Handle, C.POINTER(I64), C.POINTER(INT)]),
+    "mtpx_target_verify": (INT, [Handle, Handle, Handle, P, INT, P, P, P]),
+    "mtpx_target_commit": (INT, [Handle, INT]),
     "mtpx_profile_enable": (INT, [Handle, INT]),
     "mtpx_profile_reset": (INT, [Handle]),
     "mtpx_profile_dump": (INT, [Handle, C.c_char_p, C.c_size_t]),

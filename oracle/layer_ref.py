@@ -43,14 +43,26 @@ def download(lw, cfg):
              sin=bf(lw.rope_sin, P * rot).reshape(P, rot), QW=QW)
     w["qkv"] = q(lw.qkv_w, lw.qkv_s, lw.qkv_b, QW, H)
     w["o"] = q(lw.o_w, lw.o_s, lw.o_b, H, HQ * D)
-    m = lw.moe
+    w["moe"] = download_moe(lw.moe, cfg)
+    return w
+
+
+def download_moe(m, cfg):
+    """A layer's MoE weights (mtpx_moe_weights) as the dict O.moe_block takes."""
+    H, E, F, gs = cfg["hidden"], cfg["experts"], cfg["expert_width"], cfg["group_size"]
+
+    def bf(ptr, n):
+        return read_device(ptr, 2 * n, np.uint16)
+
+    def q(pw, ps, pb, rows, K):
+        return (read_device(pw, rows * K // 2, np.uint32).reshape(rows, K // 8),
+                bf(ps, rows * K // gs).reshape(rows, K // gs), bf(pb, rows * K // gs).reshape(rows, K // gs))
     moe = dict(router=bf(m.router, E * H).reshape(E, H), shared_gate=bf(m.shared_gate, H))
     for n, rows, K in (("gate", E * F, H), ("up", E * F, H), ("down", E * H, F),
                        ("sh_gate", F, H), ("sh_up", F, H), ("sh_down", H, F)):
         moe[n + "_w"], moe[n + "_s"], moe[n + "_b"] = q(getattr(m, n + "_w"), getattr(m, n + "_s"),
                                                          getattr(m, n + "_b"), rows, K)
-    w["moe"] = moe
-    return w
+    return moe
 
 
 def oracle_attn(w, cfg, kc, vc, h, pos0):

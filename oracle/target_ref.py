@@ -1,0 +1,103 @@
+"""Oracle-side composition of the target's verify forward -- TEST INFRASTRUCTURE ONLY.
+
+Used by tests/test_gpu_target.py: downloads a target's device weights and runs
+the verify forward through the CPU oracle in the order of
+Runner/FastModel/TrackFastModel.swift:1165-1265 (fastStreams: hyper-connection
+inject + norm, mixer, GDN or attention, inject + norm, mixer, MoE per layer;
+the final mixer) and :1330-1333 (lm_head on the mixed row), with the window
+commit of :726-731 as a replay of the committed positions.
+
+Parity unpinned: the layer wiring follows those files by reading only; every
+piece it calls is pinned on its own (tests/test_oracle_*.py).
+"""
+import numpy as np
+
+from oracle import oracle as O
+from oracle.head_ref import _mix
+from oracle.layer_ref import download, download_moe, oracle_attn, read_device
+
+
+def _bf(ptr, n):
+    return read_device(ptr, 2 * n, np.uint16)
+
+
+def _q(q4, rows, K, gs):
+    return (read_device(q4.w, rows * K // 2, np.uint32).reshape(rows, K // 8),
+            _bf(q4.s, rows * K // gs).reshape(rows, K // gs), _bf(q4.b, rows * K // gs).reshape(rows, K // gs))
+
+
+def download_hc(m, H, hc, LW, gs):
+    W = hc * H
+    return dict(scale=_bf(m.norm_scale, W), down=_q(m.down, LW, W, gs), up=_q(m.up, W, LW, gs),
+                inject=_q(m.inject, hc, W, gs) if m.inject.w else None)
+
+
+def download_gdn(w, H, hk, hv, kc, gs):
+    g = O.gdn_geom(hk, hv, kc)
+    return dict(in_proj=_q(w.in_proj, g.proj_w, H, gs), out_proj=_q(w.out_proj, H, hv * 128, gs),
+                conv_w=_bf(w.conv_w, g.conv_dim * g.kc).reshape(g.conv_dim, g.kc),
+                nea=read_device(w.neg_exp_alog, 4 * hv, np.float32), dtb=_bf(w.dt_bias, hv), nw=_bf(w.norm_w, 128),
+                geom=g)
+
+
+def download_target(t, cfg):
+    """cfg: dict with the layer config keys plus key_heads, value_heads, conv_kernel,
+    num_layers, full_attention_interval, hc, lowrank, vocab."""
+    H, gs, hc, LW, V = cfg["hidden"], cfg["group_size"], cfg["hc"], cfg["lowrank"], cfg["vocab"]
+    tw = t.weights()
+    w = dict(embed=_q(tw.embed, V, H, gs), lm_head=_q(tw.lm_head, V, H, gs),
+             final_hc=download_hc(tw.final_hc, H, hc, LW, gs), layers=[])
+    for i in range(cfg["num_layers"]):
+        lw = t.layer_weights(i)
+        L = dict(kind=lw.kind, attn_hc=download_hc(lw.attn_hc, H, hc, LW, gs),
+                 mlp_hc=download_hc(lw.mlp_hc, H, hc, LW, gs))
+        if lw.kind == 1:
+            L["attn"] = download(lw.attn, cfg)
+            L["moe"] = L["attn"]["moe"]
+        else:
+            L["gdn"] = download_gdn(lw.gdn, H, cfg["key_heads"], cfg["value_heads"], cfg["conv_kernel"], gs)
+            L["moe"] = download_moe(lw.attn.moe, cfg)
+        w["layers"].append(L)
+    return w
+
+
+def _gdn(L, proj, conv, ssm, eps):
+    d = L["gdn"]
+    return O.gdn_core(d["geom"], proj, conv, ssm, d["conv_w"], d["nea"], d["dtb"], d["nw"], eps)
+
+
+def oracle_verify(w, cfg, state, ids, pos0):
+    """state: dict(kc={layer: [HK, P, D]}, vc=..., conv={layer: ...}, ssm={layer: ...}) of the
+    committed caches (kc/vc receive the window's rows in place).
+    -> (logits [S, V], multi [S, hc*H], mixed [S, H], window) where window feeds oracle_commit."""
+    H, gs, hc, eps = cfg["hidden"], cfg["group_size"], cfg["hc"], cfg["eps"]
+    e = O.embed_rows(*w["embed"], gs, ids)
+    resid, out, inj, tile = e, None, None, True
+    window = {}
+    for i, L in enumerate(w["layers"]):
+        sA, n = O.hc_norm(resid, out, inj, L["attn_hc"]["scale"], hc, eps, tile=tile)
+        x, jA = _mix(L["attn_hc"], n, hc, gs)
+        if L["kind"] == 0:
+            proj, _ = O.qmv(*L["gdn"]["in_proj"], gs, x)
+            r = _gdn(L, proj, state["conv"][i], state["ssm"][i], eps)
+            window[i] = proj
+            ao, _ = O.qmv(*L["gdn"]["out_proj"], gs, r["gated"])
+        else:
+            ao = oracle_attn(L["attn"], cfg, state["kc"][i], state["vc"][i], x, pos0)
+        sM, n = O.hc_norm(sA, ao, jA, L["mlp_hc"]["scale"], hc, eps)
+        x, jM = _mix(L["mlp_hc"], n, hc, gs)
+        mo = O.moe_block(L["moe"], x, H, cfg["experts"], cfg["top_k"], cfg["expert_width"], gs)["y"]
+        resid, out, inj, tile = sM, mo, jM, False
+    multi, n = O.hc_norm(resid, out, inj, w["final_hc"]["scale"], hc, eps)
+    mixed, _ = _mix(w["final_hc"], n, hc, gs)
+    logits, _ = O.qmv(*w["lm_head"], gs, mixed)
+    return logits, multi, mixed, window
+
+
+def oracle_commit(w, cfg, state, window, n):
+    """Advance the GDN states of `state` by the first n positions of a verify window."""
+    for i, proj in window.items():
+        if n == 0:
+            continue
+        r = _gdn(w["layers"][i], proj[:n], state["conv"][i], state["ssm"][i], cfg["eps"])
+        state["conv"][i], state["ssm"][i] = r["conv_state"], r["ssm"]

@@ -46,3 +46,18 @@ def rand_bf16(rng, shape, sigma=1.0):
 def qweights(rng, rows, K, gs, sigma=0.02):
     w = rand_bf16(rng, (rows, K), sigma)
     return O.affine_quantize(w, gs)
+
+
+_hip = None
+
+
+def write_device(ptr: int, a: np.ndarray):
+    """Copy a host array into raw device memory (a pointer the library owns)."""
+    import ctypes as C
+    global _hip
+    if _hip is None:
+        _hip = C.CDLL("libamdhip64.so")
+        _hip.hipMemcpy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int]
+    a = np.ascontiguousarray(a)
+    torch.cuda.synchronize()
+    assert _hip.hipMemcpy(C.c_void_p(ptr), a.ctypes.data, a.nbytes, 1) == 0  # host -> device

@@ -51,6 +51,9 @@ def test_struct_layouts_match_c_compiler(tmp_path):
                                                  "shortlist_ids", "shortlist_rows"]),
         "mtpx_gdn_config": (_lib.GDNConfig, ["value_heads", "group_size", "eps"]),
         "mtpx_gdn_weights": (_lib.GDNWeights, ["conv_w", "neg_exp_alog", "norm_w", "out_proj"]),
+        "mtpx_target_config": (_lib.TargetConfig, ["key_heads", "num_layers", "lowrank", "vocab"]),
+        "mtpx_target_layer_weights": (_lib.TargetLayerWeights, ["attn", "gdn", "attn_hc", "mlp_hc"]),
+        "mtpx_target_weights": (_lib.TargetWeights, ["final_hc", "lm_head"]),
     }
     lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "mtpx.h"', "int main(void) {"]
     for name, (_, fields) in checks.items():

@@ -433,6 +433,9 @@ int mtpx_target_verify(mtpx_ctx ctx, mtpx_target t, mtpx_target_state st, const 
                        uint16_t* logits, uint16_t* multi, uint16_t* mixed);
 /* The first n (0..window) positions of the last verify become committed. */
 int mtpx_target_commit(mtpx_target_state st, int n);
+/* Distinct routed experts of each layer's MoE in the last verify (host int32 [num_layers];
+ * synchronises), for the algorithmic byte count of the expert GEMVs. */
+int mtpx_target_moe_unique(mtpx_ctx ctx, mtpx_target_state st, int32_t* out);
 
 /* ---- per-kernel timing (replaces TrackFastProfile, Runner/FastModel/TrackFastWeights.swift:81-98) ----
  * With profiling on, every launch the library issues is bracketed by HIP events

@@ -1,0 +1,220 @@
+// The hyper-connection mixer of one sublayer in two launches:
+//   k_mix_down : lo = down . n and inj = inject . n (n = the normed streams,
+//                K = hc*H), split over the lane rule's classes: the L lanes of
+//                a row's walk are grouped by lane mod Q (Q = min(L, 4)); each
+//                workgroup computes one class of a row block from that class's
+//                activation blocks only and folds the class's lanes (the
+//                butterfly levels L/2 .. Q), leaving Q partials per row
+//   k_mix_up   : every workgroup finishes the butterfly for all low-rank rows
+//                ((v0 + v2) + (v1 + v3) for Q = 4: the remaining levels Q/2 .. 1
+//                in the same order), rounds, applies SiLU and prepares the
+//                activation blocks; then the up rows of its 32 hidden
+//                positions in every stream (w), the mix
+//                x = bf16 running sum over streams of bf16(sigmoid(w) * n), the
+//                prepared blocks of x, and j = 2 * sigmoid(inj)
+// The float order of every row is the one of the single-launch GEMV (same
+// lanes, same blocks per lane, same butterfly), so the outputs are those of
+// down/inject GEMV -> SiLU -> up GEMV -> mix.
+// Reference: Runner/FastModel/TrackFastMixer.swift:14-224 (downInject, upMix),
+// Runner/FastModel/TrackFastMixerSplitK.swift (the split-K down projection),
+// Runner/FastModel/TrackFastKernels2.swift:160-280 (hcMix).
+#include "qrows.h"
+
+namespace mtpx {
+
+constexpr int MIX_THREADS = 256;
+
+template <int L, int IT>
+__global__ __launch_bounds__(MIX_THREADS) void k_mix_down(MixArgs a) {
+  static_assert(IT > 0, "exact lane tiling");
+  extern __shared__ uint32_t lds[];  // this class's activation blocks [S][nb/Q]
+  constexpr int Q = L < 4 ? L : 4;
+  constexpr int LC = L / Q;       // lanes of one row within a class
+  constexpr int RPW = 64 / LC;    // rows per wave
+  const int W = a.hc * a.H, nb = W / 32, ncb = nb / Q, S = a.S;
+  const int NR = a.LW + (a.iw ? a.hc : 0);
+  const int g = blockIdx.y;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int subc = lane % LC, grp = lane / LC;
+  const int sub = g + Q * subc;  // the lane of the single-launch walk this lane stands in for
+  const int row = blockIdx.x * (4 * RPW) + wave * RPW + grp;
+  const bool valid = row < NR;
+  const int r = valid ? row : 0;
+  const bool inj = r >= a.LW;
+  const int rr = inj ? r - a.LW : r;
+  const int ng = W / a.gs, P = sb_row_len(W, a.gs);
+  const uint32_t* wq = inj ? a.iw : a.dw;
+  const bf16* sc = inj ? a.is : a.ds;
+  const bf16* bi = inj ? a.ib : a.db;
+  const uint32_t* sb = inj ? a.isb : a.dsb;
+  QRow<L, IT> R;
+  R.load(wq + (size_t)rr * (W / 8), sc + (size_t)rr * ng, bi + (size_t)rr * ng, sb ? sb + (size_t)rr * P : nullptr,
+         nb, a.gs, sub, valid);
+  // stage the class's blocks: compact block c = subc' + LC * it holds block g + Q * subc' + L * it
+  for (int i = threadIdx.x; i < S * ncb * (XP_DW / 4); i += MIX_THREADS) {
+    const int q = i % (XP_DW / 4), c = (i / (XP_DW / 4)) % ncb, s = i / (XP_DW / 4) / ncb;
+    const int j = g + Q * (c % LC) + L * (c / LC);
+    reinterpret_cast<uint4*>(lds)[i] = reinterpret_cast<const uint4*>(a.xpW + ((size_t)s * nb + j) * XP_DW)[q];
+  }
+  __syncthreads();
+  for (int s = 0; s < S; ++s) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+      const uint32_t* xl = lds + ((size_t)s * ncb + subc + LC * it) * XP_DW;
+      acc = block_accum(acc, block_dot(R.w[it], xl), __uint_as_float(R.sb[it] << 16),
+                        __uint_as_float(R.sb[it] & 0xffff0000u), xl);
+    }
+    acc = lane_fold<LC>(acc);
+    if (subc == 0 && valid) a.part[((size_t)g * S + s) * NR + row] = acc;
+  }
+}
+
+// Butterfly levels Q/2 .. 1 over the class partials of one row.
+template <int Q>
+__device__ __forceinline__ float class_fold(const float* p, size_t stride) {
+  if constexpr (Q == 4) return (p[0] + p[2 * stride]) + (p[stride] + p[3 * stride]);
+  if constexpr (Q == 2) return p[0] + p[stride];
+  return p[0];
+}
+
+// grid (H/32), MIX_THREADS threads.  Up rows of the block: local row lr = c*32 + i
+// is global row c*H + d0 + i.
+template <int QD, int L, int IT>
+__global__ __launch_bounds__(MIX_THREADS) void k_mix_up(MixArgs a) {
+  constexpr int RW = 64 / L;
+  constexpr int MAXROWS = 8 * 32;  // hc <= 8
+  constexpr int NP = (MAXROWS + 4 * RW - 1) / (4 * RW);
+  __shared__ bf16 act[MAX_TOKENS * 512];             // [S][LW], S * LW <= 4096
+  __shared__ uint32_t xpa[MAX_TOKENS * 12 * XP_DW];  // [S][LW/32][XP_DW], S * LW / 32 <= 96
+  __shared__ bf16 wl[MAX_TOKENS][MAXROWS];
+  __shared__ uint32_t scratch[MIX_THREADS / 32][24];
+  const int S = a.S, H = a.H, hc = a.hc, LW = a.LW, W = hc * H;
+  const int NR = LW + (a.iw ? hc : 0);
+  const int nbA = LW / 32, ng = LW / a.gs, P = sb_row_len(LW, a.gs);
+  const int d0 = blockIdx.x * 32;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int sub = lane % L, grp = lane / L;
+  const int nrows = hc * 32;
+  // up rows first, so their loads are in flight during the low-rank finish
+  QRow<L, IT> U[NP];
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    const int lr = p * 4 * RW + wave * RW + grp;
+    const bool v = lr < nrows;
+    const int gr = v ? (lr / 32) * H + d0 + (lr % 32) : 0;
+    U[p].load(a.uw + (size_t)gr * (LW / 8), a.us + (size_t)gr * ng, a.ub + (size_t)gr * ng,
+              a.usb ? a.usb + (size_t)gr * P : nullptr, nbA, a.gs, sub, v);
+  }
+  // low-rank rows: finish the fold, round, SiLU
+  for (int i = threadIdx.x; i < S * LW; i += MIX_THREADS) {
+    const int s = i / LW, r = i % LW;
+    const float v = class_fold<QD>(a.part + (size_t)s * NR + r, (size_t)S * NR);
+    act[i] = f2bf(silu_bf16(round_bf(v)));
+  }
+  if (blockIdx.x == 0 && a.iw && a.j && (int)threadIdx.x < S * hc) {
+    const int s = threadIdx.x / hc, c = threadIdx.x % hc;
+    const float v = class_fold<QD>(a.part + (size_t)s * NR + LW + c, (size_t)S * NR);
+    a.j[(size_t)s * hc + c] = f2bf(2.0f * sigmoid_bf16(round_bf(v)));
+  }
+  __syncthreads();
+  // prepared blocks of the activations: 32 lanes per block
+  const int nblk = S * nbA;
+  for (int b0 = 0; b0 < nblk; b0 += MIX_THREADS / 32) {
+    const int b = b0 + (int)(threadIdx.x >> 5), li = threadIdx.x & 31;
+    int E = 0, sm = 0;
+    if (b < nblk) xprep_lanes_build(act[b * 32 + li], li, scratch[threadIdx.x >> 5], E, sm);
+    __syncthreads();
+    if (b < nblk) xprep_lanes_store(li, scratch[threadIdx.x >> 5], E, sm, xpa + (size_t)b * XP_DW);
+    __syncthreads();
+  }
+  // up rows of the block, every token
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    const int lr = p * 4 * RW + wave * RW + grp;
+    if (p * 4 * RW >= nrows) break;  // uniform
+    for (int s = 0; s < S; ++s) {
+      float v = U[p].dot(xpa + (size_t)s * nbA * XP_DW, nbA, sub);
+      v = lane_fold<L>(v);
+      if (sub == 0 && lr < nrows) wl[s][lr] = f2bf(v);
+    }
+  }
+  __syncthreads();
+  // mix: 32 lanes per token, then the prepared block of x
+  for (int s0 = 0; s0 < S; s0 += MIX_THREADS / 32) {
+    const int s = s0 + (int)(threadIdx.x >> 5), i = threadIdx.x & 31;
+    bf16 y = 0;
+    if (s < S) {
+      float acc = 0.0f;
+      for (int c = 0; c < hc; ++c) {
+        const float n = bf2f(a.normed[(size_t)s * W + (size_t)c * H + d0 + i]);
+        acc = round_bf(acc + round_bf(sigmoid_bf16(bf2f(wl[s][c * 32 + i])) * n));
+      }
+      y = f2bf(acc);
+      a.x[(size_t)s * H + d0 + i] = y;
+    }
+    int E = 0, sm = 0;
+    if (s < S) xprep_lanes_build(y, i, scratch[threadIdx.x >> 5], E, sm);
+    __syncthreads();
+    if (s < S && a.xpH)
+      xprep_lanes_store(i, scratch[threadIdx.x >> 5], E, sm, a.xpH + ((size_t)s * (H / 32) + blockIdx.x) * XP_DW);
+    __syncthreads();
+  }
+}
+
+template <int L, int IT>
+static hipError_t mix_down_li(const MixArgs& a, hipStream_t st) {
+  if constexpr (IT == 0) {
+    return hipErrorInvalidValue;  // exact tiling only (checked by the caller)
+  } else {
+    constexpr int Q = L < 4 ? L : 4;
+    constexpr int RPB = 4 * (64 / (L / Q));
+    const int W = a.hc * a.H, NR = a.LW + (a.iw ? a.hc : 0);
+    const size_t lds = (size_t)a.S * (W / 32 / Q) * XP_DW * 4;
+    static size_t cur = 0;
+    hipError_t e = ensure_lds(k_mix_down<L, IT>, lds, cur);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((k_mix_down<L, IT>), dim3((NR + RPB - 1) / RPB, Q), dim3(MIX_THREADS), lds, st, a);
+    return hipGetLastError();
+  }
+}
+
+template <int QD>
+struct MixUp {
+  template <int L, int IT>
+  static hipError_t go(const MixArgs& a, hipStream_t st) {
+    hipLaunchKernelGGL((k_mix_up<QD, L, IT>), dim3(a.H / 32), dim3(MIX_THREADS), 0, st, a);
+    return hipGetLastError();
+  }
+};
+template <int L, int IT> static hipError_t mix_up_q4(const MixArgs& a, hipStream_t st) { return MixUp<4>::go<L, IT>(a, st); }
+template <int L, int IT> static hipError_t mix_up_q2(const MixArgs& a, hipStream_t st) { return MixUp<2>::go<L, IT>(a, st); }
+template <int L, int IT> static hipError_t mix_up_q1(const MixArgs& a, hipStream_t st) { return MixUp<1>::go<L, IT>(a, st); }
+
+static hipError_t mix_down(const MixArgs& a, hipStream_t st) { MTPX_QROW_DISPATCH(a.hc * a.H / 32, mix_down_li, a, st); }
+static hipError_t mix_up4(const MixArgs& a, hipStream_t st) { MTPX_QROW_DISPATCH(a.LW / 32, mix_up_q4, a, st); }
+static hipError_t mix_up2(const MixArgs& a, hipStream_t st) { MTPX_QROW_DISPATCH(a.LW / 32, mix_up_q2, a, st); }
+static hipError_t mix_up1(const MixArgs& a, hipStream_t st) { MTPX_QROW_DISPATCH(a.LW / 32, mix_up_q1, a, st); }
+
+int mix_classes(int W) {
+  const int L = lanes_for_blocks(W / 32);
+  return L < 4 ? L : 4;
+}
+
+bool mix_supported(int H, int hc, int LW, int S) {
+  const int nb = hc * H / 32, L = lanes_for_blocks(nb);
+  return nb % L == 0 && nb / L >= 4 && nb / L <= 7 && hc <= 8 && LW % 32 == 0 && S * LW <= MAX_TOKENS * 512 &&
+         S * (LW / 32) <= MAX_TOKENS * 12 && H % 32 == 0;
+}
+
+hipError_t launch_mixer(const MixArgs& a, hipStream_t st) {
+  hipError_t e = mix_down(a, st);
+  if (e != hipSuccess) return e;
+  switch (mix_classes(a.hc * a.H)) {
+    case 4: return mix_up4(a, st);
+    case 2: return mix_up2(a, st);
+    default: return mix_up1(a, st);
+  }
+}
+
+}  // namespace mtpx

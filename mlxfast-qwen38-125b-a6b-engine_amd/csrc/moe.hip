@@ -155,6 +155,7 @@ __device__ void route_body(const MoeArgs& a) {
   if (t == 0) {
     const int n = __popcll(leadmask[0]) + (MK > 64 ? __popcll(leadmask[1]) : 0);
     d->n_unique = n;
+    if (a.nu_out) *a.nu_out = n;
     d->expert[n] = -1;
     d->count[n] = M;
     for (int m = 0; m < M; ++m) d->slot[n][m] = (int16_t)(MK + m);

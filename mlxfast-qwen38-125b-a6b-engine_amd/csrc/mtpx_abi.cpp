@@ -203,7 +203,7 @@ size_t moe_ws_bytes(const mtpx_moe_weights* w, int M) {
 // Enqueue the MoE block; workspace already reserved.
 int moe_enqueue(Ctx* c, const mtpx_moe_weights* w, const uint16_t* x, int M, uint16_t* y, int32_t* idx,
                 float* wts, float* logits, const uint16_t* resid = nullptr, uint16_t* y2 = nullptr,
-                uint32_t* xp_ready = nullptr) {
+                uint32_t* xp_ready = nullptr, int32_t* nu_out = nullptr) {
   MoeArgs a;
   a.H = w->hidden;
   a.E = w->experts;
@@ -237,6 +237,7 @@ int moe_enqueue(Ctx* c, const mtpx_moe_weights* w, const uint16_t* x, int M, uin
   a.resid = resid;
   a.y2 = y2;
   a.ticket = c->tickets;
+  a.nu_out = nu_out;
   c->last_disp = a.disp;
   c->last_H = a.H;
   c->last_E = a.E;
@@ -498,6 +499,25 @@ int hc_mix_enqueue(Ctx* c, const HcGeom& g, const mtpx_hc_weights* hw, const uin
                    int S, uint16_t* x, uint16_t* j, uint32_t* xpH) {
   const int H = g.H, W = g.hc * H, LW = g.LW, gs = g.gs;
   hipStream_t st = c->stream;
+  if (mix_supported(H, g.hc, LW, S)) {
+    MixArgs a;
+    a.H = H;
+    a.hc = g.hc;
+    a.LW = LW;
+    a.gs = gs;
+    a.S = S;
+    a.dw = hw->down.w; a.ds = hw->down.s; a.db = hw->down.b; a.dsb = hw->down.sb;
+    a.iw = hw->inject.w; a.is = hw->inject.s; a.ib = hw->inject.b; a.isb = hw->inject.sb;
+    a.uw = hw->up.w; a.us = hw->up.s; a.ub = hw->up.b; a.usb = hw->up.sb;
+    a.xpW = xpW;
+    a.normed = reinterpret_cast<const bf16*>(normed);
+    a.part = ws_take<float>(c, (size_t)mix_classes(W) * S * (LW + g.hc));
+    a.x = reinterpret_cast<bf16*>(x);
+    a.j = reinterpret_cast<bf16*>(j);
+    a.xpH = xpH;
+    LAUNCH(c, "mixer", launch_mixer(a, st));
+    return MTPX_OK;
+  }
   uint16_t* lo = ws_take<uint16_t>(c, (size_t)S * LW);
   uint16_t* act = ws_take<uint16_t>(c, (size_t)S * LW);
   uint16_t* inj = ws_take<uint16_t>(c, (size_t)S * g.hc);
@@ -874,6 +894,7 @@ struct TargetState {
   std::vector<Kv*> kv;          // per layer (attention layers), else null
   std::vector<GdnState*> gdn;   // per layer (GDN layers), else null
   std::vector<void*> allocs;
+  int32_t* moe_unique = nullptr;  // device [num_layers]: distinct routed experts of the last verify
   int64_t offset = 0;           // committed positions
   int window = 0;
 };
@@ -920,6 +941,7 @@ void target_release(Target* t) {
 }
 
 void target_state_release(TargetState* s) {
+  if (s->moe_unique) hipFree(s->moe_unique);
   for (Kv* kv : s->kv)
     if (kv) {
       hipFree(kv->k);
@@ -1551,6 +1573,12 @@ int mtpx_target_state_new(mtpx_ctx h, mtpx_target th, mtpx_target_state* out) {
   s->kv.assign(n, nullptr);
   s->gdn.assign(n, nullptr);
   int rc = MTPX_OK;
+  if (hipMalloc((void**)&s->moe_unique, 4 * (size_t)n) != hipSuccess) {
+    s->moe_unique = nullptr;
+    rc = fail(MTPX_ERR_OOM, "target state");
+  } else if (hipMemsetAsync(s->moe_unique, 0, 4 * (size_t)n, c->stream) != hipSuccess) {
+    rc = fail(MTPX_ERR_HIP, "target state");
+  }
   for (int i = 0; i < n && rc == MTPX_OK; ++i) {
     if (t->layers[i].kind == MTPX_LAYER_ATTENTION) {
       mtpx_kv k{nullptr};
@@ -1611,6 +1639,16 @@ int mtpx_target_state_info(mtpx_target_state sh, int64_t* offset, int* window) {
   ARG(s, "null state");
   if (offset) *offset = s->offset;
   if (window) *window = s->window;
+  return MTPX_OK;
+}
+
+int mtpx_target_moe_unique(mtpx_ctx h, mtpx_target_state sh, int32_t* out) {
+  Ctx* c = C(h);
+  TargetState* s = static_cast<TargetState*>(sh.ctx);
+  ARG(c && s && out, "null argument");
+  if (set_device(c)) return MTPX_ERR_HIP;
+  HIP_OK(hipMemcpyAsync(out, s->moe_unique, 4 * s->kv.size(), hipMemcpyDeviceToHost, c->stream));
+  HIP_OK(hipStreamSynchronize(c->stream));
   return MTPX_OK;
 }
 
@@ -1701,7 +1739,8 @@ int mtpx_target_verify(mtpx_ctx h, mtpx_target th, mtpx_target_state sh, const i
     LAUNCH(c, "hc_norm", launch_hc_norm(sA, ao, jA, S, hc, H, 0, L.mlp_hc.norm_scale, eps, sM, nrm, xpW, st));
     c->ws_used = mark;
     if ((rc = hc_mix_enqueue(c, hg, &L.mlp_hc, nrm, xpW, S, x, jM, xpH))) return rc;
-    if ((rc = moe_enqueue(c, &L.moe, x, S, mo, nullptr, nullptr, nullptr, nullptr, nullptr, xpH))) return rc;
+    if ((rc = moe_enqueue(c, &L.moe, x, S, mo, nullptr, nullptr, nullptr, nullptr, nullptr, xpH, s->moe_unique + i)))
+      return rc;
   }
   LAUNCH(c, "hc_norm", launch_hc_norm(sM, mo, jM, S, hc, H, 0, t->final_hc.norm_scale, eps, mt, nrm, xpW, st));
   c->ws_used = mark;

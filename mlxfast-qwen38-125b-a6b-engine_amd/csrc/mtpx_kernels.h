@@ -70,6 +70,7 @@ struct MoeArgs {
   const bf16* resid;   // [M, H] or null: y2 = bf16(resid + y)
   bf16* y2;            // [M, H] or null
   uint32_t* ticket;    // router+route ticket, zero at rest
+  int32_t* nu_out;     // if set: the route also writes the distinct routed expert count here
 };
 constexpr int DOWN_ROWS = 128;
 
@@ -121,6 +122,23 @@ hipError_t launch_hc_norm(const bf16* residual, const bf16* out, const bf16* inj
 hipError_t launch_silu_xprep(const bf16* lo, int S, int LW, bf16* act, uint32_t* xp, hipStream_t st);
 hipError_t launch_hc_mix(const bf16* w, const bf16* normed, const bf16* inj, int S, int hc, int H, bf16* input,
                          bf16* inject_out, uint32_t* xp, hipStream_t st);
+
+// --- hyper-connection mixer in two launches (mixer.hip)
+struct MixArgs {
+  int H, hc, LW, gs, S;
+  const uint32_t* dw; const bf16 *ds, *db; const uint32_t* dsb;  // down [LW, hc*H]
+  const uint32_t* iw; const bf16 *is, *ib; const uint32_t* isb;  // inject [hc, hc*H] or iw == null
+  const uint32_t* uw; const bf16 *us, *ub; const uint32_t* usb;  // up [hc*H, LW]
+  const uint32_t* xpW;                                           // [S, hc*H/32] prepared normed streams
+  const bf16* normed;                                            // [S, hc*H]
+  float* part;                                                   // [Q, S, LW + hc] class partials
+  bf16* x;                                                       // [S, H] block input
+  bf16* j;                                                       // [S, hc] 2*sigmoid(inject) or null
+  uint32_t* xpH;                                                 // [S, H/32] prepared x or null
+};
+int mix_classes(int W);
+bool mix_supported(int H, int hc, int LW, int S);
+hipError_t launch_mixer(const MixArgs& a, hipStream_t st);
 
 // --- gated-deltanet sublayer core (gdn.hip); head dims 128
 struct GdnArgs {

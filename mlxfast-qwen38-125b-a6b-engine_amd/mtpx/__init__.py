@@ -468,6 +468,11 @@ class TargetState:
     def commit(self, n: int):
         check(self.ctx.lib.mtpx_target_commit(self.h, n), "target_commit")
 
+    def moe_unique(self, num_layers: int):
+        out = (C.c_int32 * num_layers)()
+        check(self.ctx.lib.mtpx_target_moe_unique(self.ctx.h, self.h, C.cast(out, C.c_void_p)), "target_moe_unique")
+        return list(out)
+
 
 def moe_weights_from(tensors: dict, H, E, K, F, gs) -> MoEWeights:
     """Build the C struct from a dict of device tensors named like its fields."""

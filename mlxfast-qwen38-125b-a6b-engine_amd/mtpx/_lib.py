@@ -162,6 +162,7 @@ _SIGS = {
     "mtpx_target_state_info": (INT, [Handle, C.POINTER(I64), C.POINTER(INT)]),
     "mtpx_target_verify": (INT, [Handle, Handle, Handle, P, INT, P, P, P]),
     "mtpx_target_commit": (INT, [Handle, INT]),
+    "mtpx_target_moe_unique": (INT, [Handle, Handle, P]),
     "mtpx_profile_enable": (INT, [Handle, INT]),
     "mtpx_profile_reset": (INT, [Handle]),
     "mtpx_profile_dump": (INT, [Handle, C.c_char_p, C.c_size_t]),

@@ -33,11 +33,17 @@ __global__ __launch_bounds__(MIX_THREADS) void k_mix_down(MixArgs a) {
   constexpr int RPW = 64 / LC;    // rows per wave
   const int W = a.hc * a.H, nb = W / 32, ncb = nb / Q, S = a.S;
   const int NR = a.LW + (a.iw ? a.hc : 0);
-  const int g = blockIdx.y;
+  // Workgroup w -> (row block, class): the Q classes of a row block read the
+  // interleaved 16-byte blocks of the same cache lines, so they get ids 8
+  // apart -- the same XCD (ids go round-robin over the 8 XCDs) and one L2.
+  const int wg = blockIdx.x;
+  const int g = (wg / 8) % Q;
+  const int rb = (wg / (8 * Q)) * 8 + wg % 8;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int subc = lane % LC, grp = lane / LC;
   const int sub = g + Q * subc;  // the lane of the single-launch walk this lane stands in for
-  const int row = blockIdx.x * (4 * RPW) + wave * RPW + grp;
+  const int row = rb * (4 * RPW) + wave * RPW + grp;
+  if (rb * (4 * RPW) >= NR) return;
   const bool valid = row < NR;
   const int r = valid ? row : 0;
   const bool inj = r >= a.LW;
@@ -174,7 +180,8 @@ static hipError_t mix_down_li(const MixArgs& a, hipStream_t st) {
     static size_t cur = 0;
     hipError_t e = ensure_lds(k_mix_down<L, IT>, lds, cur);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((k_mix_down<L, IT>), dim3((NR + RPB - 1) / RPB, Q), dim3(MIX_THREADS), lds, st, a);
+    const int nrb = (NR + RPB - 1) / RPB;
+    hipLaunchKernelGGL((k_mix_down<L, IT>), dim3((nrb + 7) / 8 * 8 * Q), dim3(MIX_THREADS), lds, st, a);
     return hipGetLastError();
   }
 }

@@ -178,7 +178,7 @@ def run_full(args, out):
     import mtpx
 
     M, T0, gs = args.verify_width, args.cached, args.group_size
-    lc, tc = target_cfgs(gs, T0 + 64, args.layers)
+    lc, tc = target_cfgs(gs, T0 + 64 + 16 * args.rounds, args.layers)
     ctx = mtpx.Context(0)
     t_init = time.perf_counter()
     target = mtpx.Target(ctx, mtpx.TargetConfig(mtpx.LayerConfig(**lc), *[tc[k] for k in (
@@ -286,9 +286,140 @@ def run_full(args, out):
         out["roofline"]["traffic_source"] = tr["source"]
     if args.copy_calibration:
         copy_calibration()
+    if not args.no_e2e:
+        state.close()
+        results, best, _ = e2e_sweep(args, ctx, target, lc, tc, time.perf_counter())
+        out["mtp_decode"] = {
+            "what": f"BASELINE config 5 on the same target: MTP speculative decode rounds (drafter steps, verify, "
+                    f"on-device greedy accept read once per round, commit), acceptance forced at "
+                    f"p={args.accept_rate} by a seeded draw; committed tokens/s per draft depth",
+            "tok_s": results[best]["tok_s"], "best_depth": best, "depths": {str(d): r for d, r in results.items()},
+        }
+        state = mtpx.TargetState(ctx, target)
+        state.set_offset(T0)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline_full(target, state, lc, tc, M, kinds, None)
     return out
+
+
+def run_e2e(args, out):
+    """rounds of single-stream MTP speculative decode on the full-depth
+    target with the MTP head: k drafter steps, a verify of the carry + k drafts, the on-device
+    greedy accept (its result read back once per round), the target commit and the drafter
+    finalize.  Random-init drafts almost never match the target, so the accepted count is
+    forced at rate p by a seeded draw (the accept kernel still runs); the bonus token is the
+    target's argmax at the forced position."""
+    import numpy as np
+    import torch
+
+    import mtpx
+
+    T0, gs, p = args.cached, args.group_size, args.accept_rate
+    lc, tc = target_cfgs(gs, T0 + 64 + 16 * args.rounds, args.layers)
+    ctx = mtpx.Context(0)
+    t_init = time.perf_counter()
+    target = mtpx.Target(ctx, mtpx.TargetConfig(mtpx.LayerConfig(**lc), *[tc[k] for k in (
+        "key_heads", "value_heads", "conv_kernel", "num_layers", "full_attention_interval", "hc", "lowrank",
+        "vocab")]), seed=0x5EED0004)
+    results, best, init_s = e2e_sweep(args, ctx, target, lc, tc, t_init)
+    out.update({
+        "value": results[best]["tok_s"],
+        "ms_per_step": results[best]["ms_per_round"],
+        "steps": args.rounds,
+        "config": {
+            "workload": f"BASELINE config 5: single-stream MTP speculative decode rounds on the full-depth "
+                        f"random-init target ({args.layers} layers, PLE block not in the forward) with the MTP "
+                        f"head, after a synthetic committed prefix of {T0} positions; draft depths "
+                        f"{list(args.depths)}; acceptance forced at p={p} by a seeded draw; value = committed "
+                        f"tokens/s at the best depth ({best}); a step = one round",
+            "depths": {str(d): r for d, r in results.items()}, "best_depth": best, "accept_rate": p,
+            "prefix_positions": T0, "layers": args.layers, "group_size": gs, "parallelism": "none (1 GPU)",
+        },
+        "init_s": round(init_s, 1),
+    })
+    return out
+
+
+def e2e_sweep(args, ctx, target, lc, tc, t_init):
+    """Rounds per draft depth on `target` (see run_e2e) -> ({depth: stats}, best depth, init seconds)."""
+    import numpy as np
+    import torch
+
+    import mtpx
+
+    T0, p = args.cached, args.accept_rate
+    head = mtpx.MTPHead(ctx, mtpx.HeadConfig(mtpx.LayerConfig(**dict(lc, max_positions=64 + 16 * args.rounds)),
+                                             tc["hc"], tc["lowrank"], tc["vocab"], 98304, 248044), seed=0x5EED0007)
+    H, V, W = lc["hidden"], tc["vocab"], tc["hc"] * lc["hidden"]
+    g = torch.Generator(device="cuda").manual_seed(0x5EED0008)
+    kinds = [target.layer_weights(i).kind for i in range(args.layers)]
+    init_s = time.perf_counter() - t_init
+    print(f"bench: target and head initialised in {init_s:.1f} s", file=sys.stderr, flush=True)
+    results = {}
+    for k in args.depths:
+        state = mtpx.TargetState(ctx, target)
+        for i, kind in enumerate(kinds):
+            if kind == 1:
+                kp, vp, tmax = state.kv(i).buffers()
+                n_kv = lc["kv_heads"] * tmax * lc["head_dim"]
+                for ptr, tensor in ((kp, 2 * i + 1), (vp, 2 * i + 2)):
+                    mtpx.check(ctx.lib.mtpx_randn_bf16(ctx.h, C.c_void_p(ptr), n_kv, 0x5EED0006, tensor, 1.0),
+                               "randn kv")
+            else:
+                conv = torch.randn(tc["conv_kernel"] - 1, (2 * tc["key_heads"] + tc["value_heads"]) * 128,
+                                   device="cuda", generator=g).to(torch.bfloat16)
+                ssm = torch.randn(tc["value_heads"], 128, 128, device="cuda", generator=g) * 0.05
+                state.gdn(i).load(conv, ssm)
+                torch.cuda.synchronize()
+        state.set_offset(T0)
+        dr = mtpx.Drafter(ctx, head)
+        # the last committed chunk of the prompt: 8 tokens and their multi streams
+        dr.observe(torch.randint(0, V, (8,), device="cuda", generator=g, dtype=torch.int32),
+                   torch.randn(8, W, device="cuda", generator=g).to(torch.bfloat16))
+        ids = torch.empty(k + 1, dtype=torch.int32, device="cuda")
+        ids[0] = int(torch.randint(0, V, (1,), generator=torch.Generator().manual_seed(k)).item())
+        carry = torch.randn(1, W, device="cuda", generator=g).to(torch.bfloat16)
+        mo = torch.empty(k, W, dtype=torch.bfloat16, device="cuda")
+        logits = torch.empty(k + 1, V, dtype=torch.bfloat16, device="cuda")
+        multi = torch.empty(k + 1, W, dtype=torch.bfloat16, device="cuda")
+        amax = torch.empty(k + 1, dtype=torch.int32, device="cuda")
+        out3 = torch.empty(3, dtype=torch.int32, device="cuda")
+        rng = np.random.default_rng(0x5EED0009 + k)
+
+        def round_():
+            for i in range(k):
+                dr.step(ids[i:i + 1], carry if i == 0 else mo[i - 1:i], ids[i + 1:i + 2], mo[i:i + 1])
+            target.verify(state, ids, logits, multi)
+            lf = logits.float()
+            off, _ = state.info()
+            ctx.accept_greedy(lf, ids[1:], off, out3)
+            ctx.argmax_rows(lf, amax)
+            out3.cpu()  # the round's one host read
+            n = 0
+            while n < k and rng.random() < p:
+                n += 1
+            state.commit(n + 1)
+            dr.finalize(n + 1, ids[1:n + 1] if n else None, multi[:n] if n else None)
+            ids[0:1].copy_(amax[n:n + 1])
+            carry.copy_(multi[n:n + 1])
+            return n
+
+        for _ in range(min(4, args.rounds)):
+            round_()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        acc = [round_() for _ in range(args.rounds)]
+        torch.cuda.synchronize()
+        dt = time.perf_counter() - t0
+        toks = sum(a + 1 for a in acc)
+        results[k] = dict(tok_s=round(toks / dt, 2), ms_per_round=round(dt * 1e3 / args.rounds, 3),
+                          mean_accepted=round(sum(acc) / len(acc), 3), tokens=toks, rounds=args.rounds)
+        print(f"bench: depth {k}: {results[k]}", file=sys.stderr, flush=True)
+        dr.close()
+        state.close()
+    head.close()
+    best = max(results, key=lambda d: results[d]["tok_s"])
+    return results, best, init_s
 
 
 def copy_calibration():
@@ -399,12 +530,16 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", choices=("full", "layer"), default="full")
+    ap.add_argument("--workload", choices=("full", "layer", "e2e"), default="full")
+    ap.add_argument("--depths", type=int, nargs="+", default=[1, 2, 3, 4, 5], help="draft depths of the e2e workload")
+    ap.add_argument("--rounds", type=int, default=48, help="timed rounds per depth of the e2e workload")
+    ap.add_argument("--accept-rate", type=float, default=0.7)
     ap.add_argument("--layers", type=int, default=48, help="depth of the full workload")
     ap.add_argument("--verify-width", type=int, default=4)
     ap.add_argument("--cached", type=int, default=1024)
     ap.add_argument("--group-size", type=int, default=64)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-e2e", action="store_true", help="full workload: skip the speculative-decode sweep")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="after the timed steps, copy 256 MiB once (the reference kernel for HBM byte counters)")
     args = ap.parse_args()
@@ -418,7 +553,12 @@ def main() -> int:
         "vs_baseline": None, "dtype": "q4 weights x bf16 activations, exact int24 dot, f32 combine",
         "data": "synthetic (seeded random-init weights, random prefix caches and token ids)",
     }
-    out = run_full(args, out) if args.workload == "full" else run_layer(args, out)
+    if args.workload == "full":
+        out = run_full(args, out)
+    elif args.workload == "layer":
+        out = run_layer(args, out)
+    else:
+        out = run_e2e(args, out)
     print(json.dumps(out))
     return 0
 

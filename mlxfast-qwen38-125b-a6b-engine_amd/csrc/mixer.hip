@@ -25,7 +25,7 @@ namespace mtpx {
 constexpr int MIX_THREADS = 256;
 
 template <int L, int IT>
-__global__ __launch_bounds__(MIX_THREADS) void k_mix_down(MixArgs a) {
+__global__ __launch_bounds__(MIX_THREADS) __attribute__((amdgpu_waves_per_eu(1, 2))) void k_mix_down(MixArgs a) {
   static_assert(IT > 0, "exact lane tiling");
   extern __shared__ uint32_t lds[];  // this class's activation blocks [S][nb/Q]
   constexpr int Q = L < 4 ? L : 4;
@@ -57,10 +57,23 @@ __global__ __launch_bounds__(MIX_THREADS) void k_mix_down(MixArgs a) {
   R.load(wq + (size_t)rr * (W / 8), sc + (size_t)rr * ng, bi + (size_t)rr * ng, sb ? sb + (size_t)rr * P : nullptr,
          nb, a.gs, sub, valid);
   // stage the class's blocks: compact block c = subc' + LC * it holds block g + Q * subc' + L * it
-  for (int i = threadIdx.x; i < S * ncb * (XP_DW / 4); i += MIX_THREADS) {
-    const int q = i % (XP_DW / 4), c = (i / (XP_DW / 4)) % ncb, s = i / (XP_DW / 4) / ncb;
-    const int j = g + Q * (c % LC) + L * (c / LC);
-    reinterpret_cast<uint4*>(lds)[i] = reinterpret_cast<const uint4*>(a.xpW + ((size_t)s * nb + j) * XP_DW)[q];
+  {
+    const int n4 = S * ncb * (XP_DW / 4);
+    for (int base = threadIdx.x; base < n4; base += STAGE_BATCH * MIX_THREADS) {
+      uint4 v[STAGE_BATCH];
+#pragma unroll
+      for (int u = 0; u < STAGE_BATCH; ++u) {
+        const int i0 = base + u * MIX_THREADS, i = i0 < n4 ? i0 : n4 - 1;
+        const int q = i % (XP_DW / 4), c = (i / (XP_DW / 4)) % ncb, s = i / (XP_DW / 4) / ncb;
+        const int j = g + Q * (c % LC) + L * (c / LC);
+        v[u] = reinterpret_cast<const uint4*>(a.xpW + ((size_t)s * nb + j) * XP_DW)[q];
+      }
+#pragma unroll
+      for (int u = 0; u < STAGE_BATCH; ++u) {  // past the end: the last element again (same value)
+        const int i = base + u * MIX_THREADS;
+        reinterpret_cast<uint4*>(lds)[i < n4 ? i : n4 - 1] = v[u];
+      }
+    }
   }
   __syncthreads();
   for (int s = 0; s < S; ++s) {
@@ -87,7 +100,7 @@ __device__ __forceinline__ float class_fold(const float* p, size_t stride) {
 // grid (H/32), MIX_THREADS threads.  Up rows of the block: local row lr = c*32 + i
 // is global row c*H + d0 + i.
 template <int QD, int L, int IT>
-__global__ __launch_bounds__(MIX_THREADS) void k_mix_up(MixArgs a) {
+__global__ __launch_bounds__(MIX_THREADS) __attribute__((amdgpu_waves_per_eu(1, 2))) void k_mix_up(MixArgs a) {
   constexpr int RW = 64 / L;
   constexpr int MAXROWS = 8 * 32;  // hc <= 8
   constexpr int NP = (MAXROWS + 4 * RW - 1) / (4 * RW);
@@ -113,10 +126,18 @@ __global__ __launch_bounds__(MIX_THREADS) void k_mix_up(MixArgs a) {
               a.usb ? a.usb + (size_t)gr * P : nullptr, nbA, a.gs, sub, v);
   }
   // low-rank rows: finish the fold, round, SiLU
-  for (int i = threadIdx.x; i < S * LW; i += MIX_THREADS) {
-    const int s = i / LW, r = i % LW;
-    const float v = class_fold<QD>(a.part + (size_t)s * NR + r, (size_t)S * NR);
-    act[i] = f2bf(silu_bf16(round_bf(v)));
+  for (int base = threadIdx.x; base < S * LW; base += 4 * MIX_THREADS) {
+    float v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {  // the loads of four elements in flight together
+      const int i0 = base + u * MIX_THREADS, i = i0 < S * LW ? i0 : S * LW - 1;
+      v[u] = class_fold<QD>(a.part + (size_t)(i / LW) * NR + i % LW, (size_t)S * NR);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {  // past the end: the last element again (same value)
+      const int i = base + u * MIX_THREADS;
+      act[i < S * LW ? i : S * LW - 1] = f2bf(silu_bf16(round_bf(v[u])));
+    }
   }
   if (blockIdx.x == 0 && a.iw && a.j && (int)threadIdx.x < S * hc) {
     const int s = threadIdx.x / hc, c = threadIdx.x % hc;
@@ -151,11 +172,13 @@ __global__ __launch_bounds__(MIX_THREADS) void k_mix_up(MixArgs a) {
     const int s = s0 + (int)(threadIdx.x >> 5), i = threadIdx.x & 31;
     bf16 y = 0;
     if (s < S) {
+      float nv[8];
+#pragma unroll
+      for (int c = 0; c < 8; ++c) nv[c] = c < hc ? bf2f(a.normed[(size_t)s * W + (size_t)c * H + d0 + i]) : 0.0f;
       float acc = 0.0f;
-      for (int c = 0; c < hc; ++c) {
-        const float n = bf2f(a.normed[(size_t)s * W + (size_t)c * H + d0 + i]);
-        acc = round_bf(acc + round_bf(sigmoid_bf16(bf2f(wl[s][c * 32 + i])) * n));
-      }
+#pragma unroll
+      for (int c = 0; c < 8; ++c)
+        if (c < hc) acc = round_bf(acc + round_bf(sigmoid_bf16(bf2f(wl[s][c * 32 + i])) * nv[c]));
       y = f2bf(acc);
       a.x[(size_t)s * H + d0 + i] = y;
     }

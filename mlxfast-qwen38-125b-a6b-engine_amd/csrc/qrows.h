@@ -23,30 +23,42 @@ struct QRow {
   static constexpr int NB = IT ? IT : QMV_IT;
   uint32_t w[NB][4];
   uint32_t sb[NB];  // bf16 scale in the low half, bf16 bias in the high half
+  bool ok;          // a real row: dot() of a padding row is 0
 
-  // sbrow: this row's packed pairs (null: the checkpoint's scale and bias rows)
+  // sbrow: this row's packed pairs (null: the checkpoint's scale and bias rows).
+  // A padding row (valid false) must still point at a real row of the matrix:
+  // its loads are issued like any other (no branch, so no wait at a join) and
+  // its dot is forced to 0.
   __device__ __forceinline__ void load(const uint32_t* __restrict__ wrow, const bf16* __restrict__ srow,
                                        const bf16* __restrict__ brow, const uint32_t* __restrict__ sbrow, int nb,
                                        int gs, int sub, bool valid) {
+    ok = valid;
 #pragma unroll
     for (int it = 0; it < NB; ++it) {
       const int j = sub + it * L;
-      if (valid && (IT ? true : j < nb)) {
+      if (IT ? true : j < nb) {
         const uint4 v = ldg16(wrow + (size_t)j * 4);
         w[it][0] = v.x;
         w[it][1] = v.y;
         w[it][2] = v.z;
         w[it][3] = v.w;
-        if (!sbrow) {
-          const int g = gs == 64 ? (j >> 1) : j;  // group of block j (gs is 32 or 64)
-          sb[it] = (uint32_t)srow[g] | ((uint32_t)brow[g] << 16);
-        }
       } else {
         w[it][0] = w[it][1] = w[it][2] = w[it][3] = 0u;
-        sb[it] = 0u;
       }
     }
-    if (sbrow && valid) {
+    if (!sbrow) {  // every scale and bias load in flight before the first merge
+      uint32_t sv[NB], bv[NB];
+#pragma unroll
+      for (int it = 0; it < NB; ++it) {
+        const int j = sub + it * L;
+        const int g = gs == 64 ? (j >> 1) : j;  // group of block j (gs is 32 or 64)
+        const bool in = IT ? true : j < nb;
+        sv[it] = in ? srow[g] : 0u;
+        bv[it] = in ? brow[g] : 0u;
+      }
+#pragma unroll
+      for (int it = 0; it < NB; ++it) sb[it] = sv[it] | (bv[it] << 16);
+    } else {
       const int nbv = IT ? IT : (nb + L - 1) / L;  // entries per lane class
       const uint32_t* e = sbrow + (size_t)(gs == 64 ? (sub >> 1) : sub) * nbv;
       if constexpr (IT != 0) {
@@ -81,7 +93,7 @@ struct QRow {
         acc = block_accum(acc, block_dot(w[it], xl), s, b, xl);
       }
     }
-    return acc;
+    return ok ? acc : 0.0f;
   }
 };
 
@@ -104,16 +116,35 @@ __device__ __forceinline__ void dot2(const QRow<L, IT>& A, const QRow<L, IT>& B,
     // keep one block's activation words live at a time (no hoisting across blocks)
     __builtin_amdgcn_sched_barrier(0);
   }
-  ra = a;
-  rb = b;
+  ra = A.ok ? a : 0.0f;
+  rb = B.ok ? b : 0.0f;
 }
 
 // Copy `words` dwords global -> LDS, 16 bytes per access when both ends allow it.
+// Each thread issues STAGE_BATCH loads before its first LDS store: one memory
+// round trip per batch instead of one per element.  Indices past the end are
+// clamped to the last element for the load and the store alike (that element is
+// rewritten with its own value), so no load sits behind a condition the
+// compiler could sink it into.
+constexpr int STAGE_BATCH = 8;
 __device__ __forceinline__ void stage16(uint32_t* __restrict__ dst, const uint32_t* __restrict__ src, int words) {
   if ((((uintptr_t)src | (uintptr_t)dst) & 15) == 0 && (words & 3) == 0) {
     const uint4* s4 = reinterpret_cast<const uint4*>(src);
     uint4* d4 = reinterpret_cast<uint4*>(dst);
-    for (int i = threadIdx.x; i < words / 4; i += blockDim.x) d4[i] = s4[i];
+    const int n4 = words / 4, step = blockDim.x;
+    for (int base = threadIdx.x; base < n4; base += STAGE_BATCH * step) {
+      uint4 v[STAGE_BATCH];
+#pragma unroll
+      for (int u = 0; u < STAGE_BATCH; ++u) {
+        const int i = base + u * step;
+        v[u] = s4[i < n4 ? i : n4 - 1];
+      }
+#pragma unroll
+      for (int u = 0; u < STAGE_BATCH; ++u) {
+        const int i = base + u * step;
+        d4[i < n4 ? i : n4 - 1] = v[u];
+      }
+    }
   } else {
     for (int i = threadIdx.x; i < words; i += blockDim.x) dst[i] = src[i];
   }

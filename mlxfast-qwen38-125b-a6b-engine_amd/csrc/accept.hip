@@ -23,15 +23,21 @@ __device__ __forceinline__ VI vi_best(VI a, VI b) {
   return a;
 }
 
+template <int OFF>
+__device__ __forceinline__ VI vi_xor(VI x) {
+  VI o;
+  o.v = lane_xor_f<OFF>(x.v);
+  o.i = lane_xor_i<OFF>(x.i);
+  return vi_best(x, o);
+}
+
 __device__ __forceinline__ VI wave_best(VI x) {
-#pragma unroll
-  for (int off = 32; off >= 1; off /= 2) {
-    VI o;
-    o.v = __shfl_xor(x.v, off, 64);
-    o.i = __shfl_xor(x.i, off, 64);
-    x = vi_best(x, o);
-  }
-  return x;
+  x = vi_xor<32>(x);
+  x = vi_xor<16>(x);
+  x = vi_xor<8>(x);
+  x = vi_xor<4>(x);
+  x = vi_xor<2>(x);
+  return vi_xor<1>(x);
 }
 
 __device__ __forceinline__ float ld_val(const float* p) { return *p; }

@@ -246,10 +246,14 @@ __global__ __launch_bounds__(256) void k_attn_combine(const float* __restrict__ 
   float M = -__uint_as_float(0x7f800000u);
   for (int c = t; c < nch; c += nt)
     if (lc[c] > 0.0f && mc[c] > M) M = mc[c];
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) {
-    const float o = __shfl_xor(M, off, 64);
-    M = o > M ? o : M;
+  {
+    float o;
+    o = lane_xor_f<32>(M); M = o > M ? o : M;
+    o = lane_xor_f<16>(M); M = o > M ? o : M;
+    o = lane_xor_f<8>(M); M = o > M ? o : M;
+    o = lane_xor_f<4>(M); M = o > M ? o : M;
+    o = lane_xor_f<2>(M); M = o > M ? o : M;
+    o = lane_xor_f<1>(M); M = o > M ? o : M;
   }
   if ((t & 63) == 0) red[t >> 6] = M;
   __syncthreads();

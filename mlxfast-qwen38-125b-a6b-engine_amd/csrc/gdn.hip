@@ -70,9 +70,7 @@ __device__ __forceinline__ float sigmoid_f32(float x) {
 }
 
 __device__ __forceinline__ float half_wave_sum(float v) {
-#pragma unroll
-  for (int off = 16; off >= 1; off /= 2) v = v + __shfl_xor(v, off, 32);
-  return v;
+  return fold_sum<16>(v);
 }
 
 // Row r of the virtual input sequence conv_cur (KC-1 rows) ++ the P committed

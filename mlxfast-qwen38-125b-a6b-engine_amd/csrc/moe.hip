@@ -95,11 +95,19 @@ __device__ void route_body(const MoeArgs& a) {
           bj = j;
         }
       float gmax = bv;
-#pragma unroll
-      for (int off = 32; off >= 1; off /= 2) gmax = fmaxf(gmax, __shfl_xor(gmax, off, 64));
+      gmax = fmaxf(gmax, lane_xor_f<32>(gmax));
+      gmax = fmaxf(gmax, lane_xor_f<16>(gmax));
+      gmax = fmaxf(gmax, lane_xor_f<8>(gmax));
+      gmax = fmaxf(gmax, lane_xor_f<4>(gmax));
+      gmax = fmaxf(gmax, lane_xor_f<2>(gmax));
+      gmax = fmaxf(gmax, lane_xor_f<1>(gmax));
       int cand = (bj >= 0 && bv == gmax) ? lane + 64 * bj : 0x7fffffff;
-#pragma unroll
-      for (int off = 32; off >= 1; off /= 2) cand = min(cand, __shfl_xor(cand, off, 64));
+      cand = min(cand, lane_xor_i<32>(cand));
+      cand = min(cand, lane_xor_i<16>(cand));
+      cand = min(cand, lane_xor_i<8>(cand));
+      cand = min(cand, lane_xor_i<4>(cand));
+      cand = min(cand, lane_xor_i<2>(cand));
+      cand = min(cand, lane_xor_i<1>(cand));
       if (bj >= 0 && cand == lane + 64 * bj) taken |= 1u << bj;
       // only NaN logits leave no candidate; keep the index addressable
       if (cand >= E) cand = 0;

@@ -26,6 +26,51 @@ __device__ __forceinline__ bf16 f2bf(float f) {
 
 __device__ __forceinline__ float round_bf(float f) { return bf2f(f2bf(f)); }
 
+// The value lane (lane ^ OFF) holds, exactly, from register-file cross-lane
+// operations instead of an LDS permute: DPP quad permutes (OFF 1, 2), a row
+// shift pair (OFF 4), a row rotate (OFF 8; a 16-lane row rotated by 8 is the
+// xor), and the permlane row swaps (OFF 16, 32).  Every lane of the 2*OFF-lane
+// group must be active.
+__device__ __forceinline__ int lane_id() { return (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)); }
+
+template <int OFF>
+__device__ __forceinline__ uint32_t lane_xor(uint32_t v) {
+  static_assert(OFF == 1 || OFF == 2 || OFF == 4 || OFF == 8 || OFF == 16 || OFF == 32, "a power of two <= 32");
+  const int x = (int)v;
+  if constexpr (OFF == 1) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+  } else if constexpr (OFF == 2) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
+  } else if constexpr (OFF == 4) {
+    const int up = __builtin_amdgcn_update_dpp(0, x, 0x104, 0xF, 0xF, false);  // row_shl:4 (lane + 4)
+    const int dn = __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, false);  // row_shr:4 (lane - 4)
+    return (uint32_t)((lane_id() & 4) ? dn : up);
+  } else if constexpr (OFF == 8) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, x, 0x128, 0xF, 0xF, false);  // row_ror:8
+  } else if constexpr (OFF == 16) {
+    const auto p = __builtin_amdgcn_permlane16_swap(v, v, false, false);  // {r0,r0,r2,r2}, {r1,r1,r3,r3}
+    return (lane_id() & 16) ? p[0] : p[1];
+  } else {
+    const auto p = __builtin_amdgcn_permlane32_swap(v, v, false, false);  // {lo,lo}, {hi,hi}
+    return (lane_id() & 32) ? p[0] : p[1];
+  }
+}
+template <int OFF>
+__device__ __forceinline__ float lane_xor_f(float v) { return __uint_as_float(lane_xor<OFF>(__float_as_uint(v))); }
+template <int OFF>
+__device__ __forceinline__ int lane_xor_i(int v) { return (int)lane_xor<OFF>((uint32_t)v); }
+
+// v + v[lane ^ OFF] for OFF = TOP, TOP/2, ..., 1 (highest level first)
+template <int TOP>
+__device__ __forceinline__ float fold_sum(float v) {
+  if constexpr (TOP >= 1) {
+    v = v + lane_xor_f<TOP>(v);
+    return fold_sum<TOP / 2>(v);
+  } else {
+    return v;
+  }
+}
+
 // exp(x): Cody-Waite split with a two-part ln2, degree-7 Taylor polynomial on
 // |r| <= ln2/2, 2^n applied in two exact steps; x < -87.3 -> 0, x > 88.7 -> inf.
 __device__ __forceinline__ float expf_det(float x) {
@@ -147,18 +192,21 @@ __device__ __forceinline__ void xprep_lanes_build(uint32_t h, int i, uint32_t* s
   const int field = (h >> 7) & 0xff;
   const int f = field < 1 ? 1 : field;
   int E = f;
-#pragma unroll
-  for (int off = 16; off >= 1; off /= 2) {
-    const int o = __shfl_xor(E, off, 32);
-    E = o > E ? o : E;
-  }
+  E = max(E, lane_xor_i<16>(E));
+  E = max(E, lane_xor_i<8>(E));
+  E = max(E, lane_xor_i<4>(E));
+  E = max(E, lane_xor_i<2>(E));
+  E = max(E, lane_xor_i<1>(E));
   const int32_t sig = (int32_t)((field ? 0x80u : 0u) | (h & 0x7fu));
   const int sh = f - E + 15;
   const int32_t mag = (sh >= 0) ? (sig << sh) : ((sh > -31) ? (sig >> (-sh)) : 0);
   const int32_t m = (h & 0x8000u) ? -mag : mag;
   int32_t sm = m;
-#pragma unroll
-  for (int off = 16; off >= 1; off /= 2) sm += __shfl_xor(sm, off, 32);
+  sm += lane_xor_i<16>(sm);
+  sm += lane_xor_i<8>(sm);
+  sm += lane_xor_i<4>(sm);
+  sm += lane_xor_i<2>(sm);
+  sm += lane_xor_i<1>(sm);
   const uint32_t u = (uint32_t)m & 0xffffffu;
   const int t = i >> 3, k8 = i & 7;
   const int slot = (k8 & 1) ? 4 + t : t;
@@ -222,16 +270,10 @@ __device__ __forceinline__ float block_accum(float acc, float dxraw, float s, fl
 // xor butterfly over groups of L lanes (every lane of the group ends with the sum)
 template <int L>
 __device__ __forceinline__ float lane_fold(float v) {
-#pragma unroll
-  for (int off = L / 2; off >= 1; off /= 2) v = v + __shfl_xor(v, off, 64);
-  return v;
+  return fold_sum<L / 2>(v);
 }
 
-__device__ __forceinline__ float wave_fold64(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off /= 2) v = v + __shfl_xor(v, off, 64);
-  return v;
-}
+__device__ __forceinline__ float wave_fold64(float v) { return fold_sum<32>(v); }
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 

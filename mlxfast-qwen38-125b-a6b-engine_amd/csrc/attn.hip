@@ -223,7 +223,6 @@ __global__ __launch_bounds__(256) void k_attn_combine(const float* __restrict__ 
                                                       int nch, const bf16* __restrict__ qkv, int QW, int gate_off,
                                                       bf16* __restrict__ out, bf16* __restrict__ out_gated,
                                                       uint32_t* __restrict__ xp_gated) {
-  __shared__ uint32_t scratch[8][24];
   __shared__ float mc[COMBINE_MAXCH], fc[COMBINE_MAXCH], lc[COMBINE_MAXCH], red[4];
   const int ri = blockIdx.x, hk = blockIdx.y;
   const int G = HQ / HK, R = S * G;
@@ -287,17 +286,10 @@ __global__ __launch_bounds__(256) void k_attn_combine(const float* __restrict__ 
         out_gated[(size_t)s * HQ * D + h * D + d] = gated;
       }
     }
-    if (xp_gated) {
+    if (xp_gated && d < D) {
       // block (h*D + d) / 32 of row s; D % 32 == 0 so blocks never straddle heads
-      const int grp = threadIdx.x >> 5, i = threadIdx.x & 31;
-      int E, sm;
-      xprep_lanes_build(gated, i, scratch[grp], E, sm);
-      __syncthreads();
-      if (d < D) {
-        const size_t blk = (size_t)s * (HQ * D / 32) + (h * D + d0) / 32 + grp;
-        xprep_lanes_store(i, scratch[grp], E, sm, xp_gated + blk * XP_DW);
-      }
-      __syncthreads();
+      const size_t blk = (size_t)s * (HQ * D / 32) + (h * D + d0) / 32 + (threadIdx.x >> 5);
+      xprep_lanes_direct(gated, threadIdx.x & 31, xp_gated + blk * XP_DW);
     }
   }
 }
@@ -314,7 +306,6 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const bf16* __restrict__ x, con
                                                  bf16* __restrict__ sum_out, bf16* __restrict__ y,
                                                  uint32_t* __restrict__ xp) {
   __shared__ float wsum[4];
-  __shared__ uint32_t scratch[8][24];
   const int m = blockIdx.x, t = threadIdx.x, sl = blockIdx.y;
   const bf16* xr = x + (size_t)m * H;
   const bf16* rr = resid ? resid + (size_t)m * H : nullptr;
@@ -349,13 +340,7 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const bf16* __restrict__ x, con
     out = f2bf(bf2f(w[i]) * round_bf(vo * inv));
     y[(size_t)m * H + i] = out;
   }
-  if (xp) {
-    const int grp = t >> 5, li = t & 31;
-    int E, sm;
-    xprep_lanes_build(out, li, scratch[grp], E, sm);
-    __syncthreads();
-    if (i < H) xprep_lanes_store(li, scratch[grp], E, sm, xp + ((size_t)m * (H / 32) + i / 32) * XP_DW);
-  }
+  if (xp && i < H) xprep_lanes_direct(out, t & 31, xp + ((size_t)m * (H / 32) + i / 32) * XP_DW);
 }
 
 __global__ void k_add(const bf16* __restrict__ a, const bf16* __restrict__ b, int64_t n, bf16* __restrict__ out) {

@@ -88,7 +88,6 @@ __global__ __launch_bounds__(GDN_THREADS) void k_gdn_step(GdnArgs a) {
   __shared__ float qs[MAX_TOKENS][GDN_D], ks[MAX_TOKENS][GDN_D], vs[MAX_TOKENS][GDN_D], ys[MAX_TOKENS][GDN_D];
   __shared__ float dec[MAX_TOKENS], bet[MAX_TOKENS];
   __shared__ bf16 gated[MAX_TOKENS][GDN_D];
-  __shared__ uint32_t scratch[GDN_THREADS / 32][24];
   const int h = blockIdx.x, ratio = a.hv / a.hk, hk = h / ratio;
   const bool lead = (h % ratio) == 0;  // writes the q/k channels' journal and conv rows
   const int hw = threadIdx.x >> 5, l = threadIdx.x & 31;
@@ -225,17 +224,11 @@ __global__ __launch_bounds__(GDN_THREADS) void k_gdn_step(GdnArgs a) {
   __syncthreads();
 
   // ---- prepared blocks of the gated rows for the output projection (4 per head and position)
-#pragma unroll
-  for (int round = 0; round < 2; ++round) {
-    const int task = hw + round * (GDN_THREADS / 32);
-    const bool act = a.xp && task < 4 * S;
-    const int t = task >> 2, blk = task & 3;
-    int E = 0, sm = 0;
-    if (act) xprep_lanes_build(gated[t][blk * 32 + l], l, scratch[hw], E, sm);
-    __syncthreads();
-    if (act) xprep_lanes_store(l, scratch[hw], E, sm, a.xp + ((size_t)t * a.hv * 4 + h * 4 + blk) * XP_DW);
-    __syncthreads();
-  }
+  if (a.xp)
+    for (int task = hw; task < 4 * S; task += GDN_THREADS / 32) {
+      const int t = task >> 2, blk = task & 3;
+      xprep_lanes_direct(gated[t][blk * 32 + l], l, a.xp + ((size_t)t * a.hv * 4 + h * 4 + blk) * XP_DW);
+    }
 }
 
 // Committed state without modifying it: the P journal steps replayed onto the

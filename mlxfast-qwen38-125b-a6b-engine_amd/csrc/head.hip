@@ -53,7 +53,6 @@ __global__ __launch_bounds__(256) void k_hc_norm(const bf16* __restrict__ residu
                                                  bf16* __restrict__ stream, bf16* __restrict__ normed,
                                                  uint32_t* __restrict__ xp) {
   __shared__ float wsum[4];
-  __shared__ uint32_t scratch[8][24];
   const int c = blockIdx.x, s = blockIdx.y, sl = blockIdx.z, t = threadIdx.x;
   const size_t W = (size_t)hc * H;
   const size_t base = (size_t)s * W + (size_t)c * H;
@@ -94,30 +93,20 @@ __global__ __launch_bounds__(256) void k_hc_norm(const bf16* __restrict__ residu
     n = f2bf(bf2f(scale[(size_t)c * H + d]) * round_bf(vo * inv));
     normed[base + d] = n;
   }
-  if (xp) {  // blocks of the normed row [S, hc*H]: H % 32 == 0, so a block never straddles streams
-    const int grp = t >> 5, li = t & 31;
-    int E, sm;
-    xprep_lanes_build(n, li, scratch[grp], E, sm);
-    __syncthreads();
-    if (d < H) xprep_lanes_store(li, scratch[grp], E, sm, xp + (base + d) / 32 * XP_DW);
-  }
+  // blocks of the normed row [S, hc*H]: H % 32 == 0, so a block never straddles streams
+  if (xp && d < H) xprep_lanes_direct(n, t & 31, xp + (base + d) / 32 * XP_DW);
 }
 
 // grid (S, ceil(LW/256)), 256 threads; LW % 32 == 0.
 __global__ __launch_bounds__(256) void k_silu_xprep(const bf16* __restrict__ lo, int LW, bf16* __restrict__ act,
                                                     uint32_t* __restrict__ xp) {
-  __shared__ uint32_t scratch[8][24];
   const int s = blockIdx.x, j = blockIdx.y * 256 + threadIdx.x;
   bf16 a = 0;
   if (j < LW) {
     a = f2bf(silu_bf16(bf2f(lo[(size_t)s * LW + j])));
     act[(size_t)s * LW + j] = a;
   }
-  const int grp = threadIdx.x >> 5, li = threadIdx.x & 31;
-  int E, sm;
-  xprep_lanes_build(a, li, scratch[grp], E, sm);
-  __syncthreads();
-  if (j < LW) xprep_lanes_store(li, scratch[grp], E, sm, xp + ((size_t)s * LW + j) / 32 * XP_DW);
+  if (j < LW) xprep_lanes_direct(a, threadIdx.x & 31, xp + ((size_t)s * LW + j) / 32 * XP_DW);
 }
 
 // grid (S, ceil(H/256)), 256 threads.
@@ -125,7 +114,6 @@ __global__ __launch_bounds__(256) void k_hc_mix(const bf16* __restrict__ w, cons
                                                 const bf16* __restrict__ inj, int hc, int H,
                                                 bf16* __restrict__ input, bf16* __restrict__ inject_out,
                                                 uint32_t* __restrict__ xp) {
-  __shared__ uint32_t scratch[8][24];
   const int s = blockIdx.x, d = blockIdx.y * 256 + threadIdx.x;
   const size_t W = (size_t)hc * H;
   bf16 y = 0;
@@ -140,13 +128,7 @@ __global__ __launch_bounds__(256) void k_hc_mix(const bf16* __restrict__ w, cons
   }
   if (inj && inject_out && blockIdx.y == 0 && threadIdx.x < hc)
     inject_out[(size_t)s * hc + threadIdx.x] = f2bf(2.0f * sigmoid_bf16(bf2f(inj[(size_t)s * hc + threadIdx.x])));
-  if (xp) {
-    const int grp = threadIdx.x >> 5, li = threadIdx.x & 31;
-    int E, sm;
-    xprep_lanes_build(y, li, scratch[grp], E, sm);
-    __syncthreads();
-    if (d < H) xprep_lanes_store(li, scratch[grp], E, sm, xp + ((size_t)s * H + d) / 32 * XP_DW);
-  }
+  if (xp && d < H) xprep_lanes_direct(y, threadIdx.x & 31, xp + ((size_t)s * H + d) / 32 * XP_DW);
 }
 
 // ---------------------------------------------------------------------------

@@ -53,28 +53,18 @@ __global__ __launch_bounds__(MIX_THREADS) __attribute__((amdgpu_waves_per_eu(1, 
   const bf16* sc = inj ? a.is : a.ds;
   const bf16* bi = inj ? a.ib : a.db;
   const uint32_t* sb = inj ? a.isb : a.dsb;
+  // stage the class's blocks with LDS-direct loads: compact block c = subc' + LC * it holds
+  // block g + Q * subc' + L * it; unit i = (s * ncb + c) * 7 + q
+  const int n4 = S * ncb * (XP_DW / 4);
+  for (int i = threadIdx.x; i < n4; i += MIX_THREADS) {
+    const int q = i % (XP_DW / 4), c = (i / (XP_DW / 4)) % ncb, s = i / (XP_DW / 4) / ncb;
+    const int j = g + Q * (c % LC) + L * (c / LC);
+    lds_dma16(reinterpret_cast<uint4*>(lds) + (i - lane), a.xpW + ((size_t)s * nb + j) * XP_DW + 4 * q);
+  }
   QRow<L, IT> R;
   R.load(wq + (size_t)rr * (W / 8), sc + (size_t)rr * ng, bi + (size_t)rr * ng, sb ? sb + (size_t)rr * P : nullptr,
          nb, a.gs, sub, valid);
-  // stage the class's blocks: compact block c = subc' + LC * it holds block g + Q * subc' + L * it
-  {
-    const int n4 = S * ncb * (XP_DW / 4);
-    for (int base = threadIdx.x; base < n4; base += STAGE_BATCH * MIX_THREADS) {
-      uint4 v[STAGE_BATCH];
-#pragma unroll
-      for (int u = 0; u < STAGE_BATCH; ++u) {
-        const int i0 = base + u * MIX_THREADS, i = i0 < n4 ? i0 : n4 - 1;
-        const int q = i % (XP_DW / 4), c = (i / (XP_DW / 4)) % ncb, s = i / (XP_DW / 4) / ncb;
-        const int j = g + Q * (c % LC) + L * (c / LC);
-        v[u] = reinterpret_cast<const uint4*>(a.xpW + ((size_t)s * nb + j) * XP_DW)[q];
-      }
-#pragma unroll
-      for (int u = 0; u < STAGE_BATCH; ++u) {  // past the end: the last element again (same value)
-        const int i = base + u * MIX_THREADS;
-        reinterpret_cast<uint4*>(lds)[i < n4 ? i : n4 - 1] = v[u];
-      }
-    }
-  }
+  lds_dma_wait();
   __syncthreads();
   for (int s = 0; s < S; ++s) {
     float acc = 0.0f;
@@ -91,76 +81,84 @@ __global__ __launch_bounds__(MIX_THREADS) __attribute__((amdgpu_waves_per_eu(1, 
 
 // Butterfly levels Q/2 .. 1 over the class partials of one row.
 template <int Q>
-__device__ __forceinline__ float class_fold(const float* p, size_t stride) {
-  if constexpr (Q == 4) return (p[0] + p[2 * stride]) + (p[stride] + p[3 * stride]);
-  if constexpr (Q == 2) return p[0] + p[stride];
-  return p[0];
+__device__ __forceinline__ float class_fold_v(const float* v) {
+  if constexpr (Q == 4) return (v[0] + v[2]) + (v[1] + v[3]);
+  if constexpr (Q == 2) return v[0] + v[1];
+  return v[0];
 }
 
-// grid (H/32), MIX_THREADS threads.  Up rows of the block: local row lr = c*32 + i
-// is global row c*H + d0 + i.
+// grid (H/32), UP_THREADS threads.  Up rows of the block: local row lr = c*32 + i
+// is global row c*H + d0 + i.  The two halves of the workgroup (waves 0-3 and
+// 4-7) walk the same up rows for the even and the odd tokens.
+constexpr int UP_THREADS = 512;
+
 template <int QD, int L, int IT>
-__global__ __launch_bounds__(MIX_THREADS) __attribute__((amdgpu_waves_per_eu(1, 2))) void k_mix_up(MixArgs a) {
+__global__ __launch_bounds__(UP_THREADS) __attribute__((amdgpu_waves_per_eu(1, 2))) void k_mix_up(MixArgs a) {
   constexpr int RW = 64 / L;
   constexpr int MAXROWS = 8 * 32;  // hc <= 8
   constexpr int NP = (MAXROWS + 4 * RW - 1) / (4 * RW);
+  constexpr int FOLD_BATCH = 8;  // S * LW <= FOLD_BATCH * UP_THREADS: one round of partial loads
   __shared__ bf16 act[MAX_TOKENS * 512];             // [S][LW], S * LW <= 4096
   __shared__ uint32_t xpa[MAX_TOKENS * 12 * XP_DW];  // [S][LW/32][XP_DW], S * LW / 32 <= 96
   __shared__ bf16 wl[MAX_TOKENS][MAXROWS];
-  __shared__ uint32_t scratch[MIX_THREADS / 32][24];
   const int S = a.S, H = a.H, hc = a.hc, LW = a.LW, W = hc * H;
   const int NR = LW + (a.iw ? hc : 0);
   const int nbA = LW / 32, ng = LW / a.gs, P = sb_row_len(LW, a.gs);
   const int d0 = blockIdx.x * 32;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int wave = (threadIdx.x >> 6) & 3, half = threadIdx.x >> 8, lane = threadIdx.x & 63;
   const int sub = lane % L, grp = lane / L;
   const int nrows = hc * 32;
-  // up rows first, so their loads are in flight during the low-rank finish
+  // Loads in the order they are needed (the memory counter retires them in
+  // order): the class partials of the low-rank rows (S * LW <= FOLD_BATCH *
+  // UP_THREADS: one round), the normed streams for the mix, then the up rows,
+  // which stream in during the fold, SiLU and activation preparation.
+  float pp[FOLD_BATCH][QD];
+#pragma unroll
+  for (int u = 0; u < FOLD_BATCH; ++u) {
+    const int i0 = threadIdx.x + u * UP_THREADS, i = i0 < S * LW ? i0 : S * LW - 1;
+    const float* p = a.part + (size_t)(i / LW) * NR + i % LW;
+#pragma unroll
+    for (int q = 0; q < QD; ++q) pp[u][q] = p[(size_t)q * S * NR];
+  }
+  const bool jt = blockIdx.x == 0 && a.iw && a.j && (int)threadIdx.x < S * hc;  // inject gate (s, c) of this thread
+  float jp[QD];
+#pragma unroll
+  for (int q = 0; q < QD; ++q)
+    jp[q] = jt ? a.part[(size_t)q * S * NR + (size_t)(threadIdx.x / hc) * NR + LW + threadIdx.x % hc] : 0.0f;
+  const int ms = threadIdx.x >> 5, mi = threadIdx.x & 31;  // the mix: 32 lanes per token
+  float nv[8];  // unconditional loads (token and stream clamped); the mix reads only s < S, c < hc
+#pragma unroll
+  for (int c = 0; c < 8; ++c)
+    nv[c] = bf2f(a.normed[(size_t)(ms < S ? ms : 0) * W + (size_t)(c < hc ? c : 0) * H + d0 + mi]);
   QRow<L, IT> U[NP];
 #pragma unroll
   for (int p = 0; p < NP; ++p) {
+    if (p * 4 * RW >= nrows) break;  // uniform
     const int lr = p * 4 * RW + wave * RW + grp;
     const bool v = lr < nrows;
     const int gr = v ? (lr / 32) * H + d0 + (lr % 32) : 0;
     U[p].load(a.uw + (size_t)gr * (LW / 8), a.us + (size_t)gr * ng, a.ub + (size_t)gr * ng,
               a.usb ? a.usb + (size_t)gr * P : nullptr, nbA, a.gs, sub, v);
   }
-  // low-rank rows: finish the fold, round, SiLU
-  for (int base = threadIdx.x; base < S * LW; base += 4 * MIX_THREADS) {
-    float v[4];
+  // low-rank rows: finish the fold, round, SiLU (past the end: the last element again, same value)
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {  // the loads of four elements in flight together
-      const int i0 = base + u * MIX_THREADS, i = i0 < S * LW ? i0 : S * LW - 1;
-      v[u] = class_fold<QD>(a.part + (size_t)(i / LW) * NR + i % LW, (size_t)S * NR);
-    }
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {  // past the end: the last element again (same value)
-      const int i = base + u * MIX_THREADS;
-      act[i < S * LW ? i : S * LW - 1] = f2bf(silu_bf16(round_bf(v[u])));
-    }
+  for (int u = 0; u < FOLD_BATCH; ++u) {
+    const int i = threadIdx.x + u * UP_THREADS;
+    act[i < S * LW ? i : S * LW - 1] = f2bf(silu_bf16(round_bf(class_fold_v<QD>(pp[u]))));
   }
-  if (blockIdx.x == 0 && a.iw && a.j && (int)threadIdx.x < S * hc) {
-    const int s = threadIdx.x / hc, c = threadIdx.x % hc;
-    const float v = class_fold<QD>(a.part + (size_t)s * NR + LW + c, (size_t)S * NR);
-    a.j[(size_t)s * hc + c] = f2bf(2.0f * sigmoid_bf16(round_bf(v)));
-  }
+  if (jt) a.j[threadIdx.x] = f2bf(2.0f * sigmoid_bf16(round_bf(class_fold_v<QD>(jp))));  // [s * hc + c]
   __syncthreads();
   // prepared blocks of the activations: 32 lanes per block
   const int nblk = S * nbA;
-  for (int b0 = 0; b0 < nblk; b0 += MIX_THREADS / 32) {
-    const int b = b0 + (int)(threadIdx.x >> 5), li = threadIdx.x & 31;
-    int E = 0, sm = 0;
-    if (b < nblk) xprep_lanes_build(act[b * 32 + li], li, scratch[threadIdx.x >> 5], E, sm);
-    __syncthreads();
-    if (b < nblk) xprep_lanes_store(li, scratch[threadIdx.x >> 5], E, sm, xpa + (size_t)b * XP_DW);
-    __syncthreads();
-  }
-  // up rows of the block, every token
+  for (int b = (int)(threadIdx.x >> 5); b < nblk; b += UP_THREADS / 32)
+    xprep_lanes_direct(act[b * 32 + (threadIdx.x & 31)], threadIdx.x & 31, xpa + (size_t)b * XP_DW);
+  __syncthreads();
+  // up rows of the block: this half's tokens
 #pragma unroll
   for (int p = 0; p < NP; ++p) {
     const int lr = p * 4 * RW + wave * RW + grp;
     if (p * 4 * RW >= nrows) break;  // uniform
-    for (int s = 0; s < S; ++s) {
+    for (int s = half; s < S; s += 2) {
       float v = U[p].dot(xpa + (size_t)s * nbA * XP_DW, nbA, sub);
       v = lane_fold<L>(v);
       if (sub == 0 && lr < nrows) wl[s][lr] = f2bf(v);
@@ -168,26 +166,14 @@ __global__ __launch_bounds__(MIX_THREADS) __attribute__((amdgpu_waves_per_eu(1, 
   }
   __syncthreads();
   // mix: 32 lanes per token, then the prepared block of x
-  for (int s0 = 0; s0 < S; s0 += MIX_THREADS / 32) {
-    const int s = s0 + (int)(threadIdx.x >> 5), i = threadIdx.x & 31;
-    bf16 y = 0;
-    if (s < S) {
-      float nv[8];
+  if (ms < S) {
+    float acc = 0.0f;
 #pragma unroll
-      for (int c = 0; c < 8; ++c) nv[c] = c < hc ? bf2f(a.normed[(size_t)s * W + (size_t)c * H + d0 + i]) : 0.0f;
-      float acc = 0.0f;
-#pragma unroll
-      for (int c = 0; c < 8; ++c)
-        if (c < hc) acc = round_bf(acc + round_bf(sigmoid_bf16(bf2f(wl[s][c * 32 + i])) * nv[c]));
-      y = f2bf(acc);
-      a.x[(size_t)s * H + d0 + i] = y;
-    }
-    int E = 0, sm = 0;
-    if (s < S) xprep_lanes_build(y, i, scratch[threadIdx.x >> 5], E, sm);
-    __syncthreads();
-    if (s < S && a.xpH)
-      xprep_lanes_store(i, scratch[threadIdx.x >> 5], E, sm, a.xpH + ((size_t)s * (H / 32) + blockIdx.x) * XP_DW);
-    __syncthreads();
+    for (int c = 0; c < 8; ++c)
+      if (c < hc) acc = round_bf(acc + round_bf(sigmoid_bf16(bf2f(wl[ms][c * 32 + mi])) * nv[c]));
+    const bf16 y = f2bf(acc);
+    a.x[(size_t)ms * H + d0 + mi] = y;
+    if (a.xpH) xprep_lanes_direct(y, mi, a.xpH + ((size_t)ms * (H / 32) + blockIdx.x) * XP_DW);
   }
 }
 
@@ -213,7 +199,7 @@ template <int QD>
 struct MixUp {
   template <int L, int IT>
   static hipError_t go(const MixArgs& a, hipStream_t st) {
-    hipLaunchKernelGGL((k_mix_up<QD, L, IT>), dim3(a.H / 32), dim3(MIX_THREADS), 0, st, a);
+    hipLaunchKernelGGL((k_mix_up<QD, L, IT>), dim3(a.H / 32), dim3(UP_THREADS), 0, st, a);
     return hipGetLastError();
   }
 };
@@ -231,9 +217,13 @@ int mix_classes(int W) {
   return L < 4 ? L : 4;
 }
 
+// Fused path: exact lane tiling of the down rows (4..7 blocks per lane), up rows
+// walked by at most 4 lanes (their registers hold a workgroup's rows without
+// spilling), the low-rank activations and their prepared blocks within LDS.
 bool mix_supported(int H, int hc, int LW, int S) {
   const int nb = hc * H / 32, L = lanes_for_blocks(nb);
-  return nb % L == 0 && nb / L >= 4 && nb / L <= 7 && hc <= 8 && LW % 32 == 0 && S * LW <= MAX_TOKENS * 512 &&
+  return nb % L == 0 && nb / L >= 4 && nb / L <= 7 && hc <= 8 && LW % 32 == 0 && lanes_for_blocks(LW / 32) <= 4 &&
+         S * LW <= MAX_TOKENS * 512 &&
          S * (LW / 32) <= MAX_TOKENS * 12 && H % 32 == 0;
 }
 

@@ -181,16 +181,11 @@ constexpr int ROUTER_IT = 8;  // H <= 8 * 64 * 8
 __global__ __launch_bounds__(RR_THREADS) void k_moe_router_route(MoeArgs a, int row_wgs) {
   const int H = a.H, E = a.E, M = a.M;
   if ((int)blockIdx.x >= row_wgs) {
-    __shared__ uint32_t scratch[RR_THREADS / 32][24];
     const int nb = H / 32;
-    const int g = threadIdx.x >> 5, i = threadIdx.x & 31;
-    const int blk = ((int)blockIdx.x - row_wgs) * (RR_THREADS / 32) + g;
-    const bool valid = blk < M * nb;
-    const uint32_t h = valid ? a.x[(size_t)(blk / nb) * H + (size_t)(blk % nb) * 32 + i] : 0u;
-    int E, sm;
-    xprep_lanes_build(h, i, scratch[g], E, sm);
-    __syncthreads();
-    if (valid) xprep_lanes_store(i, scratch[g], E, sm, a.xp_x + (size_t)blk * XP_DW);
+    const int i = threadIdx.x & 31;
+    const int blk = ((int)blockIdx.x - row_wgs) * (RR_THREADS / 32) + (int)(threadIdx.x >> 5);
+    if (blk < M * nb)
+      xprep_lanes_direct(a.x[(size_t)(blk / nb) * H + (size_t)(blk % nb) * 32 + i], i, a.xp_x + (size_t)blk * XP_DW);
     return;
   }
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -257,7 +252,6 @@ template <int L, int IT, int GU_THREADS>
 __global__ __launch_bounds__(GU_THREADS) void k_moe_gate_up(MoeArgs a) {
   extern __shared__ uint32_t lds[];
   __shared__ bf16 actb[MAX_TOKENS][32];
-  __shared__ uint32_t scratch[MAX_TOKENS][24];
   constexpr int WAVES = GU_THREADS / 64;
   constexpr int RW = 64 / L;                                  // f rows per wave pass
   constexpr int NI = (32 + WAVES * RW - 1) / (WAVES * RW);     // passes for 32 rows
@@ -296,7 +290,7 @@ __global__ __launch_bounds__(GU_THREADS) void k_moe_gate_up(MoeArgs a) {
     const int m = slot_token(a.disp->slot[u][tk], M, K);
     stage16(lds + (size_t)tk * nb * XP_DW, a.xp_x + (size_t)m * nb * XP_DW, nb * XP_DW);
   }
-  __syncthreads();
+  stage_sync();
 #pragma unroll
   for (int p = 0; p < NI; ++p) {
     const int fi = (wave + p * WAVES) * RW + grp;
@@ -317,12 +311,8 @@ __global__ __launch_bounds__(GU_THREADS) void k_moe_gate_up(MoeArgs a) {
   // prepared activation block of this f-block for every slot: 32 lanes per slot
   {
     const int tk = threadIdx.x >> 5, i = threadIdx.x & 31;
-    int E = 0, sm = 0;
-    if (tk < cnt) xprep_lanes_build(actb[tk][i], i, scratch[tk], E, sm);
-    __syncthreads();
     if (tk < cnt)
-      xprep_lanes_store(i, scratch[tk], E, sm,
-                        a.xp_act + ((size_t)a.disp->slot[u][tk] * (F / 32) + blockIdx.x) * XP_DW);
+      xprep_lanes_direct(actb[tk][i], i, a.xp_act + ((size_t)a.disp->slot[u][tk] * (F / 32) + blockIdx.x) * XP_DW);
   }
 }
 
@@ -393,7 +383,7 @@ __global__ __launch_bounds__(256) void k_moe_down(MoeArgs a) {
   }
   for (int tk = 0; tk < cnt; ++tk)
     stage16(lds + (size_t)tk * nb * XP_DW, a.xp_act + (size_t)a.disp->slot[u][tk] * nb * XP_DW, nb * XP_DW);
-  __syncthreads();
+  stage_sync();
 #pragma unroll
   for (int p = 0; p < NI; ++p) {
     if ((wave + 4 * p) * 2 * RW >= DOWN_ROWS) break;  // uniform per wave

@@ -183,12 +183,14 @@ __device__ inline void xprep_block(const bf16* __restrict__ x32, uint32_t* __res
   out[27] = 0u;
 }
 
-// The same prepared block built by 32 consecutive lanes, lane i holding element
-// i (bf16 bits h).  `scratch` is 24 dwords of LDS private to this 32-lane group;
-// the caller must place a workgroup barrier between this call and
-// xprep_lanes_store().  Integer sums are exact, so the lane reduction order
-// does not matter.
-__device__ __forceinline__ void xprep_lanes_build(uint32_t h, int i, uint32_t* scratch, int& E_out, int& sm_out) {
+// The same prepared block built by 32 consecutive lanes (lane i holding
+// element i, bf16 bits h) and written straight to `dst` (28 dwords, LDS or
+// global), with no staging and no barrier: limb word (k, slot) holds byte k of
+// the elements t*8 + par + 2*b (b = 0..3; slot = t or 4 + t for par 0 or 1),
+// so two lane exchanges (xor 2, xor 4) assemble it and lane t*8 + par stores
+// it.  Integer sums are exact, so the lane reduction order does not matter.
+// All 32 lanes of the group must be active.
+__device__ __forceinline__ void xprep_lanes_direct(uint32_t h, int i, uint32_t* __restrict__ dst) {
   const int field = (h >> 7) & 0xff;
   const int f = field < 1 ? 1 : field;
   int E = f;
@@ -208,27 +210,25 @@ __device__ __forceinline__ void xprep_lanes_build(uint32_t h, int i, uint32_t* s
   sm += lane_xor_i<2>(sm);
   sm += lane_xor_i<1>(sm);
   const uint32_t u = (uint32_t)m & 0xffffffu;
-  const int t = i >> 3, k8 = i & 7;
-  const int slot = (k8 & 1) ? 4 + t : t;
-  const int byte = k8 >> 1;
-  uint8_t* b = reinterpret_cast<uint8_t*>(scratch);
-  b[(0 * 8 + slot) * 4 + byte] = (uint8_t)(u & 0xffu);
-  b[(1 * 8 + slot) * 4 + byte] = (uint8_t)((u >> 8) & 0xffu);
-  b[(2 * 8 + slot) * 4 + byte] = (uint8_t)((u >> 16) & 0xffu);
-  E_out = E;
-  sm_out = sm;
-}
-
-__device__ __forceinline__ void xprep_lanes_store(int i, const uint32_t* scratch, int E, int sm,
-                                                  uint32_t* __restrict__ out) {
-  if (i < 24) {
-    out[i] = scratch[i];
-  } else if (i == 24) {
-    out[24] = __float_as_uint(block_scale(E));
-  } else if (i == 25) {
-    out[25] = __float_as_uint((float)sm * block_scale(E));
-  } else if (i < 28) {
-    out[i] = 0u;
+  const int at = 4 * (i & 6);  // bit offset of this element's byte: byte (i & 7) >> 1 of its word
+  uint32_t w0 = (u & 0xffu) << at, w1 = ((u >> 8) & 0xffu) << at, w2 = (u >> 16) << at;
+  w0 |= lane_xor<2>(w0);
+  w1 |= lane_xor<2>(w1);
+  w2 |= lane_xor<2>(w2);
+  w0 |= lane_xor<4>(w0);
+  w1 |= lane_xor<4>(w1);
+  w2 |= lane_xor<4>(w2);
+  if ((i & 6) == 0) {
+    const int slot = (i & 1) ? 4 + (i >> 3) : (i >> 3);
+    dst[slot] = w0;
+    dst[8 + slot] = w1;
+    dst[16 + slot] = w2;
+  } else if (i < 8) {  // lanes 2..7: the scale words and the zero pad
+    const float p = block_scale(E);
+    if (i == 2) dst[24] = __float_as_uint(p);
+    if (i == 3) dst[25] = __float_as_uint((float)sm * p);
+    if (i == 4) dst[26] = 0u;
+    if (i == 5) dst[27] = 0u;
   }
 }
 
@@ -276,6 +276,18 @@ __device__ __forceinline__ float lane_fold(float v) {
 __device__ __forceinline__ float wave_fold64(float v) { return fold_sum<32>(v); }
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// 16 bytes global -> LDS with no register round trip (gfx950
+// global_load_lds_dwordx4): lane l of the wave writes LDS unit wave_base + l,
+// so wave_base must be the same for every lane of the wave; lanes that are
+// switched off write nothing.  The data is in LDS once this wave's vector
+// memory counter has drained: lds_dma_wait(), then a barrier for the others.
+typedef __attribute__((address_space(3))) void lds_void_t;
+__device__ __forceinline__ void lds_dma16(uint4* wave_base, const void* src) {
+  __builtin_amdgcn_global_load_lds(src, (lds_void_t*)wave_base, 16, 0, 0);
+}
+// s_waitcnt vmcnt(0): every vector memory load of this wave has landed (expcnt, lgkmcnt left open)
+__device__ __forceinline__ void lds_dma_wait() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
 // 16-byte streaming load of packed weights (read once per step: non-temporal)
 __device__ __forceinline__ uint4 ldg16(const uint32_t* p) {

@@ -11,17 +11,10 @@ namespace mtpx {
 // Activation block preparation of x [M, K] -> xp [M, K/32, XP_DW]: a 32-lane
 // group per block, eight blocks per 256-thread workgroup.
 __global__ __launch_bounds__(256) void k_xprep(const bf16* __restrict__ x, int M, int K, uint32_t* __restrict__ xp) {
-  __shared__ uint32_t scratch[8][24];
   const int nb = K / 32;
-  const int g = threadIdx.x >> 5, i = threadIdx.x & 31;
-  const int blk = blockIdx.x * 8 + g;
-  const bool valid = blk < M * nb;
-  const int m = valid ? blk / nb : 0, j = valid ? blk % nb : 0;
-  const uint32_t h = valid ? x[(size_t)m * K + (size_t)j * 32 + i] : 0u;
-  int E, sm;
-  xprep_lanes_build(h, i, scratch[g], E, sm);
-  __syncthreads();
-  if (valid) xprep_lanes_store(i, scratch[g], E, sm, xp + (size_t)blk * XP_DW);
+  const int i = threadIdx.x & 31;
+  const int blk = blockIdx.x * 8 + (int)(threadIdx.x >> 5);
+  if (blk < M * nb) xprep_lanes_direct(x[(size_t)(blk / nb) * K + (size_t)(blk % nb) * 32 + i], i, xp + (size_t)blk * XP_DW);
 }
 
 // Dense GEMV.  256 threads; every lane-group owns two rows (RPL = 2) so each
@@ -54,7 +47,7 @@ __global__ __launch_bounds__(256) void k_qmv(const uint32_t* __restrict__ wq, co
   };
   if (base < row_end) load2(base);  // first rows in flight before the staging
   stage16(lds, xp, M * nb * XP_DW);
-  __syncthreads();
+  stage_sync();
   for (bool first = true; base < row_end; base += 4 * RPW, first = false) {  // uniform per wave
     if (!first) load2(base);
     const int rA = base + grp * 2, rB = rA + 1;

@@ -120,34 +120,25 @@ __device__ __forceinline__ void dot2(const QRow<L, IT>& A, const QRow<L, IT>& B,
   rb = B.ok ? b : 0.0f;
 }
 
-// Copy `words` dwords global -> LDS, 16 bytes per access when both ends allow it.
-// Each thread issues STAGE_BATCH loads before its first LDS store: one memory
-// round trip per batch instead of one per element.  Indices past the end are
-// clamped to the last element for the load and the store alike (that element is
-// rewritten with its own value), so no load sits behind a condition the
-// compiler could sink it into.
-constexpr int STAGE_BATCH = 8;
+// Copy `words` dwords global -> LDS: 16-byte LDS-direct loads when both ends
+// allow it (thread t copies units t, t + blockDim, ...; blockDim a multiple of
+// 64), else dword copies through registers.  Follow with stage_sync() before
+// the LDS is read.
 __device__ __forceinline__ void stage16(uint32_t* __restrict__ dst, const uint32_t* __restrict__ src, int words) {
   if ((((uintptr_t)src | (uintptr_t)dst) & 15) == 0 && (words & 3) == 0) {
     const uint4* s4 = reinterpret_cast<const uint4*>(src);
     uint4* d4 = reinterpret_cast<uint4*>(dst);
-    const int n4 = words / 4, step = blockDim.x;
-    for (int base = threadIdx.x; base < n4; base += STAGE_BATCH * step) {
-      uint4 v[STAGE_BATCH];
-#pragma unroll
-      for (int u = 0; u < STAGE_BATCH; ++u) {
-        const int i = base + u * step;
-        v[u] = s4[i < n4 ? i : n4 - 1];
-      }
-#pragma unroll
-      for (int u = 0; u < STAGE_BATCH; ++u) {
-        const int i = base + u * step;
-        d4[i < n4 ? i : n4 - 1] = v[u];
-      }
-    }
+    const int n4 = words / 4, lane = threadIdx.x & 63;
+    for (int i = threadIdx.x; i < n4; i += blockDim.x) lds_dma16(d4 + (i - lane), s4 + i);
   } else {
     for (int i = threadIdx.x; i < words; i += blockDim.x) dst[i] = src[i];
   }
+}
+
+// The staged data of every wave is in LDS (this wave's loads drained, then the barrier).
+__device__ __forceinline__ void stage_sync() {
+  lds_dma_wait();
+  __syncthreads();
 }
 
 // Dispatch a launcher templated on <L, IT> for the shapes the model uses, with

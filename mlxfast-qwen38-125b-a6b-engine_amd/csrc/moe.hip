@@ -4,11 +4,17 @@
 //            finish (ticket) runs the route: top-k (value desc, index asc) +
 //            softmax, and the expert-grouped dispatch table (each selected
 //            expert once, with its tokens)
-//   gate_up: per (32-row block of F, selected expert): gate and up rows of the
-//            expert against every token routed to it, SwiGLU, and the block
-//            preparation of the activation for the down projection
-//   down   : per (128-row block of H, selected expert): down rows against the
-//            expert's activations -> routed/shared outputs per slot
+//   gate_up: one workgroup per CU over the (slot, 32-row block of F) items,
+//            slot = the shared expert of one token or one routed (token,
+//            rank) pair: gate and up rows against that token, SwiGLU -> bf16
+//            activations per slot
+//   down   : the same layout over (slot, block of H) items: block preparation
+//            of the slot's activations, down rows against them -> routed/
+//            shared outputs per slot
+// The expert kernels stream the weights with the next item's loads in flight
+// while the current item is computed; the distinct-expert count of the
+// dispatch table is what the window reads from HBM (an expert chosen by two
+// tokens is read twice, the second time from cache).
 //   combine: per (token, 256 rows of H): fold the routed outputs in rank order,
 //            add the sigmoid-gated shared expert (MLX col_reduce_small
 //            association), optionally add the residual stream
@@ -150,23 +156,24 @@ __device__ void route_body(const MoeArgs& a) {
     uid[t] = u;
     int count = 0;
     for (int m = 0; m < M; ++m) count += (tokbits[m][e >> 5] >> (e & 31)) & 1u;
-    d->expert[u] = e;
-    d->count[u] = count;
+    d->expert[u + 1] = e;
+    d->count[u + 1] = count;
   }
   __syncthreads();
+  const int n = __popcll(leadmask[0]) + (MK > 64 ? __popcll(leadmask[1]) : 0);
   if (t < MK) {
     const int u = uid[first[e]];
     int pos = 0;
     for (int m = 0; m < t / K; ++m) pos += (tokbits[m][e >> 5] >> (e & 31)) & 1u;
-    d->slot[u][pos] = (int16_t)t;
+    d->slot[u + 1][pos] = (int16_t)t;
+    if (t + 1 > n) d->expert[t + 1] = -2;  // grid rows past the routed experts: no work
   }
   if (t == 0) {
-    const int n = __popcll(leadmask[0]) + (MK > 64 ? __popcll(leadmask[1]) : 0);
     d->n_unique = n;
     if (a.nu_out) *a.nu_out = n;
-    d->expert[n] = -1;
-    d->count[n] = M;
-    for (int m = 0; m < M; ++m) d->slot[n][m] = (int16_t)(MK + m);
+    d->expert[0] = -1;
+    d->count[0] = M;
+    for (int m = 0; m < M; ++m) d->slot[0][m] = (int16_t)(MK + m);
   }
 }
 
@@ -229,90 +236,144 @@ __global__ __launch_bounds__(RR_THREADS) void k_moe_router_route(MoeArgs a, int 
   route_body(a);
 }
 
-// Dispatch entry of grid row y: row 0 is the shared expert (every token, the
-// most work per workgroup, so it is dispatched first), rows 1..nu the routed
-// experts in dispatch order; -1 for the rows beyond.
-__device__ __forceinline__ int expert_slot(int y, int nu) {
-  if (y == 0) return nu;
-  return y - 1 < nu ? y - 1 : -1;
-}
-
-__device__ __forceinline__ int slot_token(int slot, int M, int K) {
-  return slot < M * K ? slot / K : slot - M * K;
-}
 
 // ---------------------------------------------------------------------------
-// gate|up + SwiGLU.  grid (F/32, M*K+1), GU_THREADS threads.  Every lane-group
-// owns one f of the block and walks its gate row and up row; the weight loads
-// are issued before the activations are staged into LDS.
-// GU_THREADS threads: 512 (eight waves, one pass each) for a one-token window,
-// where only parallelism matters; 256 (four waves, two passes each: the second
-// pass's loads are in flight while the first is computed) for wider windows.
-template <int L, int IT, int GU_THREADS>
-__global__ __launch_bounds__(GU_THREADS) void k_moe_gate_up(MoeArgs a) {
-  extern __shared__ uint32_t lds[];
-  __shared__ bf16 actb[MAX_TOKENS][32];
+// gate|up + SwiGLU, one workgroup of GU_THREADS = 512 threads per CU over the
+// work items of the window.  An item is (slot row r, 32-row block b of F),
+// i = r * (F/32) + b, with slot rows 0..M-1 the shared expert for token r and
+// rows M.. the routed slots t = m*K + k (expert idx[t], token m) -- one token
+// per item, so every item is the same work (an expert chosen by two tokens is
+// read twice, the second time from cache).  Workgroup w takes the contiguous
+// items [w*n/G, (w+1)*n/G): at most F/32 of them, so at most two slot rows
+// and two tokens.  Every wave owns RW = 64/L f rows of an item (gate and up).
+// Order: the loads of the two tokens' activation blocks are issued first,
+// then the weight loads of the first items, then the activation blocks are
+// written to LDS (the memory counter retires loads in order, so this waits
+// for the activations only).  Each wave then walks its items in straight-line
+// code with GU_DEPTH register sets: the next item's loads are in flight while
+// item k is computed.  Items past the range re-load the first one (loads are
+// unconditional, so no register version merges) and are not computed.  The
+// expert ids come through a restrict pointer: scalar loads, off the vector
+// memory counter.  The output is the bf16 activation act[slot][F]; the down
+// projection prepares its blocks.
+constexpr int GU_THREADS = 512;
+constexpr int GU_DEPTH = 2;  // register sets: the next item's loads are in flight
+constexpr int GU_STAGE = 4;  // 16-byte staging loads per thread: 2 tokens x H/32 blocks x 7 <= 4 * 512
+
+template <int L, int IT>
+struct GateUpItem {
+  QRow<L, IT> G, U;
+  int slot, tok, f0;
+};
+
+// The gate and up matrices of the routed experts or of the shared expert.
+struct GateUpMats {
+  const uint32_t *gw, *uw, *gsb, *usb;
+  const bf16 *gs, *gb, *us, *ub;
+};
+
+__device__ __forceinline__ int gu_token(int r, int M, int K) { return r < M ? r : (r - M) / K; }
+
+// Issue the loads of item i into `it` (PK: packed scale/bias rows).  The
+// pointer pairs are selected as values with a uniform condition.
+template <int L, int IT, bool PK>
+__device__ __forceinline__ void gate_up_load(const GateUpMats rm, const GateUpMats sm, int H, int F, int gs, int M,
+                                             int K, const int32_t* __restrict__ ids, GateUpItem<L, IT>& it, int i,
+                                             int nfb, int fi, bool valid, int sub) {
+  const int nb = H / 32, ng = H / gs, P = sb_row_len(H, gs);
+  const int r = i / nfb;
+  it.f0 = (i % nfb) * 32;
+  const bool shared = r < M;
+  const int t = r - M;
+  it.slot = shared ? M * K + r : t;
+  it.tok = gu_token(r, M, K);
+  const int e = shared ? 0 : ids[t];
+  const int f = it.f0 + (valid ? fi : 0);
+  const size_t row = shared ? (size_t)f : (size_t)e * F + f;
+  const uint32_t* gw = shared ? sm.gw : rm.gw;
+  const uint32_t* uw = shared ? sm.uw : rm.uw;
+  const uint32_t* gsb = shared ? sm.gsb : rm.gsb;
+  const uint32_t* usb = shared ? sm.usb : rm.usb;
+  const bf16* gsc = shared ? sm.gs : rm.gs;
+  const bf16* gbi = shared ? sm.gb : rm.gb;
+  const bf16* usc = shared ? sm.us : rm.us;
+  const bf16* ubi = shared ? sm.ub : rm.ub;
+  it.G.template load_as<PK>(gw + row * (H / 8), gsc + row * ng, gbi + row * ng, PK ? gsb + row * P : nullptr, nb,
+                            gs, sub, valid);
+  it.U.template load_as<PK>(uw + row * (H / 8), usc + row * ng, ubi + row * ng, PK ? usb + row * P : nullptr, nb,
+                            gs, sub, valid);
+}
+
+// gate and up of the item's rows against its token (LDS slot ts); SwiGLU.
+template <int L, int IT>
+__device__ __forceinline__ void gate_up_compute(const MoeArgs& a, GateUpItem<L, IT>& it,
+                                                const uint32_t* __restrict__ xl, int ts, int fi, bool valid, int sub) {
+  const int nb = a.H / 32;
+  float g, up;
+  dot2<L, IT, false>(it.G, it.U, xl + (size_t)ts * nb * XP_DW, nb, sub, g, up);
+  g = lane_fold<L>(g);
+  up = lane_fold<L>(up);
+  if (sub == 0 && valid) a.act[(size_t)it.slot * a.F + it.f0 + fi] = f2bf(silu_bf16(round_bf(g)) * round_bf(up));
+}
+
+template <int L, int IT, bool PK, int NIT>
+__global__ __launch_bounds__(GU_THREADS) void k_moe_gate_up(MoeArgs a, const int32_t* __restrict__ ids) {
+  extern __shared__ uint32_t lds[];  // [2][H/32][XP_DW]
+  constexpr int RW = 64 / L;         // f rows per wave
   constexpr int WAVES = GU_THREADS / 64;
-  constexpr int RW = 64 / L;                                  // f rows per wave pass
-  constexpr int NI = (32 + WAVES * RW - 1) / (WAVES * RW);     // passes for 32 rows
-  const int H = a.H, F = a.F, M = a.M, K = a.K, gs = a.gs;
-  const int nb = H / 32, ng = H / gs;
-  const int nu = a.disp->n_unique;
-  const int u = expert_slot(blockIdx.y, nu);
-  if (u < 0) return;
-  const bool shared = (u == nu);
-  const int e = a.disp->expert[u];
-  const int cnt = a.disp->count[u];
-  const uint32_t* gw = shared ? a.sh_gate_w : a.gate_w + (size_t)e * F * (H / 8);
-  const bf16* gsc = shared ? a.sh_gate_s : a.gate_s + (size_t)e * F * ng;
-  const bf16* gbi = shared ? a.sh_gate_b : a.gate_b + (size_t)e * F * ng;
-  const uint32_t* uw = shared ? a.sh_up_w : a.up_w + (size_t)e * F * (H / 8);
-  const bf16* usc = shared ? a.sh_up_s : a.up_s + (size_t)e * F * ng;
-  const bf16* ubi = shared ? a.sh_up_b : a.up_b + (size_t)e * F * ng;
-  const int P = sb_row_len(H, gs);
-  const uint32_t* gsb = a.gate_sb ? (shared ? a.sh_gate_sb : a.gate_sb + (size_t)e * F * P) : nullptr;
-  const uint32_t* usb = a.gate_sb ? (shared ? a.sh_up_sb : a.up_sb + (size_t)e * F * P) : nullptr;
+  constexpr int NP = (32 + WAVES * RW - 1) / (WAVES * RW);  // passes over the 32 rows (L > 16: more than one)
+  constexpr int D = NIT < GU_DEPTH ? NIT : GU_DEPTH;         // items in flight
+  const int H = a.H, F = a.F, gs = a.gs, M = a.M, K = a.K;
+  const int nb = H / 32, nfb = F / 32;
+  const int n_items = (M + M * K) * nfb;
+  const int G = gridDim.x;
+  const int i0 = (int)(((int64_t)blockIdx.x * n_items) / G);
+  const int n = (int)(((int64_t)(blockIdx.x + 1) * n_items) / G) - i0;  // 1 <= n <= NIT
+  const int t0 = gu_token(i0 / nfb, M, K), t1 = gu_token((i0 + n - 1) / nfb, M, K);
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int sub = lane % L, grp = lane / L;
-  const int f0 = blockIdx.x * 32;
-  QRow<L, IT> G[NI], U[NI];
+  const GateUpMats rm{a.gate_w, a.up_w, a.gate_sb, a.up_sb, a.gate_s, a.gate_b, a.up_s, a.up_b};
+  const GateUpMats sm{a.sh_gate_w, a.sh_up_w, a.sh_gate_sb, a.sh_up_sb, a.sh_gate_s, a.sh_gate_b, a.sh_up_s, a.sh_up_b};
+  auto item = [&](int k) { return k < n ? i0 + k : i0; };  // past the range: re-load the first item
+  // activation loads of tokens t0 (LDS slot 0) and t1 (slot 1)
+  const int n4 = nb * (XP_DW / 4);
+  uint4 st[GU_STAGE];
 #pragma unroll
-  for (int p = 0; p < NI; ++p) {
-    const int fi = (wave + p * WAVES) * RW + grp;
+  for (int q = 0; q < GU_STAGE; ++q) {
+    const int u = threadIdx.x + q * GU_THREADS;
+    const int tk = u < n4 ? t0 : t1, w = u < n4 ? u : u - n4;
+    st[q] = u < 2 * n4 ? reinterpret_cast<const uint4*>(a.xp_x + (size_t)tk * nb * XP_DW)[w] : make_uint4(0, 0, 0, 0);
+  }
+  asm volatile("" ::: "memory");  // keep the activation loads ahead of the weight loads
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    const int fi = (wave + p * WAVES) * RW + grp;  // row of the 32-row block
+    const bool live = (wave + p * WAVES) * RW < 32;  // uniform per wave: waves past the block have no rows
     const bool valid = fi < 32;
-    const int f = f0 + (valid ? fi : 0);
-    G[p].load(gw + (size_t)f * (H / 8), gsc + (size_t)f * ng, gbi + (size_t)f * ng, gsb ? gsb + (size_t)f * P : nullptr,
-              nb, gs, sub, valid);
-    U[p].load(uw + (size_t)f * (H / 8), usc + (size_t)f * ng, ubi + (size_t)f * ng, usb ? usb + (size_t)f * P : nullptr,
-              nb, gs, sub, valid);
-  }
-  for (int tk = 0; tk < cnt; ++tk) {
-    const int m = slot_token(a.disp->slot[u][tk], M, K);
-    stage16(lds + (size_t)tk * nb * XP_DW, a.xp_x + (size_t)m * nb * XP_DW, nb * XP_DW);
-  }
-  stage_sync();
+    GateUpItem<L, IT> S[D];
+    // unconditional, also in waves without rows (they load a real row and never use it): a load
+    // under a branch would merge register versions, and the copy would wait for the loads
 #pragma unroll
-  for (int p = 0; p < NI; ++p) {
-    const int fi = (wave + p * WAVES) * RW + grp;
-    if ((wave + p * WAVES) * RW >= 32) break;  // uniform per wave
-    for (int tk = 0; tk < cnt; ++tk) {
-      float g, up;
-      dot2(G[p], U[p], lds + (size_t)tk * nb * XP_DW, nb, sub, g, up);
-      g = lane_fold<L>(g);
-      up = lane_fold<L>(up);
-      if (sub == 0 && fi < 32) {
-        const bf16 act = f2bf(silu_bf16(round_bf(g)) * round_bf(up));
-        actb[tk][fi] = act;
-        a.act[(size_t)a.disp->slot[u][tk] * F + f0 + fi] = act;
+    for (int k = 0; k + 1 < D; ++k)
+      gate_up_load<L, IT, PK>(rm, sm, H, F, gs, M, K, ids, S[k], item(k), nfb, fi, valid, sub);
+    asm volatile("" ::: "memory");  // and the first weight loads ahead of the barrier
+    if (p == 0) {
+#pragma unroll
+      for (int q = 0; q < GU_STAGE; ++q) {
+        const int u = threadIdx.x + q * GU_THREADS;
+        if (u < 2 * n4) reinterpret_cast<uint4*>(lds)[u] = st[q];
       }
+      __syncthreads();
     }
-  }
-  __syncthreads();
-  // prepared activation block of this f-block for every slot: 32 lanes per slot
-  {
-    const int tk = threadIdx.x >> 5, i = threadIdx.x & 31;
-    if (tk < cnt)
-      xprep_lanes_direct(actb[tk][i], i, a.xp_act + ((size_t)a.disp->slot[u][tk] * (F / 32) + blockIdx.x) * XP_DW);
+    if (!live) continue;
+#pragma unroll
+    for (int k = 0; k < NIT; ++k) {
+      if (k + D - 1 < NIT)
+        gate_up_load<L, IT, PK>(rm, sm, H, F, gs, M, K, ids, S[(k + D - 1) % D], item(k + D - 1), nfb, fi, valid, sub);
+      S[k % D].G.opaque();  // retire this item's loads here, computed or not
+      S[k % D].U.opaque();
+      if (k < n) gate_up_compute(a, S[k % D], lds, S[k % D].tok == t0 ? 0 : 1, fi, valid, sub);
+    }
   }
 }
 
@@ -347,55 +408,105 @@ __global__ __launch_bounds__(256) void k_moe_combine(MoeArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// down: grid (H/DOWN_ROWS, M*K+1), 256 threads; each lane-group owns two rows
-// (RPL = 2) so each LDS read of an activation block feeds two rows.
+// down, laid out like gate|up: one workgroup of DN_THREADS = 512 threads per
+// CU over the items (slot row r, block of DR = WAVES * 2 * 64/L rows of H),
+// slot rows as in gate|up (0..M-1 the shared expert of token r, then the
+// routed slots); workgroup w takes a contiguous range of at most two slot
+// rows.  Every lane-group owns two rows (each LDS read of an activation block
+// feeds both).  Order: the bf16 activation loads of the (at most two) slots,
+// then the first item's weight loads, then each 32-lane group prepares one
+// activation block into LDS (waiting for the activations only), a barrier,
+// and the straight-line walk with two register sets.
+constexpr int DN_THREADS = 512;
+constexpr int DN_STAGE = 8;  // activation elements per thread: 2 slots x F <= 8 * 512
+
 template <int L, int IT>
-__global__ __launch_bounds__(256) void k_moe_down(MoeArgs a) {
-  extern __shared__ uint32_t lds[];
+struct DownItem {
+  QRow<L, IT> A, B;
+  int slot, h0;
+};
+
+struct DownMats {
+  const uint32_t *w, *sb;
+  const bf16 *s, *b;
+};
+
+__device__ __forceinline__ int dn_slot(int r, int M, int K) { return r < M ? M * K + r : r - M; }
+
+template <int L, int IT, bool PK>
+__device__ __forceinline__ void down_load(const DownMats rm, const DownMats sm, int H, int F, int gs, int M, int K,
+                                          const int32_t* __restrict__ ids, DownItem<L, IT>& it, int i, int nhb, int hi,
+                                          int sub) {
+  constexpr int DR = (DN_THREADS / 64) * 2 * (64 / L);
+  const int nb = F / 32, ng = F / gs, P = sb_row_len(F, gs);
+  const int r = i / nhb;
+  it.h0 = (i % nhb) * DR;
+  const bool shared = r < M;
+  it.slot = dn_slot(r, M, K);
+  const int e = shared ? 0 : ids[r - M];
+  const bool va = it.h0 + hi < H, vb = it.h0 + hi + 1 < H;
+  const size_t base = shared ? 0 : (size_t)e * H;
+  const size_t ra = base + (size_t)(va ? it.h0 + hi : it.h0), rb = base + (size_t)(vb ? it.h0 + hi + 1 : it.h0);
+  const uint32_t* w = shared ? sm.w : rm.w;
+  const uint32_t* sb = shared ? sm.sb : rm.sb;
+  const bf16* sc = shared ? sm.s : rm.s;
+  const bf16* bi = shared ? sm.b : rm.b;
+  it.A.template load_as<PK>(w + ra * (F / 8), sc + ra * ng, bi + ra * ng, PK ? sb + ra * P : nullptr, nb, gs, sub, va);
+  it.B.template load_as<PK>(w + rb * (F / 8), sc + rb * ng, bi + rb * ng, PK ? sb + rb * P : nullptr, nb, gs, sub, vb);
+}
+
+template <int L, int IT, bool PK, int NIT>
+__global__ __launch_bounds__(DN_THREADS) void k_moe_down(MoeArgs a, const int32_t* __restrict__ ids) {
+  extern __shared__ uint32_t lds[];  // [2][F/32][XP_DW]
   constexpr int RW = 64 / L;
-  constexpr int NI = (DOWN_ROWS + 8 * RW - 1) / (8 * RW);  // passes of 2*RW rows per wave
-  const int H = a.H, F = a.F, K = a.K, gs = a.gs;
-  const int nb = F / 32, ng = F / gs;
-  const int nu = a.disp->n_unique;
-  const int u = expert_slot(blockIdx.y, nu);
-  if (u < 0) return;
-  const bool shared = (u == nu);
-  const int e = a.disp->expert[u];
-  const int cnt = a.disp->count[u];
-  const uint32_t* dw = shared ? a.sh_down_w : a.down_w + (size_t)e * H * (F / 8);
-  const bf16* dsc = shared ? a.sh_down_s : a.down_s + (size_t)e * H * ng;
-  const bf16* dbi = shared ? a.sh_down_b : a.down_b + (size_t)e * H * ng;
-  const int P = sb_row_len(F, gs);
-  const uint32_t* dsb = a.down_sb ? (shared ? a.sh_down_sb : a.down_sb + (size_t)e * H * P) : nullptr;
+  constexpr int DR = (DN_THREADS / 64) * 2 * RW;
+  constexpr int D = NIT < 2 ? NIT : 2;  // items in flight
+  const int H = a.H, F = a.F, gs = a.gs, M = a.M, K = a.K;
+  const int nb = F / 32, nhb = (H + DR - 1) / DR;
+  const int n_items = (M + M * K) * nhb;
+  const int G = gridDim.x;
+  const int i0 = (int)(((int64_t)blockIdx.x * n_items) / G);
+  const int n = (int)(((int64_t)(blockIdx.x + 1) * n_items) / G) - i0;  // 1 <= n <= NIT
+  const int s0 = dn_slot(i0 / nhb, M, K), s1 = dn_slot((i0 + n - 1) / nhb, M, K);
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int sub = lane % L, grp = lane / L;
-  const int h0 = blockIdx.x * DOWN_ROWS;
-  QRow<L, IT> A[NI], B[NI];
+  const int hi = wave * 2 * RW + 2 * grp;  // first of this lane-group's two rows within the block
+  const DownMats rm{a.down_w, a.down_sb, a.down_s, a.down_b};
+  const DownMats sm{a.sh_down_w, a.sh_down_sb, a.sh_down_s, a.sh_down_b};
+  auto item = [&](int k) { return k < n ? i0 + k : i0; };
+  // activation element u = q * 512 + t: block u / 32 of slot s0 (blocks 0..nb-1) or s1 (nb..2nb-1)
+  uint32_t hv[DN_STAGE];
 #pragma unroll
-  for (int p = 0; p < NI; ++p) {
-    const int hi = (wave + 4 * p) * 2 * RW + 2 * grp;
-    const bool va = hi < DOWN_ROWS && h0 + hi < H, vb = hi + 1 < DOWN_ROWS && h0 + hi + 1 < H;
-    const int ha = va ? h0 + hi : h0, hb = vb ? h0 + hi + 1 : h0;
-    A[p].load(dw + (size_t)ha * (F / 8), dsc + (size_t)ha * ng, dbi + (size_t)ha * ng,
-              dsb ? dsb + (size_t)ha * P : nullptr, nb, gs, sub, va);
-    B[p].load(dw + (size_t)hb * (F / 8), dsc + (size_t)hb * ng, dbi + (size_t)hb * ng,
-              dsb ? dsb + (size_t)hb * P : nullptr, nb, gs, sub, vb);
+  for (int q = 0; q < DN_STAGE; ++q) {
+    const int u = (int)threadIdx.x + q * DN_THREADS, bq = u >> 5;
+    const int sl = bq < nb ? s0 : s1, b = bq < nb ? bq : bq - nb;
+    hv[q] = bq < 2 * nb ? a.act[(size_t)sl * F + b * 32 + (u & 31)] : 0u;
   }
-  for (int tk = 0; tk < cnt; ++tk)
-    stage16(lds + (size_t)tk * nb * XP_DW, a.xp_act + (size_t)a.disp->slot[u][tk] * nb * XP_DW, nb * XP_DW);
-  stage_sync();
+  asm volatile("" ::: "memory");  // activation loads ahead of the weight loads
+  DownItem<L, IT> S[D];
 #pragma unroll
-  for (int p = 0; p < NI; ++p) {
-    if ((wave + 4 * p) * 2 * RW >= DOWN_ROWS) break;  // uniform per wave
-    const int hi = (wave + 4 * p) * 2 * RW + 2 * grp;
-    for (int tk = 0; tk < cnt; ++tk) {
+  for (int k = 0; k + 1 < D; ++k) down_load<L, IT, PK>(rm, sm, H, F, gs, M, K, ids, S[k], item(k), nhb, hi, sub);
+  asm volatile("" ::: "memory");  // and the first weight loads ahead of the preparation
+#pragma unroll
+  for (int q = 0; q < DN_STAGE; ++q) {
+    const int bq = ((int)threadIdx.x + q * DN_THREADS) >> 5;  // uniform per 32-lane group
+    if (bq < 2 * nb) xprep_lanes_direct(hv[q], threadIdx.x & 31, lds + (size_t)bq * XP_DW);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < NIT; ++k) {
+    if (k + D - 1 < NIT) down_load<L, IT, PK>(rm, sm, H, F, gs, M, K, ids, S[(k + D - 1) % D], item(k + D - 1), nhb, hi, sub);
+    DownItem<L, IT>& it = S[k % D];
+    it.A.opaque();  // retire this item's loads here, computed or not
+    it.B.opaque();
+    if (k < n) {
       float ra, rb;
-      dot2(A[p], B[p], lds + (size_t)tk * nb * XP_DW, nb, sub, ra, rb);
+      dot2<L, IT, false>(it.A, it.B, lds + (size_t)(it.slot == s0 ? 0 : nb) * XP_DW, nb, sub, ra, rb);
       ra = lane_fold<L>(ra);
       rb = lane_fold<L>(rb);
       // rows hi, hi+1 (hi even, H a multiple of 8): one 4-byte store of both
-      if (sub == 0 && hi < DOWN_ROWS && h0 + hi < H) {
-        bf16* dst = a.r + (size_t)a.disp->slot[u][tk] * H + h0 + hi;
+      if (sub == 0 && it.h0 + hi < H) {
+        bf16* dst = a.r + (size_t)it.slot * H + it.h0 + hi;
         *reinterpret_cast<uint32_t*>(dst) = (uint32_t)f2bf(ra) | ((uint32_t)f2bf(rb) << 16);
       }
     }
@@ -410,31 +521,74 @@ hipError_t launch_moe_router_route(const MoeArgs& a, hipStream_t st) {
   return hipGetLastError();
 }
 
-template <int L, int IT, int THREADS>
-static hipError_t gate_up_launch(const MoeArgs& a, hipStream_t st) {
-  const dim3 grid(a.F / 32, a.M * a.K + 1);
-  const size_t lds = (size_t)a.M * (a.H / 32) * XP_DW * 4;
+template <int L, int IT, bool PK, int NIT>
+static hipError_t gate_up_nit(const MoeArgs& a, int grid, hipStream_t st) {
+  const size_t lds = (size_t)2 * (a.H / 32) * XP_DW * 4;
   static size_t cur = 0;
-  hipError_t e = ensure_lds(k_moe_gate_up<L, IT, THREADS>, lds, cur);
+  hipError_t e = ensure_lds(k_moe_gate_up<L, IT, PK, NIT>, lds, cur);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((k_moe_gate_up<L, IT, THREADS>), grid, dim3(THREADS), lds, st, a);
+  hipLaunchKernelGGL((k_moe_gate_up<L, IT, PK, NIT>), dim3(grid), dim3(GU_THREADS), lds, st, a,
+                     (const int32_t*)a.idx);
   return hipGetLastError();
+}
+
+// One workgroup per CU (more when a workgroup's range would exceed F/32 items,
+// fewer for small windows); NIT = the most items a workgroup walks, rounded up
+// to 1, 2, 4 or 8.
+template <int L, int IT, bool PK>
+static hipError_t gate_up_pk(const MoeArgs& a, hipStream_t st) {
+  const int nfb = a.F / 32;
+  const int items = (a.M + a.M * a.K) * nfb;
+  int grid = items < device_cus() ? items : device_cus();
+  const int lim = nfb < 8 ? nfb : 8;  // items per workgroup: at most two slot rows, at most 8
+  if ((items + grid - 1) / grid > lim) grid = (items + lim - 1) / lim;
+  const int per = (items + grid - 1) / grid;
+  const int nit = per <= 1 ? 1 : per <= 2 ? 2 : per <= 4 ? 4 : 8;
+  switch (nit) {
+    case 1: return gate_up_nit<L, IT, PK, 1>(a, grid, st);
+    case 2: return gate_up_nit<L, IT, PK, 2>(a, grid, st);
+    case 4: return gate_up_nit<L, IT, PK, 4>(a, grid, st);
+    default: return gate_up_nit<L, IT, PK, 8>(a, grid, st);
+  }
 }
 
 template <int L, int IT>
 static hipError_t gate_up_li(const MoeArgs& a, hipStream_t st) {
-  return a.M == 1 ? gate_up_launch<L, IT, 512>(a, st) : gate_up_launch<L, IT, 256>(a, st);
+  return a.gate_sb ? gate_up_pk<L, IT, true>(a, st) : gate_up_pk<L, IT, false>(a, st);
+}
+
+template <int L, int IT, bool PK, int NIT>
+static hipError_t down_nit(const MoeArgs& a, int grid, hipStream_t st) {
+  const size_t lds = (size_t)2 * (a.F / 32) * XP_DW * 4;
+  static size_t cur = 0;
+  hipError_t e = ensure_lds(k_moe_down<L, IT, PK, NIT>, lds, cur);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL((k_moe_down<L, IT, PK, NIT>), dim3(grid), dim3(DN_THREADS), lds, st, a, (const int32_t*)a.idx);
+  return hipGetLastError();
+}
+
+template <int L, int IT, bool PK>
+static hipError_t down_pk(const MoeArgs& a, hipStream_t st) {
+  constexpr int DR = (DN_THREADS / 64) * 2 * (64 / L);
+  if (2 * a.F > DN_STAGE * DN_THREADS) return hipErrorInvalidValue;
+  const int nhb = (a.H + DR - 1) / DR;
+  const int items = (a.M + a.M * a.K) * nhb;
+  int grid = items < device_cus() ? items : device_cus();
+  const int lim = nhb < 8 ? nhb : 8;  // items per workgroup: at most two slot rows, at most 8
+  if ((items + grid - 1) / grid > lim) grid = (items + lim - 1) / lim;
+  const int per = (items + grid - 1) / grid;
+  const int nit = per <= 1 ? 1 : per <= 2 ? 2 : per <= 4 ? 4 : 8;
+  switch (nit) {
+    case 1: return down_nit<L, IT, PK, 1>(a, grid, st);
+    case 2: return down_nit<L, IT, PK, 2>(a, grid, st);
+    case 4: return down_nit<L, IT, PK, 4>(a, grid, st);
+    default: return down_nit<L, IT, PK, 8>(a, grid, st);
+  }
 }
 
 template <int L, int IT>
 static hipError_t down_li(const MoeArgs& a, hipStream_t st) {
-  const dim3 grid((a.H + DOWN_ROWS - 1) / DOWN_ROWS, a.M * a.K + 1);
-  const size_t lds = (size_t)a.M * (a.F / 32) * XP_DW * 4;
-  static size_t cur = 0;
-  hipError_t e = ensure_lds(k_moe_down<L, IT>, lds, cur);
-  if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((k_moe_down<L, IT>), grid, dim3(256), lds, st, a);
-  return hipGetLastError();
+  return a.down_sb ? down_pk<L, IT, true>(a, st) : down_pk<L, IT, false>(a, st);
 }
 
 hipError_t launch_moe_gate_up(const MoeArgs& a, hipStream_t st) { MTPX_QROW_DISPATCH(a.H / 32, gate_up_li, a, st); }

@@ -196,7 +196,7 @@ size_t moe_ws_bytes(const mtpx_moe_weights* w, int M) {
   const int H = w->hidden, E = w->experts, K = w->top_k, F = w->expert_width;
   const int slots = M * (K + 1);
   return al(4 * (size_t)M * E) + al(4 * (size_t)M) + al(4 * (size_t)M * K) * 2 + al(sizeof(MoeDispatch)) +
-         al(4 * (size_t)M * (H / 32) * XP_DW) + al(2 * (size_t)slots * F) + al(4 * (size_t)slots * (F / 32) * XP_DW) +
+         al(4 * (size_t)M * (H / 32) * XP_DW) + al(2 * (size_t)slots * F) +
          al(2 * (size_t)slots * H) + 4096;
 }
 
@@ -232,7 +232,6 @@ int moe_enqueue(Ctx* c, const mtpx_moe_weights* w, const uint16_t* x, int M, uin
   a.xp_x = xp_ready ? xp_ready : ws_take<uint32_t>(c, (size_t)M * (a.H / 32) * XP_DW);
   a.xp_ready = xp_ready != nullptr;
   a.act = ws_take<uint16_t>(c, (size_t)slots * a.F);
-  a.xp_act = ws_take<uint32_t>(c, (size_t)slots * (a.F / 32) * XP_DW);
   a.r = ws_take<uint16_t>(c, (size_t)slots * a.H);
   a.resid = resid;
   a.y2 = y2;

@@ -1,5 +1,6 @@
 // Kernel launchers shared by the C-ABI layer (host side) and the .hip files.
 #pragma once
+#include <stddef.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -23,6 +24,18 @@ inline hipError_t ensure_lds(Kern* kernel, size_t bytes, size_t& cur) {
   return e;
 }
 
+// Compute units of the current device (cached per device).
+inline int device_cus() {
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cus[dev]) {
+    int n = 0;
+    cus[dev] = (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0) ? n : 256;
+  }
+  return cus[dev];
+}
+
 // --- dense q4 GEMV and friends (qmv.hip)
 hipError_t launch_xprep(const bf16* x, int M, int K, uint32_t* xp, hipStream_t st);
 // sb: packed scale/bias rows (sb_row_len(K, gs) u32 per row) or null
@@ -36,13 +49,18 @@ hipError_t launch_randn_bf16(bf16* out, int64_t n, uint64_t seed, uint32_t tenso
 hipError_t launch_fill_bf16(bf16* out, int64_t n, bf16 v, hipStream_t st);
 
 // --- MoE (moe.hip)
+// Expert-grouped dispatch of one MoE window, indexed by the expert kernels'
+// grid row y: y = 0 the shared expert (expert -1, every token), y = 1..n_unique
+// the routed experts selected by at least one token, expert -2 beyond.
 struct MoeDispatch {
-  int n_unique;  // routed experts selected by at least one token (the shared expert is entry n_unique)
+  int n_unique;  // routed experts selected by at least one token
   int pad[3];
   int expert[MAX_TOKENS * MAX_TOPK + 1];
   int count[MAX_TOKENS * MAX_TOPK + 1];
   int16_t slot[MAX_TOKENS * MAX_TOPK + 1][MAX_TOKENS];  // m*K + k (routed) or M*K + m (shared)
 };
+static_assert(offsetof(MoeDispatch, slot) % 8 == 0 && sizeof(MoeDispatch::slot[0]) == 16,
+              "slot rows are read as two 8-byte words");
 
 struct MoeArgs {
   int H, E, K, F, gs, M;
@@ -65,14 +83,12 @@ struct MoeArgs {
   uint32_t* xp_x;      // [M, H/32, XP_DW]
   int xp_ready;        // xp_x already holds the prepared x (the router skips its preparation)
   bf16* act;           // [M*(K+1), F]
-  uint32_t* xp_act;    // [M*(K+1), F/32, XP_DW]
   bf16* r;             // [M*(K+1), H]
   const bf16* resid;   // [M, H] or null: y2 = bf16(resid + y)
   bf16* y2;            // [M, H] or null
   uint32_t* ticket;    // router+route ticket, zero at rest
   int32_t* nu_out;     // if set: the route also writes the distinct routed expert count here
 };
-constexpr int DOWN_ROWS = 128;
 
 constexpr int MOE_TICKETS = 64;
 hipError_t launch_moe_router_route(const MoeArgs& a, hipStream_t st);

@@ -80,6 +80,31 @@ struct QRow {
     }
   }
 
+  // load() with the scale/bias pairs taken from packed rows only (sbrow != null):
+  // one code path, so no load of the other layout's path is ever waited for.
+  template <bool PK>
+  __device__ __forceinline__ void load_as(const uint32_t* __restrict__ wrow, const bf16* __restrict__ srow,
+                                          const bf16* __restrict__ brow, const uint32_t* __restrict__ sbrow, int nb,
+                                          int gs, int sub, bool valid) {
+    if constexpr (PK) {
+      load(wrow, nullptr, nullptr, sbrow, nb, gs, sub, valid);
+    } else {
+      load(wrow, srow, brow, nullptr, nb, gs, sub, valid);
+    }
+  }
+
+  // Make the held words opaque to the compiler, so the nibble masks of a
+  // loop over tokens are recomputed per token instead of hoisted (which would
+  // hold two masked copies of every word live and double the registers).
+  // It also reads every loaded register, so a loop that may compute zero
+  // tokens still retires this row's loads here and not at a later reuse.
+  __device__ __forceinline__ void opaque() {
+#pragma unroll
+    for (int it = 0; it < NB; ++it) {
+      asm volatile("" : "+v"(w[it][0]), "+v"(w[it][1]), "+v"(w[it][2]), "+v"(w[it][3]), "+v"(sb[it]));
+    }
+  }
+
   // lane partial of the row against a prepared activation vector
   __device__ __forceinline__ float dot(const uint32_t* __restrict__ xpv, int nb, int sub) const {
     float acc = 0.0f;
@@ -98,8 +123,10 @@ struct QRow {
 };
 
 // Lane partials of two rows against one prepared activation vector: each
-// activation block is read from LDS once for both rows.
-template <int L, int IT>
+// activation block is read from LDS once for both rows.  FENCE: keep one
+// block's activation words live at a time (fewer registers) instead of
+// letting the scheduler overlap blocks (more LDS reads in flight).
+template <int L, int IT, bool FENCE = true>
 __device__ __forceinline__ void dot2(const QRow<L, IT>& A, const QRow<L, IT>& B, const uint32_t* __restrict__ xpv,
                                      int nb, int sub, float& ra, float& rb) {
   float a = 0.0f, b = 0.0f;
@@ -113,8 +140,7 @@ __device__ __forceinline__ void dot2(const QRow<L, IT>& A, const QRow<L, IT>& B,
       b = block_accum(b, block_dot(B.w[it], xl), __uint_as_float(B.sb[it] << 16),
                       __uint_as_float(B.sb[it] & 0xffff0000u), xl);
     }
-    // keep one block's activation words live at a time (no hoisting across blocks)
-    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (FENCE) __builtin_amdgcn_sched_barrier(0);
   }
   ra = A.ok ? a : 0.0f;
   rb = B.ok ? b : 0.0f;

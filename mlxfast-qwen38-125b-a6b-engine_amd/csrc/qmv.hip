@@ -70,6 +70,223 @@ __global__ __launch_bounds__(256) void k_qmv(const uint32_t* __restrict__ wq, co
   }
 }
 
+// ---------------------------------------------------------------------------
+// Dense GEMV on the matrix cores for 2..4 tokens (y = x . W^T, same bits as
+// k_qmv).  The exact integer block sums come from v_mfma_i32_16x16x32_i8 with
+//   A (16 x 32): row 4t + l = limb l of token t's 24-bit fixed-point block,
+//                limbs l = bits 0-6, 7-13, 14-15 (unsigned) and 16-23 (signed)
+//                of m, so every byte fits a signed i8 and four tokens fill
+//                the 16 rows;
+//   B (32 x 16): the 32 nibbles of one block of 16 weight rows;
+// lane (token t = lane / 16, row n = lane % 16) then holds the four limb sums
+// Da..Dd, and low = Da + 128 Db + 16384 Dc, D2 = Dd are the integers the
+// dot-product path forms from its byte limbs (low = sum w * (m & 0xffff),
+// D2 = sum w * (m >> 16)), so dxraw = fmaf(D2, 65536, low) and the block
+// combine are the same float operations.  The K order inside a block is the
+// prepared layout's (even elements of a word, then odd), for A and B alike.
+// Chains: block j joins chain j % L (L = lanes_for_blocks(K/32)), chains fold
+// in the lane walk's butterfly order.  A wave owns one tile of 16 rows and one
+// class c of C chain classes (chains = c mod C): its blocks j = c, c + C, ...
+// in order; the classes of a tile are waves of one workgroup and their
+// partials meet in LDS for the last log2(C) butterfly levels.  Weights stream
+// as one 16-byte load per lane per four blocks (lane group g loads block g of
+// the four), turned by a 4x4 transpose across the lane groups (two
+// permlane32 and two permlane16 swaps) into lane group g = word g of each
+// block; the next four blocks' loads are in flight while these are computed.
+constexpr int MMA_TOK = 4;   // tokens per tile (4 tokens x 4 limbs = 16 A rows)
+constexpr int MB_DW = 36;    // LDS block: [limb][word g][even, odd] (32 dwords), p, SX, pad
+constexpr int MMA_THREADS = 512;
+
+typedef int v4i_t __attribute__((ext_vector_type(4)));
+
+// Prepared blocks of M tokens (xp [M][NB][XP_DW]) -> the four-limb layout in
+// LDS [MMA_TOK][NB][MB_DW]; tokens M.. are zero (their sums are 0, p = SX = 0).
+// Unit u = (token, block, word g, even/odd) converts three limb words into
+// four; the loads (all units of this thread, then its p/SX pairs) are issued
+// by mma_stage_load, so the caller can put its own loads behind them and
+// mma_stage_store waits for these only.
+template <int NB>
+struct MmaStage {
+  static constexpr int NU = (MMA_TOK * NB * 8 + MMA_THREADS - 1) / MMA_THREADS;   // units per thread
+  static constexpr int NP = (MMA_TOK * NB + MMA_THREADS - 1) / MMA_THREADS;       // p/SX pairs per thread
+  uint32_t w[NU][3];
+  uint32_t ps[NP][2];
+
+  __device__ __forceinline__ void load(const uint32_t* __restrict__ xp, int M) {
+#pragma unroll
+    for (int k = 0; k < NU; ++k) {
+      const int u = threadIdx.x + k * MMA_THREADS;
+      const int t = u / (NB * 8), rem = u - t * (NB * 8), blk = rem >> 3, ge = rem & 7;
+      const bool in = u < MMA_TOK * NB * 8 && t < M;
+      const uint32_t* src = xp + ((size_t)(in ? t : 0) * NB + (in ? blk : 0)) * XP_DW + ((ge & 1) ? 4 : 0) + (ge >> 1);
+      w[k][0] = in ? src[0] : 0u;
+      w[k][1] = in ? src[8] : 0u;
+      w[k][2] = in ? src[16] : 0u;
+    }
+#pragma unroll
+    for (int k = 0; k < NP; ++k) {
+      const int u = threadIdx.x + k * MMA_THREADS;
+      const int t = u / NB, blk = u - t * NB;
+      const bool in = u < MMA_TOK * NB && t < M;
+      const uint32_t* src = xp + ((size_t)(in ? t : 0) * NB + (in ? blk : 0)) * XP_DW + 24;
+      ps[k][0] = in ? src[0] : 0u;
+      ps[k][1] = in ? src[1] : 0u;
+    }
+  }
+
+  __device__ __forceinline__ void store(uint32_t* __restrict__ lds) const {
+#pragma unroll
+    for (int k = 0; k < NU; ++k) {
+      const int u = threadIdx.x + k * MMA_THREADS;
+      if (u < MMA_TOK * NB * 8) {
+        const int t = u / (NB * 8), rem = u - t * (NB * 8), blk = rem >> 3, ge = rem & 7;
+        const uint32_t w0 = w[k][0], w1 = w[k][1];
+        uint32_t* dst = lds + ((size_t)t * NB + blk) * MB_DW + 2 * (ge >> 1) + (ge & 1);
+        dst[0] = w0 & 0x7f7f7f7fu;                                          // bits 0-6
+        dst[8] = ((w0 >> 7) & 0x01010101u) | ((w1 << 1) & 0x7e7e7e7eu);    // bits 7-13
+        dst[16] = (w1 >> 6) & 0x03030303u;                                  // bits 14-15
+        dst[24] = w[k][2];                                                  // bits 16-23 (signed)
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < NP; ++k) {
+      const int u = threadIdx.x + k * MMA_THREADS;
+      if (u < MMA_TOK * NB) {
+        uint32_t* dst = lds + (size_t)u * MB_DW + 32;  // u = t * NB + blk
+        dst[0] = ps[k][0];
+        dst[1] = ps[k][1];
+      }
+    }
+  }
+};
+
+// butterfly levels S, S/2, .., 1 over v[0..2S-1]: v[u] = v[u] + v[u + S] (u < S); result v[0]
+template <int S, int NV>
+__device__ __forceinline__ void fold_levels(float (&v)[NV]) {
+  if constexpr (S >= 1) {
+#pragma unroll
+    for (int u = 0; u < S; ++u) v[u] = v[u] + v[u + S];
+    fold_levels<S / 2>(v);
+  }
+}
+
+template <int L, int IT, int C>
+__global__ __launch_bounds__(MMA_THREADS) void k_qmv_mma(const uint32_t* __restrict__ wq, const uint32_t* __restrict__ sbp,
+                                                        int N, int K, int gs, const uint32_t* __restrict__ xp, int M,
+                                                        bf16* __restrict__ y, float* __restrict__ yf) {
+  constexpr int NB = L * IT;   // blocks per row
+  constexpr int LC = L / C;    // chains per class
+  constexpr int NQ = NB / C;   // blocks per class
+  constexpr int NCH = NQ / 4;  // four-block chunks per class
+  constexpr int BC = LC / 4 > 2 ? LC / 4 : 2;  // chunks per loop body: the chain index and the buffer repeat
+  constexpr int TPG = 8 / C;                   // tiles per workgroup pass
+  static_assert(NB % (4 * C) == 0 && NCH % BC == 0 && C <= L && C <= 8 && LC <= 16, "whole bodies of four-block chunks");
+  // LDS: activations [MMA_TOK][NB][MB_DW]; per wave the (scale, bias) pairs of its tile and class [16][NQ];
+  // class partials [2][8 waves][64]
+  extern __shared__ uint32_t lds[];
+  uint32_t* sbl = lds + MMA_TOK * NB * MB_DW;
+  float* part = reinterpret_cast<float*>(sbl + 8 * 16 * NQ);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int c = wave % C, tl = wave / C;
+  const int n = lane & 15, g = lane >> 4;
+  const int r = gs / 32, P = sb_row_len(K, gs);
+  const int ntiles = (N + 15) / 16, ngroups = (ntiles + TPG - 1) / TPG;
+  uint32_t* mysb = sbl + wave * 16 * NQ;
+  // A operand of lane (A row = token (lane & 15) >> 2, limb lane & 3; word g); p, SX of token g
+  const uint32_t* xa = lds + (size_t)((lane & 15) >> 2) * NB * MB_DW + (lane & 3) * 8 + 2 * g;
+  const uint32_t* xps = lds + (size_t)g * NB * MB_DW + 32;
+  // activations once per workgroup
+  {
+    MmaStage<NB> stg;
+    stg.load(xp, M);
+    stg.store(lds);
+  }
+  __syncthreads();
+  int iter = 0;
+  for (int grp = blockIdx.x; grp < ngroups; grp += gridDim.x, ++iter) {
+    const int tile = grp * TPG + tl;
+    const int row = tile * 16 + n;
+    const uint32_t* wrow = wq + (size_t)(row < N ? row : N - 1) * (K / 8);
+    // this tile's (scale, bias) pairs of the class's blocks q = 0..NQ-1 (block c + C q), gathered into LDS
+    constexpr int NG = (16 * NQ + 63) / 64;
+    uint32_t gv[NG];
+#pragma unroll
+    for (int k = 0; k < NG; ++k) {
+      const int e = lane + 64 * k, rr = e / NQ, q = e - rr * NQ, j = c + C * q;
+      const int rw = tile * 16 + rr;
+      gv[k] = e < 16 * NQ ? sbp[(size_t)(rw < N ? rw : N - 1) * P + ((j % L) / r) * IT + j / L] : 0u;
+    }
+    uint4 wv[2][BC];
+    auto load_body = [&](int ch0, int buf) {
+#pragma unroll
+      for (int cb = 0; cb < BC; ++cb) wv[buf][cb] = ldg16(wrow + (size_t)(c + C * (4 * (ch0 + cb) + g)) * 4);
+    };
+    asm volatile("" ::: "memory");  // the pair gathers ahead of the weight loads
+    load_body(0, 0);
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int k = 0; k < NG; ++k)
+      if (lane + 64 * k < 16 * NQ) mysb[lane + 64 * k] = gv[k];  // this wave's region: read back by this wave only
+    float acc[LC];
+#pragma unroll
+    for (int u = 0; u < LC; ++u) acc[u] = 0.0f;
+#pragma unroll 1
+    for (int ch0 = 0; ch0 < NCH; ch0 += 2 * BC) {
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        const int cbase = ch0 + half * BC;
+        if (cbase >= NCH) break;  // uniform
+        if (cbase + BC < NCH) load_body(cbase + BC, half ^ 1);
+#pragma unroll
+        for (int cb = 0; cb < BC; ++cb) {
+          const int ch = cbase + cb;
+          const uint4 w = wv[half][cb];
+          // 4x4 transpose across the lane groups: T[b] at lane group g = word g of block b of the chunk
+          const auto p0 = __builtin_amdgcn_permlane32_swap(w.x, w.z, false, false);
+          const auto p1 = __builtin_amdgcn_permlane32_swap(w.y, w.w, false, false);
+          const auto q0 = __builtin_amdgcn_permlane16_swap(p0[0], p1[0], false, false);
+          const auto q1 = __builtin_amdgcn_permlane16_swap(p0[1], p1[1], false, false);
+          const uint32_t T[4] = {q0[0], q0[1], q1[0], q1[1]};
+#pragma unroll
+          for (int b = 0; b < 4; ++b) {
+            const int q = 4 * ch + b, j = c + C * q;
+            const long bop = (long)(T[b] & 0x0f0f0f0fu) | ((long)((T[b] >> 4) & 0x0f0f0f0fu) << 32);
+            long aop;
+            __builtin_memcpy(&aop, xa + (size_t)j * MB_DW, 8);
+            v4i_t d = {0, 0, 0, 0};
+            d = __builtin_amdgcn_mfma_i32_16x16x32_i8(aop, bop, d, 0, 0, 0);
+            const int low = d[0] + 128 * d[1] + 16384 * d[2];
+            const float dx = __builtin_fmaf((float)d[3], 65536.0f, (float)low);
+            uint2 ps;
+            __builtin_memcpy(&ps, xps + (size_t)j * MB_DW, 8);
+            const uint32_t sb = mysb[n * NQ + q];
+            float& a = acc[(4 * cb + b + 4 * BC * half) % LC];  // chain (j % L) / C, in block order
+            a = __builtin_fmaf(__uint_as_float(sb << 16), dx * __uint_as_float(ps.x), a);
+            a = __builtin_fmaf(__uint_as_float(sb & 0xffff0000u), __uint_as_float(ps.y), a);
+          }
+        }
+        asm volatile("" ::: "memory");  // one body's operands live at a time (no LDS reads hoisted across)
+      }
+    }
+    fold_levels<LC / 2>(acc);  // butterfly levels L/2 .. C: this class's chains
+    float v = acc[0];
+    if constexpr (C > 1) {
+      float* pb = part + (iter & 1) * 8 * 64;  // by parity: the next write to it is two barriers away
+      pb[wave * 64 + lane] = v;
+      __syncthreads();
+      float pc[C];
+#pragma unroll
+      for (int q = 0; q < C; ++q) pc[q] = pb[(tl * C + q) * 64 + lane];
+      fold_levels<C / 2>(pc);  // levels C/2 .. 1 across the classes
+      v = pc[0];
+    }
+    if (c == 0 && g < M && row < N) {
+      y[(size_t)g * N + row] = f2bf(v);
+      if (yf) yf[(size_t)g * N + row] = v;
+    }
+  }
+}
+
 // MLX affine quantisation of bf16 rows; one thread per group
 // (MLX/backend/cpu/quantized.cpp:1158-1220).
 __global__ void k_quantize(const bf16* __restrict__ w, int64_t groups, int gs, uint32_t* __restrict__ wq,
@@ -205,8 +422,114 @@ static hipError_t qmv_tokens(const uint32_t* wq, const bf16* s, const bf16* b, c
   MTPX_QROW_DISPATCH(K / 32, qmv_li, wq, s, b, sb, N, K, gs, xp, M, y, yf, st);
 }
 
+template <int L, int IT, int C>
+constexpr size_t mma_lds_bytes() {
+  return (size_t)MMA_TOK * L * IT * MB_DW * 4 + (size_t)8 * 16 * (L * IT / C) * 4 + 2 * 8 * 64 * 4;
+}
+
+template <int L, int IT, int C>
+static hipError_t qmv_mma_c(const uint32_t* wq, const uint32_t* sb, int N, int K, int gs, const uint32_t* xp, int M,
+                            bf16* y, float* yf, hipStream_t st) {
+  constexpr size_t lds = mma_lds_bytes<L, IT, C>();
+  static size_t cur = 0;
+  hipError_t e = ensure_lds(k_qmv_mma<L, IT, C>, lds, cur);
+  if (e != hipSuccess) return e;
+  const int groups = ((N + 15) / 16 + 8 / C - 1) / (8 / C);
+  const int per_cu = lds <= 50 * 1024 ? 3 : lds <= 78 * 1024 ? 2 : 1;  // workgroups resident per CU
+  const int grid = groups < per_cu * device_cus() ? groups : per_cu * device_cus();
+  hipLaunchKernelGGL((k_qmv_mma<L, IT, C>), dim3(grid), dim3(MMA_THREADS), lds, st, wq, sb, N, K, gs, xp, M, y, yf);
+  return hipGetLastError();
+}
+
+template <int L, int IT, int C>
+constexpr bool mma_c_ok() {
+  constexpr int NB = L * IT, LC = L / C, BC = LC / 4 > 2 ? LC / 4 : 2;
+  // two workgroups per CU at least: above that the dot-product path is faster (measured)
+  return C >= 2 && C <= L && LC <= 16 && NB % (4 * C) == 0 && (NB / C / 4) % BC == 0 &&
+         mma_lds_bytes<L, IT, C>() <= 80 * 1024;
+}
+
+// Chain classes per tile: the fewest that give about four waves per CU.
+// Chain classes per tile: at least two (the per-wave scale/bias region of one
+// class fits beside the activations for two workgroups per CU), then the
+// fewest that give about eight waves per CU.
+template <int L, int IT>
+static hipError_t qmv_mma_li(const uint32_t* wq, const uint32_t* sb, int N, int K, int gs, const uint32_t* xp, int M,
+                             bf16* y, float* yf, hipStream_t st) {
+  const int tiles = (N + 15) / 16, want = 8 * device_cus();
+  if constexpr (mma_c_ok<L, IT, 2>()) {
+    if (tiles * 2 >= want) return qmv_mma_c<L, IT, 2>(wq, sb, N, K, gs, xp, M, y, yf, st);
+  }
+  if constexpr (mma_c_ok<L, IT, 4>()) {
+    if (tiles * 4 >= want) return qmv_mma_c<L, IT, 4>(wq, sb, N, K, gs, xp, M, y, yf, st);
+  }
+  if constexpr (mma_c_ok<L, IT, 8>()) return qmv_mma_c<L, IT, 8>(wq, sb, N, K, gs, xp, M, y, yf, st);
+  if constexpr (mma_c_ok<L, IT, 4>()) return qmv_mma_c<L, IT, 4>(wq, sb, N, K, gs, xp, M, y, yf, st);
+  if constexpr (mma_c_ok<L, IT, 2>()) return qmv_mma_c<L, IT, 2>(wq, sb, N, K, gs, xp, M, y, yf, st);
+  return hipErrorNotSupported;
+}
+
+// The matrix-core path takes 2..4 tokens of a matrix with packed scale/bias
+// rows whose blocks tile the lanes exactly in four-block chunks.
+static bool qmv_mma_ok(const uint32_t* sb, int K, int M) {
+  const int nb = K / 32, L = lanes_for_blocks(nb);
+  return sb && M >= 2 && M <= MMA_TOK && nb % L == 0 && nb % 4 == 0;
+}
+
+static hipError_t qmv_mma(const uint32_t* wq, const uint32_t* sb, int N, int K, int gs, const uint32_t* xp, int M,
+                          bf16* y, float* yf, hipStream_t st) {
+  const int nb = K / 32, L = lanes_for_blocks(nb), IT = nb / L;
+  switch (L * 16 + IT) {
+    case 16 * 16 + 4: return qmv_mma_li<16, 4>(wq, sb, N, K, gs, xp, M, y, yf, st);
+    case 16 * 16 + 5: return qmv_mma_li<16, 5>(wq, sb, N, K, gs, xp, M, y, yf, st);
+    case 32 * 16 + 4: return qmv_mma_li<32, 4>(wq, sb, N, K, gs, xp, M, y, yf, st);
+    case 32 * 16 + 6: return qmv_mma_li<32, 6>(wq, sb, N, K, gs, xp, M, y, yf, st);
+    case 64 * 16 + 4: return qmv_mma_li<64, 4>(wq, sb, N, K, gs, xp, M, y, yf, st);
+    case 64 * 16 + 5: return qmv_mma_li<64, 5>(wq, sb, N, K, gs, xp, M, y, yf, st);
+    case 8 * 16 + 4: return qmv_mma_li<8, 4>(wq, sb, N, K, gs, xp, M, y, yf, st);
+    case 8 * 16 + 5: return qmv_mma_li<8, 5>(wq, sb, N, K, gs, xp, M, y, yf, st);
+    case 4 * 16 + 4: return qmv_mma_li<4, 4>(wq, sb, N, K, gs, xp, M, y, yf, st);
+    case 4 * 16 + 5: return qmv_mma_li<4, 5>(wq, sb, N, K, gs, xp, M, y, yf, st);
+    default: return hipErrorNotSupported;
+  }
+}
+
+template <int L, int IT>
+constexpr bool mma_any_c() {
+  return mma_c_ok<L, IT, 2>() || mma_c_ok<L, IT, 4>() || mma_c_ok<L, IT, 8>();
+}
+
+static bool qmv_mma_shape(int K) {
+  const int nb = K / 32, L = lanes_for_blocks(nb), IT = nb / L;
+  switch (L * 16 + IT) {
+    case 16 * 16 + 4: return mma_any_c<16, 4>();
+    case 16 * 16 + 5: return mma_any_c<16, 5>();
+    case 32 * 16 + 4: return mma_any_c<32, 4>();
+    case 32 * 16 + 6: return mma_any_c<32, 6>();
+    case 64 * 16 + 4: return mma_any_c<64, 4>();
+    case 64 * 16 + 5: return mma_any_c<64, 5>();
+    case 8 * 16 + 4: return mma_any_c<8, 4>();
+    case 8 * 16 + 5: return mma_any_c<8, 5>();
+    case 4 * 16 + 4: return mma_any_c<4, 4>();
+    case 4 * 16 + 5: return mma_any_c<4, 5>();
+    default: return false;
+  }
+}
+
 hipError_t launch_qmv(const uint32_t* wq, const bf16* s, const bf16* b, const uint32_t* sb, int N, int K, int gs,
                       const uint32_t* xp, int M, bf16* y, float* yf, hipStream_t st) {
+  if (M >= 2 && qmv_mma_ok(sb, K, 2) && qmv_mma_shape(K)) {  // matrix cores, four tokens per launch
+    for (int m0 = 0; m0 < M; m0 += MMA_TOK) {
+      const int mc = M - m0 < MMA_TOK ? M - m0 : MMA_TOK;
+      const uint32_t* xpc = xp + (size_t)m0 * (K / 32) * XP_DW;
+      bf16* yc = y + (size_t)m0 * N;
+      float* yfc = yf ? yf + (size_t)m0 * N : nullptr;
+      const hipError_t e = mc >= 2 ? qmv_mma(wq, sb, N, K, gs, xpc, mc, yc, yfc, st)
+                                   : qmv_tokens(wq, s, b, sb, N, K, gs, xpc, mc, yc, yfc, st);
+      if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+  }
   // tokens per launch: as many prepared activation vectors as fit in one workgroup's LDS
   const size_t per_token = (size_t)(K / 32) * XP_DW * 4;
   int chunk = (int)((160 * 1024) / per_token);

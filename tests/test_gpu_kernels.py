@@ -67,6 +67,9 @@ def test_randn_deterministic_and_normal(ctx):
     (640, 2560, 64, 1), (1280, 2560, 32, 4), (2560, 640, 64, 6), (2048, 768, 64, 2),
     (768, 2048, 32, 1), (256, 6144, 64, 4), (100, 256, 32, 8), (13440, 2560, 64, 7), (37, 320, 32, 3),
     (300, 6144, 64, 8), (64, 96, 32, 5),
+    # matrix-core path (2..4 tokens per launch, packed pairs): the model's dense shapes, ragged rows
+    (16480, 2560, 64, 4), (2560, 6144, 64, 4), (1000, 2560, 64, 3), (2560, 6144, 32, 2), (4096, 2048, 64, 4),
+    (520, 10240, 64, 4), (2560, 2560, 32, 5),
 ])
 def test_qmv_bit_exact(ctx, N, K, gs, M):
     _print_case(N=N, K=K, gs=gs, M=M)

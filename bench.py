@@ -1,23 +1,32 @@
-"""Benchmark of the MTP verify step on one MI355X.
+"""Benchmark of single-stream MTP speculative decode on one MI355X.
 
-Default workload: BASELINE config 4 -- the full-depth verify forward of the
-random-init 125B-A6B model (48 layers: 36 gated-deltanet + 12 attention, each
-with hyper-connection mixers and a 512-expert top-10 + shared MoE; hidden 2560,
-vocab 248320, affine 4-bit gs64, all weights resident in HBM), a verify window
-of k+1 = 4 tokens after a committed prefix of 1024 positions.  The prefix is
-synthetic: random attention K/V rows and random GDN states stand in for the
-prompt (prefill is not part of this build).  The PLE n-gram block of layer 1 is
-not part of the forward.  A step = one verify of the 4 tokens (logits and the
-multi stream); the window is left uncommitted, so each step starts from the same
-prefix.  `--workload layer` runs config 3 instead (one full-shape decoder layer,
-plain residuals, 4 tokens over 1024 cached positions).
+Default workload: BASELINE config 5 -- rounds of MTP speculative decode on the
+full-depth random-init 125B-A6B model (48 layers: 36 gated-deltanet + 12
+attention, each with hyper-connection mixers and a 512-expert top-10 + shared
+MoE; hidden 2560, vocab 248320, affine 4-bit gs64, all weights resident in HBM)
+with the MTP head.  The committed prefix of 1024 positions is synthetic: random
+attention K/V rows and random GDN states stand in for the prompt (prefill is
+not part of this build); the PLE n-gram block of layer 1 is not part of the
+forward.  A step = one round: k drafter steps, a verify of the carried token
+and the k drafts, the on-device greedy accept (read back once per round), the
+target commit and the drafter finalize.  Random-init drafts almost never match
+the target, so the accepted count is forced at p = 0.7 by a seeded draw.  The
+draft depth is the best of a sweep over 1..5; value = expected committed tokens
+per round at p (1 + p + ... + p^k) / measured time per round, over --steps
+rounds at that depth after --warmup rounds (every round does the same work
+whatever the draw; the realized count is reported beside it).
 
-Prints ONE JSON line.  `roofline` is the routed-expert gate|up+SwiGLU kernel
-(the largest HBM stream of the step): algorithmic bytes of its average launch
-(distinct experts of every layer read back from the device) / its average
-duration from HIP events recorded on the launch stream during the timed steps.
+Before the rounds the same run measures BASELINE config 4 (a verify of k+1 = 4
+tokens, --steps timed steps; reported under "verify") and the per-kernel HIP
+event timings of that verify.  `roofline` is the routed-expert gate|up+SwiGLU
+kernel (the largest HBM stream of the step): algorithmic bytes of its average
+launch (distinct experts of every layer read back from the device) / its
+average duration from HIP events recorded on the launch stream.
 `cpu_baseline` times the CPU oracle (the same arithmetic in C) on a bounded
-sample of the same workload, scaled as stated in its `sample` field.
+sample of the same rounds, scaled as stated in its `sample` field.
+`--no-e2e` reports the config-4 verify as the value; `--workload layer` runs
+config 3 (one full-shape decoder layer, plain residuals, 4 tokens over 1024
+cached positions).
 """
 from __future__ import annotations
 
@@ -97,10 +106,10 @@ def target_cfgs(gs: int, max_positions: int, layers: int):
     return lc, tc
 
 
-def cpu_baseline_full(target, state, lc, tc, M, kinds, ids_np, seconds=15.0):
-    """The oracle on a bounded sample of one verify step: the first GDN layer and the first
-    attention layer (each with its mixers and MoE) and a slice of lm_head rows, timed on one
-    host thread and scaled to the full stack."""
+def cpu_layer_times(target, state, lc, tc, widths, kinds, seconds=12.0):
+    """The oracle on a bounded sample of the target step, one host thread: per verify width M,
+    the first GDN layer and the first attention layer (each with its mixers and MoE) and 16384
+    of the lm_head rows.  -> ({M: (t_gdn, t_attn, t_head_rows)}, rows, iterations)."""
     import numpy as np
 
     from oracle import oracle as O
@@ -130,12 +139,10 @@ def cpu_baseline_full(target, state, lc, tc, M, kinds, ids_np, seconds=15.0):
     conv = O.f32_to_bf16(r.standard_normal((g.kc - 1, g.conv_dim)).astype(np.float32))
     ssm = (r.standard_normal((g.hv, 128, 128)) * 0.05).astype(np.float32)
     rows = 16384
-    tw = target.weights()
-    head = _q(tw.lm_head, rows, H, gs)  # the first `rows` rows of lm_head
+    head = _q(target.weights().lm_head, rows, H, gs)  # the first `rows` rows of lm_head
     pos0, _ = state.info()
-    sW = O.f32_to_bf16(r.standard_normal((M, hc * H)).astype(np.float32))
 
-    def layer_step(L, gdn):
+    def layer_step(L, gdn, sW):
         s, n = O.hc_norm(sW, None, None, L["hc"]["scale"], hc, eps)
         x, j = _mix(L["hc"], n, hc, gs)
         if gdn:
@@ -149,27 +156,58 @@ def cpu_baseline_full(target, state, lc, tc, M, kinds, ids_np, seconds=15.0):
         x, j = _mix(L["mhc"], n, hc, gs)
         O.moe_block(L["moe"], x, H, lc["experts"], lc["top_k"], lc["expert_width"], gs)
 
-    xh = O.f32_to_bf16(r.standard_normal((M, H)).astype(np.float32))
-    tg = ta = th = 0.0
-    n = 0
-    t0 = time.perf_counter()
-    while n == 0 or time.perf_counter() - t0 < seconds:
-        a = time.perf_counter()
-        layer_step(Lg, True)
-        b = time.perf_counter()
-        layer_step(La, False)
-        c = time.perf_counter()
-        O.qmv(*head, gs, xh)
-        d = time.perf_counter()
-        tg, ta, th, n = tg + b - a, ta + c - b, th + d - c, n + 1
-    tg, ta, th = tg / n, ta / n, th / n
+    times, iters = {}, {}
+    for M in widths:
+        sW = O.f32_to_bf16(r.standard_normal((M, hc * H)).astype(np.float32))
+        xh = O.f32_to_bf16(r.standard_normal((M, H)).astype(np.float32))
+        tg = ta = th = 0.0
+        n = 0
+        t0 = time.perf_counter()
+        while n == 0 or time.perf_counter() - t0 < seconds / len(widths):
+            a = time.perf_counter()
+            layer_step(Lg, True, sW)
+            b = time.perf_counter()
+            layer_step(La, False, sW)
+            c = time.perf_counter()
+            O.qmv(*head, gs, xh)
+            d = time.perf_counter()
+            tg, ta, th, n = tg + b - a, ta + c - b, th + d - c, n + 1
+        times[M], iters[M] = (tg / n, ta / n, th / n), n
+    return times, rows, iters
+
+
+def cpu_baseline_full(target, state, lc, tc, M, kinds):
+    """CPU baseline of the verify step (config 4): the sampled oracle layers scaled to the stack."""
+    times, rows, iters = cpu_layer_times(target, state, lc, tc, [M], kinds)
+    tg, ta, th = times[M]
     n_gdn, n_attn = kinds.count(0), kinds.count(1)
     step_s = n_gdn * tg + n_attn * ta + th * tc["vocab"] / rows
     return dict(value=M / step_s, unit="tok/s", cores=1, kind="port",
-                sample=f"{n} x (one GDN layer {tg:.2f} s, one attention layer {ta:.2f} s, {rows} of "
+                sample=f"{iters[M]} x (one GDN layer {tg:.2f} s, one attention layer {ta:.2f} s, {rows} of "
                        f"{tc['vocab']} lm_head rows {th:.2f} s) of the same verify step (M={M}) through the C "
                        f"oracle, single thread; scaled to {n_gdn} GDN + {n_attn} attention layers and the "
                        f"whole lm_head: {step_s:.1f} s per step")
+
+
+def cpu_baseline_e2e(target, state, lc, tc, kinds, k, tokens_per_round, shortlist_rows):
+    """CPU baseline of MTP speculative decode at draft depth k: one round = k draft steps + a verify
+    of k+1 tokens.  A draft step is timed as one attention layer with its mixers and MoE at one
+    token (the head's body) plus the shortlist GEMV (lm_head rows scaled to the shortlist); the
+    verify as in cpu_baseline_full at M = k+1.  tok/s = committed tokens per round / round time."""
+    times, rows, iters = cpu_layer_times(target, state, lc, tc, sorted({1, k + 1}), kinds)
+    n_gdn, n_attn = kinds.count(0), kinds.count(1)
+    tg, ta, th = times[k + 1]
+    verify_s = n_gdn * tg + n_attn * ta + th * tc["vocab"] / rows
+    _, ta1, th1 = times[1]
+    draft_s = ta1 + th1 * shortlist_rows / rows
+    round_s = k * draft_s + verify_s
+    return dict(value=tokens_per_round / round_s, unit="tok/s", cores=1, kind="port",
+                sample=f"oracle (C, single thread) on sampled layers: verify of {k + 1} tokens = {n_gdn} x GDN "
+                       f"layer {tg:.2f} s + {n_attn} x attention layer {ta:.2f} s + lm_head {th * tc['vocab'] / rows:.2f} s "
+                       f"(from {rows} rows) = {verify_s:.1f} s; draft step = attention layer at 1 token {ta1:.2f} s + "
+                       f"{shortlist_rows} shortlist rows {th1 * shortlist_rows / rows:.2f} s = {draft_s:.2f} s; round "
+                       f"= {k} drafts + verify = {round_s:.1f} s for {tokens_per_round:.3f} committed tokens "
+                       f"(expected at the same acceptance rate); iterations per width {iters}")
 
 
 def run_full(args, out):
@@ -178,7 +216,7 @@ def run_full(args, out):
     import mtpx
 
     M, T0, gs = args.verify_width, args.cached, args.group_size
-    lc, tc = target_cfgs(gs, T0 + 64 + 16 * args.rounds, args.layers)
+    lc, tc = target_cfgs(gs, T0 + 64 + 8 * max(args.rounds, args.steps + args.warmup), args.layers)
     ctx = mtpx.Context(0)
     t_init = time.perf_counter()
     target = mtpx.Target(ctx, mtpx.TargetConfig(mtpx.LayerConfig(**lc), *[tc[k] for k in (
@@ -249,116 +287,105 @@ def run_full(args, out):
     gu_s = stats["moe_gate_up"][1] / stats["moe_gate_up"][0] / 1e3
     gu_avg = sum(gu_bytes) / len(gu_bytes)
     achieved = gu_avg / gu_s / 1e9
-    out.update({
-        "value": round(M / (ms_per_step / 1e3), 2),
-        "ms_per_step": round(ms_per_step, 4),
-        "config": {
-            "workload": f"BASELINE config 4: full-depth verify forward of the random-init 125B-A6B model "
-                        f"({args.layers} layers: {n_gdn} GDN + {n_attn} attention, hyper-connection mixers, "
-                        f"512-expert top-10 + shared MoE per layer, hidden 2560, vocab 248320, gs{gs}, weights "
-                        f"resident in HBM); verify window of {M} tokens after a committed prefix of {T0} "
-                        f"positions (synthetic: random K/V rows and GDN states); the PLE block of layer 1 is "
-                        f"not in the forward; value = verified positions/s",
-            "verify_width": M, "prefix_positions": T0, "layers": args.layers, "group_size": gs,
-            "parallelism": "none (1 GPU)",
-        },
-        "roofline": {
-            "bound": "hbm",
-            "kernel": "moe_gate_up (routed + shared gate|up GEMV + SwiGLU), average launch over all layers",
-            "achieved": round(achieved, 1),
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
-            "algorithmic_bytes": round(gu_avg),
-            "avg_us": round(gu_s * 1e6, 3),
-        },
-        "moe": {"distinct_experts_per_layer": uniq, "bytes_per_step": moe_bytes},
-        "step_bytes": step_bytes,
-        "step_GBps": round(step_bytes / (ms_per_step / 1e3) / 1e9, 1),
+    verify = {
+        "what": f"BASELINE config 4: full-depth verify forward ({args.layers} layers: {n_gdn} GDN + {n_attn} "
+                f"attention) of {M} tokens after a committed prefix of {T0} positions; value = verified "
+                f"positions/s; {args.steps} timed steps after {args.warmup} warmup",
+        "value": round(M / (ms_per_step / 1e3), 2), "unit": "positions/s", "ms_per_step": round(ms_per_step, 4),
+        "step_bytes": step_bytes, "step_GBps": round(step_bytes / (ms_per_step / 1e3) / 1e9, 1),
         "decode_roofline_frac": round(step_bytes / (ms_per_step / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
-        "init_s": round(init_s, 1),
+        "moe": {"distinct_experts_per_layer": uniq, "bytes_per_step": moe_bytes},
         "kernels": kernels,
-    })
+    }
+    out["roofline"] = {
+        "bound": "hbm",
+        "kernel": f"moe_gate_up (routed + shared gate|up GEMV + SwiGLU) in the config-4 verify (M={M}), "
+                  f"average launch over all layers",
+        "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+        "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+        "algorithmic_bytes": round(gu_avg), "avg_us": round(gu_s * 1e6, 3),
+    }
     tr = traffic_record(gs, M, T0, "full")
     if tr is not None:
         out["roofline"]["traffic"] = tr["gate_up_bytes_per_launch"]
         out["roofline"]["traffic_source"] = tr["source"]
     if args.copy_calibration:
         copy_calibration()
-    if not args.no_e2e:
-        state.close()
-        results, best, _ = e2e_sweep(args, ctx, target, lc, tc, time.perf_counter())
-        out["mtp_decode"] = {
-            "what": f"BASELINE config 5 on the same target: MTP speculative decode rounds (drafter steps, verify, "
-                    f"on-device greedy accept read once per round, commit), acceptance forced at "
-                    f"p={args.accept_rate} by a seeded draw; committed tokens/s per draft depth",
-            "tok_s": results[best]["tok_s"], "best_depth": best, "depths": {str(d): r for d, r in results.items()},
-        }
+    base_cfg = {"prefix_positions": T0, "layers": args.layers, "group_size": gs, "parallelism": "none (1 GPU)"}
+    if args.no_e2e:
+        out.update({
+            "value": verify["value"], "unit": "tok/s", "ms_per_step": verify["ms_per_step"],
+            "config": dict(base_cfg, workload=verify["what"] + " (the PLE block of layer 1 is not in the forward; "
+                                                               "prefix synthetic: random K/V rows and GDN states)",
+                           verify_width=M),
+            "verify": verify,
+        })
+        if not args.no_cpu_baseline:
+            out["cpu_baseline"] = cpu_baseline_full(target, state, lc, tc, M, kinds)
+        return out
+    state.close()
+    e2e = E2E(args, ctx, target, lc, tc, kinds)
+    sweep = {k: e2e.run(k, args.rounds, min(4, args.rounds)) for k in args.depths}
+    best = max(sweep, key=lambda d: sweep[d]["tok_s"])
+    final = e2e.run(best, args.steps, args.warmup)
+    e2e.close()
+    out.update({
+        "value": final["tok_s"],
+        "ms_per_step": final["ms_per_round"],
+        "config": dict(base_cfg, workload=(
+            f"BASELINE config 5: single-stream MTP speculative decode on the full-depth random-init 125B-A6B "
+            f"target ({args.layers} layers: {n_gdn} GDN + {n_attn} attention, hyper-connection mixers, 512-expert "
+            f"top-10 + shared MoE, hidden 2560, vocab 248320, gs{gs}, weights resident in HBM) with the MTP head "
+            f"(attention + MoE, 98584-row shortlist), after a synthetic committed prefix of {T0} positions "
+            f"(random K/V rows and GDN states; the PLE block of layer 1 is not in the forward). A step = one "
+            f"round: {best} drafter steps, a verify of {best + 1} tokens, the on-device greedy accept (read back "
+            f"once per round), target commit and drafter finalize; acceptance forced at p={args.accept_rate} by a "
+            f"seeded draw. Draft depth {best} = the best of the sweep {list(args.depths)} ({args.rounds} rounds "
+            f"each); value = expected committed tokens per round at p (1 + p + ... + p^k) / measured time per "
+            f"round over the {args.steps} timed rounds (realized_tok_s: the seeded draws' own count)"),
+            draft_depth=best, accept_rate=args.accept_rate, expected_tokens_per_round=final["expected_tokens_per_round"],
+            realized_tok_s=final["realized_tok_s"], mean_accepted=final["mean_accepted"], tokens=final["tokens"]),
+        "depth_sweep": {str(d): r for d, r in sweep.items()},
+        "verify": verify,
+    })
+    if not args.no_cpu_baseline:
         state = mtpx.TargetState(ctx, target)
         state.set_offset(T0)
-    if not args.no_cpu_baseline:
-        out["cpu_baseline"] = cpu_baseline_full(target, state, lc, tc, M, kinds, None)
+        out["cpu_baseline"] = cpu_baseline_e2e(target, state, lc, tc, kinds, best,
+                                               final["expected_tokens_per_round"], 98304 + 276)
     return out
 
 
-def run_e2e(args, out):
-    """rounds of single-stream MTP speculative decode on the full-depth
-    target with the MTP head: k drafter steps, a verify of the carry + k drafts, the on-device
-    greedy accept (its result read back once per round), the target commit and the drafter
-    finalize.  Random-init drafts almost never match the target, so the accepted count is
-    forced at rate p by a seeded draw (the accept kernel still runs); the bonus token is the
-    target's argmax at the forced position."""
-    import numpy as np
-    import torch
+class E2E:
+    """BASELINE config 5 on `target`: rounds of single-stream MTP speculative decode -- k drafter
+    steps, a verify of the carry + k drafts, the on-device greedy accept (its result read back once
+    per round), the target commit and the drafter finalize.  Random-init drafts almost never match
+    the target, so the accepted count is forced at rate p by a seeded draw (the accept kernel still
+    runs); the carried token is the target's argmax at the forced position."""
 
-    import mtpx
+    def __init__(self, args, ctx, target, lc, tc, kinds):
+        import mtpx
 
-    T0, gs, p = args.cached, args.group_size, args.accept_rate
-    lc, tc = target_cfgs(gs, T0 + 64 + 16 * args.rounds, args.layers)
-    ctx = mtpx.Context(0)
-    t_init = time.perf_counter()
-    target = mtpx.Target(ctx, mtpx.TargetConfig(mtpx.LayerConfig(**lc), *[tc[k] for k in (
-        "key_heads", "value_heads", "conv_kernel", "num_layers", "full_attention_interval", "hc", "lowrank",
-        "vocab")]), seed=0x5EED0004)
-    results, best, init_s = e2e_sweep(args, ctx, target, lc, tc, t_init)
-    out.update({
-        "value": results[best]["tok_s"],
-        "ms_per_step": results[best]["ms_per_round"],
-        "steps": args.rounds,
-        "config": {
-            "workload": f"BASELINE config 5: single-stream MTP speculative decode rounds on the full-depth "
-                        f"random-init target ({args.layers} layers, PLE block not in the forward) with the MTP "
-                        f"head, after a synthetic committed prefix of {T0} positions; draft depths "
-                        f"{list(args.depths)}; acceptance forced at p={p} by a seeded draw; value = committed "
-                        f"tokens/s at the best depth ({best}); a step = one round",
-            "depths": {str(d): r for d, r in results.items()}, "best_depth": best, "accept_rate": p,
-            "prefix_positions": T0, "layers": args.layers, "group_size": gs, "parallelism": "none (1 GPU)",
-        },
-        "init_s": round(init_s, 1),
-    })
-    return out
+        self.args, self.ctx, self.target, self.lc, self.tc, self.kinds = args, ctx, target, lc, tc, kinds
+        self.head = mtpx.MTPHead(ctx, mtpx.HeadConfig(mtpx.LayerConfig(**dict(lc, max_positions=64 + 16 * max(
+            args.rounds, args.steps + args.warmup))), tc["hc"], tc["lowrank"], tc["vocab"], 98304, 248044),
+            seed=0x5EED0007)
 
+    def close(self):
+        self.head.close()
 
-def e2e_sweep(args, ctx, target, lc, tc, t_init):
-    """Rounds per draft depth on `target` (see run_e2e) -> ({depth: stats}, best depth, init seconds)."""
-    import numpy as np
-    import torch
+    def run(self, k, rounds, warmup):
+        import numpy as np
+        import torch
 
-    import mtpx
+        import mtpx
 
-    T0, p = args.cached, args.accept_rate
-    head = mtpx.MTPHead(ctx, mtpx.HeadConfig(mtpx.LayerConfig(**dict(lc, max_positions=64 + 16 * args.rounds)),
-                                             tc["hc"], tc["lowrank"], tc["vocab"], 98304, 248044), seed=0x5EED0007)
-    H, V, W = lc["hidden"], tc["vocab"], tc["hc"] * lc["hidden"]
-    g = torch.Generator(device="cuda").manual_seed(0x5EED0008)
-    kinds = [target.layer_weights(i).kind for i in range(args.layers)]
-    init_s = time.perf_counter() - t_init
-    print(f"bench: target and head initialised in {init_s:.1f} s", file=sys.stderr, flush=True)
-    results = {}
-    for k in args.depths:
+        args, ctx, target, lc, tc = self.args, self.ctx, self.target, self.lc, self.tc
+        T0, p = args.cached, args.accept_rate
+        V, W = tc["vocab"], tc["hc"] * lc["hidden"]
+        g = torch.Generator(device="cuda").manual_seed(0x5EED0008 + k)
         state = mtpx.TargetState(ctx, target)
-        for i, kind in enumerate(kinds):
+        for i, kind in enumerate(self.kinds):
             if kind == 1:
                 kp, vp, tmax = state.kv(i).buffers()
                 n_kv = lc["kv_heads"] * tmax * lc["head_dim"]
@@ -372,7 +399,7 @@ def e2e_sweep(args, ctx, target, lc, tc, t_init):
                 state.gdn(i).load(conv, ssm)
                 torch.cuda.synchronize()
         state.set_offset(T0)
-        dr = mtpx.Drafter(ctx, head)
+        dr = mtpx.Drafter(ctx, self.head)
         # the last committed chunk of the prompt: 8 tokens and their multi streams
         dr.observe(torch.randint(0, V, (8,), device="cuda", generator=g, dtype=torch.int32),
                    torch.randn(8, W, device="cuda", generator=g).to(torch.bfloat16))
@@ -404,22 +431,24 @@ def e2e_sweep(args, ctx, target, lc, tc, t_init):
             carry.copy_(multi[n:n + 1])
             return n
 
-        for _ in range(min(4, args.rounds)):
+        for _ in range(warmup):
             round_()
         torch.cuda.synchronize()
         t0 = time.perf_counter()
-        acc = [round_() for _ in range(args.rounds)]
+        acc = [round_() for _ in range(rounds)]
         torch.cuda.synchronize()
         dt = time.perf_counter() - t0
         toks = sum(a + 1 for a in acc)
-        results[k] = dict(tok_s=round(toks / dt, 2), ms_per_round=round(dt * 1e3 / args.rounds, 3),
-                          mean_accepted=round(sum(acc) / len(acc), 3), tokens=toks, rounds=args.rounds)
-        print(f"bench: depth {k}: {results[k]}", file=sys.stderr, flush=True)
+        # committed tokens per round at acceptance rate p: 1 + p + p^2 + ... + p^k (every round does the
+        # same work whatever the draw; the draws only decide what is committed)
+        expect = sum(p ** i for i in range(k + 1))
+        res = dict(tok_s=round(expect * rounds / dt, 2), ms_per_round=round(dt * 1e3 / rounds, 3),
+                   expected_tokens_per_round=round(expect, 4), realized_tok_s=round(toks / dt, 2),
+                   mean_accepted=round(sum(acc) / len(acc), 3), tokens=toks, rounds=rounds)
+        print(f"bench: depth {k}: {res}", file=sys.stderr, flush=True)
         dr.close()
         state.close()
-    head.close()
-    best = max(results, key=lambda d: results[d]["tok_s"])
-    return results, best, init_s
+        return res
 
 
 def copy_calibration():
@@ -530,16 +559,16 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", choices=("full", "layer", "e2e"), default="full")
-    ap.add_argument("--depths", type=int, nargs="+", default=[1, 2, 3, 4, 5], help="draft depths of the e2e workload")
-    ap.add_argument("--rounds", type=int, default=48, help="timed rounds per depth of the e2e workload")
+    ap.add_argument("--workload", choices=("full", "layer"), default="full")
+    ap.add_argument("--depths", type=int, nargs="+", default=[1, 2, 3, 4, 5], help="draft depths of the decode sweep")
+    ap.add_argument("--rounds", type=int, default=48, help="rounds per depth of the decode sweep")
     ap.add_argument("--accept-rate", type=float, default=0.7)
     ap.add_argument("--layers", type=int, default=48, help="depth of the full workload")
     ap.add_argument("--verify-width", type=int, default=4)
     ap.add_argument("--cached", type=int, default=1024)
     ap.add_argument("--group-size", type=int, default=64)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--no-e2e", action="store_true", help="full workload: skip the speculative-decode sweep")
+    ap.add_argument("--no-e2e", action="store_true", help="report the config-4 verify as the value (no decode rounds)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="after the timed steps, copy 256 MiB once (the reference kernel for HBM byte counters)")
     args = ap.parse_args()
@@ -555,10 +584,8 @@ def main() -> int:
     }
     if args.workload == "full":
         out = run_full(args, out)
-    elif args.workload == "layer":
-        out = run_layer(args, out)
     else:
-        out = run_e2e(args, out)
+        out = run_layer(args, out)
     print(json.dumps(out))
     return 0
 

@@ -5,9 +5,10 @@ full-depth random-init 125B-A6B model (48 layers: 36 gated-deltanet + 12
 attention, each with hyper-connection mixers and a 512-expert top-10 + shared
 MoE; hidden 2560, vocab 248320, affine 4-bit gs64, all weights resident in HBM)
 with the MTP head.  The committed prefix of 1024 positions is synthetic: random
-attention K/V rows and random GDN states stand in for the prompt (prefill is
-not part of this build); the PLE n-gram block of layer 1 is not part of the
-forward.  A step = one round: k drafter steps, a verify of the carried token
+attention K/V rows, random GDN states and a random PLE state stand in for the
+prompt (prefill is not part of this build).  Layer 1 carries the PLE n-gram
+block with the full n-gram table (16 heads over 320,001,446 rows of 100 bytes,
+32 GB, resident in HBM; --no-ple leaves it out).  A step = one round: k drafter steps, a verify of the carried token
 and the k drafts, the on-device greedy accept (read back once per round), the
 target commit and the drafter finalize.  Random-init drafts almost never match
 the target, so the accepted count is forced at p = 0.7 by a seeded draw.  The
@@ -103,13 +104,59 @@ def target_cfgs(gs: int, max_positions: int, layers: int):
     # linear-attention dims, hyper-connections and vocabulary: fixtures/qwen3_8_125b_a6b_config.json
     tc = dict(key_heads=16, value_heads=48, conv_kernel=4, num_layers=layers, full_attention_interval=4, hc=4,
               lowrank=320, vocab=248320)
+    # the PLE n-gram block on layer index 1 (ple_layer_ids [2] is 1-based): ngram_size 3, 8 heads per
+    # n-gram, ple_embed_dim 2560, conv kernel 4, table rows 4-bit gs32, eos 248044, base 20,000,000
+    tc["ple_layer"] = 1 if layers > 1 else -1
+    tc["ple"] = dict(hidden=lc["hidden"], hc=4, embed_dim=2560, ngram_size=3, heads_per_ngram=8, conv_kernel=4,
+                     group_size=gs, row_group_size=32, eos=248044, vocab_base=20_000_000, token_vocab=248320,
+                     eps=lc["eps"])
     return lc, tc
+
+
+def target_config(mtpx, lc, tc):
+    cfg = mtpx.TargetConfig(mtpx.LayerConfig(**lc), *[tc[k] for k in (
+        "key_heads", "value_heads", "conv_kernel", "num_layers", "full_attention_interval", "hc", "lowrank",
+        "vocab")])
+    cfg.ple_layer = tc["ple_layer"]
+    cfg.ple = mtpx.PLEConfig(**tc["ple"])
+    return cfg
+
+
+def synthetic_prefix(mtpx, ctx, state, lc, tc, kinds, g, T0):
+    """Random committed state in place of a prompt: attention K/V rows, GDN conv rows and
+    recurrent states, the PLE block's conv rows and token context."""
+    import torch
+
+    for i, kind in enumerate(kinds):
+        if kind == 1:
+            kp, vp, tmax = state.kv(i).buffers()
+            n_kv = lc["kv_heads"] * tmax * lc["head_dim"]
+            for ptr, tensor in ((kp, 2 * i + 1), (vp, 2 * i + 2)):
+                mtpx.check(ctx.lib.mtpx_randn_bf16(ctx.h, C.c_void_p(ptr), n_kv, 0x5EED0006, tensor, 1.0),
+                           "randn kv")
+        else:
+            conv = torch.randn(tc["conv_kernel"] - 1, (2 * tc["key_heads"] + tc["value_heads"]) * 128,
+                               device="cuda", generator=g).to(torch.bfloat16)
+            ssm = torch.randn(tc["value_heads"], 128, 128, device="cuda", generator=g) * 0.05
+            state.gdn(i).load(conv, ssm)
+            torch.cuda.synchronize()
+    if tc["ple_layer"] >= 0:
+        pc = tc["ple"]
+        conv = torch.randn((pc["conv_kernel"] - 1) * pc["ngram_size"], pc["hc"] * pc["hidden"], device="cuda",
+                           generator=g).to(torch.bfloat16)
+        context = torch.randint(0, tc["vocab"], (pc["ngram_size"] - 1,), device="cuda", generator=g,
+                                dtype=torch.int32)
+        state.ple().load(conv, context)
+        torch.cuda.synchronize()
+    state.set_offset(T0)
 
 
 def cpu_layer_times(target, state, lc, tc, widths, kinds, seconds=12.0):
     """The oracle on a bounded sample of the target step, one host thread: per verify width M,
-    the first GDN layer and the first attention layer (each with its mixers and MoE) and 16384
-    of the lm_head rows.  -> ({M: (t_gdn, t_attn, t_head_rows)}, rows, iterations)."""
+    the first GDN layer and the first attention layer (each with its mixers and MoE), 16384 of the
+    lm_head rows and the PLE block (its projections, norms and conv from the device; the row gather
+    from the first 65536 table rows, whose cost does not depend on the table's size).
+    -> ({M: (t_gdn, t_attn, t_head_rows, t_ple)}, rows, iterations)."""
     import numpy as np
 
     from oracle import oracle as O
@@ -141,6 +188,23 @@ def cpu_layer_times(target, state, lc, tc, widths, kinds, seconds=12.0):
     rows = 16384
     head = _q(target.weights().lm_head, rows, H, gs)  # the first `rows` rows of lm_head
     pos0, _ = state.info()
+    ple = None
+    if tc["ple_layer"] >= 0:
+        pc, pw = tc["ple"], target.layer_weights(tc["ple_layer"]).ple
+        W, E, nh = hc * H, pc["embed_dim"], 2 * pc["heads_per_ngram"]
+        rd, nt = E // nh, 65536
+        table = (read_device(pw.table.w, nt * rd // 2, np.uint32).reshape(nt, rd // 8),
+                 read_device(pw.table.s, nt * rd // 16, np.uint16).reshape(nt, rd // 32),
+                 read_device(pw.table.b, nt * rd // 16, np.uint16).reshape(nt, rd // 32))
+        vocab = np.array(O.primes_above(nt // nh - 300, nh), np.int64)
+        ple = dict(key_proj=_q(pw.key_proj, W, E, gs), value_proj=_q(pw.value_proj, H, E, gs),
+                   norm_key=read_device(pw.norm_key, 2 * W, np.uint16),
+                   norm_query=read_device(pw.norm_query, 2 * W, np.uint16),
+                   norm_conv=read_device(pw.norm_conv, 2 * W, np.uint16),
+                   conv_w=read_device(pw.conv_w, 2 * W * pc["conv_kernel"], np.uint16).reshape(W, -1), table=table,
+                   mult=np.array(list(pw.table.multiplier)[:3], np.int64), vocab=vocab,
+                   offs=np.concatenate([[0], np.cumsum(vocab)[:-1]]).astype(np.int64))
+        ple_conv = O.f32_to_bf16(r.standard_normal(((pc["conv_kernel"] - 1) * pc["ngram_size"], W)).astype(np.float32))
 
     def layer_step(L, gdn, sW):
         s, n = O.hc_norm(sW, None, None, L["hc"]["scale"], hc, eps)
@@ -160,7 +224,8 @@ def cpu_layer_times(target, state, lc, tc, widths, kinds, seconds=12.0):
     for M in widths:
         sW = O.f32_to_bf16(r.standard_normal((M, hc * H)).astype(np.float32))
         xh = O.f32_to_bf16(r.standard_normal((M, H)).astype(np.float32))
-        tg = ta = th = 0.0
+        ids = r.integers(0, tc["vocab"], M).astype(np.int32)
+        tg = ta = th = tp = 0.0
         n = 0
         t0 = time.perf_counter()
         while n == 0 or time.perf_counter() - t0 < seconds / len(widths):
@@ -171,20 +236,24 @@ def cpu_layer_times(target, state, lc, tc, widths, kinds, seconds=12.0):
             c = time.perf_counter()
             O.qmv(*head, gs, xh)
             d = time.perf_counter()
-            tg, ta, th, n = tg + b - a, ta + c - b, th + d - c, n + 1
-        times[M], iters[M] = (tg / n, ta / n, th / n), n
+            if ple is not None:
+                O.ple_forward(ple, dict(tc["ple"]), sW, ids, ple_conv, ids[:2] if M >= 2 else np.r_[ids, ids])
+            e = time.perf_counter()
+            tg, ta, th, tp, n = tg + b - a, ta + c - b, th + d - c, tp + e - d, n + 1
+        times[M], iters[M] = (tg / n, ta / n, th / n, tp / n), n
     return times, rows, iters
 
 
 def cpu_baseline_full(target, state, lc, tc, M, kinds):
     """CPU baseline of the verify step (config 4): the sampled oracle layers scaled to the stack."""
     times, rows, iters = cpu_layer_times(target, state, lc, tc, [M], kinds)
-    tg, ta, th = times[M]
+    tg, ta, th, tp = times[M]
     n_gdn, n_attn = kinds.count(0), kinds.count(1)
-    step_s = n_gdn * tg + n_attn * ta + th * tc["vocab"] / rows
+    step_s = n_gdn * tg + n_attn * ta + th * tc["vocab"] / rows + tp
     return dict(value=M / step_s, unit="tok/s", cores=1, kind="port",
                 sample=f"{iters[M]} x (one GDN layer {tg:.2f} s, one attention layer {ta:.2f} s, {rows} of "
-                       f"{tc['vocab']} lm_head rows {th:.2f} s) of the same verify step (M={M}) through the C "
+                       f"{tc['vocab']} lm_head rows {th:.2f} s, the PLE block {tp:.2f} s) of the same verify step "
+                       f"(M={M}) through the C "
                        f"oracle, single thread; scaled to {n_gdn} GDN + {n_attn} attention layers and the "
                        f"whole lm_head: {step_s:.1f} s per step")
 
@@ -196,15 +265,15 @@ def cpu_baseline_e2e(target, state, lc, tc, kinds, k, tokens_per_round, shortlis
     verify as in cpu_baseline_full at M = k+1.  tok/s = committed tokens per round / round time."""
     times, rows, iters = cpu_layer_times(target, state, lc, tc, sorted({1, k + 1}), kinds)
     n_gdn, n_attn = kinds.count(0), kinds.count(1)
-    tg, ta, th = times[k + 1]
-    verify_s = n_gdn * tg + n_attn * ta + th * tc["vocab"] / rows
-    _, ta1, th1 = times[1]
+    tg, ta, th, tp = times[k + 1]
+    verify_s = n_gdn * tg + n_attn * ta + th * tc["vocab"] / rows + tp
+    _, ta1, th1, _ = times[1]
     draft_s = ta1 + th1 * shortlist_rows / rows
     round_s = k * draft_s + verify_s
     return dict(value=tokens_per_round / round_s, unit="tok/s", cores=1, kind="port",
                 sample=f"oracle (C, single thread) on sampled layers: verify of {k + 1} tokens = {n_gdn} x GDN "
                        f"layer {tg:.2f} s + {n_attn} x attention layer {ta:.2f} s + lm_head {th * tc['vocab'] / rows:.2f} s "
-                       f"(from {rows} rows) = {verify_s:.1f} s; draft step = attention layer at 1 token {ta1:.2f} s + "
+                       f"(from {rows} rows) + PLE block {tp:.2f} s = {verify_s:.1f} s; draft step = attention layer at 1 token {ta1:.2f} s + "
                        f"{shortlist_rows} shortlist rows {th1 * shortlist_rows / rows:.2f} s = {draft_s:.2f} s; round "
                        f"= {k} drafts + verify = {round_s:.1f} s for {tokens_per_round:.3f} committed tokens "
                        f"(expected at the same acceptance rate); iterations per width {iters}")
@@ -219,26 +288,13 @@ def run_full(args, out):
     lc, tc = target_cfgs(gs, T0 + 64 + 8 * max(args.rounds, args.steps + args.warmup), args.layers)
     ctx = mtpx.Context(0)
     t_init = time.perf_counter()
-    target = mtpx.Target(ctx, mtpx.TargetConfig(mtpx.LayerConfig(**lc), *[tc[k] for k in (
-        "key_heads", "value_heads", "conv_kernel", "num_layers", "full_attention_interval", "hc", "lowrank",
-        "vocab")]), seed=0x5EED0004)
+    if args.no_ple:
+        tc["ple_layer"] = -1
+    target = mtpx.Target(ctx, target_config(mtpx, lc, tc), seed=0x5EED0004)
     state = mtpx.TargetState(ctx, target)
     kinds = [target.layer_weights(i).kind for i in range(args.layers)]
     g = torch.Generator(device="cuda").manual_seed(0x5EED0005)
-    for i, kind in enumerate(kinds):
-        if kind == 1:
-            kp, vp, tmax = state.kv(i).buffers()
-            n_kv = lc["kv_heads"] * tmax * lc["head_dim"]
-            for ptr, tensor in ((kp, 2 * i + 1), (vp, 2 * i + 2)):
-                mtpx.check(ctx.lib.mtpx_randn_bf16(ctx.h, C.c_void_p(ptr), n_kv, 0x5EED0006, tensor, 1.0),
-                           "randn kv")
-        else:
-            conv = torch.randn(tc["conv_kernel"] - 1, (2 * tc["key_heads"] + tc["value_heads"]) * 128,
-                               device="cuda", generator=g).to(torch.bfloat16)
-            ssm = torch.randn(tc["value_heads"], 128, 128, device="cuda", generator=g) * 0.05
-            state.gdn(i).load(conv, ssm)
-            torch.cuda.synchronize()
-    state.set_offset(T0)
+    synthetic_prefix(mtpx, ctx, state, lc, tc, kinds, g, T0)
     torch.cuda.synchronize()
     init_s = time.perf_counter() - t_init
     print(f"bench: {args.layers}-layer target initialised in {init_s:.1f} s", file=sys.stderr, flush=True)
@@ -282,7 +338,12 @@ def run_full(args, out):
     gdn_bytes = n_gdn * (qbytes(pw, H, gs) + qbytes(H, tc["value_heads"] * 128, gs) +
                          2 * 4 * tc["value_heads"] * 128 * 128)
     hc_bytes = args.layers * 2 * (mixer + qbytes(hc, W, gs)) + mixer
-    step_bytes = moe_bytes + attn_bytes + gdn_bytes + hc_bytes + qbytes(V, H, gs) + M * qbytes(1, H, gs)
+    ple_bytes = 0
+    if tc["ple_layer"] >= 0:  # key and value projections + 16 table rows of 100 bytes per token
+        pc = tc["ple"]
+        ple_bytes = qbytes(W, pc["embed_dim"], gs) + qbytes(H, pc["embed_dim"], gs) + M * 16 * 100
+    step_bytes = (moe_bytes + attn_bytes + gdn_bytes + hc_bytes + ple_bytes + qbytes(V, H, gs) +
+                  M * qbytes(1, H, gs))
     kernels = {k: dict(launches=n, avg_us=round(1e3 * ms / n, 3)) for k, (n, ms) in stats.items()}
     gu_s = stats["moe_gate_up"][1] / stats["moe_gate_up"][0] / 1e3
     gu_avg = sum(gu_bytes) / len(gu_bytes)
@@ -311,12 +372,15 @@ def run_full(args, out):
         out["roofline"]["traffic_source"] = tr["source"]
     if args.copy_calibration:
         copy_calibration()
-    base_cfg = {"prefix_positions": T0, "layers": args.layers, "group_size": gs, "parallelism": "none (1 GPU)"}
+    base_cfg = {"prefix_positions": T0, "layers": args.layers, "group_size": gs, "parallelism": "none (1 GPU)",
+                "ple_layer": tc["ple_layer"]}
+    ple_note = ("the PLE n-gram block on layer 1 with the full 320,001,446-row table resident"
+                if tc["ple_layer"] >= 0 else "the PLE block of layer 1 left out (--no-ple)")
     if args.no_e2e:
         out.update({
             "value": verify["value"], "unit": "tok/s", "ms_per_step": verify["ms_per_step"],
-            "config": dict(base_cfg, workload=verify["what"] + " (the PLE block of layer 1 is not in the forward; "
-                                                               "prefix synthetic: random K/V rows and GDN states)",
+            "config": dict(base_cfg, workload=verify["what"] + " (" + ple_note + "; prefix synthetic: random K/V "
+                                                               "rows, GDN and PLE states)",
                            verify_width=M),
             "verify": verify,
         })
@@ -337,7 +401,7 @@ def run_full(args, out):
             f"target ({args.layers} layers: {n_gdn} GDN + {n_attn} attention, hyper-connection mixers, 512-expert "
             f"top-10 + shared MoE, hidden 2560, vocab 248320, gs{gs}, weights resident in HBM) with the MTP head "
             f"(attention + MoE, 98584-row shortlist), after a synthetic committed prefix of {T0} positions "
-            f"(random K/V rows and GDN states; the PLE block of layer 1 is not in the forward). A step = one "
+            f"(random K/V rows, GDN and PLE states; {ple_note}). A step = one "
             f"round: {best} drafter steps, a verify of {best + 1} tokens, the on-device greedy accept (read back "
             f"once per round), target commit and drafter finalize; acceptance forced at p={args.accept_rate} by a "
             f"seeded draw. Draft depth {best} = the best of the sweep {list(args.depths)} ({args.rounds} rounds "
@@ -385,20 +449,7 @@ class E2E:
         V, W = tc["vocab"], tc["hc"] * lc["hidden"]
         g = torch.Generator(device="cuda").manual_seed(0x5EED0008 + k)
         state = mtpx.TargetState(ctx, target)
-        for i, kind in enumerate(self.kinds):
-            if kind == 1:
-                kp, vp, tmax = state.kv(i).buffers()
-                n_kv = lc["kv_heads"] * tmax * lc["head_dim"]
-                for ptr, tensor in ((kp, 2 * i + 1), (vp, 2 * i + 2)):
-                    mtpx.check(ctx.lib.mtpx_randn_bf16(ctx.h, C.c_void_p(ptr), n_kv, 0x5EED0006, tensor, 1.0),
-                               "randn kv")
-            else:
-                conv = torch.randn(tc["conv_kernel"] - 1, (2 * tc["key_heads"] + tc["value_heads"]) * 128,
-                                   device="cuda", generator=g).to(torch.bfloat16)
-                ssm = torch.randn(tc["value_heads"], 128, 128, device="cuda", generator=g) * 0.05
-                state.gdn(i).load(conv, ssm)
-                torch.cuda.synchronize()
-        state.set_offset(T0)
+        synthetic_prefix(mtpx, ctx, state, lc, tc, self.kinds, g, T0)
         dr = mtpx.Drafter(ctx, self.head)
         # the last committed chunk of the prompt: 8 tokens and their multi streams
         dr.observe(torch.randint(0, V, (8,), device="cuda", generator=g, dtype=torch.int32),
@@ -568,6 +619,7 @@ def main() -> int:
     ap.add_argument("--cached", type=int, default=1024)
     ap.add_argument("--group-size", type=int, default=64)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-ple", action="store_true", help="leave the PLE block (and its 32 GB table) out")
     ap.add_argument("--no-e2e", action="store_true", help="report the config-4 verify as the value (no decode rounds)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="after the timed steps, copy 256 MiB once (the reference kernel for HBM byte counters)")

@@ -374,6 +374,83 @@ int mtpx_gdn_core(mtpx_ctx ctx, mtpx_gdn gdn, mtpx_gdn_state st, const uint16_t*
 int mtpx_gdn_forward(mtpx_ctx ctx, mtpx_gdn gdn, mtpx_gdn_state st, const uint16_t* x, int S,
                      uint16_t* y, uint16_t* gated);
 
+/* ---- a20 (part): the PLE n-gram block of the target's layer index 1 -------------------------
+ * pleForward (Runner/FastModel/TrackFastModel.swift:1011-1144) with the three-launch kernels of
+ * Runner/FastModel/TrackFastPLE.swift:
+ *   history = context (the last ctx_len tokens) ++ ids;  per position and head: a row id of the
+ *   n-gram table (docs/ngram-cache-design.md:47-96: shifted copies that never cross an eos,
+ *   mix = XOR of copy_p * multiplier_p over widths 2..ngram_size, id = mix % vocab[h] + offset[h]);
+ *   e = the rows, dequantized ([S, embed_dim]);  key = key_proj(e) [S, hc*H], value = value_proj(e)
+ *   [S, H];  per stream c: dot = sum(norm_key(key_c) * norm_query(stream_c)) in bf16;
+ *   g = sqrt(max(|dot / sqrt(H)|, 1e-6)) * sign;  gated_c = sigmoid(g) * value;
+ *   normed = norm_conv(gated);  out = gated + silu(conv1d_dilated(state ++ normed)).
+ * The table (100-byte rows at the model's geometry) is resident in device memory: the row gather
+ * of the host row source (Qwen4ExpNGramHostRowSource, TrackFastModel.swift:1033-1067) becomes a
+ * device read.  Window state as for the GDN sublayer: a forward leaves the committed conv rows
+ * and context alone; mtpx_ple_commit(n) keeps the window's first n positions (the stage /
+ * stageCaptured of :1097-1140, as an offset). */
+#define MTPX_PLE_MAX_NGRAM 8
+#define MTPX_PLE_MAX_HEADS 32
+typedef struct mtpx_ple_ { void* ctx; } mtpx_ple;
+typedef struct mtpx_ple_state_ { void* ctx; } mtpx_ple_state;
+
+typedef struct {
+  int hidden, hc;          /* the stream is hc*hidden wide (hidden % 256 == 0, <= 4096) */
+  int embed_dim;           /* ple_embed_dim (2560) = heads * row width */
+  int ngram_size;          /* 3: widths 2..ngram_size; also the conv dilation */
+  int heads_per_ngram;     /* 8 */
+  int conv_kernel;         /* ple_conv_kernel_size (4) */
+  int group_size;          /* key/value projections: 32 or 64 */
+  int row_group_size;      /* n-gram table rows: 32 */
+  int32_t eos;             /* eos_token_id (248044) */
+  int64_t vocab_base;      /* ngram_vocab_size_base (20000000): head vocabularies are the primes above it */
+  int64_t token_vocab;     /* vocab_size (248320): bounds the multipliers */
+  float eps;               /* RMS epsilon (1e-6) */
+} mtpx_ple_config;
+
+typedef struct {
+  const uint32_t* w; const uint16_t* s; const uint16_t* b; /* [rows, row_dim/8], [rows, row_dim/row_gs] x2 */
+  int64_t rows;                                            /* sum of the head vocabularies */
+  int64_t multiplier[MTPX_PLE_MAX_NGRAM];                  /* layer_multipliers */
+  int64_t vocab[MTPX_PLE_MAX_HEADS];                       /* ngram_heads_vocab_sizes */
+  int64_t offset[MTPX_PLE_MAX_HEADS];                      /* ngram_heads_offsets */
+} mtpx_ngram_table;
+
+typedef struct {
+  mtpx_q4 key_proj;              /* [hc*hidden, embed_dim] */
+  mtpx_q4 value_proj;            /* [hidden, embed_dim] */
+  const uint16_t* norm_key;      /* bf16 [hc*hidden] */
+  const uint16_t* norm_query;    /* bf16 [hc*hidden] */
+  const uint16_t* norm_conv;     /* bf16 [hc*hidden] */
+  const uint16_t* conv_w;        /* bf16 [hc*hidden, conv_kernel] */
+  mtpx_ngram_table table;
+} mtpx_ple_weights;
+
+/* Random init: q4 projections, norm weights near 1, conv taps ~ N(0, 0.3), a table of
+ * sum(head vocabularies) random rows and multipliers of the documented form (odd, below
+ * (2^63-1) / token_vocab / 2) from a splitmix64 stream of the seed. */
+int mtpx_ple_new_random(mtpx_ctx ctx, const mtpx_ple_config* cfg, uint64_t seed, mtpx_ple* out);
+int mtpx_ple_free(mtpx_ple ple);
+int mtpx_ple_weights_get(mtpx_ple ple, mtpx_ple_weights* out);
+/* Per-request state: conv rows bf16 [(conv_kernel-1)*ngram_size, hc*hidden] (zero) and the
+ * context int32 [max(1, ngram_size-1)] (eos), the reference's fresh-state defaults (:1019-1028). */
+int mtpx_ple_state_new(mtpx_ctx ctx, const mtpx_ple_config* cfg, mtpx_ple_state* out);
+int mtpx_ple_state_free(mtpx_ple_state st);
+/* Committed state in/out (device pointers).  load drops any window; store does not modify it. */
+int mtpx_ple_state_load(mtpx_ctx ctx, mtpx_ple_state st, const uint16_t* conv, const int32_t* context);
+int mtpx_ple_state_store(mtpx_ctx ctx, mtpx_ple_state st, uint16_t* conv, int32_t* context);
+int mtpx_ple_commit(mtpx_ple_state st, int n);
+int mtpx_ple_state_info(mtpx_ple_state st, int* window, int* committed);
+/* Row ids of the last S positions of a history (device int32 [ctx_len + S]) ->
+ * int32 [S, (ngram_size-1)*heads_per_ngram] (-1 where an id falls outside the table):
+ * hostRowIds(history:newCount:) (TrackFastModel.swift:1060). */
+int mtpx_ngram_row_ids(mtpx_ctx ctx, mtpx_ple ple, const int32_t* history, int S, int32_t* out);
+/* One window: ids (device int32 [S], S <= 8), stream bf16 [S, hc*hidden] -> out bf16
+ * [S, hc*hidden] (the block's output, gated + silu(conv)) and/or sum = stream + out (either may
+ * be NULL; embedded bf16 [S, embed_dim] may be NULL). */
+int mtpx_ple_forward(mtpx_ctx ctx, mtpx_ple ple, mtpx_ple_state st, const int32_t* ids, int S,
+                     const uint16_t* stream, uint16_t* out, uint16_t* sum, uint16_t* embedded);
+
 /* ---- a20: the target's verify forward ------------------------------------------------------
  * cbv2ForwardWithHiddenCaptured (Runner/FastModel/TrackFastModel.swift:1463-1475) over
  * fastStreams (:1165-1265):  residual = embed(ids);  per layer
@@ -383,8 +460,10 @@ int mtpx_gdn_forward(mtpx_ctx ctx, mtpx_gdn gdn, mtpx_gdn_state st, const uint16
  * then (multi, n) = hc_norm(residual + out * inject) with the final mixer, mixed = mix(final, n)
  * and logits = lm_head(mixed) (:1330-1333).  A verify leaves the committed state alone:
  * attention caches rewind to it and GDN states keep a journal; mtpx_target_commit(n) keeps the
- * window's first n positions.  The PLE n-gram block of layer 1 (:1188-1200) is not part of
- * this forward. */
+ * window's first n positions.  On the PLE layer (:1188-1200) the first norm's stream goes
+ * through the PLE block (mtpx_ple_forward) and is normed again before the attention mixer:
+ *   stream = hc_norm(residual + out * inject).stream;  stream += ple(stream, ids);
+ *   (stream, n) = hc_norm(stream)   (no inject). */
 #define MTPX_LAYER_GDN 0
 #define MTPX_LAYER_ATTENTION 1
 typedef struct mtpx_target_ { void* ctx; } mtpx_target;
@@ -398,6 +477,8 @@ typedef struct {
   int full_attention_interval;   /* 4: layer i is attention iff (i + 1) % interval == 0 */
   int hc, lowrank;               /* hyper-connection streams (4), mixer rank (320) */
   int64_t vocab;                 /* 248320 */
+  int ple_layer;                 /* the layer with the PLE block (1; -1: none) */
+  mtpx_ple_config ple;           /* its geometry (hidden, hc, group_size, eps: the target's) */
 } mtpx_target_config;
 
 typedef struct {
@@ -405,6 +486,7 @@ typedef struct {
   mtpx_layer_weights attn;       /* attention weights (attention layers) and the layer's MoE */
   mtpx_gdn_weights gdn;          /* GDN layers */
   mtpx_hc_weights attn_hc, mlp_hc;
+  mtpx_ple_weights ple;          /* the PLE layer */
 } mtpx_target_layer_weights;
 
 typedef struct {
@@ -424,6 +506,8 @@ int mtpx_target_state_free(mtpx_target_state st);
 /* The cache of attention layer `layer` / the state of GDN layer `layer` (owned by st). */
 int mtpx_target_state_kv(mtpx_target_state st, int layer, mtpx_kv* out);
 int mtpx_target_state_gdn(mtpx_target_state st, int layer, mtpx_gdn_state* out);
+/* The PLE block's state of the PLE layer (owned by st). */
+int mtpx_target_state_ple(mtpx_target_state st, mtpx_ple_state* out);
 /* Committed positions of every attention cache (a prefix written through mtpx_kv_buffers). */
 int mtpx_target_state_set_offset(mtpx_target_state st, int64_t offset);
 int mtpx_target_state_info(mtpx_target_state st, int64_t* offset, int* window);

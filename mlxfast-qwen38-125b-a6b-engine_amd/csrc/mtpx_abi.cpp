@@ -869,6 +869,262 @@ int gdn_enqueue(Ctx* c, const GdnLayer* L, GdnState* st, const uint16_t* proj, i
 
 
 // ---------------------------------------------------------------------------
+// The PLE n-gram block (layer index 1 of the target).
+namespace {
+
+struct PleGeom {
+  int W, nh, row_dim, ctx_len, nb;  // stream width, heads, row width, carried tokens, carried conv rows
+};
+
+PleGeom ple_geom(const mtpx_ple_config& g) {
+  PleGeom r;
+  r.W = g.hc * g.hidden;
+  r.nh = (g.ngram_size - 1) * g.heads_per_ngram;
+  r.row_dim = r.nh > 0 ? g.embed_dim / r.nh : 0;
+  r.ctx_len = g.ngram_size - 1 > 1 ? g.ngram_size - 1 : 1;
+  r.nb = (g.conv_kernel - 1) * g.ngram_size;
+  return r;
+}
+
+int ple_check(const mtpx_ple_config* g) {
+  ARG(g, "null config");
+  ARG(gs_ok(g->group_size), "group_size=%d", g->group_size);
+  ARG(g->hidden >= 256 && g->hidden % 256 == 0 && g->hidden <= 4096, "hidden=%d (a multiple of 256, <= 4096)",
+      g->hidden);
+  ARG(g->hc >= 1 && g->hc <= 8, "hc=%d", g->hc);
+  ARG(g->ngram_size >= 2 && g->ngram_size <= MTPX_PLE_MAX_NGRAM && g->ngram_size - 1 <= PLE_MAX_CTX, "ngram_size=%d",
+      g->ngram_size);
+  const PleGeom pg = ple_geom(*g);
+  ARG(g->heads_per_ngram >= 1 && pg.nh <= MTPX_PLE_MAX_HEADS, "heads_per_ngram=%d", g->heads_per_ngram);
+  ARG(g->row_group_size == 32 || g->row_group_size == 64, "row_group_size=%d", g->row_group_size);
+  ARG(g->embed_dim % 256 == 0 && g->embed_dim % pg.nh == 0 && pg.row_dim % g->row_group_size == 0 &&
+          k_ok(g->embed_dim, g->group_size),
+      "embed_dim=%d (a multiple of 256 and of the %d heads; row width %d a multiple of row_group_size)", g->embed_dim,
+      pg.nh, pg.row_dim);
+  ARG(g->conv_kernel >= 1 && g->conv_kernel <= 8, "conv_kernel=%d", g->conv_kernel);
+  ARG(g->vocab_base >= 1 && g->vocab_base < ((int64_t)1 << 30), "vocab_base=%lld", (long long)g->vocab_base);
+  ARG(g->token_vocab >= 2 && g->token_vocab < ((int64_t)1 << 31) && g->eos >= 0 && g->eos < g->token_vocab,
+      "token_vocab=%lld eos=%d", (long long)g->token_vocab, g->eos);
+  ARG(g->eps > 0.0f, "eps must be positive");
+  return MTPX_OK;
+}
+
+bool is_prime(int64_t v) {
+  if (v < 2) return false;
+  for (int64_t d = 2; d * d <= v; ++d)
+    if (v % d == 0) return false;
+  return true;
+}
+
+// Head vocabularies (consecutive primes above the base), their offsets (running
+// sum) and the table's row count: docs/ngram-cache-design.md:62-64, 84-89.
+int64_t ngram_heads(const mtpx_ple_config& g, mtpx_ngram_table* t) {
+  const int nh = ple_geom(g).nh;
+  int64_t v = g.vocab_base, off = 0;
+  for (int h = 0; h < nh; ++h) {
+    do ++v;
+    while (!is_prime(v));
+    t->vocab[h] = v;
+    t->offset[h] = off;
+    off += v;
+  }
+  t->rows = off;
+  return off;
+}
+
+struct PleLayer {
+  mtpx_ple_config cfg;
+  mtpx_ple_weights w;
+  int64_t* hash = nullptr;  // device [ngram + 2*heads]: multipliers | vocab sizes | offsets
+  std::vector<void*> allocs;
+};
+
+struct PleState {
+  mtpx_ple_config cfg;
+  uint16_t* conv[2] = {nullptr, nullptr};  // base conv rows per slot [nb, W]
+  uint16_t* win[2] = {nullptr, nullptr};   // window normed rows [MAX_TOKENS, W]
+  int32_t* ctx[2] = {nullptr, nullptr};    // base context [ctx_len]
+  int32_t* ids[2] = {nullptr, nullptr};    // window tokens [MAX_TOKENS]
+  int cur = 0, window = 0, committed = 0;
+  std::vector<void*> allocs;
+};
+
+bool ple_same(const mtpx_ple_config& a, const mtpx_ple_config& b) {
+  return a.hidden == b.hidden && a.hc == b.hc && a.ngram_size == b.ngram_size && a.conv_kernel == b.conv_kernel;
+}
+
+// Random PLE weights; the multipliers are odd and below (2^63-1) / token_vocab / 2, so every
+// product token * multiplier stays non-negative (docs/ngram-cache-design.md:71-79).
+int ple_random(Ctx* c, const mtpx_ple_config& cfg, uint64_t seed, PleLayer* L) {
+  const PleGeom pg = ple_geom(cfg);
+  const int H = cfg.hidden, W = pg.W;
+  RandInit ri{c, seed, cfg.group_size, &L->allocs};
+  mtpx_ple_weights& w = L->w;
+  memset(&w, 0, sizeof(w));
+  ri.qmat(W, cfg.embed_dim, &w.key_proj);
+  ri.qmat(H, cfg.embed_dim, &w.value_proj);
+  w.conv_w = ri.dense((int64_t)W * cfg.conv_kernel, 0.3f);
+  uint64_t hs = seed ^ 0x510e527fade682d1ull;
+  std::vector<uint16_t> nrm(3 * (size_t)W);
+  for (auto& v : nrm) v = bf16_bits((float)(0.8 + 0.4 * host_uniform(hs)));
+  uint16_t* pn = (uint16_t*)ri.alloc(2 * nrm.size());
+  if (pn && hipMemcpy(pn, nrm.data(), 2 * nrm.size(), hipMemcpyHostToDevice) != hipSuccess) ri.ok = false;
+  w.norm_key = pn;
+  w.norm_query = pn ? pn + W : nullptr;
+  w.norm_conv = pn ? pn + 2 * (size_t)W : nullptr;
+  mtpx_ngram_table& t = w.table;
+  const int64_t rows = ngram_heads(cfg, &t);
+  const uint64_t bound = 0x7fffffffffffffffull / (uint64_t)cfg.token_vocab / 2;
+  for (int p = 0; p < cfg.ngram_size; ++p)
+    t.multiplier[p] = (int64_t)(((uint64_t)(host_uniform(hs) * 9007199254740992.0) % (bound / 2)) * 2 + 1);
+  const int rgs = cfg.row_group_size;
+  uint32_t* tw = (uint32_t*)ri.alloc((size_t)rows * pg.row_dim / 2);
+  uint16_t* ts = (uint16_t*)ri.alloc((size_t)rows * (pg.row_dim / rgs) * 2);
+  uint16_t* tb = (uint16_t*)ri.alloc((size_t)rows * (pg.row_dim / rgs) * 2);
+  t.w = tw;
+  t.s = ts;
+  t.b = tb;
+  if (tw && ts && tb) {
+    // random nibbles (bf16 normal bit patterns), scales and biases ~ N(0, 0.02)
+    if (launch_randn_bf16(reinterpret_cast<bf16*>(tw), rows * pg.row_dim / 4, seed, 0x7e000001u, 1.0f, c->stream) ||
+        launch_randn_bf16(reinterpret_cast<bf16*>(ts), rows * (pg.row_dim / rgs), seed, 0x7e000002u, 0.02f,
+                          c->stream) ||
+        launch_randn_bf16(reinterpret_cast<bf16*>(tb), rows * (pg.row_dim / rgs), seed, 0x7e000003u, 0.02f,
+                          c->stream))
+      ri.ok = false;
+  }
+  const int nh = pg.nh, n = cfg.ngram_size;
+  std::vector<int64_t> hv(n + 2 * (size_t)nh);
+  for (int p = 0; p < n; ++p) hv[p] = t.multiplier[p];
+  for (int h = 0; h < nh; ++h) {
+    hv[n + h] = t.vocab[h];
+    hv[n + nh + h] = t.offset[h];
+  }
+  L->hash = (int64_t*)ri.alloc(8 * hv.size());
+  if (L->hash && hipMemcpy(L->hash, hv.data(), 8 * hv.size(), hipMemcpyHostToDevice) != hipSuccess) ri.ok = false;
+  return ri.finish("ple");
+}
+
+PleRowArgs ple_row_args(const PleLayer* L, const int32_t* ids, int S) {
+  const PleGeom pg = ple_geom(L->cfg);
+  PleRowArgs a;
+  memset(&a, 0, sizeof(a));
+  a.S = S;
+  a.ctx_len = pg.ctx_len;
+  a.ngram = L->cfg.ngram_size;
+  a.hpn = L->cfg.heads_per_ngram;
+  a.row_dim = pg.row_dim;
+  a.rgs = L->cfg.row_group_size;
+  a.eos = L->cfg.eos;
+  a.rows = L->w.table.rows;
+  a.hash = L->hash;
+  a.ids = ids;
+  a.tw = L->w.table.w;
+  a.ts = reinterpret_cast<const bf16*>(L->w.table.s);
+  a.tb = reinterpret_cast<const bf16*>(L->w.table.b);
+  return a;
+}
+
+size_t ple_ws_bytes(const mtpx_ple_config& g, int S) {
+  const PleGeom pg = ple_geom(g);
+  return al(2 * (size_t)S * g.embed_dim) + al(4 * (size_t)S * (g.embed_dim / 32) * XP_DW) +
+         al(2 * (size_t)S * pg.W) * 2 + al(2 * (size_t)S * g.hidden) + 4096;
+}
+
+// One window through the block (workspace from the context); the state's slots advance.
+int ple_enqueue(Ctx* c, const PleLayer* L, PleState* st, const int32_t* ids, int S, const uint16_t* stream,
+                uint16_t* out, uint16_t* sum, uint16_t* embedded) {
+  const mtpx_ple_config& g = L->cfg;
+  const PleGeom pg = ple_geom(g);
+  const int H = g.hidden, E = g.embed_dim, gs = g.group_size;
+  uint16_t* emb = embedded ? embedded : ws_take<uint16_t>(c, (size_t)S * E);
+  uint32_t* xp = ws_take<uint32_t>(c, (size_t)S * (E / 32) * XP_DW);
+  uint16_t* key = ws_take<uint16_t>(c, (size_t)S * pg.W);
+  uint16_t* gated = ws_take<uint16_t>(c, (size_t)S * pg.W);
+  uint16_t* value = ws_take<uint16_t>(c, (size_t)S * H);
+  const int cs = st->cur, ns = st->cur ^ 1;
+  PleRowArgs ra = ple_row_args(L, ids, S);
+  ra.P = st->committed;
+  ra.ctx_cur = st->ctx[cs];
+  ra.ids_prev = st->ids[cs];
+  ra.ctx_nxt = st->ctx[ns];
+  ra.ids_nxt = st->ids[ns];
+  ra.emb = reinterpret_cast<bf16*>(emb);
+  ra.xp = xp;
+  hipStream_t s = c->stream;
+  LAUNCH(c, "ple_rows", launch_ple_rows(ra, s));
+  const mtpx_q4& kp = L->w.key_proj;
+  const mtpx_q4& vp = L->w.value_proj;
+  LAUNCH(c, "qmv_ple_key", launch_qmv(kp.w, kp.s, kp.b, kp.sb, pg.W, E, gs, xp, S, key, nullptr, s));
+  LAUNCH(c, "qmv_ple_value", launch_qmv(vp.w, vp.s, vp.b, vp.sb, H, E, gs, xp, S, value, nullptr, s));
+  LAUNCH(c, "ple_gate", launch_ple_gate(key, stream, value, L->w.norm_key, L->w.norm_query, L->w.norm_conv, S, g.hc, H,
+                                        g.eps, gated, st->win[ns], s));
+  PleConvArgs ca;
+  ca.S = S;
+  ca.kc = g.conv_kernel;
+  ca.dil = g.ngram_size;
+  ca.P = st->committed;
+  ca.W = pg.W;
+  ca.conv_cur = st->conv[cs];
+  ca.win_cur = st->win[cs];
+  ca.win_nxt = st->win[ns];
+  ca.conv_w = L->w.conv_w;
+  ca.gated = gated;
+  ca.stream = stream;
+  ca.out = out;
+  ca.sum = sum;
+  ca.conv_nxt = st->conv[ns];
+  LAUNCH(c, "ple_conv", launch_ple_conv(ca, s));
+  st->cur = ns;
+  st->window = S;
+  st->committed = 0;
+  return MTPX_OK;
+}
+
+int ple_state_create(Ctx* c, const mtpx_ple_config& cfg, PleState** out) {
+  const PleGeom pg = ple_geom(cfg);
+  PleState* st = new PleState();
+  st->cfg = cfg;
+  bool ok = true;
+  auto take = [&](size_t bytes) -> void* {
+    void* p = nullptr;
+    if (hipMalloc(&p, bytes) != hipSuccess) {
+      ok = false;
+      return nullptr;
+    }
+    st->allocs.push_back(p);
+    return p;
+  };
+  for (int s = 0; s < 2; ++s) {
+    st->conv[s] = (uint16_t*)take(2 * (size_t)(pg.nb > 0 ? pg.nb : 1) * pg.W);
+    st->win[s] = (uint16_t*)take(2 * (size_t)MAX_TOKENS * pg.W);
+    st->ctx[s] = (int32_t*)take(4 * (size_t)PLE_MAX_CTX);
+    st->ids[s] = (int32_t*)take(4 * (size_t)MAX_TOKENS);
+  }
+  if (ok) {
+    std::vector<int32_t> eos(PLE_MAX_CTX, cfg.eos);
+    if (hipMemsetAsync(st->conv[0], 0, 2 * (size_t)(pg.nb > 0 ? pg.nb : 1) * pg.W, c->stream) != hipSuccess ||
+        hipMemcpyAsync(st->ctx[0], eos.data(), 4 * eos.size(), hipMemcpyHostToDevice, c->stream) != hipSuccess ||
+        hipStreamSynchronize(c->stream) != hipSuccess)
+      ok = false;
+  }
+  if (!ok) {
+    for (void* p : st->allocs) hipFree(p);
+    delete st;
+    return fail(MTPX_ERR_OOM, "ple state allocation failed");
+  }
+  *out = st;
+  return MTPX_OK;
+}
+
+void ple_state_release(PleState* st) {
+  for (void* p : st->allocs) hipFree(p);
+  delete st;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
 // The target model's verify forward.
 namespace {
 
@@ -885,6 +1141,7 @@ struct Target {
   std::vector<TargetLayer> layers;
   mtpx_q4 embed, lm_head;
   mtpx_hc_weights final_hc;
+  PleLayer* ple = nullptr;  // the PLE layer's block (ple_layer >= 0)
   std::vector<void*> allocs;
 };
 
@@ -892,6 +1149,7 @@ struct TargetState {
   Target* t = nullptr;
   std::vector<Kv*> kv;          // per layer (attention layers), else null
   std::vector<GdnState*> gdn;   // per layer (GDN layers), else null
+  PleState* ple = nullptr;      // the PLE layer's state
   std::vector<void*> allocs;
   int32_t* moe_unique = nullptr;  // device [num_layers]: distinct routed experts of the last verify
   int64_t offset = 0;           // committed positions
@@ -921,6 +1179,13 @@ int target_check(const mtpx_target_config* g) {
   ARG(g->hc >= 1 && g->hc <= 8 && g->lowrank >= 32 && g->lowrank % 32 == 0, "hc=%d lowrank=%d", g->hc, g->lowrank);
   ARG(k_ok(g->hc * H, gs) && k_ok(g->lowrank, gs) && g->hc * H <= 256 * 48, "unsupported mixer GEMV depths");
   ARG(g->vocab >= 1 && g->vocab < ((int64_t)1 << 31), "vocab=%lld", (long long)g->vocab);
+  ARG(g->ple_layer >= -1 && g->ple_layer < g->num_layers, "ple_layer=%d of %d layers", g->ple_layer, g->num_layers);
+  if (g->ple_layer >= 0) {
+    ARG(g->ple.hidden == H && g->ple.hc == g->hc && g->ple.group_size == gs,
+        "ple geometry (hidden %d, hc %d, group_size %d) differs from the target's", g->ple.hidden, g->ple.hc,
+        g->ple.group_size);
+    if ((rc = ple_check(&g->ple))) return rc;
+  }
   return MTPX_OK;
 }
 
@@ -934,6 +1199,10 @@ void target_release(Target* t) {
       for (void* p : L.gdn->allocs) hipFree(p);
       delete L.gdn;
     }
+  }
+  if (t->ple) {
+    for (void* p : t->ple->allocs) hipFree(p);
+    delete t->ple;
   }
   for (void* p : t->allocs) hipFree(p);
   delete t;
@@ -952,6 +1221,7 @@ void target_state_release(TargetState* s) {
       for (void* p : g->allocs) hipFree(p);
       delete g;
     }
+  if (s->ple) ple_state_release(s->ple);
   delete s;
 }
 
@@ -1486,6 +1756,140 @@ int mtpx_gdn_forward(mtpx_ctx h, mtpx_gdn gh, mtpx_gdn_state sh, const uint16_t*
 }
 
 
+int mtpx_ple_new_random(mtpx_ctx h, const mtpx_ple_config* cfg, uint64_t seed, mtpx_ple* out) {
+  Ctx* c = C(h);
+  ARG(c && cfg && out, "null argument");
+  int rc = ple_check(cfg);
+  if (rc) return rc;
+  if (set_device(c)) return MTPX_ERR_HIP;
+  PleLayer* L = new PleLayer();
+  L->cfg = *cfg;
+  if ((rc = ple_random(c, *cfg, seed, L))) {
+    for (void* p : L->allocs) hipFree(p);
+    delete L;
+    return rc;
+  }
+  out->ctx = L;
+  return MTPX_OK;
+}
+
+int mtpx_ple_free(mtpx_ple ph) {
+  PleLayer* L = static_cast<PleLayer*>(ph.ctx);
+  if (!L) return MTPX_OK;
+  for (void* p : L->allocs) hipFree(p);
+  delete L;
+  return MTPX_OK;
+}
+
+int mtpx_ple_weights_get(mtpx_ple ph, mtpx_ple_weights* out) {
+  PleLayer* L = static_cast<PleLayer*>(ph.ctx);
+  ARG(L && out, "null argument");
+  *out = L->w;
+  return MTPX_OK;
+}
+
+int mtpx_ple_state_new(mtpx_ctx h, const mtpx_ple_config* cfg, mtpx_ple_state* out) {
+  Ctx* c = C(h);
+  ARG(c && cfg && out, "null argument");
+  int rc = ple_check(cfg);
+  if (rc) return rc;
+  if (set_device(c)) return MTPX_ERR_HIP;
+  PleState* st = nullptr;
+  if ((rc = ple_state_create(c, *cfg, &st))) return rc;
+  out->ctx = st;
+  return MTPX_OK;
+}
+
+int mtpx_ple_state_free(mtpx_ple_state sh) {
+  PleState* st = static_cast<PleState*>(sh.ctx);
+  if (st) ple_state_release(st);
+  return MTPX_OK;
+}
+
+int mtpx_ple_state_load(mtpx_ctx h, mtpx_ple_state sh, const uint16_t* conv, const int32_t* context) {
+  Ctx* c = C(h);
+  PleState* st = static_cast<PleState*>(sh.ctx);
+  ARG(c && st && conv && context, "null argument");
+  if (set_device(c)) return MTPX_ERR_HIP;
+  const PleGeom pg = ple_geom(st->cfg);
+  if (pg.nb > 0)
+    HIP_OK(hipMemcpyAsync(st->conv[st->cur], conv, 2 * (size_t)pg.nb * pg.W, hipMemcpyDeviceToDevice, c->stream));
+  HIP_OK(hipMemcpyAsync(st->ctx[st->cur], context, 4 * (size_t)pg.ctx_len, hipMemcpyDeviceToDevice, c->stream));
+  st->window = 0;
+  st->committed = 0;
+  return MTPX_OK;
+}
+
+// The committed state: rows P.. of the base, then the window's first P rows (and the same for the context).
+int mtpx_ple_state_store(mtpx_ctx h, mtpx_ple_state sh, uint16_t* conv, int32_t* context) {
+  Ctx* c = C(h);
+  PleState* st = static_cast<PleState*>(sh.ctx);
+  ARG(c && st && conv && context, "null argument");
+  if (set_device(c)) return MTPX_ERR_HIP;
+  const PleGeom pg = ple_geom(st->cfg);
+  const int P = st->committed, cs = st->cur;
+  const size_t row = 2 * (size_t)pg.W;
+  const int keep = pg.nb - P > 0 ? pg.nb - P : 0;  // base rows that stay
+  if (keep > 0) HIP_OK(hipMemcpyAsync(conv, st->conv[cs] + (size_t)P * pg.W, keep * row, hipMemcpyDeviceToDevice, c->stream));
+  if (pg.nb - keep > 0)
+    HIP_OK(hipMemcpyAsync(conv + (size_t)keep * pg.W, st->win[cs] + (size_t)(P - (pg.nb - keep)) * pg.W,
+                          (pg.nb - keep) * row, hipMemcpyDeviceToDevice, c->stream));
+  const int ck = pg.ctx_len - P > 0 ? pg.ctx_len - P : 0;
+  if (ck > 0) HIP_OK(hipMemcpyAsync(context, st->ctx[cs] + P, 4 * (size_t)ck, hipMemcpyDeviceToDevice, c->stream));
+  if (pg.ctx_len - ck > 0)
+    HIP_OK(hipMemcpyAsync(context + ck, st->ids[cs] + (P - (pg.ctx_len - ck)), 4 * (size_t)(pg.ctx_len - ck),
+                          hipMemcpyDeviceToDevice, c->stream));
+  return MTPX_OK;
+}
+
+int mtpx_ple_commit(mtpx_ple_state sh, int n) {
+  PleState* st = static_cast<PleState*>(sh.ctx);
+  ARG(st, "null state");
+  if (n < 0 || n > st->window)
+    return fail(MTPX_ERR_STATE, "commit of %d positions; the last window has %d", n, st->window);
+  st->committed = n;
+  return MTPX_OK;
+}
+
+int mtpx_ple_state_info(mtpx_ple_state sh, int* window, int* committed) {
+  PleState* st = static_cast<PleState*>(sh.ctx);
+  ARG(st, "null state");
+  if (window) *window = st->window;
+  if (committed) *committed = st->committed;
+  return MTPX_OK;
+}
+
+int mtpx_ngram_row_ids(mtpx_ctx h, mtpx_ple ph, const int32_t* history, int S, int32_t* out) {
+  Ctx* c = C(h);
+  PleLayer* L = static_cast<PleLayer*>(ph.ctx);
+  ARG(c && L && history && out, "null argument");
+  ARG(S >= 1 && S <= MAX_TOKENS, "S=%d", S);
+  if (set_device(c)) return MTPX_ERR_HIP;
+  const PleGeom pg = ple_geom(L->cfg);
+  PleRowArgs a = ple_row_args(L, history + pg.ctx_len, S);
+  a.ctx_cur = history;
+  a.ids_prev = history;  // P = 0: not read
+  a.row_ids = out;
+  LAUNCH(c, "ngram_row_ids", launch_ple_rows(a, c->stream));
+  return MTPX_OK;
+}
+
+int mtpx_ple_forward(mtpx_ctx h, mtpx_ple ph, mtpx_ple_state sh, const int32_t* ids, int S, const uint16_t* stream,
+                     uint16_t* out, uint16_t* sum, uint16_t* embedded) {
+  Ctx* c = C(h);
+  PleLayer* L = static_cast<PleLayer*>(ph.ctx);
+  PleState* st = static_cast<PleState*>(sh.ctx);
+  ARG(c && L && st && ids && stream, "null argument");
+  ARG(out || sum, "neither out nor sum given");
+  ARG(S >= 1 && S <= MAX_TOKENS, "S=%d", S);
+  ARG(ple_same(L->cfg, st->cfg), "state geometry does not match the block");
+  if (set_device(c)) return MTPX_ERR_HIP;
+  int rc = ws_reserve(c, ple_ws_bytes(L->cfg, S));
+  if (rc) return rc;
+  c->ws_used = 0;
+  return ple_enqueue(c, L, st, ids, S, stream, out, sum, embedded);
+}
+
 int mtpx_target_new_random(mtpx_ctx h, const mtpx_target_config* cfg, uint64_t seed, mtpx_target* out) {
   Ctx* c = C(h);
   ARG(c && cfg && out, "null argument");
@@ -1519,6 +1923,11 @@ int mtpx_target_new_random(mtpx_ctx h, const mtpx_target_config* cfg, uint64_t s
       moe_random(gi, &lc, &L.moe);
       rc = gi.finish("target gdn layer");
     }
+  }
+  if (rc == MTPX_OK && ri.ok && cfg->ple_layer >= 0) {
+    t->ple = new PleLayer();
+    t->ple->cfg = cfg->ple;
+    rc = ple_random(c, cfg->ple, seed ^ 0x5be0cd19137e2179ull, t->ple);
   }
   const int rc2 = ri.finish("target");
   if (rc || rc2) {
@@ -1556,6 +1965,7 @@ int mtpx_target_layer_weights_get(mtpx_target th, int i, mtpx_target_layer_weigh
   if (L.gdn) out->gdn = L.gdn->w;
   out->attn_hc = L.attn_hc;
   out->mlp_hc = L.mlp_hc;
+  if (i == t->cfg.ple_layer && t->ple) out->ple = t->ple->w;
   return MTPX_OK;
 }
 
@@ -1589,6 +1999,7 @@ int mtpx_target_state_new(mtpx_ctx h, mtpx_target th, mtpx_target_state* out) {
       s->gdn[i] = static_cast<GdnState*>(g.ctx);
     }
   }
+  if (rc == MTPX_OK && t->ple) rc = ple_state_create(c, t->cfg.ple, &s->ple);
   if (rc) {
     target_state_release(s);
     return rc;
@@ -1619,6 +2030,14 @@ int mtpx_target_state_gdn(mtpx_target_state sh, int i, mtpx_gdn_state* out) {
   ARG(s && out, "null argument");
   ARG(i >= 0 && i < (int)s->gdn.size() && s->gdn[i], "layer %d is not a GDN layer", i);
   out->ctx = s->gdn[i];
+  return MTPX_OK;
+}
+
+int mtpx_target_state_ple(mtpx_target_state sh, mtpx_ple_state* out) {
+  TargetState* s = static_cast<TargetState*>(sh.ctx);
+  ARG(s && out, "null argument");
+  ARG(s->ple, "the target has no PLE layer");
+  out->ctx = s->ple;
   return MTPX_OK;
 }
 
@@ -1659,6 +2078,7 @@ int mtpx_target_commit(mtpx_target_state sh, int n) {
   if (s->window == 0) return MTPX_OK;  // nothing open: committing nothing again changes nothing
   for (GdnState* g : s->gdn)
     if (g) g->committed = n;
+  if (s->ple) s->ple->committed = n;
   s->offset += n;
   s->window = 0;
   for (Kv* kv : s->kv)
@@ -1693,8 +2113,9 @@ int mtpx_target_verify(mtpx_ctx h, mtpx_target th, mtpx_target_state sh, const i
   const Layer* any_attn = nullptr;
   for (const TargetLayer& L : t->layers)
     if (L.attn) any_attn = L.attn;
-  const size_t per_layer = std::max(mix + moe_ws_bytes(&t->layers[0].moe, S),
-                                    mix + (any_attn ? attn_ws_bytes(any_attn, S, T) : 0)) + 4096;
+  const size_t per_layer = std::max(std::max(mix + moe_ws_bytes(&t->layers[0].moe, S),
+                                             mix + (any_attn ? attn_ws_bytes(any_attn, S, T) : 0)),
+                                    t->ple ? ple_ws_bytes(t->ple->cfg, S) + al(2 * (size_t)S * W) : 0) + 4096;
   const size_t fixed = al(2 * (size_t)S * H) * 5 + al(2 * (size_t)S * W) * 4 + al(2 * (size_t)S * hc) * 2 +
                        al(4 * (size_t)S * (W / 32) * XP_DW) + al(4 * (size_t)S * XB * XP_DW) +
                        al(4 * (size_t)S * (VD / 32) * XP_DW) + al(2 * (size_t)S * gg.pw) + 4096;
@@ -1722,8 +2143,19 @@ int mtpx_target_verify(mtpx_ctx h, mtpx_target th, mtpx_target_state sh, const i
   for (int i = 0; i < (int)t->layers.size(); ++i) {
     const TargetLayer& L = t->layers[i];
     const bool first = i == 0;
-    LAUNCH(c, "hc_norm", launch_hc_norm(first ? e : sM, first ? nullptr : mo, first ? nullptr : jM, S, hc, H,
-                                        first ? 1 : 0, L.attn_hc.norm_scale, eps, sA, nrm, xpW, st));
+    c->ws_used = mark;
+    if (i == g.ple_layer && t->ple) {
+      // the stream of the first inject-norm goes through the PLE block, then is normed again
+      LAUNCH(c, "hc_norm", launch_hc_norm(first ? e : sM, first ? nullptr : mo, first ? nullptr : jM, S, hc, H,
+                                          first ? 1 : 0, L.attn_hc.norm_scale, eps, sA, nrm, nullptr, st));
+      uint16_t* sp = ws_take<uint16_t>(c, (size_t)S * W);
+      if ((rc = ple_enqueue(c, t->ple, s->ple, ids, S, sA, nullptr, sp, nullptr))) return rc;
+      LAUNCH(c, "hc_norm", launch_hc_norm(sp, nullptr, nullptr, S, hc, H, 0, L.attn_hc.norm_scale, eps, sA, nrm, xpW,
+                                          st));
+    } else {
+      LAUNCH(c, "hc_norm", launch_hc_norm(first ? e : sM, first ? nullptr : mo, first ? nullptr : jM, S, hc, H,
+                                          first ? 1 : 0, L.attn_hc.norm_scale, eps, sA, nrm, xpW, st));
+    }
     c->ws_used = mark;
     if ((rc = hc_mix_enqueue(c, hg, &L.attn_hc, nrm, xpW, S, x, jA, xpH))) return rc;
     if (L.kind == MTPX_LAYER_GDN) {

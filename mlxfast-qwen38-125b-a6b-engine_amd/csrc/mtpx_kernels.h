@@ -180,4 +180,43 @@ struct GdnArgs {
 hipError_t launch_gdn_step(const GdnArgs& a, hipStream_t st);
 hipError_t launch_gdn_replay(const GdnArgs& a, float* ssm_dst, bf16* conv_dst, hipStream_t st);
 
+// --- PLE n-gram block (ple.hip)
+constexpr int PLE_MAX_NGRAM = 8;
+constexpr int PLE_MAX_HEADS = 32;  // (ngram - 1) * heads_per_ngram
+constexpr int PLE_MAX_CTX = 8;     // carried context tokens
+
+struct PleRowArgs {
+  int S, ctx_len, ngram, hpn, row_dim, rgs, P;  // window, context, hash geometry, row width and groups, committed
+  int32_t eos;
+  int64_t rows;                  // table rows
+  const int64_t* hash;           // device [ngram + 2*heads]: multipliers | head vocab sizes | head offsets
+  const int32_t* ctx_cur;        // [ctx_len] base context of the previous window
+  const int32_t* ids_prev;       // [*] previous window's tokens
+  const int32_t* ids;            // [S] this window's tokens
+  int32_t *ctx_nxt, *ids_nxt;    // this window's base context and tokens (or null)
+  int32_t* row_ids;              // [S, heads] or null
+  const uint32_t* tw;            // table [rows, row_dim/8]
+  const bf16 *ts, *tb;           // [rows, row_dim/rgs]
+  bf16* emb;                     // [S, heads*row_dim] or null
+  uint32_t* xp;                  // prepared blocks of emb or null
+};
+hipError_t launch_ple_rows(const PleRowArgs& a, hipStream_t st);
+hipError_t launch_ple_gate(const bf16* key, const bf16* stream, const bf16* value, const bf16* kscale,
+                           const bf16* qscale, const bf16* cscale, int S, int hc, int H, float eps, bf16* gated,
+                           bf16* normed, hipStream_t st);
+struct PleConvArgs {
+  int S, kc, dil, P;
+  int64_t W;
+  const bf16* conv_cur;  // [nb, W] base rows of the previous window
+  const bf16* win_cur;   // [*, W] previous window's normed rows
+  const bf16* win_nxt;   // [S, W] this window's normed rows
+  const bf16* conv_w;    // [W, kc]
+  const bf16* gated;     // [S, W]
+  const bf16* stream;    // [S, W] (for sum)
+  bf16* out;             // [S, W] gated + silu(conv) or null
+  bf16* sum;             // [S, W] stream + out or null
+  bf16* conv_nxt;        // [nb, W] this window's base rows or null
+};
+hipError_t launch_ple_conv(const PleConvArgs& a, hipStream_t st);
+
 }  // namespace mtpx

@@ -12,10 +12,12 @@ import ctypes as C
 
 from . import _lib
 from ._lib import (DrafterInfo, GDNConfig, GDNWeights, Handle, HCWeights, HeadConfig, HeadWeights, LayerConfig,
-                   LayerWeights, MoEWeights, MtpxError, Q4, TargetConfig, TargetLayerWeights, TargetWeights, check)
+                   LayerWeights, MoEWeights, MtpxError, NGramTable, PLEConfig, PLEWeights, Q4, TargetConfig,
+                   TargetLayerWeights, TargetWeights, check)
 
-__all__ = ["Context", "KVCache", "DecoderLayer", "MTPHead", "Drafter", "GDN", "GDNState", "Target", "TargetState",
-           "MoEWeights", "LayerConfig", "HeadConfig", "GDNConfig", "TargetConfig", "MtpxError", "moe_weights_from"]
+__all__ = ["Context", "KVCache", "DecoderLayer", "MTPHead", "Drafter", "GDN", "GDNState", "PLE", "PLEState", "Target",
+           "TargetState", "MoEWeights", "LayerConfig", "HeadConfig", "GDNConfig", "PLEConfig", "TargetConfig",
+           "MtpxError", "moe_weights_from"]
 
 
 def _ptr(t):
@@ -383,6 +385,74 @@ class GDNState:
         return w.value, c.value
 
 
+class PLE:
+    """The PLE n-gram block with seeded random weights and a resident row table (mtpx_ple)."""
+
+    def __init__(self, ctx: Context, cfg: PLEConfig, seed: int):
+        self.ctx = ctx
+        self.cfg = cfg
+        self.h = Handle()
+        check(ctx.lib.mtpx_ple_new_random(ctx.h, C.byref(cfg), seed, C.byref(self.h)), "ple_new_random")
+
+    def close(self):
+        if self.h.ctx:
+            self.ctx.lib.mtpx_ple_free(self.h)
+            self.h.ctx = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def weights(self) -> PLEWeights:
+        w = PLEWeights()
+        check(self.ctx.lib.mtpx_ple_weights_get(self.h, C.byref(w)), "ple_weights_get")
+        return w
+
+    def row_ids(self, history, S: int, out):
+        check(self.ctx.lib.mtpx_ngram_row_ids(self.ctx.h, self.h, _ptr(history), S, _ptr(out)), "ngram_row_ids")
+
+    def forward(self, state: "PLEState", ids, stream, out=None, sum=None, embedded=None):
+        check(self.ctx.lib.mtpx_ple_forward(self.ctx.h, self.h, state.h, _ptr(ids), ids.shape[0], _ptr(stream),
+                                            _ptr(out), _ptr(sum), _ptr(embedded)), "ple_forward")
+
+
+class PLEState:
+    """Carried conv rows + token context of the PLE block for one request, with the last
+    window (mtpx_ple_state)."""
+
+    def __init__(self, ctx: Context, cfg: PLEConfig):
+        self.ctx = ctx
+        self.h = Handle()
+        check(ctx.lib.mtpx_ple_state_new(ctx.h, C.byref(cfg), C.byref(self.h)), "ple_state_new")
+
+    def close(self):
+        if self.h.ctx:
+            self.ctx.lib.mtpx_ple_state_free(self.h)
+            self.h.ctx = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def load(self, conv, context):
+        check(self.ctx.lib.mtpx_ple_state_load(self.ctx.h, self.h, _ptr(conv), _ptr(context)), "ple_state_load")
+
+    def store(self, conv, context):
+        check(self.ctx.lib.mtpx_ple_state_store(self.ctx.h, self.h, _ptr(conv), _ptr(context)), "ple_state_store")
+
+    def commit(self, n: int):
+        check(self.ctx.lib.mtpx_ple_commit(self.h, n), "ple_commit")
+
+    def info(self):
+        w, c = C.c_int(), C.c_int()
+        check(self.ctx.lib.mtpx_ple_state_info(self.h, C.byref(w), C.byref(c)), "ple_state_info")
+        return w.value, c.value
+
+
 def _borrowed(cls, ctx, handle):
     """A wrapper around a handle owned by another object (its close() frees nothing)."""
     o = cls.__new__(cls)
@@ -456,6 +526,11 @@ class TargetState:
         h = Handle()
         check(self.ctx.lib.mtpx_target_state_gdn(self.h, layer, C.byref(h)), "target_state_gdn")
         return _borrowed(GDNState, self.ctx, h)
+
+    def ple(self) -> PLEState:
+        h = Handle()
+        check(self.ctx.lib.mtpx_target_state_ple(self.h, C.byref(h)), "target_state_ple")
+        return _borrowed(PLEState, self.ctx, h)
 
     def set_offset(self, offset: int):
         check(self.ctx.lib.mtpx_target_state_set_offset(self.h, offset), "target_state_set_offset")

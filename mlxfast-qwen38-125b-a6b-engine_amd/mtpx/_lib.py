@@ -79,15 +79,35 @@ class GDNWeights(C.Structure):
                 ("out_proj", Q4)]
 
 
+PLE_MAX_NGRAM = 8
+PLE_MAX_HEADS = 32
+
+
+class PLEConfig(C.Structure):
+    _fields_ = [("hidden", INT), ("hc", INT), ("embed_dim", INT), ("ngram_size", INT), ("heads_per_ngram", INT),
+                ("conv_kernel", INT), ("group_size", INT), ("row_group_size", INT), ("eos", I32),
+                ("vocab_base", I64), ("token_vocab", I64), ("eps", C.c_float)]
+
+
+class NGramTable(C.Structure):
+    _fields_ = [("w", P), ("s", P), ("b", P), ("rows", I64), ("multiplier", I64 * PLE_MAX_NGRAM),
+                ("vocab", I64 * PLE_MAX_HEADS), ("offset", I64 * PLE_MAX_HEADS)]
+
+
+class PLEWeights(C.Structure):
+    _fields_ = [("key_proj", Q4), ("value_proj", Q4), ("norm_key", P), ("norm_query", P), ("norm_conv", P),
+                ("conv_w", P), ("table", NGramTable)]
+
+
 class TargetConfig(C.Structure):
     _fields_ = [("layer", LayerConfig), ("key_heads", INT), ("value_heads", INT), ("conv_kernel", INT),
                 ("num_layers", INT), ("full_attention_interval", INT), ("hc", INT), ("lowrank", INT),
-                ("vocab", I64)]
+                ("vocab", I64), ("ple_layer", INT), ("ple", PLEConfig)]
 
 
 class TargetLayerWeights(C.Structure):
     _fields_ = [("kind", INT), ("attn", LayerWeights), ("gdn", GDNWeights), ("attn_hc", HCWeights),
-                ("mlp_hc", HCWeights)]
+                ("mlp_hc", HCWeights), ("ple", PLEWeights)]
 
 
 class TargetWeights(C.Structure):
@@ -150,6 +170,18 @@ _SIGS = {
     "mtpx_gdn_state_info": (INT, [Handle, C.POINTER(INT), C.POINTER(INT)]),
     "mtpx_gdn_core": (INT, [Handle, Handle, Handle, P, INT, P]),
     "mtpx_gdn_forward": (INT, [Handle, Handle, Handle, P, INT, P, P]),
+    "mtpx_ple_new_random": (INT, [Handle, C.POINTER(PLEConfig), U64, C.POINTER(Handle)]),
+    "mtpx_ple_free": (INT, [Handle]),
+    "mtpx_ple_weights_get": (INT, [Handle, C.POINTER(PLEWeights)]),
+    "mtpx_ple_state_new": (INT, [Handle, C.POINTER(PLEConfig), C.POINTER(Handle)]),
+    "mtpx_ple_state_free": (INT, [Handle]),
+    "mtpx_ple_state_load": (INT, [Handle, Handle, P, P]),
+    "mtpx_ple_state_store": (INT, [Handle, Handle, P, P]),
+    "mtpx_ple_commit": (INT, [Handle, INT]),
+    "mtpx_ple_state_info": (INT, [Handle, C.POINTER(INT), C.POINTER(INT)]),
+    "mtpx_ngram_row_ids": (INT, [Handle, Handle, P, INT, P]),
+    "mtpx_ple_forward": (INT, [Handle, Handle, Handle, P, INT, P, P, P, P]),
+    "mtpx_target_state_ple": (INT, [Handle, C.POINTER(Handle)]),
     "mtpx_target_new_random": (INT, [Handle, C.POINTER(TargetConfig), U64, C.POINTER(Handle)]),
     "mtpx_target_free": (INT, [Handle]),
     "mtpx_target_weights_get": (INT, [Handle, C.POINTER(TargetWeights)]),

@@ -1131,3 +1131,134 @@ void o_gdn_core(const o_gdn_geom* g, const o_bf16* proj, int S, o_bf16* conv_sta
   free(dec);
   free(bet);
 }
+
+/* ======================================================================== */
+/* PLE n-gram block (layer index 1 of the target)                            */
+/* ======================================================================== */
+
+/* Row ids of the n-gram table for the last S positions of a token history
+ * (docs/ngram-cache-design.md:47-96, the hash the reference's host row source
+ * computes at FM/TrackFastModel.swift:1036-1060):
+ *   history [ctx_len + S]: the carried context, then the window's tokens;
+ *   copy p (p = 0..ngram_size-1) of position u is history[u-p], or eos when an
+ *   eos token lies strictly between u-p and u (a shift never crosses an eos);
+ *   width n = 2..ngram_size: mix = XOR_{p<n} copy_p * mult[p] (64-bit);
+ *   head h of width n (global head (n-2)*heads_per_ngram + h):
+ *   id = mix % vocab[head] + offset[head].
+ * out [S][(ngram_size-1)*heads_per_ngram]; an id outside [0, rows) -> -1.
+ * Parity: the prime rule for vocab[] is pinned by the design note's row total;
+ * the eos-barrier extent and the head order are restated from the note's
+ * prose (the fork's hash and its tests are absent): parity unpinned. */
+void o_ngram_row_ids(const int32_t* history, int ctx_len, int S, int ngram_size, int heads_per_ngram,
+                     const int64_t* mult, const int64_t* vocab, const int64_t* offs, int64_t rows, int32_t eos,
+                     int32_t* out) {
+  const int nh = (ngram_size - 1) * heads_per_ngram;
+  for (int i = 0; i < S; ++i) {
+    const int u = ctx_len + i;
+    int64_t copy[16];
+    int crossed = 0;
+    for (int p = 0; p < ngram_size; ++p) {
+      if (p >= 2 && history[u - p + 1] == eos) crossed = 1; /* eos at u-1 .. u-p+1 */
+      copy[p] = crossed ? (int64_t)eos : (int64_t)history[u - p];
+    }
+    for (int n = 2; n <= ngram_size; ++n) {
+      uint64_t mix = 0;
+      for (int p = 0; p < n; ++p) mix ^= (uint64_t)copy[p] * (uint64_t)mult[p];
+      for (int h = 0; h < heads_per_ngram; ++h) {
+        const int hd = (n - 2) * heads_per_ngram + h;
+        const int64_t m = (int64_t)mix;
+        const int64_t id = m % vocab[hd] + offs[hd];
+        out[(int64_t)i * nh + hd] = (id >= 0 && id < rows) ? (int32_t)id : -1;
+      }
+    }
+  }
+}
+
+/* The gate of one (position, stream) pair of the PLE block
+ * (FM/TrackFastPLE.swift:60-220: track_ple_prod, MLX's sum, track_ple_gated),
+ * in this build's evaluation order.  H % 128 == 0, H <= 4096; lane l of H/4
+ * owns elements 4l..4l+3, lanes form groups of 32 (NG = H/128):
+ *   kacc = fmaf chain of k^2 over the lane's 4, bfly32 per group, bfly32 over
+ *   the NG group sums (zero-padded to 32); kinv = 1/sqrt(kacc/H + eps); same q;
+ *   kn = bf16(bf16(k*kinv) * kscale); qn = bf16(bf16(q*qinv) * qscale);
+ *   p = bf16(kn*qn);
+ *   dot: MLX's bf16 row sum -- per lane t = bf16(p_i + t) over its 4, then
+ *   bf16(bfly32) per group, then bf16(bfly32) over the groups;
+ *   g = bf16(dot / bf16(sqrt(H))); g = bf16(sqrt(max(|g|, bf16(1e-6)))) * sign(g);
+ *   sgm = sigmoid_bf16(g); v = bf16(sgm * value);
+ *   vacc as kacc over v; normed = bf16(bf16(v * vinv) * cscale).
+ * key, stream, kscale, qscale, cscale, gated, normed: this pair's H elements;
+ * value [H].  Returns the bf16 dot (as float). */
+float o_ple_gate(const o_bf16* key, const o_bf16* stream, const o_bf16* value, const o_bf16* kscale,
+                 const o_bf16* qscale, const o_bf16* cscale, int H, float eps, o_bf16* gated, o_bf16* normed) {
+  const int NL = H / 4, NG = H / 128;
+  float kl[1024], ql[1024], tl[1024], grp[32], gk[32], gq[32];
+  for (int l = 0; l < NL; ++l) {
+    float ka = 0.0f, qa = 0.0f;
+    for (int i = 0; i < 4; ++i) {
+      const float k = o_bf2f(key[4 * l + i]), q = o_bf2f(stream[4 * l + i]);
+      ka = fmaf(k, k, ka);
+      qa = fmaf(q, q, qa);
+    }
+    kl[l] = ka;
+    ql[l] = qa;
+  }
+  for (int g = 0; g < 32; ++g) {
+    gk[g] = g < NG ? bfly32(kl + 32 * g) : 0.0f;
+    gq[g] = g < NG ? bfly32(ql + 32 * g) : 0.0f;
+  }
+  const float kinv = 1.0f / sqrtf(bfly32(gk) / (float)H + eps);
+  const float qinv = 1.0f / sqrtf(bfly32(gq) / (float)H + eps);
+  for (int l = 0; l < NL; ++l) {
+    float t = 0.0f;
+    for (int i = 0; i < 4; ++i) {
+      const int d = 4 * l + i;
+      const float kn = o_round_bf(o_round_bf(o_bf2f(key[d]) * kinv) * o_bf2f(kscale[d]));
+      const float qn = o_round_bf(o_round_bf(o_bf2f(stream[d]) * qinv) * o_bf2f(qscale[d]));
+      t = o_round_bf(o_round_bf(kn * qn) + t);
+    }
+    tl[l] = t;
+  }
+  for (int g = 0; g < 32; ++g) grp[g] = g < NG ? o_round_bf(bfly32(tl + 32 * g)) : 0.0f;
+  const float dot = o_round_bf(bfly32(grp));
+  const float divisor = o_round_bf(sqrtf((float)H));
+  const float floor_v = o_round_bf(1e-6f);
+  float g = o_round_bf(dot / divisor);
+  const float a = fabsf(g);
+  const float mx = isnan(a) ? a : (a > floor_v ? a : floor_v);
+  const float sg = (float)((g > 0.0f) - (g < 0.0f));
+  g = o_round_bf(o_round_bf(sqrtf(mx)) * sg);
+  const float sgm = o_sigmoid_bf16(g);
+  float vl[1024], gv[32];
+  for (int l = 0; l < NL; ++l) {
+    float va = 0.0f;
+    for (int i = 0; i < 4; ++i) {
+      const int d = 4 * l + i;
+      const float v = o_round_bf(sgm * o_bf2f(value[d]));
+      gated[d] = o_f2bf(v);
+      va = fmaf(v, v, va);
+    }
+    vl[l] = va;
+  }
+  for (int q = 0; q < 32; ++q) gv[q] = q < NG ? bfly32(vl + 32 * q) : 0.0f;
+  const float vinv = 1.0f / sqrtf(bfly32(gv) / (float)H + eps);
+  for (int d = 0; d < H; ++d)
+    normed[d] = o_f2bf(o_round_bf(o_bf2f(gated[d]) * vinv) * o_bf2f(cscale[d]));
+  return dot;
+}
+
+/* The dilated depthwise conv, SiLU and gated add of the PLE block
+ * (FM/TrackFastPLE.swift:222-262, track_ple_conv):
+ *   full [nb + S][W] (carried rows, then the window's normed rows),
+ *   nb = (kc-1)*dil; conv_w [W][kc]:
+ *   acc = sum_j full[t + j*dil][c] * conv_w[c][j] (f32, j ascending, mul then add);
+ *   out[t][c] = bf16(gated[t][c] + silu_bf16(bf16(acc))). */
+void o_ple_conv(const o_bf16* full, const o_bf16* conv_w, const o_bf16* gated, int S, int64_t W, int kc, int dil,
+                o_bf16* out) {
+  for (int t = 0; t < S; ++t)
+    for (int64_t c = 0; c < W; ++c) {
+      float acc = 0.0f;
+      for (int j = 0; j < kc; ++j) acc = acc + o_bf2f(full[(int64_t)(t + j * dil) * W + c]) * o_bf2f(conv_w[c * kc + j]);
+      out[(int64_t)t * W + c] = o_f2bf(o_bf2f(gated[(int64_t)t * W + c]) + o_silu_bf16(o_round_bf(acc)));
+    }
+}

@@ -124,6 +124,15 @@ void o_accept_sample(const float* tlogits, const float* dlogits, int k, int64_t 
                      uint64_t offset, int32_t kv_offset, int32_t* out3);
 float o_softmax_row_sum(const float* e, int64_t V);
 
+/* PLE n-gram block (layer index 1): row ids, gate, conv. */
+void o_ngram_row_ids(const int32_t* history, int ctx_len, int S, int ngram_size, int heads_per_ngram,
+                     const int64_t* mult, const int64_t* vocab, const int64_t* offs, int64_t rows, int32_t eos,
+                     int32_t* out);
+float o_ple_gate(const o_bf16* key, const o_bf16* stream, const o_bf16* value, const o_bf16* kscale,
+                 const o_bf16* qscale, const o_bf16* cscale, int H, float eps, o_bf16* gated, o_bf16* normed);
+void o_ple_conv(const o_bf16* full, const o_bf16* conv_w, const o_bf16* gated, int S, int64_t W, int kc, int dil,
+                o_bf16* out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -74,6 +74,9 @@ def _declare(L):
         "o_logaddexp0_bf16": (F32, [F32]),
         "o_sigmoid_f32": (F32, [F32]),
         "o_gdn_core": (None, [P, P, C.c_int, P, P, P, P, P, P, F32, P, P, P, P, P, P, P, P]),
+        "o_ngram_row_ids": (None, [P, C.c_int, C.c_int, C.c_int, C.c_int, P, P, P, I64, I32, P]),
+        "o_ple_gate": (F32, [P, P, P, P, P, P, C.c_int, F32, P, P]),
+        "o_ple_conv": (None, [P, P, P, C.c_int, I64, C.c_int, C.c_int, P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -380,3 +383,92 @@ def gdn_core(g, proj, conv_state, ssm, conv_w, neg_exp_alog, dt_bias, norm_w, ep
     out["conv_state"] = cs
     out["ssm"] = st
     return out
+
+
+# ---------------------------------------------------------------------------- PLE n-gram block
+def primes_above(base: int, n: int):
+    """The n consecutive primes above base (the n-gram heads' vocabulary sizes)."""
+    out, v = [], base
+    while len(out) < n:
+        v += 1
+        if v > 1 and all(v % d for d in range(2, int(v ** 0.5) + 1)):
+            out.append(v)
+    return out
+
+
+def ngram_row_ids(history, ctx_len, ngram_size, heads_per_ngram, mult, vocab, offs, rows, eos):
+    """Row ids [S, (ngram_size-1)*heads_per_ngram] of the last S = len(history) - ctx_len positions
+    (-1 where an id falls outside the table)."""
+    h = np.ascontiguousarray(history, np.int32)
+    S = h.size - ctx_len
+    nh = (ngram_size - 1) * heads_per_ngram
+    out = np.zeros((S, nh), np.int32)
+    lib().o_ngram_row_ids(_p(h), ctx_len, S, ngram_size, heads_per_ngram,
+                          _p(np.ascontiguousarray(mult, np.int64)), _p(np.ascontiguousarray(vocab, np.int64)),
+                          _p(np.ascontiguousarray(offs, np.int64)), int(rows), int(eos), _p(out))
+    return out
+
+
+def ple_gate(key, stream, value, kscale, qscale, cscale, eps):
+    """One (position, stream) pair: -> (gated [H], normed [H], dot as float)."""
+    key = np.ascontiguousarray(key, np.uint16)
+    H = key.size
+    gated = np.zeros(H, np.uint16)
+    normed = np.zeros(H, np.uint16)
+    dot = lib().o_ple_gate(_p(key), _p(np.ascontiguousarray(stream, np.uint16)),
+                           _p(np.ascontiguousarray(value, np.uint16)), _p(np.ascontiguousarray(kscale, np.uint16)),
+                           _p(np.ascontiguousarray(qscale, np.uint16)), _p(np.ascontiguousarray(cscale, np.uint16)),
+                           H, eps, _p(gated), _p(normed))
+    return gated, normed, dot
+
+
+def ple_conv(full, conv_w, gated, dil):
+    full = np.ascontiguousarray(full, np.uint16)
+    gated = np.ascontiguousarray(gated, np.uint16)
+    cw = np.ascontiguousarray(conv_w, np.uint16)
+    S, W = gated.shape
+    kc = cw.shape[1]
+    assert full.shape == (S + (kc - 1) * dil, W)
+    out = np.zeros((S, W), np.uint16)
+    lib().o_ple_conv(_p(full), _p(cw), _p(gated), S, W, kc, dil, _p(out))
+    return out
+
+
+def ple_forward(w, cfg, stream, ids, conv_state, context):
+    """The PLE block over one window (Runner/FastModel/TrackFastModel.swift:1011-1144, the three-launch
+    path) on the committed state (conv_state [nb, W], context [ctx_len] int32).
+    w: dict(key_proj, value_proj (q4 triples), norm_key, norm_query, norm_conv [W], conv_w [W, kc],
+    table (q4 triple of [rows, row_dim]), mult, vocab, offs).
+    cfg: dict(hidden, hc, ngram_size, heads_per_ngram, group_size, row_group_size, eos, eps).
+    Returns dict(out, sum, row_ids, embedded, key, value, gated, normed, full, history)."""
+    H, hc, n, hpn = cfg["hidden"], cfg["hc"], cfg["ngram_size"], cfg["heads_per_ngram"]
+    W, gs, eps = hc * H, cfg["group_size"], cfg["eps"]
+    ids = np.asarray(ids, np.int32)
+    S = ids.size
+    ctx_len = len(context)
+    hist = np.concatenate([np.asarray(context, np.int32), ids])
+    tw, ts, tb = w["table"]
+    rid = ngram_row_ids(hist, ctx_len, n, hpn, w["mult"], w["vocab"], w["offs"], tw.shape[0], cfg["eos"])
+    flat = rid.reshape(-1)
+    rows = embed_rows(tw, ts, tb, cfg["row_group_size"], np.where(flat < 0, 0, flat))
+    rows[flat < 0] = 0
+    emb = rows.reshape(S, -1)
+    key, _ = qmv(*w["key_proj"], gs, emb)
+    value, _ = qmv(*w["value_proj"], gs, emb)
+    gated = np.zeros((S, W), np.uint16)
+    normed = np.zeros((S, W), np.uint16)
+    for t in range(S):
+        for c in range(hc):
+            sl = slice(c * H, (c + 1) * H)
+            gated[t, sl], normed[t, sl], _ = ple_gate(key[t, sl], stream[t, sl], value[t], w["norm_key"][sl],
+                                                      w["norm_query"][sl], w["norm_conv"][sl], eps)
+    full = np.concatenate([np.asarray(conv_state, np.uint16).reshape(-1, W), normed])
+    out = ple_conv(full, w["conv_w"], gated, n)
+    total = f32_to_bf16(bf16_to_f32(stream) + bf16_to_f32(out))
+    return dict(out=out, sum=total, row_ids=rid, embedded=emb, key=key, value=value, gated=gated, normed=normed,
+                full=full, history=hist)
+
+
+def ple_advance(res, n, nb, ctx_len):
+    """The committed PLE state after the first n positions of a window: (conv_state, context)."""
+    return res["full"][n:n + nb].copy(), res["history"][n:n + ctx_len].copy()

@@ -5,7 +5,9 @@ the verify forward through the CPU oracle in the order of
 Runner/FastModel/TrackFastModel.swift:1165-1265 (fastStreams: hyper-connection
 inject + norm, mixer, GDN or attention, inject + norm, mixer, MoE per layer;
 the final mixer) and :1330-1333 (lm_head on the mixed row), with the window
-commit of :726-731 as a replay of the committed positions.
+commit of :726-731 as a replay of the committed positions.  On the PLE layer
+(:1188-1200) the first inject-norm's stream goes through the PLE block
+(oracle.ple_forward) and is normed again.
 
 Parity unpinned: the layer wiring follows those files by reading only; every
 piece it calls is pinned on its own (tests/test_oracle_*.py).
@@ -40,6 +42,29 @@ def download_gdn(w, H, hk, hv, kc, gs):
                 geom=g)
 
 
+def ple_cfg_dict(pc):
+    """The oracle's PLE config dict from an mtpx.PLEConfig."""
+    return dict(hidden=pc.hidden, hc=pc.hc, embed_dim=pc.embed_dim, ngram_size=pc.ngram_size,
+                heads_per_ngram=pc.heads_per_ngram, conv_kernel=pc.conv_kernel, group_size=pc.group_size,
+                row_group_size=pc.row_group_size, eos=pc.eos, eps=pc.eps)
+
+
+def download_ple(pw, pc):
+    """Device weights of a PLE block (mtpx.PLEWeights) for oracle.ple_forward."""
+    H, W, E, gs, rgs = pc.hidden, pc.hc * pc.hidden, pc.embed_dim, pc.group_size, pc.row_group_size
+    nh = (pc.ngram_size - 1) * pc.heads_per_ngram
+    rd = E // nh
+    t = pw.table
+    rows = t.rows
+    table = (read_device(t.w, rows * rd // 2, np.uint32).reshape(rows, rd // 8),
+             _bf(t.s, rows * rd // rgs).reshape(rows, rd // rgs), _bf(t.b, rows * rd // rgs).reshape(rows, rd // rgs))
+    return dict(key_proj=_q(pw.key_proj, W, E, gs), value_proj=_q(pw.value_proj, H, E, gs),
+                norm_key=_bf(pw.norm_key, W), norm_query=_bf(pw.norm_query, W), norm_conv=_bf(pw.norm_conv, W),
+                conv_w=_bf(pw.conv_w, W * pc.conv_kernel).reshape(W, pc.conv_kernel), table=table,
+                mult=np.array(list(t.multiplier)[:pc.ngram_size], np.int64),
+                vocab=np.array(list(t.vocab)[:nh], np.int64), offs=np.array(list(t.offset)[:nh], np.int64))
+
+
 def download_target(t, cfg):
     """cfg: dict with the layer config keys plus key_heads, value_heads, conv_kernel,
     num_layers, full_attention_interval, hc, lowrank, vocab."""
@@ -57,6 +82,9 @@ def download_target(t, cfg):
         else:
             L["gdn"] = download_gdn(lw.gdn, H, cfg["key_heads"], cfg["value_heads"], cfg["conv_kernel"], gs)
             L["moe"] = download_moe(lw.attn.moe, cfg)
+        if i == cfg.get("ple_layer", -1):
+            L["ple"] = download_ple(lw.ple, t.cfg.ple)
+            L["ple_cfg"] = ple_cfg_dict(t.cfg.ple)
         w["layers"].append(L)
     return w
 
@@ -67,8 +95,9 @@ def _gdn(L, proj, conv, ssm, eps):
 
 
 def oracle_verify(w, cfg, state, ids, pos0):
-    """state: dict(kc={layer: [HK, P, D]}, vc=..., conv={layer: ...}, ssm={layer: ...}) of the
-    committed caches (kc/vc receive the window's rows in place).
+    """state: dict(kc={layer: [HK, P, D]}, vc=..., conv={layer: ...}, ssm={layer: ...},
+    ple=(conv rows, context) of the PLE layer) of the committed caches (kc/vc receive the
+    window's rows in place).
     -> (logits [S, V], multi [S, hc*H], mixed [S, H], window) where window feeds oracle_commit."""
     H, gs, hc, eps = cfg["hidden"], cfg["group_size"], cfg["hc"], cfg["eps"]
     e = O.embed_rows(*w["embed"], gs, ids)
@@ -76,6 +105,11 @@ def oracle_verify(w, cfg, state, ids, pos0):
     window = {}
     for i, L in enumerate(w["layers"]):
         sA, n = O.hc_norm(resid, out, inj, L["attn_hc"]["scale"], hc, eps, tile=tile)
+        if "ple" in L:
+            conv, context = state["ple"]
+            res = O.ple_forward(L["ple"], L["ple_cfg"], sA, ids, conv, context)
+            window["ple"] = (i, res)
+            sA, n = O.hc_norm(res["sum"], None, None, L["attn_hc"]["scale"], hc, eps)
         x, jA = _mix(L["attn_hc"], n, hc, gs)
         if L["kind"] == 0:
             proj, _ = O.qmv(*L["gdn"]["in_proj"], gs, x)
@@ -95,8 +129,14 @@ def oracle_verify(w, cfg, state, ids, pos0):
 
 
 def oracle_commit(w, cfg, state, window, n):
-    """Advance the GDN states of `state` by the first n positions of a verify window."""
+    """Advance the GDN (and PLE) states of `state` by the first n positions of a verify window."""
     for i, proj in window.items():
+        if i == "ple":
+            li, res = proj
+            pc = w["layers"][li]["ple_cfg"]
+            nb = (pc["conv_kernel"] - 1) * pc["ngram_size"]
+            state["ple"] = O.ple_advance(res, n, nb, max(1, pc["ngram_size"] - 1))
+            continue
         if n == 0:
             continue
         r = _gdn(w["layers"][i], proj[:n], state["conv"][i], state["ssm"][i], cfg["eps"])

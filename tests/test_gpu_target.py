@@ -1,9 +1,10 @@
 """GPU parity of the target's verify forward (mtpx_target_*) against the oracle
 composition, bit-exact through the C ABI: logits, the multi stream and the mixed
 row over a layer stack of GDN and attention layers (each with hyper-connection
-mixers and MoE), from a random committed prefix (attention K/V rows and GDN
-states), then a partial commit, a window that is discarded by the next
-verify, and refused calls."""
+mixers and MoE), with and without the PLE n-gram block on layer 1, from a random
+committed prefix (attention K/V rows, GDN states, PLE conv rows and context),
+then a partial commit, a window that is discarded by the next verify, and
+refused calls."""
 import numpy as np
 import pytest
 import torch
@@ -29,13 +30,18 @@ def ctx():
     c.close()
 
 
-def test_target_verify_commit_discard_bit_exact(ctx):
+@pytest.mark.parametrize("ple_layer", [1, -1], ids=["ple", "no-ple"])
+def test_target_verify_commit_discard_bit_exact(ctx, ple_layer):
     import mtpx
     from oracle.target_ref import download_target, oracle_commit, oracle_verify
-    cfg = dict(LAYER, **TARGET)
+    cfg = dict(LAYER, **TARGET, ple_layer=ple_layer)
     tc = mtpx.TargetConfig(mtpx.LayerConfig(**LAYER), *[TARGET[k] for k in (
         "key_heads", "value_heads", "conv_kernel", "num_layers", "full_attention_interval", "hc", "lowrank",
         "vocab")])
+    tc.ple_layer = ple_layer
+    tc.ple = mtpx.PLEConfig(hidden=LAYER["hidden"], hc=TARGET["hc"], embed_dim=256, ngram_size=3, heads_per_ngram=2,
+                            conv_kernel=4, group_size=LAYER["group_size"], row_group_size=32, eos=7, vocab_base=300,
+                            token_vocab=TARGET["vocab"], eps=LAYER["eps"])
     t = mtpx.Target(ctx, tc, seed=17)
     ow = download_target(t, cfg)
     kinds = [L["kind"] for L in ow["layers"]]
@@ -63,6 +69,14 @@ def test_target_verify_commit_discard_bit_exact(ctx):
             ssm = (r.standard_normal((g.hv, 128, 128)) * 0.05).astype(np.float32)
             st.gdn(i).load(dev(conv), dev(ssm))
             ostate["conv"][i], ostate["ssm"][i] = conv, ssm
+    if ple_layer >= 0:
+        conv = rand_bf16(r, (9, hc * H))
+        context = np.array([3, 7], np.int32)  # 7 is the eos of this config
+        st.ple().load(dev(conv), dev(context))
+        ostate["ple"] = (conv, context)
+    else:
+        with pytest.raises(mtpx.MtpxError):
+            st.ple()
     st.set_offset(pre)
     torch.cuda.synchronize()
 
@@ -77,7 +91,7 @@ def test_target_verify_commit_discard_bit_exact(ctx):
         return want[3]
 
     print("case target window A", flush=True)
-    win = run([5, 77, 999, 0], pre)
+    win = run([5, 77, 7, 0], pre)
     assert st.info() == (pre, 4)
     st.commit(2)
     oracle_commit(ow, cfg, ostate, win, 2)

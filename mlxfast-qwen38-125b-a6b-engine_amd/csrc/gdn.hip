@@ -95,6 +95,34 @@ __global__ __launch_bounds__(GDN_THREADS) void k_gdn_step(GdnArgs a) {
   const float inv_scale = 1.0f / sqrtf((float)GDN_D);
   const float q_mul = round_bf(inv_scale * inv_scale), k_mul = round_bf(inv_scale);
 
+  // The state rows of this half-wave's recurrence (r = hw + 16 i) and the journal steps it replays,
+  // loaded before the prep so their latency hides behind it.
+  constexpr int RPH = GDN_D / (GDN_THREADS / 32);
+  float s[RPH][4];
+#pragma unroll
+  for (int i = 0; i < RPH; ++i) {
+    const float4 s4 = *reinterpret_cast<const float4*>(a.ssm + ((size_t)h * GDN_D + hw + 16 * i) * GDN_D + 4 * l);
+    s[i][0] = s4.x;
+    s[i][1] = s4.y;
+    s[i][2] = s4.z;
+    s[i][3] = s4.w;
+  }
+  float gdp[MAX_TOKENS], kpp[MAX_TOKENS][4], dlp[MAX_TOKENS][RPH];
+  if (P > 0) {
+#pragma unroll
+    for (int p = 0; p < MAX_TOKENS; ++p) {
+      const int pc = p < P ? p : P - 1;  // clamped: loads beyond P are issued but not used
+      gdp[p] = a.decay_cur[(size_t)pc * a.hv + h];
+      const uint2 kw = *reinterpret_cast<const uint2*>(a.key_cur + ((size_t)pc * a.hk + hk) * GDN_D + 4 * l);
+      kpp[p][0] = __uint_as_float(kw.x << 16);
+      kpp[p][1] = __uint_as_float(kw.x & 0xffff0000u);
+      kpp[p][2] = __uint_as_float(kw.y << 16);
+      kpp[p][3] = __uint_as_float(kw.y & 0xffff0000u);
+#pragma unroll
+      for (int i = 0; i < RPH; ++i) dlp[p][i] = a.delta_cur[((size_t)pc * a.hv + h) * GDN_D + hw + 16 * i];
+    }
+  }
+
   // ---- prep: (q, k, v) vectors x positions, 32 lanes x 4 channels each
   for (int task = hw; task < 3 * S; task += GDN_THREADS / 32) {
     const int t = task / 3, kind = task % 3;
@@ -148,57 +176,63 @@ __global__ __launch_bounds__(GDN_THREADS) void k_gdn_step(GdnArgs a) {
   }
   __syncthreads();
 
-  // ---- recurrence: 8 value rows per half-wave, lane l owns key elements 4l..4l+3
-  for (int r = hw; r < GDN_D; r += GDN_THREADS / 32) {
-    float* srow = a.ssm + ((size_t)h * GDN_D + r) * GDN_D + 4 * l;
-    const float4 s4 = *reinterpret_cast<const float4*>(srow);
-    float s[4] = {s4.x, s4.y, s4.z, s4.w};
-    for (int p = 0; p < P; ++p) {  // committed steps of the previous window
-      const float gd = a.decay_cur[(size_t)p * a.hv + h];
-      const float dl = a.delta_cur[((size_t)p * a.hv + h) * GDN_D + r];
-      const bf16* kp = a.key_cur + ((size_t)p * a.hk + hk) * GDN_D + 4 * l;
+  // ---- recurrence: 8 value rows per half-wave (r = hw + 16 i), lane l owns key elements 4l..4l+3
+  if (P > 0) {  // committed steps of the previous window, in order
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        s[i] = s[i] * gd;
-        s[i] = __builtin_fmaf(bf2f(kp[i]), dl, s[i]);
+    for (int p = 0; p < MAX_TOKENS; ++p) {
+      if (p < P) {
+#pragma unroll
+        for (int i = 0; i < RPH; ++i)
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            s[i][c] = s[i][c] * gdp[p];
+            s[i][c] = __builtin_fmaf(kpp[p][c], dlp[p][i], s[i][c]);
+          }
       }
     }
-    if (P > 0) *reinterpret_cast<float4*>(srow) = make_float4(s[0], s[1], s[2], s[3]);
+#pragma unroll
+    for (int i = 0; i < RPH; ++i)
+      *reinterpret_cast<float4*>(a.ssm + ((size_t)h * GDN_D + hw + 16 * i) * GDN_D + 4 * l) =
+          make_float4(s[i][0], s[i][1], s[i][2], s[i][3]);
+  }
+#pragma unroll
+  for (int i = 0; i < RPH; ++i) {
+    const int r = hw + 16 * i;
     for (int t = 0; t < S; ++t) {
       const float gd = dec[t];
       const float k0 = ks[t][4 * l], k1 = ks[t][4 * l + 1], k2 = ks[t][4 * l + 2], k3 = ks[t][4 * l + 3];
-      s[0] = s[0] * gd;
-      float kv = 0.0f + s[0] * k0;
+      s[i][0] = s[i][0] * gd;
+      float kv = 0.0f + s[i][0] * k0;
       float comp = 0.0f;
       {
-        s[1] = s[1] * gd;
-        const float prod = s[1] * k1, corr = prod - comp, next = kv + corr;
+        s[i][1] = s[i][1] * gd;
+        const float prod = s[i][1] * k1, corr = prod - comp, next = kv + corr;
         comp = (next - kv) - corr;
         kv = next;
       }
       {
-        s[2] = s[2] * gd;
-        const float prod = s[2] * k2, corr = prod - comp, next = kv + corr;
+        s[i][2] = s[i][2] * gd;
+        const float prod = s[i][2] * k2, corr = prod - comp, next = kv + corr;
         comp = (next - kv) - corr;
         kv = next;
       }
       {
-        s[3] = s[3] * gd;
-        const float prod = s[3] * k3, corr = prod - comp, next = kv + corr;
+        s[i][3] = s[i][3] * gd;
+        const float prod = s[i][3] * k3, corr = prod - comp, next = kv + corr;
         kv = next;
       }
       const float kvm = half_wave_sum(kv);
       const float delta = (vs[t][r] - kvm) * bet[t];
       if (l == 0) a.delta_nxt[((size_t)t * a.hv + h) * GDN_D + r] = delta;
       float o = 0.0f;
-      s[0] = __builtin_fmaf(k0, delta, s[0]);
-      o = __builtin_fmaf(s[0], qs[t][4 * l], o);
-      s[1] = __builtin_fmaf(k1, delta, s[1]);
-      o = __builtin_fmaf(s[1], qs[t][4 * l + 1], o);
-      s[2] = __builtin_fmaf(k2, delta, s[2]);
-      o = __builtin_fmaf(s[2], qs[t][4 * l + 2], o);
-      s[3] = __builtin_fmaf(k3, delta, s[3]);
-      o = __builtin_fmaf(s[3], qs[t][4 * l + 3], o);
+      s[i][0] = __builtin_fmaf(k0, delta, s[i][0]);
+      o = __builtin_fmaf(s[i][0], qs[t][4 * l], o);
+      s[i][1] = __builtin_fmaf(k1, delta, s[i][1]);
+      o = __builtin_fmaf(s[i][1], qs[t][4 * l + 1], o);
+      s[i][2] = __builtin_fmaf(k2, delta, s[i][2]);
+      o = __builtin_fmaf(s[i][2], qs[t][4 * l + 2], o);
+      s[i][3] = __builtin_fmaf(k3, delta, s[i][3]);
+      o = __builtin_fmaf(s[i][3], qs[t][4 * l + 3], o);
       const float y = half_wave_sum(o);
       if (l == 0) ys[t][r] = round_bf(y);
     }

@@ -45,8 +45,11 @@ __global__ __launch_bounds__(256) void k_embed_rows(const uint32_t* __restrict__
   for (int i = 0; i < 8; ++i) o[i] = f2bf(round_bf(scale * (float)((w >> (4 * i)) & 0xfu)) + bias);
 }
 
-// grid (hc, S, ceil(H/256)), 256 threads; H <= 256 * IT.
-template <int IT>
+// grid (hc, S, ceil(H/256)), 256 threads; H <= 256 * IT (EXACT: H == 256 * IT).
+// Every load is issued up front and unconditionally (clamped indices; a
+// missing `out` reads the residual row instead and is not used), so the
+// residual and the sublayer output arrive in one round trip.
+template <int IT, bool EXACT>
 __global__ __launch_bounds__(256) void k_hc_norm(const bf16* __restrict__ residual, const bf16* __restrict__ out,
                                                  const bf16* __restrict__ inject, int hc, int H, int tile,
                                                  const bf16* __restrict__ scale, float eps,
@@ -57,28 +60,29 @@ __global__ __launch_bounds__(256) void k_hc_norm(const bf16* __restrict__ residu
   const size_t W = (size_t)hc * H;
   const size_t base = (size_t)s * W + (size_t)c * H;
   const bf16* rr = tile ? residual + (size_t)s * H : residual + base;
-  const bf16* orow = out ? out + (size_t)s * H : nullptr;
-  const float inj = (out && inject) ? bf2f(inject[(size_t)s * hc + c]) : 0.0f;
-  float v[IT];
+  const bool has_out = out != nullptr, has_inj = has_out && inject != nullptr;
+  const bf16* orow = has_out ? out + (size_t)s * H : rr;
+  const float inj = bf2f(inject ? inject[(size_t)s * hc + c] : (bf16)0);
+  bf16 rv[IT], ov[IT];
 #pragma unroll
   for (int j = 0; j < IT; ++j) {
     const int d = t + 256 * j;
-    v[j] = d < H ? bf2f(rr[d]) : 0.0f;
+    const int dd = EXACT ? d : (d < H ? d : H - 1);
+    rv[j] = rr[dd];
+    ov[j] = orow[dd];
   }
-  if (orow) {
-#pragma unroll
-    for (int j = 0; j < IT; ++j) {
-      const int d = t + 256 * j;
-      if (d < H) {
-        const float o = bf2f(orow[d]);
-        v[j] = round_bf(v[j] + (inject ? round_bf(o * inj) : o));
-      }
-    }
-  }
+  float v[IT];
   float acc = 0.0f, vo = 0.0f;
 #pragma unroll
   for (int j = 0; j < IT; ++j) {
-    if (t + 256 * j < H) acc = __builtin_fmaf(v[j], v[j], acc);
+    const bool in = EXACT || t + 256 * j < H;
+    float x = bf2f(rv[j]);
+    if (has_out) {
+      const float o = bf2f(ov[j]);
+      x = round_bf(x + (has_inj ? round_bf(o * inj) : o));
+    }
+    v[j] = in ? x : 0.0f;
+    if (in) acc = __builtin_fmaf(v[j], v[j], acc);
     if (j == sl) vo = v[j];
   }
   acc = wave_fold64(acc);
@@ -91,7 +95,7 @@ __global__ __launch_bounds__(256) void k_hc_norm(const bf16* __restrict__ residu
   if (d < H) {
     if (stream) stream[base + d] = f2bf(vo);
     n = f2bf(bf2f(scale[(size_t)c * H + d]) * round_bf(vo * inv));
-    normed[base + d] = n;
+    if (normed) normed[base + d] = n;
   }
   // blocks of the normed row [S, hc*H]: H % 32 == 0, so a block never straddles streams
   if (xp && d < H) xprep_lanes_direct(n, t & 31, xp + (base + d) / 32 * XP_DW);
@@ -142,12 +146,15 @@ hipError_t launch_hc_norm(const bf16* residual, const bf16* out, const bf16* inj
                           int tile, const bf16* scale, float eps, bf16* stream, bf16* normed, uint32_t* xp,
                           hipStream_t st) {
   const dim3 grid(hc, S, (H + 255) / 256);
-  if (H <= 256 * 16)
-    hipLaunchKernelGGL(k_hc_norm<16>, grid, dim3(256), 0, st, residual, out, inject, hc, H, tile, scale, eps,
+  if (H == 2560)
+    hipLaunchKernelGGL((k_hc_norm<10, true>), grid, dim3(256), 0, st, residual, out, inject, hc, H, tile, scale, eps,
                        stream, normed, xp);
+  else if (H <= 256 * 16)
+    hipLaunchKernelGGL((k_hc_norm<16, false>), grid, dim3(256), 0, st, residual, out, inject, hc, H, tile, scale,
+                       eps, stream, normed, xp);
   else
-    hipLaunchKernelGGL(k_hc_norm<48>, grid, dim3(256), 0, st, residual, out, inject, hc, H, tile, scale, eps,
-                       stream, normed, xp);
+    hipLaunchKernelGGL((k_hc_norm<48, false>), grid, dim3(256), 0, st, residual, out, inject, hc, H, tile, scale,
+                       eps, stream, normed, xp);
   return hipGetLastError();
 }
 

@@ -181,8 +181,11 @@ __device__ void route_body(const MoeArgs& a) {
 // router + route: workgroups [0, row_wgs) hold one wave per router row (rows
 // 0..E-1 router, row E the shared-expert gate); lane l walks 8-element chunks
 // l, l+64, ...: acc = fmaf(w, x, acc) in element order, then an xor butterfly
-// over the wave.  The remaining workgroups prepare x's activation blocks for
-// the expert GEMVs (32 lanes per block) and take no ticket.
+// over the wave.  The window's activations are staged into LDS first, their
+// loads in flight together with the weight rows' (read from global inside the
+// token loop, each chunk would wait for its own round trip).  The remaining
+// workgroups prepare x's activation blocks for the expert GEMVs (32 lanes per
+// block) and take no ticket.
 constexpr int ROUTER_IT = 8;  // H <= 8 * 64 * 8
 
 __global__ __launch_bounds__(RR_THREADS) void k_moe_router_route(MoeArgs a, int row_wgs) {
@@ -195,25 +198,35 @@ __global__ __launch_bounds__(RR_THREADS) void k_moe_router_route(MoeArgs a, int 
       xprep_lanes_direct(a.x[(size_t)(blk / nb) * H + (size_t)(blk % nb) * 32 + i], i, a.xp_x + (size_t)blk * XP_DW);
     return;
   }
+  extern __shared__ uint4 xs[];  // [M, H/8]
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int r = blockIdx.x * (RR_THREADS / 64) + wave;
-  if (r <= E) {
-    const bf16* wrow = (r < E) ? a.router + (size_t)r * H : a.shared_gate;
-    const int nc = H / 8;
-    uint4 wv[ROUTER_IT];
+  const int nc = H / 8;
+  const bool row_ok = r <= E;
+  const bf16* wrow = (r < E) ? a.router + (size_t)r * H : a.shared_gate;
+  uint4 wv[ROUTER_IT];
 #pragma unroll
-    for (int i = 0; i < ROUTER_IT; ++i) {
-      const int c = lane + 64 * i;
-      wv[i] = (c < nc) ? *reinterpret_cast<const uint4*>(wrow + (size_t)c * 8) : make_uint4(0, 0, 0, 0);
-    }
+  for (int i = 0; i < ROUTER_IT; ++i) {
+    const int c = lane + 64 * i;
+    wv[i] = (row_ok && c < nc) ? *reinterpret_cast<const uint4*>(wrow + (size_t)c * 8) : make_uint4(0, 0, 0, 0);
+  }
+  // LDS-direct copies: no register round trip, one wait for all of them
+  stage16(reinterpret_cast<uint32_t*>(xs), reinterpret_cast<const uint32_t*>(a.x), M * H / 2);
+  stage_sync();
+  if (row_ok) {
     for (int m = 0; m < M; ++m) {
-      const bf16* xm = a.x + (size_t)m * H;
+      uint4 xr[ROUTER_IT];
+#pragma unroll
+      for (int i = 0; i < ROUTER_IT; ++i) {  // every chunk of the token read before the first use
+        const int c = lane + 64 * i;
+        xr[i] = xs[m * nc + (c < nc ? c : nc - 1)];
+      }
       float acc = 0.0f;
 #pragma unroll
       for (int i = 0; i < ROUTER_IT; ++i) {
         const int c = lane + 64 * i;
         if (c < nc) {
-          const uint4 xv = *reinterpret_cast<const uint4*>(xm + (size_t)c * 8);
+          const uint4 xv = xr[i];
           const uint32_t ww[4] = {wv[i].x, wv[i].y, wv[i].z, wv[i].w};
           const uint32_t xx[4] = {xv.x, xv.y, xv.z, xv.w};
 #pragma unroll
@@ -517,7 +530,12 @@ __global__ __launch_bounds__(DN_THREADS) void k_moe_down(MoeArgs a, const int32_
 hipError_t launch_moe_router_route(const MoeArgs& a, hipStream_t st) {
   const int row_wgs = (a.E + 1 + RR_THREADS / 64 - 1) / (RR_THREADS / 64);
   const int prep_wgs = a.xp_ready ? 0 : (a.M * (a.H / 32) + RR_THREADS / 32 - 1) / (RR_THREADS / 32);
-  hipLaunchKernelGGL(k_moe_router_route, dim3(row_wgs + prep_wgs), dim3(RR_THREADS), 0, st, a, row_wgs);
+  if (a.M < 1 || a.M > MAX_TOKENS || a.H % 8 != 0 || a.H / 8 > ROUTER_IT * 64) return hipErrorInvalidValue;
+  const size_t lds = (size_t)a.M * a.H * 2;  // the staged activations
+  static size_t cur = 0;
+  const hipError_t e = ensure_lds(k_moe_router_route, lds + 16 * 1024, cur);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(k_moe_router_route, dim3(row_wgs + prep_wgs), dim3(RR_THREADS), lds, st, a, row_wgs);
   return hipGetLastError();
 }
 

@@ -84,6 +84,16 @@ __device__ __forceinline__ float gdn_row(const GdnArgs& a, int r, int ch) {
   return bf2f(a.proj[(size_t)r * a.pw + ch]);
 }
 
+// Row r of the same virtual sequence as a pointer to its channel 0 (r is uniform).
+__device__ __forceinline__ const bf16* gdn_row_ptr(const GdnArgs& a, int r) {
+  const int KM1 = a.kc - 1;
+  if (r < KM1) return a.conv_cur + (size_t)r * a.cd;
+  r -= KM1;
+  if (r < a.P) return a.win_cur + (size_t)r * a.cd;
+  return a.proj + (size_t)(r - a.P) * a.pw;
+}
+
+template <int KC>
 __global__ __launch_bounds__(GDN_THREADS) void k_gdn_step(GdnArgs a) {
   __shared__ float qs[MAX_TOKENS][GDN_D], ks[MAX_TOKENS][GDN_D], vs[MAX_TOKENS][GDN_D], ys[MAX_TOKENS][GDN_D];
   __shared__ float dec[MAX_TOKENS], bet[MAX_TOKENS];
@@ -123,21 +133,35 @@ __global__ __launch_bounds__(GDN_THREADS) void k_gdn_step(GdnArgs a) {
     }
   }
 
-  // ---- prep: (q, k, v) vectors x positions, 32 lanes x 4 channels each
+  // ---- prep: (q, k, v) vectors x positions, 32 lanes x 4 channels each; a lane's KC input rows
+  // (4 channels each) and its 4 x KC conv taps are loaded before the first multiply
   for (int task = hw; task < 3 * S; task += GDN_THREADS / 32) {
     const int t = task / 3, kind = task % 3;
     const int vec = kind == 0 ? hk : (kind == 1 ? a.hk + hk : 2 * a.hk + h);
+    const int ch0 = vec * GDN_D + 4 * l;
+    uint2 xin[KC];
+#pragma unroll
+    for (int j = 0; j < KC; ++j) xin[j] = *reinterpret_cast<const uint2*>(gdn_row_ptr(a, P + t + j) + ch0);
+    uint32_t wt[2 * KC];  // conv_w[ch0 .. ch0+3][0 .. KC-1]: 4*KC bf16, contiguous
+#pragma unroll
+    for (int q = 0; q < 2 * KC; ++q) wt[q] = reinterpret_cast<const uint32_t*>(a.conv_w + (size_t)ch0 * KC)[q];
+    auto hbf = [](uint32_t w, int odd) { return __uint_as_float(odd ? (w & 0xffff0000u) : (w << 16)); };
     float xs[4], acc = 0.0f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int ch = vec * GDN_D + 4 * l + i;
       float c = 0.0f;
-      for (int j = 0; j < a.kc; ++j) c = c + gdn_row(a, P + t + j, ch) * bf2f(a.conv_w[(size_t)ch * a.kc + j]);
+#pragma unroll
+      for (int j = 0; j < KC; ++j) {
+        const float xv = hbf(i < 2 ? xin[j].x : xin[j].y, i & 1);
+        const int e = i * KC + j;
+        c = c + xv * hbf(wt[e >> 1], e & 1);
+      }
       const float x = silu_bf16(round_bf(c));
       xs[i] = x;
       acc = __builtin_fmaf(x, x, acc);
-      if (kind == 2 || lead) a.win_nxt[(size_t)t * a.cd + ch] = a.proj[(size_t)t * a.pw + ch];
     }
+    if (kind == 2 || lead)  // this position's conv input row (row P + t + KC-1 is projection row t)
+      *reinterpret_cast<uint2*>(a.win_nxt + (size_t)t * a.cd + ch0) = xin[KC - 1];
     if (kind < 2) {
       const float inv = 1.0f / sqrtf(half_wave_sum(acc) / 128.0f + 1e-6f);
       const float mul = kind == 0 ? q_mul : k_mul;
@@ -297,9 +321,23 @@ __global__ __launch_bounds__(GDN_THREADS) void k_gdn_replay(GdnArgs a, float* ss
   }
 }
 
-hipError_t launch_gdn_step(const GdnArgs& a, hipStream_t st) {
-  hipLaunchKernelGGL(k_gdn_step, dim3(a.hv), dim3(GDN_THREADS), 0, st, a);
+template <int KC>
+static hipError_t gdn_step_kc(const GdnArgs& a, hipStream_t st) {
+  hipLaunchKernelGGL(k_gdn_step<KC>, dim3(a.hv), dim3(GDN_THREADS), 0, st, a);
   return hipGetLastError();
+}
+
+hipError_t launch_gdn_step(const GdnArgs& a, hipStream_t st) {
+  switch (a.kc) {
+    case 2: return gdn_step_kc<2>(a, st);
+    case 3: return gdn_step_kc<3>(a, st);
+    case 4: return gdn_step_kc<4>(a, st);
+    case 5: return gdn_step_kc<5>(a, st);
+    case 6: return gdn_step_kc<6>(a, st);
+    case 7: return gdn_step_kc<7>(a, st);
+    case 8: return gdn_step_kc<8>(a, st);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 hipError_t launch_gdn_replay(const GdnArgs& a, float* ssm_dst, bf16* conv_dst, hipStream_t st) {

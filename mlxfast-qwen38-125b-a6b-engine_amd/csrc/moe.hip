@@ -406,15 +406,23 @@ __device__ __forceinline__ float colsum_small(const float* r, int K) {
   return total;
 }
 
+// K is a template parameter so the K + 1 row loads are issued together and the
+// fold is unrolled (a runtime-K loop waits for each load in turn).
+template <int K>
 __global__ __launch_bounds__(256) void k_moe_combine(MoeArgs a) {
   const int m = blockIdx.y, h = blockIdx.x * 256 + threadIdx.x;
   if (h >= a.H) return;
-  const int H = a.H, M = a.M, K = a.K;
-  float prod[MAX_TOPK];
-  for (int k = 0; k < K; ++k) prod[k] = bf2f(a.r[(size_t)(m * K + k) * H + h]) * a.w[m * K + k];
+  const int H = a.H, M = a.M;
+  float rv[K];
+#pragma unroll
+  for (int k = 0; k < K; ++k) rv[k] = bf2f(a.r[(size_t)(m * K + k) * H + h]);
+  const float shv = bf2f(a.r[(size_t)(M * K + m) * H + h]);
+  float prod[K];
+#pragma unroll
+  for (int k = 0; k < K; ++k) prod[k] = rv[k] * a.w[m * K + k];
   const float rr = round_bf(colsum_small(prod, K));
   const float sg = sigmoid_bf16(round_bf(a.gate_logit[m]));
-  const float sh = round_bf(sg * bf2f(a.r[(size_t)(M * K + m) * H + h]));
+  const float sh = round_bf(sg * shv);
   const bf16 out = f2bf(rr + sh);
   if (a.y) a.y[(size_t)m * H + h] = out;
   if (a.y2) a.y2[(size_t)m * H + h] = f2bf(bf2f(a.resid[(size_t)m * H + h]) + bf2f(out));
@@ -613,9 +621,32 @@ hipError_t launch_moe_gate_up(const MoeArgs& a, hipStream_t st) { MTPX_QROW_DISP
 
 hipError_t launch_moe_down(const MoeArgs& a, hipStream_t st) { MTPX_QROW_DISPATCH(a.F / 32, down_li, a, st); }
 
-hipError_t launch_moe_combine(const MoeArgs& a, hipStream_t st) {
-  hipLaunchKernelGGL(k_moe_combine, dim3((a.H + 255) / 256, a.M), dim3(256), 0, st, a);
+template <int K>
+static hipError_t combine_k(const MoeArgs& a, hipStream_t st) {
+  hipLaunchKernelGGL(k_moe_combine<K>, dim3((a.H + 255) / 256, a.M), dim3(256), 0, st, a);
   return hipGetLastError();
+}
+
+hipError_t launch_moe_combine(const MoeArgs& a, hipStream_t st) {
+  switch (a.K) {
+    case 1: return combine_k<1>(a, st);
+    case 2: return combine_k<2>(a, st);
+    case 3: return combine_k<3>(a, st);
+    case 4: return combine_k<4>(a, st);
+    case 5: return combine_k<5>(a, st);
+    case 6: return combine_k<6>(a, st);
+    case 7: return combine_k<7>(a, st);
+    case 8: return combine_k<8>(a, st);
+    case 9: return combine_k<9>(a, st);
+    case 10: return combine_k<10>(a, st);
+    case 11: return combine_k<11>(a, st);
+    case 12: return combine_k<12>(a, st);
+    case 13: return combine_k<13>(a, st);
+    case 14: return combine_k<14>(a, st);
+    case 15: return combine_k<15>(a, st);
+    case 16: return combine_k<16>(a, st);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 }  // namespace mtpx

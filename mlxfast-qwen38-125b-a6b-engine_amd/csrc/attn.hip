@@ -109,17 +109,14 @@ __global__ __launch_bounds__(ATTN_THREADS) void k_attn_partial(const bf16* __res
   for (int base = 0; base < nq + 2 * nkv; base += 8 * (int)blockDim.x) {
     uint4 r[8];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int i = base + u * (int)blockDim.x + (int)threadIdx.x;
-      if (i < nq) {
-        r[u] = q4[((size_t)s * HQ + hk * G) * RV + i];
-      } else if (i < nq + nkv) {
-        const int ik = i - nq;
-        r[u] = k4[((size_t)hk * tmax + i0 + ik / RV) * RV + ik % RV];
-      } else if (i < nq + 2 * nkv) {
-        const int iv = i - nq - nkv;
-        r[u] = v4[((size_t)hk * tmax + i0 + iv / RV) * RV + iv % RV];
-      }
+    for (int u = 0; u < 8; ++u) {  // the source selected by address, one unconditional load (the first q
+      const int i = base + u * (int)blockDim.x + (int)threadIdx.x;  // unit past the end): all 8 in flight
+      const int ik = i - nq, iv = i - nq - nkv;
+      const uint4* src = i < nq ? q4 + ((size_t)s * HQ + hk * G) * RV + i
+                         : i < nq + nkv ? k4 + ((size_t)hk * tmax + i0 + ik / RV) * RV + ik % RV
+                         : i < nq + 2 * nkv ? v4 + ((size_t)hk * tmax + i0 + iv / RV) * RV + iv % RV
+                                            : q4 + ((size_t)s * HQ + hk * G) * RV;
+      r[u] = *src;
     }
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
@@ -232,9 +229,13 @@ __global__ __launch_bounds__(256) void k_attn_combine(const float* __restrict__ 
   auto chunk = [&](int c) { return part + (((size_t)hk * nch + c) * R + ri) * (D + 2); };
   // one round of loads: every chunk's (m, l) into LDS, and this thread's first
   // COMBINE_BATCH output partials into registers
+  // unconditional loads (clamped chunk and dimension; the values past the end are not used), so
+  // all of them are in flight at once; the gate value too, which is needed only at the end
+  const int dc = d < D ? d : D - 1;
+  const bf16 gate_raw = out_gated ? qkv[(size_t)s * QW + gate_off + h * D + dc] : (bf16)0;
   float pv[COMBINE_BATCH];
 #pragma unroll
-  for (int u = 0; u < COMBINE_BATCH; ++u) pv[u] = (u < nch && d < D) ? chunk(u)[2 + d] : 0.0f;
+  for (int u = 0; u < COMBINE_BATCH; ++u) pv[u] = chunk(u < nch ? u : nch - 1)[2 + dc];
   for (int c = t; c < nch; c += nt) {
     const float* p = chunk(c);
     mc[c] = p[0];
@@ -269,7 +270,7 @@ __global__ __launch_bounds__(256) void k_attn_combine(const float* __restrict__ 
     if (u < nch && lc[u] > 0.0f) O = __builtin_fmaf(pv[u], fc[u], O);
   for (int cb = COMBINE_BATCH; cb < nch; cb += COMBINE_BATCH) {
 #pragma unroll
-    for (int u = 0; u < COMBINE_BATCH; ++u) pv[u] = (cb + u < nch && d < D) ? chunk(cb + u)[2 + d] : 0.0f;
+    for (int u = 0; u < COMBINE_BATCH; ++u) pv[u] = chunk(cb + u < nch ? cb + u : nch - 1)[2 + dc];
 #pragma unroll
     for (int u = 0; u < COMBINE_BATCH; ++u)
       if (cb + u < nch && lc[cb + u] > 0.0f) O = __builtin_fmaf(pv[u], fc[cb + u], O);
@@ -281,7 +282,7 @@ __global__ __launch_bounds__(256) void k_attn_combine(const float* __restrict__ 
       const bf16 att = f2bf(O / L);
       if (out) out[((size_t)s * HQ + h) * D + d] = att;
       if (out_gated) {
-        const float g = bf2f(qkv[(size_t)s * QW + gate_off + h * D + d]);
+        const float g = bf2f(gate_raw);
         gated = f2bf(bf2f(att) * sigmoid_bf16(g));
         out_gated[(size_t)s * HQ * D + h * D + d] = gated;
       }

@@ -2,7 +2,9 @@
 // for a window of S <= 8 positions: causal depthwise conv + SiLU, q/k RMS
 // norms and scales, decay/beta gates, the delta-rule recurrence with a
 // Kahan-compensated key product, and the gated output RMS norm -- one launch,
-// one workgroup per value head.
+// four workgroups per value head (each owns a quarter of the head's state
+// rows; the head's last one to finish, by a ticket, runs the gated norm over
+// the rows' outputs the others published at device scope).
 //
 // Window state.  The reference keeps the recurrent state after every window
 // position so the engine can roll back to any of them (Runner/FastModel/
@@ -14,8 +16,8 @@
 // those n steps (the same float operations, so the same bits) onto the
 // committed state and stores it, then runs its own positions.  Journal and conv
 // base are double-buffered (slot `cur` read, slot `nxt` written) so no
-// workgroup overwrites what another still reads; the recurrent state rows of a
-// head are read and written by that head's workgroup only.
+// workgroup overwrites what another still reads; each recurrent state row is
+// read and written by the one workgroup that owns it.
 //
 // Lane structure (fixes the float order): every 128-element reduction is 32
 // lanes x 4 consecutive elements, each lane in element order, then an xor
@@ -30,6 +32,7 @@ namespace mtpx {
 
 constexpr int GDN_THREADS = 512;  // 16 half-waves
 constexpr int GDN_D = 128;
+constexpr int GDN_SPLIT = 4;      // workgroups per value head, each owning 128 / GDN_SPLIT state rows
 
 // log1p(y), y in [0, 1]: 2 atanh(s), s = y / (2 + y), odd series to s^15.
 __device__ __forceinline__ float log1p_det(float y) {
@@ -99,19 +102,21 @@ __global__ __launch_bounds__(GDN_THREADS) void k_gdn_step(GdnArgs a) {
   __shared__ float dec[MAX_TOKENS], bet[MAX_TOKENS];
   __shared__ bf16 gated[MAX_TOKENS][GDN_D];
   const int h = blockIdx.x, ratio = a.hv / a.hk, hk = h / ratio;
-  const bool lead = (h % ratio) == 0;  // writes the q/k channels' journal and conv rows
+  const int r0 = blockIdx.y * (GDN_D / GDN_SPLIT);  // this workgroup's state rows r0 .. r0 + 128/GDN_SPLIT - 1
+  const bool w0 = blockIdx.y == 0;                  // writes the head's journal rows (conv, keys, decay)
+  const bool lead = (h % ratio) == 0 && w0;         // writes the q/k channels' journal and conv rows
   const int hw = threadIdx.x >> 5, l = threadIdx.x & 31;
   const int S = a.S, P = a.P, KM1 = a.kc - 1;
   const float inv_scale = 1.0f / sqrtf((float)GDN_D);
   const float q_mul = round_bf(inv_scale * inv_scale), k_mul = round_bf(inv_scale);
 
-  // The state rows of this half-wave's recurrence (r = hw + 16 i) and the journal steps it replays,
+  // The state rows of this half-wave's recurrence (r = r0 + hw + 16 i) and the journal steps it replays,
   // loaded before the prep so their latency hides behind it.
-  constexpr int RPH = GDN_D / (GDN_THREADS / 32);
+  constexpr int RPH = GDN_D / GDN_SPLIT / (GDN_THREADS / 32);
   float s[RPH][4];
 #pragma unroll
   for (int i = 0; i < RPH; ++i) {
-    const float4 s4 = *reinterpret_cast<const float4*>(a.ssm + ((size_t)h * GDN_D + hw + 16 * i) * GDN_D + 4 * l);
+    const float4 s4 = *reinterpret_cast<const float4*>(a.ssm + ((size_t)h * GDN_D + r0 + hw + 16 * i) * GDN_D + 4 * l);
     s[i][0] = s4.x;
     s[i][1] = s4.y;
     s[i][2] = s4.z;
@@ -129,7 +134,7 @@ __global__ __launch_bounds__(GDN_THREADS) void k_gdn_step(GdnArgs a) {
       kpp[p][2] = __uint_as_float(kw.y << 16);
       kpp[p][3] = __uint_as_float(kw.y & 0xffff0000u);
 #pragma unroll
-      for (int i = 0; i < RPH; ++i) dlp[p][i] = a.delta_cur[((size_t)pc * a.hv + h) * GDN_D + hw + 16 * i];
+      for (int i = 0; i < RPH; ++i) dlp[p][i] = a.delta_cur[((size_t)pc * a.hv + h) * GDN_D + r0 + hw + 16 * i];
     }
   }
 
@@ -160,7 +165,7 @@ __global__ __launch_bounds__(GDN_THREADS) void k_gdn_step(GdnArgs a) {
       xs[i] = x;
       acc = __builtin_fmaf(x, x, acc);
     }
-    if (kind == 2 || lead)  // this position's conv input row (row P + t + KC-1 is projection row t)
+    if ((kind == 2 && w0) || lead)  // this position's conv input row (row P + t + KC-1 is projection row t)
       *reinterpret_cast<uint2*>(a.win_nxt + (size_t)t * a.cd + ch0) = xin[KC - 1];
     if (kind < 2) {
       const float inv = 1.0f / sqrtf(half_wave_sum(acc) / 128.0f + 1e-6f);
@@ -188,10 +193,10 @@ __global__ __launch_bounds__(GDN_THREADS) void k_gdn_step(GdnArgs a) {
     const float d = expf_det(a.neg_exp_alog[h] * logaddexp0_bf16(ax));
     dec[t] = d;
     bet[t] = b;
-    a.decay_nxt[(size_t)t * a.hv + h] = d;
+    if (w0) a.decay_nxt[(size_t)t * a.hv + h] = d;
   }
   // the committed conv rows R[P .. P+KC-1) become the next window's base
-  for (int i = threadIdx.x; i < KM1 * 3 * GDN_D; i += GDN_THREADS) {
+  for (int i = threadIdx.x; i < (w0 ? KM1 * 3 * GDN_D : 0); i += GDN_THREADS) {
     const int j = i / (3 * GDN_D), kind = (i / GDN_D) % 3, d = i % GDN_D;
     if (kind < 2 && !lead) continue;
     const int vec = kind == 0 ? hk : (kind == 1 ? a.hk + hk : 2 * a.hk + h);
@@ -200,7 +205,7 @@ __global__ __launch_bounds__(GDN_THREADS) void k_gdn_step(GdnArgs a) {
   }
   __syncthreads();
 
-  // ---- recurrence: 8 value rows per half-wave (r = hw + 16 i), lane l owns key elements 4l..4l+3
+  // ---- recurrence: RPH value rows per half-wave (r = r0 + hw + 16 i), lane l owns key elements 4l..4l+3
   if (P > 0) {  // committed steps of the previous window, in order
 #pragma unroll
     for (int p = 0; p < MAX_TOKENS; ++p) {
@@ -216,12 +221,12 @@ __global__ __launch_bounds__(GDN_THREADS) void k_gdn_step(GdnArgs a) {
     }
 #pragma unroll
     for (int i = 0; i < RPH; ++i)
-      *reinterpret_cast<float4*>(a.ssm + ((size_t)h * GDN_D + hw + 16 * i) * GDN_D + 4 * l) =
+      *reinterpret_cast<float4*>(a.ssm + ((size_t)h * GDN_D + r0 + hw + 16 * i) * GDN_D + 4 * l) =
           make_float4(s[i][0], s[i][1], s[i][2], s[i][3]);
   }
 #pragma unroll
   for (int i = 0; i < RPH; ++i) {
-    const int r = hw + 16 * i;
+    const int r = r0 + hw + 16 * i;
     for (int t = 0; t < S; ++t) {
       const float gd = dec[t];
       const float k0 = ks[t][4 * l], k1 = ks[t][4 * l + 1], k2 = ks[t][4 * l + 2], k3 = ks[t][4 * l + 3];
@@ -258,9 +263,13 @@ __global__ __launch_bounds__(GDN_THREADS) void k_gdn_step(GdnArgs a) {
       s[i][3] = __builtin_fmaf(k3, delta, s[i][3]);
       o = __builtin_fmaf(s[i][3], qs[t][4 * l + 3], o);
       const float y = half_wave_sum(o);
-      if (l == 0) ys[t][r] = round_bf(y);
+      if (l == 0) st_pub(a.ypub + ((size_t)t * a.hv + h) * GDN_D + r, round_bf(y));
     }
   }
+  // the head's last workgroup to finish gathers every row's output and runs the gated norm
+  if (!ticket_last(a.tickets + h, GDN_SPLIT - 1)) return;
+  for (int i = threadIdx.x; i < S * GDN_D; i += GDN_THREADS)
+    ys[i / GDN_D][i % GDN_D] = ld_pub(a.ypub + ((size_t)(i / GDN_D) * a.hv + h) * GDN_D + i % GDN_D);
   __syncthreads();
 
   // ---- gated RMS norm per position
@@ -323,7 +332,8 @@ __global__ __launch_bounds__(GDN_THREADS) void k_gdn_replay(GdnArgs a, float* ss
 
 template <int KC>
 static hipError_t gdn_step_kc(const GdnArgs& a, hipStream_t st) {
-  hipLaunchKernelGGL(k_gdn_step<KC>, dim3(a.hv), dim3(GDN_THREADS), 0, st, a);
+  if (!a.tickets || !a.ypub) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_gdn_step<KC>, dim3(a.hv, GDN_SPLIT), dim3(GDN_THREADS), 0, st, a);
   return hipGetLastError();
 }
 

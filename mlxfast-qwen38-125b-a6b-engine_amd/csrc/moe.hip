@@ -34,33 +34,6 @@
 namespace mtpx {
 
 // ---------------------------------------------------------------------------
-// Agent-coherent stores/loads of ticket-published data.
-__device__ __forceinline__ void st_pub(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float ld_pub(const float* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Last-arriver ticket: every thread waits until its published stores are
-// complete, the workgroup synchronises, one thread takes the ticket; the
-// workgroup that draws `last` resets the counter and returns true.
-__device__ __forceinline__ bool ticket_last(uint32_t* ctr, uint32_t last) {
-  __shared__ int is_last;
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  __builtin_amdgcn_s_waitcnt(0);
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const uint32_t t = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    is_last = (t == last);
-    if (t == last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-  __syncthreads();
-  return is_last != 0;
-}
-
-// ---------------------------------------------------------------------------
 // route (run by one workgroup of RR_THREADS threads): wave m selects token m's
 // top-k; then the dispatch table is built in LDS by all threads: each expert
 // once (ordered by its first (token, rank) slot), with its slots ordered by

@@ -772,6 +772,8 @@ struct GdnState {
   float* delta[2] = {nullptr, nullptr};    // [MAX_TOKENS, hv, 128]
   float* decay[2] = {nullptr, nullptr};    // [MAX_TOKENS, hv]
   float* ssm = nullptr;                    // [hv, 128, 128]
+  uint32_t* tickets = nullptr;             // [hv] per-head last-arriver counters of the step, zero at rest
+  float* ypub = nullptr;                   // [MAX_TOKENS, hv, 128] the step's published recurrence outputs
   int cur = 0, window = 0, committed = 0;
   std::vector<void*> allocs;
 };
@@ -846,6 +848,8 @@ GdnArgs gdn_args(GdnState* st, const GdnLayer* L, const uint16_t* proj, int S, u
   a.delta_nxt = st->delta[n];
   a.decay_nxt = st->decay[n];
   a.ssm = st->ssm;
+  a.tickets = st->tickets;
+  a.ypub = st->ypub;
   a.gated = reinterpret_cast<bf16*>(gated);
   a.xp = xp;
   return a;
@@ -1651,7 +1655,10 @@ int mtpx_gdn_state_new(mtpx_ctx h, const mtpx_gdn_config* cfg, mtpx_gdn_state* o
     st->decay[s] = (float*)take(4 * (size_t)MAX_TOKENS * g.hv);
   }
   st->ssm = (float*)take(4 * (size_t)g.hv * 128 * 128);
+  st->tickets = (uint32_t*)take(4 * (size_t)g.hv);
+  st->ypub = (float*)take(4 * (size_t)MAX_TOKENS * g.hv * 128);
   if (ok) {
+    if (hipMemsetAsync(st->tickets, 0, 4 * (size_t)g.hv, c->stream) != hipSuccess) ok = false;
     for (int s = 0; s < 2; ++s)
       if (hipMemsetAsync(st->conv[s], 0, 2 * (size_t)(g.kc - 1) * g.cd, c->stream) != hipSuccess) ok = false;
     if (hipMemsetAsync(st->ssm, 0, 4 * (size_t)g.hv * 128 * 128, c->stream) != hipSuccess) ok = false;

@@ -36,6 +36,32 @@ inline int device_cus() {
   return cus[dev];
 }
 
+// Agent-coherent stores/loads of ticket-published data.
+__device__ __forceinline__ void st_pub(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_pub(const float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Last-arriver ticket: every thread waits until its published stores are
+// complete, the workgroup synchronises, one thread takes the ticket; the
+// workgroup that draws `last` resets the counter and returns true.
+__device__ __forceinline__ bool ticket_last(uint32_t* ctr, uint32_t last) {
+  __shared__ int is_last;
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const uint32_t t = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    is_last = (t == last);
+    if (t == last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  return is_last != 0;
+}
+
 // --- dense q4 GEMV and friends (qmv.hip)
 hipError_t launch_xprep(const bf16* x, int M, int K, uint32_t* xp, hipStream_t st);
 // sb: packed scale/bias rows (sb_row_len(K, gs) u32 per row) or null
@@ -176,6 +202,8 @@ struct GdnArgs {
   float* ssm;                                   // [hv, 128, 128] committed recurrent state (in place)
   bf16* gated;                                  // [S, hv*128] or null
   uint32_t* xp;                                 // [S, hv*4, XP_DW] prepared gated rows or null
+  uint32_t* tickets;                            // [hv] per-head last-arriver counters, zero at rest
+  float* ypub;                                  // [S, hv, 128] recurrence outputs published for the gated norm
 };
 hipError_t launch_gdn_step(const GdnArgs& a, hipStream_t st);
 hipError_t launch_gdn_replay(const GdnArgs& a, float* ssm_dst, bf16* conv_dst, hipStream_t st);

@@ -170,6 +170,16 @@ __device__ __forceinline__ void fold_levels(float (&v)[NV]) {
   }
 }
 
+// Chunks per loop body: half of the class's chunks when a class has at most 12 (two bodies: the
+// walk waits for HBM about twice), else LC/4 (at least 2); in both, 8 * BC is a multiple of LC, so
+// every body repeats the chain order.
+template <int L, int IT, int C>
+constexpr int mma_body_chunks() {
+  constexpr int LC = L / C, NCH = L * IT / C / 4, B0 = LC / 4 > 2 ? LC / 4 : 2;
+  if (LC < 1 || NCH < 2) return B0;  // no valid tiling (rejected by mma_c_ok)
+  return (NCH <= 12 && NCH % 2 == 0 && (8 * (NCH / 2)) % LC == 0 && NCH / 2 >= B0) ? NCH / 2 : B0;
+}
+
 template <int L, int IT, int C>
 __global__ __launch_bounds__(MMA_THREADS) void k_qmv_mma(const uint32_t* __restrict__ wq, const uint32_t* __restrict__ sbp,
                                                         int N, int K, int gs, const uint32_t* __restrict__ xp, int M,
@@ -178,7 +188,7 @@ __global__ __launch_bounds__(MMA_THREADS) void k_qmv_mma(const uint32_t* __restr
   constexpr int LC = L / C;    // chains per class
   constexpr int NQ = NB / C;   // blocks per class
   constexpr int NCH = NQ / 4;  // four-block chunks per class
-  constexpr int BC = LC / 4 > 2 ? LC / 4 : 2;  // chunks per loop body: the chain index and the buffer repeat
+  constexpr int BC = mma_body_chunks<L, IT, C>();  // chunks per loop body
   constexpr int TPG = 8 / C;                   // tiles per workgroup pass
   static_assert(NB % (4 * C) == 0 && NCH % BC == 0 && C <= L && C <= 8 && LC <= 16, "whole bodies of four-block chunks");
   // LDS: activations [MMA_TOK][NB][MB_DW]; per wave the (scale, bias) pairs of its tile and class [16][NQ];
@@ -443,7 +453,7 @@ static hipError_t qmv_mma_c(const uint32_t* wq, const uint32_t* sb, int N, int K
 
 template <int L, int IT, int C>
 constexpr bool mma_c_ok() {
-  constexpr int NB = L * IT, LC = L / C, BC = LC / 4 > 2 ? LC / 4 : 2;
+  constexpr int NB = L * IT, LC = L / C, BC = mma_body_chunks<L, IT, C>();
   // two workgroups per CU at least: above that the dot-product path is faster (measured)
   return C >= 2 && C <= L && LC <= 16 && NB % (4 * C) == 0 && (NB / C / 4) % BC == 0 &&
          mma_lds_bytes<L, IT, C>() <= 80 * 1024;

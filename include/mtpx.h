@@ -33,6 +33,14 @@ extern "C" {
 #define MTPX_ERR_STATE 3 /* call out of sequence (round state machine) */
 #define MTPX_ERR_OOM 4   /* device allocation failed */
 
+/* Context limit of the dense verify/draft path: offset + window <= 2048 positions.  The
+ * reference serves the same range on its fast path and hands longer contexts to the sparse
+ * QSA indexer path (Runner/FastModel/TrackFastModel.swift:1292, TrackFastHead.swift:106;
+ * indexer_budget in fixtures/qwen3_8_125b_a6b_config.json:49), which this library does not
+ * build: mtpx_layer_forward, mtpx_head_forward and mtpx_target_verify refuse a window past it
+ * with MTPX_ERR_ARG. */
+#define MTPX_INDEXER_BUDGET 2048
+
 typedef struct mtpx_ctx_ { void* ctx; } mtpx_ctx;
 typedef struct mtpx_kv_ { void* ctx; } mtpx_kv;
 typedef struct mtpx_layer_ { void* ctx; } mtpx_layer;
@@ -168,7 +176,8 @@ int mtpx_kv_trim(mtpx_kv kv, int64_t n, int64_t* trimmed);
 int mtpx_kv_buffers(mtpx_kv kv, uint16_t** k, uint16_t** v, int64_t* tmax);
 
 /* ---- a18, a21: argmax and greedy acceptance ---------------------------------
- * argmax over V per row, lowest id on ties (Runner/Qwen4ExpMTPDrafter.swift:25-27). */
+ * argmax over V per row, lowest id on ties (Runner/Qwen4ExpMTPDrafter.swift:25-27).
+ * NaN ranks above every number (the first NaN of a row wins, as numpy's argmax). */
 int mtpx_argmax_rows(mtpx_ctx ctx, const float* x, int rows, int64_t V, int32_t* out);
 /* logits f32 [k+1, V] (verify rows), drafts int32 [k] -> out3 int32 {n accepted,
  * bonus token, KV rollback index = kv_offset + n + 1}.  The engine-core accept
@@ -511,6 +520,11 @@ int mtpx_target_state_ple(mtpx_target_state st, mtpx_ple_state* out);
 /* Committed positions of every attention cache (a prefix written through mtpx_kv_buffers). */
 int mtpx_target_state_set_offset(mtpx_target_state st, int64_t offset);
 int mtpx_target_state_info(mtpx_target_state st, int64_t* offset, int* window);
+/* Back to a fresh request: every cache empty (offset 0), GDN and PLE states zero / default.
+ * A verify that fails after its first launch leaves the state refusing mtpx_target_verify and
+ * mtpx_target_commit (MTPX_ERR_STATE) until this call: some layers may already hold the failed
+ * window.  (Qwen4ExpCBv2LayerCache / recurrent state re-creation, Runner/Qwen4ExpRunner.swift:385-394.) */
+int mtpx_target_state_reset(mtpx_ctx ctx, mtpx_target_state st);
 /* S <= 8 tokens (device int32) at the committed offset -> logits bf16 [S, vocab], multi bf16
  * [S, hc*hidden], mixed bf16 [S, hidden] (each may be NULL). */
 int mtpx_target_verify(mtpx_ctx ctx, mtpx_target t, mtpx_target_state st, const int32_t* ids, int S,

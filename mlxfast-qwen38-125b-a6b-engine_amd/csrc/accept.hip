@@ -18,7 +18,9 @@ struct VI {
 };
 
 __device__ __forceinline__ VI vi_best(VI a, VI b) {
-  // larger value; lower index on equal values
+  // larger value; lower index on equal values; NaN above every number (lowest index among NaNs)
+  const bool an = a.v != a.v, bn = b.v != b.v;
+  if (an || bn) return an && bn ? (b.i < a.i ? b : a) : (bn ? b : a);
   if (b.v > a.v || (b.v == a.v && b.i < a.i)) return b;
   return a;
 }
@@ -71,12 +73,15 @@ __device__ VI reduce_parts(const float* pval, const int32_t* pidx, int parts, in
   return wave_best(best);
 }
 
-// one wave per row; with ids the winning position is mapped through them
+// one wave per row; with ids the winning position is mapped through them.  Every row has
+// V >= 1 elements, each ranked above the partials' initial index, so b.i < V; the clamp
+// only keeps the id lookup in bounds by construction.
 __global__ void k_argmax_final(const float* __restrict__ pval, const int32_t* __restrict__ pidx, int rows,
-                               int parts, const int32_t* __restrict__ ids, int32_t* __restrict__ out) {
+                               int parts, int64_t V, const int32_t* __restrict__ ids, int32_t* __restrict__ out) {
   const int row = blockIdx.x;
   const VI b = reduce_parts(pval, pidx, parts, row, threadIdx.x);
-  if (threadIdx.x == 0) out[row] = ids ? ids[b.i] : b.i;
+  const int i = b.i >= 0 && b.i < V ? b.i : 0;
+  if (threadIdx.x == 0) out[row] = ids ? ids[i] : i;
 }
 
 // one workgroup: wave r reduces row r, then thread 0 decides.
@@ -282,7 +287,7 @@ hipError_t launch_argmax_rows(const float* x, int rows, int64_t V, float* pval, 
   hipLaunchKernelGGL(k_argmax_part<float>, dim3(parts, rows), dim3(256), 0, st, x, V, parts, pval, pidx);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(k_argmax_final, dim3(rows), dim3(64), 0, st, pval, pidx, rows, parts, nullptr, out);
+  hipLaunchKernelGGL(k_argmax_final, dim3(rows), dim3(64), 0, st, pval, pidx, rows, parts, V, nullptr, out);
   return hipGetLastError();
 }
 
@@ -292,7 +297,7 @@ hipError_t launch_argmax_rows_bf16(const bf16* x, int rows, int64_t V, float* pv
   hipLaunchKernelGGL(k_argmax_part<bf16>, dim3(parts, rows), dim3(256), 0, st, x, V, parts, pval, pidx);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(k_argmax_final, dim3(rows), dim3(64), 0, st, pval, pidx, rows, parts, ids, out);
+  hipLaunchKernelGGL(k_argmax_final, dim3(rows), dim3(64), 0, st, pval, pidx, rows, parts, V, ids, out);
   return hipGetLastError();
 }
 

@@ -51,6 +51,7 @@ struct Ctx {
   void* ws = nullptr;
   size_t ws_size = 0;
   size_t ws_used = 0;
+  bool ws_over = false;              // a take ran past the reservation (see ws_take)
   MoeDispatch* last_disp = nullptr;  // inside the workspace of the last MoE call
   uint32_t* tickets = nullptr;       // MOE_TICKETS counters, zero at rest
   int last_H = 0, last_E = 0, last_F = 0, last_gs = 0;
@@ -79,6 +80,8 @@ hipEvent_t ev_get(Ctx* c) {
 // Launch `expr`; with profiling on, bracket it with events on the context stream.
 #define LAUNCH(c, name, expr)                                        \
   do {                                                               \
+    if ((c)->ws_over)                                                \
+      return fail(MTPX_ERR_STATE, "internal workspace accounting error before %s", name); \
     hipEvent_t a_ = nullptr;                                         \
     if ((c)->prof && (a_ = ev_get(c))) hipEventRecord(a_, (c)->stream); \
     HIP_OK(expr);                                                    \
@@ -129,18 +132,26 @@ int ws_reserve(Ctx* c, size_t bytes) {
   return MTPX_OK;
 }
 
+// Every entry point reserves its whole need before the first take; running
+// past the reservation is an internal accounting error.  The take then marks
+// the context (ws_over) and returns the workspace base; LAUNCH refuses every
+// launch while the mark is set, so no kernel sees memory outside the
+// allocation and the entry point returns MTPX_ERR_STATE.
 template <typename T>
 T* ws_take(Ctx* c, size_t count) {
   const size_t off = (c->ws_used + 255) & ~(size_t)255;
   c->ws_used = off + count * sizeof(T);
-  // Every entry point reserves its whole need before the first take; running
-  // past the reservation is an internal accounting error, never a user error.
-  // Stop here rather than hand a kernel memory outside the allocation.
   if (c->ws_used > c->ws_size) {
-    fprintf(stderr, "mtpx: internal workspace accounting error (%zu > %zu bytes)\n", c->ws_used, c->ws_size);
-    abort();
+    c->ws_over = true;
+    return reinterpret_cast<T*>(c->ws);
   }
   return reinterpret_cast<T*>(static_cast<char*>(c->ws) + off);
+}
+
+// Start of an entry point's workspace use.
+void ws_begin(Ctx* c) {
+  c->ws_used = 0;
+  c->ws_over = false;
 }
 
 size_t al(size_t b) { return (b + 255) & ~(size_t)255; }
@@ -1158,7 +1169,36 @@ struct TargetState {
   int32_t* moe_unique = nullptr;  // device [num_layers]: distinct routed experts of the last verify
   int64_t offset = 0;           // committed positions
   int window = 0;
+  // A verify that failed after its first launch may have advanced some layers' window state
+  // (GDN slots flipped, K/V rows written at the committed offset): the state refuses verify and
+  // commit until mtpx_target_state_reset.
+  bool broken = false;
 };
+
+// Committed GDN state back to zero (conv rows, recurrent state, tickets); no window.
+int gdn_state_zero(Ctx* c, GdnState* st) {
+  const GdnGeom g = gdn_geom(st->cfg);
+  st->cur = 0;
+  st->window = 0;
+  st->committed = 0;
+  HIP_OK(hipMemsetAsync(st->tickets, 0, 4 * (size_t)g.hv, c->stream));
+  HIP_OK(hipMemsetAsync(st->conv[0], 0, 2 * (size_t)(g.kc - 1) * g.cd, c->stream));
+  HIP_OK(hipMemsetAsync(st->ssm, 0, 4 * (size_t)g.hv * 128 * 128, c->stream));
+  return MTPX_OK;
+}
+
+// PLE state back to its fresh defaults: zero conv rows, an eos context; no window.
+int ple_state_zero(Ctx* c, PleState* st) {
+  const PleGeom pg = ple_geom(st->cfg);
+  st->cur = 0;
+  st->window = 0;
+  st->committed = 0;
+  std::vector<int32_t> eos(PLE_MAX_CTX, st->cfg.eos);
+  HIP_OK(hipMemsetAsync(st->conv[0], 0, 2 * (size_t)(pg.nb > 0 ? pg.nb : 1) * pg.W, c->stream));
+  HIP_OK(hipMemcpyAsync(st->ctx[0], eos.data(), 4 * eos.size(), hipMemcpyHostToDevice, c->stream));
+  HIP_OK(hipStreamSynchronize(c->stream));  // the host vector goes out of scope
+  return MTPX_OK;
+}
 
 mtpx_gdn_config target_gdn_cfg(const mtpx_target_config& g) {
   mtpx_gdn_config r;
@@ -1343,7 +1383,7 @@ int mtpx_qmv(mtpx_ctx h, const uint32_t* wq, const uint16_t* s, const uint16_t* 
   const size_t xpn = (size_t)M * (K / 32) * XP_DW;
   int rc = ws_reserve(c, al(xpn * 4) + 256);
   if (rc) return rc;
-  c->ws_used = 0;
+  ws_begin(c);
   uint32_t* xp = ws_take<uint32_t>(c, xpn);
   LAUNCH(c, "xprep", launch_xprep(x, M, K, xp, c->stream));
   LAUNCH(c, "qmv", launch_qmv(wq, s, b, sb, N, K, gs, xp, M, y, yf, c->stream));
@@ -1358,7 +1398,7 @@ int mtpx_moe_forward(mtpx_ctx h, const mtpx_moe_weights* w, const uint16_t* x, i
   if (rc) return rc;
   if (set_device(c)) return MTPX_ERR_HIP;
   if ((rc = ws_reserve(c, moe_ws_bytes(w, M)))) return rc;
-  c->ws_used = 0;
+  ws_begin(c);
   if ((rc = moe_enqueue(c, w, x, M, y, idx, wts, logits))) return rc;
   if (n_unique) HIP_OK(hipMemcpyAsync(n_unique, &c->last_disp->n_unique, 4, hipMemcpyDeviceToDevice, c->stream));
   return MTPX_OK;
@@ -1400,7 +1440,7 @@ int mtpx_attn_verify(mtpx_ctx h, const uint16_t* q, int S, int HQ, int HK, int D
   const size_t pf = attn_partial_floats(S, HQ, D, T);
   int rc = ws_reserve(c, al(pf * 4) + 256);
   if (rc) return rc;
-  c->ws_used = 0;
+  ws_begin(c);
   float* part = ws_take<float>(c, pf);
   LAUNCH(c, "attn_partial", launch_attn_partial(q, S, HQ, HK, D, kc, vc, tmax, T, scale, part, c->stream));
   LAUNCH(c, "attn_combine", launch_attn_combine(S, HQ, HK, D, T, part, qkv, QW, gate_off, out, out_gated, nullptr,
@@ -1488,7 +1528,7 @@ int mtpx_argmax_rows(mtpx_ctx h, const float* x, int rows, int64_t V, int32_t* o
   const size_t n = argmax_work_items(rows, V);
   int rc = ws_reserve(c, al(n * 4) * 2 + 256);
   if (rc) return rc;
-  c->ws_used = 0;
+  ws_begin(c);
   float* pv = ws_take<float>(c, n);
   int32_t* pi = ws_take<int32_t>(c, n);
   HIP_OK(launch_argmax_rows(x, rows, V, pv, pi, out, c->stream));
@@ -1504,7 +1544,7 @@ int mtpx_accept_greedy(mtpx_ctx h, const float* logits, int k, int64_t V, const 
   const size_t n = argmax_work_items(k + 1, V);
   int rc = ws_reserve(c, al(n * 4) * 2 + 256);
   if (rc) return rc;
-  c->ws_used = 0;
+  ws_begin(c);
   float* pv = ws_take<float>(c, n);
   int32_t* pi = ws_take<int32_t>(c, n);
   HIP_OK(launch_accept_greedy(logits, k, V, drafts, kv_offset, pv, pi, out3, c->stream));
@@ -1522,7 +1562,7 @@ int mtpx_accept_sample(mtpx_ctx h, const float* tlogits, const float* dlogits, i
   const size_t n = accept_sample_work_floats(k, V);
   int rc = ws_reserve(c, al(n * 4) + 256);
   if (rc) return rc;
-  c->ws_used = 0;
+  ws_begin(c);
   float* work = ws_take<float>(c, n);
   HIP_OK(launch_accept_sample(tlogits, dlogits, k, V, drafts, temperature, seed, offset, kv_offset, work, out3,
                               c->stream));
@@ -1568,6 +1608,8 @@ int mtpx_layer_forward(mtpx_ctx h, mtpx_layer lh, mtpx_kv kvh, const uint16_t* x
   ARG(kv->heads == g.kv_heads && kv->dim == g.head_dim, "kv cache geometry does not match the layer");
   ARG(kv->offset + M <= kv->tmax && kv->offset + M <= g.max_positions, "cache full (offset %lld + %d)",
       (long long)kv->offset, M);
+  ARG(kv->offset + M <= MTPX_INDEXER_BUDGET, "offset %lld + %d tokens is past the indexer budget %d",
+      (long long)kv->offset, M, MTPX_INDEXER_BUDGET);
   int rc = moe_check(&L->w.moe, M);
   if (rc) return rc;
   if (set_device(c)) return MTPX_ERR_HIP;
@@ -1577,7 +1619,7 @@ int mtpx_layer_forward(mtpx_ctx h, mtpx_layer lh, mtpx_kv kvh, const uint16_t* x
   const size_t need = moe_ws_bytes(&L->w.moe, M) + attn_ws_bytes(L, M, T) + al(2 * (size_t)M * H) * 4 +
                       al(4 * (size_t)M * XB * XP_DW) + al(4 * (size_t)M * (H / 32) * XP_DW) + 4096;
   if ((rc = ws_reserve(c, need))) return rc;
-  c->ws_used = 0;
+  ws_begin(c);
   uint16_t* h1 = ws_take<uint16_t>(c, (size_t)M * H);
   uint16_t* o = ws_take<uint16_t>(c, (size_t)M * H);
   uint16_t* s = ws_take<uint16_t>(c, (size_t)M * H);
@@ -1747,7 +1789,7 @@ int mtpx_gdn_forward(mtpx_ctx h, mtpx_gdn gh, mtpx_gdn_state sh, const uint16_t*
   const size_t xin = (size_t)S * (H / 32) * XP_DW, xout = (size_t)S * (VD / 32) * XP_DW;
   int rc = ws_reserve(c, al(xin * 4) + al(2 * (size_t)S * g.pw) + al(xout * 4) + 1024);
   if (rc) return rc;
-  c->ws_used = 0;
+  ws_begin(c);
   uint32_t* xp = ws_take<uint32_t>(c, xin);
   uint16_t* proj = ws_take<uint16_t>(c, (size_t)S * g.pw);
   uint32_t* xp2 = ws_take<uint32_t>(c, xout);
@@ -1893,7 +1935,7 @@ int mtpx_ple_forward(mtpx_ctx h, mtpx_ple ph, mtpx_ple_state sh, const int32_t* 
   if (set_device(c)) return MTPX_ERR_HIP;
   int rc = ws_reserve(c, ple_ws_bytes(L->cfg, S));
   if (rc) return rc;
-  c->ws_used = 0;
+  ws_begin(c);
   return ple_enqueue(c, L, st, ids, S, stream, out, sum, embedded);
 }
 
@@ -2059,6 +2101,23 @@ int mtpx_target_state_set_offset(mtpx_target_state sh, int64_t offset) {
   return MTPX_OK;
 }
 
+int mtpx_target_state_reset(mtpx_ctx h, mtpx_target_state sh) {
+  Ctx* c = C(h);
+  TargetState* s = static_cast<TargetState*>(sh.ctx);
+  ARG(c && s, "null argument");
+  if (set_device(c)) return MTPX_ERR_HIP;
+  int rc;
+  for (GdnState* g : s->gdn)
+    if (g && (rc = gdn_state_zero(c, g))) return rc;
+  if (s->ple && (rc = ple_state_zero(c, s->ple))) return rc;
+  s->offset = 0;
+  s->window = 0;
+  for (Kv* kv : s->kv)
+    if (kv) kv->offset = 0;
+  s->broken = false;
+  return MTPX_OK;
+}
+
 int mtpx_target_state_info(mtpx_target_state sh, int64_t* offset, int* window) {
   TargetState* s = static_cast<TargetState*>(sh.ctx);
   ARG(s, "null state");
@@ -2080,6 +2139,7 @@ int mtpx_target_moe_unique(mtpx_ctx h, mtpx_target_state sh, int32_t* out) {
 int mtpx_target_commit(mtpx_target_state sh, int n) {
   TargetState* s = static_cast<TargetState*>(sh.ctx);
   ARG(s, "null state");
+  if (s->broken) return fail(MTPX_ERR_STATE, "state left inconsistent by a failed verify; reset it first");
   if (n < 0 || n > s->window)
     return fail(MTPX_ERR_STATE, "commit of %d positions; the last verify had %d", n, s->window);
   if (s->window == 0) return MTPX_OK;  // nothing open: committing nothing again changes nothing
@@ -2093,6 +2153,11 @@ int mtpx_target_commit(mtpx_target_state sh, int n) {
   return MTPX_OK;
 }
 
+namespace {
+int target_verify_enqueue(Ctx* c, Target* t, TargetState* s, const int32_t* ids, int S, uint16_t* logits,
+                          uint16_t* multi, uint16_t* mixed, bool* launched);
+}
+
 int mtpx_target_verify(mtpx_ctx h, mtpx_target th, mtpx_target_state sh, const int32_t* ids, int S, uint16_t* logits,
                        uint16_t* multi, uint16_t* mixed) {
   Ctx* c = C(h);
@@ -2100,11 +2165,28 @@ int mtpx_target_verify(mtpx_ctx h, mtpx_target th, mtpx_target_state sh, const i
   TargetState* s = static_cast<TargetState*>(sh.ctx);
   ARG(c && t && s && ids, "null argument");
   ARG(s->t == t, "state of another target");
+  if (s->broken) return fail(MTPX_ERR_STATE, "state left inconsistent by a failed verify; reset it first");
   ARG(S >= 1 && S <= MAX_TOKENS, "S=%d", S);
+  const mtpx_layer_config& lc = t->cfg.layer;
+  ARG(s->offset + S <= lc.max_positions, "cache full (offset %lld + %d)", (long long)s->offset, S);
+  ARG(s->offset + S <= MTPX_INDEXER_BUDGET,
+      "offset %lld + %d tokens is past the indexer budget %d (the sparse-indexer path is not built)",
+      (long long)s->offset, S, MTPX_INDEXER_BUDGET);
+  if (set_device(c)) return MTPX_ERR_HIP;
+  bool launched = false;
+  const int rc = target_verify_enqueue(c, t, s, ids, S, logits, multi, mixed, &launched);
+  if (rc && launched) {
+    s->window = 0;
+    s->broken = true;
+  }
+  return rc;
+}
+
+namespace {
+int target_verify_enqueue(Ctx* c, Target* t, TargetState* s, const int32_t* ids, int S, uint16_t* logits,
+                          uint16_t* multi, uint16_t* mixed, bool* launched) {
   const mtpx_target_config& g = t->cfg;
   const mtpx_layer_config& lc = g.layer;
-  ARG(s->offset + S <= lc.max_positions, "cache full (offset %lld + %d)", (long long)s->offset, S);
-  if (set_device(c)) return MTPX_ERR_HIP;
   const int H = lc.hidden, hc = g.hc, W = hc * H, gs = lc.group_size, HQ = lc.heads, D = lc.head_dim;
   const GdnGeom gg = gdn_geom(target_gdn_cfg(g));
   const int VD = gg.hv * 128;
@@ -2128,7 +2210,7 @@ int mtpx_target_verify(mtpx_ctx h, mtpx_target th, mtpx_target_state sh, const i
                        al(4 * (size_t)S * (VD / 32) * XP_DW) + al(2 * (size_t)S * gg.pw) + 4096;
   int rc = ws_reserve(c, fixed + per_layer);
   if (rc) return rc;
-  c->ws_used = 0;
+  ws_begin(c);
   uint16_t* e = ws_take<uint16_t>(c, (size_t)S * H);
   uint16_t* x = ws_take<uint16_t>(c, (size_t)S * H);
   uint16_t* ao = ws_take<uint16_t>(c, (size_t)S * H);
@@ -2146,6 +2228,7 @@ int mtpx_target_verify(mtpx_ctx h, mtpx_target th, mtpx_target_state sh, const i
   uint16_t* proj = ws_take<uint16_t>(c, (size_t)S * gg.pw);
   const size_t mark = c->ws_used;
   hipStream_t st = c->stream;
+  *launched = true;
   LAUNCH(c, "embed", launch_embed_rows(t->embed.w, t->embed.s, t->embed.b, H, gs, g.vocab, ids, S, e, st));
   for (int i = 0; i < (int)t->layers.size(); ++i) {
     const TargetLayer& L = t->layers[i];
@@ -2191,6 +2274,7 @@ int mtpx_target_verify(mtpx_ctx h, mtpx_target th, mtpx_target_state sh, const i
   s->window = S;
   return MTPX_OK;
 }
+}  // namespace
 
 int mtpx_profile_enable(mtpx_ctx h, int on) {
   Ctx* c = C(h);
@@ -2249,7 +2333,7 @@ int mtpx_shortlist_argmax(mtpx_ctx h, const uint16_t* x, int H, const uint32_t* 
   const size_t n = argmax_work_items(1, rows);
   int rc = ws_reserve(c, al(4 * (size_t)(H / 32) * XP_DW) + al(2 * (size_t)rows) + al(n * 4) * 2 + 1024);
   if (rc) return rc;
-  c->ws_used = 0;
+  ws_begin(c);
   uint32_t* xp = ws_take<uint32_t>(c, (size_t)(H / 32) * XP_DW);
   uint16_t* y = ws_take<uint16_t>(c, (size_t)rows);
   float* pv = ws_take<float>(c, n);
@@ -2303,6 +2387,8 @@ int mtpx_head_forward(mtpx_ctx h, mtpx_head hh, mtpx_kv kvh, const int32_t* ids,
   ARG(kv->heads == lg.kv_heads && kv->dim == lg.head_dim, "kv cache geometry does not match the head");
   ARG(kv->offset + S <= kv->tmax && kv->offset + S <= lg.max_positions, "cache full (offset %lld + %d)",
       (long long)kv->offset, S);
+  ARG(kv->offset + S <= MTPX_INDEXER_BUDGET, "offset %lld + %d tokens is past the indexer budget %d",
+      (long long)kv->offset, S, MTPX_INDEXER_BUDGET);
   int rc = moe_check(&hd->w.layer.moe, S);
   if (rc) return rc;
   if (set_device(c)) return MTPX_ERR_HIP;
@@ -2311,7 +2397,7 @@ int mtpx_head_forward(mtpx_ctx h, mtpx_head hh, mtpx_kv kvh, const int32_t* ids,
   const float eps = lg.eps;
   const mtpx_head_weights& w = hd->w;
   if ((rc = ws_reserve(c, head_ws_bytes(hd, S, (int)kv->offset + S)))) return rc;
-  c->ws_used = 0;
+  ws_begin(c);
   uint16_t* e = ws_take<uint16_t>(c, (size_t)S * H);
   uint16_t* en = ws_take<uint16_t>(c, (size_t)S * H);
   uint16_t* emb = ws_take<uint16_t>(c, (size_t)S * H);

@@ -543,6 +543,9 @@ class TargetState:
     def commit(self, n: int):
         check(self.ctx.lib.mtpx_target_commit(self.h, n), "target_commit")
 
+    def reset(self):
+        check(self.ctx.lib.mtpx_target_state_reset(self.ctx.h, self.h), "target_state_reset")
+
     def moe_unique(self, num_layers: int):
         out = (C.c_int32 * num_layers)()
         check(self.ctx.lib.mtpx_target_moe_unique(self.ctx.h, self.h, C.cast(out, C.c_void_p)), "target_moe_unique")

@@ -192,6 +192,7 @@ _SIGS = {
     "mtpx_target_state_gdn": (INT, [Handle, INT, C.POINTER(Handle)]),
     "mtpx_target_state_set_offset": (INT, [Handle, I64]),
     "mtpx_target_state_info": (INT, [Handle, C.POINTER(I64), C.POINTER(INT)]),
+    "mtpx_target_state_reset": (INT, [Handle, Handle]),
     "mtpx_target_verify": (INT, [Handle, Handle, Handle, P, INT, P, P, P]),
     "mtpx_target_commit": (INT, [Handle, INT]),
     "mtpx_target_moe_unique": (INT, [Handle, Handle, P]),

@@ -14,11 +14,20 @@ exists to check it against.  Every piece it calls is pinned on its own
 import numpy as np
 
 from oracle import oracle as O
-from oracle.layer_ref import download, oracle_attn, read_device
+from oracle.layer_ref import LazyQ4, download, moe_y, oracle_attn, read_device
 
 
-def download_head(hw, hcfg):
-    """hcfg: dict with the layer config keys plus hc, lowrank, vocab."""
+def embed(e, gs, ids):
+    """Embedding rows of ids; e is a q4 triple or a LazyQ4 (rows fetched first)."""
+    if isinstance(e, LazyQ4):
+        e.fetch(ids)
+        e = e.arrays
+    return O.embed_rows(*e, gs, ids)
+
+
+def download_head(hw, hcfg, lazy=False):
+    """hcfg: dict with the layer config keys plus hc, lowrank, vocab.  lazy: embedding rows
+    and routed experts are copied from the device only as the oracle uses them."""
     H, gs, hc, LW = hcfg["hidden"], hcfg["group_size"], hcfg["hc"], hcfg["lowrank"]
     W = hc * H
 
@@ -29,7 +38,9 @@ def download_head(hw, hcfg):
         return (read_device(q4.w, rows * K // 2, np.uint32).reshape(rows, K // 8),
                 bf(q4.s, rows * K // gs).reshape(rows, K // gs), bf(q4.b, rows * K // gs).reshape(rows, K // gs))
 
-    w = dict(layer=download(hw.layer, hcfg), embed=q(hw.embed, hcfg["vocab"], H),
+    emb = (LazyQ4(hw.embed.w, hw.embed.s, hw.embed.b, hcfg["vocab"], H, gs) if lazy
+           else q(hw.embed, hcfg["vocab"], H))
+    w = dict(layer=download(hw.layer, hcfg, lazy), embed=emb,
              pre_norm_embedding=bf(hw.pre_norm_embedding, H), pre_norm_hidden=bf(hw.pre_norm_hidden, W),
              fc_embedding=q(hw.fc_embedding, H, H), fc_hidden=q(hw.fc_hidden, H, H))
     for name in ("attn_hc", "mlp_hc", "final_hc"):
@@ -54,7 +65,7 @@ def oracle_head(w, hcfg, kc, vc, ids, multi, pos0):
     """-> (multi_next [S, hc*H], sample [S, H], draft id of the last row)."""
     H, gs, hc, eps = hcfg["hidden"], hcfg["group_size"], hcfg["hc"], hcfg["eps"]
     S = len(ids)
-    e = O.embed_rows(*w["embed"], gs, ids)
+    e = embed(w["embed"], gs, ids)
     _, en = O.hc_norm(e, None, None, w["pre_norm_embedding"], 1, eps)
     emb, _ = O.qmv(*w["fc_embedding"], gs, en)
     _, mn = O.hc_norm(multi, None, None, w["pre_norm_hidden"], 1, eps)
@@ -65,7 +76,7 @@ def oracle_head(w, hcfg, kc, vc, ids, multi, pos0):
     ao = oracle_attn(w["layer"], hcfg, kc, vc, x, pos0)
     st1, n1 = O.hc_norm(st0, ao, j, w["mlp_hc"]["scale"], hc, eps)
     x, j = _mix(w["mlp_hc"], n1, hc, gs)
-    m = O.moe_block(w["layer"]["moe"], x, H, hcfg["experts"], hcfg["top_k"], hcfg["expert_width"], gs)["y"]
+    m = moe_y(w["layer"]["moe"], x, H, hcfg["experts"], hcfg["top_k"], hcfg["expert_width"], gs)
     multi_next, n2 = O.hc_norm(st1, m, j, w["final_hc"]["scale"], hc, eps)
     sample, _ = _mix(w["final_hc"], n2, hc, gs)
     logits, _ = O.qmv(*w["shortlist"], gs, sample[S - 1:S])

@@ -193,14 +193,17 @@ static float qmv_row(const uint32_t* wrow, const o_bf16* srow, const o_bf16* bro
     float acc = 0.0f;
     for (int j = l; j < nb; j += L) {
       int64_t d0 = 0, d1 = 0, d2 = 0;
-      for (int i = 0; i < 32; ++i) {
-        const uint32_t q = (wrow[(j * 32 + i) / 8] >> (4 * ((j * 32 + i) % 8))) & 0xfu;
-        const uint32_t u = (uint32_t)m[j * 32 + i] & 0xffffffu;
-        const int32_t l0 = (int32_t)(u & 0xffu), l1 = (int32_t)((u >> 8) & 0xffu);
-        const int32_t l2 = (int32_t)(int8_t)(uint8_t)(u >> 16);
-        d0 += (int64_t)q * l0;
-        d1 += (int64_t)q * l1;
-        d2 += (int64_t)q * l2;
+      for (int wd = 0; wd < 4; ++wd) {
+        const uint32_t word = wrow[j * 4 + wd];
+        for (int e = 0; e < 8; ++e) {
+          const uint32_t q = (word >> (4 * e)) & 0xfu;
+          const uint32_t u = (uint32_t)m[j * 32 + wd * 8 + e] & 0xffffffu;
+          const int32_t l0 = (int32_t)(u & 0xffu), l1 = (int32_t)((u >> 8) & 0xffu);
+          const int32_t l2 = (int32_t)(int8_t)(uint8_t)(u >> 16);
+          d0 += (int64_t)q * l0;
+          d1 += (int64_t)q * l1;
+          d2 += (int64_t)q * l2;
+        }
       }
       const int32_t low = (int32_t)(d1 * 256 + d0);
       const float dxraw = fmaf((float)(int32_t)d2, 65536.0f, (float)low);
@@ -253,6 +256,8 @@ void o_qmv(const uint32_t* wq, const o_bf16* scales, const o_bf16* biases, int64
   for (int mm = 0; mm < M; ++mm) {
     xprep_t xp;
     xprep(x + (int64_t)mm * K, K, &xp);
+    /* rows are independent: a thread per row block gives the same bits as one thread */
+#pragma omp parallel for schedule(static) if (N * (int64_t)K >= ((int64_t)1 << 20))
     for (int64_t r = 0; r < N; ++r) {
       const float v = qmv_row(wq + r * (K / 8), scales + r * ng, biases + r * ng, K, gs, xp.m,
                               xp.p, xp.SX);
@@ -289,6 +294,7 @@ static float router_row(const o_bf16* wrow, int H, const float* x) {
 
 void o_router_gemv(const o_bf16* W, int rows, int H, const float* x, int M, float* out) {
   for (int m = 0; m < M; ++m)
+#pragma omp parallel for schedule(static) if ((int64_t)rows * H >= ((int64_t)1 << 20))
     for (int r = 0; r < rows; ++r)
       out[(int64_t)m * rows + r] = router_row(W + (int64_t)r * H, H, x + (int64_t)m * H);
 }
@@ -715,12 +721,13 @@ void o_hc_mix(const o_bf16* w, const o_bf16* normed, const o_bf16* inj, int S, i
 /* out3 = {n, bonus token, kv index}.                                        */
 /* ======================================================================== */
 
+/* NaN ranks above every number: the first NaN of a row wins (numpy's argmax). */
 void o_argmax_rows(const float* x, int rows, int64_t V, int32_t* out) {
   for (int r = 0; r < rows; ++r) {
     const float* xr = x + (int64_t)r * V;
     int64_t b = 0;
-    for (int64_t v = 1; v < V; ++v)
-      if (xr[v] > xr[b]) b = v;
+    for (int64_t v = 1; v < V && !isnan(xr[b]); ++v)
+      if (isnan(xr[v]) || xr[v] > xr[b]) b = v;
     out[r] = (int32_t)b;
   }
 }
@@ -1261,4 +1268,44 @@ void o_ple_conv(const o_bf16* full, const o_bf16* conv_w, const o_bf16* gated, i
       for (int j = 0; j < kc; ++j) acc = acc + o_bf2f(full[(int64_t)(t + j * dil) * W + c]) * o_bf2f(conv_w[c * kc + j]);
       out[(int64_t)t * W + c] = o_f2bf(o_bf2f(gated[(int64_t)t * W + c]) + o_silu_bf16(o_round_bf(acc)));
     }
+}
+
+/* ======================================================================== */
+/* Thread count of the oracle's row-parallel loops (o_qmv, o_router_gemv,   */
+/* o_qmm_t_bf16).  The results do not depend on it.                          */
+/* ======================================================================== */
+#include <omp.h>
+
+void o_set_threads(int n) { omp_set_num_threads(n > 0 ? n : 1); }
+int o_get_threads(void) { return omp_get_max_threads(); }
+
+/* ======================================================================== */
+/* mlx_cpu mode: MLX's CPU quantized matmul with T = bfloat16               */
+/* (MLX/backend/cpu/quantized.cpp:153-212, _qmm_t, 4 bits): per output a    */
+/* bf16 running sum over K in element order, every operation rounded to     */
+/* bf16 as MLX's _MLX_BFloat16 operators do (MLX/types/bf16.h:72-143):      */
+/*   sum = bf16(sum + bf16(x * bf16(bf16(scale * q) + bias))).              */
+/* Used only as the CPU timing baseline (its bits are not the GPU path's).  */
+/* OpenMP over output rows when threads > 1 (MLX runs one thread per op).   */
+/* ======================================================================== */
+void o_qmm_t_bf16(const o_bf16* x, const uint32_t* wq, const o_bf16* scales, const o_bf16* biases,
+                  int M, int64_t N, int K, int gs, o_bf16* y) {
+  const int ng = K / gs;
+  for (int m = 0; m < M; ++m) {
+    const o_bf16* xm = x + (int64_t)m * K;
+#pragma omp parallel for schedule(static)
+    for (int64_t n = 0; n < N; ++n) {
+      const uint32_t* wr = wq + n * (K / 8);
+      float sum = 0.0f;
+      for (int g = 0; g < ng; ++g) {
+        const float sc = o_bf2f(scales[n * ng + g]), bi = o_bf2f(biases[n * ng + g]);
+        for (int k = g * gs; k < (g + 1) * gs; ++k) {
+          const float q = (float)((wr[k / 8] >> (4 * (k % 8))) & 0xfu);
+          const float wv = o_round_bf(o_round_bf(sc * q) + bi);
+          sum = o_round_bf(sum + o_round_bf(o_bf2f(xm[k]) * wv));
+        }
+      }
+      y[(int64_t)m * N + n] = o_f2bf(sum);
+    }
+  }
 }

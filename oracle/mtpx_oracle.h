@@ -133,6 +133,13 @@ float o_ple_gate(const o_bf16* key, const o_bf16* stream, const o_bf16* value, c
 void o_ple_conv(const o_bf16* full, const o_bf16* conv_w, const o_bf16* gated, int S, int64_t W, int kc, int dil,
                 o_bf16* out);
 
+/* Thread count of the row-parallel loops (results do not depend on it). */
+void o_set_threads(int n);
+int o_get_threads(void);
+/* mlx_cpu mode: MLX's CPU _qmm_t with bf16 accumulation (timing baseline only). */
+void o_qmm_t_bf16(const o_bf16* x, const uint32_t* wq, const o_bf16* scales, const o_bf16* biases,
+                  int M, int64_t N, int K, int gs, o_bf16* y);
+
 #ifdef __cplusplus
 }
 #endif

@@ -77,6 +77,9 @@ def _declare(L):
         "o_ngram_row_ids": (None, [P, C.c_int, C.c_int, C.c_int, C.c_int, P, P, P, I64, I32, P]),
         "o_ple_gate": (F32, [P, P, P, P, P, P, C.c_int, F32, P, P]),
         "o_ple_conv": (None, [P, P, P, C.c_int, I64, C.c_int, C.c_int, P]),
+        "o_set_threads": (None, [C.c_int]),
+        "o_get_threads": (C.c_int, []),
+        "o_qmm_t_bf16": (None, [P, P, P, P, C.c_int, I64, C.c_int, C.c_int, P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -303,6 +306,27 @@ def shortlist_argmax(y_bf16, ids):
     """Draft id: ids[argmax over the bf16 logits], lowest position on ties."""
     v = bf16_to_f32(np.asarray(y_bf16, np.uint16).reshape(-1))
     return int(np.asarray(ids, np.int32)[int(np.argmax(v))])
+
+
+def set_threads(n: int):
+    """Threads of the oracle's row-parallel loops (its results do not depend on the count)."""
+    lib().o_set_threads(int(n))
+
+
+def get_threads() -> int:
+    return int(lib().o_get_threads())
+
+
+def qmm_t_bf16(wq, scales, biases, gs, x):
+    """MLX CPU _qmm_t with bf16 accumulation (the mlx_cpu timing mode) -> bf16 [M, N]."""
+    wq = np.ascontiguousarray(wq, np.uint32)
+    s = np.ascontiguousarray(scales, np.uint16)
+    b = np.ascontiguousarray(biases, np.uint16)
+    x = np.ascontiguousarray(np.atleast_2d(x), np.uint16)
+    N, K = wq.shape[0], wq.shape[1] * 8
+    y = np.zeros((x.shape[0], N), np.uint16)
+    lib().o_qmm_t_bf16(_p(x), _p(wq), _p(s), _p(b), x.shape[0], N, K, gs, _p(y))
+    return y
 
 
 def argmax_rows(x):

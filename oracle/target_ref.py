@@ -15,8 +15,8 @@ piece it calls is pinned on its own (tests/test_oracle_*.py).
 import numpy as np
 
 from oracle import oracle as O
-from oracle.head_ref import _mix
-from oracle.layer_ref import download, download_moe, oracle_attn, read_device
+from oracle.head_ref import _mix, embed
+from oracle.layer_ref import LazyQ4, download, download_moe, moe_y, oracle_attn, read_device
 
 
 def _bf(ptr, n):
@@ -49,41 +49,61 @@ def ple_cfg_dict(pc):
                 row_group_size=pc.row_group_size, eos=pc.eos, eps=pc.eps)
 
 
-def download_ple(pw, pc):
-    """Device weights of a PLE block (mtpx.PLEWeights) for oracle.ple_forward."""
+def download_ple(pw, pc, lazy=False):
+    """Device weights of a PLE block (mtpx.PLEWeights) for oracle.ple_forward.  lazy: table rows
+    are copied from the device only as a window's n-gram ids select them (ple_fetch)."""
     H, W, E, gs, rgs = pc.hidden, pc.hc * pc.hidden, pc.embed_dim, pc.group_size, pc.row_group_size
     nh = (pc.ngram_size - 1) * pc.heads_per_ngram
     rd = E // nh
     t = pw.table
     rows = t.rows
-    table = (read_device(t.w, rows * rd // 2, np.uint32).reshape(rows, rd // 8),
-             _bf(t.s, rows * rd // rgs).reshape(rows, rd // rgs), _bf(t.b, rows * rd // rgs).reshape(rows, rd // rgs))
-    return dict(key_proj=_q(pw.key_proj, W, E, gs), value_proj=_q(pw.value_proj, H, E, gs),
+    lazy_table = None
+    if lazy:
+        lazy_table = LazyQ4(t.w, t.s, t.b, rows, rd, rgs)
+        table = lazy_table.arrays
+    else:
+        table = (read_device(t.w, rows * rd // 2, np.uint32).reshape(rows, rd // 8),
+                 _bf(t.s, rows * rd // rgs).reshape(rows, rd // rgs),
+                 _bf(t.b, rows * rd // rgs).reshape(rows, rd // rgs))
+    return dict(_lazy_table=lazy_table, key_proj=_q(pw.key_proj, W, E, gs), value_proj=_q(pw.value_proj, H, E, gs),
                 norm_key=_bf(pw.norm_key, W), norm_query=_bf(pw.norm_query, W), norm_conv=_bf(pw.norm_conv, W),
                 conv_w=_bf(pw.conv_w, W * pc.conv_kernel).reshape(W, pc.conv_kernel), table=table,
                 mult=np.array(list(t.multiplier)[:pc.ngram_size], np.int64),
                 vocab=np.array(list(t.vocab)[:nh], np.int64), offs=np.array(list(t.offset)[:nh], np.int64))
 
 
-def download_target(t, cfg):
+def ple_fetch(Lp, pc, ids, context):
+    """Copy the table rows a window's n-gram ids select (a lazily downloaded table)."""
+    lt = Lp.get("_lazy_table")
+    if lt is None:
+        return
+    hist = np.concatenate([np.asarray(context, np.int32), np.asarray(ids, np.int32)])
+    rid = O.ngram_row_ids(hist, len(context), pc["ngram_size"], pc["heads_per_ngram"], Lp["mult"], Lp["vocab"],
+                          Lp["offs"], lt.have.size, pc["eos"])
+    lt.fetch(np.concatenate([rid.reshape(-1), [0]]))
+
+
+def download_target(t, cfg, lazy=False):
     """cfg: dict with the layer config keys plus key_heads, value_heads, conv_kernel,
-    num_layers, full_attention_interval, hc, lowrank, vocab."""
+    num_layers, full_attention_interval, hc, lowrank, vocab.  lazy: embedding rows, routed
+    experts and n-gram table rows are copied from the device only as the oracle uses them."""
     H, gs, hc, LW, V = cfg["hidden"], cfg["group_size"], cfg["hc"], cfg["lowrank"], cfg["vocab"]
     tw = t.weights()
-    w = dict(embed=_q(tw.embed, V, H, gs), lm_head=_q(tw.lm_head, V, H, gs),
+    emb = LazyQ4(tw.embed.w, tw.embed.s, tw.embed.b, V, H, gs) if lazy else _q(tw.embed, V, H, gs)
+    w = dict(embed=emb, lm_head=_q(tw.lm_head, V, H, gs),
              final_hc=download_hc(tw.final_hc, H, hc, LW, gs), layers=[])
     for i in range(cfg["num_layers"]):
         lw = t.layer_weights(i)
         L = dict(kind=lw.kind, attn_hc=download_hc(lw.attn_hc, H, hc, LW, gs),
                  mlp_hc=download_hc(lw.mlp_hc, H, hc, LW, gs))
         if lw.kind == 1:
-            L["attn"] = download(lw.attn, cfg)
+            L["attn"] = download(lw.attn, cfg, lazy)
             L["moe"] = L["attn"]["moe"]
         else:
             L["gdn"] = download_gdn(lw.gdn, H, cfg["key_heads"], cfg["value_heads"], cfg["conv_kernel"], gs)
-            L["moe"] = download_moe(lw.attn.moe, cfg)
+            L["moe"] = download_moe(lw.attn.moe, cfg, lazy)
         if i == cfg.get("ple_layer", -1):
-            L["ple"] = download_ple(lw.ple, t.cfg.ple)
+            L["ple"] = download_ple(lw.ple, t.cfg.ple, lazy)
             L["ple_cfg"] = ple_cfg_dict(t.cfg.ple)
         w["layers"].append(L)
     return w
@@ -100,13 +120,14 @@ def oracle_verify(w, cfg, state, ids, pos0):
     window's rows in place).
     -> (logits [S, V], multi [S, hc*H], mixed [S, H], window) where window feeds oracle_commit."""
     H, gs, hc, eps = cfg["hidden"], cfg["group_size"], cfg["hc"], cfg["eps"]
-    e = O.embed_rows(*w["embed"], gs, ids)
+    e = embed(w["embed"], gs, ids)
     resid, out, inj, tile = e, None, None, True
     window = {}
     for i, L in enumerate(w["layers"]):
         sA, n = O.hc_norm(resid, out, inj, L["attn_hc"]["scale"], hc, eps, tile=tile)
         if "ple" in L:
             conv, context = state["ple"]
+            ple_fetch(L["ple"], L["ple_cfg"], ids, context)
             res = O.ple_forward(L["ple"], L["ple_cfg"], sA, ids, conv, context)
             window["ple"] = (i, res)
             sA, n = O.hc_norm(res["sum"], None, None, L["attn_hc"]["scale"], hc, eps)
@@ -120,7 +141,7 @@ def oracle_verify(w, cfg, state, ids, pos0):
             ao = oracle_attn(L["attn"], cfg, state["kc"][i], state["vc"][i], x, pos0)
         sM, n = O.hc_norm(sA, ao, jA, L["mlp_hc"]["scale"], hc, eps)
         x, jM = _mix(L["mlp_hc"], n, hc, gs)
-        mo = O.moe_block(L["moe"], x, H, cfg["experts"], cfg["top_k"], cfg["expert_width"], gs)["y"]
+        mo = moe_y(L["moe"], x, H, cfg["experts"], cfg["top_k"], cfg["expert_width"], gs)
         resid, out, inj, tile = sM, mo, jM, False
     multi, n = O.hc_norm(resid, out, inj, w["final_hc"]["scale"], hc, eps)
     mixed, _ = _mix(w["final_hc"], n, hc, gs)

@@ -160,6 +160,29 @@ def test_argmax_rows_bit_exact(ctx):
     assert host(out)[3] == 1000
 
 
+def test_argmax_and_accept_nan_rows(ctx):
+    """NaN ranks above every number, the first NaN of a row wins (numpy's rule): an all-NaN row
+    gives id 0, a NaN beyond the 8192-element slices of the partial pass still wins."""
+    V = 151936
+    x = np.random.default_rng(5).standard_normal((4, V)).astype(np.float32)
+    x[0, :] = np.nan
+    x[1, [70000, 150000]] = np.nan
+    x[2, 9] = np.inf
+    x[3, 100000] = np.nan
+    x[3, 5] = np.inf
+    out = torch.zeros(4, dtype=torch.int32, device="cuda")
+    ctx.argmax_rows(dev(x), out)
+    ctx.synchronize()
+    want = [int(np.argmax(r)) for r in x]
+    assert want == [0, 70000, 9, 100000]
+    assert list(host(out)) == want == list(O.argmax_rows(x))
+    out3 = torch.zeros(3, dtype=torch.int32, device="cuda")
+    drafts = np.array([0, 70000, 9], np.int32)
+    ctx.accept_greedy(dev(x), dev(drafts), 100, out3)
+    ctx.synchronize()
+    assert list(host(out3)) == list(O.accept_greedy(x, drafts, 100)) == [3, 100000, 104]
+
+
 @pytest.mark.parametrize("k", [1, 3, 5])
 @pytest.mark.parametrize("p", [0.3, 0.9])
 def test_accept_sample_bit_exact(ctx, k, p):

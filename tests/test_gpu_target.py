@@ -116,3 +116,47 @@ def test_target_verify_commit_discard_bit_exact(ctx, ple_layer):
         st.gdn(3)  # an attention layer has no GDN state
     st.close()
     t.close()
+
+
+def test_target_refusals_and_reset(ctx):
+    """A verify refused before any launch leaves the open window intact (commit still works); a window
+    past the indexer budget (2048 positions) is refused; reset returns every cache to the fresh state
+    (a verify after reset gives the bits of a verify on a new state)."""
+    import mtpx
+    layer = dict(LAYER, max_positions=2100)
+    tc = mtpx.TargetConfig(mtpx.LayerConfig(**layer), *[TARGET[k] for k in (
+        "key_heads", "value_heads", "conv_kernel", "num_layers", "full_attention_interval", "hc", "lowrank",
+        "vocab")])
+    tc.ple_layer = 1
+    tc.ple = mtpx.PLEConfig(hidden=LAYER["hidden"], hc=TARGET["hc"], embed_dim=256, ngram_size=3, heads_per_ngram=2,
+                            conv_kernel=4, group_size=LAYER["group_size"], row_group_size=32, eos=7, vocab_base=300,
+                            token_vocab=TARGET["vocab"], eps=LAYER["eps"])
+    t = mtpx.Target(ctx, tc, seed=23)
+    H, hc, V = LAYER["hidden"], TARGET["hc"], TARGET["vocab"]
+    ids = dev(np.array([3, 1, 4, 1], np.int32))
+    fresh = mtpx.TargetState(ctx, t)
+    lg0 = empty_bf16(4, V)
+    t.verify(fresh, ids, lg0)
+    st = mtpx.TargetState(ctx, t)
+    for n in (4, 2):  # advance the state: GDN and PLE states, caches and offset all move
+        t.verify(st, ids[:n], empty_bf16(n, V))
+        st.commit(n)
+    print("case target refusals", flush=True)
+    t.verify(st, ids[:3], empty_bf16(3, V))
+    with pytest.raises(mtpx.MtpxError):
+        t.verify(st, dev(np.zeros(9, np.int32)), empty_bf16(9, V))  # S > 8: refused, nothing launched
+    st.commit(2)
+    assert st.info() == (8, 0)
+    st.set_offset(2046)
+    with pytest.raises(mtpx.MtpxError, match="indexer budget"):
+        t.verify(st, ids, empty_bf16(4, V))
+    t.verify(st, ids[:2], empty_bf16(2, V))  # 2046 + 2 == 2048: served
+    print("case target reset", flush=True)
+    st.reset()
+    assert st.info() == (0, 0)
+    lg1 = empty_bf16(4, V)
+    t.verify(st, ids, lg1)
+    assert np.array_equal(host(lg1), host(lg0))
+    st.close()
+    fresh.close()
+    t.close()

@@ -423,3 +423,11 @@ def test_sample_emits_target_distribution():
 def test_softmax_row_sum_close_to_fsum():
     e = rng(16).random(151936).astype(np.float32)
     assert abs(O.softmax_row_sum(e) - math.fsum(e.astype(np.float64))) <= 1e-6 * e.sum()
+
+
+def test_argmax_nan_rule_matches_numpy():
+    x = np.array([[1.0, np.nan, 3.0, np.nan], [np.nan] * 4, [-np.inf] * 4, [2.0, 5.0, 5.0, -1.0]], np.float32)
+    got = O.argmax_rows(x)
+    assert list(got) == [int(np.argmax(r)) for r in x] == [1, 0, 0, 1]
+    out = O.accept_greedy(x[1:3].copy(), np.array([0], np.int32), 10)
+    assert list(out) == [1, 0, 12]  # row 0 all NaN: argmax 0 == draft 0 accepted; bonus row 1 -> 0

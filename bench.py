@@ -1,33 +1,31 @@
 """Benchmark of single-stream MTP speculative decode on one MI355X.
 
-Default workload: BASELINE config 5 -- rounds of MTP speculative decode on the
-full-depth random-init 125B-A6B model (48 layers: 36 gated-deltanet + 12
-attention, each with hyper-connection mixers and a 512-expert top-10 + shared
-MoE; hidden 2560, vocab 248320, affine 4-bit gs64, all weights resident in HBM)
-with the MTP head.  The committed prefix of 1024 positions is synthetic: random
-attention K/V rows, random GDN states and a random PLE state stand in for the
-prompt (prefill is not part of this build).  Layer 1 carries the PLE n-gram
-block with the full n-gram table (16 heads over 320,001,446 rows of 100 bytes,
-32 GB, resident in HBM; --no-ple leaves it out).  A step = one round: k drafter steps, a verify of the carried token
-and the k drafts, the on-device greedy accept (read back once per round), the
-target commit and the drafter finalize.  Random-init drafts almost never match
-the target, so the accepted count is forced at p = 0.7 by a seeded draw.  The
-draft depth is the best of a sweep over 1..5; value = expected committed tokens
-per round at p (1 + p + ... + p^k) / measured time per round, over --steps
-rounds at that depth after --warmup rounds (every round does the same work
-whatever the draw; the realized count is reported beside it).
+Default workload: BASELINE config 5 -- the full-depth random-init 125B-A6B model (48 layers: 36
+gated-deltanet + 12 attention, each with hyper-connection mixers and a 512-expert top-10 + shared
+MoE; hidden 2560, vocab 248320, affine 4-bit gs64, all weights resident in HBM; layer 1 carries the
+PLE n-gram block with its full 320,001,446-row table, 32 GB, --no-ple leaves it out) with the MTP
+head.  A 1024-token random prompt is processed through the verify path (windows of 8, committed),
+then 1024 tokens are generated greedily through mtpx_round (the device-resident round: k drafter
+steps, a verify of the carry and the k drafts, the on-device greedy accept read back once, target
+commit, drafter finalize).  First a serial greedy decode (k = 0) of the same 1024 tokens gives the
+reference sequence; random-init drafts would never match the target, so acceptance is forced at
+p = 0.7 by the drafter's forcing hook: each drafted position takes the reference sequence's token
+with probability p (a seeded Philox draw per position).  The accept kernel's own count drives the
+commit, and every depth must emit exactly the serial sequence.  Depths 1..5 are swept; value =
+realized tokens/s of the best depth over all rounds of its 1024-token generation; the serial decode,
+per-depth medians and accepted lengths, the draft step's time and a gs32 line (the checkpoint's
+~113 GB format, at the best depth) are reported beside it.
 
-Before the rounds the same run measures BASELINE config 4 (a verify of k+1 = 4
-tokens, --steps timed steps; reported under "verify") and the per-kernel HIP
-event timings of that verify.  `roofline` is the routed-expert gate|up+SwiGLU
-kernel (the largest HBM stream of the step): algorithmic bytes of its average
-launch (distinct experts of every layer read back from the device) / its
-average duration from HIP events recorded on the launch stream.
-`cpu_baseline` times the CPU oracle (the same arithmetic in C) on a bounded
-sample of the same rounds, scaled as stated in its `sample` field.
-`--no-e2e` reports the config-4 verify as the value; `--workload layer` runs
-config 3 (one full-shape decoder layer, plain residuals, 4 tokens over 1024
-cached positions).
+Before the decode the same run measures BASELINE config 4 (a verify of 4 tokens after the prompt,
+--steps timed steps; reported under "verify") and the per-kernel HIP event timings of that verify.
+`roofline` is the routed-expert gate|up+SwiGLU kernel (the largest HBM stream of the step):
+algorithmic bytes of its average launch (distinct experts of every layer read back from the
+device) / its average duration from HIP events recorded on the launch stream.  `cpu_baseline`
+times the CPU oracle on a bounded sample of the same round (1 thread and all host threads, the
+oracle's exact arithmetic and MLX's CPU bf16-accumulating quantized matmul), scaled as its
+`sample` field states.  `--no-e2e` reports the config-4 verify as the value; `--workload layer`
+runs config 3 (one full-shape decoder layer, plain residuals, 4 tokens over 1024 cached
+positions).
 """
 from __future__ import annotations
 
@@ -122,46 +120,58 @@ def target_config(mtpx, lc, tc):
     return cfg
 
 
-def synthetic_prefix(mtpx, ctx, state, lc, tc, kinds, g, T0):
-    """Random committed state in place of a prompt: attention K/V rows, GDN conv rows and
-    recurrent states, the PLE block's conv rows and token context."""
-    import torch
+def _mlx_cpu_patch(O):
+    """Swap the oracle's q4 GEMV and MoE block for MLX's CPU quantized matmul (_qmm_t with bf16
+    accumulation, O.qmm_t_bf16) for the mlx_cpu timing mode; returns the undo function."""
+    import numpy as np
 
-    for i, kind in enumerate(kinds):
-        if kind == 1:
-            kp, vp, tmax = state.kv(i).buffers()
-            n_kv = lc["kv_heads"] * tmax * lc["head_dim"]
-            for ptr, tensor in ((kp, 2 * i + 1), (vp, 2 * i + 2)):
-                mtpx.check(ctx.lib.mtpx_randn_bf16(ctx.h, C.c_void_p(ptr), n_kv, 0x5EED0006, tensor, 1.0),
-                           "randn kv")
-        else:
-            conv = torch.randn(tc["conv_kernel"] - 1, (2 * tc["key_heads"] + tc["value_heads"]) * 128,
-                               device="cuda", generator=g).to(torch.bfloat16)
-            ssm = torch.randn(tc["value_heads"], 128, 128, device="cuda", generator=g) * 0.05
-            state.gdn(i).load(conv, ssm)
-            torch.cuda.synchronize()
-    if tc["ple_layer"] >= 0:
-        pc = tc["ple"]
-        conv = torch.randn((pc["conv_kernel"] - 1) * pc["ngram_size"], pc["hc"] * pc["hidden"], device="cuda",
-                           generator=g).to(torch.bfloat16)
-        context = torch.randint(0, tc["vocab"], (pc["ngram_size"] - 1,), device="cuda", generator=g,
-                                dtype=torch.int32)
-        state.ple().load(conv, context)
-        torch.cuda.synchronize()
-    state.set_offset(T0)
+    qmv0, moe0 = O.qmv, O.moe_block
+
+    def qmv(wq, s_, b_, gs, x):
+        return O.qmm_t_bf16(wq, s_, b_, gs, x), None
+
+    def moe_block(w, x, H, E, K, F, gs):
+        x = np.asarray(x, np.uint16).reshape(-1, H)
+        idx, wk = O.topk_softmax(O.router_gemv(w["router"], O.bf16_to_f32(x)), K)
+        ng, ngF = H // gs, F // gs
+        y = np.zeros((x.shape[0], H), np.float32)
+        for m in range(x.shape[0]):
+            def ffn(gw, gsc, gb, uw, usc, ub, dw, dsc, db):
+                g = O.bf16_to_f32(O.qmm_t_bf16(gw, gsc, gb, gs, x[m]))
+                u = O.bf16_to_f32(O.qmm_t_bf16(uw, usc, ub, gs, x[m]))
+                a = O.f32_to_bf16(g / (1 + np.exp(-g)) * u)
+                return O.bf16_to_f32(O.qmm_t_bf16(dw, dsc, db, gs, a))[0]
+            for k, e in enumerate(idx[m]):
+                rows = slice(e * F, (e + 1) * F)
+                hrows = slice(e * H, (e + 1) * H)
+                y[m] += wk[m, k] * ffn(w["gate_w"][rows], w["gate_s"][rows], w["gate_b"][rows], w["up_w"][rows],
+                                       w["up_s"][rows], w["up_b"][rows], w["down_w"][hrows], w["down_s"][hrows],
+                                       w["down_b"][hrows])
+            gl = float(O.router_gemv(w["shared_gate"], O.bf16_to_f32(x[m]))[0, 0])
+            y[m] += ffn(w["sh_gate_w"], w["sh_gate_s"], w["sh_gate_b"], w["sh_up_w"], w["sh_up_s"], w["sh_up_b"],
+                        w["sh_down_w"], w["sh_down_s"], w["sh_down_b"]) / (1 + np.exp(-gl))
+        return dict(y=O.f32_to_bf16(y), idx=idx)
+
+    O.qmv, O.moe_block = qmv, moe_block
+
+    def undo():
+        O.qmv, O.moe_block = qmv0, moe0
+    return undo
 
 
-def cpu_layer_times(target, state, lc, tc, widths, kinds, seconds=12.0):
-    """The oracle on a bounded sample of the target step, one host thread: per verify width M,
-    the first GDN layer and the first attention layer (each with its mixers and MoE), 16384 of the
-    lm_head rows and the PLE block (its projections, norms and conv from the device; the row gather
-    from the first 65536 table rows, whose cost does not depend on the table's size).
-    -> ({M: (t_gdn, t_attn, t_head_rows, t_ple)}, rows, iterations)."""
+def cpu_layer_times(target, lc, tc, widths, kinds, T0, runs=(("port", 1, 6.0),)):
+    """The oracle on a bounded sample of the target step: per verify width M, the first GDN layer and
+    the first attention layer (each with its mixers and MoE, attention over T0 random cached positions),
+    16384 of the lm_head rows and the PLE block (the row gather from the first 65536 table rows, whose
+    cost does not depend on the table's size).  runs: (mode, threads, seconds) -- mode "port": the
+    oracle's exact int24 arithmetic; "mlx_cpu": its q4 GEMVs and MoE replaced by MLX's CPU _qmm_t (bf16
+    accumulation); threads: OpenMP threads of the row-parallel loops; at least one iteration per width.
+    -> ({(mode, threads): {M: (t_gdn, t_attn, t_head_rows, t_ple)}}, rows, {(mode, threads): iterations})."""
     import numpy as np
 
     from oracle import oracle as O
     from oracle.head_ref import _mix
-    from oracle.layer_ref import download, download_moe, oracle_attn, read_device
+    from oracle.layer_ref import download, download_moe, moe_y, oracle_attn, read_device
     from oracle.target_ref import _q, download_gdn, download_hc
 
     import torch
@@ -169,35 +179,36 @@ def cpu_layer_times(target, state, lc, tc, widths, kinds, seconds=12.0):
     torch.cuda.synchronize()
     cfg = dict(lc, **tc)
     H, gs, hc, LW, eps = lc["hidden"], lc["group_size"], tc["hc"], tc["lowrank"], lc["eps"]
+    E, K, F = lc["experts"], lc["top_k"], lc["expert_width"]
     gi, ai = kinds.index(0), kinds.index(1)
     lw_g, lw_a = target.layer_weights(gi), target.layer_weights(ai)
     Lg = dict(hc=download_hc(lw_g.attn_hc, H, hc, LW, gs), mhc=download_hc(lw_g.mlp_hc, H, hc, LW, gs),
               gdn=download_gdn(lw_g.gdn, H, tc["key_heads"], tc["value_heads"], tc["conv_kernel"], gs),
-              moe=download_moe(lw_g.attn.moe, cfg))
+              moe=download_moe(lw_g.attn.moe, cfg, lazy=True))
     La = dict(hc=download_hc(lw_a.attn_hc, H, hc, LW, gs), mhc=download_hc(lw_a.mlp_hc, H, hc, LW, gs),
-              attn=download(lw_a.attn, cfg))
+              attn=download(lw_a.attn, cfg, lazy=True))
     La["moe"] = La["attn"]["moe"]
-    kp, vp, tmax = state.kv(ai).buffers()
-    HK, D = lc["kv_heads"], lc["head_dim"]
-    kc = read_device(kp, HK * tmax * D * 2, np.uint16).reshape(HK, tmax, D)
-    vc = read_device(vp, HK * tmax * D * 2, np.uint16).reshape(HK, tmax, D)
-    g = Lg["gdn"]["geom"]
+    HK, D, P = lc["kv_heads"], lc["head_dim"], lc["max_positions"]
     r = np.random.default_rng(9)
+    kc = np.zeros((HK, P, D), np.uint16)
+    vc = np.zeros_like(kc)
+    kc[:, :T0] = O.f32_to_bf16(r.standard_normal((HK, T0, D)).astype(np.float32))
+    vc[:, :T0] = O.f32_to_bf16(r.standard_normal((HK, T0, D)).astype(np.float32))
+    g = Lg["gdn"]["geom"]
     conv = O.f32_to_bf16(r.standard_normal((g.kc - 1, g.conv_dim)).astype(np.float32))
     ssm = (r.standard_normal((g.hv, 128, 128)) * 0.05).astype(np.float32)
     rows = 16384
     head = _q(target.weights().lm_head, rows, H, gs)  # the first `rows` rows of lm_head
-    pos0, _ = state.info()
     ple = None
     if tc["ple_layer"] >= 0:
         pc, pw = tc["ple"], target.layer_weights(tc["ple_layer"]).ple
-        W, E, nh = hc * H, pc["embed_dim"], 2 * pc["heads_per_ngram"]
-        rd, nt = E // nh, 65536
+        W, Ed, nh = hc * H, pc["embed_dim"], 2 * pc["heads_per_ngram"]
+        rd, nt = Ed // nh, 65536
         table = (read_device(pw.table.w, nt * rd // 2, np.uint32).reshape(nt, rd // 8),
                  read_device(pw.table.s, nt * rd // 16, np.uint16).reshape(nt, rd // 32),
                  read_device(pw.table.b, nt * rd // 16, np.uint16).reshape(nt, rd // 32))
         vocab = np.array(O.primes_above(nt // nh - 300, nh), np.int64)
-        ple = dict(key_proj=_q(pw.key_proj, W, E, gs), value_proj=_q(pw.value_proj, H, E, gs),
+        ple = dict(key_proj=_q(pw.key_proj, W, Ed, gs), value_proj=_q(pw.value_proj, H, Ed, gs),
                    norm_key=read_device(pw.norm_key, 2 * W, np.uint16),
                    norm_query=read_device(pw.norm_query, 2 * W, np.uint16),
                    norm_conv=read_device(pw.norm_conv, 2 * W, np.uint16),
@@ -207,124 +218,205 @@ def cpu_layer_times(target, state, lc, tc, widths, kinds, seconds=12.0):
         ple_conv = O.f32_to_bf16(r.standard_normal(((pc["conv_kernel"] - 1) * pc["ngram_size"], W)).astype(np.float32))
 
     def layer_step(L, gdn, sW):
-        s, n = O.hc_norm(sW, None, None, L["hc"]["scale"], hc, eps)
+        s_, n = O.hc_norm(sW, None, None, L["hc"]["scale"], hc, eps)
         x, j = _mix(L["hc"], n, hc, gs)
         if gdn:
             d = L["gdn"]
             proj, _ = O.qmv(*d["in_proj"], gs, x)
-            out = O.gdn_core(d["geom"], proj, conv, ssm, d["conv_w"], d["nea"], d["dtb"], d["nw"], eps)
-            ao, _ = O.qmv(*d["out_proj"], gs, out["gated"])
+            o = O.gdn_core(d["geom"], proj, conv, ssm, d["conv_w"], d["nea"], d["dtb"], d["nw"], eps)
+            ao, _ = O.qmv(*d["out_proj"], gs, o["gated"])
         else:
-            ao = oracle_attn(L["attn"], cfg, kc, vc, x, pos0)
-        s2, n = O.hc_norm(s, ao, j, L["mhc"]["scale"], hc, eps)
+            ao = oracle_attn(L["attn"], cfg, kc, vc, x, T0)
+        s2, n = O.hc_norm(s_, ao, j, L["mhc"]["scale"], hc, eps)
         x, j = _mix(L["mhc"], n, hc, gs)
-        O.moe_block(L["moe"], x, H, lc["experts"], lc["top_k"], lc["expert_width"], gs)
+        moe_y(L["moe"], x, H, E, K, F, gs)
 
-    times, iters = {}, {}
+    inputs = {}
     for M in widths:
         sW = O.f32_to_bf16(r.standard_normal((M, hc * H)).astype(np.float32))
         xh = O.f32_to_bf16(r.standard_normal((M, H)).astype(np.float32))
         ids = r.integers(0, tc["vocab"], M).astype(np.int32)
-        tg = ta = th = tp = 0.0
-        n = 0
-        t0 = time.perf_counter()
-        while n == 0 or time.perf_counter() - t0 < seconds / len(widths):
-            a = time.perf_counter()
-            layer_step(Lg, True, sW)
-            b = time.perf_counter()
-            layer_step(La, False, sW)
-            c = time.perf_counter()
-            O.qmv(*head, gs, xh)
-            d = time.perf_counter()
-            if ple is not None:
-                O.ple_forward(ple, dict(tc["ple"]), sW, ids, ple_conv, ids[:2] if M >= 2 else np.r_[ids, ids])
-            e = time.perf_counter()
-            tg, ta, th, tp, n = tg + b - a, ta + c - b, th + d - c, tp + e - d, n + 1
-        times[M], iters[M] = (tg / n, ta / n, th / n, tp / n), n
-    return times, rows, iters
+        O.set_threads(cpu_threads_all())
+        layer_step(Lg, True, sW)  # fetches the routed experts of these inputs (not timed)
+        layer_step(La, False, sW)
+        inputs[M] = (sW, xh, ids)
+    all_times, all_iters = {}, {}
+    for mode, threads, seconds in runs:
+        O.set_threads(threads)
+        undo = _mlx_cpu_patch(O) if mode == "mlx_cpu" else (lambda: None)
+        times, iters = {}, {}
+        try:
+            for M in widths:
+                sW, xh, ids = inputs[M]
+                tg = ta = th = tp = 0.0
+                n = 0
+                t0 = time.perf_counter()
+                while n == 0 or time.perf_counter() - t0 < seconds / len(widths):
+                    a = time.perf_counter()
+                    layer_step(Lg, True, sW)
+                    b = time.perf_counter()
+                    layer_step(La, False, sW)
+                    c = time.perf_counter()
+                    O.qmv(*head, gs, xh)
+                    d = time.perf_counter()
+                    if ple is not None:
+                        O.ple_forward(ple, dict(tc["ple"]), sW, ids, ple_conv,
+                                      ids[:2] if M >= 2 else np.r_[ids, ids])
+                    e = time.perf_counter()
+                    tg, ta, th, tp, n = tg + b - a, ta + c - b, th + d - c, tp + e - d, n + 1
+                times[M], iters[M] = (tg / n, ta / n, th / n, tp / n), n
+        finally:
+            undo()
+        all_times[(mode, threads)], all_iters[(mode, threads)] = times, iters
+        log(f"cpu sample {mode} x{threads}: {times}")
+    O.set_threads(cpu_threads_all())
+    return all_times, rows, all_iters
 
 
-def cpu_baseline_full(target, state, lc, tc, M, kinds):
-    """CPU baseline of the verify step (config 4): the sampled oracle layers scaled to the stack."""
-    times, rows, iters = cpu_layer_times(target, state, lc, tc, [M], kinds)
-    tg, ta, th, tp = times[M]
+def _cpu_info():
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return os.cpu_count(), len(os.sched_getaffinity(0)), model
+
+
+def cpu_threads_all():
+    return int(os.environ.get("OMP_NUM_THREADS", "0")) or len(os.sched_getaffinity(0))
+
+
+def cpu_baseline_full(target, lc, tc, M, kinds, T0):
+    """CPU baseline of the verify step (config 4): the sampled oracle layers scaled to the stack, on all
+    host threads (port mode)."""
+    th = cpu_threads_all()
+    all_times, rows, all_iters = cpu_layer_times(target, lc, tc, [M], kinds, T0, runs=(("port", th, 6.0),))
+    tg, ta, thr, tp = all_times[("port", th)][M]
     n_gdn, n_attn = kinds.count(0), kinds.count(1)
-    step_s = n_gdn * tg + n_attn * ta + th * tc["vocab"] / rows + tp
-    return dict(value=M / step_s, unit="tok/s", cores=1, kind="port",
-                sample=f"{iters[M]} x (one GDN layer {tg:.2f} s, one attention layer {ta:.2f} s, {rows} of "
-                       f"{tc['vocab']} lm_head rows {th:.2f} s, the PLE block {tp:.2f} s) of the same verify step "
-                       f"(M={M}) through the C "
-                       f"oracle, single thread; scaled to {n_gdn} GDN + {n_attn} attention layers and the "
-                       f"whole lm_head: {step_s:.1f} s per step")
+    step_s = n_gdn * tg + n_attn * ta + thr * tc["vocab"] / rows + tp
+    return dict(value=M / step_s, unit="tok/s", cores=th, kind="port",
+                sample=f"{all_iters[('port', th)][M]} x (one GDN layer {tg:.3f} s, one attention layer {ta:.3f} s, "
+                       f"{rows} of {tc['vocab']} lm_head rows {thr:.3f} s, the PLE block {tp:.3f} s) of the verify "
+                       f"step (M={M}) through the C oracle on {th} threads, scaled to {n_gdn} GDN + {n_attn} "
+                       f"attention layers and the whole lm_head: {step_s:.2f} s per step")
 
 
-def cpu_baseline_e2e(target, state, lc, tc, kinds, k, tokens_per_round, shortlist_rows):
-    """CPU baseline of MTP speculative decode at draft depth k: one round = k draft steps + a verify
-    of k+1 tokens.  A draft step is timed as one attention layer with its mixers and MoE at one
-    token (the head's body) plus the shortlist GEMV (lm_head rows scaled to the shortlist); the
-    verify as in cpu_baseline_full at M = k+1.  tok/s = committed tokens per round / round time."""
-    times, rows, iters = cpu_layer_times(target, state, lc, tc, sorted({1, k + 1}), kinds)
+def cpu_baseline_e2e(target, lc, tc, kinds, k, tokens_per_round, shortlist_rows, T0):
+    """CPU baseline of MTP speculative decode at draft depth k, one round = k draft steps + a verify of
+    k+1 tokens; a draft step = one attention layer with its mixers and MoE at one token + the shortlist
+    GEMV (lm_head rows scaled); the verify = the sampled GDN and attention layers scaled to the stack +
+    lm_head + PLE.  Timed in the oracle's int24 arithmetic (port) on 1 thread and on all host threads,
+    and with MLX's CPU _qmm_t (bf16 accumulation, mlx_cpu) on all host threads (its 1-thread time is
+    one op per stream worker, not run: about threads x longer); the headline entry is the fastest."""
     n_gdn, n_attn = kinds.count(0), kinds.count(1)
-    tg, ta, th, tp = times[k + 1]
-    verify_s = n_gdn * tg + n_attn * ta + th * tc["vocab"] / rows + tp
-    _, ta1, th1, _ = times[1]
-    draft_s = ta1 + th1 * shortlist_rows / rows
-    round_s = k * draft_s + verify_s
-    return dict(value=tokens_per_round / round_s, unit="tok/s", cores=1, kind="port",
-                sample=f"oracle (C, single thread) on sampled layers: verify of {k + 1} tokens = {n_gdn} x GDN "
-                       f"layer {tg:.2f} s + {n_attn} x attention layer {ta:.2f} s + lm_head {th * tc['vocab'] / rows:.2f} s "
-                       f"(from {rows} rows) + PLE block {tp:.2f} s = {verify_s:.1f} s; draft step = attention layer at 1 token {ta1:.2f} s + "
-                       f"{shortlist_rows} shortlist rows {th1 * shortlist_rows / rows:.2f} s = {draft_s:.2f} s; round "
-                       f"= {k} drafts + verify = {round_s:.1f} s for {tokens_per_round:.3f} committed tokens "
-                       f"(expected at the same acceptance rate); iterations per width {iters}")
+    ncpu, nav, model = _cpu_info()
+    th = cpu_threads_all()
+    runs = (("port", 1, 4.0), ("port", th, 4.0), ("mlx_cpu", th, 4.0))
+    t0 = time.perf_counter()
+    all_times, rows, all_iters = cpu_layer_times(target, lc, tc, sorted({1, k + 1}), kinds, T0, runs=runs)
+    entries = []
+    for mode, threads, _ in runs:
+        times = all_times[(mode, threads)]
+        tg, ta, thr, tp = times[k + 1]
+        verify_s = n_gdn * tg + n_attn * ta + thr * tc["vocab"] / rows + tp
+        _, ta1, th1, _ = times[1]
+        draft_s = ta1 + th1 * shortlist_rows / rows
+        round_s = k * draft_s + verify_s
+        entries.append(dict(mode=mode, threads=threads, tok_s=round(tokens_per_round / round_s, 4),
+                            round_s=round(round_s, 3), verify_s=round(verify_s, 3), draft_s=round(draft_s, 4),
+                            iterations={str(m): v for m, v in all_iters[(mode, threads)].items()}))
+    best = max(entries, key=lambda e: e["tok_s"])
+    return dict(value=best["tok_s"], unit="tok/s", cores=best["threads"], kind="port",
+                sample=f"draft depth {k}, {tokens_per_round:.3f} tokens per round (the GPU run's realized rate): "
+                       f"one round = {k} draft steps (an attention layer with mixers and MoE at one token + "
+                       f"{shortlist_rows} shortlist rows) + a verify of {k + 1} tokens ({n_gdn} GDN + {n_attn} "
+                       f"attention layers scaled from one of each, lm_head from 16384 rows, PLE); mode "
+                       f"{best['mode']} on {best['threads']} threads; host: {model}, {ncpu} CPUs "
+                       f"({nav} available to this process); {time.perf_counter() - t0:.0f} s of sampling",
+                modes=entries, cpu_model=model, nproc=ncpu)
 
 
-def run_full(args, out):
-    import torch
+MAXPOS = 2048 + 16  # the indexer budget (2048 positions) plus one verify window
 
-    import mtpx
 
-    M, T0, gs = args.verify_width, args.cached, args.group_size
-    lc, tc = target_cfgs(gs, T0 + 64 + 8 * max(args.rounds, args.steps + args.warmup), args.layers)
-    ctx = mtpx.Context(0)
-    t_init = time.perf_counter()
+def build_model(mtpx, ctx, args, gs):
+    """The random-init target (and MTP head) at group size gs, weights generated on the device."""
+    lc, tc = target_cfgs(gs, MAXPOS, args.layers)
     if args.no_ple:
         tc["ple_layer"] = -1
+    t0 = time.perf_counter()
     target = mtpx.Target(ctx, target_config(mtpx, lc, tc), seed=0x5EED0004)
-    state = mtpx.TargetState(ctx, target)
-    kinds = [target.layer_weights(i).kind for i in range(args.layers)]
-    g = torch.Generator(device="cuda").manual_seed(0x5EED0005)
-    synthetic_prefix(mtpx, ctx, state, lc, tc, kinds, g, T0)
+    head = mtpx.MTPHead(ctx, mtpx.HeadConfig(mtpx.LayerConfig(**lc), tc["hc"], tc["lowrank"], tc["vocab"], 98304,
+                                             248044), seed=0x5EED0007)
+    import torch
     torch.cuda.synchronize()
-    init_s = time.perf_counter() - t_init
-    print(f"bench: {args.layers}-layer target initialised in {init_s:.1f} s", file=sys.stderr, flush=True)
-    ids = torch.randint(0, tc["vocab"], (M,), device="cuda", generator=g, dtype=torch.int32)
-    H, V, hc = lc["hidden"], tc["vocab"], tc["hc"]
+    log(f"gs{gs} model ({args.layers} layers, PLE layer {tc['ple_layer']}) initialised in "
+        f"{time.perf_counter() - t0:.1f} s")
+    return target, head, lc, tc
+
+
+def log(msg):
+    print(f"bench: {msg}", file=sys.stderr, flush=True)
+
+
+def prompt_ids(args, vocab):
+    import torch
+    g = torch.Generator().manual_seed(0x5EED0005)
+    return torch.randint(0, vocab, (args.prompt,), generator=g, dtype=torch.int32).cuda()
+
+
+def generate(session, first, k, gen):
+    """Rounds of depth k (the depth shrinks at the end so exactly `gen` tokens are emitted,
+    counting the prefill's first token).  -> (tokens, per-round seconds, accepted per round)."""
+    toks, times, acc = [first], [], []
+    while len(toks) < gen:
+        d = min(k, gen - len(toks) - 1)
+        t0 = time.perf_counter()
+        got = session.round(d)
+        times.append(time.perf_counter() - t0)
+        acc.append(len(got) - 1)
+        toks += got
+    return toks[:gen], times, acc
+
+
+def verify_measure(args, ctx, target, state, lc, tc, kinds, first, M, steps, warmup, profile):
+    """Config 4: a verify of M tokens (the carry + M-1 ids) over the committed prompt; the window
+    is left open and discarded by the next verify."""
+    import torch
+    V, W = tc["vocab"], tc["hc"] * lc["hidden"]
+    g = torch.Generator().manual_seed(0x5EED0006 + M)
+    ids = torch.randint(0, V, (M,), generator=g, dtype=torch.int32)
+    ids[0] = first
+    ids = ids.cuda()
     logits = torch.empty(M, V, dtype=torch.bfloat16, device="cuda")
-    multi = torch.empty(M, hc * H, dtype=torch.bfloat16, device="cuda")
-
-    def step():
+    multi = torch.empty(M, W, dtype=torch.bfloat16, device="cuda")
+    for _ in range(warmup):
         target.verify(state, ids, logits, multi)
-
-    for _ in range(args.warmup):
-        step()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
+    for _ in range(steps):
+        target.verify(state, ids, logits, multi)
     torch.cuda.synchronize()
-    ms_per_step = (time.perf_counter() - t0) * 1e3 / args.steps
-    ctx.profile(True)
-    ctx.profile_reset()
-    for _ in range(args.steps):
-        step()
-    stats = ctx.profile_stats()
-    ctx.profile(False)
-    uniq = state.moe_unique(args.layers)
-    print(f"bench: {ms_per_step:.3f} ms per verify step", file=sys.stderr, flush=True)
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    stats = None
+    if profile:
+        ctx.profile(True)
+        ctx.profile_reset()
+        for _ in range(steps):
+            target.verify(state, ids, logits, multi)
+        stats = ctx.profile_stats()
+        ctx.profile(False)
+    return ms, stats
 
-    F, E, K = lc["expert_width"], lc["experts"], lc["top_k"]
-    gu_bytes = [(u + 1) * 2 * qbytes(F, H, gs) for u in uniq]
+
+def step_bytes_of(lc, tc, kinds, uniq, M, T0, gs):
+    """Algorithmic HBM bytes of one verify of M tokens after T0 positions."""
+    H, V, hc = lc["hidden"], tc["vocab"], tc["hc"]
+    F, E = lc["expert_width"], lc["experts"]
     moe_bytes = sum((u + 1) * (2 * qbytes(F, H, gs) + qbytes(H, F, gs)) + 2 * E * H + 2 * H for u in uniq)
     hd = lc["heads"] * lc["head_dim"]
     qkv_rows = 2 * hd + 2 * lc["kv_heads"] * lc["head_dim"] + lc["index_dim"]
@@ -337,22 +429,122 @@ def run_full(args, out):
                            lc["head_dim"])
     gdn_bytes = n_gdn * (qbytes(pw, H, gs) + qbytes(H, tc["value_heads"] * 128, gs) +
                          2 * 4 * tc["value_heads"] * 128 * 128)
-    hc_bytes = args.layers * 2 * (mixer + qbytes(hc, W, gs)) + mixer
+    hc_bytes = len(kinds) * 2 * (mixer + qbytes(hc, W, gs)) + mixer
     ple_bytes = 0
     if tc["ple_layer"] >= 0:  # key and value projections + 16 table rows of 100 bytes per token
         pc = tc["ple"]
         ple_bytes = qbytes(W, pc["embed_dim"], gs) + qbytes(H, pc["embed_dim"], gs) + M * 16 * 100
-    step_bytes = (moe_bytes + attn_bytes + gdn_bytes + hc_bytes + ple_bytes + qbytes(V, H, gs) +
-                  M * qbytes(1, H, gs))
+    total = moe_bytes + attn_bytes + gdn_bytes + hc_bytes + ple_bytes + qbytes(V, H, gs) + M * qbytes(1, H, gs)
+    return total, moe_bytes
+
+
+def serial_token_bytes(lc, tc, gs):
+    """Active weight bytes of one serial decode token (gs64 3.823 GB): every dense matrix, the
+    router, top-k + shared experts, the PLE projections, lm_head; caches excluded."""
+    H, hc, W, LW = lc["hidden"], tc["hc"], tc["hc"] * lc["hidden"], tc["lowrank"]
+    F, E, K = lc["expert_width"], lc["experts"], lc["top_k"]
+    n = tc["num_layers"]
+    n_attn = n // tc["full_attention_interval"]
+    hd = lc["heads"] * lc["head_dim"]
+    qkv_rows = 2 * hd + 2 * lc["kv_heads"] * lc["head_dim"] + lc["index_dim"]
+    cd = (2 * tc["key_heads"] + tc["value_heads"]) * 128
+    pw = cd + tc["value_heads"] * 128 + 2 * tc["value_heads"]
+    mixer = qbytes(LW, W, gs) + qbytes(W, LW, gs)
+    b = n * ((K + 1) * (2 * qbytes(F, H, gs) + qbytes(H, F, gs)) + 2 * E * H + 2 * H)
+    b += n_attn * (qbytes(qkv_rows, H, gs) + qbytes(H, hd, gs))
+    b += (n - n_attn) * (qbytes(pw, H, gs) + qbytes(H, tc["value_heads"] * 128, gs))
+    b += n * 2 * (mixer + qbytes(hc, W, gs)) + mixer + qbytes(tc["vocab"], H, gs)
+    if tc["ple_layer"] >= 0:
+        b += qbytes(W, tc["ple"]["embed_dim"], gs) + qbytes(H, tc["ple"]["embed_dim"], gs)
+    return b
+
+
+def decode_sweep(args, mtpx, ctx, target, head, lc, tc, depths, gs):
+    """Config 5 at group size gs: the prompt, a serial greedy decode of --gen tokens (the teacher of the
+    forcing hook and the reference sequence), then speculative decode at each depth with forced acceptance
+    at rate p; every depth must emit the serial sequence exactly."""
+    import numpy as np
+    import torch
+
+    V = tc["vocab"]
+    prompt = prompt_ids(args, V)
+    sess = mtpx.Session(ctx, target, head)
+    t0 = time.perf_counter()
+    first = sess.prefill(prompt)
+    prefill_s = time.perf_counter() - t0
+    log(f"gs{gs} prefill of {args.prompt} tokens: {prefill_s * 1e3:.1f} ms")
+    ref, st, _ = generate(sess, first, 0, args.gen)
+    serial = dict(tok_s=round((args.gen - 1) / sum(st), 2), ms_per_token_median=round(1e3 * float(np.median(st)), 3),
+                  tokens=args.gen - 1)
+    log(f"gs{gs} serial decode: {serial}")
+    teacher = torch.zeros(MAXPOS, dtype=torch.int32)
+    teacher[:args.prompt] = prompt.cpu()
+    teacher[args.prompt:args.prompt + args.gen] = torch.tensor(ref, dtype=torch.int32)
+    teacher = teacher.cuda()
+    p = args.accept_rate
+    res = {}
+    for k in depths:
+        sess.reset()
+        f2 = sess.prefill(prompt)
+        sess.set_force(teacher, p, 0x5EED0009)
+        toks, times, acc = generate(sess, f2, k, args.gen)
+        same = toks == ref
+        full = [t for t, a in zip(times, acc)]
+        r = dict(tok_s=round((args.gen - 1) / sum(times), 2), rounds=len(times),
+                 ms_per_round_median=round(1e3 * float(np.median(full)), 3),
+                 ms_per_round_mean=round(1e3 * sum(times) / len(times), 3),
+                 mean_accepted=round(float(np.mean(acc)), 3),
+                 tokens_per_round=round((args.gen - 1) / len(times), 3),
+                 expected_tokens_per_round=round(sum(p ** i for i in range(k + 1)), 4),
+                 greedy_identical_to_serial=bool(same))
+        log(f"gs{gs} depth {k}: {r}")
+        if not same:
+            raise SystemExit(f"speculative decode at depth {k} emitted another sequence than the serial decode")
+        res[k] = r
+    sess.set_force(None, 0.0, 0)
+    return sess, first, prompt, serial, res, prefill_s
+
+
+def run_full(args, out):
+    import numpy as np
+    import torch
+
+    import mtpx
+
+    gs = args.group_size
+    ctx = mtpx.Context(0)
+    target, head, lc, tc = build_model(mtpx, ctx, args, gs)
+    kinds = [target.layer_weights(i).kind for i in range(args.layers)]
+    n_attn, n_gdn = kinds.count(1), kinds.count(0)
+
+    # ---- config 4: verify of M tokens after the real 1024-token prompt
+    sess = mtpx.Session(ctx, target, head)
+    prompt = prompt_ids(args, tc["vocab"])
+    first = sess.prefill(prompt)
+    T0 = sess.offset()
+    st = sess.state()
+    M = args.verify_width
+    ms_per_step, stats = verify_measure(args, ctx, target, st, lc, tc, kinds, first, M, args.steps, args.warmup, True)
+    uniq = st.moe_unique(args.layers)
+    widths = {}
+    for w in range(1, 7):
+        widths[w] = round(verify_measure(args, ctx, target, st, lc, tc, kinds, first, w, 10, 2, False)[0], 4)
+    log(f"verify of {M} tokens: {ms_per_step:.3f} ms; by width {widths}")
+    sess.close()
+    H, F = lc["hidden"], lc["expert_width"]
+    gu_bytes = [(u + 1) * 2 * qbytes(F, H, gs) for u in uniq]
+    step_bytes, moe_bytes = step_bytes_of(lc, tc, kinds, uniq, M, T0, gs)
     kernels = {k: dict(launches=n, avg_us=round(1e3 * ms / n, 3)) for k, (n, ms) in stats.items()}
     gu_s = stats["moe_gate_up"][1] / stats["moe_gate_up"][0] / 1e3
     gu_avg = sum(gu_bytes) / len(gu_bytes)
     achieved = gu_avg / gu_s / 1e9
     verify = {
         "what": f"BASELINE config 4: full-depth verify forward ({args.layers} layers: {n_gdn} GDN + {n_attn} "
-                f"attention) of {M} tokens after a committed prefix of {T0} positions; value = verified "
-                f"positions/s; {args.steps} timed steps after {args.warmup} warmup",
+                f"attention) of {M} tokens after the {T0}-token random prompt (processed by the same verify "
+                f"path in windows of 8); value = verified positions/s; {args.steps} timed steps after "
+                f"{args.warmup} warmup",
         "value": round(M / (ms_per_step / 1e3), 2), "unit": "positions/s", "ms_per_step": round(ms_per_step, 4),
+        "ms_by_width": widths,
         "step_bytes": step_bytes, "step_GBps": round(step_bytes / (ms_per_step / 1e3) / 1e9, 1),
         "decode_roofline_frac": round(step_bytes / (ms_per_step / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
         "moe": {"distinct_experts_per_layer": uniq, "bytes_per_step": moe_bytes},
@@ -366,140 +558,90 @@ def run_full(args, out):
         "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
         "algorithmic_bytes": round(gu_avg), "avg_us": round(gu_s * 1e6, 3),
     }
-    tr = traffic_record(gs, M, T0, "full")
+    tr = traffic_record(gs, M, 1024, "full")
     if tr is not None:
         out["roofline"]["traffic"] = tr["gate_up_bytes_per_launch"]
         out["roofline"]["traffic_source"] = tr["source"]
     if args.copy_calibration:
         copy_calibration()
-    base_cfg = {"prefix_positions": T0, "layers": args.layers, "group_size": gs, "parallelism": "none (1 GPU)",
+    base_cfg = {"prompt_tokens": args.prompt, "layers": args.layers, "group_size": gs, "parallelism": "none (1 GPU)",
                 "ple_layer": tc["ple_layer"]}
     ple_note = ("the PLE n-gram block on layer 1 with the full 320,001,446-row table resident"
                 if tc["ple_layer"] >= 0 else "the PLE block of layer 1 left out (--no-ple)")
     if args.no_e2e:
         out.update({
             "value": verify["value"], "unit": "tok/s", "ms_per_step": verify["ms_per_step"],
-            "config": dict(base_cfg, workload=verify["what"] + " (" + ple_note + "; prefix synthetic: random K/V "
-                                                               "rows, GDN and PLE states)",
-                           verify_width=M),
+            "config": dict(base_cfg, workload=verify["what"] + " (" + ple_note + ")", verify_width=M),
             "verify": verify,
         })
         if not args.no_cpu_baseline:
-            out["cpu_baseline"] = cpu_baseline_full(target, state, lc, tc, M, kinds)
+            out["cpu_baseline"] = cpu_baseline_full(target, lc, tc, M, kinds, T0)
         return out
-    state.close()
-    e2e = E2E(args, ctx, target, lc, tc, kinds)
-    sweep = {k: e2e.run(k, args.rounds, min(4, args.rounds)) for k in args.depths}
+
+    # ---- config 5: 1024-token prompt + 1024 generated tokens, depths swept, forced acceptance at p
+    sess, first, prompt, serial, sweep, prefill_s = decode_sweep(args, mtpx, ctx, target, head, lc, tc, args.depths, gs)
     best = max(sweep, key=lambda d: sweep[d]["tok_s"])
-    final = e2e.run(best, args.steps, args.warmup)
-    e2e.close()
+    fin = sweep[best]
+    tok_bytes = serial_token_bytes(lc, tc, gs)
+    draft_ms = {k: round((r["ms_per_round_median"] - widths[k + 1]) / k, 4) for k, r in sweep.items() if k + 1 in widths}
+    sess.close()
+    gs32 = None
+    if args.gs32_line and gs != 32:
+        target.close()
+        head.close()
+        torch.cuda.synchronize()
+        t32, h32, lc32, tc32 = build_model(mtpx, ctx, args, 32)
+        s32, _, _, serial32, sw32, pf32 = decode_sweep(args, mtpx, ctx, t32, h32, lc32, tc32, [best], 32)
+        r32 = sw32[best]
+        b32 = serial_token_bytes(lc32, tc32, 32)
+        gs32 = dict(r32, draft_depth=best, serial_tok_s=serial32["tok_s"], prefill_ms=round(pf32 * 1e3, 1),
+                    bytes_per_serial_token=b32,
+                    roofline_frac=round(r32["tok_s"] * b32 / 1e9 / HBM_PEAK_GBS, 4))
+        s32.close()
+        t32.close()
+        h32.close()
+        target = None
     out.update({
-        "value": final["tok_s"],
-        "ms_per_step": final["ms_per_round"],
+        "value": fin["tok_s"],
+        "ms_per_step": fin["ms_per_round_mean"],
+        "steps": fin["rounds"],
+        "warmup": 0,
         "config": dict(base_cfg, workload=(
             f"BASELINE config 5: single-stream MTP speculative decode on the full-depth random-init 125B-A6B "
             f"target ({args.layers} layers: {n_gdn} GDN + {n_attn} attention, hyper-connection mixers, 512-expert "
             f"top-10 + shared MoE, hidden 2560, vocab 248320, gs{gs}, weights resident in HBM) with the MTP head "
-            f"(attention + MoE, 98584-row shortlist), after a synthetic committed prefix of {T0} positions "
-            f"(random K/V rows, GDN and PLE states; {ple_note}). A step = one "
-            f"round: {best} drafter steps, a verify of {best + 1} tokens, the on-device greedy accept (read back "
-            f"once per round), target commit and drafter finalize; acceptance forced at p={args.accept_rate} by a "
-            f"seeded draw. Draft depth {best} = the best of the sweep {list(args.depths)} ({args.rounds} rounds "
-            f"each); value = expected committed tokens per round at p (1 + p + ... + p^k) / measured time per "
-            f"round over the {args.steps} timed rounds (realized_tok_s: the seeded draws' own count)"),
-            draft_depth=best, accept_rate=args.accept_rate, expected_tokens_per_round=final["expected_tokens_per_round"],
-            realized_tok_s=final["realized_tok_s"], mean_accepted=final["mean_accepted"], tokens=final["tokens"]),
-        "depth_sweep": {str(d): r for d, r in sweep.items()},
+            f"(attention + MoE, 98584-row shortlist; {ple_note}). A {args.prompt}-token random prompt is processed "
+            f"(verify windows of 8), then {args.gen} tokens are generated greedily: the step is one round (k "
+            f"drafter steps, a verify of k+1 tokens, the on-device greedy accept read back once, target commit, "
+            f"drafter finalize). Acceptance is forced at p={args.accept_rate}: each drafted position takes the "
+            f"serial greedy sequence's token with probability p (seeded per position); every depth emits "
+            f"exactly the serial sequence. Draft depth {best} = the best of {list(args.depths)}; value = "
+            f"realized tokens/s of the {args.gen - 1} round-generated tokens over all {fin['rounds']} rounds "
+            f"(steps = rounds; ms_per_step = mean round)"),
+            draft_depth=best, accept_rate=args.accept_rate, generated_tokens=args.gen,
+            mean_accepted=fin["mean_accepted"], tokens_per_round=fin["tokens_per_round"],
+            expected_tokens_per_round=fin["expected_tokens_per_round"],
+            ms_per_round_median=fin["ms_per_round_median"]),
+        "decode": {
+            "depth_sweep": {str(d): r for d, r in sweep.items()},
+            "serial_decode": serial,
+            "prefill_ms": round(prefill_s * 1e3, 1),
+            "draft_step_ms_by_depth": draft_ms,
+            "bytes_per_serial_token": tok_bytes,
+            "roofline_frac": round(fin["tok_s"] * tok_bytes / 1e9 / HBM_PEAK_GBS, 4),
+            "gs32": gs32,
+        },
         "verify": verify,
     })
-    if not args.no_cpu_baseline:
-        state = mtpx.TargetState(ctx, target)
-        state.set_offset(T0)
-        out["cpu_baseline"] = cpu_baseline_e2e(target, state, lc, tc, kinds, best,
-                                               final["expected_tokens_per_round"], 98304 + 276)
+    if not args.no_cpu_baseline and target is not None:
+        out["cpu_baseline"] = cpu_baseline_e2e(target, lc, tc, kinds, best, fin["tokens_per_round"], 98304 + 276,
+                                               T0)
+    elif not args.no_cpu_baseline:
+        t2, h2, lc2, tc2 = build_model(mtpx, ctx, args, gs)
+        out["cpu_baseline"] = cpu_baseline_e2e(t2, lc2, tc2, kinds, best, fin["tokens_per_round"], 98304 + 276, T0)
+        t2.close()
+        h2.close()
     return out
-
-
-class E2E:
-    """BASELINE config 5 on `target`: rounds of single-stream MTP speculative decode -- k drafter
-    steps, a verify of the carry + k drafts, the on-device greedy accept (its result read back once
-    per round), the target commit and the drafter finalize.  Random-init drafts almost never match
-    the target, so the accepted count is forced at rate p by a seeded draw (the accept kernel still
-    runs); the carried token is the target's argmax at the forced position."""
-
-    def __init__(self, args, ctx, target, lc, tc, kinds):
-        import mtpx
-
-        self.args, self.ctx, self.target, self.lc, self.tc, self.kinds = args, ctx, target, lc, tc, kinds
-        self.head = mtpx.MTPHead(ctx, mtpx.HeadConfig(mtpx.LayerConfig(**dict(lc, max_positions=64 + 16 * max(
-            args.rounds, args.steps + args.warmup))), tc["hc"], tc["lowrank"], tc["vocab"], 98304, 248044),
-            seed=0x5EED0007)
-
-    def close(self):
-        self.head.close()
-
-    def run(self, k, rounds, warmup):
-        import numpy as np
-        import torch
-
-        import mtpx
-
-        args, ctx, target, lc, tc = self.args, self.ctx, self.target, self.lc, self.tc
-        T0, p = args.cached, args.accept_rate
-        V, W = tc["vocab"], tc["hc"] * lc["hidden"]
-        g = torch.Generator(device="cuda").manual_seed(0x5EED0008 + k)
-        state = mtpx.TargetState(ctx, target)
-        synthetic_prefix(mtpx, ctx, state, lc, tc, self.kinds, g, T0)
-        dr = mtpx.Drafter(ctx, self.head)
-        # the last committed chunk of the prompt: 8 tokens and their multi streams
-        dr.observe(torch.randint(0, V, (8,), device="cuda", generator=g, dtype=torch.int32),
-                   torch.randn(8, W, device="cuda", generator=g).to(torch.bfloat16))
-        ids = torch.empty(k + 1, dtype=torch.int32, device="cuda")
-        ids[0] = int(torch.randint(0, V, (1,), generator=torch.Generator().manual_seed(k)).item())
-        carry = torch.randn(1, W, device="cuda", generator=g).to(torch.bfloat16)
-        mo = torch.empty(k, W, dtype=torch.bfloat16, device="cuda")
-        logits = torch.empty(k + 1, V, dtype=torch.bfloat16, device="cuda")
-        multi = torch.empty(k + 1, W, dtype=torch.bfloat16, device="cuda")
-        amax = torch.empty(k + 1, dtype=torch.int32, device="cuda")
-        out3 = torch.empty(3, dtype=torch.int32, device="cuda")
-        rng = np.random.default_rng(0x5EED0009 + k)
-
-        def round_():
-            for i in range(k):
-                dr.step(ids[i:i + 1], carry if i == 0 else mo[i - 1:i], ids[i + 1:i + 2], mo[i:i + 1])
-            target.verify(state, ids, logits, multi)
-            lf = logits.float()
-            off, _ = state.info()
-            ctx.accept_greedy(lf, ids[1:], off, out3)
-            ctx.argmax_rows(lf, amax)
-            out3.cpu()  # the round's one host read
-            n = 0
-            while n < k and rng.random() < p:
-                n += 1
-            state.commit(n + 1)
-            dr.finalize(n + 1, ids[1:n + 1] if n else None, multi[:n] if n else None)
-            ids[0:1].copy_(amax[n:n + 1])
-            carry.copy_(multi[n:n + 1])
-            return n
-
-        for _ in range(warmup):
-            round_()
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        acc = [round_() for _ in range(rounds)]
-        torch.cuda.synchronize()
-        dt = time.perf_counter() - t0
-        toks = sum(a + 1 for a in acc)
-        # committed tokens per round at acceptance rate p: 1 + p + p^2 + ... + p^k (every round does the
-        # same work whatever the draw; the draws only decide what is committed)
-        expect = sum(p ** i for i in range(k + 1))
-        res = dict(tok_s=round(expect * rounds / dt, 2), ms_per_round=round(dt * 1e3 / rounds, 3),
-                   expected_tokens_per_round=round(expect, 4), realized_tok_s=round(toks / dt, 2),
-                   mean_accepted=round(sum(acc) / len(acc), 3), tokens=toks, rounds=rounds)
-        print(f"bench: depth {k}: {res}", file=sys.stderr, flush=True)
-        dr.close()
-        state.close()
-        return res
 
 
 def copy_calibration():
@@ -612,7 +754,10 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", choices=("full", "layer"), default="full")
     ap.add_argument("--depths", type=int, nargs="+", default=[1, 2, 3, 4, 5], help="draft depths of the decode sweep")
-    ap.add_argument("--rounds", type=int, default=48, help="rounds per depth of the decode sweep")
+    ap.add_argument("--prompt", type=int, default=1024, help="prompt tokens (config 4 and 5)")
+    ap.add_argument("--gen", type=int, default=1024, help="generated tokens per decode run (config 5)")
+    ap.add_argument("--no-gs32", dest="gs32_line", action="store_false",
+                    help="skip the gs32 (checkpoint format) decode line at the best depth")
     ap.add_argument("--accept-rate", type=float, default=0.7)
     ap.add_argument("--layers", type=int, default=48, help="depth of the full workload")
     ap.add_argument("--verify-width", type=int, default=4)

@@ -185,6 +185,18 @@ int mtpx_argmax_rows(mtpx_ctx ctx, const float* x, int rows, int64_t V, int32_t*
 int mtpx_accept_greedy(mtpx_ctx ctx, const float* logits, int k, int64_t V,
                        const int32_t* drafts, int32_t kv_offset, int32_t* out3);
 
+/* The same decision on bf16 logits (the verify's output), with optional device outputs:
+ * argmax_out int32 [k+1] (every row's argmax) and tokens_out int32 [k+1] (the committed
+ * tokens: drafts[0..n-1], then the bonus), so a round needs no second argmax and no f32 copy. */
+int mtpx_accept_greedy_bf16(mtpx_ctx ctx, const uint16_t* logits, int k, int64_t V, const int32_t* drafts,
+                            int32_t kv_offset, int32_t* out3, int32_t* argmax_out, int32_t* tokens_out);
+
+/* Benchmark forcing hook (the MTP head's output forced to the target's at rate
+ * p through a seeded mask).  With probability p -- Philox4x32-10, key = seed, counter =
+ * {pos lo, pos hi, 0x46524345, 0}, so the decision belongs to the position -- *token =
+ * teacher[pos] (device int32).  No reference counterpart: a test hook on the drafter output. */
+int mtpx_force_draft(mtpx_ctx ctx, int32_t* token, const int32_t* teacher, int64_t pos, float p, uint64_t seed);
+
 /* ---- a22: temperature rejection sampling (no reference counterpart) ----------
  * tlogits f32 [k+1, V], dlogits f32 [k, V] (row i proposed drafts[i]);
  * Philox4x32-10 key = seed, counter = {offset lo, offset hi, i, 0}. */
@@ -534,6 +546,40 @@ int mtpx_target_commit(mtpx_target_state st, int n);
 /* Distinct routed experts of each layer's MoE in the last verify (host int32 [num_layers];
  * synchronises), for the algorithmic byte count of the expert GEMVs. */
 int mtpx_target_moe_unique(mtpx_ctx ctx, mtpx_target_state st, int32_t* out);
+
+/* ---- the speculative round, device-resident (SURVEY's mtpx_round) ---------------------------
+ * A session = one request: the target's caches, the drafter's request state and the carry (the
+ * next input token with the target multi stream of the position before it).  mtpx_round runs
+ * k drafter steps, the verify of the carry + k drafts, the greedy accept on the device, ONE
+ * readback of its integers (accepted count, bonus, committed tokens), the target commit of
+ * n + 1 positions, the drafter finalize with the target's own multi streams, and moves the
+ * carry on the device.  k = 0 is a serial decode step.  Replaces the engine core's accept loop
+ * (docs/qwen38-125b-a6b-port-notes.md:313-343, the un-vendored mlx-swift-lm) around
+ * CBv2MTPRequestStatefulDrafter (Runner/Qwen4ExpMTPDrafter.swift:328-454) and
+ * cbv2ForwardWithHiddenCaptured (Runner/FastModel/TrackFastModel.swift:1463-1475). */
+typedef struct mtpx_session_ { void* ctx; } mtpx_session;
+
+typedef struct {
+  const int32_t* teacher;  /* device int32 [teacher_len]: the token at each absolute position; NULL: no forcing */
+  int64_t teacher_len;
+  float rate;              /* forcing probability per position */
+  uint64_t seed;
+} mtpx_force_params;
+
+/* head may be {NULL}: serial decode only (k = 0). */
+int mtpx_session_new(mtpx_ctx ctx, mtpx_target target, mtpx_head head, mtpx_session* out);
+int mtpx_session_free(mtpx_session s);
+/* Back to an empty request (caches reset, a fresh drafter state). */
+int mtpx_session_reset(mtpx_session s);
+/* The prompt (device int32 [n], offset + n <= MTPX_INDEXER_BUDGET): verify windows of <= 8
+ * tokens, each committed and observed by the drafter; *first_token (host) = the argmax of the
+ * last position, which becomes the carry.  Synchronises once. */
+int mtpx_session_prefill(mtpx_session s, const int32_t* ids, int n, int32_t* first_token);
+/* One round of draft depth k (0..MTPX_MAX_DRAFT_DEPTH); force may be NULL.  tokens (host, k+1
+ * entries) receives the n + 1 committed tokens, *n_tokens = n + 1. */
+int mtpx_round(mtpx_session s, int k, const mtpx_force_params* force, int32_t* tokens, int* n_tokens);
+/* Committed offset; the session's target state and drafter (owned by the session). */
+int mtpx_session_info(mtpx_session s, int64_t* offset, mtpx_target_state* state, mtpx_drafter* drafter);
 
 /* ---- per-kernel timing (replaces TrackFastProfile, Runner/FastModel/TrackFastWeights.swift:81-98) ----
  * With profiling on, every launch the library issues is bracketed by HIP events

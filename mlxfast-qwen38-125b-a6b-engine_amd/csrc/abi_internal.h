@@ -1,0 +1,15 @@
+// Accessors the library's own host modules (round.cpp) use on top of the public C ABI.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include "../../include/mtpx.h"
+
+namespace mtpx {
+hipStream_t ctx_stream(mtpx_ctx ctx);
+int ctx_device(mtpx_ctx ctx);
+// Error text for the next mtpx_last_error() (returns code).
+int set_error(int code, const char* msg);
+// vocab and multi-stream width (hc * hidden) of a target; hc * hidden of a head.
+void target_dims(mtpx_target t, int64_t* vocab, int* width);
+int head_width(mtpx_head h);
+}  // namespace mtpx

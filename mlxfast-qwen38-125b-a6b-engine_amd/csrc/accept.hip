@@ -84,16 +84,21 @@ __global__ void k_argmax_final(const float* __restrict__ pval, const int32_t* __
   if (threadIdx.x == 0) out[row] = ids ? ids[i] : i;
 }
 
-// one workgroup: wave r reduces row r, then thread 0 decides.
+// one workgroup: wave r reduces row r, then thread 0 decides.  Optional outputs: amax [k+1]
+// (every row's argmax) and tokens [k+1] (the committed tokens: drafts[0..n-1], then the bonus).
 __global__ __launch_bounds__(512) void k_accept_greedy(const float* __restrict__ pval,
                                                        const int32_t* __restrict__ pidx, int k, int parts,
                                                        const int32_t* __restrict__ drafts, int32_t kv_offset,
-                                                       int32_t* __restrict__ out3) {
+                                                       int32_t* __restrict__ out3, int32_t* __restrict__ amax,
+                                                       int32_t* __restrict__ tokens) {
   __shared__ int am[MAX_TOKENS];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   if (wave <= k) {
     const VI b = reduce_parts(pval, pidx, parts, wave, lane);
-    if (lane == 0) am[wave] = b.i;
+    if (lane == 0) {
+      am[wave] = b.i;
+      if (amax) amax[wave] = b.i;
+    }
   }
   __syncthreads();
   if (threadIdx.x == 0) {
@@ -102,6 +107,10 @@ __global__ __launch_bounds__(512) void k_accept_greedy(const float* __restrict__
     out3[0] = n;
     out3[1] = am[n];
     out3[2] = kv_offset + n + 1;
+    if (tokens) {
+      for (int i = 0; i < n; ++i) tokens[i] = drafts[i];
+      tokens[n] = am[n];
+    }
   }
 }
 
@@ -124,6 +133,17 @@ __device__ __forceinline__ uint4 philox4x32_10(uint4 c, uint2 k) {
 }
 
 __device__ __forceinline__ float uniform24(uint32_t r) { return (float)(r >> 8) * 5.9604644775390625e-08f; }
+
+// The forcing hook of a benchmark drafter (a test hook, not part of the decode rule): with
+// probability p, decided by Philox4x32-10 with key = seed and counter = {pos lo, pos hi,
+// 0x46524345, 0} (so the decision is a property of the position), *token = teacher[pos].
+__global__ void k_force_draft(int32_t* __restrict__ token, const int32_t* __restrict__ teacher, int64_t pos,
+                              float p, uint64_t seed) {
+  if (threadIdx.x != 0) return;
+  const uint4 r = philox4x32_10(make_uint4((uint32_t)pos, (uint32_t)((uint64_t)pos >> 32), 0x46524345u, 0u),
+                                make_uint2((uint32_t)seed, (uint32_t)(seed >> 32)));
+  if (uniform24(r.x) < p) *token = teacher[pos];
+}
 
 // Work layout (floats): rowmax[2k+1], invZ[2k+1], state[8], csum[(2k+1)*nch], vsum[nch]
 // rows 0..k: verify rows (tlogits); rows k+1..2k: draft rows (dlogits).
@@ -301,14 +321,32 @@ hipError_t launch_argmax_rows_bf16(const bf16* x, int rows, int64_t V, float* pv
   return hipGetLastError();
 }
 
-hipError_t launch_accept_greedy(const float* logits, int k, int64_t V, const int32_t* drafts, int32_t kv_offset,
-                                float* pval, int32_t* pidx, int32_t* out3, hipStream_t st) {
+template <typename T>
+hipError_t accept_greedy_t(const T* logits, int k, int64_t V, const int32_t* drafts, int32_t kv_offset, float* pval,
+                           int32_t* pidx, int32_t* out3, int32_t* amax, int32_t* tokens, hipStream_t st) {
   const int parts = (int)((V + AM_SPAN - 1) / AM_SPAN);
-  hipLaunchKernelGGL(k_argmax_part<float>, dim3(parts, k + 1), dim3(256), 0, st, logits, V, parts, pval, pidx);
+  hipLaunchKernelGGL(k_argmax_part<T>, dim3(parts, k + 1), dim3(256), 0, st, logits, V, parts, pval, pidx);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(k_accept_greedy, dim3(1), dim3(64 * (k + 1)), 0, st, pval, pidx, k, parts, drafts, kv_offset,
-                     out3);
+                     out3, amax, tokens);
+  return hipGetLastError();
+}
+
+hipError_t launch_accept_greedy(const float* logits, int k, int64_t V, const int32_t* drafts, int32_t kv_offset,
+                                float* pval, int32_t* pidx, int32_t* out3, hipStream_t st) {
+  return accept_greedy_t(logits, k, V, drafts, kv_offset, pval, pidx, out3, nullptr, nullptr, st);
+}
+
+hipError_t launch_accept_greedy_bf16(const bf16* logits, int k, int64_t V, const int32_t* drafts, int32_t kv_offset,
+                                     float* pval, int32_t* pidx, int32_t* out3, int32_t* amax, int32_t* tokens,
+                                     hipStream_t st) {
+  return accept_greedy_t(logits, k, V, drafts, kv_offset, pval, pidx, out3, amax, tokens, st);
+}
+
+hipError_t launch_force_draft(int32_t* token, const int32_t* teacher, int64_t pos, float p, uint64_t seed,
+                              hipStream_t st) {
+  hipLaunchKernelGGL(k_force_draft, dim3(1), dim3(64), 0, st, token, teacher, pos, p, seed);
   return hipGetLastError();
 }
 

@@ -14,6 +14,7 @@
 #include <vector>
 
 #include "../../include/mtpx.h"
+#include "abi_internal.h"
 #include "drafter.h"
 #include "mtpx_kernels.h"
 
@@ -1271,6 +1272,21 @@ void target_state_release(TargetState* s) {
 
 }  // namespace
 
+namespace mtpx {
+hipStream_t ctx_stream(mtpx_ctx h) { return C(h)->stream; }
+int ctx_device(mtpx_ctx h) { return C(h)->device; }
+int set_error(int code, const char* msg) { return fail(code, "%s", msg); }
+void target_dims(mtpx_target th, int64_t* vocab, int* width) {
+  const Target* t = static_cast<const Target*>(th.ctx);
+  *vocab = t->cfg.vocab;
+  *width = t->cfg.hc * t->cfg.layer.hidden;
+}
+int head_width(mtpx_head hh) {
+  const Head* hd = static_cast<const Head*>(hh.ctx);
+  return hd->cfg.hc * hd->cfg.layer.hidden;
+}
+}  // namespace mtpx
+
 extern "C" {
 
 const char* mtpx_last_error(void) { return g_err.c_str(); }
@@ -1548,6 +1564,31 @@ int mtpx_accept_greedy(mtpx_ctx h, const float* logits, int k, int64_t V, const 
   float* pv = ws_take<float>(c, n);
   int32_t* pi = ws_take<int32_t>(c, n);
   HIP_OK(launch_accept_greedy(logits, k, V, drafts, kv_offset, pv, pi, out3, c->stream));
+  return MTPX_OK;
+}
+
+int mtpx_accept_greedy_bf16(mtpx_ctx h, const uint16_t* logits, int k, int64_t V, const int32_t* drafts,
+                            int32_t kv_offset, int32_t* out3, int32_t* argmax_out, int32_t* tokens_out) {
+  Ctx* c = C(h);
+  ARG(c && logits && out3 && (k == 0 || drafts), "null argument");
+  ARG(k >= 0 && k + 1 <= MAX_TOKENS && V >= 1 && V < (int64_t)1 << 31, "k=%d V=%lld", k, (long long)V);
+  if (set_device(c)) return MTPX_ERR_HIP;
+  const size_t n = argmax_work_items(k + 1, V);
+  int rc = ws_reserve(c, al(n * 4) * 2 + 256);
+  if (rc) return rc;
+  ws_begin(c);
+  float* pv = ws_take<float>(c, n);
+  int32_t* pi = ws_take<int32_t>(c, n);
+  LAUNCH(c, "accept_greedy", launch_accept_greedy_bf16(reinterpret_cast<const bf16*>(logits), k, V, drafts, kv_offset,
+                                                       pv, pi, out3, argmax_out, tokens_out, c->stream));
+  return MTPX_OK;
+}
+
+int mtpx_force_draft(mtpx_ctx h, int32_t* token, const int32_t* teacher, int64_t pos, float p, uint64_t seed) {
+  Ctx* c = C(h);
+  ARG(c && token && teacher && pos >= 0, "bad argument");
+  if (set_device(c)) return MTPX_ERR_HIP;
+  LAUNCH(c, "force_draft", launch_force_draft(token, teacher, pos, p, seed, c->stream));
   return MTPX_OK;
 }
 

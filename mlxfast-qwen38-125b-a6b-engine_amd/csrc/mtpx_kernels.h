@@ -147,6 +147,12 @@ hipError_t launch_argmax_rows(const float* x, int rows, int64_t V, float* pval, 
 hipError_t launch_accept_greedy(const float* logits, int k, int64_t V, const int32_t* drafts,
                                 int32_t kv_offset, float* pval, int32_t* pidx, int32_t* out3,
                                 hipStream_t st);
+// bf16 logits (the verify's output); amax [k+1] and tokens [k+1] optional (see k_accept_greedy)
+hipError_t launch_accept_greedy_bf16(const bf16* logits, int k, int64_t V, const int32_t* drafts, int32_t kv_offset,
+                                     float* pval, int32_t* pidx, int32_t* out3, int32_t* amax, int32_t* tokens,
+                                     hipStream_t st);
+hipError_t launch_force_draft(int32_t* token, const int32_t* teacher, int64_t pos, float p, uint64_t seed,
+                              hipStream_t st);
 hipError_t launch_accept_sample(const float* tlogits, const float* dlogits, int k, int64_t V,
                                 const int32_t* drafts, float temperature, uint64_t seed, uint64_t offset,
                                 int32_t kv_offset, float* work, int32_t* out3, hipStream_t st);

@@ -11,12 +11,12 @@ from __future__ import annotations
 import ctypes as C
 
 from . import _lib
-from ._lib import (DrafterInfo, GDNConfig, GDNWeights, Handle, HCWeights, HeadConfig, HeadWeights, LayerConfig,
+from ._lib import (DrafterInfo, ForceParams, GDNConfig, GDNWeights, Handle, HCWeights, HeadConfig, HeadWeights, LayerConfig,
                    LayerWeights, MoEWeights, MtpxError, NGramTable, PLEConfig, PLEWeights, Q4, TargetConfig,
                    TargetLayerWeights, TargetWeights, check)
 
 __all__ = ["Context", "KVCache", "DecoderLayer", "MTPHead", "Drafter", "GDN", "GDNState", "PLE", "PLEState", "Target",
-           "TargetState", "MoEWeights", "LayerConfig", "HeadConfig", "GDNConfig", "PLEConfig", "TargetConfig",
+           "TargetState", "Session", "MoEWeights", "LayerConfig", "HeadConfig", "GDNConfig", "PLEConfig", "TargetConfig",
            "MtpxError", "moe_weights_from"]
 
 
@@ -126,6 +126,14 @@ class Context:
         k = drafts.numel()
         check(self.lib.mtpx_accept_greedy(self.h, _ptr(logits), k, logits.shape[1], _ptr(drafts), kv_offset,
                                           _ptr(out3)), "accept_greedy")
+
+    def accept_greedy_bf16(self, logits, drafts, kv_offset, out3, argmax_out=None, tokens_out=None):
+        k = 0 if drafts is None else drafts.numel()
+        check(self.lib.mtpx_accept_greedy_bf16(self.h, _ptr(logits), k, logits.shape[1], _ptr(drafts), kv_offset,
+                                               _ptr(out3), _ptr(argmax_out), _ptr(tokens_out)), "accept_greedy_bf16")
+
+    def force_draft(self, token, teacher, pos, p, seed):
+        check(self.lib.mtpx_force_draft(self.h, _ptr(token), _ptr(teacher), pos, p, seed), "force_draft")
 
     def accept_sample(self, tlogits, dlogits, drafts, temperature, seed, offset, kv_offset, out3):
         k = drafts.numel()
@@ -559,3 +567,60 @@ def moe_weights_from(tensors: dict, H, E, K, F, gs) -> MoEWeights:
         t = tensors.get(name)
         setattr(w, name, t.data_ptr() if t is not None else None)
     return w
+
+
+class Session:
+    """One request's speculative decode (mtpx_session): prefill, then rounds of draft depth k
+    (mtpx_round), each with one host readback; k = 0 is a serial decode step."""
+
+    def __init__(self, ctx: Context, target: Target, head: "MTPHead | None" = None):
+        self.ctx = ctx
+        self.h = Handle()
+        check(ctx.lib.mtpx_session_new(ctx.h, target.h, head.h if head is not None else Handle(), C.byref(self.h)),
+              "session_new")
+        self._tok = (C.c_int32 * 16)()
+        self.force = None
+
+    def close(self):
+        if self.h.ctx:
+            self.ctx.lib.mtpx_session_free(self.h)
+            self.h.ctx = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def reset(self):
+        check(self.ctx.lib.mtpx_session_reset(self.h), "session_reset")
+
+    def prefill(self, ids) -> int:
+        first = C.c_int32()
+        check(self.ctx.lib.mtpx_session_prefill(self.h, _ptr(ids), ids.shape[0], C.byref(first)), "session_prefill")
+        return first.value
+
+    def set_force(self, teacher, rate: float, seed: int):
+        """Forcing hook: each draft becomes teacher[pos] with probability rate (None: off)."""
+        if teacher is None:
+            self.force = None
+            self._teacher = None
+        else:
+            self._teacher = teacher
+            self.force = ForceParams(teacher.data_ptr(), teacher.numel(), rate, seed)
+
+    def round(self, k: int) -> list:
+        n = C.c_int()
+        fp = C.byref(self.force) if self.force is not None else None
+        check(self.ctx.lib.mtpx_round(self.h, k, fp, C.cast(self._tok, C.c_void_p), C.byref(n)), "round")
+        return list(self._tok[:n.value])
+
+    def offset(self) -> int:
+        o = C.c_int64()
+        check(self.ctx.lib.mtpx_session_info(self.h, C.byref(o), None, None), "session_info")
+        return o.value
+
+    def state(self) -> "TargetState":
+        h = Handle()
+        check(self.ctx.lib.mtpx_session_info(self.h, None, C.byref(h), None), "session_info")
+        return _borrowed(TargetState, self.ctx, h)

@@ -63,6 +63,10 @@ class HeadWeights(C.Structure):
                 ("layer", LayerWeights), ("shortlist", Q4), ("shortlist_ids", P), ("shortlist_rows", INT)]
 
 
+class ForceParams(C.Structure):
+    _fields_ = [("teacher", P), ("teacher_len", I64), ("rate", F32), ("seed", U64)]
+
+
 class DrafterInfo(C.Structure):
     _fields_ = [(n, I64) for n in ("cache_offset", "committed_inputs", "staged_inputs", "backlog_inputs",
                                    "round_base_offset", "round_valid_offset")] + [
@@ -140,6 +144,14 @@ _SIGS = {
     "mtpx_argmax_rows": (INT, [Handle, P, INT, I64, P]),
     "mtpx_accept_greedy": (INT, [Handle, P, INT, I64, P, I32, P]),
     "mtpx_accept_sample": (INT, [Handle, P, P, INT, I64, P, F32, U64, U64, I32, P]),
+    "mtpx_accept_greedy_bf16": (INT, [Handle, P, INT, I64, P, I32, P, P, P]),
+    "mtpx_force_draft": (INT, [Handle, P, P, I64, F32, U64]),
+    "mtpx_session_new": (INT, [Handle, Handle, Handle, C.POINTER(Handle)]),
+    "mtpx_session_free": (INT, [Handle]),
+    "mtpx_session_reset": (INT, [Handle]),
+    "mtpx_session_prefill": (INT, [Handle, P, INT, C.POINTER(I32)]),
+    "mtpx_round": (INT, [Handle, INT, C.POINTER(ForceParams), P, C.POINTER(INT)]),
+    "mtpx_session_info": (INT, [Handle, C.POINTER(I64), C.POINTER(Handle), C.POINTER(Handle)]),
     "mtpx_layer_new_random": (INT, [Handle, C.POINTER(LayerConfig), U64, C.POINTER(Handle)]),
     "mtpx_layer_free": (INT, [Handle]),
     "mtpx_layer_weights_get": (INT, [Handle, C.POINTER(LayerWeights)]),

@@ -54,6 +54,7 @@ def test_struct_layouts_match_c_compiler(tmp_path):
         "mtpx_target_config": (_lib.TargetConfig, ["key_heads", "num_layers", "lowrank", "vocab"]),
         "mtpx_target_layer_weights": (_lib.TargetLayerWeights, ["attn", "gdn", "attn_hc", "mlp_hc"]),
         "mtpx_target_weights": (_lib.TargetWeights, ["final_hc", "lm_head"]),
+        "mtpx_force_params": (_lib.ForceParams, ["teacher_len", "rate", "seed"]),
     }
     lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "mtpx.h"', "int main(void) {"]
     for name, (_, fields) in checks.items():

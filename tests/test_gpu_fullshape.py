@@ -127,7 +127,7 @@ def test_head_full_dims_bit_exact(ctx, gs):
     assert hw.shortlist_rows == 98584
     cfg = dict(layer, hc=hc, lowrank=lowrank, vocab=vocab)
     ow = download_head(hw, cfg, lazy=True)
-    assert ow["shortlist_ids"][98303] == 98303 and ow["shortlist_ids"][98304] == 248044
+    assert ow["shortlist_ids"][98307] == 98307 and ow["shortlist_ids"][98308] == 248044
     kv = mtpx.KVCache(ctx, layer["kv_heads"], layer["head_dim"], P)
     HK, D, H = layer["kv_heads"], layer["head_dim"], layer["hidden"]
     r = np.random.default_rng(7 + gs)

@@ -133,6 +133,17 @@ typedef struct {
 int mtpx_moe_forward(mtpx_ctx ctx, const mtpx_moe_weights* w, const uint16_t* x, int M,
                      uint16_t* y, int32_t* idx, float* wts, float* logits, int32_t* n_unique);
 
+/* mtpx_moe_forward without any allocation: no counterpart in the reference.  For callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): the window's workspace (router logits, routing, dispatch table, prepared
+ * activations, expert activations and outputs) lives in a static device scratch array of 2 MiB per
+ * GPU, held until the process ends; windows that need more are refused (MTPX_ERR_ARG).  The
+ * context must exist (mtpx_ctx_new looks the array up).  Same arguments, kernels and bits as
+ * mtpx_moe_forward.  Every call on a GPU shares that GPU's array: calls that overlap on one GPU
+ * (two contexts or streams at once) race. */
+int mtpx_moe_forward_noalloc(mtpx_ctx ctx, const mtpx_moe_weights* w, const uint16_t* x, int M, uint16_t* y,
+                             int32_t* idx, float* wts, float* logits, int32_t* n_unique);
+
 /* ---- a13-a15: attention pieces -----------------------------------------------
  * attn_prep: qkv rows [S, QW] = q(HQ*D) | gate(HQ*D) | k(HK*D) | v(HK*D) | ...
  * -> q [S, HQ, D]; k and v written into the cache (layout [HK, tmax, D]) at

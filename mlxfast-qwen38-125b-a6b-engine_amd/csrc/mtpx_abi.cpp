@@ -55,6 +55,7 @@ struct Ctx {
   bool ws_over = false;              // a take ran past the reservation (see ws_take)
   MoeDispatch* last_disp = nullptr;  // inside the workspace of the last MoE call
   uint32_t* tickets = nullptr;       // MOE_TICKETS counters, zero at rest
+  void* scratch = nullptr;           // this device's MoE scratch array (noalloc.hip), looked up at set-up
   int last_H = 0, last_E = 0, last_F = 0, last_gs = 0;
   // per-kernel timing with events on the launch stream (off by default)
   bool prof = false;
@@ -1312,6 +1313,13 @@ int mtpx_ctx_new(mtpx_ctx* out, int device) {
     delete c;
     return fail(MTPX_ERR_HIP, "ticket allocation failed on device %d", device);
   }
+  const hipError_t se = moe_scratch_address(device, &c->scratch);
+  if (se != hipSuccess) {
+    hipFree(c->tickets);
+    hipStreamDestroy(c->own);
+    delete c;
+    return fail(MTPX_ERR_HIP, "scratch lookup failed on device %d: %s", device, hipGetErrorString(se));
+  }
   out->ctx = c;
   return MTPX_OK;
 }
@@ -1416,6 +1424,34 @@ int mtpx_moe_forward(mtpx_ctx h, const mtpx_moe_weights* w, const uint16_t* x, i
   if ((rc = ws_reserve(c, moe_ws_bytes(w, M)))) return rc;
   ws_begin(c);
   if ((rc = moe_enqueue(c, w, x, M, y, idx, wts, logits))) return rc;
+  if (n_unique) HIP_OK(hipMemcpyAsync(n_unique, &c->last_disp->n_unique, 4, hipMemcpyDeviceToDevice, c->stream));
+  return MTPX_OK;
+}
+
+int mtpx_moe_forward_noalloc(mtpx_ctx h, const mtpx_moe_weights* w, const uint16_t* x, int M, uint16_t* y,
+                             int32_t* idx, float* wts, float* logits, int32_t* n_unique) {
+  Ctx* c = C(h);
+  ARG(c && x && y, "null argument");
+  int rc = moe_check(w, M);
+  if (rc) return rc;
+  const size_t need = moe_ws_bytes(w, M);
+  ARG(need <= moe_scratch_bytes(), "the MoE window needs %zu bytes of scratch; the maximum is %zu", need,
+      moe_scratch_bytes());
+  ARG(c->scratch, "no scratch on device %d", c->device);
+  if (set_device(c)) return MTPX_ERR_HIP;
+  // The same launches as mtpx_moe_forward, with the device scratch standing in for the workspace for
+  // this call (nothing is allocated: the context's own workspace is put back afterwards).  No part of
+  // the scratch has to start at zero: the route writes every dispatch entry the expert kernels read.
+  void* ws0 = c->ws;
+  const size_t sz0 = c->ws_size;
+  c->ws = c->scratch;
+  c->ws_size = moe_scratch_bytes();
+  ws_begin(c);
+  rc = moe_enqueue(c, w, x, M, y, idx, wts, logits);
+  c->ws = ws0;
+  c->ws_size = sz0;
+  c->ws_used = 0;
+  if (rc) return rc;
   if (n_unique) HIP_OK(hipMemcpyAsync(n_unique, &c->last_disp->n_unique, 4, hipMemcpyDeviceToDevice, c->stream));
   return MTPX_OK;
 }

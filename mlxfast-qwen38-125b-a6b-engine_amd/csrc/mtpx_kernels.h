@@ -74,6 +74,10 @@ hipError_t launch_randn_bf16(bf16* out, int64_t n, uint64_t seed, uint32_t tenso
                              hipStream_t st);
 hipError_t launch_fill_bf16(bf16* out, int64_t n, bf16 v, hipStream_t st);
 
+// --- scratch of the allocation-free MoE entry point (noalloc.hip)
+size_t moe_scratch_bytes();
+hipError_t moe_scratch_address(int device, void** ptr);
+
 // --- MoE (moe.hip)
 // Expert-grouped dispatch of one MoE window, indexed by the expert kernels'
 // grid row y: y = 0 the shared expert (expert -1, every token), y = 1..n_unique

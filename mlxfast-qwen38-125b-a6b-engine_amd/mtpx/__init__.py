@@ -95,6 +95,11 @@ class Context:
         check(self.lib.mtpx_moe_forward(self.h, C.byref(w), _ptr(x), M, _ptr(y), _ptr(idx), _ptr(wts),
                                         _ptr(logits), _ptr(n_unique)), "moe_forward")
 
+    def moe_forward_noalloc(self, w: MoEWeights, x, y, idx=None, wts=None, logits=None, n_unique=None):
+        M = x.shape[0]
+        check(self.lib.mtpx_moe_forward_noalloc(self.h, C.byref(w), _ptr(x), M, _ptr(y), _ptr(idx), _ptr(wts),
+                                                _ptr(logits), _ptr(n_unique)), "moe_forward_noalloc")
+
     def attn_prep(self, qkv, HQ, HK, D, rot, qnorm, knorm, eps, cos_t, sin_t, pos0, q, kcache, vcache,
                   tmax=None):
         S, QW = qkv.shape

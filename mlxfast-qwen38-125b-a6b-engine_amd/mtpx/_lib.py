@@ -132,6 +132,7 @@ _SIGS = {
     "mtpx_q4_pack_sb": (INT, [Handle, P, P, I64, INT, INT, P]),
     "mtpx_qmv": (INT, [Handle, P, P, P, P, INT, INT, INT, P, INT, P, P]),
     "mtpx_moe_forward": (INT, [Handle, C.POINTER(MoEWeights), P, INT, P, P, P, P, P]),
+    "mtpx_moe_forward_noalloc": (INT, [Handle, C.POINTER(MoEWeights), P, INT, P, P, P, P, P]),
     "mtpx_attn_prep": (INT, [Handle, P, INT, INT, INT, INT, INT, INT, P, P, F32, P, P, INT, P, P, P, I64]),
     "mtpx_attn_verify": (INT, [Handle, P, INT, INT, INT, INT, P, P, I64, INT, F32, P, INT, INT, P, P]),
     "mtpx_rmsnorm": (INT, [Handle, P, P, INT, INT, P, F32, P, P]),

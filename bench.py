@@ -120,6 +120,37 @@ def target_config(mtpx, lc, tc):
     return cfg
 
 
+def synthetic_prefix(mtpx, ctx, state, lc, tc, kinds, T0):
+    """Random committed state in place of a prompt (--prefix synthetic, for counter runs that need
+    the verify alone): attention K/V rows, GDN conv rows and recurrent states, the PLE block's
+    conv rows and token context."""
+    import torch
+
+    g = torch.Generator(device="cuda").manual_seed(0x5EED0005)
+    for i, kind in enumerate(kinds):
+        if kind == 1:
+            kp, vp, tmax = state.kv(i).buffers()
+            n_kv = lc["kv_heads"] * tmax * lc["head_dim"]
+            for ptr, tensor in ((kp, 2 * i + 1), (vp, 2 * i + 2)):
+                mtpx.check(ctx.lib.mtpx_randn_bf16(ctx.h, C.c_void_p(ptr), n_kv, 0x5EED0006, tensor, 1.0),
+                           "randn kv")
+        else:
+            conv = torch.randn(tc["conv_kernel"] - 1, (2 * tc["key_heads"] + tc["value_heads"]) * 128,
+                               device="cuda", generator=g).to(torch.bfloat16)
+            ssm = torch.randn(tc["value_heads"], 128, 128, device="cuda", generator=g) * 0.05
+            state.gdn(i).load(conv, ssm)
+            torch.cuda.synchronize()
+    if tc["ple_layer"] >= 0:
+        pc = tc["ple"]
+        conv = torch.randn((pc["conv_kernel"] - 1) * pc["ngram_size"], pc["hc"] * pc["hidden"], device="cuda",
+                           generator=g).to(torch.bfloat16)
+        context = torch.randint(0, tc["vocab"], (pc["ngram_size"] - 1,), device="cuda", generator=g,
+                                dtype=torch.int32)
+        state.ple().load(conv, context)
+        torch.cuda.synchronize()
+    state.set_offset(T0)
+
+
 def _mlx_cpu_patch(O):
     """Swap the oracle's q4 GEMV and MoE block for MLX's CPU quantized matmul (_qmm_t with bf16
     accumulation, O.qmm_t_bf16) for the mlx_cpu timing mode; returns the undo function."""
@@ -343,7 +374,7 @@ def cpu_baseline_e2e(target, lc, tc, kinds, k, tokens_per_round, shortlist_rows,
 MAXPOS = 2048 + 16  # the indexer budget (2048 positions) plus one verify window
 
 
-def build_model(mtpx, ctx, args, gs):
+def build_model(mtpx, ctx, args, gs, with_head=True):
     """The random-init target (and MTP head) at group size gs, weights generated on the device."""
     lc, tc = target_cfgs(gs, MAXPOS, args.layers)
     if args.no_ple:
@@ -351,7 +382,7 @@ def build_model(mtpx, ctx, args, gs):
     t0 = time.perf_counter()
     target = mtpx.Target(ctx, target_config(mtpx, lc, tc), seed=0x5EED0004)
     head = mtpx.MTPHead(ctx, mtpx.HeadConfig(mtpx.LayerConfig(**lc), tc["hc"], tc["lowrank"], tc["vocab"], 98304,
-                                             248044), seed=0x5EED0007)
+                                             248044), seed=0x5EED0007) if with_head else None
     import torch
     torch.cuda.synchronize()
     log(f"gs{gs} model ({args.layers} layers, PLE layer {tc['ple_layer']}) initialised in "
@@ -513,16 +544,21 @@ def run_full(args, out):
 
     gs = args.group_size
     ctx = mtpx.Context(0)
-    target, head, lc, tc = build_model(mtpx, ctx, args, gs)
+    target, head, lc, tc = build_model(mtpx, ctx, args, gs, with_head=args.prefix == "prompt")
     kinds = [target.layer_weights(i).kind for i in range(args.layers)]
     n_attn, n_gdn = kinds.count(1), kinds.count(0)
 
     # ---- config 4: verify of M tokens after the real 1024-token prompt
-    sess = mtpx.Session(ctx, target, head)
     prompt = prompt_ids(args, tc["vocab"])
-    first = sess.prefill(prompt)
-    T0 = sess.offset()
-    st = sess.state()
+    if args.prefix == "synthetic":  # the target state alone (no head, no session)
+        sess = st = mtpx.TargetState(ctx, target)
+        synthetic_prefix(mtpx, ctx, st, lc, tc, kinds, args.prompt)
+        first, T0 = int(prompt[-1]), args.prompt
+    else:
+        sess = mtpx.Session(ctx, target, head)
+        first = sess.prefill(prompt)
+        T0 = sess.offset()
+        st = sess.state()
     M = args.verify_width
     ms_per_step, stats = verify_measure(args, ctx, target, st, lc, tc, kinds, first, M, args.steps, args.warmup, True)
     uniq = st.moe_unique(args.layers)
@@ -756,6 +792,9 @@ def main() -> int:
     ap.add_argument("--depths", type=int, nargs="+", default=[1, 2, 3, 4, 5], help="draft depths of the decode sweep")
     ap.add_argument("--prompt", type=int, default=1024, help="prompt tokens (config 4 and 5)")
     ap.add_argument("--gen", type=int, default=1024, help="generated tokens per decode run (config 5)")
+    ap.add_argument("--prefix", choices=("prompt", "synthetic"), default="prompt",
+                    help="config 4's committed state: the prompt through the verify path, or random caches "
+                         "(counter runs of the verify alone; implies --no-e2e)")
     ap.add_argument("--no-gs32", dest="gs32_line", action="store_false",
                     help="skip the gs32 (checkpoint format) decode line at the best depth")
     ap.add_argument("--accept-rate", type=float, default=0.7)
@@ -769,6 +808,8 @@ def main() -> int:
     ap.add_argument("--copy-calibration", action="store_true",
                     help="after the timed steps, copy 256 MiB once (the reference kernel for HBM byte counters)")
     args = ap.parse_args()
+    if args.prefix == "synthetic":
+        args.no_e2e = True
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
                                    "(multi-GPU sharding is a design note, not implemented)"}))
@@ -777,7 +818,7 @@ def main() -> int:
         "metric": METRIC, "value": None, "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": None, "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "q4 weights x bf16 activations, exact int24 dot, f32 combine",
-        "data": "synthetic (seeded random-init weights, random prefix caches and token ids)",
+        "data": "synthetic (seeded random-init weights, seeded random prompt token ids)",
     }
     if args.workload == "full":
         out = run_full(args, out)

@@ -303,6 +303,11 @@ typedef struct {
 } mtpx_head_weights;
 
 int mtpx_head_new_random(mtpx_ctx ctx, const mtpx_head_config* cfg, uint64_t seed, mtpx_head* out);
+/* Adopt a checkpoint's MTP head (adoptMTPHead, Runner/Qwen4ExpRunner.swift:324-342) from caller-owned
+ * device tensors, as mtpx_target_adopt: embed is the target's embed_tokens (the head has none),
+ * shortlist the lm_head rows of shortlist_ids (ascending, shortlist_rows a multiple of 8). */
+int mtpx_head_adopt(mtpx_ctx ctx, const mtpx_head_config* cfg, const mtpx_head_weights* weights, int pack_sb,
+                    mtpx_head* out);
 int mtpx_head_free(mtpx_head head);
 int mtpx_head_weights_get(mtpx_head head, mtpx_head_weights* out);
 /* One head application over S <= 8 inputs at the cache's offset (advances it by S):
@@ -528,6 +533,17 @@ typedef struct {
 } mtpx_target_weights;
 
 int mtpx_target_new_random(mtpx_ctx ctx, const mtpx_target_config* cfg, uint64_t seed, mtpx_target* out);
+/* Adopt caller-owned device weights in the checkpoint's MLX layout (runner adoption,
+ * Runner/Qwen4ExpRunner.swift:135-229: the serving model holds the SAME loaded tensors, no copy):
+ * every q4 matrix and vector is used in place and must outlive the target.  layers [num_layers]
+ * in the config's schedule (a GDN layer's MoE in attn.moe, the PLE layer's block in ple; attention
+ * norms attn_norm/post_norm unused).  The library adds only: packed scale/bias rows when pack_sb != 0
+ * and the caller gave none (else the kernels read the checkpoint's scales/biases), RoPE tables when
+ * rope_cos/rope_sin are NULL (rows max_positions), and the n-gram table's head sizes and offsets,
+ * which follow from the config (the table must hold their sum of rows; the multipliers are the
+ * caller's).  gdn.neg_exp_alog is -exp(A_log) as f32.  A missing tensor: MTPX_ERR_ARG. */
+int mtpx_target_adopt(mtpx_ctx ctx, const mtpx_target_config* cfg, const mtpx_target_weights* weights,
+                      const mtpx_target_layer_weights* layers, int pack_sb, mtpx_target* out);
 int mtpx_target_free(mtpx_target t);
 int mtpx_target_weights_get(mtpx_target t, mtpx_target_weights* out);
 int mtpx_target_layer_weights_get(mtpx_target t, int layer, mtpx_target_layer_weights* out);

@@ -123,6 +123,8 @@ __device__ void route_body(const MoeArgs& a) {
   if (lane == 0 && wave < 2) leadmask[wave] = bal;
   __syncthreads();
   MoeDispatch* d = a.disp;
+  __shared__ int cnt[MAX_TOKENS * MAX_TOPK];
+  __shared__ int pre[MAX_TOKENS * MAX_TOPK];
   if (leader) {
     const uint64_t below = (t & 63) ? (leadmask[t >> 6] & ((~0ull) >> (64 - (t & 63)))) : 0ull;
     const int u = __popcll(below) + (t >= 64 ? __popcll(leadmask[0]) : 0);
@@ -131,14 +133,24 @@ __device__ void route_body(const MoeArgs& a) {
     for (int m = 0; m < M; ++m) count += (tokbits[m][e >> 5] >> (e & 31)) & 1u;
     d->expert[u + 1] = e;
     d->count[u + 1] = count;
+    cnt[u] = count;
   }
   __syncthreads();
   const int n = __popcll(leadmask[0]) + (MK > 64 ? __popcll(leadmask[1]) : 0);
+  if (t == 0) {  // slots of the routed experts before expert u, in dispatch order
+    int acc = M;
+    for (int v = 0; v < n; ++v) {
+      pre[v] = acc;
+      acc += cnt[v];
+    }
+  }
+  __syncthreads();
   if (t < MK) {
     const int u = uid[first[e]];
     int pos = 0;
     for (int m = 0; m < t / K; ++m) pos += (tokbits[m][e >> 5] >> (e & 31)) & 1u;
     d->slot[u + 1][pos] = (int16_t)t;
+    d->order[pre[u] + pos] = (int16_t)t;
     if (t + 1 > n) d->expert[t + 1] = -2;  // grid rows past the routed experts: no work
   }
   if (t == 0) {
@@ -146,7 +158,10 @@ __device__ void route_body(const MoeArgs& a) {
     if (a.nu_out) *a.nu_out = n;
     d->expert[0] = -1;
     d->count[0] = M;
-    for (int m = 0; m < M; ++m) d->slot[0][m] = (int16_t)(MK + m);
+    for (int m = 0; m < M; ++m) {
+      d->slot[0][m] = (int16_t)(MK + m);
+      d->order[m] = (int16_t)(MK + m);
+    }
   }
 }
 
@@ -508,6 +523,132 @@ __global__ __launch_bounds__(DN_THREADS) void k_moe_down(MoeArgs a, const int32_
 }
 
 // ---------------------------------------------------------------------------
+// Expert kernels, one workgroup per (slot, row block) unit: the M*(K+1) slots are walked in
+// the route's dispatch order (the shared expert's M slots, then each selected expert's slots
+// side by side), and workgroup b takes unit (b % 8) * ceil(n/8) + b / 8: every XCD (workgroups
+// go round-robin over the 8 XCDs) walks a contiguous run of units, so the slots of one expert
+// run on one XCD at about the same time and its weight rows come from HBM once, the repeats from
+// that XCD's L2.  Every workgroup does the same work (one token, the same rows), issues its
+// weight loads first (after the one scalar read of its slot), and computes the per-slot
+// kernels' dot products (same lanes, blocks, folds), so the bits are the same.
+constexpr int DD_THREADS = 256;
+
+__device__ __forceinline__ int dd_unit(int n_units) {
+  const int per = (n_units + 7) / 8;
+  return (int)(blockIdx.x % 8) * per + (int)(blockIdx.x / 8);
+}
+
+// gate|up: an item = 32 rows of F (gate and up rows side by side); 4 waves, each 64/L rows per
+// pass, 32 / (4 * 64/L) passes.
+template <int L, int IT, bool PK>
+__global__ __launch_bounds__(DD_THREADS) void k_moe_gate_up_dd(MoeArgs a) {
+  extern __shared__ uint32_t lds[];  // [H/32][XP_DW]: the slot's token
+  constexpr int RW = 64 / L;
+  constexpr int NP = 32 / (4 * RW) > 0 ? 32 / (4 * RW) : 1;
+  static_assert(4 * RW * NP == 32, "four waves cover the 32 rows of an item");
+  const int H = a.H, F = a.F, gs = a.gs, M = a.M, K = a.K;
+  const int nb = H / 32, ng = H / gs, P = sb_row_len(H, gs), nfb = F / 32;
+  const int n_units = M * (K + 1) * nfb;
+  const int w = dd_unit(n_units);
+  if (w >= n_units) return;
+  const int o = w / nfb, f0 = (w % nfb) * 32;
+  const int sl = a.disp->order[o];
+  const bool shared = sl >= M * K;
+  const int m = shared ? sl - M * K : sl / K;
+  const int e = shared ? 0 : a.idx[sl];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int sub = lane % L, grp = lane / L;
+  const uint32_t* gw = shared ? a.sh_gate_w : a.gate_w;
+  const uint32_t* uw = shared ? a.sh_up_w : a.up_w;
+  const uint32_t* gsb = shared ? a.sh_gate_sb : a.gate_sb;
+  const uint32_t* usb = shared ? a.sh_up_sb : a.up_sb;
+  const bf16* gsc = shared ? a.sh_gate_s : a.gate_s;
+  const bf16* gbi = shared ? a.sh_gate_b : a.gate_b;
+  const bf16* usc = shared ? a.sh_up_s : a.up_s;
+  const bf16* ubi = shared ? a.sh_up_b : a.up_b;
+  const size_t rbase = shared ? 0 : (size_t)e * F;
+  QRow<L, IT> G[NP], U[NP];
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    const size_t row = rbase + f0 + (p * 4 + wave) * RW + grp;
+    G[p].template load_as<PK>(gw + row * (H / 8), gsc + row * ng, gbi + row * ng, PK ? gsb + row * P : nullptr, nb, gs,
+                              sub, true);
+    U[p].template load_as<PK>(uw + row * (H / 8), usc + row * ng, ubi + row * ng, PK ? usb + row * P : nullptr, nb, gs,
+                              sub, true);
+  }
+  // the token's prepared activation blocks -> LDS (LDS-direct, one wait)
+  stage16(lds, a.xp_x + (size_t)m * nb * XP_DW, nb * XP_DW);
+  stage_sync();
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    float g, up;
+    dot2<L, IT, false>(G[p], U[p], lds, nb, sub, g, up);
+    g = lane_fold<L>(g);
+    up = lane_fold<L>(up);
+    if (sub == 0)
+      a.act[(size_t)sl * F + f0 + (p * 4 + wave) * RW + grp] = f2bf(silu_bf16(round_bf(g)) * round_bf(up));
+  }
+}
+
+// down: an item = 4 * 2 * 64/L rows of H (two rows per lane group) of one slot; the combine
+// launch folds the slots' outputs.  (Combining in this launch -- agent-scope stores of the
+// outputs, a per-row-block ticket and the last arriver folding the block -- was measured slower:
+// the coherent stores, the wait for them and the serial tail cost more than the combine launch.)
+template <int L>
+constexpr int dd_down_rows() { return 4 * 2 * (64 / L); }
+
+template <int L, int IT, bool PK>
+__global__ __launch_bounds__(DD_THREADS) void k_moe_down_dd(MoeArgs a) {
+  extern __shared__ uint32_t lds[];  // [F/32][XP_DW]
+  constexpr int RW = 64 / L;
+  constexpr int DR = dd_down_rows<L>();
+  const int H = a.H, F = a.F, gs = a.gs, M = a.M, K = a.K;
+  const int nb = F / 32, ng = F / gs, P = sb_row_len(F, gs), nhb = (H + DR - 1) / DR;
+  const int n_units = M * (K + 1) * nhb;
+  const int wu = dd_unit(n_units);
+  if (wu >= n_units) return;
+  const int o = wu / nhb, hb = wu % nhb, h0 = hb * DR;
+  const int sl = a.disp->order[o];
+  const bool shared = sl >= M * K;
+  const int e = shared ? 0 : a.idx[sl];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int sub = lane % L, grp = lane / L;
+  const int hi = h0 + wave * 2 * RW + 2 * grp;  // this lane group's rows hi, hi + 1
+  const bool va = hi < H, vb = hi + 1 < H;
+  const uint32_t* w = shared ? a.sh_down_w : a.down_w;
+  const uint32_t* sb = shared ? a.sh_down_sb : a.down_sb;
+  const bf16* sc = shared ? a.sh_down_s : a.down_s;
+  const bf16* bi = shared ? a.sh_down_b : a.down_b;
+  const size_t base = shared ? 0 : (size_t)e * H;
+  const size_t ra = base + (va ? hi : h0), rb = base + (vb ? hi + 1 : h0);
+  // the slot's bf16 activations first (element q * 256 + t), then the weights
+  constexpr int NA = 8;  // F <= NA * 256
+  bf16 av[NA];
+#pragma unroll
+  for (int q = 0; q < NA; ++q) {
+    const int i = q * DD_THREADS + threadIdx.x;
+    av[q] = i < F ? a.act[(size_t)sl * F + i] : (bf16)0;
+  }
+  asm volatile("" ::: "memory");
+  QRow<L, IT> A, B;
+  A.template load_as<PK>(w + ra * (F / 8), sc + ra * ng, bi + ra * ng, PK ? sb + ra * P : nullptr, nb, gs, sub, va);
+  B.template load_as<PK>(w + rb * (F / 8), sc + rb * ng, bi + rb * ng, PK ? sb + rb * P : nullptr, nb, gs, sub, vb);
+  asm volatile("" ::: "memory");
+#pragma unroll
+  for (int q = 0; q < NA; ++q) {
+    const int blk = (q * DD_THREADS + (int)threadIdx.x) >> 5;  // uniform per 32-lane group
+    if (blk < nb) xprep_lanes_direct(av[q], threadIdx.x & 31, lds + (size_t)blk * XP_DW);
+  }
+  __syncthreads();
+  float x0, x1;
+  dot2<L, IT, false>(A, B, lds, nb, sub, x0, x1);
+  x0 = lane_fold<L>(x0);
+  x1 = lane_fold<L>(x1);
+  if (sub == 0 && va)  // rows hi, hi + 1 (hi even, H a multiple of 8): one 4-byte store of both
+    *reinterpret_cast<uint32_t*>(a.r + (size_t)sl * H + hi) = (uint32_t)f2bf(x0) | ((uint32_t)f2bf(x1) << 16);
+}
+
+// ---------------------------------------------------------------------------
 hipError_t launch_moe_router_route(const MoeArgs& a, hipStream_t st) {
   const int row_wgs = (a.E + 1 + RR_THREADS / 64 - 1) / (RR_THREADS / 64);
   const int prep_wgs = a.xp_ready ? 0 : (a.M * (a.H / 32) + RR_THREADS / 32 - 1) / (RR_THREADS / 32);
@@ -620,6 +761,58 @@ hipError_t launch_moe_combine(const MoeArgs& a, hipStream_t st) {
     case 16: return combine_k<16>(a, st);
     default: return hipErrorInvalidValue;
   }
+}
+
+
+// ---------------------------------------------------------------------------
+// expert-grouped launches: grid = (M*K + 1 dispatch rows) x row blocks
+template <int L, int IT, bool PK>
+static hipError_t gate_up_dd_pk(const MoeArgs& a, hipStream_t st) {
+  if constexpr (32 % (4 * (64 / L)) != 0) {
+    return hipErrorNotSupported;
+  } else {
+    const size_t lds = (size_t)(a.H / 32) * XP_DW * 4;
+    static size_t cur = 0;
+    hipError_t e = ensure_lds(k_moe_gate_up_dd<L, IT, PK>, lds, cur);
+    if (e != hipSuccess) return e;
+    const int units = a.M * (a.K + 1) * (a.F / 32);
+    hipLaunchKernelGGL((k_moe_gate_up_dd<L, IT, PK>), dim3((units + 7) / 8 * 8), dim3(DD_THREADS), lds, st, a);
+    return hipGetLastError();
+  }
+}
+
+template <int L, int IT>
+static hipError_t gate_up_dd_li(const MoeArgs& a, hipStream_t st) {
+  return a.gate_sb ? gate_up_dd_pk<L, IT, true>(a, st) : gate_up_dd_pk<L, IT, false>(a, st);
+}
+
+template <int L, int IT, bool PK>
+static hipError_t down_dd_pk(const MoeArgs& a, hipStream_t st) {
+  constexpr int DR = dd_down_rows<L>();
+  const int nhb = (a.H + DR - 1) / DR;
+  const size_t lds = (size_t)(a.F / 32) * XP_DW * 4;
+  static size_t cur = 0;
+  hipError_t e = ensure_lds(k_moe_down_dd<L, IT, PK>, lds, cur);
+  if (e != hipSuccess) return e;
+  const int units = a.M * (a.K + 1) * nhb;
+  hipLaunchKernelGGL((k_moe_down_dd<L, IT, PK>), dim3((units + 7) / 8 * 8), dim3(DD_THREADS), lds, st, a);
+  return hipGetLastError();
+}
+
+template <int L, int IT>
+static hipError_t down_dd_li(const MoeArgs& a, hipStream_t st) {
+  return a.down_sb ? down_dd_pk<L, IT, true>(a, st) : down_dd_pk<L, IT, false>(a, st);
+}
+
+hipError_t launch_moe_gate_up_dd(const MoeArgs& a, hipStream_t st) {
+  MTPX_QROW_DISPATCH(a.H / 32, gate_up_dd_li, a, st);
+}
+
+hipError_t launch_moe_down_dd(const MoeArgs& a, hipStream_t st) { MTPX_QROW_DISPATCH(a.F / 32, down_dd_li, a, st); }
+
+bool moe_dd_supported(int H, int F, int K) {
+  const int Lg = lanes_for_blocks(H / 32);
+  return 32 % (4 * (64 / Lg)) == 0 && H % 8 == 0 && F <= 8 * DD_THREADS && K >= 1;
 }
 
 }  // namespace mtpx

@@ -213,6 +213,7 @@ size_t moe_ws_bytes(const mtpx_moe_weights* w, int M) {
          al(2 * (size_t)slots * H) + 4096;
 }
 
+
 // Enqueue the MoE block; workspace already reserved.
 int moe_enqueue(Ctx* c, const mtpx_moe_weights* w, const uint16_t* x, int M, uint16_t* y, int32_t* idx,
                 float* wts, float* logits, const uint16_t* resid = nullptr, uint16_t* y2 = nullptr,
@@ -256,6 +257,12 @@ int moe_enqueue(Ctx* c, const mtpx_moe_weights* w, const uint16_t* x, int M, uin
   c->last_F = a.F;
   c->last_gs = a.gs;
   LAUNCH(c, "moe_router_route", launch_moe_router_route(a, c->stream));
+  if (moe_dd_supported(a.H, a.F, a.K)) {  // one workgroup per (slot, row block), slots in dispatch order
+    LAUNCH(c, "moe_gate_up", launch_moe_gate_up_dd(a, c->stream));
+    LAUNCH(c, "moe_down", launch_moe_down_dd(a, c->stream));
+    LAUNCH(c, "moe_combine", launch_moe_combine(a, c->stream));
+    return MTPX_OK;
+  }
   LAUNCH(c, "moe_gate_up", launch_moe_gate_up(a, c->stream));
   LAUNCH(c, "moe_down", launch_moe_down(a, c->stream));
   LAUNCH(c, "moe_combine", launch_moe_combine(a, c->stream));
@@ -373,6 +380,34 @@ void moe_random(RandInit& ri, const mtpx_layer_config* cfg, mtpx_moe_weights* mw
   ri.qmat(H, F, &m.sh_down_w, &m.sh_down_s, &m.sh_down_b, &m.sh_down_sb);
 }
 
+// Rotate-half RoPE tables [max_positions, rot] (bf16): entry d uses theta^(-2*(d mod rot/2)/rot);
+// angles and cos/sin in double.  Synchronises (the host vectors go out of scope).
+bool rope_tables(Ctx* c, const mtpx_layer_config* cfg, std::vector<void*>* allocs, const uint16_t** cos_out,
+                 const uint16_t** sin_out) {
+  const int rot = cfg->rot_dims;
+  std::vector<uint16_t> ct((size_t)cfg->max_positions * rot), st((size_t)cfg->max_positions * rot);
+  for (int64_t p = 0; p < cfg->max_positions; ++p)
+    for (int d = 0; d < rot; ++d) {
+      const int i = d % (rot / 2);
+      const double inv = std::pow((double)cfg->rope_theta, -2.0 * (double)i / (double)rot);
+      const double a = (double)p * inv;
+      ct[(size_t)p * rot + d] = bf16_bits((float)std::cos(a));
+      st[(size_t)p * rot + d] = bf16_bits((float)std::sin(a));
+    }
+  void *dc = nullptr, *ds = nullptr;
+  if (hipMalloc(&dc, ct.size() * 2) != hipSuccess) return false;
+  allocs->push_back(dc);
+  if (hipMalloc(&ds, st.size() * 2) != hipSuccess) return false;
+  allocs->push_back(ds);
+  if (hipMemcpyAsync(dc, ct.data(), ct.size() * 2, hipMemcpyHostToDevice, c->stream) != hipSuccess ||
+      hipMemcpyAsync(ds, st.data(), st.size() * 2, hipMemcpyHostToDevice, c->stream) != hipSuccess ||
+      hipStreamSynchronize(c->stream) != hipSuccess)
+    return false;
+  *cos_out = static_cast<const uint16_t*>(dc);
+  *sin_out = static_cast<const uint16_t*>(ds);
+  return true;
+}
+
 // Attention + MoE weights of one decoder layer (random init), RoPE tables from the host.
 int layer_create(Ctx* c, const mtpx_layer_config* cfg, uint64_t seed, Layer** out) {
   int rc = layer_check(cfg);
@@ -393,25 +428,7 @@ int layer_create(Ctx* c, const mtpx_layer_config* cfg, uint64_t seed, Layer** ou
   ri.qmat(QW, H, &L->w.qkv_w, &L->w.qkv_s, &L->w.qkv_b, &L->w.qkv_sb);
   ri.qmat(H, HQ * D, &L->w.o_w, &L->w.o_s, &L->w.o_b, &L->w.o_sb);
   moe_random(ri, cfg, &L->w.moe);
-  // rotate-half RoPE tables: entry d uses theta^(-2*(d mod rot/2)/rot)
-  const int rot = cfg->rot_dims;
-  std::vector<uint16_t> ct((size_t)cfg->max_positions * rot), st((size_t)cfg->max_positions * rot);
-  for (int64_t p = 0; p < cfg->max_positions; ++p)
-    for (int d = 0; d < rot; ++d) {
-      const int i = d % (rot / 2);
-      const double inv = std::pow((double)cfg->rope_theta, -2.0 * (double)i / (double)rot);
-      const double a = (double)p * inv;
-      ct[(size_t)p * rot + d] = bf16_bits((float)std::cos(a));
-      st[(size_t)p * rot + d] = bf16_bits((float)std::sin(a));
-    }
-  uint16_t* dc = (uint16_t*)ri.alloc(ct.size() * 2);
-  uint16_t* ds = (uint16_t*)ri.alloc(st.size() * 2);
-  if (dc && ds &&
-      (hipMemcpyAsync(dc, ct.data(), ct.size() * 2, hipMemcpyHostToDevice, c->stream) != hipSuccess ||
-       hipMemcpyAsync(ds, st.data(), st.size() * 2, hipMemcpyHostToDevice, c->stream) != hipSuccess))
-    ri.ok = false;
-  L->w.rope_cos = dc;
-  L->w.rope_sin = ds;
+  if (!rope_tables(c, cfg, &L->allocs, &L->w.rope_cos, &L->w.rope_sin)) ri.ok = false;
   if ((rc = ri.finish("layer"))) {
     for (void* p : L->allocs) hipFree(p);
     delete L;
@@ -2064,6 +2081,197 @@ int mtpx_target_new_random(mtpx_ctx h, const mtpx_target_config* cfg, uint64_t s
   return MTPX_OK;
 }
 
+namespace {
+
+// Adoption of caller-owned weights (MLX layout): every q4 matrix and dense vector is used in place;
+// the library adds only packed scale/bias rows (when asked and the caller gave none), RoPE tables
+// (when the caller gave none) and the n-gram table's device hash parameters.
+struct Adopt {
+  Ctx* c;
+  int gs;
+  bool pack;
+  std::vector<void*>* allocs;
+  bool ok = true;
+  std::string missing;
+
+  bool need(const void* p, const char* what) {
+    if (!p && missing.empty()) missing = what;
+    return p != nullptr;
+  }
+  void sb_rows(int64_t rows, int K, const uint16_t* s, const uint16_t* b, const uint32_t** sb) {
+    if (*sb || !pack || !s || !b) return;
+    void* p = nullptr;
+    if (hipMalloc(&p, (size_t)rows * sb_row_len(K, gs) * 4) != hipSuccess) {
+      ok = false;
+      return;
+    }
+    allocs->push_back(p);
+    if (launch_pack_sb(reinterpret_cast<const bf16*>(s), reinterpret_cast<const bf16*>(b), rows, K, gs,
+                       static_cast<uint32_t*>(p), c->stream) != hipSuccess)
+      ok = false;
+    *sb = static_cast<uint32_t*>(p);
+  }
+  void q4(mtpx_q4* q, int64_t rows, int K, const char* what, bool optional = false) {
+    if (optional && !q->w) return;
+    if (need(q->w, what) & need(q->s, what) & need(q->b, what)) sb_rows(rows, K, q->s, q->b, &q->sb);
+  }
+  void moe(mtpx_moe_weights* m, const mtpx_layer_config& lc) {
+    const int H = lc.hidden, E = lc.experts, F = lc.expert_width;
+    m->hidden = H;
+    m->experts = E;
+    m->top_k = lc.top_k;
+    m->expert_width = F;
+    m->group_size = lc.group_size;
+    need(m->router, "moe router");
+    need(m->shared_gate, "moe shared gate");
+    const int nsb = !!m->gate_sb + !!m->up_sb + !!m->down_sb + !!m->sh_gate_sb + !!m->sh_up_sb + !!m->sh_down_sb;
+    if (nsb != 0 && nsb != 6 && missing.empty()) missing = "moe packed scale/bias rows (all six or none)";
+    struct {
+      const uint32_t* w; const uint16_t* s; const uint16_t* b; const uint32_t** sb; int64_t rows; int K;
+    } mats[6] = {{m->gate_w, m->gate_s, m->gate_b, &m->gate_sb, (int64_t)E * F, H},
+                 {m->up_w, m->up_s, m->up_b, &m->up_sb, (int64_t)E * F, H},
+                 {m->down_w, m->down_s, m->down_b, &m->down_sb, (int64_t)E * H, F},
+                 {m->sh_gate_w, m->sh_gate_s, m->sh_gate_b, &m->sh_gate_sb, F, H},
+                 {m->sh_up_w, m->sh_up_s, m->sh_up_b, &m->sh_up_sb, F, H},
+                 {m->sh_down_w, m->sh_down_s, m->sh_down_b, &m->sh_down_sb, H, F}};
+    for (auto& x : mats)
+      if (need(x.w, "moe expert matrix") & need(x.s, "moe expert scales") & need(x.b, "moe expert biases") &&
+          nsb == 0)
+        sb_rows(x.rows, x.K, x.s, x.b, x.sb);
+  }
+  void hc(mtpx_hc_weights* m, int H, int hc_, int LW, bool inject) {
+    const int W = hc_ * H;
+    need(m->norm_scale, "hyper-connection norm scale");
+    q4(&m->down, LW, W, "hyper-connection down");
+    if (inject) q4(&m->inject, hc_, W, "hyper-connection inject");
+    q4(&m->up, W, LW, "hyper-connection up");
+  }
+  int finish(const char* what) {
+    if (!missing.empty()) return fail(MTPX_ERR_ARG, "%s: missing %s", what, missing.c_str());
+    if (!ok || hipStreamSynchronize(c->stream) != hipSuccess) return fail(MTPX_ERR_OOM, "%s: adoption failed", what);
+    return MTPX_OK;
+  }
+};
+
+}  // namespace
+
+int mtpx_target_adopt(mtpx_ctx h, const mtpx_target_config* cfg, const mtpx_target_weights* tw,
+                      const mtpx_target_layer_weights* layers, int pack_sb, mtpx_target* out) {
+  Ctx* c = C(h);
+  ARG(c && cfg && tw && layers && out, "null argument");
+  int rc = target_check(cfg);
+  if (rc) return rc;
+  if (set_device(c)) return MTPX_ERR_HIP;
+  const mtpx_layer_config& lc = cfg->layer;
+  const int H = lc.hidden;
+  for (int i = 0; i < cfg->num_layers; ++i) {
+    const int want = (i + 1) % cfg->full_attention_interval == 0 ? MTPX_LAYER_ATTENTION : MTPX_LAYER_GDN;
+    ARG(layers[i].kind == want, "layer %d: kind %d, the schedule has %d", i, layers[i].kind, want);
+  }
+  Target* t = new Target();
+  t->cfg = *cfg;
+  t->layers.resize(cfg->num_layers);
+  Adopt ad{c, lc.group_size, pack_sb != 0, &t->allocs};
+  t->embed = tw->embed;
+  t->lm_head = tw->lm_head;
+  t->final_hc = tw->final_hc;
+  ad.q4(&t->embed, cfg->vocab, H, "embed");
+  ad.q4(&t->lm_head, cfg->vocab, H, "lm_head");
+  ad.hc(&t->final_hc, H, cfg->hc, cfg->lowrank, false);
+  const mtpx_gdn_config gc = target_gdn_cfg(*cfg);
+  const GdnGeom gg = gdn_geom(gc);
+  for (int i = 0; i < cfg->num_layers; ++i) {
+    TargetLayer& L = t->layers[i];
+    const mtpx_target_layer_weights& in = layers[i];
+    L.kind = in.kind;
+    L.attn_hc = in.attn_hc;
+    L.mlp_hc = in.mlp_hc;
+    ad.hc(&L.attn_hc, H, cfg->hc, cfg->lowrank, true);
+    ad.hc(&L.mlp_hc, H, cfg->hc, cfg->lowrank, true);
+    if (in.kind == MTPX_LAYER_ATTENTION) {
+      L.attn = new Layer();
+      L.attn->cfg = lc;
+      L.attn->w = in.attn;
+      L.attn->QW = 2 * lc.heads * lc.head_dim + 2 * lc.kv_heads * lc.head_dim + lc.index_dim;
+      mtpx_layer_weights& w = L.attn->w;
+      w.qkv_rows = L.attn->QW;
+      ad.need(w.q_norm, "attention q_norm");
+      ad.need(w.k_norm, "attention k_norm");
+      Adopt la{c, lc.group_size, pack_sb != 0, &L.attn->allocs};
+      mtpx_q4 qkv{w.qkv_w, w.qkv_s, w.qkv_b, w.qkv_sb}, o{w.o_w, w.o_s, w.o_b, w.o_sb};
+      la.q4(&qkv, L.attn->QW, H, "attention qkv");
+      la.q4(&o, H, lc.heads * lc.head_dim, "attention o_proj");
+      w.qkv_sb = qkv.sb;
+      w.o_sb = o.sb;
+      la.moe(&w.moe, lc);
+      if ((!w.rope_cos || !w.rope_sin) && !rope_tables(c, &lc, &L.attn->allocs, &w.rope_cos, &w.rope_sin))
+        la.ok = false;
+      if ((rc = la.finish("target attention layer"))) break;
+      L.moe = w.moe;
+    } else {
+      L.gdn = new GdnLayer();
+      L.gdn->cfg = gc;
+      L.gdn->w = in.gdn;
+      mtpx_gdn_weights& g = L.gdn->w;
+      Adopt la{c, lc.group_size, pack_sb != 0, &L.gdn->allocs};
+      la.q4(&g.in_proj, gg.pw, H, "gdn in_proj");
+      la.q4(&g.out_proj, H, gg.hv * 128, "gdn out_proj");
+      la.need(g.conv_w, "gdn conv_w");
+      la.need(g.neg_exp_alog, "gdn neg_exp_alog");
+      la.need(g.dt_bias, "gdn dt_bias");
+      la.need(g.norm_w, "gdn norm_w");
+      L.moe = in.attn.moe;  // a GDN layer's MoE travels in the attention slot
+      la.moe(&L.moe, lc);
+      if ((rc = la.finish("target gdn layer"))) break;
+    }
+  }
+  if (rc == MTPX_OK && cfg->ple_layer >= 0) {
+    t->ple = new PleLayer();
+    t->ple->cfg = cfg->ple;
+    t->ple->w = layers[cfg->ple_layer].ple;
+    mtpx_ple_weights& w = t->ple->w;
+    Adopt la{c, cfg->ple.group_size, pack_sb != 0, &t->ple->allocs};
+    const PleGeom pg = ple_geom(cfg->ple);
+    la.q4(&w.key_proj, pg.W, cfg->ple.embed_dim, "ple key_proj");
+    la.q4(&w.value_proj, H, cfg->ple.embed_dim, "ple value_proj");
+    la.need(w.norm_key, "ple norm_key");
+    la.need(w.norm_query, "ple norm_query");
+    la.need(w.norm_conv, "ple norm_conv");
+    la.need(w.conv_w, "ple conv_w");
+    la.need(w.table.w, "ngram table");
+    la.need(w.table.s, "ngram table scales");
+    la.need(w.table.b, "ngram table biases");
+    // the head vocabularies and offsets follow from the config; the multipliers are the caller's
+    mtpx_ngram_table expect;
+    const int64_t rows = ngram_heads(cfg->ple, &expect);
+    if (w.table.rows != rows && la.missing.empty()) la.missing = "an n-gram table of the config's row count";
+    for (int hh = 0; hh < pg.nh; ++hh) {
+      w.table.vocab[hh] = expect.vocab[hh];
+      w.table.offset[hh] = expect.offset[hh];
+    }
+    std::vector<int64_t> hv(cfg->ple.ngram_size + 2 * (size_t)pg.nh);
+    for (int p = 0; p < cfg->ple.ngram_size; ++p) hv[p] = w.table.multiplier[p];
+    for (int hh = 0; hh < pg.nh; ++hh) {
+      hv[cfg->ple.ngram_size + hh] = w.table.vocab[hh];
+      hv[cfg->ple.ngram_size + pg.nh + hh] = w.table.offset[hh];
+    }
+    void* hp = nullptr;
+    if (hipMalloc(&hp, 8 * hv.size()) != hipSuccess ||
+        hipMemcpy(hp, hv.data(), 8 * hv.size(), hipMemcpyHostToDevice) != hipSuccess)
+      la.ok = false;
+    if (hp) t->ple->allocs.push_back(hp);
+    t->ple->hash = static_cast<int64_t*>(hp);
+    rc = la.finish("target ple block");
+  }
+  const int rc2 = rc ? rc : ad.finish("target");
+  if (rc2) {
+    target_release(t);
+    return rc2;
+  }
+  out->ctx = t;
+  return MTPX_OK;
+}
+
 int mtpx_target_free(mtpx_target th) {
   Target* t = static_cast<Target*>(th.ctx);
   if (t) target_release(t);
@@ -2429,6 +2637,64 @@ int mtpx_head_new_random(mtpx_ctx h, const mtpx_head_config* cfg, uint64_t seed,
   Head* hd = nullptr;
   int rc = head_create(c, cfg, seed, &hd);
   if (rc) return rc;
+  out->ctx = hd;
+  return MTPX_OK;
+}
+
+int mtpx_head_adopt(mtpx_ctx h, const mtpx_head_config* cfg, const mtpx_head_weights* win, int pack_sb,
+                    mtpx_head* out) {
+  Ctx* c = C(h);
+  ARG(c && cfg && win && out, "null argument");
+  int rc = head_check(cfg);
+  if (rc) return rc;
+  ARG(win->shortlist_rows >= 1 && win->shortlist_rows % 8 == 0, "shortlist_rows=%d (a positive multiple of 8)",
+      win->shortlist_rows);
+  if (set_device(c)) return MTPX_ERR_HIP;
+  const mtpx_layer_config& lc = cfg->layer;
+  const int H = lc.hidden, W = cfg->hc * H;
+  Head* hd = new Head();
+  hd->cfg = *cfg;
+  hd->w = *win;
+  hd->layer = new Layer();
+  hd->layer->cfg = lc;
+  hd->layer->w = win->layer;
+  hd->layer->QW = 2 * lc.heads * lc.head_dim + 2 * lc.kv_heads * lc.head_dim + lc.index_dim;
+  mtpx_layer_weights& lw = hd->layer->w;
+  lw.qkv_rows = hd->layer->QW;
+  Adopt ad{c, lc.group_size, pack_sb != 0, &hd->allocs};
+  Adopt la{c, lc.group_size, pack_sb != 0, &hd->layer->allocs};
+  mtpx_q4 qkv{lw.qkv_w, lw.qkv_s, lw.qkv_b, lw.qkv_sb}, o{lw.o_w, lw.o_s, lw.o_b, lw.o_sb};
+  la.q4(&qkv, hd->layer->QW, H, "head qkv");
+  la.q4(&o, H, lc.heads * lc.head_dim, "head o_proj");
+  lw.qkv_sb = qkv.sb;
+  lw.o_sb = o.sb;
+  la.need(lw.q_norm, "head q_norm");
+  la.need(lw.k_norm, "head k_norm");
+  la.moe(&lw.moe, lc);
+  if ((!lw.rope_cos || !lw.rope_sin) && !rope_tables(c, &lc, &hd->layer->allocs, &lw.rope_cos, &lw.rope_sin))
+    la.ok = false;
+  mtpx_head_weights& w = hd->w;
+  ad.q4(&w.embed, cfg->vocab, H, "head embed (the target's embed_tokens)");
+  ad.need(w.pre_norm_embedding, "pre_norm_embedding");
+  ad.need(w.pre_norm_hidden, "pre_norm_hidden");
+  ad.q4(&w.fc_embedding, H, H, "fc_embedding");
+  ad.q4(&w.fc_hidden, H, H, "fc_hidden");
+  ad.hc(&w.attn_hc, H, cfg->hc, cfg->lowrank, true);
+  ad.hc(&w.mlp_hc, H, cfg->hc, cfg->lowrank, true);
+  ad.hc(&w.final_hc, H, cfg->hc, cfg->lowrank, false);
+  ad.q4(&w.shortlist, w.shortlist_rows, H, "shortlist rows");
+  ad.need(w.shortlist_ids, "shortlist ids");
+  (void)W;
+  rc = la.finish("head layer");
+  if (!rc) rc = ad.finish("head");
+  if (rc) {
+    for (void* p : hd->allocs) hipFree(p);
+    for (void* p : hd->layer->allocs) hipFree(p);
+    delete hd->layer;
+    delete hd;
+    return rc;
+  }
+  w.layer = lw;
   out->ctx = hd;
   return MTPX_OK;
 }

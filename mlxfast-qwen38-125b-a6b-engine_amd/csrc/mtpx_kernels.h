@@ -88,6 +88,9 @@ struct MoeDispatch {
   int expert[MAX_TOKENS * MAX_TOPK + 1];
   int count[MAX_TOKENS * MAX_TOPK + 1];
   int16_t slot[MAX_TOKENS * MAX_TOPK + 1][MAX_TOKENS];  // m*K + k (routed) or M*K + m (shared)
+  // every slot once, in dispatch order: the M shared slots, then each selected expert's slots
+  // (so the slots of one expert are adjacent)
+  int16_t order[MAX_TOKENS * (MAX_TOPK + 1)];
 };
 static_assert(offsetof(MoeDispatch, slot) % 8 == 0 && sizeof(MoeDispatch::slot[0]) == 16,
               "slot rows are read as two 8-byte words");
@@ -124,6 +127,11 @@ constexpr int MOE_TICKETS = 64;
 hipError_t launch_moe_router_route(const MoeArgs& a, hipStream_t st);
 hipError_t launch_moe_gate_up(const MoeArgs& a, hipStream_t st);
 hipError_t launch_moe_down(const MoeArgs& a, hipStream_t st);
+// one workgroup per (slot, row block) in dispatch order (the slots of one expert side by side on
+// one XCD, so its weight rows are fetched from HBM once and served to the others by that L2)
+bool moe_dd_supported(int H, int F, int K);
+hipError_t launch_moe_gate_up_dd(const MoeArgs& a, hipStream_t st);
+hipError_t launch_moe_down_dd(const MoeArgs& a, hipStream_t st);
 hipError_t launch_moe_combine(const MoeArgs& a, hipStream_t st);
 
 // --- attention (attn.hip)

@@ -254,6 +254,15 @@ class MTPHead:
         self.h = Handle()
         check(ctx.lib.mtpx_head_new_random(ctx.h, C.byref(cfg), seed, C.byref(self.h)), "head_new_random")
 
+    @classmethod
+    def adopt(cls, ctx: Context, cfg: HeadConfig, weights: HeadWeights, pack_sb: bool = True):
+        """A head over caller-owned device weights (mtpx_head_adopt; the tensors must outlive it)."""
+        hd = cls.__new__(cls)
+        hd.ctx, hd.cfg, hd.h = ctx, cfg, Handle()
+        check(ctx.lib.mtpx_head_adopt(ctx.h, C.byref(cfg), C.byref(weights), 1 if pack_sb else 0, C.byref(hd.h)),
+              "head_adopt")
+        return hd
+
     def close(self):
         if self.h.ctx:
             self.ctx.lib.mtpx_head_free(self.h)
@@ -495,6 +504,17 @@ class Target:
             self.close()
         except Exception:
             pass
+
+    @classmethod
+    def adopt(cls, ctx: Context, cfg: TargetConfig, weights: TargetWeights, layers, pack_sb: bool = True):
+        """A target over caller-owned device weights (mtpx_target_adopt; the tensors must outlive it)."""
+        arr = (TargetLayerWeights * len(layers))(*layers)
+        t = cls.__new__(cls)
+        t.ctx, t.cfg, t.h = ctx, cfg, Handle()
+        t._keep = arr
+        check(ctx.lib.mtpx_target_adopt(ctx.h, C.byref(cfg), C.byref(weights), arr, 1 if pack_sb else 0,
+                                        C.byref(t.h)), "target_adopt")
+        return t
 
     def weights(self) -> TargetWeights:
         w = TargetWeights()

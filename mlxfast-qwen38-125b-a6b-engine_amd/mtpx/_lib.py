@@ -197,6 +197,9 @@ _SIGS = {
     "mtpx_target_state_ple": (INT, [Handle, C.POINTER(Handle)]),
     "mtpx_target_new_random": (INT, [Handle, C.POINTER(TargetConfig), U64, C.POINTER(Handle)]),
     "mtpx_target_free": (INT, [Handle]),
+    "mtpx_target_adopt": (INT, [Handle, C.POINTER(TargetConfig), C.POINTER(TargetWeights),
+                                C.POINTER(TargetLayerWeights), INT, C.POINTER(Handle)]),
+    "mtpx_head_adopt": (INT, [Handle, C.POINTER(HeadConfig), C.POINTER(HeadWeights), INT, C.POINTER(Handle)]),
     "mtpx_target_weights_get": (INT, [Handle, C.POINTER(TargetWeights)]),
     "mtpx_target_layer_weights_get": (INT, [Handle, INT, C.POINTER(TargetLayerWeights)]),
     "mtpx_target_state_new": (INT, [Handle, Handle, C.POINTER(Handle)]),

@@ -35,25 +35,31 @@ namespace mtpx {
 
 // ---------------------------------------------------------------------------
 // route (run by one workgroup of RR_THREADS threads): wave m selects token m's
-// top-k; then the dispatch table is built in LDS by all threads: each expert
-// once (ordered by its first (token, rank) slot), with its slots ordered by
-// token.
+// top-k and its softmax in registers; then the dispatch table is built in LDS by
+// the threads of the M*K slots: each expert once (ordered by its first (token,
+// rank) slot), with its slots ordered by token.  No serial loop over slots or
+// experts: leaders by an LDS minimum, expert offsets by a wave scan.
 constexpr int ROUTE_EPER = 16;  // E <= 1024
 constexpr int RR_THREADS = 512;
+static_assert(MAX_TOKENS * MAX_TOPK <= 128, "the slots fit the first two waves");
+
+__device__ __forceinline__ float readlane_f(float v, int l) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
 
 __device__ void route_body(const MoeArgs& a) {
   const int E = a.E, K = a.K, M = a.M;
   const int MK = M * K;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   __shared__ int sel[MAX_TOKENS * MAX_TOPK];
-  __shared__ float selv[MAX_TOKENS][MAX_TOPK];
   __shared__ int first[1024];
   __shared__ uint32_t tokbits[MAX_TOKENS][32];  // expert membership per token
   __shared__ uint64_t leadmask[2];
+  __shared__ int wtot[2];
   __shared__ int uid[MAX_TOKENS * MAX_TOPK];
+  __shared__ int pre[MAX_TOKENS * MAX_TOPK];
   for (int i = threadIdx.x; i < E; i += blockDim.x) first[i] = 0x7fffffff;
   for (int i = threadIdx.x; i < MAX_TOKENS * 32; i += blockDim.x) (&tokbits[0][0])[i] = 0u;
-  __syncthreads();
   if (wave < M) {
     const float* lr = a.logits + (size_t)wave * E;
     float v[ROUTE_EPER];
@@ -64,6 +70,8 @@ __device__ void route_body(const MoeArgs& a) {
       v[j] = (e < E) ? ld_pub(lr + e) : -__uint_as_float(0x7f800000u);
       if (e >= E) taken |= 1u << j;
     }
+    float myv = 0.0f;  // lane k < K: the k-th selected logit and expert
+    int mys = 0;
     for (int k = 0; k < K; ++k) {
       float bv = -__uint_as_float(0x7f800000u);
       int bj = -1;
@@ -90,23 +98,20 @@ __device__ void route_body(const MoeArgs& a) {
       if (bj >= 0 && cand == lane + 64 * bj) taken |= 1u << bj;
       // only NaN logits leave no candidate; keep the index addressable
       if (cand >= E) cand = 0;
-      if (lane == 0) {
-        sel[wave * K + k] = cand;
-        selv[wave][k] = gmax;
+      if (lane == k) {
+        myv = gmax;
+        mys = cand;
       }
     }
-    // softmax over the K selected: exp per lane, sum in rank order on lane 0
-    const float mx = selv[wave][0];
-    if (lane < K) selv[wave][lane] = expf_det(selv[wave][lane] - mx);
-    if (lane == 0) {
-      float sum = 0.0f;
-      for (int k = 0; k < K; ++k) sum = sum + selv[wave][k];
-      sum = 1.0f / sum;
-      for (int k = 0; k < K; ++k) selv[wave][k] = selv[wave][k] * sum;
-    }
+    // softmax over the K selected: exp per lane, sum in rank order (lane values read uniformly)
+    const float ev = expf_det(myv - readlane_f(myv, 0));
+    float sum = 0.0f;
+    for (int k = 0; k < K; ++k) sum = sum + readlane_f(ev, k);
+    sum = 1.0f / sum;
     if (lane < K) {
-      a.idx[wave * K + lane] = sel[wave * K + lane];
-      a.w[wave * K + lane] = selv[wave][lane];
+      sel[wave * K + lane] = mys;
+      a.idx[wave * K + lane] = mys;
+      a.w[wave * K + lane] = ev * sum;
     }
   }
   __syncthreads();
@@ -118,31 +123,33 @@ __device__ void route_body(const MoeArgs& a) {
     atomicOr(&tokbits[t / K][e >> 5], 1u << (e & 31));
   }
   __syncthreads();
+  // leaders (first slot of an expert) in slot order = experts in dispatch order; each leader's
+  // token count, and the exclusive scan of the counts over the slots (waves 0 and 1)
   const bool leader = t < MK && first[e] == t;
+  int count = 0;
+  if (leader)
+    for (int m = 0; m < M; ++m) count += (tokbits[m][e >> 5] >> (e & 31)) & 1u;
+  int incl = count;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int y = __shfl_up(incl, off, 64);
+    if (lane >= off) incl += y;
+  }
   const uint64_t bal = __ballot(leader);
-  if (lane == 0 && wave < 2) leadmask[wave] = bal;
+  if (wave < 2) {
+    if (lane == 0) leadmask[wave] = bal;
+    if (lane == 63) wtot[wave] = incl;
+  }
   __syncthreads();
   MoeDispatch* d = a.disp;
-  __shared__ int cnt[MAX_TOKENS * MAX_TOPK];
-  __shared__ int pre[MAX_TOKENS * MAX_TOPK];
+  const int n = __popcll(leadmask[0]) + (MK > 64 ? __popcll(leadmask[1]) : 0);
   if (leader) {
     const uint64_t below = (t & 63) ? (leadmask[t >> 6] & ((~0ull) >> (64 - (t & 63)))) : 0ull;
     const int u = __popcll(below) + (t >= 64 ? __popcll(leadmask[0]) : 0);
     uid[t] = u;
-    int count = 0;
-    for (int m = 0; m < M; ++m) count += (tokbits[m][e >> 5] >> (e & 31)) & 1u;
+    pre[u] = M + incl - count + (t >= 64 ? wtot[0] : 0);  // slots before expert u, shared ones first
     d->expert[u + 1] = e;
     d->count[u + 1] = count;
-    cnt[u] = count;
-  }
-  __syncthreads();
-  const int n = __popcll(leadmask[0]) + (MK > 64 ? __popcll(leadmask[1]) : 0);
-  if (t == 0) {  // slots of the routed experts before expert u, in dispatch order
-    int acc = M;
-    for (int v = 0; v < n; ++v) {
-      pre[v] = acc;
-      acc += cnt[v];
-    }
   }
   __syncthreads();
   if (t < MK) {
@@ -150,7 +157,7 @@ __device__ void route_body(const MoeArgs& a) {
     int pos = 0;
     for (int m = 0; m < t / K; ++m) pos += (tokbits[m][e >> 5] >> (e & 31)) & 1u;
     d->slot[u + 1][pos] = (int16_t)t;
-    d->order[pre[u] + pos] = (int16_t)t;
+    d->order[pre[u] + pos] = t | ((e + 1) << 16);
     if (t + 1 > n) d->expert[t + 1] = -2;  // grid rows past the routed experts: no work
   }
   if (t == 0) {
@@ -160,7 +167,7 @@ __device__ void route_body(const MoeArgs& a) {
     d->count[0] = M;
     for (int m = 0; m < M; ++m) {
       d->slot[0][m] = (int16_t)(MK + m);
-      d->order[m] = (int16_t)(MK + m);
+      d->order[m] = MK + m;
     }
   }
 }
@@ -538,24 +545,31 @@ __device__ __forceinline__ int dd_unit(int n_units) {
   return (int)(blockIdx.x % 8) * per + (int)(blockIdx.x / 8);
 }
 
-// gate|up: an item = 32 rows of F (gate and up rows side by side); 4 waves, each 64/L rows per
-// pass, 32 / (4 * 64/L) passes.
+// gate|up: a unit = dd_gate_up_rows<L>() rows of F (gate and up rows side by side): 16, or one
+// pass of the 4 waves when that is more (64/L rows a wave); NP passes.  Units of 16 rows keep a
+// workgroup's registers low enough for six per CU, so the launch runs in about one round
+// (measured: 23.5 -> 19.1 us per launch at M = 4 against units of 32 rows).
+template <int L>
+constexpr int dd_gate_up_rows() { return 4 * (64 / L) > 16 ? 4 * (64 / L) : 16; }
+
 template <int L, int IT, bool PK>
 __global__ __launch_bounds__(DD_THREADS) void k_moe_gate_up_dd(MoeArgs a) {
   extern __shared__ uint32_t lds[];  // [H/32][XP_DW]: the slot's token
   constexpr int RW = 64 / L;
-  constexpr int NP = 32 / (4 * RW) > 0 ? 32 / (4 * RW) : 1;
-  static_assert(4 * RW * NP == 32, "four waves cover the 32 rows of an item");
+  constexpr int UR = dd_gate_up_rows<L>();
+  constexpr int NP = UR / (4 * RW);
+  static_assert(4 * RW * NP == UR, "four waves cover the rows of a unit");
   const int H = a.H, F = a.F, gs = a.gs, M = a.M, K = a.K;
-  const int nb = H / 32, ng = H / gs, P = sb_row_len(H, gs), nfb = F / 32;
+  const int nb = H / 32, ng = H / gs, P = sb_row_len(H, gs), nfb = F / UR;
   const int n_units = M * (K + 1) * nfb;
   const int w = dd_unit(n_units);
   if (w >= n_units) return;
-  const int o = w / nfb, f0 = (w % nfb) * 32;
-  const int sl = a.disp->order[o];
+  const int o = w / nfb, f0 = (w % nfb) * UR;
+  const int ov = a.disp->order[o];
+  const int sl = ov & 0xffff;
   const bool shared = sl >= M * K;
   const int m = shared ? sl - M * K : sl / K;
-  const int e = shared ? 0 : a.idx[sl];
+  const int e = shared ? 0 : (ov >> 16) - 1;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int sub = lane % L, grp = lane / L;
   const uint32_t* gw = shared ? a.sh_gate_w : a.gate_w;
@@ -590,12 +604,13 @@ __global__ __launch_bounds__(DD_THREADS) void k_moe_gate_up_dd(MoeArgs a) {
   }
 }
 
-// down: an item = 4 * 2 * 64/L rows of H (two rows per lane group) of one slot; the combine
-// launch folds the slots' outputs.  (Combining in this launch -- agent-scope stores of the
-// outputs, a per-row-block ticket and the last arriver folding the block -- was measured slower:
-// the coherent stores, the wait for them and the serial tail cost more than the combine launch.)
+// down: a unit = 4 * 64/L rows of H (one row per lane group) of one slot (two rows per lane
+// group measured 15.3 against 13.6 us per launch at M = 4); the combine launch folds the slots'
+// outputs.  (Combining in this launch -- agent-scope stores of the outputs, a per-row-block
+// ticket and the last arriver folding the block -- was measured slower: the coherent stores, the
+// wait for them and the serial tail cost more than the combine launch.)
 template <int L>
-constexpr int dd_down_rows() { return 4 * 2 * (64 / L); }
+constexpr int dd_down_rows() { return 4 * (64 / L); }
 
 template <int L, int IT, bool PK>
 __global__ __launch_bounds__(DD_THREADS) void k_moe_down_dd(MoeArgs a) {
@@ -608,19 +623,20 @@ __global__ __launch_bounds__(DD_THREADS) void k_moe_down_dd(MoeArgs a) {
   const int wu = dd_unit(n_units);
   if (wu >= n_units) return;
   const int o = wu / nhb, hb = wu % nhb, h0 = hb * DR;
-  const int sl = a.disp->order[o];
+  const int ov = a.disp->order[o];
+  const int sl = ov & 0xffff;
   const bool shared = sl >= M * K;
-  const int e = shared ? 0 : a.idx[sl];
+  const int e = shared ? 0 : (ov >> 16) - 1;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int sub = lane % L, grp = lane / L;
-  const int hi = h0 + wave * 2 * RW + 2 * grp;  // this lane group's rows hi, hi + 1
-  const bool va = hi < H, vb = hi + 1 < H;
+  const int hi = h0 + wave * RW + grp;  // this lane group's row
+  const bool va = hi < H;
   const uint32_t* w = shared ? a.sh_down_w : a.down_w;
   const uint32_t* sb = shared ? a.sh_down_sb : a.down_sb;
   const bf16* sc = shared ? a.sh_down_s : a.down_s;
   const bf16* bi = shared ? a.sh_down_b : a.down_b;
   const size_t base = shared ? 0 : (size_t)e * H;
-  const size_t ra = base + (va ? hi : h0), rb = base + (vb ? hi + 1 : h0);
+  const size_t ra = base + (va ? hi : h0);
   // the slot's bf16 activations first (element q * 256 + t), then the weights
   constexpr int NA = 8;  // F <= NA * 256
   bf16 av[NA];
@@ -630,9 +646,8 @@ __global__ __launch_bounds__(DD_THREADS) void k_moe_down_dd(MoeArgs a) {
     av[q] = i < F ? a.act[(size_t)sl * F + i] : (bf16)0;
   }
   asm volatile("" ::: "memory");
-  QRow<L, IT> A, B;
+  QRow<L, IT> A;
   A.template load_as<PK>(w + ra * (F / 8), sc + ra * ng, bi + ra * ng, PK ? sb + ra * P : nullptr, nb, gs, sub, va);
-  B.template load_as<PK>(w + rb * (F / 8), sc + rb * ng, bi + rb * ng, PK ? sb + rb * P : nullptr, nb, gs, sub, vb);
   asm volatile("" ::: "memory");
 #pragma unroll
   for (int q = 0; q < NA; ++q) {
@@ -640,12 +655,9 @@ __global__ __launch_bounds__(DD_THREADS) void k_moe_down_dd(MoeArgs a) {
     if (blk < nb) xprep_lanes_direct(av[q], threadIdx.x & 31, lds + (size_t)blk * XP_DW);
   }
   __syncthreads();
-  float x0, x1;
-  dot2<L, IT, false>(A, B, lds, nb, sub, x0, x1);
+  float x0 = A.dot(lds, nb, sub);
   x0 = lane_fold<L>(x0);
-  x1 = lane_fold<L>(x1);
-  if (sub == 0 && va)  // rows hi, hi + 1 (hi even, H a multiple of 8): one 4-byte store of both
-    *reinterpret_cast<uint32_t*>(a.r + (size_t)sl * H + hi) = (uint32_t)f2bf(x0) | ((uint32_t)f2bf(x1) << 16);
+  if (sub == 0 && va) a.r[(size_t)sl * H + hi] = f2bf(x0);
 }
 
 // ---------------------------------------------------------------------------
@@ -768,14 +780,15 @@ hipError_t launch_moe_combine(const MoeArgs& a, hipStream_t st) {
 // expert-grouped launches: grid = (M*K + 1 dispatch rows) x row blocks
 template <int L, int IT, bool PK>
 static hipError_t gate_up_dd_pk(const MoeArgs& a, hipStream_t st) {
-  if constexpr (32 % (4 * (64 / L)) != 0) {
+  if constexpr (L < 4) {
     return hipErrorNotSupported;
   } else {
     const size_t lds = (size_t)(a.H / 32) * XP_DW * 4;
     static size_t cur = 0;
     hipError_t e = ensure_lds(k_moe_gate_up_dd<L, IT, PK>, lds, cur);
     if (e != hipSuccess) return e;
-    const int units = a.M * (a.K + 1) * (a.F / 32);
+    if (a.F % dd_gate_up_rows<L>() != 0) return hipErrorInvalidValue;
+    const int units = a.M * (a.K + 1) * (a.F / dd_gate_up_rows<L>());
     hipLaunchKernelGGL((k_moe_gate_up_dd<L, IT, PK>), dim3((units + 7) / 8 * 8), dim3(DD_THREADS), lds, st, a);
     return hipGetLastError();
   }
@@ -812,7 +825,8 @@ hipError_t launch_moe_down_dd(const MoeArgs& a, hipStream_t st) { MTPX_QROW_DISP
 
 bool moe_dd_supported(int H, int F, int K) {
   const int Lg = lanes_for_blocks(H / 32);
-  return 32 % (4 * (64 / Lg)) == 0 && H % 8 == 0 && F <= 8 * DD_THREADS && K >= 1;
+  const int ur = 4 * (64 / Lg) > 16 ? 4 * (64 / Lg) : 16;  // dd_gate_up_rows
+  return Lg >= 4 && F % ur == 0 && H % 8 == 0 && F <= 8 * DD_THREADS && K >= 1;
 }
 
 }  // namespace mtpx

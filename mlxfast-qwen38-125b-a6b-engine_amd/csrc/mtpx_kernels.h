@@ -89,8 +89,9 @@ struct MoeDispatch {
   int count[MAX_TOKENS * MAX_TOPK + 1];
   int16_t slot[MAX_TOKENS * MAX_TOPK + 1][MAX_TOKENS];  // m*K + k (routed) or M*K + m (shared)
   // every slot once, in dispatch order: the M shared slots, then each selected expert's slots
-  // (so the slots of one expert are adjacent)
-  int16_t order[MAX_TOKENS * (MAX_TOPK + 1)];
+  // (so the slots of one expert are adjacent); entry = slot | (expert + 1) << 16, expert -1
+  // the shared one, so a workgroup finds its weight rows with one load
+  int32_t order[MAX_TOKENS * (MAX_TOPK + 1)];
 };
 static_assert(offsetof(MoeDispatch, slot) % 8 == 0 && sizeof(MoeDispatch::slot[0]) == 16,
               "slot rows are read as two 8-byte words");

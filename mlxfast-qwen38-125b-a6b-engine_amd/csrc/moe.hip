@@ -67,7 +67,8 @@ __device__ void route_body(const MoeArgs& a) {
 #pragma unroll
     for (int j = 0; j < ROUTE_EPER; ++j) {
       const int e = lane + 64 * j;
-      v[j] = (e < E) ? ld_pub(lr + e) : -__uint_as_float(0x7f800000u);
+      const float x = (e < E) ? ld_pub(lr + e) : 0.0f;
+      v[j] = (e < E && x == x) ? x : -__uint_as_float(0x7f800000u);  // a NaN logit ranks as -inf
       if (e >= E) taken |= 1u << j;
     }
     float myv = 0.0f;  // lane k < K: the k-th selected logit and expert
@@ -96,8 +97,9 @@ __device__ void route_body(const MoeArgs& a) {
       cand = min(cand, lane_xor_i<2>(cand));
       cand = min(cand, lane_xor_i<1>(cand));
       if (bj >= 0 && cand == lane + 64 * bj) taken |= 1u << bj;
-      // only NaN logits leave no candidate; keep the index addressable
-      if (cand >= E) cand = 0;
+      // every rank finds an untaken expert (no NaN compares, K <= E): the K experts are distinct,
+      // so the dispatch order below is a permutation of the slots
+      if (cand >= E) cand = E - 1;  // unreachable; keeps the index addressable
       if (lane == k) {
         myv = gmax;
         mys = cand;
@@ -566,10 +568,10 @@ __global__ __launch_bounds__(DD_THREADS) void k_moe_gate_up_dd(MoeArgs a) {
   if (w >= n_units) return;
   const int o = w / nfb, f0 = (w % nfb) * UR;
   const int ov = a.disp->order[o];
-  const int sl = ov & 0xffff;
+  const int sl = min(ov & 0xffff, M * (K + 1) - 1);  // (clamps: never out of the weights, whatever the table holds)
   const bool shared = sl >= M * K;
   const int m = shared ? sl - M * K : sl / K;
-  const int e = shared ? 0 : (ov >> 16) - 1;
+  const int e = shared ? 0 : min(max((ov >> 16) - 1, 0), a.E - 1);
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int sub = lane % L, grp = lane / L;
   const uint32_t* gw = shared ? a.sh_gate_w : a.gate_w;
@@ -624,9 +626,9 @@ __global__ __launch_bounds__(DD_THREADS) void k_moe_down_dd(MoeArgs a) {
   if (wu >= n_units) return;
   const int o = wu / nhb, hb = wu % nhb, h0 = hb * DR;
   const int ov = a.disp->order[o];
-  const int sl = ov & 0xffff;
+  const int sl = min(ov & 0xffff, M * (K + 1) - 1);  // (clamps: never out of the weights, whatever the table holds)
   const bool shared = sl >= M * K;
-  const int e = shared ? 0 : (ov >> 16) - 1;
+  const int e = shared ? 0 : min(max((ov >> 16) - 1, 0), a.E - 1);
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int sub = lane % L, grp = lane / L;
   const int hi = h0 + wave * RW + grp;  // this lane group's row

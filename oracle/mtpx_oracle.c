@@ -301,7 +301,8 @@ void o_router_gemv(const o_bf16* W, int rows, int H, const float* x, int M, floa
 
 /* ======================================================================== */
 /* a8: top-k + softmax (FM/TrackFastMoE.swift:780-878): the K largest logits, */
-/* value descending, ties to the lowest index; softmax over the K selected:   */
+/* value descending, ties to the lowest index, a NaN ranked as -inf (so the K */
+/* experts are always distinct); softmax over the K selected:                 */
 /* max, e_k = exp(v_k - max), sum in rank order, w_k = e_k * (1 / sum).       */
 /* ======================================================================== */
 
@@ -313,13 +314,18 @@ void o_topk_softmax(const float* logits, int M, int E, int K, int32_t* idx, floa
     float v[64];
     for (int k = 0; k < K; ++k) {
       int best = -1;
+      float bv = -INFINITY;
       for (int e = 0; e < E; ++e) {
         if (taken[e]) continue;
-        if (best < 0 || lr[e] > lr[best]) best = e;
+        const float x = lr[e] == lr[e] ? lr[e] : -INFINITY; /* a NaN logit ranks as -inf */
+        if (best < 0 || x > bv) {
+          best = e;
+          bv = x;
+        }
       }
       taken[best] = 1;
       idx[m * K + k] = best;
-      v[k] = lr[best];
+      v[k] = bv;
     }
     const float mx = v[0];
     float e[64];

@@ -89,6 +89,31 @@ def test_moe_full_expert_shapes_bit_exact(ctx, gs, M, packed):
     run_case(ctx, w, H, E, K, F, gs, M, 77 + M, packed)
 
 
+def test_moe_nan_token_routes_distinct_experts(ctx):
+    """A token whose hidden state is NaN has NaN router logits: they rank as -inf, so the token
+    still takes K distinct experts (the lowest indices) and the dispatch stays a permutation of the
+    slots; the other tokens of the window are unaffected (bit-exact against the oracle)."""
+    import mtpx
+    print("case moe nan token", flush=True)
+    H, E, K, F, gs, M = 2560, 24, 10, 640, 64, 4
+    w = make_moe(1064, H, E, K, F, gs)
+    x = rand_bf16(np.random.default_rng(81), (M, H), 1.0)
+    x[1] = 0x7FC0  # bf16 NaN row
+    ref = O.moe_block(w, x, H, E, K, F, gs)
+    dw = {n: dev(w[n]) for n in NAMES}
+    mw = mtpx.moe_weights_from(dw, H, E, K, F, gs)
+    y = empty_bf16(M, H)
+    idx = torch.zeros(M, K, dtype=torch.int32, device="cuda")
+    ctx.moe_forward(mw, dev(x), y, idx)
+    ctx.synchronize()
+    got = host(idx)
+    assert np.array_equal(got, ref["idx"])
+    assert list(got[1]) == list(range(K))
+    assert all(len(set(row)) == K for row in got)
+    ok = [0, 2, 3]
+    assert np.array_equal(host(y)[ok], ref["y"][ok])
+
+
 def test_moe_router_ties_lowest_index(ctx):
     print("case router ties", flush=True)
     H, E, K, F, gs = 256, 16, 4, 64, 32

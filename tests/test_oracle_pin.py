@@ -205,6 +205,20 @@ def test_topk_softmax_rule_and_ties():
     assert list(idx[1]) == list(range(8))
 
 
+def test_topk_nan_ranks_as_minus_inf():
+    r = rng(10)
+    lg = r.standard_normal((3, 40)).astype(np.float32)
+    lg[0, [2, 5, 30]] = np.nan
+    lg[1, :] = np.nan               # every logit NaN: the K lowest indices
+    lg[2, ::2] = np.nan
+    idx, _ = O.topk_softmax(lg, 12)
+    for m in range(3):
+        clean = np.where(np.isnan(lg[m]), -np.inf, lg[m])
+        assert np.array_equal(idx[m], np.lexsort((np.arange(40), -clean))[:12])
+        assert len(set(idx[m])) == 12
+    assert list(idx[1]) == list(range(12))
+
+
 # ---------------------------------------------------------------------------- MoE block
 def _moe_weights(r, H, E, K, F, gs):
     def q(shape):

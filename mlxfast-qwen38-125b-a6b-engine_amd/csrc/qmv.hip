@@ -100,15 +100,17 @@ constexpr int MMA_THREADS = 512;
 typedef int v4i_t __attribute__((ext_vector_type(4)));
 
 // Prepared blocks of M tokens (xp [M][NB][XP_DW]) -> the four-limb layout in
-// LDS [MMA_TOK][NB][MB_DW]; tokens M.. are zero (their sums are 0, p = SX = 0).
+// LDS [MMA_TOK * TG][NB][MB_DW] (TG groups of four tokens); tokens M.. are zero
+// (their sums are 0, p = SX = 0).
 // Unit u = (token, block, word g, even/odd) converts three limb words into
 // four; the loads (all units of this thread, then its p/SX pairs) are issued
 // by mma_stage_load, so the caller can put its own loads behind them and
 // mma_stage_store waits for these only.
-template <int NB>
+template <int NB, int TG>
 struct MmaStage {
-  static constexpr int NU = (MMA_TOK * NB * 8 + MMA_THREADS - 1) / MMA_THREADS;   // units per thread
-  static constexpr int NP = (MMA_TOK * NB + MMA_THREADS - 1) / MMA_THREADS;       // p/SX pairs per thread
+  static constexpr int NT = MMA_TOK * TG;                                      // tokens staged
+  static constexpr int NU = (NT * NB * 8 + MMA_THREADS - 1) / MMA_THREADS;     // units per thread
+  static constexpr int NP = (NT * NB + MMA_THREADS - 1) / MMA_THREADS;         // p/SX pairs per thread
   uint32_t w[NU][3];
   uint32_t ps[NP][2];
 
@@ -117,7 +119,7 @@ struct MmaStage {
     for (int k = 0; k < NU; ++k) {
       const int u = threadIdx.x + k * MMA_THREADS;
       const int t = u / (NB * 8), rem = u - t * (NB * 8), blk = rem >> 3, ge = rem & 7;
-      const bool in = u < MMA_TOK * NB * 8 && t < M;
+      const bool in = u < NT * NB * 8 && t < M;
       const uint32_t* src = xp + ((size_t)(in ? t : 0) * NB + (in ? blk : 0)) * XP_DW + ((ge & 1) ? 4 : 0) + (ge >> 1);
       w[k][0] = in ? src[0] : 0u;
       w[k][1] = in ? src[8] : 0u;
@@ -127,7 +129,7 @@ struct MmaStage {
     for (int k = 0; k < NP; ++k) {
       const int u = threadIdx.x + k * MMA_THREADS;
       const int t = u / NB, blk = u - t * NB;
-      const bool in = u < MMA_TOK * NB && t < M;
+      const bool in = u < NT * NB && t < M;
       const uint32_t* src = xp + ((size_t)(in ? t : 0) * NB + (in ? blk : 0)) * XP_DW + 24;
       ps[k][0] = in ? src[0] : 0u;
       ps[k][1] = in ? src[1] : 0u;
@@ -138,7 +140,7 @@ struct MmaStage {
 #pragma unroll
     for (int k = 0; k < NU; ++k) {
       const int u = threadIdx.x + k * MMA_THREADS;
-      if (u < MMA_TOK * NB * 8) {
+      if (u < NT * NB * 8) {
         const int t = u / (NB * 8), rem = u - t * (NB * 8), blk = rem >> 3, ge = rem & 7;
         const uint32_t w0 = w[k][0], w1 = w[k][1];
         uint32_t* dst = lds + ((size_t)t * NB + blk) * MB_DW + 2 * (ge >> 1) + (ge & 1);
@@ -151,7 +153,7 @@ struct MmaStage {
 #pragma unroll
     for (int k = 0; k < NP; ++k) {
       const int u = threadIdx.x + k * MMA_THREADS;
-      if (u < MMA_TOK * NB) {
+      if (u < NT * NB) {
         uint32_t* dst = lds + (size_t)u * MB_DW + 32;  // u = t * NB + blk
         dst[0] = ps[k][0];
         dst[1] = ps[k][1];
@@ -180,7 +182,7 @@ constexpr int mma_body_chunks() {
   return (NCH <= 12 && NCH % 2 == 0 && (8 * (NCH / 2)) % LC == 0 && NCH / 2 >= B0) ? NCH / 2 : B0;
 }
 
-template <int L, int IT, int C>
+template <int L, int IT, int C, int TG>
 __global__ __launch_bounds__(MMA_THREADS) void k_qmv_mma(const uint32_t* __restrict__ wq, const uint32_t* __restrict__ sbp,
                                                         int N, int K, int gs, const uint32_t* __restrict__ xp, int M,
                                                         bf16* __restrict__ y, float* __restrict__ yf) {
@@ -191,10 +193,12 @@ __global__ __launch_bounds__(MMA_THREADS) void k_qmv_mma(const uint32_t* __restr
   constexpr int BC = mma_body_chunks<L, IT, C>();  // chunks per loop body
   constexpr int TPG = 8 / C;                   // tiles per workgroup pass
   static_assert(NB % (4 * C) == 0 && NCH % BC == 0 && C <= L && C <= 8 && LC <= 16, "whole bodies of four-block chunks");
-  // LDS: activations [MMA_TOK][NB][MB_DW]; per wave the (scale, bias) pairs of its tile and class [16][NQ];
-  // class partials [2][8 waves][64]
+  // LDS: activations [MMA_TOK * TG][NB][MB_DW]; per wave the (scale, bias) pairs of its tile and class
+  // [16][NQ]; class partials [2][8 waves][TG][64].  Token group tq (tokens 4 tq .. 4 tq + 3) takes its own
+  // MFMA on the same weight operand, so a launch serves up to 4 TG tokens with one read of the weights.
+  constexpr size_t TGO = (size_t)MMA_TOK * NB * MB_DW;  // one token group's activations
   extern __shared__ uint32_t lds[];
-  uint32_t* sbl = lds + MMA_TOK * NB * MB_DW;
+  uint32_t* sbl = lds + TG * TGO;
   float* part = reinterpret_cast<float*>(sbl + 8 * 16 * NQ);
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int c = wave % C, tl = wave / C;
@@ -207,7 +211,7 @@ __global__ __launch_bounds__(MMA_THREADS) void k_qmv_mma(const uint32_t* __restr
   const uint32_t* xps = lds + (size_t)g * NB * MB_DW + 32;
   // activations once per workgroup
   {
-    MmaStage<NB> stg;
+    MmaStage<NB, TG> stg;
     stg.load(xp, M);
     stg.store(lds);
   }
@@ -237,9 +241,11 @@ __global__ __launch_bounds__(MMA_THREADS) void k_qmv_mma(const uint32_t* __restr
 #pragma unroll
     for (int k = 0; k < NG; ++k)
       if (lane + 64 * k < 16 * NQ) mysb[lane + 64 * k] = gv[k];  // this wave's region: read back by this wave only
-    float acc[LC];
+    float acc[TG][LC];
 #pragma unroll
-    for (int u = 0; u < LC; ++u) acc[u] = 0.0f;
+    for (int tq = 0; tq < TG; ++tq)
+#pragma unroll
+      for (int u = 0; u < LC; ++u) acc[tq][u] = 0.0f;
 #pragma unroll 1
     for (int ch0 = 0; ch0 < NCH; ch0 += 2 * BC) {
 #pragma unroll
@@ -261,38 +267,53 @@ __global__ __launch_bounds__(MMA_THREADS) void k_qmv_mma(const uint32_t* __restr
           for (int b = 0; b < 4; ++b) {
             const int q = 4 * ch + b, j = c + C * q;
             const long bop = (long)(T[b] & 0x0f0f0f0fu) | ((long)((T[b] >> 4) & 0x0f0f0f0fu) << 32);
-            long aop;
-            __builtin_memcpy(&aop, xa + (size_t)j * MB_DW, 8);
-            v4i_t d = {0, 0, 0, 0};
-            d = __builtin_amdgcn_mfma_i32_16x16x32_i8(aop, bop, d, 0, 0, 0);
-            const int low = d[0] + 128 * d[1] + 16384 * d[2];
-            const float dx = __builtin_fmaf((float)d[3], 65536.0f, (float)low);
-            uint2 ps;
-            __builtin_memcpy(&ps, xps + (size_t)j * MB_DW, 8);
             const uint32_t sb = mysb[n * NQ + q];
-            float& a = acc[(4 * cb + b + 4 * BC * half) % LC];  // chain (j % L) / C, in block order
-            a = __builtin_fmaf(__uint_as_float(sb << 16), dx * __uint_as_float(ps.x), a);
-            a = __builtin_fmaf(__uint_as_float(sb & 0xffff0000u), __uint_as_float(ps.y), a);
+#pragma unroll
+            for (int tq = 0; tq < TG; ++tq) {
+              long aop;
+              __builtin_memcpy(&aop, xa + tq * TGO + (size_t)j * MB_DW, 8);
+              v4i_t d = {0, 0, 0, 0};
+              d = __builtin_amdgcn_mfma_i32_16x16x32_i8(aop, bop, d, 0, 0, 0);
+              const int low = d[0] + 128 * d[1] + 16384 * d[2];
+              const float dx = __builtin_fmaf((float)d[3], 65536.0f, (float)low);
+              uint2 ps;
+              __builtin_memcpy(&ps, xps + tq * TGO + (size_t)j * MB_DW, 8);
+              float& a = acc[tq][(4 * cb + b + 4 * BC * half) % LC];  // chain (j % L) / C, in block order
+              a = __builtin_fmaf(__uint_as_float(sb << 16), dx * __uint_as_float(ps.x), a);
+              a = __builtin_fmaf(__uint_as_float(sb & 0xffff0000u), __uint_as_float(ps.y), a);
+            }
           }
         }
         asm volatile("" ::: "memory");  // one body's operands live at a time (no LDS reads hoisted across)
       }
     }
-    fold_levels<LC / 2>(acc);  // butterfly levels L/2 .. C: this class's chains
-    float v = acc[0];
-    if constexpr (C > 1) {
-      float* pb = part + (iter & 1) * 8 * 64;  // by parity: the next write to it is two barriers away
-      pb[wave * 64 + lane] = v;
-      __syncthreads();
-      float pc[C];
+    float v[TG];
 #pragma unroll
-      for (int q = 0; q < C; ++q) pc[q] = pb[(tl * C + q) * 64 + lane];
-      fold_levels<C / 2>(pc);  // levels C/2 .. 1 across the classes
-      v = pc[0];
+    for (int tq = 0; tq < TG; ++tq) {
+      fold_levels<LC / 2>(acc[tq]);  // butterfly levels L/2 .. C: this class's chains
+      v[tq] = acc[tq][0];
     }
-    if (c == 0 && g < M && row < N) {
-      y[(size_t)g * N + row] = f2bf(v);
-      if (yf) yf[(size_t)g * N + row] = v;
+    if constexpr (C > 1) {
+      float* pb = part + (iter & 1) * 8 * TG * 64;  // by parity: the next write to it is two barriers away
+#pragma unroll
+      for (int tq = 0; tq < TG; ++tq) pb[(wave * TG + tq) * 64 + lane] = v[tq];
+      __syncthreads();
+#pragma unroll
+      for (int tq = 0; tq < TG; ++tq) {
+        float pc[C];
+#pragma unroll
+        for (int q = 0; q < C; ++q) pc[q] = pb[((tl * C + q) * TG + tq) * 64 + lane];
+        fold_levels<C / 2>(pc);  // levels C/2 .. 1 across the classes
+        v[tq] = pc[0];
+      }
+    }
+#pragma unroll
+    for (int tq = 0; tq < TG; ++tq) {
+      const int tok = tq * MMA_TOK + g;
+      if (c == 0 && tok < M && row < N) {
+        y[(size_t)tok * N + row] = f2bf(v[tq]);
+        if (yf) yf[(size_t)tok * N + row] = v[tq];
+      }
     }
   }
 }
@@ -432,109 +453,121 @@ static hipError_t qmv_tokens(const uint32_t* wq, const bf16* s, const bf16* b, c
   MTPX_QROW_DISPATCH(K / 32, qmv_li, wq, s, b, sb, N, K, gs, xp, M, y, yf, st);
 }
 
-template <int L, int IT, int C>
+template <int L, int IT, int C, int TG>
 constexpr size_t mma_lds_bytes() {
-  return (size_t)MMA_TOK * L * IT * MB_DW * 4 + (size_t)8 * 16 * (L * IT / C) * 4 + 2 * 8 * 64 * 4;
+  return (size_t)MMA_TOK * TG * L * IT * MB_DW * 4 + (size_t)8 * 16 * (L * IT / C) * 4 + (size_t)2 * 8 * TG * 64 * 4;
 }
 
-template <int L, int IT, int C>
+// hipErrorNotReady: a launch of two token groups (one workgroup per CU) whose tile groups would
+// need a second, nearly empty round of workgroups -- the caller runs four tokens per launch instead.
+template <int L, int IT, int C, int TG>
 static hipError_t qmv_mma_c(const uint32_t* wq, const uint32_t* sb, int N, int K, int gs, const uint32_t* xp, int M,
                             bf16* y, float* yf, hipStream_t st) {
-  constexpr size_t lds = mma_lds_bytes<L, IT, C>();
-  static size_t cur = 0;
-  hipError_t e = ensure_lds(k_qmv_mma<L, IT, C>, lds, cur);
-  if (e != hipSuccess) return e;
+  constexpr size_t lds = mma_lds_bytes<L, IT, C, TG>();
   const int groups = ((N + 15) / 16 + 8 / C - 1) / (8 / C);
   const int per_cu = lds <= 50 * 1024 ? 3 : lds <= 78 * 1024 ? 2 : 1;  // workgroups resident per CU
-  const int grid = groups < per_cu * device_cus() ? groups : per_cu * device_cus();
-  hipLaunchKernelGGL((k_qmv_mma<L, IT, C>), dim3(grid), dim3(MMA_THREADS), lds, st, wq, sb, N, K, gs, xp, M, y, yf);
+  const int slots = per_cu * device_cus();
+  if (TG > 1 && groups > slots && groups < 4 * slots) return hipErrorNotReady;
+  static size_t cur = 0;
+  hipError_t e = ensure_lds(k_qmv_mma<L, IT, C, TG>, lds, cur);
+  if (e != hipSuccess) return e;
+  const int grid = groups < slots ? groups : slots;
+  hipLaunchKernelGGL((k_qmv_mma<L, IT, C, TG>), dim3(grid), dim3(MMA_THREADS), lds, st, wq, sb, N, K, gs, xp, M, y,
+                     yf);
   return hipGetLastError();
 }
 
-template <int L, int IT, int C>
+// One token group: two workgroups per CU at least (above that the dot-product path is faster,
+// measured).  Two token groups (five to eight tokens): one workgroup per CU, the LDS of a CU.
+template <int L, int IT, int C, int TG>
 constexpr bool mma_c_ok() {
   constexpr int NB = L * IT, LC = L / C, BC = mma_body_chunks<L, IT, C>();
-  // two workgroups per CU at least: above that the dot-product path is faster (measured)
   return C >= 2 && C <= L && LC <= 16 && NB % (4 * C) == 0 && (NB / C / 4) % BC == 0 &&
-         mma_lds_bytes<L, IT, C>() <= 80 * 1024;
+         mma_lds_bytes<L, IT, C, TG>() <= (TG == 1 ? 80 : 144) * 1024;
 }
 
-// Chain classes per tile: the fewest that give about four waves per CU.
-// Chain classes per tile: at least two (the per-wave scale/bias region of one
-// class fits beside the activations for two workgroups per CU), then the
-// fewest that give about eight waves per CU.
-template <int L, int IT>
+// Chain classes per tile: at least two (the per-wave scale/bias region of one class fits beside
+// the activations), then the fewest that give about eight waves per CU; with two token groups
+// (one workgroup per CU) four classes first, for twice the tile groups to spread over the CUs.
+template <int L, int IT, int TG>
 static hipError_t qmv_mma_li(const uint32_t* wq, const uint32_t* sb, int N, int K, int gs, const uint32_t* xp, int M,
                              bf16* y, float* yf, hipStream_t st) {
   const int tiles = (N + 15) / 16, want = 8 * device_cus();
-  if constexpr (mma_c_ok<L, IT, 2>()) {
-    if (tiles * 2 >= want) return qmv_mma_c<L, IT, 2>(wq, sb, N, K, gs, xp, M, y, yf, st);
+  if constexpr (TG == 2 && mma_c_ok<L, IT, 4, TG>()) return qmv_mma_c<L, IT, 4, TG>(wq, sb, N, K, gs, xp, M, y, yf, st);
+  if constexpr (mma_c_ok<L, IT, 2, TG>()) {
+    if (tiles * 2 >= want) return qmv_mma_c<L, IT, 2, TG>(wq, sb, N, K, gs, xp, M, y, yf, st);
   }
-  if constexpr (mma_c_ok<L, IT, 4>()) {
-    if (tiles * 4 >= want) return qmv_mma_c<L, IT, 4>(wq, sb, N, K, gs, xp, M, y, yf, st);
+  if constexpr (mma_c_ok<L, IT, 4, TG>()) {
+    if (tiles * 4 >= want) return qmv_mma_c<L, IT, 4, TG>(wq, sb, N, K, gs, xp, M, y, yf, st);
   }
-  if constexpr (mma_c_ok<L, IT, 8>()) return qmv_mma_c<L, IT, 8>(wq, sb, N, K, gs, xp, M, y, yf, st);
-  if constexpr (mma_c_ok<L, IT, 4>()) return qmv_mma_c<L, IT, 4>(wq, sb, N, K, gs, xp, M, y, yf, st);
-  if constexpr (mma_c_ok<L, IT, 2>()) return qmv_mma_c<L, IT, 2>(wq, sb, N, K, gs, xp, M, y, yf, st);
+  if constexpr (mma_c_ok<L, IT, 8, TG>()) return qmv_mma_c<L, IT, 8, TG>(wq, sb, N, K, gs, xp, M, y, yf, st);
+  if constexpr (mma_c_ok<L, IT, 4, TG>()) return qmv_mma_c<L, IT, 4, TG>(wq, sb, N, K, gs, xp, M, y, yf, st);
+  if constexpr (mma_c_ok<L, IT, 2, TG>()) return qmv_mma_c<L, IT, 2, TG>(wq, sb, N, K, gs, xp, M, y, yf, st);
   return hipErrorNotSupported;
 }
 
-// The matrix-core path takes 2..4 tokens of a matrix with packed scale/bias
+// The matrix-core path takes 2..8 tokens of a matrix with packed scale/bias
 // rows whose blocks tile the lanes exactly in four-block chunks.
 static bool qmv_mma_ok(const uint32_t* sb, int K, int M) {
   const int nb = K / 32, L = lanes_for_blocks(nb);
-  return sb && M >= 2 && M <= MMA_TOK && nb % L == 0 && nb % 4 == 0;
+  return sb && M >= 2 && M <= 2 * MMA_TOK && nb % L == 0 && nb % 4 == 0;
 }
 
+template <int TG>
 static hipError_t qmv_mma(const uint32_t* wq, const uint32_t* sb, int N, int K, int gs, const uint32_t* xp, int M,
                           bf16* y, float* yf, hipStream_t st) {
   const int nb = K / 32, L = lanes_for_blocks(nb), IT = nb / L;
   switch (L * 16 + IT) {
-    case 16 * 16 + 4: return qmv_mma_li<16, 4>(wq, sb, N, K, gs, xp, M, y, yf, st);
-    case 16 * 16 + 5: return qmv_mma_li<16, 5>(wq, sb, N, K, gs, xp, M, y, yf, st);
-    case 32 * 16 + 4: return qmv_mma_li<32, 4>(wq, sb, N, K, gs, xp, M, y, yf, st);
-    case 32 * 16 + 6: return qmv_mma_li<32, 6>(wq, sb, N, K, gs, xp, M, y, yf, st);
-    case 64 * 16 + 4: return qmv_mma_li<64, 4>(wq, sb, N, K, gs, xp, M, y, yf, st);
-    case 64 * 16 + 5: return qmv_mma_li<64, 5>(wq, sb, N, K, gs, xp, M, y, yf, st);
-    case 8 * 16 + 4: return qmv_mma_li<8, 4>(wq, sb, N, K, gs, xp, M, y, yf, st);
-    case 8 * 16 + 5: return qmv_mma_li<8, 5>(wq, sb, N, K, gs, xp, M, y, yf, st);
-    case 4 * 16 + 4: return qmv_mma_li<4, 4>(wq, sb, N, K, gs, xp, M, y, yf, st);
-    case 4 * 16 + 5: return qmv_mma_li<4, 5>(wq, sb, N, K, gs, xp, M, y, yf, st);
+    case 16 * 16 + 4: return qmv_mma_li<16, 4, TG>(wq, sb, N, K, gs, xp, M, y, yf, st);
+    case 16 * 16 + 5: return qmv_mma_li<16, 5, TG>(wq, sb, N, K, gs, xp, M, y, yf, st);
+    case 32 * 16 + 4: return qmv_mma_li<32, 4, TG>(wq, sb, N, K, gs, xp, M, y, yf, st);
+    case 32 * 16 + 6: return qmv_mma_li<32, 6, TG>(wq, sb, N, K, gs, xp, M, y, yf, st);
+    case 64 * 16 + 4: return qmv_mma_li<64, 4, TG>(wq, sb, N, K, gs, xp, M, y, yf, st);
+    case 64 * 16 + 5: return qmv_mma_li<64, 5, TG>(wq, sb, N, K, gs, xp, M, y, yf, st);
+    case 8 * 16 + 4: return qmv_mma_li<8, 4, TG>(wq, sb, N, K, gs, xp, M, y, yf, st);
+    case 8 * 16 + 5: return qmv_mma_li<8, 5, TG>(wq, sb, N, K, gs, xp, M, y, yf, st);
+    case 4 * 16 + 4: return qmv_mma_li<4, 4, TG>(wq, sb, N, K, gs, xp, M, y, yf, st);
+    case 4 * 16 + 5: return qmv_mma_li<4, 5, TG>(wq, sb, N, K, gs, xp, M, y, yf, st);
     default: return hipErrorNotSupported;
   }
 }
 
-template <int L, int IT>
+template <int L, int IT, int TG>
 constexpr bool mma_any_c() {
-  return mma_c_ok<L, IT, 2>() || mma_c_ok<L, IT, 4>() || mma_c_ok<L, IT, 8>();
+  return mma_c_ok<L, IT, 2, TG>() || mma_c_ok<L, IT, 4, TG>() || mma_c_ok<L, IT, 8, TG>();
 }
 
+template <int TG>
 static bool qmv_mma_shape(int K) {
   const int nb = K / 32, L = lanes_for_blocks(nb), IT = nb / L;
   switch (L * 16 + IT) {
-    case 16 * 16 + 4: return mma_any_c<16, 4>();
-    case 16 * 16 + 5: return mma_any_c<16, 5>();
-    case 32 * 16 + 4: return mma_any_c<32, 4>();
-    case 32 * 16 + 6: return mma_any_c<32, 6>();
-    case 64 * 16 + 4: return mma_any_c<64, 4>();
-    case 64 * 16 + 5: return mma_any_c<64, 5>();
-    case 8 * 16 + 4: return mma_any_c<8, 4>();
-    case 8 * 16 + 5: return mma_any_c<8, 5>();
-    case 4 * 16 + 4: return mma_any_c<4, 4>();
-    case 4 * 16 + 5: return mma_any_c<4, 5>();
+    case 16 * 16 + 4: return mma_any_c<16, 4, TG>();
+    case 16 * 16 + 5: return mma_any_c<16, 5, TG>();
+    case 32 * 16 + 4: return mma_any_c<32, 4, TG>();
+    case 32 * 16 + 6: return mma_any_c<32, 6, TG>();
+    case 64 * 16 + 4: return mma_any_c<64, 4, TG>();
+    case 64 * 16 + 5: return mma_any_c<64, 5, TG>();
+    case 8 * 16 + 4: return mma_any_c<8, 4, TG>();
+    case 8 * 16 + 5: return mma_any_c<8, 5, TG>();
+    case 4 * 16 + 4: return mma_any_c<4, 4, TG>();
+    case 4 * 16 + 5: return mma_any_c<4, 5, TG>();
     default: return false;
   }
 }
 
 hipError_t launch_qmv(const uint32_t* wq, const bf16* s, const bf16* b, const uint32_t* sb, int N, int K, int gs,
                       const uint32_t* xp, int M, bf16* y, float* yf, hipStream_t st) {
-  if (M >= 2 && qmv_mma_ok(sb, K, 2) && qmv_mma_shape(K)) {  // matrix cores, four tokens per launch
-    for (int m0 = 0; m0 < M; m0 += MMA_TOK) {
+  if (M >= 2 && qmv_mma_ok(sb, K, 2) && qmv_mma_shape<1>(K)) {  // matrix cores
+    if (M > MMA_TOK && qmv_mma_ok(sb, K, M) && qmv_mma_shape<2>(K)) {  // five to eight tokens: one launch
+      const hipError_t e = qmv_mma<2>(wq, sb, N, K, gs, xp, M, y, yf, st);
+      if (e != hipErrorNotReady) return e;
+    }
+    for (int m0 = 0; m0 < M; m0 += MMA_TOK) {  // else four tokens per launch
       const int mc = M - m0 < MMA_TOK ? M - m0 : MMA_TOK;
       const uint32_t* xpc = xp + (size_t)m0 * (K / 32) * XP_DW;
       bf16* yc = y + (size_t)m0 * N;
       float* yfc = yf ? yf + (size_t)m0 * N : nullptr;
-      const hipError_t e = mc >= 2 ? qmv_mma(wq, sb, N, K, gs, xpc, mc, yc, yfc, st)
+      const hipError_t e = mc >= 2 ? qmv_mma<1>(wq, sb, N, K, gs, xpc, mc, yc, yfc, st)
                                    : qmv_tokens(wq, s, b, sb, N, K, gs, xpc, mc, yc, yfc, st);
       if (e != hipSuccess) return e;
     }

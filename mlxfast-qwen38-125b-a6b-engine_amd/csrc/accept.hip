@@ -10,7 +10,7 @@
 
 namespace mtpx {
 
-constexpr int AM_SPAN = 8192;  // elements per argmax partial
+constexpr int AM_SPAN = 2048;  // elements per argmax partial (8 per thread, loaded together)
 
 struct VI {
   float v;
@@ -54,8 +54,19 @@ __global__ __launch_bounds__(256) void k_argmax_part(const T* __restrict__ x, in
   const T* xr = x + (size_t)row * V;
   const int64_t b = (int64_t)part * AM_SPAN;
   const int64_t e = b + AM_SPAN < V ? b + AM_SPAN : V;
+  constexpr int PER = AM_SPAN / 256;
+  float v[PER];  // every load issued before the first comparison (past the end: the slice's first element again)
+#pragma unroll
+  for (int u = 0; u < PER; ++u) {
+    const int64_t i = b + threadIdx.x + 256 * u;
+    v[u] = ld_val(xr + (i < e ? i : b));
+  }
   VI best{-__uint_as_float(0x7f800000u), 0x7fffffff};
-  for (int64_t i = b + threadIdx.x; i < e; i += 256) best = vi_best(best, VI{ld_val(xr + i), (int)i});
+#pragma unroll
+  for (int u = 0; u < PER; ++u) {
+    const int64_t i = b + threadIdx.x + 256 * u;
+    if (i < e) best = vi_best(best, VI{v[u], (int)i});
+  }
   best = wave_best(best);
   if ((threadIdx.x & 63) == 0) wb[threadIdx.x >> 6] = best;
   __syncthreads();

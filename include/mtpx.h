@@ -603,7 +603,9 @@ int mtpx_session_reset(mtpx_session s);
  * last position, which becomes the carry.  Synchronises once. */
 int mtpx_session_prefill(mtpx_session s, const int32_t* ids, int n, int32_t* first_token);
 /* One round of draft depth k (0..MTPX_MAX_DRAFT_DEPTH); force may be NULL.  tokens (host, k+1
- * entries) receives the n + 1 committed tokens, *n_tokens = n + 1. */
+ * entries) receives the n + 1 committed tokens, *n_tokens = n + 1.  A prefill or round that fails
+ * after it began (e.g. a prompt longer than the caches: its first windows are committed) leaves the
+ * session refusing every prefill and round with MTPX_ERR_STATE until mtpx_session_reset. */
 int mtpx_round(mtpx_session s, int k, const mtpx_force_params* force, int32_t* tokens, int* n_tokens);
 /* Committed offset; the session's target state and drafter (owned by the session). */
 int mtpx_session_info(mtpx_session s, int64_t* offset, mtpx_target_state* state, mtpx_drafter* drafter);

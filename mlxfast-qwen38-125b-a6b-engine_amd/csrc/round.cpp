@@ -44,6 +44,7 @@ struct Session {
   int32_t* host = nullptr;     // pinned [OUT_WORDS]
   int64_t offset = 0;          // committed positions (mirrors the target state)
   bool primed = false;         // a carry exists (after prefill)
+  bool broken = false;         // a prefill or round failed part way: refused until mtpx_session_reset
 };
 
 #define RC(expr)             \
@@ -139,14 +140,25 @@ int mtpx_session_reset(mtpx_session sh) {
   }
   s->offset = 0;
   s->primed = false;
+  s->broken = false;
   return MTPX_OK;
 }
+
+static int prefill_windows(Session* s, const int32_t* ids, int n, int32_t* first_token);
+static int round_steps(Session* s, int k, const mtpx_force_params* force, int32_t* tokens, int* n_tokens);
 
 int mtpx_session_prefill(mtpx_session sh, const int32_t* ids, int n, int32_t* first_token) {
   Session* s = static_cast<Session*>(sh.ctx);
   if (!s || !ids || n < 1) return set_error(MTPX_ERR_ARG, "session prefill: bad argument");
+  if (s->broken) return set_error(MTPX_ERR_STATE, "session: a previous call failed part way (reset it)");
   if (s->primed) return set_error(MTPX_ERR_STATE, "session prefill: the session already holds a context");
   if (s->offset + n > MTPX_INDEXER_BUDGET) return set_error(MTPX_ERR_ARG, "session prefill: past the indexer budget");
+  const int rc = prefill_windows(s, ids, n, first_token);
+  if (rc) s->broken = true;  // windows may have been committed: the caches no longer match the offset
+  return rc;
+}
+
+static int prefill_windows(Session* s, const int32_t* ids, int n, int32_t* first_token) {
   for (int off = 0; off < n; off += 8) {
     const int S = n - off < 8 ? n - off : 8;
     const bool last = off + S == n;
@@ -170,12 +182,19 @@ int mtpx_session_prefill(mtpx_session sh, const int32_t* ids, int n, int32_t* fi
 int mtpx_round(mtpx_session sh, int k, const mtpx_force_params* force, int32_t* tokens, int* n_tokens) {
   Session* s = static_cast<Session*>(sh.ctx);
   if (!s || !tokens || !n_tokens) return set_error(MTPX_ERR_ARG, "round: null argument");
+  if (s->broken) return set_error(MTPX_ERR_STATE, "session: a previous call failed part way (reset it)");
   if (!s->primed) return set_error(MTPX_ERR_STATE, "round: no context (prefill first)");
   if (k < 0 || k > MTPX_MAX_DRAFT_DEPTH || (k > 0 && !s->drafter.ctx))
     return set_error(MTPX_ERR_ARG, "round: draft depth out of range (or no drafter)");
   if (s->offset + k + 1 > MTPX_INDEXER_BUDGET) return set_error(MTPX_ERR_ARG, "round: past the indexer budget");
   if (force && force->teacher && (force->rate < 0.0f || force->rate > 1.0f))
     return set_error(MTPX_ERR_ARG, "round: forcing rate outside [0, 1]");
+  const int rc = round_steps(s, k, force, tokens, n_tokens);
+  if (rc) s->broken = true;  // drafter and target may have advanced apart
+  return rc;
+}
+
+static int round_steps(Session* s, int k, const mtpx_force_params* force, int32_t* tokens, int* n_tokens) {
   const int64_t o = s->offset;
   for (int i = 0; i < k; ++i) {
     RC(mtpx_drafter_step(s->drafter, s->ids + i, i == 0 ? s->carry : s->mo + (size_t)(i - 1) * s->W, s->ids + i + 1,

@@ -166,3 +166,22 @@ def test_round_refusals(model):
         ns.round(1)
     ns.round(0)
     ns.close()
+
+
+def test_failed_prefill_breaks_the_session_until_reset(model):
+    """A prompt longer than the caches fails in its last windows after earlier windows were
+    committed: the session refuses further calls until reset, then works again."""
+    import mtpx
+    ctx, t, head, prompt = model
+    P = LAYER["max_positions"]
+    long_prompt = np.random.default_rng(34).integers(0, TARGET["vocab"], P + 4).astype(np.int32)
+    s = mtpx.Session(ctx, t, head)
+    with pytest.raises(mtpx.MtpxError):
+        s.prefill(dev(long_prompt))
+    with pytest.raises(mtpx.MtpxError, match="reset"):
+        s.round(1)
+    s.reset()
+    first = s.prefill(dev(prompt))
+    assert [first] + s.round(0) == serial(model)[:2]
+    s.close()
+

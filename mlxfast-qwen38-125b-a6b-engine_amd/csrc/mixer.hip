@@ -55,15 +55,16 @@ __global__ __launch_bounds__(MIX_THREADS) __attribute__((amdgpu_waves_per_eu(1, 
   const uint32_t* sb = inj ? a.isb : a.dsb;
   // stage the class's blocks with LDS-direct loads: compact block c = subc' + LC * it holds
   // block g + Q * subc' + L * it; unit i = (s * ncb + c) * 7 + q
+  QRow<L, IT> R;
+  R.load(wq + (size_t)rr * (W / 8), sc + (size_t)rr * ng, bi + (size_t)rr * ng, sb ? sb + (size_t)rr * P : nullptr,
+         nb, a.gs, sub, valid);
+  asm volatile("" ::: "memory");
   const int n4 = S * ncb * (XP_DW / 4);
   for (int i = threadIdx.x; i < n4; i += MIX_THREADS) {
     const int q = i % (XP_DW / 4), c = (i / (XP_DW / 4)) % ncb, s = i / (XP_DW / 4) / ncb;
     const int j = g + Q * (c % LC) + L * (c / LC);
     lds_dma16(reinterpret_cast<uint4*>(lds) + (i - lane), a.xpW + ((size_t)s * nb + j) * XP_DW + 4 * q);
   }
-  QRow<L, IT> R;
-  R.load(wq + (size_t)rr * (W / 8), sc + (size_t)rr * ng, bi + (size_t)rr * ng, sb ? sb + (size_t)rr * P : nullptr,
-         nb, a.gs, sub, valid);
   lds_dma_wait();
   __syncthreads();
   for (int s = 0; s < S; ++s) {
@@ -101,6 +102,8 @@ __global__ __launch_bounds__(UP_THREADS) __attribute__((amdgpu_waves_per_eu(1, 2
   __shared__ bf16 act[MAX_TOKENS * 512];             // [S][LW], S * LW <= 4096
   __shared__ uint32_t xpa[MAX_TOKENS * 12 * XP_DW];  // [S][LW/32][XP_DW], S * LW / 32 <= 96
   __shared__ bf16 wl[MAX_TOKENS][MAXROWS];
+  constexpr int MIX_ROUNDS = MAX_TOKENS * MAXROWS / UP_THREADS;  // (token, stream, position) terms per thread
+  __shared__ float term[MAX_TOKENS * MAXROWS];                    // [S][hc][32] bf16(sigmoid(w) * n)
   const int S = a.S, H = a.H, hc = a.hc, LW = a.LW, W = hc * H;
   const int NR = LW + (a.iw ? hc : 0);
   const int nbA = LW / 32, ng = LW / a.gs, P = sb_row_len(LW, a.gs);
@@ -125,11 +128,16 @@ __global__ __launch_bounds__(UP_THREADS) __attribute__((amdgpu_waves_per_eu(1, 2
 #pragma unroll
   for (int q = 0; q < QD; ++q)
     jp[q] = jt ? a.part[(size_t)q * S * NR + (size_t)(threadIdx.x / hc) * NR + LW + threadIdx.x % hc] : 0.0f;
-  const int ms = threadIdx.x >> 5, mi = threadIdx.x & 31;  // the mix: 32 lanes per token
-  float nv[8];  // unconditional loads (token and stream clamped); the mix reads only s < S, c < hc
+  // the mix's terms: thread i of round r takes (token, stream, position) u = r * UP_THREADS + i,
+  // u = (s * hc + c) * 32 + position; unconditional loads (clamped), used only for u < S * hc * 32
+  const int nterm = S * hc * 32;
+  float nv[MIX_ROUNDS];
 #pragma unroll
-  for (int c = 0; c < 8; ++c)
-    nv[c] = bf2f(a.normed[(size_t)(ms < S ? ms : 0) * W + (size_t)(c < hc ? c : 0) * H + d0 + mi]);
+  for (int r = 0; r < MIX_ROUNDS; ++r) {
+    const int u0 = r * UP_THREADS + (int)threadIdx.x, u = u0 < nterm ? u0 : nterm - 1;
+    const int sc = u >> 5;  // s * hc + c
+    nv[r] = bf2f(a.normed[(size_t)(sc / hc) * W + (size_t)(sc % hc) * H + d0 + (u & 31)]);
+  }
   QRow<L, IT> U[NP];
 #pragma unroll
   for (int p = 0; p < NP; ++p) {
@@ -140,11 +148,13 @@ __global__ __launch_bounds__(UP_THREADS) __attribute__((amdgpu_waves_per_eu(1, 2
     U[p].load(a.uw + (size_t)gr * (LW / 8), a.us + (size_t)gr * ng, a.ub + (size_t)gr * ng,
               a.usb ? a.usb + (size_t)gr * P : nullptr, nbA, a.gs, sub, v);
   }
-  // low-rank rows: finish the fold, round, SiLU (past the end: the last element again, same value)
+  // low-rank rows: finish the fold, round, SiLU
 #pragma unroll
   for (int u = 0; u < FOLD_BATCH; ++u) {
+    if (u * UP_THREADS >= S * LW) break;  // uniform: only the batches that hold rows
     const int i = threadIdx.x + u * UP_THREADS;
-    act[i < S * LW ? i : S * LW - 1] = f2bf(silu_bf16(round_bf(class_fold_v<QD>(pp[u]))));
+    const bf16 v = f2bf(silu_bf16(round_bf(class_fold_v<QD>(pp[u]))));
+    if (i < S * LW) act[i] = v;
   }
   if (jt) a.j[threadIdx.x] = f2bf(2.0f * sigmoid_bf16(round_bf(class_fold_v<QD>(jp))));  // [s * hc + c]
   __syncthreads();
@@ -165,12 +175,22 @@ __global__ __launch_bounds__(UP_THREADS) __attribute__((amdgpu_waves_per_eu(1, 2
     }
   }
   __syncthreads();
-  // mix: 32 lanes per token, then the prepared block of x
+  // mix: every term bf16(sigmoid(w) * n) by its own thread, then the running sum over the streams
+  // (in stream order) by 32 lanes per token, and the prepared block of x
+#pragma unroll
+  for (int r = 0; r < MIX_ROUNDS; ++r) {
+    if (r * UP_THREADS >= nterm) break;  // uniform
+    const int u = r * UP_THREADS + (int)threadIdx.x, uc = u < nterm ? u : nterm - 1;
+    const float tv = round_bf(sigmoid_bf16(bf2f(wl[(uc >> 5) / hc][((uc >> 5) % hc) * 32 + (uc & 31)])) * nv[r]);
+    if (u < nterm) term[u] = tv;
+  }
+  __syncthreads();
+  const int ms = threadIdx.x >> 5, mi = threadIdx.x & 31;
   if (ms < S) {
     float acc = 0.0f;
 #pragma unroll
     for (int c = 0; c < 8; ++c)
-      if (c < hc) acc = round_bf(acc + round_bf(sigmoid_bf16(bf2f(wl[ms][c * 32 + mi])) * nv[c]));
+      if (c < hc) acc = round_bf(acc + term[(ms * hc + c) * 32 + mi]);
     const bf16 y = f2bf(acc);
     a.x[(size_t)ms * H + d0 + mi] = y;
     if (a.xpH) xprep_lanes_direct(y, mi, a.xpH + ((size_t)ms * (H / 32) + blockIdx.x) * XP_DW);

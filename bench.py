@@ -470,7 +470,7 @@ def step_bytes_of(lc, tc, kinds, uniq, M, T0, gs):
 
 
 def serial_token_bytes(lc, tc, gs):
-    """Active weight bytes of one serial decode token (gs64 3.823 GB): every dense matrix, the
+    """Active weight bytes of one serial decode token (3.823 GB at gs64): every dense matrix, the
     router, top-k + shared experts, the PLE projections, lm_head; caches excluded."""
     H, hc, W, LW = lc["hidden"], tc["hc"], tc["hc"] * lc["hidden"], tc["lowrank"]
     F, E, K = lc["expert_width"], lc["experts"], lc["top_k"]

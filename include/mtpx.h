@@ -570,11 +570,24 @@ int mtpx_target_verify(mtpx_ctx ctx, mtpx_target t, mtpx_target_state st, const 
                        uint16_t* logits, uint16_t* multi, uint16_t* mixed);
 /* The first n (0..window) positions of the last verify become committed. */
 int mtpx_target_commit(mtpx_target_state st, int n);
+/* Prefill: S >= 1 prompt tokens (device int32) at the committed offset, processed and committed
+ * (an open verify window is discarded first) -> logits bf16 [vocab] of the LAST position and multi
+ * bf16 [S, hc*hidden] of every position (each may be NULL).  Every output and the state it leaves
+ * equal those of verifying and committing the tokens in windows of 8 in turn; the work runs over
+ * batches of up to 256 positions at once: one launch per kernel for the whole batch where each
+ * position's result is its own (GEMVs on the matrix cores in windows of eight tokens with the
+ * weights shared through L2, norms, mixers, attention -- every query attends to the keys up to its
+ * own position --, the MoE as windows of 8 in batched launches), the GDN and PLE recurrences window
+ * by window.  Replaces the runner's prompt prefill windows (Runner/FastModel/TrackP12Prefill.swift:1-237,
+ * TrackPrefillSort.swift:1-201, TrackPrefillIndirect.swift:5-227), with the decode path's arithmetic
+ * instead of MLX's steel GEMM: the prompt's positions get the bits the verify path gives them. */
+int mtpx_target_prefill(mtpx_ctx ctx, mtpx_target t, mtpx_target_state st, const int32_t* ids, int S,
+                        uint16_t* logits, uint16_t* multi);
 /* Distinct routed experts of each layer's MoE in the last verify (host int32 [num_layers];
  * synchronises), for the algorithmic byte count of the expert GEMVs. */
 int mtpx_target_moe_unique(mtpx_ctx ctx, mtpx_target_state st, int32_t* out);
 
-/* ---- the speculative round, device-resident (SURVEY's mtpx_round) ---------------------------
+/* ---- the speculative round, device-resident ------------------------------------------------
  * A session = one request: the target's caches, the drafter's request state and the carry (the
  * next input token with the target multi stream of the position before it).  mtpx_round runs
  * k drafter steps, the verify of the carry + k drafts, the greedy accept on the device, ONE
@@ -598,9 +611,10 @@ int mtpx_session_new(mtpx_ctx ctx, mtpx_target target, mtpx_head head, mtpx_sess
 int mtpx_session_free(mtpx_session s);
 /* Back to an empty request (caches reset, a fresh drafter state). */
 int mtpx_session_reset(mtpx_session s);
-/* The prompt (device int32 [n], offset + n <= MTPX_INDEXER_BUDGET): verify windows of <= 8
- * tokens, each committed and observed by the drafter; *first_token (host) = the argmax of the
- * last position, which becomes the carry.  Synchronises once. */
+/* The prompt (device int32 [n], offset + n <= MTPX_INDEXER_BUDGET): mtpx_target_prefill in batches
+ * of up to 256 positions, each committed and its multi streams observed by the drafter;
+ * *first_token (host) = the argmax of the last position, which becomes the carry.  Synchronises
+ * once. */
 int mtpx_session_prefill(mtpx_session s, const int32_t* ids, int n, int32_t* first_token);
 /* One round of draft depth k (0..MTPX_MAX_DRAFT_DEPTH); force may be NULL.  tokens (host, k+1
  * entries) receives the n + 1 committed tokens, *n_tokens = n + 1.  A prefill or round that fails

@@ -242,8 +242,8 @@ int mix_classes(int W) {
 // spilling), the low-rank activations and their prepared blocks within LDS.
 bool mix_supported(int H, int hc, int LW, int S) {
   const int nb = hc * H / 32, L = lanes_for_blocks(nb);
-  return nb % L == 0 && nb / L >= 4 && nb / L <= 7 && hc <= 8 && LW % 32 == 0 && lanes_for_blocks(LW / 32) <= 4 &&
-         S * LW <= MAX_TOKENS * 512 &&
+  return S >= 1 && S <= MAX_TOKENS && nb % L == 0 && nb / L >= 4 && nb / L <= 7 && hc <= 8 && LW % 32 == 0 &&
+         lanes_for_blocks(LW / 32) <= 4 && S * LW <= MAX_TOKENS * 512 &&
          S * (LW / 32) <= MAX_TOKENS * 12 && H % 32 == 0;
 }
 

@@ -40,6 +40,28 @@ namespace mtpx {
 // rank) slot), with its slots ordered by token.  No serial loop over slots or
 // experts: leaders by an LDS minimum, expert offsets by a wave scan.
 constexpr int ROUTE_EPER = 16;  // E <= 1024
+
+// Window w of a batched launch (grid dimension w, a.nwin windows of a.M tokens): the pointers of
+// its tokens and slots, its dispatch table and its ticket.
+__device__ __forceinline__ MoeArgs moe_window(MoeArgs a, int w) {
+  if (w == 0) return a;
+  const size_t t = (size_t)w * a.M, sl = t * (a.K + 1);
+  a.x += t * a.H;
+  if (a.y) a.y += t * a.H;
+  a.logits += t * a.E;
+  a.gate_logit += t;
+  a.idx += t * a.K;
+  a.w += t * a.K;
+  a.disp += w;
+  a.xp_x += t * (a.H / 32) * XP_DW;
+  a.act += sl * a.F;
+  a.r += sl * a.H;
+  if (a.resid) a.resid += t * a.H;
+  if (a.y2) a.y2 += t * a.H;
+  a.ticket += w;
+  if (a.nu_out) a.nu_out += w;
+  return a;
+}
 constexpr int RR_THREADS = 512;
 static_assert(MAX_TOKENS * MAX_TOPK <= 128, "the slots fit the first two waves");
 
@@ -185,7 +207,8 @@ __device__ void route_body(const MoeArgs& a) {
 // block) and take no ticket.
 constexpr int ROUTER_IT = 8;  // H <= 8 * 64 * 8
 
-__global__ __launch_bounds__(RR_THREADS) void k_moe_router_route(MoeArgs a, int row_wgs) {
+__global__ __launch_bounds__(RR_THREADS) void k_moe_router_route(MoeArgs a0, int row_wgs) {
+  const MoeArgs a = moe_window(a0, blockIdx.y);
   const int H = a.H, E = a.E, M = a.M;
   if ((int)blockIdx.x >= row_wgs) {
     const int nb = H / 32;
@@ -327,7 +350,9 @@ __device__ __forceinline__ void gate_up_compute(const MoeArgs& a, GateUpItem<L, 
 }
 
 template <int L, int IT, bool PK, int NIT>
-__global__ __launch_bounds__(GU_THREADS) void k_moe_gate_up(MoeArgs a, const int32_t* __restrict__ ids) {
+__global__ __launch_bounds__(GU_THREADS) void k_moe_gate_up(MoeArgs a0, const int32_t* __restrict__ ids) {
+  const MoeArgs a = moe_window(a0, blockIdx.y);
+  ids += (size_t)blockIdx.y * a0.M * a0.K;
   extern __shared__ uint32_t lds[];  // [2][H/32][XP_DW]
   constexpr int RW = 64 / L;         // f rows per wave
   constexpr int WAVES = GU_THREADS / 64;
@@ -406,7 +431,8 @@ __device__ __forceinline__ float colsum_small(const float* r, int K) {
 // K is a template parameter so the K + 1 row loads are issued together and the
 // fold is unrolled (a runtime-K loop waits for each load in turn).
 template <int K>
-__global__ __launch_bounds__(256) void k_moe_combine(MoeArgs a) {
+__global__ __launch_bounds__(256) void k_moe_combine(MoeArgs a0) {
+  const MoeArgs a = moe_window(a0, blockIdx.z);
   const int m = blockIdx.y, h = blockIdx.x * 256 + threadIdx.x;
   if (h >= a.H) return;
   const int H = a.H, M = a.M;
@@ -474,7 +500,9 @@ __device__ __forceinline__ void down_load(const DownMats rm, const DownMats sm, 
 }
 
 template <int L, int IT, bool PK, int NIT>
-__global__ __launch_bounds__(DN_THREADS) void k_moe_down(MoeArgs a, const int32_t* __restrict__ ids) {
+__global__ __launch_bounds__(DN_THREADS) void k_moe_down(MoeArgs a0, const int32_t* __restrict__ ids) {
+  const MoeArgs a = moe_window(a0, blockIdx.y);
+  ids += (size_t)blockIdx.y * a0.M * a0.K;
   extern __shared__ uint32_t lds[];  // [2][F/32][XP_DW]
   constexpr int RW = 64 / L;
   constexpr int DR = (DN_THREADS / 64) * 2 * RW;
@@ -555,7 +583,8 @@ template <int L>
 constexpr int dd_gate_up_rows() { return 4 * (64 / L) > 16 ? 4 * (64 / L) : 16; }
 
 template <int L, int IT, bool PK>
-__global__ __launch_bounds__(DD_THREADS) void k_moe_gate_up_dd(MoeArgs a) {
+__global__ __launch_bounds__(DD_THREADS) void k_moe_gate_up_dd(MoeArgs a0) {
+  const MoeArgs a = moe_window(a0, blockIdx.y);
   extern __shared__ uint32_t lds[];  // [H/32][XP_DW]: the slot's token
   constexpr int RW = 64 / L;
   constexpr int UR = dd_gate_up_rows<L>();
@@ -615,7 +644,8 @@ template <int L>
 constexpr int dd_down_rows() { return 4 * (64 / L); }
 
 template <int L, int IT, bool PK>
-__global__ __launch_bounds__(DD_THREADS) void k_moe_down_dd(MoeArgs a) {
+__global__ __launch_bounds__(DD_THREADS) void k_moe_down_dd(MoeArgs a0) {
+  const MoeArgs a = moe_window(a0, blockIdx.y);
   extern __shared__ uint32_t lds[];  // [F/32][XP_DW]
   constexpr int RW = 64 / L;
   constexpr int DR = dd_down_rows<L>();
@@ -671,7 +701,8 @@ hipError_t launch_moe_router_route(const MoeArgs& a, hipStream_t st) {
   static size_t cur = 0;
   const hipError_t e = ensure_lds(k_moe_router_route, lds + 16 * 1024, cur);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(k_moe_router_route, dim3(row_wgs + prep_wgs), dim3(RR_THREADS), lds, st, a, row_wgs);
+  if (a.nwin < 1 || a.nwin > MOE_TICKETS) return hipErrorInvalidValue;  // a ticket per window
+  hipLaunchKernelGGL(k_moe_router_route, dim3(row_wgs + prep_wgs, a.nwin), dim3(RR_THREADS), lds, st, a, row_wgs);
   return hipGetLastError();
 }
 
@@ -681,7 +712,7 @@ static hipError_t gate_up_nit(const MoeArgs& a, int grid, hipStream_t st) {
   static size_t cur = 0;
   hipError_t e = ensure_lds(k_moe_gate_up<L, IT, PK, NIT>, lds, cur);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((k_moe_gate_up<L, IT, PK, NIT>), dim3(grid), dim3(GU_THREADS), lds, st, a,
+  hipLaunchKernelGGL((k_moe_gate_up<L, IT, PK, NIT>), dim3(grid, a.nwin), dim3(GU_THREADS), lds, st, a,
                      (const int32_t*)a.idx);
   return hipGetLastError();
 }
@@ -717,7 +748,8 @@ static hipError_t down_nit(const MoeArgs& a, int grid, hipStream_t st) {
   static size_t cur = 0;
   hipError_t e = ensure_lds(k_moe_down<L, IT, PK, NIT>, lds, cur);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((k_moe_down<L, IT, PK, NIT>), dim3(grid), dim3(DN_THREADS), lds, st, a, (const int32_t*)a.idx);
+  hipLaunchKernelGGL((k_moe_down<L, IT, PK, NIT>), dim3(grid, a.nwin), dim3(DN_THREADS), lds, st, a,
+                     (const int32_t*)a.idx);
   return hipGetLastError();
 }
 
@@ -751,7 +783,7 @@ hipError_t launch_moe_down(const MoeArgs& a, hipStream_t st) { MTPX_QROW_DISPATC
 
 template <int K>
 static hipError_t combine_k(const MoeArgs& a, hipStream_t st) {
-  hipLaunchKernelGGL(k_moe_combine<K>, dim3((a.H + 255) / 256, a.M), dim3(256), 0, st, a);
+  hipLaunchKernelGGL(k_moe_combine<K>, dim3((a.H + 255) / 256, a.M, a.nwin), dim3(256), 0, st, a);
   return hipGetLastError();
 }
 
@@ -791,7 +823,7 @@ static hipError_t gate_up_dd_pk(const MoeArgs& a, hipStream_t st) {
     if (e != hipSuccess) return e;
     if (a.F % dd_gate_up_rows<L>() != 0) return hipErrorInvalidValue;
     const int units = a.M * (a.K + 1) * (a.F / dd_gate_up_rows<L>());
-    hipLaunchKernelGGL((k_moe_gate_up_dd<L, IT, PK>), dim3((units + 7) / 8 * 8), dim3(DD_THREADS), lds, st, a);
+    hipLaunchKernelGGL((k_moe_gate_up_dd<L, IT, PK>), dim3((units + 7) / 8 * 8, a.nwin), dim3(DD_THREADS), lds, st, a);
     return hipGetLastError();
   }
 }
@@ -810,7 +842,7 @@ static hipError_t down_dd_pk(const MoeArgs& a, hipStream_t st) {
   hipError_t e = ensure_lds(k_moe_down_dd<L, IT, PK>, lds, cur);
   if (e != hipSuccess) return e;
   const int units = a.M * (a.K + 1) * nhb;
-  hipLaunchKernelGGL((k_moe_down_dd<L, IT, PK>), dim3((units + 7) / 8 * 8), dim3(DD_THREADS), lds, st, a);
+  hipLaunchKernelGGL((k_moe_down_dd<L, IT, PK>), dim3((units + 7) / 8 * 8, a.nwin), dim3(DD_THREADS), lds, st, a);
   return hipGetLastError();
 }
 

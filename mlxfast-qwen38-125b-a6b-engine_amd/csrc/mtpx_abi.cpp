@@ -205,19 +205,24 @@ int moe_check(const mtpx_moe_weights* w, int M) {
   return MTPX_OK;
 }
 
-size_t moe_ws_bytes(const mtpx_moe_weights* w, int M) {
+size_t moe_ws_bytes(const mtpx_moe_weights* w, int M, int nwin = 1) {
   const int H = w->hidden, E = w->experts, K = w->top_k, F = w->expert_width;
-  const int slots = M * (K + 1);
-  return al(4 * (size_t)M * E) + al(4 * (size_t)M) + al(4 * (size_t)M * K) * 2 + al(sizeof(MoeDispatch)) +
-         al(4 * (size_t)M * (H / 32) * XP_DW) + al(2 * (size_t)slots * F) +
-         al(2 * (size_t)slots * H) + 4096;
+  const size_t T = (size_t)M * nwin, slots = T * (K + 1);
+  return al(4 * T * E) + al(4 * T) + al(4 * T * K) * 2 + al(sizeof(MoeDispatch) * (size_t)nwin) +
+         al(4 * T * (H / 32) * XP_DW) + al(2 * slots * F) + al(2 * slots * H) + 4096;
+}
+
+// Workspace of S tokens through moe_enqueue_windows (its launches reuse one region in turn).
+size_t moe_windows_ws_bytes(const mtpx_moe_weights* w, int S) {
+  const int full = S / MAX_TOKENS < MOE_TICKETS ? S / MAX_TOKENS : MOE_TICKETS, tail = S % MAX_TOKENS;
+  return std::max(full ? moe_ws_bytes(w, MAX_TOKENS, full) : (size_t)0, tail ? moe_ws_bytes(w, tail) : (size_t)0);
 }
 
 
 // Enqueue the MoE block; workspace already reserved.
 int moe_enqueue(Ctx* c, const mtpx_moe_weights* w, const uint16_t* x, int M, uint16_t* y, int32_t* idx,
                 float* wts, float* logits, const uint16_t* resid = nullptr, uint16_t* y2 = nullptr,
-                uint32_t* xp_ready = nullptr, int32_t* nu_out = nullptr) {
+                uint32_t* xp_ready = nullptr, int32_t* nu_out = nullptr, int nwin = 1) {
   MoeArgs a;
   a.H = w->hidden;
   a.E = w->experts;
@@ -237,16 +242,17 @@ int moe_enqueue(Ctx* c, const mtpx_moe_weights* w, const uint16_t* x, int M, uin
   a.sh_gate_sb = w->sh_gate_sb; a.sh_up_sb = w->sh_up_sb; a.sh_down_sb = w->sh_down_sb;
   a.x = x;
   a.y = y;
-  const int slots = M * (a.K + 1);
-  a.logits = logits ? logits : ws_take<float>(c, (size_t)M * a.E);
-  a.gate_logit = ws_take<float>(c, M);
-  a.idx = idx ? idx : ws_take<int32_t>(c, (size_t)M * a.K);
-  a.w = wts ? wts : ws_take<float>(c, (size_t)M * a.K);
-  a.disp = ws_take<MoeDispatch>(c, 1);
-  a.xp_x = xp_ready ? xp_ready : ws_take<uint32_t>(c, (size_t)M * (a.H / 32) * XP_DW);
+  a.nwin = nwin;
+  const size_t T = (size_t)M * nwin, slots = T * (a.K + 1);
+  a.logits = logits ? logits : ws_take<float>(c, T * a.E);
+  a.gate_logit = ws_take<float>(c, T);
+  a.idx = idx ? idx : ws_take<int32_t>(c, T * a.K);
+  a.w = wts ? wts : ws_take<float>(c, T * a.K);
+  a.disp = ws_take<MoeDispatch>(c, nwin);
+  a.xp_x = xp_ready ? xp_ready : ws_take<uint32_t>(c, T * (a.H / 32) * XP_DW);
   a.xp_ready = xp_ready != nullptr;
-  a.act = ws_take<uint16_t>(c, (size_t)slots * a.F);
-  a.r = ws_take<uint16_t>(c, (size_t)slots * a.H);
+  a.act = ws_take<uint16_t>(c, slots * a.F);
+  a.r = ws_take<uint16_t>(c, slots * a.H);
   a.resid = resid;
   a.y2 = y2;
   a.ticket = c->tickets;
@@ -266,6 +272,32 @@ int moe_enqueue(Ctx* c, const mtpx_moe_weights* w, const uint16_t* x, int M, uin
   LAUNCH(c, "moe_gate_up", launch_moe_gate_up(a, c->stream));
   LAUNCH(c, "moe_down", launch_moe_down(a, c->stream));
   LAUNCH(c, "moe_combine", launch_moe_combine(a, c->stream));
+  return MTPX_OK;
+}
+
+// S tokens of a prefill batch through the MoE block as windows of MAX_TOKENS tokens, routed and
+// computed as separate windows would be (each token's output is the window's): the full windows
+// in one batched launch per kernel, the remaining tokens as one more window.
+int moe_enqueue_windows(Ctx* c, const mtpx_moe_weights* w, const uint16_t* x, int S, uint16_t* y,
+                        uint32_t* xp_ready) {
+  const int full = S / MAX_TOKENS, tail = S % MAX_TOKENS, H = w->hidden;
+  const size_t mark = c->ws_used;
+  int rc;
+  for (int w0 = 0; w0 < full; w0 += MOE_TICKETS) {  // a ticket per window of a launch
+    const int nw = full - w0 < MOE_TICKETS ? full - w0 : MOE_TICKETS;
+    const size_t t0 = (size_t)w0 * MAX_TOKENS;
+    c->ws_used = mark;  // the previous launches' workspace is free again in stream order
+    if ((rc = moe_enqueue(c, w, x + t0 * H, MAX_TOKENS, y + t0 * H, nullptr, nullptr, nullptr, nullptr, nullptr,
+                          xp_ready ? xp_ready + t0 * (H / 32) * XP_DW : nullptr, nullptr, nw)))
+      return rc;
+  }
+  if (tail) {
+    const size_t t0 = (size_t)full * MAX_TOKENS;
+    c->ws_used = mark;
+    if ((rc = moe_enqueue(c, w, x + t0 * H, tail, y + t0 * H, nullptr, nullptr, nullptr, nullptr, nullptr,
+                          xp_ready ? xp_ready + t0 * (H / 32) * XP_DW : nullptr)))
+      return rc;
+  }
   return MTPX_OK;
 }
 
@@ -2440,7 +2472,7 @@ int mtpx_target_commit(mtpx_target_state sh, int n) {
 
 namespace {
 int target_verify_enqueue(Ctx* c, Target* t, TargetState* s, const int32_t* ids, int S, uint16_t* logits,
-                          uint16_t* multi, uint16_t* mixed, bool* launched);
+                          uint16_t* multi, uint16_t* mixed, bool* launched, bool prefill = false);
 }
 
 int mtpx_target_verify(mtpx_ctx h, mtpx_target th, mtpx_target_state sh, const int32_t* ids, int S, uint16_t* logits,
@@ -2467,9 +2499,49 @@ int mtpx_target_verify(mtpx_ctx h, mtpx_target th, mtpx_target_state sh, const i
   return rc;
 }
 
+constexpr int PREFILL_PASS = 256;  // positions per prefill batch (workspace: attention partials grow with it)
+
+int mtpx_target_prefill(mtpx_ctx h, mtpx_target th, mtpx_target_state sh, const int32_t* ids, int S,
+                        uint16_t* logits, uint16_t* multi) {
+  Ctx* c = C(h);
+  Target* t = static_cast<Target*>(th.ctx);
+  TargetState* s = static_cast<TargetState*>(sh.ctx);
+  ARG(c && t && s && ids, "null argument");
+  ARG(s->t == t, "state of another target");
+  if (s->broken) return fail(MTPX_ERR_STATE, "state left inconsistent by a failed verify; reset it first");
+  ARG(S >= 1, "S=%d", S);
+  const mtpx_layer_config& lc = t->cfg.layer;
+  ARG(s->offset + S <= lc.max_positions, "cache full (offset %lld + %d)", (long long)s->offset, S);
+  ARG(s->offset + S <= MTPX_INDEXER_BUDGET,
+      "offset %lld + %d tokens is past the indexer budget %d (the sparse-indexer path is not built)",
+      (long long)s->offset, S, MTPX_INDEXER_BUDGET);
+  if (set_device(c)) return MTPX_ERR_HIP;
+  const size_t W = (size_t)t->cfg.hc * lc.hidden;
+  for (int p0 = 0; p0 < S; p0 += PREFILL_PASS) {
+    const int n = S - p0 < PREFILL_PASS ? S - p0 : PREFILL_PASS;
+    bool launched = false;
+    const int rc = target_verify_enqueue(c, t, s, ids + p0, n, p0 + n == S ? logits : nullptr,
+                                         multi ? multi + (size_t)p0 * W : nullptr, nullptr, &launched, true);
+    if (rc) {
+      if (launched || p0 > 0) {  // some layers hold part of the batch
+        s->window = 0;
+        s->broken = true;
+      }
+      return rc;
+    }
+  }
+  return MTPX_OK;
+}
+
 namespace {
+// One window of S <= MAX_TOKENS positions (verify), or a prefill batch of S positions: the same
+// kernels over all S tokens where every token's output is its own (GEMVs, norms, mixers,
+// attention -- each query sees the keys up to its own position --, the MoE as windows of
+// MAX_TOKENS), the recurrent cores (GDN, PLE) window by window of MAX_TOKENS with each window
+// committed before the next, and the logits of the last position only.  Every output equals that
+// of the windows of MAX_TOKENS verified and committed in turn.
 int target_verify_enqueue(Ctx* c, Target* t, TargetState* s, const int32_t* ids, int S, uint16_t* logits,
-                          uint16_t* multi, uint16_t* mixed, bool* launched) {
+                          uint16_t* multi, uint16_t* mixed, bool* launched, bool prefill) {
   const mtpx_target_config& g = t->cfg;
   const mtpx_layer_config& lc = g.layer;
   const int H = lc.hidden, hc = g.hc, W = hc * H, gs = lc.group_size, HQ = lc.heads, D = lc.head_dim;
@@ -2487,9 +2559,10 @@ int target_verify_enqueue(Ctx* c, Target* t, TargetState* s, const int32_t* ids,
   const Layer* any_attn = nullptr;
   for (const TargetLayer& L : t->layers)
     if (L.attn) any_attn = L.attn;
-  const size_t per_layer = std::max(std::max(mix + moe_ws_bytes(&t->layers[0].moe, S),
-                                             mix + (any_attn ? attn_ws_bytes(any_attn, S, T) : 0)),
-                                    t->ple ? ple_ws_bytes(t->ple->cfg, S) + al(2 * (size_t)S * W) : 0) + 4096;
+  const int SW = S < MAX_TOKENS ? S : MAX_TOKENS;  // positions of one recurrent window
+  const size_t moe_ws = prefill ? moe_windows_ws_bytes(&t->layers[0].moe, S) : moe_ws_bytes(&t->layers[0].moe, S);
+  const size_t per_layer = std::max(std::max(mix + moe_ws, mix + (any_attn ? attn_ws_bytes(any_attn, S, T) : 0)),
+                                    t->ple ? ple_ws_bytes(t->ple->cfg, SW) + al(2 * (size_t)S * W) : 0) + 4096;
   const size_t fixed = al(2 * (size_t)S * H) * 5 + al(2 * (size_t)S * W) * 4 + al(2 * (size_t)S * hc) * 2 +
                        al(4 * (size_t)S * (W / 32) * XP_DW) + al(4 * (size_t)S * XB * XP_DW) +
                        al(4 * (size_t)S * (VD / 32) * XP_DW) + al(2 * (size_t)S * gg.pw) + 4096;
@@ -2524,7 +2597,15 @@ int target_verify_enqueue(Ctx* c, Target* t, TargetState* s, const int32_t* ids,
       LAUNCH(c, "hc_norm", launch_hc_norm(first ? e : sM, first ? nullptr : mo, first ? nullptr : jM, S, hc, H,
                                           first ? 1 : 0, L.attn_hc.norm_scale, eps, sA, nrm, nullptr, st));
       uint16_t* sp = ws_take<uint16_t>(c, (size_t)S * W);
-      if ((rc = ple_enqueue(c, t->ple, s->ple, ids, S, sA, nullptr, sp, nullptr))) return rc;
+      const size_t mark2 = c->ws_used;
+      for (int w0 = 0; w0 < S; w0 += MAX_TOKENS) {  // window by window (one window when verifying)
+        const int n = S - w0 < MAX_TOKENS ? S - w0 : MAX_TOKENS;
+        c->ws_used = mark2;
+        if ((rc = ple_enqueue(c, t->ple, s->ple, ids + w0, n, sA + (size_t)w0 * W, nullptr, sp + (size_t)w0 * W,
+                              nullptr)))
+          return rc;
+        if (prefill) s->ple->committed = n;
+      }
       LAUNCH(c, "hc_norm", launch_hc_norm(sp, nullptr, nullptr, S, hc, H, 0, L.attn_hc.norm_scale, eps, sA, nrm, xpW,
                                           st));
     } else {
@@ -2537,7 +2618,13 @@ int target_verify_enqueue(Ctx* c, Target* t, TargetState* s, const int32_t* ids,
       const mtpx_q4& ip = L.gdn->w.in_proj;
       const mtpx_q4& op = L.gdn->w.out_proj;
       LAUNCH(c, "qmv_gdn_in", launch_qmv(ip.w, ip.s, ip.b, ip.sb, gg.pw, H, gs, xpH, S, proj, nullptr, st));
-      if ((rc = gdn_enqueue(c, L.gdn, s->gdn[i], proj, S, nullptr, xpG))) return rc;
+      for (int w0 = 0; w0 < S; w0 += MAX_TOKENS) {  // window by window (one window when verifying)
+        const int n = S - w0 < MAX_TOKENS ? S - w0 : MAX_TOKENS;
+        if ((rc = gdn_enqueue(c, L.gdn, s->gdn[i], proj + (size_t)w0 * gg.pw, n, nullptr,
+                              xpG + (size_t)w0 * (VD / 32) * XP_DW)))
+          return rc;
+        if (prefill) s->gdn[i]->committed = n;
+      }
       LAUNCH(c, "qmv_gdn_out", launch_qmv(op.w, op.s, op.b, op.sb, H, VD, gs, xpG, S, ao, nullptr, st));
     } else {
       if ((rc = attn_enqueue(c, L.attn, s->kv[i], xpH, S, ao))) return rc;
@@ -2545,17 +2632,28 @@ int target_verify_enqueue(Ctx* c, Target* t, TargetState* s, const int32_t* ids,
     LAUNCH(c, "hc_norm", launch_hc_norm(sA, ao, jA, S, hc, H, 0, L.mlp_hc.norm_scale, eps, sM, nrm, xpW, st));
     c->ws_used = mark;
     if ((rc = hc_mix_enqueue(c, hg, &L.mlp_hc, nrm, xpW, S, x, jM, xpH))) return rc;
-    if ((rc = moe_enqueue(c, &L.moe, x, S, mo, nullptr, nullptr, nullptr, nullptr, nullptr, xpH, s->moe_unique + i)))
+    if (prefill) {
+      if ((rc = moe_enqueue_windows(c, &L.moe, x, S, mo, xpH))) return rc;
+    } else if ((rc = moe_enqueue(c, &L.moe, x, S, mo, nullptr, nullptr, nullptr, nullptr, nullptr, xpH,
+                                 s->moe_unique + i))) {
       return rc;
+    }
   }
   LAUNCH(c, "hc_norm", launch_hc_norm(sM, mo, jM, S, hc, H, 0, t->final_hc.norm_scale, eps, mt, nrm, xpW, st));
   c->ws_used = mark;
   if ((rc = hc_mix_enqueue(c, hg, &t->final_hc, nrm, xpW, S, mx, nullptr, xpH))) return rc;
-  if (logits)
+  if (logits) {
+    const int r0 = prefill ? S - 1 : 0;  // prefill: the last position's row only
     LAUNCH(c, "qmv_lm_head", launch_qmv(t->lm_head.w, t->lm_head.s, t->lm_head.b, t->lm_head.sb, (int)g.vocab, H, gs,
-                                        xpH, S, logits, nullptr, st));
+                                        xpH + (size_t)r0 * (H / 32) * XP_DW, S - r0, logits, nullptr, st));
+  }
   for (Kv* kv : s->kv)
     if (kv) kv->offset = s->offset + S;
+  if (prefill) {  // every window committed (the recurrent states' last window in full)
+    s->offset += S;
+    s->window = 0;
+    return MTPX_OK;
+  }
   s->window = S;
   return MTPX_OK;
 }

@@ -122,6 +122,9 @@ struct MoeArgs {
   bf16* y2;            // [M, H] or null
   uint32_t* ticket;    // router+route ticket, zero at rest
   int32_t* nu_out;     // if set: the route also writes the distinct routed expert count here
+  // windows of M tokens in one launch (a prefill batch): window w's tokens, slots, dispatch table,
+  // ticket and count follow window w-1's, each window routed and computed as its own launch would
+  int nwin = 1;
 };
 
 constexpr int MOE_TICKETS = 64;

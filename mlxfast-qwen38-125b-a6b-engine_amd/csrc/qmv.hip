@@ -19,17 +19,26 @@ __global__ __launch_bounds__(256) void k_xprep(const bf16* __restrict__ x, int M
 
 // Dense GEMV.  256 threads; every lane-group owns two rows (RPL = 2) so each
 // LDS read of a prepared activation block feeds two weight rows.  A wave's
-// rows are loaded before the activations are staged.
+// rows are loaded before the activations are staged.  Grid Y batches windows
+// of `win` tokens (window w: tokens w * win .. of the M in all), each computed
+// as its own launch would.
 template <int L, int IT>
 __global__ __launch_bounds__(256) void k_qmv(const uint32_t* __restrict__ wq, const bf16* __restrict__ sc,
                                              const bf16* __restrict__ bi, const uint32_t* __restrict__ sbp,
                                              int N, int K, int gs,
                                              const uint32_t* __restrict__ xp, int M, bf16* __restrict__ y,
-                                             float* __restrict__ yf, int rows_per_wg) {
+                                             float* __restrict__ yf, int rows_per_wg, int win) {
   extern __shared__ uint32_t lds[];
   constexpr int RW = 64 / L;
   constexpr int RPW = 2 * RW;  // rows per wave pass
   const int nb = K / 32, ng = K / gs, P = sb_row_len(K, gs);
+  {
+    const int t0 = (int)blockIdx.y * win;
+    xp += (size_t)t0 * nb * XP_DW;
+    y += (size_t)t0 * N;
+    if (yf) yf += (size_t)t0 * N;
+    M = min(M - t0, win);
+  }
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int sub = lane % L, grp = lane / L;
   const int row0 = blockIdx.x * rows_per_wg;
@@ -198,6 +207,13 @@ __global__ __launch_bounds__(MMA_THREADS) void k_qmv_mma(const uint32_t* __restr
   // MFMA on the same weight operand, so a launch serves up to 4 TG tokens with one read of the weights.
   constexpr size_t TGO = (size_t)MMA_TOK * NB * MB_DW;  // one token group's activations
   extern __shared__ uint32_t lds[];
+  {  // grid Y batches windows of 4 TG tokens (window w: tokens 4 TG w .. of the M in all)
+    const int t0 = (int)blockIdx.y * (MMA_TOK * TG);
+    xp += (size_t)t0 * NB * XP_DW;
+    y += (size_t)t0 * N;
+    if (yf) yf += (size_t)t0 * N;
+    M = min(M - t0, MMA_TOK * TG);
+  }
   uint32_t* sbl = lds + TG * TGO;
   float* part = reinterpret_cast<float*>(sbl + 8 * 16 * NQ);
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -430,27 +446,31 @@ hipError_t launch_xprep(const bf16* x, int M, int K, uint32_t* xp, hipStream_t s
   return hipGetLastError();
 }
 
+// M tokens in windows of `win` (one window: a plain launch; more: grid Y, the row grid rounded
+// up to whole XCD rounds so every window of a row range runs on the same XCD and L2).
 template <int L, int IT>
 static hipError_t qmv_li(const uint32_t* wq, const bf16* s, const bf16* b, const uint32_t* sb, int N, int K, int gs,
-                         const uint32_t* xp, int M, bf16* y, float* yf, hipStream_t st) {
+                         const uint32_t* xp, int M, bf16* y, float* yf, int win, hipStream_t st) {
   constexpr int rows_pass = 4 * (64 / L) * 2;
   // about two workgroups per CU, at least one pass each
   const int passes = (N + rows_pass - 1) / rows_pass;
   const int per = (passes + 511) / 512;
   const int rows_per_wg = per * rows_pass;
-  const int grid = (N + rows_per_wg - 1) / rows_per_wg;
-  const size_t lds = (size_t)M * (K / 32) * XP_DW * 4;
+  const int nwin = (M + win - 1) / win;
+  int grid = (N + rows_per_wg - 1) / rows_per_wg;
+  if (nwin > 1) grid = (grid + 7) / 8 * 8;
+  const size_t lds = (size_t)(M < win ? M : win) * (K / 32) * XP_DW * 4;
   static size_t cur = 0;
   hipError_t e = ensure_lds(k_qmv<L, IT>, lds, cur);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((k_qmv<L, IT>), dim3(grid), dim3(256), lds, st, wq, s, b, sb, N, K, gs, xp, M, y, yf,
-                     rows_per_wg);
+  hipLaunchKernelGGL((k_qmv<L, IT>), dim3(grid, nwin), dim3(256), lds, st, wq, s, b, sb, N, K, gs, xp, M, y, yf,
+                     rows_per_wg, win);
   return hipGetLastError();
 }
 
 static hipError_t qmv_tokens(const uint32_t* wq, const bf16* s, const bf16* b, const uint32_t* sb, int N, int K,
-                             int gs, const uint32_t* xp, int M, bf16* y, float* yf, hipStream_t st) {
-  MTPX_QROW_DISPATCH(K / 32, qmv_li, wq, s, b, sb, N, K, gs, xp, M, y, yf, st);
+                             int gs, const uint32_t* xp, int M, bf16* y, float* yf, int win, hipStream_t st) {
+  MTPX_QROW_DISPATCH(K / 32, qmv_li, wq, s, b, sb, N, K, gs, xp, M, y, yf, win, st);
 }
 
 template <int L, int IT, int C, int TG>
@@ -460,6 +480,8 @@ constexpr size_t mma_lds_bytes() {
 
 // hipErrorNotReady: a launch of two token groups (one workgroup per CU) whose tile groups would
 // need a second, nearly empty round of workgroups -- the caller runs four tokens per launch instead.
+// M > 4 TG tokens: windows of 4 TG in grid Y, one workgroup per tile group (rounded up to whole XCD
+// rounds, so the windows of a tile group share an XCD and its L2).
 template <int L, int IT, int C, int TG>
 static hipError_t qmv_mma_c(const uint32_t* wq, const uint32_t* sb, int N, int K, int gs, const uint32_t* xp, int M,
                             bf16* y, float* yf, hipStream_t st) {
@@ -467,13 +489,14 @@ static hipError_t qmv_mma_c(const uint32_t* wq, const uint32_t* sb, int N, int K
   const int groups = ((N + 15) / 16 + 8 / C - 1) / (8 / C);
   const int per_cu = lds <= 50 * 1024 ? 3 : lds <= 78 * 1024 ? 2 : 1;  // workgroups resident per CU
   const int slots = per_cu * device_cus();
-  if (TG > 1 && groups > slots && groups < 4 * slots) return hipErrorNotReady;
+  const int nwin = (M + MMA_TOK * TG - 1) / (MMA_TOK * TG);
+  if (nwin == 1 && TG > 1 && groups > slots && groups < 4 * slots) return hipErrorNotReady;
   static size_t cur = 0;
   hipError_t e = ensure_lds(k_qmv_mma<L, IT, C, TG>, lds, cur);
   if (e != hipSuccess) return e;
-  const int grid = groups < slots ? groups : slots;
-  hipLaunchKernelGGL((k_qmv_mma<L, IT, C, TG>), dim3(grid), dim3(MMA_THREADS), lds, st, wq, sb, N, K, gs, xp, M, y,
-                     yf);
+  const int grid = nwin > 1 ? (groups + 7) / 8 * 8 : groups < slots ? groups : slots;
+  hipLaunchKernelGGL((k_qmv_mma<L, IT, C, TG>), dim3(grid, nwin), dim3(MMA_THREADS), lds, st, wq, sb, N, K, gs, xp, M,
+                     y, yf);
   return hipGetLastError();
 }
 
@@ -510,7 +533,7 @@ static hipError_t qmv_mma_li(const uint32_t* wq, const uint32_t* sb, int N, int 
 // rows whose blocks tile the lanes exactly in four-block chunks.
 static bool qmv_mma_ok(const uint32_t* sb, int K, int M) {
   const int nb = K / 32, L = lanes_for_blocks(nb);
-  return sb && M >= 2 && M <= 2 * MMA_TOK && nb % L == 0 && nb % 4 == 0;
+  return sb && M >= 2 && nb % L == 0 && nb % 4 == 0;
 }
 
 template <int TG>
@@ -555,35 +578,32 @@ static bool qmv_mma_shape(int K) {
   }
 }
 
+// Every token's output is the same whatever the launch shape (exact block sums, the lane rule's
+// float order), so the token count only picks the path: the matrix cores for two or more tokens
+// where the shape allows (eight tokens per window when more than four, windows batched in one
+// launch), else the dot-product kernel with as many tokens per window as one workgroup's LDS holds.
 hipError_t launch_qmv(const uint32_t* wq, const bf16* s, const bf16* b, const uint32_t* sb, int N, int K, int gs,
                       const uint32_t* xp, int M, bf16* y, float* yf, hipStream_t st) {
   if (M >= 2 && qmv_mma_ok(sb, K, 2) && qmv_mma_shape<1>(K)) {  // matrix cores
-    if (M > MMA_TOK && qmv_mma_ok(sb, K, M) && qmv_mma_shape<2>(K)) {  // five to eight tokens: one launch
+    if (M > MMA_TOK && qmv_mma_shape<2>(K)) {  // five or more tokens: windows of eight
       const hipError_t e = qmv_mma<2>(wq, sb, N, K, gs, xp, M, y, yf, st);
       if (e != hipErrorNotReady) return e;
     }
-    for (int m0 = 0; m0 < M; m0 += MMA_TOK) {  // else four tokens per launch
-      const int mc = M - m0 < MMA_TOK ? M - m0 : MMA_TOK;
-      const uint32_t* xpc = xp + (size_t)m0 * (K / 32) * XP_DW;
-      bf16* yc = y + (size_t)m0 * N;
-      float* yfc = yf ? yf + (size_t)m0 * N : nullptr;
-      const hipError_t e = mc >= 2 ? qmv_mma<1>(wq, sb, N, K, gs, xpc, mc, yc, yfc, st)
-                                   : qmv_tokens(wq, s, b, sb, N, K, gs, xpc, mc, yc, yfc, st);
+    // else windows of four (a last window of one token takes the dot-product kernel)
+    const int full = M % MMA_TOK == 1 ? M - 1 : M;
+    if (full > 0) {
+      const hipError_t e = qmv_mma<1>(wq, sb, N, K, gs, xp, full, y, yf, st);
       if (e != hipSuccess) return e;
     }
-    return hipSuccess;
+    if (full == M) return hipSuccess;
+    return qmv_tokens(wq, s, b, sb, N, K, gs, xp + (size_t)full * (K / 32) * XP_DW, 1, y + (size_t)full * N,
+                      yf ? yf + (size_t)full * N : nullptr, 1, st);
   }
-  // tokens per launch: as many prepared activation vectors as fit in one workgroup's LDS
+  // tokens per window: as many prepared activation vectors as fit in one workgroup's LDS
   const size_t per_token = (size_t)(K / 32) * XP_DW * 4;
-  int chunk = (int)((160 * 1024) / per_token);
-  chunk = chunk < 1 ? 1 : chunk;
-  for (int m0 = 0; m0 < M; m0 += chunk) {
-    const int mc = M - m0 < chunk ? M - m0 : chunk;
-    const hipError_t e = qmv_tokens(wq, s, b, sb, N, K, gs, xp + (size_t)m0 * (K / 32) * XP_DW, mc, y + (size_t)m0 * N,
-                                    yf ? yf + (size_t)m0 * N : nullptr, st);
-    if (e != hipSuccess) return e;
-  }
-  return hipSuccess;
+  int win = (int)((160 * 1024) / per_token);
+  win = win < 1 ? 1 : win;
+  return qmv_tokens(wq, s, b, sb, N, K, gs, xp, M, y, yf, win, st);
 }
 
 hipError_t launch_quantize(const bf16* w, int64_t rows, int K, int gs, uint32_t* wq, bf16* s, bf16* b,

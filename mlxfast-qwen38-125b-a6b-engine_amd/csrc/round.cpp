@@ -26,6 +26,7 @@ namespace {
 using namespace mtpx;
 
 constexpr int OUT_WORDS = 24;  // out3 at 0, argmax rows at 4.., committed tokens at 12..
+constexpr int PROMPT_BATCH = 256;  // prompt positions per target prefill call (their multi streams are observed)
 
 struct Session {
   mtpx_ctx ctx{nullptr};
@@ -40,6 +41,7 @@ struct Session {
   uint16_t* multi = nullptr;   // bf16 [8, W]: the verify's multi streams
   uint16_t* mo = nullptr;      // bf16 [MTPX_MAX_DRAFT_DEPTH, W]: the drafter's multi streams
   uint16_t* carry = nullptr;   // bf16 [W]: multi stream paired with the carry token
+  uint16_t* pmulti = nullptr;  // bf16 [PROMPT_BATCH, W]: a prompt batch's multi streams
   int32_t* out = nullptr;      // device [OUT_WORDS]
   int32_t* host = nullptr;     // pinned [OUT_WORDS]
   int64_t offset = 0;          // committed positions (mirrors the target state)
@@ -61,7 +63,8 @@ struct Session {
 void release(Session* s) {
   if (s->drafter.ctx) mtpx_drafter_free(s->drafter);
   if (s->state.ctx) mtpx_target_state_free(s->state);
-  for (void* p : {(void*)s->ids, (void*)s->logits, (void*)s->multi, (void*)s->mo, (void*)s->carry, (void*)s->out})
+  for (void* p : {(void*)s->ids, (void*)s->logits, (void*)s->multi, (void*)s->mo, (void*)s->carry, (void*)s->out,
+                  (void*)s->pmulti})
     if (p) hipFree(p);
   if (s->host) hipHostFree(s->host);
   delete s;
@@ -75,11 +78,11 @@ int readback(Session* s) {
   return MTPX_OK;
 }
 
-// Next carry on the device: token tokens[n] -> ids[0], multi row n -> carry.
-int next_carry(Session* s, int n) {
+// Next carry on the device: token tokens[n] -> ids[0], row n of the multi streams -> carry.
+int next_carry(Session* s, const uint16_t* multi, int n) {
   hipStream_t st = ctx_stream(s->ctx);
   HIPRC(hipMemcpyAsync(s->ids, s->out + 1, 4, hipMemcpyDeviceToDevice, st));
-  HIPRC(hipMemcpyAsync(s->carry, s->multi + (size_t)n * s->W, 2 * (size_t)s->W, hipMemcpyDeviceToDevice, st));
+  HIPRC(hipMemcpyAsync(s->carry, multi + (size_t)n * s->W, 2 * (size_t)s->W, hipMemcpyDeviceToDevice, st));
   return MTPX_OK;
 }
 
@@ -110,6 +113,7 @@ int mtpx_session_new(mtpx_ctx ctx, mtpx_target target, mtpx_head head, mtpx_sess
   ok = ok && hipMalloc((void**)&s->multi, 2 * (size_t)8 * s->W) == hipSuccess;
   ok = ok && hipMalloc((void**)&s->mo, 2 * (size_t)MTPX_MAX_DRAFT_DEPTH * s->W) == hipSuccess;
   ok = ok && hipMalloc((void**)&s->carry, 2 * (size_t)s->W) == hipSuccess;
+  ok = ok && hipMalloc((void**)&s->pmulti, 2 * (size_t)PROMPT_BATCH * s->W) == hipSuccess;
   ok = ok && hipMalloc((void**)&s->out, 4 * OUT_WORDS) == hipSuccess;
   ok = ok && hipHostMalloc((void**)&s->host, 4 * OUT_WORDS, hipHostMallocDefault) == hipSuccess;
   if (!ok) {
@@ -144,7 +148,7 @@ int mtpx_session_reset(mtpx_session sh) {
   return MTPX_OK;
 }
 
-static int prefill_windows(Session* s, const int32_t* ids, int n, int32_t* first_token);
+static int prefill_batches(Session* s, const int32_t* ids, int n, int32_t* first_token);
 static int round_steps(Session* s, int k, const mtpx_force_params* force, int32_t* tokens, int* n_tokens);
 
 int mtpx_session_prefill(mtpx_session sh, const int32_t* ids, int n, int32_t* first_token) {
@@ -153,23 +157,24 @@ int mtpx_session_prefill(mtpx_session sh, const int32_t* ids, int n, int32_t* fi
   if (s->broken) return set_error(MTPX_ERR_STATE, "session: a previous call failed part way (reset it)");
   if (s->primed) return set_error(MTPX_ERR_STATE, "session prefill: the session already holds a context");
   if (s->offset + n > MTPX_INDEXER_BUDGET) return set_error(MTPX_ERR_ARG, "session prefill: past the indexer budget");
-  const int rc = prefill_windows(s, ids, n, first_token);
-  if (rc) s->broken = true;  // windows may have been committed: the caches no longer match the offset
+  const int rc = prefill_batches(s, ids, n, first_token);
+  if (rc) s->broken = true;  // batches may have been committed: the caches no longer match the offset
   return rc;
 }
 
-static int prefill_windows(Session* s, const int32_t* ids, int n, int32_t* first_token) {
-  for (int off = 0; off < n; off += 8) {
-    const int S = n - off < 8 ? n - off : 8;
+// The prompt through the target prefill in batches (each committed), the drafter observing every
+// batch's multi streams; the first generated token is the argmax of the last position's logits.
+static int prefill_batches(Session* s, const int32_t* ids, int n, int32_t* first_token) {
+  for (int off = 0; off < n; off += PROMPT_BATCH) {
+    const int S = n - off < PROMPT_BATCH ? n - off : PROMPT_BATCH;
     const bool last = off + S == n;
-    RC(mtpx_target_verify(s->ctx, s->target, s->state, ids + off, S, last ? s->logits : nullptr, s->multi, nullptr));
-    RC(mtpx_target_commit(s->state, S));
-    if (s->drafter.ctx) RC(mtpx_drafter_observe(s->drafter, ids + off, s->multi, S));
+    RC(mtpx_target_prefill(s->ctx, s->target, s->state, ids + off, S, last ? s->logits : nullptr, s->pmulti));
+    if (s->drafter.ctx) RC(mtpx_drafter_observe(s->drafter, ids + off, s->pmulti, S));
     if (last) {
-      // the first generated token: argmax of the last row (out3[1] of a depth-0 accept)
-      RC(mtpx_accept_greedy_bf16(s->ctx, s->logits + (size_t)(S - 1) * s->vocab, 0, s->vocab, nullptr,
-                                 (int32_t)(s->offset + off + S - 1), s->out, nullptr, nullptr));
-      RC(next_carry(s, S - 1));
+      // out3[1] of a depth-0 accept on the last row
+      RC(mtpx_accept_greedy_bf16(s->ctx, s->logits, 0, s->vocab, nullptr, (int32_t)(s->offset + off + S - 1), s->out,
+                                 nullptr, nullptr));
+      RC(next_carry(s, s->pmulti, S - 1));
     }
   }
   RC(readback(s));
@@ -215,7 +220,7 @@ static int round_steps(Session* s, int k, const mtpx_force_params* force, int32_
     else
       RC(mtpx_drafter_observe(s->drafter, s->ids, s->multi, 1));
   }
-  RC(next_carry(s, n));
+  RC(next_carry(s, s->multi, n));
   s->offset += n + 1;
   std::memcpy(tokens, s->host + 12, 4 * (size_t)(n + 1));
   *n_tokens = n + 1;

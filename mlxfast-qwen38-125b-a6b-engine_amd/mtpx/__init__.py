@@ -530,6 +530,11 @@ class Target:
         check(self.ctx.lib.mtpx_target_verify(self.ctx.h, self.h, state.h, _ptr(ids), ids.shape[0], _ptr(logits),
                                               _ptr(multi), _ptr(mixed)), "target_verify")
 
+    def prefill(self, state: "TargetState", ids, logits=None, multi=None):
+        """S prompt tokens processed and committed; logits [vocab] of the last position, multi [S, W]."""
+        check(self.ctx.lib.mtpx_target_prefill(self.ctx.h, self.h, state.h, _ptr(ids), ids.shape[0], _ptr(logits),
+                                               _ptr(multi)), "target_prefill")
+
 
 class TargetState:
     """Per-request caches of a Target (mtpx_target_state)."""

@@ -211,6 +211,7 @@ _SIGS = {
     "mtpx_target_state_reset": (INT, [Handle, Handle]),
     "mtpx_target_verify": (INT, [Handle, Handle, Handle, P, INT, P, P, P]),
     "mtpx_target_commit": (INT, [Handle, INT]),
+    "mtpx_target_prefill": (INT, [Handle, Handle, Handle, P, INT, P, P]),
     "mtpx_target_moe_unique": (INT, [Handle, Handle, P]),
     "mtpx_profile_enable": (INT, [Handle, INT]),
     "mtpx_profile_reset": (INT, [Handle]),

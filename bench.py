@@ -26,7 +26,7 @@ times the CPU oracle on a bounded sample of the same round (1 thread and all hos
 oracle's exact arithmetic and MLX's CPU bf16-accumulating quantized matmul), scaled as its
 `sample` field states.  `--no-e2e` reports the config-4 verify as the value; `--workload layer`
 runs config 3 (one full-shape decoder layer, plain residuals, 4 tokens over 1024 cached
-positions).
+positions); `--workload prefill` times the prompt's prefill alone.
 """
 from __future__ import annotations
 
@@ -790,12 +790,53 @@ def run_layer(args, out):
     return out
 
 
+def run_prefill(args, out):
+    """The prompt of configs 4 and 5 through mtpx_session_prefill (the target prefill in batches,
+    the drafter observing it): --warmup untimed and --steps timed prefills of a fresh session."""
+    import numpy as np
+    import torch
+
+    import mtpx
+
+    gs = args.group_size
+    ctx = mtpx.Context(0)
+    target, head, lc, tc = build_model(mtpx, ctx, args, gs, with_head=True)
+    prompt = prompt_ids(args, tc["vocab"])
+    sess = mtpx.Session(ctx, target, head)
+    times, first = [], None
+    for i in range(args.warmup + args.steps):
+        sess.reset()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        f = sess.prefill(prompt)  # synchronises once (the first token's readback)
+        dt = time.perf_counter() - t0
+        if first is None:
+            first = f
+        if f != first:
+            raise SystemExit("prefill gave another first token on a repeat")
+        if i >= args.warmup:
+            times.append(dt)
+        log(f"prefill {i}: {dt * 1e3:.1f} ms")
+    ms = 1e3 * float(np.median(times))
+    out.update({
+        "metric": "prefill tok/s (the configs' 1024-token prompt, target + drafter observation)",
+        "value": round(args.prompt / (ms / 1e3), 1), "unit": "tok/s", "ms_per_step": round(ms, 2),
+        "config": {"workload": f"mtpx_session_prefill of a {args.prompt}-token random prompt on the full-depth "
+                               f"random-init 125B-A6B target (gs{gs}, {args.layers} layers, PLE layer "
+                               f"{tc['ple_layer']}) with the MTP head; value = prompt tokens / median wall time",
+                   "prompt_tokens": args.prompt, "layers": args.layers, "group_size": gs,
+                   "parallelism": "none (1 GPU)"},
+        "first_token": int(first),
+    })
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", choices=("full", "layer"), default="full")
+    ap.add_argument("--workload", choices=("full", "layer", "prefill"), default="full")
     ap.add_argument("--depths", type=int, nargs="+", default=[1, 2, 3, 4, 5], help="draft depths of the decode sweep")
     ap.add_argument("--prompt", type=int, default=1024, help="prompt tokens (config 4 and 5)")
     ap.add_argument("--gen", type=int, default=1024, help="generated tokens per decode run (config 5)")
@@ -829,6 +870,8 @@ def main() -> int:
     }
     if args.workload == "full":
         out = run_full(args, out)
+    elif args.workload == "prefill":
+        out = run_prefill(args, out)
     else:
         out = run_layer(args, out)
     print(json.dumps(out))

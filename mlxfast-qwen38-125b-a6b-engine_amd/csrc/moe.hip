@@ -584,7 +584,7 @@ constexpr int dd_gate_up_rows() { return 4 * (64 / L) > 16 ? 4 * (64 / L) : 16; 
 
 template <int L, int IT, bool PK>
 __global__ __launch_bounds__(DD_THREADS) void k_moe_gate_up_dd(MoeArgs a0) {
-  const MoeArgs a = moe_window(a0, blockIdx.y);
+  const MoeArgs a = a0.gorder ? a0 : moe_window(a0, blockIdx.y);
   extern __shared__ uint32_t lds[];  // [H/32][XP_DW]: the slot's token
   constexpr int RW = 64 / L;
   constexpr int UR = dd_gate_up_rows<L>();
@@ -592,14 +592,16 @@ __global__ __launch_bounds__(DD_THREADS) void k_moe_gate_up_dd(MoeArgs a0) {
   static_assert(4 * RW * NP == UR, "four waves cover the rows of a unit");
   const int H = a.H, F = a.F, gs = a.gs, M = a.M, K = a.K;
   const int nb = H / 32, ng = H / gs, P = sb_row_len(H, gs), nfb = F / UR;
-  const int n_units = M * (K + 1) * nfb;
+  const int wslots = M * (K + 1), slots = a.gorder ? a.nwin * wslots : wslots;
+  const int n_units = slots * nfb;
   const int w = dd_unit(n_units);
   if (w >= n_units) return;
   const int o = w / nfb, f0 = (w % nfb) * UR;
-  const int ov = a.disp->order[o];
-  const int sl = min(ov & 0xffff, M * (K + 1) - 1);  // (clamps: never out of the weights, whatever the table holds)
-  const bool shared = sl >= M * K;
-  const int m = shared ? sl - M * K : sl / K;
+  const int ov = a.gorder ? a.gorder[o] : a.disp->order[o];
+  const int sl = min(ov & 0xffff, slots - 1);  // (clamps: never out of the weights, whatever the table holds)
+  const int win = sl / wslots, ls = sl - win * wslots;  // window and its slot (window 0 without gorder)
+  const bool shared = ls >= M * K;
+  const int m = win * M + (shared ? ls - M * K : ls / K);
   const int e = shared ? 0 : min(max((ov >> 16) - 1, 0), a.E - 1);
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int sub = lane % L, grp = lane / L;
@@ -645,19 +647,20 @@ constexpr int dd_down_rows() { return 4 * (64 / L); }
 
 template <int L, int IT, bool PK>
 __global__ __launch_bounds__(DD_THREADS) void k_moe_down_dd(MoeArgs a0) {
-  const MoeArgs a = moe_window(a0, blockIdx.y);
+  const MoeArgs a = a0.gorder ? a0 : moe_window(a0, blockIdx.y);
   extern __shared__ uint32_t lds[];  // [F/32][XP_DW]
   constexpr int RW = 64 / L;
   constexpr int DR = dd_down_rows<L>();
   const int H = a.H, F = a.F, gs = a.gs, M = a.M, K = a.K;
   const int nb = F / 32, ng = F / gs, P = sb_row_len(F, gs), nhb = (H + DR - 1) / DR;
-  const int n_units = M * (K + 1) * nhb;
+  const int wslots = M * (K + 1), slots = a.gorder ? a.nwin * wslots : wslots;
+  const int n_units = slots * nhb;
   const int wu = dd_unit(n_units);
   if (wu >= n_units) return;
   const int o = wu / nhb, hb = wu % nhb, h0 = hb * DR;
-  const int ov = a.disp->order[o];
-  const int sl = min(ov & 0xffff, M * (K + 1) - 1);  // (clamps: never out of the weights, whatever the table holds)
-  const bool shared = sl >= M * K;
+  const int ov = a.gorder ? a.gorder[o] : a.disp->order[o];
+  const int sl = min(ov & 0xffff, slots - 1);  // (clamps: never out of the weights, whatever the table holds)
+  const bool shared = sl % wslots >= M * K;
   const int e = shared ? 0 : min(max((ov >> 16) - 1, 0), a.E - 1);
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int sub = lane % L, grp = lane / L;
@@ -811,6 +814,52 @@ hipError_t launch_moe_combine(const MoeArgs& a, hipStream_t st) {
 
 
 // ---------------------------------------------------------------------------
+// The batch's expert order (one workgroup): every window's slots grouped by expert -- the
+// shared expert's slots first, then each routed expert's -- by a counting sort over the routes'
+// expert ids (a.idx of all windows, consecutive).  The order inside an expert's group follows the
+// atomics and is free: every slot's outputs are its own.
+constexpr int SORT_THREADS = 1024;
+
+__global__ __launch_bounds__(SORT_THREADS) void k_moe_sort(MoeArgs a) {
+  __shared__ int cnt[1024], base[1024];
+  const int E = a.E, K = a.K, M = a.M, T = a.nwin * M, wslots = M * (K + 1);
+  for (int e = threadIdx.x; e < E; e += SORT_THREADS) cnt[e] = 0;
+  __syncthreads();
+  for (int i = threadIdx.x; i < T * K; i += SORT_THREADS) atomicAdd(&cnt[min(max(a.idx[i], 0), E - 1)], 1);
+  __syncthreads();
+  if (threadIdx.x < 64) {  // exclusive scan of the counts by one wave, 64 experts per step
+    int run = T;  // the shared expert's T slots come first
+    for (int e0 = 0; e0 < E; e0 += 64) {
+      const int e = e0 + (int)threadIdx.x;
+      const int c = e < E ? cnt[e] : 0;
+      int incl = c;
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const int y = __shfl_up(incl, off, 64);
+        if ((int)threadIdx.x >= off) incl += y;
+      }
+      if (e < E) base[e] = run + incl - c;
+      run += __shfl(incl, 63, 64);
+    }
+  }
+  __syncthreads();
+  for (int t = threadIdx.x; t < T; t += SORT_THREADS)  // shared slots: window t / M, slot M*K + t % M
+    a.gorder[t] = (t / M) * wslots + M * K + t % M;
+  for (int i = threadIdx.x; i < T * K; i += SORT_THREADS) {
+    const int e = min(max(a.idx[i], 0), E - 1);
+    const int t = i / K, k = i % K;
+    const int pos = atomicAdd(&base[e], 1);
+    a.gorder[pos] = ((t / M) * wslots + (t % M) * K + k) | ((e + 1) << 16);
+  }
+}
+
+hipError_t launch_moe_sort(const MoeArgs& a, hipStream_t st) {
+  if (!a.gorder || a.E > 1024 || (size_t)a.nwin * a.M * (a.K + 1) > 0xffff) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_moe_sort, dim3(1), dim3(SORT_THREADS), 0, st, a);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
 // expert-grouped launches: grid = (M*K + 1 dispatch rows) x row blocks
 template <int L, int IT, bool PK>
 static hipError_t gate_up_dd_pk(const MoeArgs& a, hipStream_t st) {
@@ -822,8 +871,9 @@ static hipError_t gate_up_dd_pk(const MoeArgs& a, hipStream_t st) {
     hipError_t e = ensure_lds(k_moe_gate_up_dd<L, IT, PK>, lds, cur);
     if (e != hipSuccess) return e;
     if (a.F % dd_gate_up_rows<L>() != 0) return hipErrorInvalidValue;
-    const int units = a.M * (a.K + 1) * (a.F / dd_gate_up_rows<L>());
-    hipLaunchKernelGGL((k_moe_gate_up_dd<L, IT, PK>), dim3((units + 7) / 8 * 8, a.nwin), dim3(DD_THREADS), lds, st, a);
+    const int nw = a.gorder ? 1 : a.nwin;  // the global order: every window's units in one row of the grid
+    const int units = a.M * (a.K + 1) * (a.gorder ? a.nwin : 1) * (a.F / dd_gate_up_rows<L>());
+    hipLaunchKernelGGL((k_moe_gate_up_dd<L, IT, PK>), dim3((units + 7) / 8 * 8, nw), dim3(DD_THREADS), lds, st, a);
     return hipGetLastError();
   }
 }
@@ -841,8 +891,9 @@ static hipError_t down_dd_pk(const MoeArgs& a, hipStream_t st) {
   static size_t cur = 0;
   hipError_t e = ensure_lds(k_moe_down_dd<L, IT, PK>, lds, cur);
   if (e != hipSuccess) return e;
-  const int units = a.M * (a.K + 1) * nhb;
-  hipLaunchKernelGGL((k_moe_down_dd<L, IT, PK>), dim3((units + 7) / 8 * 8, a.nwin), dim3(DD_THREADS), lds, st, a);
+  const int nw = a.gorder ? 1 : a.nwin;
+  const int units = a.M * (a.K + 1) * (a.gorder ? a.nwin : 1) * nhb;
+  hipLaunchKernelGGL((k_moe_down_dd<L, IT, PK>), dim3((units + 7) / 8 * 8, nw), dim3(DD_THREADS), lds, st, a);
   return hipGetLastError();
 }
 

@@ -209,7 +209,8 @@ size_t moe_ws_bytes(const mtpx_moe_weights* w, int M, int nwin = 1) {
   const int H = w->hidden, E = w->experts, K = w->top_k, F = w->expert_width;
   const size_t T = (size_t)M * nwin, slots = T * (K + 1);
   return al(4 * T * E) + al(4 * T) + al(4 * T * K) * 2 + al(sizeof(MoeDispatch) * (size_t)nwin) +
-         al(4 * T * (H / 32) * XP_DW) + al(2 * slots * F) + al(2 * slots * H) + 4096;
+         al(4 * T * (H / 32) * XP_DW) + al(2 * slots * F) + al(2 * slots * H) + (nwin > 1 ? al(4 * slots) : 0) +
+         4096;
 }
 
 // Workspace of S tokens through moe_enqueue_windows (its launches reuse one region in turn).
@@ -264,6 +265,10 @@ int moe_enqueue(Ctx* c, const mtpx_moe_weights* w, const uint16_t* x, int M, uin
   c->last_gs = a.gs;
   LAUNCH(c, "moe_router_route", launch_moe_router_route(a, c->stream));
   if (moe_dd_supported(a.H, a.F, a.K)) {  // one workgroup per (slot, row block), slots in dispatch order
+    if (nwin > 1) {  // a batch of windows: one order of all their slots, grouped by expert
+      a.gorder = ws_take<int32_t>(c, slots);
+      LAUNCH(c, "moe_sort", launch_moe_sort(a, c->stream));
+    }
     LAUNCH(c, "moe_gate_up", launch_moe_gate_up_dd(a, c->stream));
     LAUNCH(c, "moe_down", launch_moe_down_dd(a, c->stream));
     LAUNCH(c, "moe_combine", launch_moe_combine(a, c->stream));

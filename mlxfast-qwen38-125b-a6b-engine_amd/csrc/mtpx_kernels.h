@@ -125,6 +125,10 @@ struct MoeArgs {
   // windows of M tokens in one launch (a prefill batch): window w's tokens, slots, dispatch table,
   // ticket and count follow window w-1's, each window routed and computed as its own launch would
   int nwin = 1;
+  // with nwin > 1: all windows' slots in one order grouped by expert (entry = global slot
+  // w * M * (K + 1) + slot | (expert + 1) << 16), walked by the expert kernels in one 1-D grid, so
+  // an expert's weight rows are fetched once for the whole batch; null: each window's own table
+  int32_t* gorder = nullptr;
 };
 
 constexpr int MOE_TICKETS = 64;
@@ -134,6 +138,7 @@ hipError_t launch_moe_down(const MoeArgs& a, hipStream_t st);
 // one workgroup per (slot, row block) in dispatch order (the slots of one expert side by side on
 // one XCD, so its weight rows are fetched from HBM once and served to the others by that L2)
 bool moe_dd_supported(int H, int F, int K);
+hipError_t launch_moe_sort(const MoeArgs& a, hipStream_t st);  // a.gorder from the windows' routes
 hipError_t launch_moe_gate_up_dd(const MoeArgs& a, hipStream_t st);
 hipError_t launch_moe_down_dd(const MoeArgs& a, hipStream_t st);
 hipError_t launch_moe_combine(const MoeArgs& a, hipStream_t st);

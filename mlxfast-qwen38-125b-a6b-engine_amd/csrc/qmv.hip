@@ -4,6 +4,8 @@
 // Weight format (MLX affine 4-bit, unchanged from the reference checkpoint):
 // packed uint32 [N, K/8], element k at bits 4*(k%8) of word k/8; bf16 scale
 // and bias [N, K/gs].  Arithmetic: see mtpx_device.h.
+#include <algorithm>
+
 #include "qrows.h"
 
 namespace mtpx {
@@ -447,14 +449,26 @@ hipError_t launch_xprep(const bf16* x, int M, int K, uint32_t* xp, hipStream_t s
 }
 
 // M tokens in windows of `win` (one window: a plain launch; more: grid Y, the row grid rounded
-// up to whole XCD rounds so every window of a row range runs on the same XCD and L2).
+// up to whole XCD rounds so every window of a row range runs on the same XCD and L2).  win = 0
+// (a prefill batch): windows and rows per workgroup chosen for about four workgroups per CU in
+// all -- short windows where the rows are few, several row passes per workgroup where the
+// windows are many -- with at most `cap` tokens (the LDS) per window.
 template <int L, int IT>
 static hipError_t qmv_li(const uint32_t* wq, const bf16* s, const bf16* b, const uint32_t* sb, int N, int K, int gs,
                          const uint32_t* xp, int M, bf16* y, float* yf, int win, hipStream_t st) {
   constexpr int rows_pass = 4 * (64 / L) * 2;
-  // about two workgroups per CU, at least one pass each
   const int passes = (N + rows_pass - 1) / rows_pass;
-  const int per = (passes + 511) / 512;
+  int per = (passes + 511) / 512;  // about two workgroups per CU, at least one pass each
+  if (win <= 0) {
+    const int cap = (int)((160 * 1024) / ((size_t)(K / 32) * XP_DW * 4));
+    const int want = 4 * device_cus();
+    int nw = (want + passes - 1) / passes;
+    nw = std::max((M + cap - 1) / cap, std::min(M, nw));
+    win = (M + nw - 1) / nw;
+    nw = (M + win - 1) / win;
+    const int g = std::max(1, std::min(passes, (want + nw - 1) / nw));
+    per = (passes + g - 1) / g;
+  }
   const int rows_per_wg = per * rows_pass;
   const int nwin = (M + win - 1) / win;
   int grid = (N + rows_per_wg - 1) / rows_per_wg;
@@ -599,11 +613,12 @@ hipError_t launch_qmv(const uint32_t* wq, const bf16* s, const bf16* b, const ui
     return qmv_tokens(wq, s, b, sb, N, K, gs, xp + (size_t)full * (K / 32) * XP_DW, 1, y + (size_t)full * N,
                       yf ? yf + (size_t)full * N : nullptr, 1, st);
   }
-  // tokens per window: as many prepared activation vectors as fit in one workgroup's LDS
+  // tokens per window: up to MAX_TOKENS as many prepared activation vectors as fit in one
+  // workgroup's LDS; a longer batch: windows sized by the row count (qmv_li)
   const size_t per_token = (size_t)(K / 32) * XP_DW * 4;
   int win = (int)((160 * 1024) / per_token);
   win = win < 1 ? 1 : win;
-  return qmv_tokens(wq, s, b, sb, N, K, gs, xp, M, y, yf, win, st);
+  return qmv_tokens(wq, s, b, sb, N, K, gs, xp, M, y, yf, M > MAX_TOKENS ? 0 : win, st);
 }
 
 hipError_t launch_quantize(const bf16* w, int64_t rows, int K, int gs, uint32_t* wq, bf16* s, bf16* b,

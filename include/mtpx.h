@@ -310,10 +310,11 @@ int mtpx_head_adopt(mtpx_ctx ctx, const mtpx_head_config* cfg, const mtpx_head_w
                     mtpx_head* out);
 int mtpx_head_free(mtpx_head head);
 int mtpx_head_weights_get(mtpx_head head, mtpx_head_weights* out);
-/* One head application over S <= 8 inputs at the cache's offset (advances it by S):
- * ids int32 [S] and multi bf16 [S, hc*H] on the device -> multi_next bf16 [S, hc*H],
- * sample bf16 [S, H] (may be NULL), draft int32 [1] (the last row's shortlist argmax;
- * may be NULL).  An id outside [0, vocab) embeds as a zero row. */
+/* One head application over S inputs at the cache's offset (advances it by S): a draft step
+ * (S <= 8) or a batch of up to 256 backlog positions (the drafter's flush after a prompt; every
+ * output equals that of windows of 8 in turn): ids int32 [S] and multi bf16 [S, hc*H] on the
+ * device -> multi_next bf16 [S, hc*H], sample bf16 [S, H] (may be NULL), draft int32 [1] (the
+ * last row's shortlist argmax; may be NULL).  An id outside [0, vocab) embeds as a zero row. */
 int mtpx_head_forward(mtpx_ctx ctx, mtpx_head head, mtpx_kv kv, const int32_t* ids, int S,
                       const uint16_t* multi, uint16_t* multi_next, uint16_t* sample,
                       int32_t* draft);

@@ -548,7 +548,8 @@ size_t head_ws_bytes(const Head* hd, int S, int T) {
   // per mixer call (three per step): lo, act [S, LW]; inj [S, hc]; xpL; w [S, W]
   const size_t mix = al(2 * (size_t)S * LW) * 2 + al(2 * (size_t)S * g.hc) + al(4 * (size_t)S * (LW / 32) * XP_DW) +
                      al(2 * (size_t)S * W);
-  return moe_ws_bytes(&hd->w.layer.moe, S) + attn_ws_bytes(hd->layer, S, T) + 3 * mix + al(2 * (size_t)S * H) * 6 +
+  const size_t moe = S > MAX_TOKENS ? moe_windows_ws_bytes(&hd->w.layer.moe, S) : moe_ws_bytes(&hd->w.layer.moe, S);
+  return moe + attn_ws_bytes(hd->layer, S, T) + 3 * mix + al(2 * (size_t)S * H) * 6 +
          al(2 * (size_t)S * W) * 5 + al(2 * (size_t)S * g.hc) + al(4 * (size_t)S * XB * XP_DW) +
          al(4 * (size_t)S * (W / 32) * XP_DW) + al(2 * (size_t)hd->w.shortlist_rows) +
          al(4 * argmax_work_items(1, hd->w.shortlist_rows)) * 2 + 8192;
@@ -762,8 +763,8 @@ struct DevBackend {
     mtpx_ctx ch{c};
     mtpx_kv kh{kv};
     int rc = MTPX_OK, last = 0;
-    for (int off = 0; off < S; off += MAX_TOKENS) {
-      last = S - off < MAX_TOKENS ? S - off : MAX_TOKENS;
+    for (int off = 0; off < S; off += HEAD_BATCH) {  // the backlog in batches (the same bits as windows of 8)
+      last = S - off < HEAD_BATCH ? S - off : HEAD_BATCH;
       const bool end = off + last == S;
       rc = mtpx_head_forward(ch, hh, kh, t + off, last, h + (size_t)off * W, multi_scratch, nullptr,
                              end ? draft : nullptr);
@@ -2829,13 +2830,13 @@ int mtpx_head_forward(mtpx_ctx h, mtpx_head hh, mtpx_kv kvh, const int32_t* ids,
   ARG(c && hd && kv && ids && multi && multi_next, "null argument");
   const mtpx_head_config& g = hd->cfg;
   const mtpx_layer_config& lg = g.layer;
-  ARG(S >= 1 && S <= MAX_TOKENS, "S=%d", S);
+  ARG(S >= 1 && S <= HEAD_BATCH, "S=%d", S);
   ARG(kv->heads == lg.kv_heads && kv->dim == lg.head_dim, "kv cache geometry does not match the head");
   ARG(kv->offset + S <= kv->tmax && kv->offset + S <= lg.max_positions, "cache full (offset %lld + %d)",
       (long long)kv->offset, S);
   ARG(kv->offset + S <= MTPX_INDEXER_BUDGET, "offset %lld + %d tokens is past the indexer budget %d",
       (long long)kv->offset, S, MTPX_INDEXER_BUDGET);
-  int rc = moe_check(&hd->w.layer.moe, S);
+  int rc = moe_check(&hd->w.layer.moe, S < MAX_TOKENS ? S : MAX_TOKENS);
   if (rc) return rc;
   if (set_device(c)) return MTPX_ERR_HIP;
   const int H = lg.hidden, hc = g.hc, W = hc * H, gs = lg.group_size, HQ = lg.heads, D = lg.head_dim;
@@ -2876,7 +2877,11 @@ int mtpx_head_forward(mtpx_ctx h, mtpx_head hh, mtpx_kv kvh, const int32_t* ids,
   // MoE block
   LAUNCH(c, "hc_norm", launch_hc_norm(st0, ao, j, S, hc, H, 0, w.mlp_hc.norm_scale, eps, st1, nrm, xpW, st));
   if ((rc = hc_mix_enqueue(c, hd, &w.mlp_hc, nrm, xpW, S, x, j, xpH))) return rc;
-  if ((rc = moe_enqueue(c, &w.layer.moe, x, S, ao, nullptr, nullptr, nullptr, nullptr, nullptr, xpH))) return rc;
+  if (S > MAX_TOKENS) {  // a batch of the drafter's backlog: the MoE as windows of MAX_TOKENS
+    if ((rc = moe_enqueue_windows(c, &w.layer.moe, x, S, ao, xpH))) return rc;
+  } else if ((rc = moe_enqueue(c, &w.layer.moe, x, S, ao, nullptr, nullptr, nullptr, nullptr, nullptr, xpH))) {
+    return rc;
+  }
   // final mixer: multi_next = st1 + m*j; sample = mix(final_hc, hc_norm(multi_next))
   LAUNCH(c, "hc_norm", launch_hc_norm(st1, ao, j, S, hc, H, 0, w.final_hc.norm_scale, eps, multi_next, nrm, xpW,
                                       st));
@@ -2915,7 +2920,7 @@ int mtpx_drafter_new(mtpx_ctx h, mtpx_head hh, mtpx_drafter* out) {
   o->be.hh = hh;
   o->be.kv = static_cast<Kv*>(kv.ctx);
   o->be.W = hd->cfg.hc * lg.hidden;
-  if (hipMalloc((void**)&o->be.multi_scratch, 2 * (size_t)MAX_TOKENS * o->be.W) != hipSuccess) {
+  if (hipMalloc((void**)&o->be.multi_scratch, 2 * (size_t)HEAD_BATCH * o->be.W) != hipSuccess) {
     mtpx_kv_free(kv);
     delete o;
     return fail(MTPX_ERR_OOM, "drafter scratch");

@@ -10,6 +10,7 @@ namespace mtpx {
 
 constexpr int QMV_IT = 8;        // max blocks per lane: K <= 8 * 32 * lanes_for_blocks(K/32)
 constexpr int MAX_TOKENS = 8;    // verify width ceiling (draft depth <= 7)
+constexpr int HEAD_BATCH = 256;  // MTP head positions per call (the drafter's backlog flush)
 constexpr int MAX_TOPK = 16;
 constexpr int ATTN_CHUNK = 32;   // keys per split-KV partial
 

@@ -4,7 +4,8 @@ committing it in windows of 8 does, and leaves the same state (the next verify i
 Against the oracle composition's windows at small dims (a prompt of two full windows and a tail,
 with the PLE block), against the GPU's own windowed verify path for a prompt of 300 positions
 (two prefill batches, 37 windows, the batched MoE launches) and at full width (hidden 2560, 512
-experts, hyper-connections 4 x 2560, the full PLE table, 4 layers) over a 1024-position prefix."""
+experts, hyper-connections 4 x 2560, the full PLE table, 4 layers) over a 1024-position prefix; and
+the MTP head over a batch of backlog positions (the drafter's flush) against windows of 8."""
 import numpy as np
 import pytest
 import torch
@@ -204,3 +205,43 @@ def test_prefill_full_width_matches_windows(ctx):
     a.close()
     b.close()
     t.close()
+
+
+@pytest.mark.parametrize("n", [37, 256])
+def test_head_batch_matches_windows(ctx, n):
+    """The MTP head over a batch of backlog positions (the drafter's flush after a prompt) equals the
+    same positions in windows of 8: every multi_next and sample row, the last draft, and the next step
+    from the caches they leave."""
+    import mtpx
+    layer = dict(LAYER, max_positions=400)
+    hc, lowrank, vocab = 4, 64, 1000
+    head = mtpx.MTPHead(ctx, mtpx.HeadConfig(mtpx.LayerConfig(**layer), hc, lowrank, vocab, 500, 980), seed=19)
+    H, W = layer["hidden"], hc * layer["hidden"]
+    kva = mtpx.KVCache(ctx, layer["kv_heads"], layer["head_dim"], layer["max_positions"])
+    kvb = mtpx.KVCache(ctx, layer["kv_heads"], layer["head_dim"], layer["max_positions"])
+    r = np.random.default_rng(n)
+    ids = dev(r.integers(0, vocab + 20, n).astype(np.int32))  # a few ids outside the vocabulary
+    multi = dev(rand_bf16(r, (n, W)))
+    print("case head batch", n, flush=True)
+    na, sa, da = empty_bf16(n, W), empty_bf16(n, H), torch.full((1,), -1, dtype=torch.int32, device="cuda")
+    head.forward(kva, ids, multi, na, sa, da)
+    nb, sb = empty_bf16(n, W), empty_bf16(n, H)
+    db = torch.full((1,), -1, dtype=torch.int32, device="cuda")
+    for w0 in range(0, n, 8):
+        w1 = min(n, w0 + 8)
+        head.forward(kvb, ids[w0:w1], multi[w0:w1], nb[w0:w1], sb[w0:w1], db if w1 == n else None)
+    assert np.array_equal(host(na), host(nb))
+    assert np.array_equal(host(sa), host(sb))
+    assert int(host(da)[0]) == int(host(db)[0])
+    assert kva.offset == kvb.offset == n
+    step_ids, step_multi = ids[:1], multi[:1]
+    oa, ob = empty_bf16(1, W), empty_bf16(1, W)
+    xa, xb = torch.full((1,), -1, dtype=torch.int32, device="cuda"), torch.full((1,), -1, dtype=torch.int32, device="cuda")
+    head.forward(kva, step_ids, step_multi, oa, None, xa)
+    head.forward(kvb, step_ids, step_multi, ob, None, xb)
+    assert np.array_equal(host(oa), host(ob)) and int(host(xa)[0]) == int(host(xb)[0])
+    with pytest.raises(mtpx.MtpxError):
+        head.forward(kva, dev(np.zeros(257, np.int32)), dev(np.zeros((257, W), np.uint16)), empty_bf16(257, W))
+    kva.close()
+    kvb.close()
+    head.close()

@@ -452,7 +452,7 @@ hipError_t launch_xprep(const bf16* x, int M, int K, uint32_t* xp, hipStream_t s
 // up to whole XCD rounds so every window of a row range runs on the same XCD and L2).  win = 0
 // (a prefill batch): windows and rows per workgroup chosen for about four workgroups per CU in
 // all -- short windows where the rows are few, several row passes per workgroup where the
-// windows are many -- with at most `cap` tokens (the LDS) per window.
+// windows are many -- with at most `cap` tokens per window (50 KB of LDS: three per CU).
 template <int L, int IT>
 static hipError_t qmv_li(const uint32_t* wq, const bf16* s, const bf16* b, const uint32_t* sb, int N, int K, int gs,
                          const uint32_t* xp, int M, bf16* y, float* yf, int win, hipStream_t st) {
@@ -460,7 +460,8 @@ static hipError_t qmv_li(const uint32_t* wq, const bf16* s, const bf16* b, const
   const int passes = (N + rows_pass - 1) / rows_pass;
   int per = (passes + 511) / 512;  // about two workgroups per CU, at least one pass each
   if (win <= 0) {
-    const int cap = (int)((160 * 1024) / ((size_t)(K / 32) * XP_DW * 4));
+    int cap = (int)((50 * 1024) / ((size_t)(K / 32) * XP_DW * 4));  // three workgroups' LDS per CU
+    cap = cap < 1 ? 1 : cap;
     const int want = 4 * device_cus();
     int nw = (want + passes - 1) / passes;
     nw = std::max((M + cap - 1) / cap, std::min(M, nw));
@@ -599,11 +600,12 @@ static bool qmv_mma_shape(int K) {
 hipError_t launch_qmv(const uint32_t* wq, const bf16* s, const bf16* b, const uint32_t* sb, int N, int K, int gs,
                       const uint32_t* xp, int M, bf16* y, float* yf, hipStream_t st) {
   if (M >= 2 && qmv_mma_ok(sb, K, 2) && qmv_mma_shape<1>(K)) {  // matrix cores
-    if (M > MMA_TOK && qmv_mma_shape<2>(K)) {  // five or more tokens: windows of eight
+    if (M > MMA_TOK && M <= MAX_TOKENS && qmv_mma_shape<2>(K)) {  // five to eight tokens: one window of eight
       const hipError_t e = qmv_mma<2>(wq, sb, N, K, gs, xp, M, y, yf, st);
       if (e != hipErrorNotReady) return e;
     }
-    // else windows of four (a last window of one token takes the dot-product kernel)
+    // else windows of four (a prefill batch too: a quarter of the LDS, three workgroups per CU, measured
+    // faster than windows of eight at one per CU); a last window of one token takes the dot-product kernel
     const int full = M % MMA_TOK == 1 ? M - 1 : M;
     if (full > 0) {
       const hipError_t e = qmv_mma<1>(wq, sb, N, K, gs, xp, full, y, yf, st);

@@ -298,6 +298,192 @@ __global__ __launch_bounds__(GDN_THREADS) void k_gdn_step(GdnArgs a) {
     }
 }
 
+// A prefill batch through the core in one launch (S positions, any count): the P committed steps
+// of the previous window replayed onto the state, then the batch window by window of MAX_TOKENS --
+// each window's prep (conv, SiLU, q/k norms, gates) into LDS and its recurrence steps, the float
+// operations of a verify window, so the same bits -- with every position committed: the state is
+// stored after the last position, the batch's last kc-1 conv input rows become the conv base
+// (slot nxt), and no journal is written.  The head's last workgroup runs the gated norm and the
+// prepared output blocks of every position, window by window.
+template <int KC>
+__global__ __launch_bounds__(GDN_THREADS) void k_gdn_batch(GdnArgs a) {
+  __shared__ float qs[MAX_TOKENS][GDN_D], ks[MAX_TOKENS][GDN_D], vs[MAX_TOKENS][GDN_D], ys[MAX_TOKENS][GDN_D];
+  __shared__ float dec[MAX_TOKENS], bet[MAX_TOKENS];
+  __shared__ bf16 gated[MAX_TOKENS][GDN_D];
+  const int h = blockIdx.x, ratio = a.hv / a.hk, hk = h / ratio;
+  const int r0 = blockIdx.y * (GDN_D / GDN_SPLIT);  // this workgroup's state rows
+  const bool w0 = blockIdx.y == 0;
+  const bool lead = (h % ratio) == 0 && w0;         // writes the q/k channels' conv base rows
+  const int hw = threadIdx.x >> 5, l = threadIdx.x & 31;
+  const int S = a.S, P = a.P, KM1 = a.kc - 1;
+  const float inv_scale = 1.0f / sqrtf((float)GDN_D);
+  const float q_mul = round_bf(inv_scale * inv_scale), k_mul = round_bf(inv_scale);
+  constexpr int RPH = GDN_D / GDN_SPLIT / (GDN_THREADS / 32);
+  float s[RPH][4];
+#pragma unroll
+  for (int i = 0; i < RPH; ++i) {
+    const float4 s4 = *reinterpret_cast<const float4*>(a.ssm + ((size_t)h * GDN_D + r0 + hw + 16 * i) * GDN_D + 4 * l);
+    s[i][0] = s4.x;
+    s[i][1] = s4.y;
+    s[i][2] = s4.z;
+    s[i][3] = s4.w;
+  }
+  // the previous window's committed steps, in order
+  for (int p = 0; p < P; ++p) {
+    const float gd = a.decay_cur[(size_t)p * a.hv + h];
+    const uint2 kw = *reinterpret_cast<const uint2*>(a.key_cur + ((size_t)p * a.hk + hk) * GDN_D + 4 * l);
+    const float kp[4] = {__uint_as_float(kw.x << 16), __uint_as_float(kw.x & 0xffff0000u),
+                         __uint_as_float(kw.y << 16), __uint_as_float(kw.y & 0xffff0000u)};
+#pragma unroll
+    for (int i = 0; i < RPH; ++i) {
+      const float dl = a.delta_cur[((size_t)p * a.hv + h) * GDN_D + r0 + hw + 16 * i];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        s[i][c] = s[i][c] * gd;
+        s[i][c] = __builtin_fmaf(kp[c], dl, s[i][c]);
+      }
+    }
+  }
+  for (int t0 = 0; t0 < S; t0 += MAX_TOKENS) {
+    const int n = S - t0 < MAX_TOKENS ? S - t0 : MAX_TOKENS;
+    // ---- prep of positions t0 .. t0 + n - 1 (window slot t = position - t0)
+    for (int task = hw; task < 3 * n; task += GDN_THREADS / 32) {
+      const int t = task / 3, kind = task % 3;
+      const int vec = kind == 0 ? hk : (kind == 1 ? a.hk + hk : 2 * a.hk + h);
+      const int ch0 = vec * GDN_D + 4 * l;
+      uint2 xin[KC];
+#pragma unroll
+      for (int j = 0; j < KC; ++j) xin[j] = *reinterpret_cast<const uint2*>(gdn_row_ptr(a, P + t0 + t + j) + ch0);
+      uint32_t wt[2 * KC];
+#pragma unroll
+      for (int q = 0; q < 2 * KC; ++q) wt[q] = reinterpret_cast<const uint32_t*>(a.conv_w + (size_t)ch0 * KC)[q];
+      auto hbf = [](uint32_t w, int odd) { return __uint_as_float(odd ? (w & 0xffff0000u) : (w << 16)); };
+      float xs[4], acc = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float c = 0.0f;
+#pragma unroll
+        for (int j = 0; j < KC; ++j) {
+          const float xv = hbf(i < 2 ? xin[j].x : xin[j].y, i & 1);
+          const int e = i * KC + j;
+          c = c + xv * hbf(wt[e >> 1], e & 1);
+        }
+        const float x = silu_bf16(round_bf(c));
+        xs[i] = x;
+        acc = __builtin_fmaf(x, x, acc);
+      }
+      if (kind < 2) {
+        const float inv = 1.0f / sqrtf(half_wave_sum(acc) / 128.0f + 1e-6f);
+        const float mul = kind == 0 ? q_mul : k_mul;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float val = round_bf(mul * round_bf(xs[i] * inv));
+          if (kind == 0)
+            qs[t][4 * l + i] = val;
+          else
+            ks[t][4 * l + i] = val;
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) vs[t][4 * l + i] = xs[i];
+      }
+    }
+    if ((int)threadIdx.x < n) {
+      const int t = threadIdx.x;
+      const bf16* prow = a.proj + (size_t)(t0 + t) * a.pw;
+      const float b = sigmoid_bf16(bf2f(prow[a.b_off + h]));
+      const float ax = round_bf(bf2f(prow[a.a_off + h]) + bf2f(a.dt_bias[h]));
+      dec[t] = expf_det(a.neg_exp_alog[h] * logaddexp0_bf16(ax));
+      bet[t] = b;
+    }
+    __syncthreads();
+    // ---- recurrence of the window's positions
+#pragma unroll
+    for (int i = 0; i < RPH; ++i) {
+      const int r = r0 + hw + 16 * i;
+      for (int t = 0; t < n; ++t) {
+        const float gd = dec[t];
+        const float k0 = ks[t][4 * l], k1 = ks[t][4 * l + 1], k2 = ks[t][4 * l + 2], k3 = ks[t][4 * l + 3];
+        s[i][0] = s[i][0] * gd;
+        float kv = 0.0f + s[i][0] * k0;
+        float comp = 0.0f;
+        {
+          s[i][1] = s[i][1] * gd;
+          const float prod = s[i][1] * k1, corr = prod - comp, next = kv + corr;
+          comp = (next - kv) - corr;
+          kv = next;
+        }
+        {
+          s[i][2] = s[i][2] * gd;
+          const float prod = s[i][2] * k2, corr = prod - comp, next = kv + corr;
+          comp = (next - kv) - corr;
+          kv = next;
+        }
+        {
+          s[i][3] = s[i][3] * gd;
+          const float prod = s[i][3] * k3, corr = prod - comp, next = kv + corr;
+          kv = next;
+        }
+        const float kvm = half_wave_sum(kv);
+        const float delta = (vs[t][r] - kvm) * bet[t];
+        float o = 0.0f;
+        s[i][0] = __builtin_fmaf(k0, delta, s[i][0]);
+        o = __builtin_fmaf(s[i][0], qs[t][4 * l], o);
+        s[i][1] = __builtin_fmaf(k1, delta, s[i][1]);
+        o = __builtin_fmaf(s[i][1], qs[t][4 * l + 1], o);
+        s[i][2] = __builtin_fmaf(k2, delta, s[i][2]);
+        o = __builtin_fmaf(s[i][2], qs[t][4 * l + 2], o);
+        s[i][3] = __builtin_fmaf(k3, delta, s[i][3]);
+        o = __builtin_fmaf(s[i][3], qs[t][4 * l + 3], o);
+        const float y = half_wave_sum(o);
+        if (l == 0) st_pub(a.ypub + ((size_t)(t0 + t) * a.hv + h) * GDN_D + r, round_bf(y));
+      }
+    }
+    __syncthreads();  // the next window's prep overwrites qs, ks, vs, dec, bet
+  }
+#pragma unroll
+  for (int i = 0; i < RPH; ++i)
+    *reinterpret_cast<float4*>(a.ssm + ((size_t)h * GDN_D + r0 + hw + 16 * i) * GDN_D + 4 * l) =
+        make_float4(s[i][0], s[i][1], s[i][2], s[i][3]);
+  // the batch's last kc-1 input rows become the conv base
+  for (int i = threadIdx.x; i < (w0 ? KM1 * 3 * GDN_D : 0); i += GDN_THREADS) {
+    const int j = i / (3 * GDN_D), kind = (i / GDN_D) % 3, d = i % GDN_D;
+    if (kind < 2 && !lead) continue;
+    const int vec = kind == 0 ? hk : (kind == 1 ? a.hk + hk : 2 * a.hk + h);
+    const int ch = vec * GDN_D + d;
+    a.conv_nxt[(size_t)j * a.cd + ch] = f2bf(gdn_row(a, P + S + j, ch));
+  }
+  if (!ticket_last(a.tickets + h, GDN_SPLIT - 1)) return;
+  for (int t0 = 0; t0 < S; t0 += MAX_TOKENS) {
+    const int n = S - t0 < MAX_TOKENS ? S - t0 : MAX_TOKENS;
+    for (int i = threadIdx.x; i < n * GDN_D; i += GDN_THREADS)
+      ys[i / GDN_D][i % GDN_D] = ld_pub(a.ypub + ((size_t)(t0 + i / GDN_D) * a.hv + h) * GDN_D + i % GDN_D);
+    __syncthreads();
+    for (int t = hw; t < n; t += GDN_THREADS / 32) {
+      float acc = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc = __builtin_fmaf(ys[t][4 * l + i], ys[t][4 * l + i], acc);
+      const float inv = 1.0f / sqrtf(half_wave_sum(acc) / 128.0f + a.eps);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int d = 4 * l + i;
+        const float nv = round_bf(bf2f(a.norm_w[d]) * round_bf(ys[t][d] * inv));
+        const float z = bf2f(a.proj[(size_t)(t0 + t) * a.pw + a.z_off + h * GDN_D + d]);
+        const bf16 out = f2bf(sigmoid_f32(z) * nv);
+        gated[t][d] = out;
+        if (a.gated) a.gated[(size_t)(t0 + t) * a.hv * GDN_D + h * GDN_D + d] = out;
+      }
+    }
+    __syncthreads();
+    if (a.xp)
+      for (int task = hw; task < 4 * n; task += GDN_THREADS / 32) {
+        const int t = task >> 2, blk = task & 3;
+        xprep_lanes_direct(gated[t][blk * 32 + l], l, a.xp + ((size_t)(t0 + t) * a.hv * 4 + h * 4 + blk) * XP_DW);
+      }
+    __syncthreads();  // ys and gated of the next window
+  }
+}
+
 // Committed state without modifying it: the P journal steps replayed onto the
 // state rows into ssm_dst, and the committed conv rows into conv_dst.
 __global__ __launch_bounds__(GDN_THREADS) void k_gdn_replay(GdnArgs a, float* ssm_dst, bf16* conv_dst) {
@@ -346,6 +532,26 @@ hipError_t launch_gdn_step(const GdnArgs& a, hipStream_t st) {
     case 6: return gdn_step_kc<6>(a, st);
     case 7: return gdn_step_kc<7>(a, st);
     case 8: return gdn_step_kc<8>(a, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+template <int KC>
+static hipError_t gdn_batch_kc(const GdnArgs& a, hipStream_t st) {
+  if (!a.tickets || !a.ypub) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_gdn_batch<KC>, dim3(a.hv, GDN_SPLIT), dim3(GDN_THREADS), 0, st, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_gdn_batch(const GdnArgs& a, hipStream_t st) {
+  switch (a.kc) {
+    case 2: return gdn_batch_kc<2>(a, st);
+    case 3: return gdn_batch_kc<3>(a, st);
+    case 4: return gdn_batch_kc<4>(a, st);
+    case 5: return gdn_batch_kc<5>(a, st);
+    case 6: return gdn_batch_kc<6>(a, st);
+    case 7: return gdn_batch_kc<7>(a, st);
+    case 8: return gdn_batch_kc<8>(a, st);
     default: return hipErrorInvalidValue;
   }
 }

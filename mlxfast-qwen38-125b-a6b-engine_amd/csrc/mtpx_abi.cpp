@@ -937,6 +937,20 @@ int gdn_enqueue(Ctx* c, const GdnLayer* L, GdnState* st, const uint16_t* proj, i
   return MTPX_OK;
 }
 
+// A prefill batch of S positions through the core in one launch, every position committed: the
+// state holds them all, the conv base is in the other slot, nothing is left to replay.
+// Workspace: S * hv * 128 floats (the published recurrence outputs).
+int gdn_enqueue_batch(Ctx* c, const GdnLayer* L, GdnState* st, const uint16_t* proj, int S, uint16_t* gated,
+                      uint32_t* xp) {
+  GdnArgs a = gdn_args(st, L, proj, S, gated, xp);
+  a.ypub = ws_take<float>(c, (size_t)S * a.hv * 128);
+  LAUNCH(c, "gdn_batch", launch_gdn_batch(a, c->stream));
+  st->cur ^= 1;
+  st->window = 0;
+  st->committed = 0;
+  return MTPX_OK;
+}
+
 }  // namespace
 
 
@@ -2567,7 +2581,9 @@ int target_verify_enqueue(Ctx* c, Target* t, TargetState* s, const int32_t* ids,
     if (L.attn) any_attn = L.attn;
   const int SW = S < MAX_TOKENS ? S : MAX_TOKENS;  // positions of one recurrent window
   const size_t moe_ws = prefill ? moe_windows_ws_bytes(&t->layers[0].moe, S) : moe_ws_bytes(&t->layers[0].moe, S);
-  const size_t per_layer = std::max(std::max(mix + moe_ws, mix + (any_attn ? attn_ws_bytes(any_attn, S, T) : 0)),
+  const size_t gdn_ws = prefill ? al(4 * (size_t)S * gg.hv * 128) : 0;  // the batch's published outputs
+  const size_t per_layer = std::max(std::max(std::max(mix + moe_ws, mix + (any_attn ? attn_ws_bytes(any_attn, S, T) : 0)),
+                                             mix + gdn_ws),
                                     t->ple ? ple_ws_bytes(t->ple->cfg, SW) + al(2 * (size_t)S * W) : 0) + 4096;
   const size_t fixed = al(2 * (size_t)S * H) * 5 + al(2 * (size_t)S * W) * 4 + al(2 * (size_t)S * hc) * 2 +
                        al(4 * (size_t)S * (W / 32) * XP_DW) + al(4 * (size_t)S * XB * XP_DW) +
@@ -2624,12 +2640,12 @@ int target_verify_enqueue(Ctx* c, Target* t, TargetState* s, const int32_t* ids,
       const mtpx_q4& ip = L.gdn->w.in_proj;
       const mtpx_q4& op = L.gdn->w.out_proj;
       LAUNCH(c, "qmv_gdn_in", launch_qmv(ip.w, ip.s, ip.b, ip.sb, gg.pw, H, gs, xpH, S, proj, nullptr, st));
-      for (int w0 = 0; w0 < S; w0 += MAX_TOKENS) {  // window by window (one window when verifying)
-        const int n = S - w0 < MAX_TOKENS ? S - w0 : MAX_TOKENS;
-        if ((rc = gdn_enqueue(c, L.gdn, s->gdn[i], proj + (size_t)w0 * gg.pw, n, nullptr,
-                              xpG + (size_t)w0 * (VD / 32) * XP_DW)))
-          return rc;
-        if (prefill) s->gdn[i]->committed = n;
+      if (prefill) {  // the batch in one launch, committed
+        const size_t mark3 = c->ws_used;
+        if ((rc = gdn_enqueue_batch(c, L.gdn, s->gdn[i], proj, S, nullptr, xpG))) return rc;
+        c->ws_used = mark3;
+      } else if ((rc = gdn_enqueue(c, L.gdn, s->gdn[i], proj, S, nullptr, xpG))) {
+        return rc;
       }
       LAUNCH(c, "qmv_gdn_out", launch_qmv(op.w, op.s, op.b, op.sb, H, VD, gs, xpG, S, ao, nullptr, st));
     } else {

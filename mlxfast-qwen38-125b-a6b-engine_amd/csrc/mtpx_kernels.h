@@ -234,6 +234,8 @@ struct GdnArgs {
   float* ypub;                                  // [S, hv, 128] recurrence outputs published for the gated norm
 };
 hipError_t launch_gdn_step(const GdnArgs& a, hipStream_t st);
+// a prefill batch of a.S positions (any count), every one committed; a.ypub holds a.S positions
+hipError_t launch_gdn_batch(const GdnArgs& a, hipStream_t st);
 hipError_t launch_gdn_replay(const GdnArgs& a, float* ssm_dst, bf16* conv_dst, hipStream_t st);
 
 // --- PLE n-gram block (ple.hip)

@@ -298,17 +298,74 @@ __global__ __launch_bounds__(GDN_THREADS) void k_gdn_step(GdnArgs a) {
     }
 }
 
-// A prefill batch through the core in one launch (S positions, any count): the P committed steps
-// of the previous window replayed onto the state, then the batch window by window of MAX_TOKENS --
-// each window's prep (conv, SiLU, q/k norms, gates) into LDS and its recurrence steps, the float
-// operations of a verify window, so the same bits -- with every position committed: the state is
-// stored after the last position, the batch's last kc-1 conv input rows become the conv base
-// (slot nxt), and no journal is written.  The head's last workgroup runs the gated norm and the
-// prepared output blocks of every position, window by window.
+// A prefill batch through the core (S positions, any count), two launches.
+//   k_gdn_prep_batch: one workgroup per position: the conv, SiLU and q/k norms of every key head's
+//     q and k and every value head's v (a half-wave per 128-channel vector, as the step kernel
+//     does them), and every head's decay and beta gates, into the batch's prep buffers;
+//   k_gdn_batch: the step kernel's workgroups (four per value head), the P committed steps of the
+//     previous window replayed onto the state, then the batch's positions in order, the next
+//     window's prepped vectors loaded while the current one's recurrence runs; every position
+//     committed: the state is stored after the last one, the batch's last kc-1 conv input rows
+//     become the conv base (slot nxt), no journal is written; the head's last workgroup runs the
+//     gated norm and the prepared output blocks of every position.
+// The float operations of every position are a verify window's, so the bits are the same.
 template <int KC>
-__global__ __launch_bounds__(GDN_THREADS) void k_gdn_batch(GdnArgs a) {
-  __shared__ float qs[MAX_TOKENS][GDN_D], ks[MAX_TOKENS][GDN_D], vs[MAX_TOKENS][GDN_D], ys[MAX_TOKENS][GDN_D];
-  __shared__ float dec[MAX_TOKENS], bet[MAX_TOKENS];
+__global__ __launch_bounds__(GDN_THREADS) void k_gdn_prep_batch(GdnArgs a, GdnBatch b) {
+  const int t = blockIdx.x, hw = threadIdx.x >> 5, l = threadIdx.x & 31;
+  const int P = a.P;
+  const float inv_scale = 1.0f / sqrtf((float)GDN_D);
+  const float q_mul = round_bf(inv_scale * inv_scale), k_mul = round_bf(inv_scale);
+  const int ntask = 2 * a.hk + a.hv;  // q of every key head, k of every key head, v of every value head
+  for (int task = hw; task < ntask; task += GDN_THREADS / 32) {
+    const int kind = task < a.hk ? 0 : (task < 2 * a.hk ? 1 : 2);
+    const int vec = task;  // channel block: q heads, then k heads, then v heads
+    const int ch0 = vec * GDN_D + 4 * l;
+    uint2 xin[KC];
+#pragma unroll
+    for (int j = 0; j < KC; ++j) xin[j] = *reinterpret_cast<const uint2*>(gdn_row_ptr(a, P + t + j) + ch0);
+    uint32_t wt[2 * KC];
+#pragma unroll
+    for (int q = 0; q < 2 * KC; ++q) wt[q] = reinterpret_cast<const uint32_t*>(a.conv_w + (size_t)ch0 * KC)[q];
+    auto hbf = [](uint32_t w, int odd) { return __uint_as_float(odd ? (w & 0xffff0000u) : (w << 16)); };
+    float xs[4], acc = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float c = 0.0f;
+#pragma unroll
+      for (int j = 0; j < KC; ++j) {
+        const float xv = hbf(i < 2 ? xin[j].x : xin[j].y, i & 1);
+        const int e = i * KC + j;
+        c = c + xv * hbf(wt[e >> 1], e & 1);
+      }
+      const float x = silu_bf16(round_bf(c));
+      xs[i] = x;
+      acc = __builtin_fmaf(x, x, acc);
+    }
+    float4 o;
+    if (kind < 2) {
+      const float inv = 1.0f / sqrtf(half_wave_sum(acc) / 128.0f + 1e-6f);
+      const float mul = kind == 0 ? q_mul : k_mul;
+      o = make_float4(round_bf(mul * round_bf(xs[0] * inv)), round_bf(mul * round_bf(xs[1] * inv)),
+                      round_bf(mul * round_bf(xs[2] * inv)), round_bf(mul * round_bf(xs[3] * inv)));
+    } else {
+      o = make_float4(xs[0], xs[1], xs[2], xs[3]);
+    }
+    *reinterpret_cast<float4*>(b.vecs + ((size_t)t * ntask + vec) * GDN_D + 4 * l) = o;
+  }
+  for (int h = threadIdx.x; h < a.hv; h += GDN_THREADS) {
+    const bf16* prow = a.proj + (size_t)t * a.pw;
+    const float bt = sigmoid_bf16(bf2f(prow[a.b_off + h]));
+    const float ax = round_bf(bf2f(prow[a.a_off + h]) + bf2f(a.dt_bias[h]));
+    b.gates[((size_t)t * a.hv + h) * 2] = expf_det(a.neg_exp_alog[h] * logaddexp0_bf16(ax));
+    b.gates[((size_t)t * a.hv + h) * 2 + 1] = bt;
+  }
+}
+
+template <int KC>
+__global__ __launch_bounds__(GDN_THREADS) void k_gdn_batch(GdnArgs a, GdnBatch b) {
+  __shared__ float qs[2][MAX_TOKENS][GDN_D], ks[2][MAX_TOKENS][GDN_D], vs[2][MAX_TOKENS][GDN_D];
+  __shared__ float dec[2][MAX_TOKENS], bet[2][MAX_TOKENS];
+  __shared__ float ys[MAX_TOKENS][GDN_D];
   __shared__ bf16 gated[MAX_TOKENS][GDN_D];
   const int h = blockIdx.x, ratio = a.hv / a.hk, hk = h / ratio;
   const int r0 = blockIdx.y * (GDN_D / GDN_SPLIT);  // this workgroup's state rows
@@ -316,9 +373,46 @@ __global__ __launch_bounds__(GDN_THREADS) void k_gdn_batch(GdnArgs a) {
   const bool lead = (h % ratio) == 0 && w0;         // writes the q/k channels' conv base rows
   const int hw = threadIdx.x >> 5, l = threadIdx.x & 31;
   const int S = a.S, P = a.P, KM1 = a.kc - 1;
-  const float inv_scale = 1.0f / sqrtf((float)GDN_D);
-  const float q_mul = round_bf(inv_scale * inv_scale), k_mul = round_bf(inv_scale);
+  const int ntask = 2 * a.hk + a.hv;
   constexpr int RPH = GDN_D / GDN_SPLIT / (GDN_THREADS / 32);
+  // a window's prepped vectors: (q, k, v) x MAX_TOKENS x 128 floats as float4 units, and the gates
+  constexpr int U4 = 3 * MAX_TOKENS * GDN_D / 4;  // float4 units of a window
+  // this thread's units: u0 = threadIdx.x and u1 = threadIdx.x + GDN_THREADS (while < U4) -> (vector which,
+  // position tt, float4 e4); the source offsets (relative to the window's first position) and the LDS targets
+  // are the same every window
+  static_assert(U4 > GDN_THREADS && U4 <= 2 * GDN_THREADS, "two units per thread");
+  auto unit = [&](int u, const float*& src, float*& dst, int& tt) {
+    const int which = u / (MAX_TOKENS * GDN_D / 4), rem = u % (MAX_TOKENS * GDN_D / 4);
+    const int e4 = rem % (GDN_D / 4);
+    tt = rem / (GDN_D / 4);
+    const int vec = which == 0 ? hk : (which == 1 ? a.hk + hk : 2 * a.hk + h);
+    src = b.vecs + (size_t)vec * GDN_D + 4 * e4;
+    dst = (which == 0 ? &qs[0][tt][0] : (which == 1 ? &ks[0][tt][0] : &vs[0][tt][0])) + 4 * e4;
+  };
+  const bool has1 = (int)threadIdx.x + GDN_THREADS < U4;
+  const float *src0, *src1;
+  float *dst0, *dst1;
+  int tt0, tt1;
+  unit((int)threadIdx.x, src0, dst0, tt0);
+  unit(has1 ? (int)threadIdx.x + GDN_THREADS : (int)threadIdx.x, src1, dst1, tt1);
+  const int gt = (int)threadIdx.x / 2, gk = (int)threadIdx.x & 1;  // gate thread: position, decay or beta
+  float4 pv0, pv1;
+  float pg = 0.0f;
+  const size_t pstride = (size_t)ntask * GDN_D;
+  // unconditional loads (clamped position: positions past S are loaded again and not used)
+#define GDN_FETCH(T0)                                                                                       \
+  do {                                                                                                      \
+    pv0 = *reinterpret_cast<const float4*>(src0 + (size_t)min((T0) + tt0, S - 1) * pstride);                \
+    pv1 = *reinterpret_cast<const float4*>(src1 + (size_t)min((T0) + tt1, S - 1) * pstride);                \
+    if ((int)threadIdx.x < 2 * MAX_TOKENS) pg = b.gates[((size_t)min((T0) + gt, S - 1) * a.hv + h) * 2 + gk]; \
+  } while (0)
+#define GDN_STORE(BUF)                                                                                     \
+  do {                                                                                                     \
+    *reinterpret_cast<float4*>(dst0 + (BUF) * MAX_TOKENS * GDN_D) = pv0;                                     \
+    if (has1) *reinterpret_cast<float4*>(dst1 + (BUF) * MAX_TOKENS * GDN_D) = pv1;                           \
+    if ((int)threadIdx.x < 2 * MAX_TOKENS) (gk ? bet : dec)[(BUF)][gt] = pg;                                \
+  } while (0)
+  GDN_FETCH(0);
   float s[RPH][4];
 #pragma unroll
   for (int i = 0; i < RPH; ++i) {
@@ -344,66 +438,19 @@ __global__ __launch_bounds__(GDN_THREADS) void k_gdn_batch(GdnArgs a) {
       }
     }
   }
-  for (int t0 = 0; t0 < S; t0 += MAX_TOKENS) {
+  GDN_STORE(0);
+  __syncthreads();
+  for (int t0 = 0, buf = 0; t0 < S; t0 += MAX_TOKENS, buf ^= 1) {
     const int n = S - t0 < MAX_TOKENS ? S - t0 : MAX_TOKENS;
-    // ---- prep of positions t0 .. t0 + n - 1 (window slot t = position - t0)
-    for (int task = hw; task < 3 * n; task += GDN_THREADS / 32) {
-      const int t = task / 3, kind = task % 3;
-      const int vec = kind == 0 ? hk : (kind == 1 ? a.hk + hk : 2 * a.hk + h);
-      const int ch0 = vec * GDN_D + 4 * l;
-      uint2 xin[KC];
-#pragma unroll
-      for (int j = 0; j < KC; ++j) xin[j] = *reinterpret_cast<const uint2*>(gdn_row_ptr(a, P + t0 + t + j) + ch0);
-      uint32_t wt[2 * KC];
-#pragma unroll
-      for (int q = 0; q < 2 * KC; ++q) wt[q] = reinterpret_cast<const uint32_t*>(a.conv_w + (size_t)ch0 * KC)[q];
-      auto hbf = [](uint32_t w, int odd) { return __uint_as_float(odd ? (w & 0xffff0000u) : (w << 16)); };
-      float xs[4], acc = 0.0f;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        float c = 0.0f;
-#pragma unroll
-        for (int j = 0; j < KC; ++j) {
-          const float xv = hbf(i < 2 ? xin[j].x : xin[j].y, i & 1);
-          const int e = i * KC + j;
-          c = c + xv * hbf(wt[e >> 1], e & 1);
-        }
-        const float x = silu_bf16(round_bf(c));
-        xs[i] = x;
-        acc = __builtin_fmaf(x, x, acc);
-      }
-      if (kind < 2) {
-        const float inv = 1.0f / sqrtf(half_wave_sum(acc) / 128.0f + 1e-6f);
-        const float mul = kind == 0 ? q_mul : k_mul;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float val = round_bf(mul * round_bf(xs[i] * inv));
-          if (kind == 0)
-            qs[t][4 * l + i] = val;
-          else
-            ks[t][4 * l + i] = val;
-        }
-      } else {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) vs[t][4 * l + i] = xs[i];
-      }
-    }
-    if ((int)threadIdx.x < n) {
-      const int t = threadIdx.x;
-      const bf16* prow = a.proj + (size_t)(t0 + t) * a.pw;
-      const float b = sigmoid_bf16(bf2f(prow[a.b_off + h]));
-      const float ax = round_bf(bf2f(prow[a.a_off + h]) + bf2f(a.dt_bias[h]));
-      dec[t] = expf_det(a.neg_exp_alog[h] * logaddexp0_bf16(ax));
-      bet[t] = b;
-    }
-    __syncthreads();
-    // ---- recurrence of the window's positions
+    const bool more = t0 + MAX_TOKENS < S;
+    if (more) GDN_FETCH(t0 + MAX_TOKENS);  // in flight during this window's recurrence
 #pragma unroll
     for (int i = 0; i < RPH; ++i) {
       const int r = r0 + hw + 16 * i;
       for (int t = 0; t < n; ++t) {
-        const float gd = dec[t];
-        const float k0 = ks[t][4 * l], k1 = ks[t][4 * l + 1], k2 = ks[t][4 * l + 2], k3 = ks[t][4 * l + 3];
+        const float gd = dec[buf][t];
+        const float k0 = ks[buf][t][4 * l], k1 = ks[buf][t][4 * l + 1], k2 = ks[buf][t][4 * l + 2],
+                    k3 = ks[buf][t][4 * l + 3];
         s[i][0] = s[i][0] * gd;
         float kv = 0.0f + s[i][0] * k0;
         float comp = 0.0f;
@@ -425,21 +472,22 @@ __global__ __launch_bounds__(GDN_THREADS) void k_gdn_batch(GdnArgs a) {
           kv = next;
         }
         const float kvm = half_wave_sum(kv);
-        const float delta = (vs[t][r] - kvm) * bet[t];
+        const float delta = (vs[buf][t][r] - kvm) * bet[buf][t];
         float o = 0.0f;
         s[i][0] = __builtin_fmaf(k0, delta, s[i][0]);
-        o = __builtin_fmaf(s[i][0], qs[t][4 * l], o);
+        o = __builtin_fmaf(s[i][0], qs[buf][t][4 * l], o);
         s[i][1] = __builtin_fmaf(k1, delta, s[i][1]);
-        o = __builtin_fmaf(s[i][1], qs[t][4 * l + 1], o);
+        o = __builtin_fmaf(s[i][1], qs[buf][t][4 * l + 1], o);
         s[i][2] = __builtin_fmaf(k2, delta, s[i][2]);
-        o = __builtin_fmaf(s[i][2], qs[t][4 * l + 2], o);
+        o = __builtin_fmaf(s[i][2], qs[buf][t][4 * l + 2], o);
         s[i][3] = __builtin_fmaf(k3, delta, s[i][3]);
-        o = __builtin_fmaf(s[i][3], qs[t][4 * l + 3], o);
+        o = __builtin_fmaf(s[i][3], qs[buf][t][4 * l + 3], o);
         const float y = half_wave_sum(o);
         if (l == 0) st_pub(a.ypub + ((size_t)(t0 + t) * a.hv + h) * GDN_D + r, round_bf(y));
       }
     }
-    __syncthreads();  // the next window's prep overwrites qs, ks, vs, dec, bet
+    if (more) GDN_STORE(buf ^ 1);  // the other buffer: last read in the previous window, before its barrier
+    __syncthreads();
   }
 #pragma unroll
   for (int i = 0; i < RPH; ++i)
@@ -537,21 +585,22 @@ hipError_t launch_gdn_step(const GdnArgs& a, hipStream_t st) {
 }
 
 template <int KC>
-static hipError_t gdn_batch_kc(const GdnArgs& a, hipStream_t st) {
-  if (!a.tickets || !a.ypub) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_gdn_batch<KC>, dim3(a.hv, GDN_SPLIT), dim3(GDN_THREADS), 0, st, a);
+static hipError_t gdn_batch_kc(const GdnArgs& a, const GdnBatch& b, hipStream_t st) {
+  if (!a.tickets || !a.ypub || !b.vecs || !b.gates || a.S < 1) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_gdn_prep_batch<KC>, dim3(a.S), dim3(GDN_THREADS), 0, st, a, b);
+  hipLaunchKernelGGL(k_gdn_batch<KC>, dim3(a.hv, GDN_SPLIT), dim3(GDN_THREADS), 0, st, a, b);
   return hipGetLastError();
 }
 
-hipError_t launch_gdn_batch(const GdnArgs& a, hipStream_t st) {
+hipError_t launch_gdn_batch(const GdnArgs& a, const GdnBatch& b, hipStream_t st) {
   switch (a.kc) {
-    case 2: return gdn_batch_kc<2>(a, st);
-    case 3: return gdn_batch_kc<3>(a, st);
-    case 4: return gdn_batch_kc<4>(a, st);
-    case 5: return gdn_batch_kc<5>(a, st);
-    case 6: return gdn_batch_kc<6>(a, st);
-    case 7: return gdn_batch_kc<7>(a, st);
-    case 8: return gdn_batch_kc<8>(a, st);
+    case 2: return gdn_batch_kc<2>(a, b, st);
+    case 3: return gdn_batch_kc<3>(a, b, st);
+    case 4: return gdn_batch_kc<4>(a, b, st);
+    case 5: return gdn_batch_kc<5>(a, b, st);
+    case 6: return gdn_batch_kc<6>(a, b, st);
+    case 7: return gdn_batch_kc<7>(a, b, st);
+    case 8: return gdn_batch_kc<8>(a, b, st);
     default: return hipErrorInvalidValue;
   }
 }

@@ -939,12 +939,15 @@ int gdn_enqueue(Ctx* c, const GdnLayer* L, GdnState* st, const uint16_t* proj, i
 
 // A prefill batch of S positions through the core in one launch, every position committed: the
 // state holds them all, the conv base is in the other slot, nothing is left to replay.
-// Workspace: S * hv * 128 floats (the published recurrence outputs).
+// Workspace: S * (hv * 128 + (2 hk + hv) * 128 + 2 hv) floats (recurrence outputs, prepped vectors, gates).
 int gdn_enqueue_batch(Ctx* c, const GdnLayer* L, GdnState* st, const uint16_t* proj, int S, uint16_t* gated,
                       uint32_t* xp) {
   GdnArgs a = gdn_args(st, L, proj, S, gated, xp);
   a.ypub = ws_take<float>(c, (size_t)S * a.hv * 128);
-  LAUNCH(c, "gdn_batch", launch_gdn_batch(a, c->stream));
+  GdnBatch b;
+  b.vecs = ws_take<float>(c, (size_t)S * (2 * a.hk + a.hv) * 128);
+  b.gates = ws_take<float>(c, (size_t)S * a.hv * 2);
+  LAUNCH(c, "gdn_batch", launch_gdn_batch(a, b, c->stream));
   st->cur ^= 1;
   st->window = 0;
   st->committed = 0;
@@ -2581,7 +2584,9 @@ int target_verify_enqueue(Ctx* c, Target* t, TargetState* s, const int32_t* ids,
     if (L.attn) any_attn = L.attn;
   const int SW = S < MAX_TOKENS ? S : MAX_TOKENS;  // positions of one recurrent window
   const size_t moe_ws = prefill ? moe_windows_ws_bytes(&t->layers[0].moe, S) : moe_ws_bytes(&t->layers[0].moe, S);
-  const size_t gdn_ws = prefill ? al(4 * (size_t)S * gg.hv * 128) : 0;  // the batch's published outputs
+  const size_t gdn_ws = prefill ? al(4 * (size_t)S * gg.hv * 128) + al(4 * (size_t)S * (2 * gg.hk + gg.hv) * 128) +
+                                      al(8 * (size_t)S * gg.hv)
+                                : 0;  // the batch's recurrence outputs, prepped vectors and gates
   const size_t per_layer = std::max(std::max(std::max(mix + moe_ws, mix + (any_attn ? attn_ws_bytes(any_attn, S, T) : 0)),
                                              mix + gdn_ws),
                                     t->ple ? ple_ws_bytes(t->ple->cfg, SW) + al(2 * (size_t)S * W) : 0) + 4096;

@@ -235,7 +235,11 @@ struct GdnArgs {
 };
 hipError_t launch_gdn_step(const GdnArgs& a, hipStream_t st);
 // a prefill batch of a.S positions (any count), every one committed; a.ypub holds a.S positions
-hipError_t launch_gdn_batch(const GdnArgs& a, hipStream_t st);
+struct GdnBatch {
+  float* vecs;   // [S, 2*hk + hv, 128] the positions' q (per key head), k (per key head), v (per value head)
+  float* gates;  // [S, hv, 2] decay, beta
+};
+hipError_t launch_gdn_batch(const GdnArgs& a, const GdnBatch& b, hipStream_t st);
 hipError_t launch_gdn_replay(const GdnArgs& a, float* ssm_dst, bf16* conv_dst, hipStream_t st);
 
 // --- PLE n-gram block (ple.hip)

@@ -92,8 +92,10 @@ int mtpx_q4_pack_sb(mtpx_ctx ctx, const uint16_t* scales, const uint16_t* biases
                     int K, int gs, uint32_t* out);
 
 /* ---- a2-a4, a12: q4 GEMV / small-M GEMM ------------------------------------
- * y[M, N] = x[M, K] . W[N, K]^T, M <= 8, bf16 out (yf: optional f32 before
- * rounding); sb: packed scale/bias rows or NULL.  Replaces MLX quantizedMM's
+ * y[M, N] = x[M, K] . W[N, K]^T, M <= 4096, bf16 out (yf: optional f32 before
+ * rounding); sb: packed scale/bias rows or NULL.  Every token's row is the
+ * same whatever M (above 8 tokens: a prefill batch's GEMM on the matrix cores
+ * where sb is given and the shape allows).  Replaces MLX quantizedMM's
  * qmv_fast / qmv / qmv_wide (MLX/backend/metal/kernels/quantized.h:758,825,989)
  * and the track's TrackQuantWeight.apply / TrackLUTGemv
  * (Runner/FastModel/TrackFastWeights.swift:40-49, Runner/FastModel/TrackAffineLUT.swift:121-368). */

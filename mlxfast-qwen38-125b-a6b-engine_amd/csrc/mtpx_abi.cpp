@@ -547,7 +547,7 @@ size_t head_ws_bytes(const Head* hd, int S, int T) {
   const int XB = (H > HQ * D ? H : HQ * D) / 32;
   // per mixer call (three per step): lo, act [S, LW]; inj [S, hc]; xpL; w [S, W]
   const size_t mix = al(2 * (size_t)S * LW) * 2 + al(2 * (size_t)S * g.hc) + al(4 * (size_t)S * (LW / 32) * XP_DW) +
-                     al(2 * (size_t)S * W);
+                     al(2 * (size_t)S * W) + (S > MAX_TOKENS ? al(4 * (size_t)S * (W / 32) * XMB_DW) : 0);
   const size_t moe = S > MAX_TOKENS ? moe_windows_ws_bytes(&hd->w.layer.moe, S) : moe_ws_bytes(&hd->w.layer.moe, S);
   return moe + attn_ws_bytes(hd->layer, S, T) + 3 * mix + al(2 * (size_t)S * H) * 6 +
          al(2 * (size_t)S * W) * 5 + al(2 * (size_t)S * g.hc) + al(4 * (size_t)S * XB * XP_DW) +
@@ -590,9 +590,15 @@ int hc_mix_enqueue(Ctx* c, const HcGeom& g, const mtpx_hc_weights* hw, const uin
   uint16_t* inj = ws_take<uint16_t>(c, (size_t)S * g.hc);
   uint32_t* xpL = ws_take<uint32_t>(c, (size_t)S * (LW / 32) * XP_DW);
   uint16_t* wm = ws_take<uint16_t>(c, (size_t)S * W);
-  LAUNCH(c, "hc_down", launch_qmv(hw->down.w, hw->down.s, hw->down.b, hw->down.sb, LW, W, gs, xpW, S, lo, nullptr, st));
-  if (hw->inject.w)
-    LAUNCH(c, "hc_inject", launch_qmv(hw->inject.w, hw->inject.s, hw->inject.b, hw->inject.sb, g.hc, W, gs, xpW, S, inj, nullptr, st));
+  if (qmv_pair_ok(hw->down.sb, hw->inject.w, hw->inject.sb, W, S)) {  // a batch: down and inject rows in one launch
+    uint32_t* xmb = ws_take<uint32_t>(c, (size_t)S * (W / 32) * XMB_DW);
+    LAUNCH(c, "hc_down_inject", launch_qmv_pair(hw->down.w, hw->down.sb, LW, reinterpret_cast<bf16*>(lo), hw->inject.w,
+                                                hw->inject.sb, g.hc, reinterpret_cast<bf16*>(inj), W, gs, xpW, xmb, S, st));
+  } else {
+    LAUNCH(c, "hc_down", launch_qmv(hw->down.w, hw->down.s, hw->down.b, hw->down.sb, LW, W, gs, xpW, S, lo, nullptr, st));
+    if (hw->inject.w)
+      LAUNCH(c, "hc_inject", launch_qmv(hw->inject.w, hw->inject.s, hw->inject.b, hw->inject.sb, g.hc, W, gs, xpW, S, inj, nullptr, st));
+  }
   LAUNCH(c, "hc_silu", launch_silu_xprep(lo, S, LW, act, xpL, st));
   LAUNCH(c, "hc_up", launch_qmv(hw->up.w, hw->up.s, hw->up.b, hw->up.sb, W, LW, gs, xpL, S, wm, nullptr, st));
   LAUNCH(c, "hc_mix", launch_hc_mix(wm, normed, hw->inject.w ? inj : nullptr, S, g.hc, H, x, j, xpH, st));
@@ -1473,7 +1479,7 @@ int mtpx_qmv(mtpx_ctx h, const uint32_t* wq, const uint16_t* s, const uint16_t* 
              const uint16_t* x, int M, uint16_t* y, float* yf) {
   Ctx* c = C(h);
   ARG(c && wq && s && b && x && y, "null argument");
-  ARG(N >= 1 && M >= 1 && M <= MAX_TOKENS, "N=%d M=%d", N, M);
+  ARG(N >= 1 && M >= 1 && M <= QMV_MAX_TOKENS, "N=%d M=%d", N, M);
   ARG(gs_ok(gs) && k_ok(K, gs), "K=%d gs=%d unsupported", K, gs);
   if (set_device(c)) return MTPX_ERR_HIP;
   const size_t xpn = (size_t)M * (K / 32) * XP_DW;
@@ -2578,7 +2584,8 @@ int target_verify_enqueue(Ctx* c, Target* t, TargetState* s, const int32_t* ids,
     if (kv) kv->offset = s->offset;
   const int T = (int)s->offset + S;
   const size_t mix = al(2 * (size_t)S * g.lowrank) * 2 + al(2 * (size_t)S * hc) +
-                     al(4 * (size_t)S * (g.lowrank / 32) * XP_DW) + al(2 * (size_t)S * W);
+                     al(4 * (size_t)S * (g.lowrank / 32) * XP_DW) + al(2 * (size_t)S * W) +
+                     (S > MAX_TOKENS ? al(4 * (size_t)S * (W / 32) * XMB_DW) : 0);
   const Layer* any_attn = nullptr;
   for (const TargetLayer& L : t->layers)
     if (L.attn) any_attn = L.attn;

@@ -11,6 +11,7 @@ namespace mtpx {
 constexpr int QMV_IT = 8;        // max blocks per lane: K <= 8 * 32 * lanes_for_blocks(K/32)
 constexpr int MAX_TOKENS = 8;    // verify width ceiling (draft depth <= 7)
 constexpr int HEAD_BATCH = 256;  // MTP head positions per call (the drafter's backlog flush)
+constexpr int QMV_MAX_TOKENS = 4096;  // tokens per mtpx_qmv call
 constexpr int MAX_TOPK = 16;
 constexpr int ATTN_CHUNK = 32;   // keys per split-KV partial
 
@@ -66,6 +67,14 @@ __device__ __forceinline__ bool ticket_last(uint32_t* ctr, uint32_t last) {
 // --- dense q4 GEMV and friends (qmv.hip)
 hipError_t launch_xprep(const bf16* x, int M, int K, uint32_t* xp, hipStream_t st);
 // sb: packed scale/bias rows (sb_row_len(K, gs) u32 per row) or null
+// Two few-row matrices (N1, N2 rows; w2 may be null) over one batch of M > MAX_TOKENS prepared
+// tokens, through xmb [M][K/32][XMB_DW] (workspace), where qmv_pair_ok holds (else launch_qmv per
+// matrix).
+constexpr int XMB_DW = 36;
+bool qmv_pair_ok(const uint32_t* sb1, const uint32_t* w2, const uint32_t* sb2, int K, int M);
+hipError_t launch_qmv_pair(const uint32_t* w1, const uint32_t* sb1, int N1, bf16* y1, const uint32_t* w2,
+                           const uint32_t* sb2, int N2, bf16* y2, int K, int gs, const uint32_t* xp, uint32_t* xmb,
+                           int M, hipStream_t st);
 hipError_t launch_qmv(const uint32_t* wq, const bf16* s, const bf16* b, const uint32_t* sb, int N, int K, int gs,
                       const uint32_t* xp, int M, bf16* y, float* yf, hipStream_t st);
 hipError_t launch_pack_sb(const bf16* s, const bf16* b, int64_t N, int K, int gs, uint32_t* out, hipStream_t st);

@@ -106,6 +106,7 @@ __global__ __launch_bounds__(256) void k_qmv(const uint32_t* __restrict__ wq, co
 // block; the next four blocks' loads are in flight while these are computed.
 constexpr int MMA_TOK = 4;   // tokens per tile (4 tokens x 4 limbs = 16 A rows)
 constexpr int MB_DW = 36;    // LDS block: [limb][word g][even, odd] (32 dwords), p, SX, pad
+static_assert(MB_DW == XMB_DW, "the four-limb block in memory");
 constexpr int MMA_THREADS = 512;
 
 typedef int v4i_t __attribute__((ext_vector_type(4)));
@@ -332,6 +333,343 @@ __global__ __launch_bounds__(MMA_THREADS) void k_qmv_mma(const uint32_t* __restr
         y[(size_t)tok * N + row] = f2bf(v[tq]);
         if (yf) yf[(size_t)tok * N + row] = v[tq];
       }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Dense GEMM on the matrix cores for a batch of many tokens (a prefill batch), with the same bits
+// as k_qmv and k_qmv_mma: one weight operand serves 4 QT tokens.  A workgroup owns 128 rows (eight
+// waves of 16) and 4 QT tokens, and walks K chain by chain.  The butterfly that folds the lane
+// rule's L chains (level S = L/2 .. 1: v[u] += v[u + S]) is a perfect binary tree over the chains
+// taken in bit-reversed order (L = 8: ((c0 + c4) + (c2 + c6)) + ((c1 + c5) + (c3 + c7))), so the
+// chains are finished in that order, four per group (leaves 4q .. 4q + 3, folded as ((a + b) +
+// (c + d))), and the groups fold by a binary counter over a stack of log2(L/4) subtrees: 4 QT
+// (token, row) sums per chain of the group and one per stack level live at a time, whatever L.
+// Step (q, it) stages block u + L it of each of the group's four chains u for the workgroup's
+// tokens in LDS (the four-limb layout of k_qmv_mma, double buffered); each lane group loads one of
+// the four blocks' 16-byte rows and the 4x4 transpose gives every lane group word g of all four.
+// The next step's weights, (scale, bias) pairs and activation words are in flight while a step is
+// computed.  Every chain adds its blocks in K order from 0 with the block combine of k_qmv_mma.
+constexpr int QMM_THREADS = 512;
+constexpr int QMM_ROWS = 128;     // eight waves x 16 rows
+constexpr int QMM_MIN_ROWS = 1024;  // smallest matrix the batch GEMM takes (fewer rows: too few workgroups)
+
+constexpr int ilog2(int v) { return v <= 1 ? 0 : 1 + ilog2(v / 2); }
+
+template <int L, int IT, int QT>
+__global__ __launch_bounds__(QMM_THREADS) void k_qmm(const uint32_t* __restrict__ wq, const uint32_t* __restrict__ sbp,
+                                                    int N, int K, int gs, const uint32_t* __restrict__ xp, int M,
+                                                    bf16* __restrict__ y, float* __restrict__ yf, int tiles,
+                                                    int tblocks) {
+  constexpr int NB = L * IT;
+  constexpr int QTOK = MMA_TOK * QT;                // tokens per workgroup
+  constexpr int LOGL = ilog2(L), LOGQ = LOGL - 2;   // stack levels: subtrees of 4, 8, .. L/2 chains
+  constexpr int STEPS = (L / 4) * IT;
+  constexpr int SDW = QTOK * 4 * MB_DW;             // one stage: [token][block of the group][MB_DW]
+  constexpr int NU = QTOK * 4 * 8 / QMM_THREADS;    // activation units (token, block, word, even/odd)
+  static_assert(L >= 4 && (1 << LOGL) == L && NU >= 1 && NU * QMM_THREADS == QTOK * 32,
+                "four chains per group, whole units per thread");
+  extern __shared__ uint32_t lds[];
+  // workgroup id -> (XCD id % 8, k = id / 8): the token blocks of a row tile are consecutive
+  // workgroups of one XCD, so they read the tile's weights through one L2
+  const int xcd = (int)blockIdx.x & 7, kk = (int)blockIdx.x >> 3;
+  const int tile = (kk / tblocks) * 8 + xcd, tb = kk - (kk / tblocks) * tblocks;
+  if (tile >= tiles) return;  // whole workgroup, before any barrier
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int n = lane & 15, g = lane >> 4;
+  const int row = tile * QMM_ROWS + wave * 16 + n;
+  const int rc = row < N ? row : N - 1;
+  const int rs = gs == 32 ? 0 : gs == 64 ? 1 : 2;  // log2 of the blocks per scale group
+  const uint32_t* wrow = wq + (size_t)rc * (K / 8);
+  const uint32_t* srow = sbp + (size_t)rc * sb_row_len(K, gs);
+  const int m0 = tb * QTOK, Mt = min(M - m0, QTOK);
+  xp += (size_t)m0 * NB * XP_DW;
+  // chain of leaf position i (bit reversal over log2 L bits)
+  auto chain = [](int i) { return (int)(__builtin_bitreverse32((uint32_t)i) >> (32 - LOGL)); };
+  // activation words of step s: unit (token t, block b, word ge >> 1, even/odd ge & 1); units with
+  // ge < 2 also carry word ge of the block's (p, SX) pair, the others a copy into the block's pad
+  // dwords, so every thread runs the same loads and stores (no branch inside a step)
+  uint32_t aw[NU][4];
+  auto load_act = [&](int s) {
+    const int q = s / IT, it = s - q * IT;
+#pragma unroll
+    for (int k = 0; k < NU; ++k) {
+      const int u = threadIdx.x + k * QMM_THREADS;
+      const int t = u >> 5, b = (u >> 3) & 3, ge = u & 7;
+      const int j = chain(4 * q + b) + L * it;  // < NB for every step index
+      const bool in = t < Mt;
+      const uint32_t* src = xp + ((size_t)(in ? t : 0) * NB + j) * XP_DW;
+      const uint32_t* sw = src + ((ge & 1) ? 4 : 0) + (ge >> 1);
+      const uint32_t v0 = sw[0], v1 = sw[8], v2 = sw[16], v3 = src[24 + (ge & 1)];
+      aw[k][0] = in ? v0 : 0u;
+      aw[k][1] = in ? v1 : 0u;
+      aw[k][2] = in ? v2 : 0u;
+      aw[k][3] = in ? v3 : 0u;
+    }
+  };
+  auto store_act = [&](uint32_t* st) {
+#pragma unroll
+    for (int k = 0; k < NU; ++k) {
+      const int u = threadIdx.x + k * QMM_THREADS;
+      const int t = u >> 5, b = (u >> 3) & 3, ge = u & 7;
+      const uint32_t w0 = aw[k][0], w1 = aw[k][1];
+      uint32_t* blk = st + (t * 4 + b) * MB_DW;
+      uint32_t* dst = blk + 2 * (ge >> 1) + (ge & 1);
+      dst[0] = w0 & 0x7f7f7f7fu;                                          // bits 0-6
+      dst[8] = ((w0 >> 7) & 0x01010101u) | ((w1 << 1) & 0x7e7e7e7eu);    // bits 7-13
+      dst[16] = (w1 >> 6) & 0x03030303u;                                  // bits 14-15
+      dst[24] = aw[k][2];                                                 // bits 16-23 (signed)
+      blk[(ge < 2 ? 32 : 34) + (ge & 1)] = aw[k][3];                      // p, SX (or the pad)
+    }
+  };
+  // weights and (scale, bias) pairs of step s for this lane's row
+  uint4 wc, wn;
+  uint32_t pc[4], pn[4];
+  auto load_w = [&](int s, uint4& w, uint32_t (&p)[4]) {
+    const int q = s / IT, it = s - q * IT;
+    w = ldg16(wrow + (size_t)(chain(4 * q + g) + L * it) * 4);
+#pragma unroll
+    for (int b = 0; b < 4; ++b) p[b] = srow[(chain(4 * q + b) >> rs) * IT + it];
+  };
+  load_act(0);
+  store_act(lds);
+  load_w(0, wc, pc);
+  load_act(1);  // past the last step the loads still address blocks of the matrix (unused)
+  __syncthreads();
+  float ch[4][QT], stk[LOGQ > 0 ? LOGQ : 1][QT], res[QT];
+#pragma unroll
+  for (int b = 0; b < 4; ++b)
+#pragma unroll
+    for (int tq = 0; tq < QT; ++tq) ch[b][tq] = 0.0f;
+  // A operand of lane: token 4 tq + (lane & 15) / 4, limb lane & 3, word g; (p, SX) of token 4 tq + g
+  const int aoff2 = ((((lane & 15) >> 2) * 4) * MB_DW + (lane & 3) * 8 + 2 * g) / 2;  // in uint2
+  const int poff2 = ((g * 4) * MB_DW + 32) / 2;
+#pragma unroll 1
+  for (int s = 0; s < STEPS; ++s) {
+    const int q = s / IT, it = s - q * IT;
+    load_w(s + 1, wn, pn);
+    const uint2* st2 = reinterpret_cast<const uint2*>(lds + (s & 1) * SDW);  // 8-byte LDS reads
+    const auto p0 = __builtin_amdgcn_permlane32_swap(wc.x, wc.z, false, false);
+    const auto p1 = __builtin_amdgcn_permlane32_swap(wc.y, wc.w, false, false);
+    const auto q0 = __builtin_amdgcn_permlane16_swap(p0[0], p1[0], false, false);
+    const auto q1 = __builtin_amdgcn_permlane16_swap(p0[1], p1[1], false, false);
+    const uint32_t T[4] = {q0[0], q0[1], q1[0], q1[1]};
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const long bop = (long)(T[b] & 0x0f0f0f0fu) | ((long)((T[b] >> 4) & 0x0f0f0f0fu) << 32);
+      const uint32_t sb = pc[b];
+      // the block's QT products first (independent), then their combines in token-group order
+      v4i_t d[QT];
+#pragma unroll
+      for (int tq = 0; tq < QT; ++tq) {
+        const long aop = *reinterpret_cast<const long*>(st2 + aoff2 + (tq * 16 + b) * (MB_DW / 2));
+        const v4i_t z = {0, 0, 0, 0};
+        d[tq] = __builtin_amdgcn_mfma_i32_16x16x32_i8(aop, bop, z, 0, 0, 0);
+      }
+#pragma unroll
+      for (int tq = 0; tq < QT; ++tq) {
+        const int low = d[tq][0] + 128 * d[tq][1] + 16384 * d[tq][2];
+        const float dx = __builtin_fmaf((float)d[tq][3], 65536.0f, (float)low);
+        const uint2 ps = st2[poff2 + (tq * 16 + b) * (MB_DW / 2)];
+        float& a = ch[b][tq];
+        a = __builtin_fmaf(__uint_as_float(sb << 16), dx * __uint_as_float(ps.x), a);
+        a = __builtin_fmaf(__uint_as_float(sb & 0xffff0000u), __uint_as_float(ps.y), a);
+      }
+      __builtin_amdgcn_sched_barrier(0);  // one block's products and operands live at a time
+    }
+    store_act(lds + ((s + 1) & 1) * SDW);
+    load_act(s + 2);
+    __syncthreads();
+    wc = wn;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) pc[b] = pn[b];
+    if (it == IT - 1) {  // the group's subtree ((a + b) + (c + d)), then the binary counter over the groups
+#pragma unroll
+      for (int tq = 0; tq < QT; ++tq) {
+        float x = (ch[0][tq] + ch[1][tq]) + (ch[2][tq] + ch[3][tq]);
+        bool open = true;
+#pragma unroll
+        for (int k = 0; k < LOGQ; ++k) {
+          if (open) {
+            if ((q >> k) & 1) {
+              x = stk[k][tq] + x;
+            } else {
+              stk[k][tq] = x;
+              open = false;
+            }
+          }
+        }
+        if (open) res[tq] = x;  // the last group (every bit of q set): the whole tree
+#pragma unroll
+        for (int b = 0; b < 4; ++b) ch[b][tq] = 0.0f;
+      }
+    }
+  }
+#pragma unroll
+  for (int tq = 0; tq < QT; ++tq) {
+    const int t = tq * MMA_TOK + g;
+    if (t < Mt && row < N) {
+      y[(size_t)(m0 + t) * N + row] = f2bf(res[tq]);
+      if (yf) yf[(size_t)(m0 + t) * N + row] = res[tq];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Prepared blocks xp [M][NB][XP_DW] -> the matrix cores' four-limb layout in memory, xmb
+// [M][NB][MB_DW] (limbs at dwords 0..31, p and SX at 32, 33): one thread per (token, block, word,
+// even/odd) unit, as the GEMMs' LDS staging converts them.
+__global__ __launch_bounds__(256) void k_xmb(const uint32_t* __restrict__ xp, int units, uint32_t* __restrict__ xmb) {
+  const int u = blockIdx.x * 256 + threadIdx.x;
+  if (u >= units) return;
+  const int blk = u >> 3, ge = u & 7;  // blk = token * NB + block
+  const uint32_t* src = xp + (size_t)blk * XP_DW;
+  const uint32_t* sw = src + ((ge & 1) ? 4 : 0) + (ge >> 1);
+  const uint32_t w0 = sw[0], w1 = sw[8];
+  uint32_t* dst = xmb + (size_t)blk * MB_DW + 2 * (ge >> 1) + (ge & 1);
+  dst[0] = w0 & 0x7f7f7f7fu;                                          // bits 0-6
+  dst[8] = ((w0 >> 7) & 0x01010101u) | ((w1 << 1) & 0x7e7e7e7eu);    // bits 7-13
+  dst[16] = (w1 >> 6) & 0x03030303u;                                  // bits 14-15
+  dst[24] = sw[16];                                                   // bits 16-23 (signed)
+  if (ge < 2) xmb[(size_t)blk * MB_DW + 32 + ge] = src[24 + ge];      // p, SX
+}
+
+// Batch GEMM for matrices of few rows and long K (the hyper-connection mixer's down and inject
+// projections over a prefill batch), same bits as k_qmv: a workgroup owns one 16-row tile of one
+// of two matrices and 4 QT tokens; its four waves take a quarter of the chain groups each (a
+// subtree of L/4 chains of the butterfly's bit-reversed leaf order, folded as in k_qmm), and the
+// quarters meet in LDS as ((n0 + n1) + (n2 + n3)).  A operands and (p, SX) pairs come straight
+// from the four-limb layout in memory (k_xmb), each step's loads in flight during the previous one.
+constexpr int QMN_THREADS = 256;
+
+template <int L, int IT, int QT>
+__global__ __launch_bounds__(QMN_THREADS) void k_qmn(const uint32_t* __restrict__ wq1, const uint32_t* __restrict__ sb1,
+                                                    int N1, bf16* __restrict__ y1, const uint32_t* __restrict__ wq2,
+                                                    const uint32_t* __restrict__ sb2, int N2, bf16* __restrict__ y2,
+                                                    int K, int gs, const uint32_t* __restrict__ xmb, int M, int tiles1,
+                                                    int tiles) {
+  constexpr int NB = L * IT, P = 4, G = L / 4 / P, LOGG = ilog2(G), STEPS = G * IT, LOGL = ilog2(L);
+  static_assert(L >= 16 && (1 << LOGL) == L && (1 << LOGG) == G, "four quarters of whole chain groups");
+  __shared__ float part[P][QT][64];
+  // workgroup id -> (XCD id % 8, k = id / 8): every tile of a token block on one XCD, so its L2 holds
+  // the block's activations for all of them
+  const int xcd = (int)blockIdx.x & 7, kk = (int)blockIdx.x >> 3;
+  const int tb = (kk / tiles) * 8 + xcd, tile = kk - (kk / tiles) * tiles;
+  if (tb * MMA_TOK * QT >= M) return;  // whole workgroup, before the barrier
+  const int p = threadIdx.x >> 6, lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
+  const bool second = tile >= tiles1;
+  const uint32_t* wq = second ? wq2 : wq1;
+  const uint32_t* sbp = second ? sb2 : sb1;
+  const int N = second ? N2 : N1;
+  const int row = (second ? tile - tiles1 : tile) * 16 + n, rc = row < N ? row : N - 1;
+  const int rs = gs == 32 ? 0 : gs == 64 ? 1 : 2;
+  const uint32_t* wrow = wq + (size_t)rc * (K / 8);
+  const uint32_t* srow = sbp + (size_t)rc * sb_row_len(K, gs);
+  const int m0 = tb * MMA_TOK * QT;
+  // this lane's A rows (token 4 tq + (lane & 15) / 4, limb lane & 3, word g) and (p, SX) rows (token
+  // 4 tq + g), tokens past M clamped (their sums are not stored)
+  const uint2* xa[QT];
+  const uint2* xs[QT];
+#pragma unroll
+  for (int tq = 0; tq < QT; ++tq) {
+    const int ta = min(m0 + 4 * tq + ((lane & 15) >> 2), M - 1), ts = min(m0 + 4 * tq + g, M - 1);
+    xa[tq] = reinterpret_cast<const uint2*>(xmb + (size_t)ta * NB * MB_DW + (lane & 3) * 8 + 2 * g);
+    xs[tq] = reinterpret_cast<const uint2*>(xmb + (size_t)ts * NB * MB_DW + 32);
+  }
+  auto chain = [](int i) { return (int)(__builtin_bitreverse32((uint32_t)i) >> (32 - LOGL)); };
+  struct Step {
+    uint4 w;
+    uint32_t pr[4];
+    uint2 a[4][QT], ps[4][QT];
+  };
+  auto load = [&](int s, Step& d) {
+    const int q = p * G + s / IT, it = s - (s / IT) * IT;
+    d.w = ldg16(wrow + (size_t)(chain(4 * q + g) + L * it) * 4);
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const int u = chain(4 * q + b), j = u + L * it;
+      d.pr[b] = srow[(u >> rs) * IT + it];
+#pragma unroll
+      for (int tq = 0; tq < QT; ++tq) {
+        d.a[b][tq] = xa[tq][(size_t)j * (MB_DW / 2)];
+        d.ps[b][tq] = xs[tq][(size_t)j * (MB_DW / 2)];
+      }
+    }
+  };
+  float ch[4][QT], stk[LOGG > 0 ? LOGG : 1][QT], res[QT];
+#pragma unroll
+  for (int b = 0; b < 4; ++b)
+#pragma unroll
+    for (int tq = 0; tq < QT; ++tq) ch[b][tq] = 0.0f;
+  auto compute = [&](int s, const Step& d) {
+    const auto p0 = __builtin_amdgcn_permlane32_swap(d.w.x, d.w.z, false, false);
+    const auto p1 = __builtin_amdgcn_permlane32_swap(d.w.y, d.w.w, false, false);
+    const auto q0 = __builtin_amdgcn_permlane16_swap(p0[0], p1[0], false, false);
+    const auto q1 = __builtin_amdgcn_permlane16_swap(p0[1], p1[1], false, false);
+    const uint32_t T[4] = {q0[0], q0[1], q1[0], q1[1]};
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const long bop = (long)(T[b] & 0x0f0f0f0fu) | ((long)((T[b] >> 4) & 0x0f0f0f0fu) << 32);
+      const uint32_t sb = d.pr[b];
+      v4i_t dd[QT];
+#pragma unroll
+      for (int tq = 0; tq < QT; ++tq) {
+        long aop;
+        __builtin_memcpy(&aop, &d.a[b][tq], 8);
+        const v4i_t z = {0, 0, 0, 0};
+        dd[tq] = __builtin_amdgcn_mfma_i32_16x16x32_i8(aop, bop, z, 0, 0, 0);
+      }
+#pragma unroll
+      for (int tq = 0; tq < QT; ++tq) {
+        const int low = dd[tq][0] + 128 * dd[tq][1] + 16384 * dd[tq][2];
+        const float dx = __builtin_fmaf((float)dd[tq][3], 65536.0f, (float)low);
+        float& a = ch[b][tq];
+        a = __builtin_fmaf(__uint_as_float(sb << 16), dx * __uint_as_float(d.ps[b][tq].x), a);
+        a = __builtin_fmaf(__uint_as_float(sb & 0xffff0000u), __uint_as_float(d.ps[b][tq].y), a);
+      }
+    }
+    const int ql = s / IT;
+    if (s - ql * IT == IT - 1) {  // the group's subtree, then the binary counter over this quarter's groups
+#pragma unroll
+      for (int tq = 0; tq < QT; ++tq) {
+        float x = (ch[0][tq] + ch[1][tq]) + (ch[2][tq] + ch[3][tq]);
+        bool open = true;
+#pragma unroll
+        for (int k = 0; k < LOGG; ++k) {
+          if (open) {
+            if ((ql >> k) & 1) {
+              x = stk[k][tq] + x;
+            } else {
+              stk[k][tq] = x;
+              open = false;
+            }
+          }
+        }
+        if (open) res[tq] = x;  // the quarter's last group: its whole subtree
+#pragma unroll
+        for (int b = 0; b < 4; ++b) ch[b][tq] = 0.0f;
+      }
+    }
+  };
+  Step d0, d1;
+  load(0, d0);
+#pragma unroll 1
+  for (int s = 0; s < STEPS; s += 2) {
+    load(s + 1 < STEPS ? s + 1 : s, d1);  // in range either way (unused past the end)
+    compute(s, d0);
+    load(s + 2 < STEPS ? s + 2 : s, d0);
+    if (s + 1 < STEPS) compute(s + 1, d1);
+  }
+#pragma unroll
+  for (int tq = 0; tq < QT; ++tq) part[p][tq][lane] = res[tq];
+  __syncthreads();
+  if (p == 0) {
+#pragma unroll
+    for (int tq = 0; tq < QT; ++tq) {
+      const float v = (part[0][tq][lane] + part[1][tq][lane]) + (part[2][tq][lane] + part[3][tq][lane]);
+      const int t = m0 + 4 * tq + g;
+      if (t < M && row < N) (second ? y2 : y1)[(size_t)t * N + row] = f2bf(v);
     }
   }
 }
@@ -593,12 +931,102 @@ static bool qmv_mma_shape(int K) {
   }
 }
 
+// Batch GEMM: row tiles of 128 in rounds of eight (one per XCD) times token blocks of 4 QT.
+template <int L, int IT, int QT>
+static hipError_t qmm_li(const uint32_t* wq, const uint32_t* sb, int N, int K, int gs, const uint32_t* xp, int M,
+                         bf16* y, float* yf, hipStream_t st) {
+  constexpr size_t lds = (size_t)2 * MMA_TOK * QT * 4 * MB_DW * 4;
+  const int tiles = (N + QMM_ROWS - 1) / QMM_ROWS;
+  const int tblocks = (M + MMA_TOK * QT - 1) / (MMA_TOK * QT);
+  const int grid = (tiles + 7) / 8 * 8 * tblocks;
+  hipLaunchKernelGGL((k_qmm<L, IT, QT>), dim3(grid), dim3(QMM_THREADS), lds, st, wq, sb, N, K, gs, xp, M, y, yf,
+                     tiles, tblocks);
+  return hipGetLastError();
+}
+
+template <int L, int IT>
+static hipError_t qmm_lq(const uint32_t* wq, const uint32_t* sb, int N, int K, int gs, const uint32_t* xp, int M,
+                         bf16* y, float* yf, hipStream_t st) {
+  if (M <= 4 * MMA_TOK) return qmm_li<L, IT, 4>(wq, sb, N, K, gs, xp, M, y, yf, st);
+  return qmm_li<L, IT, 8>(wq, sb, N, K, gs, xp, M, y, yf, st);
+}
+
+// The batch GEMM takes more than MAX_TOKENS tokens of a matrix with packed scale/bias rows whose
+// K blocks tile at least four chains exactly.
+static bool qmm_ok(const uint32_t* sb, int N, int K, int M) {
+  const int nb = K / 32, L = lanes_for_blocks(nb);
+  if (!sb || M <= MAX_TOKENS || N < QMM_MIN_ROWS || nb % L != 0) return false;
+  switch (L * 16 + nb / L) {
+    case 4 * 16 + 4: case 4 * 16 + 5: case 4 * 16 + 6: case 8 * 16 + 4: case 8 * 16 + 5: case 16 * 16 + 4:
+    case 16 * 16 + 5: case 32 * 16 + 4: case 32 * 16 + 6: case 64 * 16 + 4: case 64 * 16 + 5: return true;
+    default: return false;
+  }
+}
+
+static hipError_t qmm(const uint32_t* wq, const uint32_t* sb, int N, int K, int gs, const uint32_t* xp, int M,
+                      bf16* y, float* yf, hipStream_t st) {
+  const int nb = K / 32, L = lanes_for_blocks(nb), IT = nb / L;
+  switch (L * 16 + IT) {
+    case 4 * 16 + 4: return qmm_lq<4, 4>(wq, sb, N, K, gs, xp, M, y, yf, st);
+    case 4 * 16 + 5: return qmm_lq<4, 5>(wq, sb, N, K, gs, xp, M, y, yf, st);
+    case 4 * 16 + 6: return qmm_lq<4, 6>(wq, sb, N, K, gs, xp, M, y, yf, st);
+    case 8 * 16 + 4: return qmm_lq<8, 4>(wq, sb, N, K, gs, xp, M, y, yf, st);
+    case 8 * 16 + 5: return qmm_lq<8, 5>(wq, sb, N, K, gs, xp, M, y, yf, st);
+    case 16 * 16 + 4: return qmm_lq<16, 4>(wq, sb, N, K, gs, xp, M, y, yf, st);
+    case 16 * 16 + 5: return qmm_lq<16, 5>(wq, sb, N, K, gs, xp, M, y, yf, st);
+    case 32 * 16 + 4: return qmm_lq<32, 4>(wq, sb, N, K, gs, xp, M, y, yf, st);
+    case 32 * 16 + 6: return qmm_lq<32, 6>(wq, sb, N, K, gs, xp, M, y, yf, st);
+    case 64 * 16 + 4: return qmm_lq<64, 4>(wq, sb, N, K, gs, xp, M, y, yf, st);
+    case 64 * 16 + 5: return qmm_lq<64, 5>(wq, sb, N, K, gs, xp, M, y, yf, st);
+    default: return hipErrorNotSupported;
+  }
+}
+
+// Two few-row matrices over one batch of prepared activations (the mixer's down and inject
+// projections): k_xmb into xmb [M][K/32][MB_DW], then k_qmn.  hipErrorNotSupported: a shape or
+// matrix it does not take (the caller runs launch_qmv per matrix).
+template <int L, int IT>
+static hipError_t qmn_li(const uint32_t* w1, const uint32_t* sb1, int N1, bf16* y1, const uint32_t* w2,
+                         const uint32_t* sb2, int N2, bf16* y2, int K, int gs, const uint32_t* xmb, int M,
+                         hipStream_t st) {
+  constexpr int QT = 2;
+  const int tiles1 = (N1 + 15) / 16, tiles = tiles1 + (w2 ? (N2 + 15) / 16 : 0);
+  const int tblocks = (M + MMA_TOK * QT - 1) / (MMA_TOK * QT);
+  hipLaunchKernelGGL((k_qmn<L, IT, QT>), dim3(tiles * ((tblocks + 7) / 8 * 8)), dim3(QMN_THREADS), 0, st, w1, sb1, N1, y1, w2, sb2, N2,
+                     y2, K, gs, xmb, M, tiles1, tiles);
+  return hipGetLastError();
+}
+
+bool qmv_pair_ok(const uint32_t* sb1, const uint32_t* w2, const uint32_t* sb2, int K, int M) {
+  const int nb = K / 32, L = lanes_for_blocks(nb), IT = nb % L == 0 ? nb / L : 0;
+  return sb1 && (!w2 || sb2) && M > MAX_TOKENS &&
+         (L * 16 + IT == 64 * 16 + 5 || L * 16 + IT == 64 * 16 + 4 || L * 16 + IT == 32 * 16 + 6);
+}
+
+hipError_t launch_qmv_pair(const uint32_t* w1, const uint32_t* sb1, int N1, bf16* y1, const uint32_t* w2,
+                           const uint32_t* sb2, int N2, bf16* y2, int K, int gs, const uint32_t* xp, uint32_t* xmb,
+                           int M, hipStream_t st) {
+  if (!qmv_pair_ok(sb1, w2, sb2, K, M)) return hipErrorNotSupported;
+  const int nb = K / 32, L = lanes_for_blocks(nb), IT = nb / L;
+  const int units = M * nb * 8;
+  hipLaunchKernelGGL(k_xmb, dim3((units + 255) / 256), dim3(256), 0, st, xp, units, xmb);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  switch (L * 16 + IT) {
+    case 64 * 16 + 5: return qmn_li<64, 5>(w1, sb1, N1, y1, w2, sb2, N2, y2, K, gs, xmb, M, st);
+    case 64 * 16 + 4: return qmn_li<64, 4>(w1, sb1, N1, y1, w2, sb2, N2, y2, K, gs, xmb, M, st);
+    default: return qmn_li<32, 6>(w1, sb1, N1, y1, w2, sb2, N2, y2, K, gs, xmb, M, st);
+  }
+}
+
 // Every token's output is the same whatever the launch shape (exact block sums, the lane rule's
-// float order), so the token count only picks the path: the matrix cores for two or more tokens
+// float order), so the token count only picks the path: the batch GEMM above MAX_TOKENS tokens where
+// the shape allows, the matrix cores for two or more tokens
 // where the shape allows (eight tokens per window when more than four, windows batched in one
 // launch), else the dot-product kernel with as many tokens per window as one workgroup's LDS holds.
 hipError_t launch_qmv(const uint32_t* wq, const bf16* s, const bf16* b, const uint32_t* sb, int N, int K, int gs,
                       const uint32_t* xp, int M, bf16* y, float* yf, hipStream_t st) {
+  if (qmm_ok(sb, N, K, M)) return qmm(wq, sb, N, K, gs, xp, M, y, yf, st);
   if (M >= 2 && qmv_mma_ok(sb, K, 2) && qmv_mma_shape<1>(K)) {  // matrix cores
     if (M > MMA_TOK && M <= MAX_TOKENS && qmv_mma_shape<2>(K)) {  // five to eight tokens: one window of eight
       const hipError_t e = qmv_mma<2>(wq, sb, N, K, gs, xp, M, y, yf, st);

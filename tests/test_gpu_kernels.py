@@ -89,6 +89,47 @@ def test_qmv_bit_exact(ctx, N, K, gs, M):
         assert np.array_equal(host(y), y_o)
 
 
+# more than 8 tokens: the batch GEMM (packed pairs, 1024 rows or more) at every chain depth it takes, ragged
+# rows and token blocks; fewer rows (and checkpoint pairs): the windowed GEMV
+@pytest.mark.parametrize("N,K,gs,M", [
+    (2000, 2560, 64, 37), (1100, 6144, 64, 21), (1100, 10240, 64, 9), (2560, 2560, 32, 64), (1030, 2048, 64, 100),
+    (1030, 512, 64, 33), (1030, 640, 32, 17), (1150, 6144, 32, 40), (330, 10240, 64, 9), (4, 10240, 64, 19),
+])
+def test_qmv_batch_gemm_bit_exact(ctx, N, K, gs, M):
+    _print_case(N=N, K=K, gs=gs, M=M)
+    r = np.random.default_rng(N * 11 + K + M)
+    wq, s, b = qweights(r, N, K, gs)
+    x = rand_bf16(r, (M, K))
+    y_o, yf_o = O.qmv(wq, s, b, gs, x)
+    ds, db = dev(s), dev(b)
+    for sb in (None, ctx.pack_sb(ds, db, K, gs)):
+        y = empty_bf16(M, N)
+        yf = torch.zeros(M, N, dtype=torch.float32, device="cuda")
+        ctx.qmv(dev(wq), ds, db, gs, dev(x), y, yf, sb=sb)
+        ctx.synchronize()
+        assert np.array_equal(host(yf).view(np.uint32), yf_o.view(np.uint32))
+        assert np.array_equal(host(y), y_o)
+
+
+@pytest.mark.parametrize("N,K", [(16480, 2560), (13440, 2560), (2560, 6144), (320, 10240)])
+def test_qmv_batch_gemm_matches_windows(ctx, N, K):
+    """A prefill batch of 256 tokens at the model's shapes: the GEMM's rows equal the windows of 8."""
+    _print_case(N=N, K=K, M=256)
+    r = np.random.default_rng(N + K)
+    wq, s, b = qweights(r, N, K, 64)
+    ds, db, dq = dev(s), dev(b), dev(wq)
+    sb = ctx.pack_sb(ds, db, K, 64)
+    x = dev(rand_bf16(r, (256, K)))
+    y = empty_bf16(256, N)
+    yf = torch.zeros(256, N, dtype=torch.float32, device="cuda")
+    ctx.qmv(dq, ds, db, 64, x, y, yf, sb=sb)
+    yw = torch.zeros(256, N, dtype=torch.float32, device="cuda")
+    for w0 in range(0, 256, 8):
+        ctx.qmv(dq, ds, db, 64, x[w0:w0 + 8], empty_bf16(8, N), yw[w0:w0 + 8], sb=sb)
+    ctx.synchronize()
+    assert torch.equal(yf.view(torch.int32), yw.view(torch.int32))
+
+
 def test_qmv_repeat_is_bit_stable(ctx):
     r = np.random.default_rng(5)
     wq, s, b = qweights(r, 512, 2560, 64)
@@ -109,7 +150,7 @@ def test_qmv_rejects_bad_shapes(ctx):
     with pytest.raises(mtpx.MtpxError):
         ctx.qmv(dev(wq), dev(s), dev(b), 48, dev(rand_bf16(r, (1, 256))), empty_bf16(1, 8))
     with pytest.raises(mtpx.MtpxError):
-        ctx.qmv(dev(wq), dev(s), dev(b), 32, dev(rand_bf16(r, (9, 256))), empty_bf16(9, 8))
+        ctx.qmv(dev(wq), dev(s), dev(b), 32, dev(rand_bf16(r, (4097, 256))), empty_bf16(4097, 8))
 
 
 # ---------------------------------------------------------------------------- rmsnorm / add

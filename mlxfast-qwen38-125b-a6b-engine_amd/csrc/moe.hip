@@ -821,28 +821,50 @@ hipError_t launch_moe_combine(const MoeArgs& a, hipStream_t st) {
 constexpr int SORT_THREADS = 1024;
 
 __global__ __launch_bounds__(SORT_THREADS) void k_moe_sort(MoeArgs a) {
-  __shared__ int cnt[1024], base[1024];
+  __shared__ int cnt[1024], base[1024], cbase[1024];
   const int E = a.E, K = a.K, M = a.M, T = a.nwin * M, wslots = M * (K + 1);
   for (int e = threadIdx.x; e < E; e += SORT_THREADS) cnt[e] = 0;
   __syncthreads();
   for (int i = threadIdx.x; i < T * K; i += SORT_THREADS) atomicAdd(&cnt[min(max(a.idx[i], 0), E - 1)], 1);
   __syncthreads();
-  if (threadIdx.x < 64) {  // exclusive scan of the counts by one wave, 64 experts per step
+  const int sh_chunks = (T + MQ_CHUNK - 1) / MQ_CHUNK;
+  if (threadIdx.x < 64) {  // exclusive scans of the counts and chunk counts by one wave, 64 experts per step
     int run = T;  // the shared expert's T slots come first
+    int crun = sh_chunks;  // and its chunks
     for (int e0 = 0; e0 < E; e0 += 64) {
       const int e = e0 + (int)threadIdx.x;
-      const int c = e < E ? cnt[e] : 0;
-      int incl = c;
+      const int c = e < E ? cnt[e] : 0, cc = (c + MQ_CHUNK - 1) / MQ_CHUNK;
+      int incl = c, cincl = cc;
 #pragma unroll
       for (int off = 1; off < 64; off <<= 1) {
-        const int y = __shfl_up(incl, off, 64);
-        if ((int)threadIdx.x >= off) incl += y;
+        const int y = __shfl_up(incl, off, 64), cy = __shfl_up(cincl, off, 64);
+        if ((int)threadIdx.x >= off) {
+          incl += y;
+          cincl += cy;
+        }
       }
-      if (e < E) base[e] = run + incl - c;
+      if (e < E) {
+        base[e] = run + incl - c;
+        cbase[e] = crun + cincl - cc;
+      }
       run += __shfl(incl, 63, 64);
+      crun += __shfl(cincl, 63, 64);
     }
+    if (threadIdx.x == 0 && a.chunk_n) *a.chunk_n = crun;
   }
   __syncthreads();
+  if (a.chunks) {  // chunks of at most MQ_CHUNK slots of one expert: (order position, count | (expert + 1) << 16)
+    for (int c = threadIdx.x; c < sh_chunks; c += SORT_THREADS) {
+      a.chunks[2 * c] = c * MQ_CHUNK;
+      a.chunks[2 * c + 1] = min(MQ_CHUNK, T - c * MQ_CHUNK);
+    }
+    for (int e = threadIdx.x; e < E; e += SORT_THREADS)
+      for (int k = 0; k * MQ_CHUNK < cnt[e]; ++k) {
+        a.chunks[2 * (cbase[e] + k)] = base[e] + k * MQ_CHUNK;
+        a.chunks[2 * (cbase[e] + k) + 1] = min(MQ_CHUNK, cnt[e] - k * MQ_CHUNK) | ((e + 1) << 16);
+      }
+    __syncthreads();  // base[] is the scatter's cursor below
+  }
   for (int t = threadIdx.x; t < T; t += SORT_THREADS)  // shared slots: window t / M, slot M*K + t % M
     a.gorder[t] = (t / M) * wslots + M * K + t % M;
   for (int i = threadIdx.x; i < T * K; i += SORT_THREADS) {

@@ -209,7 +209,10 @@ size_t moe_ws_bytes(const mtpx_moe_weights* w, int M, int nwin = 1) {
   const int H = w->hidden, E = w->experts, K = w->top_k, F = w->expert_width;
   const size_t T = (size_t)M * nwin, slots = T * (K + 1);
   return al(4 * T * E) + al(4 * T) + al(4 * T * K) * 2 + al(sizeof(MoeDispatch) * (size_t)nwin) +
-         al(4 * T * (H / 32) * XP_DW) + al(2 * slots * F) + al(2 * slots * H) + (nwin > 1 ? al(4 * slots) : 0) +
+         al(4 * T * (H / 32) * XP_DW) + al(2 * slots * F) + al(2 * slots * H) +
+         (nwin > 1 ? al(4 * slots) + al(8 * (size_t)moe_max_chunks((int)T, E, K)) + al(4) +
+                         al(4 * slots * (F / 32) * XP_DW)
+                   : 0) +
          4096;
 }
 
@@ -267,7 +270,18 @@ int moe_enqueue(Ctx* c, const mtpx_moe_weights* w, const uint16_t* x, int M, uin
   if (moe_dd_supported(a.H, a.F, a.K)) {  // one workgroup per (slot, row block), slots in dispatch order
     if (nwin > 1) {  // a batch of windows: one order of all their slots, grouped by expert
       a.gorder = ws_take<int32_t>(c, slots);
+      a.chunks = ws_take<int32_t>(c, 2 * (size_t)moe_max_chunks((int)T, a.E, a.K));
+      a.chunk_n = ws_take<int32_t>(c, 1);
+      a.max_chunks = moe_max_chunks((int)T, a.E, a.K);
+      a.xp_act = ws_take<uint32_t>(c, slots * (a.F / 32) * XP_DW);
       LAUNCH(c, "moe_sort", launch_moe_sort(a, c->stream));
+      if (moe_qmm_supported(a)) {  // down over the experts' chunks on the matrix cores
+        LAUNCH(c, "moe_gate_up", launch_moe_gate_up_dd(a, c->stream));
+        LAUNCH(c, "moe_act_prep", launch_xprep(reinterpret_cast<const bf16*>(a.act), (int)slots, a.F, a.xp_act, c->stream));
+        LAUNCH(c, "moe_down", launch_moe_qmm_down(a, c->stream));
+        LAUNCH(c, "moe_combine", launch_moe_combine(a, c->stream));
+        return MTPX_OK;
+      }
     }
     LAUNCH(c, "moe_gate_up", launch_moe_gate_up_dd(a, c->stream));
     LAUNCH(c, "moe_down", launch_moe_down_dd(a, c->stream));

@@ -139,7 +139,21 @@ struct MoeArgs {
   // w * M * (K + 1) + slot | (expert + 1) << 16), walked by the expert kernels in one 1-D grid, so
   // an expert's weight rows are fetched once for the whole batch; null: each window's own table
   int32_t* gorder = nullptr;
+  // with gorder: the order cut into chunks of at most MQ_CHUNK slots of one expert (k_moe_sort):
+  // chunks[c] = (gorder position, count | (expert + 1) << 16, 0 the shared expert), *chunk_n of
+  // them, at most max_chunks; xp_act [slots][F/32][XP_DW]: the gate|up rows prepared for down
+  int32_t* chunks = nullptr;
+  int32_t* chunk_n = nullptr;
+  int max_chunks = 0;
+  uint32_t* xp_act = nullptr;
 };
+constexpr int MQ_CHUNK = 8;
+inline int moe_max_chunks(int T, int E, int K) {
+  return (T + MQ_CHUNK - 1) / MQ_CHUNK + E + (T * K + MQ_CHUNK - 1) / MQ_CHUNK;
+}
+bool moe_qmm_supported(const MoeArgs& a);
+hipError_t launch_moe_qmm_gate_up(const MoeArgs& a, hipStream_t st);
+hipError_t launch_moe_qmm_down(const MoeArgs& a, hipStream_t st);
 
 constexpr int MOE_TICKETS = 64;
 hipError_t launch_moe_router_route(const MoeArgs& a, hipStream_t st);

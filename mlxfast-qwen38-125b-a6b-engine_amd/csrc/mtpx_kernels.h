@@ -152,7 +152,6 @@ inline int moe_max_chunks(int T, int E, int K) {
   return (T + MQ_CHUNK - 1) / MQ_CHUNK + E + (T * K + MQ_CHUNK - 1) / MQ_CHUNK;
 }
 bool moe_qmm_supported(const MoeArgs& a);
-hipError_t launch_moe_qmm_gate_up(const MoeArgs& a, hipStream_t st);
 hipError_t launch_moe_qmm_down(const MoeArgs& a, hipStream_t st);
 
 constexpr int MOE_TICKETS = 64;

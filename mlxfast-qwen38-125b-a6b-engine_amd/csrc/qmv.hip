@@ -517,95 +517,102 @@ __global__ __launch_bounds__(QMM_THREADS) void k_qmm(const uint32_t* __restrict_
 }
 
 // ---------------------------------------------------------------------------
-// The MoE expert kernels of a prefill batch on the matrix cores (same bits as the slot-per-
-// workgroup kernels): the batch's slots sorted by expert are cut into chunks of at most MQ_CHUNK
-// slots of one expert (k_moe_sort), and a workgroup owns one chunk and a row tile of the expert's
-// matrix: gate|up (GU: waves 0-7 take 128 gate rows, waves 8-15 the matching up rows, against the
-// chunk's tokens' prepared x; the up waves hand their sums over in LDS and the gate waves write
-// the SwiGLU activation rows) or down (128 rows of H against the slots' prepared activations, into
-// the slots' output rows).  The chunk's tokens' K blocks are staged in LDS once (four-limb
-// layout), so the walk has no barrier.  The K walk is k_qmm's: chains in the butterfly's
-// bit-reversed leaf order, groups of four folded by a binary counter, each weight operand serving
-// every token group of the chunk that holds a slot.  The weight rows stream D steps ahead (a ring
-// of D register buffers: the expert rows are read once per chunk, so the walk waits on HBM unless
-// many loads are in flight).
-template <int L, int IT, bool GU, int D>
-__global__ __launch_bounds__(GU ? 2 * QMM_THREADS : QMM_THREADS) void k_moe_qmm(MoeArgs a, int tiles) {
+// The MoE down projection of a prefill batch on the matrix cores (same bits as the slot-per-
+// workgroup kernel): the batch's slots sorted by expert are cut into chunks of at most MQ_CHUNK
+// slots of one expert (k_moe_sort), and a workgroup owns one chunk and 128 rows of H of the expert's
+// down matrix, against the slots' prepared activation rows, into the slots' output rows.  The K
+// walk is k_qmm's: chains in the butterfly's bit-reversed leaf order, groups of four folded by a
+// binary counter, each weight operand serving every token group of the chunk that holds a slot.  A phase is one group of four chains: all IT blocks of each for
+// the chunk's tokens are staged in LDS (double buffered, the next phase's activation words loaded
+// during this one), and the weight rows stream one phase ahead (a ring of IT register buffers: an
+// expert's rows are read once per chunk, so the walk waits on HBM unless many loads are in flight).
+template <int L, int IT>
+__global__ __launch_bounds__(QMM_THREADS) void k_moe_qmm(MoeArgs a, int tiles) {
   constexpr int QT = MQ_CHUNK / MMA_TOK, QTOK = MQ_CHUNK, NB = L * IT;
-  constexpr int LOGL = ilog2(L), LOGQ = LOGL - 2, STEPS = (L / 4) * IT;
-  constexpr int TR = 128;                                 // rows of the tile
-  constexpr int NT = GU ? 2 * QMM_THREADS : QMM_THREADS;  // gate|up: 8 gate and 8 up waves
-  constexpr int NU = (QTOK * NB * 8 + NT - 1) / NT;        // staging units per thread
-  static_assert(L >= 4 && (1 << LOGL) == L && STEPS % D == 0, "whole rings of steps");
-  extern __shared__ uint32_t lds[];  // the chunk's tokens' K blocks [QTOK][NB][MB_DW], staged once
+  constexpr int LOGL = ilog2(L), LOGQ = LOGL - 2, NPH = L / 4, NBP = 4 * IT;
+  constexpr int TR = 128;                                  // rows of the tile
+  constexpr int PDW = QTOK * NBP * MB_DW;                   // one phase's staging buffer
+  constexpr int NU = (QTOK * NBP * 8 + QMM_THREADS - 1) / QMM_THREADS;  // staging units per thread
+  static_assert(L >= 4 && (1 << LOGL) == L, "groups of four chains");
+  extern __shared__ uint32_t lds[];  // [NPH > 1 ? 2 : 1][QTOK][NBP][MB_DW]
   __shared__ int slot_l[QTOK];
-  __shared__ float upart[GU ? 8 : 1][QT][64];
   const int ck = (int)blockIdx.x / tiles, tile = (int)blockIdx.x - ck * tiles;
   if (ck >= *a.chunk_n) return;  // whole workgroup, before any barrier
   const int2 cv = reinterpret_cast<const int2*>(a.chunks)[ck];
   const int cnt = min(cv.y & 0xffff, QTOK), ev = cv.y >> 16;  // ev: expert + 1, 0 the shared expert
   const bool shared = ev == 0;
   const int e = shared ? 0 : min(ev - 1, a.E - 1);
-  const int H = a.H, F = a.F, M = a.M, Kk = a.K, gs = a.gs;
-  const int wslots = M * (Kk + 1), slots = a.nwin * wslots;
-  const int K = GU ? H : F, N = GU ? F : H;
+  const int H = a.H, F = a.F, gs = a.gs;
+  const int slots = a.nwin * a.M * (a.K + 1);
+  const int K = F, N = H;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int n = lane & 15, g = lane >> 4;
-  const bool up = GU && wave >= 8;
-  const int row = tile * TR + (wave & 7) * 16 + n, rc = row < N ? row : N - 1;
+  const int row = tile * TR + wave * 16 + n, rc = row < N ? row : N - 1;
   const int rs = gs == 32 ? 0 : gs == 64 ? 1 : 2;
   const int P = sb_row_len(K, gs);
   const size_t rbase = shared ? 0 : (size_t)e * N;
-  const uint32_t* wm = GU ? (up ? (shared ? a.sh_up_w : a.up_w) : (shared ? a.sh_gate_w : a.gate_w))
-                          : (shared ? a.sh_down_w : a.down_w);
-  const uint32_t* sm = GU ? (up ? (shared ? a.sh_up_sb : a.up_sb) : (shared ? a.sh_gate_sb : a.gate_sb))
-                          : (shared ? a.sh_down_sb : a.down_sb);
+  const uint32_t* wm = shared ? a.sh_down_w : a.down_w;
+  const uint32_t* sm = shared ? a.sh_down_sb : a.down_sb;
   const uint32_t* wrow = wm + (rbase + rc) * (size_t)(K / 8);
   const uint32_t* srow = sm + (rbase + rc) * (size_t)P;
   auto chain = [](int i) { return (int)(__builtin_bitreverse32((uint32_t)i) >> (32 - LOGL)); };
-  uint4 wr[D];
-  uint32_t pr[D][4];
-  auto load_w = [&](int s, uint4& w, uint32_t (&p)[4]) {  // any s: the blocks stay inside the matrix
-    const int q = s / IT, it = s - q * IT;
+  uint4 wr[IT];
+  uint32_t pr[IT][4];
+  auto load_w = [&](int q, int it, uint4& w, uint32_t (&p)[4]) {  // any q: the blocks stay inside the matrix
     w = ldg16(wrow + (size_t)(chain(4 * q + g) + L * it) * 4);
 #pragma unroll
     for (int b = 0; b < 4; ++b) p[b] = srow[(chain(4 * q + b) >> rs) * IT + it];
   };
 #pragma unroll
-  for (int u = 0; u < D; ++u) load_w(u, wr[u], pr[u]);  // the weights first: they come from HBM
-  // the chunk's slots, then every K block of their rows into LDS (four-limb layout), once
-  int myslot = -1;
-  if (threadIdx.x < QTOK && (int)threadIdx.x < cnt)
-    myslot = min(a.gorder[min(cv.x + (int)threadIdx.x, slots - 1)] & 0xffff, slots - 1);
-  if (threadIdx.x < QTOK) slot_l[threadIdx.x] = myslot;
+  for (int it = 0; it < IT; ++it) load_w(0, it, wr[it], pr[it]);  // the weights first: they come from HBM
+  if (threadIdx.x < QTOK)
+    slot_l[threadIdx.x] = (int)threadIdx.x < cnt ? min(a.gorder[min(cv.x + (int)threadIdx.x, slots - 1)] & 0xffff, slots - 1)
+                                                 : -1;
   __syncthreads();
-#pragma unroll 2
+  // staging units (token t, phase block pb = b * IT + it, word/half ge) of this thread, their rows
+  const uint32_t* urow[NU];
+  int uoff[NU];
+#pragma unroll
   for (int k = 0; k < NU; ++k) {
-    const int u = threadIdx.x + k * NT;
-    const int t = u / (NB * 8), rem = u - t * (NB * 8), j = rem >> 3, ge = rem & 7;
-    const int sl = t < QTOK ? slot_l[t] : -1;
-    const bool in = sl >= 0;
-    const uint32_t* xrow;
-    if constexpr (GU) {  // the slot's token: window sl / wslots, routed (token, rank) or shared
-      const int s0 = in ? sl : 0, win = s0 / wslots, ls = s0 - win * wslots;
-      const int m = win * M + (ls >= M * Kk ? ls - M * Kk : ls / Kk);
-      xrow = a.xp_x + (size_t)m * NB * XP_DW;
-    } else {
-      xrow = a.xp_act + (size_t)(in ? sl : 0) * NB * XP_DW;
-    }
-    const uint32_t* src = xrow + (size_t)j * XP_DW;
-    const uint32_t* sw = src + ((ge & 1) ? 4 : 0) + (ge >> 1);
-    const uint32_t v0 = in ? sw[0] : 0u, v1 = in ? sw[8] : 0u, v2 = in ? sw[16] : 0u, v3 = in ? src[24 + (ge & 1)] : 0u;
-    if (t < QTOK) {
-      uint32_t* blk = lds + ((size_t)t * NB + j) * MB_DW;
-      uint32_t* dst = blk + 2 * (ge >> 1) + (ge & 1);
-      dst[0] = v0 & 0x7f7f7f7fu;
-      dst[8] = ((v0 >> 7) & 0x01010101u) | ((v1 << 1) & 0x7e7e7e7eu);
-      dst[16] = (v1 >> 6) & 0x03030303u;
-      dst[24] = v2;
-      blk[(ge < 2 ? 32 : 34) + (ge & 1)] = v3;
-    }
+    const int u = threadIdx.x + k * QMM_THREADS;
+    const int t = u / (NBP * 8), sl = t < QTOK ? slot_l[t] : -1;
+    uoff[k] = sl >= 0 ? u - t * (NBP * 8) : -1;  // -1: a zero unit (no slot) or past the stage
+    urow[k] = a.xp_act + (size_t)(sl >= 0 ? sl : 0) * NB * XP_DW;
   }
+  uint32_t aw[NU][4];
+  auto load_act = [&](int q) {
+#pragma unroll
+    for (int k = 0; k < NU; ++k) {
+      const int o = uoff[k] < 0 ? 0 : uoff[k], pb = o >> 3, ge = o & 7, bb = pb / IT, it = pb - bb * IT;
+      const uint32_t* src = urow[k] + (size_t)(chain(4 * q + bb) + L * it) * XP_DW;
+      const uint32_t* sw = src + ((ge & 1) ? 4 : 0) + (ge >> 1);
+      const uint32_t v0 = sw[0], v1 = sw[8], v2 = sw[16], v3 = src[24 + (ge & 1)];
+      const bool in = uoff[k] >= 0;
+      aw[k][0] = in ? v0 : 0u;
+      aw[k][1] = in ? v1 : 0u;
+      aw[k][2] = in ? v2 : 0u;
+      aw[k][3] = in ? v3 : 0u;
+    }
+  };
+  auto store_act = [&](uint32_t* st) {
+#pragma unroll
+    for (int k = 0; k < NU; ++k) {
+      const int u = threadIdx.x + k * QMM_THREADS;
+      if (u < QTOK * NBP * 8) {
+        const int t = u / (NBP * 8), o = u - t * (NBP * 8), pb = o >> 3, ge = o & 7;
+        uint32_t* blk = st + (t * NBP + pb) * MB_DW;
+        uint32_t* dst = blk + 2 * (ge >> 1) + (ge & 1);
+        dst[0] = aw[k][0] & 0x7f7f7f7fu;
+        dst[8] = ((aw[k][0] >> 7) & 0x01010101u) | ((aw[k][1] << 1) & 0x7e7e7e7eu);
+        dst[16] = (aw[k][1] >> 6) & 0x03030303u;
+        dst[24] = aw[k][2];
+        blk[(ge < 2 ? 32 : 34) + (ge & 1)] = aw[k][3];
+      }
+    }
+  };
+  load_act(0);
+  store_act(lds);
+  if (NPH > 1) load_act(1);
   __syncthreads();
   const int qte = (cnt + MMA_TOK - 1) / MMA_TOK;  // token groups holding a slot (uniform)
   float ch[4][QT], stk[LOGQ > 0 ? LOGQ : 1][QT], res[QT];
@@ -614,33 +621,33 @@ __global__ __launch_bounds__(GU ? 2 * QMM_THREADS : QMM_THREADS) void k_moe_qmm(
 #pragma unroll
     for (int tq = 0; tq < QT; ++tq) ch[b][tq] = 0.0f;
   // A operand of lane: token 4 tq + (lane & 15) / 4, limb lane & 3, word g; (p, SX) of token 4 tq + g
-  const uint2* xa = reinterpret_cast<const uint2*>(lds + (size_t)((lane & 15) >> 2) * NB * MB_DW + (lane & 3) * 8 + 2 * g);
-  const uint2* xs = reinterpret_cast<const uint2*>(lds + (size_t)g * NB * MB_DW + 32);
-  constexpr int TGS = MMA_TOK * NB * MB_DW / 2;  // one token group, in uint2
+  const int aoff2 = ((((lane & 15) >> 2) * NBP) * MB_DW + (lane & 3) * 8 + 2 * g) / 2;
+  const int poff2 = ((g * NBP) * MB_DW + 32) / 2;
+  constexpr int TGS = MMA_TOK * NBP * MB_DW / 2;  // one token group, in uint2
 #pragma unroll 1
-  for (int s0 = 0; s0 < STEPS; s0 += D) {
+  for (int q = 0; q < NPH; ++q) {
+    const uint2* st2 = reinterpret_cast<const uint2*>(lds + (NPH > 1 ? (q & 1) * PDW : 0));
 #pragma unroll
-    for (int u = 0; u < D; ++u) {
-      const int s = s0 + u, q = s / IT, it = s - q * IT;
-      const auto p0 = __builtin_amdgcn_permlane32_swap(wr[u].x, wr[u].z, false, false);
-      const auto p1 = __builtin_amdgcn_permlane32_swap(wr[u].y, wr[u].w, false, false);
+    for (int it = 0; it < IT; ++it) {
+      const auto p0 = __builtin_amdgcn_permlane32_swap(wr[it].x, wr[it].z, false, false);
+      const auto p1 = __builtin_amdgcn_permlane32_swap(wr[it].y, wr[it].w, false, false);
       const auto q0 = __builtin_amdgcn_permlane16_swap(p0[0], p1[0], false, false);
       const auto q1 = __builtin_amdgcn_permlane16_swap(p0[1], p1[1], false, false);
       const uint32_t T[4] = {q0[0], q0[1], q1[0], q1[1]};
       uint32_t sbv[4];
 #pragma unroll
-      for (int b = 0; b < 4; ++b) sbv[b] = pr[u][b];
-      load_w(s + D, wr[u], pr[u]);  // the ring slot's next step, D steps ahead
+      for (int b = 0; b < 4; ++b) sbv[b] = pr[it][b];
+      load_w(q + 1, it, wr[it], pr[it]);  // the ring slot's block of the next phase
 #pragma unroll
       for (int b = 0; b < 4; ++b) {
-        const int j = chain(4 * q + b) + L * it;
+        const int pb = b * IT + it;
         const long bop = (long)(T[b] & 0x0f0f0f0fu) | ((long)((T[b] >> 4) & 0x0f0f0f0fu) << 32);
         const uint32_t sb = sbv[b];
         v4i_t d[QT];
 #pragma unroll
         for (int tq = 0; tq < QT; ++tq) {
           if (tq < qte) {
-            const long aop = *reinterpret_cast<const long*>(xa + tq * TGS + j * (MB_DW / 2));
+            const long aop = *reinterpret_cast<const long*>(st2 + aoff2 + tq * TGS + pb * (MB_DW / 2));
             const v4i_t z = {0, 0, 0, 0};
             d[tq] = __builtin_amdgcn_mfma_i32_16x16x32_i8(aop, bop, z, 0, 0, 0);
           }
@@ -650,7 +657,7 @@ __global__ __launch_bounds__(GU ? 2 * QMM_THREADS : QMM_THREADS) void k_moe_qmm(
           if (tq < qte) {
             const int low = d[tq][0] + 128 * d[tq][1] + 16384 * d[tq][2];
             const float dx = __builtin_fmaf((float)d[tq][3], 65536.0f, (float)low);
-            const uint2 ps = xs[tq * TGS + j * (MB_DW / 2)];
+            const uint2 ps = st2[poff2 + tq * TGS + pb * (MB_DW / 2)];
             float& acc = ch[b][tq];
             acc = __builtin_fmaf(__uint_as_float(sb << 16), dx * __uint_as_float(ps.x), acc);
             acc = __builtin_fmaf(__uint_as_float(sb & 0xffff0000u), __uint_as_float(ps.y), acc);
@@ -658,49 +665,38 @@ __global__ __launch_bounds__(GU ? 2 * QMM_THREADS : QMM_THREADS) void k_moe_qmm(
         }
         __builtin_amdgcn_sched_barrier(0);
       }
-      if (it == IT - 1) {
-#pragma unroll
-        for (int tq = 0; tq < QT; ++tq) {
-          float x = (ch[0][tq] + ch[1][tq]) + (ch[2][tq] + ch[3][tq]);
-          bool open = true;
-#pragma unroll
-          for (int k = 0; k < LOGQ; ++k) {
-            if (open) {
-              if ((q >> k) & 1) {
-                x = stk[k][tq] + x;
-              } else {
-                stk[k][tq] = x;
-                open = false;
-              }
-            }
-          }
-          if (open) res[tq] = x;
-#pragma unroll
-          for (int b = 0; b < 4; ++b) ch[b][tq] = 0.0f;
-        }
-      }
     }
-  }
-  if constexpr (GU) {  // up sums -> LDS, gate waves finish the SwiGLU
-    if (up)
-#pragma unroll
-      for (int tq = 0; tq < QT; ++tq) upart[wave & 7][tq][lane] = res[tq];
-    __syncthreads();
-    if (!up)
-#pragma unroll
-      for (int tq = 0; tq < QT; ++tq) {
-        const int t = tq * MMA_TOK + g;
-        const int sl = slot_l[t];
-        if (sl >= 0 && row < N)
-          a.act[(size_t)sl * F + row] = f2bf(silu_bf16(round_bf(res[tq])) * round_bf(upart[wave & 7][tq][lane]));
-      }
-  } else {
+    // the group's subtree ((a + b) + (c + d)), then the binary counter over the groups
 #pragma unroll
     for (int tq = 0; tq < QT; ++tq) {
-      const int t = tq * MMA_TOK + g;
-      const int sl = slot_l[t];
-      if (sl >= 0 && row < N) a.r[(size_t)sl * H + row] = f2bf(res[tq]);
+      float x = (ch[0][tq] + ch[1][tq]) + (ch[2][tq] + ch[3][tq]);
+      bool open = true;
+#pragma unroll
+      for (int k = 0; k < LOGQ; ++k) {
+        if (open) {
+          if ((q >> k) & 1) {
+            x = stk[k][tq] + x;
+          } else {
+            stk[k][tq] = x;
+            open = false;
+          }
+        }
+      }
+      if (open) res[tq] = x;
+#pragma unroll
+      for (int b = 0; b < 4; ++b) ch[b][tq] = 0.0f;
     }
+    if (NPH > 1 && q + 1 < NPH) {  // the next phase's words -> the other buffer, then the one after into registers
+      store_act(lds + ((q + 1) & 1) * PDW);
+      load_act(q + 2 < NPH ? q + 2 : q + 1);
+      __syncthreads();
+    }
+  }
+#pragma unroll
+  for (int tq = 0; tq < QT; ++tq) {
+    const int t = tq * MMA_TOK + g;
+    const int sl = slot_l[t];
+    if (sl >= 0 && row < N) a.r[(size_t)sl * H + row] = f2bf(res[tq]);
   }
 }
 
@@ -1170,40 +1166,29 @@ static hipError_t qmm(const uint32_t* wq, const uint32_t* sb, int N, int K, int 
   }
 }
 
-// The MoE expert GEMMs over the chunk table: grid = max chunks x 128-row tiles (chunks past
-// *a.chunk_n exit at once); down's activations are the gate|up output rows prepared into a.xp_act.
-template <int L, int IT, bool GU>
+// The MoE down GEMM over the chunk table: grid = max chunks x 128-row tiles of H (chunks past
+// *a.chunk_n exit at once), activations = the gate|up output rows prepared into a.xp_act.
+template <int L, int IT>
 static hipError_t moe_qmm_li(const MoeArgs& a, hipStream_t st) {
-  constexpr size_t lds = (size_t)MQ_CHUNK * L * IT * MB_DW * 4;
+  constexpr size_t lds = (size_t)(L > 4 ? 2 : 1) * MQ_CHUNK * 4 * IT * MB_DW * 4;
   static size_t cur = 0;
-  constexpr int STEPS0 = (L / 4) * IT, D0 = STEPS0 <= 5 ? STEPS0 : 4;
-  const hipError_t le = ensure_lds(k_moe_qmm<L, IT, GU, D0>, lds, cur);
+  const hipError_t le = ensure_lds(k_moe_qmm<L, IT>, lds, cur);
   if (le != hipSuccess) return le;
-  constexpr int STEPS = (L / 4) * IT, D = STEPS <= 5 ? STEPS : 4;  // weight steps in flight
-  const int N = GU ? a.F : a.H, tiles = (N + 127) / 128;
-  hipLaunchKernelGGL((k_moe_qmm<L, IT, GU, D>), dim3(a.max_chunks * tiles), dim3(GU ? 2 * QMM_THREADS : QMM_THREADS), lds,
-                     st, a, tiles);
+  const int tiles = (a.H + 127) / 128;
+  hipLaunchKernelGGL((k_moe_qmm<L, IT>), dim3(a.max_chunks * tiles), dim3(QMM_THREADS), lds, st, a, tiles);
   return hipGetLastError();
 }
 
-static bool moe_qmm_shape(int K) {
+static bool moe_qmm_shape(int K) {  // the model's expert width (F = 640: four chains of five blocks)
   const int nb = K / 32, L = lanes_for_blocks(nb);
-  return nb % L == 0 && (L * 16 + nb / L == 16 * 16 + 5 || L * 16 + nb / L == 4 * 16 + 5);
+  return nb % L == 0 && L * 16 + nb / L == 4 * 16 + 5;
 }
 
-bool moe_qmm_supported(const MoeArgs& a) {
-  return a.gate_sb && a.up_sb && a.down_sb && a.sh_gate_sb && a.sh_up_sb && a.sh_down_sb && moe_qmm_shape(a.H) &&
-         moe_qmm_shape(a.F);
-}
-
-hipError_t launch_moe_qmm_gate_up(const MoeArgs& a, hipStream_t st) {
-  if (!moe_qmm_supported(a) || !a.chunks || !a.chunk_n) return hipErrorInvalidValue;
-  return lanes_for_blocks(a.H / 32) == 16 ? moe_qmm_li<16, 5, true>(a, st) : moe_qmm_li<4, 5, true>(a, st);
-}
+bool moe_qmm_supported(const MoeArgs& a) { return a.down_sb && a.sh_down_sb && moe_qmm_shape(a.F); }
 
 hipError_t launch_moe_qmm_down(const MoeArgs& a, hipStream_t st) {
   if (!moe_qmm_supported(a) || !a.chunks || !a.chunk_n || !a.xp_act) return hipErrorInvalidValue;
-  return lanes_for_blocks(a.F / 32) == 16 ? moe_qmm_li<16, 5, false>(a, st) : moe_qmm_li<4, 5, false>(a, st);
+  return moe_qmm_li<4, 5>(a, st);
 }
 
 // Two few-row matrices over one batch of prepared activations (the mixer's down and inject

@@ -224,12 +224,14 @@ __global__ __launch_bounds__(GDN_THREADS) void k_gdn_step(GdnArgs a) {
       *reinterpret_cast<float4*>(a.ssm + ((size_t)h * GDN_D + r0 + hw + 16 * i) * GDN_D + 4 * l) =
           make_float4(s[i][0], s[i][1], s[i][2], s[i][3]);
   }
+  // position by position, this thread's RPH state rows side by side (independent chains)
+  for (int t = 0; t < S; ++t) {
+    const float gd = dec[t], bt = bet[t];
+    const float k0 = ks[t][4 * l], k1 = ks[t][4 * l + 1], k2 = ks[t][4 * l + 2], k3 = ks[t][4 * l + 3];
+    const float q0 = qs[t][4 * l], q1 = qs[t][4 * l + 1], q2 = qs[t][4 * l + 2], q3 = qs[t][4 * l + 3];
 #pragma unroll
-  for (int i = 0; i < RPH; ++i) {
-    const int r = r0 + hw + 16 * i;
-    for (int t = 0; t < S; ++t) {
-      const float gd = dec[t];
-      const float k0 = ks[t][4 * l], k1 = ks[t][4 * l + 1], k2 = ks[t][4 * l + 2], k3 = ks[t][4 * l + 3];
+    for (int i = 0; i < RPH; ++i) {
+      const int r = r0 + hw + 16 * i;
       s[i][0] = s[i][0] * gd;
       float kv = 0.0f + s[i][0] * k0;
       float comp = 0.0f;
@@ -251,17 +253,17 @@ __global__ __launch_bounds__(GDN_THREADS) void k_gdn_step(GdnArgs a) {
         kv = next;
       }
       const float kvm = half_wave_sum(kv);
-      const float delta = (vs[t][r] - kvm) * bet[t];
+      const float delta = (vs[t][r] - kvm) * bt;
       if (l == 0) a.delta_nxt[((size_t)t * a.hv + h) * GDN_D + r] = delta;
       float o = 0.0f;
       s[i][0] = __builtin_fmaf(k0, delta, s[i][0]);
-      o = __builtin_fmaf(s[i][0], qs[t][4 * l], o);
+      o = __builtin_fmaf(s[i][0], q0, o);
       s[i][1] = __builtin_fmaf(k1, delta, s[i][1]);
-      o = __builtin_fmaf(s[i][1], qs[t][4 * l + 1], o);
+      o = __builtin_fmaf(s[i][1], q1, o);
       s[i][2] = __builtin_fmaf(k2, delta, s[i][2]);
-      o = __builtin_fmaf(s[i][2], qs[t][4 * l + 2], o);
+      o = __builtin_fmaf(s[i][2], q2, o);
       s[i][3] = __builtin_fmaf(k3, delta, s[i][3]);
-      o = __builtin_fmaf(s[i][3], qs[t][4 * l + 3], o);
+      o = __builtin_fmaf(s[i][3], q3, o);
       const float y = half_wave_sum(o);
       if (l == 0) st_pub(a.ypub + ((size_t)t * a.hv + h) * GDN_D + r, round_bf(y));
     }
@@ -444,13 +446,17 @@ __global__ __launch_bounds__(GDN_THREADS) void k_gdn_batch(GdnArgs a, GdnBatch b
     const int n = S - t0 < MAX_TOKENS ? S - t0 : MAX_TOKENS;
     const bool more = t0 + MAX_TOKENS < S;
     if (more) GDN_FETCH(t0 + MAX_TOKENS);  // in flight during this window's recurrence
+    // position by position, this thread's RPH state rows side by side (independent chains, each with the
+    // step kernel's operations in its order; the position's k, q and gates read once for all of them)
+    for (int t = 0; t < n; ++t) {
+      const float gd = dec[buf][t], bt = bet[buf][t];
+      const float k0 = ks[buf][t][4 * l], k1 = ks[buf][t][4 * l + 1], k2 = ks[buf][t][4 * l + 2],
+                  k3 = ks[buf][t][4 * l + 3];
+      const float q0 = qs[buf][t][4 * l], q1 = qs[buf][t][4 * l + 1], q2 = qs[buf][t][4 * l + 2],
+                  q3 = qs[buf][t][4 * l + 3];
 #pragma unroll
-    for (int i = 0; i < RPH; ++i) {
-      const int r = r0 + hw + 16 * i;
-      for (int t = 0; t < n; ++t) {
-        const float gd = dec[buf][t];
-        const float k0 = ks[buf][t][4 * l], k1 = ks[buf][t][4 * l + 1], k2 = ks[buf][t][4 * l + 2],
-                    k3 = ks[buf][t][4 * l + 3];
+      for (int i = 0; i < RPH; ++i) {
+        const int r = r0 + hw + 16 * i;
         s[i][0] = s[i][0] * gd;
         float kv = 0.0f + s[i][0] * k0;
         float comp = 0.0f;
@@ -472,16 +478,16 @@ __global__ __launch_bounds__(GDN_THREADS) void k_gdn_batch(GdnArgs a, GdnBatch b
           kv = next;
         }
         const float kvm = half_wave_sum(kv);
-        const float delta = (vs[buf][t][r] - kvm) * bet[buf][t];
+        const float delta = (vs[buf][t][r] - kvm) * bt;
         float o = 0.0f;
         s[i][0] = __builtin_fmaf(k0, delta, s[i][0]);
-        o = __builtin_fmaf(s[i][0], qs[buf][t][4 * l], o);
+        o = __builtin_fmaf(s[i][0], q0, o);
         s[i][1] = __builtin_fmaf(k1, delta, s[i][1]);
-        o = __builtin_fmaf(s[i][1], qs[buf][t][4 * l + 1], o);
+        o = __builtin_fmaf(s[i][1], q1, o);
         s[i][2] = __builtin_fmaf(k2, delta, s[i][2]);
-        o = __builtin_fmaf(s[i][2], qs[buf][t][4 * l + 2], o);
+        o = __builtin_fmaf(s[i][2], q2, o);
         s[i][3] = __builtin_fmaf(k3, delta, s[i][3]);
-        o = __builtin_fmaf(s[i][3], qs[buf][t][4 * l + 3], o);
+        o = __builtin_fmaf(s[i][3], q3, o);
         const float y = half_wave_sum(o);
         if (l == 0) st_pub(a.ypub + ((size_t)(t0 + t) * a.hv + h) * GDN_D + r, round_bf(y));
       }

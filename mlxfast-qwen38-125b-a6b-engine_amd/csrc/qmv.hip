@@ -426,9 +426,9 @@ __global__ __launch_bounds__(QMM_THREADS) void k_qmm(const uint32_t* __restrict_
   // weights and (scale, bias) pairs of step s for this lane's row
   uint4 wc, wn;
   uint32_t pc[4], pn[4];
-  auto load_w = [&](int s, uint4& w, uint32_t (&p)[4]) {
+  auto load_w = [&](int s, uint4& w, uint32_t (&p)[4]) {  // cached: the row tile's other token blocks reread it
     const int q = s / IT, it = s - q * IT;
-    w = ldg16(wrow + (size_t)(chain(4 * q + g) + L * it) * 4);
+    w = *reinterpret_cast<const uint4*>(wrow + (size_t)(chain(4 * q + g) + L * it) * 4);
 #pragma unroll
     for (int b = 0; b < 4; ++b) p[b] = srow[(chain(4 * q + b) >> rs) * IT + it];
   };
@@ -559,7 +559,7 @@ __global__ __launch_bounds__(QMM_THREADS) void k_moe_qmm(MoeArgs a, int tiles) {
   uint4 wr[IT];
   uint32_t pr[IT][4];
   auto load_w = [&](int q, int it, uint4& w, uint32_t (&p)[4]) {  // any q: the blocks stay inside the matrix
-    w = ldg16(wrow + (size_t)(chain(4 * q + g) + L * it) * 4);
+    w = *reinterpret_cast<const uint4*>(wrow + (size_t)(chain(4 * q + g) + L * it) * 4);  // cached: an expert's chunks
 #pragma unroll
     for (int b = 0; b < 4; ++b) p[b] = srow[(chain(4 * q + b) >> rs) * IT + it];
   };
@@ -769,7 +769,7 @@ __global__ __launch_bounds__(QMN_THREADS) void k_qmn(const uint32_t* __restrict_
   };
   auto load = [&](int s, Step& d) {
     const int q = p * G + s / IT, it = s - (s / IT) * IT;
-    d.w = ldg16(wrow + (size_t)(chain(4 * q + g) + L * it) * 4);
+    d.w = *reinterpret_cast<const uint4*>(wrow + (size_t)(chain(4 * q + g) + L * it) * 4);  // cached: reread per token block
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
       const int u = chain(4 * q + b), j = u + L * it;

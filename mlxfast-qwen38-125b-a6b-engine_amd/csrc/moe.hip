@@ -582,7 +582,7 @@ __device__ __forceinline__ int dd_unit(int n_units) {
 template <int L>
 constexpr int dd_gate_up_rows() { return 4 * (64 / L) > 16 ? 4 * (64 / L) : 16; }
 
-template <int L, int IT, bool PK>
+template <int L, int IT, bool PK, bool CB>
 __global__ __launch_bounds__(DD_THREADS) void k_moe_gate_up_dd(MoeArgs a0) {
   const MoeArgs a = a0.gorder ? a0 : moe_window(a0, blockIdx.y);
   extern __shared__ uint32_t lds[];  // [H/32][XP_DW]: the slot's token
@@ -618,10 +618,10 @@ __global__ __launch_bounds__(DD_THREADS) void k_moe_gate_up_dd(MoeArgs a0) {
 #pragma unroll
   for (int p = 0; p < NP; ++p) {
     const size_t row = rbase + f0 + (p * 4 + wave) * RW + grp;
-    G[p].template load_as<PK>(gw + row * (H / 8), gsc + row * ng, gbi + row * ng, PK ? gsb + row * P : nullptr, nb, gs,
-                              sub, true);
-    U[p].template load_as<PK>(uw + row * (H / 8), usc + row * ng, ubi + row * ng, PK ? usb + row * P : nullptr, nb, gs,
-                              sub, true);
+    G[p].template load_as<PK, CB>(gw + row * (H / 8), gsc + row * ng, gbi + row * ng, PK ? gsb + row * P : nullptr, nb,
+                                  gs, sub, true);
+    U[p].template load_as<PK, CB>(uw + row * (H / 8), usc + row * ng, ubi + row * ng, PK ? usb + row * P : nullptr, nb,
+                                  gs, sub, true);
   }
   // the token's prepared activation blocks -> LDS (LDS-direct, one wait)
   stage16(lds, a.xp_x + (size_t)m * nb * XP_DW, nb * XP_DW);
@@ -889,13 +889,18 @@ static hipError_t gate_up_dd_pk(const MoeArgs& a, hipStream_t st) {
     return hipErrorNotSupported;
   } else {
     const size_t lds = (size_t)(a.H / 32) * XP_DW * 4;
-    static size_t cur = 0;
-    hipError_t e = ensure_lds(k_moe_gate_up_dd<L, IT, PK>, lds, cur);
+    static size_t cur = 0, cur_b = 0;
+    hipError_t e = a.gorder ? ensure_lds(k_moe_gate_up_dd<L, IT, PK, true>, lds, cur_b)
+                            : ensure_lds(k_moe_gate_up_dd<L, IT, PK, false>, lds, cur);
     if (e != hipSuccess) return e;
     if (a.F % dd_gate_up_rows<L>() != 0) return hipErrorInvalidValue;
     const int nw = a.gorder ? 1 : a.nwin;  // the global order: every window's units in one row of the grid
     const int units = a.M * (a.K + 1) * (a.gorder ? a.nwin : 1) * (a.F / dd_gate_up_rows<L>());
-    hipLaunchKernelGGL((k_moe_gate_up_dd<L, IT, PK>), dim3((units + 7) / 8 * 8, nw), dim3(DD_THREADS), lds, st, a);
+    // the global order reads an expert's rows once per slot of the batch, side by side on one XCD: cached loads
+    if (a.gorder)
+      hipLaunchKernelGGL((k_moe_gate_up_dd<L, IT, PK, true>), dim3((units + 7) / 8 * 8, nw), dim3(DD_THREADS), lds, st, a);
+    else
+      hipLaunchKernelGGL((k_moe_gate_up_dd<L, IT, PK, false>), dim3((units + 7) / 8 * 8, nw), dim3(DD_THREADS), lds, st, a);
     return hipGetLastError();
   }
 }

@@ -24,7 +24,7 @@ __global__ __launch_bounds__(256) void k_xprep(const bf16* __restrict__ x, int M
 // rows are loaded before the activations are staged.  Grid Y batches windows
 // of `win` tokens (window w: tokens w * win .. of the M in all), each computed
 // as its own launch would.
-template <int L, int IT>
+template <int L, int IT, bool CB>
 __global__ __launch_bounds__(256) void k_qmv(const uint32_t* __restrict__ wq, const bf16* __restrict__ sc,
                                              const bf16* __restrict__ bi, const uint32_t* __restrict__ sbp,
                                              int N, int K, int gs,
@@ -51,10 +51,10 @@ __global__ __launch_bounds__(256) void k_qmv(const uint32_t* __restrict__ wq, co
     const int rA = b0 + grp * 2, rB = rA + 1;
     const bool vA = rA < row_end, vB = rB < row_end;
     const int ra = vA ? rA : row0, rb = vB ? rB : row0;
-    A.load(wq + (size_t)ra * (K / 8), sc + (size_t)ra * ng, bi + (size_t)ra * ng,
-           sbp ? sbp + (size_t)ra * P : nullptr, nb, gs, sub, vA);
-    B.load(wq + (size_t)rb * (K / 8), sc + (size_t)rb * ng, bi + (size_t)rb * ng,
-           sbp ? sbp + (size_t)rb * P : nullptr, nb, gs, sub, vB);
+    A.template load<CB>(wq + (size_t)ra * (K / 8), sc + (size_t)ra * ng, bi + (size_t)ra * ng,
+                        sbp ? sbp + (size_t)ra * P : nullptr, nb, gs, sub, vA);
+    B.template load<CB>(wq + (size_t)rb * (K / 8), sc + (size_t)rb * ng, bi + (size_t)rb * ng,
+                        sbp ? sbp + (size_t)rb * P : nullptr, nb, gs, sub, vB);
   };
   if (base < row_end) load2(base);  // first rows in flight before the staging
   stage16(lds, xp, M * nb * XP_DW);
@@ -981,7 +981,8 @@ static hipError_t qmv_li(const uint32_t* wq, const bf16* s, const bf16* b, const
   constexpr int rows_pass = 4 * (64 / L) * 2;
   const int passes = (N + rows_pass - 1) / rows_pass;
   int per = (passes + 511) / 512;  // about two workgroups per CU, at least one pass each
-  if (win <= 0) {
+  const bool batch = win <= 0;     // a prefill batch: its windows reread the rows, so cached loads
+  if (batch) {
     int cap = (int)((50 * 1024) / ((size_t)(K / 32) * XP_DW * 4));  // three workgroups' LDS per CU
     cap = cap < 1 ? 1 : cap;
     const int want = 4 * device_cus();
@@ -997,11 +998,15 @@ static hipError_t qmv_li(const uint32_t* wq, const bf16* s, const bf16* b, const
   int grid = (N + rows_per_wg - 1) / rows_per_wg;
   if (nwin > 1) grid = (grid + 7) / 8 * 8;
   const size_t lds = (size_t)(M < win ? M : win) * (K / 32) * XP_DW * 4;
-  static size_t cur = 0;
-  hipError_t e = ensure_lds(k_qmv<L, IT>, lds, cur);
+  static size_t cur = 0, cur_b = 0;
+  hipError_t e = batch ? ensure_lds(k_qmv<L, IT, true>, lds, cur_b) : ensure_lds(k_qmv<L, IT, false>, lds, cur);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((k_qmv<L, IT>), dim3(grid, nwin), dim3(256), lds, st, wq, s, b, sb, N, K, gs, xp, M, y, yf,
-                     rows_per_wg, win);
+  if (batch)
+    hipLaunchKernelGGL((k_qmv<L, IT, true>), dim3(grid, nwin), dim3(256), lds, st, wq, s, b, sb, N, K, gs, xp, M, y, yf,
+                       rows_per_wg, win);
+  else
+    hipLaunchKernelGGL((k_qmv<L, IT, false>), dim3(grid, nwin), dim3(256), lds, st, wq, s, b, sb, N, K, gs, xp, M, y,
+                       yf, rows_per_wg, win);
   return hipGetLastError();
 }
 

@@ -29,6 +29,8 @@ struct QRow {
   // A padding row (valid false) must still point at a real row of the matrix:
   // its loads are issued like any other (no branch, so no wait at a join) and
   // its dot is forced to 0.
+  // CACHED: plain loads (a prefill batch rereads the rows from L2), else streaming (non-temporal) loads
+  template <bool CACHED = false>
   __device__ __forceinline__ void load(const uint32_t* __restrict__ wrow, const bf16* __restrict__ srow,
                                        const bf16* __restrict__ brow, const uint32_t* __restrict__ sbrow, int nb,
                                        int gs, int sub, bool valid) {
@@ -37,7 +39,7 @@ struct QRow {
     for (int it = 0; it < NB; ++it) {
       const int j = sub + it * L;
       if (IT ? true : j < nb) {
-        const uint4 v = ldg16(wrow + (size_t)j * 4);
+        const uint4 v = CACHED ? *reinterpret_cast<const uint4*>(wrow + (size_t)j * 4) : ldg16(wrow + (size_t)j * 4);
         w[it][0] = v.x;
         w[it][1] = v.y;
         w[it][2] = v.z;
@@ -82,14 +84,14 @@ struct QRow {
 
   // load() with the scale/bias pairs taken from packed rows only (sbrow != null):
   // one code path, so no load of the other layout's path is ever waited for.
-  template <bool PK>
+  template <bool PK, bool CACHED = false>
   __device__ __forceinline__ void load_as(const uint32_t* __restrict__ wrow, const bf16* __restrict__ srow,
                                           const bf16* __restrict__ brow, const uint32_t* __restrict__ sbrow, int nb,
                                           int gs, int sub, bool valid) {
     if constexpr (PK) {
-      load(wrow, nullptr, nullptr, sbrow, nb, gs, sub, valid);
+      load<CACHED>(wrow, nullptr, nullptr, sbrow, nb, gs, sub, valid);
     } else {
-      load(wrow, srow, brow, nullptr, nb, gs, sub, valid);
+      load<CACHED>(wrow, srow, brow, nullptr, nb, gs, sub, valid);
     }
   }
 

@@ -33,6 +33,7 @@ namespace mtpx {
 constexpr int GDN_THREADS = 512;  // 16 half-waves
 constexpr int GDN_D = 128;
 constexpr int GDN_SPLIT = 4;      // workgroups per value head, each owning 128 / GDN_SPLIT state rows
+constexpr int GDN_BSPLIT = 8;     // the batch kernel's workgroups per value head (a long recurrence: more, shorter chains)
 
 // log1p(y), y in [0, 1]: 2 atanh(s), s = y / (2 + y), odd series to s^15.
 __device__ __forceinline__ float log1p_det(float y) {
@@ -304,7 +305,8 @@ __global__ __launch_bounds__(GDN_THREADS) void k_gdn_step(GdnArgs a) {
 //   k_gdn_prep_batch: one workgroup per position: the conv, SiLU and q/k norms of every key head's
 //     q and k and every value head's v (a half-wave per 128-channel vector, as the step kernel
 //     does them), and every head's decay and beta gates, into the batch's prep buffers;
-//   k_gdn_batch: the step kernel's workgroups (four per value head), the P committed steps of the
+//   k_gdn_batch: the step kernel's workgroup layout with eight workgroups per value head (16 state
+//     rows each: the batch's long recurrence runs as more, shorter chains), the P committed steps of the
 //     previous window replayed onto the state, then the batch's positions in order, the next
 //     window's prepped vectors loaded while the current one's recurrence runs; every position
 //     committed: the state is stored after the last one, the batch's last kc-1 conv input rows
@@ -370,13 +372,13 @@ __global__ __launch_bounds__(GDN_THREADS) void k_gdn_batch(GdnArgs a, GdnBatch b
   __shared__ float ys[MAX_TOKENS][GDN_D];
   __shared__ bf16 gated[MAX_TOKENS][GDN_D];
   const int h = blockIdx.x, ratio = a.hv / a.hk, hk = h / ratio;
-  const int r0 = blockIdx.y * (GDN_D / GDN_SPLIT);  // this workgroup's state rows
+  const int r0 = blockIdx.y * (GDN_D / GDN_BSPLIT);  // this workgroup's state rows
   const bool w0 = blockIdx.y == 0;
   const bool lead = (h % ratio) == 0 && w0;         // writes the q/k channels' conv base rows
   const int hw = threadIdx.x >> 5, l = threadIdx.x & 31;
   const int S = a.S, P = a.P, KM1 = a.kc - 1;
   const int ntask = 2 * a.hk + a.hv;
-  constexpr int RPH = GDN_D / GDN_SPLIT / (GDN_THREADS / 32);
+  constexpr int RPH = GDN_D / GDN_BSPLIT / (GDN_THREADS / 32);
   // a window's prepped vectors: (q, k, v) x MAX_TOKENS x 128 floats as float4 units, and the gates
   constexpr int U4 = 3 * MAX_TOKENS * GDN_D / 4;  // float4 units of a window
   // this thread's units: u0 = threadIdx.x and u1 = threadIdx.x + GDN_THREADS (while < U4) -> (vector which,
@@ -507,7 +509,7 @@ __global__ __launch_bounds__(GDN_THREADS) void k_gdn_batch(GdnArgs a, GdnBatch b
     const int ch = vec * GDN_D + d;
     a.conv_nxt[(size_t)j * a.cd + ch] = f2bf(gdn_row(a, P + S + j, ch));
   }
-  if (!ticket_last(a.tickets + h, GDN_SPLIT - 1)) return;
+  if (!ticket_last(a.tickets + h, GDN_BSPLIT - 1)) return;
   for (int t0 = 0; t0 < S; t0 += MAX_TOKENS) {
     const int n = S - t0 < MAX_TOKENS ? S - t0 : MAX_TOKENS;
     for (int i = threadIdx.x; i < n * GDN_D; i += GDN_THREADS)
@@ -594,7 +596,7 @@ template <int KC>
 static hipError_t gdn_batch_kc(const GdnArgs& a, const GdnBatch& b, hipStream_t st) {
   if (!a.tickets || !a.ypub || !b.vecs || !b.gates || a.S < 1) return hipErrorInvalidValue;
   hipLaunchKernelGGL(k_gdn_prep_batch<KC>, dim3(a.S), dim3(GDN_THREADS), 0, st, a, b);
-  hipLaunchKernelGGL(k_gdn_batch<KC>, dim3(a.hv, GDN_SPLIT), dim3(GDN_THREADS), 0, st, a, b);
+  hipLaunchKernelGGL(k_gdn_batch<KC>, dim3(a.hv, GDN_BSPLIT), dim3(GDN_THREADS), 0, st, a, b);
   return hipGetLastError();
 }
 

@@ -5,7 +5,7 @@ gated-deltanet + 12 attention, each with hyper-connection mixers and a 512-exper
 MoE; hidden 2560, vocab 248320, affine 4-bit gs64, all weights resident in HBM; layer 1 carries the
 PLE n-gram block with its full 320,001,446-row table, 32 GB, --no-ple leaves it out) with the MTP
 head.  A 1024-token random prompt goes through mtpx_session_prefill (the target prefill in batches of
-256 positions, bit-equal to verifying and committing windows of 8; the drafter observes it), then
+512 positions, bit-equal to verifying and committing windows of 8; the drafter observes it), then
 1024 tokens are generated greedily through mtpx_round (the device-resident round: k drafter
 steps, a verify of the carry and the k drafts, the on-device greedy accept read back once, target
 commit, drafter finalize).  First a serial greedy decode (k = 0) of the same 1024 tokens gives the

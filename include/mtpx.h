@@ -577,11 +577,11 @@ int mtpx_target_commit(mtpx_target_state st, int n);
  * (an open verify window is discarded first) -> logits bf16 [vocab] of the LAST position and multi
  * bf16 [S, hc*hidden] of every position (each may be NULL).  Every output and the state it leaves
  * equal those of verifying and committing the tokens in windows of 8 in turn; the work runs over
- * batches of up to 256 positions at once: one launch per kernel for the whole batch where each
- * position's result is its own (GEMVs on the matrix cores in windows of eight tokens with the
- * weights shared through L2, norms, mixers, attention -- every query attends to the keys up to its
- * own position --, the MoE as windows of 8 in batched launches), the GDN and PLE recurrences window
- * by window.  Replaces the runner's prompt prefill windows (Runner/FastModel/TrackP12Prefill.swift:1-237,
+ * batches of up to 512 positions at once: one launch per kernel for the whole batch where each
+ * position's result is its own (the dense projections as GEMMs on the matrix cores, norms, mixers,
+ * attention -- every query attends to the keys up to its own position --, the MoE routed as windows
+ * of 8 and its experts over the batch's slots sorted by expert, the GDN recurrence over the batch),
+ * the PLE recurrence window by window.  Replaces the runner's prompt prefill windows (Runner/FastModel/TrackP12Prefill.swift:1-237,
  * TrackPrefillSort.swift:1-201, TrackPrefillIndirect.swift:5-227), with the decode path's arithmetic
  * instead of MLX's steel GEMM: the prompt's positions get the bits the verify path gives them. */
 int mtpx_target_prefill(mtpx_ctx ctx, mtpx_target t, mtpx_target_state st, const int32_t* ids, int S,
@@ -615,7 +615,7 @@ int mtpx_session_free(mtpx_session s);
 /* Back to an empty request (caches reset, a fresh drafter state). */
 int mtpx_session_reset(mtpx_session s);
 /* The prompt (device int32 [n], offset + n <= MTPX_INDEXER_BUDGET): mtpx_target_prefill in batches
- * of up to 256 positions, each committed and its multi streams observed by the drafter;
+ * of up to 512 positions, each committed and its multi streams observed by the drafter;
  * *first_token (host) = the argmax of the last position, which becomes the carry.  Synchronises
  * once. */
 int mtpx_session_prefill(mtpx_session s, const int32_t* ids, int n, int32_t* first_token);

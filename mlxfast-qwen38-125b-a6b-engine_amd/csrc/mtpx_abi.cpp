@@ -2542,7 +2542,7 @@ int mtpx_target_verify(mtpx_ctx h, mtpx_target th, mtpx_target_state sh, const i
   return rc;
 }
 
-constexpr int PREFILL_PASS = 256;  // positions per prefill batch (workspace: attention partials grow with it)
+constexpr int PREFILL_PASS = 512;  // positions per prefill batch (workspace: attention partials grow with it)
 
 int mtpx_target_prefill(mtpx_ctx h, mtpx_target th, mtpx_target_state sh, const int32_t* ids, int S,
                         uint16_t* logits, uint16_t* multi) {

@@ -26,7 +26,7 @@ namespace {
 using namespace mtpx;
 
 constexpr int OUT_WORDS = 24;  // out3 at 0, argmax rows at 4.., committed tokens at 12..
-constexpr int PROMPT_BATCH = 256;  // prompt positions per target prefill call (their multi streams are observed)
+constexpr int PROMPT_BATCH = 512;  // prompt positions per target prefill call (their multi streams are observed)
 
 struct Session {
   mtpx_ctx ctx{nullptr};

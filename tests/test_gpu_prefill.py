@@ -15,7 +15,7 @@ pytestmark = pytest.mark.gpu
 from gpu_util import dev, empty_bf16, host, need_gpu, rand_bf16, write_device  # noqa: E402
 
 LAYER = dict(hidden=256, experts=16, top_k=4, expert_width=128, group_size=32, heads=4, kv_heads=2, head_dim=64,
-             rot_dims=16, index_dim=32, rope_theta=1e7, eps=1e-6, max_positions=400)
+             rot_dims=16, index_dim=32, rope_theta=1e7, eps=1e-6, max_positions=700)
 TARGET = dict(key_heads=1, value_heads=2, conv_kernel=4, num_layers=5, full_attention_interval=4, hc=4, lowrank=64,
               vocab=1000)
 
@@ -130,8 +130,8 @@ def test_prefill_matches_oracle_windows(ctx):
 
 
 def test_prefill_two_batches_matches_windows(ctx):
-    """300 positions: two prefill batches (256 + 44), 37 full windows and a tail of 4; then a prefill of
-    3 more positions (one short window) and a verify, each against the windowed path's state."""
+    """600 positions: two prefill batches (512 + 88), 75 full windows; then a prefill of 3 more positions
+    (one short window) and a verify, each against the windowed path's state."""
     import mtpx
     from oracle.target_ref import download_target
     t, cfg = _small_target(ctx, 41)
@@ -144,7 +144,7 @@ def test_prefill_two_batches_matches_windows(ctx):
     _load_prefix(a, kinds, geoms, cfg, pre, 8)
     _load_prefix(b, kinds, geoms, cfg, pre, 8)
     r = np.random.default_rng(4)
-    for n in (300, 3):
+    for n in (600, 3):
         ids = r.integers(0, V, n).astype(np.int32)
         ids[r.integers(0, n, max(1, n // 50))] = 7
         print("case prefill", n, "vs windows", flush=True)

@@ -1203,7 +1203,7 @@ template <int L, int IT>
 static hipError_t qmn_li(const uint32_t* w1, const uint32_t* sb1, int N1, bf16* y1, const uint32_t* w2,
                          const uint32_t* sb2, int N2, bf16* y2, int K, int gs, const uint32_t* xmb, int M,
                          hipStream_t st) {
-  constexpr int QT = 2;
+  constexpr int QT = 4;  // 16 tokens per workgroup (two token groups measured slower at 512-position batches)
   const int tiles1 = (N1 + 15) / 16, tiles = tiles1 + (w2 ? (N2 + 15) / 16 : 0);
   const int tblocks = (M + MMA_TOK * QT - 1) / (MMA_TOK * QT);
   hipLaunchKernelGGL((k_qmn<L, IT, QT>), dim3(tiles * ((tblocks + 7) / 8 * 8)), dim3(QMN_THREADS), 0, st, w1, sb1, N1, y1, w2, sb2, N2,

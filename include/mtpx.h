@@ -190,8 +190,16 @@ int mtpx_kv_buffers(mtpx_kv kv, uint16_t** k, uint16_t** v, int64_t* tmax);
 
 /* ---- a18, a21: argmax and greedy acceptance ---------------------------------
  * argmax over V per row, lowest id on ties (Runner/Qwen4ExpMTPDrafter.swift:25-27).
- * NaN ranks above every number (the first NaN of a row wins, as numpy's argmax). */
+ * A NaN ranks as -inf and never wins; a row of only -inf / NaN gives 0 (MLX's argmax,
+ * MLX/backend/metal/kernels/arg_reduce.metal:42-62). */
 int mtpx_argmax_rows(mtpx_ctx ctx, const float* x, int rows, int64_t V, int32_t* out);
+/* The two best entries of each row: ids int32 [rows, 2] and values f32 [rows, 2] (exact copies of
+ * the logits; a NaN ranks as -inf), in the argmax order: value descending, lowest id first among
+ * equal values, so ids[r][0] is the row's argmax; V >= 2.  The MTP policy's top-two query
+ * cbv2MTPTopTwo (Runner/FastModel/TrackFastModel.swift:1456-1460, CBv2MTPPolicyTopTwoProviding),
+ * which the reference answers in the un-vendored engine core. */
+int mtpx_top_two(mtpx_ctx ctx, const float* logits, int rows, int64_t V, int32_t* ids, float* values);
+int mtpx_top_two_bf16(mtpx_ctx ctx, const uint16_t* logits, int rows, int64_t V, int32_t* ids, float* values);
 /* logits f32 [k+1, V] (verify rows), drafts int32 [k] -> out3 int32 {n accepted,
  * bonus token, KV rollback index = kv_offset + n + 1}.  The engine-core accept
  * loop (docs/qwen38-125b-a6b-port-notes.md:313-343), decided on the device. */
@@ -211,11 +219,21 @@ int mtpx_accept_greedy_bf16(mtpx_ctx ctx, const uint16_t* logits, int k, int64_t
 int mtpx_force_draft(mtpx_ctx ctx, int32_t* token, const int32_t* teacher, int64_t pos, float p, uint64_t seed);
 
 /* ---- a22: temperature rejection sampling (no reference counterpart) ----------
- * tlogits f32 [k+1, V], dlogits f32 [k, V] (row i proposed drafts[i]);
- * Philox4x32-10 key = seed, counter = {offset lo, offset hi, i, 0}. */
+ * Speculative sampling (Leviathan et al. 2023): draft i is accepted when u * p_d(d_i) < p_t(d_i),
+ * the first rejection samples norm(max(0, p_t - p_d)) of its row, all accepted samples p_t of row
+ * k; probabilities at the temperature.  tlogits f32 [k+1, V], dlogits f32 [k, V] (row i proposed
+ * drafts[i]) or NULL: the draft distributions are one-hot at the drafts (a greedy drafter, as the
+ * reference's MTP head: accept with probability p_t(d_i), a rejection samples p_t without d_i).
+ * Philox4x32-10 key = seed, counter = {offset lo, offset hi, i, 0} for i = 1..k+1 (u = word 0,
+ * the resampling draw = word 1).  out3 = {n, token, kv_offset + n + 1}. */
 int mtpx_accept_sample(mtpx_ctx ctx, const float* tlogits, const float* dlogits, int k,
                        int64_t V, const int32_t* drafts, float temperature, uint64_t seed,
                        uint64_t offset, int32_t kv_offset, int32_t* out3);
+/* The same on bf16 logits (the verify's output; dlogits bf16 [k, V] or NULL), with optional
+ * tokens_out int32 [k+1]: the committed tokens, drafts[0..n-1] then the sampled token. */
+int mtpx_accept_sample_bf16(mtpx_ctx ctx, const uint16_t* tlogits, const uint16_t* dlogits, int k, int64_t V,
+                            const int32_t* drafts, float temperature, uint64_t seed, uint64_t offset,
+                            int32_t kv_offset, int32_t* out3, int32_t* tokens_out);
 
 /* ---- one full-shape decoder layer (attention + MoE) for verify windows -------
  * x -> h1 = rms(x); qkv = W_qkv h1; prep + KV append; verify attention with
@@ -624,6 +642,14 @@ int mtpx_session_prefill(mtpx_session s, const int32_t* ids, int n, int32_t* fir
  * after it began (e.g. a prompt longer than the caches: its first windows are committed) leaves the
  * session refusing every prefill and round with MTPX_ERR_STATE until mtpx_session_reset. */
 int mtpx_round(mtpx_session s, int k, const mtpx_force_params* force, int32_t* tokens, int* n_tokens);
+/* A round at temperature > 0: the same steps with the greedy accept replaced by speculative
+ * sampling over the verify's bf16 logits with one-hot draft distributions (mtpx_accept_sample_bf16
+ * with dlogits NULL): key = seed, offset = the session's committed position before the round, so
+ * every round draws from its own counters and a round's draws belong to its position.  The output
+ * is distributed as sampling the target at that temperature token by token.  temperature == 0 is
+ * mtpx_round.  No reference counterpart (the reference decodes greedily). */
+int mtpx_round_sampled(mtpx_session s, int k, const mtpx_force_params* force, float temperature, uint64_t seed,
+                       int32_t* tokens, int* n_tokens);
 /* Committed offset; the session's target state and drafter (owned by the session). */
 int mtpx_session_info(mtpx_session s, int64_t* offset, mtpx_target_state* state, mtpx_drafter* drafter);
 

@@ -1421,6 +1421,7 @@ int mtpx_ctx_free(mtpx_ctx h) {
   if (!c) return MTPX_OK;
   hipSetDevice(c->device);
   hipStreamSynchronize(c->stream);
+  moe_scratch_release(c->device, c);
   if (c->ws) hipFree(c->ws);
   if (c->tickets) hipFree(c->tickets);
   for (auto& r : c->pending) {
@@ -1530,6 +1531,8 @@ int mtpx_moe_forward_noalloc(mtpx_ctx h, const mtpx_moe_weights* w, const uint16
   ARG(need <= moe_scratch_bytes(), "the MoE window needs %zu bytes of scratch; the maximum is %zu", need,
       moe_scratch_bytes());
   ARG(c->scratch, "no scratch on device %d", c->device);
+  if (!moe_scratch_claim(c->device, c))
+    return fail(MTPX_ERR_STATE, "the allocation-free MoE scratch of device %d belongs to another context", c->device);
   if (set_device(c)) return MTPX_ERR_HIP;
   // The same launches as mtpx_moe_forward, with the device scratch standing in for the workspace for
   // this call (nothing is allocated: the context's own workspace is put back afterwards).  No part of
@@ -1543,8 +1546,10 @@ int mtpx_moe_forward_noalloc(mtpx_ctx h, const mtpx_moe_weights* w, const uint16
   c->ws = ws0;
   c->ws_size = sz0;
   c->ws_used = 0;
+  const MoeDispatch* disp = c->last_disp;
+  c->last_disp = nullptr;  // inside the shared scratch: mtpx_last_moe_bytes does not cover this call
   if (rc) return rc;
-  if (n_unique) HIP_OK(hipMemcpyAsync(n_unique, &c->last_disp->n_unique, 4, hipMemcpyDeviceToDevice, c->stream));
+  if (n_unique) HIP_OK(hipMemcpyAsync(n_unique, &disp->n_unique, 4, hipMemcpyDeviceToDevice, c->stream));
   return MTPX_OK;
 }
 
@@ -1712,6 +1717,27 @@ int mtpx_accept_greedy_bf16(mtpx_ctx h, const uint16_t* logits, int k, int64_t V
   return MTPX_OK;
 }
 
+static int top_two(Ctx* c, const float* x, const uint16_t* xb, int rows, int64_t V, int32_t* ids, float* vals) {
+  ARG(c && (x || xb) && ids && vals, "null argument");
+  ARG(rows >= 1 && V >= 2 && V < (int64_t)1 << 31, "rows=%d V=%lld", rows, (long long)V);
+  if (set_device(c)) return MTPX_ERR_HIP;
+  const size_t n = 4 * argmax_work_items(rows, V);
+  int rc = ws_reserve(c, al(n * 4) + 256);
+  if (rc) return rc;
+  ws_begin(c);
+  float* p2 = ws_take<float>(c, n);
+  LAUNCH(c, "top_two", launch_top2(x, reinterpret_cast<const bf16*>(xb), rows, V, p2, ids, vals, c->stream));
+  return MTPX_OK;
+}
+
+int mtpx_top_two(mtpx_ctx h, const float* logits, int rows, int64_t V, int32_t* ids, float* values) {
+  return top_two(C(h), logits, nullptr, rows, V, ids, values);
+}
+
+int mtpx_top_two_bf16(mtpx_ctx h, const uint16_t* logits, int rows, int64_t V, int32_t* ids, float* values) {
+  return top_two(C(h), nullptr, logits, rows, V, ids, values);
+}
+
 int mtpx_force_draft(mtpx_ctx h, int32_t* token, const int32_t* teacher, int64_t pos, float p, uint64_t seed) {
   Ctx* c = C(h);
   ARG(c && token && teacher && pos >= 0, "bad argument");
@@ -1724,7 +1750,7 @@ int mtpx_accept_sample(mtpx_ctx h, const float* tlogits, const float* dlogits, i
                        const int32_t* drafts, float temperature, uint64_t seed, uint64_t offset, int32_t kv_offset,
                        int32_t* out3) {
   Ctx* c = C(h);
-  ARG(c && tlogits && out3 && (k == 0 || (dlogits && drafts)), "null argument");
+  ARG(c && tlogits && out3 && (k == 0 || drafts), "null argument");
   ARG(k >= 0 && k + 1 <= MAX_TOKENS && V >= 1 && V < (int64_t)1 << 31, "k=%d V=%lld", k, (long long)V);
   ARG(temperature > 0.0f && std::isfinite(temperature), "temperature must be > 0");
   if (set_device(c)) return MTPX_ERR_HIP;
@@ -1733,8 +1759,28 @@ int mtpx_accept_sample(mtpx_ctx h, const float* tlogits, const float* dlogits, i
   if (rc) return rc;
   ws_begin(c);
   float* work = ws_take<float>(c, n);
-  HIP_OK(launch_accept_sample(tlogits, dlogits, k, V, drafts, temperature, seed, offset, kv_offset, work, out3,
-                              c->stream));
+  LAUNCH(c, "accept_sample", launch_accept_sample(tlogits, dlogits, k, V, drafts, temperature, seed, offset,
+                                                  kv_offset, work, out3, c->stream));
+  return MTPX_OK;
+}
+
+int mtpx_accept_sample_bf16(mtpx_ctx h, const uint16_t* tlogits, const uint16_t* dlogits, int k, int64_t V,
+                            const int32_t* drafts, float temperature, uint64_t seed, uint64_t offset,
+                            int32_t kv_offset, int32_t* out3, int32_t* tokens_out) {
+  Ctx* c = C(h);
+  ARG(c && tlogits && out3 && (k == 0 || drafts), "null argument");
+  ARG(k >= 0 && k + 1 <= MAX_TOKENS && V >= 1 && V < (int64_t)1 << 31, "k=%d V=%lld", k, (long long)V);
+  ARG(temperature > 0.0f && std::isfinite(temperature), "temperature must be > 0");
+  if (set_device(c)) return MTPX_ERR_HIP;
+  const size_t n = accept_sample_work_floats(k, V);
+  int rc = ws_reserve(c, al(n * 4) + 256);
+  if (rc) return rc;
+  ws_begin(c);
+  float* work = ws_take<float>(c, n);
+  LAUNCH(c, "accept_sample",
+         launch_accept_sample_bf16(reinterpret_cast<const bf16*>(tlogits), reinterpret_cast<const bf16*>(dlogits), k,
+                                   V, drafts, temperature, seed, offset, kv_offset, work, out3, tokens_out,
+                                   c->stream));
   return MTPX_OK;
 }
 
@@ -2742,7 +2788,7 @@ int mtpx_profile_dump(mtpx_ctx h, char* buf, size_t n) {
 int mtpx_last_moe_bytes(mtpx_ctx h, int64_t* bytes, int32_t* n_unique) {
   Ctx* c = C(h);
   ARG(c && bytes, "null argument");
-  ARG(c->last_disp, "no MoE call on this context yet");
+  ARG(c->last_disp, "no MoE call with this context's workspace yet (the allocation-free entry keeps no count)");
   if (set_device(c)) return MTPX_ERR_HIP;
   int nu = 0;
   HIP_OK(hipMemcpyAsync(&nu, &c->last_disp->n_unique, 4, hipMemcpyDeviceToHost, c->stream));

@@ -87,6 +87,8 @@ hipError_t launch_fill_bf16(bf16* out, int64_t n, bf16 v, hipStream_t st);
 // --- scratch of the allocation-free MoE entry point (noalloc.hip)
 size_t moe_scratch_bytes();
 hipError_t moe_scratch_address(int device, void** ptr);
+bool moe_scratch_claim(int device, const void* owner);
+void moe_scratch_release(int device, const void* owner);
 
 // --- MoE (moe.hip)
 // Expert-grouped dispatch of one MoE window, indexed by the expert kernels'
@@ -200,7 +202,15 @@ hipError_t launch_force_draft(int32_t* token, const int32_t* teacher, int64_t po
 hipError_t launch_accept_sample(const float* tlogits, const float* dlogits, int k, int64_t V,
                                 const int32_t* drafts, float temperature, uint64_t seed, uint64_t offset,
                                 int32_t kv_offset, float* work, int32_t* out3, hipStream_t st);
+// bf16 logits (the verify's output); dlogits null = one-hot draft rows at drafts (a greedy drafter);
+// tokens [k+1] optional: the committed tokens (drafts[0..n-1], then the sampled token)
+hipError_t launch_accept_sample_bf16(const bf16* tlogits, const bf16* dlogits, int k, int64_t V,
+                                     const int32_t* drafts, float temperature, uint64_t seed, uint64_t offset,
+                                     int32_t kv_offset, float* work, int32_t* out3, int32_t* tokens, hipStream_t st);
 size_t accept_sample_work_floats(int k, int64_t V);
+// top two of each row (x f32 or, when x is null, xb bf16): p2 = 4 * argmax_work_items(rows, V) floats
+hipError_t launch_top2(const float* x, const bf16* xb, int rows, int64_t V, float* p2, int32_t* ids, float* vals,
+                       hipStream_t st);
 size_t argmax_work_items(int rows, int64_t V);
 hipError_t launch_argmax_rows_bf16(const bf16* x, int rows, int64_t V, float* pval, int32_t* pidx,
                                    const int32_t* ids, int32_t* out, hipStream_t st);

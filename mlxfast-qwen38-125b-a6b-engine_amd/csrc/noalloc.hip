@@ -15,6 +15,7 @@ static __device__ __align__(256) uint8_t scratch[MOE_SCRATCH_BYTES];
 
 std::mutex g_mu;
 void* g_addr[64] = {nullptr};
+const void* g_owner[64] = {nullptr};  // the context that uses this device's array, until it is freed
 
 }  // namespace
 
@@ -34,6 +35,21 @@ hipError_t moe_scratch_address(int device, void** ptr) {
   }
   *ptr = g_addr[device];
   return hipSuccess;
+}
+
+// One context per device may use the array (the first that asks); another gets false, so two
+// contexts on one GPU never share it unknowingly.  The claim ends with moe_scratch_release.
+bool moe_scratch_claim(int device, const void* owner) {
+  if (device < 0 || device >= 64) return false;
+  std::lock_guard<std::mutex> lock(g_mu);
+  if (!g_owner[device]) g_owner[device] = owner;
+  return g_owner[device] == owner;
+}
+
+void moe_scratch_release(int device, const void* owner) {
+  if (device < 0 || device >= 64) return;
+  std::lock_guard<std::mutex> lock(g_mu);
+  if (g_owner[device] == owner) g_owner[device] = nullptr;
 }
 
 }  // namespace mtpx

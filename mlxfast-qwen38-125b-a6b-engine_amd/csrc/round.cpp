@@ -9,7 +9,8 @@
 // stream of the position before it).  A round with draft depth k:
 //   k drafter steps (the first flushes the drafter's backlog), each draft optionally replaced by
 //   the forcing hook; a verify of the carry and the k drafts; the greedy accept on the device
-//   (row argmaxes, accepted prefix n, bonus token, committed tokens); ONE readback of those
+//   (row argmaxes, accepted prefix n, bonus token, committed tokens) -- or, at a temperature,
+//   speculative sampling with one-hot draft distributions --; ONE readback of those
 //   integers; the target commit of n + 1 positions and the drafter finalize with the target's
 //   own multi streams; the next carry is copied on the device (bonus token, multi row n).
 // k = 0 is a plain serial decode step (verify of the carry alone, commit, observe).
@@ -149,7 +150,8 @@ int mtpx_session_reset(mtpx_session sh) {
 }
 
 static int prefill_batches(Session* s, const int32_t* ids, int n, int32_t* first_token);
-static int round_steps(Session* s, int k, const mtpx_force_params* force, int32_t* tokens, int* n_tokens);
+static int round_steps(Session* s, int k, const mtpx_force_params* force, float temperature, uint64_t seed,
+                       int32_t* tokens, int* n_tokens);
 
 int mtpx_session_prefill(mtpx_session sh, const int32_t* ids, int n, int32_t* first_token) {
   Session* s = static_cast<Session*>(sh.ctx);
@@ -185,8 +187,14 @@ static int prefill_batches(Session* s, const int32_t* ids, int n, int32_t* first
 }
 
 int mtpx_round(mtpx_session sh, int k, const mtpx_force_params* force, int32_t* tokens, int* n_tokens) {
+  return mtpx_round_sampled(sh, k, force, 0.0f, 0, tokens, n_tokens);
+}
+
+int mtpx_round_sampled(mtpx_session sh, int k, const mtpx_force_params* force, float temperature, uint64_t seed,
+                       int32_t* tokens, int* n_tokens) {
   Session* s = static_cast<Session*>(sh.ctx);
   if (!s || !tokens || !n_tokens) return set_error(MTPX_ERR_ARG, "round: null argument");
+  if (!(temperature >= 0.0f) || !(temperature < 3.4e38f)) return set_error(MTPX_ERR_ARG, "round: temperature");
   if (s->broken) return set_error(MTPX_ERR_STATE, "session: a previous call failed part way (reset it)");
   if (!s->primed) return set_error(MTPX_ERR_STATE, "round: no context (prefill first)");
   if (k < 0 || k > MTPX_MAX_DRAFT_DEPTH || (k > 0 && !s->drafter.ctx))
@@ -194,12 +202,13 @@ int mtpx_round(mtpx_session sh, int k, const mtpx_force_params* force, int32_t* 
   if (s->offset + k + 1 > MTPX_INDEXER_BUDGET) return set_error(MTPX_ERR_ARG, "round: past the indexer budget");
   if (force && force->teacher && (force->rate < 0.0f || force->rate > 1.0f))
     return set_error(MTPX_ERR_ARG, "round: forcing rate outside [0, 1]");
-  const int rc = round_steps(s, k, force, tokens, n_tokens);
+  const int rc = round_steps(s, k, force, temperature, seed, tokens, n_tokens);
   if (rc) s->broken = true;  // drafter and target may have advanced apart
   return rc;
 }
 
-static int round_steps(Session* s, int k, const mtpx_force_params* force, int32_t* tokens, int* n_tokens) {
+static int round_steps(Session* s, int k, const mtpx_force_params* force, float temperature, uint64_t seed,
+                       int32_t* tokens, int* n_tokens) {
   const int64_t o = s->offset;
   for (int i = 0; i < k; ++i) {
     RC(mtpx_drafter_step(s->drafter, s->ids + i, i == 0 ? s->carry : s->mo + (size_t)(i - 1) * s->W, s->ids + i + 1,
@@ -208,17 +217,29 @@ static int round_steps(Session* s, int k, const mtpx_force_params* force, int32_
       RC(mtpx_force_draft(s->ctx, s->ids + i + 1, force->teacher, o + i + 1, force->rate, force->seed));
   }
   RC(mtpx_target_verify(s->ctx, s->target, s->state, s->ids, k + 1, s->logits, s->multi, nullptr));
-  RC(mtpx_accept_greedy_bf16(s->ctx, s->logits, k, s->vocab, s->ids + 1, (int32_t)o, s->out, s->out + 4,
-                             s->out + 12));
+  if (temperature > 0.0f)
+    RC(mtpx_accept_sample_bf16(s->ctx, s->logits, nullptr, k, s->vocab, s->ids + 1, temperature, seed, (uint64_t)o,
+                               (int32_t)o, s->out, s->out + 12));
+  else
+    RC(mtpx_accept_greedy_bf16(s->ctx, s->logits, k, s->vocab, s->ids + 1, (int32_t)o, s->out, s->out + 4,
+                               s->out + 12));
   RC(readback(s));
   const int n = s->host[0];
   if (n < 0 || n > k) return set_error(MTPX_ERR_STATE, "round: accept count out of range");
   RC(mtpx_target_commit(s->state, n + 1));
   if (s->drafter.ctx) {
-    if (k > 0)
+    if (k > 0) {
       RC(mtpx_drafter_finalize(s->drafter, n + 1, n ? s->ids + 1 : nullptr, n ? s->multi : nullptr, n));
-    else
+    } else {
+      // A drafted round leaves no frontier: its carry (the multi stream before the carry token)
+      // is paired with the token only by the next round's first draft step.  A serial step
+      // observes the carry token instead, so the carry's stream becomes the frontier first;
+      // otherwise the transition (carry stream, carry token) would never reach the head.
+      mtpx_drafter_info di;
+      RC(mtpx_drafter_info_get(s->drafter, &di));
+      if (!di.has_frontier) RC(mtpx_drafter_observe(s->drafter, s->ids, s->carry, 1));
       RC(mtpx_drafter_observe(s->drafter, s->ids, s->multi, 1));
+    }
   }
   RC(next_carry(s, s->multi, n));
   s->offset += n + 1;

@@ -127,6 +127,12 @@ class Context:
         rows, V = x.shape
         check(self.lib.mtpx_argmax_rows(self.h, _ptr(x), rows, V, _ptr(out)), "argmax_rows")
 
+    def top_two(self, logits, ids, values):
+        """ids int32 [rows, 2], values f32 [rows, 2]: each row's two best entries (argmax order)."""
+        rows, V = logits.shape
+        fn = self.lib.mtpx_top_two_bf16 if logits.dtype.itemsize == 2 else self.lib.mtpx_top_two
+        check(fn(self.h, _ptr(logits), rows, V, _ptr(ids), _ptr(values)), "top_two")
+
     def accept_greedy(self, logits, drafts, kv_offset, out3):
         k = drafts.numel()
         check(self.lib.mtpx_accept_greedy(self.h, _ptr(logits), k, logits.shape[1], _ptr(drafts), kv_offset,
@@ -141,10 +147,18 @@ class Context:
         check(self.lib.mtpx_force_draft(self.h, _ptr(token), _ptr(teacher), pos, p, seed), "force_draft")
 
     def accept_sample(self, tlogits, dlogits, drafts, temperature, seed, offset, kv_offset, out3):
+        """dlogits None: one-hot draft distributions at the drafts (a greedy drafter)."""
         k = drafts.numel()
         check(self.lib.mtpx_accept_sample(self.h, _ptr(tlogits), _ptr(dlogits), k, tlogits.shape[1],
                                           _ptr(drafts), temperature, seed, offset, kv_offset, _ptr(out3)),
               "accept_sample")
+
+    def accept_sample_bf16(self, tlogits, dlogits, drafts, temperature, seed, offset, kv_offset, out3,
+                           tokens_out=None):
+        k = drafts.numel()
+        check(self.lib.mtpx_accept_sample_bf16(self.h, _ptr(tlogits), _ptr(dlogits), k, tlogits.shape[1],
+                                               _ptr(drafts), temperature, seed, offset, kv_offset, _ptr(out3),
+                                               _ptr(tokens_out)), "accept_sample_bf16")
 
     def shortlist_argmax(self, x, w, s, b, gs, ids, out, sb=None):
         """out[0] = ids[argmax_j bf16(W_j . x)] over the shortlist rows (lowest position on ties)."""
@@ -639,10 +653,15 @@ class Session:
             self._teacher = teacher
             self.force = ForceParams(teacher.data_ptr(), teacher.numel(), rate, seed)
 
-    def round(self, k: int) -> list:
+    def round(self, k: int, temperature: float = 0.0, seed: int = 0) -> list:
+        """One round; temperature > 0: speculative sampling (mtpx_round_sampled) with Philox key seed."""
         n = C.c_int()
         fp = C.byref(self.force) if self.force is not None else None
-        check(self.ctx.lib.mtpx_round(self.h, k, fp, C.cast(self._tok, C.c_void_p), C.byref(n)), "round")
+        if temperature > 0:
+            check(self.ctx.lib.mtpx_round_sampled(self.h, k, fp, temperature, seed, C.cast(self._tok, C.c_void_p),
+                                                  C.byref(n)), "round_sampled")
+        else:
+            check(self.ctx.lib.mtpx_round(self.h, k, fp, C.cast(self._tok, C.c_void_p), C.byref(n)), "round")
         return list(self._tok[:n.value])
 
     def offset(self) -> int:
@@ -654,3 +673,11 @@ class Session:
         h = Handle()
         check(self.ctx.lib.mtpx_session_info(self.h, None, C.byref(h), None), "session_info")
         return _borrowed(TargetState, self.ctx, h)
+
+    def drafter_info(self) -> dict:
+        """The session drafter's counts (mtpx_drafter_info)."""
+        h = Handle()
+        check(self.ctx.lib.mtpx_session_info(self.h, None, None, C.byref(h)), "session_info")
+        i = DrafterInfo()
+        check(self.ctx.lib.mtpx_drafter_info_get(h, C.byref(i)), "drafter_info")
+        return {n: getattr(i, n) for n, _ in DrafterInfo._fields_}

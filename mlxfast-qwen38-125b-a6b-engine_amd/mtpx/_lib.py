@@ -145,6 +145,9 @@ _SIGS = {
     "mtpx_argmax_rows": (INT, [Handle, P, INT, I64, P]),
     "mtpx_accept_greedy": (INT, [Handle, P, INT, I64, P, I32, P]),
     "mtpx_accept_sample": (INT, [Handle, P, P, INT, I64, P, F32, U64, U64, I32, P]),
+    "mtpx_accept_sample_bf16": (INT, [Handle, P, P, INT, I64, P, F32, U64, U64, I32, P, P]),
+    "mtpx_top_two": (INT, [Handle, P, INT, I64, P, P]),
+    "mtpx_top_two_bf16": (INT, [Handle, P, INT, I64, P, P]),
     "mtpx_accept_greedy_bf16": (INT, [Handle, P, INT, I64, P, I32, P, P, P]),
     "mtpx_force_draft": (INT, [Handle, P, P, I64, F32, U64]),
     "mtpx_session_new": (INT, [Handle, Handle, Handle, C.POINTER(Handle)]),
@@ -152,6 +155,7 @@ _SIGS = {
     "mtpx_session_reset": (INT, [Handle]),
     "mtpx_session_prefill": (INT, [Handle, P, INT, C.POINTER(I32)]),
     "mtpx_round": (INT, [Handle, INT, C.POINTER(ForceParams), P, C.POINTER(INT)]),
+    "mtpx_round_sampled": (INT, [Handle, INT, C.POINTER(ForceParams), F32, U64, P, C.POINTER(INT)]),
     "mtpx_session_info": (INT, [Handle, C.POINTER(I64), C.POINTER(Handle), C.POINTER(Handle)]),
     "mtpx_layer_new_random": (INT, [Handle, C.POINTER(LayerConfig), U64, C.POINTER(Handle)]),
     "mtpx_layer_free": (INT, [Handle]),

@@ -727,14 +727,43 @@ void o_hc_mix(const o_bf16* w, const o_bf16* normed, const o_bf16* inj, int S, i
 /* out3 = {n, bonus token, kv index}.                                        */
 /* ======================================================================== */
 
-/* NaN ranks above every number: the first NaN of a row wins (numpy's argmax). */
+/* MLX's argmax (MLX/backend/metal/kernels/arg_reduce.metal:42-62): starting from (index 0,
+ * -inf), an element replaces the best only when strictly greater, so a NaN never wins (it
+ * compares false), equal values keep the lowest index, and a row of only -inf / NaN gives 0. */
 void o_argmax_rows(const float* x, int rows, int64_t V, int32_t* out) {
   for (int r = 0; r < rows; ++r) {
     const float* xr = x + (int64_t)r * V;
     int64_t b = 0;
-    for (int64_t v = 1; v < V && !isnan(xr[b]); ++v)
-      if (isnan(xr[v]) || xr[v] > xr[b]) b = v;
+    float bv = -INFINITY;
+    for (int64_t v = 0; v < V; ++v)
+      if (xr[v] > bv) {
+        bv = xr[v];
+        b = v;
+      }
     out[r] = (int32_t)b;
+  }
+}
+
+/* Top two of each row in the argmax order (value descending, lowest index among equal values,
+ * NaN as -inf): ids[2r] = the argmax, ids[2r+1] = the argmax of the row without it; values are
+ * the entries (NaN reported as -inf).  V >= 2. */
+void o_top2_rows(const float* x, int rows, int64_t V, int32_t* ids, float* vals) {
+  for (int r = 0; r < rows; ++r) {
+    const float* xr = x + (int64_t)r * V;
+    int64_t b[2] = {-1, -1};
+    for (int j = 0; j < 2; ++j) {
+      float bv = 0.0f;
+      for (int64_t v = 0; v < V; ++v) {
+        if (v == b[0]) continue;
+        const float xv = isnan(xr[v]) ? -INFINITY : xr[v];
+        if (b[j] < 0 || xv > bv) {
+          bv = xv;
+          b[j] = v;
+        }
+      }
+      ids[2 * r + j] = (int32_t)b[j];
+      vals[2 * r + j] = bv;
+    }
   }
 }
 
@@ -861,8 +890,8 @@ static int64_t icdf(const float* vals, int64_t V, float u) {
 
 /* Softmax at temperature: e_v = exp((l_v - max) * (1/T)); p_v = e_v * (1/Z). */
 static void row_probs(const float* l, int64_t V, float invT, float* p) {
-  float mx = l[0];
-  for (int64_t v = 1; v < V; ++v)
+  float mx = -INFINITY; /* the row's argmax value: NaN never taken */
+  for (int64_t v = 0; v < V; ++v)
     if (l[v] > mx) mx = l[v];
   for (int64_t v = 0; v < V; ++v) p[v] = o_expf((l[v] - mx) * invT);
   const float invZ = 1.0f / o_softmax_row_sum(p, V);
@@ -870,7 +899,8 @@ static void row_probs(const float* l, int64_t V, float invT, float* p) {
 }
 
 /* tlogits [k+1, V]: verify rows; dlogits [k, V]: the draft distribution that
- * proposed drafts[i] is row i.  For i = 1..k (counter {offset lo, offset hi,
+ * proposed drafts[i] is row i, or NULL: one-hot draft distributions at the
+ * drafts (a greedy drafter: p_d(v) = [v == d_i]).  For i = 1..k (counter {offset lo, offset hi,
  * i, 0}, key {seed lo, seed hi}): u = U(word0), u2 = U(word1); accept draft i
  * iff u * p_d(d_i) < p_t(d_i) (p_t from verify row i-1).  First rejection at
  * i: token = icdf(max(0, p_t - p_d), u2) over row i-1, n = i-1.  All
@@ -901,10 +931,15 @@ void o_accept_sample(const float* tlogits, const float* dlogits, int k, int64_t 
       }
       break;
     }
-    row_probs(dlogits + (int64_t)(i - 1) * V, V, invT, pd);
     const int32_t d = drafts[i - 1];
     /* a draft id outside the vocabulary is rejected */
     const int ok = d >= 0 && d < V;
+    if (dlogits) {
+      row_probs(dlogits + (int64_t)(i - 1) * V, V, invT, pd);
+    } else {
+      for (int64_t v = 0; v < V; ++v) pd[v] = 0.0f;
+      if (ok) pd[d] = 1.0f;
+    }
     if (ok && u * pd[d] < pt[d]) continue;
     n = i - 1;
     for (int64_t v = 0; v < V; ++v) pd[v] = fmaxf(pt[v] - pd[v], 0.0f);

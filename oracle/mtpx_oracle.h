@@ -115,6 +115,7 @@ void o_gdn_core(const o_gdn_geom* g, const o_bf16* proj, int S, o_bf16* conv_sta
 
 /* ---- a18, a21, a22: argmax and acceptance ------------------------------- */
 void o_argmax_rows(const float* x, int rows, int64_t V, int32_t* out);
+void o_top2_rows(const float* x, int rows, int64_t V, int32_t* ids, float* vals);
 void o_accept_greedy(const float* logits, int k, int64_t V, const int32_t* drafts,
                      int32_t kv_offset, int32_t* out3);
 void o_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]);

@@ -61,6 +61,7 @@ def _declare(L):
         "o_attn_gate": (None, [P, P, C.c_int, C.c_int, C.c_int, C.c_int, P]),
         "o_rmsnorm": (None, [P, C.c_int, C.c_int, P, F32, P]),
         "o_argmax_rows": (None, [P, C.c_int, I64, P]),
+        "o_top2_rows": (None, [P, C.c_int, I64, P, P]),
         "o_accept_greedy": (None, [P, C.c_int, I64, P, I32, P]),
         "o_philox4x32_10": (None, [P, P, P]),
         "o_uniform": (F32, [C.c_uint32]),
@@ -303,9 +304,10 @@ def hc_mix(w, normed, inj, hc):
 
 
 def shortlist_argmax(y_bf16, ids):
-    """Draft id: ids[argmax over the bf16 logits], lowest position on ties."""
-    v = bf16_to_f32(np.asarray(y_bf16, np.uint16).reshape(-1))
-    return int(np.asarray(ids, np.int32)[int(np.argmax(v))])
+    """Draft id: ids[argmax over the bf16 logits], lowest position on ties, NaN never taken
+    (MLX's argmax rule, as o_argmax_rows)."""
+    v = bf16_to_f32(np.asarray(y_bf16, np.uint16).reshape(1, -1))
+    return int(np.asarray(ids, np.int32)[int(argmax_rows(v)[0])])
 
 
 def set_threads(n: int):
@@ -337,6 +339,16 @@ def argmax_rows(x):
     return out
 
 
+def top2_rows(x):
+    """(ids int32 [rows, 2], values f32 [rows, 2]) in the argmax order."""
+    x = np.ascontiguousarray(x, np.float32)
+    rows, V = x.shape
+    ids = np.zeros((rows, 2), np.int32)
+    vals = np.zeros((rows, 2), np.float32)
+    lib().o_top2_rows(_p(x), rows, V, _p(ids), _p(vals))
+    return ids, vals
+
+
 def accept_greedy(logits, drafts, kv_offset):
     lg = np.ascontiguousarray(logits, np.float32)
     d = np.ascontiguousarray(drafts, np.int32)
@@ -359,12 +371,13 @@ def uniform(r: int) -> float:
 
 
 def accept_sample(tlogits, dlogits, drafts, temperature, seed, offset, kv_offset):
+    """out3 {n, token, kv index}; dlogits None: one-hot draft distributions at the drafts."""
     t = np.ascontiguousarray(tlogits, np.float32)
-    dl = np.ascontiguousarray(dlogits, np.float32)
+    dl = None if dlogits is None else np.ascontiguousarray(dlogits, np.float32)
     d = np.ascontiguousarray(drafts, np.int32)
     out = np.zeros(3, np.int32)
-    lib().o_accept_sample(_p(t), _p(dl), d.size, t.shape[1], _p(d), temperature, seed, offset,
-                          kv_offset, _p(out))
+    lib().o_accept_sample(_p(t), None if dl is None else _p(dl), d.size, t.shape[1], _p(d), temperature, seed,
+                          offset, kv_offset, _p(out))
     return out
 
 

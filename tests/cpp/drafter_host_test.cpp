@@ -180,6 +180,34 @@ int main() {
   EXPECT(d.finalize(1, nullptr, nullptr, 0) == DR_OK);
   EXPECT(d.cache_offset() == 9 && d.backlog_inputs() == 0 && d.committed_inputs() == 9);
 
+  // serial steps after a drafted round, as the session's depth-0 round drives them: the round left
+  // no frontier, so the carry (19, its stream 700) is observed first to make 700 the frontier,
+  // then the carry token with the verify's stream 710 pairs (700, 19) into the backlog
+  EXPECT(!d.has_frontier());
+  {
+    int32_t t = 19;
+    auto carry = rows(1, 700);
+    auto verify = rows(1, 710);
+    EXPECT(d.observe(&t, carry.data(), 1, W) == DR_OK);
+    EXPECT(d.backlog_inputs() == 0 && d.has_frontier());
+    EXPECT(d.observe(&t, verify.data(), 1, W) == DR_OK);
+  }
+  EXPECT(d.backlog_inputs() == 1 && d.committed_inputs() == 10);
+  {
+    int32_t t = 20;  // the next serial step: the frontier exists, one observation
+    auto verify = rows(1, 720);
+    EXPECT(d.observe(&t, verify.data(), 1, W) == DR_OK);
+  }
+  EXPECT(d.backlog_inputs() == 2 && d.committed_inputs() == 11);
+  {
+    int32_t t = 21;  // a drafted round again: its flush holds every serial transition and the carry
+    auto h = rows(1, 720);
+    EXPECT(d.step(&t, h.data(), &draft, multi) == DR_OK);
+  }
+  EXPECT(eq(be.calls_tok.back(), {19, 20, 21}) && eqh(be.calls_hid.back(), {700, 710, 720}));
+  EXPECT(d.finalize(1, nullptr, nullptr, 0) == DR_OK);
+  EXPECT(d.cache_offset() == 12 && d.committed_inputs() == 12);
+
   // release: every later call is refused, discard stays a no-op
   d.release();
   {

@@ -161,8 +161,8 @@ def test_argmax_rows_bit_exact(ctx):
 
 
 def test_argmax_and_accept_nan_rows(ctx):
-    """NaN ranks above every number, the first NaN of a row wins (numpy's rule): an all-NaN row
-    gives id 0, a NaN beyond the 8192-element slices of the partial pass still wins."""
+    """MLX's argmax rule: a NaN never wins (it ranks as -inf), an all-NaN row gives id 0, and NaNs
+    spread over several of the partial pass's slices do not disturb the winner of another slice."""
     V = 151936
     x = np.random.default_rng(5).standard_normal((4, V)).astype(np.float32)
     x[0, :] = np.nan
@@ -173,14 +173,64 @@ def test_argmax_and_accept_nan_rows(ctx):
     out = torch.zeros(4, dtype=torch.int32, device="cuda")
     ctx.argmax_rows(dev(x), out)
     ctx.synchronize()
-    want = [int(np.argmax(r)) for r in x]
-    assert want == [0, 70000, 9, 100000]
+    want = [int(np.argmax(np.where(np.isnan(r), -np.inf, r))) for r in x]
+    assert want[0] == 0 and want[2] == 9 and want[3] == 5 and want[1] not in (70000, 150000)
     assert list(host(out)) == want == list(O.argmax_rows(x))
     out3 = torch.zeros(3, dtype=torch.int32, device="cuda")
-    drafts = np.array([0, 70000, 9], np.int32)
+    drafts = np.array([0, want[1], 9], np.int32)
     ctx.accept_greedy(dev(x), dev(drafts), 100, out3)
     ctx.synchronize()
-    assert list(host(out3)) == list(O.accept_greedy(x, drafts, 100)) == [3, 100000, 104]
+    assert list(host(out3)) == list(O.accept_greedy(x, drafts, 100)) == [3, 5, 104]
+
+
+@pytest.mark.parametrize("V", [151936, 248320, 2])
+def test_top_two_bit_exact(ctx, V):
+    """The top-two query (cbv2MTPTopTwo) on f32 logits and on bf16 logits (many exact ties after the
+    rounding) against the oracle: ids and values bit-exact, NaN rows and ties included."""
+    print("case top two", V, flush=True)
+    r = np.random.default_rng(V)
+    x = (r.standard_normal((6, V)) * 2.0).astype(np.float32)
+    if V > 2:
+        x[0, [3, V - 1]] = 50.0
+        x[1, :] = np.nan
+        x[2, 1::2] = np.nan
+        x[3, 100000 % V] = np.inf
+    for bf in (False, True):
+        xs = O.f32_to_bf16(x) if bf else x
+        ids = torch.full((6, 2), -1, dtype=torch.int32, device="cuda")
+        vals = torch.zeros(6, 2, dtype=torch.float32, device="cuda")
+        ctx.top_two(dev(xs), ids, vals)
+        wi, wv = O.top2_rows(O.bf16_to_f32(xs) if bf else x)
+        assert np.array_equal(host(ids), wi), bf
+        assert np.array_equal(host(vals).view(np.uint32), wv.view(np.uint32)), bf
+        if V > 2:
+            assert list(wi[0]) == [3, V - 1]
+
+
+@pytest.mark.parametrize("k", [0, 1, 3, 5])
+@pytest.mark.parametrize("p", [0.3, 0.9])
+def test_accept_sample_onehot_bit_exact(ctx, k, p):
+    """One-hot draft distributions (no draft logits: a greedy drafter) on f32 logits and on their
+    bf16 roundings (the verify's output, with the committed tokens): bit-exact against the oracle
+    given the same values.  Drafts at the target argmax are accepted with probability p_t."""
+    print("case sample onehot", k, p, flush=True)
+    V = 151936
+    for seed in range(3):
+        t, _, drafts = c2_case(V, max(k, 1), p, 700 + 10 * k + int(10 * p) + seed)
+        t, drafts = t[:k + 1], drafts[:k]
+        tb = O.f32_to_bf16(t)
+        for off in (0, 4321):
+            for T in (0.7, 0.2):
+                want = O.accept_sample(t, None, drafts, T, 0xBEEF + seed, off, 512)
+                out = torch.zeros(3, dtype=torch.int32, device="cuda")
+                ctx.accept_sample(dev(t), None, dev(drafts), T, 0xBEEF + seed, off, 512, out)
+                assert list(host(out)) == list(want), ("f32", seed, off, T)
+                want = O.accept_sample(O.bf16_to_f32(tb), None, drafts, T, 0xBEEF + seed, off, 512)
+                toks = torch.full((k + 1,), -1, dtype=torch.int32, device="cuda")
+                ctx.accept_sample_bf16(dev(tb), None, dev(drafts), T, 0xBEEF + seed, off, 512, out, toks)
+                assert list(host(out)) == list(want), ("bf16", seed, off, T)
+                n = int(want[0])
+                assert list(host(toks))[:n + 1] == list(drafts[:n]) + [int(want[1])]
 
 
 @pytest.mark.parametrize("k", [1, 3, 5])

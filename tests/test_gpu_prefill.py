@@ -2,10 +2,12 @@
 batch gives every position's multi stream and the last position's logits exactly as verifying and
 committing it in windows of 8 does, and leaves the same state (the next verify is bit-equal).
 Against the oracle composition's windows at small dims (a prompt of two full windows and a tail,
-with the PLE block), against the GPU's own windowed verify path for a prompt of 300 positions
-(two prefill batches, 37 windows, the batched MoE launches) and at full width (hidden 2560, 512
-experts, hyper-connections 4 x 2560, the full PLE table, 4 layers) over a 1024-position prefix; and
-the MTP head over a batch of backlog positions (the drafter's flush) against windows of 8."""
+with the PLE block), against the GPU's own windowed verify path for a prompt of 600 positions
+(two prefill batches, 75 windows, the batched MoE launches) and at full width (hidden 2560, 512
+experts, hyper-connections 4 x 2560, the full PLE table, 4 layers): 45 positions over a
+1024-position prefix, 600 positions (the benched batch of 512, then 88), and a prompt after a
+partly committed verify window; and the MTP head over a batch of backlog positions (the drafter's
+flush) against windows of 8."""
 import numpy as np
 import pytest
 import torch
@@ -169,9 +171,14 @@ def test_prefill_two_batches_matches_windows(ctx):
 
 
 @pytest.mark.timeout(600)
-def test_prefill_full_width_matches_windows(ctx):
+@pytest.mark.parametrize("pre,n,partial", [(1024, 45, False), (400, 600, False), (300, 70, True)],
+                         ids=["45-after-1024", "600-after-400", "70-after-partial-window"])
+def test_prefill_full_width_matches_windows(ctx, pre, n, partial):
     """Full width, 4 layers at gs64 (GDN 16/48 heads, attention 24/2 x 256, 512 experts top-10, the PLE
-    block with its full table): a 45-position prompt after a 1024-position prefix."""
+    block with its full table): a 45-position prompt after a 1024-position prefix; 600 positions (a
+    batch of 512 at the benched size, then 88) after 400; and a prompt after a verify window of 5 of
+    which 3 positions were committed (the batch GDN kernel replays the committed journal steps and
+    reads the conv rows of that window)."""
     import mtpx
     from oracle.target_ref import download_target
     FULL = dict(hidden=2560, experts=512, top_k=10, expert_width=640, heads=24, kv_heads=2, head_dim=256,
@@ -189,14 +196,23 @@ def test_prefill_full_width_matches_windows(ctx):
     geoms = {i: L["gdn"]["geom"] for i, L in enumerate(ow["layers"]) if L["kind"] == 0}
     V, W = cfg["vocab"], cfg["hc"] * cfg["hidden"]
     a, b = mtpx.TargetState(ctx, t), mtpx.TargetState(ctx, t)
-    _load_prefix(a, kinds, geoms, cfg, 1024, 12)
-    _load_prefix(b, kinds, geoms, cfg, 1024, 12)
-    ids = np.random.default_rng(6).integers(0, V, 45).astype(np.int32)
-    print("case prefill full width 45", flush=True)
+    _load_prefix(a, kinds, geoms, cfg, pre, 12)
+    _load_prefix(b, kinds, geoms, cfg, pre, 12)
+    if partial:
+        first = dev(np.array([11, 12, 13, 14, 15], np.int32))
+        la, lb = empty_bf16(5, V), empty_bf16(5, V)
+        t.verify(a, first, la)
+        t.verify(b, first, lb)
+        a.commit(3)
+        b.commit(3)
+        assert np.array_equal(host(la), host(lb))
+    ids = np.random.default_rng(6 + n).integers(0, V, n).astype(np.int32)
+    print("case prefill full width", n, "after", pre, "partial", partial, flush=True)
     got_mt, got_lg = _prefill(t, a, ids, V, W)
     want_mt, want_lg = _windows(t, b, ids, V, W)
     assert np.array_equal(got_mt, want_mt)
     assert np.array_equal(got_lg, want_lg)
+    assert a.info() == b.info() == (pre + (3 if partial else 0) + n, 0)
     nxt = dev(np.array([1, 2, 3, 4], np.int32))
     la, lb = empty_bf16(4, V), empty_bf16(4, V)
     t.verify(a, nxt, la)

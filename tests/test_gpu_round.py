@@ -3,7 +3,9 @@ C ABI: the prefill's first token and the serial decode (k = 0) against the oracl
 forward; speculative decode at draft depths 1..4, with the forcing hook at rate 0.7 (drafts
 replaced by the serial sequence's tokens) and without it, emits exactly the serial greedy
 sequence (the accept/rollback invariant: speculative decode changes speed, never tokens);
-the accepted counts follow the forcing mask; refused calls."""
+the accepted counts follow the forcing mask; the drafter keeps every committed transition at
+mixed depths; the sampled round (temperature > 0) against the oracle's speculative sampling;
+refused calls."""
 import numpy as np
 import pytest
 import torch
@@ -12,7 +14,7 @@ from oracle import oracle as O
 
 pytestmark = pytest.mark.gpu
 
-from gpu_util import dev, need_gpu  # noqa: E402
+from gpu_util import dev, host, need_gpu  # noqa: E402
 
 LAYER = dict(hidden=256, experts=16, top_k=4, expert_width=128, group_size=32, heads=4, kv_heads=2, head_dim=64,
              rot_dims=16, index_dim=32, rope_theta=1e7, eps=1e-6, max_positions=96)
@@ -111,6 +113,86 @@ def test_speculative_equals_serial(model, k, rate):
     if rate > 0:
         assert sum(accepted) > 0
     s.close()
+
+
+def test_mixed_depths_keep_every_transition(model):
+    """Every committed position t > 0 gives the drafter one trusted transition (multi[t-1],
+    token[t]), whatever depth produced it: after each round the drafter holds offset - 1 of them
+    (in its head cache or its backlog).  A serial step right after a drafted round (no frontier)
+    must first pair the carry's stream with the carry token; the sequence also checks that the
+    tokens stay the serial ones."""
+    import mtpx
+    ctx, t, head, prompt = model
+    ref = serial(model)
+    teacher = np.zeros(LAYER["max_positions"], np.int32)
+    teacher[:PROMPT] = prompt
+    teacher[PROMPT:PROMPT + GEN] = ref
+    s = mtpx.Session(ctx, t, head)
+    s.set_force(dev(teacher), 0.7, 0x5EED)
+    toks = [s.prefill(dev(prompt))]
+    assert s.drafter_info()["committed_inputs"] == s.offset() - 1
+    for k in [2, 0, 0, 3, 0, 1, 0, 2, 2, 0]:
+        toks += s.round(k)
+        info = s.drafter_info()
+        print("case round mixed k", k, "offset", s.offset(), "committed", info["committed_inputs"], flush=True)
+        assert info["round_in_flight"] == 0
+        assert info["committed_inputs"] == s.offset() - 1, (k, info)
+    n = len(toks)
+    assert toks == ref[:n]
+    s.close()
+
+
+@pytest.mark.parametrize("k,T", [(0, 0.7), (2, 0.7), (3, 0.2), (2, 1e-4)])
+def test_sampled_round_matches_oracle(model, k, T):
+    """mtpx_round_sampled against its parts.  Forcing at rate 1 makes every draft the teacher's
+    token, so each round's verify inputs are known: a second target state verifies the same tokens
+    (bit-equal logits) and the oracle's speculative sampling with one-hot drafts (key = seed,
+    counter offset = the committed position) decides n and the token; the round must emit exactly
+    drafts[:n] + [token].  At a temperature near 0 every row whose maximum is unique gives its
+    argmax, so the emitted tokens are the greedy ones there."""
+    import mtpx
+    ctx, t, head, prompt = model
+    ref = serial(model)
+    teacher = np.zeros(LAYER["max_positions"], np.int32)
+    teacher[:PROMPT] = prompt
+    teacher[PROMPT:PROMPT + GEN] = ref
+    seed = 0x5A3
+    s = mtpx.Session(ctx, t, head)
+    s.set_force(dev(teacher), 1.0, 11)
+    ts = mtpx.TargetState(ctx, t)
+    carry = s.prefill(dev(prompt))
+    t.prefill(ts, dev(prompt))
+    off, emitted, accepted, unique_rows = PROMPT, 1, [], 0
+    V = TARGET["vocab"]
+    while emitted < GEN:
+        depth = min(k, GEN - emitted - 1)
+        got = s.round(depth, T, seed)
+        drafts = teacher[off + 1:off + 1 + depth].copy()
+        ids = np.array([carry] + list(drafts), np.int32)
+        lg = torch.zeros(depth + 1, V, dtype=torch.bfloat16, device="cuda")
+        t.verify(ts, dev(ids), logits=lg)
+        lf = O.bf16_to_f32(host(lg))
+        want = O.accept_sample(lf, None, drafts, T, seed, off, off)
+        n = int(want[0])
+        assert got == list(drafts[:n]) + [int(want[1])], (off, got, want)
+        if T < 1e-3:
+            for i, tok in enumerate(got):
+                row = lf[i]
+                if np.sum(row == row.max()) == 1:
+                    unique_rows += 1
+                    assert tok == int(np.argmax(row)), (off, i)
+        ts.commit(n + 1)
+        accepted.append(n)
+        carry = got[-1]
+        off += n + 1
+        emitted += n + 1
+    print("case sampled round k", k, "T", T, "accepted", accepted, flush=True)
+    assert s.offset() == off
+    if T < 1e-3:
+        assert unique_rows >= GEN // 2
+        assert sum(accepted) > 0
+    s.close()
+    ts.close()
 
 
 def test_forcing_mask_decides_acceptance(model):

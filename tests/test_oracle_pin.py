@@ -434,14 +434,167 @@ def test_sample_emits_target_distribution():
     assert chi2 < 25.0, (chi2, counts, n * pt)  # 5 dof, p ~ 1e-4
 
 
+def test_sample_onehot_drafts_emit_target_distribution():
+    """One-hot draft distributions (a greedy drafter, dlogits None): the draft d is accepted with
+    probability p_t(d) and a rejection samples p_t without d, so the first emitted token is still
+    ~ p_target whatever the draft (chi-square, drafts cycling over every id); and the one-hot rule
+    equals the general rule given a draft row whose softmax is one-hot (logit gap of 1000)."""
+    V, T = 6, 0.7
+    r = rng(19)
+    t = (r.standard_normal((2, V)) * 1.5).astype(np.float32)
+    pt = np.exp((t[0] - t[0].max()) / T); pt /= pt.sum()
+    counts = np.zeros(V)
+    acc = np.zeros(V)
+    n = 6000
+    for i in range(n):
+        d = np.array([i % V], np.int32)
+        out = O.accept_sample(t, None, d, T, 4242, i, 0)
+        first = d[0] if out[0] == 1 else out[1]
+        if out[0] == 1:
+            acc[d[0]] += 1
+        else:
+            assert out[1] != d[0]  # a rejected draft is never the resample
+        counts[first] += 1
+    chi2 = ((counts - n * pt) ** 2 / (n * pt)).sum()
+    assert chi2 < 25.0, (chi2, counts, n * pt)
+    # acceptance rate of draft v = p_t(v) (each id drafted n / V times)
+    assert np.all(np.abs(acc / (n / V) - pt) < 5 * np.sqrt(pt * (1 - pt) / (n / V)) + 1e-9)
+    for i in range(200):
+        d = np.array([i % V, (i * 7) % V], np.int32)
+        t3 = (r.standard_normal((3, V)) * 1.5).astype(np.float32)
+        onehot = np.zeros((2, V), np.float32)
+        onehot[0, d[0]] = onehot[1, d[1]] = 1000.0
+        assert list(O.accept_sample(t3, None, d, T, 99, i, 5)) == list(O.accept_sample(t3, onehot, d, T, 99, i, 5))
+
+
 def test_softmax_row_sum_close_to_fsum():
     e = rng(16).random(151936).astype(np.float32)
     assert abs(O.softmax_row_sum(e) - math.fsum(e.astype(np.float64))) <= 1e-6 * e.sum()
 
 
-def test_argmax_nan_rule_matches_numpy():
-    x = np.array([[1.0, np.nan, 3.0, np.nan], [np.nan] * 4, [-np.inf] * 4, [2.0, 5.0, 5.0, -1.0]], np.float32)
+def test_argmax_nan_rule_matches_mlx():
+    """MLX's argmax (arg_reduce.metal:42-62): start at (index 0, -inf), take a value only when it is
+    strictly greater.  Restated independently as numpy's first-maximum argmax over the row with
+    every NaN replaced by -inf; known answers for the NaN / -inf corners."""
+    x = np.array([[1.0, np.nan, 3.0, np.nan], [np.nan] * 4, [-np.inf] * 4, [2.0, 5.0, 5.0, -1.0],
+                  [np.nan, -np.inf, -np.inf, -np.inf], [-np.inf, np.nan, -5.0, -5.0], [np.nan, 7.0, np.inf, np.inf]],
+                 np.float32)
     got = O.argmax_rows(x)
-    assert list(got) == [int(np.argmax(r)) for r in x] == [1, 0, 0, 1]
+    assert list(got) == [int(np.argmax(np.where(np.isnan(r), -np.inf, r))) for r in x] == [2, 0, 0, 1, 0, 2, 2]
+    big = rng(17).standard_normal((3, 5000)).astype(np.float32)
+    big[0, rng(18).integers(0, 5000, 400)] = np.nan
+    big[1, :] = np.nan
+    big[2, 4999] = np.nan
+    assert list(O.argmax_rows(big)) == [int(np.argmax(np.where(np.isnan(r), -np.inf, r))) for r in big]
     out = O.accept_greedy(x[1:3].copy(), np.array([0], np.int32), 10)
     assert list(out) == [1, 0, 12]  # row 0 all NaN: argmax 0 == draft 0 accepted; bonus row 1 -> 0
+
+
+def _top2_lexsort(x):
+    """Independent restatement: sort each row by (value desc with NaN as -inf, index asc)."""
+    ids, vals = [], []
+    for r in x:
+        v = np.where(np.isnan(r), -np.inf, r)
+        order = np.lexsort((np.arange(v.size), -v.astype(np.float64)))
+        ids.append(order[:2])
+        vals.append(v[order[:2]])
+    return np.array(ids, np.int32), np.array(vals, np.float32)
+
+
+def test_top2_rows_matches_lexsort():
+    """Top two per row against a lexsort of (value desc, index asc), with ties (equal leaders, equal
+    runners-up), NaNs, infinities and rows of only NaN / -inf; the first id is the argmax."""
+    r = rng(21)
+    x = r.standard_normal((12, 3000)).astype(np.float32)
+    x[0, [5, 900]] = 9.0                       # tied leaders: 5 then 900
+    x[1, 17] = 9.0; x[1, [40, 2999]] = 8.0     # tied runners-up: 40
+    x[2, :] = np.nan
+    x[3, :] = -np.inf
+    x[4, ::3] = np.nan
+    x[5, 7] = np.inf; x[5, 8] = np.nan
+    x[6] = np.round(x[6])                      # many exact ties
+    x[7, :] = 0.0
+    got_i, got_v = O.top2_rows(x)
+    want_i, want_v = _top2_lexsort(x)
+    assert np.array_equal(got_i, want_i) and np.array_equal(got_v, want_v)
+    assert list(got_i[:, 0]) == list(O.argmax_rows(x))
+    assert list(got_i[0]) == [5, 900] and list(got_i[1]) == [17, 40] and list(got_i[2]) == [0, 1]
+
+
+# ---------------------------------------------------------------------------- mlx_cpu mode (o_qmm_t_bf16)
+def _pack_q(q):
+    """q uint8 [N, K] in [0, 15] -> MLX 4-bit words [N, K/8] (element k at bits 4*(k%8))."""
+    q = np.asarray(q, np.uint32)
+    N, K = q.shape
+    w = np.zeros((N, K // 8), np.uint32)
+    for j in range(8):
+        w |= q[:, j::8] << np.uint32(4 * j)
+    return w
+
+
+def test_qmm_t_bf16_integer_dot_is_exact():
+    """Integer scales, biases, nibbles and activations whose running sums stay within 256 in
+    magnitude: every bf16 rounding of MLX's _qmm_t is exact, so the result is the integer dot of
+    the dequantised rows.  Four groups of 32 with different (scale, bias) and a 2 x 3 output pin
+    the nibble order, the group indexing and the operand roles."""
+    r = rng(41)
+    M, N, K, gs = 2, 3, 128, 32
+    q = r.integers(0, 16, (N, K))
+    s = r.choice([1.0, 2.0], (N, K // gs)).astype(np.float32)
+    b = r.choice([-8.0, -4.0, 0.0, 3.0], (N, K // gs)).astype(np.float32)
+    wdq = np.repeat(s, gs, 1) * q + np.repeat(b, gs, 1)
+    while True:
+        x = (r.integers(-1, 2, (M, K)) * (r.random((M, K)) < 0.15)).astype(np.float32)
+        run = np.cumsum(x[:, None, :] * wdq[None, :, :], axis=2)
+        if np.abs(run).max() <= 256 and np.abs(run[..., -1]).min() > 0:
+            break
+    got = f32(O.qmm_t_bf16(_pack_q(q), bf16(s), bf16(b), gs, bf16(x)))
+    assert np.array_equal(got, x @ wdq.T)
+
+
+def test_qmm_t_bf16_running_sum_saturates_in_bf16():
+    """256 then +1 per element: in bf16, 256 + 1 = 257 rounds (to even) back to 256, so MLX's bf16
+    running sum stays at 256; a float accumulation would return 256 + 31 = 287."""
+    gs, K = 32, 32
+    q = np.zeros((1, K), np.int64)
+    q[0, 0] = 15  # w = 1*15 + 1 = 16 at element 0, w = 1 elsewhere
+    x = np.ones((1, K), np.float32)
+    x[0, 0] = 16.0
+    got = f32(O.qmm_t_bf16(_pack_q(q), bf16([[1.0]]), bf16([[1.0]]), gs, bf16(x)))
+    assert got[0, 0] == 256.0
+    # the same terms in the other order: 31 ones reach 31 exactly, then + 256 = 287 -> bf16 288
+    q2, x2 = q[:, ::-1].copy(), x[:, ::-1].copy()
+    got2 = f32(O.qmm_t_bf16(_pack_q(q2), bf16([[1.0]]), bf16([[1.0]]), gs, bf16(x2)))
+    assert got2[0, 0] == 288.0
+
+
+def test_qmm_t_bf16_matches_torch_bf16_ops_and_float64_bound():
+    """Random operands: equal to the same sequence of operations in torch's own bf16 arithmetic
+    (each op computed in float and rounded to bf16 by torch, an implementation independent of the
+    oracle's rounding), and within the bf16 accumulation bound of the float64 dot:
+    |err| <= (K + 2) * 2^-8 * sum |x * w|."""
+    import torch
+
+    r = rng(42)
+    M, N, K, gs = 3, 5, 128, 64
+    q = r.integers(0, 16, (N, K))
+    s = bf16(r.uniform(0.001, 0.02, (N, K // gs)))
+    b = bf16(r.uniform(-0.1, 0.0, (N, K // gs)))
+    x = bf16(r.standard_normal((M, K)))
+    got = f32(O.qmm_t_bf16(_pack_q(q), s, b, gs, x))
+
+    def tb(a):
+        return torch.from_numpy(np.ascontiguousarray(f32(a))).to(torch.bfloat16)
+
+    st, bt, xt = tb(s), tb(b), tb(x)
+    qt = torch.from_numpy(q.astype(np.float32)).to(torch.bfloat16)
+    w = st.repeat_interleave(gs, 1) * qt + bt.repeat_interleave(gs, 1)  # bf16 ops: rounded each
+    acc = torch.zeros(M, N, dtype=torch.bfloat16)
+    for k in range(K):
+        acc = acc + xt[:, k:k + 1] * w[None, :, k]
+    assert np.array_equal(got, acc.float().numpy())
+    wf = w.double().numpy()
+    xf = f32(x).astype(np.float64)
+    exact = xf @ wf.T
+    bound = (K + 2) * 2.0 ** -8 * (np.abs(xf) @ np.abs(wf).T)
+    assert np.all(np.abs(got - exact) <= bound)

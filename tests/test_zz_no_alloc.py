@@ -62,3 +62,28 @@ def test_noalloc_refuses_windows_past_the_scratch():
     with pytest.raises(mtpx.MtpxError, match="scratch"):
         ctx.moe_forward_noalloc(w, x, y)
     ctx.close()
+
+
+def test_noalloc_scratch_belongs_to_one_context():
+    """The device's scratch array serves one context at a time: a second context on the same GPU is
+    refused (MTPX_ERR_STATE) while the first one lives, and gets it once the first is freed.  A
+    refused call launches nothing; mtpx_last_moe_bytes does not count allocation-free calls."""
+    need_gpu()
+    import mtpx
+    a, b = mtpx.Context(0), mtpx.Context(0)
+    layer = mtpx.DecoderLayer(b, mtpx.LayerConfig(**dict(SMALL, group_size=32)), seed=73)  # outlives a
+    mw = layer.weights().moe
+    x = dev(rand_bf16(np.random.default_rng(74), (2, SMALL["hidden"])))
+    print("case noalloc two contexts", flush=True)
+    want = _run(a, a.moe_forward, mw, x, SMALL["top_k"])
+    assert _run(a, a.moe_forward_noalloc, mw, x, SMALL["top_k"])[3] == want[3]
+    with pytest.raises(mtpx.MtpxError, match="another context"):
+        _run(b, b.moe_forward_noalloc, mw, x, SMALL["top_k"])
+    with pytest.raises(mtpx.MtpxError, match="allocation-free"):
+        a.last_moe_bytes()
+    a.close()
+    got = _run(b, b.moe_forward_noalloc, mw, x, SMALL["top_k"])
+    for u, v in zip(got[:3], want[:3]):
+        assert np.array_equal(u, v)
+    layer.close()
+    b.close()

@@ -280,10 +280,9 @@ def cpu_layer_times(target, lc, tc, widths, kinds, T0, runs=(("port", 1, 6.0),))
         try:
             for M in widths:
                 sW, xh, ids = inputs[M]
-                tg = ta = th = tp = 0.0
-                n = 0
+                samples = []
                 t0 = time.perf_counter()
-                while n == 0 or time.perf_counter() - t0 < seconds / len(widths):
+                while not samples or time.perf_counter() - t0 < seconds / len(widths):
                     a = time.perf_counter()
                     layer_step(Lg, True, sW)
                     b = time.perf_counter()
@@ -295,8 +294,9 @@ def cpu_layer_times(target, lc, tc, widths, kinds, T0, runs=(("port", 1, 6.0),))
                         O.ple_forward(ple, dict(tc["ple"]), sW, ids, ple_conv,
                                       ids[:2] if M >= 2 else np.r_[ids, ids])
                     e = time.perf_counter()
-                    tg, ta, th, tp, n = tg + b - a, ta + c - b, th + d - c, tp + e - d, n + 1
-                times[M], iters[M] = (tg / n, ta / n, th / n, tp / n), n
+                    samples.append((b - a, c - b, d - c, e - d))
+                # median of each part over the iterations that fit the bound (at least one)
+                times[M], iters[M] = tuple(float(v) for v in np.median(np.array(samples), axis=0)), len(samples)
         finally:
             undo()
         all_times[(mode, threads)], all_iters[(mode, threads)] = times, iters
@@ -341,13 +341,15 @@ def cpu_baseline_e2e(target, lc, tc, kinds, k, tokens_per_round, shortlist_rows,
     """CPU baseline of MTP speculative decode at draft depth k, one round = k draft steps + a verify of
     k+1 tokens; a draft step = one attention layer with its mixers and MoE at one token + the shortlist
     GEMV (lm_head rows scaled); the verify = the sampled GDN and attention layers scaled to the stack +
-    lm_head + PLE.  Timed in the oracle's int24 arithmetic (port) on 1 thread and on all host threads,
-    and with MLX's CPU _qmm_t (bf16 accumulation, mlx_cpu) on all host threads (its 1-thread time is
-    one op per stream worker, not run: about threads x longer); the headline entry is the fastest."""
+    lm_head + PLE.  Timed in the oracle's int24 arithmetic (port) and with MLX's CPU _qmm_t (bf16
+    accumulation, mlx_cpu), each on 1 thread (MLX runs one op at a time on its stream worker) and on all
+    host threads; the headline entry is the fastest.  Time-bounded: about 4 s per (mode, threads), split
+    over the two widths, each part the median of the iterations that fit (at least one, after one
+    untimed call that fetches the routed experts); the iteration counts are reported."""
     n_gdn, n_attn = kinds.count(0), kinds.count(1)
     ncpu, nav, model = _cpu_info()
     th = cpu_threads_all()
-    runs = (("port", 1, 4.0), ("port", th, 4.0), ("mlx_cpu", th, 4.0))
+    runs = (("port", 1, 4.0), ("port", th, 4.0), ("mlx_cpu", 1, 4.0), ("mlx_cpu", th, 4.0))
     t0 = time.perf_counter()
     all_times, rows, all_iters = cpu_layer_times(target, lc, tc, sorted({1, k + 1}), kinds, T0, runs=runs)
     entries = []
@@ -368,7 +370,8 @@ def cpu_baseline_e2e(target, lc, tc, kinds, k, tokens_per_round, shortlist_rows,
                        f"{shortlist_rows} shortlist rows) + a verify of {k + 1} tokens ({n_gdn} GDN + {n_attn} "
                        f"attention layers scaled from one of each, lm_head from 16384 rows, PLE); mode "
                        f"{best['mode']} on {best['threads']} threads; host: {model}, {ncpu} CPUs "
-                       f"({nav} available to this process); {time.perf_counter() - t0:.0f} s of sampling",
+                       f"({nav} available to this process); {time.perf_counter() - t0:.0f} s of sampling, "
+                       f"time-bounded (about 4 s per mode), each part the median of the iterations that fit",
                 modes=entries, cpu_model=model, nproc=ncpu)
 
 
@@ -491,6 +494,70 @@ def serial_token_bytes(lc, tc, gs):
     return b
 
 
+FORCE_SEED = 0x5EED0009
+
+
+def forcing_mask(ctx, prompt, gen, p, seed):
+    """The forcing hook's decision at every position up to prompt + gen + 8, read back through the hook
+    itself (a scratch token per position, one readback): True where the draft takes the teacher's token."""
+    import numpy as np
+    import torch
+    n = prompt + gen + 8
+    mark = torch.full((n,), -5, dtype=torch.int32, device="cuda")
+    tok = torch.zeros(n, dtype=torch.int32, device="cuda")
+    for pos in range(prompt, n):
+        ctx.force_draft(tok[pos:pos + 1], mark, pos, p, seed)
+    return tok.cpu().numpy() == -5
+
+
+def rounds_from_mask(mask, prompt, gen, k):
+    """Rounds of depth k that emit gen tokens (the prefill's first one included) when exactly the
+    forced drafts are accepted: each round accepts the run of forced positions after its carry."""
+    off, emitted, rounds = prompt, 1, 0
+    while emitted < gen:
+        d = min(k, gen - emitted - 1)
+        n = 0
+        while n < d and mask[off + 1 + n]:
+            n += 1
+        emitted, off, rounds = emitted + n + 1, off + n + 1, rounds + 1
+    return rounds
+
+
+def headline_runs(args, mtpx, ctx, target, head, prompt, teacher, ref, k):
+    """The headline: W warmup and then exactly K timed config-5 decodes at depth k (a step = one decode of
+    gen - 1 tokens after the prompt), each in its own session prefilled beforehand (untimed), the K
+    timed decodes back to back between two device synchronisations; every decode must emit the serial
+    sequence.  -> (seconds of the K decodes, per-decode seconds, rounds per decode)."""
+    import numpy as np
+    import torch
+    W, K = args.warmup, args.steps
+    sessions = []
+    for _ in range(W + K):
+        s = mtpx.Session(ctx, target, head)
+        first = s.prefill(prompt)
+        s.set_force(teacher, args.accept_rate, FORCE_SEED)
+        sessions.append((s, first))
+    for s, first in sessions[:W]:
+        toks, _, _ = generate(s, first, k, args.gen)
+        assert toks == ref, "warmup decode emitted another sequence than the serial decode"
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    per, rounds, outs = [], [], []
+    for s, first in sessions[W:]:
+        a = time.perf_counter()
+        toks, times, _ = generate(s, first, k, args.gen)
+        per.append(time.perf_counter() - a)
+        rounds.append(len(times))
+        outs.append(toks)
+    torch.cuda.synchronize()
+    total = time.perf_counter() - t0
+    for s, _ in sessions:
+        s.close()
+    if any(o != ref for o in outs):
+        raise SystemExit("a timed decode emitted another sequence than the serial decode")
+    return total, per, rounds
+
+
 def decode_sweep(args, mtpx, ctx, target, head, lc, tc, depths, gs):
     """Config 5 at group size gs: the prompt, a serial greedy decode of --gen tokens (the teacher of the
     forcing hook and the reference sequence), then speculative decode at each depth with forced acceptance
@@ -514,6 +581,11 @@ def decode_sweep(args, mtpx, ctx, target, head, lc, tc, depths, gs):
     teacher[args.prompt:args.prompt + args.gen] = torch.tensor(ref, dtype=torch.int32)
     teacher = teacher.cuda()
     p = args.accept_rate
+    mask = forcing_mask(ctx, args.prompt, args.gen, p, FORCE_SEED)
+    drafted = mask[args.prompt + 1:args.prompt + args.gen]
+    forcing = dict(rate=p, realized_rate=round(float(np.mean(drafted)), 4), positions=int(drafted.size),
+                   note="share of the generated positions whose draft the seeded mask forces to the serial token")
+    log(f"gs{gs} forcing mask: {forcing}")
     res = {}
     warm = []  # the prompt again for every depth: prefill times after the first (warm workspace)
     for k in depths:
@@ -521,7 +593,7 @@ def decode_sweep(args, mtpx, ctx, target, head, lc, tc, depths, gs):
         t1 = time.perf_counter()
         f2 = sess.prefill(prompt)
         warm.append(time.perf_counter() - t1)
-        sess.set_force(teacher, p, 0x5EED0009)
+        sess.set_force(teacher, p, FORCE_SEED)
         toks, times, acc = generate(sess, f2, k, args.gen)
         same = toks == ref
         full = [t for t, a in zip(times, acc)]
@@ -531,6 +603,7 @@ def decode_sweep(args, mtpx, ctx, target, head, lc, tc, depths, gs):
                  mean_accepted=round(float(np.mean(acc)), 3),
                  tokens_per_round=round((args.gen - 1) / len(times), 3),
                  expected_tokens_per_round=round(sum(p ** i for i in range(k + 1)), 4),
+                 tokens_per_round_from_mask=round((args.gen - 1) / rounds_from_mask(mask, args.prompt, args.gen, k), 3),
                  greedy_identical_to_serial=bool(same))
         log(f"gs{gs} depth {k}: {r}")
         if not same:
@@ -540,7 +613,7 @@ def decode_sweep(args, mtpx, ctx, target, head, lc, tc, depths, gs):
     prefill = dict(first_ms=round(prefill_s * 1e3, 1), warm_ms_median=round(1e3 * float(np.median(warm)), 1))
     prefill["tok_s"] = round(args.prompt / (prefill["warm_ms_median"] / 1e3), 1)
     log(f"gs{gs} prefill: {prefill}")
-    return sess, first, prompt, serial, res, prefill
+    return sess, first, prompt, serial, res, prefill, dict(teacher=teacher, ref=ref, forcing=forcing)
 
 
 def run_full(args, out):
@@ -622,19 +695,26 @@ def run_full(args, out):
         return out
 
     # ---- config 5: 1024-token prompt + 1024 generated tokens, depths swept, forced acceptance at p
-    sess, first, prompt, serial, sweep, prefill = decode_sweep(args, mtpx, ctx, target, head, lc, tc, args.depths, gs)
+    sess, first, prompt, serial, sweep, prefill, dd = decode_sweep(args, mtpx, ctx, target, head, lc, tc, args.depths,
+                                                                   gs)
     best = max(sweep, key=lambda d: sweep[d]["tok_s"])
     fin = sweep[best]
+    sess.close()
+    hl_s, hl_per, hl_rounds = headline_runs(args, mtpx, ctx, target, head, prompt, dd["teacher"], dd["ref"], best)
+    hl = dict(tok_s=round(args.steps * (args.gen - 1) / hl_s, 2), steps=args.steps, warmup=args.warmup,
+              seconds=round(hl_s, 3), ms_per_decode_mean=round(1e3 * hl_s / args.steps, 2),
+              tok_s_per_decode_min=round((args.gen - 1) / max(hl_per), 2),
+              tok_s_per_decode_max=round((args.gen - 1) / min(hl_per), 2), rounds_per_decode=sorted(set(hl_rounds)))
+    log(f"gs{gs} headline at depth {best}: {hl}")
     tok_bytes = serial_token_bytes(lc, tc, gs)
     draft_ms = {k: round((r["ms_per_round_median"] - widths[k + 1]) / k, 4) for k, r in sweep.items() if k + 1 in widths}
-    sess.close()
     gs32 = None
     if args.gs32_line and gs != 32:
         target.close()
         head.close()
         torch.cuda.synchronize()
         t32, h32, lc32, tc32 = build_model(mtpx, ctx, args, 32)
-        s32, _, _, serial32, sw32, pf32 = decode_sweep(args, mtpx, ctx, t32, h32, lc32, tc32, [best], 32)
+        s32, _, _, serial32, sw32, pf32, _ = decode_sweep(args, mtpx, ctx, t32, h32, lc32, tc32, [best], 32)
         r32 = sw32[best]
         b32 = serial_token_bytes(lc32, tc32, 32)
         gs32 = dict(r32, draft_depth=best, serial_tok_s=serial32["tok_s"], prefill=pf32,
@@ -645,33 +725,38 @@ def run_full(args, out):
         h32.close()
         target = None
     out.update({
-        "value": fin["tok_s"],
-        "ms_per_step": fin["ms_per_round_mean"],
-        "steps": fin["rounds"],
-        "warmup": 0,
+        "value": hl["tok_s"],
+        "ms_per_step": hl["ms_per_decode_mean"],
+        "steps": args.steps,
+        "warmup": args.warmup,
         "config": dict(base_cfg, workload=(
             f"BASELINE config 5: single-stream MTP speculative decode on the full-depth random-init 125B-A6B "
             f"target ({args.layers} layers: {n_gdn} GDN + {n_attn} attention, hyper-connection mixers, 512-expert "
             f"top-10 + shared MoE, hidden 2560, vocab 248320, gs{gs}, weights resident in HBM) with the MTP head "
             f"(attention + MoE, 98584-row shortlist; {ple_note}). A {args.prompt}-token random prompt is processed "
-            f"(the target prefill, observed by the drafter), then {args.gen} tokens are generated greedily: the step is one round (k "
+            f"(the target prefill, observed by the drafter), then {args.gen} tokens are generated greedily in rounds (k "
             f"drafter steps, a verify of k+1 tokens, the on-device greedy accept read back once, target commit, "
             f"drafter finalize). Acceptance is forced at p={args.accept_rate}: each drafted position takes the "
             f"serial greedy sequence's token with probability p (seeded per position); every depth emits "
-            f"exactly the serial sequence. Draft depth {best} = the best of {list(args.depths)}; value = "
-            f"realized tokens/s of the {args.gen - 1} round-generated tokens over all {fin['rounds']} rounds "
-            f"(steps = rounds; ms_per_step = mean round)"),
+            f"exactly the serial sequence. Draft depth {best} = the best of {list(args.depths)} in a sweep of "
+            f"one decode per depth. A step = one decode of the {args.gen - 1} round-generated tokens at that "
+            f"depth ({fin['rounds']} rounds) in a session whose prompt was prefilled beforehand (untimed); "
+            f"{args.warmup} warmup decodes, then {args.steps} timed decodes back to back between two device "
+            f"synchronisations; value = {args.steps} x {args.gen - 1} tokens / their seconds; ms_per_step = "
+            f"mean decode"),
             draft_depth=best, accept_rate=args.accept_rate, generated_tokens=args.gen,
             mean_accepted=fin["mean_accepted"], tokens_per_round=fin["tokens_per_round"],
             expected_tokens_per_round=fin["expected_tokens_per_round"],
-            ms_per_round_median=fin["ms_per_round_median"]),
+            ms_per_round_median=fin["ms_per_round_median"], rounds_per_decode=fin["rounds"]),
         "decode": {
+            "headline": hl,
+            "forcing": dd["forcing"],
             "depth_sweep": {str(d): r for d, r in sweep.items()},
             "serial_decode": serial,
             "prefill": prefill,
             "draft_step_ms_by_depth": draft_ms,
             "bytes_per_serial_token": tok_bytes,
-            "roofline_frac": round(fin["tok_s"] * tok_bytes / 1e9 / HBM_PEAK_GBS, 4),
+            "roofline_frac": round(hl["tok_s"] * tok_bytes / 1e9 / HBM_PEAK_GBS, 4),
             "gs32": gs32,
         },
         "verify": verify,

@@ -121,10 +121,18 @@ typedef struct {
   /* packed scale/bias rows of the six matrices above (all six, or all NULL) */
   const uint32_t* gate_sb; const uint32_t* up_sb; const uint32_t* down_sb;
   const uint32_t* sh_gate_sb; const uint32_t* sh_up_sb; const uint32_t* sh_down_sb;
+  /* The shared-expert gate as an affine-4-bit row [1, H] (the checkpoint's mlp.shared_expert_gate,
+   * Sources/MLXFastTransform/Qwen4ExpCheckpointValidation.swift:383-385): when shared_gate_w is set
+   * it replaces the bf16 row above (which may then be NULL) and the gate is the q4 GEMV of that row,
+   * rounded to bf16 like any GEMV output (the route's gate of Runner/FastModel/TrackFastMoE.swift:780-800);
+   * shared_gate_sb: its packed scale/bias row or NULL. */
+  const uint32_t* shared_gate_w; const uint16_t* shared_gate_s; const uint16_t* shared_gate_b;
+  const uint32_t* shared_gate_sb;
 } mtpx_moe_weights;
 
 /* y[M, H] = MoE(x[M, H]) for a decode/verify window of M <= 8 tokens: router
- * GEMV (bf16 weight, f32 activation), top-k (value desc, index asc) + softmax,
+ * GEMV (bf16 weight, f32 activation; the shared-expert gate as one more bf16 row, or as the
+ * q4 GEMV of shared_gate_w), top-k (value desc, index asc) + softmax,
  * expert-grouped gate|up + SwiGLU, down + rank-ordered combine + sigmoid-gated
  * shared expert.  Optional outputs (NULL to skip): idx int32 [M, K], w f32
  * [M, K], logits f32 [M, E], n_unique int32 [1] (distinct routed experts).
@@ -561,7 +569,8 @@ int mtpx_target_new_random(mtpx_ctx ctx, const mtpx_target_config* cfg, uint64_t
  * norms attn_norm/post_norm unused).  The library adds only: packed scale/bias rows when pack_sb != 0
  * and the caller gave none (else the kernels read the checkpoint's scales/biases), RoPE tables when
  * rope_cos/rope_sin are NULL (rows max_positions), and the n-gram table's head sizes and offsets,
- * which follow from the config (the table must hold their sum of rows; the multipliers are the
+ * which follow from the config (the table must hold at least their sum of rows -- a checkpoint pads it to
+ * whole shards, and rows past the sum are never read; the multipliers are the
  * caller's).  gdn.neg_exp_alog is -exp(A_log) as f32.  A missing tensor: MTPX_ERR_ARG. */
 int mtpx_target_adopt(mtpx_ctx ctx, const mtpx_target_config* cfg, const mtpx_target_weights* weights,
                       const mtpx_target_layer_weights* layers, int pack_sb, mtpx_target* out);
@@ -652,6 +661,54 @@ int mtpx_round_sampled(mtpx_session s, int k, const mtpx_force_params* force, fl
                        int32_t* tokens, int* n_tokens);
 /* Committed offset; the session's target state and drafter (owned by the session). */
 int mtpx_session_info(mtpx_session s, int64_t* offset, mtpx_target_state* state, mtpx_drafter* drafter);
+
+/* ---- safetensors checkpoints -------------------------------------------------------------------
+ * The header reader of Sources/MLXFastCore/Safetensors.swift:75-176 (Safetensors.readHeader): an
+ * 8-byte little-endian header length (0 and lengths above 100,000,000 bytes or past the file refused),
+ * a JSON object of tensors {dtype, shape, data_offsets} and an optional "__metadata__" string map;
+ * offsets within the data section.  Entries are listed in name order; the data is read from a
+ * read-only mapping of the file.  Malformed files are refused with MTPX_ERR_ARG and the reference's
+ * messages. */
+typedef struct mtpx_st_ { void* ctx; } mtpx_st;
+int mtpx_st_open(const char* path, mtpx_st* out);
+int mtpx_st_free(mtpx_st st);
+int mtpx_st_count(mtpx_st st, int64_t* n);
+/* Entry i (name order): name, dtype ("BF16", "U32", "I64", ...), shape [ndim] and byte count (pointers
+ * valid until mtpx_st_free; any may be NULL). */
+int mtpx_st_tensor(mtpx_st st, int64_t i, const char** name, const char** dtype, int* ndim, const int64_t** shape,
+                   int64_t* nbytes);
+/* The entry index of `name` (MTPX_ERR_ARG and -1 if absent). */
+int mtpx_st_find(mtpx_st st, const char* name, int64_t* i);
+/* A metadata value, or *value = NULL if the key is absent. */
+int mtpx_st_metadata(mtpx_st st, const char* key, const char** value);
+/* Copy entry i's bytes to host memory (nbytes must equal its byte count). */
+int mtpx_st_read(mtpx_st st, int64_t i, void* dst, int64_t nbytes);
+
+/* A checkpoint: the given safetensors files (a directory stands for every *.safetensors file in it), one
+ * tensor name space (a name in two files is refused). */
+typedef struct mtpx_checkpoint_ { void* ctx; } mtpx_checkpoint;
+int mtpx_checkpoint_open(const char* const* paths, int n, mtpx_checkpoint* out);
+int mtpx_checkpoint_free(mtpx_checkpoint ck);
+int mtpx_checkpoint_count(mtpx_checkpoint ck, int64_t* n);
+/* A target from an MLX affine-4-bit checkpoint of this family (the tensor inventory of
+ * Sources/MLXFastTransform/Qwen4ExpCheckpointValidation.swift:312-510; names under `prefix`, NULL =
+ * "language_model."): every tensor's dtype and shape is checked against cfg, copied to the device and
+ * transformed as the reference's binding does (Runner/FastModel/TrackFastModel.swift:365-575: norm scale
+ * = bf16(hc_norm.weight * 1/hc); GDN in-projection rows in_proj_qkv | z | b | a; neg_exp_alog =
+ * -exp(float(A_log)); q_proj rows regrouped as every head's query, then every head's gate, followed by
+ * k_proj, v_proj and the last index_dim rows of indexer.index_qk_proj; the shared-expert gate as its q4
+ * row; the PLE table as its shards' rows in order, with the checkpoint's layer_multipliers, and its
+ * ngram_heads_vocab_sizes / offsets checked against the config's), then mtpx_target_adopt (pack_sb as
+ * there).  The target owns the device copies.  Replaces the runner's module adoption
+ * (Runner/Qwen4ExpRunner.swift:135-229) over mlx-swift-lm's loader. */
+int mtpx_target_load(mtpx_ctx ctx, const mtpx_target_config* cfg, mtpx_checkpoint ck, const char* prefix,
+                     int pack_sb, mtpx_target* out);
+/* The checkpoint's embedded MTP head (prefix + "mtp.": pre_fc_norm_embedding/hidden, fc_embedding/hidden,
+ * the final mixer, layers.0 attention + MoE with its two mixers; adoptMTPHead,
+ * Runner/Qwen4ExpRunner.swift:324-342) over `target`: the head embeds with the target's embed_tokens and
+ * its shortlist rows are copies of the target's lm_head rows; the target must outlive the head. */
+int mtpx_head_load(mtpx_ctx ctx, const mtpx_head_config* cfg, mtpx_checkpoint ck, mtpx_target target,
+                   const char* prefix, int pack_sb, mtpx_head* out);
 
 /* ---- per-kernel timing (replaces TrackFastProfile, Runner/FastModel/TrackFastWeights.swift:81-98) ----
  * With profiling on, every launch the library issues is bracketed by HIP events

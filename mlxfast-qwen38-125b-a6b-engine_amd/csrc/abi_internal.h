@@ -2,6 +2,8 @@
 #pragma once
 #include <hip/hip_runtime.h>
 
+#include <vector>
+
 #include "../../include/mtpx.h"
 
 namespace mtpx {
@@ -12,4 +14,9 @@ int set_error(int code, const char* msg);
 // vocab and multi-stream width (hc * hidden) of a target; hc * hidden of a head.
 void target_dims(mtpx_target t, int64_t* vocab, int* width);
 int head_width(mtpx_head h);
+// Device buffers a target / head frees with itself (the checkpoint loader's copies).
+void target_own(mtpx_target t, void* p);
+void head_own(mtpx_head h, void* p);
+// The drafter's shortlist ids of a head configuration (ascending).
+std::vector<int32_t> head_shortlist_ids(const mtpx_head_config* cfg);
 }  // namespace mtpx

@@ -29,6 +29,8 @@
 // last-arriver ticket), :780-911 (route), :1192-1404 (gate|up+act),
 // :1412-1576 (down+combine), :2246-2310 (router GEMV),
 // FM/TrackFastKernels2.swift:21-58,512-544 (sigmoid, colsum fold, combine).
+#include <algorithm>
+
 #include "qrows.h"
 
 namespace mtpx {
@@ -207,9 +209,40 @@ __device__ void route_body(const MoeArgs& a) {
 // block) and take no ticket.
 constexpr int ROUTER_IT = 8;  // H <= 8 * 64 * 8
 
+// The shared-expert gate as a q4 row (GL lanes per token, the q4 GEMV's lane rule for K = H): the
+// workgroup after the row and preparation workgroups issues the row's loads, prepares the window's
+// activation blocks into LDS (32 lanes per block), then each group of GL lanes walks the row against
+// one token and folds its lanes (the GEMV's chains and butterfly).  The value before the bf16
+// rounding goes to gate_logit, which the combine rounds like the bf16 row's.  No ticket: the gate is
+// first read by the combine launch.
+template <int GL, int GIT>
+__device__ __forceinline__ void shared_gate_q4(const MoeArgs& a, uint32_t* __restrict__ xpl) {
+  const int H = a.H, M = a.M, nb = H / 32;
+  const int grp = (int)threadIdx.x / GL, sub = (int)threadIdx.x % GL;
+  QRow<GL, GIT> R;
+  R.load(a.sg_w, a.sg_s, a.sg_b, a.sg_sb, nb, a.gs, sub, grp < M);
+  asm volatile("" ::: "memory");
+  const int i = threadIdx.x & 31;
+  for (int blk = (int)(threadIdx.x >> 5); blk < M * nb; blk += RR_THREADS / 32)
+    xprep_lanes_direct(a.x[(size_t)(blk / nb) * H + (size_t)(blk % nb) * 32 + i], i, xpl + (size_t)blk * XP_DW);
+  __syncthreads();
+  float v = R.dot(xpl + (size_t)(grp < M ? grp : 0) * nb * XP_DW, nb, sub);
+  v = lane_fold<GL>(v);
+  if (sub == 0 && grp < M) a.gate_logit[grp] = v;
+}
+
+// GL = 0: the gate is router row E (bf16); GL > 0: the q4 row, computed by the grid's last workgroup.
+template <int GL, int GIT>
 __global__ __launch_bounds__(RR_THREADS) void k_moe_router_route(MoeArgs a0, int row_wgs) {
   const MoeArgs a = moe_window(a0, blockIdx.y);
   const int H = a.H, E = a.E, M = a.M;
+  extern __shared__ uint4 xs[];  // [M, H/8] (the router rows); the gate workgroup: [M][H/32][XP_DW]
+  if constexpr (GL > 0) {
+    if (blockIdx.x == gridDim.x - 1) {
+      shared_gate_q4<GL, GIT>(a, reinterpret_cast<uint32_t*>(xs));
+      return;
+    }
+  }
   if ((int)blockIdx.x >= row_wgs) {
     const int nb = H / 32;
     const int i = threadIdx.x & 31;
@@ -218,11 +251,10 @@ __global__ __launch_bounds__(RR_THREADS) void k_moe_router_route(MoeArgs a0, int
       xprep_lanes_direct(a.x[(size_t)(blk / nb) * H + (size_t)(blk % nb) * 32 + i], i, a.xp_x + (size_t)blk * XP_DW);
     return;
   }
-  extern __shared__ uint4 xs[];  // [M, H/8]
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int r = blockIdx.x * (RR_THREADS / 64) + wave;
   const int nc = H / 8;
-  const bool row_ok = r <= E;
+  const bool row_ok = GL > 0 ? r < E : r <= E;
   const bf16* wrow = (r < E) ? a.router + (size_t)r * H : a.shared_gate;
   uint4 wv[ROUTER_IT];
 #pragma unroll
@@ -696,17 +728,39 @@ __global__ __launch_bounds__(DD_THREADS) void k_moe_down_dd(MoeArgs a0) {
 }
 
 // ---------------------------------------------------------------------------
-hipError_t launch_moe_router_route(const MoeArgs& a, hipStream_t st) {
-  const int row_wgs = (a.E + 1 + RR_THREADS / 64 - 1) / (RR_THREADS / 64);
+template <int GL, int GIT>
+static hipError_t router_route_go(const MoeArgs& a, hipStream_t st) {
+  const int rows = GL > 0 ? a.E : a.E + 1;  // the bf16 gate row rides as router row E
+  const int row_wgs = (rows + RR_THREADS / 64 - 1) / (RR_THREADS / 64);
   const int prep_wgs = a.xp_ready ? 0 : (a.M * (a.H / 32) + RR_THREADS / 32 - 1) / (RR_THREADS / 32);
-  if (a.M < 1 || a.M > MAX_TOKENS || a.H % 8 != 0 || a.H / 8 > ROUTER_IT * 64) return hipErrorInvalidValue;
-  const size_t lds = (size_t)a.M * a.H * 2;  // the staged activations
+  size_t lds = (size_t)a.M * a.H * 2;  // the staged activations
+  if (GL > 0) lds = std::max(lds, (size_t)a.M * (a.H / 32) * XP_DW * 4);  // the gate's prepared blocks
   static size_t cur = 0;
-  const hipError_t e = ensure_lds(k_moe_router_route, lds + 16 * 1024, cur);
+  const hipError_t e = ensure_lds(k_moe_router_route<GL, GIT>, lds + 16 * 1024, cur);
   if (e != hipSuccess) return e;
-  if (a.nwin < 1 || a.nwin > MOE_TICKETS) return hipErrorInvalidValue;  // a ticket per window
-  hipLaunchKernelGGL(k_moe_router_route, dim3(row_wgs + prep_wgs, a.nwin), dim3(RR_THREADS), lds, st, a, row_wgs);
+  hipLaunchKernelGGL((k_moe_router_route<GL, GIT>), dim3(row_wgs + prep_wgs + (GL > 0 ? 1 : 0), a.nwin),
+                     dim3(RR_THREADS), lds, st, a, row_wgs);
   return hipGetLastError();
+}
+
+hipError_t launch_moe_router_route(const MoeArgs& a, hipStream_t st) {
+  if (a.M < 1 || a.M > MAX_TOKENS || a.H % 8 != 0 || a.H / 8 > ROUTER_IT * 64) return hipErrorInvalidValue;
+  if (a.nwin < 1 || a.nwin > MOE_TICKETS) return hipErrorInvalidValue;  // a ticket per window
+  if (!a.sg_w) return router_route_go<0, 0>(a, st);
+  // the q4 gate row: the model's K = H = 2560 and 2048 tiled exactly, other widths by the predicated walker
+  const int nb = a.H / 32, L = lanes_for_blocks(nb);
+  if (a.H % 32 != 0 || nb > L * QMV_IT) return hipErrorInvalidValue;
+  if (L == 16 && nb == 80) return router_route_go<16, 5>(a, st);
+  if (L == 16 && nb == 64) return router_route_go<16, 4>(a, st);
+  switch (L) {
+    case 1: return router_route_go<1, 0>(a, st);
+    case 2: return router_route_go<2, 0>(a, st);
+    case 4: return router_route_go<4, 0>(a, st);
+    case 8: return router_route_go<8, 0>(a, st);
+    case 16: return router_route_go<16, 0>(a, st);
+    case 32: return router_route_go<32, 0>(a, st);
+    default: return router_route_go<64, 0>(a, st);
+  }
 }
 
 template <int L, int IT, bool PK, int NIT>

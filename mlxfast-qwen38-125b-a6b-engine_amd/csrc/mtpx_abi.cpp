@@ -84,6 +84,7 @@ hipEvent_t ev_get(Ctx* c) {
   do {                                                               \
     if ((c)->ws_over)                                                \
       return fail(MTPX_ERR_STATE, "internal workspace accounting error before %s", name); \
+    (void)hipGetLastError(); /* an earlier call's error (already returned to its caller) is not this launch's */ \
     hipEvent_t a_ = nullptr;                                         \
     if ((c)->prof && (a_ = ev_get(c))) hipEventRecord(a_, (c)->stream); \
     HIP_OK(expr);                                                    \
@@ -197,9 +198,11 @@ int moe_check(const mtpx_moe_weights* w, int M) {
   ARG(w->hidden % 8 == 0 && w->hidden <= 4096, "hidden=%d", w->hidden);
   ARG(k_ok(w->hidden, w->group_size), "hidden=%d not a supported GEMV depth", w->hidden);
   ARG(k_ok(w->expert_width, w->group_size), "expert_width=%d not a supported GEMV depth", w->expert_width);
-  ARG(w->router && w->shared_gate && w->gate_w && w->up_w && w->down_w && w->sh_gate_w && w->sh_up_w &&
-          w->sh_down_w,
+  ARG(w->router && (w->shared_gate || w->shared_gate_w) && w->gate_w && w->up_w && w->down_w && w->sh_gate_w &&
+          w->sh_up_w && w->sh_down_w,
       "missing MoE weight pointer");
+  ARG(!w->shared_gate_w || w->shared_gate_sb || (w->shared_gate_s && w->shared_gate_b),
+      "the q4 shared-expert gate needs its scales and biases (or packed row)");
   const int nsb = !!w->gate_sb + !!w->up_sb + !!w->down_sb + !!w->sh_gate_sb + !!w->sh_up_sb + !!w->sh_down_sb;
   ARG(nsb == 0 || nsb == 6, "packed scale/bias rows: give all six matrices or none");
   return MTPX_OK;
@@ -236,6 +239,10 @@ int moe_enqueue(Ctx* c, const mtpx_moe_weights* w, const uint16_t* x, int M, uin
   a.M = M;
   a.router = w->router;
   a.shared_gate = w->shared_gate;
+  a.sg_w = w->shared_gate_w;
+  a.sg_s = reinterpret_cast<const bf16*>(w->shared_gate_s);
+  a.sg_b = reinterpret_cast<const bf16*>(w->shared_gate_b);
+  a.sg_sb = w->shared_gate_sb;
   a.gate_w = w->gate_w; a.gate_s = w->gate_s; a.gate_b = w->gate_b;
   a.up_w = w->up_w; a.up_s = w->up_s; a.up_b = w->up_b;
   a.down_w = w->down_w; a.down_s = w->down_s; a.down_b = w->down_b;
@@ -1378,6 +1385,9 @@ int head_width(mtpx_head hh) {
   const Head* hd = static_cast<const Head*>(hh.ctx);
   return hd->cfg.hc * hd->cfg.layer.hidden;
 }
+void target_own(mtpx_target th, void* p) { static_cast<Target*>(th.ctx)->allocs.push_back(p); }
+void head_own(mtpx_head hh, void* p) { static_cast<Head*>(hh.ctx)->allocs.push_back(p); }
+std::vector<int32_t> head_shortlist_ids(const mtpx_head_config* cfg) { return shortlist_ids(cfg); }
 }  // namespace mtpx
 
 extern "C" {
@@ -1461,7 +1471,7 @@ int mtpx_affine_quantize(mtpx_ctx h, const uint16_t* w, int64_t rows, int K, int
   ARG(c && w && wq && s && b, "null argument");
   ARG(gs_ok(gs) && K > 0 && K % gs == 0 && rows >= 0, "K=%d gs=%d rows=%lld", K, gs, (long long)rows);
   if (set_device(c)) return MTPX_ERR_HIP;
-  HIP_OK(launch_quantize(w, rows, K, gs, wq, s, b, c->stream));
+  LAUNCH(c, "quantize", launch_quantize(w, rows, K, gs, wq, s, b, c->stream));
   return MTPX_OK;
 }
 
@@ -1469,7 +1479,7 @@ int mtpx_randn_bf16(mtpx_ctx h, uint16_t* out, int64_t n, uint64_t seed, uint32_
   Ctx* c = C(h);
   ARG(c && out && n >= 0, "bad argument");
   if (set_device(c)) return MTPX_ERR_HIP;
-  HIP_OK(launch_randn_bf16(out, n, seed, tensor, sigma, c->stream));
+  LAUNCH(c, "randn_bf16", launch_randn_bf16(out, n, seed, tensor, sigma, c->stream));
   return MTPX_OK;
 }
 
@@ -1565,7 +1575,7 @@ int mtpx_attn_prep(mtpx_ctx h, const uint16_t* qkv, int S, int QW, int HQ, int H
   ARG(QW >= 2 * HQ * D + 2 * HK * D, "QW=%d too small", QW);
   ARG(pos0 >= 0 && pos0 + S <= tmax, "positions %d..%d beyond cache %lld", pos0, pos0 + S, (long long)tmax);
   if (set_device(c)) return MTPX_ERR_HIP;
-  HIP_OK(launch_attn_prep(qkv, S, QW, HQ, HK, D, rot, qnorm, knorm, eps, cos_t, sin_t, pos0, q, kc, vc, tmax,
+  LAUNCH(c, "attn_prep", launch_attn_prep(qkv, S, QW, HQ, HK, D, rot, qnorm, knorm, eps, cos_t, sin_t, pos0, q, kc, vc, tmax,
                           c->stream));
   return MTPX_OK;
 }
@@ -1603,7 +1613,7 @@ int mtpx_rmsnorm(mtpx_ctx h, const uint16_t* x, const uint16_t* resid, int M, in
   ARG(c && x && w && y, "null argument");
   ARG(M >= 1 && H >= 1 && H <= 4096, "M=%d H=%d (H <= 4096)", M, H);
   if (set_device(c)) return MTPX_ERR_HIP;
-  HIP_OK(launch_rmsnorm(x, resid, M, H, w, eps, sum_out, y, nullptr, c->stream));
+  LAUNCH(c, "rmsnorm", launch_rmsnorm(x, resid, M, H, w, eps, sum_out, y, nullptr, c->stream));
   return MTPX_OK;
 }
 
@@ -1680,7 +1690,7 @@ int mtpx_argmax_rows(mtpx_ctx h, const float* x, int rows, int64_t V, int32_t* o
   ws_begin(c);
   float* pv = ws_take<float>(c, n);
   int32_t* pi = ws_take<int32_t>(c, n);
-  HIP_OK(launch_argmax_rows(x, rows, V, pv, pi, out, c->stream));
+  LAUNCH(c, "argmax_rows", launch_argmax_rows(x, rows, V, pv, pi, out, c->stream));
   return MTPX_OK;
 }
 
@@ -1696,7 +1706,7 @@ int mtpx_accept_greedy(mtpx_ctx h, const float* logits, int k, int64_t V, const 
   ws_begin(c);
   float* pv = ws_take<float>(c, n);
   int32_t* pi = ws_take<int32_t>(c, n);
-  HIP_OK(launch_accept_greedy(logits, k, V, drafts, kv_offset, pv, pi, out3, c->stream));
+  LAUNCH(c, "accept_greedy", launch_accept_greedy(logits, k, V, drafts, kv_offset, pv, pi, out3, c->stream));
   return MTPX_OK;
 }
 
@@ -2227,6 +2237,7 @@ struct Adopt {
       return;
     }
     allocs->push_back(p);
+    (void)hipGetLastError();  // only this launch's error counts
     if (launch_pack_sb(reinterpret_cast<const bf16*>(s), reinterpret_cast<const bf16*>(b), rows, K, gs,
                        static_cast<uint32_t*>(p), c->stream) != hipSuccess)
       ok = false;
@@ -2244,7 +2255,12 @@ struct Adopt {
     m->expert_width = F;
     m->group_size = lc.group_size;
     need(m->router, "moe router");
-    need(m->shared_gate, "moe shared gate");
+    if (m->shared_gate_w) {  // the q4 gate row: its packed pair row when the caller gave none
+      if (need(m->shared_gate_s, "moe shared gate scales") & need(m->shared_gate_b, "moe shared gate biases"))
+        sb_rows(1, H, m->shared_gate_s, m->shared_gate_b, &m->shared_gate_sb);
+    } else {
+      need(m->shared_gate, "moe shared gate");
+    }
     const int nsb = !!m->gate_sb + !!m->up_sb + !!m->down_sb + !!m->sh_gate_sb + !!m->sh_up_sb + !!m->sh_down_sb;
     if (nsb != 0 && nsb != 6 && missing.empty()) missing = "moe packed scale/bias rows (all six or none)";
     struct {
@@ -2365,7 +2381,8 @@ int mtpx_target_adopt(mtpx_ctx h, const mtpx_target_config* cfg, const mtpx_targ
     // the head vocabularies and offsets follow from the config; the multipliers are the caller's
     mtpx_ngram_table expect;
     const int64_t rows = ngram_heads(cfg->ple, &expect);
-    if (w.table.rows != rows && la.missing.empty()) la.missing = "an n-gram table of the config's row count";
+    // a checkpoint pads the table to whole shards: rows past the heads' sum are never addressed
+    if (w.table.rows < rows && la.missing.empty()) la.missing = "an n-gram table of at least the config's row count";
     for (int hh = 0; hh < pg.nh; ++hh) {
       w.table.vocab[hh] = expect.vocab[hh];
       w.table.offset[hh] = expect.offset[hh];

@@ -118,6 +118,10 @@ struct MoeArgs {
   const bf16 *sh_gate_s, *sh_gate_b, *sh_up_s, *sh_up_b, *sh_down_s, *sh_down_b;
   // packed scale/bias rows (all six or none)
   const uint32_t *gate_sb, *up_sb, *down_sb, *sh_gate_sb, *sh_up_sb, *sh_down_sb;
+  // the shared-expert gate as a q4 row [1, H] (null: the bf16 row shared_gate)
+  const uint32_t* sg_w = nullptr;
+  const bf16 *sg_s = nullptr, *sg_b = nullptr;
+  const uint32_t* sg_sb = nullptr;
   // activations and workspace
   const bf16* x;       // [M, H]
   bf16* y;             // [M, H]

@@ -16,7 +16,7 @@ from ._lib import (DrafterInfo, ForceParams, GDNConfig, GDNWeights, Handle, HCWe
                    TargetLayerWeights, TargetWeights, check)
 
 __all__ = ["Context", "KVCache", "DecoderLayer", "MTPHead", "Drafter", "GDN", "GDNState", "PLE", "PLEState", "Target",
-           "TargetState", "Session", "MoEWeights", "LayerConfig", "HeadConfig", "GDNConfig", "PLEConfig", "TargetConfig",
+           "TargetState", "Session", "SafetensorsFile", "Checkpoint", "MoEWeights", "LayerConfig", "HeadConfig", "GDNConfig", "PLEConfig", "TargetConfig",
            "MtpxError", "moe_weights_from"]
 
 
@@ -277,6 +277,17 @@ class MTPHead:
               "head_adopt")
         return hd
 
+    @classmethod
+    def load(cls, ctx: Context, cfg: HeadConfig, ckpt: "Checkpoint", target: "Target", prefix: "str | None" = None,
+             pack_sb: bool = True):
+        """The checkpoint's MTP head over `target` (mtpx_head_load; the target must outlive it)."""
+        hd = cls.__new__(cls)
+        hd.ctx, hd.cfg, hd.h = ctx, cfg, Handle()
+        check(ctx.lib.mtpx_head_load(ctx.h, C.byref(cfg), ckpt.h, target.h,
+                                     prefix.encode() if prefix is not None else None, 1 if pack_sb else 0,
+                                     C.byref(hd.h)), "head_load")
+        return hd
+
     def close(self):
         if self.h.ctx:
             self.ctx.lib.mtpx_head_free(self.h)
@@ -530,6 +541,16 @@ class Target:
                                         C.byref(t.h)), "target_adopt")
         return t
 
+    @classmethod
+    def load(cls, ctx: Context, cfg: TargetConfig, ckpt: "Checkpoint", prefix: "str | None" = None,
+             pack_sb: bool = True):
+        """A target from a safetensors checkpoint (mtpx_target_load); it owns its device copies."""
+        t = cls.__new__(cls)
+        t.ctx, t.cfg, t.h = ctx, cfg, Handle()
+        check(ctx.lib.mtpx_target_load(ctx.h, C.byref(cfg), ckpt.h, prefix.encode() if prefix is not None else None,
+                                       1 if pack_sb else 0, C.byref(t.h)), "target_load")
+        return t
+
     def weights(self) -> TargetWeights:
         w = TargetWeights()
         check(self.ctx.lib.mtpx_target_weights_get(self.h, C.byref(w)), "target_weights_get")
@@ -681,3 +702,77 @@ class Session:
         i = DrafterInfo()
         check(self.ctx.lib.mtpx_drafter_info_get(h, C.byref(i)), "drafter_info")
         return {n: getattr(i, n) for n, _ in DrafterInfo._fields_}
+
+
+class SafetensorsFile:
+    """One safetensors file through the library's reader (mtpx_st_*): header checked, data mapped."""
+
+    def __init__(self, path: str):
+        self.lib = _lib.lib()
+        self.h = Handle()
+        check(self.lib.mtpx_st_open(str(path).encode(), C.byref(self.h)), "st_open")
+
+    def close(self):
+        if self.h.ctx:
+            self.lib.mtpx_st_free(self.h)
+            self.h.ctx = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def tensors(self) -> list:
+        """[(name, dtype, shape, nbytes)] in name order."""
+        n = C.c_int64()
+        check(self.lib.mtpx_st_count(self.h, C.byref(n)), "st_count")
+        out = []
+        for i in range(n.value):
+            name, dt, nd, sh, nb = C.c_char_p(), C.c_char_p(), C.c_int(), C.POINTER(C.c_int64)(), C.c_int64()
+            check(self.lib.mtpx_st_tensor(self.h, i, C.byref(name), C.byref(dt), C.byref(nd), C.byref(sh),
+                                          C.byref(nb)), "st_tensor")
+            out.append((name.value.decode(), dt.value.decode(), tuple(sh[k] for k in range(nd.value)), nb.value))
+        return out
+
+    def read(self, name: str) -> bytes:
+        i = C.c_int64()
+        check(self.lib.mtpx_st_find(self.h, name.encode(), C.byref(i)), "st_find")
+        nb = C.c_int64()
+        check(self.lib.mtpx_st_tensor(self.h, i.value, None, None, None, None, C.byref(nb)), "st_tensor")
+        buf = C.create_string_buffer(max(1, nb.value))
+        check(self.lib.mtpx_st_read(self.h, i.value, buf, nb.value), "st_read")
+        return buf.raw[:nb.value]
+
+    def metadata(self, key: str):
+        v = C.c_char_p()
+        check(self.lib.mtpx_st_metadata(self.h, key.encode(), C.byref(v)), "st_metadata")
+        return None if v.value is None else v.value.decode()
+
+
+class Checkpoint:
+    """Safetensors files (or directories of them) as one tensor name space (mtpx_checkpoint)."""
+
+    def __init__(self, paths):
+        if isinstance(paths, (str, bytes)):
+            paths = [paths]
+        self.lib = _lib.lib()
+        self.h = Handle()
+        arr = (C.c_char_p * len(paths))(*[str(p).encode() for p in paths])
+        check(self.lib.mtpx_checkpoint_open(arr, len(paths), C.byref(self.h)), "checkpoint_open")
+
+    def count(self) -> int:
+        n = C.c_int64()
+        check(self.lib.mtpx_checkpoint_count(self.h, C.byref(n)), "checkpoint_count")
+        return n.value
+
+    def close(self):
+        if self.h.ctx:
+            self.lib.mtpx_checkpoint_free(self.h)
+            self.h.ctx = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -29,7 +29,8 @@ class MoEWeights(C.Structure):
                     "gate_w", "gate_s", "gate_b", "up_w", "up_s", "up_b", "down_w", "down_s", "down_b",
                     "sh_gate_w", "sh_gate_s", "sh_gate_b", "sh_up_w", "sh_up_s", "sh_up_b",
                     "sh_down_w", "sh_down_s", "sh_down_b",
-                    "gate_sb", "up_sb", "down_sb", "sh_gate_sb", "sh_up_sb", "sh_down_sb")]
+                    "gate_sb", "up_sb", "down_sb", "sh_gate_sb", "sh_up_sb", "sh_down_sb",
+                    "shared_gate_w", "shared_gate_s", "shared_gate_b", "shared_gate_sb")]
 
 
 class LayerConfig(C.Structure):
@@ -147,6 +148,19 @@ _SIGS = {
     "mtpx_accept_sample": (INT, [Handle, P, P, INT, I64, P, F32, U64, U64, I32, P]),
     "mtpx_accept_sample_bf16": (INT, [Handle, P, P, INT, I64, P, F32, U64, U64, I32, P, P]),
     "mtpx_top_two": (INT, [Handle, P, INT, I64, P, P]),
+    "mtpx_st_open": (INT, [C.c_char_p, C.POINTER(Handle)]),
+    "mtpx_st_free": (INT, [Handle]),
+    "mtpx_st_count": (INT, [Handle, C.POINTER(I64)]),
+    "mtpx_st_tensor": (INT, [Handle, I64, C.POINTER(C.c_char_p), C.POINTER(C.c_char_p), C.POINTER(INT),
+                             C.POINTER(C.POINTER(I64)), C.POINTER(I64)]),
+    "mtpx_st_find": (INT, [Handle, C.c_char_p, C.POINTER(I64)]),
+    "mtpx_st_metadata": (INT, [Handle, C.c_char_p, C.POINTER(C.c_char_p)]),
+    "mtpx_st_read": (INT, [Handle, I64, P, I64]),
+    "mtpx_checkpoint_open": (INT, [C.POINTER(C.c_char_p), INT, C.POINTER(Handle)]),
+    "mtpx_checkpoint_free": (INT, [Handle]),
+    "mtpx_checkpoint_count": (INT, [Handle, C.POINTER(I64)]),
+    "mtpx_target_load": (INT, [Handle, C.POINTER(TargetConfig), Handle, C.c_char_p, INT, C.POINTER(Handle)]),
+    "mtpx_head_load": (INT, [Handle, C.POINTER(HeadConfig), Handle, Handle, C.c_char_p, INT, C.POINTER(Handle)]),
     "mtpx_top_two_bf16": (INT, [Handle, P, INT, I64, P, P]),
     "mtpx_accept_greedy_bf16": (INT, [Handle, P, INT, I64, P, I32, P, P, P]),
     "mtpx_force_draft": (INT, [Handle, P, P, I64, F32, U64]),

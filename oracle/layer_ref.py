@@ -38,7 +38,8 @@ def download(lw, cfg, lazy=False):
     def q(pw, ps, pb, rows, K):
         return (read_device(pw, rows * K // 2, np.uint32).reshape(rows, K // 8),
                 bf(ps, rows * K // gs).reshape(rows, K // gs), bf(pb, rows * K // gs).reshape(rows, K // gs))
-    w = dict(attn_norm=bf(lw.attn_norm, H), post_norm=bf(lw.post_norm, H), q_norm=bf(lw.q_norm, D),
+    w = dict(attn_norm=bf(lw.attn_norm, H) if lw.attn_norm else None,  # a target's or head's layer has none
+             post_norm=bf(lw.post_norm, H) if lw.post_norm else None, q_norm=bf(lw.q_norm, D),
              k_norm=bf(lw.k_norm, D), cos=bf(lw.rope_cos, P * rot).reshape(P, rot),
              sin=bf(lw.rope_sin, P * rot).reshape(P, rot), QW=QW)
     w["qkv"] = q(lw.qkv_w, lw.qkv_s, lw.qkv_b, QW, H)
@@ -91,7 +92,11 @@ def download_moe(m, cfg, lazy=False):
     def q(pw, ps, pb, rows, K):
         return (read_device(pw, rows * K // 2, np.uint32).reshape(rows, K // 8),
                 bf(ps, rows * K // gs).reshape(rows, K // gs), bf(pb, rows * K // gs).reshape(rows, K // gs))
-    moe = dict(router=bf(m.router, E * H).reshape(E, H), shared_gate=bf(m.shared_gate, H))
+    moe = dict(router=bf(m.router, E * H).reshape(E, H))
+    if m.shared_gate_w:  # the q4 gate row
+        moe["sg_w"], moe["sg_s"], moe["sg_b"] = q(m.shared_gate_w, m.shared_gate_s, m.shared_gate_b, 1, H)
+    else:
+        moe["shared_gate"] = bf(m.shared_gate, H)
     for n, rows, K in (("gate", E * F, H), ("up", E * F, H), ("down", E * H, F),
                        ("sh_gate", F, H), ("sh_up", F, H), ("sh_down", H, F)):
         ptrs = (getattr(m, n + "_w"), getattr(m, n + "_s"), getattr(m, n + "_b"))

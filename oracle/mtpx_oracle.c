@@ -386,7 +386,12 @@ void o_moe_block(const o_moe_weights* mw, const o_bf16* x, int M, o_bf16* y, int
     for (int h = 0; h < H; ++h) xf[h] = o_bf2f(xm[h]);
     o_router_gemv(mw->router, E, H, xf, 1, lg);
     float gl;
-    o_router_gemv(mw->shared_gate, 1, H, xf, 1, &gl);
+    if (mw->sg_w) { /* q4 row: the GEMV's value before its bf16 rounding (TrackFastMoE.swift:780-800) */
+      o_bf16 gq;
+      o_qmv(mw->sg_w, mw->sg_s, mw->sg_b, 1, H, gsz, xm, 1, &gq, &gl);
+    } else {
+      o_router_gemv(mw->shared_gate, 1, H, xf, 1, &gl);
+    }
     const float gbf = o_round_bf(gl);
     if (logits) memcpy(logits + (int64_t)m * E, lg, sizeof(float) * E);
     if (gate) gate[m] = o_f2bf(gl);

@@ -65,6 +65,8 @@ typedef struct {
   const uint32_t* sh_gate_w; const o_bf16* sh_gate_s; const o_bf16* sh_gate_b; /* [F,H/8] */
   const uint32_t* sh_up_w;   const o_bf16* sh_up_s;   const o_bf16* sh_up_b;
   const uint32_t* sh_down_w; const o_bf16* sh_down_s; const o_bf16* sh_down_b; /* [H,F/8] */
+  /* the shared-expert gate as a q4 row [1, H] (NULL: the bf16 row shared_gate) */
+  const uint32_t* sg_w; const o_bf16* sg_s; const o_bf16* sg_b;
 } o_moe_weights;
 
 void o_moe_block(const o_moe_weights* mw, const o_bf16* x, int M, o_bf16* y,

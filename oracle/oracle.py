@@ -185,7 +185,7 @@ class MoEWeightsStruct(C.Structure):
             "router", "shared_gate",
             "gate_w", "gate_s", "gate_b", "up_w", "up_s", "up_b", "down_w", "down_s", "down_b",
             "sh_gate_w", "sh_gate_s", "sh_gate_b", "sh_up_w", "sh_up_s", "sh_up_b",
-            "sh_down_w", "sh_down_s", "sh_down_b"]]
+            "sh_down_w", "sh_down_s", "sh_down_b", "sg_w", "sg_s", "sg_b"]]
 
 
 def moe_block(w: dict, x_bf16, H, E, K, F, gs):
@@ -193,6 +193,8 @@ def moe_block(w: dict, x_bf16, H, E, K, F, gs):
     st = MoEWeightsStruct(H, E, K, F, gs)
     keep = {}
     for name, _ in MoEWeightsStruct._fields_[5:]:
+        if w.get(name) is None:  # optional: the q4 gate row (sg_*), or the bf16 row when it is given
+            continue
         a = np.ascontiguousarray(w[name])
         keep[name] = a
         setattr(st, name, a.ctypes.data)

@@ -28,7 +28,7 @@ def test_version_and_error_string():
 
 def test_struct_sizes_match_header_layout():
     # offsets of the pointer block after five ints (padded to 8)
-    assert C.sizeof(_lib.MoEWeights) == 24 + 26 * 8
+    assert C.sizeof(_lib.MoEWeights) == 24 + 30 * 8
     assert _lib.LayerWeights.moe.offset == 12 * 8
 
 

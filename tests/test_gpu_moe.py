@@ -47,7 +47,12 @@ def run_case(ctx, w, H, E, K, F, gs, M, xseed, packed=False):
     r = np.random.default_rng(xseed)
     x = rand_bf16(r, (M, H), 1.0)
     ref = O.moe_block(w, x, H, E, K, F, gs)
-    dw = {n: dev(w[n]) for n in NAMES}
+    dw = {n: dev(w[n]) for n in NAMES if n in w}
+    if "sg_w" in w:  # the q4 shared-expert gate row (its packed pair row with the packed layout)
+        dw["shared_gate_w"], dw["shared_gate_s"], dw["shared_gate_b"] = (dev(w["sg_w"]), dev(w["sg_s"]),
+                                                                       dev(w["sg_b"]))
+        if packed:
+            dw["shared_gate_sb"] = ctx.pack_sb(dw["shared_gate_s"], dw["shared_gate_b"], H, gs)
     if packed:  # packed (scale, bias) rows for the expert GEMVs
         for n, Kd in (("gate", H), ("up", H), ("down", F), ("sh_gate", H), ("sh_up", H), ("sh_down", F)):
             dw[n + "_sb"] = ctx.pack_sb(dw[n + "_s"], dw[n + "_b"], Kd, gs)
@@ -87,6 +92,23 @@ def test_moe_full_expert_shapes_bit_exact(ctx, gs, M, packed):
     H, E, K, F = 2560, 24, 10, 640
     w = make_moe(1000 + gs, H, E, K, F, gs)
     run_case(ctx, w, H, E, K, F, gs, M, 77 + M, packed)
+
+
+@pytest.mark.parametrize("H,gs,M,packed", [(2560, 32, 4, True), (2560, 64, 1, False), (2560, 32, 8, False),
+                                           (2048, 64, 3, True), (512, 32, 2, True)])
+def test_moe_q4_shared_gate_bit_exact(ctx, H, gs, M, packed):
+    """The checkpoint's shared-expert gate as a q4 row (mlp.shared_expert_gate): the router launch's
+    extra workgroup computes it with the GEMV's lane rule; bit-exact against the oracle, with the
+    packed pair row or the checkpoint's scales and biases, at the model's hidden size and others."""
+    print("case moe q4 shared gate H", H, "gs", gs, "M", M, "packed", packed, flush=True)
+    E, K, F = 24, 10 if H == 2560 else 4, 640 if H == 2560 else 256
+    w = make_moe(3000 + H + gs, H, E, K, F, gs)
+    r = np.random.default_rng(H + M)
+    w["sg_w"], w["sg_s"], w["sg_b"] = O.affine_quantize(rand_bf16(r, (1, H), 0.3), gs)
+    del w["shared_gate"]
+    ref = run_case(ctx, w, H, E, K, F, gs, M, 91 + M, packed)
+    gq, _ = O.qmv(w["sg_w"], w["sg_s"], w["sg_b"], gs, rand_bf16(np.random.default_rng(91 + M), (M, H), 1.0))
+    assert np.array_equal(ref["gate"], gq[:, 0])
 
 
 def test_moe_nan_token_routes_distinct_experts(ctx):

@@ -272,6 +272,42 @@ def test_moe_block_matches_float64_textbook():
         assert np.linalg.norm(got - y) <= 2e-2 * np.linalg.norm(y), np.linalg.norm(got - y) / np.linalg.norm(y)
 
 
+def test_moe_block_q4_shared_gate():
+    """The shared-expert gate as a q4 row (the checkpoint's mlp.shared_expert_gate): the gate is the
+    q4 GEMV of that row rounded to bf16 (equal to O.qmv of it, whose arithmetic is pinned above), the
+    routing does not depend on it, and the block matches the float64 textbook MoE with the row
+    dequantised; with the bf16 row given as well, the q4 row wins."""
+    H, E, K, F, gs, M = 256, 16, 4, 128, 32, 3
+    r = rng(12)
+    w = _moe_weights(r, H, E, K, F, gs)
+    sg = bf16(r.standard_normal((1, H)).astype(np.float32) * 0.3)
+    w["sg_w"], w["sg_s"], w["sg_b"] = O.affine_quantize(sg, gs)
+    x = bf16(r.standard_normal((M, H)).astype(np.float32))
+    out = O.moe_block(w, x, H, E, K, F, gs)
+    gq, _ = O.qmv(w["sg_w"], w["sg_s"], w["sg_b"], gs, x)
+    assert np.array_equal(out["gate"], gq[:, 0])
+    base = O.moe_block({k: v for k, v in w.items() if not k.startswith("sg_")}, x, H, E, K, F, gs)
+    assert np.array_equal(out["idx"], base["idx"]) and np.array_equal(out["w"], base["w"])
+    assert not np.array_equal(out["y"], base["y"])
+    X = f32(x).astype(np.float64)
+    logits = X @ f32(w["router"]).astype(np.float64).reshape(E, H).T
+    G, U, Dn = (O.dequantize(w[n + "_w"], w[n + "_s"], w[n + "_b"], gs) for n in ("gate", "up", "down"))
+    SG, SU, SD = (O.dequantize(w[n + "_w"], w[n + "_s"], w[n + "_b"], gs) for n in ("sh_gate", "sh_up", "sh_down"))
+    SGT = O.dequantize(w["sg_w"], w["sg_s"], w["sg_b"], gs)[0]
+    silu = lambda v: v / (1 + np.exp(-v))
+    for m in range(M):
+        order = np.argsort(-logits[m], kind="stable")[:K]
+        v = logits[m, order]
+        p = np.exp(v - v.max()); p /= p.sum()
+        y = np.zeros(H)
+        for k, e in enumerate(order):
+            y += p[k] * (Dn[e] @ (silu(G[e] @ X[m]) * (U[e] @ X[m])))
+        y += (SD @ (silu(SG @ X[m]) * (SU @ X[m]))) / (1 + np.exp(-(SGT @ X[m])))
+        got = f32(out["y"][m]).astype(np.float64)
+        assert np.linalg.norm(got - y) <= 2e-2 * np.linalg.norm(y)
+        assert abs(f32(out["gate"][m]) - SGT @ X[m]) <= 1e-2 * abs(SGT @ X[m]) + 1e-3
+
+
 # ---------------------------------------------------------------------------- attention
 def test_rope_table_against_numpy():
     c, s = O.rope_table(64, 16, 1e7)

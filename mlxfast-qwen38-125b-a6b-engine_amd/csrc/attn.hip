@@ -144,7 +144,8 @@ __global__ __launch_bounds__(ATTN_THREADS) void k_attn_partial(const bf16* __res
     const uint32_t* qr = qb + (size_t)(p / C) * (D / 2);
     const uint32_t* kr = kb + (size_t)(on ? p % C : 0) * KS;
     float acc = 0.0f;
-    for (int d0 = 0; d0 < D / 2; d0 += 4) {
+#pragma unroll 4
+    for (int d0 = 0; d0 < D / 2; d0 += 4) {  // (D / 8 steps, a multiple of 4: the reads of four steps in flight)
       const uint4 q4v = *reinterpret_cast<const uint4*>(qr + d0), k4v = *reinterpret_cast<const uint4*>(kr + d0);
       const uint32_t qa[4] = {q4v.x, q4v.y, q4v.z, q4v.w}, ka[4] = {k4v.x, k4v.y, k4v.z, k4v.w};
 #pragma unroll
@@ -160,6 +161,7 @@ __global__ __launch_bounds__(ATTN_THREADS) void k_attn_partial(const bf16* __res
   // sums in key order
   for (int g = threadIdx.x; g < G; g += blockDim.x) {
     float mx = -__uint_as_float(0x7f800000u);
+#pragma unroll 8
     for (int j = 0; j < n; ++j) mx = sc[g * C + j] > mx ? sc[g * C + j] : mx;
     ml[2 * g] = (n > 0) ? mx : -__uint_as_float(0x7f800000u);
   }
@@ -178,37 +180,59 @@ __global__ __launch_bounds__(ATTN_THREADS) void k_attn_partial(const bf16* __res
   __syncthreads();
   // P.V: a thread owns the adjacent outputs (g, 2e) and (g, 2e+1), one 32-bit V
   // read per key for both; each output is the sequential key-order fmaf
+  // (blockDim is a multiple of D / 2, so outputs p, p + blockDim, ... share e: up to PVN of them side by side,
+  // one V read per key for all, 2 * PVN independent chains)
   const uint32_t* vb32 = reinterpret_cast<const uint32_t*>(vb);
-  for (int p = threadIdx.x; p < G * (D / 2); p += blockDim.x) {
-    const int g = p / (D / 2), e = p % (D / 2);
-    const float* sg = sc + (size_t)g * C;
-    float o0 = 0.0f, o1 = 0.0f;
+  constexpr int PVN = 4;
+  for (int pb = threadIdx.x; pb < G * (D / 2); pb += PVN * (int)blockDim.x) {
+    const int e = pb % (D / 2);
+    int gk[PVN];
+    float o0[PVN], o1[PVN];
+#pragma unroll
+    for (int k = 0; k < PVN; ++k) {
+      const int p = pb + k * (int)blockDim.x;
+      gk[k] = p < G * (D / 2) ? p / (D / 2) : -1;
+      o0[k] = 0.0f;
+      o1[k] = 0.0f;
+    }
     int j = 0;
     for (; j + 8 <= n; j += 8) {
-      float pv[8];
       uint32_t vv[8];
+      float pv[PVN][8];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        pv[u] = sg[j + u];
-        vv[u] = vb32[(size_t)(j + u) * (D / 2) + e];
-      }
+      for (int u = 0; u < 8; ++u) vv[u] = vb32[(size_t)(j + u) * (D / 2) + e];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        o0 = __builtin_fmaf(pv[u], __uint_as_float(vv[u] << 16), o0);
-        o1 = __builtin_fmaf(pv[u], __uint_as_float(vv[u] & 0xffff0000u), o1);
-      }
+      for (int k = 0; k < PVN; ++k)
+#pragma unroll
+        for (int u = 0; u < 8; ++u) pv[k][u] = sc[(size_t)(gk[k] < 0 ? 0 : gk[k]) * C + j + u];
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+#pragma unroll
+        for (int k = 0; k < PVN; ++k) {
+          o0[k] = __builtin_fmaf(pv[k][u], __uint_as_float(vv[u] << 16), o0[k]);
+          o1[k] = __builtin_fmaf(pv[k][u], __uint_as_float(vv[u] & 0xffff0000u), o1[k]);
+        }
     }
     for (; j < n; ++j) {
       const uint32_t v = vb32[(size_t)j * (D / 2) + e];
-      o0 = __builtin_fmaf(sg[j], __uint_as_float(v << 16), o0);
-      o1 = __builtin_fmaf(sg[j], __uint_as_float(v & 0xffff0000u), o1);
+#pragma unroll
+      for (int k = 0; k < PVN; ++k) {
+        const float w = sc[(size_t)(gk[k] < 0 ? 0 : gk[k]) * C + j];
+        o0[k] = __builtin_fmaf(w, __uint_as_float(v << 16), o0[k]);
+        o1[k] = __builtin_fmaf(w, __uint_as_float(v & 0xffff0000u), o1[k]);
+      }
     }
-    float* dst = part + (((size_t)hk * nch + c) * R + s * G + g) * (D + 2);
-    dst[2 + 2 * e] = o0;
-    dst[3 + 2 * e] = o1;
-    if (e == 0) {
-      dst[0] = ml[2 * g];
-      dst[1] = ml[2 * g + 1];
+#pragma unroll
+    for (int k = 0; k < PVN; ++k) {
+      const int g = gk[k];
+      if (g < 0) continue;
+      float* dst = part + (((size_t)hk * nch + c) * R + s * G + g) * (D + 2);
+      dst[2 + 2 * e] = o0[k];
+      dst[3 + 2 * e] = o1[k];
+      if (e == 0) {
+        dst[0] = ml[2 * g];
+        dst[1] = ml[2 * g + 1];
+      }
     }
   }
 }
@@ -261,19 +285,27 @@ __global__ __launch_bounds__(256) void k_attn_combine(const float* __restrict__ 
   // the factor of every chunk once, then L and O[d] in chunk order
   for (int c = t; c < nch; c += nt) fc[c] = lc[c] > 0.0f ? expf_det(mc[c] - M) : 0.0f;
   __syncthreads();
+  // L and O, each in chunk order, as two chains of one loop; a batch's (l, f) pairs are read from LDS
+  // before its folds (clamped indices), so the reads are in flight together
   float L = 0.0f, O = 0.0f;
-#pragma unroll 8
-  for (int c = 0; c < nch; ++c)
-    if (lc[c] > 0.0f) L = __builtin_fmaf(lc[c], fc[c], L);
+  for (int cb = 0; cb < nch; cb += COMBINE_BATCH) {
+    if (cb > 0) {
 #pragma unroll
-  for (int u = 0; u < COMBINE_BATCH; ++u)
-    if (u < nch && lc[u] > 0.0f) O = __builtin_fmaf(pv[u], fc[u], O);
-  for (int cb = COMBINE_BATCH; cb < nch; cb += COMBINE_BATCH) {
+      for (int u = 0; u < COMBINE_BATCH; ++u) pv[u] = chunk(cb + u < nch ? cb + u : nch - 1)[2 + dc];
+    }
+    float lb[COMBINE_BATCH], fb[COMBINE_BATCH];
 #pragma unroll
-    for (int u = 0; u < COMBINE_BATCH; ++u) pv[u] = chunk(cb + u < nch ? cb + u : nch - 1)[2 + dc];
+    for (int u = 0; u < COMBINE_BATCH; ++u) {
+      const int c = cb + u < nch ? cb + u : nch - 1;
+      lb[u] = lc[c];
+      fb[u] = fc[c];
+    }
 #pragma unroll
     for (int u = 0; u < COMBINE_BATCH; ++u)
-      if (cb + u < nch && lc[cb + u] > 0.0f) O = __builtin_fmaf(pv[u], fc[cb + u], O);
+      if (cb + u < nch && lb[u] > 0.0f) {
+        L = __builtin_fmaf(lb[u], fb[u], L);
+        O = __builtin_fmaf(pv[u], fb[u], O);
+      }
   }
   {
     const int d0 = 0;

@@ -151,6 +151,45 @@ def test_moe_router_ties_lowest_index(ctx):
                 assert a in sel and sel.index(a) < sel.index(b)
 
 
+@pytest.mark.parametrize("E", [512, 1024])
+def test_moe_router_ties_within_and_across_lanes(ctx, E):
+    """Equal logits among the leaders: copies of one router row on experts that share a lane of the
+    route's wave (5, 69, 133, ... : expert mod 64 equal) and on neighbouring lanes (7, 8, 71), so the
+    ranks take them in index order whether the tie is inside a lane's list or between lanes; a zero
+    token has every logit +0 (all tied: experts 0..K-1 in order).  E 1024 holds 16 experts per lane."""
+    print("case router lane ties E", E, flush=True)
+    H, K, F, gs, M = 256, 10, 64, 32, 4
+    w = make_moe(70 + E, H, E, K, F, gs)
+    r = w["router"].reshape(E, H)
+    r7 = O.bf16_to_f32(r[7])
+    b5, b7 = O.f32_to_bf16((r7 * 4.0).astype(np.float32)), O.f32_to_bf16((r7 * 8.0).astype(np.float32))
+    for e in [5, 69, 133, 261] + ([581, 965] if E > 512 else []):
+        r[e] = b5
+    for e in (7, 8, 71):
+        r[e] = b7
+    xr = np.random.default_rng(71)
+    x = rand_bf16(xr, (M, H), 1.0)
+    x[1] = 0
+    x[2] = O.f32_to_bf16((r7 * 50.0).astype(np.float32))  # along row 7: both groups lead, group 7 first
+    import mtpx
+    ref = O.moe_block(w, x, H, E, K, F, gs)
+    dw = {n: dev(w[n]) for n in NAMES}
+    mw = mtpx.moe_weights_from(dw, H, E, K, F, gs)
+    y = empty_bf16(M, H)
+    idx = torch.zeros(M, K, dtype=torch.int32, device="cuda")
+    wt = torch.zeros(M, K, dtype=torch.float32, device="cuda")
+    ctx.moe_forward(mw, dev(x), y, idx, wt)
+    ctx.synchronize()
+    got = host(idx)
+    assert np.array_equal(got, ref["idx"])
+    assert np.array_equal(host(wt).view(np.uint32), ref["w"].view(np.uint32))
+    assert np.array_equal(host(y), ref["y"])
+    assert list(got[1]) == list(range(K))
+    g5 = [5, 69, 133, 261] + ([581, 965] if E > 512 else [])
+    lead = [7, 8, 71] + g5
+    assert list(got[2][:len(lead)]) == lead
+
+
 @pytest.mark.parametrize("H,E,K,F,gs,M", [(4096, 12, 4, 256, 64, 8), (1024, 16, 4, 320, 32, 5),
                                           (512, 8, 2, 1024, 32, 3)])
 def test_moe_other_depths_bit_exact(ctx, H, E, K, F, gs, M):

@@ -2,10 +2,12 @@
 //   k_mix_down : lo = down . n and inj = inject . n (n = the normed streams,
 //                K = hc*H), split over the lane rule's classes: the L lanes of
 //                a row's walk are grouped by lane mod Q (Q = min(L, 4)); each
-//                workgroup computes one class of a row block from that class's
-//                activation blocks only and folds the class's lanes (the
-//                butterfly levels L/2 .. Q), leaving Q partials per row
-//   k_mix_up   : every workgroup finishes the butterfly for all low-rank rows
+//                workgroup computes one class of a row block for one part of
+//                the window's tokens from that class's activation blocks only
+//                and folds the class's lanes (the butterfly levels L/2 .. Q),
+//                leaving Q partials per row and token
+//   k_mix_up   : per (32 hidden positions, part of the tokens): every
+//                workgroup finishes the butterfly for its tokens' low-rank rows
 //                ((v0 + v2) + (v1 + v3) for Q = 4: the remaining levels Q/2 .. 1
 //                in the same order), rounds, applies SiLU and prepares the
 //                activation blocks; then the up rows of its 32 hidden
@@ -25,20 +27,24 @@ namespace mtpx {
 constexpr int MIX_THREADS = 256;
 
 template <int L, int IT>
-__global__ __launch_bounds__(MIX_THREADS) __attribute__((amdgpu_waves_per_eu(1, 2))) void k_mix_down(MixArgs a) {
+__global__ __launch_bounds__(MIX_THREADS) __attribute__((amdgpu_waves_per_eu(1, 2))) void k_mix_down(MixArgs a,
+                                                                                                    int tsplit) {
   static_assert(IT > 0, "exact lane tiling");
-  extern __shared__ uint32_t lds[];  // this class's activation blocks [S][nb/Q]
+  extern __shared__ uint32_t lds[];  // this class's activation blocks [tokens of this workgroup][nb/Q]
   constexpr int Q = L < 4 ? L : 4;
   constexpr int LC = L / Q;       // lanes of one row within a class
   constexpr int RPW = 64 / LC;    // rows per wave
-  const int W = a.hc * a.H, nb = W / 32, ncb = nb / Q, S = a.S;
+  const int W = a.hc * a.H, nb = W / 32, ncb = nb / Q;
   const int NR = a.LW + (a.iw ? a.hc : 0);
-  // Workgroup w -> (row block, class): the Q classes of a row block read the
-  // interleaved 16-byte blocks of the same cache lines, so they get ids 8
-  // apart -- the same XCD (ids go round-robin over the 8 XCDs) and one L2.
+  // Workgroup w -> (row block, class, token part): the Q classes of a row block read the interleaved
+  // 16-byte blocks of the same cache lines, and its token parts the same rows, so they get ids 8
+  // apart -- the same XCD (ids go round-robin over the 8 XCDs) and one L2.  The window's tokens are
+  // cut into tsplit parts (one workgroup each: more workgroups on the chip for a wide window).
   const int wg = blockIdx.x;
   const int g = (wg / 8) % Q;
-  const int rb = (wg / (8 * Q)) * 8 + wg % 8;
+  const int tp = (wg / (8 * Q)) % tsplit;
+  const int rb = (wg / (8 * Q * tsplit)) * 8 + wg % 8;
+  const int per = (a.S + tsplit - 1) / tsplit, s0 = tp * per, s1 = min(a.S, s0 + per), S = s1 - s0;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int subc = lane % LC, grp = lane / LC;
   const int sub = g + Q * subc;  // the lane of the single-launch walk this lane stands in for
@@ -61,7 +67,7 @@ __global__ __launch_bounds__(MIX_THREADS) __attribute__((amdgpu_waves_per_eu(1, 
   asm volatile("" ::: "memory");
   const int n4 = S * ncb * (XP_DW / 4);
   for (int i = threadIdx.x; i < n4; i += MIX_THREADS) {
-    const int q = i % (XP_DW / 4), c = (i / (XP_DW / 4)) % ncb, s = i / (XP_DW / 4) / ncb;
+    const int q = i % (XP_DW / 4), c = (i / (XP_DW / 4)) % ncb, s = s0 + i / (XP_DW / 4) / ncb;
     const int j = g + Q * (c % LC) + L * (c / LC);
     lds_dma16(reinterpret_cast<uint4*>(lds) + (i - lane), a.xpW + ((size_t)s * nb + j) * XP_DW + 4 * q);
   }
@@ -76,7 +82,7 @@ __global__ __launch_bounds__(MIX_THREADS) __attribute__((amdgpu_waves_per_eu(1, 
                         __uint_as_float(R.sb[it] & 0xffff0000u), xl);
     }
     acc = lane_fold<LC>(acc);
-    if (subc == 0 && valid) a.part[((size_t)g * S + s) * NR + row] = acc;
+    if (subc == 0 && valid) a.part[((size_t)g * a.S + s0 + s) * NR + row] = acc;
   }
 }
 
@@ -88,26 +94,31 @@ __device__ __forceinline__ float class_fold_v(const float* v) {
   return v[0];
 }
 
-// grid (H/32), UP_THREADS threads.  Up rows of the block: local row lr = c*32 + i
-// is global row c*H + d0 + i.  The two halves of the workgroup (waves 0-3 and
-// 4-7) walk the same up rows for the even and the odd tokens.
+// grid (H/32 position blocks x tsplit token parts, rounded to whole groups of 8), UP_THREADS threads.
+// Up rows of the block: local row lr = c*32 + i is global row c*H + d0 + i.  A workgroup takes one
+// part of the window's tokens; the two halves of the workgroup (waves 0-3 and 4-7) walk the same up
+// rows for the part's even and odd tokens.  The parts of a position block get ids 8 apart (one XCD:
+// the second reads the up rows from that L2).
 constexpr int UP_THREADS = 512;
 
 template <int QD, int L, int IT>
-__global__ __launch_bounds__(UP_THREADS) __attribute__((amdgpu_waves_per_eu(1, 2))) void k_mix_up(MixArgs a) {
+__global__ __launch_bounds__(UP_THREADS) __attribute__((amdgpu_waves_per_eu(1, 2))) void k_mix_up(MixArgs a,
+                                                                                                  int tsplit) {
   constexpr int RW = 64 / L;
   constexpr int MAXROWS = 8 * 32;  // hc <= 8
   constexpr int NP = (MAXROWS + 4 * RW - 1) / (4 * RW);
   constexpr int FOLD_BATCH = 8;  // S * LW <= FOLD_BATCH * UP_THREADS: one round of partial loads
-  __shared__ bf16 act[MAX_TOKENS * 512];             // [S][LW], S * LW <= 4096
   __shared__ uint32_t xpa[MAX_TOKENS * 12 * XP_DW];  // [S][LW/32][XP_DW], S * LW / 32 <= 96
   __shared__ bf16 wl[MAX_TOKENS][MAXROWS];
   constexpr int MIX_ROUNDS = MAX_TOKENS * MAXROWS / UP_THREADS;  // (token, stream, position) terms per thread
   __shared__ float term[MAX_TOKENS * MAXROWS];                    // [S][hc][32] bf16(sigmoid(w) * n)
-  const int S = a.S, H = a.H, hc = a.hc, LW = a.LW, W = hc * H;
+  const int H = a.H, hc = a.hc, LW = a.LW, W = hc * H;
   const int NR = LW + (a.iw ? hc : 0);
   const int nbA = LW / 32, ng = LW / a.gs, P = sb_row_len(LW, a.gs);
-  const int d0 = blockIdx.x * 32;
+  const int pb = ((int)blockIdx.x / (8 * tsplit)) * 8 + (int)blockIdx.x % 8, tp = ((int)blockIdx.x / 8) % tsplit;
+  if (pb * 32 >= H) return;
+  const int per = (a.S + tsplit - 1) / tsplit, s0 = tp * per, S = min(a.S, s0 + per) - s0;  // this part's tokens
+  const int d0 = pb * 32;
   const int wave = (threadIdx.x >> 6) & 3, half = threadIdx.x >> 8, lane = threadIdx.x & 63;
   const int sub = lane % L, grp = lane / L;
   const int nrows = hc * 32;
@@ -119,15 +130,16 @@ __global__ __launch_bounds__(UP_THREADS) __attribute__((amdgpu_waves_per_eu(1, 2
 #pragma unroll
   for (int u = 0; u < FOLD_BATCH; ++u) {
     const int i0 = threadIdx.x + u * UP_THREADS, i = i0 < S * LW ? i0 : S * LW - 1;
-    const float* p = a.part + (size_t)(i / LW) * NR + i % LW;
+    const float* p = a.part + (size_t)(s0 + i / LW) * NR + i % LW;
 #pragma unroll
-    for (int q = 0; q < QD; ++q) pp[u][q] = p[(size_t)q * S * NR];
+    for (int q = 0; q < QD; ++q) pp[u][q] = p[(size_t)q * a.S * NR];
   }
-  const bool jt = blockIdx.x == 0 && a.iw && a.j && (int)threadIdx.x < S * hc;  // inject gate (s, c) of this thread
+  // inject gate (s, c) of this thread: the first workgroup, for every token of the window
+  const bool jt = blockIdx.x == 0 && a.iw && a.j && (int)threadIdx.x < a.S * hc;
   float jp[QD];
 #pragma unroll
   for (int q = 0; q < QD; ++q)
-    jp[q] = jt ? a.part[(size_t)q * S * NR + (size_t)(threadIdx.x / hc) * NR + LW + threadIdx.x % hc] : 0.0f;
+    jp[q] = jt ? a.part[(size_t)q * a.S * NR + (size_t)(threadIdx.x / hc) * NR + LW + threadIdx.x % hc] : 0.0f;
   // the mix's terms: thread i of round r takes (token, stream, position) u = r * UP_THREADS + i,
   // u = (s * hc + c) * 32 + position; unconditional loads (clamped), used only for u < S * hc * 32
   const int nterm = S * hc * 32;
@@ -136,7 +148,7 @@ __global__ __launch_bounds__(UP_THREADS) __attribute__((amdgpu_waves_per_eu(1, 2
   for (int r = 0; r < MIX_ROUNDS; ++r) {
     const int u0 = r * UP_THREADS + (int)threadIdx.x, u = u0 < nterm ? u0 : nterm - 1;
     const int sc = u >> 5;  // s * hc + c
-    nv[r] = bf2f(a.normed[(size_t)(sc / hc) * W + (size_t)(sc % hc) * H + d0 + (u & 31)]);
+    nv[r] = bf2f(a.normed[(size_t)(s0 + sc / hc) * W + (size_t)(sc % hc) * H + d0 + (u & 31)]);
   }
   QRow<L, IT> U[NP];
 #pragma unroll
@@ -148,20 +160,17 @@ __global__ __launch_bounds__(UP_THREADS) __attribute__((amdgpu_waves_per_eu(1, 2
     U[p].load(a.uw + (size_t)gr * (LW / 8), a.us + (size_t)gr * ng, a.ub + (size_t)gr * ng,
               a.usb ? a.usb + (size_t)gr * P : nullptr, nbA, a.gs, sub, v);
   }
-  // low-rank rows: finish the fold, round, SiLU
+  // low-rank rows: finish the fold, round, SiLU, and the prepared blocks straight from the registers:
+  // item i = t + u * UP_THREADS is element i % 32 of block i / 32, and the 32 lanes of a block are 32
+  // consecutive threads (UP_THREADS and S * LW are multiples of 32, so a block is all in or all out)
 #pragma unroll
   for (int u = 0; u < FOLD_BATCH; ++u) {
     if (u * UP_THREADS >= S * LW) break;  // uniform: only the batches that hold rows
     const int i = threadIdx.x + u * UP_THREADS;
     const bf16 v = f2bf(silu_bf16(round_bf(class_fold_v<QD>(pp[u]))));
-    if (i < S * LW) act[i] = v;
+    if (i < S * LW) xprep_lanes_direct(v, threadIdx.x & 31, xpa + (size_t)(i >> 5) * XP_DW);
   }
   if (jt) a.j[threadIdx.x] = f2bf(2.0f * sigmoid_bf16(round_bf(class_fold_v<QD>(jp))));  // [s * hc + c]
-  __syncthreads();
-  // prepared blocks of the activations: 32 lanes per block
-  const int nblk = S * nbA;
-  for (int b = (int)(threadIdx.x >> 5); b < nblk; b += UP_THREADS / 32)
-    xprep_lanes_direct(act[b * 32 + (threadIdx.x & 31)], threadIdx.x & 31, xpa + (size_t)b * XP_DW);
   __syncthreads();
   // up rows of the block: this half's tokens
 #pragma unroll
@@ -192,8 +201,8 @@ __global__ __launch_bounds__(UP_THREADS) __attribute__((amdgpu_waves_per_eu(1, 2
     for (int c = 0; c < 8; ++c)
       if (c < hc) acc = round_bf(acc + term[(ms * hc + c) * 32 + mi]);
     const bf16 y = f2bf(acc);
-    a.x[(size_t)ms * H + d0 + mi] = y;
-    if (a.xpH) xprep_lanes_direct(y, mi, a.xpH + ((size_t)ms * (H / 32) + blockIdx.x) * XP_DW);
+    a.x[(size_t)(s0 + ms) * H + d0 + mi] = y;
+    if (a.xpH) xprep_lanes_direct(y, mi, a.xpH + ((size_t)(s0 + ms) * (H / 32) + pb) * XP_DW);
   }
 }
 
@@ -205,12 +214,18 @@ static hipError_t mix_down_li(const MixArgs& a, hipStream_t st) {
     constexpr int Q = L < 4 ? L : 4;
     constexpr int RPB = 4 * (64 / (L / Q));
     const int W = a.hc * a.H, NR = a.LW + (a.iw ? a.hc : 0);
-    const size_t lds = (size_t)a.S * (W / 32 / Q) * XP_DW * 4;
+    // two or more tokens in two parts: twice the workgroups, half the tokens each (measured against one
+    // part: 17.8 -> 16.1 us for the mixer pair at 2 tokens, 20.7 -> 17.5 at 4; three or four parts were
+    // slower)
+    const int tsplit = a.S >= 2 ? 2 : 1;
+    const int per = (a.S + tsplit - 1) / tsplit;
+    const size_t lds = (size_t)per * (W / 32 / Q) * XP_DW * 4;
     static size_t cur = 0;
     hipError_t e = ensure_lds(k_mix_down<L, IT>, lds, cur);
     if (e != hipSuccess) return e;
     const int nrb = (NR + RPB - 1) / RPB;
-    hipLaunchKernelGGL((k_mix_down<L, IT>), dim3((nrb + 7) / 8 * 8 * Q), dim3(MIX_THREADS), lds, st, a);
+    hipLaunchKernelGGL((k_mix_down<L, IT>), dim3((nrb + 7) / 8 * 8 * Q * tsplit), dim3(MIX_THREADS), lds, st, a,
+                       tsplit);
     return hipGetLastError();
   }
 }
@@ -219,7 +234,10 @@ template <int QD>
 struct MixUp {
   template <int L, int IT>
   static hipError_t go(const MixArgs& a, hipStream_t st) {
-    hipLaunchKernelGGL((k_mix_up<QD, L, IT>), dim3(a.H / 32), dim3(UP_THREADS), 0, st, a);
+    // (as the down launch: two parts from two tokens on; four parts need two rounds of these workgroups)
+    const int tsplit = a.S >= 2 ? 2 : 1;
+    hipLaunchKernelGGL((k_mix_up<QD, L, IT>), dim3((a.H / 32 + 7) / 8 * 8 * tsplit), dim3(UP_THREADS), 0, st, a,
+                       tsplit);
     return hipGetLastError();
   }
 };

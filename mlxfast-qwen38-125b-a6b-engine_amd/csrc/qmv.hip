@@ -1241,7 +1241,10 @@ hipError_t launch_qmv_pair(const uint32_t* w1, const uint32_t* sb1, int N1, bf16
 hipError_t launch_qmv(const uint32_t* wq, const bf16* s, const bf16* b, const uint32_t* sb, int N, int K, int gs,
                       const uint32_t* xp, int M, bf16* y, float* yf, hipStream_t st) {
   if (qmm_ok(sb, N, K, M)) return qmm(wq, sb, N, K, gs, xp, M, y, yf, st);
-  if (M >= 2 && qmv_mma_ok(sb, K, 2) && qmv_mma_shape<1>(K)) {  // matrix cores
+  // two tokens over many rows: the dot-product path (one window), measured faster than the matrix cores
+  // there (GDN in-projection 18.3 -> 15.7 us, lm_head 99.9 -> 87.4 us); from three tokens on, the matrix cores
+  const bool two_dot = M == 2 && N >= 8192;
+  if (M >= 2 && !two_dot && qmv_mma_ok(sb, K, 2) && qmv_mma_shape<1>(K)) {  // matrix cores
     if (M > MMA_TOK && M <= MAX_TOKENS && qmv_mma_shape<2>(K)) {  // five to eight tokens: one window of eight
       const hipError_t e = qmv_mma<2>(wq, sb, N, K, gs, xp, M, y, yf, st);
       if (e != hipErrorNotReady) return e;
@@ -1262,6 +1265,11 @@ hipError_t launch_qmv(const uint32_t* wq, const bf16* s, const bf16* b, const ui
   const size_t per_token = (size_t)(K / 32) * XP_DW * 4;
   int win = (int)((160 * 1024) / per_token);
   win = win < 1 ? 1 : win;
+  // three or more tokens whose rows alone leave CUs idle (fewer row workgroups than CUs): two windows,
+  // twice the workgroups with half the tokens each (the K = 6144 output projections at 4 tokens: 13.0 ->
+  // 12.6 us)
+  const int rows_pass = 8 * (64 / lanes_for_blocks(K / 32));
+  if (M >= 3 && M <= MAX_TOKENS && (N + rows_pass - 1) / rows_pass < device_cus()) win = std::min(win, (M + 1) / 2);
   return qmv_tokens(wq, s, b, sb, N, K, gs, xp, M, y, yf, M > MAX_TOKENS ? 0 : win, st);
 }
 

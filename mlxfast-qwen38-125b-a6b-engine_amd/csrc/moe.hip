@@ -37,11 +37,11 @@ namespace mtpx {
 
 // ---------------------------------------------------------------------------
 // route (run by one workgroup of RR_THREADS threads): wave m selects token m's
-// top-k and its softmax in registers; then the dispatch table is built in LDS by
+// top-k (a threshold search over order-preserving integer keys, wave ballots
+// counting the keys above each candidate) and its softmax; then the dispatch table is built in LDS by
 // the threads of the M*K slots: each expert once (ordered by its first (token,
 // rank) slot), with its slots ordered by token.  No serial loop over slots or
 // experts: leaders by an LDS minimum, expert offsets by a wave scan.
-constexpr int ROUTE_EPER = 16;  // E <= 1024
 
 // Window w of a batched launch (grid dimension w, a.nwin windows of a.M tokens): the pointers of
 // its tokens and slots, its dispatch table and its ticket.
@@ -71,6 +71,30 @@ __device__ __forceinline__ float readlane_f(float v, int l) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
 }
 
+// Order-preserving key of a router logit: key(a) > key(b) exactly when a > b as floats, -0 and +0
+// share a key, and a NaN logit ranks as -inf.  Key 0, below every logit, marks the lanes past E.
+__device__ __forceinline__ uint32_t route_key(float x) {
+  uint32_t u = __float_as_uint(x);
+  if ((u << 1) == 0u) u = 0u;
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// lanes below this one set in m
+__device__ __forceinline__ int lanes_below(uint64_t m) {
+  return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+
+// keys >= t over the wave's EPER key registers: one ballot and popcount per register
+template <int EPER>
+__device__ __forceinline__ int route_count_ge(const uint32_t (&key)[EPER], uint32_t t) {
+  int n = 0;
+#pragma unroll
+  for (int j = 0; j < EPER; ++j) n += __popcll(__ballot(key[j] >= t));
+  return n;
+}
+
+// EPER = ceil(E / 64) rounded up to 8 or 16: the logits per lane (expert lane + 64 j in register j)
+template <int EPER>
 __device__ void route_body(const MoeArgs& a) {
   const int E = a.E, K = a.K, M = a.M;
   const int MK = M * K;
@@ -82,53 +106,73 @@ __device__ void route_body(const MoeArgs& a) {
   __shared__ int wtot[2];
   __shared__ int uid[MAX_TOKENS * MAX_TOPK];
   __shared__ int pre[MAX_TOKENS * MAX_TOPK];
+  __shared__ uint32_t ckey[MAX_TOKENS][MAX_TOPK];  // the selected of each token, in expert order
+  __shared__ int cidx[MAX_TOKENS][MAX_TOPK];
+  __shared__ float cval[MAX_TOKENS][MAX_TOPK];
   for (int i = threadIdx.x; i < E; i += blockDim.x) first[i] = 0x7fffffff;
   for (int i = threadIdx.x; i < MAX_TOKENS * 32; i += blockDim.x) (&tokbits[0][0])[i] = 0u;
   if (wave < M) {
     const float* lr = a.logits + (size_t)wave * E;
-    float v[ROUTE_EPER];
-    uint32_t taken = 0;  // bit j: expert lane + 64*j already selected (or absent)
+    float v[EPER];
+    uint32_t key[EPER];
 #pragma unroll
-    for (int j = 0; j < ROUTE_EPER; ++j) {
+    for (int j = 0; j < EPER; ++j) {
       const int e = lane + 64 * j;
       const float x = (e < E) ? ld_pub(lr + e) : 0.0f;
       v[j] = (e < E && x == x) ? x : -__uint_as_float(0x7f800000u);  // a NaN logit ranks as -inf
-      if (e >= E) taken |= 1u << j;
+      key[j] = e < E ? route_key(v[j]) : 0u;
     }
-    float myv = 0.0f;  // lane k < K: the k-th selected logit and expert
-    int mys = 0;
-    for (int k = 0; k < K; ++k) {
-      float bv = -__uint_as_float(0x7f800000u);
-      int bj = -1;
-#pragma unroll
-      for (int j = 0; j < ROUTE_EPER; ++j)
-        if (!((taken >> j) & 1u) && (bj < 0 || v[j] > bv)) {
-          bv = v[j];
-          bj = j;
-        }
-      float gmax = bv;
-      gmax = fmaxf(gmax, lane_xor_f<32>(gmax));
-      gmax = fmaxf(gmax, lane_xor_f<16>(gmax));
-      gmax = fmaxf(gmax, lane_xor_f<8>(gmax));
-      gmax = fmaxf(gmax, lane_xor_f<4>(gmax));
-      gmax = fmaxf(gmax, lane_xor_f<2>(gmax));
-      gmax = fmaxf(gmax, lane_xor_f<1>(gmax));
-      int cand = (bj >= 0 && bv == gmax) ? lane + 64 * bj : 0x7fffffff;
-      cand = min(cand, lane_xor_i<32>(cand));
-      cand = min(cand, lane_xor_i<16>(cand));
-      cand = min(cand, lane_xor_i<8>(cand));
-      cand = min(cand, lane_xor_i<4>(cand));
-      cand = min(cand, lane_xor_i<2>(cand));
-      cand = min(cand, lane_xor_i<1>(cand));
-      if (bj >= 0 && cand == lane + 64 * bj) taken |= 1u << bj;
-      // every rank finds an untaken expert (no NaN compares, K <= E): the K experts are distinct,
-      // so the dispatch order below is a permutation of the slots
-      if (cand >= E) cand = E - 1;  // unreachable; keeps the index addressable
-      if (lane == k) {
-        myv = gmax;
-        mys = cand;
+    // T: the K-th largest key, the largest t with at least K keys >= t, found bit by bit from the
+    // top.  A count of exactly K ends the search early: t then parts the K largest from the rest.
+    // T >= key(-inf) > 0 (K <= E), so no lane past E is selected.
+    uint32_t T = 0u;
+    for (int b = 31; b >= 0; --b) {
+      const uint32_t c = T | (1u << b);
+      const int n = route_count_ge<EPER>(key, c);
+      if (n >= K) {
+        T = c;
+        if (n == K) break;
       }
     }
+    // selected: every key above T, and of the keys equal to T the lowest experts, K in all
+    // (value descending, expert ascending); compacted into LDS in expert order
+    const int need = K - route_count_ge<EPER>(key, T + 1u);
+    int ties = 0, before = 0;
+#pragma unroll
+    for (int j = 0; j < EPER; ++j) {
+      const uint64_t eq = __ballot(key[j] == T);
+      const bool s = key[j] > T || (key[j] == T && ties + lanes_below(eq) < need);
+      const uint64_t sm = __ballot(s);
+      if (s) {
+        const int p = before + lanes_below(sm);
+        ckey[wave][p] = key[j];
+        cidx[wave][p] = lane + 64 * j;
+        cval[wave][p] = v[j];
+      }
+      ties += __popcll(eq);
+      before += __popcll(sm);
+    }
+    // the wave reads what it wrote (LDS operations of one wave complete in order)
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // lane p < K: entry p's rank among the K, then each entry pushed to the lane of its rank
+    int rank = lane;
+    float pv = 0.0f;
+    int pe = 0;
+    if (lane < K) {
+      const uint32_t kp = ckey[wave][lane];
+      rank = 0;
+      for (int q = 0; q < K; ++q) {
+        const uint32_t kq = ckey[wave][q];
+        rank += (kq > kp || (kq == kp && q < lane)) ? 1 : 0;
+      }
+      pv = cval[wave][lane];
+      pe = cidx[wave][lane];
+    }
+    // lane k < K: the k-th selected logit and expert
+    const float myv = __int_as_float(__builtin_amdgcn_ds_permute(rank * 4, __float_as_int(pv)));
+    const int mys = __builtin_amdgcn_ds_permute(rank * 4, pe);
     // softmax over the K selected: exp per lane, sum in rank order (lane values read uniformly)
     const float ev = expf_det(myv - readlane_f(myv, 0));
     float sum = 0.0f;
@@ -298,7 +342,10 @@ __global__ __launch_bounds__(RR_THREADS) void k_moe_router_route(MoeArgs a0, int
     }
   }
   if (!ticket_last(a.ticket, (uint32_t)row_wgs - 1u)) return;
-  route_body(a);
+  if (E <= 512)
+    route_body<8>(a);
+  else
+    route_body<16>(a);
 }
 
 

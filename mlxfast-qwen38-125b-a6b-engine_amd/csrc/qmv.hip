@@ -194,7 +194,7 @@ constexpr int mma_body_chunks() {
   return (NCH <= 12 && NCH % 2 == 0 && (8 * (NCH / 2)) % LC == 0 && NCH / 2 >= B0) ? NCH / 2 : B0;
 }
 
-template <int L, int IT, int C, int TG>
+template <int L, int IT, int C, int TG, bool XPF>
 __global__ __launch_bounds__(MMA_THREADS) void k_qmv_mma(const uint32_t* __restrict__ wq, const uint32_t* __restrict__ sbp,
                                                         int N, int K, int gs, const uint32_t* __restrict__ xp, int M,
                                                         bf16* __restrict__ y, float* __restrict__ yf) {
@@ -235,31 +235,78 @@ __global__ __launch_bounds__(MMA_THREADS) void k_qmv_mma(const uint32_t* __restr
     stg.store(lds);
   }
   __syncthreads();
-  int iter = 0;
-  for (int grp = blockIdx.x; grp < ngroups; grp += gridDim.x, ++iter) {
-    const int tile = grp * TPG + tl;
-    const int row = tile * 16 + n;
-    const uint32_t* wrow = wq + (size_t)(row < N ? row : N - 1) * (K / 8);
-    // this tile's (scale, bias) pairs of the class's blocks q = 0..NQ-1 (block c + C q), gathered into LDS
-    constexpr int NG = (16 * NQ + 63) / 64;
-    uint32_t gv[NG];
+  // this tile's (scale, bias) pairs of the class's blocks q = 0..NQ-1 (block c + C q), gathered into
+  // this wave's LDS region [16][NQ] (pair q of row rr at rr * NQ + q), all at once (gather_all) or
+  // body by body (gather_body, QB blocks each, one body ahead); the weights in bodies of BC
+  // four-block chunks (lane group g: block g of each chunk), one body ahead
+  constexpr int NG = (16 * NQ + 63) / 64;
+  auto gather_all = [&](int tile, uint32_t (&gv)[NG]) {
 #pragma unroll
     for (int k = 0; k < NG; ++k) {
       const int e = lane + 64 * k, rr = e / NQ, q = e - rr * NQ, j = c + C * q;
       const int rw = tile * 16 + rr;
       gv[k] = e < 16 * NQ ? sbp[(size_t)(rw < N ? rw : N - 1) * P + ((j % L) / r) * IT + j / L] : 0u;
     }
-    uint4 wv[2][BC];
-    auto load_body = [&](int ch0, int buf) {
+  };
+  constexpr int QB = 4 * BC;
+  constexpr int NGB = (16 * QB + 63) / 64;
+  auto gather_body = [&](int tile, int body, uint32_t (&gv)[NGB]) {
 #pragma unroll
-      for (int cb = 0; cb < BC; ++cb) wv[buf][cb] = ldg16(wrow + (size_t)(c + C * (4 * (ch0 + cb) + g)) * 4);
-    };
-    asm volatile("" ::: "memory");  // the pair gathers ahead of the weight loads
-    load_body(0, 0);
-    asm volatile("" ::: "memory");
+    for (int k = 0; k < NGB; ++k) {
+      const int e = lane + 64 * k, rr = e / QB, q = body * QB + (e - rr * QB), j = c + C * q;
+      const int rw = tile * 16 + rr;
+      gv[k] = e < 16 * QB ? sbp[(size_t)(rw < N ? rw : N - 1) * P + ((j % L) / r) * IT + j / L] : 0u;
+    }
+  };
+  auto put_body = [&](int body, const uint32_t (&gv)[NGB]) {
 #pragma unroll
-    for (int k = 0; k < NG; ++k)
-      if (lane + 64 * k < 16 * NQ) mysb[lane + 64 * k] = gv[k];  // this wave's region: read back by this wave only
+    for (int k = 0; k < NGB; ++k) {
+      const int e = lane + 64 * k, rr = e / QB, q = body * QB + (e - rr * QB);
+      if (e < 16 * QB) mysb[rr * NQ + q] = gv[k];  // this wave's region: read back by this wave only
+    }
+  };
+  auto row_ptr = [&](int tile) {
+    const int rw = tile * 16 + n;
+    return wq + (size_t)(rw < N ? rw : N - 1) * (K / 8);
+  };
+  uint4 wv[2][BC];
+  auto load_body = [&](const uint32_t* wrow, int ch0, int buf) {
+#pragma unroll
+    for (int cb = 0; cb < BC; ++cb) wv[buf][cb] = ldg16(wrow + (size_t)(c + C * (4 * (ch0 + cb) + g)) * 4);
+  };
+  // XPF (a launch whose workgroups walk several tile groups) with an even number of bodies per
+  // tile: the pairs go body by body, and the last body computes buffer 1 while the next tile
+  // group's first body (buffer 0) is loaded, so a workgroup waits for HBM once, not once per
+  // group.  After its last group a workgroup loads rows 0..15 there instead (no branch around the
+  // loads; cache hits, unused).  Taken with two token groups only: with one, the registers it
+  // needs cost the second workgroup per CU, which hides more (measured).
+  constexpr bool XP = XPF && (NCH / BC) % 2 == 0;
+  uint32_t gvb[NGB];
+  bool pref = false;  // this group's first body in flight from the previous group
+  int iter = 0;
+  for (int grp = blockIdx.x; grp < ngroups; grp += gridDim.x, ++iter) {
+    const int tile = grp * TPG + tl;
+    const int row = tile * 16 + n;
+    const uint32_t* wrow = row_ptr(tile);
+    if constexpr (XP) {
+      if (!pref) {
+        gather_body(tile, 0, gvb);
+        asm volatile("" ::: "memory");  // the pair gathers ahead of the weight loads
+        load_body(wrow, 0, 0);
+        asm volatile("" ::: "memory");
+      }
+    } else {
+      uint32_t gv[NG];
+      gather_all(tile, gv);
+      asm volatile("" ::: "memory");  // the pair gathers ahead of the weight loads
+      load_body(wrow, 0, 0);
+      asm volatile("" ::: "memory");
+#pragma unroll
+      for (int k = 0; k < NG; ++k)
+        if (lane + 64 * k < 16 * NQ) mysb[lane + 64 * k] = gv[k];  // this wave's region: read back by this wave only
+    }
+    const int ngrp = grp + (int)gridDim.x;
+    const bool next = XP && ngrp < ngroups;
     float acc[TG][LC];
 #pragma unroll
     for (int tq = 0; tq < TG; ++tq)
@@ -271,7 +318,21 @@ __global__ __launch_bounds__(MMA_THREADS) void k_qmv_mma(const uint32_t* __restr
       for (int half = 0; half < 2; ++half) {
         const int cbase = ch0 + half * BC;
         if (cbase >= NCH) break;  // uniform
-        if (cbase + BC < NCH) load_body(cbase + BC, half ^ 1);
+        if constexpr (XP) {
+          put_body(cbase / BC, gvb);  // this body's pairs
+          if (cbase + BC < NCH) {
+            gather_body(tile, cbase / BC + 1, gvb);
+            asm volatile("" ::: "memory");
+            load_body(wrow, cbase + BC, half ^ 1);
+          } else if (half == 1) {
+            const int nt = next ? ngrp * TPG + tl : 0;
+            gather_body(nt, 0, gvb);
+            asm volatile("" ::: "memory");
+            load_body(row_ptr(nt), 0, 0);
+          }
+        } else {
+          if (cbase + BC < NCH) load_body(wrow, cbase + BC, half ^ 1);
+        }
 #pragma unroll
         for (int cb = 0; cb < BC; ++cb) {
           const int ch = cbase + cb;
@@ -306,6 +367,7 @@ __global__ __launch_bounds__(MMA_THREADS) void k_qmv_mma(const uint32_t* __restr
         asm volatile("" ::: "memory");  // one body's operands live at a time (no LDS reads hoisted across)
       }
     }
+    pref = next;
     float v[TG];
 #pragma unroll
     for (int tq = 0; tq < TG; ++tq) {
@@ -1033,12 +1095,22 @@ static hipError_t qmv_mma_c(const uint32_t* wq, const uint32_t* sb, int N, int K
   const int slots = per_cu * device_cus();
   const int nwin = (M + MMA_TOK * TG - 1) / (MMA_TOK * TG);
   if (nwin == 1 && TG > 1 && groups > slots && groups < 4 * slots) return hipErrorNotReady;
-  static size_t cur = 0;
-  hipError_t e = ensure_lds(k_qmv_mma<L, IT, C, TG>, lds, cur);
-  if (e != hipSuccess) return e;
   const int grid = nwin > 1 ? (groups + 7) / 8 * 8 : groups < slots ? groups : slots;
-  hipLaunchKernelGGL((k_qmv_mma<L, IT, C, TG>), dim3(grid, nwin), dim3(MMA_THREADS), lds, st, wq, sb, N, K, gs, xp, M,
-                     y, yf);
+  if constexpr (TG == 2) {  // two token groups (one workgroup per CU)
+    if (nwin == 1 && groups >= 2 * grid) {  // workgroups walk several tile groups: the next one's first body in flight
+      static size_t cur = 0;
+      hipError_t e = ensure_lds(k_qmv_mma<L, IT, C, TG, true>, lds, cur);
+      if (e != hipSuccess) return e;
+      hipLaunchKernelGGL((k_qmv_mma<L, IT, C, TG, true>), dim3(grid, nwin), dim3(MMA_THREADS), lds, st, wq, sb, N, K,
+                         gs, xp, M, y, yf);
+      return hipGetLastError();
+    }
+  }
+  static size_t cur = 0;
+  hipError_t e = ensure_lds(k_qmv_mma<L, IT, C, TG, false>, lds, cur);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL((k_qmv_mma<L, IT, C, TG, false>), dim3(grid, nwin), dim3(MMA_THREADS), lds, st, wq, sb, N, K, gs,
+                     xp, M, y, yf);
   return hipGetLastError();
 }
 

@@ -70,6 +70,8 @@ def test_randn_deterministic_and_normal(ctx):
     # matrix-core path (2..4 tokens per launch, packed pairs): the model's dense shapes, ragged rows
     (16480, 2560, 64, 4), (2560, 6144, 64, 4), (1000, 2560, 64, 3), (2560, 6144, 32, 2), (4096, 2048, 64, 4),
     (520, 10240, 64, 4), (2560, 2560, 32, 5),
+    # one token group, several tile groups per workgroup: ragged rows
+    (66001, 2560, 64, 3), (65550, 2560, 32, 4),
     # two token groups in one launch (5..8 tokens): ragged rows, several tile groups per workgroup
     (16480, 2560, 64, 6), (1000, 2560, 64, 8), (66000, 2560, 64, 5), (4096, 2048, 64, 8), (13440, 2560, 32, 7),
 ])

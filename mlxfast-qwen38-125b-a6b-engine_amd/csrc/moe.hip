@@ -93,8 +93,11 @@ __device__ __forceinline__ int route_count_ge(const uint32_t (&key)[EPER], uint3
   return n;
 }
 
-// EPER = ceil(E / 64) rounded up to 8 or 16: the logits per lane (expert lane + 64 j in register j)
-template <int EPER>
+// EPER = ceil(E / 64) rounded up to 8 or 16: the logits per lane (expert lane + 64 j in register j).
+// POLL: the logits come from the publish buffer a.pub, each token's wave loading them until none is
+// the sentinel (at most ROUTE_SPIN polls), then copying them to a.logits and putting the sentinel
+// back for the next launch; else from a.logits, complete (the ticket).
+template <int EPER, bool POLL>
 __device__ void route_body(const MoeArgs& a) {
   const int E = a.E, K = a.K, M = a.M;
   const int MK = M * K;
@@ -112,14 +115,41 @@ __device__ void route_body(const MoeArgs& a) {
   for (int i = threadIdx.x; i < E; i += blockDim.x) first[i] = 0x7fffffff;
   for (int i = threadIdx.x; i < MAX_TOKENS * 32; i += blockDim.x) (&tokbits[0][0])[i] = 0u;
   if (wave < M) {
-    const float* lr = a.logits + (size_t)wave * E;
+    float x[EPER];
+    if constexpr (POLL) {
+      float* pr = a.pub + (size_t)wave * E;
+      for (int spin = 0; spin < ROUTE_SPIN; ++spin) {
+        bool ready = true;
+#pragma unroll
+        for (int j = 0; j < EPER; ++j) {
+          const int e = lane + 64 * j;
+          x[j] = (e < E) ? ld_pub(pr + e) : 0.0f;
+          ready = ready && (e >= E || __float_as_uint(x[j]) != ROUTE_SENTINEL);
+        }
+        if (__all(ready)) break;
+      }
+#pragma unroll
+      for (int j = 0; j < EPER; ++j) {
+        const int e = lane + 64 * j;
+        if (e < E) {
+          a.logits[(size_t)wave * E + e] = x[j];
+          pr[e] = __uint_as_float(ROUTE_SENTINEL);
+        }
+      }
+    } else {
+      const float* lr = a.logits + (size_t)wave * E;
+#pragma unroll
+      for (int j = 0; j < EPER; ++j) {
+        const int e = lane + 64 * j;
+        x[j] = (e < E) ? ld_pub(lr + e) : 0.0f;
+      }
+    }
     float v[EPER];
     uint32_t key[EPER];
 #pragma unroll
     for (int j = 0; j < EPER; ++j) {
       const int e = lane + 64 * j;
-      const float x = (e < E) ? ld_pub(lr + e) : 0.0f;
-      v[j] = (e < E && x == x) ? x : -__uint_as_float(0x7f800000u);  // a NaN logit ranks as -inf
+      v[j] = (e < E && x[j] == x[j]) ? x[j] : -__uint_as_float(0x7f800000u);  // a NaN logit ranks as -inf
       key[j] = e < E ? route_key(v[j]) : 0u;
     }
     // T: the K-th largest key, the largest t with at least K keys >= t, found bit by bit from the
@@ -275,14 +305,24 @@ __device__ __forceinline__ void shared_gate_q4(const MoeArgs& a, uint32_t* __res
   if (sub == 0 && grp < M) a.gate_logit[grp] = v;
 }
 
-// GL = 0: the gate is router row E (bf16); GL > 0: the q4 row, computed by the grid's last workgroup.
+// GL = 0: the gate is router row E (bf16); GL > 0: the q4 row, computed by the workgroup after the
+// row and preparation workgroups.  route_wg >= 0 (one window): the grid's last workgroup routes,
+// polling the publish buffer (dispatched last, every row workgroup is resident or done before it
+// starts, so its wait ends); route_wg < 0: the last row workgroup to take the ticket routes.
 template <int GL, int GIT>
-__global__ __launch_bounds__(RR_THREADS) void k_moe_router_route(MoeArgs a0, int row_wgs) {
+__global__ __launch_bounds__(RR_THREADS) void k_moe_router_route(MoeArgs a0, int row_wgs, int route_wg) {
   const MoeArgs a = moe_window(a0, blockIdx.y);
   const int H = a.H, E = a.E, M = a.M;
   extern __shared__ uint4 xs[];  // [M, H/8] (the router rows); the gate workgroup: [M][H/32][XP_DW]
+  if ((int)blockIdx.x == route_wg) {
+    if (E <= 512)
+      route_body<8, true>(a);
+    else
+      route_body<16, true>(a);
+    return;
+  }
   if constexpr (GL > 0) {
-    if (blockIdx.x == gridDim.x - 1) {
+    if ((int)blockIdx.x == (route_wg >= 0 ? route_wg : (int)gridDim.x) - 1) {
       shared_gate_q4<GL, GIT>(a, reinterpret_cast<uint32_t*>(xs));
       return;
     }
@@ -335,17 +375,18 @@ __global__ __launch_bounds__(RR_THREADS) void k_moe_router_route(MoeArgs a0, int
       acc = wave_fold64(acc);
       if (lane == 0) {
         if (r < E)
-          st_pub(a.logits + (size_t)m * E + r, acc);
+          st_pub((route_wg >= 0 ? a.pub : a.logits) + (size_t)m * E + r, acc);
         else
           a.gate_logit[m] = acc;
       }
     }
   }
+  if (route_wg >= 0) return;
   if (!ticket_last(a.ticket, (uint32_t)row_wgs - 1u)) return;
   if (E <= 512)
-    route_body<8>(a);
+    route_body<8, false>(a);
   else
-    route_body<16>(a);
+    route_body<16, false>(a);
 }
 
 
@@ -780,13 +821,15 @@ static hipError_t router_route_go(const MoeArgs& a, hipStream_t st) {
   const int rows = GL > 0 ? a.E : a.E + 1;  // the bf16 gate row rides as router row E
   const int row_wgs = (rows + RR_THREADS / 64 - 1) / (RR_THREADS / 64);
   const int prep_wgs = a.xp_ready ? 0 : (a.M * (a.H / 32) + RR_THREADS / 32 - 1) / (RR_THREADS / 32);
+  const int gx = row_wgs + prep_wgs + (GL > 0 ? 1 : 0);
+  const bool poll = a.pub && a.nwin == 1;
   size_t lds = (size_t)a.M * a.H * 2;  // the staged activations
   if (GL > 0) lds = std::max(lds, (size_t)a.M * (a.H / 32) * XP_DW * 4);  // the gate's prepared blocks
   static size_t cur = 0;
   const hipError_t e = ensure_lds(k_moe_router_route<GL, GIT>, lds + 16 * 1024, cur);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((k_moe_router_route<GL, GIT>), dim3(row_wgs + prep_wgs + (GL > 0 ? 1 : 0), a.nwin),
-                     dim3(RR_THREADS), lds, st, a, row_wgs);
+  hipLaunchKernelGGL((k_moe_router_route<GL, GIT>), dim3(gx + (poll ? 1 : 0), a.nwin), dim3(RR_THREADS), lds, st, a,
+                     row_wgs, poll ? gx : -1);
   return hipGetLastError();
 }
 

@@ -55,6 +55,7 @@ struct Ctx {
   bool ws_over = false;              // a take ran past the reservation (see ws_take)
   MoeDispatch* last_disp = nullptr;  // inside the workspace of the last MoE call
   uint32_t* tickets = nullptr;       // MOE_TICKETS counters, zero at rest
+  float* route_pub = nullptr;        // [MAX_TOKENS, MAX_EXPERTS] router logits publish buffer, ROUTE_SENTINEL at rest
   void* scratch = nullptr;           // this device's MoE scratch array (noalloc.hip), looked up at set-up
   int last_H = 0, last_E = 0, last_F = 0, last_gs = 0;
   // per-kernel timing with events on the launch stream (off by default)
@@ -267,6 +268,7 @@ int moe_enqueue(Ctx* c, const mtpx_moe_weights* w, const uint16_t* x, int M, uin
   a.resid = resid;
   a.y2 = y2;
   a.ticket = c->tickets;
+  a.pub = nwin == 1 ? c->route_pub : nullptr;
   a.nu_out = nu_out;
   c->last_disp = a.disp;
   c->last_H = a.H;
@@ -1407,14 +1409,19 @@ int mtpx_ctx_new(mtpx_ctx* out, int device) {
     return fail(MTPX_ERR_HIP, "stream creation failed on device %d", device);
   }
   c->stream = c->own;
-  // ticket counters of the fused MoE launches: zeroed once, every launch leaves them at zero
-  if (hipMalloc((void**)&c->tickets, MOE_TICKETS * 4) != hipSuccess ||
-      hipMemset(c->tickets, 0, MOE_TICKETS * 4) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
+  // ticket counters of the fused MoE launches, zeroed once (every launch leaves them at zero), and the
+  // router logits' publish buffer, all sentinel once (every route puts it back)
+  const size_t pub_bytes = (size_t)MAX_TOKENS * MAX_EXPERTS * 4;
+  if (hipMalloc((void**)&c->tickets, MOE_TICKETS * 4 + pub_bytes) != hipSuccess ||
+      hipMemset(c->tickets, 0, MOE_TICKETS * 4) != hipSuccess ||
+      hipMemset(c->tickets + MOE_TICKETS, 0xff, pub_bytes) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
     if (c->tickets) hipFree(c->tickets);
     hipStreamDestroy(c->own);
     delete c;
     return fail(MTPX_ERR_HIP, "ticket allocation failed on device %d", device);
   }
+  static_assert(ROUTE_SENTINEL == 0xffffffffu, "the publish buffer is filled with 0xff bytes");
+  c->route_pub = reinterpret_cast<float*>(c->tickets + MOE_TICKETS);
   const hipError_t se = moe_scratch_address(device, &c->scratch);
   if (se != hipSuccess) {
     hipFree(c->tickets);

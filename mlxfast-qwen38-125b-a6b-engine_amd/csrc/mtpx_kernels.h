@@ -137,6 +137,9 @@ struct MoeArgs {
   const bf16* resid;   // [M, H] or null: y2 = bf16(resid + y)
   bf16* y2;            // [M, H] or null
   uint32_t* ticket;    // router+route ticket, zero at rest
+  // one window: the router logits' publish buffer [MAX_TOKENS, MAX_EXPERTS], every word
+  // ROUTE_SENTINEL at rest (the route puts it back), polled by the route; null: the ticket
+  float* pub = nullptr;
   int32_t* nu_out;     // if set: the route also writes the distinct routed expert count here
   // windows of M tokens in one launch (a prefill batch): window w's tokens, slots, dispatch table,
   // ticket and count follow window w-1's, each window routed and computed as its own launch would
@@ -161,6 +164,11 @@ bool moe_qmm_supported(const MoeArgs& a);
 hipError_t launch_moe_qmm_down(const MoeArgs& a, hipStream_t st);
 
 constexpr int MOE_TICKETS = 64;
+constexpr int MAX_EXPERTS = 1024;
+// A logit never has these bits: a NaN the GEMV makes carries the payload of a bf16 operand (low 16
+// bits zero) or the default NaN's.
+constexpr uint32_t ROUTE_SENTINEL = 0xffffffffu;
+constexpr int ROUTE_SPIN = 1 << 20;  // polls of the publish buffer before the route goes on regardless
 hipError_t launch_moe_router_route(const MoeArgs& a, hipStream_t st);
 hipError_t launch_moe_gate_up(const MoeArgs& a, hipStream_t st);
 hipError_t launch_moe_down(const MoeArgs& a, hipStream_t st);

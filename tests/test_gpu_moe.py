@@ -190,6 +190,38 @@ def test_moe_router_ties_within_and_across_lanes(ctx, E):
     assert list(got[2][:len(lead)]) == lead
 
 
+def test_moe_back_to_back_windows_route_their_own_logits():
+    """One-window launches hand the router logits to the route through a per-context buffer that each
+    route puts back to its sentinel: windows enqueued back to back on a fresh context (different
+    tokens, widths and expert counts, no synchronisation between them) each route their own logits."""
+    print("case back-to-back routes", flush=True)
+    need_gpu()
+    import mtpx
+    c = mtpx.Context(0)
+    try:
+        H, K, F, gs = 256, 10, 64, 32
+        runs = []
+        for i, (E, M) in enumerate([(512, 4), (512, 4), (1024, 8), (512, 2), (1024, 1), (512, 8)]):
+            w = make_moe(90 + E, H, E, K, F, gs)
+            x = rand_bf16(np.random.default_rng(900 + i), (M, H), 1.0)
+            dw = {n: dev(w[n]) for n in NAMES}
+            mw = mtpx.moe_weights_from(dw, H, E, K, F, gs)
+            out = (empty_bf16(M, H), torch.zeros(M, K, dtype=torch.int32, device="cuda"),
+                   torch.zeros(M, K, dtype=torch.float32, device="cuda"),
+                   torch.zeros(M, E, dtype=torch.float32, device="cuda"))
+            c.moe_forward(mw, dev(x), *out)
+            runs.append((w, x, E, M, out, dw))
+        c.synchronize()
+        for w, x, E, M, (y, idx, wt, lg), _ in runs:
+            ref = O.moe_block(w, x, H, E, K, F, gs)
+            assert np.array_equal(host(lg).view(np.uint32), ref["logits"].view(np.uint32))
+            assert np.array_equal(host(idx), ref["idx"])
+            assert np.array_equal(host(wt).view(np.uint32), ref["w"].view(np.uint32))
+            assert np.array_equal(host(y), ref["y"])
+    finally:
+        c.close()
+
+
 @pytest.mark.parametrize("H,E,K,F,gs,M", [(4096, 12, 4, 256, 64, 8), (1024, 16, 4, 320, 32, 5),
                                           (512, 8, 2, 1024, 32, 3)])
 def test_moe_other_depths_bit_exact(ctx, H, E, K, F, gs, M):

@@ -77,6 +77,12 @@ __device__ __forceinline__ float half_wave_sum(float v) {
   return fold_sum<16>(v);
 }
 
+// Element c of four bf16 packed in two words (little-endian), as a float.
+__device__ __forceinline__ float kjournal(uint2 w, int c) {
+  const uint32_t v = c < 2 ? w.x : w.y;
+  return __uint_as_float((c & 1) ? (v & 0xffff0000u) : (v << 16));
+}
+
 // Row r of the virtual input sequence conv_cur (KC-1 rows) ++ the P committed
 // journal rows ++ the window's projection rows.
 __device__ __forceinline__ float gdn_row(const GdnArgs& a, int r, int ch) {
@@ -123,21 +129,40 @@ __global__ __launch_bounds__(GDN_THREADS) void k_gdn_step(GdnArgs a) {
     s[i][2] = s4.z;
     s[i][3] = s4.w;
   }
-  float gdp[MAX_TOKENS], kpp[MAX_TOKENS][4], dlp[MAX_TOKENS][RPH];
+  float gdp[MAX_TOKENS], dlp[MAX_TOKENS][RPH];
+  uint2 kpw[MAX_TOKENS];  // the journal keys' four bf16 (raw until the replay, so no wait for them here)
   if (P > 0) {
 #pragma unroll
     for (int p = 0; p < MAX_TOKENS; ++p) {
       const int pc = p < P ? p : P - 1;  // clamped: loads beyond P are issued but not used
       gdp[p] = a.decay_cur[(size_t)pc * a.hv + h];
-      const uint2 kw = *reinterpret_cast<const uint2*>(a.key_cur + ((size_t)pc * a.hk + hk) * GDN_D + 4 * l);
-      kpp[p][0] = __uint_as_float(kw.x << 16);
-      kpp[p][1] = __uint_as_float(kw.x & 0xffff0000u);
-      kpp[p][2] = __uint_as_float(kw.y << 16);
-      kpp[p][3] = __uint_as_float(kw.y & 0xffff0000u);
+      kpw[p] = *reinterpret_cast<const uint2*>(a.key_cur + ((size_t)pc * a.hk + hk) * GDN_D + 4 * l);
 #pragma unroll
       for (int i = 0; i < RPH; ++i) dlp[p][i] = a.delta_cur[((size_t)pc * a.hv + h) * GDN_D + r0 + hw + 16 * i];
     }
   }
+
+  // The inputs of the prep's last steps, loaded now so their latency hides behind the loads above
+  // and the conv's: the positions' gate inputs (position t: thread GDN_THREADS - S + t, the last
+  // wave, which has no conv task up to five positions) and, in a head's first workgroup, the conv
+  // rows R[P .. P+KC-1) that become the next window's base (element i = (j, kind, d)).
+  // (every thread loads, position 0 outside the gate threads, no branch; raw bf16 bits until the
+  // use, so nothing waits for them here)
+  const int gt = (int)threadIdx.x - (GDN_THREADS - S);  // this thread's gate position, or < 0
+  const uint16_t* prow = reinterpret_cast<const uint16_t*>(a.proj) + (size_t)(gt >= 0 ? gt : 0) * a.pw;
+  const uint32_t g_b = prow[a.b_off + h], g_a = prow[a.a_off + h];
+  const uint32_t g_dt = reinterpret_cast<const uint16_t*>(a.dt_bias)[h];
+  const float g_al = a.neg_exp_alog[h];
+  constexpr int CN = ((KC - 1) * 3 * GDN_D + GDN_THREADS - 1) / GDN_THREADS;
+  bf16 cb[CN];
+#pragma unroll
+  for (int q = 0; q < CN; ++q) {
+    const int i = (int)threadIdx.x + q * GDN_THREADS;
+    const int j = i / (3 * GDN_D), kind = (i / GDN_D) % 3, d = i % GDN_D;
+    const int vec = kind == 0 ? hk : (kind == 1 ? a.hk + hk : 2 * a.hk + h);
+    cb[q] = (w0 && i < KM1 * 3 * GDN_D && (kind == 2 || lead)) ? gdn_row_ptr(a, P + j)[vec * GDN_D + d] : (bf16)0;
+  }
+  asm volatile("" ::: "memory");
 
   // ---- prep: (q, k, v) vectors x positions, 32 lanes x 4 channels each; a lane's KC input rows
   // (4 channels each) and its 4 x KC conv taps are loaded before the first multiply
@@ -186,23 +211,22 @@ __global__ __launch_bounds__(GDN_THREADS) void k_gdn_step(GdnArgs a) {
       for (int i = 0; i < 4; ++i) vs[t][4 * l + i] = xs[i];
     }
   }
-  if ((int)threadIdx.x < S) {
-    const int t = threadIdx.x;
-    const bf16* prow = a.proj + (size_t)t * a.pw;
-    const float b = sigmoid_bf16(bf2f(prow[a.b_off + h]));
-    const float ax = round_bf(bf2f(prow[a.a_off + h]) + bf2f(a.dt_bias[h]));
-    const float d = expf_det(a.neg_exp_alog[h] * logaddexp0_bf16(ax));
+  if (gt >= 0) {
+    const int t = gt;
+    const float b = sigmoid_bf16(__uint_as_float(g_b << 16));
+    const float ax = round_bf(__uint_as_float(g_a << 16) + __uint_as_float(g_dt << 16));
+    const float d = expf_det(g_al * logaddexp0_bf16(ax));
     dec[t] = d;
     bet[t] = b;
     if (w0) a.decay_nxt[(size_t)t * a.hv + h] = d;
   }
   // the committed conv rows R[P .. P+KC-1) become the next window's base
-  for (int i = threadIdx.x; i < (w0 ? KM1 * 3 * GDN_D : 0); i += GDN_THREADS) {
+#pragma unroll
+  for (int q = 0; q < CN; ++q) {
+    const int i = (int)threadIdx.x + q * GDN_THREADS;
     const int j = i / (3 * GDN_D), kind = (i / GDN_D) % 3, d = i % GDN_D;
-    if (kind < 2 && !lead) continue;
     const int vec = kind == 0 ? hk : (kind == 1 ? a.hk + hk : 2 * a.hk + h);
-    const int ch = vec * GDN_D + d;
-    a.conv_nxt[(size_t)j * a.cd + ch] = f2bf(gdn_row(a, P + j, ch));
+    if (w0 && i < KM1 * 3 * GDN_D && (kind == 2 || lead)) a.conv_nxt[(size_t)j * a.cd + vec * GDN_D + d] = cb[q];
   }
   __syncthreads();
 
@@ -216,7 +240,7 @@ __global__ __launch_bounds__(GDN_THREADS) void k_gdn_step(GdnArgs a) {
 #pragma unroll
           for (int c = 0; c < 4; ++c) {
             s[i][c] = s[i][c] * gdp[p];
-            s[i][c] = __builtin_fmaf(kpp[p][c], dlp[p][i], s[i][c]);
+            s[i][c] = __builtin_fmaf(kjournal(kpw[p], c), dlp[p][i], s[i][c]);
           }
       }
     }

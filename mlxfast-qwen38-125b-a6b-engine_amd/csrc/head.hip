@@ -45,11 +45,11 @@ __global__ __launch_bounds__(256) void k_embed_rows(const uint32_t* __restrict__
   for (int i = 0; i < 8; ++i) o[i] = f2bf(round_bf(scale * (float)((w >> (4 * i)) & 0xfu)) + bias);
 }
 
-// grid (hc, S, ceil(H/256)), 256 threads; H <= 256 * IT (EXACT: H == 256 * IT).
-// Every load is issued up front and unconditionally (clamped indices; a
-// missing `out` reads the residual row instead and is not used), so the
-// residual and the sublayer output arrive in one round trip.
-template <int IT, bool EXACT>
+// grid (hc, S, ceil(H/256)), 256 threads; H <= 256 * IT (EXACT: H == 256 * IT).  MODE 0: stream =
+// residual; 1: + out; 2: + bf16(out * inject).  Every load is issued up front and unconditionally
+// (clamped indices) and kept as raw bf16 bits until its use, so the residual and sublayer rows, the
+// inject value and the norm scale arrive in one round trip.
+template <int IT, bool EXACT, int MODE>
 __global__ __launch_bounds__(256) void k_hc_norm(const bf16* __restrict__ residual, const bf16* __restrict__ out,
                                                  const bf16* __restrict__ inject, int hc, int H, int tile,
                                                  const bf16* __restrict__ scale, float eps,
@@ -60,26 +60,29 @@ __global__ __launch_bounds__(256) void k_hc_norm(const bf16* __restrict__ residu
   const size_t W = (size_t)hc * H;
   const size_t base = (size_t)s * W + (size_t)c * H;
   const bf16* rr = tile ? residual + (size_t)s * H : residual + base;
-  const bool has_out = out != nullptr, has_inj = has_out && inject != nullptr;
-  const bf16* orow = has_out ? out + (size_t)s * H : rr;
-  const float inj = bf2f(inject ? inject[(size_t)s * hc + c] : (bf16)0);
+  const bf16* orow = MODE > 0 ? out + (size_t)s * H : rr;
+  const int d = sl * 256 + t;
+  const uint32_t injb = MODE == 2 ? (uint32_t)inject[(size_t)s * hc + c] : 0u;
+  const uint32_t scb = scale[(size_t)c * H + (d < H ? d : H - 1)];
   bf16 rv[IT], ov[IT];
 #pragma unroll
   for (int j = 0; j < IT; ++j) {
-    const int d = t + 256 * j;
-    const int dd = EXACT ? d : (d < H ? d : H - 1);
+    const int dj = t + 256 * j;
+    const int dd = EXACT ? dj : (dj < H ? dj : H - 1);
     rv[j] = rr[dd];
-    ov[j] = orow[dd];
+    if (MODE > 0) ov[j] = orow[dd];
   }
+  asm volatile("" ::: "memory");
+  const float inj = __uint_as_float(injb << 16);
   float v[IT];
   float acc = 0.0f, vo = 0.0f;
 #pragma unroll
   for (int j = 0; j < IT; ++j) {
     const bool in = EXACT || t + 256 * j < H;
     float x = bf2f(rv[j]);
-    if (has_out) {
+    if (MODE > 0) {
       const float o = bf2f(ov[j]);
-      x = round_bf(x + (has_inj ? round_bf(o * inj) : o));
+      x = round_bf(x + (MODE == 2 ? round_bf(o * inj) : o));
     }
     v[j] = in ? x : 0.0f;
     if (in) acc = __builtin_fmaf(v[j], v[j], acc);
@@ -90,11 +93,10 @@ __global__ __launch_bounds__(256) void k_hc_norm(const bf16* __restrict__ residu
   __syncthreads();
   const float total = ((wsum[0] + wsum[1]) + wsum[2]) + wsum[3];
   const float inv = 1.0f / sqrtf(total / (float)H + eps);
-  const int d = sl * 256 + t;
   bf16 n = 0;
   if (d < H) {
     if (stream) stream[base + d] = f2bf(vo);
-    n = f2bf(bf2f(scale[(size_t)c * H + d]) * round_bf(vo * inv));
+    n = f2bf(__uint_as_float(scb << 16) * round_bf(vo * inv));
     if (normed) normed[base + d] = n;
   }
   // blocks of the normed row [S, hc*H]: H % 32 == 0, so a block never straddles streams
@@ -142,19 +144,31 @@ hipError_t launch_embed_rows(const uint32_t* wq, const bf16* s, const bf16* b, i
   return hipGetLastError();
 }
 
+template <int IT, bool EXACT>
+static void hc_norm_mode(const dim3& grid, const bf16* residual, const bf16* out, const bf16* inject, int hc, int H,
+                         int tile, const bf16* scale, float eps, bf16* stream, bf16* normed, uint32_t* xp,
+                         hipStream_t st) {
+  if (!out)
+    hipLaunchKernelGGL((k_hc_norm<IT, EXACT, 0>), grid, dim3(256), 0, st, residual, out, inject, hc, H, tile, scale,
+                       eps, stream, normed, xp);
+  else if (!inject)
+    hipLaunchKernelGGL((k_hc_norm<IT, EXACT, 1>), grid, dim3(256), 0, st, residual, out, inject, hc, H, tile, scale,
+                       eps, stream, normed, xp);
+  else
+    hipLaunchKernelGGL((k_hc_norm<IT, EXACT, 2>), grid, dim3(256), 0, st, residual, out, inject, hc, H, tile, scale,
+                       eps, stream, normed, xp);
+}
+
 hipError_t launch_hc_norm(const bf16* residual, const bf16* out, const bf16* inject, int S, int hc, int H,
                           int tile, const bf16* scale, float eps, bf16* stream, bf16* normed, uint32_t* xp,
                           hipStream_t st) {
   const dim3 grid(hc, S, (H + 255) / 256);
   if (H == 2560)
-    hipLaunchKernelGGL((k_hc_norm<10, true>), grid, dim3(256), 0, st, residual, out, inject, hc, H, tile, scale, eps,
-                       stream, normed, xp);
+    hc_norm_mode<10, true>(grid, residual, out, inject, hc, H, tile, scale, eps, stream, normed, xp, st);
   else if (H <= 256 * 16)
-    hipLaunchKernelGGL((k_hc_norm<16, false>), grid, dim3(256), 0, st, residual, out, inject, hc, H, tile, scale,
-                       eps, stream, normed, xp);
+    hc_norm_mode<16, false>(grid, residual, out, inject, hc, H, tile, scale, eps, stream, normed, xp, st);
   else
-    hipLaunchKernelGGL((k_hc_norm<48, false>), grid, dim3(256), 0, st, residual, out, inject, hc, H, tile, scale,
-                       eps, stream, normed, xp);
+    hc_norm_mode<48, false>(grid, residual, out, inject, hc, H, tile, scale, eps, stream, normed, xp, st);
   return hipGetLastError();
 }
 

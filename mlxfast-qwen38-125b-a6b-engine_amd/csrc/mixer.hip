@@ -26,7 +26,16 @@ namespace mtpx {
 
 constexpr int MIX_THREADS = 256;
 
-template <int L, int IT>
+// SBM, the scale/bias layout the launch reads: 1 the packed pair rows (every matrix of the launch has
+// them), 0 the checkpoint's scale and bias rows (always present; the same values).  One load path per
+// launch, so no load waits at a join of the two.
+template <int SBM, int L, int IT>
+__device__ __forceinline__ void mix_row_load(QRow<L, IT>& R, const uint32_t* wrow, const bf16* srow, const bf16* brow,
+                                             const uint32_t* sbrow, int nb, int gs, int sub, bool valid) {
+  R.template load_as<SBM == 1>(wrow, srow, brow, sbrow, nb, gs, sub, valid);
+}
+
+template <int SBM, int L, int IT>
 __global__ __launch_bounds__(MIX_THREADS) __attribute__((amdgpu_waves_per_eu(1, 2))) void k_mix_down(MixArgs a,
                                                                                                     int tsplit) {
   static_assert(IT > 0, "exact lane tiling");
@@ -62,7 +71,7 @@ __global__ __launch_bounds__(MIX_THREADS) __attribute__((amdgpu_waves_per_eu(1, 
   // stage the class's blocks with LDS-direct loads: compact block c = subc' + LC * it holds
   // block g + Q * subc' + L * it; unit i = (s * ncb + c) * 7 + q
   QRow<L, IT> R;
-  R.load(wq + (size_t)rr * (W / 8), sc + (size_t)rr * ng, bi + (size_t)rr * ng, sb ? sb + (size_t)rr * P : nullptr,
+  mix_row_load<SBM>(R, wq + (size_t)rr * (W / 8), sc + (size_t)rr * ng, bi + (size_t)rr * ng, sb ? sb + (size_t)rr * P : nullptr,
          nb, a.gs, sub, valid);
   asm volatile("" ::: "memory");
   const int n4 = S * ncb * (XP_DW / 4);
@@ -101,7 +110,7 @@ __device__ __forceinline__ float class_fold_v(const float* v) {
 // the second reads the up rows from that L2).
 constexpr int UP_THREADS = 512;
 
-template <int QD, int L, int IT>
+template <int QD, int SBM, int L, int IT>
 __global__ __launch_bounds__(UP_THREADS) __attribute__((amdgpu_waves_per_eu(1, 2))) void k_mix_up(MixArgs a,
                                                                                                   int tsplit) {
   constexpr int RW = 64 / L;
@@ -157,8 +166,8 @@ __global__ __launch_bounds__(UP_THREADS) __attribute__((amdgpu_waves_per_eu(1, 2
     const int lr = p * 4 * RW + wave * RW + grp;
     const bool v = lr < nrows;
     const int gr = v ? (lr / 32) * H + d0 + (lr % 32) : 0;
-    U[p].load(a.uw + (size_t)gr * (LW / 8), a.us + (size_t)gr * ng, a.ub + (size_t)gr * ng,
-              a.usb ? a.usb + (size_t)gr * P : nullptr, nbA, a.gs, sub, v);
+    mix_row_load<SBM>(U[p], a.uw + (size_t)gr * (LW / 8), a.us + (size_t)gr * ng, a.ub + (size_t)gr * ng,
+                      a.usb ? a.usb + (size_t)gr * P : nullptr, nbA, a.gs, sub, v);
   }
   // low-rank rows: finish the fold, round, SiLU, and the prepared blocks straight from the registers:
   // item i = t + u * UP_THREADS is element i % 32 of block i / 32, and the 32 lanes of a block are 32
@@ -220,35 +229,54 @@ static hipError_t mix_down_li(const MixArgs& a, hipStream_t st) {
     const int tsplit = a.S >= 2 ? 2 : 1;
     const int per = (a.S + tsplit - 1) / tsplit;
     const size_t lds = (size_t)per * (W / 32 / Q) * XP_DW * 4;
-    static size_t cur = 0;
-    hipError_t e = ensure_lds(k_mix_down<L, IT>, lds, cur);
-    if (e != hipSuccess) return e;
     const int nrb = (NR + RPB - 1) / RPB;
-    hipLaunchKernelGGL((k_mix_down<L, IT>), dim3((nrb + 7) / 8 * 8 * Q * tsplit), dim3(MIX_THREADS), lds, st, a,
-                       tsplit);
-    return hipGetLastError();
+    const dim3 grid((nrb + 7) / 8 * 8 * Q * tsplit);
+    auto go = [&](auto kern, size_t& cur) {
+      hipError_t e = ensure_lds(kern, lds, cur);
+      if (e != hipSuccess) return e;
+      hipLaunchKernelGGL(kern, grid, dim3(MIX_THREADS), lds, st, a, tsplit);
+      return hipGetLastError();
+    };
+    static size_t cur0 = 0, cur1 = 0;
+    if (a.dsb && (!a.iw || a.isb)) return go(k_mix_down<1, L, IT>, cur1);
+    return go(k_mix_down<0, L, IT>, cur0);
+  }
+}
+
+template <int QD, int SBM, int L, int IT>
+static hipError_t mix_up_go(const MixArgs& a, hipStream_t st) {
+  // (as the down launch: two parts from two tokens on; four parts need two rounds of these workgroups)
+  const int tsplit = a.S >= 2 ? 2 : 1;
+  hipLaunchKernelGGL((k_mix_up<QD, SBM, L, IT>), dim3((a.H / 32 + 7) / 8 * 8 * tsplit), dim3(UP_THREADS), 0, st, a,
+                     tsplit);
+  return hipGetLastError();
+}
+
+// The up rows' lane rule over K = LW: at most 4 lanes a row (mix_supported), so only those walkers.
+template <int QD, int SBM>
+static hipError_t mix_up_lw(const MixArgs& a, hipStream_t st) {
+  const int nb = a.LW / 32, L = lanes_for_blocks(nb), IT = nb % L == 0 ? nb / L : 0;
+  switch (L * 16 + (IT >= 4 && IT <= 7 ? IT : 0)) {
+    case 2 * 16 + 4: return mix_up_go<QD, SBM, 2, 4>(a, st);
+    case 2 * 16 + 5: return mix_up_go<QD, SBM, 2, 5>(a, st);
+    case 4 * 16 + 4: return mix_up_go<QD, SBM, 4, 4>(a, st);
+    case 4 * 16 + 5: return mix_up_go<QD, SBM, 4, 5>(a, st);
+    case 4 * 16 + 6: return mix_up_go<QD, SBM, 4, 6>(a, st);
+    default: break;
+  }
+  switch (L) {
+    case 1: return mix_up_go<QD, SBM, 1, 0>(a, st);
+    case 2: return mix_up_go<QD, SBM, 2, 0>(a, st);
+    default: return mix_up_go<QD, SBM, 4, 0>(a, st);
   }
 }
 
 template <int QD>
-struct MixUp {
-  template <int L, int IT>
-  static hipError_t go(const MixArgs& a, hipStream_t st) {
-    // (as the down launch: two parts from two tokens on; four parts need two rounds of these workgroups)
-    const int tsplit = a.S >= 2 ? 2 : 1;
-    hipLaunchKernelGGL((k_mix_up<QD, L, IT>), dim3((a.H / 32 + 7) / 8 * 8 * tsplit), dim3(UP_THREADS), 0, st, a,
-                       tsplit);
-    return hipGetLastError();
-  }
-};
-template <int L, int IT> static hipError_t mix_up_q4(const MixArgs& a, hipStream_t st) { return MixUp<4>::go<L, IT>(a, st); }
-template <int L, int IT> static hipError_t mix_up_q2(const MixArgs& a, hipStream_t st) { return MixUp<2>::go<L, IT>(a, st); }
-template <int L, int IT> static hipError_t mix_up_q1(const MixArgs& a, hipStream_t st) { return MixUp<1>::go<L, IT>(a, st); }
+static hipError_t mix_up_q(const MixArgs& a, hipStream_t st) {
+  return a.usb ? mix_up_lw<QD, 1>(a, st) : mix_up_lw<QD, 0>(a, st);
+}
 
 static hipError_t mix_down(const MixArgs& a, hipStream_t st) { MTPX_QROW_DISPATCH(a.hc * a.H / 32, mix_down_li, a, st); }
-static hipError_t mix_up4(const MixArgs& a, hipStream_t st) { MTPX_QROW_DISPATCH(a.LW / 32, mix_up_q4, a, st); }
-static hipError_t mix_up2(const MixArgs& a, hipStream_t st) { MTPX_QROW_DISPATCH(a.LW / 32, mix_up_q2, a, st); }
-static hipError_t mix_up1(const MixArgs& a, hipStream_t st) { MTPX_QROW_DISPATCH(a.LW / 32, mix_up_q1, a, st); }
 
 int mix_classes(int W) {
   const int L = lanes_for_blocks(W / 32);
@@ -269,9 +297,9 @@ hipError_t launch_mixer(const MixArgs& a, hipStream_t st) {
   hipError_t e = mix_down(a, st);
   if (e != hipSuccess) return e;
   switch (mix_classes(a.hc * a.H)) {
-    case 4: return mix_up4(a, st);
-    case 2: return mix_up2(a, st);
-    default: return mix_up1(a, st);
+    case 4: return mix_up_q<4>(a, st);
+    case 2: return mix_up_q<2>(a, st);
+    default: return mix_up_q<1>(a, st);
   }
 }
 

@@ -23,8 +23,9 @@ __global__ __launch_bounds__(256) void k_xprep(const bf16* __restrict__ x, int M
 // LDS read of a prepared activation block feeds two weight rows.  A wave's
 // rows are loaded before the activations are staged.  Grid Y batches windows
 // of `win` tokens (window w: tokens w * win .. of the M in all), each computed
-// as its own launch would.
-template <int L, int IT, bool CB>
+// as its own launch would.  PK: the scale/bias pairs from the packed rows (sbp),
+// else from the checkpoint's rows -- one load path, so no load waits at a join.
+template <int L, int IT, bool CB, bool PK>
 __global__ __launch_bounds__(256) void k_qmv(const uint32_t* __restrict__ wq, const bf16* __restrict__ sc,
                                              const bf16* __restrict__ bi, const uint32_t* __restrict__ sbp,
                                              int N, int K, int gs,
@@ -51,10 +52,10 @@ __global__ __launch_bounds__(256) void k_qmv(const uint32_t* __restrict__ wq, co
     const int rA = b0 + grp * 2, rB = rA + 1;
     const bool vA = rA < row_end, vB = rB < row_end;
     const int ra = vA ? rA : row0, rb = vB ? rB : row0;
-    A.template load<CB>(wq + (size_t)ra * (K / 8), sc + (size_t)ra * ng, bi + (size_t)ra * ng,
-                        sbp ? sbp + (size_t)ra * P : nullptr, nb, gs, sub, vA);
-    B.template load<CB>(wq + (size_t)rb * (K / 8), sc + (size_t)rb * ng, bi + (size_t)rb * ng,
-                        sbp ? sbp + (size_t)rb * P : nullptr, nb, gs, sub, vB);
+    A.template load_as<PK, CB>(wq + (size_t)ra * (K / 8), sc + (size_t)ra * ng, bi + (size_t)ra * ng,
+                               PK ? sbp + (size_t)ra * P : nullptr, nb, gs, sub, vA);
+    B.template load_as<PK, CB>(wq + (size_t)rb * (K / 8), sc + (size_t)rb * ng, bi + (size_t)rb * ng,
+                               PK ? sbp + (size_t)rb * P : nullptr, nb, gs, sub, vB);
   };
   if (base < row_end) load2(base);  // first rows in flight before the staging
   stage16(lds, xp, M * nb * XP_DW);
@@ -1060,16 +1061,16 @@ static hipError_t qmv_li(const uint32_t* wq, const bf16* s, const bf16* b, const
   int grid = (N + rows_per_wg - 1) / rows_per_wg;
   if (nwin > 1) grid = (grid + 7) / 8 * 8;
   const size_t lds = (size_t)(M < win ? M : win) * (K / 32) * XP_DW * 4;
-  static size_t cur = 0, cur_b = 0;
-  hipError_t e = batch ? ensure_lds(k_qmv<L, IT, true>, lds, cur_b) : ensure_lds(k_qmv<L, IT, false>, lds, cur);
-  if (e != hipSuccess) return e;
-  if (batch)
-    hipLaunchKernelGGL((k_qmv<L, IT, true>), dim3(grid, nwin), dim3(256), lds, st, wq, s, b, sb, N, K, gs, xp, M, y, yf,
-                       rows_per_wg, win);
-  else
-    hipLaunchKernelGGL((k_qmv<L, IT, false>), dim3(grid, nwin), dim3(256), lds, st, wq, s, b, sb, N, K, gs, xp, M, y,
-                       yf, rows_per_wg, win);
-  return hipGetLastError();
+  auto go = [&](auto kern, size_t& cur) {
+    hipError_t e = ensure_lds(kern, lds, cur);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(kern, dim3(grid, nwin), dim3(256), lds, st, wq, s, b, sb, N, K, gs, xp, M, y, yf, rows_per_wg,
+                       win);
+    return hipGetLastError();
+  };
+  static size_t c00 = 0, c01 = 0, c10 = 0, c11 = 0;
+  if (batch) return sb ? go(k_qmv<L, IT, true, true>, c11) : go(k_qmv<L, IT, true, false>, c10);
+  return sb ? go(k_qmv<L, IT, false, true>, c01) : go(k_qmv<L, IT, false, false>, c00);
 }
 
 static hipError_t qmv_tokens(const uint32_t* wq, const bf16* s, const bf16* b, const uint32_t* sb, int N, int K,

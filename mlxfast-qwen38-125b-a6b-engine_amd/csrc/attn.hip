@@ -39,28 +39,43 @@ __global__ void k_attn_prep(const bf16* __restrict__ qkv, int S, int QW, int HQ,
   const int hh = isq ? h : h - HQ;
   const bf16* src = isq ? row + hh * D : row + 2 * HQ * D + hh * D;
   const bf16* wn = isq ? qnorm : knorm;
+  // every load first (raw bits; the rotary table at clamped positions, used below ROT only), so
+  // nothing waits before the last one is issued
+  const bf16* cs = ROT > 0 ? cos_t + (size_t)pos * ROT : src;  // (no rotary: a valid row, unused)
+  const bf16* sn = ROT > 0 ? sin_t + (size_t)pos * ROT : src;
+  bf16 xr[4], wr[4], cr[4], sr[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int d = 4 * t + i, dr = d < ROT ? d : 0;
+    xr[i] = src[d];
+    wr[i] = wn[d];
+    cr[i] = cs[dr];
+    sr[i] = sn[dr];
+  }
+  asm volatile("" ::: "memory");
   float x[4];
   float acc = 0.0f;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    x[i] = bf2f(src[4 * t + i]);
+    x[i] = bf2f(xr[i]);
     acc = __builtin_fmaf(x[i], x[i], acc);
   }
-  for (int off = L / 2; off >= 1; off >>= 1) acc = acc + __shfl_xor(acc, off, 64);
+  if (L == 64)  // one wave: the same butterfly by DPP and lane swaps instead of LDS permutes
+    acc = wave_fold64(acc);
+  else
+    for (int off = L / 2; off >= 1; off >>= 1) acc = acc + __shfl_xor(acc, off, 64);
   const float inv = 1.0f / sqrtf(acc / (float)D + eps);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) vec[4 * t + i] = round_bf(bf2f(wn[4 * t + i]) * round_bf(x[i] * inv));
+  for (int i = 0; i < 4; ++i) vec[4 * t + i] = round_bf(bf2f(wr[i]) * round_bf(x[i] * inv));
   __syncthreads();
   bf16* dst = isq ? q + ((size_t)s * HQ + hh) * D : kc + ((size_t)hh * tmax + pos) * D;
   const int half = ROT / 2;
-  const bf16* cs = cos_t + (size_t)pos * ROT;
-  const bf16* sn = sin_t + (size_t)pos * ROT;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int d = 4 * t + i;
     float o = vec[d];
     if (d < ROT) {
-      const float c = bf2f(cs[d]), sv = bf2f(sn[d]);
+      const float c = bf2f(cr[i]), sv = bf2f(sr[i]);
       if (d < half) {
         const float t1 = round_bf(vec[d] * c);
         const float t2 = round_bf(-vec[d + half] * sv);

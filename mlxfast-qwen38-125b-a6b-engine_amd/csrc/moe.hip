@@ -560,6 +560,9 @@ __global__ __launch_bounds__(256) void k_moe_combine(MoeArgs a0) {
 #pragma unroll
   for (int k = 0; k < K; ++k) rv[k] = bf2f(a.r[(size_t)(m * K + k) * H + h]);
   const float shv = bf2f(a.r[(size_t)(M * K + m) * H + h]);
+  // the residual row with the others (unconditional: without one, an expert row is read and unused)
+  const bf16 resb = (a.resid ? a.resid : a.r)[(size_t)m * H + h];
+  asm volatile("" ::: "memory");
   float prod[K];
 #pragma unroll
   for (int k = 0; k < K; ++k) prod[k] = rv[k] * a.w[m * K + k];
@@ -568,7 +571,7 @@ __global__ __launch_bounds__(256) void k_moe_combine(MoeArgs a0) {
   const float sh = round_bf(sg * shv);
   const bf16 out = f2bf(rr + sh);
   if (a.y) a.y[(size_t)m * H + h] = out;
-  if (a.y2) a.y2[(size_t)m * H + h] = f2bf(bf2f(a.resid[(size_t)m * H + h]) + bf2f(out));
+  if (a.y2) a.y2[(size_t)m * H + h] = f2bf(bf2f(resb) + bf2f(out));
 }
 
 // ---------------------------------------------------------------------------

@@ -90,68 +90,13 @@ __global__ void k_attn_prep(const bf16* __restrict__ qkv, int S, int QW, int HQ,
   }
 }
 
-// part layout: [(hk * nch + c) * R + ri] * (D + 2): {m, l, o[0..D)}, R = S * G,
-// ri = s * G + g.  grid (nch, HK, S): one workgroup per (key chunk, kv head,
-// query); its rows are the G query heads of the group.
-__global__ __launch_bounds__(ATTN_THREADS) void k_attn_partial(const bf16* __restrict__ q, int S, int HQ, int HK, int D,
-                                                      const bf16* __restrict__ kc, const bf16* __restrict__ vc,
-                                                      int64_t tmax, int T, float scale, int nch,
-                                                      float* __restrict__ part) {
-  extern __shared__ float smem[];
-  const int c = blockIdx.x, hk = blockIdx.y, s = blockIdx.z;
-  const int G = HQ / HK, R = S * G, C = ATTN_CHUNK;
-  const int i0 = c * C;
-  const int last = T - S + s;                // last key visible to this query
-  int n = last + 1 - i0;                     // visible keys of the chunk (a prefix)
-  n = n < 0 ? 0 : (n > C ? C : n);
-  // K rows padded by 4 dwords: 16-byte aligned rows for 128-bit reads, and 8
-  // consecutive keys cover all 32 banks
-  const int KS = D / 2 + 4;
-  uint32_t* qb = reinterpret_cast<uint32_t*>(smem);         // [G][D/2] bf16 pairs
-  uint32_t* kb = qb + (size_t)G * (D / 2);                  // [C][KS]
-  bf16* vb = reinterpret_cast<bf16*>(kb + (size_t)C * KS);  // [C][D]
-  float* sc = reinterpret_cast<float*>(vb + (size_t)C * D); // [G][C]
-  float* ml = sc + (size_t)G * C;                           // [G][2]
-  const uint32_t* q32 = reinterpret_cast<const uint32_t*>(q);
-  const uint32_t* k32 = reinterpret_cast<const uint32_t*>(kc);
-  const uint32_t* v32 = reinterpret_cast<const uint32_t*>(vc);
-  // staging: 16-byte loads, up to 8 in flight per thread before the LDS stores
-  const uint4* q4 = reinterpret_cast<const uint4*>(q);
-  const uint4* k4 = reinterpret_cast<const uint4*>(kc);
-  const uint4* v4 = reinterpret_cast<const uint4*>(vc);
-  const int RV = D / 8;                   // uint4 per row
-  const int nq = G * RV, nkv = n * RV;    // uint4 of q rows, of each of K and V
-  for (int base = 0; base < nq + 2 * nkv; base += 8 * (int)blockDim.x) {
-    uint4 r[8];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {  // the source selected by address, one unconditional load (the first q
-      const int i = base + u * (int)blockDim.x + (int)threadIdx.x;  // unit past the end): all 8 in flight
-      const int ik = i - nq, iv = i - nq - nkv;
-      const uint4* src = i < nq ? q4 + ((size_t)s * HQ + hk * G) * RV + i
-                         : i < nq + nkv ? k4 + ((size_t)hk * tmax + i0 + ik / RV) * RV + ik % RV
-                         : i < nq + 2 * nkv ? v4 + ((size_t)hk * tmax + i0 + iv / RV) * RV + iv % RV
-                                            : q4 + ((size_t)s * HQ + hk * G) * RV;
-      r[u] = *src;
-    }
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int i = base + u * (int)blockDim.x + (int)threadIdx.x;
-      if (i < nq) {
-        reinterpret_cast<uint4*>(qb)[i] = r[u];
-      } else if (i < nq + nkv) {
-        const int ik = i - nq;
-        uint32_t* dst = kb + (size_t)(ik / RV) * KS + (ik % RV) * 4;
-        dst[0] = r[u].x;
-        dst[1] = r[u].y;
-        dst[2] = r[u].z;
-        dst[3] = r[u].w;
-      } else if (i < nq + 2 * nkv) {
-        const int iv = i - nq - nkv;
-        reinterpret_cast<uint4*>(vb)[iv] = r[u];
-      }
-    }
-  }
-  __syncthreads();
+// The chunk's scores, softmax partials and P.V of workgroup (chunk c, kv head hk, query token s) against
+// the staged rows (qb: the token's G query rows, bf16 pairs [G][D/2]; kb: the chunk's n visible keys,
+// rows of KS dwords; vb: their values [C][D]), written to part.
+__device__ __forceinline__ void attn_chunk(int c, int hk, int s, int G, int R, int n, int D, float scale, int nch,
+                                           const uint32_t* qb, const uint32_t* kb, const bf16* vb, float* sc,
+                                           float* ml, float* __restrict__ part) {
+  const int C = ATTN_CHUNK, KS = D / 2 + 4;
   // scores: one (query row g, key j) chain per thread and pass: the sequential
   // d-order fmaf of the canonical order, fed 8 dimensions per 128-bit LDS read
   for (int p = threadIdx.x; p < G * C; p += blockDim.x) {
@@ -250,6 +195,223 @@ __global__ __launch_bounds__(ATTN_THREADS) void k_attn_partial(const bf16* __res
       }
     }
   }
+}
+
+// part layout: [(hk * nch + c) * R + ri] * (D + 2): {m, l, o[0..D)}, R = S * G,
+// ri = s * G + g.  grid (nch, HK, S): one workgroup per (key chunk, kv head,
+// query); its rows are the G query heads of the group.
+__global__ __launch_bounds__(ATTN_THREADS) void k_attn_partial(const bf16* __restrict__ q, int S, int HQ, int HK, int D,
+                                                      const bf16* __restrict__ kc, const bf16* __restrict__ vc,
+                                                      int64_t tmax, int T, float scale, int nch,
+                                                      float* __restrict__ part) {
+  extern __shared__ float smem[];
+  const int c = blockIdx.x, hk = blockIdx.y, s = blockIdx.z;
+  const int G = HQ / HK, R = S * G, C = ATTN_CHUNK;
+  const int i0 = c * C;
+  const int last = T - S + s;                // last key visible to this query
+  int n = last + 1 - i0;                     // visible keys of the chunk (a prefix)
+  n = n < 0 ? 0 : (n > C ? C : n);
+  // K rows padded by 4 dwords: 16-byte aligned rows for 128-bit reads, and 8
+  // consecutive keys cover all 32 banks
+  const int KS = D / 2 + 4;
+  uint32_t* qb = reinterpret_cast<uint32_t*>(smem);         // [G][D/2] bf16 pairs
+  uint32_t* kb = qb + (size_t)G * (D / 2);                  // [C][KS]
+  bf16* vb = reinterpret_cast<bf16*>(kb + (size_t)C * KS);  // [C][D]
+  float* sc = reinterpret_cast<float*>(vb + (size_t)C * D); // [G][C]
+  float* ml = sc + (size_t)G * C;                           // [G][2]
+  const uint32_t* q32 = reinterpret_cast<const uint32_t*>(q);
+  const uint32_t* k32 = reinterpret_cast<const uint32_t*>(kc);
+  const uint32_t* v32 = reinterpret_cast<const uint32_t*>(vc);
+  // staging: 16-byte loads, up to 8 in flight per thread before the LDS stores
+  const uint4* q4 = reinterpret_cast<const uint4*>(q);
+  const uint4* k4 = reinterpret_cast<const uint4*>(kc);
+  const uint4* v4 = reinterpret_cast<const uint4*>(vc);
+  const int RV = D / 8;                   // uint4 per row
+  const int nq = G * RV, nkv = n * RV;    // uint4 of q rows, of each of K and V
+  for (int base = 0; base < nq + 2 * nkv; base += 8 * (int)blockDim.x) {
+    uint4 r[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {  // the source selected by address, one unconditional load (the first q
+      const int i = base + u * (int)blockDim.x + (int)threadIdx.x;  // unit past the end): all 8 in flight
+      const int ik = i - nq, iv = i - nq - nkv;
+      const uint4* src = i < nq ? q4 + ((size_t)s * HQ + hk * G) * RV + i
+                         : i < nq + nkv ? k4 + ((size_t)hk * tmax + i0 + ik / RV) * RV + ik % RV
+                         : i < nq + 2 * nkv ? v4 + ((size_t)hk * tmax + i0 + iv / RV) * RV + iv % RV
+                                            : q4 + ((size_t)s * HQ + hk * G) * RV;
+      r[u] = *src;
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int i = base + u * (int)blockDim.x + (int)threadIdx.x;
+      if (i < nq) {
+        reinterpret_cast<uint4*>(qb)[i] = r[u];
+      } else if (i < nq + nkv) {
+        const int ik = i - nq;
+        uint32_t* dst = kb + (size_t)(ik / RV) * KS + (ik % RV) * 4;
+        dst[0] = r[u].x;
+        dst[1] = r[u].y;
+        dst[2] = r[u].z;
+        dst[3] = r[u].w;
+      } else if (i < nq + 2 * nkv) {
+        const int iv = i - nq - nkv;
+        reinterpret_cast<uint4*>(vb)[iv] = r[u];
+      }
+    }
+  }
+  __syncthreads();
+  attn_chunk(c, hk, s, G, R, n, D, scale, nch, qb, kb, vb, sc, ml, part);
+}
+
+// The verify window's attention with the prep folded in (S <= MAX_TOKENS, D = 256: a head row per wave,
+// four elements a lane, the prep kernel's float steps and butterfly): workgroup (chunk c, kv head hk,
+// query token s) normalises and rotates its token's G query rows into LDS itself, stages the chunk's
+// visible cached keys and values below the window (positions < T - S), and prepares the window's key
+// rows that fall in the chunk (normalised and rotated) and value rows (copied) into LDS; the last
+// query's workgroup also appends those rows to the cache.  Every load is issued before the first wait.
+constexpr int PP_D = 256;
+constexpr int PP_PASSES = 3;  // normed rows per wave: G + (window rows in the chunk) <= 8 waves x 3
+
+__global__ __launch_bounds__(ATTN_THREADS) void k_attn_partial_prep(
+    const bf16* __restrict__ qkv, int QW, int S, int HQ, int HK, int ROT, const bf16* __restrict__ qnorm,
+    const bf16* __restrict__ knorm, float eps, const bf16* __restrict__ cos_t, const bf16* __restrict__ sin_t,
+    bf16* __restrict__ kc, bf16* __restrict__ vc, int64_t tmax, int T, float scale, int nch, float* __restrict__ part) {
+  constexpr int D = PP_D, RV = D / 8, NW = ATTN_THREADS / 64;
+  extern __shared__ float smem[];
+  const int c = blockIdx.x, hk = blockIdx.y, s = blockIdx.z;
+  const int G = HQ / HK, R = S * G, C = ATTN_CHUNK;
+  const int i0 = c * C, pos0 = T - S;
+  int n = pos0 + s + 1 - i0;  // visible keys of the chunk (a prefix)
+  n = n < 0 ? 0 : (n > C ? C : n);
+  const int KS = D / 2 + 4;
+  uint32_t* qb = reinterpret_cast<uint32_t*>(smem);          // [G][D/2] bf16 pairs
+  uint32_t* kb = qb + (size_t)G * (D / 2);                   // [C][KS]
+  bf16* vb = reinterpret_cast<bf16*>(kb + (size_t)C * KS);   // [C][D]
+  float* sc = reinterpret_cast<float*>(vb + (size_t)C * D);  // [G][C]
+  float* ml = sc + (size_t)G * C;                            // [G][2]
+  float* xw = ml + (size_t)2 * G;                            // [NW][D]: a wave's normed row before the rotation
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  // the window's rows in this chunk (positions [w0, w1)), and the cached rows staged (below the window)
+  const int w0 = i0 > pos0 ? i0 : pos0, w1 = i0 + C < T ? i0 + C : T, nw = w1 > w0 ? w1 - w0 : 0;
+  const int lo = pos0 - i0, ncache = lo < 0 ? 0 : (lo > n ? n : lo);
+  const bool append = s == S - 1;
+  // loads: the normed rows' inputs (item it = wave + NW pass: the G query rows, then the nw key rows;
+  // each lane its four elements, the norm weights and the rotary table at a clamped column), the
+  // window's value rows, the cached key and value rows
+  const int items = G + nw;
+  uint2 xin[PP_PASSES], win[PP_PASSES];
+  bf16 cr[PP_PASSES][4], sr[PP_PASSES][4];
+#pragma unroll
+  for (int pass = 0; pass < PP_PASSES; ++pass) {
+    const int it = wave + NW * pass, itc = it < items ? it : 0;
+    const bool isq = itc < G;
+    const int tok = isq ? s : w0 + (itc - G) - pos0;  // the window token of the row
+    const bf16* src = qkv + (size_t)tok * QW + (isq ? (size_t)(hk * G + itc) * D : (size_t)2 * HQ * D + (size_t)hk * D);
+    xin[pass] = *reinterpret_cast<const uint2*>(src + 4 * lane);
+    win[pass] = *reinterpret_cast<const uint2*>((isq ? qnorm : knorm) + 4 * lane);
+    const size_t rp = (size_t)(pos0 + tok) * ROT;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int d = 4 * lane + i, dr = d < ROT ? d : 0;
+      cr[pass][i] = cos_t[rp + dr];
+      sr[pass][i] = sin_t[rp + dr];
+    }
+  }
+  const uint4* k4 = reinterpret_cast<const uint4*>(kc);
+  const uint4* v4 = reinterpret_cast<const uint4*>(vc);
+  const uint4* qkv4 = reinterpret_cast<const uint4*>(qkv);
+  const int nkv = ncache * RV, nwv = nw * RV;  // uint4 of the cached K and V rows each, of the window's V rows
+  constexpr int SU = (2 * ATTN_CHUNK * RV + ATTN_THREADS - 1) / ATTN_THREADS;  // staging units per thread
+  uint4 r[SU];
+#pragma unroll
+  for (int u = 0; u < SU; ++u) {  // unit i: cached K (i < nkv), cached V, then window V rows; clamped past the end
+    const int i = u * ATTN_THREADS + (int)threadIdx.x;
+    const int ik = i, iv = i - nkv, iw = i - 2 * nkv;
+    const uint4* src = i < nkv ? k4 + ((size_t)hk * tmax + i0 + ik / RV) * RV + ik % RV
+                       : i < 2 * nkv ? v4 + ((size_t)hk * tmax + i0 + iv / RV) * RV + iv % RV
+                       : i < 2 * nkv + nwv
+                           ? qkv4 + ((size_t)(w0 + iw / RV - pos0) * QW + (size_t)2 * HQ * D + (size_t)HK * D +
+                                     (size_t)hk * D) / 8 + iw % RV
+                           : qkv4 + ((size_t)s * QW) / 8;
+    r[u] = *src;
+  }
+  asm volatile("" ::: "memory");
+#pragma unroll
+  for (int u = 0; u < SU; ++u) {
+    const int i = u * ATTN_THREADS + (int)threadIdx.x;
+    if (i < nkv) {
+      uint32_t* dst = kb + (size_t)(i / RV) * KS + (i % RV) * 4;
+      dst[0] = r[u].x;
+      dst[1] = r[u].y;
+      dst[2] = r[u].z;
+      dst[3] = r[u].w;
+    } else if (i < 2 * nkv) {
+      reinterpret_cast<uint4*>(vb)[i - nkv] = r[u];
+    } else if (i < 2 * nkv + nwv) {
+      const int iw = i - 2 * nkv, row = w0 - i0 + iw / RV;
+      reinterpret_cast<uint4*>(vb)[(size_t)row * RV + iw % RV] = r[u];
+      if (append) reinterpret_cast<uint4*>(vc)[((size_t)hk * tmax + w0 + iw / RV) * RV + iw % RV] = r[u];
+    }
+  }
+  // the normed, rotated rows: q into qb, the window's k into kb (and the cache)
+  const int half = ROT / 2;
+  float* xr = xw + (size_t)wave * D;
+#pragma unroll
+  for (int pass = 0; pass < PP_PASSES; ++pass) {
+    const int it = wave + NW * pass;
+    if (it >= items) break;  // uniform per wave
+    const uint32_t xa[2] = {xin[pass].x, xin[pass].y}, wa[2] = {win[pass].x, win[pass].y};
+    float x[4];
+    float acc = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      x[i] = __uint_as_float((i & 1) ? (xa[i >> 1] & 0xffff0000u) : (xa[i >> 1] << 16));
+      acc = __builtin_fmaf(x[i], x[i], acc);
+    }
+    acc = wave_fold64(acc);
+    const float inv = 1.0f / sqrtf(acc / (float)D + eps);
+    float v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float w = __uint_as_float((i & 1) ? (wa[i >> 1] & 0xffff0000u) : (wa[i >> 1] << 16));
+      v[i] = round_bf(w * round_bf(x[i] * inv));
+      xr[4 * lane + i] = v[i];
+    }
+    // this wave reads the row it wrote (LDS operations of one wave complete in order)
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const bool isq = it < G;
+    bf16 o16[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int d = 4 * lane + i;
+      float o = v[i];
+      if (d < ROT) {
+        const float cv = bf2f(cr[pass][i]), sv = bf2f(sr[pass][i]);
+        if (d < half) {
+          const float t1 = round_bf(v[i] * cv);
+          const float t2 = round_bf(-xr[d + half] * sv);
+          o = round_bf(t1 + t2);
+        } else {
+          const float t1 = round_bf(v[i] * cv);
+          const float t2 = round_bf(xr[d - half] * sv);
+          o = round_bf(t1 + t2);
+        }
+      }
+      o16[i] = f2bf(o);
+    }
+    const uint2 packed = make_uint2((uint32_t)o16[0] | ((uint32_t)o16[1] << 16), (uint32_t)o16[2] | ((uint32_t)o16[3] << 16));
+    if (isq) {
+      reinterpret_cast<uint2*>(qb + (size_t)it * (D / 2))[lane] = packed;
+    } else {
+      const int p = w0 + (it - G);
+      reinterpret_cast<uint2*>(kb + (size_t)(p - i0) * KS)[lane] = packed;
+      if (append) reinterpret_cast<uint2*>(kc + ((size_t)hk * tmax + p) * D)[lane] = packed;
+    }
+    // the next pass rewrites this wave's row: its reads above complete first (in order)
+  }
+  __syncthreads();
+  attn_chunk(c, hk, s, G, R, n, D, scale, nch, qb, kb, vb, sc, ml, part);
 }
 
 // grid (R, HK), max(D, 64) threads (D <= 256).  Fold the chunk partials in chunk order,
@@ -419,6 +581,26 @@ hipError_t launch_attn_partial(const bf16* q, int S, int HQ, int HK, int D, cons
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(k_attn_partial, dim3(nch, HK, S), dim3(ATTN_THREADS), lds, st, q, S, HQ, HK, D, kc, vc, tmax, T,
                      scale, nch, part);
+  return hipGetLastError();
+}
+
+bool attn_prep_fused_ok(int S, int HQ, int HK, int D, int QW) {
+  return S >= 1 && S <= MAX_TOKENS && D == PP_D && HQ % HK == 0 && QW % 8 == 0 &&
+         attn_partial_lds(HQ / HK, D) + (size_t)(ATTN_THREADS / 64) * D * 4 <= 160 * 1024 &&
+         HQ / HK + MAX_TOKENS <= (ATTN_THREADS / 64) * PP_PASSES;
+}
+
+hipError_t launch_attn_partial_prep(const bf16* qkv, int QW, int S, int HQ, int HK, int D, int ROT, const bf16* qnorm,
+                                    const bf16* knorm, float eps, const bf16* cos_t, const bf16* sin_t, bf16* kcache,
+                                    bf16* vcache, int64_t tmax, int T, float scale, float* part, hipStream_t st) {
+  if (!attn_prep_fused_ok(S, HQ, HK, D, QW) || T < S) return hipErrorInvalidValue;
+  const int nch = (T + ATTN_CHUNK - 1) / ATTN_CHUNK;
+  const size_t lds = attn_partial_lds(HQ / HK, D) + (size_t)(ATTN_THREADS / 64) * D * 4;
+  static size_t cur = 0;
+  hipError_t e = ensure_lds(k_attn_partial_prep, lds, cur);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(k_attn_partial_prep, dim3(nch, HK, S), dim3(ATTN_THREADS), lds, st, qkv, QW, S, HQ, HK, ROT,
+                     qnorm, knorm, eps, cos_t, sin_t, kcache, vcache, tmax, T, scale, nch, part);
   return hipGetLastError();
 }
 

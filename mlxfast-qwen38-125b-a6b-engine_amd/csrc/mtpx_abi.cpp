@@ -512,11 +512,17 @@ int attn_enqueue(Ctx* c, const Layer* L, Kv* kv, uint32_t* xp, int M, uint16_t* 
   float* part = ws_take<float>(c, attn_partial_floats(M, HQ, D, T));
   hipStream_t st = c->stream;
   LAUNCH(c, "qmv_qkv", launch_qmv(L->w.qkv_w, L->w.qkv_s, L->w.qkv_b, L->w.qkv_sb, QW, H, gs, xp, M, qkv, nullptr, st));
-  LAUNCH(c, "attn_prep", launch_attn_prep(qkv, M, QW, HQ, HK, D, g.rot_dims, L->w.q_norm, L->w.k_norm, g.eps,
-                                          L->w.rope_cos, L->w.rope_sin, (int)kv->offset, q, kv->k, kv->v,
-                                          kv->tmax, st));
-  LAUNCH(c, "attn_partial", launch_attn_partial(q, M, HQ, HK, D, kv->k, kv->v, kv->tmax, T,
-                                                1.0f / std::sqrt((float)D), part, st));
+  if (attn_prep_fused_ok(M, HQ, HK, D, QW)) {  // a verify window: the prep inside the partial launch
+    LAUNCH(c, "attn_partial", launch_attn_partial_prep(qkv, QW, M, HQ, HK, D, g.rot_dims, L->w.q_norm, L->w.k_norm,
+                                                       g.eps, L->w.rope_cos, L->w.rope_sin, kv->k, kv->v, kv->tmax, T,
+                                                       1.0f / std::sqrt((float)D), part, st));
+  } else {
+    LAUNCH(c, "attn_prep", launch_attn_prep(qkv, M, QW, HQ, HK, D, g.rot_dims, L->w.q_norm, L->w.k_norm, g.eps,
+                                            L->w.rope_cos, L->w.rope_sin, (int)kv->offset, q, kv->k, kv->v,
+                                            kv->tmax, st));
+    LAUNCH(c, "attn_partial", launch_attn_partial(q, M, HQ, HK, D, kv->k, kv->v, kv->tmax, T,
+                                                  1.0f / std::sqrt((float)D), part, st));
+  }
   LAUNCH(c, "attn_combine", launch_attn_combine(M, HQ, HK, D, T, part, qkv, QW, HQ * D, nullptr, att, xp, st));
   LAUNCH(c, "qmv_o", launch_qmv(L->w.o_w, L->w.o_s, L->w.o_b, L->w.o_sb, H, HQ * D, gs, xp, M, o, nullptr, st));
   return MTPX_OK;

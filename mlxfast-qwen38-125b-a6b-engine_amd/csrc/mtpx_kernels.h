@@ -190,6 +190,12 @@ hipError_t launch_attn_verify(const bf16* q, int S, int HQ, int HK, int D, const
                               const bf16* qkv, int QW, int gate_off, bf16* out, bf16* out_gated,
                               uint32_t* xp_gated, hipStream_t st);
 size_t attn_partial_lds(int G, int D);
+// The verify window's prep folded into the partial launch (q/k norms, rotation, the KV append), for
+// S <= MAX_TOKENS and head dim 256.
+bool attn_prep_fused_ok(int S, int HQ, int HK, int D, int QW);
+hipError_t launch_attn_partial_prep(const bf16* qkv, int QW, int S, int HQ, int HK, int D, int ROT, const bf16* qnorm,
+                                    const bf16* knorm, float eps, const bf16* cos_t, const bf16* sin_t, bf16* kcache,
+                                    bf16* vcache, int64_t tmax, int T, float scale, float* part, hipStream_t st);
 hipError_t launch_attn_partial(const bf16* q, int S, int HQ, int HK, int D, const bf16* kc, const bf16* vc,
                                int64_t tmax, int T, float scale, float* part, hipStream_t st);
 hipError_t launch_attn_combine(int S, int HQ, int HK, int D, int T, const float* part, const bf16* qkv, int QW,

@@ -119,18 +119,18 @@ typedef int v4i_t __attribute__((ext_vector_type(4)));
 // four; the loads (all units of this thread, then its p/SX pairs) are issued
 // by mma_stage_load, so the caller can put its own loads behind them and
 // mma_stage_store waits for these only.
-template <int NB, int TG>
+template <int NB, int TG, int NTH>
 struct MmaStage {
-  static constexpr int NT = MMA_TOK * TG;                                      // tokens staged
-  static constexpr int NU = (NT * NB * 8 + MMA_THREADS - 1) / MMA_THREADS;     // units per thread
-  static constexpr int NP = (NT * NB + MMA_THREADS - 1) / MMA_THREADS;         // p/SX pairs per thread
+  static constexpr int NT = MMA_TOK * TG;                      // tokens staged
+  static constexpr int NU = (NT * NB * 8 + NTH - 1) / NTH;     // units per thread (NTH threads)
+  static constexpr int NP = (NT * NB + NTH - 1) / NTH;         // p/SX pairs per thread
   uint32_t w[NU][3];
   uint32_t ps[NP][2];
 
   __device__ __forceinline__ void load(const uint32_t* __restrict__ xp, int M) {
 #pragma unroll
     for (int k = 0; k < NU; ++k) {
-      const int u = threadIdx.x + k * MMA_THREADS;
+      const int u = threadIdx.x + k * NTH;
       const int t = u / (NB * 8), rem = u - t * (NB * 8), blk = rem >> 3, ge = rem & 7;
       const bool in = u < NT * NB * 8 && t < M;
       const uint32_t* src = xp + ((size_t)(in ? t : 0) * NB + (in ? blk : 0)) * XP_DW + ((ge & 1) ? 4 : 0) + (ge >> 1);
@@ -140,7 +140,7 @@ struct MmaStage {
     }
 #pragma unroll
     for (int k = 0; k < NP; ++k) {
-      const int u = threadIdx.x + k * MMA_THREADS;
+      const int u = threadIdx.x + k * NTH;
       const int t = u / NB, blk = u - t * NB;
       const bool in = u < NT * NB && t < M;
       const uint32_t* src = xp + ((size_t)(in ? t : 0) * NB + (in ? blk : 0)) * XP_DW + 24;
@@ -152,7 +152,7 @@ struct MmaStage {
   __device__ __forceinline__ void store(uint32_t* __restrict__ lds) const {
 #pragma unroll
     for (int k = 0; k < NU; ++k) {
-      const int u = threadIdx.x + k * MMA_THREADS;
+      const int u = threadIdx.x + k * NTH;
       if (u < NT * NB * 8) {
         const int t = u / (NB * 8), rem = u - t * (NB * 8), blk = rem >> 3, ge = rem & 7;
         const uint32_t w0 = w[k][0], w1 = w[k][1];
@@ -165,7 +165,7 @@ struct MmaStage {
     }
 #pragma unroll
     for (int k = 0; k < NP; ++k) {
-      const int u = threadIdx.x + k * MMA_THREADS;
+      const int u = threadIdx.x + k * NTH;
       if (u < NT * NB) {
         uint32_t* dst = lds + (size_t)u * MB_DW + 32;  // u = t * NB + blk
         dst[0] = ps[k][0];
@@ -195,8 +195,8 @@ constexpr int mma_body_chunks() {
   return (NCH <= 12 && NCH % 2 == 0 && (8 * (NCH / 2)) % LC == 0 && NCH / 2 >= B0) ? NCH / 2 : B0;
 }
 
-template <int L, int IT, int C, int TG, bool XPF>
-__global__ __launch_bounds__(MMA_THREADS) void k_qmv_mma(const uint32_t* __restrict__ wq, const uint32_t* __restrict__ sbp,
+template <int L, int IT, int C, int TG, bool XPF, int NWV>
+__global__ __launch_bounds__(64 * NWV) void k_qmv_mma(const uint32_t* __restrict__ wq, const uint32_t* __restrict__ sbp,
                                                         int N, int K, int gs, const uint32_t* __restrict__ xp, int M,
                                                         bf16* __restrict__ y, float* __restrict__ yf) {
   constexpr int NB = L * IT;   // blocks per row
@@ -204,10 +204,11 @@ __global__ __launch_bounds__(MMA_THREADS) void k_qmv_mma(const uint32_t* __restr
   constexpr int NQ = NB / C;   // blocks per class
   constexpr int NCH = NQ / 4;  // four-block chunks per class
   constexpr int BC = mma_body_chunks<L, IT, C>();  // chunks per loop body
-  constexpr int TPG = 8 / C;                   // tiles per workgroup pass
-  static_assert(NB % (4 * C) == 0 && NCH % BC == 0 && C <= L && C <= 8 && LC <= 16, "whole bodies of four-block chunks");
+  constexpr int TPG = NWV / C;                 // tiles per workgroup pass (NWV waves)
+  static_assert(NB % (4 * C) == 0 && NCH % BC == 0 && C <= L && C <= 8 && LC <= 16 && NWV % C == 0,
+                "whole bodies of four-block chunks, whole tiles per workgroup");
   // LDS: activations [MMA_TOK * TG][NB][MB_DW]; per wave the (scale, bias) pairs of its tile and class
-  // [16][NQ]; class partials [2][8 waves][TG][64].  Token group tq (tokens 4 tq .. 4 tq + 3) takes its own
+  // [16][NQ]; class partials [2][NWV waves][TG][64].  Token group tq (tokens 4 tq .. 4 tq + 3) takes its own
   // MFMA on the same weight operand, so a launch serves up to 4 TG tokens with one read of the weights.
   constexpr size_t TGO = (size_t)MMA_TOK * NB * MB_DW;  // one token group's activations
   extern __shared__ uint32_t lds[];
@@ -219,7 +220,7 @@ __global__ __launch_bounds__(MMA_THREADS) void k_qmv_mma(const uint32_t* __restr
     M = min(M - t0, MMA_TOK * TG);
   }
   uint32_t* sbl = lds + TG * TGO;
-  float* part = reinterpret_cast<float*>(sbl + 8 * 16 * NQ);
+  float* part = reinterpret_cast<float*>(sbl + NWV * 16 * NQ);
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int c = wave % C, tl = wave / C;
   const int n = lane & 15, g = lane >> 4;
@@ -231,7 +232,7 @@ __global__ __launch_bounds__(MMA_THREADS) void k_qmv_mma(const uint32_t* __restr
   const uint32_t* xps = lds + (size_t)g * NB * MB_DW + 32;
   // activations once per workgroup
   {
-    MmaStage<NB, TG> stg;
+    MmaStage<NB, TG, 64 * NWV> stg;
     stg.load(xp, M);
     stg.store(lds);
   }
@@ -376,7 +377,7 @@ __global__ __launch_bounds__(MMA_THREADS) void k_qmv_mma(const uint32_t* __restr
       v[tq] = acc[tq][0];
     }
     if constexpr (C > 1) {
-      float* pb = part + (iter & 1) * 8 * TG * 64;  // by parity: the next write to it is two barriers away
+      float* pb = part + (iter & 1) * NWV * TG * 64;  // by parity: the next write to it is two barriers away
 #pragma unroll
       for (int tq = 0; tq < TG; ++tq) pb[(wave * TG + tq) * 64 + lane] = v[tq];
       __syncthreads();
@@ -1078,20 +1079,24 @@ static hipError_t qmv_tokens(const uint32_t* wq, const bf16* s, const bf16* b, c
   MTPX_QROW_DISPATCH(K / 32, qmv_li, wq, s, b, sb, N, K, gs, xp, M, y, yf, win, st);
 }
 
-template <int L, int IT, int C, int TG>
+template <int L, int IT, int C, int TG, int NWV = 8>
 constexpr size_t mma_lds_bytes() {
-  return (size_t)MMA_TOK * TG * L * IT * MB_DW * 4 + (size_t)8 * 16 * (L * IT / C) * 4 + (size_t)2 * 8 * TG * 64 * 4;
+  return (size_t)MMA_TOK * TG * L * IT * MB_DW * 4 + (size_t)NWV * 16 * (L * IT / C) * 4 + (size_t)2 * NWV * TG * 64 * 4;
 }
 
 // hipErrorNotReady: a launch of two token groups (one workgroup per CU) whose tile groups would
 // need a second, nearly empty round of workgroups -- the caller runs four tokens per launch instead.
 // M > 4 TG tokens: windows of 4 TG in grid Y, one workgroup per tile group (rounded up to whole XCD
 // rounds, so the windows of a tile group share an XCD and its L2).
-template <int L, int IT, int C, int TG>
-static hipError_t qmv_mma_c(const uint32_t* wq, const uint32_t* sb, int N, int K, int gs, const uint32_t* xp, int M,
-                            bf16* y, float* yf, hipStream_t st) {
-  constexpr size_t lds = mma_lds_bytes<L, IT, C, TG>();
-  const int groups = ((N + 15) / 16 + 8 / C - 1) / (8 / C);
+// One token group: ten-wave workgroups (five tiles of two classes) where they fit a launch that
+// eight-wave ones do not in one round -- one workgroup per CU for one window (with eight, the few CUs
+// that take a second workgroup finish last: GDN in-projection, 258 groups on 256 CUs), within the
+// resident workgroups for several windows (eight: 2 x 264 workgroups of four tokens where 512 fit).
+template <int L, int IT, int C, int TG, int NWV>
+static hipError_t qmv_mma_launch(const uint32_t* wq, const uint32_t* sb, int N, int K, int gs, const uint32_t* xp,
+                                 int M, bf16* y, float* yf, hipStream_t st) {
+  constexpr size_t lds = mma_lds_bytes<L, IT, C, TG, NWV>();
+  const int groups = ((N + 15) / 16 + NWV / C - 1) / (NWV / C);
   const int per_cu = lds <= 50 * 1024 ? 3 : lds <= 78 * 1024 ? 2 : 1;  // workgroups resident per CU
   const int slots = per_cu * device_cus();
   const int nwin = (M + MMA_TOK * TG - 1) / (MMA_TOK * TG);
@@ -1100,19 +1105,33 @@ static hipError_t qmv_mma_c(const uint32_t* wq, const uint32_t* sb, int N, int K
   if constexpr (TG == 2) {  // two token groups (one workgroup per CU)
     if (nwin == 1 && groups >= 2 * grid) {  // workgroups walk several tile groups: the next one's first body in flight
       static size_t cur = 0;
-      hipError_t e = ensure_lds(k_qmv_mma<L, IT, C, TG, true>, lds, cur);
+      hipError_t e = ensure_lds(k_qmv_mma<L, IT, C, TG, true, NWV>, lds, cur);
       if (e != hipSuccess) return e;
-      hipLaunchKernelGGL((k_qmv_mma<L, IT, C, TG, true>), dim3(grid, nwin), dim3(MMA_THREADS), lds, st, wq, sb, N, K,
-                         gs, xp, M, y, yf);
+      hipLaunchKernelGGL((k_qmv_mma<L, IT, C, TG, true, NWV>), dim3(grid, nwin), dim3(64 * NWV), lds, st, wq, sb, N,
+                         K, gs, xp, M, y, yf);
       return hipGetLastError();
     }
   }
   static size_t cur = 0;
-  hipError_t e = ensure_lds(k_qmv_mma<L, IT, C, TG, false>, lds, cur);
+  hipError_t e = ensure_lds(k_qmv_mma<L, IT, C, TG, false, NWV>, lds, cur);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((k_qmv_mma<L, IT, C, TG, false>), dim3(grid, nwin), dim3(MMA_THREADS), lds, st, wq, sb, N, K, gs,
-                     xp, M, y, yf);
+  hipLaunchKernelGGL((k_qmv_mma<L, IT, C, TG, false, NWV>), dim3(grid, nwin), dim3(64 * NWV), lds, st, wq, sb, N, K,
+                     gs, xp, M, y, yf);
   return hipGetLastError();
+}
+
+template <int L, int IT, int C, int TG>
+static hipError_t qmv_mma_c(const uint32_t* wq, const uint32_t* sb, int N, int K, int gs, const uint32_t* xp, int M,
+                            bf16* y, float* yf, hipStream_t st) {
+  if constexpr (TG == 1 && C == 2 && mma_lds_bytes<L, IT, C, TG, 10>() <= 78 * 1024 &&
+                mma_lds_bytes<L, IT, C, TG, 8>() > 50 * 1024) {  // (two workgroups per CU either way)
+    const int tiles = (N + 15) / 16, g8 = (tiles + 3) / 4, g10 = (tiles + 4) / 5, cus = device_cus();
+    const int nwin = (M + MMA_TOK - 1) / MMA_TOK;
+    const bool ten = nwin == 1 ? g8 > cus && g10 <= cus
+                               : (g8 + 7) / 8 * 8 * nwin > 2 * cus && (g10 + 7) / 8 * 8 * nwin <= 2 * cus;
+    if (ten) return qmv_mma_launch<L, IT, C, TG, 10>(wq, sb, N, K, gs, xp, M, y, yf, st);
+  }
+  return qmv_mma_launch<L, IT, C, TG, 8>(wq, sb, N, K, gs, xp, M, y, yf, st);
 }
 
 // One token group: two workgroups per CU at least (above that the dot-product path is faster,

@@ -19,14 +19,14 @@ __global__ __launch_bounds__(256) void k_xprep(const bf16* __restrict__ x, int M
   if (blk < M * nb) xprep_lanes_direct(x[(size_t)(blk / nb) * K + (size_t)(blk % nb) * 32 + i], i, xp + (size_t)blk * XP_DW);
 }
 
-// Dense GEMV.  256 threads; every lane-group owns two rows (RPL = 2) so each
-// LDS read of a prepared activation block feeds two weight rows.  A wave's
+// Dense GEMV.  NWV waves (4, or 5 where that fits a launch's workgroups to the CUs); every lane-group
+// owns two rows (RPL = 2) so each LDS read of a prepared activation block feeds two weight rows.  A wave's
 // rows are loaded before the activations are staged.  Grid Y batches windows
 // of `win` tokens (window w: tokens w * win .. of the M in all), each computed
 // as its own launch would.  PK: the scale/bias pairs from the packed rows (sbp),
 // else from the checkpoint's rows -- one load path, so no load waits at a join.
-template <int L, int IT, bool CB, bool PK>
-__global__ __launch_bounds__(256) void k_qmv(const uint32_t* __restrict__ wq, const bf16* __restrict__ sc,
+template <int L, int IT, bool CB, bool PK, int NWV>
+__global__ __launch_bounds__(64 * NWV) void k_qmv(const uint32_t* __restrict__ wq, const bf16* __restrict__ sc,
                                              const bf16* __restrict__ bi, const uint32_t* __restrict__ sbp,
                                              int N, int K, int gs,
                                              const uint32_t* __restrict__ xp, int M, bf16* __restrict__ y,
@@ -60,7 +60,7 @@ __global__ __launch_bounds__(256) void k_qmv(const uint32_t* __restrict__ wq, co
   if (base < row_end) load2(base);  // first rows in flight before the staging
   stage16(lds, xp, M * nb * XP_DW);
   stage_sync();
-  for (bool first = true; base < row_end; base += 4 * RPW, first = false) {  // uniform per wave
+  for (bool first = true; base < row_end; base += NWV * RPW, first = false) {  // uniform per wave
     if (!first) load2(base);
     const int rA = base + grp * 2, rB = rA + 1;
     for (int m = 0; m < M; ++m) {
@@ -1057,21 +1057,40 @@ static hipError_t qmv_li(const uint32_t* wq, const bf16* s, const bf16* b, const
     const int g = std::max(1, std::min(passes, (want + nw - 1) / nw));
     per = (passes + g - 1) / g;
   }
-  const int rows_per_wg = per * rows_pass;
   const int nwin = (M + win - 1) / win;
-  int grid = (N + rows_per_wg - 1) / rows_per_wg;
-  if (nwin > 1) grid = (grid + 7) / 8 * 8;
   const size_t lds = (size_t)(M < win ? M : win) * (K / 32) * XP_DW * 4;
-  auto go = [&](auto kern, size_t& cur) {
+  auto go = [&](auto kern, size_t& cur, int rows_per_wg, int nthr) {
+    int grid = (N + rows_per_wg - 1) / rows_per_wg;
+    if (nwin > 1) grid = (grid + 7) / 8 * 8;
     hipError_t e = ensure_lds(kern, lds, cur);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(kern, dim3(grid, nwin), dim3(256), lds, st, wq, s, b, sb, N, K, gs, xp, M, y, yf, rows_per_wg,
+    hipLaunchKernelGGL(kern, dim3(grid, nwin), dim3(nthr), lds, st, wq, s, b, sb, N, K, gs, xp, M, y, yf, rows_per_wg,
                        win);
     return hipGetLastError();
   };
-  static size_t c00 = 0, c01 = 0, c10 = 0, c11 = 0;
-  if (batch) return sb ? go(k_qmv<L, IT, true, true>, c11) : go(k_qmv<L, IT, true, false>, c10);
-  return sb ? go(k_qmv<L, IT, false, true>, c01) : go(k_qmv<L, IT, false, false>, c00);
+  static size_t c00 = 0, c01 = 0, c10 = 0, c11 = 0, c5 = 0;
+  if (batch) return sb ? go(k_qmv<L, IT, true, true, 4>, c11, per * rows_pass, 256)
+                       : go(k_qmv<L, IT, true, false, 4>, c10, per * rows_pass, 256);
+  // Equal windows whose workgroups a five-wave launch (a fifth more rows a pass) spreads with a quarter
+  // fewer rows on the busiest CU (launch workgroups spread evenly): the K = 6144 output projections at
+  // four and six tokens, two windows of 2 x 160 four-wave workgroups on 256 CUs, the 64 CUs with two
+  // finishing last (12.35 -> 11.58 us at 4 tokens).  Not taken: a shorter last window (three tokens:
+  // 2 + 1) leaves those CUs less loaded and the larger workgroups cost more (11.10 -> 11.55 us); one
+  // window (GDN in-projection at one and two tokens, 258 two-pass four-wave workgroups against 412
+  // one-pass five-wave ones: 12.6 -> 14.4 us, 16.3 -> 17.8).
+  if (sb && nwin > 1 && M % win == 0) {
+    const int cus = device_cus();
+    constexpr int r5 = 5 * (64 / L) * 2;
+    const int per5 = ((N + r5 - 1) / r5 + 511) / 512;
+    auto busiest = [&](int rpw) {
+      const int g = (N + rpw - 1) / rpw, w = (nwin > 1 ? (g + 7) / 8 * 8 : g) * nwin;
+      return (int64_t)((w + cus - 1) / cus) * rpw;
+    };
+    if (4 * busiest(per5 * r5) <= 3 * busiest(per * rows_pass))
+      return go(k_qmv<L, IT, false, true, 5>, c5, per5 * r5, 320);
+  }
+  return sb ? go(k_qmv<L, IT, false, true, 4>, c01, per * rows_pass, 256)
+            : go(k_qmv<L, IT, false, false, 4>, c00, per * rows_pass, 256);
 }
 
 static hipError_t qmv_tokens(const uint32_t* wq, const bf16* s, const bf16* b, const uint32_t* sb, int N, int K,

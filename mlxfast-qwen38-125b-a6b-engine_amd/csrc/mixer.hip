@@ -107,20 +107,23 @@ __device__ __forceinline__ float class_fold_v(const float* v) {
 // Up rows of the block: local row lr = c*32 + i is global row c*H + d0 + i.  A workgroup takes one
 // part of the window's tokens; the two halves of the workgroup (waves 0-3 and 4-7) walk the same up
 // rows for the part's even and odd tokens.  The parts of a position block get ids 8 apart (one XCD:
-// the second reads the up rows from that L2).
+// the second reads the up rows from that L2).  FB and MR size the loads issued up front to the part's
+// tokens: FB batches of class partials (S * LW <= FB * UP_THREADS) and MR rounds of normed values
+// (S * hc * 32 <= MR * UP_THREADS), so no clamped duplicate load queues ahead of the up rows.
 constexpr int UP_THREADS = 512;
+constexpr int UP_FB_MAX = 8, UP_MR_MAX = MAX_TOKENS * 8 * 32 / UP_THREADS;  // any window: hc <= 8
 
-template <int QD, int SBM, int L, int IT>
+template <int QD, int SBM, int L, int IT, int FB, int MR>
 __global__ __launch_bounds__(UP_THREADS) __attribute__((amdgpu_waves_per_eu(1, 2))) void k_mix_up(MixArgs a,
                                                                                                   int tsplit) {
   constexpr int RW = 64 / L;
   constexpr int MAXROWS = 8 * 32;  // hc <= 8
   constexpr int NP = (MAXROWS + 4 * RW - 1) / (4 * RW);
-  constexpr int FOLD_BATCH = 8;  // S * LW <= FOLD_BATCH * UP_THREADS: one round of partial loads
+  constexpr int FOLD_BATCH = FB;  // S * LW <= FOLD_BATCH * UP_THREADS: one round of partial loads
   __shared__ uint32_t xpa[MAX_TOKENS * 12 * XP_DW];  // [S][LW/32][XP_DW], S * LW / 32 <= 96
   __shared__ bf16 wl[MAX_TOKENS][MAXROWS];
-  constexpr int MIX_ROUNDS = MAX_TOKENS * MAXROWS / UP_THREADS;  // (token, stream, position) terms per thread
-  __shared__ float term[MAX_TOKENS * MAXROWS];                    // [S][hc][32] bf16(sigmoid(w) * n)
+  constexpr int MIX_ROUNDS = MR;                    // (token, stream, position) terms per thread
+  __shared__ float term[MAX_TOKENS * MAXROWS];      // [S][hc][32] bf16(sigmoid(w) * n)
   const int H = a.H, hc = a.hc, LW = a.LW, W = hc * H;
   const int NR = LW + (a.iw ? hc : 0);
   const int nbA = LW / 32, ng = LW / a.gs, P = sb_row_len(LW, a.gs);
@@ -247,8 +250,26 @@ template <int QD, int SBM, int L, int IT>
 static hipError_t mix_up_go(const MixArgs& a, hipStream_t st) {
   // (as the down launch: two parts from two tokens on; four parts need two rounds of these workgroups)
   const int tsplit = a.S >= 2 ? 2 : 1;
-  hipLaunchKernelGGL((k_mix_up<QD, SBM, L, IT>), dim3((a.H / 32 + 7) / 8 * 8 * tsplit), dim3(UP_THREADS), 0, st, a,
-                     tsplit);
+  const dim3 grid((a.H / 32 + 7) / 8 * 8 * tsplit);
+  // the up-front loads sized to the part's tokens (the model's four classes, exact walkers)
+  const int per = (a.S + tsplit - 1) / tsplit;
+  const int fb = (per * a.LW + UP_THREADS - 1) / UP_THREADS, mr = (per * a.hc * 32 + UP_THREADS - 1) / UP_THREADS;
+  if constexpr (QD == 4 && IT > 0) {
+    if (fb <= 1 && mr <= 1) {
+      hipLaunchKernelGGL((k_mix_up<QD, SBM, L, IT, 1, 1>), grid, dim3(UP_THREADS), 0, st, a, tsplit);
+      return hipGetLastError();
+    }
+    if (fb <= 2 && mr <= 1) {
+      hipLaunchKernelGGL((k_mix_up<QD, SBM, L, IT, 2, 1>), grid, dim3(UP_THREADS), 0, st, a, tsplit);
+      return hipGetLastError();
+    }
+    if (fb <= 3 && mr <= 1) {
+      hipLaunchKernelGGL((k_mix_up<QD, SBM, L, IT, 3, 1>), grid, dim3(UP_THREADS), 0, st, a, tsplit);
+      return hipGetLastError();
+    }
+  }
+  if (fb > UP_FB_MAX || mr > UP_MR_MAX) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((k_mix_up<QD, SBM, L, IT, UP_FB_MAX, UP_MR_MAX>), grid, dim3(UP_THREADS), 0, st, a, tsplit);
   return hipGetLastError();
 }
 

@@ -271,6 +271,8 @@ __global__ __launch_bounds__(ATTN_THREADS) void k_attn_partial(const bf16* __res
 constexpr int PP_D = 256;
 constexpr int PP_PASSES = 3;  // normed rows per wave: G + (window rows in the chunk) <= 8 waves x 3
 
+// NPS: the norm passes of the launch (G + S <= 8 NPS), so its loads issued up front are all used
+template <int NPS>
 __global__ __launch_bounds__(ATTN_THREADS) void k_attn_partial_prep(
     const bf16* __restrict__ qkv, int QW, int S, int HQ, int HK, int ROT, const bf16* __restrict__ qnorm,
     const bf16* __restrict__ knorm, float eps, const bf16* __restrict__ cos_t, const bf16* __restrict__ sin_t,
@@ -298,10 +300,10 @@ __global__ __launch_bounds__(ATTN_THREADS) void k_attn_partial_prep(
   // each lane its four elements, the norm weights and the rotary table at a clamped column), the
   // window's value rows, the cached key and value rows
   const int items = G + nw;
-  uint2 xin[PP_PASSES], win[PP_PASSES];
-  bf16 cr[PP_PASSES][4], sr[PP_PASSES][4];
+  uint2 xin[NPS], win[NPS];
+  bf16 cr[NPS][4], sr[NPS][4];
 #pragma unroll
-  for (int pass = 0; pass < PP_PASSES; ++pass) {
+  for (int pass = 0; pass < NPS; ++pass) {
     const int it = wave + NW * pass, itc = it < items ? it : 0;
     const bool isq = itc < G;
     const int tok = isq ? s : w0 + (itc - G) - pos0;  // the window token of the row
@@ -356,7 +358,7 @@ __global__ __launch_bounds__(ATTN_THREADS) void k_attn_partial_prep(
   const int half = ROT / 2;
   float* xr = xw + (size_t)wave * D;
 #pragma unroll
-  for (int pass = 0; pass < PP_PASSES; ++pass) {
+  for (int pass = 0; pass < NPS; ++pass) {
     const int it = wave + NW * pass;
     if (it >= items) break;  // uniform per wave
     const uint32_t xa[2] = {xin[pass].x, xin[pass].y}, wa[2] = {win[pass].x, win[pass].y};
@@ -596,11 +598,20 @@ hipError_t launch_attn_partial_prep(const bf16* qkv, int QW, int S, int HQ, int 
   if (!attn_prep_fused_ok(S, HQ, HK, D, QW) || T < S) return hipErrorInvalidValue;
   const int nch = (T + ATTN_CHUNK - 1) / ATTN_CHUNK;
   const size_t lds = attn_partial_lds(HQ / HK, D) + (size_t)(ATTN_THREADS / 64) * D * 4;
+  // a chunk holds at most S window rows: items <= G + S
+  if (HQ / HK + S <= (ATTN_THREADS / 64) * 2) {
+    static size_t cur2 = 0;
+    hipError_t e = ensure_lds(k_attn_partial_prep<2>, lds, cur2);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(k_attn_partial_prep<2>, dim3(nch, HK, S), dim3(ATTN_THREADS), lds, st, qkv, QW, S, HQ, HK, ROT,
+                       qnorm, knorm, eps, cos_t, sin_t, kcache, vcache, tmax, T, scale, nch, part);
+    return hipGetLastError();
+  }
   static size_t cur = 0;
-  hipError_t e = ensure_lds(k_attn_partial_prep, lds, cur);
+  hipError_t e = ensure_lds(k_attn_partial_prep<PP_PASSES>, lds, cur);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(k_attn_partial_prep, dim3(nch, HK, S), dim3(ATTN_THREADS), lds, st, qkv, QW, S, HQ, HK, ROT,
-                     qnorm, knorm, eps, cos_t, sin_t, kcache, vcache, tmax, T, scale, nch, part);
+  hipLaunchKernelGGL(k_attn_partial_prep<PP_PASSES>, dim3(nch, HK, S), dim3(ATTN_THREADS), lds, st, qkv, QW, S, HQ,
+                     HK, ROT, qnorm, knorm, eps, cos_t, sin_t, kcache, vcache, tmax, T, scale, nch, part);
   return hipGetLastError();
 }
 

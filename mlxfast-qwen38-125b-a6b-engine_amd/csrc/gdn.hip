@@ -103,8 +103,11 @@ __device__ __forceinline__ const bf16* gdn_row_ptr(const GdnArgs& a, int r) {
   return a.proj + (size_t)(r - a.P) * a.pw;
 }
 
-template <int KC>
+// JP: journal steps the launch can replay (P <= JP), so the replay's loads issued up front are its
+// own, not clamped duplicates up to MAX_TOKENS ahead of the prep's loads.
+template <int KC, int JP>
 __global__ __launch_bounds__(GDN_THREADS) void k_gdn_step(GdnArgs a) {
+  static_assert(JP >= 1 && JP <= MAX_TOKENS, "journal steps");
   __shared__ float qs[MAX_TOKENS][GDN_D], ks[MAX_TOKENS][GDN_D], vs[MAX_TOKENS][GDN_D], ys[MAX_TOKENS][GDN_D];
   __shared__ float dec[MAX_TOKENS], bet[MAX_TOKENS];
   __shared__ bf16 gated[MAX_TOKENS][GDN_D];
@@ -129,11 +132,11 @@ __global__ __launch_bounds__(GDN_THREADS) void k_gdn_step(GdnArgs a) {
     s[i][2] = s4.z;
     s[i][3] = s4.w;
   }
-  float gdp[MAX_TOKENS], dlp[MAX_TOKENS][RPH];
-  uint2 kpw[MAX_TOKENS];  // the journal keys' four bf16 (raw until the replay, so no wait for them here)
+  float gdp[JP], dlp[JP][RPH];
+  uint2 kpw[JP];  // the journal keys' four bf16 (raw until the replay, so no wait for them here)
   if (P > 0) {
 #pragma unroll
-    for (int p = 0; p < MAX_TOKENS; ++p) {
+    for (int p = 0; p < JP; ++p) {
       const int pc = p < P ? p : P - 1;  // clamped: loads beyond P are issued but not used
       gdp[p] = a.decay_cur[(size_t)pc * a.hv + h];
       kpw[p] = *reinterpret_cast<const uint2*>(a.key_cur + ((size_t)pc * a.hk + hk) * GDN_D + 4 * l);
@@ -233,7 +236,7 @@ __global__ __launch_bounds__(GDN_THREADS) void k_gdn_step(GdnArgs a) {
   // ---- recurrence: RPH value rows per half-wave (r = r0 + hw + 16 i), lane l owns key elements 4l..4l+3
   if (P > 0) {  // committed steps of the previous window, in order
 #pragma unroll
-    for (int p = 0; p < MAX_TOKENS; ++p) {
+    for (int p = 0; p < JP; ++p) {
       if (p < P) {
 #pragma unroll
         for (int i = 0; i < RPH; ++i)
@@ -598,8 +601,21 @@ __global__ __launch_bounds__(GDN_THREADS) void k_gdn_replay(GdnArgs a, float* ss
 
 template <int KC>
 static hipError_t gdn_step_kc(const GdnArgs& a, hipStream_t st) {
-  if (!a.tickets || !a.ypub) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_gdn_step<KC>, dim3(a.hv, GDN_SPLIT), dim3(GDN_THREADS), 0, st, a);
+  if (!a.tickets || !a.ypub || a.P < 0 || a.P > MAX_TOKENS) return hipErrorInvalidValue;
+  const dim3 grid(a.hv, GDN_SPLIT);
+  if constexpr (KC == 4) {  // the model's conv: the replay sized to the journal (1, 2, 4 or 8 steps)
+    if (a.P <= 1) {
+      hipLaunchKernelGGL((k_gdn_step<KC, 1>), grid, dim3(GDN_THREADS), 0, st, a);
+    } else if (a.P <= 2) {
+      hipLaunchKernelGGL((k_gdn_step<KC, 2>), grid, dim3(GDN_THREADS), 0, st, a);
+    } else if (a.P <= 4) {
+      hipLaunchKernelGGL((k_gdn_step<KC, 4>), grid, dim3(GDN_THREADS), 0, st, a);
+    } else {
+      hipLaunchKernelGGL((k_gdn_step<KC, MAX_TOKENS>), grid, dim3(GDN_THREADS), 0, st, a);
+    }
+    return hipGetLastError();
+  }
+  hipLaunchKernelGGL((k_gdn_step<KC, MAX_TOKENS>), grid, dim3(GDN_THREADS), 0, st, a);
   return hipGetLastError();
 }
 

@@ -595,7 +595,8 @@ int mtpx_target_state_info(mtpx_target_state st, int64_t* offset, int* window);
  * window.  (Qwen4ExpCBv2LayerCache / recurrent state re-creation, Runner/Qwen4ExpRunner.swift:385-394.) */
 int mtpx_target_state_reset(mtpx_ctx ctx, mtpx_target_state st);
 /* S <= 8 tokens (device int32) at the committed offset -> logits bf16 [S, vocab], multi bf16
- * [S, hc*hidden], mixed bf16 [S, hidden] (each may be NULL). */
+ * [S, hc*hidden], mixed bf16 [S, hidden] (each may be NULL).  ids in plain host memory: MTPX_ERR_ARG
+ * before anything runs. */
 int mtpx_target_verify(mtpx_ctx ctx, mtpx_target t, mtpx_target_state st, const int32_t* ids, int S,
                        uint16_t* logits, uint16_t* multi, uint16_t* mixed);
 /* The first n (0..window) positions of the last verify become committed. */
@@ -610,7 +611,8 @@ int mtpx_target_commit(mtpx_target_state st, int n);
  * of 8 and its experts over the batch's slots sorted by expert, the GDN recurrence over the batch),
  * the PLE recurrence window by window.  Replaces the runner's prompt prefill windows (Runner/FastModel/TrackP12Prefill.swift:1-237,
  * TrackPrefillSort.swift:1-201, TrackPrefillIndirect.swift:5-227), with the decode path's arithmetic
- * instead of MLX's steel GEMM: the prompt's positions get the bits the verify path gives them. */
+ * instead of MLX's steel GEMM: the prompt's positions get the bits the verify path gives them.
+ * ids (device int32 [S]) in plain host memory: MTPX_ERR_ARG before anything runs. */
 int mtpx_target_prefill(mtpx_ctx ctx, mtpx_target t, mtpx_target_state st, const int32_t* ids, int S,
                         uint16_t* logits, uint16_t* multi);
 /* Distinct routed experts of each layer's MoE in the last verify (host int32 [num_layers];
@@ -644,7 +646,7 @@ int mtpx_session_reset(mtpx_session s);
 /* The prompt (device int32 [n], offset + n <= MTPX_INDEXER_BUDGET): mtpx_target_prefill in batches
  * of up to 512 positions, each committed and its multi streams observed by the drafter;
  * *first_token (host) = the argmax of the last position, which becomes the carry.  Synchronises
- * once. */
+ * once.  ids in plain host memory: MTPX_ERR_ARG, the session unchanged. */
 int mtpx_session_prefill(mtpx_session s, const int32_t* ids, int n, int32_t* first_token);
 /* One round of draft depth k (0..MTPX_MAX_DRAFT_DEPTH); force may be NULL.  tokens (host, k+1
  * entries) receives the n + 1 committed tokens, *n_tokens = n + 1.  A prefill or round that fails

@@ -7,6 +7,20 @@
 #include "../../include/mtpx.h"
 
 namespace mtpx {
+// Memory the device can read at p: device or managed memory, or host memory mapped for the device
+// (pinned or registered).  Plain host memory is refused: a kernel reading it faults the GPU.  (A
+// failed query leaves an error the next launch check would report, so it is cleared.)
+inline bool device_readable(const void* p) {
+  if (!p) return false;
+  hipPointerAttribute_t at{};
+  if (hipPointerGetAttributes(&at, p) != hipSuccess) {
+    (void)hipGetLastError();
+    return false;
+  }
+  return at.type == hipMemoryTypeDevice || at.type == hipMemoryTypeManaged ||
+         (at.type == hipMemoryTypeHost && at.devicePointer != nullptr);
+}
+
 hipStream_t ctx_stream(mtpx_ctx ctx);
 int ctx_device(mtpx_ctx ctx);
 // Error text for the next mtpx_last_error() (returns code).

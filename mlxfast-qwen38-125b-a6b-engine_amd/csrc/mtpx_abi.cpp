@@ -2600,6 +2600,7 @@ int mtpx_target_verify(mtpx_ctx h, mtpx_target th, mtpx_target_state sh, const i
   Target* t = static_cast<Target*>(th.ctx);
   TargetState* s = static_cast<TargetState*>(sh.ctx);
   ARG(c && t && s && ids, "null argument");
+  ARG(device_readable(ids), "ids: not memory the device can read (device or pinned host memory)");
   ARG(s->t == t, "state of another target");
   if (s->broken) return fail(MTPX_ERR_STATE, "state left inconsistent by a failed verify; reset it first");
   ARG(S >= 1 && S <= MAX_TOKENS, "S=%d", S);
@@ -2626,6 +2627,7 @@ int mtpx_target_prefill(mtpx_ctx h, mtpx_target th, mtpx_target_state sh, const 
   Target* t = static_cast<Target*>(th.ctx);
   TargetState* s = static_cast<TargetState*>(sh.ctx);
   ARG(c && t && s && ids, "null argument");
+  ARG(device_readable(ids), "ids: not memory the device can read (device or pinned host memory)");
   ARG(s->t == t, "state of another target");
   if (s->broken) return fail(MTPX_ERR_STATE, "state left inconsistent by a failed verify; reset it first");
   ARG(S >= 1, "S=%d", S);

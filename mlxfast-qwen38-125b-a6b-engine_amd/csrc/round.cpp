@@ -156,6 +156,8 @@ static int round_steps(Session* s, int k, const mtpx_force_params* force, float 
 int mtpx_session_prefill(mtpx_session sh, const int32_t* ids, int n, int32_t* first_token) {
   Session* s = static_cast<Session*>(sh.ctx);
   if (!s || !ids || n < 1) return set_error(MTPX_ERR_ARG, "session prefill: bad argument");
+  if (!device_readable(ids))
+    return set_error(MTPX_ERR_ARG, "session prefill: ids are not memory the device can read (device or pinned host)");
   if (s->broken) return set_error(MTPX_ERR_STATE, "session: a previous call failed part way (reset it)");
   if (s->primed) return set_error(MTPX_ERR_STATE, "session prefill: the session already holds a context");
   if (s->offset + n > MTPX_INDEXER_BUDGET) return set_error(MTPX_ERR_ARG, "session prefill: past the indexer budget");

@@ -250,6 +250,29 @@ def test_round_refusals(model):
     ns.close()
 
 
+def test_host_ids_refused_before_any_launch(model):
+    """Token ids in plain host memory are refused by the session prefill, the target verify and the
+    target prefill (a kernel reading them would fault the GPU).  Each call also carries an argument
+    refused later but still before any launch (past the indexer budget of 2048 positions, wider than
+    a verify window of 8, past the cache), so none of them launches whichever check refuses it; the
+    message says which did.  The refusals change nothing: the session then prefills and decodes."""
+    import mtpx
+    ctx, t, head, prompt = model
+    s = mtpx.Session(ctx, t, head)
+    with pytest.raises(mtpx.MtpxError, match="ids are not memory the device can read"):
+        s.prefill(torch.zeros(2048 + 1, dtype=torch.int32))
+    st = mtpx.TargetState(ctx, t)
+    with pytest.raises(mtpx.MtpxError, match="ids: not memory the device can read"):
+        t.verify(st, torch.zeros(9, dtype=torch.int32))
+    with pytest.raises(mtpx.MtpxError, match="ids: not memory the device can read"):
+        t.prefill(st, torch.zeros(LAYER["max_positions"] + 1, dtype=torch.int32))
+    st.close()
+    first = s.prefill(dev(prompt))
+    assert 0 <= first < TARGET["vocab"]
+    assert len(s.round(1)) >= 1
+    s.close()
+
+
 def test_failed_prefill_breaks_the_session_until_reset(model):
     """A prompt longer than the caches fails in its last windows after earlier windows were
     committed: the session refuses further calls until reset, then works again."""

@@ -74,6 +74,12 @@ def test_randn_deterministic_and_normal(ctx):
     (66001, 2560, 64, 3), (65550, 2560, 32, 4),
     # two token groups in one launch (5..8 tokens): ragged rows, several tile groups per workgroup
     (16480, 2560, 64, 6), (1000, 2560, 64, 8), (66000, 2560, 64, 5), (4096, 2048, 64, 8), (13440, 2560, 32, 7),
+    # one token group whose eight-wave tile groups just outnumber the CUs: ten-wave workgroups, ragged last tile
+    # (one window, and two windows of four)
+    (16470, 2560, 32, 4), (16470, 2560, 64, 6),
+    # the dot-product kernel's equal windows past the CU count: five-wave workgroups (two windows of 2 and of 3
+    # tokens, a ragged last workgroup); three tokens (2 + 1) keep four waves
+    (2560, 6144, 64, 6), (2490, 6144, 64, 4), (2560, 6144, 64, 3),
 ])
 def test_qmv_bit_exact(ctx, N, K, gs, M):
     _print_case(N=N, K=K, gs=gs, M=M)

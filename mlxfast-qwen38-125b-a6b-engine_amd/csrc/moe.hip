@@ -765,15 +765,18 @@ __global__ __launch_bounds__(DD_THREADS) void k_moe_gate_up_dd(MoeArgs a0) {
 // outputs.  (Combining in this launch -- agent-scope stores of the outputs, a per-row-block
 // ticket and the last arriver folding the block -- was measured slower: the coherent stores, the
 // wait for them and the serial tail cost more than the combine launch.)
-template <int L>
-constexpr int dd_down_rows() { return 4 * (64 / L); }
+// NW waves a unit (4, or 8 where the units of a window fit the resident workgroups: the slot's
+// activation load and block preparation shared by twice the rows).
+template <int L, int NW = 4>
+constexpr int dd_down_rows() { return NW * (64 / L); }
 
-template <int L, int IT, bool PK>
-__global__ __launch_bounds__(DD_THREADS) void k_moe_down_dd(MoeArgs a0) {
+template <int L, int IT, bool PK, int NW>
+__global__ __launch_bounds__(64 * NW) void k_moe_down_dd(MoeArgs a0) {
   const MoeArgs a = a0.gorder ? a0 : moe_window(a0, blockIdx.y);
   extern __shared__ uint32_t lds[];  // [F/32][XP_DW]
   constexpr int RW = 64 / L;
-  constexpr int DR = dd_down_rows<L>();
+  constexpr int DR = dd_down_rows<L, NW>();
+  constexpr int NT = 64 * NW;
   const int H = a.H, F = a.F, gs = a.gs, M = a.M, K = a.K;
   const int nb = F / 32, ng = F / gs, P = sb_row_len(F, gs), nhb = (H + DR - 1) / DR;
   const int wslots = M * (K + 1), slots = a.gorder ? a.nwin * wslots : wslots;
@@ -795,12 +798,12 @@ __global__ __launch_bounds__(DD_THREADS) void k_moe_down_dd(MoeArgs a0) {
   const bf16* bi = shared ? a.sh_down_b : a.down_b;
   const size_t base = shared ? 0 : (size_t)e * H;
   const size_t ra = base + (va ? hi : h0);
-  // the slot's bf16 activations first (element q * 256 + t), then the weights
-  constexpr int NA = 8;  // F <= NA * 256
+  // the slot's bf16 activations first (element q * NT + t), then the weights
+  constexpr int NA = 8 * DD_THREADS / NT;  // F <= 8 * 256
   bf16 av[NA];
 #pragma unroll
   for (int q = 0; q < NA; ++q) {
-    const int i = q * DD_THREADS + threadIdx.x;
+    const int i = q * NT + threadIdx.x;
     av[q] = i < F ? a.act[(size_t)sl * F + i] : (bf16)0;
   }
   asm volatile("" ::: "memory");
@@ -809,7 +812,7 @@ __global__ __launch_bounds__(DD_THREADS) void k_moe_down_dd(MoeArgs a0) {
   asm volatile("" ::: "memory");
 #pragma unroll
   for (int q = 0; q < NA; ++q) {
-    const int blk = (q * DD_THREADS + (int)threadIdx.x) >> 5;  // uniform per 32-lane group
+    const int blk = (q * NT + (int)threadIdx.x) >> 5;  // uniform per 32-lane group
     if (blk < nb) xprep_lanes_direct(av[q], threadIdx.x & 31, lds + (size_t)blk * XP_DW);
   }
   __syncthreads();
@@ -1059,16 +1062,24 @@ static hipError_t gate_up_dd_li(const MoeArgs& a, hipStream_t st) {
 
 template <int L, int IT, bool PK>
 static hipError_t down_dd_pk(const MoeArgs& a, hipStream_t st) {
-  constexpr int DR = dd_down_rows<L>();
-  const int nhb = (a.H + DR - 1) / DR;
   const size_t lds = (size_t)(a.F / 32) * XP_DW * 4;
-  static size_t cur = 0;
-  hipError_t e = ensure_lds(k_moe_down_dd<L, IT, PK>, lds, cur);
-  if (e != hipSuccess) return e;
   const int nw = a.gorder ? 1 : a.nwin;
-  const int units = a.M * (a.K + 1) * (a.gorder ? a.nwin : 1) * nhb;
-  hipLaunchKernelGGL((k_moe_down_dd<L, IT, PK>), dim3((units + 7) / 8 * 8, nw), dim3(DD_THREADS), lds, st, a);
-  return hipGetLastError();
+  const int slots = a.M * (a.K + 1) * (a.gorder ? a.nwin : 1);
+  auto go = [&](auto kern, size_t& cur, int dr, int nthr) {
+    hipError_t e = ensure_lds(kern, lds, cur);
+    if (e != hipSuccess) return e;
+    const int units = slots * ((a.H + dr - 1) / dr);
+    hipLaunchKernelGGL(kern, dim3((units + 7) / 8 * 8, nw), dim3(nthr), lds, st, a);
+    return hipGetLastError();
+  };
+  static size_t c4 = 0, c8 = 0;
+  // eight-wave units where the window's units then fit the resident workgroups in one round (four waves a
+  // SIMD for them) and the four-wave ones take more than half of theirs
+  constexpr int D4 = dd_down_rows<L, 4>(), D8 = dd_down_rows<L, 8>();
+  const int u4 = slots * ((a.H + D4 - 1) / D4) * nw, u8 = slots * ((a.H + D8 - 1) / D8) * nw;
+  if (!a.gorder && u8 <= 4 * device_cus() && u4 > 4 * device_cus())
+    return go(k_moe_down_dd<L, IT, PK, 8>, c8, D8, 512);
+  return go(k_moe_down_dd<L, IT, PK, 4>, c4, D4, 256);
 }
 
 template <int L, int IT>

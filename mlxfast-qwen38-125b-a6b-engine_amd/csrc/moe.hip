@@ -765,8 +765,8 @@ __global__ __launch_bounds__(DD_THREADS) void k_moe_gate_up_dd(MoeArgs a0) {
 // outputs.  (Combining in this launch -- agent-scope stores of the outputs, a per-row-block
 // ticket and the last arriver folding the block -- was measured slower: the coherent stores, the
 // wait for them and the serial tail cost more than the combine launch.)
-// NW waves a unit (4, or 8 where the units of a window fit the resident workgroups: the slot's
-// activation load and block preparation shared by twice the rows).
+// NW waves a unit (8 for a window's slots: the slot's activation load and block preparation shared by
+// twice the rows; 4 in the prefill's global order).
 template <int L, int NW = 4>
 constexpr int dd_down_rows() { return NW * (64 / L); }
 
@@ -1073,12 +1073,11 @@ static hipError_t down_dd_pk(const MoeArgs& a, hipStream_t st) {
     return hipGetLastError();
   };
   static size_t c4 = 0, c8 = 0;
-  // eight-wave units where the window's units then fit the resident workgroups in one round (four waves a
-  // SIMD for them) and the four-wave ones take more than half of theirs
+  // eight-wave units for a window (the slot's activation load and block preparation shared by twice the
+  // rows: 9.2 -> 8.4 us per launch at one token, 11.3 -> 10.2 at two, 13.2 -> 12.1 at three, 17.9 -> 17.2 at
+  // six); the prefill's global order keeps four
   constexpr int D4 = dd_down_rows<L, 4>(), D8 = dd_down_rows<L, 8>();
-  const int u4 = slots * ((a.H + D4 - 1) / D4) * nw, u8 = slots * ((a.H + D8 - 1) / D8) * nw;
-  if (!a.gorder && u8 <= 4 * device_cus() && u4 > 4 * device_cus())
-    return go(k_moe_down_dd<L, IT, PK, 8>, c8, D8, 512);
+  if (!a.gorder) return go(k_moe_down_dd<L, IT, PK, 8>, c8, D8, 512);
   return go(k_moe_down_dd<L, IT, PK, 4>, c4, D4, 256);
 }
 

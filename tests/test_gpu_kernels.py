@@ -79,7 +79,7 @@ def test_randn_deterministic_and_normal(ctx):
     (16470, 2560, 32, 4), (16470, 2560, 64, 6),
     # the dot-product kernel's equal windows past the CU count: five-wave workgroups (two windows of 2 and of 3
     # tokens, a ragged last workgroup); three tokens (2 + 1) keep four waves
-    (2560, 6144, 64, 6), (2490, 6144, 64, 4), (2560, 6144, 64, 3),
+    (2560, 6144, 64, 6), (2490, 6144, 64, 4), (2560, 6144, 64, 3), (2560, 6144, 32, 8),
 ])
 def test_qmv_bit_exact(ctx, N, K, gs, M):
     _print_case(N=N, K=K, gs=gs, M=M)

@@ -1107,10 +1107,6 @@ constexpr size_t mma_lds_bytes() {
 // need a second, nearly empty round of workgroups -- the caller runs four tokens per launch instead.
 // M > 4 TG tokens: windows of 4 TG in grid Y, one workgroup per tile group (rounded up to whole XCD
 // rounds, so the windows of a tile group share an XCD and its L2).
-// One token group: ten-wave workgroups (five tiles of two classes) where they fit a launch that
-// eight-wave ones do not in one round -- one workgroup per CU for one window (with eight, the few CUs
-// that take a second workgroup finish last: GDN in-projection, 258 groups on 256 CUs), within the
-// resident workgroups for several windows (eight: 2 x 264 workgroups of four tokens where 512 fit).
 template <int L, int IT, int C, int TG, int NWV>
 static hipError_t qmv_mma_launch(const uint32_t* wq, const uint32_t* sb, int N, int K, int gs, const uint32_t* xp,
                                  int M, bf16* y, float* yf, hipStream_t st) {
@@ -1139,6 +1135,10 @@ static hipError_t qmv_mma_launch(const uint32_t* wq, const uint32_t* sb, int N, 
   return hipGetLastError();
 }
 
+// One token group: ten-wave workgroups (five tiles of two classes) where they fit a launch that
+// eight-wave ones do not in one round -- one workgroup per CU for one window (with eight, the few CUs
+// that take a second workgroup finish last: GDN in-projection, 258 groups on 256 CUs), within the
+// resident workgroups for several windows (eight: 2 x 264 workgroups of four tokens where 512 fit).
 template <int L, int IT, int C, int TG>
 static hipError_t qmv_mma_c(const uint32_t* wq, const uint32_t* sb, int N, int K, int gs, const uint32_t* xp, int M,
                             bf16* y, float* yf, hipStream_t st) {

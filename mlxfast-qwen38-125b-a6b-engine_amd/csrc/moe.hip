@@ -760,7 +760,7 @@ __global__ __launch_bounds__(DD_THREADS) void k_moe_gate_up_dd(MoeArgs a0) {
   }
 }
 
-// down: a unit = 4 * 64/L rows of H (one row per lane group) of one slot (two rows per lane
+// down: a unit = NW * 64/L rows of H (one row per lane group) of one slot (two rows per lane
 // group measured 15.3 against 13.6 us per launch at M = 4); the combine launch folds the slots'
 // outputs.  (Combining in this launch -- agent-scope stores of the outputs, a per-row-block
 // ticket and the last arriver folding the block -- was measured slower: the coherent stores, the
